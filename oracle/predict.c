@@ -1,0 +1,40 @@
+/*
+ * Oracle (test infrastructure): batch prediction.
+ *
+ * model/predict.rs:60-97 (margin_from_trees: per-output intercepts, then
+ * accumulate_forest), :107-193 (trees summed in ascending order per
+ * (row, output): out += weight * leaf, f32), tree/regtree.rs:38-66 and
+ * tree/mod.rs:52-58 (a present value goes left iff value < split_cond; a
+ * missing one follows default_left), compact/mod.rs:1052-1095.
+ */
+#include "oracle.h"
+
+#include <math.h>
+
+static int is_missing(float v, float missing) {
+    if (isnan(missing)) return isnan(v);
+    return v == missing;
+}
+
+void or_predict_margin(const or_forest_desc *fd, const float *x, size_t n, size_t n_cols,
+                       float missing, float *out, int32_t *out_leaf) {
+    size_t k = fd->n_outputs;
+#pragma omp parallel for schedule(static)
+    for (size_t r = 0; r < n; r++) {
+        const float *row = x + r * n_cols;
+        float *o = out + r * k;
+        for (size_t c = 0; c < k; c++) o[c] = fd->base_score[c];
+        for (size_t t = 0; t < fd->n_trees; t++) {
+            uint32_t base = fd->tree_offset[t];
+            int32_t nid = 0;
+            while (fd->left[base + nid] != -1) {
+                const uint32_t at = base + (uint32_t)nid;
+                float v = row[fd->split_feature[at]];
+                int go_left = is_missing(v, missing) ? fd->default_left[at] : (v < fd->split_cond[at]);
+                nid = go_left ? fd->left[at] : fd->right[at];
+            }
+            if (out_leaf) out_leaf[r * fd->n_trees + t] = nid;
+            o[fd->tree_output[t]] += fd->tree_weight[t] * fd->leaf_value[base + (uint32_t)nid];
+        }
+    }
+}

@@ -1,0 +1,77 @@
+"""Shared data generators and fixture loaders for the test suite."""
+import json
+import os
+import struct
+
+import numpy as np
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def four_features(n=160):
+    """hessboost tests/common/mod.rs:28-39: values in [0, 1), feature 3
+    missing on every 7th row, each an f32 quotient."""
+    i = np.arange(n)
+    a = ((i * 37) % 101).astype(np.float32) / np.float32(101)
+    b = ((i * 53) % 97).astype(np.float32) / np.float32(97)
+    c = ((i * 11) % 89).astype(np.float32) / np.float32(89)
+    d = ((i * 29) % 83).astype(np.float32) / np.float32(83)
+    d[i % 7 == 0] = np.nan
+    return np.stack([a, b, c, d], axis=1).astype(np.float32)
+
+
+def train_labels(x, k=1):
+    """tests/native_format.rs:441-454: y_t = 2a - b + t*c + 0.1 in f32."""
+    a, b, c = x[:, 0], x[:, 1], x[:, 2]
+    ys = [((np.float32(2) * a - b) + np.float32(t) * c + np.float32(0.1)).astype(np.float32)
+          for t in range(k)]
+    return ys[0] if k == 1 else np.stack(ys, axis=1)
+
+
+def bits_to_f32(v):
+    return np.asarray(v, np.uint32).view(np.float32)
+
+
+def load_saved_models():
+    return json.load(open(os.path.join(GOLDEN, "saved_models.json")))
+
+
+def golden_forest(case):
+    """Flat forest arrays of a saved model, restricted to its effective trees
+    (model/mod.rs:1238-1242: best_iteration selects the first iterations)."""
+    npt = case["num_parallel_tree"]
+    k = case["n_outputs"]
+    trees = case["trees"]
+    n_trees = len(trees)
+    if case["best_iteration"] is not None:
+        n_trees = min((case["best_iteration"] + 1) * k * npt, n_trees)
+    off = [0]
+    cols = {key: [] for key in ("split_feature", "split_cond", "default_left", "left", "right", "leaf_value")}
+    for t in trees[:n_trees]:
+        for key in cols:
+            cols[key].extend(t[key])
+        off.append(len(cols["left"]))
+    return dict(
+        tree_offset=np.array(off, np.uint32),
+        split_feature=np.array(cols["split_feature"], np.uint32),
+        split_cond=bits_to_f32(cols["split_cond"]),
+        default_left=np.array(cols["default_left"], np.uint8),
+        left=np.array(cols["left"], np.int32),
+        right=np.array(cols["right"], np.int32),
+        leaf_value=bits_to_f32(cols["leaf_value"]),
+        tree_weight=bits_to_f32(case["tree_weights"][:n_trees]),
+        tree_output=np.array([(t // npt) % k for t in range(n_trees)], np.uint32),
+        base_score=bits_to_f32(case["base_score"]),
+        n_outputs=k,
+    )
+
+
+def splitmix64(seed):
+    """A splitmix64 stream (the synthetic data generator's source)."""
+    state = np.uint64(seed)
+    while True:
+        state = np.uint64((int(state) + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF)
+        z = int(state)
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
+        yield z ^ (z >> 31)

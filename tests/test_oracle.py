@@ -1,0 +1,311 @@
+"""Pins of the CPU oracle against the reference's own fixtures and known answers.
+
+Every check here compares the oracle with something it does not compute
+itself: the reference's saved models and recorded margins, the reference's
+own unit-test known answers, brute-force formulations, or closed forms.
+"""
+import json
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import (bits_to_f32, four_features, golden_forest, load_saved_models,
+                           train_labels)
+
+
+@pytest.fixture(scope="module")
+def saved():
+    return load_saved_models()
+
+
+def test_early_stopping_model_reproduced_bit_for_bit(saved):
+    """tests/native_format.rs:660-669: `train(base(), matrix(1), 4)` is the saved
+    early-stopping model; every field of its four trees must match."""
+    x = four_features()
+    y = train_labels(x)
+    ds = O.Dataset(x, max_bin=256)
+    model = O.Model(ds, y, O.params(max_depth=3), 4)
+    for ver in ("0.2.0", "0.4.3", "0.4.9"):
+        case = saved[f"{ver}/early_stopping"]
+        assert np.array_equal(model.base_score().view(np.uint32),
+                              np.array(case["base_score"], np.uint32))
+        trees = model.trees()
+        assert len(trees) == len(case["trees"])
+        for t, (mine, ref) in enumerate(zip(trees, case["trees"])):
+            assert len(mine) == len(ref["left"]), f"tree {t}"
+            for key in ("split_feature", "default_left", "left", "right"):
+                got = [int(n[key]) for n in mine]
+                assert got == [int(v) for v in ref[key]], f"tree {t} {key}"
+            for key in ("split_cond", "leaf_value", "sum_hess", "split_gain"):
+                got = np.array([n[key] for n in mine], np.float32).view(np.uint32)
+                want = np.array(ref[key], np.uint32)
+                leaf = np.array([n["left"] for n in mine]) == -1
+                if key == "split_cond":
+                    got, want = got[~leaf], want[~leaf]
+                if key == "split_gain":
+                    got, want = got[~leaf], want[~leaf]
+                assert np.array_equal(got, want), f"tree {t} {key}"
+
+
+@pytest.mark.parametrize("name", ["early_stopping", "dart", "multiclass_forest", "quantiles",
+                                  "expectiles", "aft", "dist_normal", "dist_negbinomial",
+                                  "multi_target"])
+def test_saved_model_margins_bit_exact(saved, name):
+    """tests/native_format.rs:822-860: each saved model reproduces its recorded
+    little-endian f32 margins on the closed-form rows."""
+    x = four_features()
+    for ver in ("0.2.0", "0.4.3", "0.4.9"):
+        case = saved[f"{ver}/{name}"]
+        forest = golden_forest(case)
+        out = O.predict_margin(forest, x)
+        want = np.array(case["margins"], np.uint32)
+        assert np.array_equal(out.view(np.uint32), want), f"{ver}/{name}"
+
+
+def test_splits_on_separating_feature():
+    """builder/hist/mod.rs:1065-1082: four rows, one separating feature."""
+    x = np.array([[0.0], [0.0], [1.0], [1.0]], np.float32)
+    ds = O.Dataset(x)
+    gp = np.array([[1, 1], [1, 1], [-1, 1], [-1, 1]], np.float32)
+    p = O.params(max_depth=1, reg_lambda=0.0, min_child_weight=0.0, gamma=0.0, eta=1.0)
+    nodes, leaf = ds.grow_tree(gp, p)
+    assert len(nodes) == 3
+    vals = [nodes[leaf[r]]["leaf_value"] for r in range(4)]
+    assert abs(vals[0] + 1.0) < 1e-6 and abs(vals[2] - 1.0) < 1e-6
+
+
+def test_gain_closed_forms():
+    """tree/gain.rs:148-196: w = 4/3 and gain 16/3 at G=-4, H=2, lambda=1;
+    L1 shrinks, max_delta_step clamps 100 to 1, min_child_weight zeroes."""
+    L = O.lib()
+    p = O.params(reg_lambda=1.0, min_child_weight=0.0)
+    assert abs(L.or_calc_weight(-4.0, 2.0, p) - 4.0 / 3.0) < 1e-12
+    # root_gain at the f32-rounded weight: -(2Gw + (H+l) w^2) = 16/3 to f32 precision
+    assert abs(L.or_node_gain(-4.0, 2.0, -math.inf, math.inf, p) - 16.0 / 3.0) < 1e-5
+    p1 = O.params(reg_lambda=1.0, alpha=1.0, min_child_weight=0.0)
+    assert L.or_node_gain(-4.0, 2.0, -math.inf, math.inf, p1) < L.or_node_gain(-4.0, 2.0, -math.inf, math.inf, p)
+    assert abs(L.or_calc_weight(-5.0, 1.0, O.params(reg_lambda=0.0, alpha=2.0, min_child_weight=0.0)) - 3.0) < 1e-12
+    pm = O.params(reg_lambda=0.0, max_delta_step=1.0, min_child_weight=0.0)
+    assert L.or_calc_weight(-100.0, 1.0, pm) == 1.0
+    pc = O.params(reg_lambda=1.0, min_child_weight=1.0)
+    assert L.or_calc_weight(-4.0, 0.5, pc) == 0.0
+
+
+def _sparse_one_feature(values):
+    """A CSR index of n rows holding only feature 0 of 3 (hist/mod.rs:776-786)."""
+    n = len(values)
+    return O.Dataset(csr=(np.arange(n + 1), np.zeros(n, np.uint32), np.asarray(values, np.float32)),
+                     n_cols=3)
+
+
+@pytest.mark.parametrize("threads", [1, 4])
+def test_blocked_sum_does_not_depend_on_threads(threads):
+    """tree/hist/mod.rs:937-958: 8,192 rows in one bin with g = 2^54, -2^54, 1
+    at rows 0, 4096, 4097: the two blocks sum to 0, never the chain's 1."""
+    n = 8192
+    ds = _sparse_one_feature(np.ones(n))
+    assert not ds.dense and ds.columns() is None
+    gp = np.zeros((n, 2), np.float32)
+    gp[:, 1] = 1.0
+    gp[0, 0] = 2.0 ** 54
+    gp[4096, 0] = -(2.0 ** 54)
+    gp[4097, 0] = 1.0
+    O.set_threads(threads)
+    try:
+        h = ds.build_hist(np.arange(n), gp)
+    finally:
+        O.set_threads(8)
+    assert h[0, 0] == 0.0 and h[0, 1] == float(n)
+    assert np.all(h[1:] == 0.0)
+
+
+def test_blocked_build_matches_block_order_reference():
+    """tree/hist/mod.rs:965-1005: blocks of `grain` rows each chained from zero,
+    partials added in block order; the case separates block from chain."""
+    n = 6 * 4096 + 123
+    x = (np.arange(n) % 7).astype(np.float32)
+    ds = _sparse_one_feature(x)
+    i = np.arange(n)
+    scale = np.float32(2.0) ** ((i * 37 % 61) - 30).astype(np.float32)
+    g = ((i * 7919) % 1237).astype(np.float32) / np.float32(331.0) * scale - np.float32(1.0)
+    gp = np.stack([g, scale], axis=1).astype(np.float32)
+    rows = i[i % 11 != 3].astype(np.uint32)
+    grain = -(-len(rows) // (len(rows) // 4096))
+    bins = np.array([O.lib().or_index_feature_bin(ds.index, int(r), 0) for r in range(n)])
+    total = ds.total_bins
+    expect = np.zeros((total, 2))
+    for start in range(0, len(rows), grain):
+        part = np.zeros((total, 2))
+        for r in rows[start:start + grain]:
+            part[bins[r], 0] += float(gp[r, 0])
+            part[bins[r], 1] += float(gp[r, 1])
+        expect += part if start else 0.0
+        if not start:
+            expect = part.copy()
+    chain = np.zeros((total, 2))
+    for r in rows:
+        chain[bins[r], 0] += float(gp[r, 0])
+        chain[bins[r], 1] += float(gp[r, 1])
+    assert not np.array_equal(expect, chain)
+    got = ds.build_hist(rows, gp)
+    assert np.array_equal(got, expect)
+
+
+def test_sum_order_describes_the_build():
+    """tree/hist/mod.rs:877-903 (sum_order known answers)."""
+    L = O.lib()
+    big = (1 << 18) + 1
+    pt = 8192
+    assert L.or_sum_order_grain(0, big, pt - 1, 0) == 0
+    assert L.or_sum_order_grain(0, big, pt, 1) == -(-pt // 2)
+    assert L.or_sum_order_grain(1, big, pt, 1) == 0
+    assert L.or_sum_order_grain(1, big, pt, 0) == -(-pt // 2)
+    assert L.or_sum_order_grain(1, 1 << 18, pt, 0) == 0
+    m = 6 * 4096 + 123
+    assert L.or_sum_order_grain(0, big, m, 0) == -(-m // 6)
+
+
+def test_dense_sweeps_match_row_order_reference():
+    """tree/hist/mod.rs:757-773, :775-826: every bin receives its rows in
+    ascending order, for the whole range, a subset and an offset range."""
+    n, f = 3 * 8192 + 129, 7
+    x = (((np.arange(n * f) * 2654435761) % 1009).astype(np.float32) / np.float32(7.0)).reshape(n, f)
+    ds = O.Dataset(x, max_bin=64)
+    assert ds.dense and ds.columns() is not None
+    i = np.arange(n)
+    gp = np.stack([((i * 7919) % 1237).astype(np.float32) / np.float32(331.0) - np.float32(1.9),
+                   np.float32(0.25) + (i % 5).astype(np.float32)], axis=1).astype(np.float32)
+    row_ptr, gbins = ds.row_bins()
+    gbins = gbins.reshape(n, f)
+    for rows in (i, i[i % 3 != 1], np.arange(1000, 1000 + 8192)):
+        ref = np.zeros((ds.total_bins, 2))
+        # one row-order chain per bin (np.add.at adds in index order)
+        for c in range(f):
+            np.add.at(ref[:, 0], gbins[rows, c], gp[rows, 0].astype(np.float64))
+            np.add.at(ref[:, 1], gbins[rows, c], gp[rows, 1].astype(np.float64))
+        got = ds.build_hist(rows, gp)
+        assert np.array_equal(got, ref)
+
+
+def test_cuts_closed_form_for_few_distinct_values():
+    """sketch.rs:914-930, quantile.rs:926-996: with at most max_bin distinct
+    values the cuts are every distinct value but the minimum, then the
+    sentinel max + (|max| + 1e-5); a constant feature has one bin."""
+    rng = np.random.default_rng(0)
+    vals = np.round(rng.normal(size=40) * 100).astype(np.float32)
+    x = np.stack([rng.choice(vals, size=5000), np.full(5000, 3.0, np.float32)], axis=1)
+    ds = O.Dataset(x, max_bin=256)
+    off = ds.feature_offset
+    cuts = ds.cut_values
+    d = np.unique(x[:, 0])
+    mx = d[-1]
+    want = np.concatenate([d[1:], [np.float32(mx + (abs(mx) + np.float32(1e-5)))]]).astype(np.float32)
+    assert np.array_equal(cuts[off[0]:off[1]], want)
+    assert off[2] - off[1] == 1
+    c3 = np.float32(3.0)
+    assert cuts[off[1]] == np.float32(c3 + (abs(c3) + np.float32(1e-5)))
+
+
+def test_cuts_quantile_properties_on_continuous_data():
+    """quantile.rs:926-996 invariants: strictly increasing cuts, at most
+    max_bin + 1 per feature, and bins of near-equal mass (rank error within
+    the sketch's eps = 1/max_bin)."""
+    rng = np.random.default_rng(1)
+    n = 200_000
+    x = rng.normal(size=(n, 3)).astype(np.float32)
+    for max_bin in (16, 256):
+        ds = O.Dataset(x, max_bin=max_bin)
+        off = ds.feature_offset
+        cuts = ds.cut_values
+        _, gb = ds.row_bins()
+        gb = gb.reshape(n, 3)
+        for f in range(3):
+            c = cuts[off[f]:off[f + 1]]
+            assert len(c) <= max_bin + 1 and np.all(np.diff(c) > 0)
+            counts = np.bincount(gb[:, f] - off[f], minlength=len(c))
+            assert counts.max() <= n / max_bin * 1.5 + 2
+
+
+def test_bin_assignment_is_upper_bound_count():
+    """quantile.rs:285-296: bin = #{cuts <= v}, clamped to the last bin."""
+    rng = np.random.default_rng(2)
+    x = rng.normal(size=(3000, 2)).astype(np.float32)
+    x[::17, 1] = np.nan
+    ds = O.Dataset(x, max_bin=32)
+    off = ds.feature_offset
+    cuts = ds.cut_values
+    fb = ds.feature_bins()
+    for f in range(2):
+        c = cuts[off[f]:off[f + 1]]
+        v = x[:, f]
+        present = ~np.isnan(v)
+        want = np.minimum(np.searchsorted(c, v[present], side="right"), len(c) - 1) + off[f]
+        assert np.array_equal(fb[present, f], want)
+        assert np.all(fb[~present, f] == -1)
+
+
+def test_partition_matches_per_row_routing():
+    """builder/partition.rs:325+: stable, each row where its own bin decides,
+    missing rows following default_left, on dense columns and on CSR rows."""
+    rng = np.random.default_rng(3)
+    n = 5000
+    x = rng.normal(size=(n, 4)).astype(np.float32)
+    x[rng.random((n, 4)) < 0.1] = np.nan
+    ds = O.Dataset(x, max_bin=64)
+    fb = ds.feature_bins()
+    rows = np.sort(rng.choice(n, size=3000, replace=False)).astype(np.uint32)
+    off = ds.feature_offset
+    for feat in range(4):
+        for b in (-1, int(off[feat]) + 5, int(off[feat + 1]) - 1):
+            for dl in (0, 1):
+                L, R = ds.partition(rows, feat, b, dl)
+                v = fb[rows, feat]
+                go = np.where(v < 0, bool(dl), (v >= 0) & (v <= b) & (b >= 0))
+                assert np.array_equal(L, rows[go]) and np.array_equal(R, rows[~go])
+
+
+def test_logistic_gradient_vector_and_scalar_paths():
+    """simd/x86_64.rs:106-160 vs simd/scalar.rs:8-29: vectors of 8 rows with
+    all |m| <= 80 take the polynomial, the tail (n % 8 rows, or every row
+    when n < 16) and out-of-range vectors the libm sigmoid; both are within
+    a few f32 ulps of the exact logistic."""
+    rng = np.random.default_rng(4)
+    for n in (7, 15, 16, 23, 1000):
+        m = (rng.normal(size=n) * 6).astype(np.float32)
+        if n == 1000:
+            m[100] = 95.0  # one vector leaves the polynomial's range
+        y = (rng.random(n) < 0.5).astype(np.float32)
+        g = O.gradient(O.OBJ_LOGISTIC, m, y)
+        p = 1.0 / (1.0 + np.exp(-m.astype(np.float64)))
+        pf = (g[:, 0] + y).astype(np.float64)
+        ulp = np.spacing(p.astype(np.float32)).astype(np.float64)
+        assert np.all(np.abs(pf - p) <= 8 * ulp + 1e-7)
+        vec = n - n % 8 if n >= 16 else 0
+        tail = np.arange(vec, n)
+        for r in tail:
+            s = O.lib().or_sigmoid(float(m[r]))
+            assert np.float32(s - y[r]) == g[r, 0]
+        h = g[:, 1]
+        assert np.all(h >= np.float32(1e-16))
+
+
+def test_softmax_gradient_closed_form():
+    """objective/multiclass.rs:124-139: zero margins give p = 1/3, g = p - 1 on
+    the label, h = 2p(1-p)."""
+    g = O.gradient(O.OBJ_SOFTMAX, np.zeros(6, np.float32), np.array([0, 2], np.float32), num_class=3)
+    assert abs(g[0, 0, 0] - (1 / 3 - 1)) < 1e-6 and abs(g[0, 1, 0] - 1 / 3) < 1e-6
+    assert abs(g[1, 2, 0] - (1 / 3 - 1)) < 1e-6
+    assert abs(g[0, 0, 1] - 2 * (1 / 3) * (2 / 3)) < 1e-6
+
+
+def test_base_margins():
+    """classification.rs:276-339 and multiclass base margins: the logit of the
+    positive rate; centered log frequencies for softmax (uniform -> zeros)."""
+    p = O.params(objective=O.OBJ_LOGISTIC)
+    assert O.base_margins(np.array([1, 0], np.float32), p)[0] == 0.0
+    q = O.base_margins(np.array([1, 0, 0, 0], np.float32), p)[0]
+    assert abs(q - math.log(0.25 / 0.75)) < 1e-6
+    ps = O.params(objective=O.OBJ_SOFTMAX, num_class=3)
+    assert np.all(O.base_margins(np.array([0, 1, 2], np.float32), ps) == 0.0)
