@@ -1,0 +1,601 @@
+"""Python mirror of hessboost's hist training and prediction API on MI355X.
+
+``DMatrix``, ``train`` and ``Booster.predict`` keep the reference's names and
+argument meaning (python/python/hessboost/_training.py, _booster.py) for
+the `tree_method=hist` path; every computation runs in libhbrocm.so (cuts and
+binning on the host, growth and prediction on the GPU).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _capi as A
+
+
+# ---- cuts and the binned index ---------------------------------------------------
+
+class Cuts:
+    """HistCuts (src/data/quantile.rs:28-296): per-feature cut values."""
+
+    def __init__(self, handle):
+        self._h = handle
+
+    @classmethod
+    def from_dense(cls, x, max_bin=256, weights=None, missing=np.nan):
+        x = np.ascontiguousarray(x, np.float32)
+        w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+        h = C.c_void_p()
+        A.check(A.lib().hbr_cuts_from_dense(A.ptr(x), x.shape[0], x.shape[1], max_bin, A.ptr(w),
+                                            float(missing), C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_csr(cls, row_ptr, col, val, n_cols, max_bin=256, weights=None):
+        row_ptr = np.ascontiguousarray(row_ptr, np.uint64)
+        col = np.ascontiguousarray(col, np.uint32)
+        val = np.ascontiguousarray(val, np.float32)
+        w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+        h = C.c_void_p()
+        A.check(A.lib().hbr_cuts_from_csr(A.ptr(row_ptr), A.ptr(col), A.ptr(val), len(row_ptr) - 1, n_cols,
+                                          max_bin, A.ptr(w), C.byref(h)))
+        return cls(h)
+
+    def __del__(self):
+        try:
+            A.lib().hbr_cuts_free(self._h)
+        except Exception:
+            pass
+
+    def arrays(self):
+        n, total = C.c_uint64(), C.c_uint64()
+        A.check(A.lib().hbr_cuts_info(self._h, C.byref(n), C.byref(total)))
+        fo = np.empty(n.value + 1, np.uint32)
+        cv = np.empty(total.value, np.float32)
+        A.check(A.lib().hbr_cuts_copy(self._h, A.ptr(fo), A.ptr(cv)))
+        return fo, cv
+
+
+class BinnedIndex:
+    """GHistIndex (src/data/ghist.rs:195-257) built on the host."""
+
+    def __init__(self, cuts: Cuts, x=None, csr=None, n_cols=None, missing=np.nan):
+        self.cuts = cuts
+        h = C.c_void_p()
+        if csr is not None:
+            row_ptr = np.ascontiguousarray(csr[0], np.uint64)
+            col = np.ascontiguousarray(csr[1], np.uint32)
+            val = np.ascontiguousarray(csr[2], np.float32)
+            A.check(A.lib().hbr_index_from_csr(A.ptr(row_ptr), A.ptr(col), A.ptr(val), len(row_ptr) - 1, n_cols,
+                                               cuts._h, C.byref(h)))
+        else:
+            x = np.ascontiguousarray(x, np.float32)
+            A.check(A.lib().hbr_index_from_dense(A.ptr(x), x.shape[0], x.shape[1], float(missing), cuts._h,
+                                                 C.byref(h)))
+        self._h = h
+        self.desc = A.IndexDesc()
+        A.check(A.lib().hbr_index_describe(h, C.byref(self.desc)))
+
+    def __del__(self):
+        try:
+            A.lib().hbr_index_free(self._h)
+        except Exception:
+            pass
+
+    @property
+    def n_rows(self):
+        return self.desc.n_rows
+
+    @property
+    def n_cols(self):
+        return self.desc.n_cols
+
+    @property
+    def dense(self):
+        return bool(self.desc.dense)
+
+    def feature_offset(self):
+        return np.ctypeslib.as_array(self.desc.feature_offset, shape=(self.n_cols + 1,)).copy()
+
+    def cut_values(self):
+        fo = self.feature_offset()
+        return np.ctypeslib.as_array(self.desc.cut_values, shape=(int(fo[-1]),)).copy()
+
+    def row_bins(self):
+        d = self.desc
+        row_ptr = np.ctypeslib.as_array(d.row_ptr, shape=(d.n_rows + 1,)).copy()
+        nnz = int(row_ptr[-1])
+        dt = np.uint16 if d.row_bin_width == 2 else np.uint32
+        if nnz == 0:
+            return row_ptr, np.zeros(0, dt)
+        buf = (C.c_char * (nnz * d.row_bin_width)).from_address(d.row_bins)
+        return row_ptr, np.frombuffer(buf, dt).copy()
+
+    def columns(self):
+        d = self.desc
+        if d.col_bin_width == 0:
+            return None
+        dt = {1: np.uint8, 2: np.uint16, 4: np.uint32}[d.col_bin_width]
+        cells = d.n_rows * d.n_cols
+        buf = (C.c_char * (cells * d.col_bin_width)).from_address(d.col_bins)
+        cols = np.frombuffer(buf, dt).reshape(d.n_cols, d.n_rows).copy()
+        miss = None
+        if d.missing:
+            words = (d.n_rows + 63) // 64
+            miss = np.ctypeslib.as_array(d.missing, shape=(words * d.n_cols,)).copy()
+        return cols, miss
+
+
+# ---- the device engine (HistogramBackend + RowEngine) ----------------------------------
+
+class Engine:
+    """One binned index resident on one GPU (src/tree/hist/mod.rs:73-295)."""
+
+    def __init__(self, index: BinnedIndex, ordinal: int = 0):
+        self.index = index
+        h = C.c_void_p()
+        A.check(A.lib().hbr_engine_open(ordinal, C.byref(index.desc), C.byref(h)))
+        self._h = h
+        fo = index.feature_offset()
+        self.total_bins = int(fo[-1])
+
+    def close(self):
+        if getattr(self, "_h", None):
+            A.lib().hbr_engine_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prepare(self, gpair):
+        gpair = np.ascontiguousarray(gpair, np.float32).reshape(-1)
+        A.check(A.lib().hbr_prepare(self._h, A.ptr(gpair), len(gpair) // 2))
+
+    def build(self, rows):
+        rows = np.ascontiguousarray(rows, np.uint32)
+        out = np.empty(2 * self.total_bins, np.float64)
+        A.check(A.lib().hbr_build(self._h, A.ptr(rows), len(rows), A.ptr(out)))
+        return out.reshape(-1, 2)
+
+    def begin_tree(self):
+        seg = A.Segment()
+        A.check(A.lib().hbr_begin_tree(self._h, self.index.n_rows, C.byref(seg)))
+        return seg
+
+    def root_total(self, seg, fixed=False):
+        out = np.empty(2, np.float64)
+        fx = np.empty(2, np.int64)
+        A.check(A.lib().hbr_root_total_fixed(self._h, C.byref(seg), A.ptr(out), A.ptr(fx)))
+        return (out, fx) if fixed else out
+
+    def partition(self, splits):
+        """splits: [(segment, feature, below, default_left)] -> [(left, right)]."""
+        arr = (A.RowSplit * len(splits))()
+        for i, (seg, f, below, dl) in enumerate(splits):
+            arr[i].seg = seg
+            arr[i].feature = f
+            arr[i].below = below
+            arr[i].default_left = int(dl)
+        out = (A.Partitioned * len(splits))()
+        A.check(A.lib().hbr_partition(self._h, arr, len(splits), out))
+        return [(out[i].left, out[i].right) for i in range(len(splits))]
+
+    def histograms(self, segs):
+        arr = (A.Segment * len(segs))(*segs)
+        out = np.empty(len(segs) * 2 * self.total_bins, np.float64)
+        A.check(A.lib().hbr_histograms(self._h, arr, len(segs), A.ptr(out)))
+        return out.reshape(len(segs), -1, 2)
+
+    def rows(self, seg):
+        out = np.empty(seg.len, np.uint32)
+        A.check(A.lib().hbr_rows(self._h, C.byref(seg), A.ptr(out)))
+        return out
+
+    def load_margins(self, margins, n_outputs=1):
+        m = np.ascontiguousarray(margins, np.float32).reshape(-1)
+        A.check(A.lib().hbr_load_margins(self._h, A.ptr(m), len(m), n_outputs))
+
+    def gradients(self, kind, labels, weights=None, scale_pos_weight=1.0):
+        n = self.index.n_rows
+        loss = A.DeviceLoss(kind, scale_pos_weight, 1e-16, 80.0, n - n % 8 if n >= 16 else 0)
+        labels = np.ascontiguousarray(labels, np.float32)
+        w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+        ok = C.c_int()
+        A.check(A.lib().hbr_gradients(self._h, C.byref(loss), A.ptr(labels), A.ptr(w), n, C.byref(ok)))
+        return bool(ok.value)
+
+    def read_gradients(self):
+        out = np.empty(2 * self.index.n_rows, np.float32)
+        A.check(A.lib().hbr_read_gradients(self._h, A.ptr(out), self.index.n_rows))
+        return out.reshape(-1, 2)
+
+    def add_leaf_values(self, segs, values):
+        arr = (A.Segment * len(segs))(*segs)
+        v = np.ascontiguousarray(values, np.float32)
+        A.check(A.lib().hbr_add_leaf_values(self._h, arr, A.ptr(v), len(segs)))
+
+    def read_margins(self, n):
+        out = np.empty(n, np.float32)
+        A.check(A.lib().hbr_read_margins(self._h, A.ptr(out), n))
+        return out
+
+    def reserve_hists(self, slots):
+        fits = C.c_int()
+        A.check(A.lib().hbr_reserve_hists(self._h, slots, C.byref(fits)))
+        return bool(fits.value)
+
+    def build_resident(self, nodes, siblings=()):
+        segs = (A.Segment * max(1, len(nodes)))(*[s for s, _ in nodes])
+        slots = np.array([sl for _, sl in nodes], np.uint32)
+        par = np.array([p for p, _ in siblings], np.uint32)
+        blt = np.array([b for _, b in siblings], np.uint32)
+        A.check(A.lib().hbr_build_resident(self._h, segs, A.ptr(slots), len(nodes), A.ptr(par), A.ptr(blt),
+                                           len(siblings)))
+
+    def scan_resident(self, reg, requests):
+        """requests: dicts with slot, total (g, h), fixed (g, h) or None,
+        root_gain, lower, upper; every feature, no monotone directions."""
+        n_cols = self.index.n_cols
+        feats = np.arange(n_cols, dtype=np.uint32)
+        arr = (A.ScanRequest * len(requests))()
+        for i, r in enumerate(requests):
+            q = arr[i]
+            q.slot = r["slot"]
+            q.total_g, q.total_h = r["total"]
+            if r.get("fixed") is not None:
+                q.has_fixed = 1
+                q.fixed_g, q.fixed_h = (int(v) for v in r["fixed"])
+            q.root_gain = r["root_gain"]
+            q.lower = r.get("lower", -math.inf)
+            q.upper = r.get("upper", math.inf)
+            q.n_features = n_cols
+            q.features = A.typed(feats, C.c_uint32)
+        out = (A.NodeScan * len(requests))()
+        rp = A.RegParams(*reg)
+        A.check(A.lib().hbr_scan_resident(self._h, C.byref(rp), arr, len(requests), out))
+        return [out[i] for i in range(len(requests))]
+
+    def read_hist(self, slot):
+        out = np.empty(2 * self.total_bins, np.float64)
+        A.check(A.lib().hbr_read_hist(self._h, slot, A.ptr(out)))
+        return out.reshape(-1, 2)
+
+    def set_profiling(self, on=True, kernel_prefix=None):
+        """Time kernels (those whose name starts with kernel_prefix) with HIP
+        events on the engine's stream."""
+        A.check(A.lib().hbr_set_profiling(self._h, int(on), None if kernel_prefix is None else kernel_prefix.encode()))
+
+    def kernel_stats(self):
+        buf = C.create_string_buffer(1 << 16)
+        A.check(A.lib().hbr_kernel_stats(self._h, buf, len(buf)))
+        return A.kernel_stats(buf.value.decode())
+
+    def counters(self):
+        c = A.EngineCounters()
+        A.check(A.lib().hbr_engine_counters_read(self._h, C.byref(c)))
+        return {k: getattr(c, k) for k, _ in A.EngineCounters._fields_}
+
+
+# ---- data -------------------------------------------------------------------------------
+
+class DMatrix:
+    """Training or prediction data (python/python/hessboost/_core.py DMatrix):
+    a dense f32 matrix or CSR triplet, labels, optional weights, and the
+    missing-value marker (NaN by default)."""
+
+    def __init__(self, data, label=None, weight=None, missing=np.nan, n_cols=None):
+        if isinstance(data, tuple):
+            self.csr = (np.ascontiguousarray(data[0], np.uint64), np.ascontiguousarray(data[1], np.uint32),
+                        np.ascontiguousarray(data[2], np.float32))
+            self.x = None
+            self.n_rows = len(self.csr[0]) - 1
+            self.n_cols = int(n_cols)
+        else:
+            self.x = np.ascontiguousarray(data, np.float32)
+            self.csr = None
+            self.n_rows, self.n_cols = self.x.shape
+        self.label = None if label is None else np.ascontiguousarray(label, np.float32)
+        self.weight = None if weight is None else np.ascontiguousarray(weight, np.float32)
+        self.missing = missing
+        self._index = {}
+
+    def index(self, max_bin=256) -> BinnedIndex:
+        """The binned index for max_bin (DMatrix::hist_index, src/data/dmatrix.rs:931), cached."""
+        if max_bin not in self._index:
+            if self.csr is not None:
+                cuts = Cuts.from_csr(*self.csr, self.n_cols, max_bin=max_bin, weights=self.weight)
+                self._index[max_bin] = BinnedIndex(cuts, csr=self.csr, n_cols=self.n_cols)
+            else:
+                cuts = Cuts.from_dense(self.x, max_bin=max_bin, weights=self.weight, missing=self.missing)
+                self._index[max_bin] = BinnedIndex(cuts, x=self.x, missing=self.missing)
+        return self._index[max_bin]
+
+    def dense(self):
+        if self.x is not None:
+            return self.x
+        out = np.full((self.n_rows, self.n_cols), np.nan, np.float32)
+        rp, col, val = self.csr
+        for r in range(self.n_rows):
+            out[r, col[rp[r]:rp[r + 1]]] = val[rp[r]:rp[r + 1]]
+        return out
+
+
+# ---- training ---------------------------------------------------------------------------
+
+_OBJECTIVES = {"reg:squarederror": A.OBJ_SQUARED_ERROR, "binary:logistic": A.OBJ_LOGISTIC,
+               "reg:logistic": A.OBJ_LOGISTIC, "binary:logitraw": A.OBJ_LOGISTIC,
+               "multi:softprob": A.OBJ_SOFTMAX, "multi:softmax": A.OBJ_SOFTMAX}
+
+
+def _device_ordinal(device):
+    if device in ("rocm", "gpu", "cuda", None):
+        return 0
+    if isinstance(device, str) and ":" in device:
+        return int(device.split(":")[1])
+    raise ValueError(f"unsupported device {device!r}: this backend runs rocm[:N]")
+
+
+@dataclass
+class Booster:
+    """A trained model: scalar-leaf trees in the reference's Node layout
+    (src/tree/regtree.rs:38-66), intercepts and the objective."""
+    objective: str
+    base_score: np.ndarray
+    trees: list = field(default_factory=list)
+    n_outputs: int = 1
+    n_features: int = 0
+    tree_weights: np.ndarray | None = None
+    _forest: object = None
+    _forest_ordinal: int = -1
+
+    def num_trees(self):
+        return len(self.trees)
+
+    def forest_desc(self, trees=None):
+        trees = self.trees if trees is None else trees
+        k = self.n_outputs
+        off = np.zeros(len(trees) + 1, np.uint64)
+        cols = {key: [] for key in ("split_feature", "split_cond", "default_left", "left", "right", "leaf_value")}
+        for i, t in enumerate(trees):
+            for key in cols:
+                cols[key].append(np.asarray(t[key]))
+            off[i + 1] = off[i] + len(t["left"])
+        arrs = dict(tree_offset=off,
+                    split_feature=np.concatenate(cols["split_feature"]).astype(np.uint32),
+                    split_cond=np.concatenate(cols["split_cond"]).astype(np.float32),
+                    default_left=np.concatenate(cols["default_left"]).astype(np.uint8),
+                    left=np.concatenate(cols["left"]).astype(np.int32),
+                    right=np.concatenate(cols["right"]).astype(np.int32),
+                    leaf_value=np.concatenate(cols["leaf_value"]).astype(np.float32),
+                    tree_weight=(np.ones(len(trees), np.float32) if self.tree_weights is None
+                                 else np.asarray(self.tree_weights[:len(trees)], np.float32)),
+                    tree_output=np.array([t % k for t in range(len(trees))], np.uint32),
+                    base_score=np.asarray(self.base_score, np.float32))
+        return arrs
+
+    def forest(self, ordinal=0):
+        if self._forest is None or self._forest_ordinal != ordinal:
+            self._forest = Forest(self.forest_desc(), self.n_outputs, ordinal)
+            self._forest_ordinal = ordinal
+        return self._forest
+
+    def predict(self, data, *, output_margin=False, pred_leaf=False, missing=np.nan, device="rocm:0"):
+        x = data.dense() if isinstance(data, DMatrix) else np.ascontiguousarray(data, np.float32)
+        f = self.forest(_device_ordinal(device))
+        if pred_leaf:
+            return f.predict_leaf(x, missing)
+        m = f.predict_margin(x, missing)
+        m = m if self.n_outputs == 1 else m.reshape(-1, self.n_outputs)
+        if output_margin or self.objective in ("reg:squarederror", "binary:logitraw"):
+            return m
+        if self.objective in ("binary:logistic", "reg:logistic"):
+            # XGBoost's common::Sigmoid (simd/mod.rs:425-427) per value, in f32
+            t = np.minimum(-m, np.float32(88.7)).astype(np.float32)
+            return (np.float32(1.0) / (np.exp(t, dtype=np.float32) + np.float32(1.0))).astype(np.float32)
+        z = np.exp((m - m.max(axis=1, keepdims=True)).astype(np.float32))
+        return (z / z.sum(axis=1, keepdims=True)).astype(np.float32)
+
+    def save_model_json(self):
+        """The reference's JSON model document for scalar trees (model/serde.rs)."""
+        trees = []
+        for t in self.trees:
+            nodes = []
+            for i in range(len(t["left"])):
+                nodes.append(dict(split_feature=int(t["split_feature"][i]), split_cond=float(t["split_cond"][i]),
+                                  default_left=bool(t["default_left"][i]), left=int(t["left"][i]),
+                                  right=int(t["right"][i]), leaf_value=float(t["leaf_value"][i]),
+                                  sum_hess=float(t["sum_hess"][i]), split_gain=float(t["split_gain"][i]),
+                                  is_categorical=False, cat_begin=0, cat_end=0))
+            trees.append(dict(nodes=nodes, categories=[], size_leaf_vector=0, leaf_vectors=[], linear=None))
+        return json.dumps(dict(trees=trees, base_score=[float(b) for b in self.base_score],
+                               objective=self.objective, num_class=self.n_outputs if self.n_outputs > 1 else 0,
+                               n_outputs=self.n_outputs, n_targets=1, n_features=self.n_features,
+                               best_iteration=None, tree_weights=[1.0] * len(trees), num_parallel_tree=1))
+
+
+class Trainer:
+    """Device-resident boosting over an engine (src/training/round.rs:105-148)."""
+
+    def __init__(self, engine: Engine, params: dict, labels, weights=None):
+        p = A.TrainParams()
+        p.eta = params.get("eta", params.get("learning_rate", 0.3))
+        p.gamma = params.get("gamma", 0.0)
+        p.lambda_ = params.get("lambda", params.get("reg_lambda", 1.0))
+        p.alpha = params.get("alpha", params.get("reg_alpha", 0.0))
+        p.min_child_weight = params.get("min_child_weight", 1.0)
+        p.max_delta_step = params.get("max_delta_step", 0.0)
+        md = params.get("max_depth", 6)
+        p.max_depth = 0 if md is None else md
+        ml = params.get("max_leaves", 0)
+        p.max_leaves = 0 if ml is None else ml
+        p.grow_policy = A.GROW_LOSSGUIDE if params.get("grow_policy", "depthwise") == "lossguide" else A.GROW_DEPTHWISE
+        self.objective = params.get("objective", "reg:squarederror")
+        p.objective = _OBJECTIVES[self.objective]
+        p.num_class = params.get("num_class", 0)
+        p.scale_pos_weight = params.get("scale_pos_weight", 1.0)
+        mono = params.get("monotone_constraints")
+        self._mono = None
+        if mono:
+            self._mono = np.array(mono, np.int8)
+            p.monotone = A.typed(self._mono, C.c_int8)
+            p.n_monotone = len(mono)
+        if params.get("base_score") is not None:
+            p.base_score = params["base_score"]
+            p.has_base_score = 1
+        self.params = p
+        self.engine = engine
+        self.labels = np.ascontiguousarray(labels, np.float32)
+        self.weights = None if weights is None else np.ascontiguousarray(weights, np.float32)
+        h = C.c_void_p()
+        A.check(A.lib().hbr_trainer_create(engine._h, C.byref(p), A.ptr(self.labels), A.ptr(self.weights),
+                                           len(self.labels), C.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        try:
+            A.lib().hbr_trainer_free(self._h)
+        except Exception:
+            pass
+
+    def boost(self, rounds=1):
+        A.check(A.lib().hbr_trainer_boost(self._h, rounds))
+
+    @property
+    def n_outputs(self):
+        k = C.c_uint32()
+        A.check(A.lib().hbr_trainer_num_outputs(self._h, C.byref(k)))
+        return k.value
+
+    def base_score(self):
+        out = np.empty(self.n_outputs, np.float32)
+        A.check(A.lib().hbr_trainer_base_score(self._h, A.ptr(out)))
+        return out
+
+    def trees(self):
+        n = C.c_uint64()
+        A.check(A.lib().hbr_trainer_num_trees(self._h, C.byref(n)))
+        out = []
+        for t in range(n.value):
+            m = C.c_uint64()
+            A.check(A.lib().hbr_trainer_tree_size(self._h, t, C.byref(m)))
+            k = m.value
+            d = dict(split_feature=np.empty(k, np.uint32), split_cond=np.empty(k, np.float32),
+                     default_left=np.empty(k, np.uint8), left=np.empty(k, np.int32), right=np.empty(k, np.int32),
+                     leaf_value=np.empty(k, np.float32), sum_hess=np.empty(k, np.float32),
+                     split_gain=np.empty(k, np.float32), split_bin=np.empty(k, np.int64))
+            A.check(A.lib().hbr_trainer_tree(self._h, t, *[A.ptr(d[key]) for key in
+                                                           ("split_feature", "split_cond", "default_left", "left",
+                                                            "right", "leaf_value", "sum_hess", "split_gain",
+                                                            "split_bin")]))
+            out.append(d)
+        return out
+
+    def margins(self):
+        out = np.empty(len(self.labels) * self.n_outputs, np.float32)
+        A.check(A.lib().hbr_trainer_margins(self._h, A.ptr(out)))
+        return out
+
+    def booster(self, n_features):
+        return Booster(objective=self.objective, base_score=self.base_score(), trees=self.trees(),
+                       n_outputs=self.n_outputs, n_features=n_features)
+
+
+def train(params: dict, dtrain: DMatrix, num_boost_round: int = 10, *, device="rocm:0") -> Booster:
+    """hessboost.train for `tree_method=hist` on one MI355X
+    (src/training/api.rs:228-234)."""
+    if params.get("tree_method", "hist") not in ("hist", "auto"):
+        raise ValueError("this backend trains tree_method=hist")
+    index = dtrain.index(params.get("max_bin", 256))
+    engine = Engine(index, _device_ordinal(device))
+    t = Trainer(engine, params, dtrain.label, dtrain.weight)
+    t.boost(num_boost_round)
+    b = t.booster(dtrain.n_cols)
+    return b
+
+
+# ---- prediction -----------------------------------------------------------------------------
+
+class Forest:
+    """GpuModel (src/backend/cuda/predict.rs:401-520): a forest uploaded once."""
+
+    def __init__(self, arrs: dict, n_outputs: int = 1, ordinal: int = 0):
+        dtypes = dict(tree_offset=np.uint64, split_feature=np.uint32, split_cond=np.float32,
+                      default_left=np.uint8, left=np.int32, right=np.int32, leaf_value=np.float32,
+                      tree_weight=np.float32, tree_output=np.uint32, base_score=np.float32)
+        a = {k: np.ascontiguousarray(arrs[k], dt) for k, dt in dtypes.items()}
+        self.arrs = a
+        self.n_trees = len(a["tree_offset"]) - 1
+        self.n_outputs = n_outputs
+        fd = A.ForestDesc(self.n_trees, A.typed(a["tree_offset"], C.c_uint64),
+                          A.typed(a["split_feature"], C.c_uint32), A.typed(a["split_cond"], C.c_float),
+                          A.typed(a["default_left"], C.c_uint8), A.typed(a["left"], C.c_int32),
+                          A.typed(a["right"], C.c_int32), A.typed(a["leaf_value"], C.c_float),
+                          A.typed(a["tree_weight"], C.c_float), A.typed(a["tree_output"], C.c_uint32),
+                          n_outputs, 0, A.typed(a["base_score"], C.c_float))
+        h = C.c_void_p()
+        A.check(A.lib().hbr_forest_upload(ordinal, C.byref(fd), C.byref(h)))
+        self._h = h
+        self.ordinal = ordinal
+
+    def __del__(self):
+        try:
+            A.lib().hbr_forest_free(self._h)
+        except Exception:
+            pass
+
+    def predict_margin(self, x, missing=np.nan):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape[0] * self.n_outputs, np.float32)
+        A.check(A.lib().hbr_predict_margin(self._h, A.ptr(x), x.shape[0], x.shape[1], float(missing), A.ptr(out)))
+        return out
+
+    def predict_leaf(self, x, missing=np.nan):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape[0] * self.n_trees, np.int32)
+        A.check(A.lib().hbr_predict_leaf(self._h, A.ptr(x), x.shape[0], x.shape[1], float(missing), A.ptr(out)))
+        return out.reshape(x.shape[0], self.n_trees)
+
+    def predict_margin_device(self, d_x, n_rows, n_cols, d_out, d_leaf=None, missing=np.nan):
+        A.check(A.lib().hbr_predict_margin_device(self._h, C.c_void_p(d_x), n_rows, n_cols, float(missing),
+                                                  C.c_void_p(d_out), None if d_leaf is None else C.c_void_p(d_leaf)))
+
+    def set_profiling(self, on=True, kernel_prefix=None):
+        A.check(A.lib().hbr_forest_set_profiling(self._h, int(on),
+                                                  None if kernel_prefix is None else kernel_prefix.encode()))
+
+    def kernel_stats(self):
+        buf = C.create_string_buffer(1 << 16)
+        A.check(A.lib().hbr_forest_kernel_stats(self._h, buf, len(buf)))
+        return A.kernel_stats(buf.value.decode())
+
+
+class DeviceBuffer:
+    """Device memory held by the library (inputs kept resident in HBM)."""
+
+    def __init__(self, nbytes, ordinal=0):
+        p = C.c_void_p()
+        A.check(A.lib().hbr_device_alloc(ordinal, nbytes, C.byref(p)))
+        self.ptr, self.nbytes, self.ordinal = p.value, nbytes, ordinal
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        A.check(A.lib().hbr_device_upload(self.ordinal, C.c_void_p(self.ptr), A.ptr(arr), arr.nbytes))
+
+    def download(self, dtype, count):
+        out = np.empty(count, dtype)
+        A.check(A.lib().hbr_device_download(self.ordinal, A.ptr(out), C.c_void_p(self.ptr), out.nbytes))
+        return out
+
+    def __del__(self):
+        try:
+            A.lib().hbr_device_free(self.ordinal, C.c_void_p(self.ptr))
+        except Exception:
+            pass

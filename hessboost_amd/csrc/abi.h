@@ -1,0 +1,292 @@
+// Kernel argument records shared by the HIP kernels and the host runtime.
+//
+// Every kernel takes exactly one of these structs by value; the host launches
+// it through hipModuleLaunchKernel with a single kernel parameter. Plain C
+// layout, fixed-width fields, device pointers as typed pointers (64-bit on
+// both sides).
+#pragma once
+#include <stdint.h>
+
+namespace hbr {
+
+// Rows per partition tile (one workgroup).
+constexpr uint32_t kPartTile = 2048;
+constexpr uint32_t kPartThreads = 256;
+// Rows per histogram tile of one workgroup.
+constexpr uint32_t kHistTile = 8192;
+constexpr uint32_t kHistThreads = 512;
+// Bins of one feature the split scan processes per pass (4 per lane).
+constexpr uint32_t kScanChunk = 256;
+// Threads of the elementwise kernels.
+constexpr uint32_t kThreads = 256;
+
+// One row's gradient and Hessian (GradPair, objective/mod.rs:92-97).
+struct GPair {
+    float g;
+    float h;
+};
+
+// Fixed-point histogram bin: the exact integer sums of the quantized
+// gradients and Hessians of the rows in the bin.
+struct QBin {
+    int64_t g;
+    int64_t h;
+};
+
+// Per-tree quantization: x is stored as rint(x * 2^-exp), exp chosen so that
+// no sum over the tree's rows can exceed 2^62 in magnitude.
+struct QScale {
+    int32_t exp_g;
+    int32_t exp_h;
+    uint32_t max_g_bits;  // |g| maximum as f32 bits (non-negative floats order as ints)
+    uint32_t max_h_bits;
+    uint32_t nonfinite;   // count of rows with a non-finite g or h
+    uint32_t scalar_rows; // logistic rows the vector kernel could not reproduce
+    uint32_t pad[2];
+};
+
+// A node's rows: `len` row ids at `offset` of row buffer `buf` (0 or 1).
+struct Seg {
+    uint32_t offset;
+    uint32_t len;
+    uint32_t buf;
+    uint32_t pad;
+};
+
+// ---- index ---------------------------------------------------------------------
+// Dense re-encode: a chunk of rows' global bins (row-major, n_cols per row)
+// to feature-local u8 bins, row-major (stride bytes per row) and feature-major.
+struct EncodeArgs {
+    const uint16_t *g16;      // chunk's global bins (u16), or null
+    const uint32_t *g32;      // or u32
+    const uint32_t *feature_offset;
+    uint8_t *rows8;
+    uint8_t *cols8;
+    uint64_t n_rows;          // whole index
+    uint64_t row0;            // first row of the chunk
+    uint32_t chunk_rows;
+    uint32_t n_cols;
+    uint32_t stride;
+    uint32_t pad;
+};
+
+// ---- gradients ---------------------------------------------------------------
+enum LossKind : uint32_t { kSquaredError = 0, kLogistic = 1 };
+
+struct GradArgs {
+    const float *margins;   // n (one output)
+    const float *labels;    // n
+    const float *weights;   // n or null
+    GPair *gpair;           // n
+    QScale *scale;          // max folds (atomics) land here
+    uint32_t *scalar_list;  // rows needing the host's scalar path
+    uint32_t n;
+    uint32_t vec_rows;      // logistic: rows covered by 8-row vectors
+    uint32_t loss;
+    float scale_pos_weight;
+    float min_hess;
+    float max_input;        // logistic vector range (80)
+};
+
+// ---- row buffers -------------------------------------------------------------
+struct IotaArgs {
+    uint32_t *rows;
+    uint32_t first;
+    uint32_t n;
+};
+
+// ---- root totals -------------------------------------------------------------
+struct TotalArgs {
+    const uint32_t *rows;   // null: contiguous from `first`
+    uint32_t first;
+    uint32_t n;
+    const GPair *gpair;
+    const QScale *scale;
+    QBin *out;              // accumulated with 64-bit atomics (zeroed before)
+};
+
+// ---- partition -----------------------------------------------------------------
+// One node to partition: its segment, the split's routing and where its
+// children's statistics go.
+struct PartSplit {
+    Seg seg;                // parent rows (source buffer seg.buf)
+    uint32_t feature;
+    uint32_t limit;         // present local bins < limit go left
+    uint32_t default_left;
+    uint32_t tile_begin;    // first partition tile of this split
+    uint32_t fresh_slot;    // histogram slot for the built child
+    uint32_t parent_slot;   // parent's slot, becomes the sibling's
+    uint32_t pad[2];
+};
+
+// Device decision per split after the scan of tile counts.
+struct PartOut {
+    uint32_t left_len;
+    uint32_t built_left;    // 1: the left child is the smaller (built) one
+    uint32_t pad[2];
+};
+
+struct PartArgs {
+    const PartSplit *splits;
+    uint32_t n_splits;
+    uint32_t n_tiles;
+    const uint32_t *tile_split;  // tile -> split
+    uint32_t *tile_left;         // per tile left count (count pass) / left offset (after scan)
+    PartOut *out;
+    const uint32_t *src_rows[2];
+    uint32_t *dst_rows[2];
+    // routing data
+    uint32_t dense;              // dense columns present
+    const uint8_t *cols8;        // feature-major local bins [f][n] (u8)
+    const uint16_t *cols16;      // or u16
+    const uint64_t *missing;     // feature-major bitmap (ceil(n/64) words per feature) or null
+    const uint64_t *row_ptr;     // CSR (no columns)
+    const uint32_t *gbins;       // CSR global bins
+    const uint32_t *feature_offset;
+    uint32_t n_rows;
+    uint32_t words;              // bitmap words per feature
+};
+
+// ---- histograms ----------------------------------------------------------------
+// A histogram tile: rows [row0, row0 + tile) of a node, features [f0, f0+nf).
+struct HistTile {
+    uint32_t node;      // index into the node table
+    uint32_t row0;
+    uint32_t f0;
+    uint32_t nf;
+};
+
+// One node whose histogram is built into `slot`. When `from_split` is set,
+// the node is the smaller child of split `split` and its segment comes from
+// the partition's device output.
+struct HistNode {
+    Seg seg;
+    uint32_t slot;
+    uint32_t from_split;
+    uint32_t split;
+    uint32_t contiguous; // rows are seg.offset .. seg.offset+len (no row buffer)
+};
+
+struct HistArgs {
+    const HistNode *nodes;
+    const HistTile *tiles;
+    const PartSplit *splits;
+    const PartOut *part_out;
+    const uint32_t *rows[2];
+    const GPair *gpair;
+    const QScale *scale;
+    const uint8_t *bins8;       // dense row-major local bins [n][stride]
+    const uint16_t *bins16;
+    uint32_t stride;            // bytes (u8) or elements (u16) per row
+    const uint64_t *row_ptr;    // CSR
+    const uint32_t *gbins;
+    const uint32_t *feature_offset;
+    QBin *hist;                 // slots * total_bins
+    uint32_t total_bins;
+    uint32_t tile_rows;
+};
+
+// sibling = parent - built, in place in the parent's slot, for each split.
+struct SubArgs {
+    const PartSplit *splits;
+    uint32_t n_splits;
+    QBin *hist;
+    uint32_t total_bins;
+};
+
+struct ZeroArgs {
+    QBin *hist;
+    const uint32_t *slots;
+    uint32_t n_slots;
+    uint32_t total_bins;
+};
+
+// ---- split scan ------------------------------------------------------------------
+struct ScanNode {
+    uint32_t slot;           // histogram slot (ignored when from_split)
+    uint32_t from_split;     // slot decided by the partition: child `child` of split `split`
+    uint32_t split;
+    uint32_t child;          // 0 left, 1 right
+    QBin total;              // node statistics (fixed point)
+    float root_gain;
+    float lower, upper;
+    uint32_t pad;
+};
+
+struct ScanParams {
+    double lambda, alpha, max_delta_step, min_child_weight;
+};
+
+// Best candidate of one feature (or of one node after the merge).
+struct ScanBest {
+    float loss;              // -inf: none
+    uint32_t feature;
+    uint32_t index;          // candidate order within the feature
+    uint32_t flags;          // bit0 backward, bit1 NaN seen
+    QBin left;
+    QBin right;
+};
+
+struct ScanArgs {
+    const ScanNode *nodes;
+    uint32_t n_nodes;
+    uint32_t n_features;
+    const PartSplit *splits;
+    const PartOut *part_out;
+    const QBin *hist;
+    uint32_t total_bins;
+    const uint32_t *feature_offset;
+    const int8_t *monotone;  // per feature or null
+    const QScale *scale;
+    ScanParams reg;
+    uint32_t dense;          // index without missing values: forward pass only
+    ScanBest *per_feature;   // n_nodes * n_features
+    ScanBest *best;          // n_nodes
+};
+
+// ---- leaves -----------------------------------------------------------------------
+struct LeafSeg {
+    Seg seg;
+    float value;
+    uint32_t pad[3];
+};
+
+struct LeafArgs {
+    const LeafSeg *leaves;
+    const uint32_t *tile_leaf;   // tile -> leaf
+    const uint32_t *tile_row0;
+    const uint32_t *rows[2];
+    float *margins;
+    uint32_t stride;             // outputs per row
+    uint32_t output;
+    uint32_t tile_rows;
+    uint32_t n_tiles;
+};
+
+// ---- prediction ---------------------------------------------------------------------
+// Forest nodes are structure-of-arrays: value (threshold or leaf value bits),
+// meta (feature | default_left << 30 | leaf << 31), left child (absolute
+// index; the right child is left + 1, as the reference's trees allocate them).
+struct PredictArgs {
+    const uint32_t *node_value;   // f32 bits
+    const uint32_t *node_meta;    // feature | default_left<<30 | leaf<<31
+    const uint32_t *node_left;    // left child (absolute), right = left + 1
+    const int32_t *node_orig;     // the node's id in its tree as the caller numbered it
+    const uint32_t *tree_root;    // n_trees
+    const float *tree_weight;
+    const uint32_t *tree_output;
+    const float *base_score;
+    const float *x;               // n x n_cols row-major
+    float *out;                   // n x n_outputs
+    int32_t *leaf_out;            // n x n_trees or null
+    uint32_t n;
+    uint32_t n_cols;
+    uint32_t n_trees;
+    uint32_t n_outputs;
+    float missing;
+    uint32_t missing_is_nan;
+    uint32_t trees_per_chunk;
+    uint32_t pad;
+};
+
+}  // namespace hbr

@@ -1,0 +1,628 @@
+// The extern "C" boundary (include/hessboost_rocm.h): argument checks,
+// status codes, per-handle locking and the sticky failure flag.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "cuts.h"
+#include "engine.h"
+#include "forest.h"
+#include "hessboost_rocm.h"
+#include "trainer.h"
+
+using namespace hbr;
+
+struct hbr_cuts {
+    Cuts c;
+};
+struct hbr_index {
+    Index ix;
+};
+struct hbr_engine {
+    std::unique_ptr<Engine> e;
+};
+struct hbr_trainer {
+    hbr_engine *engine;
+    std::unique_ptr<Trainer> t;
+};
+struct hbr_forest {
+    std::unique_ptr<Forest> f;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int set_error(int status, const std::string &msg) {
+    g_error = msg;
+    return status;
+}
+
+template <typename F>
+int guard(F &&fn) {
+    try {
+        g_error.clear();
+        fn();
+        return HBR_OK;
+    } catch (const Error &e) {
+        return set_error(e.status, e.what());
+    } catch (const std::bad_alloc &) {
+        return set_error(HBR_REFUSED, "host allocation failed");
+    } catch (const std::exception &e) {
+        return set_error(HBR_INVALID, e.what());
+    }
+}
+
+// Run fn under the engine's lock; a device error poisons the engine.
+template <typename F>
+int with_engine(hbr_engine *h, F &&fn) {
+    if (!h || !h->e) return set_error(HBR_INVALID, "null engine");
+    Engine &e = *h->e;
+    std::lock_guard<std::mutex> lock(e.mu);
+    if (e.failed) return set_error(HBR_DEVICE_ERROR, "the engine failed earlier; every call is refused");
+    int st = guard([&] {
+        e.dev().activate();
+        fn(e);
+    });
+    if (st == HBR_DEVICE_ERROR) e.failed = true;
+    return st;
+}
+
+template <typename F>
+int with_forest(hbr_forest *h, F &&fn) {
+    if (!h || !h->f) return set_error(HBR_INVALID, "null forest");
+    Forest &f = *h->f;
+    std::lock_guard<std::mutex> lock(f.mu);
+    if (f.failed) return set_error(HBR_DEVICE_ERROR, "the forest's device failed earlier");
+    int st = guard([&] {
+        f.dev().activate();
+        fn(f);
+    });
+    if (st == HBR_DEVICE_ERROR) f.failed = true;
+    return st;
+}
+
+Segment seg_of(const Engine &e, const hbr_segment &s) {
+    if (s.tree != e.tree()) fail(kRefused, "segment of an earlier tree");
+    if (s.buffer > 1 || s.offset + s.len > e.n_rows()) fail(kInvalid, "segment outside the row buffers");
+    return Segment{(uint32_t)s.offset, (uint32_t)s.len, s.buffer};
+}
+
+hbr_segment seg_out(const Engine &e, const Segment &s) {
+    hbr_segment o{};
+    o.offset = s.offset;
+    o.len = s.len;
+    o.buffer = s.buf;
+    o.contiguous = 0;
+    o.tree = e.tree();
+    return o;
+}
+
+void dequant_hist(const Engine &e, const std::vector<QBin> &q, double *out) {
+    const int eg = e.scale().exp_g, eh = e.scale().exp_h;
+    for (size_t b = 0; b < q.size(); b++) {
+        out[2 * b] = std::ldexp((double)q[b].g, eg);
+        out[2 * b + 1] = std::ldexp((double)q[b].h, eh);
+    }
+}
+
+std::string stats_string(Device &d) {
+    std::string s;
+    for (auto &kv : d.kernel_stats()) {
+        char buf[160];
+        std::snprintf(buf, sizeof buf, "%s=%.6f,%llu;", kv.first.c_str(), kv.second.total_ms,
+                      (unsigned long long)kv.second.launches);
+        s += buf;
+    }
+    return s;
+}
+
+size_t copy_string(const std::string &s, char *buf, size_t len) {
+    if (buf && len) {
+        const size_t n = std::min(len - 1, s.size());
+        std::memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+    return s.size();
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t hbr_last_error(char *buf, size_t len) { return copy_string(g_error, buf, len); }
+
+int hbr_device_count(int *count) {
+    return guard([&] {
+        if (!count) fail(kInvalid, "null count");
+        *count = device_count();
+    });
+}
+
+// ---- cuts and index -----------------------------------------------------------
+
+int hbr_cuts_from_dense(const float *x, uint64_t n, uint64_t f, uint32_t max_bin, const float *weights,
+                        float missing, hbr_cuts **out) {
+    return guard([&] {
+        if (!out || (!x && n > 0 && f > 0) || max_bin < 2) fail(kInvalid, "cuts: bad arguments");
+        *out = new hbr_cuts{cuts_from_dense(x, n, f, max_bin, weights, missing)};
+    });
+}
+
+int hbr_cuts_from_csr(const uint64_t *row_ptr, const uint32_t *col, const float *val, uint64_t n, uint64_t f,
+                      uint32_t max_bin, const float *weights, hbr_cuts **out) {
+    return guard([&] {
+        if (!out || !row_ptr || max_bin < 2) fail(kInvalid, "cuts: bad arguments");
+        for (uint64_t e = 0; e < row_ptr[n]; e++)
+            if (col[e] >= f) fail(kInvalid, "cuts: column index beyond n_cols");
+        *out = new hbr_cuts{cuts_from_csr(row_ptr, col, val, n, f, max_bin, weights)};
+    });
+}
+
+int hbr_cuts_from_values(const uint32_t *fo, const float *values, uint64_t n_cols, hbr_cuts **out) {
+    return guard([&] {
+        if (!out || !fo || !values) fail(kInvalid, "cuts: bad arguments");
+        hbr_cuts *c = new hbr_cuts;
+        c->c.feature_offset.assign(fo, fo + n_cols + 1);
+        for (uint64_t f = 0; f < n_cols; f++)
+            if (fo[f + 1] <= fo[f]) {
+                delete c;
+                fail(kInvalid, "cuts: every feature owns at least one bin");
+            }
+        c->c.values.assign(values, values + fo[n_cols]);
+        *out = c;
+    });
+}
+
+int hbr_cuts_info(const hbr_cuts *c, uint64_t *n_cols, uint64_t *total_bins) {
+    return guard([&] {
+        if (!c) fail(kInvalid, "null cuts");
+        if (n_cols) *n_cols = c->c.n_cols();
+        if (total_bins) *total_bins = c->c.total_bins();
+    });
+}
+
+int hbr_cuts_copy(const hbr_cuts *c, uint32_t *fo, float *values) {
+    return guard([&] {
+        if (!c) fail(kInvalid, "null cuts");
+        if (fo) std::memcpy(fo, c->c.feature_offset.data(), c->c.feature_offset.size() * 4);
+        if (values) std::memcpy(values, c->c.values.data(), c->c.values.size() * 4);
+    });
+}
+
+void hbr_cuts_free(hbr_cuts *c) { delete c; }
+
+int hbr_index_from_dense(const float *x, uint64_t n, uint64_t f, float missing, const hbr_cuts *cuts,
+                         hbr_index **out) {
+    return guard([&] {
+        if (!out || !cuts || cuts->c.n_cols() != f) fail(kInvalid, "index: cuts do not match the matrix");
+        *out = new hbr_index{index_from_dense(x, n, f, missing, cuts->c)};
+    });
+}
+
+int hbr_index_from_csr(const uint64_t *row_ptr, const uint32_t *col, const float *val, uint64_t n, uint64_t f,
+                       const hbr_cuts *cuts, hbr_index **out) {
+    return guard([&] {
+        if (!out || !cuts || cuts->c.n_cols() != f) fail(kInvalid, "index: cuts do not match the matrix");
+        *out = new hbr_index{index_from_csr(row_ptr, col, val, n, f, cuts->c)};
+    });
+}
+
+void hbr_index_free(hbr_index *ix) { delete ix; }
+
+int hbr_index_describe(const hbr_index *h, hbr_index_desc *d) {
+    return guard([&] {
+        if (!h || !d) fail(kInvalid, "null index");
+        const Index &ix = h->ix;
+        *d = hbr_index_desc{};
+        d->n_rows = ix.n_rows;
+        d->n_cols = ix.n_cols;
+        d->feature_offset = ix.cuts.feature_offset.data();
+        d->cut_values = ix.cuts.values.data();
+        d->row_ptr = ix.row_ptr.data();
+        d->row_bin_width = ix.row_width;
+        d->row_bins = ix.row_width == 2 ? (const void *)ix.rows16.data() : (const void *)ix.rows32.data();
+        d->dense = ix.dense ? 1u : 0u;
+        d->col_bin_width = ix.col_width;
+        d->col_bins = ix.col_width == 1   ? (const void *)ix.cols8.data()
+                      : ix.col_width == 2 ? (const void *)ix.cols16.data()
+                      : ix.col_width == 4 ? (const void *)ix.cols32.data()
+                                          : nullptr;
+        d->missing = ix.missing.empty() ? nullptr : ix.missing.data();
+    });
+}
+
+// ---- engine -----------------------------------------------------------------------
+
+int hbr_engine_open(int ordinal, const hbr_index_desc *index, hbr_engine **out) {
+    return guard([&] {
+        if (!index || !out) fail(kInvalid, "engine: null argument");
+        auto *h = new hbr_engine;
+        try {
+            h->e = std::make_unique<Engine>(ordinal, *index);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+void hbr_engine_close(hbr_engine *e) { delete e; }
+
+int hbr_prepare(hbr_engine *h, const float *gpair, uint64_t n) {
+    return with_engine(h, [&](Engine &e) { e.prepare(gpair, n); });
+}
+
+int hbr_build(hbr_engine *h, const uint32_t *rows, uint64_t m, double *out) {
+    return with_engine(h, [&](Engine &e) {
+        if (!out || (!rows && m)) fail(kInvalid, "build: null argument");
+        dequant_hist(e, e.build_rows(rows, m), out);
+    });
+}
+
+int hbr_begin_tree(hbr_engine *h, uint64_t n_rows, hbr_segment *root) {
+    return with_engine(h, [&](Engine &e) {
+        if (n_rows != e.n_rows()) fail(kRefused, "begin_tree: only an unsampled tree over every row");
+        e.begin_tree();
+        *root = seg_out(e, Segment{0, (uint32_t)n_rows, 0});
+        root->contiguous = 1;
+    });
+}
+
+int hbr_root_total_fixed(hbr_engine *h, const hbr_segment *seg, double out[2], int64_t fixed[2]) {
+    return with_engine(h, [&](Engine &e) {
+        const QBin t = e.root_total(seg_of(e, *seg));
+        out[0] = std::ldexp((double)t.g, e.scale().exp_g);
+        out[1] = std::ldexp((double)t.h, e.scale().exp_h);
+        if (fixed) {
+            fixed[0] = t.g;
+            fixed[1] = t.h;
+        }
+    });
+}
+
+int hbr_root_total(hbr_engine *h, const hbr_segment *seg, double out[2]) {
+    return hbr_root_total_fixed(h, seg, out, nullptr);
+}
+
+int hbr_partition(hbr_engine *h, const hbr_row_split *splits, uint64_t n, hbr_partitioned *out) {
+    return with_engine(h, [&](Engine &e) {
+        std::vector<LevelSplit> ls(n);
+        for (uint64_t i = 0; i < n; i++) {
+            ls[i].seg = seg_of(e, splits[i].seg);
+            if (splits[i].feature >= e.n_cols()) fail(kInvalid, "partition: feature beyond the index");
+            ls[i].feature = splits[i].feature;
+            ls[i].limit = splits[i].below;
+            ls[i].default_left = splits[i].default_left ? 1u : 0u;
+        }
+        auto kids = e.level(ls, true);
+        for (uint64_t i = 0; i < n; i++) {
+            out[i].left = seg_out(e, kids[2 * i].seg);
+            out[i].right = seg_out(e, kids[2 * i + 1].seg);
+        }
+    });
+}
+
+int hbr_histograms(hbr_engine *h, const hbr_segment *segs, uint64_t n, double *out) {
+    return with_engine(h, [&](Engine &e) {
+        std::vector<Segment> ss;
+        std::vector<uint32_t> slots;
+        for (uint64_t i = 0; i < n; i++) {
+            ss.push_back(seg_of(e, segs[i]));
+            slots.push_back(e.alloc_slot());
+        }
+        e.build_nodes(ss, slots);
+        for (uint64_t i = 0; i < n; i++) {
+            dequant_hist(e, e.read_slot(slots[i]), out + i * 2 * (uint64_t)e.total_bins());
+            e.free_slot(slots[i]);
+        }
+    });
+}
+
+int hbr_rows(hbr_engine *h, const hbr_segment *seg, uint32_t *out) {
+    return with_engine(h, [&](Engine &e) {
+        auto r = e.rows_of(seg_of(e, *seg));
+        std::memcpy(out, r.data(), r.size() * 4);
+    });
+}
+
+int hbr_load_margins(hbr_engine *h, const float *m, uint64_t n, uint32_t k) {
+    return with_engine(h, [&](Engine &e) { e.load_margins(m, n, k ? k : 1); });
+}
+
+int hbr_gradients(hbr_engine *h, const hbr_device_loss *loss, const float *labels, const float *weights,
+                  uint64_t n, int *all_finite) {
+    return with_engine(h, [&](Engine &e) {
+        if (!loss || !labels) fail(kInvalid, "gradients: null argument");
+        if (!e.labels_loaded()) e.set_labels(labels, weights, n);
+        const bool ok = e.compute_gradients(*loss, 0);
+        if (all_finite) *all_finite = ok ? 1 : 0;
+    });
+}
+
+int hbr_read_gradients(hbr_engine *h, float *out, uint64_t n) {
+    return with_engine(h, [&](Engine &e) {
+        if (!out) fail(kInvalid, "read_gradients: null output");
+        e.read_gradients(out, n);
+    });
+}
+
+int hbr_add_leaf_values(hbr_engine *h, const hbr_segment *segs, const float *values, uint64_t n) {
+    return with_engine(h, [&](Engine &e) {
+        std::vector<Segment> ss;
+        for (uint64_t i = 0; i < n; i++) ss.push_back(seg_of(e, segs[i]));
+        e.add_leaves(ss, std::vector<float>(values, values + n), 0);
+    });
+}
+
+int hbr_read_margins(hbr_engine *h, float *out, uint64_t n) {
+    return with_engine(h, [&](Engine &e) { e.read_margins(out, n); });
+}
+
+int hbr_reserve_hists(hbr_engine *h, uint64_t slots, int *fits) {
+    return with_engine(h, [&](Engine &e) { *fits = e.reserve_slots(slots) ? 1 : 0; });
+}
+
+int hbr_build_resident(hbr_engine *h, const hbr_segment *segs, const uint32_t *slots, uint64_t n,
+                       const uint32_t *sib_parent, const uint32_t *sib_built, uint64_t n_sib) {
+    return with_engine(h, [&](Engine &e) {
+        std::vector<Segment> ss;
+        for (uint64_t i = 0; i < n; i++) ss.push_back(seg_of(e, segs[i]));
+        e.build_nodes(ss, std::vector<uint32_t>(slots, slots + n));
+        e.subtract(std::vector<uint32_t>(sib_parent, sib_parent + n_sib),
+                   std::vector<uint32_t>(sib_built, sib_built + n_sib));
+        e.dev().sync();
+    });
+}
+
+int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_request *req, uint64_t n,
+                      hbr_node_scan *out) {
+    return with_engine(h, [&](Engine &e) {
+        if (!reg || (!req && n)) fail(kInvalid, "scan: null argument");
+        std::vector<int8_t> dirs;
+        if (n && req[0].directions) {
+            dirs.assign(e.n_cols(), 0);
+            for (uint32_t i = 0; i < req[0].n_features; i++)
+                if (req[0].features[i] < e.n_cols()) dirs[req[0].features[i]] = req[0].directions[i];
+        }
+        e.set_scan_params(ScanParams{reg->lambda, reg->alpha, reg->max_delta_step, reg->min_child_weight}, dirs);
+        std::vector<ScanInput> in(n);
+        for (uint64_t i = 0; i < n; i++) {
+            if (req[i].n_features != e.n_cols()) fail(kRefused, "scan: a feature subset (column sampling)");
+            QBin t;
+            if (req[i].has_fixed) {
+                t = QBin{req[i].fixed_g, req[i].fixed_h};
+            } else {
+                t = QBin{(int64_t)std::llrint(std::ldexp(req[i].total_g, -e.scale().exp_g)),
+                         (int64_t)std::llrint(std::ldexp(req[i].total_h, -e.scale().exp_h))};
+            }
+            in[i] = ScanInput{req[i].slot, t, req[i].root_gain, req[i].lower, req[i].upper};
+        }
+        auto best = e.scan(in);
+        const auto &fo = e.feature_offset();
+        for (uint64_t i = 0; i < n; i++) {
+            hbr_node_scan o{};
+            const ScanBest &b = best[i];
+            if (b.index == 0xffffffffu) {
+                o.kind = HBR_SCAN_EMPTY;
+                out[i] = o;
+                continue;
+            }
+            const uint32_t nb = fo[b.feature + 1] - fo[b.feature];
+            o.kind = HBR_SCAN_NUMERIC;
+            o.feature = b.feature;
+            o.loss_chg = b.loss;
+            o.backward = b.index >= nb ? 1u : 0u;
+            o.offset = o.backward ? nb - 1 - (b.index - nb) : b.index;
+            const int eg = e.scale().exp_g, eh = e.scale().exp_h;
+            o.left_g = std::ldexp((double)b.left.g, eg);
+            o.left_h = std::ldexp((double)b.left.h, eh);
+            o.right_g = std::ldexp((double)b.right.g, eg);
+            o.right_h = std::ldexp((double)b.right.h, eh);
+            o.acc_g = o.backward ? o.right_g : o.left_g;
+            o.acc_h = o.backward ? o.right_h : o.left_h;
+            o.fixed_left_g = b.left.g;
+            o.fixed_left_h = b.left.h;
+            o.fixed_right_g = b.right.g;
+            o.fixed_right_h = b.right.h;
+            out[i] = o;
+        }
+    });
+}
+
+int hbr_read_hist(hbr_engine *h, uint32_t slot, double *out) {
+    return with_engine(h, [&](Engine &e) { dequant_hist(e, e.read_slot(slot), out); });
+}
+
+int hbr_engine_counters_read(hbr_engine *h, hbr_engine_counters *out) {
+    return with_engine(h, [&](Engine &e) {
+        if (!out) fail(kInvalid, "counters: null output");
+        *out = e.counters;
+    });
+}
+
+int hbr_set_profiling(hbr_engine *h, int on, const char *prefix) {
+    return with_engine(h, [&](Engine &e) { e.dev().set_profiling(on != 0, prefix ? prefix : ""); });
+}
+
+int hbr_kernel_stats(hbr_engine *h, char *buf, size_t len) {
+    return with_engine(h, [&](Engine &e) { copy_string(stats_string(e.dev()), buf, len); });
+}
+
+// ---- training ------------------------------------------------------------------------
+
+int hbr_trainer_create(hbr_engine *h, const hbr_train_params *p, const float *labels, const float *weights,
+                       uint64_t n, hbr_trainer **out) {
+    return with_engine(h, [&](Engine &e) {
+        if (!p || !labels || !out) fail(kInvalid, "trainer: null argument");
+        TrainParams tp;
+        tp.grow.reg = reg_from(p->lambda, p->alpha, p->max_delta_step, p->min_child_weight);
+        tp.grow.gamma = p->gamma;
+        tp.grow.max_depth = p->max_depth > 0 ? (uint64_t)p->max_depth : UINT64_MAX;
+        tp.grow.max_leaves = p->max_leaves > 0 ? (uint64_t)p->max_leaves : UINT64_MAX;
+        tp.grow.policy = p->grow_policy;
+        tp.grow.eta = (float)p->eta;
+        if (p->monotone) tp.grow.monotone.assign(p->monotone, p->monotone + p->n_monotone);
+        tp.objective = p->objective;
+        tp.num_class = p->num_class > 0 ? (uint32_t)p->num_class : 0;
+        tp.scale_pos_weight = p->scale_pos_weight;
+        tp.has_base_score = p->has_base_score != 0;
+        tp.base_score = p->base_score;
+        if (tp.objective < 0 || tp.objective > 2) fail(kInvalid, "trainer: unknown objective");
+        auto *t = new hbr_trainer{h, nullptr};
+        try {
+            t->t = std::make_unique<Trainer>(e, tp, labels, weights, n);
+        } catch (...) {
+            delete t;
+            throw;
+        }
+        *out = t;
+    });
+}
+
+int hbr_trainer_boost(hbr_trainer *t, uint64_t rounds) {
+    if (!t) return set_error(HBR_INVALID, "null trainer");
+    return with_engine(t->engine, [&](Engine &) { t->t->boost(rounds); });
+}
+
+int hbr_trainer_num_trees(hbr_trainer *t, uint64_t *n) {
+    if (!t) return set_error(HBR_INVALID, "null trainer");
+    return guard([&] { *n = t->t->trees().size(); });
+}
+
+int hbr_trainer_num_outputs(hbr_trainer *t, uint32_t *k) {
+    if (!t) return set_error(HBR_INVALID, "null trainer");
+    return guard([&] { *k = t->t->outputs(); });
+}
+
+int hbr_trainer_base_score(hbr_trainer *t, float *out) {
+    if (!t) return set_error(HBR_INVALID, "null trainer");
+    return guard([&] {
+        const auto &b = t->t->base_score();
+        std::memcpy(out, b.data(), b.size() * 4);
+    });
+}
+
+int hbr_trainer_tree_size(hbr_trainer *t, uint64_t tree, uint64_t *n_nodes) {
+    if (!t) return set_error(HBR_INVALID, "null trainer");
+    return guard([&] {
+        if (tree >= t->t->trees().size()) fail(kInvalid, "no such tree");
+        *n_nodes = t->t->trees()[tree].nodes.size();
+    });
+}
+
+int hbr_trainer_tree(hbr_trainer *t, uint64_t tree, uint32_t *split_feature, float *split_cond, uint8_t *default_left,
+                     int32_t *left, int32_t *right, float *leaf_value, float *sum_hess, float *split_gain,
+                     int64_t *split_bin) {
+    if (!t) return set_error(HBR_INVALID, "null trainer");
+    return guard([&] {
+        if (tree >= t->t->trees().size()) fail(kInvalid, "no such tree");
+        const auto &nodes = t->t->trees()[tree].nodes;
+        for (size_t i = 0; i < nodes.size(); i++) {
+            const TreeNode &n = nodes[i];
+            if (split_feature) split_feature[i] = n.split_feature;
+            if (split_cond) split_cond[i] = n.split_cond;
+            if (default_left) default_left[i] = n.default_left;
+            if (left) left[i] = n.left;
+            if (right) right[i] = n.right;
+            if (leaf_value) leaf_value[i] = n.leaf_value;
+            if (sum_hess) sum_hess[i] = n.sum_hess;
+            if (split_gain) split_gain[i] = n.split_gain;
+            if (split_bin) split_bin[i] = n.split_bin;
+        }
+    });
+}
+
+int hbr_trainer_margins(hbr_trainer *t, float *out) {
+    if (!t) return set_error(HBR_INVALID, "null trainer");
+    return with_engine(t->engine, [&](Engine &) { t->t->margins(out); });
+}
+
+void hbr_trainer_free(hbr_trainer *t) { delete t; }
+
+// ---- prediction -------------------------------------------------------------------------
+
+int hbr_forest_upload(int ordinal, const hbr_forest_desc *fd, hbr_forest **out) {
+    return guard([&] {
+        if (!fd || !out) fail(kInvalid, "forest: null argument");
+        auto *f = new hbr_forest;
+        try {
+            f->f = std::make_unique<Forest>(ordinal, *fd);
+        } catch (...) {
+            delete f;
+            throw;
+        }
+        *out = f;
+    });
+}
+
+void hbr_forest_free(hbr_forest *f) { delete f; }
+
+int hbr_predict_margin_device(hbr_forest *h, const float *x, uint64_t n, uint64_t n_cols, float missing, float *out,
+                              int32_t *leaf_out) {
+    return with_forest(h, [&](Forest &f) { f.predict_device(x, n, n_cols, missing, out, leaf_out); });
+}
+
+int hbr_predict_margin(hbr_forest *h, const float *x, uint64_t n, uint64_t n_cols, float missing, float *out) {
+    return with_forest(h, [&](Forest &f) {
+        if (n == 0) return;
+        DBuf<float> dx(n * n_cols), dout(n * f.n_outputs());
+        dx.upload(x, n * n_cols, f.dev().stream());
+        f.predict_device(dx.get(), n, n_cols, missing, dout.get(), nullptr);
+        dout.download(out, n * f.n_outputs(), f.dev().stream());
+        f.dev().sync();
+    });
+}
+
+int hbr_predict_leaf(hbr_forest *h, const float *x, uint64_t n, uint64_t n_cols, float missing, int32_t *out) {
+    return with_forest(h, [&](Forest &f) {
+        if (n == 0) return;
+        DBuf<float> dx(n * n_cols), dout(n * f.n_outputs());
+        DBuf<int32_t> dleaf(std::max<uint64_t>(1, n * f.n_trees()));
+        dx.upload(x, n * n_cols, f.dev().stream());
+        f.predict_device(dx.get(), n, n_cols, missing, dout.get(), dleaf.get());
+        dleaf.download(out, n * f.n_trees(), f.dev().stream());
+        f.dev().sync();
+    });
+}
+
+int hbr_forest_set_profiling(hbr_forest *h, int on, const char *prefix) {
+    return with_forest(h, [&](Forest &f) { f.dev().set_profiling(on != 0, prefix ? prefix : ""); });
+}
+
+int hbr_forest_kernel_stats(hbr_forest *h, char *buf, size_t len) {
+    return with_forest(h, [&](Forest &f) { copy_string(stats_string(f.dev()), buf, len); });
+}
+
+int hbr_device_alloc(int ordinal, uint64_t bytes, void **out) {
+    return guard([&] {
+        device(ordinal);
+        HBR_HIP(hipMalloc(out, bytes ? bytes : 1));
+    });
+}
+
+int hbr_device_free(int ordinal, void *p) {
+    return guard([&] {
+        device(ordinal);
+        HBR_HIP(hipFree(p));
+    });
+}
+
+int hbr_device_upload(int ordinal, void *dst, const void *src, uint64_t bytes) {
+    return guard([&] {
+        device(ordinal);
+        HBR_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    });
+}
+
+int hbr_device_download(int ordinal, void *dst, const void *src, uint64_t bytes) {
+    return guard([&] {
+        device(ordinal);
+        HBR_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,682 @@
+#include "engine.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace hbr {
+
+namespace {
+
+constexpr uint32_t kLeafTile = 4096;
+
+uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// Quantization exponent for a maximum magnitude (f32 bits) over `rows` rows:
+// with M = m 2^e (m in [0.5, 1)), exp = e + ceil(log2 rows) - 62 keeps every
+// sum of the tree's quantized values within 2^62.
+int32_t exp_for(uint32_t bits, uint64_t rows) {
+    if (bits == 0 || bits >= 0x7f800000u) return 0;
+    float m;
+    std::memcpy(&m, &bits, 4);
+    int e = 0;
+    std::frexp(m, &e);
+    int log_n = rows > 1 ? 64 - __builtin_clzll(rows - 1) : 0;
+    return e + log_n - 62;
+}
+
+uint32_t abs_bits(float x) {
+    uint32_t b;
+    std::memcpy(&b, &x, 4);
+    return b & 0x7fffffffu;
+}
+
+// The reference's scalar logistic gradient (simd/scalar.rs:8-29 with
+// simd/mod.rs:425-427), for the rows its vector kernel leaves to libm.
+void logistic_scalar(float m, float y, float w, float spw, float min_hess, float *g, float *h) {
+    float t = std::fmin(-m, 88.7f);
+    float p = 1.0f / (std::exp(t) + 1.0f);
+    if (y == 1.0f) w *= spw;
+    *g = (p - y) * w;
+    *h = std::fmax(p * (1.0f - p), min_hess) * w;
+}
+
+}  // namespace
+
+Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) {
+    upload_index(desc);
+    scale_.resize(1);
+    d_total_.resize(1);
+}
+
+Engine::~Engine() {
+    try {
+        dev_.activate();
+        dev_.sync();
+    } catch (...) {
+    }
+}
+
+void Engine::upload_index(const hbr_index_desc &d) {
+    if (!d.feature_offset || !d.row_ptr || (!d.row_bins && d.row_ptr[d.n_rows] > 0))
+        fail(kInvalid, "index: feature_offset, row_ptr and row_bins are required");
+    if (d.n_rows >= (uint64_t)UINT32_MAX) fail(kRefused, "index: more than 2^32 - 1 rows");
+    if (d.row_bin_width != 2 && d.row_bin_width != 4) fail(kInvalid, "index: row_bin_width must be 2 or 4");
+    n_rows_ = d.n_rows;
+    n_cols_ = (uint32_t)d.n_cols;
+    fo_.assign(d.feature_offset, d.feature_offset + n_cols_ + 1);
+    total_bins_ = fo_[n_cols_];
+    if (d.cut_values) cuts_.assign(d.cut_values, d.cut_values + total_bins_);
+    dense_ = d.dense != 0;
+    uint32_t widest = 0;
+    for (uint32_t f = 0; f < n_cols_; f++) widest = std::max(widest, fo_[f + 1] - fo_[f]);
+    hipStream_t s = dev_.stream();
+    d_fo_.resize(n_cols_ + 1);
+    d_fo_.upload(fo_.data(), n_cols_ + 1, s);
+    words_ = (uint32_t)((n_rows_ + 63) / 64);
+
+    if (dense_ && widest <= 256 && n_cols_ > 0) {
+        dense_u8_ = true;
+        have_cols_ = true;
+        stride_ = (n_cols_ + 15) / 16 * 16;
+        rows8_.resize(n_rows_ * stride_);
+        rows8_.zero(s);
+        cols8_.resize(n_rows_ * n_cols_);
+        // re-encode in chunks of rows, each chunk's global bins staged once
+        const uint64_t chunk = std::max<uint64_t>(1, (64ull << 20) / (n_cols_ * (uint64_t)d.row_bin_width));
+        DBuf<uint8_t> staging(chunk * n_cols_ * d.row_bin_width);
+        for (uint64_t r0 = 0; r0 < n_rows_; r0 += chunk) {
+            const uint64_t rows = std::min<uint64_t>(chunk, n_rows_ - r0);
+            const size_t bytes = rows * n_cols_ * d.row_bin_width;
+            const char *src = static_cast<const char *>(d.row_bins) + r0 * n_cols_ * d.row_bin_width;
+            HBR_HIP(hipMemcpyAsync(staging.get(), src, bytes, hipMemcpyHostToDevice, s));
+            EncodeArgs a{};
+            a.g16 = d.row_bin_width == 2 ? (const uint16_t *)staging.get() : nullptr;
+            a.g32 = d.row_bin_width == 4 ? (const uint32_t *)staging.get() : nullptr;
+            a.feature_offset = d_fo_.get();
+            a.rows8 = rows8_.get();
+            a.cols8 = cols8_.get();
+            a.n_rows = n_rows_;
+            a.row0 = r0;
+            a.chunk_rows = (uint32_t)rows;
+            a.n_cols = n_cols_;
+            a.stride = stride_;
+            const uint64_t cells = rows * n_cols_;
+            dev_.launch("hbr_encode_dense", dim3(std::min<uint64_t>(ceil_div(cells, 256), 65535)), dim3(256), a);
+            dev_.sync();
+        }
+        return;
+    }
+    // CSR rows for histograms (global bins widened to u32).
+    const uint64_t nnz = d.row_ptr[n_rows_];
+    row_ptr_.resize(n_rows_ + 1);
+    row_ptr_.upload(d.row_ptr, n_rows_ + 1, s);
+    gbins_.resize(nnz ? nnz : 1);
+    if (d.row_bin_width == 4) {
+        gbins_.upload(static_cast<const uint32_t *>(d.row_bins), nnz, s);
+    } else {
+        const uint16_t *g16 = static_cast<const uint16_t *>(d.row_bins);
+        const uint64_t chunk = 1ull << 24;
+        std::vector<uint32_t> wide;
+        for (uint64_t e0 = 0; e0 < nnz; e0 += chunk) {
+            const uint64_t m = std::min(chunk, nnz - e0);
+            wide.assign(g16 + e0, g16 + e0 + m);
+            gbins_.upload(wide.data(), m, s, e0);
+            dev_.sync();
+        }
+    }
+    // feature-major columns route rows when the index keeps them
+    if (d.col_bins && (d.col_bin_width == 1 || d.col_bin_width == 2)) {
+        have_cols_ = true;
+        const uint64_t cells = n_rows_ * n_cols_;
+        if (d.col_bin_width == 1) {
+            cols8_.resize(cells ? cells : 1);
+            cols8_.upload(static_cast<const uint8_t *>(d.col_bins), cells, s);
+        } else {
+            cols16_.resize(cells ? cells : 1);
+            cols16_.upload(static_cast<const uint16_t *>(d.col_bins), cells, s);
+        }
+        if (d.missing) {
+            missing_.resize((uint64_t)words_ * n_cols_);
+            missing_.upload(d.missing, (uint64_t)words_ * n_cols_, s);
+        }
+    }
+    dev_.sync();
+}
+
+// ---- gradients -----------------------------------------------------------------
+
+void Engine::load_margins(const float *m, uint64_t n, uint32_t outputs) {
+    if (n != n_rows_ * outputs) fail(kInvalid, "load_margins: length is not n_rows * n_outputs");
+    outputs_ = outputs;
+    margins_.resize(n);
+    margins_.upload(m, n, dev_.stream());
+    labels_loaded_ = false;
+    dev_.sync();
+}
+
+void Engine::set_labels(const float *labels, const float *weights, uint64_t n) {
+    if (n != n_rows_) fail(kInvalid, "labels: one per row");
+    labels_.resize(n);
+    labels_.upload(labels, n, dev_.stream());
+    labels_host_.assign(labels, labels + n);
+    has_weights_ = weights != nullptr;
+    if (weights) {
+        weights_.resize(n);
+        weights_.upload(weights, n, dev_.stream());
+        weights_host_.assign(weights, weights + n);
+    } else {
+        weights_host_.clear();
+    }
+    labels_loaded_ = true;
+    dev_.sync();
+}
+
+void Engine::read_margins(float *out, uint64_t n) {
+    if (n > margins_.size()) fail(kInvalid, "read_margins: longer than the margins");
+    margins_.download(out, n, dev_.stream());
+    dev_.sync();
+}
+
+void Engine::read_gradients(float *out, uint64_t n) {
+    if (n != n_rows_ || gpair_.size() < n_rows_) fail(kInvalid, "read_gradients: nothing staged for every row");
+    gpair_.download(reinterpret_cast<GPair *>(out), n, dev_.stream());
+    dev_.sync();
+}
+
+double Engine::unit_g() const { return std::ldexp(1.0, scale_host_.exp_g); }
+double Engine::unit_h() const { return std::ldexp(1.0, scale_host_.exp_h); }
+
+void Engine::prepare(const float *gpair, uint64_t n) {
+    if (n != n_rows_) fail(kInvalid, "prepare: one gradient pair per row");
+    gpair_.resize(n_rows_ ? n_rows_ : 1);
+    gpair_.upload(reinterpret_cast<const GPair *>(gpair), n, dev_.stream());
+    QScale q{};
+    for (uint64_t i = 0; i < n; i++) {
+        const float g = gpair[2 * i], h = gpair[2 * i + 1];
+        if (!std::isfinite(g) || !std::isfinite(h)) {
+            q.nonfinite++;
+            continue;
+        }
+        q.max_g_bits = std::max(q.max_g_bits, abs_bits(g));
+        q.max_h_bits = std::max(q.max_h_bits, abs_bits(h));
+    }
+    q.exp_g = exp_for(q.max_g_bits, n_rows_);
+    q.exp_h = exp_for(q.max_h_bits, n_rows_);
+    scale_host_ = q;
+    scale_.upload(&scale_host_, 1, dev_.stream());
+    dev_.sync();
+    if (q.nonfinite) fail(kRefused, "a staged gradient is not finite");
+}
+
+bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
+    if (!labels_loaded_) fail(kInvalid, "gradients: no labels since load_margins");
+    if (outputs_ != 1 || output != 0) fail(kRefused, "device gradients run for one output");
+    hipStream_t s = dev_.stream();
+    gpair_.resize(n_rows_ ? n_rows_ : 1);
+    scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
+    scale_.zero(s);
+    GradArgs a{};
+    a.margins = margins_.get();
+    a.labels = labels_.get();
+    a.weights = has_weights_ ? weights_.get() : nullptr;
+    a.gpair = gpair_.get();
+    a.scale = scale_.get();
+    a.scalar_list = scalar_list_.get();
+    a.n = (uint32_t)n_rows_;
+    a.vec_rows = (uint32_t)std::min<uint64_t>(loss.vector_rows, n_rows_);
+    a.loss = loss.kind == HBR_LOSS_LOGISTIC ? kLogistic : kSquaredError;
+    a.scale_pos_weight = loss.scale_pos_weight;
+    a.min_hess = loss.min_hess;
+    a.max_input = loss.max_input;
+    dev_.launch("hbr_gradients", dim3(ceil_div(n_rows_, kThreads)), dim3(kThreads), a);
+    QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
+    scale_.download(q, 1, s);
+    dev_.sync();
+    stage_.reset();
+    QScale host = *q;
+    if (host.scalar_rows) {
+        // rows the reference computes with libm's expf: computed here
+        std::vector<uint32_t> list(host.scalar_rows);
+        scalar_list_.download(list.data(), list.size(), s);
+        std::vector<float> m;
+        const bool whole = list.size() > 4096;
+        if (whole) {
+            m.resize(n_rows_);
+            margins_.download(m.data(), n_rows_, s);
+        } else {
+            m.resize(list.size());
+            for (size_t k = 0; k < list.size(); k++) margins_.download(&m[k], 1, s, list[k]);
+        }
+        dev_.sync();
+        for (size_t k = 0; k < list.size(); k++) {
+            const uint32_t r = list[k];
+            const float mr = whole ? m[r] : m[k];
+            const float w = has_weights_ ? weights_host_[r] : 1.0f;
+            GPair p;
+            logistic_scalar(mr, labels_host_[r], w, loss.scale_pos_weight, loss.min_hess, &p.g, &p.h);
+            if (!std::isfinite(p.g) || !std::isfinite(p.h)) host.nonfinite++;
+            host.max_g_bits = std::max(host.max_g_bits, abs_bits(p.g));
+            host.max_h_bits = std::max(host.max_h_bits, abs_bits(p.h));
+            gpair_.upload(&p, 1, s, r);
+            dev_.sync();
+        }
+    }
+    host.exp_g = exp_for(host.max_g_bits, n_rows_);
+    host.exp_h = exp_for(host.max_h_bits, n_rows_);
+    scale_host_ = host;
+    scale_.upload(&scale_host_, 1, s);
+    dev_.sync();
+    return host.nonfinite == 0;
+}
+
+// ---- tree growth -------------------------------------------------------------------
+
+void Engine::ensure_rows() {
+    for (auto &r : rows_) r.reserve(n_rows_ ? n_rows_ : 1);
+}
+
+uint64_t Engine::begin_tree() {
+    ensure_rows();
+    IotaArgs a{rows_[0].get(), 0, (uint32_t)n_rows_};
+    dev_.launch("hbr_iota", dim3(ceil_div(n_rows_, kThreads)), dim3(kThreads), a);
+    identity_rows0_ = true;
+    counters.trees++;
+    return ++tree_;
+}
+
+// A segment whose rows are the identity run 0..n-1 (the root of an
+// unsampled tree) is summed without reading its row list.
+bool Engine::contiguous(const Segment &sg) const {
+    return identity_rows0_ && sg.buf == 0 && sg.offset == 0 && sg.len == n_rows_;
+}
+
+QBin Engine::root_total(const Segment &sg) {
+    hipStream_t s = dev_.stream();
+    d_total_.zero(s);
+    TotalArgs a{};
+    a.rows = rows_[sg.buf].get() + sg.offset;
+    a.first = 0;
+    a.n = sg.len;
+    a.gpair = gpair_.get();
+    a.scale = scale_.get();
+    a.out = d_total_.get();
+    const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(sg.len, kThreads)), 2048);
+    dev_.launch("hbr_total", dim3(blocks), dim3(kThreads), a);
+    QBin *out = static_cast<QBin *>(stage_.alloc(sizeof(QBin)));
+    d_total_.download(out, 1, s);
+    dev_.sync();
+    QBin t = *out;
+    stage_.reset();
+    return t;
+}
+
+uint32_t Engine::alloc_slot() {
+    if (free_slots_.empty()) {
+        const uint32_t cap = std::max<uint32_t>(8, slot_cap_ * 2);
+        if (!reserve_slots(cap)) fail(kRefused, "histogram slots do not fit in device memory");
+    }
+    const uint32_t s = free_slots_.back();
+    free_slots_.pop_back();
+    return s;
+}
+
+void Engine::free_slot(uint32_t s) { free_slots_.push_back(s); }
+
+bool Engine::reserve_slots(uint64_t n) {
+    if (n <= slot_cap_) return true;
+    size_t free_b = 0, total_b = 0;
+    HBR_HIP(hipMemGetInfo(&free_b, &total_b));
+    const uint64_t bytes = n * (uint64_t)total_bins_ * sizeof(QBin);
+    if (bytes > free_b / 2) return false;
+    DBuf<QBin> grown(n * (uint64_t)total_bins_ + 1);
+    if (slot_cap_)
+        HBR_HIP(hipMemcpyAsync(grown.get(), hist_.get(), (uint64_t)slot_cap_ * total_bins_ * sizeof(QBin),
+                               hipMemcpyDeviceToDevice, dev_.stream()));
+    dev_.sync();
+    hist_ = std::move(grown);
+    for (uint32_t s = (uint32_t)n; s-- > slot_cap_;) free_slots_.push_back(s);
+    slot_cap_ = (uint32_t)n;
+    return true;
+}
+
+// Per row: its bins (one byte per feature for a dense u8 index, else four
+// per stored entry), its gradient pair, and its id when the node's rows are
+// gathered through a row list.
+uint64_t Engine::hist_bytes(uint64_t rows, bool gathered) const {
+    const uint64_t bins = dense_u8_ ? n_cols_ : 4ull * (n_rows_ ? gbins_.size() / n_rows_ : 0);
+    return rows * (bins + 8 + (gathered ? 4 : 0));
+}
+
+void Engine::set_scan_params(const ScanParams &p, const std::vector<int8_t> &monotone) {
+    scan_params_ = p;
+    has_monotone_ = false;
+    for (int8_t d : monotone) has_monotone_ |= d != 0;
+    if (has_monotone_) {
+        std::vector<int8_t> dirs(n_cols_, 0);
+        for (size_t f = 0; f < monotone.size() && f < n_cols_; f++) dirs[f] = monotone[f];
+        monotone_.resize(n_cols_);
+        monotone_.upload(dirs.data(), n_cols_, dev_.stream());
+        dev_.sync();
+    }
+}
+
+void Engine::launch_hist(const std::vector<HistNode> &nodes, const std::vector<uint32_t> &upper_len,
+                         const PartSplit *splits_dev, const uint32_t *rows0) {
+    std::vector<HistTile> tiles;
+    const uint32_t fg = dense_u8_ ? hist_features_per_group : 0;
+    for (uint32_t i = 0; i < nodes.size(); i++) {
+        for (uint32_t r0 = 0; r0 < upper_len[i]; r0 += kHistTile) {
+            if (!dense_u8_) {
+                tiles.push_back(HistTile{i, r0, 0, 0});
+                continue;
+            }
+            for (uint32_t f0 = 0; f0 < n_cols_; f0 += fg)
+                tiles.push_back(HistTile{i, r0, f0, std::min(fg, n_cols_ - f0)});
+        }
+    }
+    if (tiles.empty()) return;
+    hipStream_t s = dev_.stream();
+    upload_vec(d_hnodes_, nodes, stage_, s);
+    upload_vec(d_htiles_, tiles, stage_, s);
+    HistArgs a{};
+    a.nodes = d_hnodes_.get();
+    a.tiles = d_htiles_.get();
+    a.splits = splits_dev;
+    a.part_out = d_part_out_.get();
+    a.rows[0] = rows0 ? rows0 : rows_[0].get();
+    a.rows[1] = rows_[1].get();
+    a.gpair = gpair_.get();
+    a.scale = scale_.get();
+    a.bins8 = rows8_.get();
+    a.stride = stride_;
+    a.row_ptr = row_ptr_.get();
+    a.gbins = gbins_.get();
+    a.feature_offset = d_fo_.get();
+    a.hist = hist_.get();
+    a.total_bins = total_bins_;
+    a.tile_rows = kHistTile;
+    const char *k = !dense_u8_ ? "hbr_hist_csr"
+                    : fg <= 8  ? "hbr_hist_dense8_fg8"
+                    : fg <= 16 ? "hbr_hist_dense8_fg16"
+                               : "hbr_hist_dense8_fg32";
+    dev_.launch(k, dim3((uint32_t)tiles.size()), dim3(kHistThreads), a);
+}
+
+void Engine::build_nodes(const std::vector<Segment> &segs, const std::vector<uint32_t> &slots) {
+    if (segs.empty()) return;
+    hipStream_t s = dev_.stream();
+    upload_vec(d_slots_, slots, stage_, s);
+    ZeroArgs z{hist_.get(), d_slots_.get(), (uint32_t)slots.size(), total_bins_};
+    dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), (uint32_t)slots.size()),
+                dim3(256), z);
+    std::vector<HistNode> nodes;
+    std::vector<uint32_t> lens;
+    for (size_t i = 0; i < segs.size(); i++) {
+        HistNode n{};
+        n.seg = Seg{segs[i].offset, segs[i].len, segs[i].buf, 0};
+        n.slot = slots[i];
+        n.contiguous = contiguous(segs[i]) ? 1u : 0u;
+        nodes.push_back(n);
+        lens.push_back(segs[i].len);
+        counters.hist_nodes++;
+        counters.hist_rows += segs[i].len;
+        counters.hist_bytes += hist_bytes(segs[i].len, !n.contiguous);
+    }
+    launch_hist(nodes, lens, nullptr);
+}
+
+void Engine::subtract(const std::vector<uint32_t> &parents, const std::vector<uint32_t> &built) {
+    if (parents.empty()) return;
+    std::vector<PartSplit> sp(parents.size());
+    for (size_t i = 0; i < parents.size(); i++) {
+        sp[i] = PartSplit{};
+        sp[i].parent_slot = parents[i];
+        sp[i].fresh_slot = built[i];
+    }
+    upload_vec(d_splits_, sp, stage_, dev_.stream());
+    SubArgs a{d_splits_.get(), (uint32_t)sp.size(), hist_.get(), total_bins_};
+    dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), (uint32_t)sp.size()),
+                dim3(256), a);
+}
+
+void Engine::launch_scan(const std::vector<ScanNode> &nodes, ScanBest *host_out) {
+    hipStream_t s = dev_.stream();
+    upload_vec(d_snodes_, nodes, stage_, s);
+    const uint64_t pairs = (uint64_t)nodes.size() * n_cols_;
+    d_per_feature_.reserve(pairs ? pairs : 1);
+    d_best_.reserve(nodes.size());
+    ScanArgs a{};
+    a.nodes = d_snodes_.get();
+    a.n_nodes = (uint32_t)nodes.size();
+    a.n_features = n_cols_;
+    a.splits = d_splits_.get();
+    a.part_out = d_part_out_.get();
+    a.hist = hist_.get();
+    a.total_bins = total_bins_;
+    a.feature_offset = d_fo_.get();
+    a.monotone = has_monotone_ ? monotone_.get() : nullptr;
+    a.scale = scale_.get();
+    a.reg = scan_params_;
+    a.dense = dense_ ? 1u : 0u;
+    a.per_feature = d_per_feature_.get();
+    a.best = d_best_.get();
+    dev_.launch("hbr_scan_features", dim3(ceil_div(pairs, 4)), dim3(256), a);
+    dev_.launch("hbr_scan_merge", dim3((uint32_t)nodes.size()), dim3(64), a);
+    d_best_.download(host_out, nodes.size(), s);
+}
+
+std::vector<ScanBest> Engine::scan(const std::vector<ScanInput> &in) {
+    std::vector<ScanBest> out(in.size());
+    if (in.empty()) return out;
+    std::vector<ScanNode> nodes(in.size());
+    for (size_t i = 0; i < in.size(); i++) {
+        ScanNode n{};
+        n.slot = in[i].slot;
+        n.total = in[i].total;
+        n.root_gain = in[i].root_gain;
+        n.lower = in[i].lower;
+        n.upper = in[i].upper;
+        nodes[i] = n;
+    }
+    ScanBest *staged = static_cast<ScanBest *>(stage_.alloc(in.size() * sizeof(ScanBest)));
+    launch_scan(nodes, staged);
+    dev_.sync();
+    std::memcpy(out.data(), staged, in.size() * sizeof(ScanBest));
+    stage_.reset();
+    return out;
+}
+
+std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, bool terminal) {
+    const uint32_t P = (uint32_t)splits.size();
+    std::vector<LevelChild> children(2 * P);
+    if (P == 0) return children;
+    hipStream_t s = dev_.stream();
+    std::vector<PartSplit> ps(P);
+    std::vector<uint32_t> tile_split;
+    std::vector<uint32_t> fresh(P, 0);
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < P; i++) {
+        const LevelSplit &l = splits[i];
+        PartSplit p{};
+        p.seg = Seg{l.seg.offset, l.seg.len, l.seg.buf, 0};
+        p.feature = l.feature;
+        p.limit = l.limit;
+        p.default_left = l.default_left;
+        p.tile_begin = tiles;
+        if (!terminal) {
+            fresh[i] = alloc_slot();
+            p.fresh_slot = fresh[i];
+            p.parent_slot = l.parent_slot;
+        }
+        const uint32_t nt = ceil_div(l.seg.len, kPartTile);
+        for (uint32_t t = 0; t < nt; t++) tile_split.push_back(i);
+        tiles += nt;
+        ps[i] = p;
+    }
+    upload_vec(d_splits_, ps, stage_, s);
+    upload_vec(d_tile_split_, tile_split, stage_, s);
+    d_tile_left_.reserve(tiles ? tiles : 1);
+    d_part_out_.reserve(P);
+    PartArgs a{};
+    a.splits = d_splits_.get();
+    a.n_splits = P;
+    a.n_tiles = tiles;
+    a.tile_split = d_tile_split_.get();
+    a.tile_left = d_tile_left_.get();
+    a.out = d_part_out_.get();
+    a.src_rows[0] = rows_[0].get();
+    a.src_rows[1] = rows_[1].get();
+    a.dst_rows[0] = rows_[0].get();
+    a.dst_rows[1] = rows_[1].get();
+    a.dense = have_cols_ ? 1u : 0u;
+    a.cols8 = cols8_.size() ? cols8_.get() : nullptr;
+    a.cols16 = cols16_.size() ? cols16_.get() : nullptr;
+    a.missing = missing_.size() ? missing_.get() : nullptr;
+    a.row_ptr = row_ptr_.get();
+    a.gbins = gbins_.get();
+    a.feature_offset = d_fo_.get();
+    a.n_rows = (uint32_t)n_rows_;
+    a.words = words_;
+    dev_.launch("hbr_part_count", dim3(tiles), dim3(kPartThreads), a);
+    dev_.launch("hbr_part_scan", dim3(P), dim3(kPartThreads), a);
+    dev_.launch("hbr_part_scatter", dim3(tiles), dim3(kPartThreads), a);
+
+    ScanBest *best_staged = nullptr;
+    if (!terminal) {
+        upload_vec(d_slots_, fresh, stage_, s);
+        ZeroArgs z{hist_.get(), d_slots_.get(), P, total_bins_};
+        dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), z);
+        std::vector<HistNode> hn(P);
+        std::vector<uint32_t> upper(P);
+        for (uint32_t i = 0; i < P; i++) {
+            HistNode n{};
+            n.slot = fresh[i];
+            n.from_split = 1;
+            n.split = i;
+            hn[i] = n;
+            upper[i] = splits[i].seg.len / 2;
+        }
+        launch_hist(hn, upper, d_splits_.get());
+        SubArgs sub{d_splits_.get(), P, hist_.get(), total_bins_};
+        dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), sub);
+        std::vector<ScanNode> sn(2 * P);
+        for (uint32_t i = 0; i < P; i++) {
+            for (uint32_t c = 0; c < 2; c++) {
+                ScanNode n{};
+                n.from_split = 1;
+                n.split = i;
+                n.child = c;
+                n.total = splits[i].child_total[c];
+                n.root_gain = splits[i].child_root_gain[c];
+                n.lower = splits[i].child_lower[c];
+                n.upper = splits[i].child_upper[c];
+                sn[2 * i + c] = n;
+            }
+        }
+        best_staged = static_cast<ScanBest *>(stage_.alloc(2 * P * sizeof(ScanBest)));
+        launch_scan(sn, best_staged);
+    }
+    PartOut *po = static_cast<PartOut *>(stage_.alloc(P * sizeof(PartOut)));
+    d_part_out_.download(po, P, s);
+    dev_.sync();
+    for (uint32_t i = 0; i < P; i++) {
+        const Segment &pseg = splits[i].seg;
+        const uint32_t nl = po[i].left_len;
+        LevelChild &L = children[2 * i];
+        LevelChild &R = children[2 * i + 1];
+        L.seg = Segment{pseg.offset, nl, pseg.buf ^ 1u};
+        R.seg = Segment{pseg.offset + nl, pseg.len - nl, pseg.buf ^ 1u};
+        counters.partition_rows += pseg.len;
+        if (!terminal) {
+            const bool built_left = po[i].built_left != 0;
+            L.slot = built_left ? fresh[i] : splits[i].parent_slot;
+            R.slot = built_left ? splits[i].parent_slot : fresh[i];
+            L.best = best_staged[2 * i];
+            R.best = best_staged[2 * i + 1];
+            const uint32_t built = built_left ? nl : pseg.len - nl;
+            counters.hist_nodes++;
+            counters.hist_rows += built;
+            counters.hist_bytes += hist_bytes(built, true);
+        }
+    }
+    // the scatter wrote every split's rows into the other buffer
+    identity_rows0_ = false;
+    stage_.reset();
+    return children;
+}
+
+void Engine::add_leaves(const std::vector<Segment> &segs, const std::vector<float> &values, uint32_t output) {
+    if (segs.empty()) return;
+    std::vector<LeafSeg> leaves(segs.size());
+    std::vector<uint32_t> tile_leaf, tile_row0;
+    for (uint32_t i = 0; i < segs.size(); i++) {
+        LeafSeg l{};
+        l.seg = Seg{segs[i].offset, segs[i].len, segs[i].buf, 0};
+        l.value = values[i];
+        leaves[i] = l;
+        for (uint32_t r0 = 0; r0 < segs[i].len; r0 += kLeafTile) {
+            tile_leaf.push_back(i);
+            tile_row0.push_back(r0);
+        }
+    }
+    if (tile_leaf.empty()) return;
+    hipStream_t s = dev_.stream();
+    upload_vec(d_leaves_, leaves, stage_, s);
+    upload_vec(d_tile_leaf_, tile_leaf, stage_, s);
+    upload_vec(d_tile_row0_, tile_row0, stage_, s);
+    LeafArgs a{};
+    a.leaves = d_leaves_.get();
+    a.tile_leaf = d_tile_leaf_.get();
+    a.tile_row0 = d_tile_row0_.get();
+    a.rows[0] = rows_[0].get();
+    a.rows[1] = rows_[1].get();
+    a.margins = margins_.get();
+    a.stride = outputs_;
+    a.output = output;
+    a.tile_rows = kLeafTile;
+    a.n_tiles = (uint32_t)tile_leaf.size();
+    dev_.launch("hbr_add_leaves", dim3(a.n_tiles), dim3(256), a);
+    dev_.sync();
+    stage_.reset();
+}
+
+std::vector<QBin> Engine::build_rows(const uint32_t *rows, uint64_t m) {
+    for (uint64_t i = 0; i < m; i++)
+        if (rows[i] >= n_rows_) fail(kRefused, "build: a row beyond the index");
+    hipStream_t s = dev_.stream();
+    host_rows_.reserve(m ? m : 1);
+    host_rows_.upload(rows, m, s);
+    const uint32_t slot = alloc_slot();
+    std::vector<uint32_t> slots{slot};
+    upload_vec(d_slots_, slots, stage_, s);
+    ZeroArgs z{hist_.get(), d_slots_.get(), 1, total_bins_};
+    dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), 1), dim3(256), z);
+    HistNode n{};
+    n.seg = Seg{0, (uint32_t)m, 0, 0};
+    n.slot = slot;
+    launch_hist({n}, {(uint32_t)m}, nullptr, host_rows_.get());
+    std::vector<QBin> out(total_bins_);
+    hist_.download(out.data(), total_bins_, s, (size_t)slot * total_bins_);
+    dev_.sync();
+    stage_.reset();
+    free_slot(slot);
+    return out;
+}
+
+std::vector<uint32_t> Engine::rows_of(const Segment &sg) {
+    std::vector<uint32_t> out(sg.len);
+    rows_[sg.buf].download(out.data(), sg.len, dev_.stream(), sg.offset);
+    dev_.sync();
+    return out;
+}
+
+std::vector<QBin> Engine::read_slot(uint32_t slot) {
+    if (slot >= slot_cap_) fail(kInvalid, "read_hist: no such slot");
+    std::vector<QBin> out(total_bins_);
+    hist_.download(out.data(), total_bins_, dev_.stream(), (size_t)slot * total_bins_);
+    dev_.sync();
+    return out;
+}
+
+}  // namespace hbr

@@ -1,0 +1,175 @@
+// The device engine: one binned index resident on one GPU, its gradients,
+// margins, row buffers and histogram slots, and the level-batched growth
+// steps the tree builder drives (the reference's HistogramBackend and
+// RowEngine, src/tree/hist/mod.rs:73-295).
+#pragma once
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../abi.h"
+#include "runtime.h"
+
+#include "hessboost_rocm.h"
+
+namespace hbr {
+
+// A node's rows on the device: `len` ids at `offset` of row buffer `buf`.
+struct Segment {
+    uint32_t offset = 0, len = 0, buf = 0;
+};
+
+// One split of a level: the parent's rows, slot and routing.
+struct LevelSplit {
+    Segment seg;
+    uint32_t parent_slot = 0;  // parent's histogram (becomes the sibling's); unused when terminal
+    uint32_t feature = 0;
+    uint32_t limit = 0;        // present local bins below go left
+    uint32_t default_left = 0;
+    // child scan inputs (non-terminal levels)
+    QBin child_total[2];
+    float child_root_gain[2];
+    float child_lower[2], child_upper[2];
+};
+
+struct LevelChild {
+    Segment seg;
+    uint32_t slot = 0;
+    ScanBest best;  // valid when the level was not terminal
+};
+
+struct ScanInput {
+    uint32_t slot;
+    QBin total;
+    float root_gain, lower, upper;
+};
+
+class Engine {
+public:
+    Engine(int ordinal, const hbr_index_desc &desc);
+    ~Engine();
+
+    std::mutex mu;
+    bool failed = false;
+
+    Device &dev() { return dev_; }
+    uint64_t n_rows() const { return n_rows_; }
+    uint32_t n_cols() const { return n_cols_; }
+    uint32_t total_bins() const { return total_bins_; }
+    bool dense() const { return dense_; }
+    const std::vector<uint32_t> &feature_offset() const { return fo_; }
+    const std::vector<float> &cut_values() const { return cuts_; }
+
+    // ---- gradients -----------------------------------------------------------
+    // Stage host gradient pairs for the next tree (HistogramBackend::prepare).
+    void prepare(const float *gpair, uint64_t n);
+    // Device margins and labels (RowEngine::load_margins / gradients).
+    void load_margins(const float *m, uint64_t n, uint32_t outputs);
+    void set_labels(const float *labels, const float *weights, uint64_t n);
+    bool labels_loaded() const { return labels_loaded_; }
+    // Gradients of output `output` from the device margins; false when some
+    // gradient is not finite.
+    bool compute_gradients(const hbr_device_loss &loss, uint32_t output);
+    void read_margins(float *out, uint64_t n);
+    void read_gradients(float *out, uint64_t n);
+    const QScale &scale() const { return scale_host_; }
+    double unit_g() const;
+    double unit_h() const;
+
+    // ---- tree growth ------------------------------------------------------------
+    uint64_t begin_tree();  // every row in buffer 0; returns the tree stamp
+    uint64_t tree() const { return tree_; }
+    QBin root_total(const Segment &s);
+    // Build node histograms into their (zeroed) slots, then parent -= built.
+    void build_nodes(const std::vector<Segment> &segs, const std::vector<uint32_t> &slots);
+    void subtract(const std::vector<uint32_t> &parents, const std::vector<uint32_t> &built);
+    std::vector<ScanBest> scan(const std::vector<ScanInput> &nodes);
+    // Partition + (non-terminal) smaller-child histograms, sibling subtraction
+    // and the children's split search, with one host synchronisation.
+    std::vector<LevelChild> level(const std::vector<LevelSplit> &splits, bool terminal);
+    void add_leaves(const std::vector<Segment> &segs, const std::vector<float> &values, uint32_t output);
+    // HistogramBackend::build of a host row list (per-node host growth).
+    std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
+    std::vector<uint32_t> rows_of(const Segment &s);
+    std::vector<QBin> read_slot(uint32_t slot);
+
+    // ---- histogram slots ------------------------------------------------------
+    uint32_t alloc_slot();
+    void free_slot(uint32_t s);
+    bool reserve_slots(uint64_t n);
+
+    // scan regularization and monotone directions for the next scans
+    void set_scan_params(const ScanParams &p, const std::vector<int8_t> &monotone);
+
+    hbr_engine_counters counters{};
+    // algorithmic bytes of summing `rows` rows into a histogram
+    uint64_t hist_bytes(uint64_t rows, bool gathered) const;
+
+private:
+    void upload_index(const hbr_index_desc &desc);
+    void ensure_rows();
+    bool contiguous(const Segment &sg) const;
+    bool identity_rows0_ = false;
+    void launch_hist(const std::vector<HistNode> &nodes, const std::vector<uint32_t> &upper_len,
+                     const PartSplit *splits_dev, const uint32_t *rows0 = nullptr);
+    void launch_scan(const std::vector<ScanNode> &nodes, ScanBest *host_out);
+    void finish_scale(uint32_t rows);
+
+    Device &dev_;
+    uint64_t n_rows_ = 0;
+    uint32_t n_cols_ = 0, total_bins_ = 0;
+    bool dense_ = false;      // reference's is_dense: complete rows
+    bool have_cols_ = false;  // feature-major local columns for routing
+    bool dense_u8_ = false;   // row-major u8 local bins for the dense histogram
+    uint32_t stride_ = 0;     // row-major stride in bytes
+    uint32_t words_ = 0;      // bitmap words per feature
+    std::vector<uint32_t> fo_;
+    std::vector<float> cuts_;
+    DBuf<uint32_t> d_fo_;
+    DBuf<uint8_t> rows8_, cols8_;
+    DBuf<uint16_t> cols16_;
+    DBuf<uint64_t> missing_, row_ptr_;
+    DBuf<uint32_t> gbins_;
+
+    // training state
+    DBuf<GPair> gpair_;
+    DBuf<float> margins_, labels_, weights_;
+    uint32_t outputs_ = 1;
+    bool labels_loaded_ = false, has_weights_ = false;
+    DBuf<QScale> scale_;
+    QScale scale_host_{};
+    DBuf<uint32_t> scalar_list_;
+    DBuf<uint32_t> rows_[2];
+    DBuf<uint32_t> host_rows_;
+    uint64_t tree_ = 0;
+    std::vector<float> labels_host_, weights_host_;
+
+    // histogram slots
+    DBuf<QBin> hist_;
+    uint32_t slot_cap_ = 0;
+    std::vector<uint32_t> free_slots_;
+
+    // scan configuration
+    ScanParams scan_params_{1.0, 0.0, 0.0, 1.0};
+    DBuf<int8_t> monotone_;
+    bool has_monotone_ = false;
+
+    // per-call scratch
+    Stage stage_;
+    DBuf<PartSplit> d_splits_;
+    DBuf<uint32_t> d_tile_split_, d_tile_left_, d_slots_;
+    DBuf<PartOut> d_part_out_;
+    DBuf<HistNode> d_hnodes_;
+    DBuf<HistTile> d_htiles_;
+    DBuf<ScanNode> d_snodes_;
+    DBuf<ScanBest> d_per_feature_, d_best_;
+    DBuf<QBin> d_total_;
+    DBuf<LeafSeg> d_leaves_;
+    DBuf<uint32_t> d_tile_leaf_, d_tile_row0_;
+
+public:
+    uint32_t hist_features_per_group = 16;
+};
+
+}  // namespace hbr

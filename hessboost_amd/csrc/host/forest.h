@@ -1,0 +1,35 @@
+// A forest resident on one device for batch prediction (the reference's
+// GpuModel, src/backend/cuda/predict.rs:401-520).
+#pragma once
+#include <cstdint>
+#include <mutex>
+#include <vector>
+
+#include "../abi.h"
+#include "hessboost_rocm.h"
+#include "runtime.h"
+
+namespace hbr {
+
+class Forest {
+public:
+    Forest(int ordinal, const hbr_forest_desc &fd);
+    std::mutex mu;
+    bool failed = false;
+    Device &dev() { return dev_; }
+    uint32_t n_outputs() const { return n_outputs_; }
+    uint64_t n_trees() const { return n_trees_; }
+    // x, out, leaf_out: device pointers.
+    void predict_device(const float *x, uint64_t n, uint64_t n_cols, float missing, float *out, int32_t *leaf_out);
+
+private:
+    Device &dev_;
+    uint64_t n_trees_ = 0;
+    uint32_t n_outputs_ = 1;
+    uint32_t max_feature_ = 0;
+    DBuf<uint32_t> value_, meta_, left_, root_, output_;
+    DBuf<int32_t> orig_;
+    DBuf<float> weight_, base_;
+};
+
+}  // namespace hbr

@@ -1,0 +1,180 @@
+#include "runtime.h"
+
+#include <dlfcn.h>
+
+#include <memory>
+
+namespace hbr {
+
+void fail(int status, const std::string &msg) { throw Error(status, msg); }
+
+void check_hip(hipError_t e, const char *what) {
+    if (e != hipSuccess) fail(kDeviceError, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// The code object sits beside this library: <dir of libhbrocm.so>/hbrocm_gfx950.hsaco.
+static std::string code_object_path() {
+    Dl_info info;
+    if (dladdr((void *)&code_object_path, &info) && info.dli_fname) {
+        std::string so = info.dli_fname;
+        auto slash = so.rfind('/');
+        std::string dir = slash == std::string::npos ? "." : so.substr(0, slash);
+        return dir + "/hbrocm_gfx950.hsaco";
+    }
+    return "hbrocm_gfx950.hsaco";
+}
+
+Device::Device(int ordinal) : ordinal_(ordinal) {
+    int count = 0;
+    HBR_HIP(hipGetDeviceCount(&count));
+    if (ordinal < 0 || ordinal >= count)
+        fail(kInvalid, "no ROCm device with ordinal " + std::to_string(ordinal));
+    HBR_HIP(hipSetDevice(ordinal));
+    hipDeviceProp_t prop;
+    HBR_HIP(hipGetDeviceProperties(&prop, ordinal));
+    if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
+        fail(kRefused, std::string("device is ") + prop.gcnArchName + ", the code object is gfx950");
+    cu_count_ = prop.multiProcessorCount;
+    HBR_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    std::string path = code_object_path();
+    hipError_t e = hipModuleLoad(&module_, path.c_str());
+    if (e != hipSuccess) fail(kDeviceError, "hipModuleLoad(" + path + "): " + hipGetErrorString(e));
+}
+
+Device::~Device() {
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (auto &p : pending_) {
+        (void)hipEventDestroy(p.start);
+        (void)hipEventDestroy(p.stop);
+    }
+    for (auto e : event_pool_) (void)hipEventDestroy(e);
+    if (module_) (void)hipModuleUnload(module_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Device::activate() const { HBR_HIP(hipSetDevice(ordinal_)); }
+
+hipFunction_t Device::function(const char *kernel) {
+    auto it = functions_.find(kernel);
+    if (it != functions_.end()) return it->second;
+    hipFunction_t f;
+    hipError_t e = hipModuleGetFunction(&f, module_, kernel);
+    if (e != hipSuccess) fail(kDeviceError, std::string("kernel ") + kernel + " not in the code object");
+    functions_.emplace(kernel, f);
+    return f;
+}
+
+void Device::launch_raw(const char *kernel, dim3 grid, dim3 block, const void *args, size_t size) {
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) return;
+    hipFunction_t f = function(kernel);
+    (void)size;
+    // one by-value struct parameter: its address is the parameter's
+    void *params[] = {const_cast<void *>(args)};
+    const bool timed = profiling_ && std::strncmp(kernel, profile_prefix_.c_str(), profile_prefix_.size()) == 0;
+    Pending ev{};
+    if (timed) {
+        ev.start = take_event();
+        ev.stop = take_event();
+        HBR_HIP(hipEventRecord(ev.start, stream_));
+    }
+    HBR_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream_, params,
+                                  nullptr));
+    if (timed) {
+        HBR_HIP(hipEventRecord(ev.stop, stream_));
+        ev.name = kernel;
+        pending_.push_back(ev);
+    }
+}
+
+hipEvent_t Device::take_event() {
+    if (!event_pool_.empty()) {
+        hipEvent_t e = event_pool_.back();
+        event_pool_.pop_back();
+        return e;
+    }
+    hipEvent_t e;
+    HBR_HIP(hipEventCreate(&e));
+    return e;
+}
+
+void Device::sync() {
+    HBR_HIP(hipStreamSynchronize(stream_));
+    if (!pending_.empty()) drain_events();
+}
+
+void Device::drain_events() {
+    for (auto &p : pending_) {
+        float ms = 0.0f;
+        HBR_HIP(hipEventElapsedTime(&ms, p.start, p.stop));
+        auto &s = stats_[p.name];
+        s.total_ms += ms;
+        s.launches++;
+        event_pool_.push_back(p.start);
+        event_pool_.push_back(p.stop);
+    }
+    pending_.clear();
+}
+
+void Device::set_profiling(bool on, const std::string &prefix) {
+    sync();
+    profiling_ = on;
+    profile_prefix_ = prefix;
+}
+
+std::unordered_map<std::string, Device::KernelStat> Device::kernel_stats() {
+    sync();
+    return stats_;
+}
+
+void Device::reset_stats() {
+    sync();
+    stats_.clear();
+}
+
+static std::mutex g_devices_mu;
+static std::unordered_map<int, std::unique_ptr<Device>> g_devices;
+
+Device &device(int ordinal) {
+    std::lock_guard<std::mutex> lock(g_devices_mu);
+    auto it = g_devices.find(ordinal);
+    if (it != g_devices.end()) {
+        it->second->activate();
+        return *it->second;
+    }
+    auto d = std::make_unique<Device>(ordinal);
+    Device &ref = *d;
+    g_devices.emplace(ordinal, std::move(d));
+    return ref;
+}
+
+int device_count() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+Stage::~Stage() {
+    for (auto &b : blocks_) (void)hipHostFree(b.p);
+}
+
+void *Stage::alloc(size_t bytes) {
+    bytes = (bytes + 255) & ~size_t(255);
+    for (auto &b : blocks_) {
+        if (b.cap - b.used >= bytes) {
+            void *p = static_cast<char *>(b.p) + b.used;
+            b.used += bytes;
+            return p;
+        }
+    }
+    size_t cap = bytes > (size_t(1) << 20) ? bytes : (size_t(1) << 20);
+    void *p = nullptr;
+    HBR_HIP(hipHostMalloc(&p, cap, hipHostMallocDefault));
+    blocks_.push_back({p, cap, bytes});
+    return p;
+}
+
+void Stage::reset() {
+    for (auto &b : blocks_) b.used = 0;
+}
+
+}  // namespace hbr

@@ -1,0 +1,428 @@
+#include "trainer.h"
+
+#include <cfloat>
+#include <cmath>
+#include <cstring>
+#include <limits>
+
+namespace hbr {
+
+namespace {
+
+// total order of f64 (f64::total_cmp) as a signed key
+int64_t total_key(double x) {
+    int64_t b;
+    std::memcpy(&b, &x, 8);
+    return b ^ (int64_t)(((uint64_t)(b >> 63)) >> 1);
+}
+
+}  // namespace
+
+TreeBuilder::TreeBuilder(Engine &e, const GrowParams &p) : e_(e), p_(p) {}
+
+double TreeBuilder::deq_g(int64_t k) const { return std::ldexp((double)k, e_.scale().exp_g); }
+double TreeBuilder::deq_h(int64_t k) const { return std::ldexp((double)k, e_.scale().exp_h); }
+
+// The winner as the reference records it: SplitPos from the candidate's
+// place in its feature's order (forward bins, then the backward pass), the
+// children's statistics, bounded f32 weights, and BestSplit::valid
+// (builder/mod.rs:167-193).
+TreeBuilder::Decision TreeBuilder::decide(const Open &o) const {
+    Decision d;
+    if (!o.searched || o.best.index == 0xffffffffu) return d;
+    const ScanBest &b = o.best;
+    const auto &fo = e_.feature_offset();
+    const uint32_t f = b.feature, fs = fo[f], nb = fo[f + 1] - fs;
+    d.feature = f;
+    d.loss = (double)b.loss;
+    if (b.index < nb) {
+        d.bin = (int64_t)fs + b.index;
+        d.limit = b.index + 1;
+        d.default_left = 0;
+    } else {
+        const uint32_t off = nb - 1 - (b.index - nb);
+        d.bin = off == 0 ? -1 : (int64_t)fs + off - 1;
+        d.limit = off;
+        d.default_left = 1;
+    }
+    d.left = b.left;
+    d.right = b.right;
+    d.lg = deq_g(b.left.g);
+    d.lh = deq_h(b.left.h);
+    d.rg = deq_g(b.right.g);
+    d.rh = deq_h(b.right.h);
+    d.wl = xgb_weight(d.lg, d.lh, p_.reg, o.lower, o.upper);
+    d.wr = xgb_weight(d.rg, d.rh, p_.reg, o.lower, o.upper);
+    d.valid = d.loss > 1e-6 && d.loss >= p_.gamma && children_valid(d.lh, d.rh, p_.reg.min_child_weight);
+    return d;
+}
+
+LevelSplit TreeBuilder::expand(Tree &t, const Open &o, const Decision &d, double cb[4]) {
+    const int dir = d.feature < p_.monotone.size() ? p_.monotone[d.feature] : 0;
+    child_bounds(o.lower, o.upper, dir, (double)d.wl, (double)d.wr, cb);
+    TreeNode &n = t.nodes[o.nid];
+    n.split_feature = d.feature;
+    n.split_cond = d.bin >= 0 ? e_.cut_values()[d.bin] : -FLT_MAX;
+    n.default_left = (uint8_t)d.default_left;
+    n.split_bin = d.bin;
+    n.split_gain = (float)d.loss;
+    const int32_t left = (int32_t)t.nodes.size();
+    n.left = left;
+    n.right = left + 1;
+    TreeNode ln, rn;
+    ln.leaf_value = d.wl;
+    ln.sum_hess = (float)d.lh;
+    rn.leaf_value = d.wr;
+    rn.sum_hess = (float)d.rh;
+    t.nodes.push_back(ln);
+    t.nodes.push_back(rn);
+    g_.push_back(d.lg);
+    h_.push_back(d.lh);
+    lower_.push_back(cb[0]);
+    upper_.push_back(cb[1]);
+    g_.push_back(d.rg);
+    h_.push_back(d.rh);
+    lower_.push_back(cb[2]);
+    upper_.push_back(cb[3]);
+    LevelSplit s;
+    s.seg = o.seg;
+    s.parent_slot = o.slot;
+    s.feature = d.feature;
+    s.limit = d.limit;
+    s.default_left = d.default_left;
+    s.child_total[0] = d.left;
+    s.child_total[1] = d.right;
+    s.child_root_gain[0] = xgb_node_gain(d.lg, d.lh, p_.reg, cb[0], cb[1]);
+    s.child_root_gain[1] = xgb_node_gain(d.rg, d.rh, p_.reg, cb[2], cb[3]);
+    s.child_lower[0] = (float)cb[0];
+    s.child_upper[0] = (float)cb[1];
+    s.child_lower[1] = (float)cb[2];
+    s.child_upper[1] = (float)cb[3];
+    return s;
+}
+
+void TreeBuilder::leaf(const Open &o) {
+    leaves_.push_back({o.nid, o.seg});
+    if (o.has_slot) e_.free_slot(o.slot);
+}
+
+Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out) {
+    Tree t;
+    g_.clear();
+    h_.clear();
+    lower_.clear();
+    upper_.clear();
+    leaves_.clear();
+    const uint64_t limit = p_.max_depth;
+    e_.set_scan_params(ScanParams{p_.reg.lambda, p_.reg.alpha, p_.reg.max_delta_step, p_.reg.min_child_weight},
+                       p_.monotone);
+
+    // root (builder/hist/mod.rs:345-456): statistics, histogram, search
+    e_.begin_tree();
+    Open root{};
+    root.nid = 0;
+    root.depth = 0;
+    root.seg = Segment{0, (uint32_t)e_.n_rows(), 0};
+    root.total = e_.root_total(root.seg);
+    root.lower = -std::numeric_limits<double>::infinity();
+    root.upper = std::numeric_limits<double>::infinity();
+    const double rg = deq_g(root.total.g), rh = deq_h(root.total.h);
+    TreeNode rn;
+    rn.sum_hess = (float)rh;
+    t.nodes.push_back(rn);
+    g_.push_back(rg);
+    h_.push_back(rh);
+    lower_.push_back(root.lower);
+    upper_.push_back(root.upper);
+    if (limit > 0) {
+        root.slot = e_.alloc_slot();
+        root.has_slot = true;
+        e_.build_nodes({root.seg}, {root.slot});
+        ScanInput in{root.slot, root.total, xgb_node_gain(rg, rh, p_.reg, root.lower, root.upper),
+                     (float)root.lower, (float)root.upper};
+        root.best = e_.scan({in})[0];
+        root.searched = true;
+    }
+
+    if (p_.policy == HBR_GROW_DEPTHWISE) {
+        std::vector<Open> frontier{root};
+        uint64_t depth = 0;
+        while (depth < limit && !frontier.empty()) {
+            std::vector<LevelSplit> splits;
+            std::vector<std::pair<int32_t, int32_t>> ids;  // children's node ids
+            std::vector<Open> parents;
+            for (const Open &o : frontier) {
+                const Decision d = decide(o);
+                if (!d.valid) {
+                    leaf(o);
+                    continue;
+                }
+                double cb[4];
+                const int32_t left = (int32_t)t.nodes.size();
+                splits.push_back(expand(t, o, d, cb));
+                ids.push_back({left, left + 1});
+                parents.push_back(o);
+            }
+            const bool terminal = depth + 1 >= limit;
+            std::vector<LevelChild> kids = e_.level(splits, terminal);
+            std::vector<Open> next;
+            for (size_t i = 0; i < splits.size(); i++) {
+                for (int c = 0; c < 2; c++) {
+                    Open ch{};
+                    ch.nid = c == 0 ? ids[i].first : ids[i].second;
+                    ch.depth = depth + 1;
+                    ch.seg = kids[2 * i + c].seg;
+                    ch.total = splits[i].child_total[c];
+                    ch.lower = lower_[ch.nid];
+                    ch.upper = upper_[ch.nid];
+                    if (terminal) {
+                        leaves_.push_back({ch.nid, ch.seg});
+                    } else {
+                        ch.slot = kids[2 * i + c].slot;
+                        ch.has_slot = true;
+                        ch.best = kids[2 * i + c].best;
+                        ch.searched = true;
+                        next.push_back(ch);
+                    }
+                }
+                if (terminal && parents[i].has_slot) e_.free_slot(parents[i].slot);
+            }
+            frontier.swap(next);
+            depth++;
+        }
+        for (const Open &o : frontier) leaf(o);
+    } else {
+        // std::collections::BinaryHeap by best.loss_chg (total_cmp): push =
+        // sift_up; pop = swap-remove the root, sift_down_to_bottom, sift_up.
+        std::vector<Open> heap;
+        // a node without a candidate holds BestSplit::none, whose loss is 0
+        auto key = [&](const Open &o) -> int64_t {
+            return total_key(o.searched && o.best.index != 0xffffffffu ? (double)o.best.loss : 0.0);
+        };
+        auto sift_up = [&](size_t start, size_t pos) {
+            Open elem = heap[pos];
+            const int64_t k = key(elem);
+            while (pos > start) {
+                size_t parent = (pos - 1) / 2;
+                if (k <= key(heap[parent])) break;
+                heap[pos] = heap[parent];
+                pos = parent;
+            }
+            heap[pos] = elem;
+        };
+        auto push = [&](const Open &o) {
+            heap.push_back(o);
+            sift_up(0, heap.size() - 1);
+        };
+        auto pop = [&](Open *out) -> bool {
+            if (heap.empty()) return false;
+            Open item = heap.back();
+            heap.pop_back();
+            if (!heap.empty()) {
+                std::swap(item, heap[0]);
+                size_t end = heap.size(), pos = 0;
+                Open elem = heap[0];
+                size_t child = 1;
+                while (child + 2 <= end) {
+                    if (key(heap[child]) <= key(heap[child + 1])) child++;
+                    heap[pos] = heap[child];
+                    pos = child;
+                    child = 2 * pos + 1;
+                }
+                if (child == end - 1) {
+                    heap[pos] = heap[child];
+                    pos = child;
+                }
+                heap[pos] = elem;
+                sift_up(0, pos);
+            }
+            *out = item;
+            return true;
+        };
+        push(root);
+        uint64_t n_leaves = 1;
+        Open o;
+        while (pop(&o)) {
+            if (n_leaves >= p_.max_leaves) {
+                leaf(o);
+                break;
+            }
+            const Decision d = decide(o);
+            if (!(o.depth < limit && d.valid)) {
+                leaf(o);
+                continue;
+            }
+            double cb[4];
+            const int32_t left = (int32_t)t.nodes.size();
+            std::vector<LevelSplit> one{expand(t, o, d, cb)};
+            std::vector<LevelChild> kids = e_.level(one, false);
+            n_leaves++;
+            for (int c = 0; c < 2; c++) {
+                Open ch{};
+                ch.nid = left + c;
+                ch.depth = o.depth + 1;
+                ch.seg = kids[c].seg;
+                ch.slot = kids[c].slot;
+                ch.has_slot = true;
+                ch.total = one[0].child_total[c];
+                ch.lower = lower_[ch.nid];
+                ch.upper = upper_[ch.nid];
+                ch.best = kids[c].best;
+                ch.searched = true;
+                push(ch);
+            }
+        }
+        for (const Open &rest : heap) leaf(rest);
+    }
+
+    // finalize_leaf_values (builder/shared.rs:174-187), then scale_leaves(eta)
+    for (auto &lf : leaves_) {
+        TreeNode &n = t.nodes[lf.first];
+        const double w = calc_weight_bounded(g_[lf.first], h_[lf.first], p_.reg, lower_[lf.first], upper_[lf.first]);
+        n.leaf_value = (float)w * p_.eta;
+        n.left = n.right = -1;
+        n.split_bin = -2;
+        if (leaves_out) leaves_out->push_back({lf.second, n.leaf_value});
+    }
+    return t;
+}
+
+// ---- the boosting loop ----------------------------------------------------------
+
+static float weighted_label_mean(const float *labels, const float *weights, uint64_t n) {
+    double mean = 0.0;
+    if (weights) {
+        double sum_w = 0.0;
+        for (uint64_t i = 0; i < n; i++) sum_w += (double)weights[i];
+        if (sum_w > 0.0)
+            for (uint64_t i = 0; i < n; i++) mean += (double)labels[i] / sum_w * (double)weights[i];
+    } else if (n > 0) {
+        const double dn = (double)n;
+        for (uint64_t i = 0; i < n; i++) mean += (double)labels[i] / dn;
+    }
+    return (float)mean;
+}
+
+static float logit(float p) {
+    const float eps = 1e-6f;
+    p = p < eps ? eps : (p > 1.0f - eps ? 1.0f - eps : p);
+    return -std::log(1.0f / p - 1.0f);
+}
+
+std::vector<float> base_margins(const TrainParams &p, const float *labels, const float *weights, uint64_t n) {
+    if (p.objective == HBR_OBJ_SOFTMAX) {
+        const uint32_t k = p.num_class;
+        std::vector<float> m(k, 0.0f);
+        if (p.has_base_score) {
+            for (auto &v : m) v = p.base_score;
+            return m;
+        }
+        for (uint64_t i = 0; i < n; i++) {
+            if (labels[i] >= 0.0f && (uint32_t)labels[i] < k) m[(uint32_t)labels[i]] += weights ? weights[i] : 1.0f;
+        }
+        double sum_w = 0.0;
+        if (weights)
+            for (uint64_t i = 0; i < n; i++) sum_w += (double)weights[i];
+        else
+            sum_w = (double)(float)n;
+        const double inv = 1.0 / sum_w;
+        for (auto &v : m) v = std::log((float)((double)v * inv) + 1e-6f);
+        const float kf = (float)k;
+        float mean = -0.0f;
+        for (float v : m) mean += v / kf;
+        for (auto &v : m) v -= mean;
+        return m;
+    }
+    if (p.objective == HBR_OBJ_LOGISTIC)
+        return {p.has_base_score ? logit(p.base_score) : logit(weighted_label_mean(labels, weights, n))};
+    return {p.has_base_score ? p.base_score : weighted_label_mean(labels, weights, n)};
+}
+
+Trainer::Trainer(Engine &e, const TrainParams &p, const float *labels, const float *weights, uint64_t n)
+    : e_(e), p_(p), n_(n) {
+    if (n != e.n_rows()) fail(kInvalid, "trainer: one label per index row");
+    k_ = p.objective == HBR_OBJ_SOFTMAX ? p.num_class : 1;
+    if (k_ == 0) fail(kInvalid, "softmax needs num_class");
+    labels_.assign(labels, labels + n);
+    if (weights) weights_.assign(weights, weights + n);
+    base_ = base_margins(p, labels, weights, n);
+    std::vector<float> m((size_t)n * k_);
+    for (uint64_t r = 0; r < n; r++)
+        for (uint32_t c = 0; c < k_; c++) m[r * k_ + c] = base_[c];
+    e_.load_margins(m.data(), m.size(), k_);
+    e_.set_labels(labels, weights, n);
+}
+
+// simd/mod.rs:580-600, one row at a time: shift by max(f32::MIN_POSITIVE,
+// preds), sum of expf in f64, p = expf(x - wmax) / (f32)sum.
+void Trainer::softmax_gradients(std::vector<float> &out) {
+    std::vector<float> m((size_t)n_ * k_);
+    e_.read_margins(m.data(), m.size());
+    out.resize(2 * (size_t)n_ * k_);
+    const float min_hess = 1e-16f;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < (int64_t)n_; r++) {
+        const float *p = &m[(size_t)r * k_];
+        float wmax = FLT_MIN;
+        for (uint32_t c = 0; c < k_; c++) wmax = std::fmax(p[c], wmax);
+        double wsum = 0.0;
+        for (uint32_t c = 0; c < k_; c++) wsum += (double)std::exp(p[c] - wmax);
+        const float ws = (float)wsum;
+        const float w = weights_.empty() ? 1.0f : weights_[r];
+        const uint32_t label = (uint32_t)labels_[r];
+        for (uint32_t c = 0; c < k_; c++) {
+            const float pc = std::exp(p[c] - wmax) / ws;
+            const float h = std::fmax(2.0f * pc * (1.0f - pc) * w, min_hess);
+            const float g = c == label ? pc - 1.0f : pc;
+            out[2 * ((size_t)r * k_ + c)] = g * w;
+            out[2 * ((size_t)r * k_ + c) + 1] = h;
+        }
+    }
+}
+
+void Trainer::boost(uint64_t rounds) {
+    TreeBuilder b(e_, p_.grow);
+    for (uint64_t it = 0; it < rounds; it++) {
+        if (p_.objective == HBR_OBJ_SOFTMAX) {
+            std::vector<float> all, gk(2 * (size_t)n_);
+            softmax_gradients(all);
+            for (uint32_t c = 0; c < k_; c++) {
+                for (uint64_t r = 0; r < n_; r++) {
+                    gk[2 * r] = all[2 * (r * k_ + c)];
+                    gk[2 * r + 1] = all[2 * (r * k_ + c) + 1];
+                }
+                e_.prepare(gk.data(), n_);
+                std::vector<std::pair<Segment, float>> leaves;
+                trees_.push_back(b.grow(&leaves));
+                std::vector<Segment> segs;
+                std::vector<float> vals;
+                for (auto &l : leaves) {
+                    segs.push_back(l.first);
+                    vals.push_back(l.second);
+                }
+                e_.add_leaves(segs, vals, c);
+            }
+            continue;
+        }
+        hbr_device_loss loss{};
+        loss.kind = p_.objective == HBR_OBJ_LOGISTIC ? HBR_LOSS_LOGISTIC : HBR_LOSS_SQUARED_ERROR;
+        loss.scale_pos_weight = p_.scale_pos_weight;
+        loss.min_hess = 1e-16f;
+        loss.max_input = 80.0f;
+        loss.vector_rows = n_ >= 16 ? n_ - n_ % 8 : 0;
+        if (!e_.compute_gradients(loss, 0)) fail(kRefused, "a gradient is not finite: the round runs on the host");
+        std::vector<std::pair<Segment, float>> leaves;
+        trees_.push_back(b.grow(&leaves));
+        std::vector<Segment> segs;
+        std::vector<float> vals;
+        for (auto &l : leaves) {
+            segs.push_back(l.first);
+            vals.push_back(l.second);
+        }
+        e_.add_leaves(segs, vals, 0);
+    }
+}
+
+void Trainer::margins(float *out) { e_.read_margins(out, n_ * k_); }
+
+}  // namespace hbr

@@ -1,0 +1,124 @@
+// Tree growth and the boosting loop over the device engine.
+//
+// TreeBuilder restates the hist builder's orchestration
+// (builder/hist/mod.rs:261-573 host growth, hist/device.rs:147-696 device
+// growth): node ids in expansion order, the depthwise frontier and the
+// loss-guided heap, child bounds and statistics, terminal children at the
+// depth limit, and the final leaf values (builder/shared.rs:174-187). The
+// engine partitions, builds and searches whole levels; the host keeps the
+// tree and decides each expansion from the winners the device returns.
+//
+// Trainer restates a plain gbtree run (training/round.rs:105-148,
+// :214-424; training/train.rs:406-436): intercepts, then per iteration the
+// gradients of the device margins, one tree per output, and each leaf's
+// value added to its rows' margins.
+#pragma once
+#include <cstdint>
+#include <vector>
+
+#include "engine.h"
+#include "split_math.h"
+
+namespace hbr {
+
+struct TreeNode {
+    uint32_t split_feature = 0;
+    float split_cond = 0.0f;
+    uint8_t default_left = 1;
+    int32_t left = -1, right = -1;
+    float leaf_value = 0.0f, sum_hess = 0.0f, split_gain = 0.0f;
+    int64_t split_bin = -2;
+};
+
+struct Tree {
+    std::vector<TreeNode> nodes;
+};
+
+struct GrowParams {
+    Reg reg{1.0, 0.0, 0.0, 1.0};
+    double gamma = 0.0;
+    uint64_t max_depth = 6;    // UINT64_MAX: unbounded
+    uint64_t max_leaves = UINT64_MAX;
+    int policy = HBR_GROW_DEPTHWISE;
+    float eta = 0.3f;
+    std::vector<int8_t> monotone;
+};
+
+class TreeBuilder {
+public:
+    TreeBuilder(Engine &e, const GrowParams &p);
+    // Grow one tree from the staged gradients over every row; each leaf's
+    // segment and (eta-scaled) value go to `leaves`.
+    Tree grow(std::vector<std::pair<Segment, float>> *leaves);
+
+private:
+    struct Open {
+        int32_t nid;
+        uint64_t depth;
+        Segment seg;
+        uint32_t slot;
+        bool has_slot;
+        QBin total;
+        double lower, upper;
+        ScanBest best;
+        bool searched;
+    };
+    struct Decision {
+        bool valid = false;
+        uint32_t feature = 0;
+        int64_t bin = -1;
+        uint32_t limit = 0;
+        uint32_t default_left = 0;
+        QBin left{}, right{};
+        double lg = 0, lh = 0, rg = 0, rh = 0;
+        float wl = 0, wr = 0;
+        double loss = 0.0;
+    };
+    Decision decide(const Open &o) const;
+    // Expand node o by d: children appended to the tree; returns the level split.
+    LevelSplit expand(Tree &t, const Open &o, const Decision &d, double cb[4]);
+    void leaf(const Open &o);
+    double deq_g(int64_t k) const;
+    double deq_h(int64_t k) const;
+
+    Engine &e_;
+    GrowParams p_;
+    // per node id
+    std::vector<double> g_, h_, lower_, upper_;
+    std::vector<std::pair<int32_t, Segment>> leaves_;
+};
+
+struct TrainParams {
+    GrowParams grow;
+    int objective = HBR_OBJ_SQUARED_ERROR;
+    uint32_t num_class = 0;
+    float scale_pos_weight = 1.0f;
+    bool has_base_score = false;
+    float base_score = 0.5f;
+};
+
+class Trainer {
+public:
+    Trainer(Engine &e, const TrainParams &p, const float *labels, const float *weights, uint64_t n);
+    void boost(uint64_t rounds);
+    uint32_t outputs() const { return k_; }
+    const std::vector<float> &base_score() const { return base_; }
+    const std::vector<Tree> &trees() const { return trees_; }
+    void margins(float *out);
+
+private:
+    void softmax_gradients(std::vector<float> &gpair_all);
+
+    Engine &e_;
+    TrainParams p_;
+    uint32_t k_ = 1;
+    uint64_t n_;
+    std::vector<float> labels_, weights_;
+    std::vector<float> base_;
+    std::vector<Tree> trees_;
+};
+
+// The loss's intercepts (objective base margins, train.rs:406-436).
+std::vector<float> base_margins(const TrainParams &p, const float *labels, const float *weights, uint64_t n);
+
+}  // namespace hbr

@@ -1,0 +1,128 @@
+// Gradient kernels: squared error and the logistic loss, with the host's
+// exact f32 operations, plus the per-tree quantization scale.
+//
+// Squared error restates objective/regression.rs:42-58: w scaled by
+// scale_pos_weight for a label of exactly 1, g = (p - y) w, h = w.
+//
+// The logistic loss restates the reference's AVX2/FMA vector kernel
+// (simd/x86_64.rs:22-160) one lane per row: a row belongs to the 8-row
+// vector [8k, 8k + 8) and takes the polynomial path only when every margin
+// of that vector is finite with magnitude <= 80 and the vector lies below
+// vec_rows (simd/mod.rs:57-66). Each intrinsic becomes the same single IEEE
+// f32 operation: _mm256_fmadd_ps/_fnmadd_ps are fmaf, _mm256_cvtps_epi32 is
+// round-to-nearest-even, divisions are correctly rounded. Rows outside that
+// path use libm's expf on the host; the kernel lists them instead.
+#include "common.h"
+
+namespace hbr {
+
+// Exponential of x in [-80, 0] as simd/x86_64.rs:22-51 computes it.
+__device__ __forceinline__ float exp_vector(float x) {
+    float t = x * 1.44269504088896341f;
+    int k = (int)__builtin_rintf(t);
+    float kf = (float)k;
+    float r = __builtin_fmaf(-kf, 0.6933594f, x);
+    r = __builtin_fmaf(kf, 2.1219444e-4f, r);
+    float r2 = r * r;
+    float r4 = r2 * r2;
+    float p0 = 1.0f + r;
+    float p1 = __builtin_fmaf(1.0f / 6.0f, r, 0.5f);
+    float p2 = __builtin_fmaf(1.0f / 120.0f, r, 1.0f / 24.0f);
+    float p3 = __builtin_fmaf(1.0f / 5040.0f, r, 1.0f / 720.0f);
+    float lo = __builtin_fmaf(p1, r2, p0);
+    float hi = __builtin_fmaf(p3, r2, p2);
+    float poly = __builtin_fmaf(hi, r4, lo);
+    uint32_t bits = (uint32_t)(k + 127) << 23;
+    return poly * __uint_as_float(bits);
+}
+
+__device__ __forceinline__ void fold_max(QScale *s, float g, float h, bool active) {
+    uint32_t mg = active ? (__float_as_uint(g) & 0x7fffffffu) : 0u;
+    uint32_t mh = active ? (__float_as_uint(h) & 0x7fffffffu) : 0u;
+    bool bad = active && (!__builtin_isfinite(g) || !__builtin_isfinite(h));
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        mg = max(mg, (uint32_t)__shfl_xor((int)mg, d, kWave));
+        mh = max(mh, (uint32_t)__shfl_xor((int)mh, d, kWave));
+    }
+    uint64_t nb = __ballot(bad);
+    if (lane_id() == 0) {
+        if (mg) atomicMax(&s->max_g_bits, mg);
+        if (mh) atomicMax(&s->max_h_bits, mh);
+        if (nb) atomicAdd(&s->nonfinite, (uint32_t)__popcll(nb));
+    }
+}
+
+}  // namespace hbr
+
+using namespace hbr;
+
+extern "C" __global__ __launch_bounds__(256) void hbr_gradients(GradArgs a) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool active = i < a.n;
+    float m = active ? a.margins[i] : 0.0f;
+    float y = active ? a.labels[i] : 0.0f;
+    float w = (active && a.weights) ? a.weights[i] : 1.0f;
+    float g = 0.0f, h = 0.0f;
+    bool host_row = false;
+    if (a.loss == kSquaredError) {
+        if (y == 1.0f) w *= a.scale_pos_weight;
+        g = (m - y) * w;
+        h = w;
+    } else {
+        bool ok = active && __builtin_fabsf(m) <= a.max_input;
+        uint64_t ballot = __ballot(ok || !active);
+        uint64_t group = 0xffull << (lane_id() & ~7u);
+        bool vector = active && i < a.vec_rows && (ballot & group) == group;
+        if (vector) {
+            float e = exp_vector(0.0f - __builtin_fabsf(m));
+            float den = 1.0f + e;
+            float pos = 1.0f / den;
+            float neg = e / den;
+            float p = m >= 0.0f ? pos : neg;
+            float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
+            g = (p - y) * ww;
+            float q = p * (1.0f - p);
+            h = (q > a.min_hess ? q : a.min_hess) * ww;
+        } else if (active) {
+            host_row = true;
+        }
+    }
+    if (active) {
+        if (host_row) {
+            uint32_t slot = atomicAdd(&a.scale->scalar_rows, 1u);
+            a.scalar_list[slot] = i;
+            a.gpair[i] = GPair{0.0f, 0.0f};
+        } else {
+            a.gpair[i] = GPair{g, h};
+        }
+    }
+    fold_max(a.scale, g, h, active && !host_row);
+}
+
+extern "C" __global__ __launch_bounds__(256) void hbr_iota(IotaArgs a) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.n) a.rows[i] = a.first + i;
+}
+
+// Root statistics: the exact integer sums of the quantized pairs of a
+// segment (order-free, so any launch shape gives the same totals).
+extern "C" __global__ __launch_bounds__(256) void hbr_total(TotalArgs a) {
+    const int eg = a.scale->exp_g, eh = a.scale->exp_h;
+    int64_t sg = 0, sh = 0;
+    for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < a.n; j += gridDim.x * blockDim.x) {
+        uint32_t r = a.rows ? a.rows[j] : a.first + j;
+        GPair p = a.gpair[r];
+        sg += quantize(p.g, eg);
+        sh += quantize(p.h, eh);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        sg += __shfl_xor(sg, d, kWave);
+        sh += __shfl_xor(sh, d, kWave);
+    }
+    if (lane_id() == 0) {
+        atomicAdd((unsigned long long *)&a.out->g, (unsigned long long)sg);
+        atomicAdd((unsigned long long *)&a.out->h, (unsigned long long)sh);
+    }
+}

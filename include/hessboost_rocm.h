@@ -1,0 +1,382 @@
+/*
+ * hessboost-rocm: the MI355X (gfx950) hist backend's C ABI.
+ *
+ * The drop-in boundary for hessboost's `tree_method=hist` path. A Rust
+ * shim implements the reference's two backend traits over these calls:
+ *
+ *   HistogramBackend   src/tree/hist/mod.rs:73-105
+ *   RowEngine          src/tree/hist/mod.rs:213-295
+ *   GpuModel           src/backend/cuda/predict.rs:401-520 (BoostedModel::to_cuda)
+ *
+ * plus the index and cut construction the trainer runs once per dataset
+ * (src/data/quantile.rs:65-78, src/data/ghist.rs:213-257) and a whole
+ * device-resident boosting loop (src/training/round.rs:105-148).
+ *
+ * Conventions. Every call returns an int status:
+ *   HBR_OK           the call ran;
+ *   HBR_REFUSED      the device does not run this call for these inputs and
+ *                    changed nothing: the caller does the work itself (the
+ *                    traits' `None`);
+ *   HBR_DEVICE_ERROR a HIP error: the handle is poisoned and refuses every
+ *                    later call (the CUDA backend's sticky `failed` flag,
+ *                    src/backend/cuda/mod.rs:1806-1826);
+ *   HBR_INVALID      malformed arguments.
+ * hbr_last_error() returns the calling thread's last message. All pointers
+ * are host pointers unless a parameter says "device". Handles are safe to
+ * use from several threads: each serializes behind its own mutex. No call
+ * invokes the caller back.
+ */
+#ifndef HESSBOOST_ROCM_H
+#define HESSBOOST_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HBR_OK 0
+#define HBR_REFUSED 1
+#define HBR_DEVICE_ERROR 2
+#define HBR_INVALID 3
+
+/* The calling thread's last error message (empty after success). Writes at
+ * most len bytes including the terminator; returns the full length. */
+size_t hbr_last_error(char *buf, size_t len);
+
+/* Number of ROCm devices visible to the process. */
+int hbr_device_count(int *count);
+
+/* ------------------------------------------------------------------------- */
+/* Cuts and binned index (host; once per dataset).                            */
+/* ------------------------------------------------------------------------- */
+
+typedef struct hbr_cuts hbr_cuts;
+typedef struct hbr_index hbr_index;
+
+/* HistCuts::from_dmatrix (src/data/quantile.rs:65-78): per-feature cuts from
+ * XGBoost's weighted quantile sketch (src/data/sketch.rs:480-708) over a
+ * dense row-major f32 matrix; cells equal to `missing` (any NaN when missing
+ * is NaN) are absent. weights may be NULL. */
+int hbr_cuts_from_dense(const float *x, uint64_t n_rows, uint64_t n_cols, uint32_t max_bin,
+                        const float *weights, float missing, hbr_cuts **out);
+/* The same over CSR storage (row_ptr[n_rows+1], col, val); every stored
+ * entry is present. */
+int hbr_cuts_from_csr(const uint64_t *row_ptr, const uint32_t *col, const float *val,
+                      uint64_t n_rows, uint64_t n_cols, uint32_t max_bin, const float *weights,
+                      hbr_cuts **out);
+/* Cuts given by the caller (feature_offset[n_cols+1], cut_values). */
+int hbr_cuts_from_values(const uint32_t *feature_offset, const float *cut_values, uint64_t n_cols,
+                         hbr_cuts **out);
+int hbr_cuts_info(const hbr_cuts *c, uint64_t *n_cols, uint64_t *total_bins);
+int hbr_cuts_copy(const hbr_cuts *c, uint32_t *feature_offset, float *cut_values);
+void hbr_cuts_free(hbr_cuts *c);
+
+/* GHistIndex::from_dmatrix (src/data/ghist.rs:213-257): global row bins
+ * (u16 up to 65,536 bins, else u32), feature-major local columns when at
+ * least half full (u8/u16/u32 by the widest feature) with a missing bitmap
+ * when any cell is missing, and the `dense` flag. The index keeps its own
+ * copy of the cuts. */
+int hbr_index_from_dense(const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                         const hbr_cuts *cuts, hbr_index **out);
+int hbr_index_from_csr(const uint64_t *row_ptr, const uint32_t *col, const float *val,
+                       uint64_t n_rows, uint64_t n_cols, const hbr_cuts *cuts, hbr_index **out);
+void hbr_index_free(hbr_index *ix);
+
+/* A binned index as the reference's GHistIndex lays it out
+ * (src/data/ghist.rs:195-209, :315-360). */
+typedef struct hbr_index_desc {
+    uint64_t n_rows;
+    uint64_t n_cols;
+    const uint32_t *feature_offset; /* n_cols + 1: feature f owns global bins [fo[f], fo[f+1]) */
+    const float *cut_values;        /* fo[n_cols] cut values */
+    const uint64_t *row_ptr;        /* n_rows + 1 */
+    const void *row_bins;           /* row_ptr[n_rows] global bins */
+    uint32_t row_bin_width;         /* 2 (u16) or 4 (u32) */
+    uint32_t dense;                 /* every row holds every feature in feature order */
+    const void *col_bins;           /* feature-major local bins [f][r], or NULL */
+    uint32_t col_bin_width;         /* 1, 2 or 4 */
+    uint32_t pad;
+    const uint64_t *missing;        /* ceil(n_rows/64) words per feature, bit set = missing; or NULL */
+} hbr_index_desc;
+
+/* A read-only view of an index built by hbr_index_from_* (valid while it lives). */
+int hbr_index_describe(const hbr_index *ix, hbr_index_desc *out);
+
+/* ------------------------------------------------------------------------- */
+/* The engine: HistogramBackend + RowEngine over one index on one device.    */
+/* ------------------------------------------------------------------------- */
+
+typedef struct hbr_engine hbr_engine;
+
+/* CudaHistBackend::new(index, ordinal) (src/backend/cuda/mod.rs:1626-1671):
+ * upload the index and re-encode it on the device. */
+int hbr_engine_open(int ordinal, const hbr_index_desc *index, hbr_engine **out);
+void hbr_engine_close(hbr_engine *e);
+
+/* HistogramBackend::prepare (src/tree/hist/mod.rs:96): stage a tree's
+ * gradient pairs (interleaved g, h f32; one per index row). */
+int hbr_prepare(hbr_engine *e, const float *gpair, uint64_t n);
+
+/* HistogramBackend::build (src/tree/hist/mod.rs:76): the histogram of
+ * `rows` (ascending, distinct) from the staged gradients; out holds
+ * 2 * total_bins f64 (g, h interleaved), overwritten. Each bin is the exact
+ * sum of its rows' fixed-point gradients, converted to f64. */
+int hbr_build(hbr_engine *e, const uint32_t *rows, uint64_t m, double *out);
+
+/* A node's rows on the device (the reference's Segment, src/tree/hist/mod.rs:107-164):
+ * issued by the engine, stamped with its tree. */
+typedef struct hbr_segment {
+    uint64_t offset;
+    uint64_t len;
+    uint32_t buffer;
+    uint32_t contiguous;
+    uint64_t tree;
+} hbr_segment;
+
+/* RowEngine::begin_tree: every index row (in order) as the root segment.
+ * The reference's `rows` argument is the full ascending row list of an
+ * unsampled tree; other row lists are refused. */
+int hbr_begin_tree(hbr_engine *e, uint64_t n_rows, hbr_segment *root);
+
+/* RowEngine::root_total: the segment's statistics (f64 of the exact
+ * fixed-point sums). */
+int hbr_root_total(hbr_engine *e, const hbr_segment *seg, double out[2]);
+
+/* One split to partition (RowSplit, src/tree/hist/mod.rs:180-190): present
+ * feature-local bins below `below` go left, missing values follow
+ * default_left. */
+typedef struct hbr_row_split {
+    hbr_segment seg;
+    uint32_t feature;
+    uint32_t below;
+    uint32_t default_left;
+    uint32_t pad;
+} hbr_row_split;
+
+typedef struct hbr_partitioned {
+    hbr_segment left;
+    hbr_segment right;
+} hbr_partitioned;
+
+/* RowEngine::partition: stable, in one batch; the children replace the
+ * consumed segments. */
+int hbr_partition(hbr_engine *e, const hbr_row_split *splits, uint64_t n, hbr_partitioned *out);
+
+/* RowEngine::histograms: out holds n * 2 * total_bins f64. */
+int hbr_histograms(hbr_engine *e, const hbr_segment *segs, uint64_t n, double *out);
+
+/* RowEngine::rows: the row ids of one segment (len entries). */
+int hbr_rows(hbr_engine *e, const hbr_segment *seg, uint32_t *out);
+
+/* RowEngine::load_margins: start a margin run (n_rows * n_outputs f32). */
+int hbr_load_margins(hbr_engine *e, const float *margins, uint64_t n, uint32_t n_outputs);
+
+/* The device loss (DeviceLoss, src/tree/hist/mod.rs:355-365). */
+#define HBR_LOSS_SQUARED_ERROR 0
+#define HBR_LOSS_LOGISTIC 1
+typedef struct hbr_device_loss {
+    uint32_t kind;
+    float scale_pos_weight;
+    float min_hess;         /* logistic: 1e-16 */
+    float max_input;        /* logistic: the vector kernel's range, 80 */
+    uint64_t vector_rows;   /* logistic: rows the host runs 8-wide (VectorSplit.rows) */
+} hbr_device_loss;
+
+/* RowEngine::gradients: the loss's gradients of the device margins, with the
+ * host's bits; labels (and weights, may be NULL) are copied on the first
+ * call after hbr_load_margins. all_finite = 0 when a gradient is not finite. */
+int hbr_gradients(hbr_engine *e, const hbr_device_loss *loss, const float *labels,
+                  const float *weights, uint64_t n, int *all_finite);
+
+/* The staged gradient pairs (interleaved g, h; n = n_rows), for checking a
+ * device loss against the host's bits. No counterpart in the reference:
+ * a diagnostic read of what hbr_gradients / hbr_prepare staged. */
+int hbr_read_gradients(hbr_engine *e, float *out, uint64_t n);
+
+/* RowEngine::add_leaf_values: margins[row] += value for each leaf's rows. */
+int hbr_add_leaf_values(hbr_engine *e, const hbr_segment *segs, const float *values, uint64_t n);
+
+/* RowEngine::read_margins. */
+int hbr_read_margins(hbr_engine *e, float *out, uint64_t n);
+
+/* RowEngine::reserve_hists: fits = 0 (nothing reserved) when `slots`
+ * histograms do not fit. */
+int hbr_reserve_hists(hbr_engine *e, uint64_t slots, int *fits);
+
+/* RowEngine::build_resident: build each node's histogram into its slot,
+ * then turn each (parent, built) pair's parent slot into parent - built. */
+int hbr_build_resident(hbr_engine *e, const hbr_segment *segs, const uint32_t *slots, uint64_t n,
+                       const uint32_t *sibling_parent, const uint32_t *sibling_built, uint64_t n_siblings);
+
+/* The split-search regularization (RegParams, src/tree/gain.rs:63-89; values
+ * already rounded to f32 and widened). */
+typedef struct hbr_reg_params {
+    double lambda;
+    double alpha;
+    double max_delta_step;
+    double min_child_weight;
+} hbr_reg_params;
+
+/* ScanRequest (src/tree/hist/mod.rs:304-311). `directions` may be NULL
+ * (no monotone constraints); features must list every feature 0..n_cols-1.
+ * The engine sums in fixed point: when has_fixed is set, fixed_g/fixed_h
+ * are the node's exact sums as an earlier call returned them (preferred);
+ * otherwise the f64 totals are converted, which is exact while they hold
+ * at most 53 significant bits of the tree's fixed-point unit. */
+typedef struct hbr_scan_request {
+    uint32_t slot;
+    uint32_t has_fixed;
+    double total_g;
+    double total_h;
+    int64_t fixed_g;
+    int64_t fixed_h;
+    float root_gain;
+    float lower;
+    float upper;
+    uint32_t n_features;
+    const uint32_t *features;
+    const int8_t *directions;
+} hbr_scan_request;
+
+/* NodeScan (src/tree/hist/mod.rs:327-350). */
+#define HBR_SCAN_EMPTY 0
+#define HBR_SCAN_NUMERIC 2
+typedef struct hbr_node_scan {
+    uint32_t kind;
+    uint32_t feature;
+    float loss_chg;
+    uint32_t backward;      /* the winner came from the missing-left pass */
+    uint32_t offset;        /* forward: last local bin going left; backward: first local bin going right */
+    uint32_t pad;
+    double acc_g, acc_h;    /* the pass's accumulated statistics (left forward, right backward) */
+    double left_g, left_h, right_g, right_h;
+    int64_t fixed_left_g, fixed_left_h, fixed_right_g, fixed_right_h; /* exact sums */
+} hbr_node_scan;
+
+/* RowEngine::root_total with the exact fixed-point sums as well. */
+int hbr_root_total_fixed(hbr_engine *e, const hbr_segment *seg, double out[2], int64_t fixed[2]);
+
+/* RowEngine::scan_resident. */
+int hbr_scan_resident(hbr_engine *e, const hbr_reg_params *reg, const hbr_scan_request *requests,
+                      uint64_t n, hbr_node_scan *out);
+
+/* RowEngine::read_hist: 2 * total_bins f64. */
+int hbr_read_hist(hbr_engine *e, uint32_t slot, double *out);
+
+/* Work counters since the engine opened (no counterpart in the reference;
+ * they give the algorithmic bytes the roofline figures divide by). */
+typedef struct hbr_engine_counters {
+    uint64_t hist_nodes;       /* node histograms built (siblings excluded) */
+    uint64_t hist_rows;        /* rows summed into them */
+    uint64_t hist_bytes;       /* algorithmic bytes: rows * (bin bytes + 8 (+ 4 gathered)) */
+    uint64_t partition_rows;   /* rows routed */
+    uint64_t trees;
+} hbr_engine_counters;
+int hbr_engine_counters_read(hbr_engine *e, hbr_engine_counters *out);
+
+/* Per-kernel device time (HIP events on the engine's stream); profiling is
+ * off until enabled. buf receives "name=ms,launches;..." */
+int hbr_set_profiling(hbr_engine *e, int on, const char *kernel_prefix);
+int hbr_kernel_stats(hbr_engine *e, char *buf, size_t len);
+
+/* ------------------------------------------------------------------------- */
+/* Device-resident training (src/training/round.rs:105-148, grow_round).     */
+/* ------------------------------------------------------------------------- */
+
+#define HBR_OBJ_SQUARED_ERROR 0
+#define HBR_OBJ_LOGISTIC 1
+#define HBR_OBJ_SOFTMAX 2
+#define HBR_GROW_DEPTHWISE 0
+#define HBR_GROW_LOSSGUIDE 1
+
+/* TrainingParams fields of the path (src/config/params.rs:415-674). */
+typedef struct hbr_train_params {
+    double eta, gamma, lambda, alpha, min_child_weight, max_delta_step;
+    int64_t max_depth;       /* <= 0: unbounded */
+    int64_t max_leaves;      /* <= 0: unbounded */
+    int32_t grow_policy;
+    int32_t objective;
+    int32_t num_class;
+    float scale_pos_weight;
+    const int8_t *monotone;  /* per feature or NULL */
+    uint64_t n_monotone;
+    float base_score;
+    int32_t has_base_score;
+} hbr_train_params;
+
+typedef struct hbr_trainer hbr_trainer;
+
+int hbr_trainer_create(hbr_engine *e, const hbr_train_params *p, const float *labels,
+                       const float *weights, uint64_t n_rows, hbr_trainer **out);
+/* Run `rounds` boosting iterations. */
+int hbr_trainer_boost(hbr_trainer *t, uint64_t rounds);
+int hbr_trainer_num_trees(hbr_trainer *t, uint64_t *n);
+int hbr_trainer_num_outputs(hbr_trainer *t, uint32_t *k);
+int hbr_trainer_base_score(hbr_trainer *t, float *out);
+/* Tree t's node count. */
+int hbr_trainer_tree_size(hbr_trainer *t, uint64_t tree, uint64_t *n_nodes);
+/* A tree in the reference's Node layout (src/tree/regtree.rs:38-66), one
+ * array per field (n_nodes each). split_bin receives each split's global bin
+ * (-1 below every bin, -2 for leaves). */
+int hbr_trainer_tree(hbr_trainer *t, uint64_t tree, uint32_t *split_feature, float *split_cond,
+                     uint8_t *default_left, int32_t *left, int32_t *right, float *leaf_value,
+                     float *sum_hess, float *split_gain, int64_t *split_bin);
+/* The training margins (n_rows * n_outputs). */
+int hbr_trainer_margins(hbr_trainer *t, float *out);
+void hbr_trainer_free(hbr_trainer *t);
+
+/* ------------------------------------------------------------------------- */
+/* Batch prediction (GpuModel, src/backend/cuda/predict.rs:401-520).          */
+/* ------------------------------------------------------------------------- */
+
+typedef struct hbr_forest hbr_forest;
+
+/* A scalar-leaf numeric forest: per tree its nodes in the reference's
+ * layout; tree t adds tree_weight[t] * leaf to output tree_output[t]. */
+typedef struct hbr_forest_desc {
+    uint64_t n_trees;
+    const uint64_t *tree_offset;    /* n_trees + 1 */
+    const uint32_t *split_feature;
+    const float *split_cond;
+    const uint8_t *default_left;
+    const int32_t *left;
+    const int32_t *right;
+    const float *leaf_value;
+    const float *tree_weight;       /* n_trees */
+    const uint32_t *tree_output;    /* n_trees */
+    uint32_t n_outputs;
+    uint32_t pad;
+    const float *base_score;        /* n_outputs */
+} hbr_forest_desc;
+
+/* BoostedModel::to_cuda: upload the forest once. */
+int hbr_forest_upload(int ordinal, const hbr_forest_desc *fd, hbr_forest **out);
+void hbr_forest_free(hbr_forest *f);
+
+/* GpuModel::predict_margin over host rows (n_rows x n_cols f32, row-major;
+ * `missing` as for the matrix): out[n_rows * n_outputs]. */
+int hbr_predict_margin(hbr_forest *f, const float *x, uint64_t n_rows, uint64_t n_cols,
+                       float missing, float *out);
+/* The same over device memory (x, out and optional leaf ids [n_rows * n_trees]
+ * all device pointers): inputs already resident, nothing copied. */
+int hbr_predict_margin_device(hbr_forest *f, const float *x, uint64_t n_rows, uint64_t n_cols,
+                              float missing, float *out, int32_t *leaf_out);
+/* BoostedModel::predict_leaf: each row's leaf node id per tree (host). */
+int hbr_predict_leaf(hbr_forest *f, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                     int32_t *out);
+int hbr_forest_set_profiling(hbr_forest *f, int on, const char *kernel_prefix);
+int hbr_forest_kernel_stats(hbr_forest *f, char *buf, size_t len);
+
+/* Device memory for callers that keep inputs resident (bytes on device
+ * `ordinal`). */
+int hbr_device_alloc(int ordinal, uint64_t bytes, void **out);
+int hbr_device_free(int ordinal, void *p);
+int hbr_device_upload(int ordinal, void *dst, const void *src, uint64_t bytes);
+int hbr_device_download(int ordinal, void *dst, const void *src, uint64_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -363,6 +363,10 @@ def forest_arrays(trees, tree_weight=None, tree_output=None, n_outputs=1, base_s
     off = [0]
     feat, cond, dl, left, right, leaf = [], [], [], [], [], []
     for t in trees:
+        if isinstance(t, dict):  # one array per field
+            t = [dict(split_feature=int(t["split_feature"][i]), split_cond=float(t["split_cond"][i]),
+                      default_left=bool(t["default_left"][i]), left=int(t["left"][i]), right=int(t["right"][i]),
+                      leaf_value=float(t["leaf_value"][i])) for i in range(len(t["left"]))]
         for nd in t:
             feat.append(nd["split_feature"])
             cond.append(nd["split_cond"])

@@ -1,0 +1,71 @@
+"""The product's host cuts and binned index equal the oracle's restatement
+bit for bit (HistCuts, src/data/quantile.rs:65-296; GHistIndex,
+src/data/ghist.rs:213-257), on dense, missing, weighted and CSR data."""
+import numpy as np
+import pytest
+
+import hessboost_amd as hb
+from oracle import oracle as O
+
+
+def _compare(x=None, csr=None, n_cols=None, max_bin=256, weights=None, missing=np.nan):
+    if csr is not None:
+        ref = O.Dataset(csr=csr, n_cols=n_cols, max_bin=max_bin, weights=weights)
+        cuts = hb.Cuts.from_csr(*csr, n_cols, max_bin=max_bin, weights=weights)
+        ix = hb.BinnedIndex(cuts, csr=csr, n_cols=n_cols)
+    else:
+        ref = O.Dataset(x, max_bin=max_bin, weights=weights, missing=missing)
+        cuts = hb.Cuts.from_dense(x, max_bin=max_bin, weights=weights, missing=missing)
+        ix = hb.BinnedIndex(cuts, x=x, missing=missing)
+    fo, cv = cuts.arrays()
+    assert np.array_equal(fo, ref.feature_offset)
+    assert np.array_equal(cv.view(np.uint32), ref.cut_values.view(np.uint32))
+    rp, rb = ix.row_bins()
+    rrp, rrb = ref.row_bins()
+    assert np.array_equal(rp, rrp.astype(np.uint64)) and np.array_equal(rb, rrb)
+    assert ix.dense == ref.dense
+    c, rc = ix.columns(), ref.columns()
+    assert (c is None) == (rc is None)
+    if c is not None:
+        assert np.array_equal(c[0], rc[0])
+        assert (c[1] is None) == (rc[1] is None)
+        if c[1] is not None:
+            assert np.array_equal(c[1], rc[1])
+
+
+def test_dense_continuous():
+    rng = np.random.default_rng(10)
+    _compare(rng.standard_normal((50_000, 6), dtype=np.float32), max_bin=256)
+    _compare(rng.standard_normal((20_000, 3), dtype=np.float32), max_bin=16)
+
+
+def test_dense_with_missing_and_repeats():
+    rng = np.random.default_rng(11)
+    x = np.round(rng.standard_normal((30_000, 5)) * 3).astype(np.float32)
+    x[rng.random(x.shape) < 0.2] = np.nan
+    x[:, 4] = 7.0
+    _compare(x, max_bin=64)
+
+
+def test_weighted():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((20_000, 4), dtype=np.float32)
+    w = rng.random(20_000).astype(np.float32) * 3
+    _compare(x, weights=w, max_bin=32)
+
+
+def test_custom_missing_marker():
+    rng = np.random.default_rng(13)
+    x = rng.integers(-3, 4, (5_000, 3)).astype(np.float32)
+    _compare(x, missing=0.0, max_bin=256)
+
+
+def test_csr_sparse():
+    from hessboost_amd import synthetic
+    (rp, col, val), _, f = synthetic.sparse_wide(n=3_000, f=200, density=0.1, seed=3)
+    _compare(csr=(rp, col, val), n_cols=f, max_bin=64)
+
+
+def test_four_features_golden_data():
+    from tests.helpers import four_features
+    _compare(four_features(), max_bin=256)

@@ -1,0 +1,71 @@
+"""GPU batch prediction against the reference's recorded margins and the oracle."""
+import numpy as np
+import pytest
+
+import hessboost_amd as hb
+from hessboost_amd import synthetic
+from oracle import oracle as O
+from tests.helpers import four_features, golden_forest, load_saved_models
+
+pytestmark = pytest.mark.gpu
+
+CASES = ["early_stopping", "dart", "multiclass_forest", "quantiles", "expectiles", "aft", "dist_normal",
+         "dist_negbinomial", "multi_target"]
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_saved_models_reproduce_recorded_margins(name):
+    """tests/native_format.rs:822-860: recorded f32 margins, bit for bit."""
+    saved = load_saved_models()
+    x = four_features()
+    for ver in ("0.2.0", "0.4.3", "0.4.9"):
+        case = saved[f"{ver}/{name}"]
+        arrs = golden_forest(case)
+        f = hb.Forest(arrs, case["n_outputs"])
+        got = f.predict_margin(x)
+        assert np.array_equal(got.view(np.uint32), np.array(case["margins"], np.uint32)), f"{ver}/{name}"
+
+
+def test_synthetic_forest_leaves_and_margins_match_oracle():
+    trees = synthetic.forest(n_trees=50, depth=8, n_features=100, seed=7)
+    x = synthetic.predict_rows(n=20_000, f=100, seed=8)
+    arrs = O.forest_arrays(trees)
+    want, want_leaf = O.predict_margin(arrs, x, with_leaf=True)
+    f = hb.Forest(arrs, 1)
+    got = f.predict_margin(x)
+    leaf = f.predict_leaf(x)
+    assert np.array_equal(leaf, want_leaf)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_device_resident_prediction():
+    trees = synthetic.forest(n_trees=20, depth=6, n_features=30, seed=9)
+    x = synthetic.predict_rows(n=5_000, f=30, seed=10)
+    arrs = O.forest_arrays(trees)
+    want = O.predict_margin(arrs, x)
+    f = hb.Forest(arrs, 1)
+    dx = hb.DeviceBuffer(x.nbytes)
+    dx.upload(x)
+    dout = hb.DeviceBuffer(4 * len(x))
+    f.predict_margin_device(dx.ptr, len(x), 30, dout.ptr)
+    got = dout.download(np.float32, len(x))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_trained_model_predictions_match_training_margins():
+    x, y = synthetic.regression_100k(n=5_000, f=8, seed=11)
+    dm = hb.DMatrix(x, label=y)
+    params = {"max_depth": 4}
+    index = dm.index(256)
+    eng = hb.Engine(index)
+    t = hb.Trainer(eng, params, y)
+    t.boost(5)
+    model = t.booster(8)
+    assert np.array_equal(model.predict(x, output_margin=True).view(np.uint32), t.margins().view(np.uint32))
+
+
+def test_malformed_forest_is_refused():
+    arrs = O.forest_arrays([[dict(split_feature=0, split_cond=0.0, default_left=True, left=0, right=0,
+                                  leaf_value=0.0)]])
+    with pytest.raises(hb.HbrError):
+        hb.Forest(arrs, 1)

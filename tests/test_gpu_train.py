@@ -1,0 +1,100 @@
+"""GPU training parity: whole trees and boosting runs against the oracle and
+the reference's own saved model."""
+import numpy as np
+import pytest
+
+import hessboost_amd as hb
+from hessboost_amd import synthetic
+from oracle import oracle as O
+from tests.helpers import four_features, load_saved_models, train_labels
+
+pytestmark = pytest.mark.gpu
+
+
+def compare_trees(gpu_trees, ref_trees, leaf_rtol=1e-5, exact=False):
+    """Identical structure (split feature, threshold, default direction,
+    children), leaf values within leaf_rtol (bit-exact when `exact`)."""
+    assert len(gpu_trees) == len(ref_trees)
+    for t, (g, r) in enumerate(zip(gpu_trees, ref_trees)):
+        assert len(g["left"]) == len(r), f"tree {t}: node count"
+        for i, nd in enumerate(r):
+            assert g["left"][i] == nd["left"] and g["right"][i] == nd["right"], (t, i)
+            if nd["left"] != -1:
+                assert g["split_feature"][i] == nd["split_feature"], (t, i)
+                assert np.float32(g["split_cond"][i]) == np.float32(nd["split_cond"]), (t, i)
+                assert bool(g["default_left"][i]) == bool(nd["default_left"]), (t, i)
+            else:
+                a, b = np.float32(g["leaf_value"][i]), np.float32(nd["leaf_value"])
+                if exact:
+                    assert a == b, (t, i, a, b)
+                else:
+                    assert abs(a - b) <= leaf_rtol * abs(b) + 1e-12, (t, i, a, b)
+
+
+def test_saved_model_retrained_on_gpu():
+    """tests/native_format.rs:660-669: the reference's saved early-stopping
+    model (hist, depth 3, 4 rounds, squared error, a feature with missing
+    values) is grown again on the GPU: the same trees node for node."""
+    saved = load_saved_models()["0.4.9/early_stopping"]
+    x = four_features()
+    y = train_labels(x)
+    model = hb.train({"max_depth": 3}, hb.DMatrix(x, label=y), 4)
+    assert np.float32(model.base_score[0]).view(np.uint32) == np.uint32(saved["base_score"][0])
+    for t, (g, ref) in enumerate(zip(model.trees, saved["trees"])):
+        assert list(g["left"]) == ref["left"] and list(g["right"]) == ref["right"], t
+        internal = np.array(ref["left"]) != -1
+        assert np.array_equal(g["split_feature"][internal], np.array(ref["split_feature"])[internal])
+        assert np.array_equal(g["split_cond"].view(np.uint32)[internal], np.array(ref["split_cond"], np.uint32)[internal])
+        assert np.array_equal(g["default_left"][internal], np.array(ref["default_left"], np.uint8)[internal])
+        assert np.array_equal(g["split_gain"].view(np.uint32)[internal], np.array(ref["split_gain"], np.uint32)[internal])
+        lv = g["leaf_value"].view(np.uint32)[~internal]
+        want = np.array(ref["leaf_value"], np.uint32)[~internal]
+        assert np.array_equal(lv, want), t
+        assert np.array_equal(g["sum_hess"].view(np.uint32), np.array(ref["sum_hess"], np.uint32)), t
+
+
+@pytest.mark.parametrize("objective", ["reg:squarederror", "binary:logistic"])
+def test_boosting_matches_oracle(objective):
+    """Several rounds, depthwise, free-running: identical structure every
+    round, leaf values within 1e-5, margins within 1e-5."""
+    x, y = synthetic.regression_100k(n=20_000, f=16, seed=1)
+    if objective == "binary:logistic":
+        y = (y > 0).astype(np.float32)
+    params = {"objective": objective, "max_depth": 6, "eta": 0.3}
+    ds = O.Dataset(x, max_bin=256)
+    ref = O.Model(ds, y, O.params(objective=O.OBJ_LOGISTIC if objective != "reg:squarederror" else O.OBJ_SQUARED_ERROR,
+                                 max_depth=6, eta=0.3), 8)
+    model = hb.train(params, hb.DMatrix(x, label=y), 8)
+    compare_trees(model.trees, ref.trees())
+    m = model.predict(x, output_margin=True)
+    assert np.max(np.abs(m - ref.margins())) <= 1e-5
+
+
+def test_lossguide_matches_oracle():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((8_000, 8), dtype=np.float32)
+    x[rng.random(x.shape) < 0.1] = np.nan
+    y = (np.nan_to_num(x[:, 0]) * 2 + np.nan_to_num(x[:, 1]) ** 2).astype(np.float32)
+    params = {"grow_policy": "lossguide", "max_depth": 0, "max_leaves": 31, "eta": 0.3}
+    ref = O.Model(O.Dataset(x), y, O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=0, max_leaves=31), 3)
+    model = hb.train(params, hb.DMatrix(x, label=y), 3)
+    compare_trees(model.trees, ref.trees())
+
+
+def test_softmax_matches_oracle():
+    x, y = synthetic.multiclass(n=6_000, f=10, k=4, seed=3)
+    params = {"objective": "multi:softprob", "num_class": 4, "max_depth": 4, "eta": 0.3}
+    ref = O.Model(O.Dataset(x), y, O.params(objective=O.OBJ_SOFTMAX, num_class=4, max_depth=4), 3)
+    model = hb.train(params, hb.DMatrix(x, label=y), 3)
+    compare_trees(model.trees, ref.trees())
+
+
+def test_monotone_and_regularization_match_oracle():
+    x, y = synthetic.regression_100k(n=10_000, f=6, seed=4)
+    mono = [1, -1, 0, 0, 1, 0]
+    params = {"max_depth": 5, "eta": 0.5, "lambda": 2.0, "alpha": 0.5, "gamma": 0.1,
+              "min_child_weight": 3.0, "monotone_constraints": mono}
+    ref = O.Model(O.Dataset(x), y, O.params(max_depth=5, eta=0.5, reg_lambda=2.0, alpha=0.5, gamma=0.1,
+                                            min_child_weight=3.0, monotone=mono), 4)
+    model = hb.train(params, hb.DMatrix(x, label=y), 4)
+    compare_trees(model.trees, ref.trees())
