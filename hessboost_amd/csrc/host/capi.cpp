@@ -563,7 +563,10 @@ void hbr_forest_free(hbr_forest *f) { delete f; }
 
 int hbr_predict_margin_device(hbr_forest *h, const float *x, uint64_t n, uint64_t n_cols, float missing, float *out,
                               int32_t *leaf_out) {
-    return with_forest(h, [&](Forest &f) { f.predict_device(x, n, n_cols, missing, out, leaf_out); });
+    return with_forest(h, [&](Forest &f) {
+        f.predict_device(x, n, n_cols, missing, out, leaf_out);
+        f.dev().sync();  // the outputs are complete when the call returns
+    });
 }
 
 int hbr_predict_margin(hbr_forest *h, const float *x, uint64_t n, uint64_t n_cols, float missing, float *out) {

@@ -360,7 +360,8 @@ void hbr_forest_free(hbr_forest *f);
 int hbr_predict_margin(hbr_forest *f, const float *x, uint64_t n_rows, uint64_t n_cols,
                        float missing, float *out);
 /* The same over device memory (x, out and optional leaf ids [n_rows * n_trees]
- * all device pointers): inputs already resident, nothing copied. */
+ * all device pointers): inputs already resident, nothing copied. The
+ * outputs are complete when the call returns. */
 int hbr_predict_margin_device(hbr_forest *f, const float *x, uint64_t n_rows, uint64_t n_cols,
                               float missing, float *out, int32_t *leaf_out);
 /* BoostedModel::predict_leaf: each row's leaf node id per tree (host). */
