@@ -24,6 +24,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "train rounds/s at 10.5M×28 depth-8 logistic; batch predict Mrows/s (1 GPU)"
 HBM_PEAK_GBS = 8000.0
+HIST_KERNEL = "hbr_hist_dense8"
 
 
 def log(msg):
@@ -51,6 +52,7 @@ def main():
     ap.add_argument("--predict-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-predict", action="store_true")
+    ap.add_argument("--breakdown-steps", type=int, default=5)
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     args = ap.parse_args()
     if args.gpus != 1:
@@ -79,7 +81,8 @@ def main():
     trainer.boost(args.warmup)
     log(f"{args.warmup} warmup rounds done")
     before = eng.counters()
-    eng.set_profiling(True, "hbr_hist")
+    # HIP events around the dense histogram kernel only, on the engine's stream
+    eng.set_profiling(True, HIST_KERNEL)
     t0 = time.perf_counter()
     trainer.boost(args.steps)
     t1 = time.perf_counter()
@@ -88,12 +91,23 @@ def main():
     eng.set_profiling(False)
     elapsed = t1 - t0
     rounds_per_s = args.steps / elapsed
-    hist_ms = sum(ms for k, (ms, n) in stats.items() if k.startswith("hbr_hist"))
-    hist_launches = sum(n for k, (ms, n) in stats.items() if k.startswith("hbr_hist"))
+    hist_ms = sum(ms for k, (ms, n) in stats.items() if k.startswith(HIST_KERNEL))
+    hist_launches = sum(n for k, (ms, n) in stats.items() if k.startswith(HIST_KERNEL))
+    hist_names = sorted(k for k in stats if k.startswith(HIST_KERNEL))
     hist_bytes = after["hist_bytes"] - before["hist_bytes"]
     achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
-    log(f"{args.steps} rounds in {elapsed:.3f}s = {rounds_per_s:.1f} rounds/s; hist kernel {hist_ms:.1f} ms "
-        f"over {hist_launches} launches, {achieved:.0f} GB/s algorithmic")
+    log(f"{args.steps} rounds in {elapsed:.3f}s = {rounds_per_s:.1f} rounds/s; {'/'.join(hist_names)} "
+        f"{hist_ms:.1f} ms over {hist_launches} launches, {achieved:.0f} GB/s algorithmic")
+    # per-kernel time per round, from a few more rounds with every kernel timed
+    breakdown = {}
+    if args.breakdown_steps > 0:
+        eng.set_profiling(True, "")
+        trainer.boost(args.breakdown_steps)
+        bstats = eng.kernel_stats()
+        eng.set_profiling(False)
+        breakdown = {k: round(ms / args.breakdown_steps, 4)
+                     for k, (ms, n) in sorted(bstats.items(), key=lambda kv: -kv[1][0])}
+        log("ms per round by kernel: " + ", ".join(f"{k} {v}" for k, v in breakdown.items()))
     n_trees = len(trainer.trees())
 
     result = {
@@ -115,7 +129,7 @@ def main():
             "rows": args.rows, "features": 28, "max_depth": 8, "max_bin": 256, "trees_grown": n_trees,
         },
         "roofline": {
-            "kernel": "hbr_hist_dense8 (fixed-point histogram)",
+            "kernel": "/".join(hist_names) or HIST_KERNEL,
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
@@ -126,6 +140,7 @@ def main():
             "avg_launch_ms": round(hist_ms / max(1, hist_launches), 4),
             "algorithmic_bytes_per_launch": int(hist_bytes / max(1, hist_launches)),
         },
+        "kernel_ms_per_round": breakdown,
     }
     del eng, trainer
 

@@ -12,9 +12,10 @@ namespace hbr {
 // Rows per partition tile (one workgroup).
 constexpr uint32_t kPartTile = 2048;
 constexpr uint32_t kPartThreads = 256;
-// Rows per histogram tile of one workgroup.
-constexpr uint32_t kHistTile = 8192;
+// Histogram workgroups: threads, and the fewest rows a tile is cut to (tiles
+// are sized per launch so that about one wave of workgroups covers it).
 constexpr uint32_t kHistThreads = 512;
+constexpr uint32_t kHistMinRows = 4096;
 // Bins of one feature the split scan processes per pass (4 per lane).
 constexpr uint32_t kScanChunk = 256;
 // Threads of the elementwise kernels.
@@ -132,6 +133,7 @@ struct PartArgs {
     uint32_t n_tiles;
     const uint32_t *tile_split;  // tile -> split
     uint32_t *tile_left;         // per tile left count (count pass) / left offset (after scan)
+    uint64_t *decisions;         // per tile kPartTile / 64 ballots of "goes left" (count pass)
     PartOut *out;
     const uint32_t *src_rows[2];
     uint32_t *dst_rows[2];
@@ -148,42 +150,74 @@ struct PartArgs {
 };
 
 // ---- histograms ----------------------------------------------------------------
-// A histogram tile: rows [row0, row0 + tile) of a node, features [f0, f0+nf).
+// A row tile of one node: rows [row0, row0 + rows) of node `node`, the k-th
+// of that node's tiles. Every feature group of the launch takes the tile.
 struct HistTile {
     uint32_t node;      // index into the node table
     uint32_t row0;
-    uint32_t f0;
-    uint32_t nf;
+    uint32_t rows;
+    uint32_t k;
 };
 
 // One node whose histogram is built into `slot`. When `from_split` is set,
 // the node is the smaller child of split `split` and its segment comes from
-// the partition's device output.
+// the partition's device output (the plan kernel resolves it in place).
 struct HistNode {
     Seg seg;
     uint32_t slot;
     uint32_t from_split;
     uint32_t split;
     uint32_t contiguous; // rows are seg.offset .. seg.offset+len (no row buffer)
+    uint32_t tile_begin; // first row tile (written by the plan kernel)
+    uint32_t n_tiles;    // row tiles of the node (written by the plan kernel)
+    uint32_t pad[2];
+};
+
+// Device tiling of a histogram launch: each node's rows cut into tiles of
+// `tile_rows` (a multiple of 512, at least min_rows), sized so that the
+// launch holds about target_tiles tiles; at most target_tiles + n_nodes.
+struct PlanArgs {
+    HistNode *nodes;
+    uint32_t n_nodes;
+    uint32_t target_tiles;
+    const PartSplit *splits;
+    const PartOut *part_out;
+    HistTile *tiles;
+    uint32_t *counts;           // [0] tiles, [1] tile_rows
+    uint32_t min_rows;
+    uint32_t pad;
 };
 
 struct HistArgs {
     const HistNode *nodes;
     const HistTile *tiles;
-    const PartSplit *splits;
-    const PartOut *part_out;
+    const uint32_t *counts;     // plan output: [0] tiles
     const uint32_t *rows[2];
     const GPair *gpair;
     const QScale *scale;
     const uint8_t *bins8;       // dense row-major local bins [n][stride]
-    const uint16_t *bins16;
-    uint32_t stride;            // bytes (u8) or elements (u16) per row
+    uint32_t stride;            // bytes per row
+    uint32_t n_cols;
     const uint64_t *row_ptr;    // CSR
     const uint32_t *gbins;
     const uint32_t *feature_offset;
     QBin *hist;                 // slots * total_bins
+    QBin *partial;              // per (tile, feature group): fg * 256 bins
     uint32_t total_bins;
-    uint32_t tile_rows;
+    uint32_t groups;            // feature groups per tile
+};
+
+// Sum of a node's tile partials into its slot (nodes of one tile are
+// written by the histogram kernel directly).
+struct ReduceArgs {
+    const HistNode *nodes;
+    const QBin *partial;
+    QBin *hist;
+    const uint32_t *feature_offset;
+    uint32_t n_cols;
+    uint32_t total_bins;
+    uint32_t groups;
+    uint32_t fg;
 };
 
 // sibling = parent - built, in place in the parent's slot, for each split.
@@ -261,6 +295,23 @@ struct LeafArgs {
     uint32_t output;
     uint32_t tile_rows;
     uint32_t n_tiles;
+};
+
+// A grown tree routed over the binned rows: node meta is feature | limit
+// << 16 | leaf << 31 (present local bins below `limit` go left), left child
+// absolute with the right child at left + 1, leaf values as f32.
+struct WalkArgs {
+    const uint32_t *meta;
+    const uint32_t *left;
+    const float *value;
+    const uint8_t *bins8;        // dense row-major local bins [n][stride]
+    float *margins;
+    uint32_t stride;
+    uint32_t n;
+    uint32_t m_stride;           // outputs per row
+    uint32_t output;
+    uint32_t n_nodes;
+    uint32_t pad;
 };
 
 // ---- prediction ---------------------------------------------------------------------

@@ -2,6 +2,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 namespace hbr {
@@ -44,6 +45,20 @@ void logistic_scalar(float m, float y, float w, float spw, float min_hess, float
 }  // namespace
 
 Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) {
+    // launch-shape overrides for tuning sweeps (results do not depend on them)
+    if (const char *v = std::getenv("HBROCM_HIST_FG")) {
+        const long fg = std::strtol(v, nullptr, 10);
+        if (fg == 8 || fg == 16 || fg == 32) hist_features_per_group = (uint32_t)fg;
+    }
+    if (const char *v = std::getenv("HBROCM_HIST_THREADS")) {
+        const long t = std::strtol(v, nullptr, 10);
+        if (t == 512 || t == 1024) hist_threads = (uint32_t)t;
+    }
+    if (const char *v = std::getenv("HBROCM_HIST_VARIANT")) hist_variant = v;
+    if (const char *v = std::getenv("HBROCM_HIST_WAVES")) {
+        const long w = std::strtol(v, nullptr, 10);
+        if (w >= 1 && w <= 64) hist_waves = (uint32_t)w;
+    }
     upload_index(desc);
     scale_.resize(1);
     d_total_.resize(1);
@@ -78,7 +93,9 @@ void Engine::upload_index(const hbr_index_desc &d) {
     if (dense_ && widest <= 256 && n_cols_ > 0) {
         dense_u8_ = true;
         have_cols_ = true;
-        stride_ = (n_cols_ + 15) / 16 * 16;
+        // a whole number of the widest feature group (32 bytes), so that a
+        // group's load never crosses past the row's end
+        stride_ = (n_cols_ + 31) / 32 * 32;
         rows8_.resize(n_rows_ * stride_);
         rows8_.zero(s);
         cols8_.resize(n_rows_ * n_cols_);
@@ -229,7 +246,10 @@ bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
     a.scale_pos_weight = loss.scale_pos_weight;
     a.min_hess = loss.min_hess;
     a.max_input = loss.max_input;
-    dev_.launch("hbr_gradients", dim3(ceil_div(n_rows_, kThreads)), dim3(kThreads), a);
+    // grid-stride: a few workgroups per CU, one max fold each
+    const uint32_t grad_blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)),
+                                                    (uint32_t)dev_.cu_count() * 8);
+    dev_.launch("hbr_gradients", dim3(grad_blocks), dim3(kThreads), a);
     QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
     scale_.download(q, 1, s);
     dev_.sync();
@@ -295,8 +315,9 @@ QBin Engine::root_total(const Segment &sg) {
     hipStream_t s = dev_.stream();
     d_total_.zero(s);
     TotalArgs a{};
-    a.rows = rows_[sg.buf].get() + sg.offset;
-    a.first = 0;
+    const bool ident = contiguous(sg);
+    a.rows = ident ? nullptr : rows_[sg.buf].get() + sg.offset;
+    a.first = ident ? sg.offset : 0;
     a.n = sg.len;
     a.gpair = gpair_.get();
     a.scale = scale_.get();
@@ -361,69 +382,95 @@ void Engine::set_scan_params(const ScanParams &p, const std::vector<int8_t> &mon
     }
 }
 
-void Engine::launch_hist(const std::vector<HistNode> &nodes, const std::vector<uint32_t> &upper_len,
-                         const PartSplit *splits_dev, const uint32_t *rows0) {
-    std::vector<HistTile> tiles;
-    const uint32_t fg = dense_u8_ ? hist_features_per_group : 0;
-    for (uint32_t i = 0; i < nodes.size(); i++) {
-        for (uint32_t r0 = 0; r0 < upper_len[i]; r0 += kHistTile) {
-            if (!dense_u8_) {
-                tiles.push_back(HistTile{i, r0, 0, 0});
-                continue;
-            }
-            for (uint32_t f0 = 0; f0 < n_cols_; f0 += fg)
-                tiles.push_back(HistTile{i, r0, f0, std::min(fg, n_cols_ - f0)});
-        }
-    }
-    if (tiles.empty()) return;
+// Histograms of a batch of nodes into their slots: the plan kernel cuts the
+// nodes' rows into tiles (about `per_cu` resident workgroups per CU over the
+// launch), then one workgroup per (tile, feature group). Dense u8 tiles
+// write their sums with plain stores (the reduce kernel adds up nodes of
+// several tiles); CSR tiles add into slots zeroed first.
+void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *splits_dev, const uint32_t *rows0) {
+    if (nodes.empty()) return;
     hipStream_t s = dev_.stream();
+    const uint32_t n = (uint32_t)nodes.size();
+    const uint32_t fg = hist_features_per_group;
+    const uint32_t groups = dense_u8_ ? ceil_div(n_cols_, fg) : 1;
+    // LDS per workgroup is fg features x 257 words x 16 bytes of 160 KiB
+    const uint32_t per_cu = !dense_u8_ ? 4 : fg <= 8 ? 4 : fg <= 16 ? 2 : 1;
+    const uint32_t target = std::max<uint32_t>(1, (uint32_t)dev_.cu_count() * per_cu * hist_waves / groups);
+    if (!dense_u8_) {
+        std::vector<uint32_t> slots(n);
+        for (uint32_t i = 0; i < n; i++) slots[i] = nodes[i].slot;
+        upload_vec(d_slots_, slots, stage_, s);
+        ZeroArgs z{hist_.get(), d_slots_.get(), n, total_bins_};
+        dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), n), dim3(256), z);
+    }
     upload_vec(d_hnodes_, nodes, stage_, s);
-    upload_vec(d_htiles_, tiles, stage_, s);
+    d_htiles_.reserve(target + n);
+    d_hcounts_.reserve(4);
+    if (dense_u8_) d_partial_.reserve((size_t)2 * target * groups * fg * 256);
+
+    PlanArgs p{};
+    p.nodes = d_hnodes_.get();
+    p.n_nodes = n;
+    p.target_tiles = target;
+    p.splits = splits_dev;
+    p.part_out = d_part_out_.get();
+    p.tiles = d_htiles_.get();
+    p.counts = d_hcounts_.get();
+    p.min_rows = kHistMinRows;
+    dev_.launch("hbr_hist_plan", dim3(1), dim3(256), p);
+
     HistArgs a{};
     a.nodes = d_hnodes_.get();
     a.tiles = d_htiles_.get();
-    a.splits = splits_dev;
-    a.part_out = d_part_out_.get();
+    a.counts = d_hcounts_.get();
     a.rows[0] = rows0 ? rows0 : rows_[0].get();
     a.rows[1] = rows_[1].get();
     a.gpair = gpair_.get();
     a.scale = scale_.get();
     a.bins8 = rows8_.get();
     a.stride = stride_;
+    a.n_cols = n_cols_;
     a.row_ptr = row_ptr_.get();
     a.gbins = gbins_.get();
     a.feature_offset = d_fo_.get();
     a.hist = hist_.get();
+    a.partial = d_partial_.get();
     a.total_bins = total_bins_;
-    a.tile_rows = kHistTile;
-    const char *k = !dense_u8_ ? "hbr_hist_csr"
+    a.groups = groups;
+    std::string k = !dense_u8_ ? "hbr_hist_csr"
                     : fg <= 8  ? "hbr_hist_dense8_fg8"
                     : fg <= 16 ? "hbr_hist_dense8_fg16"
                                : "hbr_hist_dense8_fg32";
-    dev_.launch(k, dim3((uint32_t)tiles.size()), dim3(kHistThreads), a);
+    if (dense_u8_ && !hist_variant.empty()) k += "_" + hist_variant;
+    dev_.launch(k.c_str(), dim3((target + n) * groups), dim3(dense_u8_ ? hist_threads : kHistThreads), a);
+    if (dense_u8_) {
+        ReduceArgs r{};
+        r.nodes = d_hnodes_.get();
+        r.partial = d_partial_.get();
+        r.hist = hist_.get();
+        r.feature_offset = d_fo_.get();
+        r.n_cols = n_cols_;
+        r.total_bins = total_bins_;
+        r.groups = groups;
+        r.fg = fg;
+        dev_.launch("hbr_hist_reduce", dim3(n_cols_ * 4, n), dim3(1024), r);
+    }
 }
 
 void Engine::build_nodes(const std::vector<Segment> &segs, const std::vector<uint32_t> &slots) {
     if (segs.empty()) return;
-    hipStream_t s = dev_.stream();
-    upload_vec(d_slots_, slots, stage_, s);
-    ZeroArgs z{hist_.get(), d_slots_.get(), (uint32_t)slots.size(), total_bins_};
-    dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), (uint32_t)slots.size()),
-                dim3(256), z);
     std::vector<HistNode> nodes;
-    std::vector<uint32_t> lens;
     for (size_t i = 0; i < segs.size(); i++) {
         HistNode n{};
         n.seg = Seg{segs[i].offset, segs[i].len, segs[i].buf, 0};
         n.slot = slots[i];
         n.contiguous = contiguous(segs[i]) ? 1u : 0u;
         nodes.push_back(n);
-        lens.push_back(segs[i].len);
         counters.hist_nodes++;
         counters.hist_rows += segs[i].len;
         counters.hist_bytes += hist_bytes(segs[i].len, !n.contiguous);
     }
-    launch_hist(nodes, lens, nullptr);
+    launch_hist(nodes, nullptr);
 }
 
 void Engine::subtract(const std::vector<uint32_t> &parents, const std::vector<uint32_t> &built) {
@@ -517,6 +564,7 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
     upload_vec(d_splits_, ps, stage_, s);
     upload_vec(d_tile_split_, tile_split, stage_, s);
     d_tile_left_.reserve(tiles ? tiles : 1);
+    d_decisions_.reserve((size_t)(tiles ? tiles : 1) * (kPartTile / 64));
     d_part_out_.reserve(P);
     PartArgs a{};
     a.splits = d_splits_.get();
@@ -524,6 +572,7 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
     a.n_tiles = tiles;
     a.tile_split = d_tile_split_.get();
     a.tile_left = d_tile_left_.get();
+    a.decisions = d_decisions_.get();
     a.out = d_part_out_.get();
     a.src_rows[0] = rows_[0].get();
     a.src_rows[1] = rows_[1].get();
@@ -544,20 +593,15 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
 
     ScanBest *best_staged = nullptr;
     if (!terminal) {
-        upload_vec(d_slots_, fresh, stage_, s);
-        ZeroArgs z{hist_.get(), d_slots_.get(), P, total_bins_};
-        dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), z);
         std::vector<HistNode> hn(P);
-        std::vector<uint32_t> upper(P);
         for (uint32_t i = 0; i < P; i++) {
             HistNode n{};
             n.slot = fresh[i];
             n.from_split = 1;
             n.split = i;
             hn[i] = n;
-            upper[i] = splits[i].seg.len / 2;
         }
-        launch_hist(hn, upper, d_splits_.get());
+        launch_hist(hn, d_splits_.get());
         SubArgs sub{d_splits_.get(), P, hist_.get(), total_bins_};
         dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), sub);
         std::vector<ScanNode> sn(2 * P);
@@ -641,6 +685,40 @@ void Engine::add_leaves(const std::vector<Segment> &segs, const std::vector<floa
     stage_.reset();
 }
 
+void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint32_t> &left,
+                      const std::vector<float> &value, uint32_t output) {
+    if (!dense_u8_) fail(kRefused, "walk_add: the index has no row-major u8 bins");
+    const size_t n = meta.size();
+    if (n == 0 || left.size() != n || value.size() != n) fail(kInvalid, "walk_add: one meta, left, value per node");
+    for (size_t i = 0; i < n; i++) {
+        if (meta[i] >> 31) continue;
+        if ((meta[i] & 0xffffu) >= n_cols_ || (uint64_t)left[i] + 1 >= n)
+            fail(kInvalid, "walk_add: a split names a missing feature or child");
+    }
+    if (output >= outputs_) fail(kInvalid, "walk_add: no such output");
+    hipStream_t s = dev_.stream();
+    upload_vec(d_walk_meta_, meta, stage_, s);
+    upload_vec(d_walk_left_, left, stage_, s);
+    upload_vec(d_walk_value_, value, stage_, s);
+    WalkArgs a{};
+    a.meta = d_walk_meta_.get();
+    a.left = d_walk_left_.get();
+    a.value = d_walk_value_.get();
+    a.bins8 = rows8_.get();
+    a.margins = margins_.get();
+    a.stride = stride_;
+    a.n = (uint32_t)n_rows_;
+    a.m_stride = outputs_;
+    a.output = output;
+    a.n_nodes = (uint32_t)n;
+    // 32-byte rows and trees that fit the LDS table take the staged walk
+    const bool staged = stride_ == 32 && n <= 1024;
+    const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)),
+                                               (uint32_t)dev_.cu_count() * (staged ? 8 : 16));
+    dev_.launch(staged ? "hbr_walk_leaves32" : "hbr_walk_leaves", dim3(blocks), dim3(256), a);
+    // the staged node tables are released at the next synchronisation
+}
+
 std::vector<QBin> Engine::build_rows(const uint32_t *rows, uint64_t m) {
     for (uint64_t i = 0; i < m; i++)
         if (rows[i] >= n_rows_) fail(kRefused, "build: a row beyond the index");
@@ -648,14 +726,10 @@ std::vector<QBin> Engine::build_rows(const uint32_t *rows, uint64_t m) {
     host_rows_.reserve(m ? m : 1);
     host_rows_.upload(rows, m, s);
     const uint32_t slot = alloc_slot();
-    std::vector<uint32_t> slots{slot};
-    upload_vec(d_slots_, slots, stage_, s);
-    ZeroArgs z{hist_.get(), d_slots_.get(), 1, total_bins_};
-    dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), 1), dim3(256), z);
     HistNode n{};
     n.seg = Seg{0, (uint32_t)m, 0, 0};
     n.slot = slot;
-    launch_hist({n}, {(uint32_t)m}, nullptr, host_rows_.get());
+    launch_hist({n}, nullptr, host_rows_.get());
     std::vector<QBin> out(total_bins_);
     hist_.download(out.data(), total_bins_, s, (size_t)slot * total_bins_);
     dev_.sync();

@@ -89,6 +89,12 @@ public:
     // and the children's split search, with one host synchronisation.
     std::vector<LevelChild> level(const std::vector<LevelSplit> &splits, bool terminal);
     void add_leaves(const std::vector<Segment> &segs, const std::vector<float> &values, uint32_t output);
+    // Dense u8 index: margins of output `output` += the leaf each row reaches
+    // through the tree (meta/left/value as WalkArgs lays them out); needs no
+    // row segments, so the depth limit's level can skip its partition.
+    bool can_walk() const { return dense_u8_; }
+    void walk_add(const std::vector<uint32_t> &meta, const std::vector<uint32_t> &left,
+                  const std::vector<float> &value, uint32_t output);
     // HistogramBackend::build of a host row list (per-node host growth).
     std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
     std::vector<uint32_t> rows_of(const Segment &s);
@@ -111,8 +117,7 @@ private:
     void ensure_rows();
     bool contiguous(const Segment &sg) const;
     bool identity_rows0_ = false;
-    void launch_hist(const std::vector<HistNode> &nodes, const std::vector<uint32_t> &upper_len,
-                     const PartSplit *splits_dev, const uint32_t *rows0 = nullptr);
+    void launch_hist(const std::vector<HistNode> &nodes, const PartSplit *splits_dev, const uint32_t *rows0 = nullptr);
     void launch_scan(const std::vector<ScanNode> &nodes, ScanBest *host_out);
     void finish_scale(uint32_t rows);
 
@@ -162,6 +167,11 @@ private:
     DBuf<PartOut> d_part_out_;
     DBuf<HistNode> d_hnodes_;
     DBuf<HistTile> d_htiles_;
+    DBuf<uint32_t> d_hcounts_;
+    DBuf<QBin> d_partial_;
+    DBuf<uint64_t> d_decisions_;
+    DBuf<uint32_t> d_walk_meta_, d_walk_left_;
+    DBuf<float> d_walk_value_;
     DBuf<ScanNode> d_snodes_;
     DBuf<ScanBest> d_per_feature_, d_best_;
     DBuf<QBin> d_total_;
@@ -169,7 +179,13 @@ private:
     DBuf<uint32_t> d_tile_leaf_, d_tile_row0_;
 
 public:
-    uint32_t hist_features_per_group = 16;
+    // histogram launch shape: features per workgroup (8, 16 or 32), threads
+    // per dense workgroup (512 or 1024) and resident waves of workgroups the
+    // plan sizes a launch for
+    uint32_t hist_features_per_group = 32;
+    uint32_t hist_threads = 1024;
+    uint32_t hist_waves = 1;
+    std::string hist_variant;  // kernel name suffix of a code variant (tuning)
 };
 
 }  // namespace hbr

@@ -117,6 +117,7 @@ void Device::drain_events() {
 
 void Device::set_profiling(bool on, const std::string &prefix) {
     sync();
+    if (on) stats_.clear();
     profiling_ = on;
     profile_prefix_ = prefix;
 }

@@ -65,6 +65,7 @@ LevelSplit TreeBuilder::expand(Tree &t, const Open &o, const Decision &d, double
     n.split_cond = d.bin >= 0 ? e_.cut_values()[d.bin] : -FLT_MAX;
     n.default_left = (uint8_t)d.default_left;
     n.split_bin = d.bin;
+    n.split_limit = d.limit;
     n.split_gain = (float)d.loss;
     const int32_t left = (int32_t)t.nodes.size();
     n.left = left;
@@ -106,7 +107,7 @@ void TreeBuilder::leaf(const Open &o) {
     if (o.has_slot) e_.free_slot(o.slot);
 }
 
-Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out) {
+Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool walk) {
     Tree t;
     g_.clear();
     h_.clear();
@@ -164,7 +165,10 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out) {
                 parents.push_back(o);
             }
             const bool terminal = depth + 1 >= limit;
-            std::vector<LevelChild> kids = e_.level(splits, terminal);
+            // the depth limit's children are only needed for their rows'
+            // margins, which the walk finds without a partition
+            std::vector<LevelChild> kids =
+                terminal && walk ? std::vector<LevelChild>(2 * splits.size()) : e_.level(splits, terminal);
             std::vector<Open> next;
             for (size_t i = 0; i < splits.size(); i++) {
                 for (int c = 0; c < 2; c++) {
@@ -380,6 +384,40 @@ void Trainer::softmax_gradients(std::vector<float> &out) {
     }
 }
 
+// Leaf values onto the margins (training/margins.rs:247-289): by routing
+// every row through the tree on its bins when the index allows it, else
+// over each leaf's row segment.
+void Trainer::grow_and_add(TreeBuilder &b, uint32_t output) {
+    const bool walk = e_.can_walk();
+    std::vector<std::pair<Segment, float>> leaves;
+    trees_.push_back(b.grow(&leaves, walk));
+    const Tree &t = trees_.back();
+    if (walk) {
+        const size_t n = t.nodes.size();
+        std::vector<uint32_t> meta(n), left(n, 0);
+        std::vector<float> value(n, 0.0f);
+        for (size_t i = 0; i < n; i++) {
+            const TreeNode &nd = t.nodes[i];
+            if (nd.left < 0) {
+                meta[i] = 1u << 31;
+                value[i] = nd.leaf_value;
+            } else {
+                meta[i] = nd.split_feature | (nd.split_limit << 16);
+                left[i] = (uint32_t)nd.left;
+            }
+        }
+        e_.walk_add(meta, left, value, output);
+        return;
+    }
+    std::vector<Segment> segs;
+    std::vector<float> vals;
+    for (auto &l : leaves) {
+        segs.push_back(l.first);
+        vals.push_back(l.second);
+    }
+    e_.add_leaves(segs, vals, output);
+}
+
 void Trainer::boost(uint64_t rounds) {
     TreeBuilder b(e_, p_.grow);
     for (uint64_t it = 0; it < rounds; it++) {
@@ -392,15 +430,7 @@ void Trainer::boost(uint64_t rounds) {
                     gk[2 * r + 1] = all[2 * (r * k_ + c) + 1];
                 }
                 e_.prepare(gk.data(), n_);
-                std::vector<std::pair<Segment, float>> leaves;
-                trees_.push_back(b.grow(&leaves));
-                std::vector<Segment> segs;
-                std::vector<float> vals;
-                for (auto &l : leaves) {
-                    segs.push_back(l.first);
-                    vals.push_back(l.second);
-                }
-                e_.add_leaves(segs, vals, c);
+                grow_and_add(b, c);
             }
             continue;
         }
@@ -411,15 +441,7 @@ void Trainer::boost(uint64_t rounds) {
         loss.max_input = 80.0f;
         loss.vector_rows = n_ >= 16 ? n_ - n_ % 8 : 0;
         if (!e_.compute_gradients(loss, 0)) fail(kRefused, "a gradient is not finite: the round runs on the host");
-        std::vector<std::pair<Segment, float>> leaves;
-        trees_.push_back(b.grow(&leaves));
-        std::vector<Segment> segs;
-        std::vector<float> vals;
-        for (auto &l : leaves) {
-            segs.push_back(l.first);
-            vals.push_back(l.second);
-        }
-        e_.add_leaves(segs, vals, 0);
+        grow_and_add(b, 0);
     }
 }
 

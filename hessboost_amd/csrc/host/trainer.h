@@ -28,6 +28,7 @@ struct TreeNode {
     int32_t left = -1, right = -1;
     float leaf_value = 0.0f, sum_hess = 0.0f, split_gain = 0.0f;
     int64_t split_bin = -2;
+    uint32_t split_limit = 0;  // present local bins below go left
 };
 
 struct Tree {
@@ -48,8 +49,10 @@ class TreeBuilder {
 public:
     TreeBuilder(Engine &e, const GrowParams &p);
     // Grow one tree from the staged gradients over every row; each leaf's
-    // segment and (eta-scaled) value go to `leaves`.
-    Tree grow(std::vector<std::pair<Segment, float>> *leaves);
+    // segment and (eta-scaled) value go to `leaves`. With `walk`, the rows
+    // of the depth limit's children are not partitioned (their segments are
+    // empty): the caller routes rows through the tree instead.
+    Tree grow(std::vector<std::pair<Segment, float>> *leaves, bool walk = false);
 
 private:
     struct Open {
@@ -108,6 +111,8 @@ public:
 
 private:
     void softmax_gradients(std::vector<float> &gpair_all);
+    // one grown tree onto the margins of output `output`
+    void grow_and_add(TreeBuilder &b, uint32_t output);
 
     Engine &e_;
     TrainParams p_;

@@ -36,20 +36,32 @@ __device__ __forceinline__ float exp_vector(float x) {
     return poly * __uint_as_float(bits);
 }
 
-__device__ __forceinline__ void fold_max(QScale *s, float g, float h, bool active) {
-    uint32_t mg = active ? (__float_as_uint(g) & 0x7fffffffu) : 0u;
-    uint32_t mh = active ? (__float_as_uint(h) & 0x7fffffffu) : 0u;
-    bool bad = active && (!__builtin_isfinite(g) || !__builtin_isfinite(h));
+// Workgroup-wide fold of the magnitude maxima and the non-finite count,
+// then one atomic per workgroup (non-negative f32 bits order as integers).
+__device__ __forceinline__ void fold_block(QScale *s, uint32_t mg, uint32_t mh, uint32_t bad) {
+    __shared__ uint32_t red[3][256 / kWave];
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
         mg = max(mg, (uint32_t)__shfl_xor((int)mg, d, kWave));
         mh = max(mh, (uint32_t)__shfl_xor((int)mh, d, kWave));
+        bad += (uint32_t)__shfl_xor((int)bad, d, kWave);
     }
-    uint64_t nb = __ballot(bad);
+    const uint32_t wave = threadIdx.x / kWave;
     if (lane_id() == 0) {
+        red[0][wave] = mg;
+        red[1][wave] = mh;
+        red[2][wave] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / kWave; w++) {
+            mg = max(mg, red[0][w]);
+            mh = max(mh, red[1][w]);
+            bad += red[2][w];
+        }
         if (mg) atomicMax(&s->max_g_bits, mg);
         if (mh) atomicMax(&s->max_h_bits, mh);
-        if (nb) atomicAdd(&s->nonfinite, (uint32_t)__popcll(nb));
+        if (bad) atomicAdd(&s->nonfinite, bad);
     }
 }
 
@@ -57,47 +69,56 @@ __device__ __forceinline__ void fold_max(QScale *s, float g, float h, bool activ
 
 using namespace hbr;
 
+// Grid-stride over rows; the stride is a multiple of 64, so every wave
+// covers 64 consecutive rows and its lanes form whole 8-row vectors.
 extern "C" __global__ __launch_bounds__(256) void hbr_gradients(GradArgs a) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    const bool active = i < a.n;
-    float m = active ? a.margins[i] : 0.0f;
-    float y = active ? a.labels[i] : 0.0f;
-    float w = (active && a.weights) ? a.weights[i] : 1.0f;
-    float g = 0.0f, h = 0.0f;
-    bool host_row = false;
-    if (a.loss == kSquaredError) {
-        if (y == 1.0f) w *= a.scale_pos_weight;
-        g = (m - y) * w;
-        h = w;
-    } else {
-        bool ok = active && __builtin_fabsf(m) <= a.max_input;
-        uint64_t ballot = __ballot(ok || !active);
-        uint64_t group = 0xffull << (lane_id() & ~7u);
-        bool vector = active && i < a.vec_rows && (ballot & group) == group;
-        if (vector) {
-            float e = exp_vector(0.0f - __builtin_fabsf(m));
-            float den = 1.0f + e;
-            float pos = 1.0f / den;
-            float neg = e / den;
-            float p = m >= 0.0f ? pos : neg;
-            float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
-            g = (p - y) * ww;
-            float q = p * (1.0f - p);
-            h = (q > a.min_hess ? q : a.min_hess) * ww;
-        } else if (active) {
-            host_row = true;
-        }
-    }
-    if (active) {
-        if (host_row) {
-            uint32_t slot = atomicAdd(&a.scale->scalar_rows, 1u);
-            a.scalar_list[slot] = i;
-            a.gpair[i] = GPair{0.0f, 0.0f};
+    uint32_t mg = 0, mh = 0, bad = 0;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    const uint32_t end = (a.n + kWave - 1) / kWave * kWave;  // whole waves stay in the loop
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < end; i += stride) {
+        const bool active = i < a.n;
+        float m = active ? a.margins[i] : 0.0f;
+        float y = active ? a.labels[i] : 0.0f;
+        float w = (active && a.weights) ? a.weights[i] : 1.0f;
+        float g = 0.0f, h = 0.0f;
+        bool host_row = false;
+        if (a.loss == kSquaredError) {
+            if (y == 1.0f) w *= a.scale_pos_weight;
+            g = (m - y) * w;
+            h = w;
         } else {
-            a.gpair[i] = GPair{g, h};
+            bool ok = active && __builtin_fabsf(m) <= a.max_input;
+            uint64_t ballot = __ballot(ok || !active);
+            uint64_t group = 0xffull << (lane_id() & ~7u);
+            bool vector = active && i < a.vec_rows && (ballot & group) == group;
+            if (vector) {
+                float e = exp_vector(0.0f - __builtin_fabsf(m));
+                float den = 1.0f + e;
+                float pos = 1.0f / den;
+                float neg = e / den;
+                float p = m >= 0.0f ? pos : neg;
+                float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
+                g = (p - y) * ww;
+                float q = p * (1.0f - p);
+                h = (q > a.min_hess ? q : a.min_hess) * ww;
+            } else if (active) {
+                host_row = true;
+            }
+        }
+        if (active) {
+            if (host_row) {
+                uint32_t slot = atomicAdd(&a.scale->scalar_rows, 1u);
+                a.scalar_list[slot] = i;
+                a.gpair[i] = GPair{0.0f, 0.0f};
+            } else {
+                a.gpair[i] = GPair{g, h};
+                mg = max(mg, __float_as_uint(g) & 0x7fffffffu);
+                mh = max(mh, __float_as_uint(h) & 0x7fffffffu);
+                bad += (!__builtin_isfinite(g) || !__builtin_isfinite(h)) ? 1u : 0u;
+            }
         }
     }
-    fold_max(a.scale, g, h, active && !host_row);
+    fold_block(a.scale, mg, mh, bad);
 }
 
 extern "C" __global__ __launch_bounds__(256) void hbr_iota(IotaArgs a) {
@@ -116,12 +137,22 @@ extern "C" __global__ __launch_bounds__(256) void hbr_total(TotalArgs a) {
         sg += quantize(p.g, eg);
         sh += quantize(p.h, eh);
     }
+    __shared__ int64_t red[2][256 / kWave];
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
         sg += __shfl_xor(sg, d, kWave);
         sh += __shfl_xor(sh, d, kWave);
     }
     if (lane_id() == 0) {
+        red[0][threadIdx.x / kWave] = sg;
+        red[1][threadIdx.x / kWave] = sh;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / kWave; w++) {
+            sg += red[0][w];
+            sh += red[1][w];
+        }
         atomicAdd((unsigned long long *)&a.out->g, (unsigned long long)sg);
         atomicAdd((unsigned long long *)&a.out->h, (unsigned long long)sh);
     }

@@ -6,16 +6,20 @@
 // gives the same bins; when the reference's own sums are exact
 // (backend/exact_sum.rs:14-37) these equal its f64 bins bit for bit.
 //
+// A launch covers a batch of nodes. hbr_hist_plan cuts every node's rows
+// into tiles sized so that the batch is about one wave of workgroups (the
+// nodes of a level are only known on the device, after the partition).
 // Dense indexes read row-major local bins (u8 for <= 256 bins per feature):
-// a workgroup takes a tile of one node's rows and a group of features,
-// accumulates into an LDS sub-histogram with 64-bit integer atomics, and
-// flushes the non-zero bins to the node's slot with 64-bit global atomics.
+// a workgroup takes one tile and one group of FG features, accumulates into
+// LDS with 64-bit integer atomics, then writes its sub-histogram with plain
+// stores: straight into the node's slot when the node is one tile, else to
+// a partial that hbr_hist_reduce sums. No device-scope atomics.
 // Sparse (CSR) indexes add each stored entry straight to the slot.
 #include "common.h"
 
 namespace hbr {
 
-__device__ __forceinline__ Seg resolve_node(const HistArgs &a, const HistNode &nd) {
+__device__ __forceinline__ Seg resolve_node(const PlanArgs &a, const HistNode &nd) {
     if (!nd.from_split) return nd.seg;
     const PartSplit sp = a.splits[nd.split];
     const PartOut po = a.part_out[nd.split];
@@ -32,64 +36,153 @@ __device__ __forceinline__ Seg resolve_node(const HistArgs &a, const HistNode &n
     return s;
 }
 
+// LDS row of one feature: 256 bins plus one pad word, so that the same bin
+// of consecutive features falls in different banks.
+constexpr uint32_t kLdsFeature = 257;
+
+// Rotate the FG feature bytes held in W words right by `rot` bytes: byte i
+// of the result is byte (i + rot) mod 4W of the input.
+template <int W>
+__device__ __forceinline__ void rotate_bytes(uint32_t (&w)[W], uint32_t rot) {
+    const uint32_t wr = rot >> 2;
+#pragma unroll
+    for (int b = 1; b < W; b <<= 1) {
+        // a bit blend rather than a select, which the compiler would turn
+        // into a dynamically indexed (scratch) array read
+        const uint32_t m = (wr & (uint32_t)b) ? ~0u : 0u;
+        uint32_t t[W];
+#pragma unroll
+        for (int i = 0; i < W; i++) t[i] = w[i] ^ ((w[i] ^ w[(i + b) % W]) & m);
+#pragma unroll
+        for (int i = 0; i < W; i++) w[i] = t[i];
+    }
+    const uint32_t sh = (rot & 3u) * 8u;
+    uint32_t t[W];
+#pragma unroll
+    for (int i = 0; i < W; i++) t[i] = __builtin_amdgcn_alignbit(w[(i + 1) % W], w[i], sh);
+#pragma unroll
+    for (int i = 0; i < W; i++) w[i] = t[i];
+}
+
 template <int FG>
+__device__ __forceinline__ void load_bins(const uint8_t *p, uint32_t (&w)[FG / 4]) {
+    if constexpr (FG == 8) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        w[0] = v.x;
+        w[1] = v.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < FG / 16; i++) {
+            const uint4 v = reinterpret_cast<const uint4 *>(p)[i];
+            w[4 * i] = v.x;
+            w[4 * i + 1] = v.y;
+            w[4 * i + 2] = v.z;
+            w[4 * i + 3] = v.w;
+        }
+    }
+}
+
+// Row loop of one workgroup. ROT: lane l starts at feature l mod FG (bytes
+// rotated in registers), so that rows piled in one bin of one feature do not
+// all hit the same LDS word in one instruction; features past nf then go to
+// a per-lane dummy word instead of a branch. U rows per thread are loaded
+// before any of them is added, to keep U gathers in flight.
+template <int FG, bool ROT, int U>
 __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
-    __shared__ unsigned long long lds[FG * 256 * 2];
-    const HistTile t = a.tiles[blockIdx.x];
+    constexpr int W = FG / 4;
+    constexpr uint32_t kDummy = FG * kLdsFeature;
+    __shared__ unsigned long long lg[FG * kLdsFeature + kWave];
+    __shared__ unsigned long long lh[FG * kLdsFeature + kWave];
+    const uint32_t entry = blockIdx.x / a.groups, grp = blockIdx.x % a.groups;
+    if (entry >= a.counts[0]) return;  // uniform across the workgroup
+    const HistTile t = a.tiles[entry];
     const HistNode nd = a.nodes[t.node];
-    const Seg seg = resolve_node(a, nd);
-    if (t.row0 >= seg.len) return;  // uniform across the workgroup
-    const uint32_t end = min(t.row0 + a.tile_rows, seg.len);
-    const uint32_t nf = t.nf;
-    for (uint32_t i = threadIdx.x; i < nf * 512u; i += blockDim.x) lds[i] = 0ull;
+    const uint32_t f0 = grp * FG;
+    const uint32_t nf = min((uint32_t)FG, a.n_cols - f0);
+    for (uint32_t i = threadIdx.x; i < FG * kLdsFeature + kWave; i += blockDim.x) {
+        lg[i] = 0ull;
+        lh[i] = 0ull;
+    }
     __syncthreads();
     const int eg = a.scale->exp_g, eh = a.scale->exp_h;
-    const uint32_t *rows = a.rows[seg.buf];
-    const uint32_t nw = (nf + 3) / 4;
-    for (uint32_t j = t.row0 + threadIdx.x; j < end; j += blockDim.x) {
-        const uint32_t r = nd.contiguous ? seg.offset + j : rows[seg.offset + j];
-        const GPair p = a.gpair[r];
-        const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
-        const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
-        const uint32_t *b = (const uint32_t *)(a.bins8 + (size_t)r * a.stride + t.f0);
-        uint32_t words[(FG + 3) / 4];
+    const uint32_t *rows = a.rows[nd.seg.buf] + nd.seg.offset;
+    const uint32_t lane = lane_id();
+    const uint32_t rot = ROT ? lane & (FG - 1) : 0u;
+    const uint32_t end = t.row0 + t.rows;
+    const uint32_t step = blockDim.x;
+    for (uint32_t j0 = t.row0 + threadIdx.x; j0 < end; j0 += U * step) {
+        uint32_t w[U][W];
+        unsigned long long qg[U], qh[U];
+        bool live[U];
 #pragma unroll
-        for (int w = 0; w < (FG + 3) / 4; w++) words[w] = (uint32_t)w < nw ? b[w] : 0u;
+        for (int u = 0; u < U; u++) {
+            const uint32_t j = j0 + (uint32_t)u * step;
+            live[u] = j < end;
+            // a row past the end reads row 0 (it exists) and is not added
+            const uint32_t r = live[u] ? (nd.contiguous ? nd.seg.offset + j : rows[j]) : 0u;
+            const GPair p = a.gpair[r];
+            load_bins<FG>(a.bins8 + (size_t)r * a.stride + f0, w[u]);
+            qg[u] = (unsigned long long)quantize(p.g, eg);
+            qh[u] = (unsigned long long)quantize(p.h, eh);
+        }
+        if (ROT) {
 #pragma unroll
-        for (int f = 0; f < FG; f++) {
-            if ((uint32_t)f < nf) {
-                const uint32_t bin = (words[f >> 2] >> ((f & 3) * 8)) & 0xffu;
-                const uint32_t at = ((uint32_t)f * 256u + bin) * 2u;
-                atomicAdd(&lds[at], qg);
-                atomicAdd(&lds[at + 1], qh);
+            for (int u = 0; u < U; u++) rotate_bytes<W>(w[u], rot);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (!live[u]) break;  // rows past the tile end come last
+            if (ROT) {
+#pragma unroll
+                for (int f = 0; f < FG; f++) {
+                    const uint32_t ff = ((uint32_t)f + rot) & (FG - 1);
+                    const uint32_t bin = (w[u][f >> 2] >> ((f & 3) * 8)) & 0xffu;
+                    const uint32_t at = ff < nf ? ff * kLdsFeature + bin : kDummy + lane;
+                    atomicAdd(&lg[at], qg[u]);
+                    atomicAdd(&lh[at], qh[u]);
+                }
+            } else {
+#pragma unroll
+                for (int f = 0; f < FG; f++) {
+                    if ((uint32_t)f < nf) {
+                        const uint32_t bin = (w[u][f >> 2] >> ((f & 3) * 8)) & 0xffu;
+                        const uint32_t at = (uint32_t)f * kLdsFeature + bin;
+                        atomicAdd(&lg[at], qg[u]);
+                        atomicAdd(&lh[at], qh[u]);
+                    }
+                }
             }
         }
     }
     __syncthreads();
-    QBin *dst = a.hist + (size_t)nd.slot * a.total_bins;
-    const uint32_t *fo = a.feature_offset + t.f0;
-    for (uint32_t i = threadIdx.x; i < nf * 256u; i += blockDim.x) {
-        const uint32_t f = i >> 8, bin = i & 255u;
-        const uint32_t lo = fo[f], nb = fo[f + 1] - lo;
-        if (bin >= nb) continue;
-        const unsigned long long g = lds[2 * i], h = lds[2 * i + 1];
-        if ((g | h) == 0ull) continue;
-        atomicAdd((unsigned long long *)&dst[lo + bin].g, g);
-        atomicAdd((unsigned long long *)&dst[lo + bin].h, h);
+    const uint32_t *fo = a.feature_offset + f0;
+    if (nd.n_tiles == 1) {
+        QBin *dst = a.hist + (size_t)nd.slot * a.total_bins;
+        for (uint32_t i = threadIdx.x; i < nf * 256u; i += blockDim.x) {
+            const uint32_t ff = i >> 8, bin = i & 255u;
+            const uint32_t lo = fo[ff], nb = fo[ff + 1] - lo;
+            if (bin < nb) dst[lo + bin] = QBin{(int64_t)lg[ff * kLdsFeature + bin], (int64_t)lh[ff * kLdsFeature + bin]};
+        }
+    } else {
+        QBin *dst = a.partial + ((size_t)(nd.pad[0] + t.k) * a.groups + grp) * (FG * 256u);
+        for (uint32_t i = threadIdx.x; i < nf * 256u; i += blockDim.x) {
+            const uint32_t ff = i >> 8, bin = i & 255u;
+            dst[i] = QBin{(int64_t)lg[ff * kLdsFeature + bin], (int64_t)lh[ff * kLdsFeature + bin]};
+        }
     }
 }
 
 __device__ __forceinline__ void hist_csr(const HistArgs &a) {
-    const HistTile t = a.tiles[blockIdx.x];
+    const uint32_t entry = blockIdx.x;
+    if (entry >= a.counts[0]) return;
+    const HistTile t = a.tiles[entry];
     const HistNode nd = a.nodes[t.node];
-    const Seg seg = resolve_node(a, nd);
-    if (t.row0 >= seg.len) return;
-    const uint32_t end = min(t.row0 + a.tile_rows, seg.len);
     const int eg = a.scale->exp_g, eh = a.scale->exp_h;
-    const uint32_t *rows = a.rows[seg.buf];
+    const uint32_t *rows = a.rows[nd.seg.buf] + nd.seg.offset;
     QBin *dst = a.hist + (size_t)nd.slot * a.total_bins;
+    const uint32_t end = t.row0 + t.rows;
     for (uint32_t j = t.row0 + threadIdx.x; j < end; j += blockDim.x) {
-        const uint32_t r = nd.contiguous ? seg.offset + j : rows[seg.offset + j];
+        const uint32_t r = nd.contiguous ? nd.seg.offset + j : rows[j];
         const GPair p = a.gpair[r];
         const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
         const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
@@ -105,10 +198,102 @@ __device__ __forceinline__ void hist_csr(const HistArgs &a) {
 
 using namespace hbr;
 
-extern "C" __global__ __launch_bounds__(512) void hbr_hist_dense8_fg8(HistArgs a) { hist_dense8<8>(a); }
-extern "C" __global__ __launch_bounds__(512) void hbr_hist_dense8_fg16(HistArgs a) { hist_dense8<16>(a); }
-extern "C" __global__ __launch_bounds__(512) void hbr_hist_dense8_fg32(HistArgs a) { hist_dense8<32>(a); }
+// One workgroup: resolve each node's rows, choose the tile size, number the
+// tiles (and the partials of nodes cut into several tiles).
+extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
+    __shared__ unsigned long long sum_lds[256 / kWave];
+    unsigned long long sum = 0;
+    for (uint32_t i = threadIdx.x; i < a.n_nodes; i += blockDim.x) {
+        HistNode nd = a.nodes[i];
+        const Seg s = resolve_node(a, nd);
+        a.nodes[i].seg = s;
+        sum += s.len;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, kWave);
+    if (lane_id() == 0) sum_lds[threadIdx.x / kWave] = sum;
+    __syncthreads();
+    unsigned long long total = 0;
+    for (uint32_t w = 0; w < 256 / kWave; w++) total += sum_lds[w];
+    const unsigned long long want = (total + a.target_tiles - 1) / a.target_tiles;
+    const uint32_t tile_rows =
+        (uint32_t)((max(want, (unsigned long long)a.min_rows) + kHistThreads - 1) / kHistThreads * kHistThreads);
+    uint32_t carry = 0, part_carry = 0;
+    for (uint32_t base = 0; base < a.n_nodes; base += blockDim.x) {
+        const uint32_t i = base + threadIdx.x;
+        const uint32_t len = i < a.n_nodes ? a.nodes[i].seg.len : 0u;
+        const uint32_t n = (len + tile_rows - 1) / tile_rows;
+        uint32_t all, part_all;
+        const uint32_t first = block_exclusive_scan<256>(n, &all);
+        const uint32_t part_first = block_exclusive_scan<256>(n > 1 ? n : 0u, &part_all);
+        if (i < a.n_nodes) {
+            a.nodes[i].tile_begin = carry + first;
+            a.nodes[i].n_tiles = n;
+            a.nodes[i].pad[0] = part_carry + part_first;
+            for (uint32_t k = 0; k < n; k++) {
+                HistTile t;
+                t.node = i;
+                t.row0 = k * tile_rows;
+                t.rows = min(tile_rows, len - k * tile_rows);
+                t.k = k;
+                a.tiles[carry + first + k] = t;
+            }
+        }
+        carry += all;
+        part_carry += part_all;
+    }
+    if (threadIdx.x == 0) {
+        a.counts[0] = carry;
+        a.counts[1] = tile_rows;
+        a.counts[2] = part_carry;
+    }
+}
+
+// Launched with 512 or 1024 threads.
+#define HBR_HIST_DENSE8(FG, ROT, U, NAME) \
+    extern "C" __global__ __launch_bounds__(1024) void NAME(HistArgs a) { hist_dense8<FG, ROT, U>(a); }
+HBR_HIST_DENSE8(8, true, 1, hbr_hist_dense8_fg8)
+HBR_HIST_DENSE8(16, true, 1, hbr_hist_dense8_fg16)
+HBR_HIST_DENSE8(32, true, 1, hbr_hist_dense8_fg32)
+HBR_HIST_DENSE8(32, true, 2, hbr_hist_dense8_fg32_u2)
+HBR_HIST_DENSE8(32, false, 1, hbr_hist_dense8_fg32_plain)
+HBR_HIST_DENSE8(32, false, 2, hbr_hist_dense8_fg32_plain_u2)
+HBR_HIST_DENSE8(16, true, 2, hbr_hist_dense8_fg16_u2)
+HBR_HIST_DENSE8(16, false, 2, hbr_hist_dense8_fg16_plain_u2)
 extern "C" __global__ __launch_bounds__(512) void hbr_hist_csr(HistArgs a) { hist_csr(a); }
+
+// Nodes cut into several tiles: the slot is the sum of the tiles' partials.
+// A workgroup takes 64 bins of one feature of one node; its 16 waves split
+// the node's tiles, then combine in LDS.
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_reduce(ReduceArgs a) {
+    __shared__ int64_t acc[2][16][64];
+    const uint32_t f = blockIdx.x >> 2, quarter = blockIdx.x & 3u;
+    const HistNode nd = a.nodes[blockIdx.y];
+    if (f >= a.n_cols || nd.n_tiles == 1) return;  // uniform across the workgroup
+    const uint32_t lo = a.feature_offset[f], nb = a.feature_offset[f + 1] - lo;
+    if (quarter * 64u >= nb) return;
+    const uint32_t col = threadIdx.x & 63u, ks = threadIdx.x >> 6;
+    const uint32_t bin = quarter * 64u + col;
+    const uint32_t grp = f / a.fg, local = (f % a.fg) * 256u + bin;
+    int64_t g = 0, h = 0;
+    if (bin < nb) {
+        for (uint32_t k = ks; k < nd.n_tiles; k += 16) {
+            const QBin q = a.partial[((size_t)(nd.pad[0] + k) * a.groups + grp) * (a.fg * 256u) + local];
+            g += q.g;
+            h += q.h;
+        }
+    }
+    acc[0][ks][col] = g;
+    acc[1][ks][col] = h;
+    __syncthreads();
+    if (ks == 0 && bin < nb) {
+        for (uint32_t k = 1; k < 16; k++) {
+            g += acc[0][k][col];
+            h += acc[1][k][col];
+        }
+        a.hist[(size_t)nd.slot * a.total_bins + lo + bin] = QBin{g, h};
+    }
+}
 
 // sibling = parent - built (exact in integers), in the parent's slot.
 extern "C" __global__ __launch_bounds__(256) void hbr_subtract(SubArgs a) {

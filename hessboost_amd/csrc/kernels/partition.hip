@@ -6,14 +6,17 @@
 // the parent's ascending row order (left child first in the segment).
 //
 // Three passes over fixed tiles of kPartTile rows: count the left rows of
-// each tile, scan the tile counts of each split (which also fixes each
-// child's length and which child is the smaller, built one), then scatter
-// every row to its stable position in the other row buffer.
+// each tile (keeping each wave's 64-row ballot of decisions), scan the tile
+// counts of each split (which also fixes each child's length and which
+// child is the smaller, built one), then scatter every row to its stable
+// position in the other row buffer from the ballots, without routing it
+// again. Row j of a tile is handled by lane j % 64 of ballot j / 64.
 #include "common.h"
 
 namespace hbr {
 
 constexpr uint32_t kRowsPerThread = kPartTile / kPartThreads;  // 8
+constexpr uint32_t kBallots = kPartTile / kWave;                // 32 per tile
 
 __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp, uint32_t r) {
     if (a.dense) {
@@ -33,47 +36,36 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
     return sp.default_left != 0;
 }
 
-// Exclusive block scan of one value per thread (kPartThreads threads).
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *total) {
-    __shared__ uint32_t wave_sums[kPartThreads / kWave];
-    const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
-    uint32_t x = v;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        uint32_t t = __shfl_up(x, d, kWave);
-        if (lane >= (uint32_t)d) x += t;
-    }
-    if (lane == kWave - 1) wave_sums[wave] = x;
-    __syncthreads();
-    uint32_t base = 0, all = 0;
-    for (uint32_t w = 0; w < kPartThreads / kWave; w++) {
-        if (w < wave) base += wave_sums[w];
-        all += wave_sums[w];
-    }
-    __syncthreads();
-    *total = all;
-    return base + x - v;
-}
-
 }  // namespace hbr
 
 using namespace hbr;
 
 extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
+    __shared__ uint32_t wave_count[kPartThreads / kWave];
     const uint32_t tile = blockIdx.x;
     if (tile >= a.n_tiles) return;
     const PartSplit sp = a.splits[a.tile_split[tile]];
     const uint32_t base = (tile - sp.tile_begin) * kPartTile;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
+    const uint32_t wave = threadIdx.x / kWave;
+    uint64_t *dec = a.decisions + (size_t)tile * kBallots;
     uint32_t cnt = 0;
 #pragma unroll
     for (uint32_t k = 0; k < kRowsPerThread; k++) {
-        const uint32_t j = base + threadIdx.x * kRowsPerThread + k;
-        if (j < sp.seg.len) cnt += goes_left(a, sp, src[j]) ? 1u : 0u;
+        const uint32_t q = k * (kPartThreads / kWave) + wave;
+        const uint32_t j = base + q * kWave + lane_id();
+        const bool left = j < sp.seg.len && goes_left(a, sp, src[j]);
+        const uint64_t m = __ballot(left);
+        if (lane_id() == 0) dec[q] = m;
+        cnt += (uint32_t)__popcll(m);
     }
-    uint32_t total;
-    block_exclusive_scan(cnt, &total);
-    if (threadIdx.x == 0) a.tile_left[tile] = total;
+    if (lane_id() == 0) wave_count[wave] = cnt;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t total = 0;
+        for (uint32_t w = 0; w < kPartThreads / kWave; w++) total += wave_count[w];
+        a.tile_left[tile] = total;
+    }
 }
 
 // One workgroup per split: exclusive scan of its tiles' left counts.
@@ -87,7 +79,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_scan(PartArgs a) {
         const uint32_t t = t0 + threadIdx.x;
         const uint32_t v = t < n_tiles ? a.tile_left[sp.tile_begin + t] : 0u;
         uint32_t total;
-        const uint32_t ex = block_exclusive_scan(v, &total);
+        const uint32_t ex = block_exclusive_scan<kPartThreads>(v, &total);
         if (t < n_tiles) a.tile_left[sp.tile_begin + t] = carry + ex;
         carry += total;
     }
@@ -100,6 +92,8 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_scan(PartArgs a) {
     }
 }
 
+// Every wave walks the tile's ballots in row order, keeping the count of
+// left rows before the current ballot; it moves the rows of its own ballots.
 extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     const uint32_t tile = blockIdx.x;
     if (tile >= a.n_tiles) return;
@@ -111,33 +105,26 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     const uint32_t right_before = tile_pos - left_before;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
     uint32_t *dst = a.dst_rows[sp.seg.buf ^ 1u] + sp.seg.offset;
-    uint32_t row[kRowsPerThread];
-    uint32_t flags = 0, nl = 0, nr = 0;
-#pragma unroll
-    for (uint32_t k = 0; k < kRowsPerThread; k++) {
-        const uint32_t j = tile_pos + threadIdx.x * kRowsPerThread + k;
-        row[k] = 0;
-        if (j < sp.seg.len) {
-            row[k] = src[j];
-            if (goes_left(a, sp, row[k])) {
-                flags |= 1u << k;
-                nl++;
-            } else {
-                nr++;
+    const uint64_t *dec = a.decisions + (size_t)tile * kBallots;
+    const uint32_t wave = threadIdx.x / kWave, lane = lane_id();
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint32_t run = 0;  // left rows of the ballots before q
+    for (uint32_t q = 0; q < kBallots; q++) {
+        const uint64_t m = dec[q];
+        if (q % (kPartThreads / kWave) == wave) {
+            const uint32_t j = tile_pos + q * kWave + lane;
+            if (j < sp.seg.len) {
+                const uint32_t r = src[j];
+                if ((m >> lane) & 1ull) {
+                    dst[left_before + run + (uint32_t)__popcll(m & below)] = r;
+                } else {
+                    // every row before j in the tile exists: q*64 + lane rows
+                    const uint32_t rights = q * kWave - run + (uint32_t)__popcll(~m & below);
+                    dst[left_len + right_before + rights] = r;
+                }
             }
         }
-    }
-    uint32_t tl, tr;
-    uint32_t lpos = block_exclusive_scan(nl, &tl);
-    uint32_t rpos = block_exclusive_scan(nr, &tr);
-#pragma unroll
-    for (uint32_t k = 0; k < kRowsPerThread; k++) {
-        const uint32_t j = tile_pos + threadIdx.x * kRowsPerThread + k;
-        if (j >= sp.seg.len) continue;
-        if ((flags >> k) & 1u)
-            dst[left_before + lpos++] = row[k];
-        else
-            dst[left_len + right_before + rpos++] = row[k];
+        run += (uint32_t)__popcll(m);
     }
 }
 
@@ -154,5 +141,67 @@ extern "C" __global__ __launch_bounds__(256) void hbr_add_leaves(LeafArgs a) {
         const uint32_t r = rows[j];
         float *m = a.margins + (size_t)r * a.stride + a.output;
         *m = *m + lf.value;
+    }
+}
+
+// The same margins update for a dense u8 index, in row order: each row is
+// routed down the grown tree on its own local bins (the routing of the
+// partition: bin < limit goes left), so the last level needs no partition
+// and the margins are read and written once, coalesced. A node table that
+// does not lead to a leaf within n_nodes steps leaves the row unchanged.
+extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves(WalkArgs a) {
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += gridDim.x * blockDim.x) {
+        const uint8_t *b = a.bins8 + (size_t)r * a.stride;
+        uint32_t nid = 0, meta = a.meta[0];
+        for (uint32_t step = 0; step < a.n_nodes && !(meta >> 31); step++) {
+            const uint32_t f = meta & 0xffffu, lim = (meta >> 16) & 0x7fffu;
+            nid = a.left[nid] + ((uint32_t)b[f] < lim ? 0u : 1u);
+            nid = nid < a.n_nodes ? nid : 0u;
+            meta = a.meta[nid];
+        }
+        if (meta >> 31) {
+            float *m = a.margins + (size_t)r * a.m_stride + a.output;
+            *m = *m + a.value[nid];
+        }
+    }
+}
+
+// The walk for 32-byte rows and trees of at most kWalkLdsNodes nodes: the
+// node table sits in LDS, and each thread copies its row's 32 bins into its
+// own LDS slot with two 16-byte loads, then reads the bytes it routes on
+// from there (one coalesced row read instead of one byte load per level).
+constexpr uint32_t kWalkLdsNodes = 1024;
+
+extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves32(WalkArgs a) {
+    __shared__ uint32_t s_meta[kWalkLdsNodes];
+    __shared__ uint32_t s_left[kWalkLdsNodes];
+    __shared__ float s_value[kWalkLdsNodes];
+    __shared__ uint2 s_rows[256 * 5];  // 40 bytes per thread: 32 bins + pad
+    for (uint32_t i = threadIdx.x; i < a.n_nodes; i += blockDim.x) {
+        s_meta[i] = a.meta[i];
+        s_left[i] = a.left[i];
+        s_value[i] = a.value[i];
+    }
+    __syncthreads();
+    uint2 *mine = s_rows + threadIdx.x * 5;
+    const uint8_t *bins = reinterpret_cast<const uint8_t *>(mine);
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += gridDim.x * blockDim.x) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.bins8 + (size_t)r * 32u);
+        const uint4 x = src[0], y = src[1];
+        mine[0] = make_uint2(x.x, x.y);
+        mine[1] = make_uint2(x.z, x.w);
+        mine[2] = make_uint2(y.x, y.y);
+        mine[3] = make_uint2(y.z, y.w);
+        uint32_t nid = 0, meta = s_meta[0];
+        for (uint32_t step = 0; step < a.n_nodes && !(meta >> 31); step++) {
+            const uint32_t f = meta & 31u, lim = (meta >> 16) & 0x7fffu;
+            nid = s_left[nid] + ((uint32_t)bins[f] < lim ? 0u : 1u);
+            nid = nid < a.n_nodes ? nid : 0u;
+            meta = s_meta[nid];
+        }
+        if (meta >> 31) {
+            float *m = a.margins + (size_t)r * a.m_stride + a.output;
+            *m = *m + s_value[nid];
+        }
     }
 }

@@ -277,7 +277,8 @@ typedef struct hbr_engine_counters {
 int hbr_engine_counters_read(hbr_engine *e, hbr_engine_counters *out);
 
 /* Per-kernel device time (HIP events on the engine's stream); profiling is
- * off until enabled. buf receives "name=ms,launches;..." */
+ * off until enabled, and enabling it clears the previous statistics.
+ * buf receives "name=ms,launches;..." */
 int hbr_set_profiling(hbr_engine *e, int on, const char *kernel_prefix);
 int hbr_kernel_stats(hbr_engine *e, char *buf, size_t len);
 
