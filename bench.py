@@ -31,6 +31,24 @@ def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a known-size copy),
+    with the algorithmic bytes per launch of the run it was measured on."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", f"{kernel}_*hbm_counters.md"))):
+        vals = {}
+        for line in open(path):
+            if ":" in line and line.split(":", 1)[0].strip() in ("traffic_bytes_per_launch",
+                                                                    "traffic_algorithmic_bytes_per_launch"):
+                k, v = line.split(":", 1)
+                vals[k.strip()] = int(v.strip())
+        if "traffic_bytes_per_launch" in vals:
+            return vals["traffic_bytes_per_launch"], vals.get("traffic_algorithmic_bytes_per_launch"), \
+                os.path.relpath(path, ROOT)
+    return None, None, None
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -53,6 +71,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-predict", action="store_true")
     ap.add_argument("--breakdown-steps", type=int, default=5)
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="first run a device-to-device copy of this many MiB (a known-size kernel for "
+                         "scaling hardware byte counters in profiles)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     args = ap.parse_args()
     if args.gpus != 1:
@@ -64,6 +85,14 @@ def main():
 
     import hessboost_amd as hb
     from hessboost_amd import synthetic
+
+    if args.copy_probe_mb > 0:
+        nbytes = args.copy_probe_mb << 20
+        a_buf, b_buf = hb.DeviceBuffer(nbytes), hb.DeviceBuffer(nbytes)
+        for _ in range(3):
+            b_buf.copy_from(a_buf)
+        log(f"copy probe: 3 device copies of {nbytes} bytes")
+        del a_buf, b_buf
 
     # ---------------- training --------------------------------------------------------
     params = {"objective": "binary:logistic", "max_depth": 8, "eta": 0.1, "max_bin": 256}
@@ -109,6 +138,7 @@ def main():
                      for k, (ms, n) in sorted(bstats.items(), key=lambda kv: -kv[1][0])}
         log("ms per round by kernel: " + ", ".join(f"{k} {v}" for k, v in breakdown.items()))
     n_trees = len(trainer.trees())
+    traffic, traffic_alg, traffic_src = measured_traffic(hist_names[0] if hist_names else HIST_KERNEL)
 
     result = {
         "metric": METRIC,
@@ -135,7 +165,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
+            "traffic_run_algorithmic_bytes": traffic_alg,
             "launches": hist_launches,
             "avg_launch_ms": round(hist_ms / max(1, hist_launches), 4),
             "algorithmic_bytes_per_launch": int(hist_bytes / max(1, hist_launches)),
@@ -201,7 +233,9 @@ def main():
         pstats = forest.kernel_stats()
         forest.set_profiling(False)
         mrows = n * args.predict_steps / (t1 - t0) / 1e6
-        pms, pl = pstats.get("hbr_predict", (0.0, 0))
+        pkern = sorted(k for k in pstats if k.startswith("hbr_predict"))
+        pms = sum(pstats[k][0] for k in pkern)
+        pl = sum(pstats[k][1] for k in pkern)
         pbytes = n * (4 * f + 4)
         pach = pbytes / (pms / max(1, pl) * 1e-3) / 1e9 if pms > 0 else 0.0
         node_steps = n * args.predict_trees * 8
@@ -210,7 +244,8 @@ def main():
             "metric": "batch predict Mrows/s", "value": round(mrows, 2), "unit": "Mrows/s",
             "steps": args.predict_steps,
             "config": {"workload": f"{args.predict_trees}-tree depth-8 forest, {n:,} x {f} f32 rows, 2% NaN"},
-            "roofline": {"kernel": "hbr_predict", "bound": "hbm", "achieved": round(pach, 1), "peak": HBM_PEAK_GBS,
+            "roofline": {"kernel": "/".join(pkern) or "hbr_predict", "bound": "hbm", "achieved": round(pach, 1),
+                         "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(pach / HBM_PEAK_GBS, 4), "traffic": None,
                          "avg_launch_ms": round(pms / max(1, pl), 4),
                          "node_steps_per_s": round(node_steps / (pms / max(1, pl) * 1e-3), 1) if pms else None},

@@ -156,6 +156,7 @@ SIGNATURES = {
     "hbr_device_free": (C.c_int, [C.c_int, C.c_void_p]),
     "hbr_device_upload": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.c_uint64]),
     "hbr_device_download": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.c_uint64]),
+    "hbr_device_copy": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.c_uint64]),
 }
 
 _lib = None

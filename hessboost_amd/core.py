@@ -594,6 +594,12 @@ class DeviceBuffer:
         A.check(A.lib().hbr_device_download(self.ordinal, A.ptr(out), C.c_void_p(self.ptr), out.nbytes))
         return out
 
+    def copy_from(self, other, nbytes=None):
+        """Device-to-device copy of `nbytes` (default: all of `other`)."""
+        n = other.nbytes if nbytes is None else nbytes
+        assert n <= self.nbytes and n <= other.nbytes
+        A.check(A.lib().hbr_device_copy(self.ordinal, C.c_void_p(self.ptr), C.c_void_p(other.ptr), n))
+
     def __del__(self):
         try:
             A.lib().hbr_device_free(self.ordinal, C.c_void_p(self.ptr))

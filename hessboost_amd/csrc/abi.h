@@ -318,7 +318,24 @@ struct WalkArgs {
 // Forest nodes are structure-of-arrays: value (threshold or leaf value bits),
 // meta (feature | default_left << 30 | leaf << 31), left child (absolute
 // index; the right child is left + 1, as the reference's trees allocate them).
+// One forest node as the staged prediction kernel reads it (one 16-byte load).
+struct PredNode {
+    uint32_t value;               // threshold or leaf value (f32 bits)
+    uint32_t meta;                // feature | default_left << 30 | leaf << 31
+    uint32_t left;                // left child (absolute), right = left + 1
+    int32_t orig;                 // the node's id in its tree as the caller numbered it
+};
+
+// A compact forest node: value bits, then feature (16 bits), the left
+// child's offset from this node (14 bits; right = left + 1), default_left,
+// leaf.
+struct CompactNode {
+    uint32_t value;
+    uint32_t meta;
+};
+
 struct PredictArgs {
+    const PredNode *nodes;
     const uint32_t *node_value;   // f32 bits
     const uint32_t *node_meta;    // feature | default_left<<30 | leaf<<31
     const uint32_t *node_left;    // left child (absolute), right = left + 1
@@ -338,6 +355,14 @@ struct PredictArgs {
     uint32_t missing_is_nan;
     uint32_t trees_per_chunk;
     uint32_t pad;
+    // tree chunks for hbr_predict_chunked: chunk c holds trees
+    // [chunk_tree[c], chunk_tree[c + 1]) whose nodes are the compact records
+    // [chunk_node[c], chunk_node[c + 1]) of `compact`
+    const CompactNode *compact;      // (value bits, feature | rel_left << 16 | dl << 30 | leaf << 31)
+    const uint32_t *chunk_tree;   // n_chunks + 1
+    const uint32_t *chunk_node;   // n_chunks + 1
+    uint32_t n_chunks;
+    uint32_t chunk_cap;           // LDS node capacity
 };
 
 }  // namespace hbr

@@ -628,4 +628,11 @@ int hbr_device_download(int ordinal, void *dst, const void *src, uint64_t bytes)
     });
 }
 
+int hbr_device_copy(int ordinal, void *dst, const void *src, uint64_t bytes) {
+    return guard([&] {
+        device(ordinal);
+        HBR_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    });
+}
+
 }  // extern "C"

@@ -54,7 +54,6 @@ Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) 
         const long t = std::strtol(v, nullptr, 10);
         if (t == 512 || t == 1024) hist_threads = (uint32_t)t;
     }
-    if (const char *v = std::getenv("HBROCM_HIST_VARIANT")) hist_variant = v;
     if (const char *v = std::getenv("HBROCM_HIST_WAVES")) {
         const long w = std::strtol(v, nullptr, 10);
         if (w >= 1 && w <= 64) hist_waves = (uint32_t)w;
@@ -437,12 +436,11 @@ void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *sp
     a.partial = d_partial_.get();
     a.total_bins = total_bins_;
     a.groups = groups;
-    std::string k = !dense_u8_ ? "hbr_hist_csr"
+    const char *k = !dense_u8_ ? "hbr_hist_csr"
                     : fg <= 8  ? "hbr_hist_dense8_fg8"
                     : fg <= 16 ? "hbr_hist_dense8_fg16"
                                : "hbr_hist_dense8_fg32";
-    if (dense_u8_ && !hist_variant.empty()) k += "_" + hist_variant;
-    dev_.launch(k.c_str(), dim3((target + n) * groups), dim3(dense_u8_ ? hist_threads : kHistThreads), a);
+    dev_.launch(k, dim3((target + n) * groups), dim3(dense_u8_ ? hist_threads : kHistThreads), a);
     if (dense_u8_) {
         ReduceArgs r{};
         r.nodes = d_hnodes_.get();

@@ -185,7 +185,6 @@ public:
     uint32_t hist_features_per_group = 32;
     uint32_t hist_threads = 1024;
     uint32_t hist_waves = 1;
-    std::string hist_variant;  // kernel name suffix of a code variant (tuning)
 };
 
 }  // namespace hbr

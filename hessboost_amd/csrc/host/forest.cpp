@@ -1,6 +1,9 @@
 #include "forest.h"
 
+#include <algorithm>
+#include <cstdlib>
 #include <cstring>
+#include <string>
 
 namespace hbr {
 
@@ -67,6 +70,28 @@ Forest::Forest(int ordinal, const hbr_forest_desc &fd) : dev_(device(ordinal)) {
     up(root_, root);
     up(output_, output);
     up(orig_, orig);
+    std::vector<PredNode> nodes(value.size());
+    for (size_t i = 0; i < value.size(); i++) nodes[i] = PredNode{value[i], meta[i], left[i], orig[i]};
+    up(nodes_, nodes);
+    // compact records: feature < 2^16, left child within 2^14 - 1 nodes
+    compact_ok_ = true;
+    std::vector<CompactNode> compact(value.size());
+    for (size_t i = 0; i < value.size(); i++) {
+        if (meta[i] >> 31) {
+            compact[i] = CompactNode{value[i], 1u << 31};
+            continue;
+        }
+        const uint32_t f = meta[i] & 0xfffffu, rel = left[i] - (uint32_t)i;
+        if (f >= (1u << 16) || rel >= (1u << 14)) compact_ok_ = false;
+        compact[i] = CompactNode{value[i], (f & 0xffffu) | ((rel & 0x3fffu) << 16) | (meta[i] & (1u << 30))};
+    }
+    if (compact_ok_) up(compact_, compact);
+    tree_nodes_.resize(n_trees_);
+    for (uint64_t t = 0; t < n_trees_; t++) {
+        const uint32_t end = t + 1 < n_trees_ ? root[t + 1] : (uint32_t)value.size();
+        tree_nodes_[t] = end - root[t];
+        largest_tree_ = std::max(largest_tree_, tree_nodes_[t]);
+    }
     up(weight_, weight);
     up(base_, base);
     dev_.sync();
@@ -78,6 +103,7 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     if (n_trees_ && n_cols <= max_feature_) fail(kInvalid, "predict: rows have fewer columns than the forest reads");
     if (n >= (uint64_t)UINT32_MAX) fail(kRefused, "predict: more than 2^32 - 1 rows per call");
     PredictArgs a{};
+    a.nodes = nodes_.get();
     a.node_value = value_.get();
     a.node_meta = meta_.get();
     a.node_left = left_.get();
@@ -95,7 +121,64 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     a.n_outputs = n_outputs_;
     a.missing = missing;
     a.missing_is_nan = missing != missing ? 1u : 0u;
+    // trees resident in LDS, rows streamed: row blocks of `waves` waves plus
+    // a node table holding at least the largest tree
+    const uint64_t row_block = n_cols * 65ull * sizeof(float);
+    const uint64_t lds_total = 160ull * 1024;
+    uint32_t waves = 4;
+    if (const char *v = std::getenv("HBROCM_PRED_WAVES")) waves = (uint32_t)std::max(1L, std::min(4L, std::strtol(v, nullptr, 10)));
+    while (waves > 1 && waves * row_block > lds_total / 2) waves--;
+    const uint64_t tree_tables = 2ull * 256 * sizeof(uint32_t);  // roots and weights of a chunk
+    if (n_trees_ && compact_ok_ && waves * row_block + tree_tables + 8ull * largest_tree_ <= lds_total) {
+        const uint32_t cap = (uint32_t)((lds_total - waves * row_block - tree_tables) / 8);
+        plan_chunks(cap);
+        a.compact = compact_.get();
+        a.chunk_tree = chunk_tree_.get();
+        a.chunk_node = chunk_node_.get();
+        a.n_chunks = n_chunks_;
+        a.chunk_cap = cap;
+        const uint64_t blocks = (n + 63) / 64;
+        const uint64_t grid = std::min<uint64_t>((blocks + waves - 1) / waves, (uint64_t)dev_.cu_count());
+        const char *k = missing != missing ? "hbr_predict_chunked_nan" : "hbr_predict_chunked";
+        dev_.launch(k, dim3((uint32_t)grid), dim3(64 * waves), a,
+                    (uint32_t)(8ull * cap + tree_tables + waves * row_block));
+        return;
+    }
+    // rows staged in LDS when 64 of them fit in a quarter of a CU's LDS
+    const uint64_t lds = n_cols * 65ull * sizeof(float);
+    if (n_trees_ && lds <= 40ull * 1024) {
+        const uint64_t blocks = (n + 63) / 64;
+        const uint64_t grid = std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count() * 64);
+        dev_.launch("hbr_predict_staged", dim3((uint32_t)grid), dim3(64), a, (uint32_t)lds);
+        return;
+    }
     dev_.launch("hbr_predict", dim3((uint32_t)((n + 255) / 256)), dim3(256), a);
+}
+
+// Consecutive whole trees per chunk, as many as `cap` nodes hold (at most
+// 256 trees, the kernel's root and weight tables).
+void Forest::plan_chunks(uint32_t cap) {
+    if (cap == chunk_cap_ && n_chunks_) return;
+    std::vector<uint32_t> tree{0}, node{0};
+    uint32_t used = 0, at = 0;
+    for (uint64_t t = 0; t < n_trees_; t++) {
+        if (used + tree_nodes_[t] > cap || (uint32_t)t - tree.back() >= 256) {
+            tree.push_back((uint32_t)t);
+            node.push_back(at);
+            used = 0;
+        }
+        used += tree_nodes_[t];
+        at += tree_nodes_[t];
+    }
+    tree.push_back((uint32_t)n_trees_);
+    node.push_back(at);
+    n_chunks_ = (uint32_t)tree.size() - 1;
+    chunk_cap_ = cap;
+    chunk_tree_.resize(tree.size());
+    chunk_node_.resize(node.size());
+    chunk_tree_.upload(tree.data(), tree.size(), dev_.stream());
+    chunk_node_.upload(node.data(), node.size(), dev_.stream());
+    dev_.sync();
 }
 
 }  // namespace hbr

@@ -28,6 +28,17 @@ private:
     uint32_t n_outputs_ = 1;
     uint32_t max_feature_ = 0;
     DBuf<uint32_t> value_, meta_, left_, root_, output_;
+    DBuf<PredNode> nodes_;
+    // compact nodes for the chunked walk (absent when a feature id or a
+    // child offset does not fit the compact record)
+    bool compact_ok_ = false;
+    DBuf<CompactNode> compact_;
+    std::vector<uint32_t> tree_nodes_;  // nodes per tree
+    uint32_t largest_tree_ = 0;
+    // chunk tables for the last LDS capacity used
+    uint32_t chunk_cap_ = 0, n_chunks_ = 0;
+    DBuf<uint32_t> chunk_tree_, chunk_node_;
+    void plan_chunks(uint32_t cap);
     DBuf<int32_t> orig_;
     DBuf<float> weight_, base_;
 };

@@ -64,10 +64,9 @@ hipFunction_t Device::function(const char *kernel) {
     return f;
 }
 
-void Device::launch_raw(const char *kernel, dim3 grid, dim3 block, const void *args, size_t size) {
+void Device::launch_raw(const char *kernel, dim3 grid, dim3 block, const void *args, uint32_t lds_bytes) {
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) return;
     hipFunction_t f = function(kernel);
-    (void)size;
     // one by-value struct parameter: its address is the parameter's
     void *params[] = {const_cast<void *>(args)};
     const bool timed = profiling_ && std::strncmp(kernel, profile_prefix_.c_str(), profile_prefix_.size()) == 0;
@@ -77,7 +76,7 @@ void Device::launch_raw(const char *kernel, dim3 grid, dim3 block, const void *a
         ev.stop = take_event();
         HBR_HIP(hipEventRecord(ev.start, stream_));
     }
-    HBR_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream_, params,
+    HBR_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, lds_bytes, stream_, params,
                                   nullptr));
     if (timed) {
         HBR_HIP(hipEventRecord(ev.stop, stream_));

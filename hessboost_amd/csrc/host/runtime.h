@@ -44,8 +44,8 @@ public:
     void activate() const;
 
     template <typename Args>
-    void launch(const char *kernel, dim3 grid, dim3 block, const Args &args) {
-        launch_raw(kernel, grid, block, &args, sizeof(Args));
+    void launch(const char *kernel, dim3 grid, dim3 block, const Args &args, uint32_t lds_bytes = 0) {
+        launch_raw(kernel, grid, block, &args, lds_bytes);
     }
     void sync();
 
@@ -60,7 +60,7 @@ public:
     void reset_stats();
 
 private:
-    void launch_raw(const char *kernel, dim3 grid, dim3 block, const void *args, size_t size);
+    void launch_raw(const char *kernel, dim3 grid, dim3 block, const void *args, uint32_t lds_bytes);
     hipFunction_t function(const char *kernel);
     void drain_events();
 

@@ -82,12 +82,12 @@ __device__ __forceinline__ void load_bins(const uint8_t *p, uint32_t (&w)[FG / 4
     }
 }
 
-// Row loop of one workgroup. ROT: lane l starts at feature l mod FG (bytes
+// Row loop of one workgroup. Lane l starts at feature l mod FG (the bytes
 // rotated in registers), so that rows piled in one bin of one feature do not
-// all hit the same LDS word in one instruction; features past nf then go to
-// a per-lane dummy word instead of a branch. U rows per thread are loaded
-// before any of them is added, to keep U gathers in flight.
-template <int FG, bool ROT, int U>
+// all hit the same LDS word in one instruction (on data with point masses
+// this runs 2.3x faster than feature-in-lockstep, and as fast on smooth
+// data); features past nf go to a per-lane dummy word instead of a branch.
+template <int FG>
 __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
     constexpr int W = FG / 4;
     constexpr uint32_t kDummy = FG * kLdsFeature;
@@ -107,51 +107,23 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
     const int eg = a.scale->exp_g, eh = a.scale->exp_h;
     const uint32_t *rows = a.rows[nd.seg.buf] + nd.seg.offset;
     const uint32_t lane = lane_id();
-    const uint32_t rot = ROT ? lane & (FG - 1) : 0u;
+    const uint32_t rot = lane & (FG - 1);
     const uint32_t end = t.row0 + t.rows;
-    const uint32_t step = blockDim.x;
-    for (uint32_t j0 = t.row0 + threadIdx.x; j0 < end; j0 += U * step) {
-        uint32_t w[U][W];
-        unsigned long long qg[U], qh[U];
-        bool live[U];
+    for (uint32_t j = t.row0 + threadIdx.x; j < end; j += blockDim.x) {
+        const uint32_t r = nd.contiguous ? nd.seg.offset + j : rows[j];
+        const GPair p = a.gpair[r];
+        uint32_t w[W];
+        load_bins<FG>(a.bins8 + (size_t)r * a.stride + f0, w);
+        const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
+        const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
+        rotate_bytes<W>(w, rot);
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint32_t j = j0 + (uint32_t)u * step;
-            live[u] = j < end;
-            // a row past the end reads row 0 (it exists) and is not added
-            const uint32_t r = live[u] ? (nd.contiguous ? nd.seg.offset + j : rows[j]) : 0u;
-            const GPair p = a.gpair[r];
-            load_bins<FG>(a.bins8 + (size_t)r * a.stride + f0, w[u]);
-            qg[u] = (unsigned long long)quantize(p.g, eg);
-            qh[u] = (unsigned long long)quantize(p.h, eh);
-        }
-        if (ROT) {
-#pragma unroll
-            for (int u = 0; u < U; u++) rotate_bytes<W>(w[u], rot);
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (!live[u]) break;  // rows past the tile end come last
-            if (ROT) {
-#pragma unroll
-                for (int f = 0; f < FG; f++) {
-                    const uint32_t ff = ((uint32_t)f + rot) & (FG - 1);
-                    const uint32_t bin = (w[u][f >> 2] >> ((f & 3) * 8)) & 0xffu;
-                    const uint32_t at = ff < nf ? ff * kLdsFeature + bin : kDummy + lane;
-                    atomicAdd(&lg[at], qg[u]);
-                    atomicAdd(&lh[at], qh[u]);
-                }
-            } else {
-#pragma unroll
-                for (int f = 0; f < FG; f++) {
-                    if ((uint32_t)f < nf) {
-                        const uint32_t bin = (w[u][f >> 2] >> ((f & 3) * 8)) & 0xffu;
-                        const uint32_t at = (uint32_t)f * kLdsFeature + bin;
-                        atomicAdd(&lg[at], qg[u]);
-                        atomicAdd(&lh[at], qh[u]);
-                    }
-                }
-            }
+        for (int f = 0; f < FG; f++) {
+            const uint32_t ff = ((uint32_t)f + rot) & (FG - 1);
+            const uint32_t bin = (w[f >> 2] >> ((f & 3) * 8)) & 0xffu;
+            const uint32_t at = ff < nf ? ff * kLdsFeature + bin : kDummy + lane;
+            atomicAdd(&lg[at], qg);
+            atomicAdd(&lh[at], qh);
         }
     }
     __syncthreads();
@@ -250,16 +222,9 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
 }
 
 // Launched with 512 or 1024 threads.
-#define HBR_HIST_DENSE8(FG, ROT, U, NAME) \
-    extern "C" __global__ __launch_bounds__(1024) void NAME(HistArgs a) { hist_dense8<FG, ROT, U>(a); }
-HBR_HIST_DENSE8(8, true, 1, hbr_hist_dense8_fg8)
-HBR_HIST_DENSE8(16, true, 1, hbr_hist_dense8_fg16)
-HBR_HIST_DENSE8(32, true, 1, hbr_hist_dense8_fg32)
-HBR_HIST_DENSE8(32, true, 2, hbr_hist_dense8_fg32_u2)
-HBR_HIST_DENSE8(32, false, 1, hbr_hist_dense8_fg32_plain)
-HBR_HIST_DENSE8(32, false, 2, hbr_hist_dense8_fg32_plain_u2)
-HBR_HIST_DENSE8(16, true, 2, hbr_hist_dense8_fg16_u2)
-HBR_HIST_DENSE8(16, false, 2, hbr_hist_dense8_fg16_plain_u2)
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg8(HistArgs a) { hist_dense8<8>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16(HistArgs a) { hist_dense8<16>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32(HistArgs a) { hist_dense8<32>(a); }
 extern "C" __global__ __launch_bounds__(512) void hbr_hist_csr(HistArgs a) { hist_csr(a); }
 
 // Nodes cut into several tiles: the slot is the sum of the tiles' partials.

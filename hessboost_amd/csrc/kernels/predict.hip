@@ -1,10 +1,19 @@
-// Batched ensemble prediction: one thread per row, trees in order.
+// Batched ensemble prediction: one lane per row, trees in order.
 //
 // Restates the margin walk (model/predict.rs:60-193, compact/mod.rs:1052-1095):
 // out = base_score, then for every tree in ascending order
 // out[output(t)] += weight(t) * leaf(t, row) in f32 (a multiply, then an
 // add); a present value goes left iff value < threshold, a missing one
 // follows default_left (tree/mod.rs:52-58).
+//
+// hbr_predict_staged: a workgroup is one wave and 64 rows. The rows are
+// copied into LDS feature-major (coalesced global reads; row `lane` of
+// feature f at f * 65 + lane, so lanes reading different features hit
+// different banks), then every lane walks its row through all trees, four
+// trees at a time so that four node loads are in flight; the leaf values
+// are still added one tree after another, in order. Nodes are 16-byte
+// records read through the caches. hbr_predict reads features from the
+// row-major rows directly (rows too wide for LDS).
 #include "common.h"
 
 using namespace hbr;
@@ -19,6 +28,44 @@ __device__ __forceinline__ uint32_t walk(const PredictArgs &a, const float *row,
         const bool miss = a.missing_is_nan ? __builtin_isnan(v) : (v == a.missing);
         const bool left = miss ? ((meta >> 30) & 1u) != 0 : (v < __uint_as_float(a.node_value[nid]));
         nid = a.node_left[nid] + (left ? 0u : 1u);
+    }
+}
+
+constexpr uint32_t kPredLanes = 64;
+constexpr uint32_t kPredPitch = 65;  // LDS words per feature (64 rows + 1)
+constexpr int kPredChains = 8;
+
+// Copy a block of `rows` consecutive rows (rows * n_cols floats, contiguous;
+// 16-byte aligned when the rows are, blocks starting at multiples of 64 rows) into LDS
+// feature-major, s_x[f * kPredPitch + row]. The wave's lanes read 16 bytes
+// each, consecutive, several loads in flight.
+__device__ __forceinline__ void stage_rows(float *s_x, const float *src, uint32_t rows, uint32_t n_cols,
+                                           uint32_t lane) {
+    const uint32_t total = rows * n_cols;
+    const uint32_t n4 = ((uintptr_t)src & 15u) == 0 ? total / 4 : 0;  // an unaligned caller pointer: scalar
+    const float inv = 1.0f / (float)n_cols;
+    const float4 *src4 = reinterpret_cast<const float4 *>(src);
+#pragma unroll 5
+    for (uint32_t i = lane; i < n4; i += kPredLanes) {
+        const float4 v = src4[i];
+        const uint32_t e = i * 4;
+        uint32_t rl = (uint32_t)((float)e * inv);  // e < 2^24: exact, then corrected
+        if (rl * n_cols > e) rl--;
+        if ((rl + 1) * n_cols <= e) rl++;
+        uint32_t f = e - rl * n_cols;
+        const float vals[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            s_x[f * kPredPitch + rl] = vals[j];
+            if (++f == n_cols) {
+                f = 0;
+                rl++;
+            }
+        }
+    }
+    for (uint32_t e = n4 * 4 + lane; e < total; e += kPredLanes) {
+        const uint32_t rl = e / n_cols;
+        s_x[(e - rl * n_cols) * kPredPitch + rl] = src[e];
     }
 }
 
@@ -49,3 +96,175 @@ extern "C" __global__ __launch_bounds__(256) void hbr_predict(PredictArgs a) {
         *o = *o + contrib;
     }
 }
+
+// Dynamic LDS: n_cols * kPredPitch floats. Grid-stride over 64-row blocks.
+extern "C" __global__ __launch_bounds__(64) void hbr_predict_staged(PredictArgs a) {
+    extern __shared__ float s_x[];
+    const uint32_t lane = threadIdx.x;
+    const uint32_t n_blocks = (a.n + kPredLanes - 1) / kPredLanes;
+    for (uint32_t blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
+        const uint32_t r0 = blk * kPredLanes;
+        const uint32_t rows = min(kPredLanes, a.n - r0);
+        stage_rows(s_x, a.x + (size_t)r0 * a.n_cols, rows, a.n_cols, lane);
+        __syncthreads();
+        if (lane < rows) {
+            const uint32_t r = r0 + lane;
+            const float *xr = s_x + lane;
+            float *out = a.out + (size_t)r * a.n_outputs;
+            float acc = a.base_score[0];
+            if (a.n_outputs != 1)
+                for (uint32_t c = 0; c < a.n_outputs; c++) out[c] = a.base_score[c];
+            for (uint32_t t0 = 0; t0 < a.n_trees; t0 += kPredChains) {
+                uint32_t nid[kPredChains];
+                PredNode nd[kPredChains];
+#pragma unroll
+                for (int k = 0; k < kPredChains; k++) {
+                    nid[k] = a.tree_root[min(t0 + (uint32_t)k, a.n_trees - 1)];
+                    nd[k] = a.nodes[nid[k]];
+                }
+                // every chain moves one level per round until all sit at
+                // leaves (a chain at its leaf re-reads it; no branches, so
+                // the loads of all chains overlap)
+                for (;;) {
+                    float v[kPredChains];
+#pragma unroll
+                    for (int k = 0; k < kPredChains; k++) v[k] = xr[(nd[k].meta & 0xfffffu) * kPredPitch];
+                    bool open = false;
+#pragma unroll
+                    for (int k = 0; k < kPredChains; k++) {
+                        const bool miss = a.missing_is_nan ? __builtin_isnan(v[k]) : (v[k] == a.missing);
+                        const bool left =
+                            miss ? ((nd[k].meta >> 30) & 1u) != 0 : (v[k] < __uint_as_float(nd[k].value));
+                        nid[k] = (nd[k].meta >> 31) ? nid[k] : nd[k].left + (left ? 0u : 1u);
+                    }
+#pragma unroll
+                    for (int k = 0; k < kPredChains; k++) {
+                        nd[k] = a.nodes[nid[k]];
+                        open = open || !(nd[k].meta >> 31);
+                    }
+                    if (!open) break;
+                }
+#pragma unroll
+                for (int k = 0; k < kPredChains; k++) {
+                    const uint32_t t = t0 + (uint32_t)k;
+                    if (t < a.n_trees) {
+                        if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = nd[k].orig;
+                        const float contrib = a.tree_weight[t] * __uint_as_float(nd[k].value);
+                        if (a.n_outputs == 1) {
+                            acc = acc + contrib;
+                        } else {
+                            float *o = out + a.tree_output[t];
+                            *o = *o + contrib;
+                        }
+                    }
+                }
+            }
+            if (a.n_outputs == 1) out[0] = acc;
+        }
+        __syncthreads();
+    }
+}
+
+// Trees resident, rows streamed. The forest is cut into chunks of whole
+// trees that fit the LDS node table; for each chunk in order, the
+// workgroup copies the chunk's compact nodes, roots and weights into LDS,
+// then every wave stages its 64-row blocks (feature-major, as above) and
+// walks them through the chunk's trees. Each row's margin is carried from
+// chunk to chunk in `out` (the same wave owns the same rows in every
+// chunk), so the f32 adds keep the tree order. MISSING_NAN: the missing
+// value is NaN (the comparison that tests it is specialised). Dynamic LDS:
+// chunk_cap compact nodes, kChunkTrees roots and weights, then one
+// n_cols * kPredPitch block per wave.
+constexpr uint32_t kChunkTrees = 256;
+
+template <bool MISSING_NAN>
+__device__ __forceinline__ void predict_chunked(const PredictArgs &a) {
+    extern __shared__ uint32_t lds[];
+    CompactNode *s_nodes = reinterpret_cast<CompactNode *>(lds);
+    uint32_t *s_root = lds + 2 * a.chunk_cap;
+    float *s_weight = reinterpret_cast<float *>(s_root + kChunkTrees);
+    const uint32_t wave = threadIdx.x / kWave, lane = lane_id();
+    const uint32_t waves = blockDim.x / kWave;
+    float *s_x = s_weight + kChunkTrees + wave * (a.n_cols * kPredPitch);
+    const float *xr = s_x + lane;
+    const uint32_t n_blocks = (a.n + kPredLanes - 1) / kPredLanes;
+    for (uint32_t c = 0; c < a.n_chunks; c++) {
+        const uint32_t nb = a.chunk_node[c], cnt = a.chunk_node[c + 1] - nb;
+        const uint32_t t_lo = a.chunk_tree[c], t_hi = a.chunk_tree[c + 1];
+        __syncthreads();  // every wave is done with the previous chunk
+        for (uint32_t i = threadIdx.x; i < cnt; i += blockDim.x) s_nodes[i] = a.compact[nb + i];
+        for (uint32_t i = threadIdx.x; i < t_hi - t_lo; i += blockDim.x) {
+            s_root[i] = a.tree_root[t_lo + i] - nb;
+            s_weight[i] = a.tree_weight[t_lo + i];
+        }
+        __syncthreads();
+        for (uint32_t blk = blockIdx.x * waves + wave; blk < n_blocks; blk += gridDim.x * waves) {
+            const uint32_t r0 = blk * kPredLanes;
+            const uint32_t rows = min(kPredLanes, a.n - r0);
+            const float *src = a.x + (size_t)r0 * a.n_cols;
+            const uint32_t r = r0 + min(lane, rows - 1);
+            float *out = a.out + (size_t)r * a.n_outputs;
+            float acc = c == 0 ? a.base_score[0] : out[0];
+            // the wave's previous walk has read its block: lanes finish in lockstep
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            stage_rows(s_x, src, rows, a.n_cols, lane);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (c == 0 && lane < rows && a.n_outputs != 1)
+                for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = a.base_score[o];
+            if (lane >= rows) continue;
+            for (uint32_t t0 = t_lo; t0 < t_hi; t0 += kPredChains) {
+                uint32_t nid[kPredChains];
+                CompactNode nd[kPredChains];
+#pragma unroll
+                for (int k = 0; k < kPredChains; k++) {
+                    nid[k] = s_root[min(t0 + (uint32_t)k, t_hi - 1) - t_lo];
+                    nd[k] = s_nodes[nid[k]];
+                }
+                // branch-free rounds: a chain at its leaf re-reads it, so
+                // the LDS reads of all chains overlap
+                for (;;) {
+                    float v[kPredChains];
+#pragma unroll
+                    for (int k = 0; k < kPredChains; k++) v[k] = xr[(nd[k].meta & 0xffffu) * kPredPitch];
+                    bool open = false;
+#pragma unroll
+                    for (int k = 0; k < kPredChains; k++) {
+                        const uint32_t meta = nd[k].meta;
+                        const bool miss = MISSING_NAN ? v[k] != v[k] : v[k] == a.missing;
+                        uint32_t right = v[k] < __uint_as_float(nd[k].value) ? 0u : 1u;
+                        right = miss ? (~meta >> 30) & 1u : right;  // missing: right unless default_left
+                        const uint32_t next = nid[k] + ((meta >> 16) & 0x3fffu) + right;
+                        nid[k] = (meta >> 31) ? nid[k] : next;
+                    }
+#pragma unroll
+                    for (int k = 0; k < kPredChains; k++) {
+                        nd[k] = s_nodes[nid[k]];
+                        open = open || !(nd[k].meta >> 31);
+                    }
+                    if (!open) break;
+                }
+#pragma unroll
+                for (int k = 0; k < kPredChains; k++) {
+                    const uint32_t t = t0 + (uint32_t)k;
+                    if (t < t_hi) {
+                        if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.node_orig[nb + nid[k]];
+                        const float contrib = s_weight[t - t_lo] * __uint_as_float(nd[k].value);
+                        if (a.n_outputs == 1) {
+                            acc = acc + contrib;
+                        } else {
+                            float *o = out + a.tree_output[t];
+                            *o = *o + contrib;
+                        }
+                    }
+                }
+            }
+            if (a.n_outputs == 1) out[0] = acc;
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void hbr_predict_chunked_nan(PredictArgs a) { predict_chunked<true>(a); }
+extern "C" __global__ __launch_bounds__(256) void hbr_predict_chunked(PredictArgs a) { predict_chunked<false>(a); }

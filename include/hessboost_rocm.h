@@ -377,6 +377,10 @@ int hbr_device_alloc(int ordinal, uint64_t bytes, void **out);
 int hbr_device_free(int ordinal, void *p);
 int hbr_device_upload(int ordinal, void *dst, const void *src, uint64_t bytes);
 int hbr_device_download(int ordinal, void *dst, const void *src, uint64_t bytes);
+/* Device-to-device copy (completes before the call returns). No counterpart
+ * in the reference: a plain copy of known size, which profiles use to scale
+ * hardware byte counters. */
+int hbr_device_copy(int ordinal, void *dst, const void *src, uint64_t bytes);
 
 #ifdef __cplusplus
 }

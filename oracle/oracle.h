@@ -23,8 +23,20 @@
  *   train.c     training/round.rs:214-424, training/margins.rs:129-289,
  *               training/train.rs:406-436
  *
- * Parity pins are listed per function in the test suite (tests/test_oracle_*.py)
- * and in the oracle section of the design notes.
+ * Pins (tests/test_oracle.py): the reference's saved early-stopping model is
+ * retrained bit for bit (sketch, index, hist, split, depthwise grow,
+ * squared error, train, predict); nine saved models' margins are reproduced
+ * bit for bit (predict); the reference's KATs pin the gains, the separating
+ * split and the blocked-sum order; closed forms pin cuts of few distinct
+ * values, bin assignment, partition routing, both logistic paths, softmax
+ * (to 1e-6) and the intercepts.
+ *
+ * Parity unpinned (nothing the reference holds reaches them):
+ *   - the weighted sketch's prune/merge on data with more distinct values
+ *     than max_bin (checked by quantile properties only);
+ *   - the lossguide expansion order (heap ties), grow.c;
+ *   - softmax gradients bit for bit: they call the host libm expf, as the
+ *     reference's f32::exp does, so bits match only for the same libm.
  */
 #ifndef HB_ORACLE_H
 #define HB_ORACLE_H
