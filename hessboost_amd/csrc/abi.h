@@ -117,7 +117,8 @@ struct PartSplit {
     uint32_t tile_begin;    // first partition tile of this split
     uint32_t fresh_slot;    // histogram slot for the built child
     uint32_t parent_slot;   // parent's slot, becomes the sibling's
-    uint32_t pad[2];
+    uint32_t identity;      // the parent's rows are seg.offset + j (no row list is read)
+    uint32_t pad;
 };
 
 // Device decision per split after the scan of tile counts.
@@ -170,12 +171,13 @@ struct HistNode {
     uint32_t contiguous; // rows are seg.offset .. seg.offset+len (no row buffer)
     uint32_t tile_begin; // first row tile (written by the plan kernel)
     uint32_t n_tiles;    // row tiles of the node (written by the plan kernel)
-    uint32_t pad[2];
+    uint32_t pad[2];     // [0]: first partial of a multi-tile node (plan kernel)
 };
 
 // Device tiling of a histogram launch: each node's rows cut into tiles of
-// `tile_rows` (a multiple of 512, at least min_rows), sized so that the
-// launch holds about target_tiles tiles; at most target_tiles + n_nodes.
+// `tile_rows` rows (a multiple of 64, at least min_rows), the smallest size
+// that gives at most target_tiles tiles (one tile per node when the nodes
+// outnumber it); never more than target_tiles + n_nodes tiles.
 struct PlanArgs {
     HistNode *nodes;
     uint32_t n_nodes;
@@ -276,6 +278,17 @@ struct ScanArgs {
     uint32_t dense;          // index without missing values: forward pass only
     ScanBest *per_feature;   // n_nodes * n_features
     ScanBest *best;          // n_nodes
+    const QBin *root_total;  // nodes flagged kScanDeviceRoot take total and root gain from here
+};
+
+// ScanNode.pad flag: the node's total is *root_total (on the device) and its
+// root gain is computed there from it (the unconstrained root).
+constexpr uint32_t kScanDeviceRoot = 1;
+
+// Per-tree quantisation exponents from the folded maxima, on the device.
+struct FinishArgs {
+    QScale *scale;
+    uint64_t n_rows;
 };
 
 // ---- leaves -----------------------------------------------------------------------

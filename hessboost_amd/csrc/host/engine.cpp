@@ -1,5 +1,7 @@
 #include "engine.h"
 
+#include "split_math.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -220,12 +222,13 @@ void Engine::prepare(const float *gpair, uint64_t n) {
     q.exp_g = exp_for(q.max_g_bits, n_rows_);
     q.exp_h = exp_for(q.max_h_bits, n_rows_);
     scale_host_ = q;
+    scale_checked_ = true;
     scale_.upload(&scale_host_, 1, dev_.stream());
     dev_.sync();
     if (q.nonfinite) fail(kRefused, "a staged gradient is not finite");
 }
 
-bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
+void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     if (!labels_loaded_) fail(kInvalid, "gradients: no labels since load_margins");
     if (outputs_ != 1 || output != 0) fail(kRefused, "device gradients run for one output");
     hipStream_t s = dev_.stream();
@@ -249,13 +252,15 @@ bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
     const uint32_t grad_blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)),
                                                     (uint32_t)dev_.cu_count() * 8);
     dev_.launch("hbr_gradients", dim3(grad_blocks), dim3(kThreads), a);
-    QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
-    scale_.download(q, 1, s);
-    dev_.sync();
-    stage_.reset();
-    QScale host = *q;
+    last_loss_ = loss;
+}
+
+// The rows the kernel listed (the reference computes them with libm's expf)
+// are computed here; then the exponents, on the host, and the scale goes
+// back to the device.
+bool Engine::finish_gradients_on_host(QScale host) {
+    hipStream_t s = dev_.stream();
     if (host.scalar_rows) {
-        // rows the reference computes with libm's expf: computed here
         std::vector<uint32_t> list(host.scalar_rows);
         scalar_list_.download(list.data(), list.size(), s);
         std::vector<float> m;
@@ -268,25 +273,44 @@ bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
             for (size_t k = 0; k < list.size(); k++) margins_.download(&m[k], 1, s, list[k]);
         }
         dev_.sync();
+        std::vector<GPair> fixed(list.size());
         for (size_t k = 0; k < list.size(); k++) {
             const uint32_t r = list[k];
             const float mr = whole ? m[r] : m[k];
             const float w = has_weights_ ? weights_host_[r] : 1.0f;
-            GPair p;
-            logistic_scalar(mr, labels_host_[r], w, loss.scale_pos_weight, loss.min_hess, &p.g, &p.h);
+            GPair &p = fixed[k];
+            logistic_scalar(mr, labels_host_[r], w, last_loss_.scale_pos_weight, last_loss_.min_hess, &p.g, &p.h);
             if (!std::isfinite(p.g) || !std::isfinite(p.h)) host.nonfinite++;
             host.max_g_bits = std::max(host.max_g_bits, abs_bits(p.g));
             host.max_h_bits = std::max(host.max_h_bits, abs_bits(p.h));
-            gpair_.upload(&p, 1, s, r);
-            dev_.sync();
         }
+        for (size_t k = 0; k < list.size(); k++) gpair_.upload(&fixed[k], 1, s, list[k]);
     }
+    host.scalar_rows = 0;
     host.exp_g = exp_for(host.max_g_bits, n_rows_);
     host.exp_h = exp_for(host.max_h_bits, n_rows_);
     scale_host_ = host;
     scale_.upload(&scale_host_, 1, s);
     dev_.sync();
     return host.nonfinite == 0;
+}
+
+bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
+    launch_gradients(loss, output);
+    QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
+    scale_.download(q, 1, dev_.stream());
+    dev_.sync();
+    const QScale host = *q;
+    stage_.reset();
+    scale_checked_ = true;
+    return finish_gradients_on_host(host);
+}
+
+void Engine::compute_gradients_async(const hbr_device_loss &loss, uint32_t output) {
+    launch_gradients(loss, output);
+    FinishArgs f{scale_.get(), n_rows_};
+    dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
+    scale_checked_ = false;  // grow_root reads the scale back and checks it
 }
 
 // ---- tree growth -------------------------------------------------------------------
@@ -297,11 +321,19 @@ void Engine::ensure_rows() {
 
 uint64_t Engine::begin_tree() {
     ensure_rows();
-    IotaArgs a{rows_[0].get(), 0, (uint32_t)n_rows_};
-    dev_.launch("hbr_iota", dim3(ceil_div(n_rows_, kThreads)), dim3(kThreads), a);
+    // the root's rows are the identity run: kernels that take the root read
+    // no row list, and the list itself is written only if something asks
     identity_rows0_ = true;
+    rows0_written_ = false;
     counters.trees++;
     return ++tree_;
+}
+
+void Engine::write_identity_rows() {
+    if (!identity_rows0_ || rows0_written_) return;
+    IotaArgs a{rows_[0].get(), 0, (uint32_t)n_rows_};
+    dev_.launch("hbr_iota", dim3(ceil_div(n_rows_, kThreads)), dim3(kThreads), a);
+    rows0_written_ = true;
 }
 
 // A segment whose rows are the identity run 0..n-1 (the root of an
@@ -329,6 +361,57 @@ QBin Engine::root_total(const Segment &sg) {
     QBin t = *out;
     stage_.reset();
     return t;
+}
+
+// The root without a host synchronisation before its split search: the
+// total sums into d_total_, the histogram builds, and the scan takes the
+// total and the root gain from the device. One synchronisation then brings
+// back the winner, the total and the scale. After asynchronous gradients
+// whose kernel left rows to the host's scalar path, those rows are computed
+// here and the root is done again synchronously.
+bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best) {
+    hipStream_t s = dev_.stream();
+    d_total_.zero(s);
+    TotalArgs t{};
+    const bool ident = contiguous(seg);
+    t.rows = ident ? nullptr : rows_[seg.buf].get() + seg.offset;
+    t.first = ident ? seg.offset : 0;
+    t.n = seg.len;
+    t.gpair = gpair_.get();
+    t.scale = scale_.get();
+    t.out = d_total_.get();
+    dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(seg.len, kThreads)), 2048)),
+                dim3(kThreads), t);
+    build_nodes({seg}, {slot});
+    ScanNode n{};
+    n.slot = slot;
+    n.lower = lower;
+    n.upper = upper;
+    n.pad = kScanDeviceRoot;
+    ScanBest *b = static_cast<ScanBest *>(stage_.alloc(sizeof(ScanBest)));
+    launch_scan({n}, b);
+    QBin *tot = static_cast<QBin *>(stage_.alloc(sizeof(QBin)));
+    QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
+    d_total_.download(tot, 1, s);
+    scale_.download(q, 1, s);
+    dev_.sync();
+    *best = *b;
+    *total = *tot;
+    const QScale host = *q;
+    stage_.reset();
+    if (scale_checked_) return true;
+    scale_checked_ = true;
+    if (host.scalar_rows == 0 && host.nonfinite == 0) {
+        scale_host_ = host;
+        return true;
+    }
+    if (!finish_gradients_on_host(host)) return false;
+    *total = root_total(seg);
+    build_nodes({seg}, {slot});
+    const double g = std::ldexp((double)total->g, scale_host_.exp_g), h = std::ldexp((double)total->h, scale_host_.exp_h);
+    const Reg r{scan_params_.lambda, scan_params_.alpha, scan_params_.max_delta_step, scan_params_.min_child_weight};
+    *best = scan({ScanInput{slot, *total, xgb_node_gain(g, h, r, lower, upper), lower, upper}})[0];
+    return true;
 }
 
 uint32_t Engine::alloc_slot() {
@@ -388,6 +471,7 @@ void Engine::set_scan_params(const ScanParams &p, const std::vector<int8_t> &mon
 // several tiles); CSR tiles add into slots zeroed first.
 void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *splits_dev, const uint32_t *rows0) {
     if (nodes.empty()) return;
+    if (gpair_.size() < n_rows_ || !gpair_.get()) fail(kInvalid, "histograms: no gradients staged");
     hipStream_t s = dev_.stream();
     const uint32_t n = (uint32_t)nodes.size();
     const uint32_t fg = hist_features_per_group;
@@ -506,6 +590,7 @@ void Engine::launch_scan(const std::vector<ScanNode> &nodes, ScanBest *host_out)
     a.dense = dense_ ? 1u : 0u;
     a.per_feature = d_per_feature_.get();
     a.best = d_best_.get();
+    a.root_total = d_total_.get();
     dev_.launch("hbr_scan_features", dim3(ceil_div(pairs, 4)), dim3(256), a);
     dev_.launch("hbr_scan_merge", dim3((uint32_t)nodes.size()), dim3(64), a);
     d_best_.download(host_out, nodes.size(), s);
@@ -548,6 +633,7 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
         p.feature = l.feature;
         p.limit = l.limit;
         p.default_left = l.default_left;
+        p.identity = contiguous(l.seg) ? 1u : 0u;
         p.tile_begin = tiles;
         if (!terminal) {
             fresh[i] = alloc_slot();
@@ -586,7 +672,7 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
     a.n_rows = (uint32_t)n_rows_;
     a.words = words_;
     dev_.launch("hbr_part_count", dim3(tiles), dim3(kPartThreads), a);
-    dev_.launch("hbr_part_scan", dim3(P), dim3(kPartThreads), a);
+    dev_.launch("hbr_part_scan", dim3(P), dim3(1024), a);
     dev_.launch("hbr_part_scatter", dim3(tiles), dim3(kPartThreads), a);
 
     ScanBest *best_staged = nullptr;
@@ -663,6 +749,7 @@ void Engine::add_leaves(const std::vector<Segment> &segs, const std::vector<floa
         }
     }
     if (tile_leaf.empty()) return;
+    write_identity_rows();
     hipStream_t s = dev_.stream();
     upload_vec(d_leaves_, leaves, stage_, s);
     upload_vec(d_tile_leaf_, tile_leaf, stage_, s);
@@ -738,6 +825,7 @@ std::vector<QBin> Engine::build_rows(const uint32_t *rows, uint64_t m) {
 
 std::vector<uint32_t> Engine::rows_of(const Segment &sg) {
     std::vector<uint32_t> out(sg.len);
+    write_identity_rows();
     rows_[sg.buf].download(out.data(), sg.len, dev_.stream(), sg.offset);
     dev_.sync();
     return out;

@@ -3,6 +3,7 @@
 // steps the tree builder drives (the reference's HistogramBackend and
 // RowEngine, src/tree/hist/mod.rs:73-295).
 #pragma once
+#include <algorithm>
 #include <cstdint>
 #include <mutex>
 #include <string>
@@ -71,6 +72,17 @@ public:
     // Gradients of output `output` from the device margins; false when some
     // gradient is not finite.
     bool compute_gradients(const hbr_device_loss &loss, uint32_t output);
+    // The same without a host synchronisation: the exponents are computed on
+    // the device and checked by the next grow_root (which finishes on the
+    // host the rows the kernel left to the scalar path). Eligible when such
+    // rows are rare (not a tail of the 8-row vectors).
+    void compute_gradients_async(const hbr_device_loss &loss, uint32_t output);
+    bool gradients_async_ok(const hbr_device_loss &loss) const {
+        return loss.kind != HBR_LOSS_LOGISTIC || std::min<uint64_t>(loss.vector_rows, n_rows_) == n_rows_;
+    }
+    // The root's total, histogram (into `slot`) and split search with one
+    // host synchronisation; false when a gradient is not finite.
+    bool grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best);
     void read_margins(float *out, uint64_t n);
     void read_gradients(float *out, uint64_t n);
     const QScale &scale() const { return scale_host_; }
@@ -117,9 +129,14 @@ private:
     void ensure_rows();
     bool contiguous(const Segment &sg) const;
     bool identity_rows0_ = false;
+    bool rows0_written_ = false;
+    void write_identity_rows();  // buffer 0 := 0..n-1, once per tree, when a row list is read
     void launch_hist(const std::vector<HistNode> &nodes, const PartSplit *splits_dev, const uint32_t *rows0 = nullptr);
     void launch_scan(const std::vector<ScanNode> &nodes, ScanBest *host_out);
-    void finish_scale(uint32_t rows);
+    void launch_gradients(const hbr_device_loss &loss, uint32_t output);
+    bool finish_gradients_on_host(QScale staged);
+    hbr_device_loss last_loss_{};
+    bool scale_checked_ = true;  // the host has seen the scale of the staged gradients
 
     Device &dev_;
     uint64_t n_rows_ = 0;

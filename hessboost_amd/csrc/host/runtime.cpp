@@ -39,6 +39,16 @@ Device::Device(int ordinal) : ordinal_(ordinal) {
     std::string path = code_object_path();
     hipError_t e = hipModuleLoad(&module_, path.c_str());
     if (e != hipSuccess) fail(kDeviceError, "hipModuleLoad(" + path + "): " + hipGetErrorString(e));
+    // the kernels' argument records must be the ones this library fills
+    hipDeviceptr_t stamp_ptr = nullptr;
+    size_t stamp_size = 0;
+    e = hipModuleGetGlobal(&stamp_ptr, &stamp_size, module_, "hbr_abi_stamp");
+    if (e != hipSuccess || stamp_size != sizeof(uint32_t))
+        fail(kDeviceError, path + " carries no argument-layout stamp: rebuild hessboost_amd/csrc");
+    uint32_t stamp = 0;
+    HBR_HIP(hipMemcpy(&stamp, stamp_ptr, sizeof(stamp), hipMemcpyDeviceToHost));
+    if (stamp != HBR_ABI_STAMP)
+        fail(kDeviceError, path + " was built from a different abi.h than libhbrocm.so: rebuild hessboost_amd/csrc");
 }
 
 Device::~Device() {

@@ -124,9 +124,19 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool 
     root.nid = 0;
     root.depth = 0;
     root.seg = Segment{0, (uint32_t)e_.n_rows(), 0};
-    root.total = e_.root_total(root.seg);
     root.lower = -std::numeric_limits<double>::infinity();
     root.upper = std::numeric_limits<double>::infinity();
+    if (limit > 0) {
+        // total, histogram and search in one round trip (the root gain is
+        // computed on the device from the device total)
+        root.slot = e_.alloc_slot();
+        root.has_slot = true;
+        if (!e_.grow_root(root.seg, root.slot, (float)root.lower, (float)root.upper, &root.total, &root.best))
+            fail(kRefused, "a gradient is not finite: the round runs on the host");
+        root.searched = true;
+    } else {
+        root.total = e_.root_total(root.seg);
+    }
     const double rg = deq_g(root.total.g), rh = deq_h(root.total.h);
     TreeNode rn;
     rn.sum_hess = (float)rh;
@@ -135,15 +145,6 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool 
     h_.push_back(rh);
     lower_.push_back(root.lower);
     upper_.push_back(root.upper);
-    if (limit > 0) {
-        root.slot = e_.alloc_slot();
-        root.has_slot = true;
-        e_.build_nodes({root.seg}, {root.slot});
-        ScanInput in{root.slot, root.total, xgb_node_gain(rg, rh, p_.reg, root.lower, root.upper),
-                     (float)root.lower, (float)root.upper};
-        root.best = e_.scan({in})[0];
-        root.searched = true;
-    }
 
     if (p_.policy == HBR_GROW_DEPTHWISE) {
         std::vector<Open> frontier{root};
@@ -440,7 +441,11 @@ void Trainer::boost(uint64_t rounds) {
         loss.min_hess = 1e-16f;
         loss.max_input = 80.0f;
         loss.vector_rows = n_ >= 16 ? n_ - n_ % 8 : 0;
-        if (!e_.compute_gradients(loss, 0)) fail(kRefused, "a gradient is not finite: the round runs on the host");
+        if (e_.gradients_async_ok(loss)) {
+            e_.compute_gradients_async(loss, 0);  // checked at the root's synchronisation
+        } else if (!e_.compute_gradients(loss, 0)) {
+            fail(kRefused, "a gradient is not finite: the round runs on the host");
+        }
         grow_and_add(b, 0);
     }
 }

@@ -157,3 +157,21 @@ extern "C" __global__ __launch_bounds__(256) void hbr_total(TotalArgs a) {
         atomicAdd((unsigned long long *)&a.out->h, (unsigned long long)sh);
     }
 }
+
+// exp = e + ceil(log2 n) - 62 with M = m 2^e (m in [0.5, 1)) the maximum
+// magnitude, 0 for a zero or non-finite maximum: the host's exponent rule.
+__device__ __forceinline__ int32_t exponent_for(uint32_t bits, uint64_t rows) {
+    if (bits == 0 || bits >= 0x7f800000u) return 0;
+    int e = 0;
+    (void)__builtin_frexpf(__uint_as_float(bits), &e);
+    const int log_n = rows > 1 ? 64 - __builtin_clzll(rows - 1) : 0;
+    return e + log_n - 62;
+}
+
+extern "C" __global__ __launch_bounds__(64) void hbr_finish_scale(FinishArgs a) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    QScale q = *a.scale;
+    q.exp_g = exponent_for(q.max_g_bits, a.n_rows);
+    q.exp_h = exponent_for(q.max_h_bits, a.n_rows);
+    *a.scale = q;
+}

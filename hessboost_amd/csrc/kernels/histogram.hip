@@ -170,26 +170,77 @@ __device__ __forceinline__ void hist_csr(const HistArgs &a) {
 
 using namespace hbr;
 
+// Sum of one value per thread over the (256-thread) workgroup.
+__device__ __forceinline__ unsigned long long block_sum(unsigned long long v) {
+    __shared__ unsigned long long lds[256 / kWave];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+    __syncthreads();  // earlier readers of lds are done
+    if (lane_id() == 0) lds[threadIdx.x / kWave] = v;
+    __syncthreads();
+    unsigned long long total = 0;
+    for (uint32_t w = 0; w < 256 / kWave; w++) total += lds[w];
+    return total;
+}
+
 // One workgroup: resolve each node's rows, choose the tile size, number the
-// tiles (and the partials of nodes cut into several tiles).
+// tiles (and the partials of nodes cut into several tiles). The tile size is
+// the smallest that cuts the nodes into at most target_tiles tiles, so that
+// a launch is one wave of workgroups (no lone tail wave); when the nodes
+// outnumber the target, every node is one tile.
+constexpr uint32_t kPlanLdsNodes = 4096;
+
 extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
-    __shared__ unsigned long long sum_lds[256 / kWave];
-    unsigned long long sum = 0;
+    __shared__ uint32_t s_len[kPlanLdsNodes];  // node lengths, for the candidate counts
+    unsigned long long sum = 0, longest = 0;
     for (uint32_t i = threadIdx.x; i < a.n_nodes; i += blockDim.x) {
         HistNode nd = a.nodes[i];
         const Seg s = resolve_node(a, nd);
         a.nodes[i].seg = s;
+        if (i < kPlanLdsNodes) s_len[i] = s.len;
         sum += s.len;
+        longest = max(longest, (unsigned long long)s.len);
     }
+    const unsigned long long total = block_sum(sum);
+    {
+        __shared__ unsigned long long lds_max[256 / kWave];
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, kWave);
-    if (lane_id() == 0) sum_lds[threadIdx.x / kWave] = sum;
-    __syncthreads();
-    unsigned long long total = 0;
-    for (uint32_t w = 0; w < 256 / kWave; w++) total += sum_lds[w];
-    const unsigned long long want = (total + a.target_tiles - 1) / a.target_tiles;
-    const uint32_t tile_rows =
-        (uint32_t)((max(want, (unsigned long long)a.min_rows) + kHistThreads - 1) / kHistThreads * kHistThreads);
+        for (int d = 32; d >= 1; d >>= 1) longest = max(longest, __shfl_xor(longest, d, kWave));
+        if (lane_id() == 0) lds_max[threadIdx.x / kWave] = longest;
+        __syncthreads();
+        for (uint32_t w = 0; w < 256 / kWave; w++) longest = max(longest, lds_max[w]);
+    }
+    // Candidate sizes spaced geometrically over [lo, hi], one per thread,
+    // each counted against every node at once; the smallest that fits wins.
+    // hi = the longest node fits whenever the nodes do not outnumber the
+    // target (one tile each).
+    const unsigned long long lo =
+        max((total + a.target_tiles - 1) / a.target_tiles, (unsigned long long)a.min_rows);
+    const unsigned long long hi = max(longest, lo);
+    const double ratio = (double)hi / (double)lo;
+    unsigned long long cand = threadIdx.x == blockDim.x - 1
+                                  ? hi
+                                  : (unsigned long long)((double)lo * pow(ratio, (double)threadIdx.x /
+                                                                                          (double)(blockDim.x - 1)));
+    cand = min(max(cand, lo), hi);
+    const uint32_t c32 = (uint32_t)min(cand, 0xffffffffull);  // 32-bit divisions
+    unsigned long long c = 0;
+    for (uint32_t i = 0; i < a.n_nodes; i++) {
+        const uint32_t len = i < kPlanLdsNodes ? s_len[i] : a.nodes[i].seg.len;
+        c += len / c32 + (len % c32 != 0 ? 1u : 0u);
+    }
+    unsigned long long pick = c <= a.target_tiles || threadIdx.x == blockDim.x - 1 ? cand : ~0ull;
+    {
+        __shared__ unsigned long long lds_min[256 / kWave];
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) pick = min(pick, __shfl_xor(pick, d, kWave));
+        __syncthreads();
+        if (lane_id() == 0) lds_min[threadIdx.x / kWave] = pick;
+        __syncthreads();
+        for (uint32_t w = 0; w < 256 / kWave; w++) pick = min(pick, lds_min[w]);
+    }
+    const unsigned long long size = pick;
+    const uint32_t tile_rows = (uint32_t)((size + kWave - 1) / kWave * kWave);
     uint32_t carry = 0, part_carry = 0;
     for (uint32_t base = 0; base < a.n_nodes; base += blockDim.x) {
         const uint32_t i = base + threadIdx.x;

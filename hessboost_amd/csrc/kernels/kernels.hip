@@ -5,3 +5,7 @@
 #include "partition.hip"
 #include "split.hip"
 #include "predict.hip"
+
+// The abi.h checksum this code object was built with (checked by the host
+// library at module load).
+extern "C" __device__ const unsigned int hbr_abi_stamp = HBR_ABI_STAMP;

@@ -40,6 +40,8 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
 
 using namespace hbr;
 
+// Every load of the tile is issued before the first store, so the wave's
+// eight row-id loads and routing gathers are in flight together.
 extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
     __shared__ uint32_t wave_count[kPartThreads / kWave];
     const uint32_t tile = blockIdx.x;
@@ -48,16 +50,21 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
     const uint32_t base = (tile - sp.tile_begin) * kPartTile;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
     const uint32_t wave = threadIdx.x / kWave;
+    uint32_t r[kRowsPerThread];
+#pragma unroll
+    for (uint32_t k = 0; k < kRowsPerThread; k++) {
+        const uint32_t j = base + (k * (kPartThreads / kWave) + wave) * kWave + lane_id();
+        r[k] = j < sp.seg.len ? (sp.identity ? sp.seg.offset + j : src[j]) : 0xffffffffu;
+    }
+    uint64_t m[kRowsPerThread];
+#pragma unroll
+    for (uint32_t k = 0; k < kRowsPerThread; k++) m[k] = __ballot(r[k] != 0xffffffffu && goes_left(a, sp, r[k]));
     uint64_t *dec = a.decisions + (size_t)tile * kBallots;
     uint32_t cnt = 0;
 #pragma unroll
     for (uint32_t k = 0; k < kRowsPerThread; k++) {
-        const uint32_t q = k * (kPartThreads / kWave) + wave;
-        const uint32_t j = base + q * kWave + lane_id();
-        const bool left = j < sp.seg.len && goes_left(a, sp, src[j]);
-        const uint64_t m = __ballot(left);
-        if (lane_id() == 0) dec[q] = m;
-        cnt += (uint32_t)__popcll(m);
+        if (lane_id() == 0) dec[k * (kPartThreads / kWave) + wave] = m[k];
+        cnt += (uint32_t)__popcll(m[k]);
     }
     if (lane_id() == 0) wave_count[wave] = cnt;
     __syncthreads();
@@ -69,17 +76,18 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
 }
 
 // One workgroup per split: exclusive scan of its tiles' left counts.
-extern "C" __global__ __launch_bounds__(256) void hbr_part_scan(PartArgs a) {
+constexpr uint32_t kScanThreads = 1024;
+extern "C" __global__ __launch_bounds__(1024) void hbr_part_scan(PartArgs a) {
     const uint32_t s = blockIdx.x;
     if (s >= a.n_splits) return;
     const PartSplit sp = a.splits[s];
     const uint32_t n_tiles = (sp.seg.len + kPartTile - 1) / kPartTile;
     uint32_t carry = 0;
-    for (uint32_t t0 = 0; t0 < n_tiles; t0 += kPartThreads) {
+    for (uint32_t t0 = 0; t0 < n_tiles; t0 += kScanThreads) {
         const uint32_t t = t0 + threadIdx.x;
         const uint32_t v = t < n_tiles ? a.tile_left[sp.tile_begin + t] : 0u;
         uint32_t total;
-        const uint32_t ex = block_exclusive_scan<kPartThreads>(v, &total);
+        const uint32_t ex = block_exclusive_scan<kScanThreads>(v, &total);
         if (t < n_tiles) a.tile_left[sp.tile_begin + t] = carry + ex;
         carry += total;
     }
@@ -114,7 +122,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
         if (q % (kPartThreads / kWave) == wave) {
             const uint32_t j = tile_pos + q * kWave + lane;
             if (j < sp.seg.len) {
-                const uint32_t r = src[j];
+                const uint32_t r = sp.identity ? sp.seg.offset + j : src[j];
                 if ((m >> lane) & 1ull) {
                     dst[left_before + run + (uint32_t)__popcll(m & below)] = r;
                 } else {

@@ -43,6 +43,13 @@ __device__ __forceinline__ double gain_at(double g, double h, const ScanParams &
     return -(2.0 * g * (double)w + (h + r.lambda) * (double)w2 + 2.0 * r.alpha * (double)__builtin_fabsf(w));
 }
 
+// xgb_node_gain (builder/shared.rs:131-141): the node's own gain at its
+// bounded weight, rounded to f32; 0 for a non-positive Hessian.
+__device__ __forceinline__ float node_gain(double g, double h, const ScanParams &r, float lower, float upper) {
+    if (h <= 0.0) return 0.0f;
+    return (float)gain_at(g, h, r, bounded_weight(g, h, r, lower, upper));
+}
+
 // loss_chg of one candidate; false when the candidate is not offered.
 __device__ __forceinline__ bool score(double lg, double lh, double rg, double rh, const ScanParams &r,
                                       float lower, float upper, int dir, float root_gain, float *loss) {
@@ -114,7 +121,11 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
         const QBin *h = a.hist + (size_t)node_slot(a, nd) * a.total_bins + fs;
         const int eg = a.scale->exp_g, eh = a.scale->exp_h;
         const int dir = a.monotone ? (int)a.monotone[f] : 0;
-        const int64_t tg = nd.total.g, th = nd.total.h;
+        const bool dev_root = (nd.pad & kScanDeviceRoot) != 0;
+        const int64_t tg = dev_root ? a.root_total->g : nd.total.g;
+        const int64_t th = dev_root ? a.root_total->h : nd.total.h;
+        const float root_gain = dev_root ? node_gain(dequant(tg, eg), dequant(th, eh), a.reg, nd.lower, nd.upper)
+                                         : nd.root_gain;
         int64_t carry_g = 0, carry_h = 0;
         // forward pass: bins <= b left, missing right
         for (uint32_t c0 = 0; c0 < nb; c0 += kScanChunk) {
@@ -137,7 +148,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
                 const int64_t ag = xg + sg[k], ah = xh + sh[k];
                 float loss;
                 if (score(dequant(ag, eg), dequant(ah, eh), dequant(tg - ag, eg), dequant(th - ah, eh),
-                          a.reg, nd.lower, nd.upper, dir, nd.root_gain, &loss))
+                          a.reg, nd.lower, nd.upper, dir, root_gain, &loss))
                     offer(best, nan_seen, loss, b0 + k, ag, ah, tg - ag, th - ah, 0);
             }
             carry_g += wave_broadcast(ig, kWave - 1);
@@ -168,7 +179,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
                     const int64_t sgv = fg - (xg + eg_[k]), shv = fh - (xh + eh_[k]);  // suffix from bin o
                     float loss;
                     if (score(dequant(tg - sgv, eg), dequant(th - shv, eh), dequant(sgv, eg), dequant(shv, eh),
-                              a.reg, nd.lower, nd.upper, dir, nd.root_gain, &loss))
+                              a.reg, nd.lower, nd.upper, dir, root_gain, &loss))
                         offer(best, nan_seen, loss, nb + (nb - 1 - o), tg - sgv, th - shv, sgv, shv, 1);
                 }
                 carry_g += wave_broadcast(ig, kWave - 1);
