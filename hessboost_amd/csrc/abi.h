@@ -171,7 +171,9 @@ struct HistNode {
     uint32_t contiguous; // rows are seg.offset .. seg.offset+len (no row buffer)
     uint32_t tile_begin; // first row tile (written by the plan kernel)
     uint32_t n_tiles;    // row tiles of the node (written by the plan kernel)
-    uint32_t pad[2];     // [0]: first partial of a multi-tile node (plan kernel)
+    uint32_t pad[2];     // [0]: first partial of a multi-tile node; [1]: parent slot + 1 of a
+                         // split's built child, whose sibling = parent - built as bins complete
+                         // (dense kernels; both written by the plan kernel)
 };
 
 // Device tiling of a histogram launch: each node's rows cut into tiles of
@@ -187,7 +189,7 @@ struct PlanArgs {
     HistTile *tiles;
     uint32_t *counts;           // [0] tiles, [1] tile_rows
     uint32_t min_rows;
-    uint32_t pad;
+    uint32_t fuse_subtract;     // built children of splits also update their siblings (dense kernels)
 };
 
 struct HistArgs {
@@ -278,11 +280,14 @@ struct ScanArgs {
     uint32_t dense;          // index without missing values: forward pass only
     ScanBest *per_feature;   // n_nodes * n_features
     ScanBest *best;          // n_nodes
-    const QBin *root_total;  // nodes flagged kScanDeviceRoot take total and root gain from here
+    QBin *root_total;        // nodes flagged kScanDeviceRoot: their total (read, or written when dense)
 };
 
-// ScanNode.pad flag: the node's total is *root_total (on the device) and its
-// root gain is computed there from it (the unconstrained root).
+// ScanNode.pad flag: the node's total is on the device and its root gain is
+// computed there from it (the unconstrained root). On a dense index every
+// row has one bin per feature, so each feature's bins sum to the total: the
+// scan sums them itself and the feature-0 wave stores the sum in
+// *root_total; otherwise *root_total holds the total already.
 constexpr uint32_t kScanDeviceRoot = 1;
 
 // Per-tree quantisation exponents from the folded maxima, on the device.

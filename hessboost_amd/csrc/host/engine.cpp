@@ -56,6 +56,7 @@ Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) 
         const long t = std::strtol(v, nullptr, 10);
         if (t == 512 || t == 1024) hist_threads = (uint32_t)t;
     }
+    if (const char *v = std::getenv("HBROCM_HIST_BIN_MAJOR")) hist_bin_major = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_HIST_WAVES")) {
         const long w = std::strtol(v, nullptr, 10);
         if (w >= 1 && w <= 64) hist_waves = (uint32_t)w;
@@ -371,17 +372,21 @@ QBin Engine::root_total(const Segment &sg) {
 // here and the root is done again synchronously.
 bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best) {
     hipStream_t s = dev_.stream();
-    d_total_.zero(s);
-    TotalArgs t{};
-    const bool ident = contiguous(seg);
-    t.rows = ident ? nullptr : rows_[seg.buf].get() + seg.offset;
-    t.first = ident ? seg.offset : 0;
-    t.n = seg.len;
-    t.gpair = gpair_.get();
-    t.scale = scale_.get();
-    t.out = d_total_.get();
-    dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(seg.len, kThreads)), 2048)),
-                dim3(kThreads), t);
+    // a dense index's root total is the sum of any feature's bins: the scan
+    // takes it from feature 0's (which must have bins); else it is summed here
+    if (!(dense_ && n_cols_ > 0 && fo_[1] > fo_[0])) {
+        d_total_.zero(s);
+        TotalArgs t{};
+        const bool ident = contiguous(seg);
+        t.rows = ident ? nullptr : rows_[seg.buf].get() + seg.offset;
+        t.first = ident ? seg.offset : 0;
+        t.n = seg.len;
+        t.gpair = gpair_.get();
+        t.scale = scale_.get();
+        t.out = d_total_.get();
+        dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(seg.len, kThreads)), 2048)),
+                    dim3(kThreads), t);
+    }
     build_nodes({seg}, {slot});
     ScanNode n{};
     n.slot = slot;
@@ -500,6 +505,7 @@ void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *sp
     p.tiles = d_htiles_.get();
     p.counts = d_hcounts_.get();
     p.min_rows = kHistMinRows;
+    p.fuse_subtract = dense_u8_ ? 1u : 0u;
     dev_.launch("hbr_hist_plan", dim3(1), dim3(256), p);
 
     HistArgs a{};
@@ -520,10 +526,11 @@ void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *sp
     a.partial = d_partial_.get();
     a.total_bins = total_bins_;
     a.groups = groups;
+    const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"
                     : fg <= 8  ? "hbr_hist_dense8_fg8"
-                    : fg <= 16 ? "hbr_hist_dense8_fg16"
-                               : "hbr_hist_dense8_fg32";
+                    : fg <= 16 ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
+                               : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");
     dev_.launch(k, dim3((target + n) * groups), dim3(dense_u8_ ? hist_threads : kHistThreads), a);
     if (dense_u8_) {
         ReduceArgs r{};
@@ -686,8 +693,10 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
             hn[i] = n;
         }
         launch_hist(hn, d_splits_.get());
-        SubArgs sub{d_splits_.get(), P, hist_.get(), total_bins_};
-        dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), sub);
+        if (!dense_u8_) {  // the dense kernels turn each parent into the sibling as they finish
+            SubArgs sub{d_splits_.get(), P, hist_.get(), total_bins_};
+            dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), sub);
+        }
         std::vector<ScanNode> sn(2 * P);
         for (uint32_t i = 0; i < P; i++) {
             for (uint32_t c = 0; c < 2; c++) {

@@ -202,6 +202,7 @@ public:
     uint32_t hist_features_per_group = 32;
     uint32_t hist_threads = 1024;
     uint32_t hist_waves = 1;
+    bool hist_bin_major = true;  // [bin][feature] LDS layout (16 and 32 feature groups)
 };
 
 }  // namespace hbr

@@ -86,20 +86,27 @@ __device__ __forceinline__ void load_bins(const uint8_t *p, uint32_t (&w)[FG / 4
 // rotated in registers), so that rows piled in one bin of one feature do not
 // all hit the same LDS word in one instruction (on data with point masses
 // this runs 2.3x faster than feature-in-lockstep, and as fast on smooth
-// data); features past nf go to a per-lane dummy word instead of a branch.
-template <int FG>
+// data).
+//
+// BIN_MAJOR: the LDS sub-histogram is [bin][feature]. A 64-bit word's bank
+// pair then depends on its feature only, and the rotation gives the lanes
+// of each 16-lane group 16 different features: their atomics never share a
+// bank, whatever the bins. Otherwise [feature][257] (bins padded), where
+// the banks follow the data, and features past nf go to per-lane dummies.
+template <int FG, bool BIN_MAJOR>
 __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
     constexpr int W = FG / 4;
+    constexpr uint32_t kWords = BIN_MAJOR ? FG * 256 : FG * kLdsFeature + kWave;
     constexpr uint32_t kDummy = FG * kLdsFeature;
-    __shared__ unsigned long long lg[FG * kLdsFeature + kWave];
-    __shared__ unsigned long long lh[FG * kLdsFeature + kWave];
+    __shared__ unsigned long long lg[kWords];
+    __shared__ unsigned long long lh[kWords];
     const uint32_t entry = blockIdx.x / a.groups, grp = blockIdx.x % a.groups;
     if (entry >= a.counts[0]) return;  // uniform across the workgroup
     const HistTile t = a.tiles[entry];
     const HistNode nd = a.nodes[t.node];
     const uint32_t f0 = grp * FG;
     const uint32_t nf = min((uint32_t)FG, a.n_cols - f0);
-    for (uint32_t i = threadIdx.x; i < FG * kLdsFeature + kWave; i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < kWords; i += blockDim.x) {
         lg[i] = 0ull;
         lh[i] = 0ull;
     }
@@ -121,25 +128,35 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
         for (int f = 0; f < FG; f++) {
             const uint32_t ff = ((uint32_t)f + rot) & (FG - 1);
             const uint32_t bin = (w[f >> 2] >> ((f & 3) * 8)) & 0xffu;
-            const uint32_t at = ff < nf ? ff * kLdsFeature + bin : kDummy + lane;
+            // bin-major: a feature past nf adds its (padding) byte into its
+            // own column, which is never read back
+            const uint32_t at = BIN_MAJOR ? bin * FG + ff : (ff < nf ? ff * kLdsFeature + bin : kDummy + lane);
             atomicAdd(&lg[at], qg);
             atomicAdd(&lh[at], qh);
         }
     }
     __syncthreads();
     const uint32_t *fo = a.feature_offset + f0;
-    if (nd.n_tiles == 1) {
-        QBin *dst = a.hist + (size_t)nd.slot * a.total_bins;
-        for (uint32_t i = threadIdx.x; i < nf * 256u; i += blockDim.x) {
-            const uint32_t ff = i >> 8, bin = i & 255u;
+    QBin *dst = nd.n_tiles == 1 ? a.hist + (size_t)nd.slot * a.total_bins
+                                : a.partial + ((size_t)(nd.pad[0] + t.k) * a.groups + grp) * (FG * 256u);
+    for (uint32_t i = threadIdx.x; i < FG * 256u; i += blockDim.x) {
+        // bin-major: consecutive threads read consecutive features (no bank conflicts)
+        const uint32_t ff = BIN_MAJOR ? i % FG : i >> 8, bin = BIN_MAJOR ? i / FG : i & 255u;
+        if (ff >= nf) continue;
+        const uint32_t at = BIN_MAJOR ? i : ff * kLdsFeature + bin;
+        const QBin v{(int64_t)lg[at], (int64_t)lh[at]};
+        if (nd.n_tiles == 1) {
             const uint32_t lo = fo[ff], nb = fo[ff + 1] - lo;
-            if (bin < nb) dst[lo + bin] = QBin{(int64_t)lg[ff * kLdsFeature + bin], (int64_t)lh[ff * kLdsFeature + bin]};
-        }
-    } else {
-        QBin *dst = a.partial + ((size_t)(nd.pad[0] + t.k) * a.groups + grp) * (FG * 256u);
-        for (uint32_t i = threadIdx.x; i < nf * 256u; i += blockDim.x) {
-            const uint32_t ff = i >> 8, bin = i & 255u;
-            dst[i] = QBin{(int64_t)lg[ff * kLdsFeature + bin], (int64_t)lh[ff * kLdsFeature + bin]};
+            if (bin < nb) {
+                dst[lo + bin] = v;
+                if (nd.pad[1]) {  // this workgroup alone completes these bins: sibling = parent - built
+                    QBin *par = a.hist + (size_t)(nd.pad[1] - 1u) * a.total_bins + lo + bin;
+                    const QBin pv = *par;
+                    *par = QBin{pv.g - v.g, pv.h - v.h};
+                }
+            }
+        } else {
+            dst[ff * 256u + bin] = v;
         }
     }
 }
@@ -197,6 +214,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
         HistNode nd = a.nodes[i];
         const Seg s = resolve_node(a, nd);
         a.nodes[i].seg = s;
+        a.nodes[i].pad[1] = nd.from_split && a.fuse_subtract ? a.splits[nd.split].parent_slot + 1u : 0u;
         if (i < kPlanLdsNodes) s_len[i] = s.len;
         sum += s.len;
         longest = max(longest, (unsigned long long)s.len);
@@ -273,9 +291,11 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
 }
 
 // Launched with 512 or 1024 threads.
-extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg8(HistArgs a) { hist_dense8<8>(a); }
-extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16(HistArgs a) { hist_dense8<16>(a); }
-extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32(HistArgs a) { hist_dense8<32>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg8(HistArgs a) { hist_dense8<8, false>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16(HistArgs a) { hist_dense8<16, false>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32(HistArgs a) { hist_dense8<32, false>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16_bm(HistArgs a) { hist_dense8<16, true>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm(HistArgs a) { hist_dense8<32, true>(a); }
 extern "C" __global__ __launch_bounds__(512) void hbr_hist_csr(HistArgs a) { hist_csr(a); }
 
 // Nodes cut into several tiles: the slot is the sum of the tiles' partials.
@@ -308,6 +328,11 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_hist_reduce(ReduceArgs a)
             h += acc[1][k][col];
         }
         a.hist[(size_t)nd.slot * a.total_bins + lo + bin] = QBin{g, h};
+        if (nd.pad[1]) {  // sibling = parent - built
+            QBin *par = a.hist + (size_t)(nd.pad[1] - 1u) * a.total_bins + lo + bin;
+            const QBin pv = *par;
+            *par = QBin{pv.g - g, pv.h - h};
+        }
     }
 }
 

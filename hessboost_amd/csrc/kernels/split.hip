@@ -117,13 +117,31 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
     best.lg = best.lh = best.rg = best.rh = 0;
     best.backward = 0;
     bool nan_seen = false;
+    const QBin *h = a.hist + (size_t)node_slot(a, nd) * a.total_bins + fs;
+    const bool dev_root = (nd.pad & kScanDeviceRoot) != 0;
+    int64_t tg = nd.total.g, th = nd.total.h;
+    if (dev_root && a.dense) {
+        // the host routes a dense root here only when feature 0 has bins
+        int64_t sg = 0, sh = 0;
+        for (uint32_t b = lane; b < nb; b += kWave) {
+            sg += h[b].g;
+            sh += h[b].h;
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            sg += __shfl_xor(sg, d, kWave);
+            sh += __shfl_xor(sh, d, kWave);
+        }
+        tg = sg;
+        th = sh;
+        if (f == 0 && lane == 0) *a.root_total = QBin{tg, th};
+    } else if (dev_root) {
+        tg = a.root_total->g;
+        th = a.root_total->h;
+    }
     if (nb > 1) {
-        const QBin *h = a.hist + (size_t)node_slot(a, nd) * a.total_bins + fs;
         const int eg = a.scale->exp_g, eh = a.scale->exp_h;
         const int dir = a.monotone ? (int)a.monotone[f] : 0;
-        const bool dev_root = (nd.pad & kScanDeviceRoot) != 0;
-        const int64_t tg = dev_root ? a.root_total->g : nd.total.g;
-        const int64_t th = dev_root ? a.root_total->h : nd.total.h;
         const float root_gain = dev_root ? node_gain(dequant(tg, eg), dequant(th, eh), a.reg, nd.lower, nd.upper)
                                          : nd.root_gain;
         int64_t carry_g = 0, carry_h = 0;
