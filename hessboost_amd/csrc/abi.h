@@ -131,8 +131,7 @@ struct PartOut {
 struct PartArgs {
     const PartSplit *splits;
     uint32_t n_splits;
-    uint32_t n_tiles;
-    const uint32_t *tile_split;  // tile -> split
+    uint32_t n_tiles;            // tiles of split s: [tile_begin, next split's tile_begin)
     uint32_t *tile_left;         // per tile left count (count pass) / left offset (after scan)
     uint64_t *decisions;         // per tile kPartTile / 64 ballots of "goes left" (count pass)
     PartOut *out;

@@ -394,7 +394,7 @@ bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upp
     n.upper = upper;
     n.pad = kScanDeviceRoot;
     ScanBest *b = static_cast<ScanBest *>(stage_.alloc(sizeof(ScanBest)));
-    launch_scan({n}, b);
+    scan_host_nodes({n}, b);
     QBin *tot = static_cast<QBin *>(stage_.alloc(sizeof(QBin)));
     QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
     d_total_.download(tot, 1, s);
@@ -474,7 +474,8 @@ void Engine::set_scan_params(const ScanParams &p, const std::vector<int8_t> &mon
 // launch), then one workgroup per (tile, feature group). Dense u8 tiles
 // write their sums with plain stores (the reduce kernel adds up nodes of
 // several tiles); CSR tiles add into slots zeroed first.
-void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *splits_dev, const uint32_t *rows0) {
+void Engine::launch_hist(const HistNode *nodes_dev, const std::vector<HistNode> &nodes, const PartSplit *splits_dev,
+                         const PartOut *part_out_dev, const uint32_t *rows0) {
     if (nodes.empty()) return;
     if (gpair_.size() < n_rows_ || !gpair_.get()) fail(kInvalid, "histograms: no gradients staged");
     hipStream_t s = dev_.stream();
@@ -491,17 +492,17 @@ void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *sp
         ZeroArgs z{hist_.get(), d_slots_.get(), n, total_bins_};
         dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), n), dim3(256), z);
     }
-    upload_vec(d_hnodes_, nodes, stage_, s);
     d_htiles_.reserve(target + n);
     d_hcounts_.reserve(4);
     if (dense_u8_) d_partial_.reserve((size_t)2 * target * groups * fg * 256);
 
+    HistNode *nodes_rw = const_cast<HistNode *>(nodes_dev);  // the plan kernel resolves them in place
     PlanArgs p{};
-    p.nodes = d_hnodes_.get();
+    p.nodes = nodes_rw;
     p.n_nodes = n;
     p.target_tiles = target;
     p.splits = splits_dev;
-    p.part_out = d_part_out_.get();
+    p.part_out = part_out_dev;
     p.tiles = d_htiles_.get();
     p.counts = d_hcounts_.get();
     p.min_rows = kHistMinRows;
@@ -509,7 +510,7 @@ void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *sp
     dev_.launch("hbr_hist_plan", dim3(1), dim3(256), p);
 
     HistArgs a{};
-    a.nodes = d_hnodes_.get();
+    a.nodes = nodes_dev;
     a.tiles = d_htiles_.get();
     a.counts = d_hcounts_.get();
     a.rows[0] = rows0 ? rows0 : rows_[0].get();
@@ -534,7 +535,7 @@ void Engine::launch_hist(const std::vector<HistNode> &nodes, const PartSplit *sp
     dev_.launch(k, dim3((target + n) * groups), dim3(dense_u8_ ? hist_threads : kHistThreads), a);
     if (dense_u8_) {
         ReduceArgs r{};
-        r.nodes = d_hnodes_.get();
+        r.nodes = nodes_dev;
         r.partial = d_partial_.get();
         r.hist = hist_.get();
         r.feature_offset = d_fo_.get();
@@ -559,7 +560,8 @@ void Engine::build_nodes(const std::vector<Segment> &segs, const std::vector<uin
         counters.hist_rows += segs[i].len;
         counters.hist_bytes += hist_bytes(segs[i].len, !n.contiguous);
     }
-    launch_hist(nodes, nullptr);
+    upload_vec(d_hnodes_, nodes, stage_, dev_.stream());
+    launch_hist(d_hnodes_.get(), nodes, nullptr, nullptr);
 }
 
 void Engine::subtract(const std::vector<uint32_t> &parents, const std::vector<uint32_t> &built) {
@@ -576,18 +578,16 @@ void Engine::subtract(const std::vector<uint32_t> &parents, const std::vector<ui
                 dim3(256), a);
 }
 
-void Engine::launch_scan(const std::vector<ScanNode> &nodes, ScanBest *host_out) {
-    hipStream_t s = dev_.stream();
-    upload_vec(d_snodes_, nodes, stage_, s);
-    const uint64_t pairs = (uint64_t)nodes.size() * n_cols_;
+void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit *splits_dev,
+                         const PartOut *part_out_dev, ScanBest *best_dev) {
+    const uint64_t pairs = (uint64_t)n * n_cols_;
     d_per_feature_.reserve(pairs ? pairs : 1);
-    d_best_.reserve(nodes.size());
     ScanArgs a{};
-    a.nodes = d_snodes_.get();
-    a.n_nodes = (uint32_t)nodes.size();
+    a.nodes = nodes_dev;
+    a.n_nodes = n;
     a.n_features = n_cols_;
-    a.splits = d_splits_.get();
-    a.part_out = d_part_out_.get();
+    a.splits = splits_dev;
+    a.part_out = part_out_dev;
     a.hist = hist_.get();
     a.total_bins = total_bins_;
     a.feature_offset = d_fo_.get();
@@ -596,11 +596,20 @@ void Engine::launch_scan(const std::vector<ScanNode> &nodes, ScanBest *host_out)
     a.reg = scan_params_;
     a.dense = dense_ ? 1u : 0u;
     a.per_feature = d_per_feature_.get();
-    a.best = d_best_.get();
+    a.best = best_dev;
     a.root_total = d_total_.get();
     dev_.launch("hbr_scan_features", dim3(ceil_div(pairs, 4)), dim3(256), a);
-    dev_.launch("hbr_scan_merge", dim3((uint32_t)nodes.size()), dim3(64), a);
-    d_best_.download(host_out, nodes.size(), s);
+    dev_.launch("hbr_scan_merge", dim3(n), dim3(64), a);
+}
+
+// Scan nodes given on the host: upload, scan, copy the winners into `out`
+// (pinned; valid after the next synchronisation).
+void Engine::scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out) {
+    hipStream_t s = dev_.stream();
+    upload_vec(d_snodes_, nodes, stage_, s);
+    d_best_.reserve(nodes.size());
+    launch_scan(d_snodes_.get(), (uint32_t)nodes.size(), nullptr, nullptr, d_best_.get());
+    d_best_.download(out, nodes.size(), s);
 }
 
 std::vector<ScanBest> Engine::scan(const std::vector<ScanInput> &in) {
@@ -617,20 +626,46 @@ std::vector<ScanBest> Engine::scan(const std::vector<ScanInput> &in) {
         nodes[i] = n;
     }
     ScanBest *staged = static_cast<ScanBest *>(stage_.alloc(in.size() * sizeof(ScanBest)));
-    launch_scan(nodes, staged);
+    scan_host_nodes(nodes, staged);
     dev_.sync();
     std::memcpy(out.data(), staged, in.size() * sizeof(ScanBest));
     stage_.reset();
     return out;
 }
 
+// Bump layout of one level's records in one host block and one device block.
+namespace {
+struct Layout {
+    size_t bytes = 0;
+    size_t add(size_t n) {
+        const size_t at = bytes;
+        bytes += (n + 255) & ~size_t(255);
+        return at;
+    }
+};
+}  // namespace
+
 std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, bool terminal) {
     const uint32_t P = (uint32_t)splits.size();
     std::vector<LevelChild> children(2 * P);
     if (P == 0) return children;
     hipStream_t s = dev_.stream();
-    std::vector<PartSplit> ps(P);
-    std::vector<uint32_t> tile_split;
+    // inputs: splits, built-child histogram nodes, children's scan nodes;
+    // outputs: partition results and the children's winners. One copy each way.
+    Layout in, out;
+    const size_t o_splits = in.add(P * sizeof(PartSplit));
+    const size_t o_hnodes = terminal ? 0 : in.add(P * sizeof(HistNode));
+    const size_t o_snodes = terminal ? 0 : in.add(2 * P * sizeof(ScanNode));
+    const size_t o_pout = out.add(P * sizeof(PartOut));
+    const size_t o_best = terminal ? 0 : out.add(2 * P * sizeof(ScanBest));
+    char *host_in = static_cast<char *>(stage_.alloc(in.bytes));
+    char *host_out = static_cast<char *>(stage_.alloc(out.bytes));
+    d_level_in_.reserve(in.bytes);
+    d_level_out_.reserve(out.bytes);
+    char *dev_in = reinterpret_cast<char *>(d_level_in_.get());
+    char *dev_out = reinterpret_cast<char *>(d_level_out_.get());
+
+    PartSplit *ps = reinterpret_cast<PartSplit *>(host_in + o_splits);
     std::vector<uint32_t> fresh(P, 0);
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < P; i++) {
@@ -647,24 +682,46 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
             p.fresh_slot = fresh[i];
             p.parent_slot = l.parent_slot;
         }
-        const uint32_t nt = ceil_div(l.seg.len, kPartTile);
-        for (uint32_t t = 0; t < nt; t++) tile_split.push_back(i);
-        tiles += nt;
+        tiles += ceil_div(l.seg.len, kPartTile);
         ps[i] = p;
     }
-    upload_vec(d_splits_, ps, stage_, s);
-    upload_vec(d_tile_split_, tile_split, stage_, s);
+    std::vector<HistNode> hn;
+    if (!terminal) {
+        hn.resize(P);
+        ScanNode *sn = reinterpret_cast<ScanNode *>(host_in + o_snodes);
+        for (uint32_t i = 0; i < P; i++) {
+            HistNode n{};
+            n.slot = fresh[i];
+            n.from_split = 1;
+            n.split = i;
+            hn[i] = n;
+            for (uint32_t c = 0; c < 2; c++) {
+                ScanNode m{};
+                m.from_split = 1;
+                m.split = i;
+                m.child = c;
+                m.total = splits[i].child_total[c];
+                m.root_gain = splits[i].child_root_gain[c];
+                m.lower = splits[i].child_lower[c];
+                m.upper = splits[i].child_upper[c];
+                sn[2 * i + c] = m;
+            }
+        }
+        std::memcpy(host_in + o_hnodes, hn.data(), P * sizeof(HistNode));
+    }
+    HBR_HIP(hipMemcpyAsync(dev_in, host_in, in.bytes, hipMemcpyHostToDevice, s));
+    const PartSplit *splits_dev = reinterpret_cast<const PartSplit *>(dev_in + o_splits);
+    PartOut *pout_dev = reinterpret_cast<PartOut *>(dev_out + o_pout);
+
     d_tile_left_.reserve(tiles ? tiles : 1);
     d_decisions_.reserve((size_t)(tiles ? tiles : 1) * (kPartTile / 64));
-    d_part_out_.reserve(P);
     PartArgs a{};
-    a.splits = d_splits_.get();
+    a.splits = splits_dev;
     a.n_splits = P;
     a.n_tiles = tiles;
-    a.tile_split = d_tile_split_.get();
     a.tile_left = d_tile_left_.get();
     a.decisions = d_decisions_.get();
-    a.out = d_part_out_.get();
+    a.out = pout_dev;
     a.src_rows[0] = rows_[0].get();
     a.src_rows[1] = rows_[1].get();
     a.dst_rows[0] = rows_[0].get();
@@ -682,41 +739,19 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
     dev_.launch("hbr_part_scan", dim3(P), dim3(1024), a);
     dev_.launch("hbr_part_scatter", dim3(tiles), dim3(kPartThreads), a);
 
-    ScanBest *best_staged = nullptr;
     if (!terminal) {
-        std::vector<HistNode> hn(P);
-        for (uint32_t i = 0; i < P; i++) {
-            HistNode n{};
-            n.slot = fresh[i];
-            n.from_split = 1;
-            n.split = i;
-            hn[i] = n;
-        }
-        launch_hist(hn, d_splits_.get());
+        launch_hist(reinterpret_cast<const HistNode *>(dev_in + o_hnodes), hn, splits_dev, pout_dev);
         if (!dense_u8_) {  // the dense kernels turn each parent into the sibling as they finish
-            SubArgs sub{d_splits_.get(), P, hist_.get(), total_bins_};
+            SubArgs sub{splits_dev, P, hist_.get(), total_bins_};
             dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), sub);
         }
-        std::vector<ScanNode> sn(2 * P);
-        for (uint32_t i = 0; i < P; i++) {
-            for (uint32_t c = 0; c < 2; c++) {
-                ScanNode n{};
-                n.from_split = 1;
-                n.split = i;
-                n.child = c;
-                n.total = splits[i].child_total[c];
-                n.root_gain = splits[i].child_root_gain[c];
-                n.lower = splits[i].child_lower[c];
-                n.upper = splits[i].child_upper[c];
-                sn[2 * i + c] = n;
-            }
-        }
-        best_staged = static_cast<ScanBest *>(stage_.alloc(2 * P * sizeof(ScanBest)));
-        launch_scan(sn, best_staged);
+        launch_scan(reinterpret_cast<const ScanNode *>(dev_in + o_snodes), 2 * P, splits_dev, pout_dev,
+                    reinterpret_cast<ScanBest *>(dev_out + o_best));
     }
-    PartOut *po = static_cast<PartOut *>(stage_.alloc(P * sizeof(PartOut)));
-    d_part_out_.download(po, P, s);
+    HBR_HIP(hipMemcpyAsync(host_out, dev_out, out.bytes, hipMemcpyDeviceToHost, s));
     dev_.sync();
+    const PartOut *po = reinterpret_cast<const PartOut *>(host_out + o_pout);
+    const ScanBest *best_staged = terminal ? nullptr : reinterpret_cast<const ScanBest *>(host_out + o_best);
     for (uint32_t i = 0; i < P; i++) {
         const Segment &pseg = splits[i].seg;
         const uint32_t nl = po[i].left_len;
@@ -823,7 +858,9 @@ std::vector<QBin> Engine::build_rows(const uint32_t *rows, uint64_t m) {
     HistNode n{};
     n.seg = Seg{0, (uint32_t)m, 0, 0};
     n.slot = slot;
-    launch_hist({n}, nullptr, host_rows_.get());
+    const std::vector<HistNode> one{n};
+    upload_vec(d_hnodes_, one, stage_, s);
+    launch_hist(d_hnodes_.get(), one, nullptr, nullptr, host_rows_.get());
     std::vector<QBin> out(total_bins_);
     hist_.download(out.data(), total_bins_, s, (size_t)slot * total_bins_);
     dev_.sync();

@@ -131,8 +131,11 @@ private:
     bool identity_rows0_ = false;
     bool rows0_written_ = false;
     void write_identity_rows();  // buffer 0 := 0..n-1, once per tree, when a row list is read
-    void launch_hist(const std::vector<HistNode> &nodes, const PartSplit *splits_dev, const uint32_t *rows0 = nullptr);
-    void launch_scan(const std::vector<ScanNode> &nodes, ScanBest *host_out);
+    void launch_hist(const HistNode *nodes_dev, const std::vector<HistNode> &nodes, const PartSplit *splits_dev,
+                     const PartOut *part_out_dev, const uint32_t *rows0 = nullptr);
+    void launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit *splits_dev, const PartOut *part_out_dev,
+                     ScanBest *best_dev);
+    void scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out);
     void launch_gradients(const hbr_device_loss &loss, uint32_t output);
     bool finish_gradients_on_host(QScale staged);
     hbr_device_loss last_loss_{};
@@ -180,8 +183,8 @@ private:
     // per-call scratch
     Stage stage_;
     DBuf<PartSplit> d_splits_;
-    DBuf<uint32_t> d_tile_split_, d_tile_left_, d_slots_;
-    DBuf<PartOut> d_part_out_;
+    DBuf<uint32_t> d_tile_left_, d_slots_;
+    DBuf<uint8_t> d_level_in_, d_level_out_;  // one level's records (bytes)
     DBuf<HistNode> d_hnodes_;
     DBuf<HistTile> d_htiles_;
     DBuf<uint32_t> d_hcounts_;

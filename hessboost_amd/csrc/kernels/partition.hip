@@ -36,6 +36,18 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
     return sp.default_left != 0;
 }
 
+// The split owning a tile: the last split whose first tile is at or before
+// it (a split without rows shares its first tile with the next split).
+__device__ __forceinline__ uint32_t split_of_tile(const PartArgs &a, uint32_t tile) {
+    uint32_t lo = 0, hi = a.n_splits;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (a.splits[mid].tile_begin <= tile) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
 }  // namespace hbr
 
 using namespace hbr;
@@ -46,7 +58,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
     __shared__ uint32_t wave_count[kPartThreads / kWave];
     const uint32_t tile = blockIdx.x;
     if (tile >= a.n_tiles) return;
-    const PartSplit sp = a.splits[a.tile_split[tile]];
+    const PartSplit sp = a.splits[split_of_tile(a, tile)];
     const uint32_t base = (tile - sp.tile_begin) * kPartTile;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
     const uint32_t wave = threadIdx.x / kWave;
@@ -105,7 +117,7 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_part_scan(PartArgs a) {
 extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     const uint32_t tile = blockIdx.x;
     if (tile >= a.n_tiles) return;
-    const uint32_t s = a.tile_split[tile];
+    const uint32_t s = split_of_tile(a, tile);
     const PartSplit sp = a.splits[s];
     const uint32_t left_len = a.out[s].left_len;
     const uint32_t tile_pos = (tile - sp.tile_begin) * kPartTile;
