@@ -62,8 +62,7 @@ Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) 
         if (w >= 1 && w <= 64) hist_waves = (uint32_t)w;
     }
     upload_index(desc);
-    scale_.resize(1);
-    d_total_.resize(1);
+    root_.resize(1);
 }
 
 Engine::~Engine() {
@@ -224,7 +223,7 @@ void Engine::prepare(const float *gpair, uint64_t n) {
     q.exp_h = exp_for(q.max_h_bits, n_rows_);
     scale_host_ = q;
     scale_checked_ = true;
-    scale_.upload(&scale_host_, 1, dev_.stream());
+    HBR_HIP(hipMemcpyAsync(scale_dev(), &scale_host_, sizeof(QScale), hipMemcpyHostToDevice, dev_.stream()));
     dev_.sync();
     if (q.nonfinite) fail(kRefused, "a staged gradient is not finite");
 }
@@ -235,13 +234,13 @@ void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     hipStream_t s = dev_.stream();
     gpair_.resize(n_rows_ ? n_rows_ : 1);
     scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
-    scale_.zero(s);
+    HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
     GradArgs a{};
     a.margins = margins_.get();
     a.labels = labels_.get();
     a.weights = has_weights_ ? weights_.get() : nullptr;
     a.gpair = gpair_.get();
-    a.scale = scale_.get();
+    a.scale = scale_dev();
     a.scalar_list = scalar_list_.get();
     a.n = (uint32_t)n_rows_;
     a.vec_rows = (uint32_t)std::min<uint64_t>(loss.vector_rows, n_rows_);
@@ -291,7 +290,7 @@ bool Engine::finish_gradients_on_host(QScale host) {
     host.exp_g = exp_for(host.max_g_bits, n_rows_);
     host.exp_h = exp_for(host.max_h_bits, n_rows_);
     scale_host_ = host;
-    scale_.upload(&scale_host_, 1, s);
+    HBR_HIP(hipMemcpyAsync(scale_dev(), &scale_host_, sizeof(QScale), hipMemcpyHostToDevice, s));
     dev_.sync();
     return host.nonfinite == 0;
 }
@@ -299,7 +298,7 @@ bool Engine::finish_gradients_on_host(QScale host) {
 bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
     launch_gradients(loss, output);
     QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
-    scale_.download(q, 1, dev_.stream());
+    HBR_HIP(hipMemcpyAsync(q, scale_dev(), sizeof(QScale), hipMemcpyDeviceToHost, dev_.stream()));
     dev_.sync();
     const QScale host = *q;
     stage_.reset();
@@ -309,7 +308,7 @@ bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
 
 void Engine::compute_gradients_async(const hbr_device_loss &loss, uint32_t output) {
     launch_gradients(loss, output);
-    FinishArgs f{scale_.get(), n_rows_};
+    FinishArgs f{scale_dev(), n_rows_};
     dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
     scale_checked_ = false;  // grow_root reads the scale back and checks it
 }
@@ -345,19 +344,19 @@ bool Engine::contiguous(const Segment &sg) const {
 
 QBin Engine::root_total(const Segment &sg) {
     hipStream_t s = dev_.stream();
-    d_total_.zero(s);
+    HBR_HIP(hipMemsetAsync(total_dev(), 0, sizeof(QBin), s));
     TotalArgs a{};
     const bool ident = contiguous(sg);
     a.rows = ident ? nullptr : rows_[sg.buf].get() + sg.offset;
     a.first = ident ? sg.offset : 0;
     a.n = sg.len;
     a.gpair = gpair_.get();
-    a.scale = scale_.get();
-    a.out = d_total_.get();
+    a.scale = scale_dev();
+    a.out = total_dev();
     const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(sg.len, kThreads)), 2048);
     dev_.launch("hbr_total", dim3(blocks), dim3(kThreads), a);
     QBin *out = static_cast<QBin *>(stage_.alloc(sizeof(QBin)));
-    d_total_.download(out, 1, s);
+    HBR_HIP(hipMemcpyAsync(out, total_dev(), sizeof(QBin), hipMemcpyDeviceToHost, s));
     dev_.sync();
     QBin t = *out;
     stage_.reset();
@@ -365,7 +364,7 @@ QBin Engine::root_total(const Segment &sg) {
 }
 
 // The root without a host synchronisation before its split search: the
-// total sums into d_total_, the histogram builds, and the scan takes the
+// total sums on the device, the histogram builds, and the scan takes the
 // total and the root gain from the device. One synchronisation then brings
 // back the winner, the total and the scale. After asynchronous gradients
 // whose kernel left rows to the host's scalar path, those rows are computed
@@ -375,34 +374,50 @@ bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upp
     // a dense index's root total is the sum of any feature's bins: the scan
     // takes it from feature 0's (which must have bins); else it is summed here
     if (!(dense_ && n_cols_ > 0 && fo_[1] > fo_[0])) {
-        d_total_.zero(s);
+        HBR_HIP(hipMemsetAsync(total_dev(), 0, sizeof(QBin), s));
         TotalArgs t{};
         const bool ident = contiguous(seg);
         t.rows = ident ? nullptr : rows_[seg.buf].get() + seg.offset;
         t.first = ident ? seg.offset : 0;
         t.n = seg.len;
         t.gpair = gpair_.get();
-        t.scale = scale_.get();
-        t.out = d_total_.get();
+        t.scale = scale_dev();
+        t.out = total_dev();
         dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(seg.len, kThreads)), 2048)),
                     dim3(kThreads), t);
     }
-    build_nodes({seg}, {slot});
+    // the root's histogram node and scan node in one upload; the winner, the
+    // total and the scale back in one copy
+    HistNode hn{};
+    hn.seg = Seg{seg.offset, seg.len, seg.buf, 0};
+    hn.slot = slot;
+    hn.contiguous = contiguous(seg) ? 1u : 0u;
+    counters.hist_nodes++;
+    counters.hist_rows += seg.len;
+    counters.hist_bytes += hist_bytes(seg.len, !hn.contiguous);
     ScanNode n{};
     n.slot = slot;
     n.lower = lower;
     n.upper = upper;
     n.pad = kScanDeviceRoot;
-    ScanBest *b = static_cast<ScanBest *>(stage_.alloc(sizeof(ScanBest)));
-    scan_host_nodes({n}, b);
-    QBin *tot = static_cast<QBin *>(stage_.alloc(sizeof(QBin)));
-    QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
-    d_total_.download(tot, 1, s);
-    scale_.download(q, 1, s);
+    struct RootIn {
+        HistNode h;
+        ScanNode s;
+    };
+    RootIn *rin = static_cast<RootIn *>(stage_.alloc(sizeof(RootIn)));
+    rin->h = hn;
+    rin->s = n;
+    d_level_in_.reserve(sizeof(RootIn));
+    RootIn *rdev = reinterpret_cast<RootIn *>(d_level_in_.get());
+    HBR_HIP(hipMemcpyAsync(rdev, rin, sizeof(RootIn), hipMemcpyHostToDevice, s));
+    launch_hist(&rdev->h, {hn}, nullptr, nullptr);
+    launch_scan(&rdev->s, 1, nullptr, nullptr, root_best_dev());
+    RootBlock *rb = static_cast<RootBlock *>(stage_.alloc(sizeof(RootBlock)));
+    HBR_HIP(hipMemcpyAsync(rb, root_.get(), sizeof(RootBlock), hipMemcpyDeviceToHost, s));
     dev_.sync();
-    *best = *b;
-    *total = *tot;
-    const QScale host = *q;
+    *best = rb->best;
+    *total = rb->total;
+    const QScale host = rb->scale;
     stage_.reset();
     if (scale_checked_) return true;
     scale_checked_ = true;
@@ -516,7 +531,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, const std::vector<HistNode> 
     a.rows[0] = rows0 ? rows0 : rows_[0].get();
     a.rows[1] = rows_[1].get();
     a.gpair = gpair_.get();
-    a.scale = scale_.get();
+    a.scale = scale_dev();
     a.bins8 = rows8_.get();
     a.stride = stride_;
     a.n_cols = n_cols_;
@@ -592,12 +607,12 @@ void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit 
     a.total_bins = total_bins_;
     a.feature_offset = d_fo_.get();
     a.monotone = has_monotone_ ? monotone_.get() : nullptr;
-    a.scale = scale_.get();
+    a.scale = scale_dev();
     a.reg = scan_params_;
     a.dense = dense_ ? 1u : 0u;
     a.per_feature = d_per_feature_.get();
     a.best = best_dev;
-    a.root_total = d_total_.get();
+    a.root_total = total_dev();
     dev_.launch("hbr_scan_features", dim3(ceil_div(pairs, 4)), dim3(256), a);
     dev_.launch("hbr_scan_merge", dim3(n), dim3(64), a);
 }
@@ -826,13 +841,19 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
     }
     if (output >= outputs_) fail(kInvalid, "walk_add: no such output");
     hipStream_t s = dev_.stream();
-    upload_vec(d_walk_meta_, meta, stage_, s);
-    upload_vec(d_walk_left_, left, stage_, s);
-    upload_vec(d_walk_value_, value, stage_, s);
+    // the three node tables in one upload
+    const size_t bytes = 3 * n * sizeof(uint32_t);
+    char *host = static_cast<char *>(stage_.alloc(bytes));
+    std::memcpy(host, meta.data(), n * 4);
+    std::memcpy(host + n * 4, left.data(), n * 4);
+    std::memcpy(host + 2 * n * 4, value.data(), n * 4);
+    d_walk_.reserve(bytes);
+    char *dev = reinterpret_cast<char *>(d_walk_.get());
+    HBR_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, s));
     WalkArgs a{};
-    a.meta = d_walk_meta_.get();
-    a.left = d_walk_left_.get();
-    a.value = d_walk_value_.get();
+    a.meta = reinterpret_cast<const uint32_t *>(dev);
+    a.left = reinterpret_cast<const uint32_t *>(dev + n * 4);
+    a.value = reinterpret_cast<const float *>(dev + 2 * n * 4);
     a.bins8 = rows8_.get();
     a.margins = margins_.get();
     a.stride = stride_;

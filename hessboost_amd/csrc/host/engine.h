@@ -162,7 +162,17 @@ private:
     DBuf<float> margins_, labels_, weights_;
     uint32_t outputs_ = 1;
     bool labels_loaded_ = false, has_weights_ = false;
-    DBuf<QScale> scale_;
+    // the per-tree scale, the root total and the root's winner, adjacent so
+    // that the root's synchronisation reads them back with one copy
+    struct RootBlock {
+        QScale scale;
+        QBin total;
+        ScanBest best;
+    };
+    DBuf<RootBlock> root_;
+    QScale *scale_dev() const { return &root_.get()->scale; }
+    QBin *total_dev() const { return &root_.get()->total; }
+    ScanBest *root_best_dev() const { return &root_.get()->best; }
     QScale scale_host_{};
     DBuf<uint32_t> scalar_list_;
     DBuf<uint32_t> rows_[2];
@@ -190,11 +200,9 @@ private:
     DBuf<uint32_t> d_hcounts_;
     DBuf<QBin> d_partial_;
     DBuf<uint64_t> d_decisions_;
-    DBuf<uint32_t> d_walk_meta_, d_walk_left_;
-    DBuf<float> d_walk_value_;
+    DBuf<uint8_t> d_walk_;  // a tree's meta, left and value tables, one after another
     DBuf<ScanNode> d_snodes_;
     DBuf<ScanBest> d_per_feature_, d_best_;
-    DBuf<QBin> d_total_;
     DBuf<LeafSeg> d_leaves_;
     DBuf<uint32_t> d_tile_leaf_, d_tile_row0_;
 
