@@ -25,6 +25,8 @@ sys.path.insert(0, ROOT)
 METRIC = "train rounds/s at 10.5M×28 depth-8 logistic; batch predict Mrows/s (1 GPU)"
 HBM_PEAK_GBS = 8000.0
 HIST_KERNEL = "hbr_hist_dense8"
+# 64-bit LDS atomics: 64 lanes x 8 B per 4 clocks per CU (128 B/clk LDS), 256 CUs at 2.4 GHz
+LDS_ATOMIC_PEAK_T = 256 * 2.4e9 * 16 / 1e12
 
 
 def log(msg):
@@ -124,6 +126,7 @@ def main():
     hist_launches = sum(n for k, (ms, n) in stats.items() if k.startswith(HIST_KERNEL))
     hist_names = sorted(k for k in stats if k.startswith(HIST_KERNEL))
     hist_bytes = after["hist_bytes"] - before["hist_bytes"]
+    lds_atomics = (after["hist_rows"] - before["hist_rows"]) * x.shape[1] * 2
     achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
     log(f"{args.steps} rounds in {elapsed:.3f}s = {rounds_per_s:.1f} rounds/s; {'/'.join(hist_names)} "
         f"{hist_ms:.1f} ms over {hist_launches} launches, {achieved:.0f} GB/s algorithmic")
@@ -171,6 +174,14 @@ def main():
             "launches": hist_launches,
             "avg_launch_ms": round(hist_ms / max(1, hist_launches), 4),
             "algorithmic_bytes_per_launch": int(hist_bytes / max(1, hist_launches)),
+            # the kernel's other bound: two 64-bit LDS integer adds per (row, feature)
+            "lds_atomics": {
+                "achieved": round(lds_atomics / (hist_ms * 1e-3) / 1e12, 3) if hist_ms > 0 else 0.0,
+                "peak": LDS_ATOMIC_PEAK_T,
+                "unit": "T lane-ops/s",
+                "frac": round(lds_atomics / (hist_ms * 1e-3) / 1e12 / LDS_ATOMIC_PEAK_T, 4) if hist_ms > 0 else 0.0,
+                "per_launch": int(lds_atomics / max(1, hist_launches)),
+            },
         },
         "kernel_ms_per_round": breakdown,
     }

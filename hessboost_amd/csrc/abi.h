@@ -331,6 +331,14 @@ struct WalkArgs {
     uint32_t pad;
 };
 
+// The margin walk of a finished tree followed, row by row, by the next
+// round's gradients of the updated margin (the gradient kernel's arithmetic
+// and max fold; w.margins and g.margins are the same array).
+struct WalkGradArgs {
+    WalkArgs w;
+    GradArgs g;
+};
+
 // ---- prediction ---------------------------------------------------------------------
 // Forest nodes are structure-of-arrays: value (threshold or leaf value bits),
 // meta (feature | default_left << 30 | leaf << 31), left child (absolute

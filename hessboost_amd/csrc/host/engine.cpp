@@ -228,13 +228,7 @@ void Engine::prepare(const float *gpair, uint64_t n) {
     if (q.nonfinite) fail(kRefused, "a staged gradient is not finite");
 }
 
-void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
-    if (!labels_loaded_) fail(kInvalid, "gradients: no labels since load_margins");
-    if (outputs_ != 1 || output != 0) fail(kRefused, "device gradients run for one output");
-    hipStream_t s = dev_.stream();
-    gpair_.resize(n_rows_ ? n_rows_ : 1);
-    scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
-    HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
+GradArgs Engine::grad_args(const hbr_device_loss &loss) {
     GradArgs a{};
     a.margins = margins_.get();
     a.labels = labels_.get();
@@ -248,6 +242,17 @@ void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     a.scale_pos_weight = loss.scale_pos_weight;
     a.min_hess = loss.min_hess;
     a.max_input = loss.max_input;
+    return a;
+}
+
+void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
+    if (!labels_loaded_) fail(kInvalid, "gradients: no labels since load_margins");
+    if (outputs_ != 1 || output != 0) fail(kRefused, "device gradients run for one output");
+    hipStream_t s = dev_.stream();
+    gpair_.resize(n_rows_ ? n_rows_ : 1);
+    scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
+    HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
+    const GradArgs a = grad_args(loss);
     // grid-stride: a few workgroups per CU, one max fold each
     const uint32_t grad_blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)),
                                                     (uint32_t)dev_.cu_count() * 8);
@@ -829,8 +834,12 @@ void Engine::add_leaves(const std::vector<Segment> &segs, const std::vector<floa
     stage_.reset();
 }
 
+bool Engine::can_walk_gradients(size_t n_nodes) const {
+    return dense_u8_ && stride_ == 32 && n_nodes <= 1024 && outputs_ == 1 && labels_loaded_;
+}
+
 void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint32_t> &left,
-                      const std::vector<float> &value, uint32_t output) {
+                      const std::vector<float> &value, uint32_t output, const hbr_device_loss *next_loss) {
     if (!dense_u8_) fail(kRefused, "walk_add: the index has no row-major u8 bins");
     const size_t n = meta.size();
     if (n == 0 || left.size() != n || value.size() != n) fail(kInvalid, "walk_add: one meta, left, value per node");
@@ -865,6 +874,22 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
     const bool staged = stride_ == 32 && n <= 1024;
     const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)),
                                                (uint32_t)dev_.cu_count() * (staged ? 8 : 16));
+    if (next_loss) {
+        // the next round's gradients from the updated margins, in the same pass
+        if (!can_walk_gradients(n)) fail(kInvalid, "walk_add: gradients need the staged walk of one output");
+        gpair_.resize(n_rows_ ? n_rows_ : 1);
+        scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
+        HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
+        WalkGradArgs wg{};
+        wg.w = a;
+        wg.g = grad_args(*next_loss);
+        dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
+        FinishArgs f{scale_dev(), n_rows_};
+        dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
+        last_loss_ = *next_loss;
+        scale_checked_ = false;  // grow_root reads the scale back and checks it
+        return;
+    }
     dev_.launch(staged ? "hbr_walk_leaves32" : "hbr_walk_leaves", dim3(blocks), dim3(256), a);
     // the staged node tables are released at the next synchronisation
 }

@@ -105,8 +105,11 @@ public:
     // through the tree (meta/left/value as WalkArgs lays them out); needs no
     // row segments, so the depth limit's level can skip its partition.
     bool can_walk() const { return dense_u8_; }
+    // With next_loss, the same pass also computes the next round's gradients
+    // of the updated margins (like compute_gradients_async; can_walk_gradients).
     void walk_add(const std::vector<uint32_t> &meta, const std::vector<uint32_t> &left,
-                  const std::vector<float> &value, uint32_t output);
+                  const std::vector<float> &value, uint32_t output, const hbr_device_loss *next_loss = nullptr);
+    bool can_walk_gradients(size_t n_nodes) const;
     // HistogramBackend::build of a host row list (per-node host growth).
     std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
     std::vector<uint32_t> rows_of(const Segment &s);
@@ -137,6 +140,7 @@ private:
                      ScanBest *best_dev);
     void scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out);
     void launch_gradients(const hbr_device_loss &loss, uint32_t output);
+    GradArgs grad_args(const hbr_device_loss &loss);
     bool finish_gradients_on_host(QScale staged);
     hbr_device_loss last_loss_{};
     bool scale_checked_ = true;  // the host has seen the scale of the staged gradients

@@ -388,11 +388,12 @@ void Trainer::softmax_gradients(std::vector<float> &out) {
 // Leaf values onto the margins (training/margins.rs:247-289): by routing
 // every row through the tree on its bins when the index allows it, else
 // over each leaf's row segment.
-void Trainer::grow_and_add(TreeBuilder &b, uint32_t output) {
+void Trainer::grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_loss *next_loss) {
     const bool walk = e_.can_walk();
     std::vector<std::pair<Segment, float>> leaves;
     trees_.push_back(b.grow(&leaves, walk));
     const Tree &t = trees_.back();
+    grads_ready_ = false;
     if (walk) {
         const size_t n = t.nodes.size();
         std::vector<uint32_t> meta(n), left(n, 0);
@@ -407,7 +408,12 @@ void Trainer::grow_and_add(TreeBuilder &b, uint32_t output) {
                 left[i] = (uint32_t)nd.left;
             }
         }
-        e_.walk_add(meta, left, value, output);
+        if (next_loss && e_.can_walk_gradients(n)) {
+            e_.walk_add(meta, left, value, output, next_loss);
+            grads_ready_ = true;
+        } else {
+            e_.walk_add(meta, left, value, output);
+        }
         return;
     }
     std::vector<Segment> segs;
@@ -441,12 +447,16 @@ void Trainer::boost(uint64_t rounds) {
         loss.min_hess = 1e-16f;
         loss.max_input = 80.0f;
         loss.vector_rows = n_ >= 16 ? n_ - n_ % 8 : 0;
-        if (e_.gradients_async_ok(loss)) {
+        if (grads_ready_) {
+            // computed with the previous tree's margin update (checked at the root)
+        } else if (e_.gradients_async_ok(loss)) {
             e_.compute_gradients_async(loss, 0);  // checked at the root's synchronisation
         } else if (!e_.compute_gradients(loss, 0)) {
             fail(kRefused, "a gradient is not finite: the round runs on the host");
         }
-        grow_and_add(b, 0);
+        // the margin update also computes the next round's gradients when the
+        // asynchronous path is allowed for this loss
+        grow_and_add(b, 0, e_.gradients_async_ok(loss) ? &loss : nullptr);
     }
 }
 

@@ -111,8 +111,10 @@ public:
 
 private:
     void softmax_gradients(std::vector<float> &gpair_all);
-    // one grown tree onto the margins of output `output`
-    void grow_and_add(TreeBuilder &b, uint32_t output);
+    // one grown tree onto the margins of output `output` (and, given
+    // next_loss, the next round's gradients in the same pass)
+    void grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_loss *next_loss = nullptr);
+    bool grads_ready_ = false;  // the device holds the next round's gradients
 
     Engine &e_;
     TrainParams p_;

@@ -69,15 +69,14 @@ __device__ __forceinline__ void fold_block(QScale *s, uint32_t mg, uint32_t mh, 
 
 using namespace hbr;
 
-// Grid-stride over rows; the stride is a multiple of 64, so every wave
-// covers 64 consecutive rows and its lanes form whole 8-row vectors.
-extern "C" __global__ __launch_bounds__(256) void hbr_gradients(GradArgs a) {
-    uint32_t mg = 0, mh = 0, bad = 0;
-    const uint32_t stride = gridDim.x * blockDim.x;
-    const uint32_t end = (a.n + kWave - 1) / kWave * kWave;  // whole waves stay in the loop
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < end; i += stride) {
-        const bool active = i < a.n;
-        float m = active ? a.margins[i] : 0.0f;
+namespace hbr {
+
+// Row i's gradient pair from margin m (all lanes of the wave call it
+// together: the logistic vector test is a ballot over 8-row groups). Rows
+// the vector kernel does not cover are listed for the host.
+__device__ __forceinline__ void row_gradient(const GradArgs &a, uint32_t i, bool active, float m, uint32_t &mg,
+                                             uint32_t &mh, uint32_t &bad) {
+    {
         float y = active ? a.labels[i] : 0.0f;
         float w = (active && a.weights) ? a.weights[i] : 1.0f;
         float g = 0.0f, h = 0.0f;
@@ -117,6 +116,20 @@ extern "C" __global__ __launch_bounds__(256) void hbr_gradients(GradArgs a) {
                 bad += (!__builtin_isfinite(g) || !__builtin_isfinite(h)) ? 1u : 0u;
             }
         }
+    }
+}
+
+}  // namespace hbr
+
+// Grid-stride over rows; the stride is a multiple of 64, so every wave
+// covers 64 consecutive rows and its lanes form whole 8-row vectors.
+extern "C" __global__ __launch_bounds__(256) void hbr_gradients(GradArgs a) {
+    uint32_t mg = 0, mh = 0, bad = 0;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    const uint32_t end = (a.n + kWave - 1) / kWave * kWave;  // whole waves stay in the loop
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < end; i += stride) {
+        const bool active = i < a.n;
+        row_gradient(a, i, active, active ? a.margins[i] : 0.0f, mg, mh, bad);
     }
     fold_block(a.scale, mg, mh, bad);
 }

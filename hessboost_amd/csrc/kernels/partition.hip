@@ -225,3 +225,52 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves32(WalkArgs a) 
         }
     }
 }
+
+// hbr_walk_leaves32 and, for the same row while its updated margin is in
+// registers, the next round's gradient pair (row_gradient: the gradient
+// kernel's arithmetic, its 8-row vector test and its max fold). Whole waves
+// stay in the loop past the last row, as in hbr_gradients.
+extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs args) {
+    const WalkArgs &a = args.w;
+    __shared__ uint32_t s_meta[kWalkLdsNodes];
+    __shared__ uint32_t s_left[kWalkLdsNodes];
+    __shared__ float s_value[kWalkLdsNodes];
+    __shared__ uint2 s_rows[256 * 5];
+    for (uint32_t i = threadIdx.x; i < a.n_nodes; i += blockDim.x) {
+        s_meta[i] = a.meta[i];
+        s_left[i] = a.left[i];
+        s_value[i] = a.value[i];
+    }
+    __syncthreads();
+    uint2 *mine = s_rows + threadIdx.x * 5;
+    const uint8_t *bins = reinterpret_cast<const uint8_t *>(mine);
+    uint32_t mg = 0, mh = 0, bad = 0;
+    const uint32_t end = (a.n + kWave - 1) / kWave * kWave;
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < end; r += gridDim.x * blockDim.x) {
+        const bool active = r < a.n;
+        float m = 0.0f;
+        if (active) {
+            const uint4 *src = reinterpret_cast<const uint4 *>(a.bins8 + (size_t)r * 32u);
+            const uint4 x = src[0], y = src[1];
+            mine[0] = make_uint2(x.x, x.y);
+            mine[1] = make_uint2(x.z, x.w);
+            mine[2] = make_uint2(y.x, y.y);
+            mine[3] = make_uint2(y.z, y.w);
+            uint32_t nid = 0, meta = s_meta[0];
+            for (uint32_t step = 0; step < a.n_nodes && !(meta >> 31); step++) {
+                const uint32_t f = meta & 31u, lim = (meta >> 16) & 0x7fffu;
+                nid = s_left[nid] + ((uint32_t)bins[f] < lim ? 0u : 1u);
+                nid = nid < a.n_nodes ? nid : 0u;
+                meta = s_meta[nid];
+            }
+            float *mp = a.margins + (size_t)r * a.m_stride + a.output;
+            m = *mp;
+            if (meta >> 31) {
+                m = m + s_value[nid];
+                *mp = m;
+            }
+        }
+        row_gradient(args.g, r, active, m, mg, mh, bad);
+    }
+    fold_block(args.g.scale, mg, mh, bad);
+}
