@@ -106,6 +106,22 @@ struct TotalArgs {
     QBin *out;              // accumulated with 64-bit atomics (zeroed before)
 };
 
+// ---- level counts on the device ---------------------------------------------------
+// A depthwise tree grown on the device: each level's decision kernel writes
+// how many splits and partition tiles the level has, and the kernels of the
+// level read their work counts from here (their grids are launched for the
+// most the level can hold, and the surplus workgroups exit).
+struct GrowCounts {
+    uint32_t n_front;       // frontier nodes of the level being decided
+    uint32_t n_splits;      // splits of the last decided level (0 at the depth limit)
+    uint32_t n_tiles;       // their partition tiles
+    uint32_t n_nodes;       // tree nodes so far
+    uint32_t hist_nodes;    // histograms built this tree (root included)
+    uint32_t error;         // nonzero: a level needed more slots than reserved
+    uint64_t hist_rows;     // rows summed into built children this tree (root excluded)
+    uint64_t part_rows;     // rows partitioned this tree
+};
+
 // ---- partition -----------------------------------------------------------------
 // One node to partition: its segment, the split's routing and where its
 // children's statistics go.
@@ -147,6 +163,7 @@ struct PartArgs {
     const uint32_t *feature_offset;
     uint32_t n_rows;
     uint32_t words;              // bitmap words per feature
+    const GrowCounts *grow;      // non-null: n_splits and n_tiles are read from here
 };
 
 // ---- histograms ----------------------------------------------------------------
@@ -189,6 +206,7 @@ struct PlanArgs {
     uint32_t *counts;           // [0] tiles, [1] tile_rows
     uint32_t min_rows;
     uint32_t fuse_subtract;     // built children of splits also update their siblings (dense kernels)
+    const GrowCounts *grow;     // non-null: one node per split of the level, n_splits read from here
 };
 
 struct HistArgs {
@@ -221,6 +239,7 @@ struct ReduceArgs {
     uint32_t total_bins;
     uint32_t groups;
     uint32_t fg;
+    const GrowCounts *grow;     // non-null: nodes = its n_splits (the grid covers the most)
 };
 
 // sibling = parent - built, in place in the parent's slot, for each split.
@@ -280,6 +299,7 @@ struct ScanArgs {
     ScanBest *per_feature;   // n_nodes * n_features
     ScanBest *best;          // n_nodes
     QBin *root_total;        // nodes flagged kScanDeviceRoot: their total (read, or written when dense)
+    const GrowCounts *grow;  // non-null: nodes = 2 x its n_splits (the grid covers the most)
 };
 
 // ScanNode.pad flag: the node's total is on the device and its root gain is
@@ -294,6 +314,62 @@ struct FinishArgs {
     QScale *scale;
     uint64_t n_rows;
 };
+
+// ---- depthwise growth on the device -------------------------------------------------
+// A frontier node: statistics, monotone bounds and tree node id. Its rows
+// and slot come from the split that made it (child j & 1 of split j >> 1 of
+// the previous level; the root's are the identity run and root_slot).
+struct GrowNode {
+    QBin total;
+    double lower, upper;
+    uint32_t nid;
+    uint32_t pad[3];
+};
+
+// One node of the device-grown tree; the right child is left + 1.
+struct GrowTreeNode {
+    int32_t left;           // -1: leaf
+    uint32_t feature;
+    uint32_t limit;         // present local bins below go left
+    int32_t bin;            // global bin boundary (bins <= bin go left), -1 below every bin, -2 leaf
+    uint32_t default_left;
+    float value;            // leaf: final (eta-scaled) value; else the node's bounded weight
+    float sum_hess;
+    float gain;
+};
+
+// The decision of one level: every frontier node's winner becomes a split
+// (children appended to the tree, partition/histogram/scan records of the
+// level written) or a leaf (final value written).
+struct GrowArgs {
+    GrowCounts *counts;
+    const GrowNode *front;        // this level's frontier (level > 0)
+    GrowNode *next;               // the children (non-terminal levels)
+    const PartSplit *prev_splits; // the previous level's splits and their partition results
+    const PartOut *prev_out;
+    const ScanBest *best;         // the frontier's winners
+    const QBin *root_total;       // level 0
+    const QScale *scale;
+    PartSplit *splits;            // this level's splits, built children and children's scan nodes
+    HistNode *hnodes;
+    ScanNode *snodes;
+    GrowTreeNode *tree;
+    const uint32_t *feature_offset;
+    const int8_t *monotone;       // per feature, or null
+    uint32_t n_monotone;
+    uint32_t level;
+    uint32_t terminal;            // the children are at the depth limit (leaves)
+    uint32_t n_rows;
+    uint32_t root_slot;
+    uint32_t slot_cap;            // histogram slots the tree may use: [0, slot_cap)
+    ScanParams reg;
+    double gamma;
+    float eta;
+    uint32_t pad;
+};
+
+// Most slots a device-grown tree may hold (the LDS free-slot table).
+constexpr uint32_t kGrowMaxSlots = 4096;
 
 // ---- leaves -----------------------------------------------------------------------
 struct LeafSeg {

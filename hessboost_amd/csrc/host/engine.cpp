@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <limits>
 
 namespace hbr {
 
@@ -57,12 +58,13 @@ Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) 
         if (t == 512 || t == 1024) hist_threads = (uint32_t)t;
     }
     if (const char *v = std::getenv("HBROCM_HIST_BIN_MAJOR")) hist_bin_major = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_HIST_WAVES")) {
         const long w = std::strtol(v, nullptr, 10);
         if (w >= 1 && w <= 64) hist_waves = (uint32_t)w;
     }
     upload_index(desc);
-    root_.resize(1);
+    block_.resize(kTreeAt + kMaxDeviceNodes * sizeof(GrowTreeNode));
 }
 
 Engine::~Engine() {
@@ -374,7 +376,7 @@ QBin Engine::root_total(const Segment &sg) {
 // back the winner, the total and the scale. After asynchronous gradients
 // whose kernel left rows to the host's scalar path, those rows are computed
 // here and the root is done again synchronously.
-bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best) {
+void Engine::launch_root(const Segment &seg, uint32_t slot, float lower, float upper) {
     hipStream_t s = dev_.stream();
     // a dense index's root total is the sum of any feature's bins: the scan
     // takes it from feature 0's (which must have bins); else it is summed here
@@ -415,10 +417,16 @@ bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upp
     d_level_in_.reserve(sizeof(RootIn));
     RootIn *rdev = reinterpret_cast<RootIn *>(d_level_in_.get());
     HBR_HIP(hipMemcpyAsync(rdev, rin, sizeof(RootIn), hipMemcpyHostToDevice, s));
-    launch_hist(&rdev->h, {hn}, nullptr, nullptr);
+    const std::vector<HistNode> one{hn};
+    launch_hist(&rdev->h, 1, &one, nullptr, nullptr);
     launch_scan(&rdev->s, 1, nullptr, nullptr, root_best_dev());
+}
+
+bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best) {
+    hipStream_t s = dev_.stream();
+    launch_root(seg, slot, lower, upper);
     RootBlock *rb = static_cast<RootBlock *>(stage_.alloc(sizeof(RootBlock)));
-    HBR_HIP(hipMemcpyAsync(rb, root_.get(), sizeof(RootBlock), hipMemcpyDeviceToHost, s));
+    HBR_HIP(hipMemcpyAsync(rb, root_block(), sizeof(RootBlock), hipMemcpyDeviceToHost, s));
     dev_.sync();
     *best = rb->best;
     *total = rb->total;
@@ -494,20 +502,22 @@ void Engine::set_scan_params(const ScanParams &p, const std::vector<int8_t> &mon
 // launch), then one workgroup per (tile, feature group). Dense u8 tiles
 // write their sums with plain stores (the reduce kernel adds up nodes of
 // several tiles); CSR tiles add into slots zeroed first.
-void Engine::launch_hist(const HistNode *nodes_dev, const std::vector<HistNode> &nodes, const PartSplit *splits_dev,
-                         const PartOut *part_out_dev, const uint32_t *rows0) {
-    if (nodes.empty()) return;
+void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vector<HistNode> *host_nodes,
+                         const PartSplit *splits_dev, const PartOut *part_out_dev, const uint32_t *rows0,
+                         const GrowCounts *grow) {
+    if (n == 0) return;
     if (gpair_.size() < n_rows_ || !gpair_.get()) fail(kInvalid, "histograms: no gradients staged");
+    if (!dense_u8_ && grow) fail(kInvalid, "histograms: device-counted levels need the dense kernels");
     hipStream_t s = dev_.stream();
-    const uint32_t n = (uint32_t)nodes.size();
     const uint32_t fg = hist_features_per_group;
     const uint32_t groups = dense_u8_ ? ceil_div(n_cols_, fg) : 1;
     // LDS per workgroup is fg features x 257 words x 16 bytes of 160 KiB
     const uint32_t per_cu = !dense_u8_ ? 4 : fg <= 8 ? 4 : fg <= 16 ? 2 : 1;
     const uint32_t target = std::max<uint32_t>(1, (uint32_t)dev_.cu_count() * per_cu * hist_waves / groups);
     if (!dense_u8_) {
+        if (!host_nodes) fail(kInvalid, "histograms: sparse nodes need their slots on the host");
         std::vector<uint32_t> slots(n);
-        for (uint32_t i = 0; i < n; i++) slots[i] = nodes[i].slot;
+        for (uint32_t i = 0; i < n; i++) slots[i] = (*host_nodes)[i].slot;
         upload_vec(d_slots_, slots, stage_, s);
         ZeroArgs z{hist_.get(), d_slots_.get(), n, total_bins_};
         dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), n), dim3(256), z);
@@ -527,6 +537,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, const std::vector<HistNode> 
     p.counts = d_hcounts_.get();
     p.min_rows = kHistMinRows;
     p.fuse_subtract = dense_u8_ ? 1u : 0u;
+    p.grow = grow;
     dev_.launch("hbr_hist_plan", dim3(1), dim3(256), p);
 
     HistArgs a{};
@@ -563,6 +574,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, const std::vector<HistNode> 
         r.total_bins = total_bins_;
         r.groups = groups;
         r.fg = fg;
+        r.grow = grow;
         dev_.launch("hbr_hist_reduce", dim3(n_cols_ * 4, n), dim3(1024), r);
     }
 }
@@ -581,7 +593,7 @@ void Engine::build_nodes(const std::vector<Segment> &segs, const std::vector<uin
         counters.hist_bytes += hist_bytes(segs[i].len, !n.contiguous);
     }
     upload_vec(d_hnodes_, nodes, stage_, dev_.stream());
-    launch_hist(d_hnodes_.get(), nodes, nullptr, nullptr);
+    launch_hist(d_hnodes_.get(), (uint32_t)nodes.size(), &nodes, nullptr, nullptr);
 }
 
 void Engine::subtract(const std::vector<uint32_t> &parents, const std::vector<uint32_t> &built) {
@@ -599,7 +611,7 @@ void Engine::subtract(const std::vector<uint32_t> &parents, const std::vector<ui
 }
 
 void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit *splits_dev,
-                         const PartOut *part_out_dev, ScanBest *best_dev) {
+                         const PartOut *part_out_dev, ScanBest *best_dev, const GrowCounts *grow) {
     const uint64_t pairs = (uint64_t)n * n_cols_;
     d_per_feature_.reserve(pairs ? pairs : 1);
     ScanArgs a{};
@@ -618,6 +630,7 @@ void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit 
     a.per_feature = d_per_feature_.get();
     a.best = best_dev;
     a.root_total = total_dev();
+    a.grow = grow;
     dev_.launch("hbr_scan_features", dim3(ceil_div(pairs, 4)), dim3(256), a);
     dev_.launch("hbr_scan_merge", dim3(n), dim3(64), a);
 }
@@ -664,6 +677,28 @@ struct Layout {
     }
 };
 }  // namespace
+
+// Routing data and row buffers of the partition kernels (splits, counts and
+// outputs are the caller's).
+PartArgs Engine::part_args() const {
+    PartArgs a{};
+    a.tile_left = d_tile_left_.get();
+    a.decisions = d_decisions_.get();
+    a.src_rows[0] = rows_[0].get();
+    a.src_rows[1] = rows_[1].get();
+    a.dst_rows[0] = rows_[0].get();
+    a.dst_rows[1] = rows_[1].get();
+    a.dense = have_cols_ ? 1u : 0u;
+    a.cols8 = cols8_.size() ? cols8_.get() : nullptr;
+    a.cols16 = cols16_.size() ? cols16_.get() : nullptr;
+    a.missing = missing_.size() ? missing_.get() : nullptr;
+    a.row_ptr = row_ptr_.get();
+    a.gbins = gbins_.get();
+    a.feature_offset = d_fo_.get();
+    a.n_rows = (uint32_t)n_rows_;
+    a.words = words_;
+    return a;
+}
 
 std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, bool terminal) {
     const uint32_t P = (uint32_t)splits.size();
@@ -735,32 +770,17 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
 
     d_tile_left_.reserve(tiles ? tiles : 1);
     d_decisions_.reserve((size_t)(tiles ? tiles : 1) * (kPartTile / 64));
-    PartArgs a{};
+    PartArgs a = part_args();
     a.splits = splits_dev;
     a.n_splits = P;
     a.n_tiles = tiles;
-    a.tile_left = d_tile_left_.get();
-    a.decisions = d_decisions_.get();
     a.out = pout_dev;
-    a.src_rows[0] = rows_[0].get();
-    a.src_rows[1] = rows_[1].get();
-    a.dst_rows[0] = rows_[0].get();
-    a.dst_rows[1] = rows_[1].get();
-    a.dense = have_cols_ ? 1u : 0u;
-    a.cols8 = cols8_.size() ? cols8_.get() : nullptr;
-    a.cols16 = cols16_.size() ? cols16_.get() : nullptr;
-    a.missing = missing_.size() ? missing_.get() : nullptr;
-    a.row_ptr = row_ptr_.get();
-    a.gbins = gbins_.get();
-    a.feature_offset = d_fo_.get();
-    a.n_rows = (uint32_t)n_rows_;
-    a.words = words_;
     dev_.launch("hbr_part_count", dim3(tiles), dim3(kPartThreads), a);
     dev_.launch("hbr_part_scan", dim3(P), dim3(1024), a);
     dev_.launch("hbr_part_scatter", dim3(tiles), dim3(kPartThreads), a);
 
     if (!terminal) {
-        launch_hist(reinterpret_cast<const HistNode *>(dev_in + o_hnodes), hn, splits_dev, pout_dev);
+        launch_hist(reinterpret_cast<const HistNode *>(dev_in + o_hnodes), P, &hn, splits_dev, pout_dev);
         if (!dense_u8_) {  // the dense kernels turn each parent into the sibling as they finish
             SubArgs sub{splits_dev, P, hist_.get(), total_bins_};
             dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), sub);
@@ -796,6 +816,123 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
     identity_rows0_ = false;
     stage_.reset();
     return children;
+}
+
+// Depthwise growth on the device. Per level: the decision kernel (splits,
+// leaves, the level's partition/histogram/scan records, tree nodes), then
+// the partition, the built children's histograms (siblings by subtraction)
+// and the children's search. Grids are launched for the most the level can
+// hold (2^level splits, every row in a split); the kernels read the real
+// counts from the device. The tree, its counts and the scale come back with
+// one copy after the last level.
+bool Engine::can_grow_device(uint64_t max_depth) const {
+    if (!device_grow || !dense_u8_ || max_depth < 1 || max_depth > kMaxDeviceDepth || n_rows_ == 0) return false;
+    const uint64_t slots = uint64_t(1) << (max_depth - 1);
+    if (slots > kGrowMaxSlots) return false;
+    // surplus scan workgroups stay few: both children of every possible split
+    const uint64_t pmax = max_depth >= 2 ? uint64_t(1) << (max_depth - 2) : 1;
+    if (2 * pmax * n_cols_ > (uint64_t(1) << 22)) return false;
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return false;
+    return std::max<uint64_t>(slots, slot_cap_) * (uint64_t)total_bins_ * sizeof(QBin) <= free_b / 2;
+}
+
+bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vector<GrowTreeNode> &nodes) {
+    if (!can_grow_device(max_depth)) fail(kInvalid, "device growth: index or depth not supported");
+    hipStream_t s = dev_.stream();
+    const uint32_t depth = (uint32_t)max_depth;
+    const uint32_t slot_cap = 1u << (depth - 1);
+    if (!reserve_slots(slot_cap)) fail(kRefused, "histogram slots do not fit in device memory");
+    const uint32_t pmax_all = depth >= 2 ? 1u << (depth - 2) : 1u;
+    const uint32_t row_tiles = ceil_div(n_rows_, kPartTile);
+    for (int b = 0; b < 2; b++) {
+        g_front_[b].reserve(slot_cap);
+        g_splits_[b].reserve(pmax_all);
+        g_pout_[b].reserve(pmax_all);
+    }
+    d_hnodes_.reserve(pmax_all);
+    d_snodes_.reserve(2 * pmax_all);
+    d_best_.reserve(2 * pmax_all);
+    d_tile_left_.reserve(row_tiles + pmax_all);
+    d_decisions_.reserve((size_t)(row_tiles + pmax_all) * (kPartTile / 64));
+    GrowCounts *counts = grow_counts_dev();
+
+    // the root: total, histogram into slot 0, search (queued)
+    const Segment root{0, (uint32_t)n_rows_, 0};
+    const float inf = std::numeric_limits<float>::infinity();
+    launch_root(root, 0, -inf, inf);
+    for (uint32_t lv = 0; lv < depth; lv++) {
+        const bool terminal = lv + 1 >= depth;
+        const uint32_t pmax = (uint32_t)std::min<uint64_t>(uint64_t(1) << lv, n_rows_);
+        GrowArgs g{};
+        g.counts = counts;
+        g.front = g_front_[lv & 1].get();
+        g.next = g_front_[(lv + 1) & 1].get();
+        g.prev_splits = g_splits_[(lv + 1) & 1].get();
+        g.prev_out = g_pout_[(lv + 1) & 1].get();
+        g.best = lv == 0 ? root_best_dev() : d_best_.get();
+        g.root_total = total_dev();
+        g.scale = scale_dev();
+        g.splits = g_splits_[lv & 1].get();
+        g.hnodes = d_hnodes_.get();
+        g.snodes = d_snodes_.get();
+        g.tree = grow_tree_dev();
+        g.feature_offset = d_fo_.get();
+        g.monotone = has_monotone_ ? monotone_.get() : nullptr;
+        g.n_monotone = has_monotone_ ? n_cols_ : 0u;
+        g.level = lv;
+        g.terminal = terminal ? 1u : 0u;
+        g.n_rows = (uint32_t)n_rows_;
+        g.root_slot = 0;
+        g.slot_cap = slot_cap;
+        g.reg = scan_params_;
+        g.gamma = gamma;
+        g.eta = eta;
+        dev_.launch("hbr_grow_decide", dim3(1), dim3(1024), g);
+        if (terminal) break;
+        PartArgs a = part_args();
+        a.splits = g_splits_[lv & 1].get();
+        a.n_splits = pmax;
+        a.n_tiles = row_tiles + pmax;
+        a.out = g_pout_[lv & 1].get();
+        a.grow = counts;
+        dev_.launch("hbr_part_count", dim3(a.n_tiles), dim3(kPartThreads), a);
+        dev_.launch("hbr_part_scan", dim3(pmax), dim3(1024), a);
+        dev_.launch("hbr_part_scatter", dim3(a.n_tiles), dim3(kPartThreads), a);
+        launch_hist(d_hnodes_.get(), pmax, nullptr, a.splits, a.out, nullptr, counts);
+        launch_scan(d_snodes_.get(), 2 * pmax, a.splits, a.out, d_best_.get(), counts);
+    }
+    const size_t n_max = (size_t(2) << depth) - 1;
+    const size_t bytes = kTreeAt + n_max * sizeof(GrowTreeNode);
+    uint8_t *host = static_cast<uint8_t *>(stage_.alloc(bytes));
+    HBR_HIP(hipMemcpyAsync(host, block_.get(), bytes, hipMemcpyDeviceToHost, s));
+    dev_.sync();
+    RootBlock rb;
+    GrowCounts gc;
+    std::memcpy(&rb, host, sizeof(rb));
+    std::memcpy(&gc, host + kCountsAt, sizeof(gc));
+    if (gc.error) fail(kInvalid, "device growth: a level needed more histogram slots than reserved");
+    if (gc.n_nodes > n_max) fail(kInvalid, "device growth: node count out of range");
+    nodes.resize(gc.n_nodes);
+    std::memcpy(nodes.data(), host + kTreeAt, gc.n_nodes * sizeof(GrowTreeNode));
+    stage_.reset();
+    // every level's scatter wrote into the other buffer
+    identity_rows0_ = false;
+    // (the root's histogram was counted when it was queued)
+    counters.hist_nodes += gc.hist_nodes - 1;
+    counters.hist_rows += gc.hist_rows;
+    counters.hist_bytes += hist_bytes(gc.hist_rows, true);
+    counters.partition_rows += gc.part_rows;
+    if (scale_checked_) return true;
+    scale_checked_ = true;
+    if (rb.scale.scalar_rows == 0 && rb.scale.nonfinite == 0) {
+        scale_host_ = rb.scale;
+        return true;
+    }
+    // rows the vector kernel left to the host's scalar path: finish them,
+    // then grow the tree again from the corrected gradients
+    if (!finish_gradients_on_host(rb.scale)) return false;
+    return grow_device(max_depth, gamma, eta, nodes);
 }
 
 void Engine::add_leaves(const std::vector<Segment> &segs, const std::vector<float> &values, uint32_t output) {
@@ -906,7 +1043,7 @@ std::vector<QBin> Engine::build_rows(const uint32_t *rows, uint64_t m) {
     n.slot = slot;
     const std::vector<HistNode> one{n};
     upload_vec(d_hnodes_, one, stage_, s);
-    launch_hist(d_hnodes_.get(), one, nullptr, nullptr, host_rows_.get());
+    launch_hist(d_hnodes_.get(), (uint32_t)one.size(), &one, nullptr, nullptr, host_rows_.get());
     std::vector<QBin> out(total_bins_);
     hist_.download(out.data(), total_bins_, s, (size_t)slot * total_bins_);
     dev_.sync();

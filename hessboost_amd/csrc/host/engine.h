@@ -110,6 +110,15 @@ public:
     void walk_add(const std::vector<uint32_t> &meta, const std::vector<uint32_t> &left,
                   const std::vector<float> &value, uint32_t output, const hbr_device_loss *next_loss = nullptr);
     bool can_walk_gradients(size_t n_nodes) const;
+    // ---- depthwise growth on the device ----------------------------------------
+    // A whole depthwise tree decided level by level on the device from the
+    // staged gradients and read back with one synchronisation: the nodes in
+    // tree order. Needs a dense u8 index (the depth limit's rows are routed
+    // by the walk, not partitioned) and max_depth in [1, kMaxDeviceDepth].
+    static constexpr uint32_t kMaxDeviceDepth = 13;
+    bool can_grow_device(uint64_t max_depth) const;
+    // false when a gradient is not finite
+    bool grow_device(uint64_t max_depth, double gamma, float eta, std::vector<GrowTreeNode> &nodes);
     // HistogramBackend::build of a host row list (per-node host growth).
     std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
     std::vector<uint32_t> rows_of(const Segment &s);
@@ -134,10 +143,16 @@ private:
     bool identity_rows0_ = false;
     bool rows0_written_ = false;
     void write_identity_rows();  // buffer 0 := 0..n-1, once per tree, when a row list is read
-    void launch_hist(const HistNode *nodes_dev, const std::vector<HistNode> &nodes, const PartSplit *splits_dev,
-                     const PartOut *part_out_dev, const uint32_t *rows0 = nullptr);
+    // `n` nodes (the most a device-grown level can hold, with `grow`);
+    // host_nodes: their slots are zeroed first (CSR)
+    void launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vector<HistNode> *host_nodes,
+                     const PartSplit *splits_dev, const PartOut *part_out_dev, const uint32_t *rows0 = nullptr,
+                     const GrowCounts *grow = nullptr);
     void launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit *splits_dev, const PartOut *part_out_dev,
-                     ScanBest *best_dev);
+                     ScanBest *best_dev, const GrowCounts *grow = nullptr);
+    // the root's total, histogram and split search, queued (no synchronisation)
+    void launch_root(const Segment &seg, uint32_t slot, float lower, float upper);
+    PartArgs part_args() const;
     void scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out);
     void launch_gradients(const hbr_device_loss &loss, uint32_t output);
     GradArgs grad_args(const hbr_device_loss &loss);
@@ -173,10 +188,22 @@ private:
         QBin total;
         ScanBest best;
     };
-    DBuf<RootBlock> root_;
-    QScale *scale_dev() const { return &root_.get()->scale; }
-    QBin *total_dev() const { return &root_.get()->total; }
-    ScanBest *root_best_dev() const { return &root_.get()->best; }
+    // followed by a device-grown tree's counts and nodes, so that the tree's
+    // one synchronisation reads back everything with one copy
+    DBuf<uint8_t> block_;
+    static constexpr size_t kCountsAt = (sizeof(RootBlock) + 63) / 64 * 64;
+    static constexpr size_t kTreeAt = kCountsAt + (sizeof(GrowCounts) + 63) / 64 * 64;
+    static constexpr size_t kMaxDeviceNodes = (size_t(2) << kMaxDeviceDepth) - 1;
+    RootBlock *root_block() const { return reinterpret_cast<RootBlock *>(block_.get()); }
+    QScale *scale_dev() const { return &root_block()->scale; }
+    QBin *total_dev() const { return &root_block()->total; }
+    ScanBest *root_best_dev() const { return &root_block()->best; }
+    GrowCounts *grow_counts_dev() const { return reinterpret_cast<GrowCounts *>(block_.get() + kCountsAt); }
+    GrowTreeNode *grow_tree_dev() const { return reinterpret_cast<GrowTreeNode *>(block_.get() + kTreeAt); }
+    // device-grown levels: frontiers, splits and partition results, two of each
+    DBuf<GrowNode> g_front_[2];
+    DBuf<PartSplit> g_splits_[2];
+    DBuf<PartOut> g_pout_[2];
     QScale scale_host_{};
     DBuf<uint32_t> scalar_list_;
     DBuf<uint32_t> rows_[2];
@@ -218,6 +245,7 @@ public:
     uint32_t hist_threads = 1024;
     uint32_t hist_waves = 1;
     bool hist_bin_major = true;  // [bin][feature] LDS layout (16 and 32 feature groups)
+    bool device_grow = true;     // depthwise trees decided on the device where eligible
 };
 
 }  // namespace hbr

@@ -118,6 +118,35 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool 
     e_.set_scan_params(ScanParams{p_.reg.lambda, p_.reg.alpha, p_.reg.max_delta_step, p_.reg.min_child_weight},
                        p_.monotone);
 
+    // a depthwise tree whose depth limit's rows the walk routes: decided on
+    // the device level by level, read back once
+    if (walk && p_.policy == HBR_GROW_DEPTHWISE && e_.can_grow_device(limit)) {
+        e_.begin_tree();
+        std::vector<GrowTreeNode> dn;
+        if (!e_.grow_device(limit, p_.gamma, p_.eta, dn))
+            fail(kRefused, "a gradient is not finite: the round runs on the host");
+        const auto &cuts = e_.cut_values();
+        t.nodes.resize(dn.size());
+        for (size_t i = 0; i < dn.size(); i++) {
+            const GrowTreeNode &d = dn[i];
+            TreeNode &n = t.nodes[i];
+            n.leaf_value = d.value;
+            n.sum_hess = d.sum_hess;
+            if (d.left < 0) continue;  // a leaf keeps the defaults (split_bin -2)
+            if (d.left + 1 >= (int32_t)dn.size() || (d.bin >= 0 && (size_t)d.bin >= cuts.size()))
+                fail(kInvalid, "device growth: malformed node");
+            n.split_feature = d.feature;
+            n.split_cond = d.bin >= 0 ? cuts[d.bin] : -FLT_MAX;
+            n.default_left = (uint8_t)d.default_left;
+            n.left = d.left;
+            n.right = d.left + 1;
+            n.split_gain = d.gain;
+            n.split_bin = d.bin;
+            n.split_limit = d.limit;
+        }
+        return t;
+    }
+
     // root (builder/hist/mod.rs:345-456): statistics, histogram, search
     e_.begin_tree();
     Open root{};

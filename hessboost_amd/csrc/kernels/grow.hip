@@ -1,0 +1,285 @@
+// Depthwise growth decided on the device: one workgroup per level turns the
+// frontier's winners into splits or leaves, so that a whole tree is grown
+// from one stream of launches and read back once.
+//
+// Restates, per frontier node and in frontier order, the host builder's
+// level step (builder/hist/mod.rs:458-573 depthwise frontier;
+// builder/mod.rs:167-193 SplitPos and BestSplit::valid; builder/shared.rs:
+// 89-141 bounded weights and node gains, :174-187 final leaf values;
+// tree/constraints.rs child bounds at the f64 midpoint): node ids of the
+// children are appended in frontier order (left, right), a split whose
+// children sit at the depth limit makes two leaves, and every leaf's value
+// is calc_weight clamped to its bounds, rounded to f32, times eta.
+//
+// Histogram slots: the built child of split i takes the i-th slot (in
+// ascending order) that no splitting parent holds; its sibling keeps the
+// parent's slot (the histogram kernels turn the parent into the sibling).
+#include "common.h"
+
+namespace hbr {
+
+// calc_weight (tree/gain.rs:107-116) then Bounds::clamp, in f64.
+__device__ __forceinline__ double leaf_weight(double g, double h, const ScanParams &r, double lower, double upper) {
+    double w = 0.0;
+    if (!(h < r.min_child_weight || h <= 0.0)) {
+        w = -threshold_l1(g, r.alpha) / (h + r.lambda);
+        if (r.max_delta_step > 0.0)
+            w = w < -r.max_delta_step ? -r.max_delta_step : (w > r.max_delta_step ? r.max_delta_step : w);
+    }
+    if (w < lower) w = lower;
+    if (w > upper) w = upper;
+    return w;
+}
+
+// f64::midpoint.
+__device__ __forceinline__ double midpoint(double a, double b) {
+    const double hi = 1.7976931348623157e308 / 2.0, lo = 2.2250738585072014e-308 * 2.0;
+    if (__builtin_fabs(a) <= hi && __builtin_fabs(b) <= hi) return (a + b) / 2.0;
+    if (__builtin_fabs(a) < lo) return a + b / 2.0;
+    if (__builtin_fabs(b) < lo) return a / 2.0 + b;
+    return a / 2.0 + b / 2.0;
+}
+
+constexpr uint32_t kGrowThreads = 1024;
+constexpr uint32_t kGrowSlotWords = kGrowMaxSlots / 32;
+
+}  // namespace hbr
+
+using namespace hbr;
+
+extern "C" __global__ __launch_bounds__(1024) void hbr_grow_decide(GrowArgs a) {
+    __shared__ uint32_t s_used[kGrowSlotWords];   // slots of splitting parents
+    __shared__ uint32_t s_free[kGrowMaxSlots];    // the other slots, ascending
+    const uint32_t tid = threadIdx.x;
+    GrowCounts c0 = *a.counts;
+    if (a.level == 0) {
+        c0.n_front = 1;
+        c0.n_nodes = 1;
+        c0.hist_nodes = 1;
+        c0.error = 0;
+        c0.hist_rows = 0;
+        c0.part_rows = 0;
+    }
+    const uint32_t n_front = c0.n_front, node_base = c0.n_nodes;
+    const int eg = a.scale->exp_g, eh = a.scale->exp_h;
+    for (uint32_t w = tid; w < kGrowSlotWords; w += kGrowThreads) s_used[w] = 0u;
+    __syncthreads();
+
+    uint32_t split_carry = 0, tile_carry = 0;
+    unsigned long long hist_rows = 0, part_rows = 0;
+    for (uint32_t base = 0; base < n_front; base += kGrowThreads) {
+        const uint32_t j = base + tid;
+        const bool active = j < n_front;
+        // the node: its rows, slot, statistics and bounds
+        Seg seg{0u, 0u, 0u, 0u};
+        uint32_t slot = 0, nid = 0, identity = 0;
+        QBin total{0, 0};
+        double lower = -__builtin_inf(), upper = __builtin_inf();
+        if (active && a.level == 0) {
+            seg = Seg{0u, a.n_rows, 0u, 0u};
+            identity = 1;
+            slot = a.root_slot;
+            total = *a.root_total;
+        } else if (active) {
+            const GrowNode g = a.front[j];
+            const uint32_t i = j >> 1, c = j & 1u;
+            const PartSplit sp = a.prev_splits[i];
+            const PartOut po = a.prev_out[i];
+            const uint32_t nl = po.left_len;
+            seg.buf = sp.seg.buf ^ 1u;
+            seg.offset = c == 0 ? sp.seg.offset : sp.seg.offset + nl;
+            seg.len = c == 0 ? nl : sp.seg.len - nl;
+            const bool built = (c == 0) == (po.built_left != 0);
+            slot = built ? sp.fresh_slot : sp.parent_slot;
+            total = g.total;
+            lower = g.lower;
+            upper = g.upper;
+            nid = g.nid;
+            if (c == 0) {
+                part_rows += sp.seg.len;
+                hist_rows += po.built_left ? nl : sp.seg.len - nl;
+            }
+        }
+        const double ng = dequant(total.g, eg), nh = dequant(total.h, eh);
+        // the winner as a split position (builder/mod.rs:167-193)
+        bool valid = false;
+        ScanBest b{};
+        uint32_t f = 0, limit = 0, dl = 0;
+        int32_t bin = -1;
+        double lg = 0, lh = 0, rg = 0, rh = 0;
+        float wl = 0.0f, wr = 0.0f;
+        if (active) {
+            b = a.best[a.level == 0 ? 0 : j];
+            if (b.index != 0xffffffffu) {
+                f = b.feature;
+                const uint32_t fs = a.feature_offset[f], nb = a.feature_offset[f + 1] - fs;
+                if (b.index < nb) {
+                    bin = (int32_t)(fs + b.index);
+                    limit = b.index + 1;
+                    dl = 0;
+                } else {
+                    const uint32_t off = nb - 1 - (b.index - nb);
+                    bin = off == 0 ? -1 : (int32_t)(fs + off - 1);
+                    limit = off;
+                    dl = 1;
+                }
+                lg = dequant(b.left.g, eg);
+                lh = dequant(b.left.h, eh);
+                rg = dequant(b.right.g, eg);
+                rh = dequant(b.right.h, eh);
+                wl = bounded_weight(lg, lh, a.reg, (float)lower, (float)upper);
+                wr = bounded_weight(rg, rh, a.reg, (float)lower, (float)upper);
+                const double loss = (double)b.loss;
+                valid = loss > 1e-6 && loss >= a.gamma && lh > 0.0 && rh > 0.0 && lh >= a.reg.min_child_weight &&
+                        rh >= a.reg.min_child_weight;
+            }
+        }
+        const uint32_t tiles = valid && !a.terminal ? (seg.len + kPartTile - 1) / kPartTile : 0u;
+        uint32_t n_valid, n_tiles;
+        const uint32_t i = split_carry + block_exclusive_scan<kGrowThreads>(valid ? 1u : 0u, &n_valid);
+        const uint32_t tile_begin = tile_carry + block_exclusive_scan<kGrowThreads>(tiles, &n_tiles);
+        if (active && a.level == 0) {
+            GrowTreeNode r{};
+            r.left = -1;
+            r.bin = -2;
+            r.default_left = 1;
+            r.sum_hess = (float)nh;
+            a.tree[0] = r;
+        }
+        if (active && !valid) {
+            // a leaf: builder/shared.rs:174-187 then scale_leaves(eta)
+            const float w = (float)leaf_weight(ng, nh, a.reg, lower, upper);
+            a.tree[nid].value = w * a.eta;
+        } else if (active) {
+            const uint32_t left = node_base + 2 * i;
+            GrowTreeNode &r = a.tree[nid];
+            r.left = (int32_t)left;
+            r.feature = f;
+            r.limit = limit;
+            r.bin = bin;
+            r.default_left = dl;
+            r.gain = b.loss;
+            // child bounds (tree/constraints.rs) at the midpoint of the f32 weights
+            double cb[4] = {lower, upper, lower, upper};
+            const int dir = f < a.n_monotone && a.monotone ? (int)a.monotone[f] : 0;
+            if (dir != 0) {
+                const double mid = midpoint((double)wl, (double)wr);
+                if (dir > 0) {
+                    cb[1] = mid;
+                    cb[2] = mid;
+                } else {
+                    cb[0] = mid;
+                    cb[3] = mid;
+                }
+            }
+            const double cg[2] = {lg, rg}, ch[2] = {lh, rh};
+            const float cw[2] = {wl, wr};
+            const QBin ct[2] = {b.left, b.right};
+#pragma unroll
+            for (uint32_t c = 0; c < 2; c++) {
+                GrowTreeNode k{};
+                k.left = -1;
+                k.bin = -2;
+                k.default_left = 1;
+                k.value = cw[c];
+                k.sum_hess = (float)ch[c];
+                if (a.terminal) {
+                    const float w = (float)leaf_weight(cg[c], ch[c], a.reg, cb[2 * c], cb[2 * c + 1]);
+                    k.value = w * a.eta;
+                } else {
+                    GrowNode g{};
+                    g.total = ct[c];
+                    g.lower = cb[2 * c];
+                    g.upper = cb[2 * c + 1];
+                    g.nid = left + c;
+                    a.next[2 * i + c] = g;
+                    ScanNode s{};
+                    s.from_split = 1;
+                    s.split = i;
+                    s.child = c;
+                    s.total = ct[c];
+                    s.root_gain = node_gain(cg[c], ch[c], a.reg, (float)cb[2 * c], (float)cb[2 * c + 1]);
+                    s.lower = (float)cb[2 * c];
+                    s.upper = (float)cb[2 * c + 1];
+                    a.snodes[2 * i + c] = s;
+                }
+                a.tree[left + c] = k;
+            }
+            if (!a.terminal) {
+                PartSplit p{};
+                p.seg = seg;
+                p.feature = f;
+                p.limit = limit;
+                p.default_left = dl;
+                p.identity = identity;
+                p.tile_begin = tile_begin;
+                p.parent_slot = slot;
+                a.splits[i] = p;
+                HistNode h{};
+                h.from_split = 1;
+                h.split = i;
+                a.hnodes[i] = h;
+                if (slot < a.slot_cap && slot < kGrowMaxSlots) atomicOr(&s_used[slot >> 5], 1u << (slot & 31));
+            }
+        }
+        split_carry += n_valid;
+        tile_carry += n_tiles;
+    }
+    // the built children's slots: the split_carry lowest slots no splitting parent holds
+    __syncthreads();
+    const uint32_t n_splits = a.terminal ? 0u : split_carry;
+    {
+        const uint32_t w = tid;
+        const uint32_t cap_words = (min(a.slot_cap, kGrowMaxSlots) + 31) / 32;
+        uint32_t free_bits = 0;
+        if (w < cap_words) {
+            const uint32_t valid_bits = (w + 1) * 32 <= a.slot_cap ? ~0u : (1u << (a.slot_cap - w * 32)) - 1u;
+            free_bits = ~s_used[w] & valid_bits;
+        }
+        uint32_t n_free;
+        const uint32_t first = block_exclusive_scan<kGrowThreads>((uint32_t)__popc(free_bits), &n_free);
+        uint32_t k = first;
+        while (free_bits) {
+            const uint32_t bit = (uint32_t)__builtin_ctz(free_bits);
+            free_bits &= free_bits - 1u;
+            s_free[k++] = w * 32 + bit;
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < n_splits; i += kGrowThreads) {
+            const uint32_t slot = i < n_free ? s_free[i] : 0u;
+            a.splits[i].fresh_slot = slot;
+            a.hnodes[i].slot = slot;
+        }
+        if (tid == 0) {
+            GrowCounts c = c0;
+            c.n_front = n_splits * 2;
+            c.n_splits = n_splits;
+            c.n_tiles = a.terminal ? 0u : tile_carry;
+            c.n_nodes = node_base + 2 * split_carry;
+            c.hist_nodes += n_splits;
+            if (n_splits > n_free) c.error = 1;
+            a.counts[0] = c;
+        }
+    }
+    // per-thread row counts of the previous level's splits
+    __shared__ unsigned long long s_rows[2][kGrowThreads / kWave];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        hist_rows += __shfl_xor(hist_rows, d, kWave);
+        part_rows += __shfl_xor(part_rows, d, kWave);
+    }
+    if (lane_id() == 0) {
+        s_rows[0][tid / kWave] = hist_rows;
+        s_rows[1][tid / kWave] = part_rows;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long hr = 0, pr = 0;
+        for (uint32_t w = 0; w < kGrowThreads / kWave; w++) {
+            hr += s_rows[0][w];
+            pr += s_rows[1][w];
+        }
+        a.counts->hist_rows = c0.hist_rows + hr;
+        a.counts->part_rows = c0.part_rows + pr;
+    }
+}

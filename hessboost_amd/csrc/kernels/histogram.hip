@@ -209,8 +209,10 @@ constexpr uint32_t kPlanLdsNodes = 4096;
 
 extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
     __shared__ uint32_t s_len[kPlanLdsNodes];  // node lengths, for the candidate counts
+    __shared__ uint32_t s_first[256], s_count[256];
+    const uint32_t n_nodes = a.grow ? a.grow->n_splits : a.n_nodes;
     unsigned long long sum = 0, longest = 0;
-    for (uint32_t i = threadIdx.x; i < a.n_nodes; i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < n_nodes; i += blockDim.x) {
         HistNode nd = a.nodes[i];
         const Seg s = resolve_node(a, nd);
         a.nodes[i].seg = s;
@@ -243,7 +245,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
     cand = min(max(cand, lo), hi);
     const uint32_t c32 = (uint32_t)min(cand, 0xffffffffull);  // 32-bit divisions
     unsigned long long c = 0;
-    for (uint32_t i = 0; i < a.n_nodes; i++) {
+    for (uint32_t i = 0; i < n_nodes; i++) {
         const uint32_t len = i < kPlanLdsNodes ? s_len[i] : a.nodes[i].seg.len;
         c += len / c32 + (len % c32 != 0 ? 1u : 0u);
     }
@@ -260,26 +262,36 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
     const unsigned long long size = pick;
     const uint32_t tile_rows = (uint32_t)((size + kWave - 1) / kWave * kWave);
     uint32_t carry = 0, part_carry = 0;
-    for (uint32_t base = 0; base < a.n_nodes; base += blockDim.x) {
+    for (uint32_t base = 0; base < n_nodes; base += blockDim.x) {
         const uint32_t i = base + threadIdx.x;
-        const uint32_t len = i < a.n_nodes ? a.nodes[i].seg.len : 0u;
+        const uint32_t len = i < n_nodes ? (i < kPlanLdsNodes ? s_len[i] : a.nodes[i].seg.len) : 0u;
         const uint32_t n = (len + tile_rows - 1) / tile_rows;
         uint32_t all, part_all;
         const uint32_t first = block_exclusive_scan<256>(n, &all);
         const uint32_t part_first = block_exclusive_scan<256>(n > 1 ? n : 0u, &part_all);
-        if (i < a.n_nodes) {
+        if (i < n_nodes) {
             a.nodes[i].tile_begin = carry + first;
             a.nodes[i].n_tiles = n;
             a.nodes[i].pad[0] = part_carry + part_first;
-            for (uint32_t k = 0; k < n; k++) {
+        }
+        s_first[threadIdx.x] = carry + first;
+        s_count[threadIdx.x] = n;
+        __syncthreads();
+        // each wave writes the tiles of every fourth node, one tile per lane
+        const uint32_t chunk = min(n_nodes - base, (uint32_t)blockDim.x);
+        for (uint32_t q = threadIdx.x / kWave; q < chunk; q += blockDim.x / kWave) {
+            const uint32_t qn = s_count[q], qf = s_first[q];
+            const uint32_t qlen = base + q < kPlanLdsNodes ? s_len[base + q] : a.nodes[base + q].seg.len;
+            for (uint32_t k = lane_id(); k < qn; k += kWave) {
                 HistTile t;
-                t.node = i;
+                t.node = base + q;
                 t.row0 = k * tile_rows;
-                t.rows = min(tile_rows, len - k * tile_rows);
+                t.rows = min(tile_rows, qlen - k * tile_rows);
                 t.k = k;
-                a.tiles[carry + first + k] = t;
+                a.tiles[qf + k] = t;
             }
         }
+        __syncthreads();
         carry += all;
         part_carry += part_all;
     }
@@ -304,6 +316,7 @@ extern "C" __global__ __launch_bounds__(512) void hbr_hist_csr(HistArgs a) { his
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_reduce(ReduceArgs a) {
     __shared__ int64_t acc[2][16][64];
     const uint32_t f = blockIdx.x >> 2, quarter = blockIdx.x & 3u;
+    if (a.grow && blockIdx.y >= a.grow->n_splits) return;
     const HistNode nd = a.nodes[blockIdx.y];
     if (f >= a.n_cols || nd.n_tiles == 1) return;  // uniform across the workgroup
     const uint32_t lo = a.feature_offset[f], nb = a.feature_offset[f + 1] - lo;

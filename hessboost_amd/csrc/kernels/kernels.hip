@@ -4,6 +4,7 @@
 #include "histogram.hip"
 #include "partition.hip"
 #include "split.hip"
+#include "grow.hip"
 #include "predict.hip"
 
 // The abi.h checksum this code object was built with (checked by the host

@@ -38,8 +38,8 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
 
 // The split owning a tile: the last split whose first tile is at or before
 // it (a split without rows shares its first tile with the next split).
-__device__ __forceinline__ uint32_t split_of_tile(const PartArgs &a, uint32_t tile) {
-    uint32_t lo = 0, hi = a.n_splits;
+__device__ __forceinline__ uint32_t split_of_tile(const PartArgs &a, uint32_t n_splits, uint32_t tile) {
+    uint32_t lo = 0, hi = n_splits;
     while (hi - lo > 1) {
         const uint32_t mid = (lo + hi) / 2;
         if (a.splits[mid].tile_begin <= tile) lo = mid;
@@ -47,6 +47,10 @@ __device__ __forceinline__ uint32_t split_of_tile(const PartArgs &a, uint32_t ti
     }
     return lo;
 }
+
+// The level's counts: from the device when a grown level set them.
+__device__ __forceinline__ uint32_t part_splits(const PartArgs &a) { return a.grow ? a.grow->n_splits : a.n_splits; }
+__device__ __forceinline__ uint32_t part_tiles(const PartArgs &a) { return a.grow ? a.grow->n_tiles : a.n_tiles; }
 
 }  // namespace hbr
 
@@ -57,8 +61,8 @@ using namespace hbr;
 extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
     __shared__ uint32_t wave_count[kPartThreads / kWave];
     const uint32_t tile = blockIdx.x;
-    if (tile >= a.n_tiles) return;
-    const PartSplit sp = a.splits[split_of_tile(a, tile)];
+    if (tile >= part_tiles(a)) return;
+    const PartSplit sp = a.splits[split_of_tile(a, part_splits(a), tile)];
     const uint32_t base = (tile - sp.tile_begin) * kPartTile;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
     const uint32_t wave = threadIdx.x / kWave;
@@ -91,7 +95,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
 constexpr uint32_t kScanThreads = 1024;
 extern "C" __global__ __launch_bounds__(1024) void hbr_part_scan(PartArgs a) {
     const uint32_t s = blockIdx.x;
-    if (s >= a.n_splits) return;
+    if (s >= part_splits(a)) return;
     const PartSplit sp = a.splits[s];
     const uint32_t n_tiles = (sp.seg.len + kPartTile - 1) / kPartTile;
     uint32_t carry = 0;
@@ -116,8 +120,8 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_part_scan(PartArgs a) {
 // left rows before the current ballot; it moves the rows of its own ballots.
 extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     const uint32_t tile = blockIdx.x;
-    if (tile >= a.n_tiles) return;
-    const uint32_t s = split_of_tile(a, tile);
+    if (tile >= part_tiles(a)) return;
+    const uint32_t s = split_of_tile(a, part_splits(a), tile);
     const PartSplit sp = a.splits[s];
     const uint32_t left_len = a.out[s].left_len;
     const uint32_t tile_pos = (tile - sp.tile_begin) * kPartTile;

@@ -92,6 +92,9 @@ __device__ __forceinline__ void offer(Cand &best, bool &nan_seen, float loss, ui
     }
 }
 
+// Nodes of the launch: both children of every split of a device-grown level.
+__device__ __forceinline__ uint32_t scan_nodes(const ScanArgs &a) { return a.grow ? 2u * a.grow->n_splits : a.n_nodes; }
+
 __device__ __forceinline__ uint32_t node_slot(const ScanArgs &a, const ScanNode &nd) {
     if (!nd.from_split) return nd.slot;
     const PartSplit sp = a.splits[nd.split];
@@ -107,7 +110,7 @@ using namespace hbr;
 extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) {
     const uint32_t wave = threadIdx.x / kWave, lane = lane_id();
     const uint32_t pair = blockIdx.x * (blockDim.x / kWave) + wave;
-    if (pair >= a.n_nodes * a.n_features) return;  // uniform per wave
+    if (pair >= scan_nodes(a) * a.n_features) return;  // uniform per wave
     const uint32_t node = pair / a.n_features, f = pair % a.n_features;
     const ScanNode nd = a.nodes[node];
     const uint32_t fs = a.feature_offset[f], nb = a.feature_offset[f + 1] - fs;
@@ -247,7 +250,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
 // (loss 0); equal losses keep the lower feature.
 extern "C" __global__ __launch_bounds__(64) void hbr_scan_merge(ScanArgs a) {
     const uint32_t node = blockIdx.x;
-    if (node >= a.n_nodes) return;
+    if (node >= scan_nodes(a)) return;
     const uint32_t lane = lane_id();
     float bl = 0.0f;
     uint32_t bf = 0xffffffffu;

@@ -98,3 +98,70 @@ def test_monotone_and_regularization_match_oracle():
                                             min_child_weight=3.0, monotone=mono), 4)
     model = hb.train(params, hb.DMatrix(x, label=y), 4)
     compare_trees(model.trees, ref.trees())
+
+
+def _grow_both(x, y, params, rounds):
+    """Train twice on one index: trees decided on the device (default for
+    a dense u8 index, depthwise) and trees decided by the host level by
+    level (HBROCM_DEVICE_GROW=0, read when an engine is made)."""
+    import os
+    dm = hb.DMatrix(x, label=y)
+    index = dm.index(params.get("max_bin", 256))
+    out = []
+    for flag in (None, "0"):
+        old = os.environ.pop("HBROCM_DEVICE_GROW", None)
+        if flag is not None:
+            os.environ["HBROCM_DEVICE_GROW"] = flag
+        try:
+            eng = hb.Engine(index, 0)
+        finally:
+            os.environ.pop("HBROCM_DEVICE_GROW", None)
+            if old is not None:
+                os.environ["HBROCM_DEVICE_GROW"] = old
+        tr = hb.Trainer(eng, params, y)
+        eng.set_profiling(True, "hbr_grow_decide")
+        tr.boost(rounds)
+        launches = sum(n for _, (_, n) in eng.kernel_stats().items())
+        eng.set_profiling(False)
+        out.append((tr.trees(), tr.margins(), launches))
+    return out
+
+
+@pytest.mark.parametrize("depth,params", [
+    (1, {"objective": "reg:squarederror"}),
+    (3, {"objective": "binary:logistic", "gamma": 0.5, "max_delta_step": 0.7}),
+    (8, {"objective": "binary:logistic", "alpha": 0.3, "lambda": 2.0, "min_child_weight": 5.0}),
+    (11, {"objective": "reg:squarederror", "monotone_constraints": [1, -1, 0, 1, 0, 0, -1, 0]}),
+])
+def test_device_decided_growth_equals_host_decided(depth, params):
+    """The device's level decisions (split positions, validity, child bounds,
+    slot reuse, node ids, final leaf values) give the trees the host's
+    decisions give, every field bit for bit, and the same margins; the
+    device path is the one that ran (one decision launch per level)."""
+    rng = np.random.default_rng(depth)
+    n, f = 30_000, 8
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    x[:, 3] = np.round(x[:, 3] * 2)  # a few distinct values: ties, empty bins
+    y = (x[:, 0] - 0.5 * x[:, 1] ** 2 + 0.3 * x[:, 3] + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    if params["objective"] == "binary:logistic":
+        y = (y > 0).astype(np.float32)
+    p = dict(params, max_depth=depth, eta=0.3)
+    rounds = 4
+    (dev_trees, dev_m, dev_launches), (host_trees, host_m, host_launches) = _grow_both(x, y, p, rounds)
+    assert dev_launches == rounds * depth and host_launches == 0
+    assert len(dev_trees) == len(host_trees) == rounds
+    for t, (a, b) in enumerate(zip(dev_trees, host_trees)):
+        for key in ("left", "right", "split_feature", "default_left", "split_bin"):
+            assert np.array_equal(a[key], b[key]), (t, key)
+        for key in ("split_cond", "leaf_value", "sum_hess", "split_gain"):
+            assert np.array_equal(a[key].view(np.uint32), b[key].view(np.uint32)), (t, key)
+    assert np.array_equal(dev_m.view(np.uint32), host_m.view(np.uint32))
+    # and the oracle's trees
+    obj = O.OBJ_LOGISTIC if params["objective"] == "binary:logistic" else O.OBJ_SQUARED_ERROR
+    kw = {k: v for k, v in params.items() if k in ("gamma", "max_delta_step", "alpha", "min_child_weight")}
+    if "lambda" in params:
+        kw["reg_lambda"] = params["lambda"]
+    if "monotone_constraints" in params:
+        kw["monotone"] = params["monotone_constraints"]
+    ref = O.Model(O.Dataset(x, max_bin=256), y, O.params(objective=obj, max_depth=depth, eta=0.3, **kw), rounds)
+    compare_trees(dev_trees, ref.trees())
