@@ -365,6 +365,8 @@ struct GrowArgs {
     ScanParams reg;
     double gamma;
     float eta;
+    uint32_t front_cap;           // the most frontier nodes this level can have (records read ahead)
+    uint32_t n_features;
     uint32_t pad;
 };
 

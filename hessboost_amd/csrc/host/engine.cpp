@@ -888,7 +888,9 @@ bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vecto
         g.reg = scan_params_;
         g.gamma = gamma;
         g.eta = eta;
-        dev_.launch("hbr_grow_decide", dim3(1), dim3(1024), g);
+        g.front_cap = lv == 0 ? 1u : std::min<uint32_t>(1u << lv, slot_cap);
+        g.n_features = n_cols_;
+        dev_.launch("hbr_grow_decide", dim3(1), dim3(512), g);
         if (terminal) break;
         PartArgs a = part_args();
         a.splits = g_splits_[lv & 1].get();

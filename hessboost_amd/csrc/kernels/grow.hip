@@ -40,17 +40,39 @@ __device__ __forceinline__ double midpoint(double a, double b) {
     return a / 2.0 + b / 2.0;
 }
 
-constexpr uint32_t kGrowThreads = 1024;
+constexpr uint32_t kGrowThreads = 512;
+constexpr uint32_t kGrowLdsOffsets = 4096;  // feature offsets kept in LDS (more features read them from memory)
 constexpr uint32_t kGrowSlotWords = kGrowMaxSlots / 32;
 
 }  // namespace hbr
 
 using namespace hbr;
 
-extern "C" __global__ __launch_bounds__(1024) void hbr_grow_decide(GrowArgs a) {
+extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
     __shared__ uint32_t s_used[kGrowSlotWords];   // slots of splitting parents
     __shared__ uint32_t s_free[kGrowMaxSlots];    // the other slots, ascending
+    __shared__ uint32_t s_fo[kGrowLdsOffsets + 1];
     const uint32_t tid = threadIdx.x;
+    const bool fo_lds = a.n_features <= kGrowLdsOffsets;
+    if (fo_lds)
+        for (uint32_t k = tid; k <= a.n_features; k += kGrowThreads) s_fo[k] = a.feature_offset[k];
+    // Every record a thread may need is loaded at once, before the counts
+    // say which frontier nodes exist (the arrays hold front_cap records), so
+    // that the level costs one round trip to memory.
+    const uint32_t j0 = tid;
+    const bool cap0 = j0 < a.front_cap;
+    GrowNode g0{};
+    PartSplit sp0{};
+    PartOut po0{};
+    ScanBest b0{};
+    if (cap0 && a.level > 0) {
+        g0 = a.front[j0];
+        sp0 = a.prev_splits[j0 >> 1];
+        po0 = a.prev_out[j0 >> 1];
+    }
+    if (cap0) b0 = a.best[a.level == 0 ? 0 : j0];
+    QBin root_total{0, 0};
+    if (a.level == 0) root_total = *a.root_total;
     GrowCounts c0 = *a.counts;
     if (a.level == 0) {
         c0.n_front = 1;
@@ -75,16 +97,20 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_grow_decide(GrowArgs a) {
         uint32_t slot = 0, nid = 0, identity = 0;
         QBin total{0, 0};
         double lower = -__builtin_inf(), upper = __builtin_inf();
+        ScanBest b{};
         if (active && a.level == 0) {
             seg = Seg{0u, a.n_rows, 0u, 0u};
             identity = 1;
             slot = a.root_slot;
-            total = *a.root_total;
+            total = root_total;
+            b = b0;
         } else if (active) {
-            const GrowNode g = a.front[j];
+            const bool first = base == 0;
+            const GrowNode g = first ? g0 : a.front[j];
             const uint32_t i = j >> 1, c = j & 1u;
-            const PartSplit sp = a.prev_splits[i];
-            const PartOut po = a.prev_out[i];
+            const PartSplit sp = first ? sp0 : a.prev_splits[i];
+            const PartOut po = first ? po0 : a.prev_out[i];
+            b = first ? b0 : a.best[j];
             const uint32_t nl = po.left_len;
             seg.buf = sp.seg.buf ^ 1u;
             seg.offset = c == 0 ? sp.seg.offset : sp.seg.offset + nl;
@@ -103,16 +129,15 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_grow_decide(GrowArgs a) {
         const double ng = dequant(total.g, eg), nh = dequant(total.h, eh);
         // the winner as a split position (builder/mod.rs:167-193)
         bool valid = false;
-        ScanBest b{};
         uint32_t f = 0, limit = 0, dl = 0;
         int32_t bin = -1;
         double lg = 0, lh = 0, rg = 0, rh = 0;
         float wl = 0.0f, wr = 0.0f;
         if (active) {
-            b = a.best[a.level == 0 ? 0 : j];
             if (b.index != 0xffffffffu) {
                 f = b.feature;
-                const uint32_t fs = a.feature_offset[f], nb = a.feature_offset[f + 1] - fs;
+                const uint32_t fs = fo_lds ? s_fo[f] : a.feature_offset[f];
+                const uint32_t nb = (fo_lds ? s_fo[f + 1] : a.feature_offset[f + 1]) - fs;
                 if (b.index < nb) {
                     bin = (int32_t)(fs + b.index);
                     limit = b.index + 1;

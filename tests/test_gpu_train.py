@@ -165,3 +165,43 @@ def test_device_decided_growth_equals_host_decided(depth, params):
         kw["monotone"] = params["monotone_constraints"]
     ref = O.Model(O.Dataset(x, max_bin=256), y, O.params(objective=obj, max_depth=depth, eta=0.3, **kw), rounds)
     compare_trees(dev_trees, ref.trees())
+
+
+@pytest.mark.parametrize("env", [
+    {"HBROCM_HIST_WAVES": "2"},
+    {"HBROCM_HIST_FG": "16"},
+    {"HBROCM_HIST_FG": "8"},
+    {"HBROCM_HIST_BIN_MAJOR": "0", "HBROCM_HIST_THREADS": "512"},
+    {"HBROCM_HIST_WAVES": "3", "HBROCM_DEVICE_GROW": "0"},
+])
+def test_launch_shapes_give_identical_trees(env):
+    """Histograms are exact integer sums, so the launch shape (features per
+    workgroup, LDS layout, threads, tiles per launch, levels decided on the
+    device or the host) cannot change a bit of the trees or the margins."""
+    import os
+    rng = np.random.default_rng(7)
+    n, f = 60_000, 40
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    x[:, 5] = np.round(x[:, 5])
+    y = (x[:, 0] + x[:, 5] * x[:, 1] + 0.2 * rng.standard_normal(n) > 0).astype(np.float32)
+    params = {"objective": "binary:logistic", "max_depth": 7, "eta": 0.3}
+    index = hb.DMatrix(x, label=y).index(256)
+    runs = []
+    for e in ({}, env):
+        saved = {k: os.environ.pop(k, None) for k in e}
+        os.environ.update(e)
+        try:
+            eng = hb.Engine(index, 0)
+        finally:
+            for k in e:
+                os.environ.pop(k, None)
+                if saved[k] is not None:
+                    os.environ[k] = saved[k]
+        tr = hb.Trainer(eng, params, y)
+        tr.boost(3)
+        runs.append((tr.trees(), tr.margins()))
+    (ta, ma), (tb, mb) = runs
+    for a, b in zip(ta, tb):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
