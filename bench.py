@@ -73,6 +73,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-predict", action="store_true")
     ap.add_argument("--breakdown-steps", type=int, default=5)
+    ap.add_argument("--no-kernel-events", action="store_true",
+                    help="time the rounds without HIP events around the histogram kernel")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="first run a device-to-device copy of this many MiB (a known-size kernel for "
                          "scaling hardware byte counters in profiles)")
@@ -113,7 +115,7 @@ def main():
     log(f"{args.warmup} warmup rounds done")
     before = eng.counters()
     # HIP events around the dense histogram kernel only, on the engine's stream
-    eng.set_profiling(True, HIST_KERNEL)
+    eng.set_profiling(not args.no_kernel_events, HIST_KERNEL)
     t0 = time.perf_counter()
     trainer.boost(args.steps)
     t1 = time.perf_counter()

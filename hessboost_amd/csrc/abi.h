@@ -315,6 +315,12 @@ struct FinishArgs {
     uint64_t n_rows;
 };
 
+// saved = live, then live cleared for the next fold (one thread).
+struct RotateArgs {
+    QScale *live;
+    QScale *saved;
+};
+
 // ---- depthwise growth on the device -------------------------------------------------
 // A frontier node: statistics, monotone bounds and tree node id. Its rows
 // and slot come from the split that made it (child j & 1 of split j >> 1 of
@@ -407,6 +413,16 @@ struct WalkArgs {
     uint32_t output;
     uint32_t n_nodes;
     uint32_t pad;
+    // A device-grown tree is read from its records (n_nodes from counts)
+    // instead of meta/left/value.
+    const GrowTreeNode *tree;
+    const GrowCounts *counts;
+    // Non-null: the walk and the gradients happen only when the gradients
+    // the tree was grown from were final (no rows left to the host, none
+    // non-finite) and no earlier guarded walk was skipped; a skip sets
+    // *poison, which stays set until the host clears it.
+    const QScale *guard;
+    uint32_t *poison;
 };
 
 // The margin walk of a finished tree followed, row by row, by the next

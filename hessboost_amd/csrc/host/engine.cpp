@@ -486,9 +486,11 @@ uint64_t Engine::hist_bytes(uint64_t rows, bool gathered) const {
 
 void Engine::set_scan_params(const ScanParams &p, const std::vector<int8_t> &monotone) {
     scan_params_ = p;
+    const bool same = has_monotone_ && monotone == monotone_host_;
     has_monotone_ = false;
     for (int8_t d : monotone) has_monotone_ |= d != 0;
-    if (has_monotone_) {
+    if (has_monotone_ && !same) {
+        monotone_host_ = monotone;
         std::vector<int8_t> dirs(n_cols_, 0);
         for (size_t f = 0; f < monotone.size() && f < n_cols_; f++) dirs[f] = monotone[f];
         monotone_.resize(n_cols_);
@@ -837,8 +839,50 @@ bool Engine::can_grow_device(uint64_t max_depth) const {
     return std::max<uint64_t>(slots, slot_cap_) * (uint64_t)total_bins_ * sizeof(QBin) <= free_b / 2;
 }
 
-bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vector<GrowTreeNode> &nodes) {
+// The root of a device-grown tree: its histogram and scan records never
+// change (all rows as the identity run, slot 0, unbounded), so they are
+// uploaded once.
+void Engine::launch_device_root() {
+    struct RootIn {
+        HistNode h;
+        ScanNode s;
+    };
+    if (d_root_in_.size() < sizeof(RootIn)) {
+        RootIn r{};
+        r.h.seg = Seg{0, (uint32_t)n_rows_, 0, 0};
+        r.h.slot = 0;
+        r.h.contiguous = 1;
+        r.s.slot = 0;
+        r.s.lower = -std::numeric_limits<float>::infinity();
+        r.s.upper = std::numeric_limits<float>::infinity();
+        r.s.pad = kScanDeviceRoot;
+        d_root_in_.resize(sizeof(RootIn));
+        HBR_HIP(hipMemcpy(d_root_in_.get(), &r, sizeof(RootIn), hipMemcpyHostToDevice));
+    }
+    hipStream_t s = dev_.stream();
+    if (!(dense_ && n_cols_ > 0 && fo_[1] > fo_[0])) {
+        HBR_HIP(hipMemsetAsync(total_dev(), 0, sizeof(QBin), s));
+        TotalArgs t{};
+        t.rows = nullptr;
+        t.first = 0;
+        t.n = (uint32_t)n_rows_;
+        t.gpair = gpair_.get();
+        t.scale = scale_dev();
+        t.out = total_dev();
+        dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)), 2048)),
+                    dim3(kThreads), t);
+    }
+    counters.hist_nodes++;
+    counters.hist_rows += n_rows_;
+    counters.hist_bytes += hist_bytes(n_rows_, false);
+    RootIn *rdev = reinterpret_cast<RootIn *>(d_root_in_.get());
+    launch_hist(&rdev->h, 1, nullptr, nullptr, nullptr);
+    launch_scan(&rdev->s, 1, nullptr, nullptr, root_best_dev());
+}
+
+Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, float eta) {
     if (!can_grow_device(max_depth)) fail(kInvalid, "device growth: index or depth not supported");
+    if (gpair_.size() < n_rows_ || !gpair_.get()) fail(kInvalid, "device growth: no gradients staged");
     hipStream_t s = dev_.stream();
     const uint32_t depth = (uint32_t)max_depth;
     const uint32_t slot_cap = 1u << (depth - 1);
@@ -857,10 +901,11 @@ bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vecto
     d_decisions_.reserve((size_t)(row_tiles + pmax_all) * (kPartTile / 64));
     GrowCounts *counts = grow_counts_dev();
 
-    // the root: total, histogram into slot 0, search (queued)
-    const Segment root{0, (uint32_t)n_rows_, 0};
-    const float inf = std::numeric_limits<float>::infinity();
-    launch_root(root, 0, -inf, inf);
+    TreeTicket t;
+    t.slot = tree_seq_++ & 1u;
+    t.check = !scale_checked_;
+    scale_checked_ = true;
+    launch_device_root();
     for (uint32_t lv = 0; lv < depth; lv++) {
         const bool terminal = lv + 1 >= depth;
         const uint32_t pmax = (uint32_t)std::min<uint64_t>(uint64_t(1) << lv, n_rows_);
@@ -904,37 +949,104 @@ bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vecto
         launch_hist(d_hnodes_.get(), pmax, nullptr, a.splits, a.out, nullptr, counts);
         launch_scan(d_snodes_.get(), 2 * pmax, a.splits, a.out, d_best_.get(), counts);
     }
+    // every level's scatter wrote into the other buffer
+    identity_rows0_ = false;
+    // the scale, counts and nodes back in one copy
+    const size_t bytes = kTreeAt + kMaxDeviceNodes * sizeof(GrowTreeNode);
+    void *host = tree_stage_[t.slot].reserve(bytes);
+    if (!tree_done_[t.slot]) HBR_HIP(hipEventCreate(&tree_done_[t.slot]));
     const size_t n_max = (size_t(2) << depth) - 1;
-    const size_t bytes = kTreeAt + n_max * sizeof(GrowTreeNode);
-    uint8_t *host = static_cast<uint8_t *>(stage_.alloc(bytes));
-    HBR_HIP(hipMemcpyAsync(host, block_.get(), bytes, hipMemcpyDeviceToHost, s));
-    dev_.sync();
+    HBR_HIP(hipMemcpyAsync(host, block_.get(), kTreeAt + n_max * sizeof(GrowTreeNode), hipMemcpyDeviceToHost, s));
+    HBR_HIP(hipEventRecord(tree_done_[t.slot], s));
+    return t;
+}
+
+Engine::TreeState Engine::finish_device_tree(const TreeTicket &t, std::vector<GrowTreeNode> &nodes, QScale *scale) {
+    HBR_HIP(hipEventSynchronize(tree_done_[t.slot]));
+    const uint8_t *host = static_cast<const uint8_t *>(tree_stage_[t.slot].get());
     RootBlock rb;
     GrowCounts gc;
     std::memcpy(&rb, host, sizeof(rb));
     std::memcpy(&gc, host + kCountsAt, sizeof(gc));
     if (gc.error) fail(kInvalid, "device growth: a level needed more histogram slots than reserved");
-    if (gc.n_nodes > n_max) fail(kInvalid, "device growth: node count out of range");
+    if (gc.n_nodes == 0 || gc.n_nodes > kMaxDeviceNodes) fail(kInvalid, "device growth: node count out of range");
     nodes.resize(gc.n_nodes);
     std::memcpy(nodes.data(), host + kTreeAt, gc.n_nodes * sizeof(GrowTreeNode));
-    stage_.reset();
-    // every level's scatter wrote into the other buffer
-    identity_rows0_ = false;
     // (the root's histogram was counted when it was queued)
     counters.hist_nodes += gc.hist_nodes - 1;
     counters.hist_rows += gc.hist_rows;
     counters.hist_bytes += hist_bytes(gc.hist_rows, true);
     counters.partition_rows += gc.part_rows;
-    if (scale_checked_) return true;
+    if (scale) *scale = rb.scale;
+    if (!t.check) return kTreeOk;
+    if (rb.scale.scalar_rows != 0 || rb.scale.nonfinite != 0) return kTreeNeedsHost;
+    scale_host_ = rb.scale;
+    return kTreeOk;
+}
+
+bool Engine::recover_gradients(const QScale &scale) {
+    dev_.sync();
+    stage_.reset();
     scale_checked_ = true;
-    if (rb.scale.scalar_rows == 0 && rb.scale.nonfinite == 0) {
-        scale_host_ = rb.scale;
-        return true;
+    if (!finish_gradients_on_host(scale)) return false;
+    if (poison_.size()) {
+        HBR_HIP(hipMemsetAsync(poison_.get(), 0, sizeof(uint32_t), dev_.stream()));
+        dev_.sync();
     }
-    // rows the vector kernel left to the host's scalar path: finish them,
-    // then grow the tree again from the corrected gradients
-    if (!finish_gradients_on_host(rb.scale)) return false;
-    return grow_device(max_depth, gamma, eta, nodes);
+    return true;
+}
+
+bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vector<GrowTreeNode> &nodes) {
+    for (;;) {
+        const TreeTicket t = queue_device_tree(max_depth, gamma, eta);
+        QScale sc;
+        if (finish_device_tree(t, nodes, &sc) == kTreeOk) return true;
+        // rows the vector kernel left to the host's scalar path: finish
+        // them, then grow the tree again from the corrected gradients
+        if (!recover_gradients(sc)) return false;
+    }
+}
+
+void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss) {
+    if (!dense_u8_ || stride_ != 32) fail(kRefused, "walk: the index has no 32-byte row-major u8 bins");
+    if (output >= outputs_) fail(kInvalid, "walk: no such output");
+    hipStream_t s = dev_.stream();
+    WalkArgs a{};
+    a.tree = grow_tree_dev();
+    a.counts = grow_counts_dev();
+    a.bins8 = rows8_.get();
+    a.margins = margins_.get();
+    a.stride = stride_;
+    a.n = (uint32_t)n_rows_;
+    a.m_stride = outputs_;
+    a.output = output;
+    const uint32_t blocks =
+        std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)), (uint32_t)dev_.cu_count() * 8);
+    if (!next_loss) {
+        dev_.launch("hbr_walk_leaves32", dim3(blocks), dim3(256), a);
+        return;
+    }
+    if (outputs_ != 1 || !labels_loaded_) fail(kInvalid, "walk: gradients need one output and labels");
+    gpair_.resize(n_rows_ ? n_rows_ : 1);
+    scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
+    if (!poison_.size()) {
+        poison_.resize(1);
+        guard_scale_.resize(1);
+        HBR_HIP(hipMemsetAsync(poison_.get(), 0, sizeof(uint32_t), s));
+    }
+    // the tree's scale aside (the walk's guard), the live one cleared for the fold
+    RotateArgs r{scale_dev(), guard_scale_.get()};
+    dev_.launch("hbr_scale_rotate", dim3(1), dim3(64), r);
+    a.guard = guard_scale_.get();
+    a.poison = poison_.get();
+    WalkGradArgs wg{};
+    wg.w = a;
+    wg.g = grad_args(*next_loss);
+    dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
+    FinishArgs f{scale_dev(), n_rows_};
+    dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
+    last_loss_ = *next_loss;
+    scale_checked_ = false;  // the next tree's finish checks the scale
 }
 
 void Engine::add_leaves(const std::vector<Segment> &segs, const std::vector<float> &values, uint32_t output) {

@@ -119,6 +119,29 @@ public:
     bool can_grow_device(uint64_t max_depth) const;
     // false when a gradient is not finite
     bool grow_device(uint64_t max_depth, double gamma, float eta, std::vector<GrowTreeNode> &nodes);
+    // The same in two halves, so that a tree can be queued before the
+    // previous one is read back: queue (no synchronisation), then finish
+    // (waits for that tree's readback only). kTreeNeedsHost: the gradients
+    // it was grown from had rows for the host's scalar path or non-finite
+    // values; recover_gradients (after the stream drains) finishes them and
+    // the tree is grown again.
+    struct TreeTicket {
+        uint32_t slot = 0;
+        bool check = false;  // the gradients' scale is checked at finish
+    };
+    enum TreeState { kTreeOk = 0, kTreeNeedsHost = 1 };
+    TreeTicket queue_device_tree(uint64_t max_depth, double gamma, float eta);
+    TreeState finish_device_tree(const TreeTicket &t, std::vector<GrowTreeNode> &nodes, QScale *scale);
+    bool recover_gradients(const QScale &scale);  // false: a gradient is not finite
+    // The last queued device tree's leaves onto the margins of `output`,
+    // routed on the device from its records (no readback); with next_loss
+    // also the next round's gradients, guarded: skipped (and every later
+    // guarded walk with it, until recover_gradients) when the tree's own
+    // gradients were not final.
+    bool can_walk_device_tree(uint64_t max_depth) const {
+        return can_grow_device(max_depth) && stride_ == 32 && max_depth <= 9 && outputs_ == 1 && labels_loaded_;
+    }
+    void walk_device_tree(uint32_t output, const hbr_device_loss *next_loss);
     // HistogramBackend::build of a host row list (per-node host growth).
     std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
     std::vector<uint32_t> rows_of(const Segment &s);
@@ -152,6 +175,18 @@ private:
                      ScanBest *best_dev, const GrowCounts *grow = nullptr);
     // the root's total, histogram and split search, queued (no synchronisation)
     void launch_root(const Segment &seg, uint32_t slot, float lower, float upper);
+    // the same for a device-grown tree (slot 0, unbounded) from records
+    // uploaded once
+    void launch_device_root();
+    DBuf<uint8_t> d_root_in_;
+    // device-grown trees in flight: pinned readbacks and their events; the
+    // guarded walk's saved scale and skip flag
+    PinnedBuf tree_stage_[2];
+    hipEvent_t tree_done_[2] = {nullptr, nullptr};
+    uint32_t tree_seq_ = 0;
+    DBuf<QScale> guard_scale_;
+    DBuf<uint32_t> poison_;
+    std::vector<int8_t> monotone_host_;
     PartArgs part_args() const;
     void scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out);
     void launch_gradients(const hbr_device_loss &loss, uint32_t output);

@@ -1,6 +1,7 @@
 #include "runtime.h"
 
 #include <dlfcn.h>
+#include <cstdlib>
 
 #include <memory>
 
@@ -101,8 +102,14 @@ hipEvent_t Device::take_event() {
         event_pool_.pop_back();
         return e;
     }
+    // timing events without the system-scope fence a plain event adds (the
+    // fence stalls the stream around every timed kernel)
+    static const bool fence = [] {
+        const char *v = std::getenv("HBROCM_EVENT_FENCE");
+        return v && std::strtol(v, nullptr, 10) != 0;
+    }();
     hipEvent_t e;
-    HBR_HIP(hipEventCreate(&e));
+    HBR_HIP(hipEventCreateWithFlags(&e, fence ? hipEventDefault : hipEventDisableSystemFence));
     return e;
 }
 

@@ -161,6 +161,34 @@ private:
     std::vector<Block> blocks_;
 };
 
+// Pinned host memory that outlives staging resets (a copy into it may still
+// be queued when the owner resets its stage).
+class PinnedBuf {
+public:
+    PinnedBuf() = default;
+    ~PinnedBuf() {
+        if (p_) (void)hipHostFree(p_);
+    }
+    PinnedBuf(const PinnedBuf &) = delete;
+    PinnedBuf &operator=(const PinnedBuf &) = delete;
+    // At least `bytes` (contents not kept); only while no copy uses it.
+    void *reserve(size_t bytes) {
+        if (bytes > n_) {
+            if (p_) (void)hipHostFree(p_);
+            p_ = nullptr;
+            n_ = 0;
+            HBR_HIP(hipHostMalloc(&p_, bytes, hipHostMallocDefault));
+            n_ = bytes;
+        }
+        return p_;
+    }
+    void *get() const { return p_; }
+
+private:
+    void *p_ = nullptr;
+    size_t n_ = 0;
+};
+
 // Grow `buf` (keeping nothing) and copy `v` into it through `stage`.
 template <typename T>
 void upload_vec(DBuf<T> &buf, const std::vector<T> &v, Stage &stage, hipStream_t s) {

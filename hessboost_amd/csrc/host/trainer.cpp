@@ -3,6 +3,7 @@
 #include <cfloat>
 #include <cmath>
 #include <cstring>
+#include <deque>
 #include <limits>
 
 namespace hbr {
@@ -107,6 +108,39 @@ void TreeBuilder::leaf(const Open &o) {
     if (o.has_slot) e_.free_slot(o.slot);
 }
 
+Engine::TreeTicket TreeBuilder::queue_device() {
+    e_.set_scan_params(ScanParams{p_.reg.lambda, p_.reg.alpha, p_.reg.max_delta_step, p_.reg.min_child_weight},
+                       p_.monotone);
+    e_.begin_tree();
+    return e_.queue_device_tree(p_.max_depth, p_.gamma, p_.eta);
+}
+
+// A device-grown tree's records as the model's nodes (split thresholds from
+// the cuts on the host).
+Tree TreeBuilder::tree_from(const std::vector<GrowTreeNode> &dn) const {
+    Tree t;
+    const auto &cuts = e_.cut_values();
+    t.nodes.resize(dn.size());
+    for (size_t i = 0; i < dn.size(); i++) {
+        const GrowTreeNode &d = dn[i];
+        TreeNode &n = t.nodes[i];
+        n.leaf_value = d.value;
+        n.sum_hess = d.sum_hess;
+        if (d.left < 0) continue;  // a leaf keeps the defaults (split_bin -2)
+        if (d.left + 1 >= (int32_t)dn.size() || (d.bin >= 0 && (size_t)d.bin >= cuts.size()))
+            fail(kInvalid, "device growth: malformed node");
+        n.split_feature = d.feature;
+        n.split_cond = d.bin >= 0 ? cuts[d.bin] : -FLT_MAX;
+        n.default_left = (uint8_t)d.default_left;
+        n.left = d.left;
+        n.right = d.left + 1;
+        n.split_gain = d.gain;
+        n.split_bin = d.bin;
+        n.split_limit = d.limit;
+    }
+    return t;
+}
+
 Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool walk) {
     Tree t;
     g_.clear();
@@ -125,26 +159,7 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool 
         std::vector<GrowTreeNode> dn;
         if (!e_.grow_device(limit, p_.gamma, p_.eta, dn))
             fail(kRefused, "a gradient is not finite: the round runs on the host");
-        const auto &cuts = e_.cut_values();
-        t.nodes.resize(dn.size());
-        for (size_t i = 0; i < dn.size(); i++) {
-            const GrowTreeNode &d = dn[i];
-            TreeNode &n = t.nodes[i];
-            n.leaf_value = d.value;
-            n.sum_hess = d.sum_hess;
-            if (d.left < 0) continue;  // a leaf keeps the defaults (split_bin -2)
-            if (d.left + 1 >= (int32_t)dn.size() || (d.bin >= 0 && (size_t)d.bin >= cuts.size()))
-                fail(kInvalid, "device growth: malformed node");
-            n.split_feature = d.feature;
-            n.split_cond = d.bin >= 0 ? cuts[d.bin] : -FLT_MAX;
-            n.default_left = (uint8_t)d.default_left;
-            n.left = d.left;
-            n.right = d.left + 1;
-            n.split_gain = d.gain;
-            n.split_bin = d.bin;
-            n.split_limit = d.limit;
-        }
-        return t;
+        return tree_from(dn);
     }
 
     // root (builder/hist/mod.rs:345-456): statistics, histogram, search
@@ -454,7 +469,48 @@ void Trainer::grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_los
     e_.add_leaves(segs, vals, output);
 }
 
+// Rounds with the device a tree ahead of the host: tree t+1 and its
+// margin walk are queued before tree t is read back, so the device never
+// waits for the host. A tree whose gradients turn out not to be final
+// (logistic rows left to the host's scalar path) had its walk skipped on
+// the device, and so had every tree queued after it; the host then
+// finishes those gradients and grows the tree again.
+void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
+    TreeBuilder b(e_, p_.grow);
+    std::deque<Engine::TreeTicket> inflight;
+    uint64_t queued = 0, done = 0;
+    while (done < rounds) {
+        while (queued < rounds && inflight.size() < 2) {
+            if (!grads_ready_) e_.compute_gradients_async(loss, 0);
+            inflight.push_back(b.queue_device());
+            e_.walk_device_tree(0, &loss);
+            grads_ready_ = true;
+            queued++;
+        }
+        std::vector<GrowTreeNode> nodes;
+        QScale sc{};
+        const Engine::TreeState st = e_.finish_device_tree(inflight.front(), nodes, &sc);
+        inflight.pop_front();
+        if (st == Engine::kTreeOk) {
+            trees_.push_back(b.tree_from(nodes));
+            done++;
+            continue;
+        }
+        inflight.clear();  // grown from the unfinished gradients too
+        if (!e_.recover_gradients(sc)) fail(kRefused, "a gradient is not finite: the round runs on the host");
+        queued = done;
+    }
+}
+
 void Trainer::boost(uint64_t rounds) {
+    if (p_.objective != HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE &&
+        e_.can_walk_device_tree(p_.grow.max_depth)) {
+        hbr_device_loss loss = device_loss();
+        if (e_.gradients_async_ok(loss)) {
+            boost_pipelined(rounds, loss);
+            return;
+        }
+    }
     TreeBuilder b(e_, p_.grow);
     for (uint64_t it = 0; it < rounds; it++) {
         if (p_.objective == HBR_OBJ_SOFTMAX) {
@@ -470,12 +526,7 @@ void Trainer::boost(uint64_t rounds) {
             }
             continue;
         }
-        hbr_device_loss loss{};
-        loss.kind = p_.objective == HBR_OBJ_LOGISTIC ? HBR_LOSS_LOGISTIC : HBR_LOSS_SQUARED_ERROR;
-        loss.scale_pos_weight = p_.scale_pos_weight;
-        loss.min_hess = 1e-16f;
-        loss.max_input = 80.0f;
-        loss.vector_rows = n_ >= 16 ? n_ - n_ % 8 : 0;
+        const hbr_device_loss loss = device_loss();
         if (grads_ready_) {
             // computed with the previous tree's margin update (checked at the root)
         } else if (e_.gradients_async_ok(loss)) {
@@ -487,6 +538,16 @@ void Trainer::boost(uint64_t rounds) {
         // asynchronous path is allowed for this loss
         grow_and_add(b, 0, e_.gradients_async_ok(loss) ? &loss : nullptr);
     }
+}
+
+hbr_device_loss Trainer::device_loss() const {
+    hbr_device_loss loss{};
+    loss.kind = p_.objective == HBR_OBJ_LOGISTIC ? HBR_LOSS_LOGISTIC : HBR_LOSS_SQUARED_ERROR;
+    loss.scale_pos_weight = p_.scale_pos_weight;
+    loss.min_hess = 1e-16f;
+    loss.max_input = 80.0f;
+    loss.vector_rows = n_ >= 16 ? n_ - n_ % 8 : 0;
+    return loss;
 }
 
 void Trainer::margins(float *out) { e_.read_margins(out, n_ * k_); }

@@ -53,6 +53,10 @@ public:
     // of the depth limit's children are not partitioned (their segments are
     // empty): the caller routes rows through the tree instead.
     Tree grow(std::vector<std::pair<Segment, float>> *leaves, bool walk = false);
+    // A depthwise tree queued on the device (Engine::queue_device_tree),
+    // and a finished one's records as a Tree.
+    Engine::TreeTicket queue_device();
+    Tree tree_from(const std::vector<GrowTreeNode> &nodes) const;
 
 private:
     struct Open {
@@ -111,6 +115,8 @@ public:
 
 private:
     void softmax_gradients(std::vector<float> &gpair_all);
+    void boost_pipelined(uint64_t rounds, const hbr_device_loss &loss);
+    hbr_device_loss device_loss() const;
     // one grown tree onto the margins of output `output` (and, given
     // next_loss, the next round's gradients in the same pass)
     void grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_loss *next_loss = nullptr);

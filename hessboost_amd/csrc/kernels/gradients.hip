@@ -188,3 +188,9 @@ extern "C" __global__ __launch_bounds__(64) void hbr_finish_scale(FinishArgs a) 
     q.exp_h = exponent_for(q.max_h_bits, a.n_rows);
     *a.scale = q;
 }
+
+extern "C" __global__ __launch_bounds__(64) void hbr_scale_rotate(RotateArgs a) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    *a.saved = *a.live;
+    *a.live = QScale{0, 0, 0u, 0u, 0u, 0u, {0u, 0u}};
+}

@@ -190,6 +190,26 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves(WalkArgs a) {
     }
 }
 
+// The walk's node table in LDS: from meta/left/value, or from a
+// device-grown tree's records (a leaf's left is -1).
+__device__ __forceinline__ uint32_t walk_nodes(const WalkArgs &a) { return a.tree ? a.counts->n_nodes : a.n_nodes; }
+
+__device__ __forceinline__ void load_walk_table(const WalkArgs &a, uint32_t n_nodes, uint32_t *s_meta, uint32_t *s_left,
+                                                float *s_value) {
+    for (uint32_t i = threadIdx.x; i < n_nodes; i += blockDim.x) {
+        if (a.tree) {
+            const GrowTreeNode t = a.tree[i];
+            s_meta[i] = t.left < 0 ? 1u << 31 : t.feature | (t.limit << 16);
+            s_left[i] = t.left < 0 ? 0u : (uint32_t)t.left;
+            s_value[i] = t.value;
+        } else {
+            s_meta[i] = a.meta[i];
+            s_left[i] = a.left[i];
+            s_value[i] = a.value[i];
+        }
+    }
+}
+
 // The walk for 32-byte rows and trees of at most kWalkLdsNodes nodes: the
 // node table sits in LDS, and each thread copies its row's 32 bins into its
 // own LDS slot with two 16-byte loads, then reads the bytes it routes on
@@ -201,11 +221,8 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves32(WalkArgs a) 
     __shared__ uint32_t s_left[kWalkLdsNodes];
     __shared__ float s_value[kWalkLdsNodes];
     __shared__ uint2 s_rows[256 * 5];  // 40 bytes per thread: 32 bins + pad
-    for (uint32_t i = threadIdx.x; i < a.n_nodes; i += blockDim.x) {
-        s_meta[i] = a.meta[i];
-        s_left[i] = a.left[i];
-        s_value[i] = a.value[i];
-    }
+    const uint32_t n_nodes = min(walk_nodes(a), kWalkLdsNodes);
+    load_walk_table(a, n_nodes, s_meta, s_left, s_value);
     __syncthreads();
     uint2 *mine = s_rows + threadIdx.x * 5;
     const uint8_t *bins = reinterpret_cast<const uint8_t *>(mine);
@@ -217,10 +234,10 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves32(WalkArgs a) 
         mine[2] = make_uint2(y.x, y.y);
         mine[3] = make_uint2(y.z, y.w);
         uint32_t nid = 0, meta = s_meta[0];
-        for (uint32_t step = 0; step < a.n_nodes && !(meta >> 31); step++) {
+        for (uint32_t step = 0; step < n_nodes && !(meta >> 31); step++) {
             const uint32_t f = meta & 31u, lim = (meta >> 16) & 0x7fffu;
             nid = s_left[nid] + ((uint32_t)bins[f] < lim ? 0u : 1u);
-            nid = nid < a.n_nodes ? nid : 0u;
+            nid = nid < n_nodes ? nid : 0u;
             meta = s_meta[nid];
         }
         if (meta >> 31) {
@@ -240,11 +257,15 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
     __shared__ uint32_t s_left[kWalkLdsNodes];
     __shared__ float s_value[kWalkLdsNodes];
     __shared__ uint2 s_rows[256 * 5];
-    for (uint32_t i = threadIdx.x; i < a.n_nodes; i += blockDim.x) {
-        s_meta[i] = a.meta[i];
-        s_left[i] = a.left[i];
-        s_value[i] = a.value[i];
+    if (a.guard) {  // uniform: every workgroup reads the same words
+        const QScale q = *a.guard;
+        if (q.scalar_rows != 0 || q.nonfinite != 0 || *a.poison != 0) {
+            if (blockIdx.x == 0 && threadIdx.x == 0) *a.poison = 1u;
+            return;
+        }
     }
+    const uint32_t n_nodes = min(walk_nodes(a), kWalkLdsNodes);
+    load_walk_table(a, n_nodes, s_meta, s_left, s_value);
     __syncthreads();
     uint2 *mine = s_rows + threadIdx.x * 5;
     const uint8_t *bins = reinterpret_cast<const uint8_t *>(mine);
@@ -261,10 +282,10 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
             mine[2] = make_uint2(y.x, y.y);
             mine[3] = make_uint2(y.z, y.w);
             uint32_t nid = 0, meta = s_meta[0];
-            for (uint32_t step = 0; step < a.n_nodes && !(meta >> 31); step++) {
+            for (uint32_t step = 0; step < n_nodes && !(meta >> 31); step++) {
                 const uint32_t f = meta & 31u, lim = (meta >> 16) & 0x7fffu;
                 nid = s_left[nid] + ((uint32_t)bins[f] < lim ? 0u : 1u);
-                nid = nid < a.n_nodes ? nid : 0u;
+                nid = nid < n_nodes ? nid : 0u;
                 meta = s_meta[nid];
             }
             float *mp = a.margins + (size_t)r * a.m_stride + a.output;

@@ -5,6 +5,7 @@ import pytest
 
 import hessboost_amd as hb
 from hessboost_amd import synthetic
+from hessboost_amd._capi import LOSS_LOGISTIC
 from oracle import oracle as O
 from tests.helpers import four_features, load_saved_models, train_labels
 
@@ -205,3 +206,46 @@ def test_launch_shapes_give_identical_trees(env):
         for key in a:
             assert np.array_equal(a[key], b[key]), key
     assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
+
+
+def test_pipelined_rounds_recover_rows_left_to_the_host():
+    """Rows whose logistic margin is beyond the vector kernel's range (|m| >
+    80) get their gradients from the host's scalar path. The pipelined
+    rounds find out only when a tree is read back, after the next tree was
+    queued: the guarded walks must have left the margins alone, and the
+    trees grown again from the finished gradients must equal, bit for bit,
+    those of rounds decided by the host (which finishes the gradients
+    before the root)."""
+    import os
+    rng = np.random.default_rng(11)
+    n, f = 20_000, 8
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    y = (x[:, 0] + 0.5 * x[:, 1] > 0).astype(np.float32)
+    m0 = np.zeros(n, np.float32)
+    far = rng.choice(n, 200, replace=False)
+    m0[far] = np.where(rng.random(200) < 0.5, -100.0, 100.0).astype(np.float32)
+    params = {"objective": "binary:logistic", "max_depth": 4, "eta": 0.5}
+    index = hb.DMatrix(x, label=y).index(256)
+    runs = []
+    for flag in (None, "0"):
+        old = os.environ.pop("HBROCM_DEVICE_GROW", None)
+        if flag is not None:
+            os.environ["HBROCM_DEVICE_GROW"] = flag
+        try:
+            eng = hb.Engine(index, 0)
+        finally:
+            os.environ.pop("HBROCM_DEVICE_GROW", None)
+            if old is not None:
+                os.environ["HBROCM_DEVICE_GROW"] = old
+        tr = hb.Trainer(eng, params, y)
+        eng.load_margins(m0)
+        eng.gradients(LOSS_LOGISTIC, y)  # labels back on the device after the margins
+        tr.boost(3)
+        runs.append((tr.trees(), tr.margins()))
+    (ta, ma), (tb, mb) = runs
+    assert len(ta) == len(tb) == 3
+    for a, b in zip(ta, tb):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
+    assert np.all(np.abs(ma[far]) > 80)
