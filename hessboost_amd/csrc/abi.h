@@ -164,6 +164,7 @@ struct PartArgs {
     uint32_t n_rows;
     uint32_t words;              // bitmap words per feature
     const GrowCounts *grow;      // non-null: n_splits and n_tiles are read from here
+    const uint32_t *tile_split;  // non-null: the split of every tile (else found by binary search)
 };
 
 // ---- histograms ----------------------------------------------------------------
@@ -344,6 +345,16 @@ struct GrowTreeNode {
     float gain;
 };
 
+// A finished device tree as it is read back: the scale its gradients were
+// quantized with and its counts (written by the last level's decision),
+// followed by its nodes.
+struct TreeHeader {
+    QScale scale;
+    GrowCounts counts;
+};
+constexpr uint32_t kTreeHeaderBytes = 128;
+static_assert(sizeof(TreeHeader) <= kTreeHeaderBytes, "tree header");
+
 // The decision of one level: every frontier node's winner becomes a split
 // (children appended to the tree, partition/histogram/scan records of the
 // level written) or a leaf (final value written).
@@ -359,7 +370,9 @@ struct GrowArgs {
     PartSplit *splits;            // this level's splits, built children and children's scan nodes
     HistNode *hnodes;
     ScanNode *snodes;
+    uint32_t *tile_split;         // the split owning each of the level's partition tiles
     GrowTreeNode *tree;
+    TreeHeader *header;           // written by the last level (terminal) with the final counts
     const uint32_t *feature_offset;
     const int8_t *monotone;       // per feature, or null
     uint32_t n_monotone;

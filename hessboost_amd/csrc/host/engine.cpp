@@ -64,13 +64,21 @@ Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) 
         if (w >= 1 && w <= 64) hist_waves = (uint32_t)w;
     }
     upload_index(desc);
-    block_.resize(kTreeAt + kMaxDeviceNodes * sizeof(GrowTreeNode));
+    block_.resize(kBlockBytes);
 }
 
 Engine::~Engine() {
     try {
         dev_.activate();
         dev_.sync();
+        if (copy_stream_) {
+            (void)hipStreamSynchronize(copy_stream_);
+            for (uint32_t r = 0; r < kTreeRing; r++) {
+                (void)hipEventDestroy(tree_ready_[r]);
+                (void)hipEventDestroy(tree_copied_[r]);
+            }
+            (void)hipStreamDestroy(copy_stream_);
+        }
     } catch (...) {
     }
 }
@@ -899,12 +907,25 @@ Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, f
     d_best_.reserve(2 * pmax_all);
     d_tile_left_.reserve(row_tiles + pmax_all);
     d_decisions_.reserve((size_t)(row_tiles + pmax_all) * (kPartTile / 64));
+    d_tile_split_.reserve(row_tiles + pmax_all);
     GrowCounts *counts = grow_counts_dev();
 
+    if (!copy_stream_) {
+        HBR_HIP(hipStreamCreate(&copy_stream_));
+        d_tree_ring_.resize(kTreeRing * ring_bytes());
+        for (uint32_t r = 0; r < kTreeRing; r++) {
+            HBR_HIP(hipEventCreateWithFlags(&tree_ready_[r], hipEventDisableTiming));
+            HBR_HIP(hipEventCreateWithFlags(&tree_copied_[r], hipEventDisableTiming));
+        }
+    }
     TreeTicket t;
-    t.slot = tree_seq_++ & 1u;
+    t.slot = tree_seq_++ % kTreeRing;
     t.check = !scale_checked_;
     scale_checked_ = true;
+    last_ring_ = t.slot;
+    // the slot's previous tree must have been read back before it is overwritten
+    if (ring_used_[t.slot]) HBR_HIP(hipStreamWaitEvent(s, tree_copied_[t.slot], 0));
+    ring_used_[t.slot] = true;
     launch_device_root();
     for (uint32_t lv = 0; lv < depth; lv++) {
         const bool terminal = lv + 1 >= depth;
@@ -921,7 +942,9 @@ Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, f
         g.splits = g_splits_[lv & 1].get();
         g.hnodes = d_hnodes_.get();
         g.snodes = d_snodes_.get();
-        g.tree = grow_tree_dev();
+        g.tile_split = d_tile_split_.get();
+        g.tree = ring_nodes(t.slot);
+        g.header = ring_header(t.slot);
         g.feature_offset = d_fo_.get();
         g.monotone = has_monotone_ ? monotone_.get() : nullptr;
         g.n_monotone = has_monotone_ ? n_cols_ : 0u;
@@ -943,6 +966,7 @@ Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, f
         a.n_tiles = row_tiles + pmax;
         a.out = g_pout_[lv & 1].get();
         a.grow = counts;
+        a.tile_split = d_tile_split_.get();
         dev_.launch("hbr_part_count", dim3(a.n_tiles), dim3(kPartThreads), a);
         dev_.launch("hbr_part_scan", dim3(pmax), dim3(1024), a);
         dev_.launch("hbr_part_scatter", dim3(a.n_tiles), dim3(kPartThreads), a);
@@ -951,41 +975,42 @@ Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, f
     }
     // every level's scatter wrote into the other buffer
     identity_rows0_ = false;
-    // the scale, counts and nodes back in one copy
-    const size_t bytes = kTreeAt + kMaxDeviceNodes * sizeof(GrowTreeNode);
-    void *host = tree_stage_[t.slot].reserve(bytes);
-    if (!tree_done_[t.slot]) HBR_HIP(hipEventCreate(&tree_done_[t.slot]));
+    // the header and nodes back in one copy, on the copy stream
+    void *host = tree_stage_[t.slot].reserve(ring_bytes());
     const size_t n_max = (size_t(2) << depth) - 1;
-    HBR_HIP(hipMemcpyAsync(host, block_.get(), kTreeAt + n_max * sizeof(GrowTreeNode), hipMemcpyDeviceToHost, s));
-    HBR_HIP(hipEventRecord(tree_done_[t.slot], s));
+    HBR_HIP(hipEventRecord(tree_ready_[t.slot], s));
+    HBR_HIP(hipStreamWaitEvent(copy_stream_, tree_ready_[t.slot], 0));
+    HBR_HIP(hipMemcpyAsync(host, ring_header(t.slot), kTreeHeaderBytes + n_max * sizeof(GrowTreeNode),
+                           hipMemcpyDeviceToHost, copy_stream_));
+    HBR_HIP(hipEventRecord(tree_copied_[t.slot], copy_stream_));
     return t;
 }
 
 Engine::TreeState Engine::finish_device_tree(const TreeTicket &t, std::vector<GrowTreeNode> &nodes, QScale *scale) {
-    HBR_HIP(hipEventSynchronize(tree_done_[t.slot]));
+    HBR_HIP(hipEventSynchronize(tree_copied_[t.slot]));
     const uint8_t *host = static_cast<const uint8_t *>(tree_stage_[t.slot].get());
-    RootBlock rb;
-    GrowCounts gc;
-    std::memcpy(&rb, host, sizeof(rb));
-    std::memcpy(&gc, host + kCountsAt, sizeof(gc));
+    TreeHeader th;
+    std::memcpy(&th, host, sizeof(th));
+    const GrowCounts &gc = th.counts;
     if (gc.error) fail(kInvalid, "device growth: a level needed more histogram slots than reserved");
     if (gc.n_nodes == 0 || gc.n_nodes > kMaxDeviceNodes) fail(kInvalid, "device growth: node count out of range");
     nodes.resize(gc.n_nodes);
-    std::memcpy(nodes.data(), host + kTreeAt, gc.n_nodes * sizeof(GrowTreeNode));
+    std::memcpy(nodes.data(), host + kTreeHeaderBytes, gc.n_nodes * sizeof(GrowTreeNode));
     // (the root's histogram was counted when it was queued)
     counters.hist_nodes += gc.hist_nodes - 1;
     counters.hist_rows += gc.hist_rows;
     counters.hist_bytes += hist_bytes(gc.hist_rows, true);
     counters.partition_rows += gc.part_rows;
-    if (scale) *scale = rb.scale;
+    if (scale) *scale = th.scale;
     if (!t.check) return kTreeOk;
-    if (rb.scale.scalar_rows != 0 || rb.scale.nonfinite != 0) return kTreeNeedsHost;
-    scale_host_ = rb.scale;
+    if (th.scale.scalar_rows != 0 || th.scale.nonfinite != 0) return kTreeNeedsHost;
+    scale_host_ = th.scale;
     return kTreeOk;
 }
 
 bool Engine::recover_gradients(const QScale &scale) {
     dev_.sync();
+    if (copy_stream_) HBR_HIP(hipStreamSynchronize(copy_stream_));
     stage_.reset();
     scale_checked_ = true;
     if (!finish_gradients_on_host(scale)) return false;
@@ -1012,8 +1037,8 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss)
     if (output >= outputs_) fail(kInvalid, "walk: no such output");
     hipStream_t s = dev_.stream();
     WalkArgs a{};
-    a.tree = grow_tree_dev();
-    a.counts = grow_counts_dev();
+    a.tree = ring_nodes(last_ring_);
+    a.counts = &ring_header(last_ring_)->counts;
     a.bins8 = rows8_.get();
     a.margins = margins_.get();
     a.stride = stride_;

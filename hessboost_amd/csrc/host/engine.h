@@ -179,11 +179,25 @@ private:
     // uploaded once
     void launch_device_root();
     DBuf<uint8_t> d_root_in_;
-    // device-grown trees in flight: pinned readbacks and their events; the
-    // guarded walk's saved scale and skip flag
-    PinnedBuf tree_stage_[2];
-    hipEvent_t tree_done_[2] = {nullptr, nullptr};
-    uint32_t tree_seq_ = 0;
+    // Device-grown trees in flight: each is written into a ring slot in
+    // device memory and read back on a copy stream (the growth stream never
+    // waits for a readback); pinned readbacks and their events. The guarded
+    // walk's saved scale and skip flag.
+    static constexpr uint32_t kTreeRing = 3;
+    static constexpr size_t ring_bytes() { return kTreeHeaderBytes + kMaxDeviceNodes * sizeof(GrowTreeNode); }
+    DBuf<uint8_t> d_tree_ring_;
+    PinnedBuf tree_stage_[kTreeRing];
+    hipEvent_t tree_ready_[kTreeRing] = {};
+    hipEvent_t tree_copied_[kTreeRing] = {};
+    bool ring_used_[kTreeRing] = {};
+    hipStream_t copy_stream_ = nullptr;
+    uint32_t tree_seq_ = 0, last_ring_ = 0;
+    TreeHeader *ring_header(uint32_t r) const {
+        return reinterpret_cast<TreeHeader *>(d_tree_ring_.get() + r * ring_bytes());
+    }
+    GrowTreeNode *ring_nodes(uint32_t r) const {
+        return reinterpret_cast<GrowTreeNode *>(d_tree_ring_.get() + r * ring_bytes() + kTreeHeaderBytes);
+    }
     DBuf<QScale> guard_scale_;
     DBuf<uint32_t> poison_;
     std::vector<int8_t> monotone_host_;
@@ -223,18 +237,16 @@ private:
         QBin total;
         ScanBest best;
     };
-    // followed by a device-grown tree's counts and nodes, so that the tree's
-    // one synchronisation reads back everything with one copy
+    // followed by the level counts of the device-grown tree being grown
     DBuf<uint8_t> block_;
     static constexpr size_t kCountsAt = (sizeof(RootBlock) + 63) / 64 * 64;
-    static constexpr size_t kTreeAt = kCountsAt + (sizeof(GrowCounts) + 63) / 64 * 64;
+    static constexpr size_t kBlockBytes = kCountsAt + (sizeof(GrowCounts) + 63) / 64 * 64;
     static constexpr size_t kMaxDeviceNodes = (size_t(2) << kMaxDeviceDepth) - 1;
     RootBlock *root_block() const { return reinterpret_cast<RootBlock *>(block_.get()); }
     QScale *scale_dev() const { return &root_block()->scale; }
     QBin *total_dev() const { return &root_block()->total; }
     ScanBest *root_best_dev() const { return &root_block()->best; }
     GrowCounts *grow_counts_dev() const { return reinterpret_cast<GrowCounts *>(block_.get() + kCountsAt); }
-    GrowTreeNode *grow_tree_dev() const { return reinterpret_cast<GrowTreeNode *>(block_.get() + kTreeAt); }
     // device-grown levels: frontiers, splits and partition results, two of each
     DBuf<GrowNode> g_front_[2];
     DBuf<PartSplit> g_splits_[2];
@@ -259,7 +271,7 @@ private:
     // per-call scratch
     Stage stage_;
     DBuf<PartSplit> d_splits_;
-    DBuf<uint32_t> d_tile_left_, d_slots_;
+    DBuf<uint32_t> d_tile_left_, d_slots_, d_tile_split_;
     DBuf<uint8_t> d_level_in_, d_level_out_;  // one level's records (bytes)
     DBuf<HistNode> d_hnodes_;
     DBuf<HistTile> d_htiles_;

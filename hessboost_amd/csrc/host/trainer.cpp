@@ -480,7 +480,7 @@ void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
     std::deque<Engine::TreeTicket> inflight;
     uint64_t queued = 0, done = 0;
     while (done < rounds) {
-        while (queued < rounds && inflight.size() < 2) {
+        while (queued < rounds && inflight.size() < 3) {
             if (!grads_ready_) e_.compute_gradients_async(loss, 0);
             inflight.push_back(b.queue_device());
             e_.walk_device_tree(0, &loss);

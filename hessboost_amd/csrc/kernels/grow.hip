@@ -52,6 +52,7 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
     __shared__ uint32_t s_used[kGrowSlotWords];   // slots of splitting parents
     __shared__ uint32_t s_free[kGrowMaxSlots];    // the other slots, ascending
     __shared__ uint32_t s_fo[kGrowLdsOffsets + 1];
+    __shared__ uint32_t s_tile_begin[kGrowMaxSlots / 2];  // first tile of each split
     const uint32_t tid = threadIdx.x;
     const bool fo_lds = a.n_features <= kGrowLdsOffsets;
     if (fo_lds)
@@ -240,6 +241,7 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
                 p.tile_begin = tile_begin;
                 p.parent_slot = slot;
                 a.splits[i] = p;
+                s_tile_begin[i] = tile_begin;
                 HistNode h{};
                 h.from_split = 1;
                 h.split = i;
@@ -275,6 +277,19 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
             a.splits[i].fresh_slot = slot;
             a.hnodes[i].slot = slot;
         }
+        // the split of every partition tile: the last split whose first tile
+        // is at or before it (a split's tiles are contiguous)
+        if (a.tile_split && n_splits > 0) {
+            for (uint32_t t = tid; t < tile_carry; t += kGrowThreads) {
+                uint32_t lo = 0, hi = n_splits;
+                while (hi - lo > 1) {
+                    const uint32_t mid = (lo + hi) / 2;
+                    if (s_tile_begin[mid] <= t) lo = mid;
+                    else hi = mid;
+                }
+                a.tile_split[t] = lo;
+            }
+        }
         if (tid == 0) {
             GrowCounts c = c0;
             c.n_front = n_splits * 2;
@@ -306,5 +321,11 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
         }
         a.counts->hist_rows = c0.hist_rows + hr;
         a.counts->part_rows = c0.part_rows + pr;
+        if (a.terminal && a.header) {
+            TreeHeader h;
+            h.scale = *a.scale;
+            h.counts = *a.counts;
+            *a.header = h;
+        }
     }
 }

@@ -39,6 +39,7 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
 // The split owning a tile: the last split whose first tile is at or before
 // it (a split without rows shares its first tile with the next split).
 __device__ __forceinline__ uint32_t split_of_tile(const PartArgs &a, uint32_t n_splits, uint32_t tile) {
+    if (a.tile_split) return a.tile_split[tile];
     uint32_t lo = 0, hi = n_splits;
     while (hi - lo > 1) {
         const uint32_t mid = (lo + hi) / 2;
@@ -56,8 +57,34 @@ __device__ __forceinline__ uint32_t part_tiles(const PartArgs &a) { return a.gro
 
 using namespace hbr;
 
-// Every load of the tile is issued before the first store, so the wave's
-// eight row-id loads and routing gathers are in flight together.
+// The routing bytes of a thread's rows, all loads issued before the first
+// is used (a dense index with u8 columns; rows past the segment read
+// nothing and route right).
+template <bool MISSING>
+__device__ __forceinline__ void route_dense8(const PartArgs &a, const PartSplit &sp, const uint32_t (&r)[kRowsPerThread],
+                                             bool (&left)[kRowsPerThread]) {
+    const uint8_t *col = a.cols8 + (size_t)sp.feature * a.n_rows;
+    uint32_t b[kRowsPerThread];
+#pragma unroll
+    for (uint32_t k = 0; k < kRowsPerThread; k++) b[k] = r[k] != 0xffffffffu ? (uint32_t)col[r[k]] : 0xffffffffu;
+    uint64_t w[kRowsPerThread];
+    if constexpr (MISSING) {
+        const uint64_t *bits = a.missing + (size_t)sp.feature * a.words;
+#pragma unroll
+        for (uint32_t k = 0; k < kRowsPerThread; k++) w[k] = r[k] != 0xffffffffu ? bits[r[k] >> 6] : 0ull;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kRowsPerThread; k++) {
+        bool l = b[k] < sp.limit;
+        if constexpr (MISSING) {
+            if ((w[k] >> (r[k] & 63u)) & 1ull) l = sp.default_left != 0;
+        }
+        left[k] = r[k] != 0xffffffffu && l;
+    }
+}
+
+// Count pass: each wave's 64-row ballots of "goes left" and the tile's left
+// count. The row ids, then the routing bytes, are loaded eight at a time.
 extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
     __shared__ uint32_t wave_count[kPartThreads / kWave];
     const uint32_t tile = blockIdx.x;
@@ -72,9 +99,17 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
         const uint32_t j = base + (k * (kPartThreads / kWave) + wave) * kWave + lane_id();
         r[k] = j < sp.seg.len ? (sp.identity ? sp.seg.offset + j : src[j]) : 0xffffffffu;
     }
+    bool left[kRowsPerThread];
+    if (a.dense && a.cols8) {
+        if (a.missing) route_dense8<true>(a, sp, r, left);
+        else route_dense8<false>(a, sp, r, left);
+    } else {
+#pragma unroll
+        for (uint32_t k = 0; k < kRowsPerThread; k++) left[k] = r[k] != 0xffffffffu && goes_left(a, sp, r[k]);
+    }
     uint64_t m[kRowsPerThread];
 #pragma unroll
-    for (uint32_t k = 0; k < kRowsPerThread; k++) m[k] = __ballot(r[k] != 0xffffffffu && goes_left(a, sp, r[k]));
+    for (uint32_t k = 0; k < kRowsPerThread; k++) m[k] = __ballot(left[k]);
     uint64_t *dec = a.decisions + (size_t)tile * kBallots;
     uint32_t cnt = 0;
 #pragma unroll
@@ -116,8 +151,10 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_part_scan(PartArgs a) {
     }
 }
 
-// Every wave walks the tile's ballots in row order, keeping the count of
-// left rows before the current ballot; it moves the rows of its own ballots.
+// Scatter pass: lanes 0..31 of every wave load the tile's 32 ballots at
+// once and scan their left counts; each wave then moves the rows of its own
+// eight ballots (row ids loaded together), left rows to the left child's
+// run and right rows to the right child's, both in row order.
 extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     const uint32_t tile = blockIdx.x;
     if (tile >= part_tiles(a)) return;
@@ -132,23 +169,37 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     const uint64_t *dec = a.decisions + (size_t)tile * kBallots;
     const uint32_t wave = threadIdx.x / kWave, lane = lane_id();
     const uint64_t below = (1ull << lane) - 1ull;
-    uint32_t run = 0;  // left rows of the ballots before q
-    for (uint32_t q = 0; q < kBallots; q++) {
-        const uint64_t m = dec[q];
-        if (q % (kPartThreads / kWave) == wave) {
-            const uint32_t j = tile_pos + q * kWave + lane;
-            if (j < sp.seg.len) {
-                const uint32_t r = sp.identity ? sp.seg.offset + j : src[j];
-                if ((m >> lane) & 1ull) {
-                    dst[left_before + run + (uint32_t)__popcll(m & below)] = r;
-                } else {
-                    // every row before j in the tile exists: q*64 + lane rows
-                    const uint32_t rights = q * kWave - run + (uint32_t)__popcll(~m & below);
-                    dst[left_len + right_before + rights] = r;
-                }
-            }
+    // ballot q sits in lane q; its left rows and the left rows before it
+    const uint64_t mine = lane < kBallots ? dec[lane] : 0ull;
+    const uint32_t cnt = (uint32_t)__popcll(mine);
+    uint32_t incl = cnt;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t t = __shfl_up(incl, d, kWave);
+        if (lane >= (uint32_t)d) incl += t;
+    }
+    const uint32_t excl = incl - cnt;
+    uint32_t r[kRowsPerThread];
+#pragma unroll
+    for (uint32_t k = 0; k < kRowsPerThread; k++) {
+        const uint32_t q = k * (kPartThreads / kWave) + wave;
+        const uint32_t j = tile_pos + q * kWave + lane;
+        r[k] = j < sp.seg.len ? (sp.identity ? sp.seg.offset + j : src[j]) : 0xffffffffu;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kRowsPerThread; k++) {
+        const uint32_t q = k * (kPartThreads / kWave) + wave;
+        const uint64_t m = (uint64_t)(uint32_t)__shfl((int)(uint32_t)mine, q, kWave) |
+                           ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(mine >> 32), q, kWave) << 32);
+        const uint32_t run = (uint32_t)__shfl((int)excl, q, kWave);  // left rows of the ballots before q
+        if (r[k] == 0xffffffffu) continue;
+        if ((m >> lane) & 1ull) {
+            dst[left_before + run + (uint32_t)__popcll(m & below)] = r[k];
+        } else {
+            // every row before this one in the tile exists: q*64 + lane rows
+            const uint32_t rights = q * kWave - run + (uint32_t)__popcll(~m & below);
+            dst[left_len + right_before + rights] = r[k];
         }
-        run += (uint32_t)__popcll(m);
     }
 }
 
