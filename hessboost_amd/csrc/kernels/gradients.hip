@@ -71,14 +71,13 @@ using namespace hbr;
 
 namespace hbr {
 
-// Row i's gradient pair from margin m (all lanes of the wave call it
-// together: the logistic vector test is a ballot over 8-row groups). Rows
-// the vector kernel does not cover are listed for the host.
-__device__ __forceinline__ void row_gradient(const GradArgs &a, uint32_t i, bool active, float m, uint32_t &mg,
-                                             uint32_t &mh, uint32_t &bad) {
+// Row i's gradient pair from margin m, label y and weight w (all lanes of
+// the wave call it together: the logistic vector test is a ballot over
+// 8-row groups). Rows the vector kernel does not cover are listed for the
+// host.
+__device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, bool active, float m, float y, float w,
+                                                uint32_t &mg, uint32_t &mh, uint32_t &bad) {
     {
-        float y = active ? a.labels[i] : 0.0f;
-        float w = (active && a.weights) ? a.weights[i] : 1.0f;
         float g = 0.0f, h = 0.0f;
         bool host_row = false;
         if (a.loss == kSquaredError) {
@@ -117,6 +116,13 @@ __device__ __forceinline__ void row_gradient(const GradArgs &a, uint32_t i, bool
             }
         }
     }
+}
+
+__device__ __forceinline__ void row_gradient(const GradArgs &a, uint32_t i, bool active, float m, uint32_t &mg,
+                                             uint32_t &mh, uint32_t &bad) {
+    const float y = active ? a.labels[i] : 0.0f;
+    const float w = (active && a.weights) ? a.weights[i] : 1.0f;
+    row_gradient_yw(a, i, active, m, y, w, mg, mh, bad);
 }
 
 }  // namespace hbr

@@ -261,53 +261,110 @@ __device__ __forceinline__ void load_walk_table(const WalkArgs &a, uint32_t n_no
     }
 }
 
-// The walk for 32-byte rows and trees of at most kWalkLdsNodes nodes: the
-// node table sits in LDS, and each thread copies its row's 32 bins into its
-// own LDS slot with two 16-byte loads, then reads the bytes it routes on
-// from there (one coalesced row read instead of one byte load per level).
+// The walks for 32-byte rows and trees of at most kWalkLdsNodes nodes: the
+// node table sits in LDS as (meta, left) pairs, and each thread walks
+// kWalkRows rows per pass with every memory load of the pass issued before
+// the first walk (a row's 32 bins in eight registers, its margin, label and
+// weight); the routing byte is picked out of the registers.
 constexpr uint32_t kWalkLdsNodes = 1024;
+constexpr uint32_t kWalkRows = 4;
+
+__device__ __forceinline__ uint32_t pick_byte(const uint32_t (&w)[8], uint32_t f) {
+    // bit blends rather than selects on the array (which the compiler would
+    // turn into a dynamically indexed scratch read)
+    const uint32_t m4 = (f & 16u) ? ~0u : 0u, m2 = (f & 8u) ? ~0u : 0u, m1 = (f & 4u) ? ~0u : 0u;
+    const uint32_t a0 = w[0] ^ ((w[0] ^ w[4]) & m4), a1 = w[1] ^ ((w[1] ^ w[5]) & m4);
+    const uint32_t a2 = w[2] ^ ((w[2] ^ w[6]) & m4), a3 = w[3] ^ ((w[3] ^ w[7]) & m4);
+    const uint32_t b0 = a0 ^ ((a0 ^ a2) & m2), b1 = a1 ^ ((a1 ^ a3) & m2);
+    const uint32_t c = b0 ^ ((b0 ^ b1) & m1);
+    return (c >> ((f & 3u) * 8u)) & 0xffu;
+}
+
+__device__ __forceinline__ uint32_t load_walk_nodes(const WalkArgs &a, uint2 *s_node, float *s_value) {
+    const uint32_t n_nodes = min(walk_nodes(a), kWalkLdsNodes);
+    for (uint32_t i = threadIdx.x; i < n_nodes; i += blockDim.x) {
+        uint32_t meta, left;
+        float value;
+        if (a.tree) {
+            const GrowTreeNode t = a.tree[i];
+            meta = t.left < 0 ? 1u << 31 : t.feature | (t.limit << 16);
+            left = t.left < 0 ? 0u : (uint32_t)t.left;
+            value = t.value;
+        } else {
+            meta = a.meta[i];
+            left = a.left[i];
+            value = a.value[i];
+        }
+        s_node[i] = make_uint2(meta, left);
+        s_value[i] = value;
+    }
+    return n_nodes;
+}
+
+// The leaf a row reaches (n_nodes steps at most; -1 when no leaf is reached).
+__device__ __forceinline__ int32_t walk_row(const uint2 *s_node, uint32_t n_nodes, const uint32_t (&w)[8]) {
+    uint32_t nid = 0;
+    uint2 nd = s_node[0];
+    for (uint32_t step = 0; step < n_nodes && !(nd.x >> 31); step++) {
+        const uint32_t f = nd.x & 31u, lim = (nd.x >> 16) & 0x7fffu;
+        nid = nd.y + (pick_byte(w, f) < lim ? 0u : 1u);
+        nid = nid < n_nodes ? nid : 0u;
+        nd = s_node[nid];
+    }
+    return (nd.x >> 31) ? (int32_t)nid : -1;
+}
+
+__device__ __forceinline__ void load_row_bins(const WalkArgs &a, uint32_t r, uint32_t (&w)[8]) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(a.bins8 + (size_t)r * 32u);
+    const uint4 x = src[0], y = src[1];
+    w[0] = x.x;
+    w[1] = x.y;
+    w[2] = x.z;
+    w[3] = x.w;
+    w[4] = y.x;
+    w[5] = y.y;
+    w[6] = y.z;
+    w[7] = y.w;
+}
 
 extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves32(WalkArgs a) {
-    __shared__ uint32_t s_meta[kWalkLdsNodes];
-    __shared__ uint32_t s_left[kWalkLdsNodes];
+    __shared__ uint2 s_node[kWalkLdsNodes];
     __shared__ float s_value[kWalkLdsNodes];
-    __shared__ uint2 s_rows[256 * 5];  // 40 bytes per thread: 32 bins + pad
-    const uint32_t n_nodes = min(walk_nodes(a), kWalkLdsNodes);
-    load_walk_table(a, n_nodes, s_meta, s_left, s_value);
+    const uint32_t n_nodes = load_walk_nodes(a, s_node, s_value);
     __syncthreads();
-    uint2 *mine = s_rows + threadIdx.x * 5;
-    const uint8_t *bins = reinterpret_cast<const uint8_t *>(mine);
-    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += gridDim.x * blockDim.x) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.bins8 + (size_t)r * 32u);
-        const uint4 x = src[0], y = src[1];
-        mine[0] = make_uint2(x.x, x.y);
-        mine[1] = make_uint2(x.z, x.w);
-        mine[2] = make_uint2(y.x, y.y);
-        mine[3] = make_uint2(y.z, y.w);
-        uint32_t nid = 0, meta = s_meta[0];
-        for (uint32_t step = 0; step < n_nodes && !(meta >> 31); step++) {
-            const uint32_t f = meta & 31u, lim = (meta >> 16) & 0x7fffu;
-            nid = s_left[nid] + ((uint32_t)bins[f] < lim ? 0u : 1u);
-            nid = nid < n_nodes ? nid : 0u;
-            meta = s_meta[nid];
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t r0 = blockIdx.x * blockDim.x + threadIdx.x; r0 < a.n; r0 += kWalkRows * stride) {
+        uint32_t w[kWalkRows][8];
+        float m[kWalkRows];
+#pragma unroll
+        for (uint32_t k = 0; k < kWalkRows; k++) {
+            const uint32_t r = r0 + k * stride;
+            if (r < a.n) {
+                load_row_bins(a, r, w[k]);
+                m[k] = a.margins[(size_t)r * a.m_stride + a.output];
+            }
         }
-        if (meta >> 31) {
-            float *m = a.margins + (size_t)r * a.m_stride + a.output;
-            *m = *m + s_value[nid];
+#pragma unroll
+        for (uint32_t k = 0; k < kWalkRows; k++) {
+            const uint32_t r = r0 + k * stride;
+            if (r >= a.n) continue;
+            const int32_t leaf = walk_row(s_node, n_nodes, w[k]);
+            if (leaf >= 0) a.margins[(size_t)r * a.m_stride + a.output] = m[k] + s_value[leaf];
         }
     }
 }
 
-// hbr_walk_leaves32 and, for the same row while its updated margin is in
-// registers, the next round's gradient pair (row_gradient: the gradient
-// kernel's arithmetic, its 8-row vector test and its max fold). Whole waves
-// stay in the loop past the last row, as in hbr_gradients.
+// hbr_walk_leaves32 and, for the same rows while their updated margins are
+// in registers, the next round's gradient pairs (row_gradient_yw: the
+// gradient kernel's arithmetic, its 8-row vector test and its max fold).
+// The rows of a wave are 64 consecutive rows (the strides are multiples of
+// 64), and whole waves stay in the loop past the last row, as in
+// hbr_gradients.
 extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs args) {
     const WalkArgs &a = args.w;
-    __shared__ uint32_t s_meta[kWalkLdsNodes];
-    __shared__ uint32_t s_left[kWalkLdsNodes];
+    const GradArgs &ga = args.g;
+    __shared__ uint2 s_node[kWalkLdsNodes];
     __shared__ float s_value[kWalkLdsNodes];
-    __shared__ uint2 s_rows[256 * 5];
     if (a.guard) {  // uniform: every workgroup reads the same words
         const QScale q = *a.guard;
         if (q.scalar_rows != 0 || q.nonfinite != 0 || *a.poison != 0) {
@@ -315,38 +372,40 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
             return;
         }
     }
-    const uint32_t n_nodes = min(walk_nodes(a), kWalkLdsNodes);
-    load_walk_table(a, n_nodes, s_meta, s_left, s_value);
+    const uint32_t n_nodes = load_walk_nodes(a, s_node, s_value);
     __syncthreads();
-    uint2 *mine = s_rows + threadIdx.x * 5;
-    const uint8_t *bins = reinterpret_cast<const uint8_t *>(mine);
     uint32_t mg = 0, mh = 0, bad = 0;
     const uint32_t end = (a.n + kWave - 1) / kWave * kWave;
-    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < end; r += gridDim.x * blockDim.x) {
-        const bool active = r < a.n;
-        float m = 0.0f;
-        if (active) {
-            const uint4 *src = reinterpret_cast<const uint4 *>(a.bins8 + (size_t)r * 32u);
-            const uint4 x = src[0], y = src[1];
-            mine[0] = make_uint2(x.x, x.y);
-            mine[1] = make_uint2(x.z, x.w);
-            mine[2] = make_uint2(y.x, y.y);
-            mine[3] = make_uint2(y.z, y.w);
-            uint32_t nid = 0, meta = s_meta[0];
-            for (uint32_t step = 0; step < n_nodes && !(meta >> 31); step++) {
-                const uint32_t f = meta & 31u, lim = (meta >> 16) & 0x7fffu;
-                nid = s_left[nid] + ((uint32_t)bins[f] < lim ? 0u : 1u);
-                nid = nid < n_nodes ? nid : 0u;
-                meta = s_meta[nid];
-            }
-            float *mp = a.margins + (size_t)r * a.m_stride + a.output;
-            m = *mp;
-            if (meta >> 31) {
-                m = m + s_value[nid];
-                *mp = m;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t r0 = blockIdx.x * blockDim.x + threadIdx.x; r0 < end; r0 += kWalkRows * stride) {
+        uint32_t w[kWalkRows][8];
+        float m[kWalkRows], y[kWalkRows], wt[kWalkRows];
+#pragma unroll
+        for (uint32_t k = 0; k < kWalkRows; k++) {
+            const uint32_t r = r0 + k * stride;
+            m[k] = 0.0f;
+            y[k] = 0.0f;
+            wt[k] = 1.0f;
+            if (r < a.n) {
+                load_row_bins(a, r, w[k]);
+                m[k] = a.margins[(size_t)r * a.m_stride + a.output];
+                y[k] = ga.labels[r];
+                if (ga.weights) wt[k] = ga.weights[r];
             }
         }
-        row_gradient(args.g, r, active, m, mg, mh, bad);
+#pragma unroll
+        for (uint32_t k = 0; k < kWalkRows; k++) {
+            const uint32_t r = r0 + k * stride;
+            const bool active = r < a.n;
+            if (active) {
+                const int32_t leaf = walk_row(s_node, n_nodes, w[k]);
+                if (leaf >= 0) {
+                    m[k] = m[k] + s_value[leaf];
+                    a.margins[(size_t)r * a.m_stride + a.output] = m[k];
+                }
+            }
+            if (r < end) row_gradient_yw(ga, r, active, m[k], y[k], wt[k], mg, mh, bad);
+        }
     }
-    fold_block(args.g.scale, mg, mh, bad);
+    fold_block(ga.scale, mg, mh, bad);
 }
