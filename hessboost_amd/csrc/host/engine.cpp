@@ -59,6 +59,10 @@ Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) 
     }
     if (const char *v = std::getenv("HBROCM_HIST_BIN_MAJOR")) hist_bin_major = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_WALK_BLOCKS")) {
+        const long b = std::strtol(v, nullptr, 10);
+        if (b >= 1 && b <= 64) walk_blocks_per_cu = (uint32_t)b;
+    }
     if (const char *v = std::getenv("HBROCM_HIST_WAVES")) {
         const long w = std::strtol(v, nullptr, 10);
         if (w >= 1 && w <= 64) hist_waves = (uint32_t)w;
@@ -1046,7 +1050,7 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss)
     a.m_stride = outputs_;
     a.output = output;
     const uint32_t blocks =
-        std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)), (uint32_t)dev_.cu_count() * 8);
+        std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)), (uint32_t)dev_.cu_count() * walk_blocks_per_cu);
     if (!next_loss) {
         dev_.launch("hbr_walk_leaves32", dim3(blocks), dim3(256), a);
         return;

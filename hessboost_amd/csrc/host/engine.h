@@ -293,6 +293,7 @@ public:
     uint32_t hist_waves = 1;
     bool hist_bin_major = true;  // [bin][feature] LDS layout (16 and 32 feature groups)
     bool device_grow = true;     // depthwise trees decided on the device where eligible
+    uint32_t walk_blocks_per_cu = 4;  // workgroups per CU of the device-tree margin walk (one resident wave)
 };
 
 }  // namespace hbr

@@ -267,7 +267,7 @@ __device__ __forceinline__ void load_walk_table(const WalkArgs &a, uint32_t n_no
 // the first walk (a row's 32 bins in eight registers, its margin, label and
 // weight); the routing byte is picked out of the registers.
 constexpr uint32_t kWalkLdsNodes = 1024;
-constexpr uint32_t kWalkRows = 4;
+constexpr uint32_t kWalkRows = 8;
 
 __device__ __forceinline__ uint32_t pick_byte(const uint32_t (&w)[8], uint32_t f) {
     // bit blends rather than selects on the array (which the compiler would
