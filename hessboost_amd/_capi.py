@@ -39,6 +39,12 @@ class IndexDesc(C.Structure):
                 ("col_bin_width", C.c_uint32), ("pad", C.c_uint32), ("missing", u64p)]
 
 
+class IndexInfo(C.Structure):
+    _fields_ = [("dense", C.c_uint32), ("dense_u8", C.c_uint32), ("has_cols", C.c_uint32),
+                ("has_missing", C.c_uint32), ("stride", C.c_uint32), ("pad", C.c_uint32),
+                ("entries", C.c_uint64)]
+
+
 class Segment(C.Structure):
     _fields_ = [("offset", C.c_uint64), ("len", C.c_uint64), ("buffer", C.c_uint32),
                 ("contiguous", C.c_uint32), ("tree", C.c_uint64)]
@@ -116,6 +122,11 @@ SIGNATURES = {
     "hbr_index_describe": (C.c_int, [C.c_void_p, P(IndexDesc)]),
     "hbr_engine_open": (C.c_int, [C.c_int, P(IndexDesc), P(C.c_void_p)]),
     "hbr_engine_close": (None, [C.c_void_p]),
+    "hbr_engine_open_dense": (C.c_int, [C.c_int, C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_void_p,
+                                        C.c_int, P(C.c_void_p)]),
+    "hbr_engine_index_info": (C.c_int, [C.c_void_p, P(IndexInfo)]),
+    "hbr_engine_index_read": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        C.c_void_p]),
     "hbr_prepare": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
     "hbr_build": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "hbr_begin_tree": (C.c_int, [C.c_void_p, C.c_uint64, P(Segment)]),

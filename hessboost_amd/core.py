@@ -130,6 +130,23 @@ class BinnedIndex:
         return cols, miss
 
 
+class DeviceBinnedIndex:
+    """The shape and cuts of an index binned on the device
+    (Engine.from_dense); its layouts live in the engine only."""
+
+    def __init__(self, cuts: Cuts, n_rows: int, n_cols: int):
+        self.cuts = cuts
+        self.n_rows = n_rows
+        self.n_cols = n_cols
+        self._fo, self._cv = cuts.arrays()
+
+    def feature_offset(self):
+        return self._fo.copy()
+
+    def cut_values(self):
+        return self._cv.copy()
+
+
 # ---- the device engine (HistogramBackend + RowEngine) ----------------------------------
 
 class Engine:
@@ -142,6 +159,47 @@ class Engine:
         self._h = h
         fo = index.feature_offset()
         self.total_bins = int(fo[-1])
+
+    @classmethod
+    def from_dense(cls, x, cuts: Cuts, ordinal: int = 0, missing=np.nan, n_rows=None, n_cols=None):
+        """The engine over a dense f32 matrix binned on the device against
+        `cuts` (hbr_engine_open_dense): the same index hbr_index_from_dense
+        builds on the host. `x` is a row-major numpy array, or a DeviceBuffer
+        (with n_rows and n_cols) already on this ordinal."""
+        self = cls.__new__(cls)
+        on_device = isinstance(x, DeviceBuffer)
+        if on_device:
+            ptr, n, f = C.c_void_p(x.ptr), int(n_rows), int(n_cols)
+        else:
+            x = np.ascontiguousarray(x, np.float32)
+            n, f = x.shape
+            ptr = A.ptr(x)
+        h = C.c_void_p()
+        A.check(A.lib().hbr_engine_open_dense(ordinal, ptr, n, f, float(missing), cuts._h, 1 if on_device else 0,
+                                              C.byref(h)))
+        self._h = h
+        self.index = DeviceBinnedIndex(cuts, n, f)
+        self.total_bins = int(self.index.feature_offset()[-1])
+        return self
+
+    def index_info(self):
+        i = A.IndexInfo()
+        A.check(A.lib().hbr_engine_index_info(self._h, C.byref(i)))
+        return {k: int(getattr(i, k)) for k in ("dense", "dense_u8", "has_cols", "has_missing", "stride", "entries")}
+
+    def read_index(self):
+        """The engine's device layouts as numpy arrays (absent ones are None)."""
+        info = self.index_info()
+        n, f = self.index.n_rows, self.index.n_cols
+        words = (n + 63) // 64
+        rows8 = np.empty((n, info["stride"]), np.uint8) if info["dense_u8"] else None
+        cols8 = np.empty((f, n), np.uint8) if info["has_cols"] else None
+        miss = np.empty(f * words, np.uint64) if info["has_missing"] else None
+        row_ptr = np.empty(n + 1, np.uint64) if not info["dense"] else None
+        gbins = np.empty(info["entries"], np.uint32) if not info["dense"] else None
+        A.check(A.lib().hbr_engine_index_read(self._h, A.ptr(rows8), A.ptr(cols8), A.ptr(miss), A.ptr(row_ptr),
+                                              A.ptr(gbins)))
+        return {"rows8": rows8, "cols8": cols8, "missing": miss, "row_ptr": row_ptr, "gbins": gbins, **info}
 
     def close(self):
         if getattr(self, "_h", None):
@@ -305,17 +363,38 @@ class DMatrix:
         self.weight = None if weight is None else np.ascontiguousarray(weight, np.float32)
         self.missing = missing
         self._index = {}
+        self._cuts = {}
+
+    def cuts(self, max_bin=256) -> Cuts:
+        """HistCuts for max_bin (src/data/quantile.rs:65-78), cached."""
+        if max_bin not in self._cuts:
+            if self.csr is not None:
+                self._cuts[max_bin] = Cuts.from_csr(*self.csr, self.n_cols, max_bin=max_bin, weights=self.weight)
+            else:
+                self._cuts[max_bin] = Cuts.from_dense(self.x, max_bin=max_bin, weights=self.weight,
+                                                      missing=self.missing)
+        return self._cuts[max_bin]
 
     def index(self, max_bin=256) -> BinnedIndex:
         """The binned index for max_bin (DMatrix::hist_index, src/data/dmatrix.rs:931), cached."""
         if max_bin not in self._index:
+            cuts = self.cuts(max_bin)
             if self.csr is not None:
-                cuts = Cuts.from_csr(*self.csr, self.n_cols, max_bin=max_bin, weights=self.weight)
                 self._index[max_bin] = BinnedIndex(cuts, csr=self.csr, n_cols=self.n_cols)
             else:
-                cuts = Cuts.from_dense(self.x, max_bin=max_bin, weights=self.weight, missing=self.missing)
                 self._index[max_bin] = BinnedIndex(cuts, x=self.x, missing=self.missing)
         return self._index[max_bin]
+
+    def engine(self, max_bin=256, ordinal=0) -> "Engine":
+        """A device engine over this matrix: a dense matrix is binned on the
+        device against the host cuts (features of at most 256 bins); CSR
+        input, or wider features, go through the host index."""
+        if self.x is not None:
+            cuts = self.cuts(max_bin)
+            fo, _ = cuts.arrays()
+            if fo.size > 1 and int(np.max(np.diff(fo))) <= 256:
+                return Engine.from_dense(self.x, cuts, ordinal, missing=self.missing)
+        return Engine(self.index(max_bin), ordinal)
 
     def dense(self):
         if self.x is not None:
@@ -512,8 +591,7 @@ def train(params: dict, dtrain: DMatrix, num_boost_round: int = 10, *, device="r
     (src/training/api.rs:228-234)."""
     if params.get("tree_method", "hist") not in ("hist", "auto"):
         raise ValueError("this backend trains tree_method=hist")
-    index = dtrain.index(params.get("max_bin", 256))
-    engine = Engine(index, _device_ordinal(device))
+    engine = dtrain.engine(params.get("max_bin", 256), _device_ordinal(device))
     t = Trainer(engine, params, dtrain.label, dtrain.weight)
     t.boost(num_boost_round)
     b = t.booster(dtrain.n_cols)

@@ -71,6 +71,56 @@ struct EncodeArgs {
     uint32_t pad;
 };
 
+// Binning on the device (HistCuts::bin_of, src/data/quantile.rs:285-296,
+// and the GHistIndex layouts, src/data/ghist.rs:213-257): a chunk of a
+// dense f32 matrix to feature-local u8 bins (features of at most 256 bins),
+// the missing bitmap and each row's count of present values. One thread per
+// row; a chunk starts at a multiple of 64 rows.
+struct BinArgs {
+    const float *x;                 // the chunk's rows, row-major [chunk_rows][n_cols]
+    const float *cut_values;        // total_bins
+    const uint32_t *feature_offset; // n_cols + 1
+    uint8_t *rows8;                 // [n_rows][stride] local bins, or null
+    uint8_t *cols8;                 // [n_cols][n_rows] local bins (0 where missing)
+    uint64_t *missing;              // [n_cols][words], bit set = missing
+    uint32_t *row_count;            // per row: present values
+    uint64_t n_rows;
+    uint64_t row0;
+    uint32_t chunk_rows;
+    uint32_t n_cols;
+    uint32_t stride;
+    uint32_t words;
+    uint32_t total_bins;
+    float missing_value;            // the absent marker (NaN: any NaN)
+    uint32_t missing_is_nan;
+    uint32_t pad;
+};
+
+// Exclusive scan of the rows' present counts into row_ptr (n_rows + 1):
+// per block of kCountBlock rows its total, then (with the blocks' offsets,
+// scanned on the host) every row's offset.
+constexpr uint32_t kCountBlock = 8192;
+struct CountScanArgs {
+    const uint32_t *row_count;
+    uint64_t *block_total;          // per block (first pass)
+    const uint64_t *block_offset;   // per block (second pass)
+    uint64_t *row_ptr;              // n_rows + 1 (second pass)
+    uint64_t n_rows;
+};
+
+// CSR global bins of the present cells, in feature order per row, from the
+// local columns and the missing bitmap.
+struct CsrFillArgs {
+    const uint8_t *cols8;
+    const uint64_t *missing;
+    const uint32_t *feature_offset;
+    const uint64_t *row_ptr;
+    uint32_t *gbins;
+    uint64_t n_rows;
+    uint32_t n_cols;
+    uint32_t words;
+};
+
 // ---- gradients ---------------------------------------------------------------
 enum LossKind : uint32_t { kSquaredError = 0, kLogistic = 1 };
 

@@ -252,6 +252,43 @@ int hbr_engine_open(int ordinal, const hbr_index_desc *index, hbr_engine **out) 
 
 void hbr_engine_close(hbr_engine *e) { delete e; }
 
+int hbr_engine_open_dense(int ordinal, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                          const hbr_cuts *cuts, int x_on_device, hbr_engine **out) {
+    return guard([&] {
+        if (!x || !cuts || !out) fail(kInvalid, "engine: null argument");
+        if (n_cols != cuts->c.n_cols()) fail(kInvalid, "engine: the cuts are for another number of features");
+        Engine::DenseSource src;
+        src.x = x;
+        src.on_device = x_on_device != 0;
+        src.n_rows = n_rows;
+        src.n_cols = n_cols;
+        src.missing = missing;
+        src.feature_offset = cuts->c.feature_offset.data();
+        src.cut_values = cuts->c.values.data();
+        auto *h = new hbr_engine;
+        try {
+            h->e = std::make_unique<Engine>(ordinal, src);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+int hbr_engine_index_info(hbr_engine *h, hbr_index_info *out) {
+    return with_engine(h, [&](Engine &e) {
+        if (!out) fail(kInvalid, "index_info: null argument");
+        const Engine::IndexInfo i = e.index_info();
+        *out = hbr_index_info{i.dense, i.dense_u8, i.has_cols, i.has_missing, i.stride, 0, i.entries};
+    });
+}
+
+int hbr_engine_index_read(hbr_engine *h, uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint64_t *row_ptr,
+                          uint32_t *gbins) {
+    return with_engine(h, [&](Engine &e) { e.read_index(rows8, cols8, missing, row_ptr, gbins); });
+}
+
 int hbr_prepare(hbr_engine *h, const float *gpair, uint64_t n) {
     return with_engine(h, [&](Engine &e) { e.prepare(gpair, n); });
 }

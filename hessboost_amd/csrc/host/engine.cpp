@@ -48,7 +48,19 @@ void logistic_scalar(float m, float y, float w, float spw, float min_hess, float
 }  // namespace
 
 Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) {
-    // launch-shape overrides for tuning sweeps (results do not depend on them)
+    read_tunables();
+    upload_index(desc);
+    block_.resize(kBlockBytes);
+}
+
+Engine::Engine(int ordinal, const DenseSource &src) : dev_(device(ordinal)) {
+    read_tunables();
+    bin_dense(src);
+    block_.resize(kBlockBytes);
+}
+
+// Launch-shape overrides for tuning sweeps (results do not depend on them).
+void Engine::read_tunables() {
     if (const char *v = std::getenv("HBROCM_HIST_FG")) {
         const long fg = std::strtol(v, nullptr, 10);
         if (fg == 8 || fg == 16 || fg == 32) hist_features_per_group = (uint32_t)fg;
@@ -67,8 +79,6 @@ Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) 
         const long w = std::strtol(v, nullptr, 10);
         if (w >= 1 && w <= 64) hist_waves = (uint32_t)w;
     }
-    upload_index(desc);
-    block_.resize(kBlockBytes);
 }
 
 Engine::~Engine() {
@@ -98,6 +108,7 @@ void Engine::upload_index(const hbr_index_desc &d) {
     total_bins_ = fo_[n_cols_];
     if (d.cut_values) cuts_.assign(d.cut_values, d.cut_values + total_bins_);
     dense_ = d.dense != 0;
+    entries_ = d.row_ptr[n_rows_];
     uint32_t widest = 0;
     for (uint32_t f = 0; f < n_cols_; f++) widest = std::max(widest, fo_[f + 1] - fo_[f]);
     hipStream_t s = dev_.stream();
@@ -173,6 +184,147 @@ void Engine::upload_index(const hbr_index_desc &d) {
             missing_.upload(d.missing, (uint64_t)words_ * n_cols_, s);
         }
     }
+    dev_.sync();
+}
+
+// The index binned on the device: one pass over the matrix writes the local
+// columns, the missing bitmap, each row's present count and (speculatively)
+// the row-major u8 rows. A matrix without absent cells is then the dense u8
+// index; otherwise the counts are scanned into row_ptr and the CSR global
+// bins are filled from the columns, and the columns and bitmap are kept when
+// cells <= 2 x entries (src/data/ghist.rs:235), as on the host.
+void Engine::bin_dense(const DenseSource &src) {
+    if (!src.x || !src.feature_offset || (!src.cut_values && src.feature_offset[src.n_cols] > 0))
+        fail(kInvalid, "binning: x, feature_offset and cut_values are required");
+    if (src.n_rows == 0 || src.n_cols == 0) fail(kInvalid, "binning: an empty matrix");
+    if (src.n_rows >= (uint64_t)UINT32_MAX) fail(kRefused, "binning: more than 2^32 - 1 rows");
+    n_rows_ = src.n_rows;
+    n_cols_ = (uint32_t)src.n_cols;
+    fo_.assign(src.feature_offset, src.feature_offset + n_cols_ + 1);
+    total_bins_ = fo_[n_cols_];
+    cuts_.assign(src.cut_values, src.cut_values + total_bins_);
+    for (uint32_t f = 0; f < n_cols_; f++) {
+        const uint32_t nb = fo_[f + 1] - fo_[f];
+        if (fo_[f + 1] < fo_[f]) fail(kInvalid, "binning: feature_offset must not decrease");
+        if (nb == 0) fail(kInvalid, "binning: a feature without bins");
+        if (nb > 256) fail(kRefused, "binning on the device: a feature with more than 256 bins");
+    }
+    hipStream_t s = dev_.stream();
+    d_fo_.resize(n_cols_ + 1);
+    d_fo_.upload(fo_.data(), n_cols_ + 1, s);
+    DBuf<float> d_cuts(total_bins_);
+    d_cuts.upload(cuts_.data(), total_bins_, s);
+    words_ = (uint32_t)((n_rows_ + 63) / 64);
+    stride_ = (n_cols_ + 31) / 32 * 32;
+    rows8_.resize(n_rows_ * stride_);
+    rows8_.zero(s);
+    cols8_.resize(n_rows_ * n_cols_);
+    missing_.resize((uint64_t)words_ * n_cols_);
+    DBuf<uint32_t> count(n_rows_);
+    // chunks of whole 64-row groups; host rows go through a staging buffer
+    const uint64_t row_bytes = n_cols_ * sizeof(float);
+    uint64_t chunk = std::max<uint64_t>(64, ((256ull << 20) / row_bytes) / 64 * 64);
+    if (src.on_device) chunk = std::min<uint64_t>(n_rows_, (uint64_t)UINT32_MAX / 2) / 64 * 64 + 64;
+    DBuf<float> staging(src.on_device ? 0 : std::min<uint64_t>(chunk, n_rows_) * n_cols_);
+    for (uint64_t r0 = 0; r0 < n_rows_; r0 += chunk) {
+        const uint64_t rows = std::min<uint64_t>(chunk, n_rows_ - r0);
+        const float *xs = src.x + r0 * n_cols_;
+        if (!src.on_device) {
+            HBR_HIP(hipMemcpyAsync(staging.get(), xs, rows * row_bytes, hipMemcpyHostToDevice, s));
+            xs = staging.get();
+        }
+        BinArgs a{};
+        a.x = xs;
+        a.cut_values = d_cuts.get();
+        a.feature_offset = d_fo_.get();
+        a.rows8 = rows8_.get();
+        a.cols8 = cols8_.get();
+        a.missing = missing_.get();
+        a.row_count = count.get();
+        a.n_rows = n_rows_;
+        a.row0 = r0;
+        a.chunk_rows = (uint32_t)rows;
+        a.n_cols = n_cols_;
+        a.stride = stride_;
+        a.words = words_;
+        a.total_bins = total_bins_;
+        a.missing_value = src.missing;
+        a.missing_is_nan = std::isnan(src.missing) ? 1u : 0u;
+        dev_.launch("hbr_bin_dense", dim3(ceil_div(rows, 256)), dim3(256), a);
+        if (!src.on_device) dev_.sync();  // the staging buffer is reused
+    }
+    // the present counts: totals per block, their offsets on the host, row_ptr
+    const uint32_t blocks = ceil_div(n_rows_, kCountBlock);
+    DBuf<uint64_t> block_total(blocks), block_offset(blocks);
+    CountScanArgs c{};
+    c.row_count = count.get();
+    c.block_total = block_total.get();
+    c.n_rows = n_rows_;
+    dev_.launch("hbr_count_blocks", dim3(blocks), dim3(1024), c);
+    std::vector<uint64_t> totals(blocks), offsets(blocks);
+    block_total.download(totals.data(), blocks, s);
+    dev_.sync();
+    uint64_t entries = 0;
+    for (uint32_t b = 0; b < blocks; b++) {
+        offsets[b] = entries;
+        entries += totals[b];
+    }
+    entries_ = entries;
+    const uint64_t cells = n_rows_ * n_cols_;
+    dense_ = entries == cells;
+    if (dense_) {
+        // the dense u8 index: row-major rows for histograms, columns for routing
+        dense_u8_ = true;
+        have_cols_ = true;
+        missing_.release();
+        dev_.sync();
+        return;
+    }
+    rows8_.release();
+    stride_ = 0;
+    block_offset.upload(offsets.data(), blocks, s);
+    row_ptr_.resize(n_rows_ + 1);
+    c.block_offset = block_offset.get();
+    c.row_ptr = row_ptr_.get();
+    dev_.launch("hbr_count_offsets", dim3(blocks), dim3(1024), c);
+    gbins_.resize(entries ? entries : 1);
+    CsrFillArgs g{};
+    g.cols8 = cols8_.get();
+    g.missing = missing_.get();
+    g.feature_offset = d_fo_.get();
+    g.row_ptr = row_ptr_.get();
+    g.gbins = gbins_.get();
+    g.n_rows = n_rows_;
+    g.n_cols = n_cols_;
+    g.words = words_;
+    dev_.launch("hbr_csr_fill", dim3(ceil_div(n_rows_, 256)), dim3(256), g);
+    dev_.sync();
+    if (cells <= 2 * entries) {
+        have_cols_ = true;
+    } else {
+        cols8_.release();
+        missing_.release();
+    }
+}
+
+Engine::IndexInfo Engine::index_info() const {
+    IndexInfo i{};
+    i.dense = dense_;
+    i.dense_u8 = dense_u8_;
+    i.has_cols = have_cols_;
+    i.has_missing = missing_.size() > 0;
+    i.stride = stride_;
+    i.entries = dense_ ? n_rows_ * n_cols_ : entries_;
+    return i;
+}
+
+void Engine::read_index(uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint64_t *row_ptr, uint32_t *gbins) {
+    hipStream_t s = dev_.stream();
+    if (rows8 && rows8_.size()) rows8_.download(rows8, rows8_.size(), s);
+    if (cols8 && cols8_.size()) cols8_.download(cols8, n_rows_ * n_cols_, s);
+    if (missing && missing_.size()) missing_.download(missing, (uint64_t)words_ * n_cols_, s);
+    if (row_ptr && row_ptr_.size()) row_ptr_.download(row_ptr, n_rows_ + 1, s);
+    if (gbins && !dense_ && gbins_.size()) gbins_.download(gbins, entries_, s);
     dev_.sync();
 }
 

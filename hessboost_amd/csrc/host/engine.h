@@ -49,6 +49,32 @@ struct ScanInput {
 class Engine {
 public:
     Engine(int ordinal, const hbr_index_desc &desc);
+    // A dense f32 matrix (row-major n_rows x n_cols, host or device memory)
+    // binned on the device against host cuts (HistCuts::bin_of,
+    // src/data/quantile.rs:285-296) into the layouts GHistIndex::from_dmatrix
+    // would give (src/data/ghist.rs:213-257). Features of at most 256 bins.
+    struct DenseSource {
+        const float *x = nullptr;
+        bool on_device = false;
+        uint64_t n_rows = 0, n_cols = 0;
+        float missing = 0.0f;
+        const uint32_t *feature_offset = nullptr;  // n_cols + 1
+        const float *cut_values = nullptr;
+    };
+    Engine(int ordinal, const DenseSource &src);
+    // The engine's index as it sits on the device (for checking): whether it
+    // is dense, its row-major stride (dense u8), stored entries, and whether
+    // it keeps local columns and a missing bitmap.
+    struct IndexInfo {
+        bool dense, dense_u8, has_cols, has_missing;
+        uint32_t stride;
+        uint64_t entries;
+    };
+    IndexInfo index_info() const;
+    // Copies of the layouts (null pointers skip one): rows8 n_rows x stride,
+    // cols8 n_cols x n_rows, missing n_cols x words, row_ptr n_rows + 1,
+    // gbins entries.
+    void read_index(uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint64_t *row_ptr, uint32_t *gbins);
     ~Engine();
 
     std::mutex mu;
@@ -161,6 +187,9 @@ public:
 
 private:
     void upload_index(const hbr_index_desc &desc);
+    void bin_dense(const DenseSource &src);
+    void read_tunables();
+    uint64_t entries_ = 0;
     void ensure_rows();
     bool contiguous(const Segment &sg) const;
     bool identity_rows0_ = false;

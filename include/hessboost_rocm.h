@@ -115,6 +115,33 @@ typedef struct hbr_engine hbr_engine;
 int hbr_engine_open(int ordinal, const hbr_index_desc *index, hbr_engine **out);
 void hbr_engine_close(hbr_engine *e);
 
+/* The engine over a dense f32 matrix binned on the device: the index
+ * GHistIndex::from_dmatrix (src/data/ghist.rs:213-257) builds on the host,
+ * with bins from HistCuts::bin_of (src/data/quantile.rs:285-296) against
+ * `cuts`, computed by the GPU. x is row-major n_rows x n_cols, in host memory
+ * or (x_on_device) in this ordinal's device memory; cells equal to `missing`
+ * (any NaN when it is NaN) are absent. Refused when a feature has more than
+ * 256 bins. The layouts equal hbr_index_from_dense's byte for byte. */
+int hbr_engine_open_dense(int ordinal, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                          const hbr_cuts *cuts, int x_on_device, hbr_engine **out);
+
+/* The engine's index as it sits on the device, for checking a build
+ * (no reference counterpart: the reference reads GHistIndex fields).
+ * dense: every row holds every feature; dense_u8: row-major u8 rows of
+ * `stride` bytes are kept; has_cols/has_missing: local columns and the
+ * missing bitmap are kept; entries: stored cells. */
+typedef struct hbr_index_info {
+    uint32_t dense, dense_u8, has_cols, has_missing;
+    uint32_t stride, pad;
+    uint64_t entries;
+} hbr_index_info;
+int hbr_engine_index_info(hbr_engine *e, hbr_index_info *out);
+/* Copies of the layouts (NULL skips one): rows8 n_rows x stride (dense u8),
+ * cols8 n_cols x n_rows (u8 columns), missing n_cols x ceil(n_rows/64),
+ * row_ptr n_rows + 1 and gbins (u32 global bins, entries) of a CSR index. */
+int hbr_engine_index_read(hbr_engine *e, uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint64_t *row_ptr,
+                          uint32_t *gbins);
+
 /* HistogramBackend::prepare (src/tree/hist/mod.rs:96): stage a tree's
  * gradient pairs (interleaved g, h f32; one per index row). */
 int hbr_prepare(hbr_engine *e, const float *gpair, uint64_t n);

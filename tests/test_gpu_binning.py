@@ -1,0 +1,98 @@
+"""Device binning (hbr_engine_open_dense): a dense f32 matrix binned on the GPU
+against host cuts must give the index the host builds (HistCuts::bin_of,
+src/data/quantile.rs:285-296; GHistIndex::from_dmatrix,
+src/data/ghist.rs:213-257) byte for byte, in every layout the engine keeps."""
+import numpy as np
+import pytest
+
+import hessboost_amd as hb
+
+pytestmark = pytest.mark.gpu
+
+
+def _layouts(x, max_bin, missing=np.nan, on_device=False):
+    dm = hb.DMatrix(x, missing=missing)
+    cuts = dm.cuts(max_bin)
+    host = hb.Engine(dm.index(max_bin), 0).read_index()
+    if on_device:
+        buf = hb.DeviceBuffer(x.nbytes)
+        buf.upload(x)
+        dev = hb.Engine.from_dense(buf, cuts, 0, missing=missing, n_rows=x.shape[0], n_cols=x.shape[1])
+    else:
+        dev = hb.Engine.from_dense(x, cuts, 0, missing=missing)
+    return host, dev.read_index()
+
+
+def _same(host, dev):
+    for k in ("dense", "dense_u8", "has_cols", "has_missing", "entries"):
+        assert host[k] == dev[k], k
+    for k in ("rows8", "cols8", "missing", "row_ptr", "gbins"):
+        if host[k] is None:
+            assert dev[k] is None, k
+        else:
+            assert np.array_equal(host[k], dev[k]), k
+
+
+def test_dense_matrix_bins_equal_host_bins():
+    rng = np.random.default_rng(20)
+    x = rng.standard_normal((30_001, 40)).astype(np.float32)  # a ragged last 64-row group
+    x[:, 7] = np.round(x[:, 7])                                 # few distinct values
+    x[:, 8] = 3.0                                               # a constant feature
+    host, dev = _layouts(x, 256)
+    assert dev["dense_u8"] == 1
+    _same(host, dev)
+
+
+def test_values_on_cut_points_signed_zeros_and_infinities():
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((8_192, 6)).astype(np.float32)
+    x[:500, 0] = 0.0
+    x[500:1000, 0] = -0.0
+    x[1000:1100, 1] = np.inf
+    x[1100:1200, 1] = -np.inf
+    x[1200:1300, 2] = np.float32(1e-40)                         # subnormal
+    dm = hb.DMatrix(x)
+    _, cv = dm.cuts(64).arrays()
+    x[2000:2000 + len(cv), 3] = cv[:min(len(cv), 6192)]         # exactly the cut values
+    host, dev = _layouts(x, 64)
+    _same(host, dev)
+
+
+@pytest.mark.parametrize("frac", [0.1, 0.9])
+def test_missing_values_give_the_host_csr_columns_and_bitmap(frac):
+    """10% NaN keeps columns and a missing bitmap beside the CSR rows; 90%
+    NaN over 300 features keeps CSR rows only (cells > 2 x entries)."""
+    rng = np.random.default_rng(22)
+    n, f = (20_000, 30) if frac < 0.5 else (6_000, 300)
+    x = rng.exponential(size=(n, f)).astype(np.float32)
+    x[rng.random(x.shape) < frac] = np.nan
+    host, dev = _layouts(x, 64)
+    assert dev["dense"] == 0
+    assert dev["has_cols"] == (1 if frac < 0.5 else 0)
+    _same(host, dev)
+
+
+def test_missing_marker_other_than_nan():
+    """With -999 as the marker, -999 cells are absent and NaN cells present
+    (bin_of puts a NaN in the feature's last bin)."""
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((10_000, 12)).astype(np.float32)
+    x[rng.random(x.shape) < 0.05] = -999.0
+    x[rng.random(x.shape) < 0.01] = np.nan
+    host, dev = _layouts(x, 128, missing=-999.0)
+    _same(host, dev)
+
+
+def test_rows_already_on_the_device():
+    rng = np.random.default_rng(24)
+    x = rng.standard_normal((12_345, 28)).astype(np.float32)
+    host, dev = _layouts(x, 256, on_device=True)
+    _same(host, dev)
+
+
+def test_features_wider_than_256_bins_are_refused():
+    rng = np.random.default_rng(25)
+    x = rng.standard_normal((5_000, 3)).astype(np.float32)
+    cuts = hb.DMatrix(x).cuts(1024)
+    with pytest.raises(hb.HbrError):
+        hb.Engine.from_dense(x, cuts, 0)
