@@ -269,10 +269,13 @@ class Engine:
         A.check(A.lib().hbr_gradients(self._h, C.byref(loss), A.ptr(labels), A.ptr(w), n, C.byref(ok)))
         return bool(ok.value)
 
-    def read_gradients(self):
-        out = np.empty(2 * self.index.n_rows, np.float32)
-        A.check(A.lib().hbr_read_gradients(self._h, A.ptr(out), self.index.n_rows))
-        return out.reshape(-1, 2)
+    def read_gradients(self, n_classes=1):
+        """The staged pairs, (n_rows, 2); after softmax gradients of k
+        classes, n_classes=k gives every class's, (k, n_rows, 2)."""
+        n = self.index.n_rows * n_classes
+        out = np.empty(2 * n, np.float32)
+        A.check(A.lib().hbr_read_gradients(self._h, A.ptr(out), n))
+        return out.reshape(-1, 2) if n_classes == 1 else out.reshape(n_classes, -1, 2)
 
     def add_leaf_values(self, segs, values):
         arr = (A.Segment * len(segs))(*segs)

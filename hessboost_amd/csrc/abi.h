@@ -139,6 +139,24 @@ struct GradArgs {
     float max_input;        // logistic vector range (80)
 };
 
+// Softmax gradients of every class of every row (simd/mod.rs:502-600),
+// class-major: row r's pair for class c at gpair[c * n + r]. Class c's
+// magnitude maxima and non-finite count fold into scales[c]. Rows below
+// `batched` (2 or 4 classes) take the vector batches of 8 / k rows.
+constexpr uint32_t kSoftmaxMaxClasses = 1024;
+struct SoftmaxArgs {
+    const float *margins;       // [n][k]
+    const float *labels;        // n
+    const float *weights;       // n or null
+    GPair *gpair;               // [k][n]
+    QScale *scales;             // k
+    const uint64_t *exp_table;  // 32 entries: bits(2^(i/32)) - (i << 47)
+    uint32_t n;
+    uint32_t k;
+    uint32_t batched;
+    float min_hess;
+};
+
 // ---- row buffers -------------------------------------------------------------
 struct IotaArgs {
     uint32_t *rows;
@@ -363,6 +381,14 @@ constexpr uint32_t kScanDeviceRoot = 1;
 // Per-tree quantisation exponents from the folded maxima, on the device.
 struct FinishArgs {
     QScale *scale;
+    uint64_t n_rows;
+};
+
+// to = from with the exponents of n_rows rows (one thread): one class's
+// folded softmax maxima become the live scale.
+struct SelectArgs {
+    const QScale *from;
+    QScale *to;
     uint64_t n_rows;
 };
 

@@ -375,7 +375,13 @@ int hbr_gradients(hbr_engine *h, const hbr_device_loss *loss, const float *label
     return with_engine(h, [&](Engine &e) {
         if (!loss || !labels) fail(kInvalid, "gradients: null argument");
         if (!e.labels_loaded()) e.set_labels(labels, weights, n);
-        const bool ok = e.compute_gradients(*loss, 0);
+        bool ok;
+        if (loss->kind == HBR_LOSS_SOFTMAX) {
+            e.softmax_gradients_async(loss->min_hess);
+            ok = e.softmax_all_finite();
+        } else {
+            ok = e.compute_gradients(*loss, 0);
+        }
         if (all_finite) *all_finite = ok ? 1 : 0;
     });
 }

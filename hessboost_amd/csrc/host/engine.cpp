@@ -333,6 +333,8 @@ void Engine::read_index(uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint6
 void Engine::load_margins(const float *m, uint64_t n, uint32_t outputs) {
     if (n != n_rows_ * outputs) fail(kInvalid, "load_margins: length is not n_rows * n_outputs");
     outputs_ = outputs;
+    active_pairs_ = nullptr;
+    class_outputs_ = 0;
     margins_.resize(n);
     margins_.upload(m, n, dev_.stream());
     labels_loaded_ = false;
@@ -363,8 +365,12 @@ void Engine::read_margins(float *out, uint64_t n) {
 }
 
 void Engine::read_gradients(float *out, uint64_t n) {
-    if (n != n_rows_ || gpair_.size() < n_rows_) fail(kInvalid, "read_gradients: nothing staged for every row");
-    gpair_.download(reinterpret_cast<GPair *>(out), n, dev_.stream());
+    if (softmax_staged() && n == n_rows_ * outputs_) {
+        class_pairs_.download(reinterpret_cast<GPair *>(out), n, dev_.stream());
+    } else {
+        if (n != n_rows_ || !pairs_staged()) fail(kInvalid, "read_gradients: nothing staged for every row");
+        HBR_HIP(hipMemcpyAsync(out, pairs(), n * sizeof(GPair), hipMemcpyDeviceToHost, dev_.stream()));
+    }
     dev_.sync();
 }
 
@@ -373,6 +379,8 @@ double Engine::unit_h() const { return std::ldexp(1.0, scale_host_.exp_h); }
 
 void Engine::prepare(const float *gpair, uint64_t n) {
     if (n != n_rows_) fail(kInvalid, "prepare: one gradient pair per row");
+    active_pairs_ = nullptr;
+    class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
     gpair_.upload(reinterpret_cast<const GPair *>(gpair), n, dev_.stream());
     QScale q{};
@@ -415,6 +423,8 @@ void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     if (!labels_loaded_) fail(kInvalid, "gradients: no labels since load_margins");
     if (outputs_ != 1 || output != 0) fail(kRefused, "device gradients run for one output");
     hipStream_t s = dev_.stream();
+    active_pairs_ = nullptr;
+    class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
     scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
     HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
@@ -484,6 +494,71 @@ void Engine::compute_gradients_async(const hbr_device_loss &loss, uint32_t outpu
     scale_checked_ = false;  // grow_root reads the scale back and checks it
 }
 
+// The table of the expf restatement: bits(2^(i/32)) - (i << 47), from the
+// host's exp2 (exact: 2^(i/32) correctly rounded).
+static std::vector<uint64_t> expf_table() {
+    std::vector<uint64_t> t(32);
+    for (uint32_t i = 0; i < 32; i++) {
+        const double v = std::exp2((double)i / 32.0);
+        uint64_t b;
+        std::memcpy(&b, &v, sizeof b);
+        t[i] = b - ((uint64_t)i << 47);
+    }
+    return t;
+}
+
+void Engine::softmax_gradients_async(float min_hess) {
+    if (!labels_loaded_) fail(kInvalid, "softmax gradients: no labels since load_margins");
+    const uint32_t k = outputs_;
+    if (k < 1 || k > kSoftmaxMaxClasses) fail(kRefused, "softmax gradients: 1 to 1024 classes");
+    if (n_rows_ == 0) fail(kInvalid, "softmax gradients: no rows");
+    hipStream_t s = dev_.stream();
+    if (!exp_table_.size()) {
+        const std::vector<uint64_t> t = expf_table();
+        exp_table_.resize(t.size());
+        exp_table_.upload(t.data(), t.size(), s);
+        dev_.sync();
+    }
+    active_pairs_ = nullptr;
+    class_pairs_.reserve((size_t)k * n_rows_);
+    class_scales_.reserve(k);
+    class_outputs_ = k;
+    HBR_HIP(hipMemsetAsync(class_scales_.get(), 0, k * sizeof(QScale), s));
+    SoftmaxArgs a{};
+    a.margins = margins_.get();
+    a.labels = labels_.get();
+    a.weights = has_weights_ ? weights_.get() : nullptr;
+    a.gpair = class_pairs_.get();
+    a.scales = class_scales_.get();
+    a.exp_table = exp_table_.get();
+    a.n = (uint32_t)n_rows_;
+    a.k = k;
+    // simd/mod.rs:515-519: the 2- and 4-class vector batches need 16 margins
+    a.batched = (k == 2 || k == 4) && n_rows_ * k >= 16 ? (uint32_t)(n_rows_ - n_rows_ % (8 / k)) : 0u;
+    a.min_hess = min_hess;
+    const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)),
+                                               (uint32_t)dev_.cu_count() * 8);
+    dev_.launch("hbr_softmax_grad", dim3(blocks), dim3(kThreads), a);
+}
+
+void Engine::select_class(uint32_t c) {
+    if (!softmax_staged() || c >= class_outputs_) fail(kInvalid, "select_class: no softmax gradients of that class");
+    SelectArgs a{class_scales_.get() + c, scale_dev(), n_rows_};
+    dev_.launch("hbr_scale_select", dim3(1), dim3(64), a);
+    active_pairs_ = class_pairs_.get() + (size_t)c * n_rows_;
+    scale_checked_ = false;  // the tree's root or finish reads the class's scale back
+}
+
+bool Engine::softmax_all_finite() {
+    if (!softmax_staged()) fail(kInvalid, "softmax: no gradients staged");
+    std::vector<QScale> q(class_outputs_);
+    class_scales_.download(q.data(), q.size(), dev_.stream());
+    dev_.sync();
+    for (const QScale &c : q)
+        if (c.nonfinite) return false;
+    return true;
+}
+
 // ---- tree growth -------------------------------------------------------------------
 
 void Engine::ensure_rows() {
@@ -521,7 +596,7 @@ QBin Engine::root_total(const Segment &sg) {
     a.rows = ident ? nullptr : rows_[sg.buf].get() + sg.offset;
     a.first = ident ? sg.offset : 0;
     a.n = sg.len;
-    a.gpair = gpair_.get();
+    a.gpair = pairs();
     a.scale = scale_dev();
     a.out = total_dev();
     const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(sg.len, kThreads)), 2048);
@@ -551,7 +626,7 @@ void Engine::launch_root(const Segment &seg, uint32_t slot, float lower, float u
         t.rows = ident ? nullptr : rows_[seg.buf].get() + seg.offset;
         t.first = ident ? seg.offset : 0;
         t.n = seg.len;
-        t.gpair = gpair_.get();
+        t.gpair = pairs();
         t.scale = scale_dev();
         t.out = total_dev();
         dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(seg.len, kThreads)), 2048)),
@@ -672,7 +747,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
                          const PartSplit *splits_dev, const PartOut *part_out_dev, const uint32_t *rows0,
                          const GrowCounts *grow) {
     if (n == 0) return;
-    if (gpair_.size() < n_rows_ || !gpair_.get()) fail(kInvalid, "histograms: no gradients staged");
+    if (!pairs_staged()) fail(kInvalid, "histograms: no gradients staged");
     if (!dense_u8_ && grow) fail(kInvalid, "histograms: device-counted levels need the dense kernels");
     hipStream_t s = dev_.stream();
     const uint32_t fg = hist_features_per_group;
@@ -712,7 +787,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.counts = d_hcounts_.get();
     a.rows[0] = rows0 ? rows0 : rows_[0].get();
     a.rows[1] = rows_[1].get();
-    a.gpair = gpair_.get();
+    a.gpair = pairs();
     a.scale = scale_dev();
     a.bins8 = rows8_.get();
     a.stride = stride_;
@@ -1030,7 +1105,7 @@ void Engine::launch_device_root() {
         t.rows = nullptr;
         t.first = 0;
         t.n = (uint32_t)n_rows_;
-        t.gpair = gpair_.get();
+        t.gpair = pairs();
         t.scale = scale_dev();
         t.out = total_dev();
         dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)), 2048)),
@@ -1046,7 +1121,7 @@ void Engine::launch_device_root() {
 
 Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, float eta) {
     if (!can_grow_device(max_depth)) fail(kInvalid, "device growth: index or depth not supported");
-    if (gpair_.size() < n_rows_ || !gpair_.get()) fail(kInvalid, "device growth: no gradients staged");
+    if (!pairs_staged()) fail(kInvalid, "device growth: no gradients staged");
     hipStream_t s = dev_.stream();
     const uint32_t depth = (uint32_t)max_depth;
     const uint32_t slot_cap = 1u << (depth - 1);
@@ -1075,6 +1150,7 @@ Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, f
         }
     }
     TreeTicket t;
+    last_depth_ = depth;
     t.slot = tree_seq_++ % kTreeRing;
     t.check = !scale_checked_;
     scale_checked_ = true;
@@ -1189,8 +1265,11 @@ bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vecto
 }
 
 void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss) {
-    if (!dense_u8_ || stride_ != 32) fail(kRefused, "walk: the index has no 32-byte row-major u8 bins");
+    if (!dense_u8_) fail(kRefused, "walk: the index has no row-major u8 bins");
     if (output >= outputs_) fail(kInvalid, "walk: no such output");
+    // the staged walk: 32-byte rows and trees whose nodes fit its LDS table
+    const bool staged = stride_ == 32 && last_depth_ <= 9;
+    if (next_loss && !staged) fail(kRefused, "walk: gradients need 32-byte rows and depth <= 9");
     hipStream_t s = dev_.stream();
     WalkArgs a{};
     a.tree = ring_nodes(last_ring_);
@@ -1204,10 +1283,12 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss)
     const uint32_t blocks =
         std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)), (uint32_t)dev_.cu_count() * walk_blocks_per_cu);
     if (!next_loss) {
-        dev_.launch("hbr_walk_leaves32", dim3(blocks), dim3(256), a);
+        dev_.launch(staged ? "hbr_walk_leaves32" : "hbr_walk_leaves", dim3(blocks), dim3(256), a);
         return;
     }
     if (outputs_ != 1 || !labels_loaded_) fail(kInvalid, "walk: gradients need one output and labels");
+    active_pairs_ = nullptr;
+    class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
     scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
     if (!poison_.size()) {
@@ -1309,6 +1390,8 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
     if (next_loss) {
         // the next round's gradients from the updated margins, in the same pass
         if (!can_walk_gradients(n)) fail(kInvalid, "walk_add: gradients need the staged walk of one output");
+        active_pairs_ = nullptr;
+        class_outputs_ = 0;
         gpair_.resize(n_rows_ ? n_rows_ : 1);
         scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
         HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));

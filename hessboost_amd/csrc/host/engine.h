@@ -109,6 +109,18 @@ public:
     // The root's total, histogram (into `slot`) and split search with one
     // host synchronisation; false when a gradient is not finite.
     bool grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best);
+    // Softmax gradients of every class (the margins' outputs, at most
+    // kSoftmaxMaxClasses) from the device margins, with the host's bits,
+    // class-major on the device, each class's scale folded; no
+    // synchronisation. select_class(c) then stages class c's pairs and scale
+    // for the next tree (checked by its root or its finish, like
+    // compute_gradients_async).
+    void softmax_gradients_async(float min_hess);
+    void select_class(uint32_t c);
+    bool softmax_staged() const { return class_pairs_.size() > 0 && class_outputs_ == outputs_; }
+    // compute_gradients' check for the softmax: false when a class has a
+    // gradient that is not finite
+    bool softmax_all_finite();
     void read_margins(float *out, uint64_t n);
     void read_gradients(float *out, uint64_t n);
     const QScale &scale() const { return scale_host_; }
@@ -167,6 +179,8 @@ public:
     bool can_walk_device_tree(uint64_t max_depth) const {
         return can_grow_device(max_depth) && stride_ == 32 && max_depth <= 9 && outputs_ == 1 && labels_loaded_;
     }
+    // The walk alone (no gradients): any dense u8 index, any output.
+    bool can_route_device_tree(uint64_t max_depth) const { return can_grow_device(max_depth); }
     void walk_device_tree(uint32_t output, const hbr_device_loss *next_loss);
     // HistogramBackend::build of a host row list (per-node host growth).
     std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
@@ -227,6 +241,7 @@ private:
     GrowTreeNode *ring_nodes(uint32_t r) const {
         return reinterpret_cast<GrowTreeNode *>(d_tree_ring_.get() + r * ring_bytes() + kTreeHeaderBytes);
     }
+    uint32_t last_depth_ = 0;  // max_depth of the last queued device tree
     DBuf<QScale> guard_scale_;
     DBuf<uint32_t> poison_;
     std::vector<int8_t> monotone_host_;
@@ -256,6 +271,15 @@ private:
 
     // training state
     DBuf<GPair> gpair_;
+    // softmax: every class's pairs ([class][row]) and scales; the selected
+    // class's pairs stand in for gpair_ while active_pairs_ is set
+    DBuf<GPair> class_pairs_;
+    DBuf<QScale> class_scales_;
+    DBuf<uint64_t> exp_table_;
+    uint32_t class_outputs_ = 0;
+    GPair *active_pairs_ = nullptr;
+    GPair *pairs() const { return active_pairs_ ? active_pairs_ : gpair_.get(); }
+    bool pairs_staged() const { return active_pairs_ || (gpair_.size() >= n_rows_ && gpair_.get()); }
     DBuf<float> margins_, labels_, weights_;
     uint32_t outputs_ = 1;
     bool labels_loaded_ = false, has_weights_ = false;

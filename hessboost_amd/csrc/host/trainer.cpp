@@ -338,6 +338,9 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool 
 
 // ---- the boosting loop ----------------------------------------------------------
 
+// the Hessian floor of the logistic and softmax losses (objective/mod.rs:150)
+constexpr float kMinHess = 1e-16f;
+
 static float weighted_label_mean(const float *labels, const float *weights, uint64_t n) {
     double mean = 0.0;
     if (weights) {
@@ -392,6 +395,15 @@ Trainer::Trainer(Engine &e, const TrainParams &p, const float *labels, const flo
     if (n != e.n_rows()) fail(kInvalid, "trainer: one label per index row");
     k_ = p.objective == HBR_OBJ_SOFTMAX ? p.num_class : 1;
     if (k_ == 0) fail(kInvalid, "softmax needs num_class");
+    if (p.objective == HBR_OBJ_SOFTMAX) {
+        if (k_ > kSoftmaxMaxClasses) fail(kRefused, "softmax: at most 1024 classes");
+        // multiclass.rs:96-100: class indices, non-negative integers below num_class
+        for (uint64_t i = 0; i < n; i++) {
+            const float y = labels[i];
+            if (!(y >= 0.0f && y < (float)k_) || y != std::floor(y))
+                fail(kInvalid, "softmax labels must be class indices below num_class");
+        }
+    }
     labels_.assign(labels, labels + n);
     if (weights) weights_.assign(weights, weights + n);
     base_ = base_margins(p, labels, weights, n);
@@ -400,33 +412,6 @@ Trainer::Trainer(Engine &e, const TrainParams &p, const float *labels, const flo
         for (uint32_t c = 0; c < k_; c++) m[r * k_ + c] = base_[c];
     e_.load_margins(m.data(), m.size(), k_);
     e_.set_labels(labels, weights, n);
-}
-
-// simd/mod.rs:580-600, one row at a time: shift by max(f32::MIN_POSITIVE,
-// preds), sum of expf in f64, p = expf(x - wmax) / (f32)sum.
-void Trainer::softmax_gradients(std::vector<float> &out) {
-    std::vector<float> m((size_t)n_ * k_);
-    e_.read_margins(m.data(), m.size());
-    out.resize(2 * (size_t)n_ * k_);
-    const float min_hess = 1e-16f;
-#pragma omp parallel for schedule(static)
-    for (int64_t r = 0; r < (int64_t)n_; r++) {
-        const float *p = &m[(size_t)r * k_];
-        float wmax = FLT_MIN;
-        for (uint32_t c = 0; c < k_; c++) wmax = std::fmax(p[c], wmax);
-        double wsum = 0.0;
-        for (uint32_t c = 0; c < k_; c++) wsum += (double)std::exp(p[c] - wmax);
-        const float ws = (float)wsum;
-        const float w = weights_.empty() ? 1.0f : weights_[r];
-        const uint32_t label = (uint32_t)labels_[r];
-        for (uint32_t c = 0; c < k_; c++) {
-            const float pc = std::exp(p[c] - wmax) / ws;
-            const float h = std::fmax(2.0f * pc * (1.0f - pc) * w, min_hess);
-            const float g = c == label ? pc - 1.0f : pc;
-            out[2 * ((size_t)r * k_ + c)] = g * w;
-            out[2 * ((size_t)r * k_ + c) + 1] = h;
-        }
-    }
 }
 
 // Leaf values onto the margins (training/margins.rs:247-289): by routing
@@ -502,7 +487,44 @@ void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
     }
 }
 
+// Softmax rounds with the device ahead of the host: every class's
+// gradients at the start of a round (one kernel, from the margins every
+// earlier tree has been walked into), then the round's trees, class by
+// class, each grown from its class's pairs and walked into its class's
+// margins on the device; up to three trees in flight before the host reads
+// the oldest back.
+void Trainer::boost_softmax_pipelined(uint64_t rounds) {
+    TreeBuilder b(e_, p_.grow);
+    std::deque<Engine::TreeTicket> inflight;
+    const uint64_t total = rounds * k_;
+    uint64_t queued = 0, done = 0;
+    while (done < total) {
+        while (queued < total && inflight.size() < 3) {
+            const uint32_t c = (uint32_t)(queued % k_);
+            if (c == 0) e_.softmax_gradients_async(kMinHess);
+            e_.select_class(c);
+            inflight.push_back(b.queue_device());
+            e_.walk_device_tree(c, nullptr);
+            queued++;
+        }
+        std::vector<GrowTreeNode> nodes;
+        const Engine::TreeState st = e_.finish_device_tree(inflight.front(), nodes, nullptr);
+        inflight.pop_front();
+        if (st != Engine::kTreeOk) {
+            e_.dev().sync();
+            fail(kRefused, "a gradient is not finite");
+        }
+        trees_.push_back(b.tree_from(nodes));
+        done++;
+    }
+}
+
 void Trainer::boost(uint64_t rounds) {
+    if (p_.objective == HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE &&
+        e_.can_route_device_tree(p_.grow.max_depth)) {
+        boost_softmax_pipelined(rounds);
+        return;
+    }
     if (p_.objective != HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE &&
         e_.can_walk_device_tree(p_.grow.max_depth)) {
         hbr_device_loss loss = device_loss();
@@ -514,14 +536,10 @@ void Trainer::boost(uint64_t rounds) {
     TreeBuilder b(e_, p_.grow);
     for (uint64_t it = 0; it < rounds; it++) {
         if (p_.objective == HBR_OBJ_SOFTMAX) {
-            std::vector<float> all, gk(2 * (size_t)n_);
-            softmax_gradients(all);
+            // every class's gradients from the round's starting margins
+            e_.softmax_gradients_async(kMinHess);
             for (uint32_t c = 0; c < k_; c++) {
-                for (uint64_t r = 0; r < n_; r++) {
-                    gk[2 * r] = all[2 * (r * k_ + c)];
-                    gk[2 * r + 1] = all[2 * (r * k_ + c) + 1];
-                }
-                e_.prepare(gk.data(), n_);
+                e_.select_class(c);
                 grow_and_add(b, c);
             }
             continue;
@@ -544,7 +562,7 @@ hbr_device_loss Trainer::device_loss() const {
     hbr_device_loss loss{};
     loss.kind = p_.objective == HBR_OBJ_LOGISTIC ? HBR_LOSS_LOGISTIC : HBR_LOSS_SQUARED_ERROR;
     loss.scale_pos_weight = p_.scale_pos_weight;
-    loss.min_hess = 1e-16f;
+    loss.min_hess = kMinHess;
     loss.max_input = 80.0f;
     loss.vector_rows = n_ >= 16 ? n_ - n_ % 8 : 0;
     return loss;

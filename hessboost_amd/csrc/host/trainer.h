@@ -114,7 +114,7 @@ public:
     void margins(float *out);
 
 private:
-    void softmax_gradients(std::vector<float> &gpair_all);
+    void boost_softmax_pipelined(uint64_t rounds);
     void boost_pipelined(uint64_t rounds, const hbr_device_loss &loss);
     hbr_device_loss device_loss() const;
     // one grown tree onto the margins of output `output` (and, given

@@ -13,6 +13,7 @@
 // round-to-nearest-even, divisions are correctly rounded. Rows outside that
 // path use libm's expf on the host; the kernel lists them instead.
 #include "common.h"
+#include "libm_expf.h"
 
 namespace hbr {
 
@@ -199,4 +200,129 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scale_rotate(RotateArgs a) 
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     *a.saved = *a.live;
     *a.live = QScale{0, 0, 0u, 0u, 0u, 0u, {0u, 0u}};
+}
+
+extern "C" __global__ __launch_bounds__(64) void hbr_scale_select(SelectArgs a) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    QScale q = *a.from;
+    q.exp_g = exponent_for(q.max_g_bits, a.n_rows);
+    q.exp_h = exponent_for(q.max_h_bits, a.n_rows);
+    q.scalar_rows = 0;
+    *a.to = q;
+}
+
+namespace hbr {
+
+// Rust's saturating `label as usize` (simd/mod.rs:549): NaN and values below
+// 1 give class 0, k stands for every index past the last class.
+__device__ __forceinline__ uint32_t label_class(float y, uint32_t k) {
+    if (!(y >= 1.0f)) return 0u;
+    return y < (float)k ? (uint32_t)y : k;
+}
+
+}  // namespace hbr
+
+// One thread per row, grid-stride over whole waves. The scalar row
+// (simd/mod.rs:580-600): shift by max(f32::MIN_POSITIVE, margins), f64 sum
+// of expf, p = expf(x - max) / (f32)sum, h = max(2p(1 - p)w, min_hess),
+// g = (p - [class == label])w, with expf as the host libm computes it. The
+// 2- and 4-class vector batches (simd/x86_64.rs:160-335): a batch of 8 / k
+// consecutive rows is vectorised when each of its rows is free of NaN and
+// max(f32::MIN_POSITIVE, row max) - row min <= 80 (the reference's lane
+// permutes give every lane of a row these values); then e = the vector exp
+// of x - max, the f32 row sum (e0 + e1, or (e0 + e1) + (e2 + e3)) and
+// p = e * (1 / sum). Each class's magnitude maxima fold per wave, then per
+// workgroup in LDS, then one atomic per class.
+extern "C" __global__ __launch_bounds__(256) void hbr_softmax_grad(SoftmaxArgs a) {
+    __shared__ uint64_t s_tab[32];
+    __shared__ uint32_t s_fold[3][kSoftmaxMaxClasses];
+    const uint32_t k = a.k;
+    if (threadIdx.x < 32) s_tab[threadIdx.x] = a.exp_table[threadIdx.x];
+    for (uint32_t c = threadIdx.x; c < k; c += blockDim.x) s_fold[0][c] = s_fold[1][c] = s_fold[2][c] = 0u;
+    __syncthreads();
+    const uint32_t per = k == 2 ? 4u : 2u;  // rows per vector batch (k = 2 or 4)
+    const uint64_t group = (per == 4u ? 0xfull : 0x3ull) << (lane_id() & ~(per - 1u));
+    const uint32_t stride = gridDim.x * blockDim.x;
+    const uint32_t end = (a.n + kWave - 1) / kWave * kWave;  // whole waves stay in the loop
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < end; i += stride) {
+        const bool active = i < a.n;
+        const float *m = a.margins + (size_t)(active ? i : 0) * k;
+        const float y = active ? a.labels[i] : 0.0f;
+        const float w = (active && a.weights) ? a.weights[i] : 1.0f;
+        const uint32_t label = label_class(y, k);
+        // the vector batch test (a.batched is 0 unless k is 2 or 4)
+        bool vec = false;
+        float vmax = 0.0f, inv = 0.0f;
+        if (a.batched) {
+            const bool in_batch = i < a.batched;
+            bool regular = false;
+            if (in_batch) {
+                float v[4];
+#pragma unroll
+                for (uint32_t c = 0; c < 4; c++) v[c] = c < k ? m[c] : v[0];
+                bool nan = false;
+                float hi = v[0], lo = v[0];
+#pragma unroll
+                for (uint32_t c = 0; c < 4; c++) {
+                    nan |= __builtin_isnan(v[c]);
+                    hi = __builtin_fmaxf(hi, v[c]);
+                    lo = __builtin_fminf(lo, v[c]);
+                }
+                vmax = 0x1p-126f > hi ? 0x1p-126f : hi;
+                regular = !nan && vmax - lo <= 80.0f;
+                if (regular) {
+                    float e[4];
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; c++) e[c] = exp_vector(v[c] - vmax);
+                    const float sum = k == 2 ? e[0] + e[1] : (e[0] + e[1]) + (e[2] + e[3]);
+                    inv = 1.0f / sum;
+                }
+            }
+            const uint64_t ok = __ballot(regular || !in_batch);
+            vec = in_batch && (ok & group) == group;
+        }
+        float wmax = 0x1p-126f, ws = 1.0f;  // f32::MIN_POSITIVE
+        if (active && !vec) {
+            for (uint32_t c = 0; c < k; c++) wmax = __builtin_fmaxf(m[c], wmax);
+            double sum = 0.0;
+            for (uint32_t c = 0; c < k; c++) sum += (double)hbr_expf_libm(m[c] - wmax, s_tab);
+            ws = (float)sum;
+        }
+        for (uint32_t c = 0; c < k; c++) {
+            float g = 0.0f, h = 0.0f;
+            if (active) {
+                const float mc = m[c];
+                if (vec) {
+                    const float p = exp_vector(mc - vmax) * inv;
+                    g = (p - (c == label ? 1.0f : 0.0f)) * w;
+                    const float q = ((p * 2.0f) * (1.0f - p)) * w;
+                    h = q > a.min_hess ? q : a.min_hess;
+                } else {
+                    const float p = hbr_expf_libm(mc - wmax, s_tab) / ws;
+                    h = __builtin_fmaxf(2.0f * p * (1.0f - p) * w, a.min_hess);
+                    g = (c == label ? p - 1.0f : p) * w;
+                }
+                a.gpair[(size_t)c * a.n + i] = GPair{g, h};
+            }
+            uint32_t mg = __float_as_uint(g) & 0x7fffffffu, mh = __float_as_uint(h) & 0x7fffffffu;
+            const uint32_t bad =
+                (uint32_t)__builtin_popcountll(__ballot(active && (!__builtin_isfinite(g) || !__builtin_isfinite(h))));
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) {
+                mg = max(mg, (uint32_t)__shfl_xor((int)mg, d, kWave));
+                mh = max(mh, (uint32_t)__shfl_xor((int)mh, d, kWave));
+            }
+            if (lane_id() == 0) {
+                if (mg) atomicMax(&s_fold[0][c], mg);
+                if (mh) atomicMax(&s_fold[1][c], mh);
+                if (bad) atomicAdd(&s_fold[2][c], bad);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t c = threadIdx.x; c < k; c += blockDim.x) {
+        if (s_fold[0][c]) atomicMax(&a.scales[c].max_g_bits, s_fold[0][c]);
+        if (s_fold[1][c]) atomicMax(&a.scales[c].max_h_bits, s_fold[1][c]);
+        if (s_fold[2][c]) atomicAdd(&a.scales[c].nonfinite, s_fold[2][c]);
+    }
 }

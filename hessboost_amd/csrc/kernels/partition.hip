@@ -224,42 +224,41 @@ extern "C" __global__ __launch_bounds__(256) void hbr_add_leaves(LeafArgs a) {
 // partition: bin < limit goes left), so the last level needs no partition
 // and the margins are read and written once, coalesced. A node table that
 // does not lead to a leaf within n_nodes steps leaves the row unchanged.
+// The node count of the walked tree: given, or from a device-grown tree's
+// counts (whose records are then read instead of meta/left/value; a leaf's
+// left is -1).
+__device__ __forceinline__ uint32_t walk_nodes(const WalkArgs &a) { return a.tree ? a.counts->n_nodes : a.n_nodes; }
+
+__device__ __forceinline__ uint32_t node_meta(const WalkArgs &a, uint32_t i, uint32_t *left) {
+    if (!a.tree) {
+        *left = a.left[i];
+        return a.meta[i];
+    }
+    const GrowTreeNode t = a.tree[i];
+    *left = t.left < 0 ? 0u : (uint32_t)t.left;
+    return t.left < 0 ? 1u << 31 : t.feature | (t.limit << 16);
+}
+
 extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves(WalkArgs a) {
+    const uint32_t n_nodes = walk_nodes(a);
     for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += gridDim.x * blockDim.x) {
         const uint8_t *b = a.bins8 + (size_t)r * a.stride;
-        uint32_t nid = 0, meta = a.meta[0];
-        for (uint32_t step = 0; step < a.n_nodes && !(meta >> 31); step++) {
+        uint32_t nid = 0, left;
+        uint32_t meta = node_meta(a, 0, &left);
+        for (uint32_t step = 0; step < n_nodes && !(meta >> 31); step++) {
             const uint32_t f = meta & 0xffffu, lim = (meta >> 16) & 0x7fffu;
-            nid = a.left[nid] + ((uint32_t)b[f] < lim ? 0u : 1u);
-            nid = nid < a.n_nodes ? nid : 0u;
-            meta = a.meta[nid];
+            nid = left + ((uint32_t)b[f] < lim ? 0u : 1u);
+            nid = nid < n_nodes ? nid : 0u;
+            meta = node_meta(a, nid, &left);
         }
         if (meta >> 31) {
             float *m = a.margins + (size_t)r * a.m_stride + a.output;
-            *m = *m + a.value[nid];
+            *m = *m + (a.tree ? a.tree[nid].value : a.value[nid]);
         }
     }
 }
 
-// The walk's node table in LDS: from meta/left/value, or from a
-// device-grown tree's records (a leaf's left is -1).
-__device__ __forceinline__ uint32_t walk_nodes(const WalkArgs &a) { return a.tree ? a.counts->n_nodes : a.n_nodes; }
 
-__device__ __forceinline__ void load_walk_table(const WalkArgs &a, uint32_t n_nodes, uint32_t *s_meta, uint32_t *s_left,
-                                                float *s_value) {
-    for (uint32_t i = threadIdx.x; i < n_nodes; i += blockDim.x) {
-        if (a.tree) {
-            const GrowTreeNode t = a.tree[i];
-            s_meta[i] = t.left < 0 ? 1u << 31 : t.feature | (t.limit << 16);
-            s_left[i] = t.left < 0 ? 0u : (uint32_t)t.left;
-            s_value[i] = t.value;
-        } else {
-            s_meta[i] = a.meta[i];
-            s_left[i] = a.left[i];
-            s_value[i] = a.value[i];
-        }
-    }
-}
 
 // The walks for 32-byte rows and trees of at most kWalkLdsNodes nodes: the
 // node table sits in LDS as (meta, left) pairs, and each thread walks

@@ -203,6 +203,11 @@ int hbr_load_margins(hbr_engine *e, const float *margins, uint64_t n, uint32_t n
 /* The device loss (DeviceLoss, src/tree/hist/mod.rs:355-365). */
 #define HBR_LOSS_SQUARED_ERROR 0
 #define HBR_LOSS_LOGISTIC 1
+/* Every class of a softmax (the margins' k outputs, k <= 1024; labels are
+ * class indices): no counterpart among the reference's DeviceLoss kinds
+ * (src/tree/hist/mod.rs:355-370), whose softmax gradients stay on the host
+ * (objective/multiclass.rs:43-55, simd/mod.rs:502-600); the same bits. */
+#define HBR_LOSS_SOFTMAX 2
 typedef struct hbr_device_loss {
     uint32_t kind;
     float scale_pos_weight;
@@ -218,8 +223,9 @@ int hbr_gradients(hbr_engine *e, const hbr_device_loss *loss, const float *label
                   const float *weights, uint64_t n, int *all_finite);
 
 /* The staged gradient pairs (interleaved g, h; n = n_rows), for checking a
- * device loss against the host's bits. No counterpart in the reference:
- * a diagnostic read of what hbr_gradients / hbr_prepare staged. */
+ * device loss against the host's bits; after softmax gradients n = n_rows *
+ * k gives every class's, class-major ([class][row]). No counterpart in the
+ * reference: a diagnostic read of what hbr_gradients / hbr_prepare staged. */
 int hbr_read_gradients(hbr_engine *e, float *out, uint64_t n);
 
 /* RowEngine::add_leaf_values: margins[row] += value for each leaf's rows. */

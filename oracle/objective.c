@@ -114,27 +114,105 @@ void or_gradient_logistic(const float *preds, const float *labels, const float *
     for (size_t i = vec_rows; i < n; i++) logistic_scalar(preds, labels, weights, spw, out, i);
 }
 
+/* simd/mod.rs:502-528 with simd/x86_64.rs:160-335: with 2 or 4 classes and
+ * at least 16 margins, the reference's x86-64 build takes an AVX2 path over
+ * batches of 8 / K whole rows (one vector): the row maximum and minimum by
+ * the in-lane permutes of row_reduce, shifted by max(f32::MIN_POSITIVE, row
+ * max); when every row of the batch is finite and spans at most 80, the
+ * vector exp of x - max, the row sum in f32 by the same permutes ((e0 + e1)
+ * + (e2 + e3) for four classes) and p = e * (1 / sum); a batch with a row
+ * outside that range, and the rows after the last whole batch, take the
+ * scalar row (simd/mod.rs:580-600). The trainer accepts only class indices
+ * as labels (multiclass.rs:96-100); other labels follow the reference's
+ * casts. */
+/* Rust's saturating `label as usize` (simd/mod.rs:549): NaN and values
+ * below 1 give class 0; k stands for every index past the last class. */
+static size_t label_class(float y, size_t k) {
+    if (!(y >= 1.0f)) return 0;
+    return y < (float)k ? (size_t)y : k;
+}
+
+static void softmax_row_scalar(const float *p, float label_f, float weight, size_t k, float *o) {
+    float wmax = FLT_MIN;
+    for (size_t c = 0; c < k; c++) wmax = fmaxf(p[c], wmax);
+    double wsum = 0.0;
+    for (size_t c = 0; c < k; c++) wsum += (double)expf(p[c] - wmax);
+    float ws = (float)wsum;
+    size_t label = label_class(label_f, k);
+    for (size_t c = 0; c < k; c++) {
+        float pc = expf(p[c] - wmax) / ws;
+        float h = fmaxf(2.0f * pc * (1.0f - pc) * weight, MIN_HESS);
+        float g = c == label ? pc - 1.0f : pc;
+        o[2 * c] = g * weight;
+        o[2 * c + 1] = h;
+    }
+}
+
+#define ROW_REDUCE(name, op)                                                          \
+    __attribute__((target("avx2,fma"))) static __m256 name(__m256 v, size_t k) {     \
+        __m256 r = op(v, _mm256_permute_ps(v, 0xB1)); /* swap adjacent lanes */       \
+        return k == 2 ? r : op(r, _mm256_permute_ps(r, 0x4E)); /* swap lane pairs */ \
+    }
+ROW_REDUCE(row_max, _mm256_max_ps)
+ROW_REDUCE(row_min, _mm256_min_ps)
+ROW_REDUCE(row_sum, _mm256_add_ps)
+
+/* 0 when a row of the batch is out of the vector path's range */
+__attribute__((target("avx2,fma"))) static int softmax_batch(const float *preds, const float *labels,
+                                                            const float *weights, size_t k, size_t row,
+                                                            float *out) {
+    __m256 v = _mm256_loadu_ps(preds + row * k);
+    __m256 maximum = _mm256_max_ps(_mm256_set1_ps(FLT_MIN), row_max(v, k));
+    __m256 minimum = row_min(v, k);
+    __m256 regular = _mm256_cmp_ps(_mm256_sub_ps(maximum, minimum), _mm256_set1_ps(MAX_FAST_EXP_INPUT), _CMP_LE_OQ);
+    if (_mm256_movemask_ps(regular) != 0xFF) return 0;
+    __m256 one = _mm256_set1_ps(1.0f);
+    __m256 e = exp_f32(_mm256_sub_ps(v, maximum));
+    __m256 p = _mm256_mul_ps(e, _mm256_div_ps(one, row_sum(e, k)));
+    float ind[8], wt[8];
+    for (size_t j = 0; j < WIDTH; j++) {
+        ind[j] = label_class(labels[row + j / k], k) == j % k ? 1.0f : 0.0f;
+        wt[j] = weights ? weights[row + j / k] : 1.0f;
+    }
+    __m256 weight = _mm256_loadu_ps(wt);
+    __m256 grad = _mm256_mul_ps(_mm256_sub_ps(p, _mm256_loadu_ps(ind)), weight);
+    __m256 hess = _mm256_max_ps(_mm256_mul_ps(_mm256_mul_ps(_mm256_mul_ps(p, _mm256_set1_ps(2.0f)),
+                                                            _mm256_sub_ps(one, p)), weight),
+                                _mm256_set1_ps(MIN_HESS));
+    float g[8], h[8];
+    _mm256_storeu_ps(g, grad);
+    _mm256_storeu_ps(h, hess);
+    float *o = out + 2 * row * k;
+    for (size_t j = 0; j < WIDTH; j++) {
+        o[2 * j] = g[j];
+        o[2 * j + 1] = h[j];
+    }
+    return 1;
+}
+
+void or_gradient_softmax_scalar(const float *preds, const float *labels, const float *weights,
+                                size_t n, size_t k, float *out) {
+#pragma omp parallel for schedule(static)
+    for (size_t r = 0; r < n; r++)
+        softmax_row_scalar(preds + r * k, labels[r], weights ? weights[r] : 1.0f, k, out + 2 * r * k);
+}
+
 void or_gradient_softmax(const float *preds, const float *labels, const float *weights,
                          size_t n, size_t k, float *out) {
+    size_t batched = 0;
+    if ((k == 2 || k == 4) && n * k >= MIN_SIMD_LEN) {
+        const size_t per = WIDTH / k;
+        batched = n - n % per;
 #pragma omp parallel for schedule(static)
-    for (size_t r = 0; r < n; r++) {
-        const float *p = preds + r * k;
-        float *o = out + 2 * r * k;
-        float wmax = FLT_MIN;
-        for (size_t c = 0; c < k; c++) wmax = fmaxf(p[c], wmax);
-        double wsum = 0.0;
-        for (size_t c = 0; c < k; c++) wsum += (double)expf(p[c] - wmax);
-        float ws = (float)wsum;
-        float weight = weights ? weights[r] : 1.0f;
-        size_t label = (size_t)labels[r];
-        for (size_t c = 0; c < k; c++) {
-            float pc = expf(p[c] - wmax) / ws;
-            float h = fmaxf(2.0f * pc * (1.0f - pc) * weight, MIN_HESS);
-            float g = c == label ? pc - 1.0f : pc;
-            o[2 * c] = g * weight;
-            o[2 * c + 1] = h;
+        for (size_t r = 0; r < batched; r += per) {
+            if (softmax_batch(preds, labels, weights, k, r, out)) continue;
+            for (size_t q = r; q < r + per; q++)
+                softmax_row_scalar(preds + q * k, labels[q], weights ? weights[q] : 1.0f, k, out + 2 * q * k);
         }
     }
+#pragma omp parallel for schedule(static)
+    for (size_t r = batched; r < n; r++)
+        softmax_row_scalar(preds + r * k, labels[r], weights ? weights[r] : 1.0f, k, out + 2 * r * k);
 }
 
 static float weighted_label_mean(const float *labels, const float *weights, size_t n) {

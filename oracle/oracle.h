@@ -29,14 +29,18 @@
  * bit for bit (predict); the reference's KATs pin the gains, the separating
  * split and the blocked-sum order; closed forms pin cuts of few distinct
  * values, bin assignment, partition routing, both logistic paths, softmax
- * (to 1e-6) and the intercepts.
+ * (to 1e-6) and the intercepts; the reference's own softmax tests
+ * (simd/tests.rs:133-285) pin the 2- and 4-class vector batches to the
+ * scalar rows (1e-6, and bit for bit on underflowing rows).
  *
  * Parity unpinned (nothing the reference holds reaches them):
  *   - the weighted sketch's prune/merge on data with more distinct values
  *     than max_bin (checked by quantile properties only);
  *   - the lossguide expansion order (heap ties), grow.c;
- *   - softmax gradients bit for bit: they call the host libm expf, as the
- *     reference's f32::exp does, so bits match only for the same libm.
+ *   - softmax gradients bit for bit: the scalar rows call the host libm
+ *     expf, as the reference's f32::exp does, so bits match only for the
+ *     same libm; the 2- and 4-class vector batches follow the reference's
+ *     intrinsic sequence, pinned to 1e-6 only.
  */
 #ifndef HB_ORACLE_H
 #define HB_ORACLE_H
@@ -180,6 +184,9 @@ void or_gradient_logistic(const float *preds, const float *labels,
 /* preds n*k row-major; out n*k pairs row-major [row][class]. */
 void or_gradient_softmax(const float *preds, const float *labels,
                          const float *weights, size_t n, size_t k, float *out);
+/* The same with every row on the scalar path (simd/mod.rs:536-555). */
+void or_gradient_softmax_scalar(const float *preds, const float *labels,
+                                const float *weights, size_t n, size_t k, float *out);
 float or_sigmoid(float x);
 /* Per-output intercepts (base margins). out[k]. */
 void or_base_margins(const float *labels, const float *weights, size_t n,

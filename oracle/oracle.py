@@ -116,6 +116,7 @@ def lib():
         for name in ("or_gradient_squared_error", "or_gradient_logistic"):
             getattr(L, name).argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_float, C.c_void_p]
         L.or_gradient_softmax.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]
+        L.or_gradient_softmax_scalar.argtypes = L.or_gradient_softmax.argtypes
         L.or_sigmoid.restype = C.c_float
         L.or_sigmoid.argtypes = [C.c_float]
         L.or_base_margins.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, P(Params), C.c_void_p]
@@ -296,7 +297,7 @@ def sum_rows(gpair, rows):
     return out
 
 
-def gradient(objective, preds, labels, weights=None, scale_pos_weight=1.0, num_class=0):
+def gradient(objective, preds, labels, weights=None, scale_pos_weight=1.0, num_class=0, scalar_rows=False):
     preds = np.ascontiguousarray(preds, np.float32)
     labels = np.ascontiguousarray(labels, np.float32)
     w = None if weights is None else np.ascontiguousarray(weights, np.float32)
@@ -304,7 +305,8 @@ def gradient(objective, preds, labels, weights=None, scale_pos_weight=1.0, num_c
     L = lib()
     if objective == OBJ_SOFTMAX:
         out = np.empty(2 * n * num_class, np.float32)
-        L.or_gradient_softmax(_ptr(preds), _ptr(labels), _ptr(w), n, num_class, _ptr(out))
+        fn = L.or_gradient_softmax_scalar if scalar_rows else L.or_gradient_softmax
+        fn(_ptr(preds), _ptr(labels), _ptr(w), n, num_class, _ptr(out))
         return out.reshape(n, num_class, 2)
     out = np.empty(2 * n, np.float32)
     fn = L.or_gradient_squared_error if objective == OBJ_SQUARED_ERROR else L.or_gradient_logistic

@@ -198,3 +198,76 @@ def test_device_gradients_match_oracle_bits():
                 got = eng.read_gradients()
                 want = O.gradient(obj, m, y, weights, scale_pos_weight=1.5)
                 assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, obj)
+
+
+def _softmax_case(rng, n, k, spread=3.0):
+    m = (rng.standard_normal(n * k) * spread).astype(np.float32)
+    if n > 8:
+        m[k * 5 + k - 1] = -90.0   # a row spanning more than 80: its batch leaves the vector path
+        m[k * 7: k * 8] = -30.0    # every margin below f32::MIN_POSITIVE
+    y = rng.integers(0, k, n).astype(np.float32)
+    w = (rng.random(n) * 2).astype(np.float32)
+    return m, y, w
+
+
+def test_device_softmax_gradients_match_oracle_bits():
+    """Every class's pairs against the oracle (simd/mod.rs:502-600): the
+    2- and 4-class vector batches and their scalar tails, rows that leave a
+    batch to the scalar path, and other class counts, bit for bit."""
+    rng = np.random.default_rng(16)
+    for k in (1, 2, 3, 4, 10, 17):
+        for n in (3, 5, 37, 4099):
+            x = rng.standard_normal((n, 2), dtype=np.float32)
+            ix, eng = make(x)
+            m, y, w = _softmax_case(rng, n, k)
+            for weights in (None, w):
+                eng.load_margins(m, k)
+                print("softmax", k, n, weights is not None, flush=True)
+                assert eng.gradients(A.LOSS_SOFTMAX, y, weights)
+                got = eng.read_gradients(k).reshape(k, n, 2)   # [class][row]
+                want = O.gradient(O.OBJ_SOFTMAX, m, y, weights, num_class=k)  # [row][class]
+                assert np.array_equal(got.view(np.uint32), want.transpose(1, 0, 2).view(np.uint32)), (k, n)
+
+
+def test_device_softmax_expf_sweep_matches_host_libm():
+    """Margins sweeping the f32 values in [-104, 0] (every 61st bit pattern,
+    through the subnormal results and the underflow to 0) against the
+    oracle's host expf: 16 classes per row, class 0 at 0."""
+    k = 16
+    xs = np.arange(0x80000000, 0xC2D00001, 61, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    n = -(-len(xs) // (k - 1))
+    m = np.zeros((n, k), np.float32)
+    flat = np.zeros(n * (k - 1), np.float32)
+    flat[:len(xs)] = xs
+    m[:, 1:] = flat.reshape(n, k - 1)
+    m = m.reshape(-1)
+    y = (np.arange(n) % k).astype(np.float32)
+    x = np.zeros((n, 1), np.float32)
+    x[::2] = 1.0
+    ix, eng = make(x)
+    eng.load_margins(m, k)
+    assert eng.gradients(A.LOSS_SOFTMAX, y)
+    got = eng.read_gradients(k)
+    want = O.gradient(O.OBJ_SOFTMAX, m, y, num_class=k)
+    bad = np.count_nonzero(got.view(np.uint32) != want.transpose(1, 0, 2).view(np.uint32))
+    assert bad == 0, f"{bad} of {got.size} values differ"
+
+
+def test_device_softmax_non_finite_rows_are_reported():
+    """Rows of -200 underflow every exponential (0/0): NaN gradients, as
+    the host's, and the gradients are reported not finite."""
+    rng = np.random.default_rng(17)
+    for k in (2, 4, 5):
+        n = 64
+        m, y, _ = _softmax_case(rng, n, k)
+        m[k * 3: k * 4] = -200.0
+        x = rng.standard_normal((n, 2), dtype=np.float32)
+        ix, eng = make(x)
+        eng.load_margins(m, k)
+        assert not eng.gradients(A.LOSS_SOFTMAX, y)
+        got = eng.read_gradients(k).transpose(1, 0, 2)
+        with np.errstate(invalid="ignore"):
+            want = O.gradient(O.OBJ_SOFTMAX, m, y, num_class=k)
+        assert np.array_equal(np.isnan(got), np.isnan(want)) and np.isnan(want[3, :, 0]).all()
+        fin = ~np.isnan(want)
+        assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))

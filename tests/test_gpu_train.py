@@ -90,6 +90,37 @@ def test_softmax_matches_oracle():
     compare_trees(model.trees, ref.trees())
 
 
+def test_softmax_two_classes_weighted_deep_and_lossguide_match_oracle():
+    """The 2-class vector batches with weights (depth 10: the walk of
+    trees too deep for its LDS table), three classes grown level by level
+    from the device's class pairs (lossguide), against the oracle."""
+    x, y = synthetic.multiclass(n=7_001, f=12, k=2, seed=5)
+    w = np.random.default_rng(5).random(len(y)).astype(np.float32) + 0.25
+    params = {"objective": "multi:softprob", "num_class": 2, "max_depth": 10, "eta": 0.3}
+    ref = O.Model(O.Dataset(x, weights=w), y, O.params(objective=O.OBJ_SOFTMAX, num_class=2, max_depth=10), 3,
+                  weights=w)
+    model = hb.train(params, hb.DMatrix(x, label=y, weight=w), 3)
+    compare_trees(model.trees, ref.trees())
+    x, y = synthetic.multiclass(n=5_000, f=7, k=3, seed=6)
+    params = {"objective": "multi:softprob", "num_class": 3, "grow_policy": "lossguide", "max_depth": 0,
+              "max_leaves": 15, "eta": 0.3}
+    ref = O.Model(O.Dataset(x), y, O.params(objective=O.OBJ_SOFTMAX, num_class=3, grow_policy=O.GROW_LOSSGUIDE,
+                                            max_depth=0, max_leaves=15), 3)
+    model = hb.train(params, hb.DMatrix(x, label=y), 3)
+    compare_trees(model.trees, ref.trees())
+
+
+def test_softmax_labels_must_be_class_indices():
+    """multiclass.rs:96-100: a label that is not a class index is refused."""
+    x, y = synthetic.multiclass(n=500, f=4, k=3, seed=7)
+    params = {"objective": "multi:softprob", "num_class": 3, "max_depth": 3}
+    for bad in (1.5, -1.0, 3.0, np.nan):
+        yb = y.copy()
+        yb[17] = bad
+        with pytest.raises(Exception, match="class indices"):
+            hb.train(params, hb.DMatrix(x, label=yb), 1)
+
+
 def test_monotone_and_regularization_match_oracle():
     x, y = synthetic.regression_100k(n=10_000, f=6, seed=4)
     mono = [1, -1, 0, 0, 1, 0]

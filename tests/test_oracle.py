@@ -309,3 +309,95 @@ def test_base_margins():
     assert abs(q - math.log(0.25 / 0.75)) < 1e-6
     ps = O.params(objective=O.OBJ_SOFTMAX, num_class=3)
     assert np.all(O.base_margins(np.array([0, 1, 2], np.float32), ps) == 0.0)
+
+
+def _sawtooth(n, period, start, step):
+    """start + (i % period) * step in f32 (simd/tests.rs:24-30)."""
+    i = (np.arange(n) % period).astype(np.float32)
+    return (np.float32(start) + i * np.float32(step)).astype(np.float32)
+
+
+def _close_pairs(actual, expected):
+    """simd/tests.rs:3-16: within 1e-6 of max(|expected|, 1)."""
+    tol = 1e-6 * np.maximum(np.abs(expected.astype(np.float64)), 1.0)
+    assert np.all(np.abs(actual.astype(np.float64) - expected) <= tol)
+
+
+def test_softmax_vector_batches_are_taken_and_close_to_scalar_rows():
+    """simd/tests.rs:116-161: the whole-matrix gradient (with the 2- and
+    4-class vector batches) against every row on the scalar path, across
+    batch boundaries; the batches differ from the scalar rows in some
+    bits, so they are the path taken."""
+    for k in (2, 3, 4, 8, 17, 32, 33, 128, 131):
+        rows = 257
+        preds = _sawtooth(rows * k, 211, -2.5, 0.025)
+        labels = (np.arange(rows) % k).astype(np.float32)
+        wv = _sawtooth(rows, 11, 0.5, 0.125)
+        for w in (None, wv):
+            full = O.gradient(O.OBJ_SOFTMAX, preds, labels, w, num_class=k)
+            scal = O.gradient(O.OBJ_SOFTMAX, preds, labels, w, num_class=k, scalar_rows=True)
+            _close_pairs(full, scal)
+            differs = not np.array_equal(full.view(np.uint32), scal.view(np.uint32))
+            assert differs == (k in (2, 4)), k
+    for k in (2, 3, 4):
+        for rows in list(range(18)) + [127, 256, 257]:
+            i = np.arange(rows * k)
+            preds = (((i * 71) % 211).astype(np.float32) * np.float32(0.375) - np.float32(39.0)).astype(np.float32)
+            labels = (np.arange(rows) % k).astype(np.float32)
+            wv = ((np.arange(rows) % 7).astype(np.float32) * np.float32(0.25)).astype(np.float32)
+            for w in (None, wv):
+                full = O.gradient(O.OBJ_SOFTMAX, preds, labels, w, num_class=k)
+                scal = O.gradient(O.OBJ_SOFTMAX, preds, labels, w, num_class=k, scalar_rows=True)
+                _close_pairs(full, scal)
+                if rows * k < 16 or k == 3:  # no batch: the scalar rows themselves
+                    assert np.array_equal(full.view(np.uint32), scal.view(np.uint32))
+
+
+def test_softmax_exceptional_rows_and_label_casts():
+    """simd/tests.rs:163-215: one exceptional margin at every position, with
+    labels and weights that exercise the casts: NaN stays NaN, infinities
+    equal, the rest within 3e-7 of the scalar rows."""
+    labels = np.array([np.nan, -2.0, np.inf, 1.5, np.finfo(np.float32).max, float(2**32 - 1), 2.0, 3.0, -np.inf],
+                      np.float32)
+    weights = np.array([0.0, 0.25, 1.0, np.nan, np.inf, -1.0, 2.0, 0.5, 1.0], np.float32)
+    fmax = np.finfo(np.float32).max
+    with np.errstate(invalid="ignore"):
+        for k in (2, 3, 4):
+            for pos in range(len(labels) * k):
+                for exc in (np.nan, np.inf, -np.inf, -81.0, 81.0, -80.0, 80.0, fmax):
+                    preds = np.zeros(len(labels) * k, np.float32)
+                    preds[pos] = exc
+                    for w in (None, weights):
+                        full = O.gradient(O.OBJ_SOFTMAX, preds, labels, w, num_class=k).astype(np.float64)
+                        scal = O.gradient(O.OBJ_SOFTMAX, preds, labels, w, num_class=k,
+                                          scalar_rows=True).astype(np.float64)
+                        nan = np.isnan(scal)
+                        assert np.array_equal(np.isnan(full), nan)
+                        inf = np.isinf(scal)
+                        assert np.array_equal(full[inf], scal[inf])
+                        ok = ~nan & ~inf
+                        assert np.all(np.abs(full[ok] - scal[ok]) <= 3e-7)
+
+
+def test_softmax_underflowing_rows_are_nan_bit_for_bit():
+    """simd/tests.rs:217-285: rows of -200 underflow every exponential under
+    the f32::MIN_POSITIVE shift (0/0): the gradient is that NaN, bit for bit
+    with the scalar rows; rows of -30 and ordinary rows stay close."""
+    for k in (2, 3, 4, 8):
+        rows = 24
+        preds = np.empty(rows * k, np.float32)
+        for r in range(rows):
+            for c in range(k):
+                preds[r * k + c] = (-200.0, -30.0, ((r * 7 + c * 5) % 11) * np.float32(0.4) - 2.0)[r % 3]
+        labels = np.array([(r * 5) % k for r in range(rows)], np.float32)
+        wv = np.array([0.5 + (r % 4) * 0.25 for r in range(rows)], np.float32)
+        for w in (None, wv):
+            with np.errstate(invalid="ignore"):
+                full = O.gradient(O.OBJ_SOFTMAX, preds, labels, w, num_class=k)
+                scal = O.gradient(O.OBJ_SOFTMAX, preds, labels, w, num_class=k, scalar_rows=True)
+            for r in range(rows):
+                if r % 3 == 0:
+                    assert np.all(np.isnan(scal[r, :, 0]))
+                    assert np.array_equal(full[r].view(np.uint32), scal[r].view(np.uint32))
+                else:
+                    _close_pairs(full[r], scal[r])
