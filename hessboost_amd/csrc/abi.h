@@ -42,8 +42,7 @@ struct QScale {
     uint32_t max_g_bits;  // |g| maximum as f32 bits (non-negative floats order as ints)
     uint32_t max_h_bits;
     uint32_t nonfinite;   // count of rows with a non-finite g or h
-    uint32_t scalar_rows; // logistic rows the vector kernel could not reproduce
-    uint32_t pad[2];
+    uint32_t pad[3];
 };
 
 // A node's rows: `len` row ids at `offset` of row buffer `buf` (0 or 1).
@@ -130,7 +129,7 @@ struct GradArgs {
     const float *weights;   // n or null
     GPair *gpair;           // n
     QScale *scale;          // max folds (atomics) land here
-    uint32_t *scalar_list;  // rows needing the host's scalar path
+    const uint64_t *exp_table;  // the expf restatement's 32 entries (scalar rows)
     uint32_t n;
     uint32_t vec_rows;      // logistic: rows covered by 8-row vectors
     uint32_t loss;

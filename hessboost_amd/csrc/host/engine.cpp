@@ -37,13 +37,6 @@ uint32_t abs_bits(float x) {
 
 // The reference's scalar logistic gradient (simd/scalar.rs:8-29 with
 // simd/mod.rs:425-427), for the rows its vector kernel leaves to libm.
-void logistic_scalar(float m, float y, float w, float spw, float min_hess, float *g, float *h) {
-    float t = std::fmin(-m, 88.7f);
-    float p = 1.0f / (std::exp(t) + 1.0f);
-    if (y == 1.0f) w *= spw;
-    *g = (p - y) * w;
-    *h = std::fmax(p * (1.0f - p), min_hess) * w;
-}
 
 }  // namespace
 
@@ -337,6 +330,7 @@ void Engine::load_margins(const float *m, uint64_t n, uint32_t outputs) {
     class_outputs_ = 0;
     margins_.resize(n);
     margins_.upload(m, n, dev_.stream());
+    if (poison_.size()) HBR_HIP(hipMemsetAsync(poison_.get(), 0, sizeof(uint32_t), dev_.stream()));
     labels_loaded_ = false;
     dev_.sync();
 }
@@ -345,14 +339,10 @@ void Engine::set_labels(const float *labels, const float *weights, uint64_t n) {
     if (n != n_rows_) fail(kInvalid, "labels: one per row");
     labels_.resize(n);
     labels_.upload(labels, n, dev_.stream());
-    labels_host_.assign(labels, labels + n);
     has_weights_ = weights != nullptr;
     if (weights) {
         weights_.resize(n);
         weights_.upload(weights, n, dev_.stream());
-        weights_host_.assign(weights, weights + n);
-    } else {
-        weights_host_.clear();
     }
     labels_loaded_ = true;
     dev_.sync();
@@ -402,6 +392,19 @@ void Engine::prepare(const float *gpair, uint64_t n) {
     if (q.nonfinite) fail(kRefused, "a staged gradient is not finite");
 }
 
+// The table of the expf restatement: bits(2^(i/32)) - (i << 47), from the
+// host's exp2 (exact: 2^(i/32) correctly rounded).
+static std::vector<uint64_t> expf_table() {
+    std::vector<uint64_t> t(32);
+    for (uint32_t i = 0; i < 32; i++) {
+        const double v = std::exp2((double)i / 32.0);
+        uint64_t b;
+        std::memcpy(&b, &v, sizeof b);
+        t[i] = b - ((uint64_t)i << 47);
+    }
+    return t;
+}
+
 GradArgs Engine::grad_args(const hbr_device_loss &loss) {
     GradArgs a{};
     a.margins = margins_.get();
@@ -409,7 +412,7 @@ GradArgs Engine::grad_args(const hbr_device_loss &loss) {
     a.weights = has_weights_ ? weights_.get() : nullptr;
     a.gpair = gpair_.get();
     a.scale = scale_dev();
-    a.scalar_list = scalar_list_.get();
+    a.exp_table = expf_table_dev();
     a.n = (uint32_t)n_rows_;
     a.vec_rows = (uint32_t)std::min<uint64_t>(loss.vector_rows, n_rows_);
     a.loss = loss.kind == HBR_LOSS_LOGISTIC ? kLogistic : kSquaredError;
@@ -426,52 +429,21 @@ void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     active_pairs_ = nullptr;
     class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
-    scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
     HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
     const GradArgs a = grad_args(loss);
     // grid-stride: a few workgroups per CU, one max fold each
     const uint32_t grad_blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)),
                                                     (uint32_t)dev_.cu_count() * 8);
     dev_.launch("hbr_gradients", dim3(grad_blocks), dim3(kThreads), a);
-    last_loss_ = loss;
 }
 
-// The rows the kernel listed (the reference computes them with libm's expf)
-// are computed here; then the exponents, on the host, and the scale goes
-// back to the device.
-bool Engine::finish_gradients_on_host(QScale host) {
-    hipStream_t s = dev_.stream();
-    if (host.scalar_rows) {
-        std::vector<uint32_t> list(host.scalar_rows);
-        scalar_list_.download(list.data(), list.size(), s);
-        std::vector<float> m;
-        const bool whole = list.size() > 4096;
-        if (whole) {
-            m.resize(n_rows_);
-            margins_.download(m.data(), n_rows_, s);
-        } else {
-            m.resize(list.size());
-            for (size_t k = 0; k < list.size(); k++) margins_.download(&m[k], 1, s, list[k]);
-        }
-        dev_.sync();
-        std::vector<GPair> fixed(list.size());
-        for (size_t k = 0; k < list.size(); k++) {
-            const uint32_t r = list[k];
-            const float mr = whole ? m[r] : m[k];
-            const float w = has_weights_ ? weights_host_[r] : 1.0f;
-            GPair &p = fixed[k];
-            logistic_scalar(mr, labels_host_[r], w, last_loss_.scale_pos_weight, last_loss_.min_hess, &p.g, &p.h);
-            if (!std::isfinite(p.g) || !std::isfinite(p.h)) host.nonfinite++;
-            host.max_g_bits = std::max(host.max_g_bits, abs_bits(p.g));
-            host.max_h_bits = std::max(host.max_h_bits, abs_bits(p.h));
-        }
-        for (size_t k = 0; k < list.size(); k++) gpair_.upload(&fixed[k], 1, s, list[k]);
-    }
-    host.scalar_rows = 0;
+// The exponents of the folded maxima, on the host (the device's rule), and
+// the scale back to the device; false when a gradient is not finite.
+bool Engine::check_scale(QScale host) {
     host.exp_g = exp_for(host.max_g_bits, n_rows_);
     host.exp_h = exp_for(host.max_h_bits, n_rows_);
     scale_host_ = host;
-    HBR_HIP(hipMemcpyAsync(scale_dev(), &scale_host_, sizeof(QScale), hipMemcpyHostToDevice, s));
+    HBR_HIP(hipMemcpyAsync(scale_dev(), &scale_host_, sizeof(QScale), hipMemcpyHostToDevice, dev_.stream()));
     dev_.sync();
     return host.nonfinite == 0;
 }
@@ -484,7 +456,7 @@ bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
     const QScale host = *q;
     stage_.reset();
     scale_checked_ = true;
-    return finish_gradients_on_host(host);
+    return check_scale(host);
 }
 
 void Engine::compute_gradients_async(const hbr_device_loss &loss, uint32_t output) {
@@ -494,17 +466,14 @@ void Engine::compute_gradients_async(const hbr_device_loss &loss, uint32_t outpu
     scale_checked_ = false;  // grow_root reads the scale back and checks it
 }
 
-// The table of the expf restatement: bits(2^(i/32)) - (i << 47), from the
-// host's exp2 (exact: 2^(i/32) correctly rounded).
-static std::vector<uint64_t> expf_table() {
-    std::vector<uint64_t> t(32);
-    for (uint32_t i = 0; i < 32; i++) {
-        const double v = std::exp2((double)i / 32.0);
-        uint64_t b;
-        std::memcpy(&b, &v, sizeof b);
-        t[i] = b - ((uint64_t)i << 47);
+const uint64_t *Engine::expf_table_dev() {
+    if (!exp_table_.size()) {
+        const std::vector<uint64_t> t = expf_table();
+        exp_table_.resize(t.size());
+        exp_table_.upload(t.data(), t.size(), dev_.stream());
+        dev_.sync();
     }
-    return t;
+    return exp_table_.get();
 }
 
 void Engine::softmax_gradients_async(float min_hess) {
@@ -513,12 +482,6 @@ void Engine::softmax_gradients_async(float min_hess) {
     if (k < 1 || k > kSoftmaxMaxClasses) fail(kRefused, "softmax gradients: 1 to 1024 classes");
     if (n_rows_ == 0) fail(kInvalid, "softmax gradients: no rows");
     hipStream_t s = dev_.stream();
-    if (!exp_table_.size()) {
-        const std::vector<uint64_t> t = expf_table();
-        exp_table_.resize(t.size());
-        exp_table_.upload(t.data(), t.size(), s);
-        dev_.sync();
-    }
     active_pairs_ = nullptr;
     class_pairs_.reserve((size_t)k * n_rows_);
     class_scales_.reserve(k);
@@ -530,7 +493,7 @@ void Engine::softmax_gradients_async(float min_hess) {
     a.weights = has_weights_ ? weights_.get() : nullptr;
     a.gpair = class_pairs_.get();
     a.scales = class_scales_.get();
-    a.exp_table = exp_table_.get();
+    a.exp_table = expf_table_dev();
     a.n = (uint32_t)n_rows_;
     a.k = k;
     // simd/mod.rs:515-519: the 2- and 4-class vector batches need 16 margins
@@ -612,9 +575,7 @@ QBin Engine::root_total(const Segment &sg) {
 // The root without a host synchronisation before its split search: the
 // total sums on the device, the histogram builds, and the scan takes the
 // total and the root gain from the device. One synchronisation then brings
-// back the winner, the total and the scale. After asynchronous gradients
-// whose kernel left rows to the host's scalar path, those rows are computed
-// here and the root is done again synchronously.
+// back the winner, the total and the scale.
 void Engine::launch_root(const Segment &seg, uint32_t slot, float lower, float upper) {
     hipStream_t s = dev_.stream();
     // a dense index's root total is the sum of any feature's bins: the scan
@@ -673,17 +634,8 @@ bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upp
     stage_.reset();
     if (scale_checked_) return true;
     scale_checked_ = true;
-    if (host.scalar_rows == 0 && host.nonfinite == 0) {
-        scale_host_ = host;
-        return true;
-    }
-    if (!finish_gradients_on_host(host)) return false;
-    *total = root_total(seg);
-    build_nodes({seg}, {slot});
-    const double g = std::ldexp((double)total->g, scale_host_.exp_g), h = std::ldexp((double)total->h, scale_host_.exp_h);
-    const Reg r{scan_params_.lambda, scan_params_.alpha, scan_params_.max_delta_step, scan_params_.min_child_weight};
-    *best = scan({ScanInput{slot, *total, xgb_node_gain(g, h, r, lower, upper), lower, upper}})[0];
-    return true;
+    scale_host_ = host;
+    return host.nonfinite == 0;
 }
 
 uint32_t Engine::alloc_slot() {
@@ -1235,33 +1187,27 @@ Engine::TreeState Engine::finish_device_tree(const TreeTicket &t, std::vector<Gr
     counters.partition_rows += gc.part_rows;
     if (scale) *scale = th.scale;
     if (!t.check) return kTreeOk;
-    if (th.scale.scalar_rows != 0 || th.scale.nonfinite != 0) return kTreeNeedsHost;
+    if (th.scale.nonfinite != 0) return kTreeNotFinite;
     scale_host_ = th.scale;
     return kTreeOk;
 }
 
-bool Engine::recover_gradients(const QScale &scale) {
+void Engine::drain() {
     dev_.sync();
     if (copy_stream_) HBR_HIP(hipStreamSynchronize(copy_stream_));
     stage_.reset();
     scale_checked_ = true;
-    if (!finish_gradients_on_host(scale)) return false;
     if (poison_.size()) {
         HBR_HIP(hipMemsetAsync(poison_.get(), 0, sizeof(uint32_t), dev_.stream()));
         dev_.sync();
     }
-    return true;
 }
 
 bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vector<GrowTreeNode> &nodes) {
-    for (;;) {
-        const TreeTicket t = queue_device_tree(max_depth, gamma, eta);
-        QScale sc;
-        if (finish_device_tree(t, nodes, &sc) == kTreeOk) return true;
-        // rows the vector kernel left to the host's scalar path: finish
-        // them, then grow the tree again from the corrected gradients
-        if (!recover_gradients(sc)) return false;
-    }
+    const TreeTicket t = queue_device_tree(max_depth, gamma, eta);
+    if (finish_device_tree(t, nodes, nullptr) == kTreeOk) return true;
+    drain();
+    return false;
 }
 
 void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss) {
@@ -1290,7 +1236,6 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss)
     active_pairs_ = nullptr;
     class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
-    scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
     if (!poison_.size()) {
         poison_.resize(1);
         guard_scale_.resize(1);
@@ -1307,7 +1252,6 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss)
     dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
     FinishArgs f{scale_dev(), n_rows_};
     dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
-    last_loss_ = *next_loss;
     scale_checked_ = false;  // the next tree's finish checks the scale
 }
 
@@ -1393,7 +1337,6 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
         active_pairs_ = nullptr;
         class_outputs_ = 0;
         gpair_.resize(n_rows_ ? n_rows_ : 1);
-        scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
         HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
         WalkGradArgs wg{};
         wg.w = a;
@@ -1401,7 +1344,6 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
         dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
         FinishArgs f{scale_dev(), n_rows_};
         dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
-        last_loss_ = *next_loss;
         scale_checked_ = false;  // grow_root reads the scale back and checks it
         return;
     }

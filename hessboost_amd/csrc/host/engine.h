@@ -99,13 +99,8 @@ public:
     // gradient is not finite.
     bool compute_gradients(const hbr_device_loss &loss, uint32_t output);
     // The same without a host synchronisation: the exponents are computed on
-    // the device and checked by the next grow_root (which finishes on the
-    // host the rows the kernel left to the scalar path). Eligible when such
-    // rows are rare (not a tail of the 8-row vectors).
+    // the device and checked by the next tree's root or finish.
     void compute_gradients_async(const hbr_device_loss &loss, uint32_t output);
-    bool gradients_async_ok(const hbr_device_loss &loss) const {
-        return loss.kind != HBR_LOSS_LOGISTIC || std::min<uint64_t>(loss.vector_rows, n_rows_) == n_rows_;
-    }
     // The root's total, histogram (into `slot`) and split search with one
     // host synchronisation; false when a gradient is not finite.
     bool grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best);
@@ -159,23 +154,23 @@ public:
     bool grow_device(uint64_t max_depth, double gamma, float eta, std::vector<GrowTreeNode> &nodes);
     // The same in two halves, so that a tree can be queued before the
     // previous one is read back: queue (no synchronisation), then finish
-    // (waits for that tree's readback only). kTreeNeedsHost: the gradients
-    // it was grown from had rows for the host's scalar path or non-finite
-    // values; recover_gradients (after the stream drains) finishes them and
-    // the tree is grown again.
+    // (waits for that tree's readback only). kTreeNotFinite: the gradients
+    // it was grown from were not all finite; its guarded walk and every
+    // later one were skipped, so the margins hold the trees before it
+    // (drain() then waits for the queued work and clears the skip flag).
     struct TreeTicket {
         uint32_t slot = 0;
         bool check = false;  // the gradients' scale is checked at finish
     };
-    enum TreeState { kTreeOk = 0, kTreeNeedsHost = 1 };
+    enum TreeState { kTreeOk = 0, kTreeNotFinite = 1 };
     TreeTicket queue_device_tree(uint64_t max_depth, double gamma, float eta);
     TreeState finish_device_tree(const TreeTicket &t, std::vector<GrowTreeNode> &nodes, QScale *scale);
-    bool recover_gradients(const QScale &scale);  // false: a gradient is not finite
+    void drain();
     // The last queued device tree's leaves onto the margins of `output`,
     // routed on the device from its records (no readback); with next_loss
     // also the next round's gradients, guarded: skipped (and every later
-    // guarded walk with it, until recover_gradients) when the tree's own
-    // gradients were not final.
+    // guarded walk with it, until drain) when the tree's own gradients were
+    // not finite.
     bool can_walk_device_tree(uint64_t max_depth) const {
         return can_grow_device(max_depth) && stride_ == 32 && max_depth <= 9 && outputs_ == 1 && labels_loaded_;
     }
@@ -249,8 +244,8 @@ private:
     void scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out);
     void launch_gradients(const hbr_device_loss &loss, uint32_t output);
     GradArgs grad_args(const hbr_device_loss &loss);
-    bool finish_gradients_on_host(QScale staged);
-    hbr_device_loss last_loss_{};
+    bool check_scale(QScale folded);
+    const uint64_t *expf_table_dev();  // the expf restatement's table, uploaded once
     bool scale_checked_ = true;  // the host has seen the scale of the staged gradients
 
     Device &dev_;
@@ -305,11 +300,9 @@ private:
     DBuf<PartSplit> g_splits_[2];
     DBuf<PartOut> g_pout_[2];
     QScale scale_host_{};
-    DBuf<uint32_t> scalar_list_;
     DBuf<uint32_t> rows_[2];
     DBuf<uint32_t> host_rows_;
     uint64_t tree_ = 0;
-    std::vector<float> labels_host_, weights_host_;
 
     // histogram slots
     DBuf<QBin> hist_;

@@ -456,10 +456,9 @@ void Trainer::grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_los
 
 // Rounds with the device a tree ahead of the host: tree t+1 and its
 // margin walk are queued before tree t is read back, so the device never
-// waits for the host. A tree whose gradients turn out not to be final
-// (logistic rows left to the host's scalar path) had its walk skipped on
-// the device, and so had every tree queued after it; the host then
-// finishes those gradients and grows the tree again.
+// waits for the host. A tree whose gradients turn out not to be finite had
+// its walk skipped on the device, and so had every tree queued after it:
+// the margins hold the trees before it, and training stops there.
 void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
     TreeBuilder b(e_, p_.grow);
     std::deque<Engine::TreeTicket> inflight;
@@ -473,17 +472,14 @@ void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
             queued++;
         }
         std::vector<GrowTreeNode> nodes;
-        QScale sc{};
-        const Engine::TreeState st = e_.finish_device_tree(inflight.front(), nodes, &sc);
+        const Engine::TreeState st = e_.finish_device_tree(inflight.front(), nodes, nullptr);
         inflight.pop_front();
-        if (st == Engine::kTreeOk) {
-            trees_.push_back(b.tree_from(nodes));
-            done++;
-            continue;
+        if (st != Engine::kTreeOk) {
+            e_.drain();
+            fail(kRefused, "a gradient is not finite");
         }
-        inflight.clear();  // grown from the unfinished gradients too
-        if (!e_.recover_gradients(sc)) fail(kRefused, "a gradient is not finite: the round runs on the host");
-        queued = done;
+        trees_.push_back(b.tree_from(nodes));
+        done++;
     }
 }
 
@@ -511,7 +507,7 @@ void Trainer::boost_softmax_pipelined(uint64_t rounds) {
         const Engine::TreeState st = e_.finish_device_tree(inflight.front(), nodes, nullptr);
         inflight.pop_front();
         if (st != Engine::kTreeOk) {
-            e_.dev().sync();
+            e_.drain();
             fail(kRefused, "a gradient is not finite");
         }
         trees_.push_back(b.tree_from(nodes));
@@ -527,11 +523,8 @@ void Trainer::boost(uint64_t rounds) {
     }
     if (p_.objective != HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE &&
         e_.can_walk_device_tree(p_.grow.max_depth)) {
-        hbr_device_loss loss = device_loss();
-        if (e_.gradients_async_ok(loss)) {
-            boost_pipelined(rounds, loss);
-            return;
-        }
+        boost_pipelined(rounds, device_loss());
+        return;
     }
     TreeBuilder b(e_, p_.grow);
     for (uint64_t it = 0; it < rounds; it++) {
@@ -545,16 +538,10 @@ void Trainer::boost(uint64_t rounds) {
             continue;
         }
         const hbr_device_loss loss = device_loss();
-        if (grads_ready_) {
-            // computed with the previous tree's margin update (checked at the root)
-        } else if (e_.gradients_async_ok(loss)) {
-            e_.compute_gradients_async(loss, 0);  // checked at the root's synchronisation
-        } else if (!e_.compute_gradients(loss, 0)) {
-            fail(kRefused, "a gradient is not finite: the round runs on the host");
-        }
-        // the margin update also computes the next round's gradients when the
-        // asynchronous path is allowed for this loss
-        grow_and_add(b, 0, e_.gradients_async_ok(loss) ? &loss : nullptr);
+        // after the first round, the previous tree's margin update computed
+        // this round's gradients; either way the root checks them
+        if (!grads_ready_) e_.compute_gradients_async(loss, 0);
+        grow_and_add(b, 0, &loss);
     }
 }
 

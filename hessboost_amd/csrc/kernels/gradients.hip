@@ -11,7 +11,9 @@
 // vec_rows (simd/mod.rs:57-66). Each intrinsic becomes the same single IEEE
 // f32 operation: _mm256_fmadd_ps/_fnmadd_ps are fmaf, _mm256_cvtps_epi32 is
 // round-to-nearest-even, divisions are correctly rounded. Rows outside that
-// path use libm's expf on the host; the kernel lists them instead.
+// path take the scalar sigmoid, 1 / (expf(min(-x, 88.7)) + 1)
+// (simd/mod.rs:425-427, simd/scalar.rs:8-29), with the host libm's expf
+// restated bit for bit.
 #include "common.h"
 #include "libm_expf.h"
 
@@ -74,13 +76,11 @@ namespace hbr {
 
 // Row i's gradient pair from margin m, label y and weight w (all lanes of
 // the wave call it together: the logistic vector test is a ballot over
-// 8-row groups). Rows the vector kernel does not cover are listed for the
-// host.
+// 8-row groups).
 __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, bool active, float m, float y, float w,
                                                 uint32_t &mg, uint32_t &mh, uint32_t &bad) {
     {
         float g = 0.0f, h = 0.0f;
-        bool host_row = false;
         if (a.loss == kSquaredError) {
             if (y == 1.0f) w *= a.scale_pos_weight;
             g = (m - y) * w;
@@ -101,20 +101,17 @@ __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, b
                 float q = p * (1.0f - p);
                 h = (q > a.min_hess ? q : a.min_hess) * ww;
             } else if (active) {
-                host_row = true;
+                const float p = 1.0f / (hbr_expf_libm(__builtin_fminf(-m, 88.7f), a.exp_table) + 1.0f);
+                const float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
+                g = (p - y) * ww;
+                h = __builtin_fmaxf(p * (1.0f - p), a.min_hess) * ww;
             }
         }
         if (active) {
-            if (host_row) {
-                uint32_t slot = atomicAdd(&a.scale->scalar_rows, 1u);
-                a.scalar_list[slot] = i;
-                a.gpair[i] = GPair{0.0f, 0.0f};
-            } else {
-                a.gpair[i] = GPair{g, h};
-                mg = max(mg, __float_as_uint(g) & 0x7fffffffu);
-                mh = max(mh, __float_as_uint(h) & 0x7fffffffu);
-                bad += (!__builtin_isfinite(g) || !__builtin_isfinite(h)) ? 1u : 0u;
-            }
+            a.gpair[i] = GPair{g, h};
+            mg = max(mg, __float_as_uint(g) & 0x7fffffffu);
+            mh = max(mh, __float_as_uint(h) & 0x7fffffffu);
+            bad += (!__builtin_isfinite(g) || !__builtin_isfinite(h)) ? 1u : 0u;
         }
     }
 }
@@ -199,7 +196,7 @@ extern "C" __global__ __launch_bounds__(64) void hbr_finish_scale(FinishArgs a) 
 extern "C" __global__ __launch_bounds__(64) void hbr_scale_rotate(RotateArgs a) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     *a.saved = *a.live;
-    *a.live = QScale{0, 0, 0u, 0u, 0u, 0u, {0u, 0u}};
+    *a.live = QScale{};
 }
 
 extern "C" __global__ __launch_bounds__(64) void hbr_scale_select(SelectArgs a) {
@@ -207,7 +204,6 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scale_select(SelectArgs a) 
     QScale q = *a.from;
     q.exp_g = exponent_for(q.max_g_bits, a.n_rows);
     q.exp_h = exponent_for(q.max_h_bits, a.n_rows);
-    q.scalar_rows = 0;
     *a.to = q;
 }
 

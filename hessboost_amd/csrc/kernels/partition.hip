@@ -366,7 +366,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
     __shared__ float s_value[kWalkLdsNodes];
     if (a.guard) {  // uniform: every workgroup reads the same words
         const QScale q = *a.guard;
-        if (q.scalar_rows != 0 || q.nonfinite != 0 || *a.poison != 0) {
+        if (q.nonfinite != 0 || *a.poison != 0) {
             if (blockIdx.x == 0 && threadIdx.x == 0) *a.poison = 1u;
             return;
         }

@@ -189,15 +189,21 @@ def test_device_gradients_match_oracle_bits():
         m = (rng.standard_normal(n) * 5).astype(np.float32)
         if n > 1000:
             m[123] = 90.0  # a vector beyond the polynomial's range
+            # the scalar sigmoid's edges: min(-x, 88.7) clamps NaN and -inf too
+            m[200:210] = [np.nan, np.inf, -np.inf, 88.7, -88.7, 88.8, -88.8, 1e30, -1e30, 103.9]
         y = (rng.random(n) < 0.4).astype(np.float32)
         w = (rng.random(n) * 2).astype(np.float32)
         for obj, kind in ((O.OBJ_LOGISTIC, A.LOSS_LOGISTIC), (O.OBJ_SQUARED_ERROR, A.LOSS_SQUARED_ERROR)):
             for weights in (None, w):
                 eng.load_margins(m)
-                assert eng.gradients(kind, y, weights, scale_pos_weight=1.5)
+                ok = eng.gradients(kind, y, weights, scale_pos_weight=1.5)
                 got = eng.read_gradients()
-                want = O.gradient(obj, m, y, weights, scale_pos_weight=1.5)
-                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, obj)
+                with np.errstate(invalid="ignore", over="ignore"):
+                    want = O.gradient(obj, m, y, weights, scale_pos_weight=1.5)
+                assert ok == bool(np.all(np.isfinite(want))), (n, obj)
+                nan = np.isnan(want)
+                assert np.array_equal(np.isnan(got), nan), (n, obj)
+                assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), (n, obj)
 
 
 def _softmax_case(rng, n, k, spread=3.0):

@@ -239,17 +239,15 @@ def test_launch_shapes_give_identical_trees(env):
     assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
 
 
-def test_pipelined_rounds_recover_rows_left_to_the_host():
+def test_pipelined_rounds_with_rows_beyond_the_vector_range():
     """Rows whose logistic margin is beyond the vector kernel's range (|m| >
-    80) get their gradients from the host's scalar path. The pipelined
-    rounds find out only when a tree is read back, after the next tree was
-    queued: the guarded walks must have left the margins alone, and the
-    trees grown again from the finished gradients must equal, bit for bit,
-    those of rounds decided by the host (which finishes the gradients
-    before the root)."""
+    80), and a tail of n % 8 rows, take the scalar sigmoid
+    (simd/mod.rs:425-427) on the device. Pipelined rounds (device-decided
+    trees, the next round's gradients in the margin walk) equal, bit for
+    bit, rounds decided by the host level by level."""
     import os
     rng = np.random.default_rng(11)
-    n, f = 20_000, 8
+    n, f = 20_003, 8
     x = rng.standard_normal((n, f)).astype(np.float32)
     y = (x[:, 0] + 0.5 * x[:, 1] > 0).astype(np.float32)
     m0 = np.zeros(n, np.float32)
