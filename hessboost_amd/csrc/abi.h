@@ -42,7 +42,8 @@ struct QScale {
     uint32_t max_g_bits;  // |g| maximum as f32 bits (non-negative floats order as ints)
     uint32_t max_h_bits;
     uint32_t nonfinite;   // count of rows with a non-finite g or h
-    uint32_t pad[3];
+    uint32_t scalar_rows; // rows listed for the scalar sigmoid (until hbr_finish_scale)
+    uint32_t pad[2];
 };
 
 // A node's rows: `len` row ids at `offset` of row buffer `buf` (0 or 1).
@@ -130,6 +131,7 @@ struct GradArgs {
     GPair *gpair;           // n
     QScale *scale;          // max folds (atomics) land here
     const uint64_t *exp_table;  // the expf restatement's 32 entries (scalar rows)
+    uint32_t *scalar_list;  // where kernels that defer the scalar rows list them
     uint32_t n;
     uint32_t vec_rows;      // logistic: rows covered by 8-row vectors
     uint32_t loss;
@@ -377,10 +379,13 @@ struct ScanArgs {
 // *root_total; otherwise *root_total holds the total already.
 constexpr uint32_t kScanDeviceRoot = 1;
 
-// Per-tree quantisation exponents from the folded maxima, on the device.
+// Per-tree quantisation exponents from the folded maxima, on the device,
+// after the rows a deferring kernel listed (grad.scalar_list, when not
+// null) have their scalar-sigmoid pairs and are folded in.
 struct FinishArgs {
     QScale *scale;
     uint64_t n_rows;
+    GradArgs grad;
 };
 
 // to = from with the exponents of n_rows rows (one thread): one class's

@@ -413,6 +413,8 @@ GradArgs Engine::grad_args(const hbr_device_loss &loss) {
     a.gpair = gpair_.get();
     a.scale = scale_dev();
     a.exp_table = expf_table_dev();
+    scalar_list_.reserve(n_rows_ ? n_rows_ : 1);
+    a.scalar_list = scalar_list_.get();
     a.n = (uint32_t)n_rows_;
     a.vec_rows = (uint32_t)std::min<uint64_t>(loss.vector_rows, n_rows_);
     a.loss = loss.kind == HBR_LOSS_LOGISTIC ? kLogistic : kSquaredError;
@@ -461,8 +463,9 @@ bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
 
 void Engine::compute_gradients_async(const hbr_device_loss &loss, uint32_t output) {
     launch_gradients(loss, output);
-    FinishArgs f{scale_dev(), n_rows_};
-    dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
+    FinishArgs f{scale_dev(), n_rows_, grad_args(loss)};
+    f.grad.scalar_list = nullptr;  // the gradient kernel lists no rows
+    dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
     scale_checked_ = false;  // grow_root reads the scale back and checks it
 }
 
@@ -1250,8 +1253,8 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss)
     wg.w = a;
     wg.g = grad_args(*next_loss);
     dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
-    FinishArgs f{scale_dev(), n_rows_};
-    dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
+    FinishArgs f{scale_dev(), n_rows_, wg.g};
+    dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
     scale_checked_ = false;  // the next tree's finish checks the scale
 }
 
@@ -1342,8 +1345,8 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
         wg.w = a;
         wg.g = grad_args(*next_loss);
         dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
-        FinishArgs f{scale_dev(), n_rows_};
-        dev_.launch("hbr_finish_scale", dim3(1), dim3(64), f);
+        FinishArgs f{scale_dev(), n_rows_, wg.g};
+        dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
         scale_checked_ = false;  // grow_root reads the scale back and checks it
         return;
     }

@@ -300,6 +300,7 @@ private:
     DBuf<PartSplit> g_splits_[2];
     DBuf<PartOut> g_pout_[2];
     QScale scale_host_{};
+    DBuf<uint32_t> scalar_list_;  // rows the fused walk defers to hbr_finish_scale
     DBuf<uint32_t> rows_[2];
     DBuf<uint32_t> host_rows_;
     uint64_t tree_ = 0;

@@ -74,9 +74,19 @@ using namespace hbr;
 
 namespace hbr {
 
+// The scalar sigmoid's pair (simd/mod.rs:425-427, simd/scalar.rs:8-29):
+// p = 1 / (expf(min(-m, 88.7)) + 1), w scaled for a label of exactly 1.
+__device__ __forceinline__ GPair logistic_scalar_pair(const GradArgs &a, float m, float y, float w) {
+    const float p = 1.0f / (hbr_expf_libm(__builtin_fminf(-m, 88.7f), a.exp_table) + 1.0f);
+    const float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
+    return GPair{(p - y) * ww, __builtin_fmaxf(p * (1.0f - p), a.min_hess) * ww};
+}
+
 // Row i's gradient pair from margin m, label y and weight w (all lanes of
 // the wave call it together: the logistic vector test is a ballot over
-// 8-row groups).
+// 8-row groups). kDefer: a row outside the vector path is listed for
+// hbr_finish_scale instead (keeping the f64 expf out of a hot loop).
+template <bool kDefer>
 __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, bool active, float m, float y, float w,
                                                 uint32_t &mg, uint32_t &mh, uint32_t &bad) {
     {
@@ -101,10 +111,13 @@ __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, b
                 float q = p * (1.0f - p);
                 h = (q > a.min_hess ? q : a.min_hess) * ww;
             } else if (active) {
-                const float p = 1.0f / (hbr_expf_libm(__builtin_fminf(-m, 88.7f), a.exp_table) + 1.0f);
-                const float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
-                g = (p - y) * ww;
-                h = __builtin_fmaxf(p * (1.0f - p), a.min_hess) * ww;
+                if (kDefer) {
+                    a.scalar_list[atomicAdd(&a.scale->scalar_rows, 1u)] = i;
+                    return;
+                }
+                const GPair q = logistic_scalar_pair(a, m, y, w);
+                g = q.g;
+                h = q.h;
             }
         }
         if (active) {
@@ -120,7 +133,7 @@ __device__ __forceinline__ void row_gradient(const GradArgs &a, uint32_t i, bool
                                              uint32_t &mh, uint32_t &bad) {
     const float y = active ? a.labels[i] : 0.0f;
     const float w = (active && a.weights) ? a.weights[i] : 1.0f;
-    row_gradient_yw(a, i, active, m, y, w, mg, mh, bad);
+    row_gradient_yw<false>(a, i, active, m, y, w, mg, mh, bad);
 }
 
 }  // namespace hbr
@@ -185,9 +198,43 @@ __device__ __forceinline__ int32_t exponent_for(uint32_t bits, uint64_t rows) {
     return e + log_n - 62;
 }
 
-extern "C" __global__ __launch_bounds__(64) void hbr_finish_scale(FinishArgs a) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    QScale q = *a.scale;
+// One workgroup: the listed rows' pairs and their maxima, merged into the
+// scale (read before anything here writes it), then the exponents.
+extern "C" __global__ __launch_bounds__(256) void hbr_finish_scale(FinishArgs a) {
+    if (blockIdx.x != 0) return;
+    const QScale start = *a.scale;
+    const uint32_t listed = a.grad.scalar_list ? start.scalar_rows : 0u;
+    uint32_t mg = 0, mh = 0, bad = 0;
+    for (uint32_t j = threadIdx.x; j < listed; j += blockDim.x) {
+        const uint32_t r = a.grad.scalar_list[j];
+        const float w = a.grad.weights ? a.grad.weights[r] : 1.0f;
+        const GPair p = logistic_scalar_pair(a.grad, a.grad.margins[r], a.grad.labels[r], w);
+        a.grad.gpair[r] = p;
+        mg = max(mg, __float_as_uint(p.g) & 0x7fffffffu);
+        mh = max(mh, __float_as_uint(p.h) & 0x7fffffffu);
+        bad += (!__builtin_isfinite(p.g) || !__builtin_isfinite(p.h)) ? 1u : 0u;
+    }
+    __shared__ uint32_t red[3][256 / kWave];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        mg = max(mg, (uint32_t)__shfl_xor((int)mg, d, kWave));
+        mh = max(mh, (uint32_t)__shfl_xor((int)mh, d, kWave));
+        bad += (uint32_t)__shfl_xor((int)bad, d, kWave);
+    }
+    if (lane_id() == 0) {
+        red[0][threadIdx.x / kWave] = mg;
+        red[1][threadIdx.x / kWave] = mh;
+        red[2][threadIdx.x / kWave] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    QScale q = start;
+    for (uint32_t w = 0; w < blockDim.x / kWave; w++) {
+        q.max_g_bits = max(q.max_g_bits, red[0][w]);
+        q.max_h_bits = max(q.max_h_bits, red[1][w]);
+        q.nonfinite += red[2][w];
+    }
+    q.scalar_rows = 0;
     q.exp_g = exponent_for(q.max_g_bits, a.n_rows);
     q.exp_h = exponent_for(q.max_h_bits, a.n_rows);
     *a.scale = q;

@@ -403,7 +403,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
                     a.margins[(size_t)r * a.m_stride + a.output] = m[k];
                 }
             }
-            if (r < end) row_gradient_yw(ga, r, active, m[k], y[k], wt[k], mg, mh, bad);
+            if (r < end) row_gradient_yw<true>(ga, r, active, m[k], y[k], wt[k], mg, mh, bad);
         }
     }
     fold_block(ga.scale, mg, mh, bad);
