@@ -3,7 +3,6 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
-#include <string>
 
 namespace hbr {
 
@@ -121,10 +120,23 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     a.n_outputs = n_outputs_;
     a.missing = missing;
     a.missing_is_nan = missing != missing ? 1u : 0u;
-    // trees resident in LDS, rows streamed: row blocks of `waves` waves plus
-    // a node table holding at least the largest tree
     const uint64_t row_block = n_cols * 65ull * sizeof(float);
     const uint64_t lds_total = 160ull * 1024;
+    // rows resident in LDS (one 64-row block per one-wave workgroup), trees
+    // streamed through the caches: the rows are read once, however large
+    // the forest (HBROCM_PRED_KERNEL=chunked selects the LDS-chunked walk)
+    const char *kind = std::getenv("HBROCM_PRED_KERNEL");
+    const bool chunked = kind && std::strcmp(kind, "chunked") == 0;
+    if (n_trees_ && compact_ok_ && !chunked && row_block <= lds_total / 4) {
+        a.compact = compact_.get();
+        const uint64_t blocks = (n + 63) / 64;
+        const uint64_t grid = std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count() * (lds_total / row_block));
+        dev_.launch(missing != missing ? "hbr_predict_resident_nan" : "hbr_predict_resident", dim3((uint32_t)grid),
+                    dim3(64), a, (uint32_t)row_block);
+        return;
+    }
+    // trees resident in LDS, rows streamed: row blocks of `waves` waves plus
+    // a node table holding at least the largest tree
     uint32_t waves = 4;
     if (const char *v = std::getenv("HBROCM_PRED_WAVES")) waves = (uint32_t)std::max(1L, std::min(4L, std::strtol(v, nullptr, 10)));
     while (waves > 1 && waves * row_block > lds_total / 2) waves--;

@@ -6,6 +6,13 @@
 // add); a present value goes left iff value < threshold, a missing one
 // follows default_left (tree/mod.rs:52-58).
 //
+// hbr_predict_resident (the default): a workgroup is one wave; it stages a
+// 64-row block in LDS once and walks it through every tree, 16 trees in
+// flight per lane, reading compact node records through the caches (below).
+// hbr_predict_chunked keeps chunks of the forest in LDS instead and
+// re-stages the rows for every chunk; it serves rows too wide for the
+// resident walk's LDS block.
+//
 // hbr_predict_staged: a workgroup is one wave and 64 rows. The rows are
 // copied into LDS feature-major (coalesced global reads; row `lane` of
 // feature f at f * 65 + lane, so lanes reading different features hit
@@ -39,6 +46,7 @@ constexpr int kPredChains = 8;
 // 16-byte aligned when the rows are, blocks starting at multiples of 64 rows) into LDS
 // feature-major, s_x[f * kPredPitch + row]. The wave's lanes read 16 bytes
 // each, consecutive, several loads in flight.
+template <bool NT = false>
 __device__ __forceinline__ void stage_rows(float *s_x, const float *src, uint32_t rows, uint32_t n_cols,
                                            uint32_t lane) {
     const uint32_t total = rows * n_cols;
@@ -47,7 +55,9 @@ __device__ __forceinline__ void stage_rows(float *s_x, const float *src, uint32_
     const float4 *src4 = reinterpret_cast<const float4 *>(src);
 #pragma unroll 5
     for (uint32_t i = lane; i < n4; i += kPredLanes) {
-        const float4 v = src4[i];
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        const f4 nv = NT ? __builtin_nontemporal_load(reinterpret_cast<const f4 *>(src4) + i) : f4{};
+        const float4 v = NT ? float4{nv.x, nv.y, nv.z, nv.w} : src4[i];
         const uint32_t e = i * 4;
         uint32_t rl = (uint32_t)((float)e * inv);  // e < 2^24: exact, then corrected
         if (rl * n_cols > e) rl--;
@@ -268,3 +278,91 @@ __device__ __forceinline__ void predict_chunked(const PredictArgs &a) {
 
 extern "C" __global__ __launch_bounds__(256) void hbr_predict_chunked_nan(PredictArgs a) { predict_chunked<true>(a); }
 extern "C" __global__ __launch_bounds__(256) void hbr_predict_chunked(PredictArgs a) { predict_chunked<false>(a); }
+
+// Rows resident, trees streamed through the caches. A workgroup is one wave;
+// it stages a 64-row block in LDS once (feature-major, as above) and walks
+// it through every tree of the forest, CH trees at a time, reading the
+// compact node records from global memory (a wave's lanes walk the same
+// trees, so a level's reads share a few cache lines and the forest stays in
+// L2/MALL). The rows are read from HBM once, however large the forest.
+template <bool MISSING_NAN, int CH, bool NT = false>
+__device__ __forceinline__ void predict_resident(const PredictArgs &a) {
+    extern __shared__ float s_rows[];
+    const uint32_t lane = lane_id();
+    const float *xr = s_rows + lane;
+    const uint32_t n_blocks = (a.n + kPredLanes - 1) / kPredLanes;
+    for (uint32_t blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
+        const uint32_t r0 = blk * kPredLanes;
+        const uint32_t rows = min(kPredLanes, a.n - r0);
+        // the previous block's walk has read its rows: lanes finish in lockstep
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        stage_rows<NT>(s_rows, a.x + (size_t)r0 * a.n_cols, rows, a.n_cols, lane);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane >= rows) continue;
+        const uint32_t r = r0 + lane;
+        float *out = a.out + (size_t)r * a.n_outputs;
+        if (a.n_outputs != 1)
+            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = a.base_score[o];
+        float acc = a.base_score[0];
+        for (uint32_t t0 = 0; t0 < a.n_trees; t0 += CH) {
+            uint32_t g[CH];
+            CompactNode nd[CH];
+#pragma unroll
+            for (int k = 0; k < CH; k++) {
+                g[k] = a.tree_root[min(t0 + (uint32_t)k, a.n_trees - 1)];
+                nd[k] = a.compact[g[k]];
+            }
+            // branch-free rounds: a chain at its leaf re-reads it, so the
+            // node loads of all chains are in flight together
+            for (;;) {
+                float v[CH];
+#pragma unroll
+                for (int k = 0; k < CH; k++) v[k] = xr[(nd[k].meta & 0xffffu) * kPredPitch];
+#pragma unroll
+                for (int k = 0; k < CH; k++) {
+                    const uint32_t meta = nd[k].meta;
+                    const bool miss = MISSING_NAN ? v[k] != v[k] : v[k] == a.missing;
+                    uint32_t right = v[k] < __uint_as_float(nd[k].value) ? 0u : 1u;
+                    right = miss ? (~meta >> 30) & 1u : right;  // missing: right unless default_left
+                    const uint32_t next = g[k] + ((meta >> 16) & 0x3fffu) + right;
+                    g[k] = (meta >> 31) ? g[k] : next;
+                }
+                bool open = false;
+#pragma unroll
+                for (int k = 0; k < CH; k++) {
+                    nd[k] = a.compact[g[k]];
+                    open = open || !(nd[k].meta >> 31);
+                }
+                if (!open) break;
+            }
+#pragma unroll
+            for (int k = 0; k < CH; k++) {
+                const uint32_t t = t0 + (uint32_t)k;
+                if (t < a.n_trees) {
+                    if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.node_orig[g[k]];
+                    const float contrib = a.tree_weight[t] * __uint_as_float(nd[k].value);
+                    if (a.n_outputs == 1) {
+                        acc = acc + contrib;
+                    } else {
+                        float *o = out + a.tree_output[t];
+                        *o = *o + contrib;
+                    }
+                }
+            }
+        }
+        if (a.n_outputs == 1) out[0] = acc;
+    }
+}
+
+// 16 trees in flight per lane (8 leave the node loads latency-bound, 32
+// gain nothing more); rows staged with non-temporal loads, so that the
+// streamed rows do not push the forest out of L2.
+extern "C" __global__ __launch_bounds__(64) void hbr_predict_resident_nan(PredictArgs a) {
+    predict_resident<true, 16, true>(a);
+}
+extern "C" __global__ __launch_bounds__(64) void hbr_predict_resident(PredictArgs a) {
+    predict_resident<false, 16, true>(a);
+}
