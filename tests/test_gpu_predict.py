@@ -42,13 +42,16 @@ def test_resident_and_chunked_walks_agree_with_the_oracle():
     """The rows-resident walk (the default: 16 trees in flight per lane,
     nodes through the caches) and the LDS-chunked walk: margins bit for bit
     with the oracle, leaves exact, on a ragged row count, a non-NaN missing
-    value and a multi-output forest."""
+    value (with NaN, inf and -0 cells) and a multi-output forest."""
     import os
     trees = synthetic.forest(n_trees=37, depth=6, n_features=23, seed=9)
     x = synthetic.predict_rows(n=3_001, f=23, seed=10)
     arrs = O.forest_arrays(trees)
     want, want_leaf = O.predict_margin(arrs, x, with_leaf=True)
     x9 = np.where(np.isnan(x), np.float32(-9.0), x).astype(np.float32)
+    x9[::97, 3] = np.nan  # NaN that is not the missing value: every comparison false, so right
+    x9[::89, 5] = np.inf
+    x9[::83, 7] = -0.0
     want9 = O.predict_margin(arrs, x9, missing=-9.0)
     multi = dict(arrs)
     multi["tree_output"] = (np.arange(len(trees)) % 3).astype(np.uint32)
