@@ -234,6 +234,8 @@ struct PartArgs {
     uint32_t words;              // bitmap words per feature
     const GrowCounts *grow;      // non-null: n_splits and n_tiles are read from here
     const uint32_t *tile_split;  // non-null: the split of every tile (else found by binary search)
+    uint32_t csr_ascending;      // every CSR row's global bins ascend: routing binary-searches them
+    uint32_t pad;
 };
 
 // ---- histograms ----------------------------------------------------------------
@@ -295,8 +297,13 @@ struct HistArgs {
     QBin *hist;                 // slots * total_bins
     QBin *partial;              // per (tile, feature group): fg * 256 bins
     uint32_t total_bins;
-    uint32_t groups;            // feature groups per tile
+    uint32_t groups;            // feature groups (dense) or bin ranges (CSR) per tile
 };
+
+// CSR histograms: a workgroup sums one tile's rows into one range of
+// kCsrGroupBins global bins in LDS.
+constexpr uint32_t kCsrGroupBins = 8192;
+constexpr uint32_t kCsrThreads = 1024;
 
 // Sum of a node's tile partials into its slot (nodes of one tile are
 // written by the histogram kernel directly).
@@ -317,13 +324,6 @@ struct SubArgs {
     const PartSplit *splits;
     uint32_t n_splits;
     QBin *hist;
-    uint32_t total_bins;
-};
-
-struct ZeroArgs {
-    QBin *hist;
-    const uint32_t *slots;
-    uint32_t n_slots;
     uint32_t total_bins;
 };
 

@@ -148,6 +148,19 @@ void Engine::upload_index(const hbr_index_desc &d) {
     row_ptr_.resize(n_rows_ + 1);
     row_ptr_.upload(d.row_ptr, n_rows_ + 1, s);
     gbins_.resize(nnz ? nnz : 1);
+    // whether every row's global bins ascend (entries in feature order)
+    csr_ascending_ = true;
+    for (uint64_t r = 0; r < n_rows_ && csr_ascending_; r++)
+        for (uint64_t e = d.row_ptr[r] + 1; e < d.row_ptr[r + 1]; e++) {
+            const uint32_t prev = d.row_bin_width == 4 ? static_cast<const uint32_t *>(d.row_bins)[e - 1]
+                                                        : static_cast<const uint16_t *>(d.row_bins)[e - 1];
+            const uint32_t cur = d.row_bin_width == 4 ? static_cast<const uint32_t *>(d.row_bins)[e]
+                                                       : static_cast<const uint16_t *>(d.row_bins)[e];
+            if (cur <= prev) {
+                csr_ascending_ = false;
+                break;
+            }
+        }
     if (d.row_bin_width == 4) {
         gbins_.upload(static_cast<const uint32_t *>(d.row_bins), nnz, s);
     } else {
@@ -704,23 +717,17 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     if (n == 0) return;
     if (!pairs_staged()) fail(kInvalid, "histograms: no gradients staged");
     if (!dense_u8_ && grow) fail(kInvalid, "histograms: device-counted levels need the dense kernels");
-    hipStream_t s = dev_.stream();
     const uint32_t fg = hist_features_per_group;
-    const uint32_t groups = dense_u8_ ? ceil_div(n_cols_, fg) : 1;
-    // LDS per workgroup is fg features x 257 words x 16 bytes of 160 KiB
-    const uint32_t per_cu = !dense_u8_ ? 4 : fg <= 8 ? 4 : fg <= 16 ? 2 : 1;
+    // dense: feature groups of fg features; CSR: ranges of kCsrGroupBins
+    // global bins (every range of every tile is written: no slot zeroing)
+    const uint32_t groups = dense_u8_ ? ceil_div(n_cols_, fg) : ceil_div(total_bins_, kCsrGroupBins);
+    // LDS per workgroup: fg features x 257 words x 16 bytes, or 128 KiB, of 160 KiB
+    const uint32_t per_cu = !dense_u8_ ? 1 : fg <= 8 ? 4 : fg <= 16 ? 2 : 1;
     const uint32_t target = std::max<uint32_t>(1, (uint32_t)dev_.cu_count() * per_cu * hist_waves / groups);
-    if (!dense_u8_) {
-        if (!host_nodes) fail(kInvalid, "histograms: sparse nodes need their slots on the host");
-        std::vector<uint32_t> slots(n);
-        for (uint32_t i = 0; i < n; i++) slots[i] = (*host_nodes)[i].slot;
-        upload_vec(d_slots_, slots, stage_, s);
-        ZeroArgs z{hist_.get(), d_slots_.get(), n, total_bins_};
-        dev_.launch("hbr_zero_slots", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), n), dim3(256), z);
-    }
+    (void)host_nodes;
     d_htiles_.reserve(target + n);
     d_hcounts_.reserve(4);
-    if (dense_u8_) d_partial_.reserve((size_t)2 * target * groups * fg * 256);
+    d_partial_.reserve((size_t)(dense_u8_ ? 2 * target : target + n) * groups * (dense_u8_ ? fg * 256 : kCsrGroupBins));
 
     HistNode *nodes_rw = const_cast<HistNode *>(nodes_dev);  // the plan kernel resolves them in place
     PlanArgs p{};
@@ -759,7 +766,16 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
                     : fg <= 8  ? "hbr_hist_dense8_fg8"
                     : fg <= 16 ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
                                : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");
-    dev_.launch(k, dim3((target + n) * groups), dim3(dense_u8_ ? hist_threads : kHistThreads), a);
+    dev_.launch(k, dim3((target + n) * groups), dim3(dense_u8_ ? hist_threads : kCsrThreads), a);
+    if (!dense_u8_) {
+        ReduceArgs r{};
+        r.nodes = nodes_dev;
+        r.partial = d_partial_.get();
+        r.hist = hist_.get();
+        r.total_bins = total_bins_;
+        r.groups = groups;
+        dev_.launch("hbr_hist_reduce_csr", dim3(ceil_div(total_bins_, 256), n), dim3(256), r);
+    }
     if (dense_u8_) {
         ReduceArgs r{};
         r.nodes = nodes_dev;
@@ -890,6 +906,7 @@ PartArgs Engine::part_args() const {
     a.missing = missing_.size() ? missing_.get() : nullptr;
     a.row_ptr = row_ptr_.get();
     a.gbins = gbins_.get();
+    a.csr_ascending = csr_ascending_ ? 1u : 0u;
     a.feature_offset = d_fo_.get();
     a.n_rows = (uint32_t)n_rows_;
     a.words = words_;

@@ -199,6 +199,7 @@ private:
     void bin_dense(const DenseSource &src);
     void read_tunables();
     uint64_t entries_ = 0;
+    bool csr_ascending_ = true;  // every CSR row's global bins ascend (device binning writes them so)
     void ensure_rows();
     bool contiguous(const Segment &sg) const;
     bool identity_rows0_ = false;
@@ -318,7 +319,7 @@ private:
     // per-call scratch
     Stage stage_;
     DBuf<PartSplit> d_splits_;
-    DBuf<uint32_t> d_tile_left_, d_slots_, d_tile_split_;
+    DBuf<uint32_t> d_tile_left_, d_tile_split_;
     DBuf<uint8_t> d_level_in_, d_level_out_;  // one level's records (bytes)
     DBuf<HistNode> d_hnodes_;
     DBuf<HistTile> d_htiles_;

@@ -161,26 +161,66 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
     }
 }
 
+// Sparse rows into one range of kCsrGroupBins global bins, privately in
+// LDS: the workgroup's 16 waves take the tile's rows, each wave four rows
+// at a time (their row pointers, pairs and entries loaded together), its
+// lanes 64 entries of a row at a time; an entry in the range adds its
+// row's quantised pair with LDS atomics. Then the range goes to the node's
+// slot (a node of one tile) or to the tile's partial, summed by
+// hbr_hist_reduce_csr. Every range of every tile is written, so slots need
+// no zeroing.
+constexpr uint32_t kCsrRows = 4;
+
 __device__ __forceinline__ void hist_csr(const HistArgs &a) {
-    const uint32_t entry = blockIdx.x;
-    if (entry >= a.counts[0]) return;
+    __shared__ unsigned long long s_g[kCsrGroupBins], s_h[kCsrGroupBins];
+    const uint32_t entry = blockIdx.x / a.groups, grp = blockIdx.x % a.groups;
+    if (entry >= a.counts[0]) return;  // uniform across the workgroup
     const HistTile t = a.tiles[entry];
     const HistNode nd = a.nodes[t.node];
+    const uint32_t lo_bin = grp * kCsrGroupBins;
+    const uint32_t nb = min(kCsrGroupBins, a.total_bins - lo_bin);
+    for (uint32_t i = threadIdx.x; i < nb; i += blockDim.x) s_g[i] = s_h[i] = 0ull;
+    __syncthreads();
     const int eg = a.scale->exp_g, eh = a.scale->exp_h;
     const uint32_t *rows = a.rows[nd.seg.buf] + nd.seg.offset;
-    QBin *dst = a.hist + (size_t)nd.slot * a.total_bins;
     const uint32_t end = t.row0 + t.rows;
-    for (uint32_t j = t.row0 + threadIdx.x; j < end; j += blockDim.x) {
-        const uint32_t r = nd.contiguous ? nd.seg.offset + j : rows[j];
-        const GPair p = a.gpair[r];
-        const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
-        const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
-        for (uint64_t e = a.row_ptr[r]; e < a.row_ptr[r + 1]; e++) {
-            const uint32_t gb = a.gbins[e];
-            atomicAdd((unsigned long long *)&dst[gb].g, qg);
-            atomicAdd((unsigned long long *)&dst[gb].h, qh);
+    const uint32_t wave = threadIdx.x / kWave, waves = blockDim.x / kWave, lane = lane_id();
+    for (uint32_t j0 = t.row0 + wave; j0 < end; j0 += kCsrRows * waves) {
+        uint64_t b[kCsrRows], e[kCsrRows];
+        unsigned long long qg[kCsrRows], qh[kCsrRows];
+        uint32_t iters = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < kCsrRows; u++) {
+            const uint32_t j = j0 + u * waves;
+            const bool ok = j < end;
+            const uint32_t r = ok ? (nd.contiguous ? nd.seg.offset + j : rows[j]) : 0u;
+            b[u] = ok ? a.row_ptr[r] : 0ull;
+            e[u] = ok ? a.row_ptr[r + 1] : 0ull;
+            const GPair p = ok ? a.gpair[r] : GPair{0.0f, 0.0f};
+            qg[u] = (unsigned long long)quantize(p.g, eg);
+            qh[u] = (unsigned long long)quantize(p.h, eh);
+            iters = max(iters, (uint32_t)((e[u] - b[u] + kWave - 1) / kWave));
+        }
+        for (uint32_t k = 0; k < iters; k++) {
+            uint32_t d[kCsrRows];
+#pragma unroll
+            for (uint32_t u = 0; u < kCsrRows; u++) {
+                const uint64_t x = b[u] + (uint64_t)k * kWave + lane;
+                d[u] = x < e[u] ? a.gbins[x] - lo_bin : 0xffffffffu;
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kCsrRows; u++) {
+                if (d[u] < nb) {
+                    atomicAdd(&s_g[d[u]], qg[u]);
+                    atomicAdd(&s_h[d[u]], qh[u]);
+                }
+            }
         }
     }
+    __syncthreads();
+    QBin *dst = nd.n_tiles == 1 ? a.hist + (size_t)nd.slot * a.total_bins + lo_bin
+                                : a.partial + ((size_t)(nd.pad[0] + t.k) * a.groups + grp) * kCsrGroupBins;
+    for (uint32_t i = threadIdx.x; i < nb; i += blockDim.x) dst[i] = QBin{(int64_t)s_g[i], (int64_t)s_h[i]};
 }
 
 }  // namespace hbr
@@ -308,7 +348,7 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16(HistArgs
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32(HistArgs a) { hist_dense8<32, false>(a); }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16_bm(HistArgs a) { hist_dense8<16, true>(a); }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm(HistArgs a) { hist_dense8<32, true>(a); }
-extern "C" __global__ __launch_bounds__(512) void hbr_hist_csr(HistArgs a) { hist_csr(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_csr(HistArgs a) { hist_csr(a); }
 
 // Nodes cut into several tiles: the slot is the sum of the tiles' partials.
 // A workgroup takes 64 bins of one feature of one node; its 16 waves split
@@ -349,6 +389,22 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_hist_reduce(ReduceArgs a)
     }
 }
 
+// Nodes of several tiles (CSR): slot bin b = the sum of the tiles' partials.
+extern "C" __global__ __launch_bounds__(256) void hbr_hist_reduce_csr(ReduceArgs a) {
+    const HistNode nd = a.nodes[blockIdx.y];
+    const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (nd.n_tiles == 1 || b >= a.total_bins) return;
+    const QBin *src = a.partial + (size_t)nd.pad[0] * a.groups * kCsrGroupBins + (size_t)(b / kCsrGroupBins) * kCsrGroupBins +
+                      b % kCsrGroupBins;
+    int64_t g = 0, h = 0;
+    for (uint32_t k = 0; k < nd.n_tiles; k++) {
+        const QBin q = src[(size_t)k * a.groups * kCsrGroupBins];
+        g += q.g;
+        h += q.h;
+    }
+    a.hist[(size_t)nd.slot * a.total_bins + b] = QBin{g, h};
+}
+
 // sibling = parent - built (exact in integers), in the parent's slot.
 extern "C" __global__ __launch_bounds__(256) void hbr_subtract(SubArgs a) {
     const uint32_t s = blockIdx.y;
@@ -365,10 +421,3 @@ extern "C" __global__ __launch_bounds__(256) void hbr_subtract(SubArgs a) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void hbr_zero_slots(ZeroArgs a) {
-    const uint32_t s = blockIdx.y;
-    if (s >= a.n_slots) return;
-    QBin *h = a.hist + (size_t)a.slots[s] * a.total_bins;
-    for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < a.total_bins; b += gridDim.x * blockDim.x)
-        h[b] = QBin{0, 0};
-}

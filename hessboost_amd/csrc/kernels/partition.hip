@@ -28,10 +28,26 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
         const uint32_t local = a.cols8 ? (uint32_t)a.cols8[at] : (uint32_t)a.cols16[at];
         return local < sp.limit;
     }
+    // a row's global bins ascend (its entries are in feature order, and a
+    // feature's bins follow the previous feature's): the first bin >= fs,
+    // by binary search, is the feature's entry if it lies below fe
     const uint32_t fs = a.feature_offset[sp.feature], fe = a.feature_offset[sp.feature + 1];
-    for (uint64_t e = a.row_ptr[r]; e < a.row_ptr[r + 1]; e++) {
-        const uint32_t gb = a.gbins[e];
-        if (gb >= fs && gb < fe) return gb - fs < sp.limit;
+    if (!a.csr_ascending) {  // entries in the caller's order: scan them
+        for (uint64_t e = a.row_ptr[r]; e < a.row_ptr[r + 1]; e++) {
+            const uint32_t gb = a.gbins[e];
+            if (gb >= fs && gb < fe) return gb - fs < sp.limit;
+        }
+        return sp.default_left != 0;
+    }
+    uint64_t lo = a.row_ptr[r], hi = a.row_ptr[r + 1];
+    while (lo < hi) {
+        const uint64_t mid = lo + (hi - lo) / 2;
+        if (a.gbins[mid] < fs) lo = mid + 1;
+        else hi = mid;
+    }
+    if (lo < a.row_ptr[r + 1]) {
+        const uint32_t gb = a.gbins[lo];
+        if (gb < fe) return gb - fs < sp.limit;
     }
     return sp.default_left != 0;
 }

@@ -40,6 +40,26 @@ def test_c3_shape_sparse_missing_lossguide_matches_oracle():
         "no split sent missing values left"
 
 
+def test_csr_rows_in_any_column_order_give_the_same_trees():
+    """Routing binary-searches a row's ascending global bins; a CSR whose
+    rows list their columns out of order keeps the caller's entry order in
+    the index, so routing scans the row instead. Both give the oracle's
+    trees (two 8,192-bin ranges per tile: 150 features x 64 bins)."""
+    (row_ptr, col, val), y, _ = synthetic.sparse_wide(n=12_000, f=150, density=0.2, seed=8)
+    rng = np.random.default_rng(8)
+    col_s, val_s = col.copy(), val.copy()
+    for r in range(len(row_ptr) - 1):
+        a, b = int(row_ptr[r]), int(row_ptr[r + 1])
+        p = rng.permutation(b - a)
+        col_s[a:b], val_s[a:b] = col[a:b][p], val[a:b][p]
+    params = {"grow_policy": "lossguide", "max_depth": 0, "max_leaves": 63, "eta": 0.3, "max_bin": 64}
+    ds = O.Dataset(csr=(row_ptr, col, val), n_cols=150, max_bin=64)
+    ref = O.Model(ds, y, O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=0, max_leaves=63, eta=0.3, max_bin=64), 2)
+    for c, v in ((col, val), (col_s, val_s)):
+        model = hb.train(params, hb.DMatrix((row_ptr, c, v), label=y, n_cols=150), 2)
+        compare_trees(model.trees, ref.trees())
+
+
 def test_c4_shape_softmax_matches_oracle():
     x, y = synthetic.multiclass(n=50_000, f=50, k=10, seed=0)
     params = {"objective": "multi:softprob", "num_class": 10, "max_depth": 6, "eta": 0.3, "max_bin": 256}
