@@ -202,8 +202,8 @@ struct PartSplit {
     uint32_t tile_begin;    // first partition tile of this split
     uint32_t fresh_slot;    // histogram slot for the built child
     uint32_t parent_slot;   // parent's slot, becomes the sibling's
-    uint32_t identity;      // the parent's rows are seg.offset + j (no row list is read)
-    uint32_t pad;
+    uint32_t identity;      // the parent's rows are j (seg.offset % n_rows + j; no row list is read)
+    uint32_t tree;          // tree of a batched level (the class of a softmax round)
 };
 
 // Device decision per split after the scan of tile counts.
@@ -262,6 +262,9 @@ struct HistNode {
     uint32_t pad[2];     // [0]: first partial of a multi-tile node; [1]: parent slot + 1 of a
                          // split's built child, whose sibling = parent - built as bins complete
                          // (dense kernels; both written by the plan kernel)
+    uint32_t cls;        // class (tree) of a batched level: pairs at gpair + cls * class_rows,
+                         // quantised with scale[cls]
+    uint32_t pad2[3];
 };
 
 // Device tiling of a histogram launch: each node's rows cut into tiles of
@@ -298,6 +301,8 @@ struct HistArgs {
     QBin *partial;              // per (tile, feature group): fg * 256 bins
     uint32_t total_bins;
     uint32_t groups;            // feature groups (dense) or bin ranges (CSR) per tile
+    uint32_t class_rows;        // batched levels: the pairs of class c start at gpair + c * class_rows
+    uint32_t pad;
 };
 
 // CSR histograms: a workgroup sums one tile's rows into one range of
@@ -336,7 +341,7 @@ struct ScanNode {
     QBin total;              // node statistics (fixed point)
     float root_gain;
     float lower, upper;
-    uint32_t pad;
+    uint32_t pad;            // flags (kScanDeviceRoot) | class << kScanClassShift
 };
 
 struct ScanParams {
@@ -378,6 +383,7 @@ struct ScanArgs {
 // scan sums them itself and the feature-0 wave stores the sum in
 // *root_total; otherwise *root_total holds the total already.
 constexpr uint32_t kScanDeviceRoot = 1;
+constexpr uint32_t kScanClassShift = 8;
 
 // Per-tree quantisation exponents from the folded maxima, on the device,
 // after the rows a deferring kernel listed (grad.scalar_list, when not
@@ -386,6 +392,13 @@ struct FinishArgs {
     QScale *scale;
     uint64_t n_rows;
     GradArgs grad;
+};
+
+// Every class's exponents from its folded maxima, in place (one thread per class).
+struct ScalesArgs {
+    QScale *scales;
+    uint32_t k;
+    uint64_t n_rows;
 };
 
 // to = from with the exponents of n_rows rows (one thread): one class's
@@ -409,8 +422,9 @@ struct RotateArgs {
 struct GrowNode {
     QBin total;
     double lower, upper;
-    uint32_t nid;
-    uint32_t pad[3];
+    uint32_t nid;           // id within its tree
+    uint32_t tree;          // tree of a batched level
+    uint32_t pad[2];
 };
 
 // One node of the device-grown tree; the right child is left + 1.
@@ -466,11 +480,19 @@ struct GrowArgs {
     float eta;
     uint32_t front_cap;           // the most frontier nodes this level can have (records read ahead)
     uint32_t n_features;
-    uint32_t pad;
+    // A batched level grows n_trees trees at once (level 0: their roots, root
+    // t in slot root_slot + t with root_total[t], best[t], scale[t]); tree t's
+    // header and nodes sit tree_bytes after tree t - 1's, and tree_nodes[t]
+    // counts its nodes. The frontier is in tree order.
+    uint32_t n_trees;
+    uint32_t tree_bytes;
+    uint32_t *tree_nodes;
 };
 
 // Most slots a device-grown tree may hold (the LDS free-slot table).
 constexpr uint32_t kGrowMaxSlots = 4096;
+// Most trees a batched level may hold.
+constexpr uint32_t kGrowMaxTrees = 256;
 
 // ---- leaves -----------------------------------------------------------------------
 struct LeafSeg {

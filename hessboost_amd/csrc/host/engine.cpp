@@ -715,7 +715,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
                          const PartSplit *splits_dev, const PartOut *part_out_dev, const uint32_t *rows0,
                          const GrowCounts *grow) {
     if (n == 0) return;
-    if (!pairs_staged()) fail(kInvalid, "histograms: no gradients staged");
+    if (!level_pairs_ && !pairs_staged()) fail(kInvalid, "histograms: no gradients staged");
     if (!dense_u8_ && grow) fail(kInvalid, "histograms: device-counted levels need the dense kernels");
     const uint32_t fg = hist_features_per_group;
     // dense: feature groups of fg features; CSR: ranges of kCsrGroupBins
@@ -749,8 +749,9 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.counts = d_hcounts_.get();
     a.rows[0] = rows0 ? rows0 : rows_[0].get();
     a.rows[1] = rows_[1].get();
-    a.gpair = pairs();
-    a.scale = scale_dev();
+    a.gpair = level_pairs_ ? level_pairs_ : pairs();
+    a.scale = level_scale_ ? level_scale_ : scale_dev();
+    a.class_rows = level_pairs_ ? (uint32_t)n_rows_ : 0u;
     a.bins8 = rows8_.get();
     a.stride = stride_;
     a.n_cols = n_cols_;
@@ -836,12 +837,12 @@ void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit 
     a.total_bins = total_bins_;
     a.feature_offset = d_fo_.get();
     a.monotone = has_monotone_ ? monotone_.get() : nullptr;
-    a.scale = scale_dev();
+    a.scale = level_scale_ ? level_scale_ : scale_dev();
     a.reg = scan_params_;
     a.dense = dense_ ? 1u : 0u;
     a.per_feature = d_per_feature_.get();
     a.best = best_dev;
-    a.root_total = total_dev();
+    a.root_total = level_totals_ ? level_totals_ : total_dev();
     a.grow = grow;
     dev_.launch("hbr_scan_features", dim3(ceil_div(pairs, 4)), dim3(256), a);
     dev_.launch("hbr_scan_merge", dim3(n), dim3(64), a);
@@ -1038,117 +1039,178 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
 // hold (2^level splits, every row in a split); the kernels read the real
 // counts from the device. The tree, its counts and the scale come back with
 // one copy after the last level.
-bool Engine::can_grow_device(uint64_t max_depth) const {
+bool Engine::can_grow_device(uint64_t max_depth, uint32_t n_trees) const {
     if (!device_grow || !dense_u8_ || max_depth < 1 || max_depth > kMaxDeviceDepth || n_rows_ == 0) return false;
-    const uint64_t slots = uint64_t(1) << (max_depth - 1);
+    if (n_trees < 1 || n_trees > kGrowMaxTrees || (uint64_t)n_trees * n_rows_ > UINT32_MAX) return false;
+    const uint64_t slots = (uint64_t)n_trees << (max_depth - 1);
     if (slots > kGrowMaxSlots) return false;
+    // the decision kernel's table of each split's first tile
+    if ((uint64_t)n_trees * (max_depth >= 2 ? uint64_t(1) << (max_depth - 2) : 1) > kGrowMaxSlots / 2) return false;
     // surplus scan workgroups stay few: both children of every possible split
-    const uint64_t pmax = max_depth >= 2 ? uint64_t(1) << (max_depth - 2) : 1;
+    const uint64_t pmax = (uint64_t)n_trees * (max_depth >= 2 ? uint64_t(1) << (max_depth - 2) : 1);
     if (2 * pmax * n_cols_ > (uint64_t(1) << 22)) return false;
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return false;
     return std::max<uint64_t>(slots, slot_cap_) * (uint64_t)total_bins_ * sizeof(QBin) <= free_b / 2;
 }
 
-// The root of a device-grown tree: its histogram and scan records never
-// change (all rows as the identity run, slot 0, unbounded), so they are
-// uploaded once.
-void Engine::launch_device_root() {
-    struct RootIn {
-        HistNode h;
-        ScanNode s;
-    };
-    if (d_root_in_.size() < sizeof(RootIn)) {
-        RootIn r{};
-        r.h.seg = Seg{0, (uint32_t)n_rows_, 0, 0};
-        r.h.slot = 0;
-        r.h.contiguous = 1;
-        r.s.slot = 0;
-        r.s.lower = -std::numeric_limits<float>::infinity();
-        r.s.upper = std::numeric_limits<float>::infinity();
-        r.s.pad = kScanDeviceRoot;
-        d_root_in_.resize(sizeof(RootIn));
-        HBR_HIP(hipMemcpy(d_root_in_.get(), &r, sizeof(RootIn), hipMemcpyHostToDevice));
+// The roots of a device-grown batch of n_trees trees: their histogram and
+// scan records (all rows as the identity run, root t in slot t, of class t,
+// unbounded) never change, so they are uploaded once per batch size.
+void Engine::launch_device_roots(uint32_t n_trees) {
+    const size_t bytes = n_trees * (sizeof(HistNode) + sizeof(ScanNode));
+    if (root_in_trees_ != n_trees) {
+        std::vector<uint8_t> host(bytes);
+        HistNode *hn = reinterpret_cast<HistNode *>(host.data());
+        ScanNode *sn = reinterpret_cast<ScanNode *>(host.data() + n_trees * sizeof(HistNode));
+        for (uint32_t t = 0; t < n_trees; t++) {
+            HistNode h{};
+            h.seg = Seg{0, (uint32_t)n_rows_, 0, 0};
+            h.slot = t;
+            h.contiguous = 1;
+            h.cls = t;
+            hn[t] = h;
+            ScanNode r{};
+            r.slot = t;
+            r.lower = -std::numeric_limits<float>::infinity();
+            r.upper = std::numeric_limits<float>::infinity();
+            r.pad = kScanDeviceRoot | (t << kScanClassShift);
+            sn[t] = r;
+        }
+        d_root_in_.resize(bytes);
+        HBR_HIP(hipMemcpy(d_root_in_.get(), host.data(), bytes, hipMemcpyHostToDevice));
+        root_in_trees_ = n_trees;
     }
     hipStream_t s = dev_.stream();
+    QBin *totals = level_totals_ ? level_totals_ : total_dev();
     if (!(dense_ && n_cols_ > 0 && fo_[1] > fo_[0])) {
-        HBR_HIP(hipMemsetAsync(total_dev(), 0, sizeof(QBin), s));
-        TotalArgs t{};
-        t.rows = nullptr;
-        t.first = 0;
-        t.n = (uint32_t)n_rows_;
-        t.gpair = pairs();
-        t.scale = scale_dev();
-        t.out = total_dev();
-        dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)), 2048)),
-                    dim3(kThreads), t);
+        HBR_HIP(hipMemsetAsync(totals, 0, n_trees * sizeof(QBin), s));
+        for (uint32_t t = 0; t < n_trees; t++) {
+            TotalArgs a{};
+            a.rows = nullptr;
+            a.first = 0;
+            a.n = (uint32_t)n_rows_;
+            a.gpair = (level_pairs_ ? level_pairs_ : pairs()) + (level_pairs_ ? (size_t)t * n_rows_ : 0);
+            a.scale = (level_scale_ ? level_scale_ : scale_dev()) + t;
+            a.out = totals + t;
+            dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)), 2048)),
+                        dim3(kThreads), a);
+        }
     }
-    counters.hist_nodes++;
-    counters.hist_rows += n_rows_;
-    counters.hist_bytes += hist_bytes(n_rows_, false);
-    RootIn *rdev = reinterpret_cast<RootIn *>(d_root_in_.get());
-    launch_hist(&rdev->h, 1, nullptr, nullptr, nullptr);
-    launch_scan(&rdev->s, 1, nullptr, nullptr, root_best_dev());
+    counters.hist_nodes += n_trees;
+    counters.hist_rows += n_trees * n_rows_;
+    counters.hist_bytes += n_trees * hist_bytes(n_rows_, false);
+    const HistNode *hn = reinterpret_cast<const HistNode *>(d_root_in_.get());
+    const ScanNode *sn = reinterpret_cast<const ScanNode *>(d_root_in_.get() + n_trees * sizeof(HistNode));
+    launch_hist(hn, n_trees, nullptr, nullptr, nullptr);
+    launch_scan(sn, n_trees, nullptr, nullptr, n_trees == 1 ? root_best_dev() : d_best_.get());
 }
 
 Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, float eta) {
-    if (!can_grow_device(max_depth)) fail(kInvalid, "device growth: index or depth not supported");
     if (!pairs_staged()) fail(kInvalid, "device growth: no gradients staged");
+    return queue_device_forest(1, max_depth, gamma, eta);
+}
+
+Engine::TreeTicket Engine::queue_class_trees(uint64_t max_depth, double gamma, float eta) {
+    if (!softmax_staged()) fail(kInvalid, "device growth: no softmax gradients staged");
+    const uint32_t k = class_outputs_;
+    if (k > kGrowMaxTrees) fail(kRefused, "device growth: at most 256 class trees per batch");
+    // every class's exponents from its folded maxima
+    ScalesArgs f{class_scales_.get(), k, n_rows_};
+    dev_.launch("hbr_class_scales_finish", dim3(ceil_div(k, 64)), dim3(64), f);
+    d_root_totals_.reserve(k);
+    counters.trees += k - 1;  // begin_tree counted one
+    scale_checked_ = false;   // each class's scale is checked at finish
+    level_pairs_ = class_pairs_.get();
+    level_scale_ = class_scales_.get();
+    level_totals_ = d_root_totals_.get();
+    try {
+        const TreeTicket t = queue_device_forest(k, max_depth, gamma, eta);
+        level_pairs_ = nullptr;
+        level_scale_ = nullptr;
+        level_totals_ = nullptr;
+        return t;
+    } catch (...) {
+        level_pairs_ = nullptr;
+        level_scale_ = nullptr;
+        level_totals_ = nullptr;
+        throw;
+    }
+}
+
+Engine::TreeTicket Engine::queue_device_forest(uint32_t n_trees, uint64_t max_depth, double gamma, float eta) {
+    if (!can_grow_device(max_depth, n_trees)) fail(kInvalid, "device growth: index or depth not supported");
     hipStream_t s = dev_.stream();
     const uint32_t depth = (uint32_t)max_depth;
-    const uint32_t slot_cap = 1u << (depth - 1);
+    const uint32_t slot_cap = n_trees << (depth - 1);
     if (!reserve_slots(slot_cap)) fail(kRefused, "histogram slots do not fit in device memory");
-    const uint32_t pmax_all = depth >= 2 ? 1u << (depth - 2) : 1u;
-    const uint32_t row_tiles = ceil_div(n_rows_, kPartTile);
+    const uint32_t pmax_all = n_trees * (depth >= 2 ? 1u << (depth - 2) : 1u);
+    // every level partitions at most n_trees x n_rows rows, each tree's in its own region
+    const uint32_t row_tiles = (uint32_t)ceil_div((uint64_t)n_trees * n_rows_, kPartTile);
     for (int b = 0; b < 2; b++) {
-        g_front_[b].reserve(slot_cap);
+        g_front_[b].reserve(std::max<uint32_t>(slot_cap, n_trees));
         g_splits_[b].reserve(pmax_all);
         g_pout_[b].reserve(pmax_all);
     }
+    for (auto &r : rows_) r.reserve((size_t)n_trees * (n_rows_ ? n_rows_ : 1));
     d_hnodes_.reserve(pmax_all);
     d_snodes_.reserve(2 * pmax_all);
-    d_best_.reserve(2 * pmax_all);
+    d_best_.reserve(std::max<uint32_t>(2 * pmax_all, n_trees));
     d_tile_left_.reserve(row_tiles + pmax_all);
     d_decisions_.reserve((size_t)(row_tiles + pmax_all) * (kPartTile / 64));
     d_tile_split_.reserve(row_tiles + pmax_all);
+    d_tree_nodes_.reserve(n_trees);
     GrowCounts *counts = grow_counts_dev();
 
+    // tree t of a ring slot: its header, then its nodes, at t * stride
+    const size_t n_max = (size_t(2) << depth) - 1;
+    const size_t stride = (kTreeHeaderBytes + n_max * sizeof(GrowTreeNode) + 255) / 256 * 256;
+    const size_t slot_bytes = n_trees * stride;
     if (!copy_stream_) {
         HBR_HIP(hipStreamCreate(&copy_stream_));
-        d_tree_ring_.resize(kTreeRing * ring_bytes());
         for (uint32_t r = 0; r < kTreeRing; r++) {
             HBR_HIP(hipEventCreateWithFlags(&tree_ready_[r], hipEventDisableTiming));
             HBR_HIP(hipEventCreateWithFlags(&tree_copied_[r], hipEventDisableTiming));
         }
     }
+    if (slot_bytes > ring_slot_bytes_) {
+        // nothing may still read or copy the old ring
+        dev_.sync();
+        HBR_HIP(hipStreamSynchronize(copy_stream_));
+        d_tree_ring_.resize(kTreeRing * slot_bytes);
+        ring_slot_bytes_ = slot_bytes;
+    }
     TreeTicket t;
-    last_depth_ = depth;
     t.slot = tree_seq_++ % kTreeRing;
     t.check = !scale_checked_;
+    t.n_trees = n_trees;
+    t.stride = stride;
     scale_checked_ = true;
     last_ring_ = t.slot;
-    // the slot's previous tree must have been read back before it is overwritten
+    last_stride_ = stride;
+    last_depth_ = depth;
+    // the slot's previous batch must have been read back before it is overwritten
     if (ring_used_[t.slot]) HBR_HIP(hipStreamWaitEvent(s, tree_copied_[t.slot], 0));
     ring_used_[t.slot] = true;
-    launch_device_root();
+    launch_device_roots(n_trees);
     for (uint32_t lv = 0; lv < depth; lv++) {
         const bool terminal = lv + 1 >= depth;
-        const uint32_t pmax = (uint32_t)std::min<uint64_t>(uint64_t(1) << lv, n_rows_);
+        const uint32_t pmax = (uint32_t)std::min<uint64_t>((uint64_t)n_trees << lv, (uint64_t)n_trees * n_rows_);
         GrowArgs g{};
         g.counts = counts;
         g.front = g_front_[lv & 1].get();
         g.next = g_front_[(lv + 1) & 1].get();
         g.prev_splits = g_splits_[(lv + 1) & 1].get();
         g.prev_out = g_pout_[(lv + 1) & 1].get();
-        g.best = lv == 0 ? root_best_dev() : d_best_.get();
-        g.root_total = total_dev();
-        g.scale = scale_dev();
+        g.best = lv == 0 && n_trees == 1 ? root_best_dev() : d_best_.get();
+        g.root_total = level_totals_ ? level_totals_ : total_dev();
+        g.scale = level_scale_ ? level_scale_ : scale_dev();
         g.splits = g_splits_[lv & 1].get();
         g.hnodes = d_hnodes_.get();
         g.snodes = d_snodes_.get();
         g.tile_split = d_tile_split_.get();
-        g.tree = ring_nodes(t.slot);
-        g.header = ring_header(t.slot);
+        g.tree = ring_nodes(t.slot, 0, stride);
+        g.header = ring_header(t.slot, 0, stride);
         g.feature_offset = d_fo_.get();
         g.monotone = has_monotone_ ? monotone_.get() : nullptr;
         g.n_monotone = has_monotone_ ? n_cols_ : 0u;
@@ -1160,9 +1222,12 @@ Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, f
         g.reg = scan_params_;
         g.gamma = gamma;
         g.eta = eta;
-        g.front_cap = lv == 0 ? 1u : std::min<uint32_t>(1u << lv, slot_cap);
+        g.front_cap = lv == 0 ? n_trees : std::min<uint32_t>(n_trees << lv, slot_cap);
         g.n_features = n_cols_;
-        dev_.launch("hbr_grow_decide", dim3(1), dim3(512), g);
+        g.n_trees = n_trees;
+        g.tree_bytes = (uint32_t)stride;
+        g.tree_nodes = d_tree_nodes_.get();
+        dev_.launch(n_trees == 1 ? "hbr_grow_decide" : "hbr_grow_decide_batch", dim3(1), dim3(512), g);
         if (terminal) break;
         PartArgs a = part_args();
         a.splits = g_splits_[lv & 1].get();
@@ -1179,37 +1244,51 @@ Engine::TreeTicket Engine::queue_device_tree(uint64_t max_depth, double gamma, f
     }
     // every level's scatter wrote into the other buffer
     identity_rows0_ = false;
-    // the header and nodes back in one copy, on the copy stream
-    void *host = tree_stage_[t.slot].reserve(ring_bytes());
-    const size_t n_max = (size_t(2) << depth) - 1;
+    // the batch's headers and nodes back in one copy, on the copy stream
+    void *host = tree_stage_[t.slot].reserve(slot_bytes);
     HBR_HIP(hipEventRecord(tree_ready_[t.slot], s));
     HBR_HIP(hipStreamWaitEvent(copy_stream_, tree_ready_[t.slot], 0));
-    HBR_HIP(hipMemcpyAsync(host, ring_header(t.slot), kTreeHeaderBytes + n_max * sizeof(GrowTreeNode),
-                           hipMemcpyDeviceToHost, copy_stream_));
+    HBR_HIP(hipMemcpyAsync(host, ring_header(t.slot, 0, stride), slot_bytes, hipMemcpyDeviceToHost, copy_stream_));
     HBR_HIP(hipEventRecord(tree_copied_[t.slot], copy_stream_));
     return t;
 }
 
-Engine::TreeState Engine::finish_device_tree(const TreeTicket &t, std::vector<GrowTreeNode> &nodes, QScale *scale) {
+Engine::TreeState Engine::finish_device_forest(const TreeTicket &t, std::vector<std::vector<GrowTreeNode>> &trees) {
     HBR_HIP(hipEventSynchronize(tree_copied_[t.slot]));
     const uint8_t *host = static_cast<const uint8_t *>(tree_stage_[t.slot].get());
-    TreeHeader th;
-    std::memcpy(&th, host, sizeof(th));
-    const GrowCounts &gc = th.counts;
-    if (gc.error) fail(kInvalid, "device growth: a level needed more histogram slots than reserved");
-    if (gc.n_nodes == 0 || gc.n_nodes > kMaxDeviceNodes) fail(kInvalid, "device growth: node count out of range");
-    nodes.resize(gc.n_nodes);
-    std::memcpy(nodes.data(), host + kTreeHeaderBytes, gc.n_nodes * sizeof(GrowTreeNode));
-    // (the root's histogram was counted when it was queued)
-    counters.hist_nodes += gc.hist_nodes - 1;
-    counters.hist_rows += gc.hist_rows;
-    counters.hist_bytes += hist_bytes(gc.hist_rows, true);
-    counters.partition_rows += gc.part_rows;
-    if (scale) *scale = th.scale;
-    if (!t.check) return kTreeOk;
-    if (th.scale.nonfinite != 0) return kTreeNotFinite;
-    scale_host_ = th.scale;
-    return kTreeOk;
+    trees.resize(t.n_trees);
+    TreeState st = kTreeOk;
+    const size_t n_max = (t.stride - kTreeHeaderBytes) / sizeof(GrowTreeNode);
+    for (uint32_t k = 0; k < t.n_trees; k++) {
+        TreeHeader th;
+        std::memcpy(&th, host + k * t.stride, sizeof(th));
+        const GrowCounts &gc = th.counts;
+        if (gc.error) fail(kInvalid, "device growth: a level needed more histogram slots than reserved");
+        if (gc.n_nodes == 0 || gc.n_nodes > n_max) fail(kInvalid, "device growth: node count out of range");
+        trees[k].resize(gc.n_nodes);
+        std::memcpy(trees[k].data(), host + k * t.stride + kTreeHeaderBytes, gc.n_nodes * sizeof(GrowTreeNode));
+        if (k == 0) {  // the level counts are the batch's totals (the roots were counted when queued)
+            counters.hist_nodes += gc.hist_nodes - t.n_trees;
+            counters.hist_rows += gc.hist_rows;
+            counters.hist_bytes += hist_bytes(gc.hist_rows, true);
+            counters.partition_rows += gc.part_rows;
+        }
+        if (t.check && th.scale.nonfinite != 0) st = kTreeNotFinite;
+        if (t.check && k == 0 && t.n_trees == 1 && st == kTreeOk) scale_host_ = th.scale;
+    }
+    return st;
+}
+
+Engine::TreeState Engine::finish_device_tree(const TreeTicket &t, std::vector<GrowTreeNode> &nodes, QScale *scale) {
+    std::vector<std::vector<GrowTreeNode>> trees;
+    const TreeState st = finish_device_forest(t, trees);
+    nodes = std::move(trees[0]);
+    if (scale) {
+        TreeHeader th;
+        std::memcpy(&th, tree_stage_[t.slot].get(), sizeof(th));
+        *scale = th.scale;
+    }
+    return st;
 }
 
 void Engine::drain() {
@@ -1230,7 +1309,7 @@ bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vecto
     return false;
 }
 
-void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss) {
+void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree) {
     if (!dense_u8_) fail(kRefused, "walk: the index has no row-major u8 bins");
     if (output >= outputs_) fail(kInvalid, "walk: no such output");
     // the staged walk: 32-byte rows and trees whose nodes fit its LDS table
@@ -1238,8 +1317,8 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss)
     if (next_loss && !staged) fail(kRefused, "walk: gradients need 32-byte rows and depth <= 9");
     hipStream_t s = dev_.stream();
     WalkArgs a{};
-    a.tree = ring_nodes(last_ring_);
-    a.counts = &ring_header(last_ring_)->counts;
+    a.tree = ring_nodes(last_ring_, tree, last_stride_);
+    a.counts = &ring_header(last_ring_, tree, last_stride_)->counts;
     a.bins8 = rows8_.get();
     a.margins = margins_.get();
     a.stride = stride_;

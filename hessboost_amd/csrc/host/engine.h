@@ -149,7 +149,7 @@ public:
     // tree order. Needs a dense u8 index (the depth limit's rows are routed
     // by the walk, not partitioned) and max_depth in [1, kMaxDeviceDepth].
     static constexpr uint32_t kMaxDeviceDepth = 13;
-    bool can_grow_device(uint64_t max_depth) const;
+    bool can_grow_device(uint64_t max_depth, uint32_t n_trees = 1) const;
     // false when a gradient is not finite
     bool grow_device(uint64_t max_depth, double gamma, float eta, std::vector<GrowTreeNode> &nodes);
     // The same in two halves, so that a tree can be queued before the
@@ -161,10 +161,19 @@ public:
     struct TreeTicket {
         uint32_t slot = 0;
         bool check = false;  // the gradients' scale is checked at finish
+        uint32_t n_trees = 1;
+        size_t stride = 0;   // bytes between the trees of the ring slot
     };
     enum TreeState { kTreeOk = 0, kTreeNotFinite = 1 };
     TreeTicket queue_device_tree(uint64_t max_depth, double gamma, float eta);
     TreeState finish_device_tree(const TreeTicket &t, std::vector<GrowTreeNode> &nodes, QScale *scale);
+    // The trees of every softmax class at once (the staged softmax pairs,
+    // each class with its own scale), level by level: one launch of each
+    // kernel per level for all of them. finish_device_forest reads the
+    // batch back, tree c for class c; walk_device_tree(c, nullptr, c) adds
+    // tree c to the margins of class c.
+    TreeTicket queue_class_trees(uint64_t max_depth, double gamma, float eta);
+    TreeState finish_device_forest(const TreeTicket &t, std::vector<std::vector<GrowTreeNode>> &trees);
     void drain();
     // The last queued device tree's leaves onto the margins of `output`,
     // routed on the device from its records (no readback); with next_loss
@@ -176,7 +185,7 @@ public:
     }
     // The walk alone (no gradients): any dense u8 index, any output.
     bool can_route_device_tree(uint64_t max_depth) const { return can_grow_device(max_depth); }
-    void walk_device_tree(uint32_t output, const hbr_device_loss *next_loss);
+    void walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree = 0);
     // HistogramBackend::build of a host row list (per-node host growth).
     std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
     std::vector<uint32_t> rows_of(const Segment &s);
@@ -214,16 +223,26 @@ private:
                      ScanBest *best_dev, const GrowCounts *grow = nullptr);
     // the root's total, histogram and split search, queued (no synchronisation)
     void launch_root(const Segment &seg, uint32_t slot, float lower, float upper);
-    // the same for a device-grown tree (slot 0, unbounded) from records
-    // uploaded once
-    void launch_device_root();
+    // the roots of a device-grown batch (root t in slot t, of class t,
+    // unbounded) from records uploaded once per batch size
+    void launch_device_roots(uint32_t n_trees);
+    TreeTicket queue_device_forest(uint32_t n_trees, uint64_t max_depth, double gamma, float eta);
     DBuf<uint8_t> d_root_in_;
+    uint32_t root_in_trees_ = 0;
+    // a batched level's pairs (class-major), scales and root totals; null:
+    // the staged pairs, the live scale, the root block's total
+    const GPair *level_pairs_ = nullptr;
+    QScale *level_scale_ = nullptr;
+    QBin *level_totals_ = nullptr;
+    DBuf<QBin> d_root_totals_;
+    DBuf<uint32_t> d_tree_nodes_;
     // Device-grown trees in flight: each is written into a ring slot in
     // device memory and read back on a copy stream (the growth stream never
     // waits for a readback); pinned readbacks and their events. The guarded
     // walk's saved scale and skip flag.
     static constexpr uint32_t kTreeRing = 3;
-    static constexpr size_t ring_bytes() { return kTreeHeaderBytes + kMaxDeviceNodes * sizeof(GrowTreeNode); }
+    size_t ring_slot_bytes_ = 0;  // a ring slot holds a batch: its trees `stride` bytes apart
+    size_t last_stride_ = 0;
     DBuf<uint8_t> d_tree_ring_;
     PinnedBuf tree_stage_[kTreeRing];
     hipEvent_t tree_ready_[kTreeRing] = {};
@@ -231,11 +250,12 @@ private:
     bool ring_used_[kTreeRing] = {};
     hipStream_t copy_stream_ = nullptr;
     uint32_t tree_seq_ = 0, last_ring_ = 0;
-    TreeHeader *ring_header(uint32_t r) const {
-        return reinterpret_cast<TreeHeader *>(d_tree_ring_.get() + r * ring_bytes());
+    TreeHeader *ring_header(uint32_t r, uint32_t tree, size_t stride) const {
+        return reinterpret_cast<TreeHeader *>(d_tree_ring_.get() + r * ring_slot_bytes_ + tree * stride);
     }
-    GrowTreeNode *ring_nodes(uint32_t r) const {
-        return reinterpret_cast<GrowTreeNode *>(d_tree_ring_.get() + r * ring_bytes() + kTreeHeaderBytes);
+    GrowTreeNode *ring_nodes(uint32_t r, uint32_t tree, size_t stride) const {
+        return reinterpret_cast<GrowTreeNode *>(d_tree_ring_.get() + r * ring_slot_bytes_ + tree * stride +
+                                                kTreeHeaderBytes);
     }
     uint32_t last_depth_ = 0;  // max_depth of the last queued device tree
     DBuf<QScale> guard_scale_;

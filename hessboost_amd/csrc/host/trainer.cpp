@@ -2,6 +2,7 @@
 
 #include <cfloat>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <deque>
 #include <limits>
@@ -113,6 +114,13 @@ Engine::TreeTicket TreeBuilder::queue_device() {
                        p_.monotone);
     e_.begin_tree();
     return e_.queue_device_tree(p_.max_depth, p_.gamma, p_.eta);
+}
+
+Engine::TreeTicket TreeBuilder::queue_classes() {
+    e_.set_scan_params(ScanParams{p_.reg.lambda, p_.reg.alpha, p_.reg.max_delta_step, p_.reg.min_child_weight},
+                       p_.monotone);
+    e_.begin_tree();
+    return e_.queue_class_trees(p_.max_depth, p_.gamma, p_.eta);
 }
 
 // A device-grown tree's records as the model's nodes (split thresholds from
@@ -406,6 +414,7 @@ Trainer::Trainer(Engine &e, const TrainParams &p, const float *labels, const flo
     }
     labels_.assign(labels, labels + n);
     if (weights) weights_.assign(weights, weights + n);
+    if (const char *v = std::getenv("HBROCM_SOFTMAX_BATCH")) softmax_batches = std::strtol(v, nullptr, 10) != 0;
     base_ = base_margins(p, labels, weights, n);
     std::vector<float> m((size_t)n * k_);
     for (uint64_t r = 0; r < n; r++)
@@ -515,7 +524,39 @@ void Trainer::boost_softmax_pipelined(uint64_t rounds) {
     }
 }
 
+// Softmax rounds as batches: every class's gradients, then the round's K
+// class trees grown together level by level (one launch of each kernel per
+// level for all of them), then each walked into its class's margins; up
+// to three rounds in flight before the host reads the oldest back.
+void Trainer::boost_softmax_batched(uint64_t rounds) {
+    TreeBuilder b(e_, p_.grow);
+    std::deque<Engine::TreeTicket> inflight;
+    uint64_t queued = 0, done = 0;
+    while (done < rounds) {
+        while (queued < rounds && inflight.size() < 3) {
+            e_.softmax_gradients_async(kMinHess);
+            inflight.push_back(b.queue_classes());
+            for (uint32_t c = 0; c < k_; c++) e_.walk_device_tree(c, nullptr, c);
+            queued++;
+        }
+        std::vector<std::vector<GrowTreeNode>> trees;
+        const Engine::TreeState st = e_.finish_device_forest(inflight.front(), trees);
+        inflight.pop_front();
+        if (st != Engine::kTreeOk) {
+            e_.drain();
+            fail(kRefused, "a gradient is not finite");
+        }
+        for (const auto &t : trees) trees_.push_back(b.tree_from(t));
+        done++;
+    }
+}
+
 void Trainer::boost(uint64_t rounds) {
+    if (p_.objective == HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE && softmax_batches &&
+        e_.can_grow_device(p_.grow.max_depth, k_)) {
+        boost_softmax_batched(rounds);
+        return;
+    }
     if (p_.objective == HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE &&
         e_.can_route_device_tree(p_.grow.max_depth)) {
         boost_softmax_pipelined(rounds);

@@ -56,6 +56,8 @@ public:
     // A depthwise tree queued on the device (Engine::queue_device_tree),
     // and a finished one's records as a Tree.
     Engine::TreeTicket queue_device();
+    // every softmax class's tree at once (Engine::queue_class_trees)
+    Engine::TreeTicket queue_classes();
     Tree tree_from(const std::vector<GrowTreeNode> &nodes) const;
 
 private:
@@ -112,9 +114,13 @@ public:
     const std::vector<float> &base_score() const { return base_; }
     const std::vector<Tree> &trees() const { return trees_; }
     void margins(float *out);
+    // softmax depthwise rounds grow their class trees as one batch (else one
+    // class tree after another); HBROCM_SOFTMAX_BATCH=0 turns it off
+    bool softmax_batches = true;
 
 private:
     void boost_softmax_pipelined(uint64_t rounds);
+    void boost_softmax_batched(uint64_t rounds);
     void boost_pipelined(uint64_t rounds, const hbr_device_loss &loss);
     hbr_device_loss device_loss() const;
     // one grown tree onto the margins of output `output` (and, given

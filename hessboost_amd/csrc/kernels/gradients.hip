@@ -246,6 +246,16 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scale_rotate(RotateArgs a) 
     *a.live = QScale{};
 }
 
+extern "C" __global__ __launch_bounds__(64) void hbr_class_scales_finish(ScalesArgs a) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= a.k) return;
+    QScale q = a.scales[c];
+    q.exp_g = exponent_for(q.max_g_bits, a.n_rows);
+    q.exp_h = exponent_for(q.max_h_bits, a.n_rows);
+    q.scalar_rows = 0;
+    a.scales[c] = q;
+}
+
 extern "C" __global__ __launch_bounds__(64) void hbr_scale_select(SelectArgs a) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     QScale q = *a.from;

@@ -14,6 +14,12 @@
 // Histogram slots: the built child of split i takes the i-th slot (in
 // ascending order) that no splitting parent holds; its sibling keeps the
 // parent's slot (the histogram kernels turn the parent into the sibling).
+//
+// A batched level decides the levels of several trees at once (the class
+// trees of a softmax round): the frontier holds their nodes in tree order,
+// each tree numbers its own nodes (children appended in its frontier order)
+// and writes its own records and header; slots, splits and tiles are
+// shared.
 #include "common.h"
 
 namespace hbr {
@@ -44,16 +50,44 @@ constexpr uint32_t kGrowThreads = 512;
 constexpr uint32_t kGrowLdsOffsets = 4096;  // feature offsets kept in LDS (more features read them from memory)
 constexpr uint32_t kGrowSlotWords = kGrowMaxSlots / 32;
 
+__device__ __forceinline__ GrowTreeNode *tree_of(const GrowArgs &a, uint32_t t) {
+    return reinterpret_cast<GrowTreeNode *>(reinterpret_cast<char *>(a.tree) + (size_t)t * a.tree_bytes);
+}
+
+__device__ __forceinline__ TreeHeader *header_of(const GrowArgs &a, uint32_t t) {
+    return reinterpret_cast<TreeHeader *>(reinterpret_cast<char *>(a.header) + (size_t)t * a.tree_bytes);
+}
+
 }  // namespace hbr
 
 using namespace hbr;
 
-extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
+template <bool BATCHED>
+__device__ __forceinline__ void grow_decide(const GrowArgs &a) {
     __shared__ uint32_t s_used[kGrowSlotWords];   // slots of splitting parents
     __shared__ uint32_t s_free[kGrowMaxSlots];    // the other slots, ascending
     __shared__ uint32_t s_fo[kGrowLdsOffsets + 1];
     __shared__ uint32_t s_tile_begin[kGrowMaxSlots / 2];  // first tile of each split
+    // batched: each tree's node count before this level, its first split of
+    // the level, its splits and its quantisation exponents
+    __shared__ uint32_t s_base[BATCHED ? kGrowMaxTrees : 1];
+    __shared__ uint32_t s_first[BATCHED ? kGrowMaxTrees : 1];
+    __shared__ uint32_t s_nsplit[BATCHED ? kGrowMaxTrees : 1];
+    __shared__ int2 s_exp[BATCHED ? kGrowMaxTrees : 1];
+    __shared__ GrowCounts s_final;  // the level's counts as thread 0 writes them
     const uint32_t tid = threadIdx.x;
+    const uint32_t n_trees = BATCHED ? a.n_trees : 1u;
+    if (BATCHED) {
+        // the per-tree loads first: a wait for a load waits for every load
+        // issued before it; these are needed before the first barrier, the
+        // records read ahead below only in the loop
+        for (uint32_t t = tid; t < n_trees; t += kGrowThreads) {
+            s_first[t] = 0xffffffffu;
+            s_nsplit[t] = 0u;
+            s_exp[t] = make_int2(a.scale[t].exp_g, a.scale[t].exp_h);
+            s_base[t] = a.level == 0 ? 1u : a.tree_nodes[t];
+        }
+    }
     const bool fo_lds = a.n_features <= kGrowLdsOffsets;
     if (fo_lds)
         for (uint32_t k = tid; k <= a.n_features; k += kGrowThreads) s_fo[k] = a.feature_offset[k];
@@ -71,20 +105,20 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
         sp0 = a.prev_splits[j0 >> 1];
         po0 = a.prev_out[j0 >> 1];
     }
-    if (cap0) b0 = a.best[a.level == 0 ? 0 : j0];
+    if (cap0) b0 = a.best[j0];
     QBin root_total{0, 0};
-    if (a.level == 0) root_total = *a.root_total;
+    if (a.level == 0 && cap0) root_total = a.root_total[j0];
     GrowCounts c0 = *a.counts;
     if (a.level == 0) {
-        c0.n_front = 1;
-        c0.n_nodes = 1;
-        c0.hist_nodes = 1;
+        c0.n_front = n_trees;
+        c0.n_nodes = n_trees;
+        c0.hist_nodes = n_trees;
         c0.error = 0;
         c0.hist_rows = 0;
         c0.part_rows = 0;
     }
     const uint32_t n_front = c0.n_front, node_base = c0.n_nodes;
-    const int eg = a.scale->exp_g, eh = a.scale->exp_h;
+    const int eg1 = BATCHED ? 0 : a.scale->exp_g, eh1 = BATCHED ? 0 : a.scale->exp_h;
     for (uint32_t w = tid; w < kGrowSlotWords; w += kGrowThreads) s_used[w] = 0u;
     __syncthreads();
 
@@ -95,14 +129,15 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
         const bool active = j < n_front;
         // the node: its rows, slot, statistics and bounds
         Seg seg{0u, 0u, 0u, 0u};
-        uint32_t slot = 0, nid = 0, identity = 0;
+        uint32_t slot = 0, nid = 0, identity = 0, tree = 0;
         QBin total{0, 0};
         double lower = -__builtin_inf(), upper = __builtin_inf();
         ScanBest b{};
         if (active && a.level == 0) {
-            seg = Seg{0u, a.n_rows, 0u, 0u};
+            tree = j;  // the roots: all rows of each tree, in its own region of the row buffers
+            seg = Seg{j * a.n_rows, a.n_rows, 0u, 0u};
             identity = 1;
-            slot = a.root_slot;
+            slot = a.root_slot + j;
             total = root_total;
             b = b0;
         } else if (active) {
@@ -122,11 +157,14 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
             lower = g.lower;
             upper = g.upper;
             nid = g.nid;
+            tree = g.tree;
             if (c == 0) {
                 part_rows += sp.seg.len;
                 hist_rows += po.built_left ? nl : sp.seg.len - nl;
             }
         }
+        const int eg = BATCHED ? s_exp[active ? tree : 0u].x : eg1, eh = BATCHED ? s_exp[active ? tree : 0u].y : eh1;
+        GrowTreeNode *records = BATCHED ? tree_of(a, tree) : a.tree;
         const double ng = dequant(total.g, eg), nh = dequant(total.h, eh);
         // the winner as a split position (builder/mod.rs:167-193)
         bool valid = false;
@@ -164,21 +202,29 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
         uint32_t n_valid, n_tiles;
         const uint32_t i = split_carry + block_exclusive_scan<kGrowThreads>(valid ? 1u : 0u, &n_valid);
         const uint32_t tile_begin = tile_carry + block_exclusive_scan<kGrowThreads>(tiles, &n_tiles);
+        // each tree's first split of the level (the frontier is in tree order)
+        if (BATCHED) {
+            if (active && valid) {
+                atomicMin(&s_first[tree], i);
+                atomicAdd(&s_nsplit[tree], 1u);
+            }
+            __syncthreads();
+        }
         if (active && a.level == 0) {
             GrowTreeNode r{};
             r.left = -1;
             r.bin = -2;
             r.default_left = 1;
             r.sum_hess = (float)nh;
-            a.tree[0] = r;
+            records[0] = r;
         }
         if (active && !valid) {
             // a leaf: builder/shared.rs:174-187 then scale_leaves(eta)
             const float w = (float)leaf_weight(ng, nh, a.reg, lower, upper);
-            a.tree[nid].value = w * a.eta;
+            records[nid].value = w * a.eta;
         } else if (active) {
-            const uint32_t left = node_base + 2 * i;
-            GrowTreeNode &r = a.tree[nid];
+            const uint32_t left = BATCHED ? s_base[tree] + 2 * (i - s_first[tree]) : node_base + 2 * i;
+            GrowTreeNode &r = records[nid];
             r.left = (int32_t)left;
             r.feature = f;
             r.limit = limit;
@@ -218,18 +264,20 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
                     g.lower = cb[2 * c];
                     g.upper = cb[2 * c + 1];
                     g.nid = left + c;
+                    g.tree = tree;
                     a.next[2 * i + c] = g;
                     ScanNode s{};
                     s.from_split = 1;
                     s.split = i;
                     s.child = c;
+                    s.pad = tree << kScanClassShift;
                     s.total = ct[c];
                     s.root_gain = node_gain(cg[c], ch[c], a.reg, (float)cb[2 * c], (float)cb[2 * c + 1]);
                     s.lower = (float)cb[2 * c];
                     s.upper = (float)cb[2 * c + 1];
                     a.snodes[2 * i + c] = s;
                 }
-                a.tree[left + c] = k;
+                records[left + c] = k;
             }
             if (!a.terminal) {
                 PartSplit p{};
@@ -240,11 +288,13 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
                 p.identity = identity;
                 p.tile_begin = tile_begin;
                 p.parent_slot = slot;
+                p.tree = tree;
                 a.splits[i] = p;
                 s_tile_begin[i] = tile_begin;
                 HistNode h{};
                 h.from_split = 1;
                 h.split = i;
+                h.cls = tree;
                 a.hnodes[i] = h;
                 if (slot < a.slot_cap && slot < kGrowMaxSlots) atomicOr(&s_used[slot >> 5], 1u << (slot & 31));
             }
@@ -299,7 +349,10 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
             c.hist_nodes += n_splits;
             if (n_splits > n_free) c.error = 1;
             a.counts[0] = c;
+            s_final = c;
         }
+        if (BATCHED)
+            for (uint32_t t = tid; t < n_trees; t += kGrowThreads) a.tree_nodes[t] = s_base[t] + 2 * s_nsplit[t];
     }
     // per-thread row counts of the previous level's splits
     __shared__ unsigned long long s_rows[2][kGrowThreads / kWave];
@@ -321,11 +374,22 @@ extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) {
         }
         a.counts->hist_rows = c0.hist_rows + hr;
         a.counts->part_rows = c0.part_rows + pr;
-        if (a.terminal && a.header) {
+        s_final.hist_rows = c0.hist_rows + hr;
+        s_final.part_rows = c0.part_rows + pr;
+    }
+    // each tree's header: its scale and node count, and the level counts
+    // (a batch's totals)
+    if (a.terminal && a.header) {
+        __syncthreads();
+        for (uint32_t t = tid; t < n_trees; t += kGrowThreads) {
             TreeHeader h;
-            h.scale = *a.scale;
-            h.counts = *a.counts;
-            *a.header = h;
+            h.scale = a.scale[t];
+            h.counts = s_final;
+            if (BATCHED) h.counts.n_nodes = s_base[t] + 2 * s_nsplit[t];
+            *header_of(a, t) = h;
         }
     }
 }
+
+extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide(GrowArgs a) { grow_decide<false>(a); }
+extern "C" __global__ __launch_bounds__(512) void hbr_grow_decide_batch(GrowArgs a) { grow_decide<true>(a); }

@@ -111,14 +111,15 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
         lh[i] = 0ull;
     }
     __syncthreads();
-    const int eg = a.scale->exp_g, eh = a.scale->exp_h;
+    const int eg = a.scale[nd.cls].exp_g, eh = a.scale[nd.cls].exp_h;
+    const GPair *gpair = a.gpair + (size_t)nd.cls * a.class_rows;
     const uint32_t *rows = a.rows[nd.seg.buf] + nd.seg.offset;
     const uint32_t lane = lane_id();
     const uint32_t rot = lane & (FG - 1);
     const uint32_t end = t.row0 + t.rows;
     for (uint32_t j = t.row0 + threadIdx.x; j < end; j += blockDim.x) {
         const uint32_t r = nd.contiguous ? nd.seg.offset + j : rows[j];
-        const GPair p = a.gpair[r];
+        const GPair p = gpair[r];
         uint32_t w[W];
         load_bins<FG>(a.bins8 + (size_t)r * a.stride + f0, w);
         const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
@@ -181,7 +182,8 @@ __device__ __forceinline__ void hist_csr(const HistArgs &a) {
     const uint32_t nb = min(kCsrGroupBins, a.total_bins - lo_bin);
     for (uint32_t i = threadIdx.x; i < nb; i += blockDim.x) s_g[i] = s_h[i] = 0ull;
     __syncthreads();
-    const int eg = a.scale->exp_g, eh = a.scale->exp_h;
+    const int eg = a.scale[nd.cls].exp_g, eh = a.scale[nd.cls].exp_h;
+    const GPair *gpair = a.gpair + (size_t)nd.cls * a.class_rows;
     const uint32_t *rows = a.rows[nd.seg.buf] + nd.seg.offset;
     const uint32_t end = t.row0 + t.rows;
     const uint32_t wave = threadIdx.x / kWave, waves = blockDim.x / kWave, lane = lane_id();
@@ -196,7 +198,7 @@ __device__ __forceinline__ void hist_csr(const HistArgs &a) {
             const uint32_t r = ok ? (nd.contiguous ? nd.seg.offset + j : rows[j]) : 0u;
             b[u] = ok ? a.row_ptr[r] : 0ull;
             e[u] = ok ? a.row_ptr[r + 1] : 0ull;
-            const GPair p = ok ? a.gpair[r] : GPair{0.0f, 0.0f};
+            const GPair p = ok ? gpair[r] : GPair{0.0f, 0.0f};
             qg[u] = (unsigned long long)quantize(p.g, eg);
             qh[u] = (unsigned long long)quantize(p.h, eh);
             iters = max(iters, (uint32_t)((e[u] - b[u] + kWave - 1) / kWave));

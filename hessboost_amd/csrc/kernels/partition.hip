@@ -108,12 +108,13 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
     const PartSplit sp = a.splits[split_of_tile(a, part_splits(a), tile)];
     const uint32_t base = (tile - sp.tile_begin) * kPartTile;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
+    const uint32_t id0 = sp.identity ? sp.seg.offset % a.n_rows : 0u;  // a root of a batched level
     const uint32_t wave = threadIdx.x / kWave;
     uint32_t r[kRowsPerThread];
 #pragma unroll
     for (uint32_t k = 0; k < kRowsPerThread; k++) {
         const uint32_t j = base + (k * (kPartThreads / kWave) + wave) * kWave + lane_id();
-        r[k] = j < sp.seg.len ? (sp.identity ? sp.seg.offset + j : src[j]) : 0xffffffffu;
+        r[k] = j < sp.seg.len ? (sp.identity ? id0 + j : src[j]) : 0xffffffffu;
     }
     bool left[kRowsPerThread];
     if (a.dense && a.cols8) {
@@ -182,6 +183,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     const uint32_t right_before = tile_pos - left_before;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
     uint32_t *dst = a.dst_rows[sp.seg.buf ^ 1u] + sp.seg.offset;
+    const uint32_t id0 = sp.identity ? sp.seg.offset % a.n_rows : 0u;
     const uint64_t *dec = a.decisions + (size_t)tile * kBallots;
     const uint32_t wave = threadIdx.x / kWave, lane = lane_id();
     const uint64_t below = (1ull << lane) - 1ull;
@@ -200,7 +202,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     for (uint32_t k = 0; k < kRowsPerThread; k++) {
         const uint32_t q = k * (kPartThreads / kWave) + wave;
         const uint32_t j = tile_pos + q * kWave + lane;
-        r[k] = j < sp.seg.len ? (sp.identity ? sp.seg.offset + j : src[j]) : 0xffffffffu;
+        r[k] = j < sp.seg.len ? (sp.identity ? id0 + j : src[j]) : 0xffffffffu;
     }
 #pragma unroll
     for (uint32_t k = 0; k < kRowsPerThread; k++) {

@@ -122,6 +122,8 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
     bool nan_seen = false;
     const QBin *h = a.hist + (size_t)node_slot(a, nd) * a.total_bins + fs;
     const bool dev_root = (nd.pad & kScanDeviceRoot) != 0;
+    const uint32_t cls = nd.pad >> kScanClassShift;
+    QBin *root_total = a.root_total + cls;
     int64_t tg = nd.total.g, th = nd.total.h;
     if (dev_root && a.dense) {
         // the host routes a dense root here only when feature 0 has bins
@@ -137,13 +139,13 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
         }
         tg = sg;
         th = sh;
-        if (f == 0 && lane == 0) *a.root_total = QBin{tg, th};
+        if (f == 0 && lane == 0) *root_total = QBin{tg, th};
     } else if (dev_root) {
-        tg = a.root_total->g;
-        th = a.root_total->h;
+        tg = root_total->g;
+        th = root_total->h;
     }
     if (nb > 1) {
-        const int eg = a.scale->exp_g, eh = a.scale->exp_h;
+        const int eg = a.scale[cls].exp_g, eh = a.scale[cls].exp_h;
         const int dir = a.monotone ? (int)a.monotone[f] : 0;
         const float root_gain = dev_root ? node_gain(dequant(tg, eg), dequant(th, eh), a.reg, nd.lower, nd.upper)
                                          : nd.root_gain;

@@ -110,6 +110,34 @@ def test_softmax_two_classes_weighted_deep_and_lossguide_match_oracle():
     compare_trees(model.trees, ref.trees())
 
 
+@pytest.mark.parametrize("k,depth,weighted", [(2, 5, True), (3, 6, False), (10, 4, True)])
+def test_batched_class_trees_equal_one_class_at_a_time(k, depth, weighted):
+    """A softmax round's class trees grown as one batch (every level of all
+    of them in one launch of each kernel) equal, bit for bit, the trees
+    grown one class after another, and the final margins too."""
+    import os
+    x, y = synthetic.multiclass(n=9_001, f=12, k=k, seed=20 + k)
+    w = np.random.default_rng(k).random(len(y)).astype(np.float32) + 0.5 if weighted else None
+    params = {"objective": "multi:softprob", "num_class": k, "max_depth": depth, "eta": 0.3,
+              "lambda": 1.5, "min_child_weight": 0.5}
+    dm = hb.DMatrix(x, label=y, weight=w)
+    runs = []
+    for flag in ("1", "0"):
+        os.environ["HBROCM_SOFTMAX_BATCH"] = flag
+        try:
+            tr = hb.Trainer(dm.engine(256), params, y, w)
+            tr.boost(3)
+            runs.append((tr.trees(), tr.margins()))
+        finally:
+            os.environ.pop("HBROCM_SOFTMAX_BATCH", None)
+    (ta, ma), (tb, mb) = runs
+    assert len(ta) == len(tb) == 3 * k
+    for a, b in zip(ta, tb):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
+
+
 def test_softmax_labels_must_be_class_indices():
     """multiclass.rs:96-100: a label that is not a class index is refused."""
     x, y = synthetic.multiclass(n=500, f=4, k=3, seed=7)
