@@ -303,6 +303,18 @@ struct HistArgs {
     uint32_t groups;            // feature groups (dense) or bin ranges (CSR) per tile
     uint32_t class_rows;        // batched levels: the pairs of class c start at gpair + c * class_rows
     uint32_t pad;
+    // CSR rows whose global bins ascend: row r's entries of bin range g are
+    // row_ptr[r] + [csr_ranges[r * (groups + 1) + g], ... + g + 1]) (null: scan the row)
+    const uint32_t *csr_ranges;
+};
+
+// Each CSR row's first entry of every kCsrGroupBins range (rows' global bins ascend).
+struct CsrRangeArgs {
+    const uint64_t *row_ptr;
+    const uint32_t *gbins;
+    uint32_t *ranges;            // n_rows x (groups + 1), relative to row_ptr[r]
+    uint32_t n_rows;
+    uint32_t groups;
 };
 
 // CSR histograms: a workgroup sums one tile's rows into one range of

@@ -44,12 +44,14 @@ Engine::Engine(int ordinal, const hbr_index_desc &desc) : dev_(device(ordinal)) 
     read_tunables();
     upload_index(desc);
     block_.resize(kBlockBytes);
+    build_csr_ranges();
 }
 
 Engine::Engine(int ordinal, const DenseSource &src) : dev_(device(ordinal)) {
     read_tunables();
     bin_dense(src);
     block_.resize(kBlockBytes);
+    build_csr_ranges();
 }
 
 // Launch-shape overrides for tuning sweeps (results do not depend on them).
@@ -64,6 +66,7 @@ void Engine::read_tunables() {
     }
     if (const char *v = std::getenv("HBROCM_HIST_BIN_MAJOR")) hist_bin_major = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_CSR_RANGES")) csr_range_table = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_WALK_BLOCKS")) {
         const long b = std::strtol(v, nullptr, 10);
         if (b >= 1 && b <= 64) walk_blocks_per_cu = (uint32_t)b;
@@ -199,6 +202,21 @@ void Engine::upload_index(const hbr_index_desc &d) {
 // index; otherwise the counts are scanned into row_ptr and the CSR global
 // bins are filled from the columns, and the columns and bitmap are kept when
 // cells <= 2 x entries (src/data/ghist.rs:235), as on the host.
+// Sparse rows in feature order: each row's first entry of every bin range
+// of the CSR histogram, so that a range's workgroups read only its entries
+// (when the table takes at most 1 GiB).
+void Engine::build_csr_ranges() {
+    csr_ranges_.release();
+    if (!csr_range_table || dense_u8_ || !csr_ascending_ || n_rows_ == 0) return;
+    const uint32_t groups = ceil_div(total_bins_, kCsrGroupBins);
+    const uint64_t words = n_rows_ * (uint64_t)(groups + 1);
+    if (groups < 2 || words * sizeof(uint32_t) > (uint64_t(1) << 30)) return;
+    csr_ranges_.resize(words);
+    CsrRangeArgs a{row_ptr_.get(), gbins_.get(), csr_ranges_.get(), (uint32_t)n_rows_, groups};
+    dev_.launch("hbr_csr_ranges", dim3(ceil_div(n_rows_, 256)), dim3(256), a);
+    dev_.sync();
+}
+
 void Engine::bin_dense(const DenseSource &src) {
     if (!src.x || !src.feature_offset || (!src.cut_values && src.feature_offset[src.n_cols] > 0))
         fail(kInvalid, "binning: x, feature_offset and cut_values are required");
@@ -752,6 +770,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.gpair = level_pairs_ ? level_pairs_ : pairs();
     a.scale = level_scale_ ? level_scale_ : scale_dev();
     a.class_rows = level_pairs_ ? (uint32_t)n_rows_ : 0u;
+    a.csr_ranges = !dense_u8_ && csr_ranges_.size() ? csr_ranges_.get() : nullptr;
     a.bins8 = rows8_.get();
     a.stride = stride_;
     a.n_cols = n_cols_;

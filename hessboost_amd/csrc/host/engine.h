@@ -209,6 +209,8 @@ private:
     void read_tunables();
     uint64_t entries_ = 0;
     bool csr_ascending_ = true;  // every CSR row's global bins ascend (device binning writes them so)
+    void build_csr_ranges();
+    DBuf<uint32_t> csr_ranges_;  // each CSR row's first entry of every histogram bin range
     void ensure_rows();
     bool contiguous(const Segment &sg) const;
     bool identity_rows0_ = false;
@@ -361,6 +363,7 @@ public:
     uint32_t hist_waves = 1;
     bool hist_bin_major = true;  // [bin][feature] LDS layout (16 and 32 feature groups)
     bool device_grow = true;     // depthwise trees decided on the device where eligible
+    bool csr_range_table = true; // CSR histograms read each bin range's entries from a per-row table
     uint32_t walk_blocks_per_cu = 4;  // workgroups per CU of the device-tree margin walk (one resident wave)
 };
 

@@ -198,6 +198,11 @@ __device__ __forceinline__ void hist_csr(const HistArgs &a) {
             const uint32_t r = ok ? (nd.contiguous ? nd.seg.offset + j : rows[j]) : 0u;
             b[u] = ok ? a.row_ptr[r] : 0ull;
             e[u] = ok ? a.row_ptr[r + 1] : 0ull;
+            if (ok && a.csr_ranges) {  // only this range's entries
+                const uint32_t *rg = a.csr_ranges + (size_t)r * (a.groups + 1) + grp;
+                e[u] = b[u] + rg[1];
+                b[u] += rg[0];
+            }
             const GPair p = ok ? gpair[r] : GPair{0.0f, 0.0f};
             qg[u] = (unsigned long long)quantize(p.g, eg);
             qh[u] = (unsigned long long)quantize(p.h, eh);
@@ -389,6 +394,22 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_hist_reduce(ReduceArgs a)
             *par = QBin{pv.g - g, pv.h - h};
         }
     }
+}
+
+// One thread per row: the row's first entry of every bin range (the
+// entries' global bins ascend), relative to the row's first entry.
+extern "C" __global__ __launch_bounds__(256) void hbr_csr_ranges(CsrRangeArgs a) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= a.n_rows) return;
+    const uint64_t b = a.row_ptr[r], e = a.row_ptr[r + 1];
+    uint32_t *out = a.ranges + (size_t)r * (a.groups + 1);
+    uint32_t g = 0;
+    out[0] = 0;
+    for (uint64_t x = b; x < e; x++) {
+        const uint32_t gg = min(a.gbins[x] / kCsrGroupBins, a.groups);
+        while (g < gg) out[++g] = (uint32_t)(x - b);
+    }
+    while (g < a.groups) out[++g] = (uint32_t)(e - b);
 }
 
 // Nodes of several tiles (CSR): slot bin b = the sum of the tiles' partials.
