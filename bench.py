@@ -63,6 +63,72 @@ def cpu_model():
     return platform.processor()
 
 
+def other_workload(args):
+    """Training rounds/s of the multiclass or the sparse configuration: the
+    matrix binned once (excluded), `warmup` rounds, then `steps` timed
+    rounds with the index, labels and margins resident in HBM; the oracle
+    times a bounded sample of the same rounds on the host."""
+    import numpy as np
+
+    import hessboost_amd as hb
+    from hessboost_amd import synthetic
+
+    t = time.time()
+    if args.workload == "multiclass":
+        x, y = synthetic.multiclass(n=2_000_000, f=50, k=10, seed=0)
+        params = {"objective": "multi:softprob", "num_class": 10, "max_depth": 6, "eta": 0.3, "max_bin": 256}
+        dm = hb.DMatrix(x, label=y)
+        workload = "multiclass softmax hist training, 2,000,000 x 50 f32, 10 classes, max_bin 256, max_depth 6, " \
+                   "eta 0.3, depthwise (10 trees per round)"
+        cpu_rounds = 1
+    else:
+        (row_ptr, col, val), y, _ = synthetic.sparse_wide(n=500_000, f=2000, density=0.1, seed=0)
+        params = {"objective": "reg:squarederror", "grow_policy": "lossguide", "max_depth": 0, "max_leaves": 255,
+                  "eta": 0.3, "max_bin": 64}
+        dm = hb.DMatrix((row_ptr, col, val), label=y, n_cols=2000)
+        workload = "sparse hist training, 500,000 x 2,000 CSR f32 (90% missing), max_bin 64, lossguide 255 leaves"
+        cpu_rounds = 2
+    log(f"generated {args.workload} data in {time.time() - t:.1f}s")
+    eng = dm.engine(params["max_bin"])
+    trainer = hb.Trainer(eng, params, y)
+    trainer.boost(args.warmup)
+    t0 = time.perf_counter()
+    trainer.boost(args.steps)
+    t1 = time.perf_counter()
+    dt = (t1 - t0) / args.steps
+    # the kernel breakdown from further rounds with HIP events around every kernel
+    extra = max(1, min(args.steps, 10))
+    eng.set_profiling(True, "hbr_")
+    trainer.boost(extra)
+    stats = eng.kernel_stats()
+    eng.set_profiling(False)
+    kern = {k: round(v[0] / extra, 4) for k, v in sorted(stats.items(), key=lambda kv: -kv[1][0])}
+    log(f"{args.steps} rounds in {t1 - t0:.3f}s = {1 / dt:.2f} rounds/s; ms per round by kernel: "
+        + ", ".join(f"{k} {v}" for k, v in list(kern.items())[:8]))
+    result = {
+        "metric": f"train rounds/s ({args.workload})", "value": round(1 / dt, 3), "unit": "rounds/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int64", "data": "synthetic",
+        "config": {"workload": workload}, "kernel_ms_per_round": kern,
+    }
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        O.set_threads(args.cpu_threads)
+        if args.workload == "multiclass":
+            ds = O.Dataset(x, max_bin=256)
+            p = O.params(objective=O.OBJ_SOFTMAX, num_class=10, max_depth=6, eta=0.3)
+        else:
+            ds = O.Dataset(csr=(row_ptr, col, val), n_cols=2000, max_bin=64)
+            p = O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=0, max_leaves=255, eta=0.3, max_bin=64)
+        m = O.Model(ds, y, p, 1)
+        t = time.time()
+        m.more(cpu_rounds)
+        ce = (time.time() - t) / cpu_rounds
+        result["cpu_baseline"] = {"value": round(1 / ce, 4), "unit": "rounds/s", "cores": args.cpu_threads,
+                                  "kind": "port", "sample": f"{'round 2' if cpu_rounds == 1 else f'rounds 2-{1 + cpu_rounds}'} of the same workload, oracle"}
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,6 +147,10 @@ def main():
                     help="first run a device-to-device copy of this many MiB (a known-size kernel for "
                          "scaling hardware byte counters in profiles)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--workload", choices=("higgs", "multiclass", "sparse"), default="higgs",
+                    help="higgs: the default line; multiclass (2M x 50, 10-class softmax, depth 6) and "
+                         "sparse (500k x 2000 CSR, 90%% missing, lossguide 255 leaves): their training "
+                         "rounds/s on a line of their own")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -91,6 +161,10 @@ def main():
 
     import hessboost_amd as hb
     from hessboost_amd import synthetic
+
+    if args.workload != "higgs":
+        other_workload(args)
+        return
 
     if args.copy_probe_mb > 0:
         nbytes = args.copy_probe_mb << 20
