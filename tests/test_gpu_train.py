@@ -138,6 +138,28 @@ def test_batched_class_trees_equal_one_class_at_a_time(k, depth, weighted):
     assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
 
 
+@pytest.mark.parametrize("n,k", [(5, 3), (33, 3), (70, 1), (130, 7)])
+def test_batched_class_trees_on_tiny_inputs_match_oracle(n, k):
+    """Batched class trees where rows are few (fewer than the classes, or a
+    part of one partition tile) and a one-class softmax: the oracle's trees,
+    and the same as one class after another."""
+    import os
+    x, y = synthetic.multiclass(n=n, f=6, k=max(k, 2), seed=n + k)
+    y = (y % k).astype(np.float32)
+    params = {"objective": "multi:softprob", "num_class": k, "max_depth": 4, "eta": 0.3, "min_child_weight": 0.0}
+    ref = O.Model(O.Dataset(x), y, O.params(objective=O.OBJ_SOFTMAX, num_class=k, max_depth=4,
+                                            min_child_weight=0.0), 2)
+    trees = []
+    for flag in ("1", "0"):
+        os.environ["HBROCM_SOFTMAX_BATCH"] = flag
+        try:
+            trees.append(hb.train(params, hb.DMatrix(x, label=y), 2).trees)
+        finally:
+            os.environ.pop("HBROCM_SOFTMAX_BATCH", None)
+    compare_trees(trees[0], ref.trees())
+    compare_trees(trees[1], ref.trees())
+
+
 def test_softmax_labels_must_be_class_indices():
     """multiclass.rs:96-100: a label that is not a class index is refused."""
     x, y = synthetic.multiclass(n=500, f=4, k=3, seed=7)
