@@ -102,3 +102,61 @@ def test_malformed_forest_is_refused():
                                   leaf_value=0.0)]])
     with pytest.raises(hb.HbrError):
         hb.Forest(arrs, 1)
+
+
+def _random_tree(rng, n_features, max_depth):
+    """An unbalanced tree in the reference's node layout, nodes numbered in
+    depth-first order (the upload re-lays them out breadth-first)."""
+    nodes = []
+
+    def grow(depth):
+        i = len(nodes)
+        nodes.append(None)
+        if depth >= max_depth or rng.random() < 0.25 * depth / max(1, max_depth):
+            nodes[i] = (-1, -1, 0, 0.0, 0, float(rng.normal(0, 0.1)))
+            return i
+        f = int(rng.integers(0, n_features))
+        cond = float(np.float32(rng.normal()))
+        dl = int(rng.integers(0, 2))
+        left = grow(depth + 1)
+        right = grow(depth + 1)
+        nodes[i] = (left, right, f, cond, dl, 0.0)
+        return i
+
+    grow(0)
+    return dict(left=np.array([n[0] for n in nodes], np.int32), right=np.array([n[1] for n in nodes], np.int32),
+                split_feature=np.array([n[2] for n in nodes], np.uint32),
+                split_cond=np.array([n[3] for n in nodes], np.float32),
+                default_left=np.array([n[4] for n in nodes], np.uint8),
+                leaf_value=np.array([n[5] for n in nodes], np.float32))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_forests_match_oracle(seed):
+    """Random unbalanced forests (depth 0 to 12, several outputs, tree
+    weights, NaN or a non-NaN missing value), both walks, bit for bit."""
+    import os
+    rng = np.random.default_rng(500 + seed)
+    f = int(rng.integers(1, 40))
+    n_trees = int(rng.integers(1, 90))
+    k = int(rng.choice([1, 1, 3]))
+    trees = [_random_tree(rng, f, int(rng.integers(0, 13))) for _ in range(n_trees)]
+    arrs = O.forest_arrays(trees)
+    arrs["tree_output"] = (np.arange(n_trees) % k).astype(np.uint32)
+    arrs["tree_weight"] = rng.uniform(0.5, 1.5, n_trees).astype(np.float32)
+    arrs["n_outputs"] = k
+    arrs["base_score"] = rng.normal(0, 1, k).astype(np.float32)
+    n = int(rng.choice([1, 63, 64, 65, 2_049]))
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    missing = np.nan if rng.random() < 0.6 else -7.0
+    x[rng.random((n, f)) < 0.1] = missing
+    want, want_leaf = O.predict_margin(arrs, x, missing=missing, with_leaf=True)
+    for kind in ("resident", "chunked"):
+        os.environ["HBROCM_PRED_KERNEL"] = kind
+        try:
+            fo = hb.Forest(arrs, k)
+            got = fo.predict_margin(x, missing=missing)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seed, kind)
+            assert np.array_equal(fo.predict_leaf(x, missing=missing), want_leaf), (seed, kind)
+        finally:
+            os.environ.pop("HBROCM_PRED_KERNEL", None)
