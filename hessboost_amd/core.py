@@ -427,22 +427,36 @@ def _device_ordinal(device):
 @dataclass
 class Booster:
     """A trained model: scalar-leaf trees in the reference's Node layout
-    (src/tree/regtree.rs:38-66), intercepts and the objective."""
+    (src/tree/regtree.rs:38-66), intercepts and the objective, with the
+    fields of the reference's JSON model document (model/serde.rs)."""
     objective: str
     base_score: np.ndarray
     trees: list = field(default_factory=list)
     n_outputs: int = 1
     n_features: int = 0
     tree_weights: np.ndarray | None = None
+    num_class: int = 0
+    n_targets: int = 1
+    best_iteration: int | None = None
+    num_parallel_tree: int = 1
+    objective_params: dict = field(default_factory=dict)
     _forest: object = None
     _forest_ordinal: int = -1
 
     def num_trees(self):
         return len(self.trees)
 
+    def effective_trees(self):
+        """The trees predictions use (model/mod.rs:1238-1242): with a best
+        iteration, the first (best_iteration + 1) x n_outputs x
+        num_parallel_tree."""
+        if self.best_iteration is None:
+            return self.trees
+        return self.trees[:(self.best_iteration + 1) * self.n_outputs * self.num_parallel_tree]
+
     def forest_desc(self, trees=None):
-        trees = self.trees if trees is None else trees
-        k = self.n_outputs
+        trees = self.effective_trees() if trees is None else trees
+        k, npt = self.n_outputs, max(1, self.num_parallel_tree)
         off = np.zeros(len(trees) + 1, np.uint64)
         cols = {key: [] for key in ("split_feature", "split_cond", "default_left", "left", "right", "leaf_value")}
         for i, t in enumerate(trees):
@@ -458,7 +472,7 @@ class Booster:
                     leaf_value=np.concatenate(cols["leaf_value"]).astype(np.float32),
                     tree_weight=(np.ones(len(trees), np.float32) if self.tree_weights is None
                                  else np.asarray(self.tree_weights[:len(trees)], np.float32)),
-                    tree_output=np.array([t % k for t in range(len(trees))], np.uint32),
+                    tree_output=np.array([(t // npt) % k for t in range(len(trees))], np.uint32),
                     base_score=np.asarray(self.base_score, np.float32))
         return arrs
 
@@ -484,22 +498,71 @@ class Booster:
         z = np.exp((m - m.max(axis=1, keepdims=True)).astype(np.float32))
         return (z / z.sum(axis=1, keepdims=True)).astype(np.float32)
 
+    # The reference's JSON model document (model/serde.rs:57-136): every
+    # field predictions depend on is written, the nullable ones as null.
+    _JSON_UNSUPPORTED = ("linear", "shrinkage", "boulevard", "ebm")
+
     def save_model_json(self):
-        """The reference's JSON model document for scalar trees (model/serde.rs)."""
+        """The reference's JSON model document (model/serde.rs:13-55) of
+        scalar-leaf, numeric-split trees; hessboost loads it with
+        BoostedModel::load (model/io.rs:119-131)."""
+        def f32(v):
+            return float(np.float32(v))
+
         trees = []
         for t in self.trees:
-            nodes = []
-            for i in range(len(t["left"])):
-                nodes.append(dict(split_feature=int(t["split_feature"][i]), split_cond=float(t["split_cond"][i]),
-                                  default_left=bool(t["default_left"][i]), left=int(t["left"][i]),
-                                  right=int(t["right"][i]), leaf_value=float(t["leaf_value"][i]),
-                                  sum_hess=float(t["sum_hess"][i]), split_gain=float(t["split_gain"][i]),
-                                  is_categorical=False, cat_begin=0, cat_end=0))
+            n = len(t["left"])
+            gain = t.get("split_gain", np.zeros(n, np.float32))
+            hess = t.get("sum_hess", np.zeros(n, np.float32))
+            nodes = [dict(split_feature=int(t["split_feature"][i]), split_cond=f32(t["split_cond"][i]),
+                          default_left=bool(t["default_left"][i]), left=int(t["left"][i]), right=int(t["right"][i]),
+                          leaf_value=f32(t["leaf_value"][i]), sum_hess=f32(hess[i]), split_gain=f32(gain[i]),
+                          is_categorical=False, cat_begin=0, cat_end=0) for i in range(n)]
             trees.append(dict(nodes=nodes, categories=[], size_leaf_vector=0, leaf_vectors=[], linear=None))
-        return json.dumps(dict(trees=trees, base_score=[float(b) for b in self.base_score],
-                               objective=self.objective, num_class=self.n_outputs if self.n_outputs > 1 else 0,
-                               n_outputs=self.n_outputs, n_targets=1, n_features=self.n_features,
-                               best_iteration=None, tree_weights=[1.0] * len(trees), num_parallel_tree=1))
+        weights = np.ones(len(trees), np.float32) if self.tree_weights is None else self.tree_weights
+        doc = dict(trees=trees, base_score=[f32(b) for b in np.atleast_1d(self.base_score)],
+                   objective=self.objective, objective_params=dict(self.objective_params),
+                   num_class=int(self.num_class), n_outputs=int(self.n_outputs), n_targets=int(self.n_targets),
+                   n_features=int(self.n_features), best_iteration=self.best_iteration,
+                   tree_weights=[f32(w) for w in weights], num_parallel_tree=int(self.num_parallel_tree),
+                   linear=None, shrinkage=None, boulevard=None, ebm=None)
+        return json.dumps(doc)
+
+    @classmethod
+    def load_model_json(cls, text):
+        """A Booster from the reference's JSON model document: scalar-leaf
+        trees with numeric splits. Categorical splits, vector or linear
+        leaves, the linear booster, shrinkage, Boulevard and EBM models are
+        refused with a ValueError naming the feature."""
+        doc = json.loads(text)
+        for key in cls._JSON_UNSUPPORTED:
+            if doc.get(key) is not None:
+                raise ValueError(f"model: '{key}' is not carried by this backend")
+        trees = []
+        for i, t in enumerate(doc["trees"]):
+            if t.get("size_leaf_vector", 0) > 1 or t.get("leaf_vectors"):
+                raise ValueError(f"model: tree {i} has vector leaves")
+            if t.get("linear") is not None:
+                raise ValueError(f"model: tree {i} has linear leaves")
+            nodes = t["nodes"]
+            if any(n.get("is_categorical") for n in nodes):
+                raise ValueError(f"model: tree {i} has categorical splits")
+            trees.append({
+                "split_feature": np.array([n["split_feature"] for n in nodes], np.uint32),
+                "split_cond": np.array([n["split_cond"] for n in nodes], np.float32),
+                "default_left": np.array([n["default_left"] for n in nodes], np.uint8),
+                "left": np.array([n["left"] for n in nodes], np.int32),
+                "right": np.array([n["right"] for n in nodes], np.int32),
+                "leaf_value": np.array([n["leaf_value"] for n in nodes], np.float32),
+                "sum_hess": np.array([n.get("sum_hess", 0.0) for n in nodes], np.float32),
+                "split_gain": np.array([n.get("split_gain", 0.0) for n in nodes], np.float32),
+            })
+        return cls(objective=doc["objective"], base_score=np.array(doc["base_score"], np.float32), trees=trees,
+                   n_outputs=int(doc["n_outputs"]), n_features=int(doc["n_features"]),
+                   tree_weights=np.array(doc["tree_weights"], np.float32), num_class=int(doc["num_class"]),
+                   n_targets=int(doc.get("n_targets", 1)),
+                   best_iteration=doc.get("best_iteration"), num_parallel_tree=int(doc["num_parallel_tree"]),
+                   objective_params=dict(doc.get("objective_params") or {}))
 
 
 class Trainer:
@@ -585,8 +648,12 @@ class Trainer:
         return out
 
     def booster(self, n_features):
+        softmax = self.objective in ("multi:softprob", "multi:softmax")
         return Booster(objective=self.objective, base_score=self.base_score(), trees=self.trees(),
-                       n_outputs=self.n_outputs, n_features=n_features)
+                       n_outputs=self.n_outputs, n_features=n_features,
+                       num_class=self.n_outputs if softmax else 0,
+                       objective_params={"scale_pos_weight": float(self.params.scale_pos_weight),
+                                         "max_delta_step": float(self.params.max_delta_step)})
 
 
 def train(params: dict, dtrain: DMatrix, num_boost_round: int = 10, *, device="rocm:0") -> Booster:

@@ -8,6 +8,12 @@ tree weights and outputs, the base score, and the recorded margins, every
 f32 stored as its bit pattern. The input rows are not stored: they are
 regenerated in closed form (tests/common/mod.rs:28-39, four_features).
 
+It also copies, minified, the 0.4.9 JSON model documents themselves into
+tests/golden/models/ (the JSON model format, model/serde.rs): the saved
+models of the cases above, which the JSON reader and writer must reproduce,
+and three whose features this path does not carry (categorical splits, a
+linear booster, vector leaves), which the reader must refuse.
+
 Run once in a checkout that has the reference under /root/reference:
     python tests/golden/make_fixtures.py
 """
@@ -64,6 +70,12 @@ def main():
             }
     json.dump(out, open(OUT, "w"), separators=(",", ":"))
     print(f"wrote {len(out)} cases to {OUT}")
+    models = os.path.join(os.path.dirname(OUT), "models")
+    os.makedirs(models, exist_ok=True)
+    for case in CASES + ["categorical_splits", "gblinear", "vector_leaves"]:
+        doc = json.load(open(os.path.join(REF, "0.4.9", case + ".json")))
+        json.dump(doc, open(os.path.join(models, case + ".json"), "w"), separators=(",", ":"))
+    print(f"copied {len(CASES) + 3} JSON models to {models}")
 
 
 if __name__ == "__main__":

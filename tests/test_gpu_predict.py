@@ -26,6 +26,32 @@ def test_saved_models_reproduce_recorded_margins(name):
         assert np.array_equal(got.view(np.uint32), np.array(case["margins"], np.uint32)), f"{ver}/{name}"
 
 
+@pytest.mark.parametrize("name", CASES)
+def test_reference_json_models_predict_recorded_margins(name):
+    """The reference's saved JSON models (tests/golden/models, read with
+    Booster.load_model_json) predict the recorded f32 margins bit for bit."""
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "models", name + ".json")
+    b = hb.Booster.load_model_json(open(path).read())
+    got = b.predict(four_features(), output_margin=True)
+    want = np.array(load_saved_models()[f"0.4.9/{name}"]["margins"], np.uint32)
+    assert np.array_equal(np.asarray(got, np.float32).reshape(-1).view(np.uint32), want)
+
+
+def test_trained_model_survives_json_round_trip():
+    x = synthetic.predict_rows(n=5_000, f=9, seed=12)
+    y = (np.nan_to_num(x[:, 0]) > 0).astype(np.float32) + (np.nan_to_num(x[:, 1]) > 0.5).astype(np.float32)
+    for params in ({"objective": "binary:logistic", "max_depth": 5, "scale_pos_weight": 2.0},
+                   {"objective": "multi:softprob", "num_class": 3, "max_depth": 4},
+                   {"objective": "reg:squarederror", "grow_policy": "lossguide", "max_depth": 0, "max_leaves": 12}):
+        yy = (y > 0).astype(np.float32) if params["objective"] == "binary:logistic" else y
+        model = hb.train(params, hb.DMatrix(x, label=yy), 4)
+        back = hb.Booster.load_model_json(model.save_model_json())
+        a = model.predict(x, output_margin=True)
+        c = back.predict(x, output_margin=True)
+        assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(c).view(np.uint32)), params
+
+
 def test_synthetic_forest_leaves_and_margins_match_oracle():
     trees = synthetic.forest(n_trees=50, depth=8, n_features=100, seed=7)
     x = synthetic.predict_rows(n=20_000, f=100, seed=8)
