@@ -404,8 +404,8 @@ class DMatrix:
             return self.x
         out = np.full((self.n_rows, self.n_cols), np.nan, np.float32)
         rp, col, val = self.csr
-        for r in range(self.n_rows):
-            out[r, col[rp[r]:rp[r + 1]]] = val[rp[r]:rp[r + 1]]
+        rows = np.repeat(np.arange(self.n_rows), np.diff(rp.astype(np.int64)))
+        out[rows, col[:rp[-1]]] = val[:rp[-1]]
         return out
 
 
@@ -647,6 +647,32 @@ class Trainer:
         A.check(A.lib().hbr_trainer_margins(self._h, A.ptr(out)))
         return out
 
+    def add_eval(self, data: "DMatrix", base_margin=None) -> int:
+        """An evaluation set whose margins the device keeps up to date as
+        trees are grown (the host's add_tree_to_evals,
+        src/training/margins.rs:148-152, called from round.rs:141-143):
+        base score (or `base_margin`, [n_rows][n_outputs]) plus every tree,
+        routed by raw value. Returns the set's number."""
+        x = np.ascontiguousarray(data.dense(), np.float32)
+        self._evals = getattr(self, "_evals", [])
+        bm = None
+        if base_margin is not None:
+            bm = np.ascontiguousarray(base_margin, np.float32).reshape(-1)
+            if bm.size != x.shape[0] * self.n_outputs:
+                raise ValueError("base_margin must hold n_rows * n_outputs values")
+        idx = C.c_uint32()
+        A.check(A.lib().hbr_trainer_add_eval(self._h, A.ptr(x), x.shape[0], x.shape[1], float(data.missing),
+                                             A.ptr(bm), C.byref(idx)))
+        self._evals.append(x.shape[0])
+        return idx.value
+
+    def eval_margins(self, index: int):
+        """Eval set `index`'s margins, [n_rows][n_outputs]."""
+        n = self._evals[index]
+        out = np.empty(n * self.n_outputs, np.float32)
+        A.check(A.lib().hbr_trainer_eval_margins(self._h, index, A.ptr(out)))
+        return out.reshape(n, self.n_outputs)
+
     def booster(self, n_features):
         softmax = self.objective in ("multi:softprob", "multi:softmax")
         return Booster(objective=self.objective, base_score=self.base_score(), trees=self.trees(),
@@ -656,15 +682,26 @@ class Trainer:
                                          "max_delta_step": float(self.params.max_delta_step)})
 
 
-def train(params: dict, dtrain: DMatrix, num_boost_round: int = 10, *, device="rocm:0") -> Booster:
+def train(params: dict, dtrain: DMatrix, num_boost_round: int = 10, *, evals=(), device="rocm:0") -> Booster:
     """hessboost.train for `tree_method=hist` on one MI355X
-    (src/training/api.rs:228-234)."""
+    (src/training/api.rs:228-234; python/python/hessboost/_training.py:161-175).
+
+    `evals`: (DMatrix, name) pairs with dtrain's features; their margins are
+    updated on the device after every tree and returned as the booster's
+    `eval_margins` ({name: [n_rows][n_outputs]}). Metrics over them are the
+    caller's."""
     if params.get("tree_method", "hist") not in ("hist", "auto"):
         raise ValueError("this backend trains tree_method=hist")
     engine = dtrain.engine(params.get("max_bin", 256), _device_ordinal(device))
     t = Trainer(engine, params, dtrain.label, dtrain.weight)
+    names = []
+    for data, name in evals:
+        if data.n_cols != dtrain.n_cols:
+            raise ValueError(f"eval set {name!r} does not have the training matrix's features")
+        names.append((t.add_eval(data), name))
     t.boost(num_boost_round)
     b = t.booster(dtrain.n_cols)
+    b.eval_margins = {name: t.eval_margins(i) for i, name in names}
     return b
 
 

@@ -552,6 +552,28 @@ struct WalkArgs {
     uint32_t *poison;
 };
 
+// A finished tree added to the margins of an evaluation set by raw value:
+// a present value goes left iff value < cut_values[bin] (-FLT_MAX for bin
+// -1), a missing one follows default_left.
+constexpr uint32_t kEvalLdsNodes = 2048;
+struct EvalWalkArgs {
+    const float *x;              // [n][n_cols] row-major
+    const GrowTreeNode *tree;    // the tree's records
+    const GrowCounts *counts;    // a device-grown tree's node count, or null (n_nodes)
+    const float *cut_values;     // global bin -> threshold
+    float *margins;              // [n][m_stride]
+    const uint32_t *poison;      // non-null: nothing is added while *poison is set
+    uint64_t n;
+    uint32_t n_cols;
+    uint32_t m_stride;
+    uint32_t output;
+    uint32_t n_nodes;
+    float missing_value;         // the absent marker (NaN: any NaN)
+    uint32_t missing_is_nan;
+    uint32_t total_bins;         // cut_values' length
+    uint32_t pad;
+};
+
 // The margin walk of a finished tree followed, row by row, by the next
 // round's gradients of the updated margin (the gradient kernel's arithmetic
 // and max fold; w.margins and g.margins are the same array).

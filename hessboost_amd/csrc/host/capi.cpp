@@ -584,6 +584,18 @@ int hbr_trainer_margins(hbr_trainer *t, float *out) {
     return with_engine(t->engine, [&](Engine &) { t->t->margins(out); });
 }
 
+int hbr_trainer_add_eval(hbr_trainer *t, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                         const float *base_margin, uint32_t *index) {
+    if (!t || !x || !index) return set_error(HBR_INVALID, "trainer: null argument");
+    return with_engine(t->engine,
+                       [&](Engine &) { *index = t->t->add_eval(x, n_rows, n_cols, missing, base_margin); });
+}
+
+int hbr_trainer_eval_margins(hbr_trainer *t, uint32_t index, float *out) {
+    if (!t || !out) return set_error(HBR_INVALID, "trainer: null argument");
+    return with_engine(t->engine, [&](Engine &) { t->t->eval_margins(index, out); });
+}
+
 void hbr_trainer_free(hbr_trainer *t) { delete t; }
 
 // ---- prediction -------------------------------------------------------------------------

@@ -1373,6 +1373,87 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     scale_checked_ = false;  // the next tree's finish checks the scale
 }
 
+uint32_t Engine::add_eval_set(const float *x, uint64_t n_rows, uint64_t n_cols, float missing, const float *init,
+                              uint32_t outputs) {
+    if (!x || !init) fail(kInvalid, "evaluation set: null argument");
+    if (n_cols != n_cols_) fail(kInvalid, "evaluation set: not the training matrix's features");
+    if (n_rows == 0) fail(kInvalid, "evaluation set: no rows");
+    if (outputs == 0) fail(kInvalid, "evaluation set: no outputs");
+    hipStream_t s = dev_.stream();
+    if (d_cuts_.size() != total_bins_ && total_bins_ > 0) {
+        d_cuts_.resize(total_bins_);
+        d_cuts_.upload(cuts_.data(), total_bins_, s);
+    }
+    auto set = std::make_unique<EvalSet>();
+    set->n_rows = n_rows;
+    set->outputs = outputs;
+    set->missing = missing;
+    set->x.resize(n_rows * n_cols);
+    set->x.upload(x, n_rows * n_cols, s);
+    set->margins.resize(n_rows * outputs);
+    set->margins.upload(init, n_rows * outputs, s);
+    dev_.sync();
+    evals_.push_back(std::move(set));
+    return (uint32_t)evals_.size() - 1;
+}
+
+uint64_t Engine::eval_rows(uint32_t set) const {
+    if (set >= evals_.size()) fail(kInvalid, "evaluation set: no such set");
+    return evals_[set]->n_rows;
+}
+
+void Engine::read_eval_margins(uint32_t set, float *out) {
+    if (set >= evals_.size()) fail(kInvalid, "evaluation set: no such set");
+    const EvalSet &e = *evals_[set];
+    e.margins.download(out, e.n_rows * e.outputs, dev_.stream());
+    dev_.sync();
+}
+
+void Engine::launch_eval_walk(const EvalSet &set, const GrowTreeNode *tree, const GrowCounts *counts,
+                              uint32_t n_nodes, uint32_t output, const uint32_t *poison) {
+    if (output >= set.outputs) fail(kInvalid, "evaluation walk: no such output");
+    EvalWalkArgs a{};
+    a.x = set.x.get();
+    a.tree = tree;
+    a.counts = counts;
+    a.cut_values = d_cuts_.get();
+    a.margins = set.margins.get();
+    a.poison = poison;
+    a.n = set.n_rows;
+    a.n_cols = n_cols_;
+    a.m_stride = set.outputs;
+    a.output = output;
+    a.n_nodes = n_nodes;
+    a.missing_value = set.missing;
+    a.missing_is_nan = std::isnan(set.missing) ? 1u : 0u;
+    a.total_bins = (uint32_t)total_bins_;
+    const uint64_t want = (set.n_rows + 255) / 256;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>(want, (uint64_t)dev_.cu_count() * 8);
+    dev_.launch("hbr_eval_walk", dim3(blocks), dim3(256), a);
+}
+
+void Engine::walk_evals_device(uint32_t output, uint32_t tree, bool guarded) {
+    if (evals_.empty()) return;
+    if (guarded && !poison_.size()) fail(kInvalid, "evaluation walk: no guarded walk before it");
+    for (const auto &set : evals_)
+        launch_eval_walk(*set, ring_nodes(last_ring_, tree, last_stride_),
+                         &ring_header(last_ring_, tree, last_stride_)->counts, 0, output,
+                         guarded ? poison_.get() : nullptr);
+}
+
+void Engine::walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output) {
+    if (evals_.empty() || nodes.empty()) return;
+    upload_vec(d_eval_tree_, nodes, stage_, dev_.stream());
+    for (const auto &set : evals_) launch_eval_walk(*set, d_eval_tree_.get(), nullptr, (uint32_t)nodes.size(), output, nullptr);
+}
+
+void Engine::walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output) {
+    if (set >= evals_.size()) fail(kInvalid, "evaluation set: no such set");
+    if (nodes.empty()) return;
+    upload_vec(d_eval_tree_, nodes, stage_, dev_.stream());
+    launch_eval_walk(*evals_[set], d_eval_tree_.get(), nullptr, (uint32_t)nodes.size(), output, nullptr);
+}
+
 void Engine::add_leaves(const std::vector<Segment> &segs, const std::vector<float> &values, uint32_t output) {
     if (segs.empty()) return;
     std::vector<LeafSeg> leaves(segs.size());

@@ -4,6 +4,7 @@
 // RowEngine, src/tree/hist/mod.rs:73-295).
 #pragma once
 #include <algorithm>
+#include <memory>
 #include <cstdint>
 #include <mutex>
 #include <string>
@@ -186,6 +187,25 @@ public:
     // The walk alone (no gradients): any dense u8 index, any output.
     bool can_route_device_tree(uint64_t max_depth) const { return can_grow_device(max_depth); }
     void walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree = 0);
+
+    // ---- evaluation sets ----------------------------------------------------------
+    // A dense f32 matrix (row-major, the index's features, `missing` marks
+    // an absent value; NaN: any NaN) kept on the device with its margins
+    // ([n][outputs], from `init`), into which finished trees are walked by
+    // raw value. Returns the set's number.
+    uint32_t add_eval_set(const float *x, uint64_t n_rows, uint64_t n_cols, float missing, const float *init,
+                          uint32_t outputs);
+    // The last queued device tree (as walk_device_tree names it) into every
+    // set's margins of `output`; `guarded`: not when the guarded training
+    // walk before it skipped the tree.
+    void walk_evals_device(uint32_t output, uint32_t tree, bool guarded);
+    // A tree given as records (a host-grown tree) into every set's margins.
+    void walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output);
+    // ... into one set's margins only (a set added after trees were grown).
+    void walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output);
+    uint32_t n_eval_sets() const { return (uint32_t)evals_.size(); }
+    uint64_t eval_rows(uint32_t set) const;
+    void read_eval_margins(uint32_t set, float *out);
     // HistogramBackend::build of a host row list (per-node host growth).
     std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
     std::vector<uint32_t> rows_of(const Segment &s);
@@ -299,6 +319,17 @@ private:
     GPair *pairs() const { return active_pairs_ ? active_pairs_ : gpair_.get(); }
     bool pairs_staged() const { return active_pairs_ || (gpair_.size() >= n_rows_ && gpair_.get()); }
     DBuf<float> margins_, labels_, weights_;
+    struct EvalSet {
+        DBuf<float> x, margins;
+        uint64_t n_rows = 0;
+        uint32_t outputs = 1;
+        float missing = 0.0f;
+    };
+    std::vector<std::unique_ptr<EvalSet>> evals_;
+    DBuf<float> d_cuts_;             // cut values for the evaluation walks
+    DBuf<GrowTreeNode> d_eval_tree_; // a host-grown tree's records
+    void launch_eval_walk(const EvalSet &set, const GrowTreeNode *tree, const GrowCounts *counts, uint32_t n_nodes,
+                          uint32_t output, const uint32_t *poison);
     uint32_t outputs_ = 1;
     bool labels_loaded_ = false, has_weights_ = false;
     // the per-tree scale, the root total and the root's winner, adjacent so

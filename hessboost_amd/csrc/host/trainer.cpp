@@ -432,6 +432,7 @@ void Trainer::grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_los
     trees_.push_back(b.grow(&leaves, walk));
     const Tree &t = trees_.back();
     grads_ready_ = false;
+    if (e_.n_eval_sets()) e_.walk_evals(records_of(t), output);
     if (walk) {
         const size_t n = t.nodes.size();
         std::vector<uint32_t> meta(n), left(n, 0);
@@ -477,6 +478,7 @@ void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
             if (!grads_ready_) e_.compute_gradients_async(loss, 0);
             inflight.push_back(b.queue_device());
             e_.walk_device_tree(0, &loss);
+            e_.walk_evals_device(0, 0, true);
             grads_ready_ = true;
             queued++;
         }
@@ -510,6 +512,7 @@ void Trainer::boost_softmax_pipelined(uint64_t rounds) {
             e_.select_class(c);
             inflight.push_back(b.queue_device());
             e_.walk_device_tree(c, nullptr);
+            e_.walk_evals_device(c, 0, false);
             queued++;
         }
         std::vector<GrowTreeNode> nodes;
@@ -536,7 +539,10 @@ void Trainer::boost_softmax_batched(uint64_t rounds) {
         while (queued < rounds && inflight.size() < 3) {
             e_.softmax_gradients_async(kMinHess);
             inflight.push_back(b.queue_classes());
-            for (uint32_t c = 0; c < k_; c++) e_.walk_device_tree(c, nullptr, c);
+            for (uint32_t c = 0; c < k_; c++) {
+                e_.walk_device_tree(c, nullptr, c);
+                e_.walk_evals_device(c, c, false);
+            }
             queued++;
         }
         std::vector<std::vector<GrowTreeNode>> trees;
@@ -597,5 +603,37 @@ hbr_device_loss Trainer::device_loss() const {
 }
 
 void Trainer::margins(float *out) { e_.read_margins(out, n_ * k_); }
+
+// A tree's nodes as the device walks read them: split bin (the threshold is
+// its cut value), feature, default direction, children, leaf value.
+std::vector<GrowTreeNode> records_of(const Tree &t) {
+    std::vector<GrowTreeNode> r(t.nodes.size());
+    for (size_t i = 0; i < t.nodes.size(); i++) {
+        const TreeNode &n = t.nodes[i];
+        GrowTreeNode &g = r[i];
+        g = GrowTreeNode{};
+        g.left = n.left;
+        g.value = n.leaf_value;
+        if (n.left < 0) continue;
+        g.feature = n.split_feature;
+        g.bin = (int32_t)n.split_bin;
+        g.default_left = n.default_left;
+    }
+    return r;
+}
+
+// An evaluation set (training/margins.rs:148-152): its margins start from
+// `base_margin` ([n][outputs]) or the base score, then take every tree
+// grown so far, and every later tree as it is grown.
+uint32_t Trainer::add_eval(const float *x, uint64_t n, uint64_t n_cols, float missing, const float *base_margin) {
+    std::vector<float> init(n * k_);
+    for (uint64_t r = 0; r < n; r++)
+        for (uint32_t c = 0; c < k_; c++) init[r * k_ + c] = base_margin ? base_margin[r * k_ + c] : base_[c];
+    const uint32_t set = e_.add_eval_set(x, n, n_cols, missing, init.data(), k_);
+    for (size_t t = 0; t < trees_.size(); t++) e_.walk_evals_one(set, records_of(trees_[t]), (uint32_t)(t % k_));
+    return set;
+}
+
+void Trainer::eval_margins(uint32_t set, float *out) { e_.read_eval_margins(set, out); }
 
 }  // namespace hbr

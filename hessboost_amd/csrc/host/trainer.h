@@ -114,6 +114,12 @@ public:
     const std::vector<float> &base_score() const { return base_; }
     const std::vector<Tree> &trees() const { return trees_; }
     void margins(float *out);
+    // Evaluation sets: a dense f32 matrix of the training features whose
+    // margins follow the trees on the device (base_margin: [n][outputs] or
+    // null for the base score).
+    uint32_t add_eval(const float *x, uint64_t n, uint64_t n_cols, float missing, const float *base_margin);
+    void eval_margins(uint32_t set, float *out);
+    uint64_t eval_rows(uint32_t set) const { return e_.eval_rows(set); }
     // softmax depthwise rounds grow their class trees as one batch (else one
     // class tree after another); HBROCM_SOFTMAX_BATCH=0 turns it off
     bool softmax_batches = true;
@@ -136,6 +142,8 @@ private:
     std::vector<float> base_;
     std::vector<Tree> trees_;
 };
+
+std::vector<GrowTreeNode> records_of(const Tree &t);
 
 // The loss's intercepts (objective base margins, train.rs:406-436).
 std::vector<float> base_margins(const TrainParams &p, const float *labels, const float *weights, uint64_t n);

@@ -366,3 +366,74 @@ extern "C" __global__ __launch_bounds__(64) void hbr_predict_resident_nan(Predic
 extern "C" __global__ __launch_bounds__(64) void hbr_predict_resident(PredictArgs a) {
     predict_resident<false, 16, true>(a);
 }
+
+// ---- evaluation sets --------------------------------------------------------
+//
+// A finished tree added into an evaluation set's margins as the host's
+// training loop adds it (training/margins.rs:148-152 via add_tree_margins,
+// :186-196): margin[output] += leaf(tree, row), one f32 add, the row routed
+// by raw value. A device-grown tree is read from its records where its
+// growth wrote them, so the walk queues behind the growth on the stream;
+// a split's threshold is the cut value of its bin boundary, as the tree's
+// host copy records it. Thread per row; the tree's nodes sit in LDS as
+// (threshold, feature | default_left << 31, left child or ~0 for a leaf,
+// value) when they fit.
+
+namespace {
+
+__device__ __forceinline__ uint4 eval_node(const EvalWalkArgs &a, uint32_t i) {
+    const GrowTreeNode t = a.tree[i];
+    uint4 w;
+    if (t.left < 0) {
+        w.x = 0u;
+        w.y = 0u;
+        w.z = 0xffffffffu;
+    } else {
+        const float cond =
+            t.bin >= 0 && (uint32_t)t.bin < a.total_bins ? a.cut_values[t.bin] : -__FLT_MAX__;
+        w.x = __float_as_uint(cond);
+        w.y = min(t.feature, a.n_cols - 1u) | (t.default_left ? 1u << 31 : 0u);
+        w.z = (uint32_t)t.left;
+    }
+    w.w = __float_as_uint(t.value);
+    return w;
+}
+
+template <bool kLds>
+__device__ __forceinline__ void eval_walk(const EvalWalkArgs &a, const uint4 *s_node, uint32_t n_nodes) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += stride) {
+        const float *row = a.x + r * a.n_cols;
+        uint4 nd = kLds ? s_node[0] : eval_node(a, 0);
+        bool leaf = nd.z == 0xffffffffu;
+        for (uint32_t step = 0; step < n_nodes && !leaf; step++) {
+            const float v = row[nd.y & 0x7fffffffu];
+            const bool absent = a.missing_is_nan ? __builtin_isnan(v) : v == a.missing_value;
+            const bool go_left = absent ? (nd.y >> 31) != 0u : v < __uint_as_float(nd.x);
+            const uint32_t nid = nd.z + (go_left ? 0u : 1u);
+            if (nid >= n_nodes) break;  // a malformed record: the row gets nothing
+            nd = kLds ? s_node[nid] : eval_node(a, nid);
+            leaf = nd.z == 0xffffffffu;
+        }
+        if (leaf) {
+            float *m = a.margins + r * a.m_stride + a.output;
+            *m = *m + __uint_as_float(nd.w);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void hbr_eval_walk(EvalWalkArgs a) {
+    __shared__ uint4 s_node[kEvalLdsNodes];
+    if (a.poison && *a.poison != 0u) return;  // uniform: the tree was not kept
+    const uint32_t n_nodes = a.counts ? a.counts->n_nodes : a.n_nodes;
+    if (n_nodes == 0 || a.n_cols == 0) return;
+    if (n_nodes <= kEvalLdsNodes) {
+        for (uint32_t i = threadIdx.x; i < n_nodes; i += blockDim.x) s_node[i] = eval_node(a, i);
+        __syncthreads();
+        eval_walk<true>(a, s_node, n_nodes);
+    } else {
+        eval_walk<false>(a, nullptr, n_nodes);
+    }
+}

@@ -359,6 +359,18 @@ int hbr_trainer_tree(hbr_trainer *t, uint64_t tree, uint32_t *split_feature, flo
                      float *sum_hess, float *split_gain, int64_t *split_bin);
 /* The training margins (n_rows * n_outputs). */
 int hbr_trainer_margins(hbr_trainer *t, float *out);
+/* An evaluation set (the `evals` of training, src/training/margins.rs:148-152
+ * and src/training/round.rs:141-143, where the host adds each tree to every
+ * eval set's margins): a dense row-major f32 matrix with the training
+ * matrix's n_cols features (`missing` marks an absent value, NaN: any NaN),
+ * copied to the device. Its margins start from base_margin (n_rows *
+ * n_outputs, or NULL for the base score), take every tree grown so far and
+ * then every later tree on the device as it is grown, routed by raw value.
+ * *index receives the set's number. */
+int hbr_trainer_add_eval(hbr_trainer *t, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                         const float *base_margin, uint32_t *index);
+/* Eval set `index`'s margins (n_rows * n_outputs, row-major). */
+int hbr_trainer_eval_margins(hbr_trainer *t, uint32_t index, float *out);
 void hbr_trainer_free(hbr_trainer *t);
 
 /* ------------------------------------------------------------------------- */

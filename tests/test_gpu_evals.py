@@ -1,0 +1,146 @@
+"""Evaluation sets on the device: after training, each eval set's margins are
+the base score (or its base margin) plus every tree walked over its raw
+rows, which the oracle's margin walk computes from the same trees
+(or_predict_margin: base, then one f32 add per tree in order). Bit-exact,
+for every growth path that grows the trees: the pipelined scalar losses
+(guarded device walks), the batched and per-class softmax rounds, and the
+host-driven growth (lossguide, CSR training input)."""
+import numpy as np
+import pytest
+
+import hessboost_amd as hb
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def expected(booster, x, missing=np.nan, base_margin=None):
+    k = booster.n_outputs
+    arrs = O.forest_arrays(booster.trees, tree_output=[t % k for t in range(len(booster.trees))], n_outputs=k,
+                           base_score=booster.base_score if base_margin is None else np.zeros(k))
+    out = O.predict_margin(arrs, x, missing=missing).reshape(-1, k)
+    if base_margin is not None:
+        # base margin first, then the trees in order (the walk's order of adds)
+        out = np.asarray(base_margin, np.float32).reshape(-1, k).copy()
+        for t, tree in enumerate(booster.trees):
+            one = O.forest_arrays([tree], tree_output=[t % k], n_outputs=k, base_score=np.zeros(k))
+            out = (out + O.predict_margin(one, x, missing=missing).reshape(-1, k)).astype(np.float32)
+    return out
+
+
+def data(n, f, seed, objective="reg:squarederror", k=1, missing=0.0):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    z = x[:, 0] - 0.5 * x[:, 1 % f] + np.sin(2 * x[:, 2 % f])
+    if objective == "reg:squarederror":
+        y = (z + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    elif objective == "binary:logistic":
+        y = (rng.random(n) < 1 / (1 + np.exp(-2 * z))).astype(np.float32)
+    else:
+        y = np.clip(np.floor((z - z.min()) / (np.ptp(z) + 1e-9) * k), 0, k - 1).astype(np.float32)
+    if missing > 0:
+        x[rng.random((n, f)) < missing] = np.nan
+    return x, y
+
+
+def eval_matrix(n, f, seed):
+    """Rows beyond the training range, infinities and missing values."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((n, f)) * 1.5).astype(np.float32)
+    x[rng.random((n, f)) < 0.1] = np.nan
+    x[0, :] = np.inf
+    x[1, :] = -np.inf
+    x[2, :] = 1e30
+    x[3, :] = -1e30
+    return x
+
+
+CASES = [
+    # name, params, n_features, training missing fraction
+    ("pipelined squared error", {"objective": "reg:squarederror", "max_depth": 6}, 28, 0.0),
+    ("pipelined logistic", {"objective": "binary:logistic", "max_depth": 5}, 20, 0.0),
+    ("batched softmax", {"objective": "multi:softprob", "num_class": 3, "max_depth": 4}, 12, 0.0),
+    ("lossguide", {"objective": "reg:squarederror", "grow_policy": "lossguide", "max_depth": 0,
+                   "max_leaves": 17}, 10, 0.0),
+    ("missing values in training", {"objective": "binary:logistic", "max_depth": 4}, 9, 0.2),
+    ("wide rows", {"objective": "reg:squarederror", "max_depth": 7}, 40, 0.0),
+    ("deep tree off LDS", {"objective": "reg:squarederror", "max_depth": 12, "min_child_weight": 0.0,
+                           "lambda": 0.0}, 6, 0.0),
+]
+
+
+@pytest.mark.parametrize("name,params,f,miss", CASES, ids=[c[0] for c in CASES])
+def test_eval_margins_match_oracle_walk(name, params, f, miss):
+    print("eval case", name, flush=True)
+    k = params.get("num_class", 1)
+    x, y = data(20_000, f, 7, params["objective"], k, miss)
+    ev1 = eval_matrix(3_001, f, 8)
+    ev2 = data(777, f, 9, params["objective"], k)[0]
+    dtrain = hb.DMatrix(x, label=y)
+    model = hb.train(dict(params, eta=0.3), dtrain, 6,
+                     evals=[(hb.DMatrix(ev1), "a"), (hb.DMatrix(ev2), "b")])
+    assert set(model.eval_margins) == {"a", "b"}
+    if name == "deep tree off LDS":  # trees beyond the walk's LDS node table
+        assert max(len(t["left"]) for t in model.trees) > 2048
+    for ev, key in ((ev1, "a"), (ev2, "b")):
+        got = model.eval_margins[key]
+        want = expected(model, ev)
+        assert got.shape == want.shape
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=f"{name} {key}")
+        # and the product's own prediction of the same rows
+        np.testing.assert_array_equal(got.reshape(-1), model.predict(ev, output_margin=True).reshape(-1))
+
+
+def test_softmax_per_class_rounds(monkeypatch):
+    monkeypatch.setenv("HBROCM_SOFTMAX_BATCH", "0")
+    x, y = data(8_000, 10, 11, "multi:softprob", 4)
+    ev = eval_matrix(1_500, 10, 12)
+    model = hb.train({"objective": "multi:softprob", "num_class": 4, "max_depth": 5}, hb.DMatrix(x, label=y), 4,
+                     evals=[(hb.DMatrix(ev), "e")])
+    np.testing.assert_array_equal(model.eval_margins["e"].view(np.uint32), expected(model, ev).view(np.uint32))
+
+
+def test_csr_training_input():
+    x, y = data(6_000, 15, 13, "reg:squarederror", 1, 0.4)
+    present = ~np.isnan(x)
+    rp = np.zeros(x.shape[0] + 1, np.uint64)
+    rp[1:] = np.cumsum(present.sum(1))
+    rows, cols = np.nonzero(present)
+    dtrain = hb.DMatrix((rp, cols.astype(np.uint32), x[rows, cols]), label=y, n_cols=15)
+    ev = eval_matrix(900, 15, 14)
+    model = hb.train({"objective": "reg:squarederror", "max_depth": 5}, dtrain, 5, evals=[(hb.DMatrix(ev), "e")])
+    np.testing.assert_array_equal(model.eval_margins["e"].view(np.uint32), expected(model, ev).view(np.uint32))
+
+
+def test_added_after_rounds_with_base_margin_and_missing_marker():
+    """A set added after some rounds takes the trees already grown; a base
+    margin replaces the base score; a non-NaN missing marker is honoured."""
+    x, y = data(10_000, 16, 15, "binary:logistic")
+    dtrain = hb.DMatrix(x, label=y)
+    engine = dtrain.engine(256)
+    t = hb.Trainer(engine, {"objective": "binary:logistic", "max_depth": 6}, y)
+    ev = eval_matrix(2_000, 16, 16)
+    ev[np.isnan(ev)] = -999.0
+    bm = np.linspace(-1, 1, ev.shape[0], dtype=np.float32)
+    first = t.add_eval(hb.DMatrix(ev, missing=-999.0), base_margin=bm)
+    t.boost(3)
+    late = t.add_eval(hb.DMatrix(ev, missing=-999.0))
+    t.boost(4)
+    booster = t.booster(16)
+    assert booster.num_trees() == 7
+    np.testing.assert_array_equal(t.eval_margins(first).view(np.uint32),
+                                  expected(booster, ev, -999.0, bm).view(np.uint32))
+    np.testing.assert_array_equal(t.eval_margins(late).view(np.uint32),
+                                  expected(booster, ev, -999.0).view(np.uint32))
+    # the training rows as an eval set: their margins are the trainer's own
+    tr = t.add_eval(dtrain)
+    np.testing.assert_array_equal(t.eval_margins(tr).reshape(-1), t.margins())
+
+
+def test_rejects_other_features():
+    x, y = data(2_000, 8, 17)
+    with pytest.raises(ValueError):
+        hb.train({"max_depth": 3}, hb.DMatrix(x, label=y), 1, evals=[(hb.DMatrix(x[:, :5]), "bad")])
+    t = hb.Trainer(hb.DMatrix(x, label=y).engine(256), {"max_depth": 3}, y)
+    with pytest.raises(hb.HbrError):
+        t.add_eval(hb.DMatrix(x[:, :5]))
