@@ -287,6 +287,31 @@ class Engine:
         A.check(A.lib().hbr_read_margins(self._h, A.ptr(out), n))
         return out
 
+    def add_eval(self, x, init_margins, missing=np.nan) -> int:
+        """An evaluation set (dense f32 rows of the index's features) with
+        its starting margins [n_rows][n_outputs], kept on the device."""
+        x = np.ascontiguousarray(x, np.float32)
+        init = np.ascontiguousarray(init_margins, np.float32).reshape(x.shape[0], -1)
+        idx = C.c_uint32()
+        A.check(A.lib().hbr_engine_add_eval(self._h, A.ptr(x), x.shape[0], x.shape[1], float(missing), A.ptr(init),
+                                            init.shape[1], C.byref(idx)))
+        self._eval_shapes = getattr(self, "_eval_shapes", [])
+        self._eval_shapes.append(init.shape)
+        return idx.value
+
+    def eval_add_tree(self, tree: dict, output=0):
+        """One tree (node arrays as the trainer returns them) added to every
+        eval set's margins of `output`, on the device."""
+        arrs = [np.ascontiguousarray(tree[k], dt) for k, dt in
+                (("split_feature", np.uint32), ("split_cond", np.float32), ("default_left", np.uint8),
+                 ("left", np.int32), ("right", np.int32), ("leaf_value", np.float32))]
+        A.check(A.lib().hbr_engine_eval_add_tree(self._h, *[A.ptr(a) for a in arrs], len(arrs[3]), output))
+
+    def eval_margins(self, index):
+        out = np.empty(self._eval_shapes[index], np.float32)
+        A.check(A.lib().hbr_engine_eval_margins(self._h, index, A.ptr(out)))
+        return out
+
     def reserve_hists(self, slots):
         fits = C.c_int()
         A.check(A.lib().hbr_reserve_hists(self._h, slots, C.byref(fits)))

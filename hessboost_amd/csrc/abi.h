@@ -561,6 +561,7 @@ struct EvalWalkArgs {
     const GrowTreeNode *tree;    // the tree's records
     const GrowCounts *counts;    // a device-grown tree's node count, or null (n_nodes)
     const float *cut_values;     // global bin -> threshold
+    const float *cond;           // per node thresholds (a caller's tree), or null: from the bins
     float *margins;              // [n][m_stride]
     const uint32_t *poison;      // non-null: nothing is added while *poison is set
     uint64_t n;

@@ -405,6 +405,47 @@ int hbr_read_margins(hbr_engine *h, float *out, uint64_t n) {
     return with_engine(h, [&](Engine &e) { e.read_margins(out, n); });
 }
 
+int hbr_engine_add_eval(hbr_engine *h, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                        const float *init_margins, uint32_t n_outputs, uint32_t *index) {
+    return with_engine(h, [&](Engine &e) {
+        if (!x || !init_margins || !index) fail(kInvalid, "evaluation set: null argument");
+        *index = e.add_eval_set(x, n_rows, n_cols, missing, init_margins, n_outputs);
+    });
+}
+
+int hbr_engine_eval_add_tree(hbr_engine *h, const uint32_t *split_feature, const float *split_cond,
+                             const uint8_t *default_left, const int32_t *left, const int32_t *right,
+                             const float *leaf_value, uint64_t n_nodes, uint32_t output) {
+    return with_engine(h, [&](Engine &e) {
+        if (!split_feature || !split_cond || !default_left || !left || !right || !leaf_value)
+            fail(kInvalid, "evaluation walk: null argument");
+        if (n_nodes == 0) fail(kInvalid, "evaluation walk: a tree without nodes");
+        std::vector<GrowTreeNode> nodes(n_nodes);
+        std::vector<float> cond(n_nodes, 0.0f);
+        for (uint64_t i = 0; i < n_nodes; i++) {
+            GrowTreeNode &g = nodes[i];
+            g = GrowTreeNode{};
+            g.left = left[i] < 0 ? -1 : left[i];
+            g.value = leaf_value[i];
+            if (left[i] < 0) continue;
+            if ((uint64_t)left[i] + 1 >= n_nodes || right[i] != left[i] + 1)
+                fail(kInvalid, "evaluation walk: children must be a pair of existing nodes (right = left + 1)");
+            if (split_feature[i] >= e.n_cols()) fail(kInvalid, "evaluation walk: split feature out of range");
+            g.feature = split_feature[i];
+            g.default_left = default_left[i] ? 1u : 0u;
+            cond[i] = split_cond[i];
+        }
+        e.walk_evals(nodes, output, &cond);
+    });
+}
+
+int hbr_engine_eval_margins(hbr_engine *h, uint32_t index, float *out) {
+    return with_engine(h, [&](Engine &e) {
+        if (!out) fail(kInvalid, "evaluation set: null argument");
+        e.read_eval_margins(index, out);
+    });
+}
+
 int hbr_reserve_hists(hbr_engine *h, uint64_t slots, int *fits) {
     return with_engine(h, [&](Engine &e) { *fits = e.reserve_slots(slots) ? 1 : 0; });
 }

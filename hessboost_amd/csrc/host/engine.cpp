@@ -1410,13 +1410,14 @@ void Engine::read_eval_margins(uint32_t set, float *out) {
 }
 
 void Engine::launch_eval_walk(const EvalSet &set, const GrowTreeNode *tree, const GrowCounts *counts,
-                              uint32_t n_nodes, uint32_t output, const uint32_t *poison) {
+                              uint32_t n_nodes, uint32_t output, const uint32_t *poison, const float *cond) {
     if (output >= set.outputs) fail(kInvalid, "evaluation walk: no such output");
     EvalWalkArgs a{};
     a.x = set.x.get();
     a.tree = tree;
     a.counts = counts;
     a.cut_values = d_cuts_.get();
+    a.cond = cond;
     a.margins = set.margins.get();
     a.poison = poison;
     a.n = set.n_rows;
@@ -1441,10 +1442,19 @@ void Engine::walk_evals_device(uint32_t output, uint32_t tree, bool guarded) {
                          guarded ? poison_.get() : nullptr);
 }
 
-void Engine::walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output) {
+void Engine::walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output, const std::vector<float> *cond) {
     if (evals_.empty() || nodes.empty()) return;
+    if (nodes.size() > UINT32_MAX) fail(kRefused, "evaluation walk: a tree of more than 2^32 - 1 nodes");
+    for (const auto &set : evals_)
+        if (output >= set->outputs) fail(kInvalid, "evaluation walk: no such output");
     upload_vec(d_eval_tree_, nodes, stage_, dev_.stream());
-    for (const auto &set : evals_) launch_eval_walk(*set, d_eval_tree_.get(), nullptr, (uint32_t)nodes.size(), output, nullptr);
+    if (cond) {
+        if (cond->size() != nodes.size()) fail(kInvalid, "evaluation walk: one threshold per node");
+        upload_vec(d_eval_cond_, *cond, stage_, dev_.stream());
+    }
+    for (const auto &set : evals_)
+        launch_eval_walk(*set, d_eval_tree_.get(), nullptr, (uint32_t)nodes.size(), output, nullptr,
+                         cond ? d_eval_cond_.get() : nullptr);
 }
 
 void Engine::walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output) {

@@ -199,8 +199,10 @@ public:
     // set's margins of `output`; `guarded`: not when the guarded training
     // walk before it skipped the tree.
     void walk_evals_device(uint32_t output, uint32_t tree, bool guarded);
-    // A tree given as records (a host-grown tree) into every set's margins.
-    void walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output);
+    // A tree given as records (a host-grown tree) into every set's margins;
+    // `cond`: per node thresholds instead of the split bins' cut values.
+    void walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output,
+                    const std::vector<float> *cond = nullptr);
     // ... into one set's margins only (a set added after trees were grown).
     void walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output);
     uint32_t n_eval_sets() const { return (uint32_t)evals_.size(); }
@@ -328,8 +330,9 @@ private:
     std::vector<std::unique_ptr<EvalSet>> evals_;
     DBuf<float> d_cuts_;             // cut values for the evaluation walks
     DBuf<GrowTreeNode> d_eval_tree_; // a host-grown tree's records
+    DBuf<float> d_eval_cond_;
     void launch_eval_walk(const EvalSet &set, const GrowTreeNode *tree, const GrowCounts *counts, uint32_t n_nodes,
-                          uint32_t output, const uint32_t *poison);
+                          uint32_t output, const uint32_t *poison, const float *cond = nullptr);
     uint32_t outputs_ = 1;
     bool labels_loaded_ = false, has_weights_ = false;
     // the per-tree scale, the root total and the root's winner, adjacent so

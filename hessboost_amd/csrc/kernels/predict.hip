@@ -375,7 +375,8 @@ extern "C" __global__ __launch_bounds__(64) void hbr_predict_resident(PredictArg
 // by raw value. A device-grown tree is read from its records where its
 // growth wrote them, so the walk queues behind the growth on the stream;
 // a split's threshold is the cut value of its bin boundary, as the tree's
-// host copy records it. Thread per row; the tree's nodes sit in LDS as
+// host copy records it (or, for a tree the caller passes, its own
+// thresholds). Thread per row; the tree's nodes sit in LDS as
 // (threshold, feature | default_left << 31, left child or ~0 for a leaf,
 // value) when they fit.
 
@@ -389,8 +390,9 @@ __device__ __forceinline__ uint4 eval_node(const EvalWalkArgs &a, uint32_t i) {
         w.y = 0u;
         w.z = 0xffffffffu;
     } else {
-        const float cond =
-            t.bin >= 0 && (uint32_t)t.bin < a.total_bins ? a.cut_values[t.bin] : -__FLT_MAX__;
+        const float cond = a.cond ? a.cond[i]
+                           : t.bin >= 0 && (uint32_t)t.bin < a.total_bins ? a.cut_values[t.bin]
+                                                                          : -__FLT_MAX__;
         w.x = __float_as_uint(cond);
         w.y = min(t.feature, a.n_cols - 1u) | (t.default_left ? 1u << 31 : 0u);
         w.z = (uint32_t)t.left;

@@ -234,6 +234,26 @@ int hbr_add_leaf_values(hbr_engine *e, const hbr_segment *segs, const float *val
 /* RowEngine::read_margins. */
 int hbr_read_margins(hbr_engine *e, float *out, uint64_t n);
 
+/* Evaluation sets at the engine level, for a caller that drives its own
+ * rounds (src/training/round.rs:141-143, where the host then adds each
+ * finished tree to every eval set: margins.rs:148-152 add_tree_to_evals ->
+ * :186-196 add_tree_margins). hbr_engine_add_eval copies a dense row-major
+ * f32 matrix of the index's n_cols features (`missing` marks an absent
+ * value, NaN: any NaN) and its starting margins (n_rows * n_outputs) to the
+ * device; *index receives the set's number. hbr_engine_eval_add_tree adds
+ * one tree (the reference's Node fields, src/tree/regtree.rs:38-66, one
+ * array per field; children in pairs, right = left + 1; left < 0 marks a
+ * leaf) to every set's margins of `output`, each row routed by raw value (a
+ * present value goes left iff value < split_cond, a missing one follows
+ * default_left), queued on the engine's stream with no synchronisation. */
+int hbr_engine_add_eval(hbr_engine *e, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                        const float *init_margins, uint32_t n_outputs, uint32_t *index);
+int hbr_engine_eval_add_tree(hbr_engine *e, const uint32_t *split_feature, const float *split_cond,
+                             const uint8_t *default_left, const int32_t *left, const int32_t *right,
+                             const float *leaf_value, uint64_t n_nodes, uint32_t output);
+/* Eval set `index`'s margins (n_rows * n_outputs, row-major). */
+int hbr_engine_eval_margins(hbr_engine *e, uint32_t index, float *out);
+
 /* RowEngine::reserve_hists: fits = 0 (nothing reserved) when `slots`
  * histograms do not fit. */
 int hbr_reserve_hists(hbr_engine *e, uint64_t slots, int *fits);

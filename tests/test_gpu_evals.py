@@ -144,3 +144,47 @@ def test_rejects_other_features():
     t = hb.Trainer(hb.DMatrix(x, label=y).engine(256), {"max_depth": 3}, y)
     with pytest.raises(hb.HbrError):
         t.add_eval(hb.DMatrix(x[:, :5]))
+
+
+def test_engine_level_eval_sets_take_caller_trees():
+    """The engine-level entry points a caller driving its own rounds binds:
+    trees passed as node arrays with their own thresholds (here the
+    thresholds of unbalanced random trees, not cut values) added to two
+    sets of two outputs."""
+    rng = np.random.default_rng(21)
+    f = 7
+    x, y = data(3_000, f, 22)
+    engine = hb.DMatrix(x, label=y).engine(64)
+    ev = [eval_matrix(1_234, f, 23), eval_matrix(99, f, 24)]
+    init = [rng.standard_normal((e.shape[0], 2)).astype(np.float32) for e in ev]
+    ids = [engine.add_eval(e, i) for e, i in zip(ev, init)]
+    trees, outputs = [], []
+    for t in range(9):
+        nodes = [dict(leaf_value=float(rng.standard_normal()))]
+        n_splits = int(rng.integers(0, 40))
+        for _ in range(n_splits):  # split a random leaf into a pair of leaves
+            leaves = [i for i, nd in enumerate(nodes) if "left" not in nd]
+            i = int(rng.choice(leaves))
+            nodes[i].update(left=len(nodes), right=len(nodes) + 1, split_feature=int(rng.integers(0, f)),
+                            split_cond=float(np.float32(rng.standard_normal())), default_left=bool(rng.random() < 0.5))
+            nodes += [dict(leaf_value=float(rng.standard_normal())), dict(leaf_value=float(rng.standard_normal()))]
+        for nd in nodes:
+            nd.setdefault("left", -1)
+            nd.setdefault("right", -1)
+            nd.setdefault("split_feature", 0)
+            nd.setdefault("split_cond", 0.0)
+            nd.setdefault("default_left", True)
+        tree = {k: np.array([nd[k] for nd in nodes]) for k in nodes[0]}
+        out = t % 2
+        engine.eval_add_tree(tree, out)
+        trees.append(nodes)
+        outputs.append(out)
+    for i, e, m0 in zip(ids, ev, init):
+        want = m0.copy()
+        for nodes, out in zip(trees, outputs):
+            one = O.forest_arrays([nodes], tree_output=[out], n_outputs=2, base_score=np.zeros(2))
+            want = (want + O.predict_margin(one, e).reshape(-1, 2)).astype(np.float32)
+        np.testing.assert_array_equal(engine.eval_margins(i).view(np.uint32), want.view(np.uint32))
+    with pytest.raises(hb.HbrError):  # children not a pair
+        engine.eval_add_tree(dict(split_feature=[0, 0, 0], split_cond=[0.0, 0, 0], default_left=[1, 1, 1],
+                                  left=[2, -1, -1], right=[1, -1, -1], leaf_value=[0.0, 1, 2]))
