@@ -103,7 +103,9 @@ class ForestDesc(C.Structure):
     _fields_ = [("n_trees", C.c_uint64), ("tree_offset", u64p), ("split_feature", u32p),
                 ("split_cond", f32p), ("default_left", u8p), ("left", i32p), ("right", i32p),
                 ("leaf_value", f32p), ("tree_weight", f32p), ("tree_output", u32p),
-                ("n_outputs", C.c_uint32), ("pad", C.c_uint32), ("base_score", f32p)]
+                ("n_outputs", C.c_uint32), ("pad", C.c_uint32), ("base_score", f32p),
+                ("is_categorical", u8p), ("cat_begin", u32p), ("cat_end", u32p), ("categories", u32p),
+                ("n_categories", C.c_uint64)]
 
 
 # name -> (restype, argtypes); every entry point include/hessboost_rocm.h declares

@@ -499,6 +499,18 @@ class Booster:
                                  else np.asarray(self.tree_weights[:len(trees)], np.float32)),
                     tree_output=np.array([(t // npt) % k for t in range(len(trees))], np.uint32),
                     base_score=np.asarray(self.base_score, np.float32))
+        if any(np.any(t.get("is_categorical", ())) for t in trees):
+            # every tree's category pool concatenated, node ranges made absolute
+            isc, beg, end, pool = [], [], [], []
+            for t in trees:
+                n = len(t["left"])
+                base = sum(len(p) for p in pool)
+                isc.append(np.asarray(t.get("is_categorical", np.zeros(n)), np.uint8))
+                beg.append(np.asarray(t.get("cat_begin", np.zeros(n)), np.uint64) + base)
+                end.append(np.asarray(t.get("cat_end", np.zeros(n)), np.uint64) + base)
+                pool.append(np.asarray(t.get("categories", ()), np.uint32))
+            arrs.update(is_categorical=np.concatenate(isc), cat_begin=np.concatenate(beg).astype(np.uint32),
+                        cat_end=np.concatenate(end).astype(np.uint32), categories=np.concatenate(pool))
         return arrs
 
     def forest(self, ordinal=0):
@@ -539,11 +551,16 @@ class Booster:
             n = len(t["left"])
             gain = t.get("split_gain", np.zeros(n, np.float32))
             hess = t.get("sum_hess", np.zeros(n, np.float32))
+            isc = t.get("is_categorical", np.zeros(n, np.uint8))
+            beg = t.get("cat_begin", np.zeros(n, np.uint32))
+            end = t.get("cat_end", np.zeros(n, np.uint32))
             nodes = [dict(split_feature=int(t["split_feature"][i]), split_cond=f32(t["split_cond"][i]),
                           default_left=bool(t["default_left"][i]), left=int(t["left"][i]), right=int(t["right"][i]),
                           leaf_value=f32(t["leaf_value"][i]), sum_hess=f32(hess[i]), split_gain=f32(gain[i]),
-                          is_categorical=False, cat_begin=0, cat_end=0) for i in range(n)]
-            trees.append(dict(nodes=nodes, categories=[], size_leaf_vector=0, leaf_vectors=[], linear=None))
+                          is_categorical=bool(isc[i]), cat_begin=int(beg[i]), cat_end=int(end[i]))
+                     for i in range(n)]
+            trees.append(dict(nodes=nodes, categories=[int(c) for c in t.get("categories", ())], size_leaf_vector=0,
+                              leaf_vectors=[], linear=None))
         weights = np.ones(len(trees), np.float32) if self.tree_weights is None else self.tree_weights
         doc = dict(trees=trees, base_score=[f32(b) for b in np.atleast_1d(self.base_score)],
                    objective=self.objective, objective_params=dict(self.objective_params),
@@ -556,9 +573,12 @@ class Booster:
     @classmethod
     def load_model_json(cls, text):
         """A Booster from the reference's JSON model document: scalar-leaf
-        trees with numeric splits. Categorical splits, vector or linear
-        leaves, the linear booster, shrinkage, Boulevard and EBM models are
-        refused with a ValueError naming the feature."""
+        trees with numeric or categorical splits. Vector or linear leaves,
+        the linear booster, shrinkage, Boulevard and EBM models are refused
+        with a ValueError naming the feature, and so are the categorical
+        nodes the reference's loader refuses (a leaf marked categorical, a
+        split with no categories or a range beyond the tree's pool;
+        tests/native_format.rs:391-409)."""
         doc = json.loads(text)
         for key in cls._JSON_UNSUPPORTED:
             if doc.get(key) is not None:
@@ -570,9 +590,19 @@ class Booster:
             if t.get("linear") is not None:
                 raise ValueError(f"model: tree {i} has linear leaves")
             nodes = t["nodes"]
-            if any(n.get("is_categorical") for n in nodes):
-                raise ValueError(f"model: tree {i} has categorical splits")
+            pool = [int(c) for c in t.get("categories", [])]
+            for j, n in enumerate(nodes):
+                if not n.get("is_categorical"):
+                    continue
+                if n["left"] < 0:
+                    raise ValueError(f"model: tree {i} node {j}: a leaf marked categorical")
+                if not (0 <= n["cat_begin"] < n["cat_end"] <= len(pool)):
+                    raise ValueError(f"model: tree {i} node {j}: a categorical split needs categories in the pool")
             trees.append({
+                "is_categorical": np.array([bool(n.get("is_categorical")) for n in nodes], np.uint8),
+                "cat_begin": np.array([n.get("cat_begin", 0) for n in nodes], np.uint32),
+                "cat_end": np.array([n.get("cat_end", 0) for n in nodes], np.uint32),
+                "categories": np.array(pool, np.uint32),
                 "split_feature": np.array([n["split_feature"] for n in nodes], np.uint32),
                 "split_cond": np.array([n["split_cond"] for n in nodes], np.float32),
                 "default_left": np.array([n["default_left"] for n in nodes], np.uint8),
@@ -740,6 +770,10 @@ class Forest:
                       default_left=np.uint8, left=np.int32, right=np.int32, leaf_value=np.float32,
                       tree_weight=np.float32, tree_output=np.uint32, base_score=np.float32)
         a = {k: np.ascontiguousarray(arrs[k], dt) for k, dt in dtypes.items()}
+        if arrs.get("is_categorical") is not None:  # categorical splits (tree/mod.rs:34-58)
+            for k, dt in (("is_categorical", np.uint8), ("cat_begin", np.uint32), ("cat_end", np.uint32),
+                          ("categories", np.uint32)):
+                a[k] = np.ascontiguousarray(arrs[k], dt)
         self.arrs = a
         self.n_trees = len(a["tree_offset"]) - 1
         self.n_outputs = n_outputs
@@ -748,7 +782,12 @@ class Forest:
                           A.typed(a["default_left"], C.c_uint8), A.typed(a["left"], C.c_int32),
                           A.typed(a["right"], C.c_int32), A.typed(a["leaf_value"], C.c_float),
                           A.typed(a["tree_weight"], C.c_float), A.typed(a["tree_output"], C.c_uint32),
-                          n_outputs, 0, A.typed(a["base_score"], C.c_float))
+                          n_outputs, 0, A.typed(a["base_score"], C.c_float),
+                          A.typed(a.get("is_categorical"), C.c_uint8), A.typed(a.get("cat_begin"), C.c_uint32),
+                          A.typed(a.get("cat_end"), C.c_uint32),
+                          A.typed(a["categories"] if a.get("categories") is not None and a["categories"].size else None,
+                                  C.c_uint32),
+                          0 if a.get("categories") is None else int(a["categories"].size))
         h = C.c_void_p()
         A.check(A.lib().hbr_forest_upload(ordinal, C.byref(fd), C.byref(h)))
         self._h = h

@@ -606,7 +606,7 @@ struct CompactNode {
 struct PredictArgs {
     const PredNode *nodes;
     const uint32_t *node_value;   // f32 bits
-    const uint32_t *node_meta;    // feature | default_left<<30 | leaf<<31
+    const uint32_t *node_meta;    // feature | categorical<<29 | default_left<<30 | leaf<<31
     const uint32_t *node_left;    // left child (absolute), right = left + 1
     const int32_t *node_orig;     // the node's id in its tree as the caller numbered it
     const uint32_t *tree_root;    // n_trees
@@ -632,6 +632,12 @@ struct PredictArgs {
     const uint32_t *chunk_node;   // n_chunks + 1
     uint32_t n_chunks;
     uint32_t chunk_cap;           // LDS node capacity
+    // categorical splits (hbr_predict only): a node with kPredCategorical in
+    // its meta holds cat_begin as its value; its set is
+    // categories[value, node_cat_end[node])
+    const uint32_t *categories;
+    const uint32_t *node_cat_end;
 };
+constexpr uint32_t kPredCategorical = 1u << 29;
 
 }  // namespace hbr

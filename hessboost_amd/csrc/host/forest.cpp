@@ -13,7 +13,7 @@ namespace hbr {
 Forest::Forest(int ordinal, const hbr_forest_desc &fd) : dev_(device(ordinal)) {
     n_trees_ = fd.n_trees;
     n_outputs_ = fd.n_outputs ? fd.n_outputs : 1;
-    std::vector<uint32_t> value, meta, left, root, output;
+    std::vector<uint32_t> value, meta, left, root, output, cat_end;
     std::vector<int32_t> orig;
     std::vector<float> weight(n_trees_), base(n_outputs_);
     for (uint32_t c = 0; c < n_outputs_; c++) base[c] = fd.base_score ? fd.base_score[c] : 0.0f;
@@ -42,6 +42,7 @@ Forest::Forest(int ordinal, const hbr_forest_desc &fd) : dev_(device(ordinal)) {
                 value.push_back(bits);
                 meta.push_back(1u << 31);
                 left.push_back(0);
+                cat_end.push_back(0);
                 continue;
             }
             if (l < 0 || r < 0 || (uint64_t)l >= count || (uint64_t)r >= count || seen[l] || seen[r])
@@ -50,8 +51,22 @@ Forest::Forest(int ordinal, const hbr_forest_desc &fd) : dev_(device(ordinal)) {
             seen[l] = seen[r] = 1;
             uint32_t bits;
             std::memcpy(&bits, &fd.split_cond[at], 4);
+            uint32_t m = fd.split_feature[at] | ((fd.default_left[at] ? 1u : 0u) << 30);
+            uint32_t end = 0;
+            if (fd.is_categorical && fd.is_categorical[at]) {
+                // the value slot holds the start of the node's category range
+                if (!fd.cat_begin || !fd.cat_end || !fd.categories || fd.cat_begin[at] > fd.cat_end[at] ||
+                    fd.cat_end[at] > fd.n_categories)
+                    fail(kInvalid, "forest: a categorical split's categories are out of range in tree " +
+                                       std::to_string(t));
+                bits = fd.cat_begin[at];
+                end = fd.cat_end[at];
+                m |= kPredCategorical;
+                has_categorical_ = true;
+            }
             value.push_back(bits);
-            meta.push_back(fd.split_feature[at] | ((fd.default_left[at] ? 1u : 0u) << 30));
+            meta.push_back(m);
+            cat_end.push_back(end);
             left.push_back(base_id + (uint32_t)queue.size());
             queue.push_back(l);
             queue.push_back(r);
@@ -69,11 +84,16 @@ Forest::Forest(int ordinal, const hbr_forest_desc &fd) : dev_(device(ordinal)) {
     up(root_, root);
     up(output_, output);
     up(orig_, orig);
+    if (has_categorical_) {
+        up(cat_end_, cat_end);
+        std::vector<uint32_t> pool(fd.categories, fd.categories + fd.n_categories);
+        up(categories_, pool);
+    }
     std::vector<PredNode> nodes(value.size());
     for (size_t i = 0; i < value.size(); i++) nodes[i] = PredNode{value[i], meta[i], left[i], orig[i]};
     up(nodes_, nodes);
     // compact records: feature < 2^16, left child within 2^14 - 1 nodes
-    compact_ok_ = true;
+    compact_ok_ = !has_categorical_;  // the compact walks compare thresholds only
     std::vector<CompactNode> compact(value.size());
     for (size_t i = 0; i < value.size(); i++) {
         if (meta[i] >> 31) {
@@ -120,6 +140,12 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     a.n_outputs = n_outputs_;
     a.missing = missing;
     a.missing_is_nan = missing != missing ? 1u : 0u;
+    if (has_categorical_) {  // the category sets are read by hbr_predict's walk
+        a.categories = categories_.get();
+        a.node_cat_end = cat_end_.get();
+        dev_.launch("hbr_predict", dim3((uint32_t)((n + 255) / 256)), dim3(256), a);
+        return;
+    }
     const uint64_t row_block = n_cols * 65ull * sizeof(float);
     const uint64_t lds_total = 160ull * 1024;
     // rows resident in LDS (one 64-row block per one-wave workgroup), trees

@@ -32,6 +32,8 @@ private:
     // compact nodes for the chunked walk (absent when a feature id or a
     // child offset does not fit the compact record)
     bool compact_ok_ = false;
+    bool has_categorical_ = false;
+    DBuf<uint32_t> categories_, cat_end_;  // the category pool; per node the end of its range
     DBuf<CompactNode> compact_;
     std::vector<uint32_t> tree_nodes_;  // nodes per tree
     uint32_t largest_tree_ = 0;

@@ -4,7 +4,9 @@
 // out = base_score, then for every tree in ascending order
 // out[output(t)] += weight(t) * leaf(t, row) in f32 (a multiply, then an
 // add); a present value goes left iff value < threshold, a missing one
-// follows default_left (tree/mod.rs:52-58).
+// follows default_left (tree/mod.rs:52-58). A categorical split sends a
+// present value left iff its category is in the node's set; forests with
+// such splits take hbr_predict (the category pool read from global memory).
 //
 // hbr_predict_resident (the default): a workgroup is one wave; it stages a
 // 64-row block in LDS once and walks it through every tree, 16 trees in
@@ -27,13 +29,35 @@ using namespace hbr;
 
 namespace hbr {
 
+// Rust's saturating `v as u32`: NaN and values below 1 give 0, values at or
+// above 2^32 give u32::MAX, the rest truncate (tree/mod.rs:34-36).
+__device__ __forceinline__ uint32_t category_of(float v) {
+    if (!(v >= 1.0f)) return 0u;
+    if (v >= 4294967296.0f) return 0xffffffffu;
+    return (uint32_t)v;
+}
+
+__device__ __forceinline__ bool in_categories(const PredictArgs &a, uint32_t nid, float v) {
+    const uint32_t c = category_of(v);
+    const uint32_t end = a.node_cat_end[nid];
+    bool hit = false;
+    for (uint32_t i = a.node_value[nid]; i < end; i++) hit |= a.categories[i] == c;
+    return hit;
+}
+
 __device__ __forceinline__ uint32_t walk(const PredictArgs &a, const float *row, uint32_t nid) {
     for (;;) {
         const uint32_t meta = a.node_meta[nid];
         if (meta >> 31) return nid;
         const float v = row[meta & 0xfffffu];
         const bool miss = a.missing_is_nan ? __builtin_isnan(v) : (v == a.missing);
-        const bool left = miss ? ((meta >> 30) & 1u) != 0 : (v < __uint_as_float(a.node_value[nid]));
+        bool left;
+        if (miss)
+            left = ((meta >> 30) & 1u) != 0;
+        else if (meta & kPredCategorical)
+            left = in_categories(a, nid, v);
+        else
+            left = v < __uint_as_float(a.node_value[nid]);
         nid = a.node_left[nid] + (left ? 0u : 1u);
     }
 }

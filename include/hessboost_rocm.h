@@ -399,8 +399,13 @@ void hbr_trainer_free(hbr_trainer *t);
 
 typedef struct hbr_forest hbr_forest;
 
-/* A scalar-leaf numeric forest: per tree its nodes in the reference's
- * layout; tree t adds tree_weight[t] * leaf to output tree_output[t]. */
+/* A scalar-leaf forest: per tree its nodes in the reference's layout; tree
+ * t adds tree_weight[t] * leaf to output tree_output[t]. Categorical splits
+ * (src/tree/regtree.rs:59-66, tree/mod.rs:34-58): node i with
+ * is_categorical[i] sends a present value left iff its saturating u32 cast
+ * is one of categories[cat_begin[i], cat_end[i]) (ranges into the forest's
+ * one pool of n_categories entries); is_categorical NULL: every split
+ * numeric. */
 typedef struct hbr_forest_desc {
     uint64_t n_trees;
     const uint64_t *tree_offset;    /* n_trees + 1 */
@@ -415,6 +420,11 @@ typedef struct hbr_forest_desc {
     uint32_t n_outputs;
     uint32_t pad;
     const float *base_score;        /* n_outputs */
+    const uint8_t *is_categorical;  /* per node, or NULL */
+    const uint32_t *cat_begin;      /* per node (categorical nodes) */
+    const uint32_t *cat_end;
+    const uint32_t *categories;     /* n_categories */
+    uint64_t n_categories;
 } hbr_forest_desc;
 
 /* BoostedModel::to_cuda: upload the forest once. */

@@ -205,6 +205,11 @@ typedef struct or_forest_desc {
     const uint32_t *tree_output;   /* n_trees */
     size_t n_outputs;
     const float *base_score;       /* n_outputs */
+    /* categorical splits (NULL: every split numeric): node i's categories
+     * routed left are categories[cat_begin[i], cat_end[i]) */
+    const uint8_t *is_categorical;
+    const uint32_t *cat_begin, *cat_end;
+    const uint32_t *categories;
 } or_forest_desc;
 
 /* margins out[n * n_outputs]; leaf ids (per tree, may be NULL) out_leaf[n * n_trees]. */

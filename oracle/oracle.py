@@ -66,7 +66,9 @@ class ForestDesc(C.Structure):
                 ("default_left", C.POINTER(C.c_uint8)), ("left", C.POINTER(C.c_int32)),
                 ("right", C.POINTER(C.c_int32)), ("leaf_value", C.POINTER(C.c_float)),
                 ("tree_weight", C.POINTER(C.c_float)), ("tree_output", C.POINTER(C.c_uint32)),
-                ("n_outputs", C.c_size_t), ("base_score", C.POINTER(C.c_float))]
+                ("n_outputs", C.c_size_t), ("base_score", C.POINTER(C.c_float)),
+                ("is_categorical", C.POINTER(C.c_uint8)), ("cat_begin", C.POINTER(C.c_uint32)),
+                ("cat_end", C.POINTER(C.c_uint32)), ("categories", C.POINTER(C.c_uint32))]
 
 
 _lib = None
@@ -404,6 +406,16 @@ def predict_margin(arrs, x, missing=np.nan, with_leaf=False):
                     arrs["tree_weight"].ctypes.data_as(P(C.c_float)),
                     arrs["tree_output"].ctypes.data_as(P(C.c_uint32)),
                     arrs["n_outputs"], arrs["base_score"].ctypes.data_as(P(C.c_float)))
+    if arrs.get("is_categorical") is not None:
+        cat = {key: np.ascontiguousarray(arrs[key], dt) for key, dt in
+               (("is_categorical", np.uint8), ("cat_begin", np.uint32), ("cat_end", np.uint32),
+                ("categories", np.uint32))}
+        if cat["categories"].size == 0:
+            cat["categories"] = np.zeros(1, np.uint32)
+        fd.is_categorical = cat["is_categorical"].ctypes.data_as(P(C.c_uint8))
+        fd.cat_begin = cat["cat_begin"].ctypes.data_as(P(C.c_uint32))
+        fd.cat_end = cat["cat_end"].ctypes.data_as(P(C.c_uint32))
+        fd.categories = cat["categories"].ctypes.data_as(P(C.c_uint32))
     k = arrs["n_outputs"]
     out = np.empty(n * k, np.float32)
     leaf = np.empty(n * fd.n_trees, np.int32) if with_leaf else None

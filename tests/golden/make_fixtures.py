@@ -3,16 +3,19 @@
 Reads hessboost's own saved models and recorded margins
 (tests/data/saved/<version>/<case>.json and <case>.margins, checked by
 tests/native_format.rs:822-860) and writes tests/golden/saved_models.json:
-for every numeric, scalar-leaf case, the trees as flat node arrays, the
+for every scalar-leaf case, the trees as flat node arrays (categorical
+splits with their category ranges and each tree's category pool), the
 tree weights and outputs, the base score, and the recorded margins, every
 f32 stored as its bit pattern. The input rows are not stored: they are
-regenerated in closed form (tests/common/mod.rs:28-39, four_features).
+regenerated in closed form (tests/common/mod.rs:28-39, four_features;
+the categorical case replaces column 0 by the codes i % 5,
+tests/native_format.rs:508-513).
 
 It also copies, minified, the 0.4.9 JSON model documents themselves into
 tests/golden/models/ (the JSON model format, model/serde.rs): the saved
 models of the cases above, which the JSON reader and writer must reproduce,
-and three whose features this path does not carry (categorical splits, a
-linear booster, vector leaves), which the reader must refuse.
+and two whose features this path does not carry (a linear booster, vector
+leaves), which the reader must refuse.
 
 Run once in a checkout that has the reference under /root/reference:
     python tests/golden/make_fixtures.py
@@ -26,7 +29,7 @@ import numpy as np
 REF = "/root/reference/tests/data/saved"
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "saved_models.json")
 CASES = ["early_stopping", "dart", "multiclass_forest", "quantiles", "expectiles", "aft",
-         "dist_normal", "dist_negbinomial", "multi_target"]
+         "dist_normal", "dist_negbinomial", "multi_target", "categorical_splits"]
 
 
 def f32_bits(x):
@@ -45,8 +48,11 @@ def main():
             for t in doc["trees"]:
                 assert t.get("size_leaf_vector", 0) <= 1 and not t.get("linear")
                 nodes = t["nodes"]
-                assert not any(n["is_categorical"] for n in nodes)
                 trees.append({
+                    "is_categorical": [int(n["is_categorical"]) for n in nodes],
+                    "cat_begin": [n["cat_begin"] for n in nodes],
+                    "cat_end": [n["cat_end"] for n in nodes],
+                    "categories": list(t["categories"]),
                     "split_feature": [n["split_feature"] for n in nodes],
                     "split_cond": [f32_bits(n["split_cond"]) for n in nodes],
                     "default_left": [int(n["default_left"]) for n in nodes],
@@ -72,10 +78,10 @@ def main():
     print(f"wrote {len(out)} cases to {OUT}")
     models = os.path.join(os.path.dirname(OUT), "models")
     os.makedirs(models, exist_ok=True)
-    for case in CASES + ["categorical_splits", "gblinear", "vector_leaves"]:
+    for case in CASES + ["gblinear", "vector_leaves"]:
         doc = json.load(open(os.path.join(REF, "0.4.9", case + ".json")))
         json.dump(doc, open(os.path.join(models, case + ".json"), "w"), separators=(",", ":"))
-    print(f"copied {len(CASES) + 3} JSON models to {models}")
+    print(f"copied {len(CASES) + 2} JSON models to {models}")
 
 
 if __name__ == "__main__":

@@ -20,6 +20,14 @@ def four_features(n=160):
     return np.stack([a, b, c, d], axis=1).astype(np.float32)
 
 
+def categorical_features(n=160):
+    """tests/native_format.rs:508-513: four_features with column 0 replaced
+    by the category codes i % 5."""
+    x = four_features(n)
+    x[:, 0] = (np.arange(n) % 5).astype(np.float32)
+    return x
+
+
 def train_labels(x, k=1):
     """tests/native_format.rs:441-454: y_t = 2a - b + t*c + 0.1 in f32."""
     a, b, c = x[:, 0], x[:, 1], x[:, 2]
@@ -47,11 +55,23 @@ def golden_forest(case):
         n_trees = min((case["best_iteration"] + 1) * k * npt, n_trees)
     off = [0]
     cols = {key: [] for key in ("split_feature", "split_cond", "default_left", "left", "right", "leaf_value")}
+    cat = {key: [] for key in ("is_categorical", "cat_begin", "cat_end", "categories")}
     for t in trees[:n_trees]:
         for key in cols:
             cols[key].extend(t[key])
         off.append(len(cols["left"]))
-    return dict(
+        # category ranges made absolute in the forest's concatenated pool
+        base = len(cat["categories"])
+        cat["is_categorical"].extend(t.get("is_categorical", [0] * len(t["left"])))
+        cat["cat_begin"].extend(base + b for b in t.get("cat_begin", [0] * len(t["left"])))
+        cat["cat_end"].extend(base + e for e in t.get("cat_end", [0] * len(t["left"])))
+        cat["categories"].extend(t.get("categories", []))
+    extra = {}
+    if any(cat["is_categorical"]):
+        extra = dict(is_categorical=np.array(cat["is_categorical"], np.uint8),
+                     cat_begin=np.array(cat["cat_begin"], np.uint32), cat_end=np.array(cat["cat_end"], np.uint32),
+                     categories=np.array(cat["categories"], np.uint32))
+    return dict(**extra,
         tree_offset=np.array(off, np.uint32),
         split_feature=np.array(cols["split_feature"], np.uint32),
         split_cond=bits_to_f32(cols["split_cond"]),

@@ -5,19 +5,25 @@ import pytest
 import hessboost_amd as hb
 from hessboost_amd import synthetic
 from oracle import oracle as O
-from tests.helpers import four_features, golden_forest, load_saved_models
+from tests.helpers import categorical_features, four_features, golden_forest, load_saved_models
 
 pytestmark = pytest.mark.gpu
 
 CASES = ["early_stopping", "dart", "multiclass_forest", "quantiles", "expectiles", "aft", "dist_normal",
-         "dist_negbinomial", "multi_target"]
+         "dist_negbinomial", "multi_target", "categorical_splits"]
+
+
+def rows_for(name):
+    """The rows each saved model's margins were recorded on (the categorical
+    case's column 0 holds category codes)."""
+    return categorical_features() if name == "categorical_splits" else four_features()
 
 
 @pytest.mark.parametrize("name", CASES)
 def test_saved_models_reproduce_recorded_margins(name):
     """tests/native_format.rs:822-860: recorded f32 margins, bit for bit."""
     saved = load_saved_models()
-    x = four_features()
+    x = rows_for(name)
     for ver in ("0.2.0", "0.4.3", "0.4.9"):
         case = saved[f"{ver}/{name}"]
         arrs = golden_forest(case)
@@ -33,9 +39,70 @@ def test_reference_json_models_predict_recorded_margins(name):
     import os
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "models", name + ".json")
     b = hb.Booster.load_model_json(open(path).read())
-    got = b.predict(four_features(), output_margin=True)
+    got = b.predict(rows_for(name), output_margin=True)
     want = np.array(load_saved_models()[f"0.4.9/{name}"]["margins"], np.uint32)
     assert np.array_equal(np.asarray(got, np.float32).reshape(-1).view(np.uint32), want)
+
+
+def test_categorical_casts_saturate_and_missing_follows_default():
+    """src/backend/cuda/predict.rs:702-724: the set {0, 2, u32::MAX}; rows
+    -2.5, -0.0, 0.8, 1.9, 2.9, 2^32 and NaN, on the GPU as in the oracle,
+    for both default directions and a non-NaN missing marker."""
+    x = np.array([[-2.5], [-0.0], [0.8], [1.9], [2.9], [4294967296.0], [np.nan], [np.inf], [-np.inf],
+                  [4294967040.0], [3.0]], np.float32)
+    for dl in (0, 1):
+        for missing in (np.nan, 3.0):
+            arrs = O.forest_arrays([[dict(split_feature=0, split_cond=0.0, default_left=bool(dl), left=1, right=2,
+                                          leaf_value=1.0),
+                                     dict(split_feature=0, split_cond=0.0, default_left=True, left=-1, right=-1,
+                                          leaf_value=0.25),
+                                     dict(split_feature=0, split_cond=0.0, default_left=True, left=-1, right=-1,
+                                          leaf_value=-0.75)]])
+            arrs.update(is_categorical=np.array([1, 0, 0], np.uint8), cat_begin=np.array([0, 0, 0], np.uint32),
+                        cat_end=np.array([3, 0, 0], np.uint32), categories=np.array([0, 2, 2**32 - 1], np.uint32))
+            want = O.predict_margin(arrs, x, missing=missing)
+            got = hb.Forest(arrs, 1).predict_margin(x, missing)
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_random_categorical_forests_match_oracle():
+    """Unbalanced random trees mixing numeric and categorical splits (sets of
+    up to 70 categories from 0..99), several outputs, category codes with
+    fractions, negatives and missing values; margins and leaf ids."""
+    rng = np.random.default_rng(31)
+    f, k = 6, 3
+    trees, pool = [], []
+    for t in range(40):
+        nodes = [dict(leaf_value=float(rng.standard_normal()))]
+        for _ in range(int(rng.integers(0, 30))):
+            i = int(rng.choice([j for j, nd in enumerate(nodes) if "left" not in nd]))
+            nodes[i].update(left=len(nodes), right=len(nodes) + 1, split_feature=int(rng.integers(0, f)),
+                            split_cond=float(np.float32(rng.standard_normal() * 20)),
+                            default_left=bool(rng.random() < 0.5), is_categorical=bool(rng.random() < 0.5))
+            nodes += [dict(leaf_value=float(rng.standard_normal())), dict(leaf_value=float(rng.standard_normal()))]
+        for nd in nodes:
+            for key, v in (("left", -1), ("right", -1), ("split_feature", 0), ("split_cond", 0.0),
+                           ("default_left", True), ("is_categorical", False)):
+                nd.setdefault(key, v)
+            if nd["is_categorical"]:
+                cats = rng.choice(100, size=int(rng.integers(1, 71)), replace=False)
+                nd["cat_begin"], nd["cat_end"] = len(pool), len(pool) + len(cats)
+                pool.extend(int(c) for c in cats)
+            else:
+                nd["cat_begin"] = nd["cat_end"] = 0
+        trees.append(nodes)
+    arrs = O.forest_arrays(trees, tree_output=[t % k for t in range(len(trees))], n_outputs=k,
+                           base_score=[0.5, -0.5, 0.0])
+    flat = [nd for nodes in trees for nd in nodes]
+    arrs.update(is_categorical=np.array([nd["is_categorical"] for nd in flat], np.uint8),
+                cat_begin=np.array([nd["cat_begin"] for nd in flat], np.uint32),
+                cat_end=np.array([nd["cat_end"] for nd in flat], np.uint32), categories=np.array(pool, np.uint32))
+    x = (rng.integers(-5, 110, (20_000, f)) + rng.choice([0.0, 0.25, 0.99], (20_000, f))).astype(np.float32)
+    x[rng.random(x.shape) < 0.05] = np.nan
+    want, want_leaf = O.predict_margin(arrs, x, with_leaf=True)
+    forest = hb.Forest(arrs, k)
+    np.testing.assert_array_equal(forest.predict_margin(x).reshape(-1).view(np.uint32), want.view(np.uint32))
+    np.testing.assert_array_equal(forest.predict_leaf(x).reshape(want_leaf.shape), want_leaf)
 
 
 def test_trained_model_survives_json_round_trip():

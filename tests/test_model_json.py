@@ -13,7 +13,7 @@ import hessboost_amd as hb
 
 MODELS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "models")
 CARRIED = ["early_stopping", "dart", "multiclass_forest", "quantiles", "expectiles", "aft", "dist_normal",
-           "dist_negbinomial", "multi_target"]
+           "dist_negbinomial", "multi_target", "categorical_splits"]
 
 
 def same(a, b, path="doc"):
@@ -43,11 +43,43 @@ def test_reference_model_documents_round_trip(case):
     same(out, json.loads(hb.Booster.load_model_json(json.dumps(out)).save_model_json()))
 
 
-@pytest.mark.parametrize("case,what", [("categorical_splits", "categorical"), ("gblinear", "linear"),
-                                       ("vector_leaves", "vector leaves")])
+@pytest.mark.parametrize("case,what", [("gblinear", "linear"), ("vector_leaves", "vector leaves")])
 def test_models_beyond_this_path_are_refused(case, what):
     with pytest.raises(ValueError, match=what):
         hb.Booster.load_model_json(open(os.path.join(MODELS, case + ".json")).read())
+
+
+def test_malformed_categorical_nodes_are_refused():
+    """tests/native_format.rs:391-409: a categorical split needs at least
+    one category; a leaf is never categorical."""
+    doc = json.loads(open(os.path.join(MODELS, "categorical_splits.json")).read())
+    node = doc["trees"][0]["nodes"][0]
+    assert node["is_categorical"]
+    node["cat_end"] = node["cat_begin"]
+    with pytest.raises(ValueError, match="categor"):
+        hb.Booster.load_model_json(json.dumps(doc))
+    doc = json.loads(open(os.path.join(MODELS, "categorical_splits.json")).read())
+    leaf = next(n for n in doc["trees"][0]["nodes"] if n["left"] == -1)
+    leaf["is_categorical"] = True
+    with pytest.raises(ValueError, match="leaf marked categorical"):
+        hb.Booster.load_model_json(json.dumps(doc))
+
+
+def test_categorical_forest_arrays_take_absolute_ranges():
+    b = hb.Booster.load_model_json(open(os.path.join(MODELS, "categorical_splits.json")).read())
+    d = b.forest_desc()
+    doc = json.loads(open(os.path.join(MODELS, "categorical_splits.json")).read())
+    pool = [c for t in doc["trees"] for c in t["categories"]]
+    assert list(d["categories"]) == pool
+    at, base = 0, 0
+    for t in doc["trees"]:
+        for n in t["nodes"]:
+            assert bool(d["is_categorical"][at]) == n["is_categorical"]
+            if n["is_categorical"]:
+                assert list(d["categories"][d["cat_begin"][at]:d["cat_end"][at]]) == \
+                    t["categories"][n["cat_begin"]:n["cat_end"]]
+            at += 1
+        base += len(t["categories"])
 
 
 def test_effective_trees_and_outputs_follow_the_document():

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import (bits_to_f32, four_features, golden_forest, load_saved_models,
+from tests.helpers import (bits_to_f32, categorical_features, four_features, golden_forest, load_saved_models,
                            train_labels)
 
 
@@ -51,17 +51,37 @@ def test_early_stopping_model_reproduced_bit_for_bit(saved):
 
 @pytest.mark.parametrize("name", ["early_stopping", "dart", "multiclass_forest", "quantiles",
                                   "expectiles", "aft", "dist_normal", "dist_negbinomial",
-                                  "multi_target"])
+                                  "multi_target", "categorical_splits"])
 def test_saved_model_margins_bit_exact(saved, name):
     """tests/native_format.rs:822-860: each saved model reproduces its recorded
     little-endian f32 margins on the closed-form rows."""
-    x = four_features()
+    x = categorical_features() if name == "categorical_splits" else four_features()
     for ver in ("0.2.0", "0.4.3", "0.4.9"):
         case = saved[f"{ver}/{name}"]
         forest = golden_forest(case)
         out = O.predict_margin(forest, x)
         want = np.array(case["margins"], np.uint32)
         assert np.array_equal(out.view(np.uint32), want), f"{ver}/{name}"
+
+
+def test_categorical_casts_saturate_and_missing_follows_default():
+    """src/backend/cuda/predict.rs:702-724: the set {0, 2, u32::MAX} on one
+    feature, rows -2.5, -0.0, 0.8, 1.9, 2.9, 2^32 and NaN; Rust's saturating
+    `as u32` puts the first three in category 0, 1.9 in 1, 2.9 in 2 and 2^32
+    in u32::MAX; NaN is missing."""
+    x = np.array([[-2.5], [-0.0], [0.8], [1.9], [2.9], [4294967296.0], [np.nan]], np.float32)
+    for dl in (0, 1):
+        arrs = O.forest_arrays([[dict(split_feature=0, split_cond=0.0, default_left=bool(dl), left=1, right=2,
+                                      leaf_value=1.0),
+                                 dict(split_feature=0, split_cond=0.0, default_left=True, left=-1, right=-1,
+                                      leaf_value=0.25),
+                                 dict(split_feature=0, split_cond=0.0, default_left=True, left=-1, right=-1,
+                                      leaf_value=-0.75)]])
+        arrs.update(is_categorical=np.array([1, 0, 0], np.uint8), cat_begin=np.array([0, 0, 0], np.uint32),
+                    cat_end=np.array([3, 0, 0], np.uint32), categories=np.array([0, 2, 2**32 - 1], np.uint32))
+        got = O.predict_margin(arrs, x)
+        want = np.array([0.25, 0.25, 0.25, -0.75, 0.25, 0.25, 0.25 if dl else -0.75], np.float32)
+        np.testing.assert_array_equal(got, want)
 
 
 def test_splits_on_separating_feature():
