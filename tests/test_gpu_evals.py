@@ -188,3 +188,25 @@ def test_engine_level_eval_sets_take_caller_trees():
     with pytest.raises(hb.HbrError):  # children not a pair
         engine.eval_add_tree(dict(split_feature=[0, 0, 0], split_cond=[0.0, 0, 0], default_left=[1, 1, 1],
                                   left=[2, -1, -1], right=[1, -1, -1], leaf_value=[0.0, 1, 2]))
+
+
+def test_trees_discarded_by_the_device_are_added_to_no_eval_set():
+    """Pipelined rounds whose gradients overflow: with eta 1e30 the second
+    tree's leaves overflow to infinity, so the third round's gradients are
+    not finite and the device skips that tree's walks and those of every
+    tree queued after it. Training stops with an error; each eval set then
+    holds exactly the kept trees, like the training margins."""
+    x, y = data(6_000, 10, 25)
+    dtrain = hb.DMatrix(x, label=y)
+    t = hb.Trainer(dtrain.engine(256), {"objective": "reg:squarederror", "max_depth": 3, "eta": 1e30,
+                                        "lambda": 0.0}, y)
+    own = t.add_eval(dtrain)
+    other = t.add_eval(hb.DMatrix(eval_matrix(1_000, 10, 26)))
+    with pytest.raises(hb.HbrError, match="not finite"):
+        t.boost(6)
+    booster = t.booster(10)
+    assert 1 <= booster.num_trees() < 6
+    np.testing.assert_array_equal(t.eval_margins(own).reshape(-1).view(np.uint32), t.margins().view(np.uint32))
+    np.testing.assert_array_equal(t.eval_margins(own).view(np.uint32), expected(booster, x).view(np.uint32))
+    ev = eval_matrix(1_000, 10, 26)
+    np.testing.assert_array_equal(t.eval_margins(other).view(np.uint32), expected(booster, ev).view(np.uint32))
