@@ -206,6 +206,7 @@ public:
     // ... into one set's margins only (a set added after trees were grown).
     void walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output);
     uint32_t n_eval_sets() const { return (uint32_t)evals_.size(); }
+    void clear_eval_sets() { evals_.clear(); }
     uint64_t eval_rows(uint32_t set) const;
     void read_eval_margins(uint32_t set, float *out);
     // HistogramBackend::build of a host row list (per-node host growth).

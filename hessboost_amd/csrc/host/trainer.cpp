@@ -401,6 +401,7 @@ std::vector<float> base_margins(const TrainParams &p, const float *labels, const
 Trainer::Trainer(Engine &e, const TrainParams &p, const float *labels, const float *weights, uint64_t n)
     : e_(e), p_(p), n_(n) {
     if (n != e.n_rows()) fail(kInvalid, "trainer: one label per index row");
+    e.clear_eval_sets();  // an earlier trainer's sets would take this one's trees
     k_ = p.objective == HBR_OBJ_SOFTMAX ? p.num_class : 1;
     if (k_ == 0) fail(kInvalid, "softmax needs num_class");
     if (p.objective == HBR_OBJ_SOFTMAX) {

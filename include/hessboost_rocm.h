@@ -386,7 +386,8 @@ int hbr_trainer_margins(hbr_trainer *t, float *out);
  * copied to the device. Its margins start from base_margin (n_rows *
  * n_outputs, or NULL for the base score), take every tree grown so far and
  * then every later tree on the device as it is grown, routed by raw value.
- * *index receives the set's number. */
+ * *index receives the set's number. The sets belong to the engine's latest
+ * trainer: creating a trainer on the engine drops every set added before. */
 int hbr_trainer_add_eval(hbr_trainer *t, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
                          const float *base_margin, uint32_t *index);
 /* Eval set `index`'s margins (n_rows * n_outputs, row-major). */

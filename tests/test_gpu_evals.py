@@ -137,6 +137,24 @@ def test_added_after_rounds_with_base_margin_and_missing_marker():
     np.testing.assert_array_equal(t.eval_margins(tr).reshape(-1), t.margins())
 
 
+def test_a_new_trainer_drops_the_engine_eval_sets():
+    x, y = data(4_000, 8, 27)
+    engine = hb.DMatrix(x, label=y).engine(256)
+    ev = eval_matrix(500, 8, 28)
+    first = hb.Trainer(engine, {"max_depth": 4}, y)
+    first.add_eval(hb.DMatrix(ev))
+    first.boost(2)
+    before = first.eval_margins(0).copy()
+    second = hb.Trainer(engine, {"max_depth": 3}, y)
+    i = second.add_eval(hb.DMatrix(ev))
+    assert i == 0
+    second.boost(3)
+    np.testing.assert_array_equal(second.eval_margins(0).view(np.uint32),
+                                  expected(second.booster(8), ev).view(np.uint32))
+    np.testing.assert_array_equal(before.view(np.uint32),
+                                  expected(first.booster(8), ev).view(np.uint32))
+
+
 def test_rejects_other_features():
     x, y = data(2_000, 8, 17)
     with pytest.raises(ValueError):
