@@ -139,6 +139,8 @@ def main():
     ap.add_argument("--predict-trees", type=int, default=1000)
     ap.add_argument("--predict-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eval-rows", type=int, default=0,
+                    help="train with an eval set of this many rows (0: none, the headline workload)")
     ap.add_argument("--no-predict", action="store_true")
     ap.add_argument("--breakdown-steps", type=int, default=5)
     ap.add_argument("--no-kernel-events", action="store_true",
@@ -201,6 +203,11 @@ def main():
     log(f"device binning: {t_bin * 1e3:.1f} ms from HBM ({bin_bytes / t_bin / 1e9:.0f} GB/s), "
         f"{t_bin_host * 1e3:.1f} ms from host rows")
     trainer = hb.Trainer(eng, params, y)
+    if args.eval_rows > 0:
+        # an evaluation set (the first eval_rows training rows) whose margins
+        # take every tree on the device, as training's `evals` do
+        trainer.add_eval(hb.DMatrix(x[:args.eval_rows]))
+        log(f"eval set: {min(args.eval_rows, x.shape[0]):,} rows")
     trainer.boost(args.warmup)
     log(f"{args.warmup} warmup rounds done")
     before = eng.counters()
@@ -252,6 +259,7 @@ def main():
             "workload": f"binary logistic hist training, {args.rows:,} x 28 f32 (higgs-like), max_bin 256, "
                         "max_depth 8, eta 0.1, depthwise",
             "rows": args.rows, "features": 28, "max_depth": 8, "max_bin": 256, "trees_grown": n_trees,
+            **({"eval_rows": args.eval_rows} if args.eval_rows > 0 else {}),
         },
         "roofline": {
             "kernel": "/".join(hist_names) or HIST_KERNEL,
