@@ -206,7 +206,12 @@ public:
     // ... into one set's margins only (a set added after trees were grown).
     void walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output);
     uint32_t n_eval_sets() const { return (uint32_t)evals_.size(); }
-    void clear_eval_sets() { evals_.clear(); }
+    // Drops every set; returns the new owner's number (eval_owner()).
+    uint64_t clear_eval_sets() {
+        evals_.clear();
+        return ++eval_owner_;
+    }
+    uint64_t eval_owner() const { return eval_owner_; }
     uint64_t eval_rows(uint32_t set) const;
     void read_eval_margins(uint32_t set, float *out);
     // HistogramBackend::build of a host row list (per-node host growth).
@@ -329,6 +334,7 @@ private:
         float missing = 0.0f;
     };
     std::vector<std::unique_ptr<EvalSet>> evals_;
+    uint64_t eval_owner_ = 0;  // bumped whenever the sets are dropped
     DBuf<float> d_cuts_;             // cut values for the evaluation walks
     DBuf<GrowTreeNode> d_eval_tree_; // a host-grown tree's records
     DBuf<float> d_eval_cond_;

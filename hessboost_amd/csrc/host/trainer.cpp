@@ -401,7 +401,7 @@ std::vector<float> base_margins(const TrainParams &p, const float *labels, const
 Trainer::Trainer(Engine &e, const TrainParams &p, const float *labels, const float *weights, uint64_t n)
     : e_(e), p_(p), n_(n) {
     if (n != e.n_rows()) fail(kInvalid, "trainer: one label per index row");
-    e.clear_eval_sets();  // an earlier trainer's sets would take this one's trees
+    eval_owner_ = e.clear_eval_sets();  // an earlier trainer's sets would take this one's trees
     k_ = p.objective == HBR_OBJ_SOFTMAX ? p.num_class : 1;
     if (k_ == 0) fail(kInvalid, "softmax needs num_class");
     if (p.objective == HBR_OBJ_SOFTMAX) {
@@ -627,6 +627,7 @@ std::vector<GrowTreeNode> records_of(const Tree &t) {
 // `base_margin` ([n][outputs]) or the base score, then take every tree
 // grown so far, and every later tree as it is grown.
 uint32_t Trainer::add_eval(const float *x, uint64_t n, uint64_t n_cols, float missing, const float *base_margin) {
+    check_eval_owner();
     std::vector<float> init(n * k_);
     for (uint64_t r = 0; r < n; r++)
         for (uint32_t c = 0; c < k_; c++) init[r * k_ + c] = base_margin ? base_margin[r * k_ + c] : base_[c];
@@ -635,6 +636,14 @@ uint32_t Trainer::add_eval(const float *x, uint64_t n, uint64_t n_cols, float mi
     return set;
 }
 
-void Trainer::eval_margins(uint32_t set, float *out) { e_.read_eval_margins(set, out); }
+void Trainer::eval_margins(uint32_t set, float *out) {
+    check_eval_owner();
+    e_.read_eval_margins(set, out);
+}
+
+void Trainer::check_eval_owner() const {
+    if (e_.eval_owner() != eval_owner_)
+        fail(kInvalid, "evaluation sets: a newer trainer on this engine owns them");
+}
 
 }  // namespace hbr

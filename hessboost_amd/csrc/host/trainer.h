@@ -120,6 +120,7 @@ public:
     uint32_t add_eval(const float *x, uint64_t n, uint64_t n_cols, float missing, const float *base_margin);
     void eval_margins(uint32_t set, float *out);
     uint64_t eval_rows(uint32_t set) const { return e_.eval_rows(set); }
+    void check_eval_owner() const;
     // softmax depthwise rounds grow their class trees as one batch (else one
     // class tree after another); HBROCM_SOFTMAX_BATCH=0 turns it off
     bool softmax_batches = true;
@@ -141,6 +142,7 @@ private:
     std::vector<float> labels_, weights_;
     std::vector<float> base_;
     std::vector<Tree> trees_;
+    uint64_t eval_owner_ = 0;  // the engine's eval-set owner number at construction
 };
 
 std::vector<GrowTreeNode> records_of(const Tree &t);

@@ -153,6 +153,8 @@ def test_a_new_trainer_drops_the_engine_eval_sets():
                                   expected(second.booster(8), ev).view(np.uint32))
     np.testing.assert_array_equal(before.view(np.uint32),
                                   expected(first.booster(8), ev).view(np.uint32))
+    with pytest.raises(hb.HbrError, match="newer trainer"):
+        first.eval_margins(0)
 
 
 def test_rejects_other_features():
