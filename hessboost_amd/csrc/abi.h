@@ -556,6 +556,7 @@ struct WalkArgs {
 // a present value goes left iff value < cut_values[bin] (-FLT_MAX for bin
 // -1), a missing one follows default_left.
 constexpr uint32_t kEvalLdsNodes = 2048;
+constexpr uint32_t kEvalStagedCols = 64;  // hbr_eval_walk_staged: rows of at most this many features
 struct EvalWalkArgs {
     const float *x;              // [n][n_cols] row-major
     const GrowTreeNode *tree;    // the tree's records

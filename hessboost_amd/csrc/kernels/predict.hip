@@ -450,6 +450,53 @@ __device__ __forceinline__ void eval_walk(const EvalWalkArgs &a, const uint4 *s_
 
 }  // namespace
 
+// Rows of at most kEvalStagedCols features: each wave stages a 64-row block
+// in LDS feature-major with coalesced non-temporal loads (stage_rows), then
+// each lane walks its row from LDS. Dynamic LDS: 4 waves x n_cols x
+// kPredPitch floats. Every wave of a workgroup runs the same number of
+// passes (a wave past the last block stages and walks nothing), so the
+// barriers are uniform.
+extern "C" __global__ __launch_bounds__(256) void hbr_eval_walk_staged(EvalWalkArgs a) {
+    __shared__ uint4 s_node[kEvalLdsNodes];
+    extern __shared__ float s_rows[];
+    if (a.poison && *a.poison != 0u) return;  // uniform: the tree was not kept
+    const uint32_t n_nodes = a.counts ? a.counts->n_nodes : a.n_nodes;
+    if (n_nodes == 0 || a.n_cols == 0 || a.n_cols > kEvalStagedCols) return;
+    const bool lds_nodes = n_nodes <= kEvalLdsNodes;
+    if (lds_nodes)
+        for (uint32_t i = threadIdx.x; i < n_nodes; i += blockDim.x) s_node[i] = eval_node(a, i);
+    const uint32_t wave = threadIdx.x / kPredLanes, lane = threadIdx.x % kPredLanes;
+    const uint32_t waves = blockDim.x / kPredLanes;
+    float *s_x = s_rows + (size_t)wave * a.n_cols * kPredPitch;
+    const uint64_t n_blocks = (a.n + kPredLanes - 1) / kPredLanes;
+    const uint64_t step = (uint64_t)gridDim.x * waves;
+    for (uint64_t base = (uint64_t)blockIdx.x * waves; base < n_blocks; base += step) {
+        const uint64_t blk = base + wave;
+        const uint64_t r0 = blk * kPredLanes;
+        const uint32_t rows = blk >= n_blocks ? 0u : a.n - r0 < kPredLanes ? (uint32_t)(a.n - r0) : kPredLanes;
+        __syncthreads();  // the previous pass's reads of s_x are done (and the node table is written)
+        if (rows) stage_rows<true>(s_x, a.x + r0 * a.n_cols, rows, a.n_cols, lane);
+        __syncthreads();
+        if (lane >= rows) continue;
+        const float *row = s_x + lane;
+        uint4 nd = lds_nodes ? s_node[0] : eval_node(a, 0);
+        bool leaf = nd.z == 0xffffffffu;
+        for (uint32_t st = 0; st < n_nodes && !leaf; st++) {
+            const float v = row[(nd.y & 0x7fffffffu) * kPredPitch];
+            const bool absent = a.missing_is_nan ? __builtin_isnan(v) : v == a.missing_value;
+            const bool go_left = absent ? (nd.y >> 31) != 0u : v < __uint_as_float(nd.x);
+            const uint32_t nid = nd.z + (go_left ? 0u : 1u);
+            if (nid >= n_nodes) break;  // a malformed record: the row gets nothing
+            nd = lds_nodes ? s_node[nid] : eval_node(a, nid);
+            leaf = nd.z == 0xffffffffu;
+        }
+        if (leaf) {
+            float *m = a.margins + (r0 + lane) * a.m_stride + a.output;
+            *m = *m + __uint_as_float(nd.w);
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void hbr_eval_walk(EvalWalkArgs a) {
     __shared__ uint4 s_node[kEvalLdsNodes];
     if (a.poison && *a.poison != 0u) return;  // uniform: the tree was not kept

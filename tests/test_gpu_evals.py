@@ -66,7 +66,24 @@ CASES = [
     ("wide rows", {"objective": "reg:squarederror", "max_depth": 7}, 40, 0.0),
     ("deep tree off LDS", {"objective": "reg:squarederror", "max_depth": 12, "min_child_weight": 0.0,
                            "lambda": 0.0}, 6, 0.0),
+    ("rows wider than the staged walk", {"objective": "reg:squarederror", "max_depth": 5}, 70, 0.0),
 ]
+
+
+def test_in_place_walk_matches_staged(monkeypatch):
+    """The in-place walk (rows read from HBM per step) and the staged one
+    (64-row blocks in LDS) give the same bits."""
+    x, y = data(9_000, 28, 29, "binary:logistic")
+    ev = eval_matrix(4_099, 28, 30)
+    out = []
+    for in_place in (False, True):
+        if in_place:
+            monkeypatch.setenv("HBROCM_EVAL_IN_PLACE", "1")
+        model = hb.train({"objective": "binary:logistic", "max_depth": 6}, hb.DMatrix(x, label=y), 5,
+                         evals=[(hb.DMatrix(ev), "e")])
+        out.append(model.eval_margins["e"])
+        np.testing.assert_array_equal(out[-1].view(np.uint32), expected(model, ev).view(np.uint32))
+    np.testing.assert_array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
 
 
 @pytest.mark.parametrize("name,params,f,miss", CASES, ids=[c[0] for c in CASES])
