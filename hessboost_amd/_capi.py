@@ -17,7 +17,7 @@ CODE_OBJECT = os.path.join(LIB_DIR, "hbrocm_gfx950.hsaco")
 
 OK, REFUSED, DEVICE_ERROR, INVALID = 0, 1, 2, 3
 LOSS_SQUARED_ERROR, LOSS_LOGISTIC, LOSS_SOFTMAX = 0, 1, 2
-OBJ_SQUARED_ERROR, OBJ_LOGISTIC, OBJ_SOFTMAX = 0, 1, 2
+OBJ_SQUARED_ERROR, OBJ_LOGISTIC, OBJ_SOFTMAX, OBJ_LOGITRAW = 0, 1, 2, 3
 GROW_DEPTHWISE, GROW_LOSSGUIDE = 0, 1
 SCAN_EMPTY, SCAN_NUMERIC = 0, 2
 

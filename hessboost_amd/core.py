@@ -424,6 +424,14 @@ class DMatrix:
                 return Engine.from_dense(self.x, cuts, ordinal, missing=self.missing)
         return Engine(self.index(max_bin), ordinal)
 
+    @property
+    def marker(self):
+        """The value that marks a missing cell in dense(): the caller's
+        marker for dense input; NaN for CSR input, whose absent entries are
+        the missing ones (DMatrix::from_csr, src/data/dmatrix.rs:459-510,
+        keeps NaN as the marker and stores only finite values)."""
+        return np.nan if self.csr is not None else self.missing
+
     def dense(self):
         if self.x is not None:
             return self.x
@@ -437,7 +445,7 @@ class DMatrix:
 # ---- training ---------------------------------------------------------------------------
 
 _OBJECTIVES = {"reg:squarederror": A.OBJ_SQUARED_ERROR, "binary:logistic": A.OBJ_LOGISTIC,
-               "reg:logistic": A.OBJ_LOGISTIC, "binary:logitraw": A.OBJ_LOGISTIC,
+               "reg:logistic": A.OBJ_LOGISTIC, "binary:logitraw": A.OBJ_LOGITRAW,
                "multi:softprob": A.OBJ_SOFTMAX, "multi:softmax": A.OBJ_SOFTMAX}
 
 
@@ -519,8 +527,15 @@ class Booster:
             self._forest_ordinal = ordinal
         return self._forest
 
-    def predict(self, data, *, output_margin=False, pred_leaf=False, missing=np.nan, device="rocm:0"):
-        x = data.dense() if isinstance(data, DMatrix) else np.ascontiguousarray(data, np.float32)
+    def predict(self, data, *, output_margin=False, pred_leaf=False, missing=None, device="rocm:0"):
+        """Margins, transformed predictions or leaf ids. `missing` marks an
+        absent cell of an array input (NaN when None); a DMatrix carries
+        its own marker."""
+        if isinstance(data, DMatrix):
+            x, missing = data.dense(), data.marker
+        else:
+            x = np.ascontiguousarray(data, np.float32)
+            missing = np.nan if missing is None else missing
         f = self.forest(_device_ordinal(device))
         if pred_leaf:
             return f.predict_leaf(x, missing)
@@ -716,7 +731,7 @@ class Trainer:
             if bm.size != x.shape[0] * self.n_outputs:
                 raise ValueError("base_margin must hold n_rows * n_outputs values")
         idx = C.c_uint32()
-        A.check(A.lib().hbr_trainer_add_eval(self._h, A.ptr(x), x.shape[0], x.shape[1], float(data.missing),
+        A.check(A.lib().hbr_trainer_add_eval(self._h, A.ptr(x), x.shape[0], x.shape[1], float(data.marker),
                                              A.ptr(bm), C.byref(idx)))
         self._evals.append(x.shape[0])
         return idx.value

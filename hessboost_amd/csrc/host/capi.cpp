@@ -555,7 +555,7 @@ int hbr_trainer_create(hbr_engine *h, const hbr_train_params *p, const float *la
         tp.scale_pos_weight = p->scale_pos_weight;
         tp.has_base_score = p->has_base_score != 0;
         tp.base_score = p->base_score;
-        if (tp.objective < 0 || tp.objective > 2) fail(kInvalid, "trainer: unknown objective");
+        if (tp.objective < 0 || tp.objective > 3) fail(kInvalid, "trainer: unknown objective");
         auto *t = new hbr_trainer{h, nullptr};
         try {
             t->t = std::make_unique<Trainer>(e, tp, labels, weights, n);

@@ -369,6 +369,29 @@ static float logit(float p) {
     return -std::log(1.0f / p - 1.0f);
 }
 
+// newton_intercepts (objective/mod.rs:528-547): one Newton step from
+// all-zero margins, fit_stump (:552-566: -G / max(H, 1e-6) with G, H summed
+// in f64 in row order, rounded once to f32); the caller applies
+// pred_transform and the link. The pairs at a zero margin in closed form,
+// with w' = w scaled by scale_pos_weight for a label of exactly 1:
+//   squared error (regression.rs:42-58): g = (0 - y) w', h = w';
+//   logistic (simd/scalar.rs:8-29): both of the reference's paths give
+//   p = 1 / (1 + 1) = 0.5 exactly (the AVX2 exp polynomial and libm expf
+//   both return 1 at 0), so g = (0.5 - y) w', h = max(0.25, 1e-16) w'.
+static float newton_step(bool logistic, const float *labels, const float *weights, uint64_t n, float spw) {
+    double g = 0.0, h = 0.0;
+    for (uint64_t i = 0; i < n; i++) {
+        const float y = labels[i];
+        float w = weights ? weights[i] : 1.0f;
+        if (y == 1.0f) w *= spw;
+        const float gi = logistic ? (0.5f - y) * w : (0.0f - y) * w;
+        const float hi = logistic ? std::fmax(0.25f, kMinHess) * w : w;
+        g += (double)gi;
+        h += (double)hi;
+    }
+    return (float)(-g / std::fmax(h, 1e-6));
+}
+
 std::vector<float> base_margins(const TrainParams &p, const float *labels, const float *weights, uint64_t n) {
     if (p.objective == HBR_OBJ_SOFTMAX) {
         const uint32_t k = p.num_class;
@@ -393,9 +416,24 @@ std::vector<float> base_margins(const TrainParams &p, const float *labels, const
         for (auto &v : m) v -= mean;
         return m;
     }
-    if (p.objective == HBR_OBJ_LOGISTIC)
-        return {p.has_base_score ? logit(p.base_score) : logit(weighted_label_mean(labels, weights, n))};
-    return {p.has_base_score ? p.base_score : weighted_label_mean(labels, weights, n)};
+    if (p.objective == HBR_OBJ_LOGISTIC || p.objective == HBR_OBJ_LOGITRAW) {
+        // classification.rs:67-72: binary:logitraw's link is the identity;
+        // :132-141: a scale_pos_weight away from 1 takes the Newton step
+        const bool raw = p.objective == HBR_OBJ_LOGITRAW;
+        if (p.has_base_score) return {raw ? p.base_score : logit(p.base_score)};
+        if (std::fabs(p.scale_pos_weight - 1.0f) > 1e-6f) {
+            const float step = newton_step(true, labels, weights, n, p.scale_pos_weight);
+            if (raw) return {step};
+            return {logit(1.0f / (std::exp(std::fmin(-step, 88.7f)) + 1.0f))};  // sigmoid_scalar, simd/mod.rs:425-427
+        }
+        const float mean = weighted_label_mean(labels, weights, n);
+        return {raw ? mean : logit(mean)};
+    }
+    // regression.rs:66-74: the Newton step when scale_pos_weight != 1
+    if (p.has_base_score) return {p.base_score};
+    if (std::fabs(p.scale_pos_weight - 1.0f) > 1e-6f)
+        return {newton_step(false, labels, weights, n, p.scale_pos_weight)};
+    return {weighted_label_mean(labels, weights, n)};
 }
 
 Trainer::Trainer(Engine &e, const TrainParams &p, const float *labels, const float *weights, uint64_t n)
@@ -417,6 +455,9 @@ Trainer::Trainer(Engine &e, const TrainParams &p, const float *labels, const flo
     if (weights) weights_.assign(weights, weights + n);
     if (const char *v = std::getenv("HBROCM_SOFTMAX_BATCH")) softmax_batches = std::strtol(v, nullptr, 10) != 0;
     base_ = base_margins(p, labels, weights, n);
+    // training/train.rs:425-433: a non-finite intercept is an error
+    for (float b : base_)
+        if (!std::isfinite(b)) fail(kInvalid, "estimated intercept is not finite; check the labels");
     std::vector<float> m((size_t)n * k_);
     for (uint64_t r = 0; r < n; r++)
         for (uint32_t c = 0; c < k_; c++) m[r * k_ + c] = base_[c];
@@ -595,7 +636,8 @@ void Trainer::boost(uint64_t rounds) {
 
 hbr_device_loss Trainer::device_loss() const {
     hbr_device_loss loss{};
-    loss.kind = p_.objective == HBR_OBJ_LOGISTIC ? HBR_LOSS_LOGISTIC : HBR_LOSS_SQUARED_ERROR;
+    loss.kind = p_.objective == HBR_OBJ_LOGISTIC || p_.objective == HBR_OBJ_LOGITRAW ? HBR_LOSS_LOGISTIC
+                                                                                     : HBR_LOSS_SQUARED_ERROR;
     loss.scale_pos_weight = p_.scale_pos_weight;
     loss.min_hess = kMinHess;
     loss.max_input = 80.0f;

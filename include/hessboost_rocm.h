@@ -342,6 +342,9 @@ int hbr_kernel_stats(hbr_engine *e, char *buf, size_t len);
 #define HBR_OBJ_SQUARED_ERROR 0
 #define HBR_OBJ_LOGISTIC 1
 #define HBR_OBJ_SOFTMAX 2
+/* binary:logitraw: the logistic loss with the identity link (raw margins
+ * and a raw intercept, src/objective/classification.rs:55-72). */
+#define HBR_OBJ_LOGITRAW 3
 #define HBR_GROW_DEPTHWISE 0
 #define HBR_GROW_LOSSGUIDE 1
 

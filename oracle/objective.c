@@ -10,7 +10,10 @@
  * simd/mod.rs:580-600 (softmax row: shift by max(f32::MIN_POSITIVE, preds),
  * f64 sum of expf, p = expf(x - wmax) / (f32)sum, h = max(2p(1-p)w, 1e-16)),
  * objective/mod.rs:645-666 (weighted label mean), classification.rs:66-77
- * (logit link), multiclass.rs:68-94 (centered log class frequencies).
+ * (logit link; the identity for binary:logitraw), classification.rs:132-141
+ * and regression.rs:66-74 with objective/mod.rs:528-566 (one Newton step
+ * from zero margins when scale_pos_weight != 1), multiclass.rs:68-94 (centered log class
+ * frequencies).
  *
  * The vector kernel is written with the same AVX2 intrinsics, in the same
  * order, so the oracle reproduces the reference's host bits on any x86-64
@@ -21,6 +24,7 @@
 #include <float.h>
 #include <immintrin.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define MIN_HESS 1e-16f
@@ -236,6 +240,27 @@ static float logit_link(float p) {
     return -logf(1.0f / p - 1.0f);
 }
 
+/* newton_intercepts (src/objective/mod.rs:528-547): the loss's own
+   gradient at all-zero margins, then fit_stump (:552-566: f64 sums of g and
+   h in row order, -G / max(H, 1e-6) rounded once to f32). The caller applies
+   pred_transform and the link. */
+static float newton_step(int objective, const float *labels, const float *weights, size_t n, float spw) {
+    float *zeros = (float *)calloc(n ? n : 1, sizeof(float));
+    float *gp = (float *)malloc(2 * (n ? n : 1) * sizeof(float));
+    if (objective == OR_OBJ_SQUARED_ERROR)
+        or_gradient_squared_error(zeros, labels, weights, n, spw, gp);
+    else
+        or_gradient_logistic(zeros, labels, weights, n, spw, gp);
+    double g = 0.0, h = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        g += (double)gp[2 * i];
+        h += (double)gp[2 * i + 1];
+    }
+    free(zeros);
+    free(gp);
+    return (float)(-g / fmax(h, 1e-6));
+}
+
 void or_base_margins(const float *labels, const float *weights, size_t n, const or_params *p,
                      float *out) {
     if (p->objective == OR_OBJ_SOFTMAX) {
@@ -263,10 +288,26 @@ void or_base_margins(const float *labels, const float *weights, size_t n, const 
         for (size_t c = 0; c < k; c++) out[c] -= mean;
         return;
     }
-    if (p->objective == OR_OBJ_LOGISTIC) {
-        out[0] = p->has_base_score ? logit_link(p->base_score)
-                                   : logit_link(weighted_label_mean(labels, weights, n));
+    if (p->objective == OR_OBJ_LOGISTIC || p->objective == OR_OBJ_LOGITRAW) {
+        /* classification.rs:67-72: binary:logitraw's link is the identity */
+        const int raw = p->objective == OR_OBJ_LOGITRAW;
+        if (p->has_base_score)
+            out[0] = raw ? p->base_score : logit_link(p->base_score);
+        else if (fabsf(p->scale_pos_weight - 1.0f) > 1e-6f) /* classification.rs:132-141 */
+        {
+            const float w = newton_step(p->objective, labels, weights, n, p->scale_pos_weight);
+            out[0] = raw ? w : logit_link(or_sigmoid(w)); /* sigmoid_scalar, then the logit */
+        }
+        else
+            out[0] = raw ? weighted_label_mean(labels, weights, n)
+                         : logit_link(weighted_label_mean(labels, weights, n));
         return;
     }
-    out[0] = p->has_base_score ? p->base_score : weighted_label_mean(labels, weights, n);
+    /* regression.rs:66-74: the Newton step when scale_pos_weight != 1 */
+    if (p->has_base_score)
+        out[0] = p->base_score;
+    else if (fabsf(p->scale_pos_weight - 1.0f) > 1e-6f)
+        out[0] = newton_step(p->objective, labels, weights, n, p->scale_pos_weight);
+    else
+        out[0] = weighted_label_mean(labels, weights, n);
 }

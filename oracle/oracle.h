@@ -105,7 +105,9 @@ void or_sum_rows(const float *gpair, const uint32_t *rows, size_t m, double *out
 size_t or_sum_order_grain(int dense, size_t index_rows, size_t len, int contiguous);
 
 /* ---- training parameters ------------------------------------------------ */
-enum { OR_OBJ_SQUARED_ERROR = 0, OR_OBJ_LOGISTIC = 1, OR_OBJ_SOFTMAX = 2 };
+/* OR_OBJ_LOGITRAW: binary:logitraw, the logistic loss with the identity link
+   (src/objective/classification.rs:55-72). */
+enum { OR_OBJ_SQUARED_ERROR = 0, OR_OBJ_LOGISTIC = 1, OR_OBJ_SOFTMAX = 2, OR_OBJ_LOGITRAW = 3 };
 enum { OR_GROW_DEPTHWISE = 0, OR_GROW_LOSSGUIDE = 1 };
 
 typedef struct or_params {

@@ -15,7 +15,7 @@ import numpy as np
 _DIR = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_DIR, "liboracle.so")
 
-OBJ_SQUARED_ERROR, OBJ_LOGISTIC, OBJ_SOFTMAX = 0, 1, 2
+OBJ_SQUARED_ERROR, OBJ_LOGISTIC, OBJ_SOFTMAX, OBJ_LOGITRAW = 0, 1, 2, 3
 GROW_DEPTHWISE, GROW_LOSSGUIDE = 0, 1
 
 

@@ -39,7 +39,7 @@ void or_set_threads(int n) {
 static void gradients(or_model *m, const float *labels, const float *weights, const or_params *p) {
     if (p->objective == OR_OBJ_SQUARED_ERROR)
         or_gradient_squared_error(m->margins, labels, weights, m->n, p->scale_pos_weight, m->gpair);
-    else if (p->objective == OR_OBJ_LOGISTIC)
+    else if (p->objective == OR_OBJ_LOGISTIC || p->objective == OR_OBJ_LOGITRAW)
         or_gradient_logistic(m->margins, labels, weights, m->n, p->scale_pos_weight, m->gpair);
     else
         or_gradient_softmax(m->margins, labels, weights, m->n, m->k, m->gpair);

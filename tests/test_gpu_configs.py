@@ -29,6 +29,25 @@ def test_c1_full_size_matches_oracle():
     assert np.max(np.abs(m - ref.margins())) <= 1e-5
 
 
+def test_c2_full_size_matches_oracle():
+    """The binary logistic workload at its full size: 10,500,000 x 28
+    higgs-like rows, depth 8, eta 0.1, 256 bins, free-running for 10 rounds.
+    At this row count the per-tree fixed-point unit is 2^(e_max - 38), the
+    regime where integer sums and the reference's f64 chains differ in their
+    last bits: every tree must still match node for node (split feature,
+    threshold, default direction, children), leaves within 1e-5, and the
+    final margins within 1e-5."""
+    x, y = synthetic.higgs_like(n=10_500_000, seed=0)
+    O.set_threads(16)
+    ref = O.Model(O.Dataset(x, max_bin=256), y, O.params(objective=O.OBJ_LOGISTIC, max_depth=8, eta=0.1), 10)
+    params = {"objective": "binary:logistic", "max_depth": 8, "eta": 0.1, "max_bin": 256}
+    d = hb.DMatrix(x, label=y)
+    t = hb.Trainer(d.engine(256), params, y)
+    t.boost(10)
+    compare_trees(t.trees(), ref.trees())
+    assert np.max(np.abs(t.margins() - ref.margins())) <= 1e-5
+
+
 def test_c3_shape_sparse_missing_lossguide_matches_oracle():
     (row_ptr, col, val), y, _ = synthetic.sparse_wide(n=20_000, f=300, density=0.1, seed=7)
     params = {"grow_policy": "lossguide", "max_depth": 0, "max_leaves": 255, "eta": 0.3, "max_bin": 64}

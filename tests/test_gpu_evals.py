@@ -129,6 +129,31 @@ def test_csr_training_input():
     np.testing.assert_array_equal(model.eval_margins["e"].view(np.uint32), expected(model, ev).view(np.uint32))
 
 
+def test_csr_eval_set_with_a_non_nan_marker_and_dmatrix_predict():
+    """A CSR eval set's absent entries are its missing values whatever marker
+    the DMatrix was given (DMatrix::from_csr keeps NaN as the marker and
+    stores only finite values, src/data/dmatrix.rs:459-510), so explicit
+    zeros stay present values; Booster.predict of a DMatrix reads the
+    matrix's own marker (-999 here) instead of NaN."""
+    x, y = data(6_000, 12, 33, "reg:squarederror", 1, 0.0)
+    ev = eval_matrix(900, 12, 34)
+    ev[np.isinf(ev)] = np.copysign(np.float32(3e38), ev[np.isinf(ev)])  # CSR stores finite values only
+    ev[5:50, :4] = 0.0  # explicit zeros: present in CSR
+    present = ~np.isnan(ev)
+    rp = np.zeros(ev.shape[0] + 1, np.uint64)
+    rp[1:] = np.cumsum(present.sum(1))
+    rows, cols = np.nonzero(present)
+    dcsr = hb.DMatrix((rp, cols.astype(np.uint32), ev[rows, cols]), n_cols=12, missing=0.0)
+    model = hb.train({"objective": "reg:squarederror", "max_depth": 5}, hb.DMatrix(x, label=y), 4,
+                     evals=[(dcsr, "csr")])
+    np.testing.assert_array_equal(model.eval_margins["csr"].view(np.uint32), expected(model, ev).view(np.uint32))
+    np.testing.assert_array_equal(model.predict(dcsr, output_margin=True).view(np.uint32),
+                                  expected(model, ev).reshape(-1).view(np.uint32))
+    marked = np.where(np.isnan(ev), np.float32(-999.0), ev).astype(np.float32)
+    got = model.predict(hb.DMatrix(marked, missing=-999.0), output_margin=True)
+    np.testing.assert_array_equal(got.view(np.uint32), expected(model, ev).reshape(-1).view(np.uint32))
+
+
 def test_added_after_rounds_with_base_margin_and_missing_marker():
     """A set added after some rounds takes the trees already grown; a base
     margin replaces the base score; a non-NaN missing marker is honoured."""

@@ -14,6 +14,7 @@ pytestmark = pytest.mark.gpu
 
 OBJECTIVES = {"reg:squarederror": O.OBJ_SQUARED_ERROR, "binary:logistic": O.OBJ_LOGISTIC,
               "multi:softprob": O.OBJ_SOFTMAX}
+ORACLE_OBJECTIVES = dict(OBJECTIVES, **{"binary:logitraw": O.OBJ_LOGITRAW})
 
 
 def draw(seed):
@@ -47,6 +48,11 @@ def draw(seed):
         cfg["params"]["num_class"] = k
     if rng.random() < 0.3:
         cfg["params"]["monotone_constraints"] = [int(v) for v in rng.integers(-1, 2, f)]
+    # drawn last, so the draws above keep their values for every seed
+    if objective != "multi:softprob" and rng.random() < 0.35:
+        cfg["params"]["scale_pos_weight"] = float(rng.choice([0.5, 2.0, 3.0]))
+    if objective == "binary:logistic" and rng.random() < 0.3:
+        cfg["objective"] = cfg["params"]["objective"] = "binary:logitraw"
     return cfg
 
 
@@ -58,7 +64,7 @@ def data(cfg, seed):
     z = x[:, 0] + 0.5 * np.sin(2 * x[:, 1 % f]) - 0.3 * x[:, 2 % f] * x[:, 3 % f]
     if cfg["objective"] == "reg:squarederror":
         y = (z + 0.1 * rng.standard_normal(n)).astype(np.float32)
-    elif cfg["objective"] == "binary:logistic":
+    elif cfg["objective"] in ("binary:logistic", "binary:logitraw"):
         y = (rng.random(n) < 1 / (1 + np.exp(-2 * z))).astype(np.float32)
     else:
         y = np.clip(np.floor((z - z.min()) / (np.ptp(z) + 1e-9) * cfg["k"]), 0, cfg["k"] - 1).astype(np.float32)
@@ -70,12 +76,13 @@ def data(cfg, seed):
 
 def oracle_params(cfg):
     p = cfg["params"]
-    return O.params(objective=OBJECTIVES[cfg["objective"]], eta=p["eta"], gamma=p["gamma"], reg_lambda=p["lambda"],
+    return O.params(objective=ORACLE_OBJECTIVES[cfg["objective"]], eta=p["eta"], gamma=p["gamma"], reg_lambda=p["lambda"],
                     alpha=p["alpha"], min_child_weight=p["min_child_weight"], max_delta_step=p["max_delta_step"],
                     max_depth=p["max_depth"], max_leaves=p.get("max_leaves", 0),
                     grow_policy=O.GROW_LOSSGUIDE if p.get("grow_policy") == "lossguide" else O.GROW_DEPTHWISE,
                     num_class=cfg["k"] if cfg["objective"] == "multi:softprob" else 0,
-                    monotone=p.get("monotone_constraints"), max_bin=cfg["max_bin"])
+                    monotone=p.get("monotone_constraints"), max_bin=cfg["max_bin"],
+                    scale_pos_weight=p.get("scale_pos_weight", 1.0))
 
 
 def to_csr(x):
@@ -101,4 +108,6 @@ def test_random_configuration_matches_oracle(seed):
         dm = hb.DMatrix(x, label=y, weight=w)
     ref = O.Model(ds, y, oracle_params(cfg), 3, weights=w)
     model = hb.train(params, dm, 3)
+    assert np.array_equal(np.asarray(model.base_score, np.float32).view(np.uint32),
+                          np.asarray(ref.base_score(), np.float32).view(np.uint32))
     compare_trees(model.trees, ref.trees())

@@ -71,6 +71,34 @@ def test_boosting_matches_oracle(objective):
     assert np.max(np.abs(m - ref.margins())) <= 1e-5
 
 
+@pytest.mark.parametrize("objective,spw,weighted", [
+    ("binary:logistic", 2.0, False), ("binary:logistic", 0.5, True), ("binary:logitraw", 1.0, False),
+    ("binary:logitraw", 2.0, True), ("reg:squarederror", 2.0, True)])
+def test_intercepts_match_oracle(objective, spw, weighted):
+    """classification.rs:132-141 / regression.rs:66-74: scale_pos_weight away
+    from 1 takes one Newton step for the intercept (objective/mod.rs:528-566);
+    binary:logitraw keeps the label mean and the step raw
+    (classification.rs:67-72). The base score bit for bit, then the trees
+    and margins, against the oracle."""
+    x, y = synthetic.regression_100k(n=9_003, f=8, seed=11)
+    y = (y > 0.7).astype(np.float32) if objective != "reg:squarederror" else y
+    if objective == "reg:squarederror":
+        y[::5] = 1.0  # labels of exactly 1 are the ones scale_pos_weight reweighs
+    w = np.random.default_rng(11).random(len(y)).astype(np.float32) + 0.2 if weighted else None
+    obj = {"binary:logistic": O.OBJ_LOGISTIC, "binary:logitraw": O.OBJ_LOGITRAW,
+           "reg:squarederror": O.OBJ_SQUARED_ERROR}[objective]
+    ref = O.Model(O.Dataset(x, weights=w), y, O.params(objective=obj, max_depth=5, eta=0.3, scale_pos_weight=spw), 4,
+                  weights=w)
+    model = hb.train({"objective": objective, "max_depth": 5, "eta": 0.3, "scale_pos_weight": spw},
+                     hb.DMatrix(x, label=y, weight=w), 4)
+    assert np.float32(model.base_score[0]).view(np.uint32) == np.float32(ref.base_score()[0]).view(np.uint32)
+    compare_trees(model.trees, ref.trees())
+    m = model.predict(x, output_margin=True)
+    assert np.max(np.abs(m - ref.margins())) <= 1e-5
+    if objective == "binary:logitraw":
+        assert np.array_equal(model.predict(x), m)  # predictions stay raw margins
+
+
 def test_lossguide_matches_oracle():
     rng = np.random.default_rng(2)
     x = rng.standard_normal((8_000, 8), dtype=np.float32)

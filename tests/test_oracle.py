@@ -331,6 +331,82 @@ def test_base_margins():
     assert np.all(O.base_margins(np.array([0, 1, 2], np.float32), ps) == 0.0)
 
 
+def _libm():
+    import ctypes
+    m = ctypes.CDLL("libm.so.6")
+    for fn in (m.expf, m.logf):
+        fn.restype, fn.argtypes = ctypes.c_float, [ctypes.c_float]
+    return m
+
+
+def _logit_of_sigmoid(step):
+    """sigmoid_scalar (simd/mod.rs:425-427) then the logistic link
+    (classification.rs:74-77), each in f32 with the host libm the reference
+    calls through f32::exp / f32::ln."""
+    m = _libm()
+    f = np.float32
+    p = f(1.0) / (f(m.expf(f(min(-f(step), f(88.7))))) + f(1.0))
+    p = min(max(p, f(1e-6)), f(1.0) - f(1e-6))
+    return -f(m.logf(f(1.0) / p - f(1.0)))
+
+
+def test_logitraw_intercept_is_the_label_mean():
+    """classification.rs:298-303: binary:logitraw's intercept is the label
+    mean itself (the identity link); a given base_score is kept as is."""
+    p = O.params(objective=O.OBJ_LOGITRAW)
+    assert O.base_margins(np.array([1, 0, 0, 0], np.float32), p)[0] == np.float32(0.25)
+    pb = O.params(objective=O.OBJ_LOGITRAW, base_score=-3.5)
+    assert O.base_margins(np.array([1, 0], np.float32), pb)[0] == np.float32(-3.5)
+
+
+def test_newton_intercepts_closed_forms():
+    """classification.rs:132-141 and regression.rs:66-74: with
+    scale_pos_weight away from 1 the intercept is one Newton step from zero
+    margins (objective/mod.rs:528-566). Labels [1, 0] with spw 3 give the
+    reference's gradient KAT pairs (classification.rs:262-273: (-1.5, 0.75),
+    (0.5, 0.25)), so -G/H = 1.0, then sigmoid and logit; logitraw keeps the
+    step; squared error over [1, 0, 2] with spw 2 weighs the 1 twice:
+    -G/H = 4/4."""
+    y = np.array([1, 0], np.float32)
+    lg = O.base_margins(y, O.params(objective=O.OBJ_LOGISTIC, scale_pos_weight=3.0))[0]
+    assert lg == _logit_of_sigmoid(1.0)
+    assert O.base_margins(y, O.params(objective=O.OBJ_LOGITRAW, scale_pos_weight=3.0))[0] == np.float32(1.0)
+    ys = np.array([1, 0, 2], np.float32)
+    assert O.base_margins(ys, O.params(objective=O.OBJ_SQUARED_ERROR, scale_pos_weight=2.0))[0] == np.float32(1.0)
+    # 25% positives: spw 1.5 -> G = 3 * 0.5 - 0.75 = 0.75, H = 0.75 + 0.375
+    y4 = np.array([1, 0, 0, 0], np.float32)
+    step = np.float32(-0.75 / 1.125)
+    got = O.base_margins(y4, O.params(objective=O.OBJ_LOGISTIC, scale_pos_weight=1.5))[0]
+    assert got == _logit_of_sigmoid(step)
+    assert abs(got - np.float32(-np.log(3.0))) > 0.1  # not the logit of the positive rate
+    # |spw - 1| <= 1e-6 (f32) keeps the label-mean path
+    mean_path = O.base_margins(y4, O.params(objective=O.OBJ_LOGISTIC, scale_pos_weight=1.0000005))[0]
+    assert mean_path == O.base_margins(y4, O.params(objective=O.OBJ_LOGISTIC))[0]
+
+
+@pytest.mark.parametrize("spw,weighted", [(0.5, True), (2.0, False), (3.0, True)])
+def test_newton_intercept_over_the_vector_gradient_path(spw, weighted):
+    """1,001 rows (125 AVX2 vectors and a scalar tail) through the oracle's
+    gradient at zero margins equal the per-row closed form at p = 0.5,
+    summed as one f64 chain in row order (fit_stump, objective/mod.rs:552-566)."""
+    rng = np.random.default_rng(int(spw * 10))
+    y = (rng.random(1001) < 0.3).astype(np.float32)
+    y[::97] = 0.25  # labels other than 0 and 1 are not reweighted
+    w = (rng.random(1001) * 3 + 0.1).astype(np.float32) if weighted else np.ones(1001, np.float32)
+    wp = np.where(y == 1.0, w * np.float32(spw), w).astype(np.float32)
+    g = np.cumsum(((np.float32(0.5) - y) * wp).astype(np.float32).astype(np.float64))[-1]
+    h = np.cumsum((np.float32(0.25) * wp).astype(np.float32).astype(np.float64))[-1]
+    step = np.float32(-g / max(h, 1e-6))
+    for obj, want in ((O.OBJ_LOGISTIC, _logit_of_sigmoid(step)), (O.OBJ_LOGITRAW, step)):
+        got = O.base_margins(y, O.params(objective=obj, scale_pos_weight=spw), weights=w if weighted else None)[0]
+        assert got == want, (obj, got, want)
+    gs = np.cumsum(((np.float32(0.0) - y) * wp).astype(np.float32).astype(np.float64))[-1]
+    hs = np.cumsum(wp.astype(np.float64))[-1]
+    sq = O.base_margins(y, O.params(objective=O.OBJ_SQUARED_ERROR, scale_pos_weight=spw),
+                        weights=w if weighted else None)[0]
+    assert sq == np.float32(-gs / hs)
+
+
 def _sawtooth(n, period, start, step):
     """start + (i % period) * step in f32 (simd/tests.rs:24-30)."""
     i = (np.arange(n) % period).astype(np.float32)
