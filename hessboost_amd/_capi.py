@@ -131,6 +131,7 @@ SIGNATURES = {
                                         C.c_void_p]),
     "hbr_prepare": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
     "hbr_build": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "hbr_build_device_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "hbr_begin_tree": (C.c_int, [C.c_void_p, C.c_uint64, P(Segment)]),
     "hbr_root_total": (C.c_int, [C.c_void_p, P(Segment), C.c_void_p]),
     "hbr_root_total_fixed": (C.c_int, [C.c_void_p, P(Segment), C.c_void_p, C.c_void_p]),

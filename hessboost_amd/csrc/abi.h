@@ -322,6 +322,22 @@ struct CsrRangeArgs {
 constexpr uint32_t kCsrGroupBins = 8192;
 constexpr uint32_t kCsrThreads = 1024;
 
+// A histogram of a caller's device row list built in a fixed scratch area
+// (no allocation): the row ids are checked against the index, the one node
+// record is written on the device, and the int64 bins of the output are
+// turned into f64 in place at the end.
+struct FixedBuildArgs {
+    const uint32_t *rows;       // caller's device row ids
+    uint64_t m;
+    uint32_t n_rows;            // index rows: ids at or beyond are refused
+    uint32_t total_bins;
+    uint32_t *flag;             // scratch word: nonzero when some id is out of range
+    HistNode *node;             // scratch node record
+    QBin *bins;                 // the caller's output, first as int64 bins
+    double *out;                // the same memory as f64 (g, h) pairs
+    const QScale *scale;        // the staged tree's exponents
+};
+
 // Sum of a node's tile partials into its slot (nodes of one tile are
 // written by the histogram kernel directly).
 struct ReduceArgs {

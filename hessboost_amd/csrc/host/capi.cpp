@@ -9,6 +9,7 @@
 #include "cuts.h"
 #include "engine.h"
 #include "forest.h"
+#include "noalloc.h"
 #include "hessboost_rocm.h"
 #include "trainer.h"
 
@@ -297,6 +298,15 @@ int hbr_build(hbr_engine *h, const uint32_t *rows, uint64_t m, double *out) {
     return with_engine(h, [&](Engine &e) {
         if (!out || (!rows && m)) fail(kInvalid, "build: null argument");
         dequant_hist(e, e.build_rows(rows, m), out);
+    });
+}
+
+int hbr_build_device_noalloc(hbr_engine *h, const uint32_t *rows, uint64_t m, double *out) {
+    return with_engine(h, [&](Engine &e) {
+        if (!out || (!rows && m)) fail(kInvalid, "build: null argument");
+        uint64_t bytes = 0;
+        uint8_t *scratch = fixed_scratch(e.dev().ordinal(), &bytes);
+        if (!e.build_rows_fixed(rows, m, out, scratch, bytes)) fail(kInvalid, "build: a row beyond the index");
     });
 }
 

@@ -1589,6 +1589,106 @@ std::vector<QBin> Engine::build_rows(const uint32_t *rows, uint64_t m) {
     return out;
 }
 
+// Scratch layout of build_rows_fixed: the row-check word and the plan's
+// counts, the node record, the tile plan (at most kFixedMaxTiles tiles),
+// then the tile partials.
+constexpr uint64_t kFixedNodeAt = 256, kFixedTilesAt = 4096, kFixedMaxTiles = 4096, kFixedPartialAt = 128 * 1024;
+static_assert(kFixedTilesAt + (kFixedMaxTiles + 1) * sizeof(HistTile) <= kFixedPartialAt, "tile plan overlaps");
+
+bool Engine::build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uint8_t *scratch, uint64_t bytes) {
+    if (!level_pairs_ && !pairs_staged()) fail(kInvalid, "build: no gradients staged");
+    if (m >= (uint64_t)UINT32_MAX) fail(kInvalid, "build: more than 2^32 - 2 rows in one call");
+    if (!scratch || bytes <= kFixedPartialAt) fail(kInvalid, "build: no scratch");
+    const uint32_t fg = hist_features_per_group;
+    const uint32_t groups = dense_u8_ ? ceil_div(n_cols_, fg) : ceil_div(total_bins_, kCsrGroupBins);
+    const uint64_t per_tile = (uint64_t)groups * (dense_u8_ ? fg * 256ull : (uint64_t)kCsrGroupBins) * sizeof(QBin);
+    const uint64_t budget = bytes - kFixedPartialAt;
+    if (per_tile > budget)
+        fail(kInvalid, "build (fixed scratch): one row tile's partial sums take " + std::to_string(per_tile) +
+                           " bytes, beyond the " + std::to_string(budget) + " bytes the scratch holds for them");
+    const uint32_t per_cu = !dense_u8_ ? 1 : fg <= 8 ? 4 : fg <= 16 ? 2 : 1;
+    uint64_t target = std::max<uint64_t>(1, (uint64_t)dev_.cu_count() * per_cu * hist_waves / groups);
+    target = std::min<uint64_t>({target, budget / per_tile, kFixedMaxTiles - 1});
+
+    hipStream_t s = dev_.stream();
+    uint32_t *flag = reinterpret_cast<uint32_t *>(scratch);
+    uint32_t *counts = flag + 4;
+    HistNode *node = reinterpret_cast<HistNode *>(scratch + kFixedNodeAt);
+    HistTile *tiles = reinterpret_cast<HistTile *>(scratch + kFixedTilesAt);
+    QBin *partial = reinterpret_cast<QBin *>(scratch + kFixedPartialAt);
+
+    FixedBuildArgs f{};
+    f.rows = rows;
+    f.m = m;
+    f.n_rows = (uint32_t)n_rows_;
+    f.total_bins = total_bins_;
+    f.flag = flag;
+    f.node = node;
+    f.bins = reinterpret_cast<QBin *>(out);
+    f.out = out;
+    f.scale = level_scale_ ? level_scale_ : scale_dev();
+    // the word starts at zero on every call (a kernel, not a memset)
+    dev_.launch("hbr_fixed_begin", dim3(1), dim3(64), f);
+    if (m) {
+        const uint64_t blocks = std::min<uint64_t>((m + 255) / 256, (uint64_t)dev_.cu_count() * 8);
+        dev_.launch("hbr_fixed_check", dim3((uint32_t)blocks), dim3(256), f);
+    }
+    dev_.launch("hbr_fixed_node", dim3(1), dim3(64), f);
+
+    PlanArgs p{};
+    p.nodes = node;
+    p.n_nodes = 1;
+    p.target_tiles = (uint32_t)target;
+    p.tiles = tiles;
+    p.counts = counts;
+    p.min_rows = kHistMinRows;
+    dev_.launch("hbr_hist_plan", dim3(1), dim3(256), p);
+
+    HistArgs a{};
+    a.nodes = node;
+    a.tiles = tiles;
+    a.counts = counts;
+    a.rows[0] = a.rows[1] = rows;
+    a.gpair = level_pairs_ ? level_pairs_ : pairs();
+    a.scale = f.scale;
+    a.class_rows = level_pairs_ ? (uint32_t)n_rows_ : 0u;
+    a.csr_ranges = !dense_u8_ && csr_ranges_.size() ? csr_ranges_.get() : nullptr;
+    a.bins8 = rows8_.get();
+    a.stride = stride_;
+    a.n_cols = n_cols_;
+    a.row_ptr = row_ptr_.get();
+    a.gbins = gbins_.get();
+    a.feature_offset = d_fo_.get();
+    a.hist = f.bins;
+    a.partial = partial;
+    a.total_bins = total_bins_;
+    a.groups = groups;
+    const bool bm = hist_bin_major && fg >= 16;
+    const char *k = !dense_u8_ ? "hbr_hist_csr"
+                    : fg <= 8  ? "hbr_hist_dense8_fg8"
+                    : fg <= 16 ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
+                               : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");
+    dev_.launch(k, dim3((uint32_t)(target + 1) * groups), dim3(dense_u8_ ? hist_threads : kCsrThreads), a);
+    ReduceArgs r{};
+    r.nodes = node;
+    r.partial = partial;
+    r.hist = f.bins;
+    r.feature_offset = d_fo_.get();
+    r.n_cols = n_cols_;
+    r.total_bins = total_bins_;
+    r.groups = groups;
+    r.fg = fg;
+    if (dense_u8_)
+        dev_.launch("hbr_hist_reduce", dim3(n_cols_ * 4, 1), dim3(1024), r);
+    else
+        dev_.launch("hbr_hist_reduce_csr", dim3(ceil_div(total_bins_, 256), 1), dim3(256), r);
+    dev_.launch("hbr_fixed_finish", dim3(ceil_div(total_bins_, 256)), dim3(256), f);
+    uint32_t bad = 0;
+    HBR_HIP(hipMemcpyAsync(&bad, flag, sizeof bad, hipMemcpyDeviceToHost, s));
+    dev_.sync();
+    return bad == 0;
+}
+
 std::vector<uint32_t> Engine::rows_of(const Segment &sg) {
     std::vector<uint32_t> out(sg.len);
     write_identity_rows();

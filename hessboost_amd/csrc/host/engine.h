@@ -216,6 +216,13 @@ public:
     void read_eval_margins(uint32_t set, float *out);
     // HistogramBackend::build of a host row list (per-node host growth).
     std::vector<QBin> build_rows(const uint32_t *rows, uint64_t m);
+    // The same over a device row list into a device output (2 x total_bins
+    // f64, g and h interleaved), with every intermediate buffer (the tile
+    // plan, tile partials, the node record, a row-check word) inside
+    // `scratch` (`bytes` of device memory the caller keeps): nothing is
+    // allocated. Refuses an index whose tile partials cannot fit; returns
+    // false when a row id is beyond the index (the output then holds zeros).
+    bool build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uint8_t *scratch, uint64_t bytes);
     std::vector<uint32_t> rows_of(const Segment &s);
     std::vector<QBin> read_slot(uint32_t slot);
 

@@ -428,6 +428,41 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_reduce_csr(ReduceArgs
     a.hist[(size_t)nd.slot * a.total_bins + b] = QBin{g, h};
 }
 
+// ---- a histogram of a caller's device row list in a fixed scratch area ----
+
+extern "C" __global__ __launch_bounds__(64) void hbr_fixed_begin(FixedBuildArgs a) {
+    if (threadIdx.x == 0) *a.flag = 0u;
+}
+
+// Any row id at or beyond the index's rows sets the word.
+extern "C" __global__ __launch_bounds__(256) void hbr_fixed_check(FixedBuildArgs a) {
+    bool bad = false;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.m; i += (uint64_t)gridDim.x * blockDim.x)
+        bad |= a.rows[i] >= a.n_rows;
+    if (__ballot(bad) != 0ull && lane_id() == 0) atomicOr(a.flag, 1u);
+}
+
+// The node record: every row of the list, or none when an id was out of
+// range (the kernels after it then read no row and the bins are zero).
+extern "C" __global__ __launch_bounds__(64) void hbr_fixed_node(FixedBuildArgs a) {
+    if (threadIdx.x != 0) return;
+    HistNode nd{};
+    nd.seg = Seg{0u, *a.flag ? 0u : (uint32_t)a.m, 0u, 0u};
+    nd.slot = 0u;
+    *a.node = nd;
+}
+
+// int64 bins to f64 pairs in place, each by its exponent: the host's
+// ldexp((double)q, e) on the same bits.
+extern "C" __global__ __launch_bounds__(256) void hbr_fixed_finish(FixedBuildArgs a) {
+    const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= a.total_bins) return;
+    const QBin q = a.bins[b];
+    const int eg = a.scale->exp_g, eh = a.scale->exp_h;
+    a.out[2 * (size_t)b] = ldexp((double)q.g, eg);
+    a.out[2 * (size_t)b + 1] = ldexp((double)q.h, eh);
+}
+
 // sibling = parent - built (exact in integers), in the parent's slot.
 extern "C" __global__ __launch_bounds__(256) void hbr_subtract(SubArgs a) {
     const uint32_t s = blockIdx.y;

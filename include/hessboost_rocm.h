@@ -152,6 +152,22 @@ int hbr_prepare(hbr_engine *e, const float *gpair, uint64_t n);
  * sum of its rows' fixed-point gradients, converted to f64. */
 int hbr_build(hbr_engine *e, const uint32_t *rows, uint64_t m, double *out);
 
+/* No counterpart in the reference: hbr_build for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). rows (m ids, device memory) and
+ * out (2 * total_bins f64, device memory) are the caller's; the tile plan,
+ * the tiles' partial sums, the node record and a row-check word live in one
+ * fixed scratch array of the library per device (32 MiB + 128 KiB, held
+ * from the first call on a device until the process ends), so the call
+ * allocates nothing and returns with out complete. Bins equal hbr_build's
+ * for the same rows bit for bit. HBR_INVALID when a row id is at or beyond
+ * the index's rows (out then holds zeros), when m >= 2^32 - 1, or when one
+ * row tile's partial sums exceed the scratch (more than 8,192 features of a
+ * dense u8 index, or more than 2,097,152 bins of a CSR index). Every call
+ * on one GPU shares that GPU's scratch: calls that overlap on one GPU (two
+ * engines on it used from two threads) race. */
+int hbr_build_device_noalloc(hbr_engine *e, const uint32_t *rows, uint64_t m, double *out);
+
 /* A node's rows on the device (the reference's Segment, src/tree/hist/mod.rs:107-164):
  * issued by the engine, stamped with its tree. */
 typedef struct hbr_segment {
