@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(LIB_DIR, "libhbrocm.so")
 CODE_OBJECT = os.path.join(LIB_DIR, "hbrocm_gfx950.hsaco")
 
 OK, REFUSED, DEVICE_ERROR, INVALID = 0, 1, 2, 3
+SUMS_EXACT, SUMS_FIXED_POINT = 0, 1
 LOSS_SQUARED_ERROR, LOSS_LOGISTIC, LOSS_SOFTMAX = 0, 1, 2
 OBJ_SQUARED_ERROR, OBJ_LOGISTIC, OBJ_SOFTMAX, OBJ_LOGITRAW = 0, 1, 2, 3
 GROW_DEPTHWISE, GROW_LOSSGUIDE = 0, 1
@@ -130,6 +131,7 @@ SIGNATURES = {
     "hbr_engine_index_read": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                         C.c_void_p]),
     "hbr_prepare": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
+    "hbr_engine_set_sums": (C.c_int, [C.c_void_p, C.c_int]),
     "hbr_build": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "hbr_build_device_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "hbr_begin_tree": (C.c_int, [C.c_void_p, C.c_uint64, P(Segment)]),

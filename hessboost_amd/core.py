@@ -212,6 +212,14 @@ class Engine:
         except Exception:
             pass
 
+    def set_sums(self, mode):
+        """"exact" (the default): build / histograms / root_total / the
+        resident scan refuse outside the exact domain, where they could not
+        equal the CPU's f64 sums (src/backend/exact_sum.rs:14-37);
+        "fixed_point": they return the engine's fixed-point sums anyway."""
+        code = {"exact": A.SUMS_EXACT, "fixed_point": A.SUMS_FIXED_POINT}[mode]
+        A.check(A.lib().hbr_engine_set_sums(self._h, code))
+
     def prepare(self, gpair):
         gpair = np.ascontiguousarray(gpair, np.float32).reshape(-1)
         A.check(A.lib().hbr_prepare(self._h, A.ptr(gpair), len(gpair) // 2))

@@ -43,7 +43,7 @@ struct QScale {
     uint32_t max_h_bits;
     uint32_t nonfinite;   // count of rows with a non-finite g or h
     uint32_t scalar_rows; // rows listed for the scalar sigmoid (until hbr_finish_scale)
-    uint32_t pad[2];
+    uint32_t pad[2];      // hbr_grain_fold: 1024 - (grain + 150) of g and of h (0: all zero)
 };
 
 // A node's rows: `len` row ids at `offset` of row buffer `buf` (0 or 1).

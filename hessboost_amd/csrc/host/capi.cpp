@@ -109,6 +109,18 @@ void dequant_hist(const Engine &e, const std::vector<QBin> &q, double *out) {
     }
 }
 
+// The trait's promise (src/tree/hist/mod.rs:205-207, :220-224): histograms
+// and root totals equal the CPU's f64 sums bit for bit. The engine keeps it
+// by refusing (the trait's None: the host sums itself, as the CUDA backend
+// does outside its exact domain, src/backend/cuda/mod.rs:2758-2776) unless
+// every sum of `m` staged pairs is exact, or the caller has chosen
+// fixed-point sums (hbr_engine_set_sums).
+void require_exact(const Engine &e, uint64_t m, const char *what) {
+    if (e.exact_sums_only && !e.sums_exact(m))
+        fail(kRefused, std::string(what) + ": the staged gradients are outside the exact domain, where fixed-point "
+                                           "sums can differ from the CPU's f64 sums (hbr_engine_set_sums selects them)");
+}
+
 std::string stats_string(Device &d) {
     std::string s;
     for (auto &kv : d.kernel_stats()) {
@@ -297,6 +309,7 @@ int hbr_prepare(hbr_engine *h, const float *gpair, uint64_t n) {
 int hbr_build(hbr_engine *h, const uint32_t *rows, uint64_t m, double *out) {
     return with_engine(h, [&](Engine &e) {
         if (!out || (!rows && m)) fail(kInvalid, "build: null argument");
+        require_exact(e, m, "build");
         dequant_hist(e, e.build_rows(rows, m), out);
     });
 }
@@ -304,6 +317,7 @@ int hbr_build(hbr_engine *h, const uint32_t *rows, uint64_t m, double *out) {
 int hbr_build_device_noalloc(hbr_engine *h, const uint32_t *rows, uint64_t m, double *out) {
     return with_engine(h, [&](Engine &e) {
         if (!out || (!rows && m)) fail(kInvalid, "build: null argument");
+        require_exact(e, m, "build");
         uint64_t bytes = 0;
         uint8_t *scratch = fixed_scratch(e.dev().ordinal(), &bytes);
         if (!e.build_rows_fixed(rows, m, out, scratch, bytes)) fail(kInvalid, "build: a row beyond the index");
@@ -321,7 +335,9 @@ int hbr_begin_tree(hbr_engine *h, uint64_t n_rows, hbr_segment *root) {
 
 int hbr_root_total_fixed(hbr_engine *h, const hbr_segment *seg, double out[2], int64_t fixed[2]) {
     return with_engine(h, [&](Engine &e) {
-        const QBin t = e.root_total(seg_of(e, *seg));
+        const Segment sg = seg_of(e, *seg);
+        require_exact(e, sg.len, "root_total");
+        const QBin t = e.root_total(sg);
         out[0] = std::ldexp((double)t.g, e.scale().exp_g);
         out[1] = std::ldexp((double)t.h, e.scale().exp_h);
         if (fixed) {
@@ -359,8 +375,9 @@ int hbr_histograms(hbr_engine *h, const hbr_segment *segs, uint64_t n, double *o
         std::vector<uint32_t> slots;
         for (uint64_t i = 0; i < n; i++) {
             ss.push_back(seg_of(e, segs[i]));
-            slots.push_back(e.alloc_slot());
+            require_exact(e, ss.back().len, "histograms");
         }
+        for (uint64_t i = 0; i < n; i++) slots.push_back(e.alloc_slot());
         e.build_nodes(ss, slots);
         for (uint64_t i = 0; i < n; i++) {
             dequant_hist(e, e.read_slot(slots[i]), out + i * 2 * (uint64_t)e.total_bins());
@@ -476,6 +493,7 @@ int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_r
                       hbr_node_scan *out) {
     return with_engine(h, [&](Engine &e) {
         if (!reg || (!req && n)) fail(kInvalid, "scan: null argument");
+        require_exact(e, e.n_rows(), "scan_resident");
         std::vector<int8_t> dirs;
         if (n && req[0].directions) {
             dirs.assign(e.n_cols(), 0);
@@ -528,7 +546,17 @@ int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_r
 }
 
 int hbr_read_hist(hbr_engine *h, uint32_t slot, double *out) {
-    return with_engine(h, [&](Engine &e) { dequant_hist(e, e.read_slot(slot), out); });
+    return with_engine(h, [&](Engine &e) {
+        require_exact(e, e.n_rows(), "read_hist");
+        dequant_hist(e, e.read_slot(slot), out);
+    });
+}
+
+int hbr_engine_set_sums(hbr_engine *h, int mode) {
+    return with_engine(h, [&](Engine &e) {
+        if (mode != HBR_SUMS_EXACT && mode != HBR_SUMS_FIXED_POINT) fail(kInvalid, "set_sums: unknown mode");
+        e.exact_sums_only = mode == HBR_SUMS_EXACT;
+    });
 }
 
 int hbr_engine_counters_read(hbr_engine *h, hbr_engine_counters *out) {

@@ -398,6 +398,34 @@ void Engine::read_gradients(float *out, uint64_t n) {
 double Engine::unit_g() const { return std::ldexp(1.0, scale_host_.exp_g); }
 double Engine::unit_h() const { return std::ldexp(1.0, scale_host_.exp_h); }
 
+// backend/exact_sum.rs:244-254: the exponent of v's lowest set bit, as
+// the code hbr_grain_fold folds (1024 - (grain + 150); 0 for zero).
+static uint32_t grain_code(float v) {
+    uint32_t bits;
+    std::memcpy(&bits, &v, 4);
+    const uint32_t biased = (bits >> 23) & 0xffu, mant = bits & 0x7fffffu;
+    if (biased == 0xffu || (biased == 0u && mant == 0u)) return 0u;
+    const uint32_t sig = biased == 0u ? mant : (mant | 0x800000u);
+    const int32_t grain = (biased == 0u ? -149 : (int32_t)biased - 150) + __builtin_ctz(sig);
+    return (uint32_t)(1024 - (grain + 150));
+}
+
+bool Engine::sums_exact(uint64_t m) const {
+    if (!grains_known_ || scale_host_.nonfinite) return false;
+    auto one = [&](uint32_t max_bits, uint32_t code, int32_t exp) {
+        if (code == 0) return true;  // every value zero
+        const int32_t grain = (int32_t)(1024 - code) - 150;
+        if (grain < exp) return false;  // values below the fixed-point unit
+        float mx;
+        std::memcpy(&mx, &max_bits, 4);
+        const double units = std::ldexp((double)mx, -grain);  // an exact integer
+        const double limit = 9007199254740992.0;             // 2^53
+        return units <= limit && (unsigned __int128)m * (unsigned __int128)(uint64_t)units <= (unsigned __int128)(1ull << 53);
+    };
+    return one(scale_host_.max_g_bits, scale_host_.pad[0], scale_host_.exp_g) &&
+           one(scale_host_.max_h_bits, scale_host_.pad[1], scale_host_.exp_h);
+}
+
 void Engine::prepare(const float *gpair, uint64_t n) {
     if (n != n_rows_) fail(kInvalid, "prepare: one gradient pair per row");
     active_pairs_ = nullptr;
@@ -413,10 +441,13 @@ void Engine::prepare(const float *gpair, uint64_t n) {
         }
         q.max_g_bits = std::max(q.max_g_bits, abs_bits(g));
         q.max_h_bits = std::max(q.max_h_bits, abs_bits(h));
+        q.pad[0] = std::max(q.pad[0], grain_code(g));
+        q.pad[1] = std::max(q.pad[1], grain_code(h));
     }
     q.exp_g = exp_for(q.max_g_bits, n_rows_);
     q.exp_h = exp_for(q.max_h_bits, n_rows_);
     scale_host_ = q;
+    grains_known_ = true;
     scale_checked_ = true;
     HBR_HIP(hipMemcpyAsync(scale_dev(), &scale_host_, sizeof(QScale), hipMemcpyHostToDevice, dev_.stream()));
     dev_.sync();
@@ -459,6 +490,7 @@ void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     if (!labels_loaded_) fail(kInvalid, "gradients: no labels since load_margins");
     if (outputs_ != 1 || output != 0) fail(kRefused, "device gradients run for one output");
     hipStream_t s = dev_.stream();
+    grains_known_ = false;
     active_pairs_ = nullptr;
     class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
@@ -483,13 +515,20 @@ bool Engine::check_scale(QScale host) {
 
 bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
     launch_gradients(loss, output);
+    {  // the grains of the pairs, for the exact-domain check of later sums
+        const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)),
+                                                   (uint32_t)dev_.cu_count() * 8);
+        dev_.launch("hbr_grain_fold", dim3(blocks), dim3(kThreads), grad_args(loss));
+    }
     QScale *q = static_cast<QScale *>(stage_.alloc(sizeof(QScale)));
     HBR_HIP(hipMemcpyAsync(q, scale_dev(), sizeof(QScale), hipMemcpyDeviceToHost, dev_.stream()));
     dev_.sync();
     const QScale host = *q;
     stage_.reset();
     scale_checked_ = true;
-    return check_scale(host);
+    const bool ok = check_scale(host);
+    grains_known_ = true;
+    return ok;
 }
 
 void Engine::compute_gradients_async(const hbr_device_loss &loss, uint32_t output) {
@@ -517,6 +556,7 @@ void Engine::softmax_gradients_async(float min_hess) {
     if (n_rows_ == 0) fail(kInvalid, "softmax gradients: no rows");
     hipStream_t s = dev_.stream();
     active_pairs_ = nullptr;
+    grains_known_ = false;
     class_pairs_.reserve((size_t)k * n_rows_);
     class_scales_.reserve(k);
     class_outputs_ = k;
@@ -543,6 +583,7 @@ void Engine::select_class(uint32_t c) {
     SelectArgs a{class_scales_.get() + c, scale_dev(), n_rows_};
     dev_.launch("hbr_scale_select", dim3(1), dim3(64), a);
     active_pairs_ = class_pairs_.get() + (size_t)c * n_rows_;
+    grains_known_ = false;
     scale_checked_ = false;  // the tree's root or finish reads the class's scale back
 }
 
@@ -1352,6 +1393,7 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     }
     if (outputs_ != 1 || !labels_loaded_) fail(kInvalid, "walk: gradients need one output and labels");
     active_pairs_ = nullptr;
+    grains_known_ = false;
     class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
     if (!poison_.size()) {
@@ -1553,6 +1595,7 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
         if (!can_walk_gradients(n)) fail(kInvalid, "walk_add: gradients need the staged walk of one output");
         active_pairs_ = nullptr;
         class_outputs_ = 0;
+        grains_known_ = false;
         gpair_.resize(n_rows_ ? n_rows_ : 1);
         HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
         WalkGradArgs wg{};

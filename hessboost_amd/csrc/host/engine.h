@@ -120,6 +120,16 @@ public:
     void read_margins(float *out, uint64_t n);
     void read_gradients(float *out, uint64_t n);
     const QScale &scale() const { return scale_host_; }
+    // Whether every sum of at most m staged pairs, in any order, is the
+    // reference's f64 sum bit for bit (backend/exact_sum.rs:14-37): every
+    // value finite, n x max <= 2^53 grains of each component, and the
+    // fixed-point unit at or below the grain (the quantisation is then
+    // lossless). False when the staged pairs' grains are not known (the
+    // trainer's fused rounds, softmax classes).
+    bool sums_exact(uint64_t m) const;
+    // The trait's contract for build / histograms / root_total / the
+    // resident scan: when set, they refuse outside the exact domain.
+    bool exact_sums_only = true;
     double unit_g() const;
     double unit_h() const;
 
@@ -371,6 +381,7 @@ private:
     DBuf<PartSplit> g_splits_[2];
     DBuf<PartOut> g_pout_[2];
     QScale scale_host_{};
+    bool grains_known_ = false;  // scale_host_.pad holds the staged pairs' grain codes
     DBuf<uint32_t> scalar_list_;  // rows the fused walk defers to hbr_finish_scale
     DBuf<uint32_t> rows_[2];
     DBuf<uint32_t> host_rows_;

@@ -151,6 +151,37 @@ extern "C" __global__ __launch_bounds__(256) void hbr_gradients(GradArgs a) {
     fold_block(a.scale, mg, mh, bad);
 }
 
+// The exact domain's grains (backend/exact_sum.rs:244-254): for every
+// finite nonzero g and h, the exponent of its lowest set bit; the smallest
+// over the rows lands in scale->pad[0] (g) and pad[1] (h) as 1024 - (grain
+// + 150), folded by maximum (0: every value zero; the memset leaves 0).
+__device__ __forceinline__ uint32_t grain_fold_code(float v) {
+    const uint32_t bits = __float_as_uint(v);
+    const uint32_t biased = (bits >> 23) & 0xffu, mant = bits & 0x7fffffu;
+    if (biased == 0xffu || (biased == 0u && mant == 0u)) return 0u;  // non-finite (counted elsewhere) or zero
+    const uint32_t sig = biased == 0u ? mant : (mant | 0x800000u);
+    const int32_t grain = (biased == 0u ? -149 : (int32_t)biased - 150) + (int32_t)__builtin_ctz(sig);
+    return (uint32_t)(1024 - (grain + 150));
+}
+
+extern "C" __global__ __launch_bounds__(256) void hbr_grain_fold(GradArgs a) {
+    uint32_t cg = 0, ch = 0;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += gridDim.x * blockDim.x) {
+        const GPair p = a.gpair[i];
+        cg = max(cg, grain_fold_code(p.g));
+        ch = max(ch, grain_fold_code(p.h));
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        cg = max(cg, (uint32_t)__shfl_xor((int)cg, d, kWave));
+        ch = max(ch, (uint32_t)__shfl_xor((int)ch, d, kWave));
+    }
+    if (lane_id() == 0) {
+        if (cg) atomicMax(&a.scale->pad[0], cg);
+        if (ch) atomicMax(&a.scale->pad[1], ch);
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void hbr_iota(IotaArgs a) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < a.n) a.rows[i] = a.first + i;

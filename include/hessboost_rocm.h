@@ -142,6 +142,29 @@ int hbr_engine_index_info(hbr_engine *e, hbr_index_info *out);
 int hbr_engine_index_read(hbr_engine *e, uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint64_t *row_ptr,
                           uint32_t *gbins);
 
+/* The sums hbr_build, hbr_build_device_noalloc, hbr_histograms,
+ * hbr_root_total[_fixed], hbr_scan_resident and hbr_read_hist return.
+ * The trait promises the CPU's f64 bits (src/tree/hist/mod.rs:205-207,
+ * :220-224). The engine sums the staged pairs in fixed point: integers in a
+ * per-tree unit of 2^e, exact and order-free. Inside the reference's exact
+ * domain (src/backend/exact_sum.rs:14-37: every pair finite, n x max <=
+ * 2^53 grains of its component, with the unit at or below the grain) those
+ * sums are the CPU's f64 sums bit for bit, in any order. Outside it they
+ * differ from the CPU's row-order f64 chain by that chain's own rounding
+ * (relative error about n x 2^-53).
+ *   HBR_SUMS_EXACT (the default): those calls return HBR_REFUSED outside
+ *     the exact domain, as the CUDA backend refuses or falls back there
+ *     (src/backend/cuda/mod.rs:2758-2776); the caller sums on the host.
+ *   HBR_SUMS_FIXED_POINT: they return the fixed-point sums everywhere (a
+ *     tolerance of the chain's rounding; split choices can differ from the
+ *     CPU's on near-ties).
+ * The exact domain is known for pairs staged by hbr_prepare and by
+ * hbr_gradients; after other staging (softmax classes, the trainer's
+ * rounds) it is treated as not exact. */
+#define HBR_SUMS_EXACT 0
+#define HBR_SUMS_FIXED_POINT 1
+int hbr_engine_set_sums(hbr_engine *e, int mode);
+
 /* HistogramBackend::prepare (src/tree/hist/mod.rs:96): stage a tree's
  * gradient pairs (interleaved g, h f32; one per index row). */
 int hbr_prepare(hbr_engine *e, const float *gpair, uint64_t n);

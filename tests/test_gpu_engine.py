@@ -74,9 +74,14 @@ def test_histogram_general_gradients_match_integer_sums_and_oracle():
     ref = O.Dataset(x)
     gp = np.stack([rng.standard_normal(n, dtype=np.float32),
                    rng.random(n, dtype=np.float32) * np.float32(0.25) + np.float32(1e-3)], 1).astype(np.float32)
+    gp[3, 0] = np.float32(1e-30)  # a grain of about 2^-123: far outside the exact domain
     eng.prepare(gp)
     eg, eh = quant_exp(gp[:, 0], n), quant_exp(gp[:, 1], n)
-    rows = np.sort(rng.choice(n, 12_345, replace=False))
+    rows = np.sort(np.concatenate([[3], rng.choice(np.arange(4, n), 12_344, replace=False)]))
+    with pytest.raises(A.HbrError) as refused:  # the trait's contract: no f64-equal sums here
+        eng.build(rows)
+    assert refused.value.status == A.REFUSED
+    eng.set_sums("fixed_point")
     got = eng.build(rows)
     assert np.array_equal(got, integer_histogram(dense_rows(ix), rows, gp, eng.total_bins, eg, eh))
     want = ref.build_hist(rows, gp)
@@ -105,11 +110,56 @@ def test_histogram_is_independent_of_row_order_and_tiles():
     ix, eng = make(x)
     gp = np.stack([rng.standard_normal(n, dtype=np.float32), rng.random(n, dtype=np.float32)], 1)
     eng.prepare(gp)
+    eng.set_sums("fixed_point")
     rows = np.sort(rng.choice(n, 30_000, replace=False))
     a = eng.build(rows)
     b = eng.build(rows[::-1].copy())
     c = eng.build(np.concatenate([rows[1::2], rows[::2]]))
     assert np.array_equal(a, b) and np.array_equal(a, c)
+
+
+def test_exact_contract_refuses_outside_the_exact_domain():
+    """The trait promises the CPU's f64 bits (src/tree/hist/mod.rs:205-207,
+    :220-224). Gradients of grain 2^-20 with largest magnitude 2^23 are
+    2^43 grains each: a node of 1,024 rows is inside the exact domain
+    (backend/exact_sum.rs:14-37: n x max <= 2^53 grains) and its bins equal
+    the oracle's f64 sums bit for bit; 1,025 rows are outside, and build,
+    histograms and root_total refuse (HBR_REFUSED, the trait's None) until
+    fixed-point sums are chosen. Device gradients are folded the same way:
+    logistic pairs over margins in [-20, 20] hold Hessians near 2e-9 beside
+    0.25 (about 2^51 grains each) and refuse; squared error over quarter
+    margins and eighth labels is exact."""
+    rng = np.random.default_rng(9)
+    n = 2_000
+    x = rng.standard_normal((n, 6), dtype=np.float32)
+    ix, eng = make(x)
+    ref = O.Dataset(x)
+    g = (rng.integers(-4, 5, n).astype(np.float32) * np.float32(2.0 ** -20))
+    g[7] = np.float32(2.0 ** 23)
+    g[1500] = np.float32(-(2.0 ** 23))
+    gp = np.stack([g, np.ones(n, np.float32)], 1).astype(np.float32)
+    eng.prepare(gp)
+    inside = np.arange(1_024, dtype=np.uint32)
+    assert np.array_equal(eng.build(inside), ref.build_hist(inside, gp))
+    outside = np.arange(1_025, dtype=np.uint32)
+    for call in (lambda: eng.build(outside), lambda: eng.root_total(eng.begin_tree())):
+        with pytest.raises(A.HbrError) as refused:
+            call()
+        assert refused.value.status == A.REFUSED
+    eng.set_sums("fixed_point")
+    assert np.array_equal(eng.build(outside), ref.build_hist(outside, gp))  # sums that happen to be exact
+    eng.set_sums("exact")
+    # device gradients
+    y = (rng.random(n) < 0.5).astype(np.float32)
+    eng.load_margins(np.linspace(-20, 20, n).astype(np.float32))
+    assert eng.gradients(A.LOSS_LOGISTIC, y)
+    with pytest.raises(A.HbrError) as refused:
+        eng.build(inside)
+    assert refused.value.status == A.REFUSED
+    eng.load_margins((rng.integers(-8, 8, n) / 4.0).astype(np.float32))
+    assert eng.gradients(A.LOSS_SQUARED_ERROR, (rng.integers(-8, 8, n) / 8.0).astype(np.float32))
+    gp2 = eng.read_gradients()
+    assert np.array_equal(eng.build(inside), ref.build_hist(inside, gp2.astype(np.float32)))
 
 
 def test_partition_matches_oracle_routing():
