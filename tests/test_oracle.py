@@ -497,3 +497,106 @@ def test_softmax_underflowing_rows_are_nan_bit_for_bit():
                     assert np.array_equal(full[r].view(np.uint32), scal[r].view(np.uint32))
                 else:
                     _close_pairs(full[r], scal[r])
+
+
+# ---- loss-guided growth: expansion order and node numbering ----------------------------
+
+def _canon(nodes, i=0):
+    """A tree up to node numbering: splits (feature, threshold bits, default
+    direction) and leaf values, recursively."""
+    nd = nodes[i]
+    if nd["left"] == -1:
+        return ("leaf", np.float32(nd["leaf_value"]).view(np.uint32).item())
+    return ("split", nd["split_feature"], np.float32(nd["split_cond"]).view(np.uint32).item(),
+            bool(nd["default_left"]), _canon(nodes, nd["left"]), _canon(nodes, nd["right"]))
+
+
+def _lossguide_data(seed, n=3_000, f=5):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    x[rng.random((n, f)) < 0.05] = np.nan
+    z = np.nan_to_num(x)
+    y = (1.5 * z[:, 0] - z[:, 1] ** 2 + np.sin(2 * z[:, 2]) + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    gp = np.stack([-y, np.ones(n, np.float32)], 1).astype(np.float32)  # squared error at zero margins
+    return O.Dataset(x, max_bin=64), gp
+
+
+@pytest.mark.parametrize("seed,depth", [(0, 3), (1, 4), (2, 5)])
+def test_lossguide_with_room_for_every_leaf_is_the_depthwise_tree(seed, depth):
+    """With max_leaves >= 2^depth, loss-guided growth expands every
+    expandable node (builder/hist/mod.rs:505-573), so it grows the depthwise
+    tree (:459-503) up to node numbering; with max_leaves = 2 it grows the
+    depth-1 stump."""
+    ds, gp = _lossguide_data(seed)
+    dw, _ = ds.grow_tree(gp, O.params(max_depth=depth, eta=0.3, max_bin=64))
+    lg, _ = ds.grow_tree(gp, O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=depth, max_leaves=1 << depth,
+                                      eta=0.3, max_bin=64))
+    assert _canon(lg) == _canon(dw)
+    stump, _ = ds.grow_tree(gp, O.params(max_depth=1, eta=0.3, max_bin=64))
+    two, _ = ds.grow_tree(gp, O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=0, max_leaves=2, eta=0.3,
+                                       max_bin=64))
+    assert _canon(two) == _canon(stump) and len(two) == 3
+
+
+def _best_first(dw, max_leaves):
+    """Brute-force best-first growth over the depthwise tree's own splits:
+    the frontier node of largest split gain among those the depthwise tree
+    split is expanded next, its children numbered next (left, then right),
+    until max_leaves leaves. Returns (new node -> depthwise node, children)."""
+    of = [0]
+    kids = {}
+    frontier = [0]
+    leaves = 1
+    while leaves < max_leaves:
+        cand = [v for v in frontier if dw[of[v]]["left"] != -1]
+        if not cand:
+            break
+        gains = [dw[of[v]]["split_gain"] for v in cand]
+        best = int(np.argmax(gains))
+        assert gains.count(gains[best]) == 1, "tied gains: the check needs distinct ones"
+        v = cand[best]
+        frontier.remove(v)
+        left = len(of)
+        of += [dw[of[v]]["left"], dw[of[v]]["right"]]
+        kids[v] = (left, left + 1)
+        frontier += [left, left + 1]
+        leaves += 1
+    return of, kids
+
+
+@pytest.mark.parametrize("seed,depth,leaves", [(3, 6, 9), (4, 7, 23), (5, 5, 14), (6, 8, 40)])
+def test_lossguide_expands_in_gain_order_and_numbers_children_next(seed, depth, leaves):
+    """The loss-guided tree equals a brute-force best-first expansion of the
+    depthwise tree's splits (a node's best split does not depend on when it
+    is expanded): node for node, including the ids, which the reference
+    assigns in expansion order (max-heap on loss_chg, hist/mod.rs:132-149)."""
+    ds, gp = _lossguide_data(seed)
+    dw, _ = ds.grow_tree(gp, O.params(max_depth=depth, eta=0.3, max_bin=64))
+    lg, _ = ds.grow_tree(gp, O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=depth, max_leaves=leaves, eta=0.3,
+                                      max_bin=64))
+    of, kids = _best_first(dw, leaves)
+    assert len(lg) == len(of)
+    for v, d in enumerate(of):
+        a, b = lg[v], dw[d]
+        assert np.float32(a["sum_hess"]) == np.float32(b["sum_hess"]), v
+        if v in kids:
+            assert (a["left"], a["right"]) == kids[v], v
+            assert a["split_feature"] == b["split_feature"] and a["default_left"] == b["default_left"], v
+            assert np.float32(a["split_cond"]).view(np.uint32) == np.float32(b["split_cond"]).view(np.uint32), v
+            assert np.float32(a["split_gain"]) == np.float32(b["split_gain"]), v
+        else:
+            assert a["left"] == -1, v
+            if b["left"] == -1:
+                assert np.float32(a["leaf_value"]) == np.float32(b["leaf_value"]), v
+
+
+def test_lossguide_respects_max_leaves():
+    """builder/hist/mod.rs:1322-1343: 64 rows of alternating gradients on
+    one feature, max_leaves 4, unlimited depth, no regularisation."""
+    x = np.arange(64, dtype=np.float32).reshape(-1, 1)
+    g = np.where(np.arange(64) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    gp = np.stack([g, np.ones(64, np.float32)], 1)
+    ds = O.Dataset(x, max_bin=256)
+    t, _ = ds.grow_tree(gp, O.params(grow_policy=O.GROW_LOSSGUIDE, max_leaves=4, max_depth=0, min_child_weight=0.0,
+                                     gamma=0.0, reg_lambda=0.0))
+    assert sum(nd["left"] == -1 for nd in t) <= 4
