@@ -593,6 +593,57 @@ class Booster:
                    linear=None, shrinkage=None, boulevard=None, ebm=None)
         return json.dumps(doc)
 
+    def save_raw(self, format="binary"):
+        """The model's bytes (python/python/hessboost/_booster.py save_raw):
+        "binary", the reference's native container as one zstd frame
+        (src/model/native.rs; an uncompressed container where no libzstd
+        is present, which the reference reads as well), or "json", its
+        JSON document."""
+        if format == "json":
+            return self.save_model_json().encode()
+        if format != "binary":
+            raise ValueError(f"unsupported model format {format!r}")
+        from . import native_model
+        try:
+            return native_model.encode(self)
+        except native_model.ModelFormatError:
+            return native_model.encode(self, compress=False)
+
+    def save_model(self, fname, *, format=None):
+        """Write the model to fname: JSON for a .json name, else the native
+        binary format (_booster.py:912-921)."""
+        if format is None:
+            format = "json" if str(fname).endswith(".json") else "binary"
+        with open(fname, "wb") as f:
+            f.write(self.save_raw(format))
+
+    def load_model(self, fname, *, format=None):
+        """Replace the model with one read from a path or bytes, in the
+        format its content has (native binary, zstd or not, or JSON), as
+        _booster.py:923-940 does for these two formats."""
+        from . import native_model
+        data = bytes(fname) if isinstance(fname, (bytes, bytearray, memoryview)) else open(fname, "rb").read()
+        if format is None:
+            format = "binary" if native_model.is_native(data) else "json"
+        if format == "binary":
+            fields = native_model.decode(data)
+        elif format == "json":
+            other = type(self).load_model_json(data.decode())
+            fields = {k: getattr(other, k) for k in ("objective", "base_score", "trees", "n_outputs", "n_features",
+                                                     "tree_weights", "num_class", "n_targets", "best_iteration",
+                                                     "num_parallel_tree", "objective_params")}
+        else:
+            raise ValueError(f"unsupported model format {format!r}")
+        for key, value in fields.items():
+            setattr(self, key, value)
+        self._forest, self._forest_ordinal = None, -1
+        return self
+
+    @classmethod
+    def from_bytes(cls, data):
+        """A Booster read from a native or JSON model's bytes."""
+        return cls(objective="reg:squarederror", base_score=np.zeros(1, np.float32)).load_model(data)
+
     @classmethod
     def load_model_json(cls, text):
         """A Booster from the reference's JSON model document: scalar-leaf

@@ -15,7 +15,8 @@ It also copies, minified, the 0.4.9 JSON model documents themselves into
 tests/golden/models/ (the JSON model format, model/serde.rs): the saved
 models of the cases above, which the JSON reader and writer must reproduce,
 and two whose features this path does not carry (a linear booster, vector
-leaves), which the reader must refuse.
+leaves), which the reader must refuse; and the native binary files
+(<case>.bin, src/model/native.rs) of every version into tests/golden/native/.
 
 Run once in a checkout that has the reference under /root/reference:
     python tests/golden/make_fixtures.py
@@ -82,6 +83,20 @@ def main():
         doc = json.load(open(os.path.join(REF, "0.4.9", case + ".json")))
         json.dump(doc, open(os.path.join(models, case + ".json"), "w"), separators=(",", ":"))
     print(f"copied {len(CASES) + 2} JSON models to {models}")
+    # the native binary files of every version, as the reference saved them
+    # (zstd frames of the HBM container, src/model/native.rs), for the
+    # native reader and writer
+    native = os.path.join(os.path.dirname(OUT), "native")
+    copied = 0
+    for ver in sorted(os.listdir(REF)):
+        os.makedirs(os.path.join(native, ver), exist_ok=True)
+        for case in CASES + ["gblinear", "vector_leaves"]:
+            src = os.path.join(REF, ver, case + ".bin")
+            if os.path.exists(src):
+                with open(src, "rb") as f, open(os.path.join(native, ver, case + ".bin"), "wb") as g:
+                    g.write(f.read())
+                copied += 1
+    print(f"copied {copied} native model files to {native}")
 
 
 if __name__ == "__main__":

@@ -44,6 +44,39 @@ def test_reference_json_models_predict_recorded_margins(name):
     assert np.array_equal(np.asarray(got, np.float32).reshape(-1).view(np.uint32), want)
 
 
+@pytest.mark.parametrize("ver", ["0.2.0", "0.4.3", "0.4.9"])
+def test_reference_native_models_predict_recorded_margins(ver):
+    """The reference's saved native binary files (zstd frames of the HBM
+    container, tests/golden/native) load with Booster.load_model and
+    predict the recorded f32 margins bit for bit on the GPU."""
+    import os
+    for name in CASES:
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "native", ver, name + ".bin")
+        b = hb.Booster(objective="reg:squarederror", base_score=np.zeros(1, np.float32)).load_model(path)
+        got = b.predict(rows_for(name), output_margin=True)
+        want = np.array(load_saved_models()[f"{ver}/{name}"]["margins"], np.uint32)
+        assert np.array_equal(np.asarray(got, np.float32).reshape(-1).view(np.uint32), want), name
+
+
+def test_trained_model_survives_native_round_trip(tmp_path):
+    """A trained model written in the native binary format and read back
+    predicts the same margins bit for bit; its container re-saves byte for
+    byte."""
+    from hessboost_amd import native_model as N
+    x = synthetic.predict_rows(n=5_000, f=9, seed=13)
+    y = (np.nan_to_num(x[:, 0]) > 0).astype(np.float32)
+    for params in ({"objective": "binary:logistic", "max_depth": 5, "scale_pos_weight": 2.0},
+                   {"objective": "reg:squarederror", "grow_policy": "lossguide", "max_depth": 0, "max_leaves": 12}):
+        model = hb.train(params, hb.DMatrix(x, label=y), 4)
+        model.save_model(tmp_path / "m.bin")
+        back = hb.Booster(objective="reg:squarederror", base_score=np.zeros(1, np.float32)).load_model(
+            tmp_path / "m.bin")
+        assert N.container(back) == N.container(model)
+        a = model.predict(x, output_margin=True)
+        c = back.predict(x, output_margin=True)
+        assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(c).view(np.uint32)), params
+
+
 def test_categorical_casts_saturate_and_missing_follows_default():
     """src/backend/cuda/predict.rs:702-724: the set {0, 2, u32::MAX}; rows
     -2.5, -0.0, 0.8, 1.9, 2.9, 2^32 and NaN, on the GPU as in the oracle,
