@@ -11,7 +11,10 @@
  * builder/mod.rs:143-193 (expand with f32 child weights and covers,
  * split_gain, child_bounds); builder/shared.rs:174-187 (finalize_leaf_values
  * with calc_weight_bounded); tree/regtree.rs:599-601 (scale_leaves);
- * training/round.rs:422-424 (tree_eta = eta as f32).
+ * training/round.rs:422-424 (tree_eta = eta as f32); categorical splits
+ * (builder/mod.rs:105-120, :175-182: the set recorded as the left child,
+ * its codes sorted into the tree's category pool; quantile.rs:316-333 and
+ * partition.rs:146-160: rows routed by their bin's code).
  */
 #include "oracle.h"
 
@@ -129,16 +132,52 @@ typedef struct pending_t {
     int terminal;
 } pending_t;
 
+/* A category code: the saturating `cut as u32` (in_category_set). */
+static uint32_t category_code(float v) {
+    if (!(v >= 0.0f)) return 0;
+    if (v >= 4294967296.0f) return 0xffffffffu;
+    return (uint32_t)v;
+}
+
+static int cmp_u32(const void *a, const void *b) {
+    uint32_t x = *(const uint32_t *)a, y = *(const uint32_t *)b;
+    return (x > y) - (x < y);
+}
+
+/* The categories of a categorical split's set (its local bins' codes,
+ * sorted: BestSplit's `set.sort_unstable()`), appended to the tree's pool. */
+static void record_categories(ctx_t *c, or_node *n, const or_split *b) {
+    const uint32_t fs = c->ix->cuts->feature_offset[b->feature];
+    const uint32_t nb = c->ix->cuts->feature_offset[b->feature + 1] - fs;
+    or_tree *t = c->tree;
+    n->is_categorical = 1;
+    n->cat_begin = (uint32_t)t->n_categories;
+    for (uint32_t i = 0; i < nb; i++) {
+        if (!(b->cat_left[i / 32] >> (i % 32) & 1u)) continue;
+        if (t->n_categories == t->cat_cap) {
+            t->cat_cap = t->cat_cap ? 2 * t->cat_cap : 64;
+            t->categories = (uint32_t *)realloc(t->categories, t->cat_cap * sizeof(uint32_t));
+        }
+        t->categories[t->n_categories++] = category_code(c->ix->cuts->cut_values[fs + i]);
+    }
+    n->cat_end = (uint32_t)t->n_categories;
+    qsort(t->categories + n->cat_begin, n->cat_end - n->cat_begin, sizeof(uint32_t), cmp_u32);
+}
+
 static pending_t prepare_split(ctx_t *c, entry_t *e) {
     pending_t s;
     const or_split *b = &e->best;
     int dir = dir_of(c->p, b->feature);
-    child_bounds(e->lower, e->upper, dir, b->w_left, b->w_right, &s.l_lo, &s.l_up, &s.r_lo, &s.r_up);
+    if (b->categorical) /* bounds in the orientation the split was scored in (builder/mod.rs:175-182) */
+        child_bounds(e->lower, e->upper, dir, b->w_right, b->w_left, &s.r_lo, &s.r_up, &s.l_lo, &s.l_up);
+    else
+        child_bounds(e->lower, e->upper, dir, b->w_left, b->w_right, &s.l_lo, &s.l_up, &s.r_lo, &s.r_up);
     or_node *n = &c->tree->nodes[e->nid];
-    n->split_cond = b->bin >= 0 ? c->ix->cuts->cut_values[b->bin] : -FLT_MAX;
+    n->split_cond = b->categorical ? 0.0f : (b->bin >= 0 ? c->ix->cuts->cut_values[b->bin] : -FLT_MAX);
     n->split_feature = b->feature;
     n->default_left = b->default_left;
     n->split_bin = b->bin;
+    if (b->categorical) record_categories(c, n, b);
     int64_t left_id = (int64_t)c->tree->n_nodes;
     n->left = (int32_t)left_id;
     n->right = (int32_t)(left_id + 1);
@@ -183,12 +222,43 @@ size_t or_partition(const or_index *ix, const uint32_t *rows, size_t m, uint32_t
     return nl;
 }
 
+size_t or_partition_categorical(const or_index *ix, const uint32_t *rows, size_t m, uint32_t feature,
+                                const uint32_t *cat_left, int default_left, uint32_t *out_left,
+                                uint32_t *out_right) {
+    /* categories_left (quantile.rs:316-333): a bin goes left when its code
+     * is one of the set's codes */
+    const uint32_t fs = ix->cuts->feature_offset[feature];
+    const uint32_t nb = ix->cuts->feature_offset[feature + 1] - fs;
+    uint8_t *left_bin = (uint8_t *)calloc(nb ? nb : 1, 1);
+    for (uint32_t i = 0; i < nb; i++) {
+        if (!(cat_left[i / 32] >> (i % 32) & 1u)) continue;
+        const uint32_t code = category_code(ix->cuts->cut_values[fs + i]);
+        for (uint32_t k = 0; k < nb; k++)
+            if (category_code(ix->cuts->cut_values[fs + k]) == code) left_bin[k] = 1;
+    }
+    size_t nl = 0, nr = 0;
+    for (size_t i = 0; i < m; i++) {
+        uint32_t r = rows[i];
+        int64_t gb = or_index_feature_bin(ix, r, feature);
+        int left = gb < 0 ? default_left : left_bin[gb - (int64_t)fs];
+        if (left)
+            out_left[nl++] = r;
+        else
+            out_right[nr++] = r;
+    }
+    free(left_bin);
+    return nl;
+}
+
 static void build_children(ctx_t *c, pending_t *s, entry_t *out_l, entry_t *out_r) {
     entry_t *e = &s->entry;
     const or_split *b = &e->best;
     uint32_t *lrows = (uint32_t *)malloc((e->n_rows ? e->n_rows : 1) * sizeof(uint32_t));
     uint32_t *rrows = (uint32_t *)malloc((e->n_rows ? e->n_rows : 1) * sizeof(uint32_t));
-    size_t nl = or_partition(c->ix, e->rows, e->n_rows, b->feature, b->bin, b->default_left, lrows, rrows);
+    size_t nl = b->categorical ? or_partition_categorical(c->ix, e->rows, e->n_rows, b->feature, b->cat_left,
+                                                          b->default_left, lrows, rrows)
+                               : or_partition(c->ix, e->rows, e->n_rows, b->feature, b->bin, b->default_left,
+                                              lrows, rrows);
     size_t nr = e->n_rows - nl;
     free(e->rows);
     e->rows = NULL;
@@ -408,8 +478,11 @@ or_tree *or_grow_tree(const or_index *ix, const float *gpair, const or_params *p
 void or_tree_free(or_tree *t) {
     if (!t) return;
     free(t->nodes);
+    free(t->categories);
     free(t);
 }
 
 size_t or_tree_n_nodes(const or_tree *t) { return t->n_nodes; }
+size_t or_tree_n_categories(const or_tree *t) { return t->n_categories; }
+const uint32_t *or_tree_categories(const or_tree *t) { return t->categories; }
 const or_node *or_tree_nodes(const or_tree *t) { return t->nodes; }

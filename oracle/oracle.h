@@ -57,7 +57,11 @@ typedef struct or_cuts {
     size_t n_features;
     uint32_t *feature_offset; /* n_features + 1 */
     float *cut_values;        /* feature_offset[n_features] values */
+    uint8_t *is_categorical;  /* per feature, or NULL (every feature numeric) */
 } or_cuts;
+
+/* The most bins (distinct categories) of a categorical feature. */
+#define OR_MAX_CAT_BINS 1024
 
 /* Dense f32 matrix (row-major, n x f) with `missing` marking absent cells
  * (NaN matches any NaN). weights may be NULL (unit weights). */
@@ -67,9 +71,18 @@ or_cuts *or_cuts_from_dense(const float *x, size_t n, size_t f, size_t max_bin,
 or_cuts *or_cuts_from_csr(const size_t *row_ptr, const uint32_t *col,
                           const float *val, size_t n, size_t f, size_t max_bin,
                           const float *weights);
+/* The same with per-feature types (categorical != 0: one bin per distinct
+ * present value, quantile.rs:524-672; NULL: every feature numeric). */
+or_cuts *or_cuts_from_dense_typed(const float *x, size_t n, size_t f, size_t max_bin,
+                                  const float *weights, float missing, const uint8_t *categorical);
+or_cuts *or_cuts_from_csr_typed(const size_t *row_ptr, const uint32_t *col,
+                                const float *val, size_t n, size_t f, size_t max_bin,
+                                const float *weights, const uint8_t *categorical);
 void or_cuts_free(or_cuts *c);
 size_t or_cuts_total_bins(const or_cuts *c);
-/* Global bin of value v (present) for feature f: #{cuts <= v}, clamped. */
+/* Global bin of value v (present) for feature f: #{cuts <= v}, clamped; a
+ * categorical feature's bin holding v exactly, else its first bin
+ * (quantile.rs:285-296). */
 uint32_t or_bin_of(const or_cuts *c, size_t f, float v);
 
 /* ---- binned index (GHistIndex) ------------------------------------------ */
@@ -133,6 +146,11 @@ typedef struct or_split {
     int default_left;
     double left_g, left_h, right_g, right_h;
     double w_left, w_right;
+    /* a categorical split (builder/categorical.rs:48-170): the local bins
+     * whose categories go left (the set XGBoost routes to its right child,
+     * recorded as the tree's left child); bin is then -1 */
+    int categorical;
+    uint32_t cat_left[OR_MAX_CAT_BINS / 32];
 } or_split;
 
 /* Sequential hist split search over every feature of the node. */
@@ -143,6 +161,12 @@ int or_split_valid(const or_split *s, const or_params *p);
 float or_node_gain(double g, double h, double lower, double upper, const or_params *p);
 /* tree/gain.rs:107-116 calc_weight (0 below min_child_weight). */
 double or_calc_weight(double g, double h, const or_params *p);
+/* sweep_categorical (builder/categorical.rs:48-170) of one feature's n
+ * categories (ascending codes, stats[2i], stats[2i+1] = G, H, zero for a
+ * category the node lacks) against the node total, merged into *best with
+ * the tie rule; a winning set lands in best->cat_left by position. */
+void or_sweep_categorical(const double *stats, size_t n, double total_g, double total_h, double lower,
+                          double upper, int dir, const or_params *p, uint32_t feature, or_split *best);
 
 /* ---- partition ------------------------------------------------------------ */
 /* Stable partition of rows[m] on (feature, bin, default_left). Returns the
@@ -150,6 +174,11 @@ double or_calc_weight(double g, double h, const or_params *p);
 size_t or_partition(const or_index *ix, const uint32_t *rows, size_t m,
                     uint32_t feature, int64_t bin, int default_left,
                     uint32_t *out_left, uint32_t *out_right);
+/* The same for a categorical split (partition.rs:146-160): a present row
+ * goes left when its local bin's bit is set in cat_left. */
+size_t or_partition_categorical(const or_index *ix, const uint32_t *rows, size_t m, uint32_t feature,
+                                const uint32_t *cat_left, int default_left, uint32_t *out_left,
+                                uint32_t *out_right);
 
 /* ---- trees ------------------------------------------------------------------ */
 typedef struct or_node {
@@ -161,11 +190,17 @@ typedef struct or_node {
     /* diagnostics (not part of the model format) */
     int64_t split_bin;     /* global bin, -1 BelowBins, -2 leaf */
     double stat_g, stat_h; /* node statistics the builder stored */
+    /* categorical splits: the node's categories (going left) are
+     * categories[cat_begin, cat_end) of its tree (regtree.rs:59-66) */
+    int32_t is_categorical;
+    uint32_t cat_begin, cat_end;
 } or_node;
 
 typedef struct or_tree {
     or_node *nodes;
     size_t n_nodes, cap;
+    uint32_t *categories;
+    size_t n_categories, cat_cap;
 } or_tree;
 
 /* Grow one tree over all rows of the index from gpair; leaves scaled by
@@ -175,6 +210,8 @@ or_tree *or_grow_tree(const or_index *ix, const float *gpair, const or_params *p
                       int32_t *leaf_of_row);
 void or_tree_free(or_tree *t);
 size_t or_tree_n_nodes(const or_tree *t);
+size_t or_tree_n_categories(const or_tree *t);
+const uint32_t *or_tree_categories(const or_tree *t);
 const or_node *or_tree_nodes(const or_tree *t);
 
 /* ---- objectives ------------------------------------------------------------- */

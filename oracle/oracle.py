@@ -25,7 +25,9 @@ def build() -> None:
 
 class Cuts(C.Structure):
     _fields_ = [("n_features", C.c_size_t), ("feature_offset", C.POINTER(C.c_uint32)),
-                ("cut_values", C.POINTER(C.c_float))]
+                ("cut_values", C.POINTER(C.c_float)), ("is_categorical", C.POINTER(C.c_uint8))]
+
+MAX_CAT_BINS = 1024
 
 
 class Index(C.Structure):
@@ -50,14 +52,15 @@ class Split(C.Structure):
     _fields_ = [("loss_chg", C.c_double), ("feature", C.c_uint32), ("bin", C.c_int64),
                 ("default_left", C.c_int), ("left_g", C.c_double), ("left_h", C.c_double),
                 ("right_g", C.c_double), ("right_h", C.c_double), ("w_left", C.c_double),
-                ("w_right", C.c_double)]
+                ("w_right", C.c_double), ("categorical", C.c_int), ("cat_left", C.c_uint32 * (1024 // 32))]
 
 
 class Node(C.Structure):
     _fields_ = [("split_feature", C.c_uint32), ("split_cond", C.c_float),
                 ("default_left", C.c_int32), ("left", C.c_int32), ("right", C.c_int32),
                 ("leaf_value", C.c_float), ("sum_hess", C.c_float), ("split_gain", C.c_float),
-                ("split_bin", C.c_int64), ("stat_g", C.c_double), ("stat_h", C.c_double)]
+                ("split_bin", C.c_int64), ("stat_g", C.c_double), ("stat_h", C.c_double),
+                ("is_categorical", C.c_int32), ("cat_begin", C.c_uint32), ("cat_end", C.c_uint32)]
 
 
 class ForestDesc(C.Structure):
@@ -85,6 +88,10 @@ def lib():
         L.or_cuts_from_dense.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_float]
         L.or_cuts_from_csr.restype = P(Cuts)
         L.or_cuts_from_csr.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p]
+        L.or_cuts_from_dense_typed.restype = P(Cuts)
+        L.or_cuts_from_dense_typed.argtypes = L.or_cuts_from_dense.argtypes + [C.c_void_p]
+        L.or_cuts_from_csr_typed.restype = P(Cuts)
+        L.or_cuts_from_csr_typed.argtypes = L.or_cuts_from_csr.argtypes + [C.c_void_p]
         L.or_cuts_free.argtypes = [P(Cuts)]
         L.or_cuts_total_bins.restype = C.c_size_t
         L.or_cuts_total_bins.argtypes = [P(Cuts)]
@@ -106,6 +113,15 @@ def lib():
         L.or_calc_weight.argtypes = [C.c_double, C.c_double, P(Params)]
         L.or_node_gain.restype = C.c_float
         L.or_node_gain.argtypes = [C.c_double, C.c_double, C.c_double, C.c_double, P(Params)]
+        L.or_sweep_categorical.argtypes = [C.c_void_p, C.c_size_t, C.c_double, C.c_double, C.c_double, C.c_double,
+                                           C.c_int, P(Params), C.c_uint32, P(Split)]
+        L.or_partition_categorical.restype = C.c_size_t
+        L.or_partition_categorical.argtypes = [P(Index), C.c_void_p, C.c_size_t, C.c_uint32, C.c_void_p, C.c_int,
+                                               C.c_void_p, C.c_void_p]
+        L.or_tree_n_categories.restype = C.c_size_t
+        L.or_tree_n_categories.argtypes = [C.c_void_p]
+        L.or_tree_categories.restype = P(C.c_uint32)
+        L.or_tree_categories.argtypes = [C.c_void_p]
         L.or_partition.restype = C.c_size_t
         L.or_partition.argtypes = [P(Index), C.c_void_p, C.c_size_t, C.c_uint32, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
         L.or_grow_tree.restype = C.c_void_p
@@ -166,9 +182,16 @@ def params(objective=OBJ_SQUARED_ERROR, eta=0.3, gamma=0.0, reg_lambda=1.0, alph
 class Dataset:
     """Cuts plus the binned index of a dense f32 matrix (or CSR)."""
 
-    def __init__(self, x=None, max_bin=256, weights=None, missing=np.nan, csr=None, n_cols=None):
+    def __init__(self, x=None, max_bin=256, weights=None, missing=np.nan, csr=None, n_cols=None,
+                 feature_types=None):
+        """feature_types: per feature "c" (categorical) or "q" (numeric),
+        or None for every feature numeric."""
         L = lib()
         self._keep = []
+        cat = None
+        if feature_types is not None:
+            cat = np.array([1 if t in ("c", "categorical") else 0 for t in feature_types], np.uint8)
+            self._keep.append(cat)
         if csr is not None:
             row_ptr, col, val = (np.ascontiguousarray(csr[0], np.uintp),
                                  np.ascontiguousarray(csr[1], np.uint32),
@@ -176,14 +199,15 @@ class Dataset:
             n = len(row_ptr) - 1
             self._keep += [row_ptr, col, val]
             w = None if weights is None else np.ascontiguousarray(weights, np.float32)
-            self.cuts = L.or_cuts_from_csr(_ptr(row_ptr), _ptr(col), _ptr(val), n, n_cols, max_bin, _ptr(w))
+            self.cuts = L.or_cuts_from_csr_typed(_ptr(row_ptr), _ptr(col), _ptr(val), n, n_cols, max_bin, _ptr(w),
+                                                 _ptr(cat))
             self.index = L.or_index_from_csr(_ptr(row_ptr), _ptr(col), _ptr(val), n, n_cols, self.cuts)
             self.n_rows, self.n_cols = n, n_cols
         else:
             x = np.ascontiguousarray(x, np.float32)
             n, f = x.shape
             w = None if weights is None else np.ascontiguousarray(weights, np.float32)
-            self.cuts = L.or_cuts_from_dense(_ptr(x), n, f, max_bin, _ptr(w), missing)
+            self.cuts = L.or_cuts_from_dense_typed(_ptr(x), n, f, max_bin, _ptr(w), missing, _ptr(cat))
             self.index = L.or_index_from_dense(_ptr(x), n, f, missing, self.cuts)
             self.n_rows, self.n_cols = n, f
 
@@ -278,16 +302,22 @@ class Dataset:
 
 
 def tree_nodes(t):
+    """A tree's nodes as dicts; a categorical split's node lists its
+    categories (going left) under "categories"."""
     L = lib()
     n = L.or_tree_n_nodes(t)
     arr = L.or_tree_nodes(t)
+    nc = L.or_tree_n_categories(t)
+    pool = np.ctypeslib.as_array(L.or_tree_categories(t), shape=(nc,)).tolist() if nc else []
     out = []
     for i in range(n):
         nd = arr[i]
         out.append(dict(split_feature=nd.split_feature, split_cond=nd.split_cond,
                         default_left=bool(nd.default_left), left=nd.left, right=nd.right,
                         leaf_value=nd.leaf_value, sum_hess=nd.sum_hess, split_gain=nd.split_gain,
-                        split_bin=nd.split_bin, stat_g=nd.stat_g, stat_h=nd.stat_h))
+                        split_bin=nd.split_bin, stat_g=nd.stat_g, stat_h=nd.stat_h,
+                        is_categorical=bool(nd.is_categorical),
+                        categories=pool[nd.cat_begin:nd.cat_end] if nd.is_categorical else []))
     return out
 
 
@@ -366,11 +396,17 @@ def forest_arrays(trees, tree_weight=None, tree_output=None, n_outputs=1, base_s
     """Flatten per-tree node dicts into the arrays or_predict_margin reads."""
     off = [0]
     feat, cond, dl, left, right, leaf = [], [], [], [], [], []
+    isc, cb, ce, pool = [], [], [], []
     for t in trees:
-        if isinstance(t, dict):  # one array per field
+        if isinstance(t, dict):  # one array per field (categories: the tree's pool, by ranges)
+            tp = list(t.get("categories", []))
             t = [dict(split_feature=int(t["split_feature"][i]), split_cond=float(t["split_cond"][i]),
                       default_left=bool(t["default_left"][i]), left=int(t["left"][i]), right=int(t["right"][i]),
-                      leaf_value=float(t["leaf_value"][i])) for i in range(len(t["left"]))]
+                      leaf_value=float(t["leaf_value"][i]),
+                      is_categorical=bool(t["is_categorical"][i]) if "is_categorical" in t else False,
+                      categories=tp[int(t["cat_begin"][i]):int(t["cat_end"][i])] if "is_categorical" in t
+                      and t["is_categorical"][i] else [])
+                 for i in range(len(t["left"]))]
         for nd in t:
             feat.append(nd["split_feature"])
             cond.append(nd["split_cond"])
@@ -378,6 +414,11 @@ def forest_arrays(trees, tree_weight=None, tree_output=None, n_outputs=1, base_s
             left.append(nd["left"])
             right.append(nd["right"])
             leaf.append(nd["leaf_value"])
+            c = nd.get("categories", []) if nd.get("is_categorical") else []
+            isc.append(1 if nd.get("is_categorical") else 0)
+            cb.append(len(pool))
+            pool.extend(c)
+            ce.append(len(pool))
         off.append(len(feat))
     nt = len(trees)
     arrs = dict(
@@ -388,6 +429,9 @@ def forest_arrays(trees, tree_weight=None, tree_output=None, n_outputs=1, base_s
         tree_weight=np.ones(nt, np.float32) if tree_weight is None else np.asarray(tree_weight, np.float32),
         tree_output=np.zeros(nt, np.uint32) if tree_output is None else np.asarray(tree_output, np.uint32),
         base_score=np.asarray(base_score, np.float32), n_outputs=n_outputs)
+    if any(isc):
+        arrs.update(is_categorical=np.array(isc, np.uint8), cat_begin=np.array(cb, np.uint32),
+                    cat_end=np.array(ce, np.uint32), categories=np.array(pool, np.uint32))
     return arrs
 
 

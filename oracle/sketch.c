@@ -397,14 +397,66 @@ static or_cuts *assemble(float **per, size_t *per_len, size_t f) {
 
 /* quantile.rs:65-78, :122-238: every feature's present values, in row order,
  * into its own sketch. */
+/* f32::total_cmp as an integer key */
+static int32_t total_key32(float v) {
+    int32_t b;
+    memcpy(&b, &v, 4);
+    return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+static int cmp_total(const void *a, const void *b) {
+    int32_t ka = total_key32(*(const float *)a), kb = total_key32(*(const float *)b);
+    return (ka > kb) - (ka < kb);
+}
+
+/* A categorical feature's cuts (quantile.rs:524-672): its present values
+ * sorted by total_cmp and deduplicated by bit pattern, then one bin per
+ * distinct value by `!=` (build_categorical_cuts); a feature with no
+ * present value keeps one degenerate bin at 0. `vals` is consumed. */
+static void categorical_cuts(float *vals, size_t m, float **out, size_t *out_len) {
+    qsort(vals, m, sizeof(float), cmp_total);
+    size_t k = 0;
+    for (size_t i = 0; i < m; i++) {
+        uint32_t a, b;
+        memcpy(&a, &vals[i], 4);
+        if (k) memcpy(&b, &vals[k - 1], 4);
+        if (k == 0 || a != b) vals[k++] = vals[i];
+    }
+    float *cuts = (float *)malloc((k ? k : 1) * sizeof(float));
+    size_t n = 0;
+    if (k == 0)
+        cuts[n++] = 0.0f;
+    else {
+        cuts[n++] = vals[0];
+        for (size_t i = 1; i < k; i++)
+            if (vals[i - 1] != vals[i]) cuts[n++] = vals[i];
+    }
+    *out = cuts;
+    *out_len = n;
+}
+
 or_cuts *or_cuts_from_dense(const float *x, size_t n, size_t f, size_t max_bin,
                             const float *weights, float missing) {
+    return or_cuts_from_dense_typed(x, n, f, max_bin, weights, missing, NULL);
+}
+
+or_cuts *or_cuts_from_dense_typed(const float *x, size_t n, size_t f, size_t max_bin,
+                                  const float *weights, float missing, const uint8_t *categorical) {
     float **per = (float **)calloc(f, sizeof(float *));
     size_t *per_len = (size_t *)calloc(f, sizeof(size_t));
 #pragma omp parallel for schedule(dynamic, 1)
     for (size_t j = 0; j < f; j++) {
         size_t present = 0;
         for (size_t r = 0; r < n; r++) present += !is_missing(x[r * f + j], missing);
+        if (categorical && categorical[j]) {
+            float *vals = (float *)malloc((present ? present : 1) * sizeof(float));
+            size_t m = 0;
+            for (size_t r = 0; r < n; r++)
+                if (!is_missing(x[r * f + j], missing)) vals[m++] = x[r * f + j];
+            categorical_cuts(vals, m, &per[j], &per_len[j]);
+            free(vals);
+            continue;
+        }
         sketch s;
         sk_init(&s, present, max_bin);
         for (size_t r = 0; r < n; r++) {
@@ -419,12 +471,22 @@ or_cuts *or_cuts_from_dense(const float *x, size_t n, size_t f, size_t max_bin,
     or_cuts *c = assemble(per, per_len, f);
     free(per);
     free(per_len);
+    if (categorical) {
+        c->is_categorical = (uint8_t *)malloc(f ? f : 1);
+        for (size_t j = 0; j < f; j++) c->is_categorical[j] = categorical[j] ? 1 : 0;
+    }
     return c;
 }
 
 or_cuts *or_cuts_from_csr(const size_t *row_ptr, const uint32_t *col,
                           const float *val, size_t n, size_t f, size_t max_bin,
                           const float *weights) {
+    return or_cuts_from_csr_typed(row_ptr, col, val, n, f, max_bin, weights, NULL);
+}
+
+or_cuts *or_cuts_from_csr_typed(const size_t *row_ptr, const uint32_t *col,
+                                const float *val, size_t n, size_t f, size_t max_bin,
+                                const float *weights, const uint8_t *categorical) {
     /* CSC view: each feature's stored entries in row order (quantile.rs:219-232). */
     size_t *count = (size_t *)calloc(f + 1, sizeof(size_t));
     size_t nnz = row_ptr[n];
@@ -445,6 +507,13 @@ or_cuts *or_cuts_from_csr(const size_t *row_ptr, const uint32_t *col,
 #pragma omp parallel for schedule(dynamic, 1)
     for (size_t j = 0; j < f; j++) {
         size_t lo = count[j], hi = count[j + 1];
+        if (categorical && categorical[j]) {
+            float *vals = (float *)malloc((hi - lo ? hi - lo : 1) * sizeof(float));
+            memcpy(vals, cval + lo, (hi - lo) * sizeof(float));
+            categorical_cuts(vals, hi - lo, &per[j], &per_len[j]);
+            free(vals);
+            continue;
+        }
         sketch s;
         sk_init(&s, hi - lo, max_bin);
         for (size_t p = lo; p < hi; p++) sk_push(&s, cval[p], weights ? weights[crow[p]] : 1.0f);
@@ -453,6 +522,10 @@ or_cuts *or_cuts_from_csr(const size_t *row_ptr, const uint32_t *col,
         sk_free(&s);
     }
     or_cuts *c = assemble(per, per_len, f);
+    if (categorical) {
+        c->is_categorical = (uint8_t *)malloc(f ? f : 1);
+        for (size_t j = 0; j < f; j++) c->is_categorical[j] = categorical[j] ? 1 : 0;
+    }
     free(per);
     free(per_len);
     free(count);
@@ -466,6 +539,7 @@ void or_cuts_free(or_cuts *c) {
     if (!c) return;
     free(c->feature_offset);
     free(c->cut_values);
+    free(c->is_categorical);
     free(c);
 }
 
@@ -474,6 +548,20 @@ size_t or_cuts_total_bins(const or_cuts *c) { return c->feature_offset[c->n_feat
 /* quantile.rs:285-296: upper_bound count of cuts <= v, clamped to the last bin. */
 uint32_t or_bin_of(const or_cuts *c, size_t f, float v) {
     size_t start = c->feature_offset[f], end = c->feature_offset[f + 1];
+    if (c->is_categorical && c->is_categorical[f]) {
+        /* the bin whose category equals v (binary search by partial_cmp), else bin 0 */
+        size_t lo = 0, hi = end - start;
+        while (lo < hi) {
+            size_t mid = (lo + hi) / 2;
+            float cv = c->cut_values[start + mid];
+            if (cv == v) return (uint32_t)(start + mid);
+            if (cv < v)
+                lo = mid + 1;
+            else
+                hi = mid;
+        }
+        return (uint32_t)start;
+    }
     size_t lo = 0, hi = end - start;
     const float *cuts = c->cut_values + start;
     while (lo < hi) {

@@ -11,7 +11,8 @@
  * on a non-dense index whose forward total differs from the node total),
  * builder/mod.rs:313-342 (need_replace, xgb_update), :167-193 (found,
  * valid), hist/search.rs:171-259 (feature-order merge; a feature with at
- * most one bin has no candidate).
+ * most one bin has no candidate); builder/categorical.rs:48-170 (a
+ * categorical feature's one-hot or weight-sorted partition sweep).
  */
 #include "oracle.h"
 
@@ -117,6 +118,140 @@ static void offer(scan_ctx *c, uint32_t f, int dir, int64_t bin, int default_lef
     b->right_h = rh;
     b->w_left = (double)wl;
     b->w_right = (double)wr;
+    b->categorical = 0;
+}
+
+/* ---- categorical features (builder/categorical.rs:48-170) ---------------- */
+
+#define MAX_CAT_TO_ONEHOT 4
+#define MAX_CAT_THRESHOLD 64
+
+/* A feature's best categorical candidate in XGBoost's orientation: the set
+ * is its right child, default_left routes missing values. */
+typedef struct cat_local {
+    int has;
+    float loss, wl, wr;
+    int default_left;
+    double lg, lh, rg, rh;
+} cat_local;
+
+/* SplitScorer::loss_chg (builder/split.rs:37-56); 0 when not offered. */
+static int score_children(const scan_ctx *c, int dir, double lg, double lh, double rg, double rh, float *loss,
+                          float *wl, float *wr) {
+    if (!children_valid(lh, rh, c->r.min_child_weight)) return 0;
+    *wl = xgb_weight(lg, lh, &c->r, c->lower, c->upper);
+    *wr = xgb_weight(rg, rh, &c->r, c->lower, c->upper);
+    if (!satisfies(dir, (double)*wl, (double)*wr)) return 0;
+    float gain = (float)gain_given_weight(lg, lh, &c->r, *wl) + (float)gain_given_weight(rg, rh, &c->r, *wr);
+    *loss = gain - c->root_gain;
+    return 1;
+}
+
+/* SplitEntry::Update on the feature's own entry, which starts at loss 0. */
+static int cat_offer(const scan_ctx *c, int dir, uint32_t f, cat_local *local, int default_left, double lg,
+                     double lh, double rg, double rh) {
+    float loss, wl, wr;
+    if (!score_children(c, dir, lg, lh, rg, rh, &loss, &wl, &wr)) return 0;
+    if (!need_replace(local->has ? local->loss : 0.0f, f, loss, f)) return 0;
+    local->has = 1;
+    local->loss = loss;
+    local->wl = wl;
+    local->wr = wr;
+    local->default_left = default_left;
+    local->lg = lg;
+    local->lh = lh;
+    local->rg = rg;
+    local->rh = rh;
+    return 1;
+}
+
+/* p_best->Update: the feature's candidate against the node's best; the
+ * recorded split puts the set on the left (children and missing direction
+ * swapped, Children::swapped / Score::swapped). `set` lists local bins. */
+static void cat_merge(or_split *best, const cat_local *local, uint32_t f, const size_t *set, size_t n_set) {
+    if (!local->has) return;
+    if (!need_replace((float)best->loss_chg, best->feature, local->loss, f)) return;
+    best->loss_chg = (double)local->loss;
+    best->feature = f;
+    best->bin = -1;
+    best->default_left = !local->default_left;
+    best->left_g = local->rg;
+    best->left_h = local->rh;
+    best->right_g = local->lg;
+    best->right_h = local->lh;
+    best->w_left = (double)local->wr;
+    best->w_right = (double)local->wl;
+    best->categorical = 1;
+    memset(best->cat_left, 0, sizeof(best->cat_left));
+    for (size_t i = 0; i < n_set; i++) best->cat_left[set[i] / 32] |= 1u << (set[i] % 32);
+}
+
+static void sweep(const scan_ctx *c, const double *st, size_t n, double tg, double th, int dir, uint32_t f,
+                  or_split *best) {
+    if (n > OR_MAX_CAT_BINS) return;
+    if (n < MAX_CAT_TO_ONEHOT) {
+        /* EnumerateOneHot: each category alone, missing values on either side */
+        double pg = 0.0, ph = 0.0;
+        for (size_t i = 0; i < n; i++) {
+            pg += st[2 * i];
+            ph += st[2 * i + 1];
+        }
+        double mg = tg - pg, mh = th - ph;
+        cat_local local = {0};
+        size_t chosen = 0;
+        for (size_t i = 0; i < n; i++) {
+            double rg = st[2 * i], rh = st[2 * i + 1];
+            if (cat_offer(c, dir, f, &local, 1, tg - rg, th - rh, rg, rh)) chosen = i;
+            rg += mg;
+            rh += mh;
+            if (cat_offer(c, dir, f, &local, 0, tg - rg, th - rh, rg, rh)) chosen = i;
+        }
+        cat_merge(best, &local, f, &chosen, 1);
+        return;
+    }
+    /* EnumeratePart: categories stably sorted by weight (CalcWeightCat) */
+    float keys[OR_MAX_CAT_BINS];
+    size_t sorted[OR_MAX_CAT_BINS];
+    for (size_t i = 0; i < n; i++) {
+        double g = st[2 * i], h = st[2 * i + 1];
+        keys[i] = h < c->r.min_child_weight ? 0.0f : (float)xgb_calc_weight(g, h, &c->r);
+        sorted[i] = i;
+    }
+    for (size_t i = 1; i < n; i++) { /* stable insertion sort */
+        size_t v = sorted[i], j = i;
+        while (j > 0 && keys[v] < keys[sorted[j - 1]]) {
+            sorted[j] = sorted[j - 1];
+            j--;
+        }
+        sorted[j] = v;
+    }
+    size_t depth = n < MAX_CAT_THRESHOLD ? n : MAX_CAT_THRESHOLD;
+    for (int forward = 1; forward >= 0; forward--) {
+        double ag = 0.0, ah = 0.0;
+        cat_local local = {0};
+        size_t best_partition = 0;
+        for (size_t step = 0; step + 1 < depth; step++) {
+            size_t j = forward ? step : n - 1 - step;
+            ag += st[2 * sorted[j]];
+            ah += st[2 * sorted[j] + 1];
+            size_t partition = forward ? step + 1 : j;
+            int offered = forward ? cat_offer(c, dir, f, &local, 1, tg - ag, th - ah, ag, ah)
+                                  : cat_offer(c, dir, f, &local, 0, ag, ah, tg - ag, th - ah);
+            if (offered) best_partition = partition;
+        }
+        cat_merge(best, &local, f, sorted, best_partition);
+    }
+}
+
+void or_sweep_categorical(const double *stats, size_t n, double total_g, double total_h, double lower,
+                          double upper, int dir, const or_params *p, uint32_t feature, or_split *best) {
+    scan_ctx c;
+    c.r = reg_of(p);
+    c.lower = lower;
+    c.upper = upper;
+    c.root_gain = or_node_gain(total_g, total_h, lower, upper, p);
+    c.best = best;
+    sweep(&c, stats, n, total_g, total_h, dir, feature, best);
 }
 
 void or_evaluate(const or_index *ix, const double *hist, double total_g, double total_h,
@@ -135,8 +270,13 @@ void or_evaluate(const or_index *ix, const double *hist, double total_g, double 
     const uint32_t *off = ix->cuts->feature_offset;
     for (size_t f = 0; f < ix->n_cols; f++) {
         size_t fs = off[f], fe = off[f + 1];
-        if (fe <= fs + 1) continue;
         int dir = (p->monotone && f < p->n_monotone) ? p->monotone[f] : 0;
+        if (ix->cuts->is_categorical && ix->cuts->is_categorical[f]) {
+            /* category_stats (hist/search.rs:402-407): every category's bin */
+            sweep(&c, hist + 2 * fs, fe - fs, total_g, total_h, dir, (uint32_t)f, out);
+            continue;
+        }
+        if (fe <= fs + 1) continue;
         double ag = 0.0, ah = 0.0;
         for (size_t b = fs; b < fe; b++) {
             ag += hist[2 * b];

@@ -600,3 +600,101 @@ def test_lossguide_respects_max_leaves():
     t, _ = ds.grow_tree(gp, O.params(grow_policy=O.GROW_LOSSGUIDE, max_leaves=4, max_depth=0, min_child_weight=0.0,
                                      gamma=0.0, reg_lambda=0.0))
     assert sum(nd["left"] == -1 for nd in t) <= 4
+
+
+# ---- categorical splits --------------------------------------------------------------------
+
+def test_categorical_splits_model_retrained_bit_for_bit(saved):
+    """tests/native_format.rs:508-540: the saved categorical-splits model
+    (base(): hist, depth 3, eta 0.3; four_features with column 0 the
+    category codes i % 5, categorical; y = [0, 2, -1, 3, 1][i % 5] + x1)
+    grown again by the oracle: every tree's structure, category sets, split
+    gains, Hessian sums and leaf values bit for bit, in three versions."""
+    x = categorical_features()
+    y = (np.array([0.0, 2.0, -1.0, 3.0, 1.0], np.float32)[np.arange(len(x)) % 5] + x[:, 1]).astype(np.float32)
+    ds = O.Dataset(x, max_bin=256, feature_types=["c", "q", "q", "q"])
+    for ver in ("0.2.0", "0.4.3", "0.4.9"):
+        case = saved[f"{ver}/categorical_splits"]
+        model = O.Model(ds, y, O.params(max_depth=3), len(case["trees"]))
+        assert np.array_equal(model.base_score().view(np.uint32), np.array(case["base_score"], np.uint32))
+        for t, (mine, ref) in enumerate(zip(model.trees(), case["trees"])):
+            assert [n["left"] for n in mine] == ref["left"] and [n["right"] for n in mine] == ref["right"], t
+            pool = ref["categories"]
+            for i, n in enumerate(mine):
+                assert n["is_categorical"] == bool(ref["is_categorical"][i]), (t, i)
+                if n["is_categorical"]:
+                    assert n["categories"] == pool[ref["cat_begin"][i]:ref["cat_end"][i]], (t, i)
+                if n["left"] != -1:
+                    assert n["split_feature"] == ref["split_feature"][i], (t, i)
+                    assert bool(n["default_left"]) == bool(ref["default_left"][i]), (t, i)
+                    assert np.float32(n["split_cond"]).view(np.uint32) == ref["split_cond"][i], (t, i)
+                    assert np.float32(n["split_gain"]).view(np.uint32) == ref["split_gain"][i], (t, i)
+                assert np.float32(n["leaf_value"]).view(np.uint32) == ref["leaf_value"][i], (t, i)
+                assert np.float32(n["sum_hess"]).view(np.uint32) == ref["sum_hess"][i], (t, i)
+        assert np.array_equal(model.margins().view(np.uint32), np.array(case["margins"], np.uint32))
+
+
+def _sweep(cats, total, reg_lambda=0.0):
+    """builder/categorical.rs:180-201: sweep_categorical unregularized over
+    (G, H) per category, against the node total; the winner's set by bin."""
+    p = O.params(reg_lambda=reg_lambda, alpha=0.0, max_delta_step=0.0, min_child_weight=0.0)
+    best = O.Split()
+    best.loss_chg, best.feature, best.bin, best.default_left = 0.0, 0, -1, 1
+    st = np.ascontiguousarray(np.array(cats, np.float64).reshape(-1))
+    O.lib().or_sweep_categorical(st.ctypes.data, len(cats), total[0], total[1], -math.inf, math.inf, 0, p, 0, best)
+    chosen = [i for i in range(len(cats)) if best.cat_left[i // 32] >> (i % 32) & 1]
+    return best, chosen
+
+
+def test_categorical_sweep_known_answers():
+    """builder/categorical.rs:211-263: a lone category splits from the
+    missing values (loss 4, missing to the other child); four categories of
+    weights -2, -1, 1, 2 with missing gradients -3 and 3 both choose {0, 1},
+    missing with the set only when its weight fits them, loss 4.5 + 12 - 1.8."""
+    best, chosen = _sweep([(2.0, 2.0)], (0.0, 4.0))
+    assert best.categorical and chosen == [0] and not best.default_left
+    assert abs(best.loss_chg - 4.0) < 1e-6
+    cats = [(2.0, 1.0), (1.0, 1.0), (-1.0, 1.0), (-2.0, 1.0)]
+    for missing_grad, with_set in ((-3.0, False), (3.0, True)):
+        best, chosen = _sweep(cats, (missing_grad, 5.0))
+        assert chosen == [0, 1], missing_grad
+        assert bool(best.default_left) == with_set, missing_grad
+        assert abs(best.loss_chg - (4.5 + 12.0 - 1.8)) < 1e-5
+
+
+def test_categorical_sweep_brute_force():
+    """Every candidate the reference enumerates, scored in closed form in
+    f64 (loss = G_l^2/H_l + G_r^2/H_r - G^2/H, unregularized): the sweep's
+    winner is the maximum over one-hot sets (fewer than 4 categories) or
+    over prefixes and suffixes of the weight order (4 or more), with missing
+    values on either side."""
+    rng = np.random.default_rng(21)
+    for trial in range(200):
+        n = int(rng.integers(1, 9))
+        g = rng.normal(0, 1, n).round(2)
+        h = rng.uniform(0.5, 2, n).round(2)
+        mg, mh = round(float(rng.normal(0, 1)), 2), round(float(rng.uniform(0, 1)), 2)
+        total = (float(g.sum() + mg), float(h.sum() + mh))
+        best, chosen = _sweep(list(zip(g, h)), total)
+
+        def loss(sg, sh):
+            ogh = total[1] - sh
+            if sh <= 0 or ogh <= 0:
+                return -np.inf
+            return sg * sg / sh + (total[0] - sg) ** 2 / ogh - total[0] ** 2 / total[1]
+        cands = []
+        if n < 4:
+            for i in range(n):
+                cands += [(loss(g[i], h[i]), [i]), (loss(g[i] + mg, h[i] + mh), [i])]
+        else:
+            order = sorted(range(n), key=lambda i: -g[i] / h[i])
+            for k in range(1, n):
+                s = order[:k]
+                cands += [(loss(g[s].sum(), h[s].sum()), sorted(s)),
+                          (loss(g[s].sum() + mg, h[s].sum() + mh), sorted(s))]
+        top = max(c[0] for c in cands)
+        if top <= 1e-3:
+            continue
+        assert best.categorical, trial
+        assert abs(best.loss_chg - top) <= 1e-3 * max(1.0, abs(top)), (trial, best.loss_chg, top)
+        assert any(abs(c[0] - top) <= 1e-3 * max(1.0, abs(top)) and c[1] == chosen for c in cands), trial
