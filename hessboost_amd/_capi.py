@@ -37,7 +37,8 @@ class IndexDesc(C.Structure):
     _fields_ = [("n_rows", C.c_uint64), ("n_cols", C.c_uint64), ("feature_offset", u32p),
                 ("cut_values", f32p), ("row_ptr", u64p), ("row_bins", C.c_void_p),
                 ("row_bin_width", C.c_uint32), ("dense", C.c_uint32), ("col_bins", C.c_void_p),
-                ("col_bin_width", C.c_uint32), ("pad", C.c_uint32), ("missing", u64p)]
+                ("col_bin_width", C.c_uint32), ("pad", C.c_uint32), ("missing", u64p),
+                ("is_categorical", C.POINTER(C.c_uint8))]
 
 
 class IndexInfo(C.Structure):
@@ -118,6 +119,13 @@ SIGNATURES = {
     "hbr_cuts_from_values": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, P(C.c_void_p)]),
     "hbr_cuts_info": (C.c_int, [C.c_void_p, P(C.c_uint64), P(C.c_uint64)]),
     "hbr_cuts_copy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "hbr_cuts_from_dense_typed": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.c_void_p, C.c_float,
+                                            C.c_void_p, P(C.c_void_p)]),
+    "hbr_cuts_from_csr_typed": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32,
+                                          C.c_void_p, C.c_void_p, P(C.c_void_p)]),
+    "hbr_cuts_categorical": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "hbr_trainer_tree_categories": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p, C.c_void_p,
+                                              C.c_void_p, P(C.c_uint64)]),
     "hbr_cuts_free": (None, [C.c_void_p]),
     "hbr_index_from_dense": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_void_p, P(C.c_void_p)]),
     "hbr_index_from_csr": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_void_p, P(C.c_void_p)]),

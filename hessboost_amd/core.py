@@ -19,6 +19,18 @@ from . import _capi as A
 
 # ---- cuts and the binned index ---------------------------------------------------
 
+def _categorical_flags(feature_types, n_cols):
+    """The DMatrix's feature_types (python/python/hessboost/_data.py: "c" or
+    "categorical" marks a categorical feature; "q", "float", "int" numeric)
+    as per-feature bytes, or None when every feature is numeric."""
+    if feature_types is None:
+        return None
+    if len(feature_types) != n_cols:
+        raise ValueError("feature_types needs one entry per feature")
+    flags = np.array([1 if t in ("c", "categorical") else 0 for t in feature_types], np.uint8)
+    return flags if flags.any() else None
+
+
 class Cuts:
     """HistCuts (src/data/quantile.rs:28-296): per-feature cut values."""
 
@@ -26,24 +38,34 @@ class Cuts:
         self._h = handle
 
     @classmethod
-    def from_dense(cls, x, max_bin=256, weights=None, missing=np.nan):
+    def from_dense(cls, x, max_bin=256, weights=None, missing=np.nan, feature_types=None):
         x = np.ascontiguousarray(x, np.float32)
         w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+        cat = _categorical_flags(feature_types, x.shape[1])
         h = C.c_void_p()
-        A.check(A.lib().hbr_cuts_from_dense(A.ptr(x), x.shape[0], x.shape[1], max_bin, A.ptr(w),
-                                            float(missing), C.byref(h)))
+        A.check(A.lib().hbr_cuts_from_dense_typed(A.ptr(x), x.shape[0], x.shape[1], max_bin, A.ptr(w),
+                                                  float(missing), A.ptr(cat), C.byref(h)))
         return cls(h)
 
     @classmethod
-    def from_csr(cls, row_ptr, col, val, n_cols, max_bin=256, weights=None):
+    def from_csr(cls, row_ptr, col, val, n_cols, max_bin=256, weights=None, feature_types=None):
         row_ptr = np.ascontiguousarray(row_ptr, np.uint64)
         col = np.ascontiguousarray(col, np.uint32)
         val = np.ascontiguousarray(val, np.float32)
         w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+        cat = _categorical_flags(feature_types, n_cols)
         h = C.c_void_p()
-        A.check(A.lib().hbr_cuts_from_csr(A.ptr(row_ptr), A.ptr(col), A.ptr(val), len(row_ptr) - 1, n_cols,
-                                          max_bin, A.ptr(w), C.byref(h)))
+        A.check(A.lib().hbr_cuts_from_csr_typed(A.ptr(row_ptr), A.ptr(col), A.ptr(val), len(row_ptr) - 1, n_cols,
+                                                max_bin, A.ptr(w), A.ptr(cat), C.byref(h)))
         return cls(h)
+
+    def categorical(self):
+        """Per feature, whether its bins are categories."""
+        n = C.c_uint64()
+        A.check(A.lib().hbr_cuts_info(self._h, C.byref(n), None))
+        out = np.zeros(n.value, np.uint8)
+        A.check(A.lib().hbr_cuts_categorical(self._h, A.ptr(out)))
+        return out.astype(bool)
 
     def __del__(self):
         try:
@@ -384,7 +406,7 @@ class DMatrix:
     a dense f32 matrix or CSR triplet, labels, optional weights, and the
     missing-value marker (NaN by default)."""
 
-    def __init__(self, data, label=None, weight=None, missing=np.nan, n_cols=None):
+    def __init__(self, data, label=None, weight=None, missing=np.nan, n_cols=None, feature_types=None):
         if isinstance(data, tuple):
             self.csr = (np.ascontiguousarray(data[0], np.uint64), np.ascontiguousarray(data[1], np.uint32),
                         np.ascontiguousarray(data[2], np.float32))
@@ -398,6 +420,8 @@ class DMatrix:
         self.label = None if label is None else np.ascontiguousarray(label, np.float32)
         self.weight = None if weight is None else np.ascontiguousarray(weight, np.float32)
         self.missing = missing
+        self.feature_types = None if feature_types is None else list(feature_types)
+        _categorical_flags(self.feature_types, self.n_cols)  # validates the length
         self._index = {}
         self._cuts = {}
 
@@ -405,10 +429,11 @@ class DMatrix:
         """HistCuts for max_bin (src/data/quantile.rs:65-78), cached."""
         if max_bin not in self._cuts:
             if self.csr is not None:
-                self._cuts[max_bin] = Cuts.from_csr(*self.csr, self.n_cols, max_bin=max_bin, weights=self.weight)
+                self._cuts[max_bin] = Cuts.from_csr(*self.csr, self.n_cols, max_bin=max_bin, weights=self.weight,
+                                                    feature_types=self.feature_types)
             else:
                 self._cuts[max_bin] = Cuts.from_dense(self.x, max_bin=max_bin, weights=self.weight,
-                                                      missing=self.missing)
+                                                      missing=self.missing, feature_types=self.feature_types)
         return self._cuts[max_bin]
 
     def index(self, max_bin=256) -> BinnedIndex:
@@ -424,8 +449,9 @@ class DMatrix:
     def engine(self, max_bin=256, ordinal=0) -> "Engine":
         """A device engine over this matrix: a dense matrix is binned on the
         device against the host cuts (features of at most 256 bins); CSR
-        input, or wider features, go through the host index."""
-        if self.x is not None:
+        input, wider features, or categorical features (binned by exact
+        match) go through the host index."""
+        if self.x is not None and _categorical_flags(self.feature_types, self.n_cols) is None:
             cuts = self.cuts(max_bin)
             fo, _ = cuts.arrays()
             if fo.size > 1 and int(np.max(np.diff(fo))) <= 256:
@@ -768,6 +794,16 @@ class Trainer:
                                                            ("split_feature", "split_cond", "default_left", "left",
                                                             "right", "leaf_value", "sum_hess", "split_gain",
                                                             "split_bin")]))
+            nc = C.c_uint64()
+            cat = dict(is_categorical=np.zeros(k, np.uint8), cat_begin=np.zeros(k, np.uint32),
+                       cat_end=np.zeros(k, np.uint32))
+            A.check(A.lib().hbr_trainer_tree_categories(self._h, t, A.ptr(cat["is_categorical"]),
+                                                        A.ptr(cat["cat_begin"]), A.ptr(cat["cat_end"]), None,
+                                                        C.byref(nc)))
+            if cat["is_categorical"].any():
+                pool = np.zeros(nc.value, np.uint32)
+                A.check(A.lib().hbr_trainer_tree_categories(self._h, t, None, None, None, A.ptr(pool), None))
+                d.update(cat, categories=pool)
             out.append(d)
         return out
 

@@ -204,6 +204,9 @@ struct PartSplit {
     uint32_t parent_slot;   // parent's slot, becomes the sibling's
     uint32_t identity;      // the parent's rows are j (seg.offset % n_rows + j; no row list is read)
     uint32_t tree;          // tree of a batched level (the class of a softmax round)
+    uint32_t table;         // categorical split: 1 + its row in PartArgs::cat_tables (present local
+                            // bins whose bit is set go left; limit is unused); 0: numeric
+    uint32_t pad[3];
 };
 
 // Device decision per split after the scan of tile counts.
@@ -236,6 +239,7 @@ struct PartArgs {
     const uint32_t *tile_split;  // non-null: the split of every tile (else found by binary search)
     uint32_t csr_ascending;      // every CSR row's global bins ascend: routing binary-searches them
     uint32_t pad;
+    const uint32_t *cat_tables;  // kCatWords words per categorical split: its left local bins
 };
 
 // ---- histograms ----------------------------------------------------------------
@@ -376,12 +380,20 @@ struct ScanParams {
     double lambda, alpha, max_delta_step, min_child_weight;
 };
 
+// Categorical features (builder/categorical.rs): at most kCatMaxBins
+// categories (bins) each; a split's set is a bitmask of kCatWords words over
+// the feature's local bins.
+constexpr uint32_t kCatMaxBins = 1024;
+constexpr uint32_t kCatWords = kCatMaxBins / 32;
+constexpr uint32_t kScanCategorical = 4u;
+
 // Best candidate of one feature (or of one node after the merge).
 struct ScanBest {
     float loss;              // -inf: none
     uint32_t feature;
     uint32_t index;          // candidate order within the feature
-    uint32_t flags;          // bit0 backward, bit1 NaN seen
+    uint32_t flags;          // bit0 backward (categorical: missing values go left), bit1 NaN seen,
+                             // bit2 (kScanCategorical) a categorical split: `left` is its set's child
     QBin left;
     QBin right;
 };
@@ -403,6 +415,15 @@ struct ScanArgs {
     ScanBest *best;          // n_nodes
     QBin *root_total;        // nodes flagged kScanDeviceRoot: their total (read, or written when dense)
     const GrowCounts *grow;  // non-null: nodes = 2 x its n_splits (the grid covers the most)
+    // categorical features: per feature its rank among them (0xffffffff:
+    // numeric), their count, each (node, categorical feature)'s best set and
+    // each node's winning set (kCatWords words each), or null without any
+    const uint32_t *cat_rank;
+    const uint32_t *cat_feature;  // the feature of each rank
+    uint32_t n_cat;
+    uint32_t pad2;
+    uint32_t *cat_sets;
+    uint32_t *best_sets;
 };
 
 // ScanNode.pad flag: the node's total is on the device and its root gain is

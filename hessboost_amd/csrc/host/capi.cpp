@@ -174,6 +174,31 @@ int hbr_cuts_from_csr(const uint64_t *row_ptr, const uint32_t *col, const float 
     });
 }
 
+int hbr_cuts_from_dense_typed(const float *x, uint64_t n, uint64_t f, uint32_t max_bin, const float *weights,
+                              float missing, const uint8_t *categorical, hbr_cuts **out) {
+    return guard([&] {
+        if (!out || (!x && n > 0 && f > 0) || max_bin < 2) fail(kInvalid, "cuts: bad arguments");
+        *out = new hbr_cuts{cuts_from_dense(x, n, f, max_bin, weights, missing, categorical)};
+    });
+}
+
+int hbr_cuts_from_csr_typed(const uint64_t *row_ptr, const uint32_t *col, const float *val, uint64_t n, uint64_t f,
+                            uint32_t max_bin, const float *weights, const uint8_t *categorical, hbr_cuts **out) {
+    return guard([&] {
+        if (!out || !row_ptr || max_bin < 2) fail(kInvalid, "cuts: bad arguments");
+        for (uint64_t e = 0; e < row_ptr[n]; e++)
+            if (col[e] >= f) fail(kInvalid, "cuts: column index beyond n_cols");
+        *out = new hbr_cuts{cuts_from_csr(row_ptr, col, val, n, f, max_bin, weights, categorical)};
+    });
+}
+
+int hbr_cuts_categorical(const hbr_cuts *c, uint8_t *out) {
+    return guard([&] {
+        if (!c || !out) fail(kInvalid, "null cuts");
+        for (uint32_t f = 0; f < c->c.n_cols(); f++) out[f] = c->c.is_categorical(f) ? 1 : 0;
+    });
+}
+
 int hbr_cuts_from_values(const uint32_t *fo, const float *values, uint64_t n_cols, hbr_cuts **out) {
     return guard([&] {
         if (!out || !fo || !values) fail(kInvalid, "cuts: bad arguments");
@@ -244,6 +269,7 @@ int hbr_index_describe(const hbr_index *h, hbr_index_desc *d) {
                       : ix.col_width == 4 ? (const void *)ix.cols32.data()
                                           : nullptr;
         d->missing = ix.missing.empty() ? nullptr : ix.missing.data();
+        d->is_categorical = ix.cuts.categorical.empty() ? nullptr : ix.cuts.categorical.data();
     });
 }
 
@@ -655,6 +681,22 @@ int hbr_trainer_tree(hbr_trainer *t, uint64_t tree, uint32_t *split_feature, flo
             if (split_gain) split_gain[i] = n.split_gain;
             if (split_bin) split_bin[i] = n.split_bin;
         }
+    });
+}
+
+int hbr_trainer_tree_categories(hbr_trainer *t, uint64_t tree, uint8_t *is_categorical, uint32_t *cat_begin,
+                                uint32_t *cat_end, uint32_t *categories, uint64_t *n_categories) {
+    if (!t) return set_error(HBR_INVALID, "null trainer");
+    return guard([&] {
+        if (tree >= t->t->trees().size()) fail(kInvalid, "no such tree");
+        const Tree &tr = t->t->trees()[tree];
+        for (size_t i = 0; i < tr.nodes.size(); i++) {
+            if (is_categorical) is_categorical[i] = tr.nodes[i].is_categorical;
+            if (cat_begin) cat_begin[i] = tr.nodes[i].cat_begin;
+            if (cat_end) cat_end[i] = tr.nodes[i].cat_end;
+        }
+        if (categories) std::memcpy(categories, tr.categories.data(), tr.categories.size() * sizeof(uint32_t));
+        if (n_categories) *n_categories = tr.categories.size();
     });
 }
 

@@ -248,14 +248,40 @@ private:
 
 bool absent(float v, float missing) { return std::isnan(missing) ? std::isnan(v) : v == missing; }
 
-Cuts assemble(std::vector<std::vector<float>> &per) {
+Cuts assemble(std::vector<std::vector<float>> &per, const uint8_t *categorical) {
     Cuts c;
     c.feature_offset.push_back(0);
     for (auto &v : per) {
         c.values.insert(c.values.end(), v.begin(), v.end());
         c.feature_offset.push_back((uint32_t)c.values.size());
     }
+    if (categorical)
+        for (size_t j = 0; j < per.size(); j++) c.categorical.push_back(categorical[j] ? 1 : 0);
     return c;
+}
+
+// f32::total_cmp as an unsigned key
+uint32_t total_order(float v) {
+    uint32_t b;
+    std::memcpy(&b, &v, 4);
+    return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+
+// A categorical feature's cuts (quantile.rs:524-672, build_categorical_cuts
+// :676-689): the present values sorted by total_cmp, deduplicated by bit
+// pattern, then one bin per value that differs (`!=`) from the one before;
+// a feature without a present value keeps one degenerate bin at 0.
+std::vector<float> category_cuts(std::vector<float> vals) {
+    std::sort(vals.begin(), vals.end(), [](float a, float b) { return total_order(a) < total_order(b); });
+    vals.erase(std::unique(vals.begin(), vals.end(),
+                           [](float a, float b) { return std::memcmp(&a, &b, 4) == 0; }),
+               vals.end());
+    std::vector<float> out;
+    if (vals.empty()) return {0.0f};
+    out.push_back(vals[0]);
+    for (size_t i = 1; i < vals.size(); i++)
+        if (vals[i - 1] != vals[i]) out.push_back(vals[i]);
+    return out;
 }
 
 }  // namespace
@@ -263,18 +289,32 @@ Cuts assemble(std::vector<std::vector<float>> &per) {
 uint32_t Cuts::bin_of(uint32_t f, float v) const {
     const float *lo = values.data() + feature_offset[f];
     const float *hi = values.data() + feature_offset[f + 1];
+    if (is_categorical(f)) {
+        // the bin whose category equals v, else the feature's first bin
+        const float *at = std::lower_bound(lo, hi, v);
+        return feature_offset[f] + (at != hi && *at == v ? (uint32_t)(at - lo) : 0u);
+    }
     const size_t n = (size_t)(hi - lo);
     size_t k = (size_t)(std::upper_bound(lo, hi, v) - lo);
     if (k > n - 1) k = n - 1;
     return feature_offset[f] + (uint32_t)k;
 }
 
-Cuts cuts_from_dense(const float *x, uint64_t n, uint64_t f, uint32_t max_bin, const float *weights, float missing) {
+Cuts cuts_from_dense(const float *x, uint64_t n, uint64_t f, uint32_t max_bin, const float *weights, float missing,
+                     const uint8_t *categorical) {
     std::vector<std::vector<float>> per(f);
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t j = 0; j < (int64_t)f; j++) {
         size_t present = 0;
         for (uint64_t r = 0; r < n; r++) present += !absent(x[r * f + j], missing);
+        if (categorical && categorical[j]) {
+            std::vector<float> vals;
+            vals.reserve(present);
+            for (uint64_t r = 0; r < n; r++)
+                if (!absent(x[r * f + j], missing)) vals.push_back(x[r * f + j]);
+            per[j] = category_cuts(std::move(vals));
+            continue;
+        }
         Sketch s(present, max_bin);
         for (uint64_t r = 0; r < n; r++) {
             const float v = x[r * f + j];
@@ -282,22 +322,29 @@ Cuts cuts_from_dense(const float *x, uint64_t n, uint64_t f, uint32_t max_bin, c
         }
         per[j] = s.cut_values();
     }
-    return assemble(per);
+    return assemble(per, categorical);
 }
 
 Cuts cuts_from_csr(const uint64_t *row_ptr, const uint32_t *col, const float *val, uint64_t n, uint64_t f,
-                   uint32_t max_bin, const float *weights) {
+                   uint32_t max_bin, const float *weights, const uint8_t *categorical) {
     std::vector<std::vector<std::pair<uint32_t, float>>> csc(f);
     for (uint64_t r = 0; r < n; r++)
         for (uint64_t e = row_ptr[r]; e < row_ptr[r + 1]; e++) csc[col[e]].push_back({(uint32_t)r, val[e]});
     std::vector<std::vector<float>> per(f);
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t j = 0; j < (int64_t)f; j++) {
+        if (categorical && categorical[j]) {
+            std::vector<float> vals;
+            vals.reserve(csc[j].size());
+            for (auto &rv : csc[j]) vals.push_back(rv.second);
+            per[j] = category_cuts(std::move(vals));
+            continue;
+        }
         Sketch s(csc[j].size(), max_bin);
         for (auto &rv : csc[j]) s.push(rv.second, weights ? weights[rv.first] : 1.0f);
         per[j] = s.cut_values();
     }
-    return assemble(per);
+    return assemble(per, categorical);
 }
 
 namespace {

@@ -111,6 +111,25 @@ void Engine::upload_index(const hbr_index_desc &d) {
     d_fo_.resize(n_cols_ + 1);
     d_fo_.upload(fo_.data(), n_cols_ + 1, s);
     words_ = (uint32_t)((n_rows_ + 63) / 64);
+    if (d.is_categorical) {
+        cat_rank_.assign(n_cols_, 0xffffffffu);
+        for (uint32_t f = 0; f < n_cols_; f++) {
+            if (!d.is_categorical[f]) continue;
+            if (fo_[f + 1] - fo_[f] > kCatMaxBins) fail(kRefused, "index: a categorical feature beyond 1,024 categories");
+            cat_rank_[f] = (uint32_t)cat_feature_.size();
+            cat_feature_.push_back(f);
+        }
+        n_cat_ = (uint32_t)cat_feature_.size();
+        if (n_cat_) {
+            d_cat_rank_.resize(n_cols_);
+            d_cat_rank_.upload(cat_rank_.data(), n_cols_, s);
+            d_cat_feature_.resize(n_cat_);
+            d_cat_feature_.upload(cat_feature_.data(), n_cat_, s);
+            d_root_set_.resize(kCatWords);
+        } else {
+            cat_rank_.clear();
+        }
+    }
 
     if (dense_ && widest <= 256 && n_cols_ > 0) {
         dense_u8_ = true;
@@ -694,17 +713,24 @@ void Engine::launch_root(const Segment &seg, uint32_t slot, float lower, float u
     HBR_HIP(hipMemcpyAsync(rdev, rin, sizeof(RootIn), hipMemcpyHostToDevice, s));
     const std::vector<HistNode> one{hn};
     launch_hist(&rdev->h, 1, &one, nullptr, nullptr);
-    launch_scan(&rdev->s, 1, nullptr, nullptr, root_best_dev());
+    launch_scan(&rdev->s, 1, nullptr, nullptr, root_best_dev(), nullptr, n_cat_ ? d_root_set_.get() : nullptr);
 }
 
-bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best) {
+bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best,
+                       uint32_t *best_set) {
     hipStream_t s = dev_.stream();
     launch_root(seg, slot, lower, upper);
     RootBlock *rb = static_cast<RootBlock *>(stage_.alloc(sizeof(RootBlock)));
     HBR_HIP(hipMemcpyAsync(rb, root_block(), sizeof(RootBlock), hipMemcpyDeviceToHost, s));
+    uint32_t *set = nullptr;
+    if (n_cat_) {
+        set = static_cast<uint32_t *>(stage_.alloc(kCatWords * sizeof(uint32_t)));
+        HBR_HIP(hipMemcpyAsync(set, d_root_set_.get(), kCatWords * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    }
     dev_.sync();
     *best = rb->best;
     *total = rb->total;
+    if (best_set && set) std::memcpy(best_set, set, kCatWords * sizeof(uint32_t));
     const QScale host = rb->scale;
     stage_.reset();
     if (scale_checked_) return true;
@@ -884,7 +910,8 @@ void Engine::subtract(const std::vector<uint32_t> &parents, const std::vector<ui
 }
 
 void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit *splits_dev,
-                         const PartOut *part_out_dev, ScanBest *best_dev, const GrowCounts *grow) {
+                         const PartOut *part_out_dev, ScanBest *best_dev, const GrowCounts *grow,
+                         uint32_t *best_sets_dev) {
     const uint64_t pairs = (uint64_t)n * n_cols_;
     d_per_feature_.reserve(pairs ? pairs : 1);
     ScanArgs a{};
@@ -904,7 +931,17 @@ void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit 
     a.best = best_dev;
     a.root_total = level_totals_ ? level_totals_ : total_dev();
     a.grow = grow;
+    if (n_cat_) {
+        if (grow) fail(kInvalid, "scan: device-counted levels have no categorical sweep");
+        d_cat_sets_.reserve((size_t)n * n_cat_ * kCatWords);
+        a.cat_rank = d_cat_rank_.get();
+        a.cat_feature = d_cat_feature_.get();
+        a.n_cat = n_cat_;
+        a.cat_sets = d_cat_sets_.get();
+        a.best_sets = best_sets_dev;
+    }
     dev_.launch("hbr_scan_features", dim3(ceil_div(pairs, 4)), dim3(256), a);
+    if (n_cat_) dev_.launch("hbr_scan_categorical", dim3(n * n_cat_), dim3(64), a);
     dev_.launch("hbr_scan_merge", dim3(n), dim3(64), a);
 }
 
@@ -921,6 +958,7 @@ void Engine::scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out) 
 std::vector<ScanBest> Engine::scan(const std::vector<ScanInput> &in) {
     std::vector<ScanBest> out(in.size());
     if (in.empty()) return out;
+    if (n_cat_) fail(kRefused, "scan: categorical features are searched by the engine's own tree growth");
     std::vector<ScanNode> nodes(in.size());
     for (size_t i = 0; i < in.size(); i++) {
         ScanNode n{};
@@ -985,8 +1023,12 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
     const size_t o_splits = in.add(P * sizeof(PartSplit));
     const size_t o_hnodes = terminal ? 0 : in.add(P * sizeof(HistNode));
     const size_t o_snodes = terminal ? 0 : in.add(2 * P * sizeof(ScanNode));
+    uint32_t n_tables = 0;
+    for (const LevelSplit &l : splits) n_tables += l.categorical ? 1u : 0u;
+    const size_t o_tables = n_tables ? in.add((size_t)n_tables * kCatWords * sizeof(uint32_t)) : 0;
     const size_t o_pout = out.add(P * sizeof(PartOut));
     const size_t o_best = terminal ? 0 : out.add(2 * P * sizeof(ScanBest));
+    const size_t o_sets = terminal || !n_cat_ ? 0 : out.add(2 * P * kCatWords * sizeof(uint32_t));
     char *host_in = static_cast<char *>(stage_.alloc(in.bytes));
     char *host_out = static_cast<char *>(stage_.alloc(out.bytes));
     d_level_in_.reserve(in.bytes);
@@ -995,8 +1037,9 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
     char *dev_out = reinterpret_cast<char *>(d_level_out_.get());
 
     PartSplit *ps = reinterpret_cast<PartSplit *>(host_in + o_splits);
+    uint32_t *tables = n_tables ? reinterpret_cast<uint32_t *>(host_in + o_tables) : nullptr;
     std::vector<uint32_t> fresh(P, 0);
-    uint32_t tiles = 0;
+    uint32_t tiles = 0, table = 0;
     for (uint32_t i = 0; i < P; i++) {
         const LevelSplit &l = splits[i];
         PartSplit p{};
@@ -1004,6 +1047,11 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
         p.feature = l.feature;
         p.limit = l.limit;
         p.default_left = l.default_left;
+        if (l.categorical) {
+            if (!is_categorical(l.feature)) fail(kInvalid, "level: a categorical split on a numeric feature");
+            std::memcpy(tables + (size_t)table * kCatWords, l.table.data(), kCatWords * sizeof(uint32_t));
+            p.table = ++table;
+        }
         p.identity = contiguous(l.seg) ? 1u : 0u;
         p.tile_begin = tiles;
         if (!terminal) {
@@ -1049,6 +1097,7 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
     a.n_splits = P;
     a.n_tiles = tiles;
     a.out = pout_dev;
+    a.cat_tables = n_tables ? reinterpret_cast<const uint32_t *>(dev_in + o_tables) : nullptr;
     dev_.launch("hbr_part_count", dim3(tiles), dim3(kPartThreads), a);
     dev_.launch("hbr_part_scan", dim3(P), dim3(1024), a);
     dev_.launch("hbr_part_scatter", dim3(tiles), dim3(kPartThreads), a);
@@ -1060,7 +1109,8 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
             dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), sub);
         }
         launch_scan(reinterpret_cast<const ScanNode *>(dev_in + o_snodes), 2 * P, splits_dev, pout_dev,
-                    reinterpret_cast<ScanBest *>(dev_out + o_best));
+                    reinterpret_cast<ScanBest *>(dev_out + o_best), nullptr,
+                    n_cat_ ? reinterpret_cast<uint32_t *>(dev_out + o_sets) : nullptr);
     }
     HBR_HIP(hipMemcpyAsync(host_out, dev_out, out.bytes, hipMemcpyDeviceToHost, s));
     dev_.sync();
@@ -1080,6 +1130,11 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
             R.slot = built_left ? splits[i].parent_slot : fresh[i];
             L.best = best_staged[2 * i];
             R.best = best_staged[2 * i + 1];
+            if (n_cat_) {
+                const uint32_t *sets = reinterpret_cast<const uint32_t *>(host_out + o_sets);
+                std::memcpy(L.best_set.data(), sets + (size_t)(2 * i) * kCatWords, kCatWords * sizeof(uint32_t));
+                std::memcpy(R.best_set.data(), sets + (size_t)(2 * i + 1) * kCatWords, kCatWords * sizeof(uint32_t));
+            }
             const uint32_t built = built_left ? nl : pseg.len - nl;
             counters.hist_nodes++;
             counters.hist_rows += built;
@@ -1101,6 +1156,7 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
 // one copy after the last level.
 bool Engine::can_grow_device(uint64_t max_depth, uint32_t n_trees) const {
     if (!device_grow || !dense_u8_ || max_depth < 1 || max_depth > kMaxDeviceDepth || n_rows_ == 0) return false;
+    if (n_cat_) return false;  // categorical splits are decided by the host
     if (n_trees < 1 || n_trees > kGrowMaxTrees || (uint64_t)n_trees * n_rows_ > UINT32_MAX) return false;
     const uint64_t slots = (uint64_t)n_trees << (max_depth - 1);
     if (slots > kGrowMaxSlots) return false;
@@ -1419,6 +1475,7 @@ uint32_t Engine::add_eval_set(const float *x, uint64_t n_rows, uint64_t n_cols, 
                               uint32_t outputs) {
     if (!x || !init) fail(kInvalid, "evaluation set: null argument");
     if (n_cols != n_cols_) fail(kInvalid, "evaluation set: not the training matrix's features");
+    if (n_cat_) fail(kRefused, "evaluation set: the device walk does not route categorical splits");
     if (n_rows == 0) fail(kInvalid, "evaluation set: no rows");
     if (outputs == 0) fail(kInvalid, "evaluation set: no outputs");
     hipStream_t s = dev_.stream();

@@ -3,6 +3,7 @@
 // steps the tree builder drives (the reference's HistogramBackend and
 // RowEngine, src/tree/hist/mod.rs:73-295).
 #pragma once
+#include <array>
 #include <algorithm>
 #include <memory>
 #include <cstdint>
@@ -29,6 +30,9 @@ struct LevelSplit {
     uint32_t feature = 0;
     uint32_t limit = 0;        // present local bins below go left
     uint32_t default_left = 0;
+    // a categorical split: the local bins that go left (RowRule::Table)
+    bool categorical = false;
+    std::array<uint32_t, kCatWords> table{};
     // child scan inputs (non-terminal levels)
     QBin child_total[2];
     float child_root_gain[2];
@@ -39,6 +43,7 @@ struct LevelChild {
     Segment seg;
     uint32_t slot = 0;
     ScanBest best;  // valid when the level was not terminal
+    std::array<uint32_t, kCatWords> best_set{};  // the local bins of a categorical winner's set
 };
 
 struct ScanInput {
@@ -104,7 +109,15 @@ public:
     void compute_gradients_async(const hbr_device_loss &loss, uint32_t output);
     // The root's total, histogram (into `slot`) and split search with one
     // host synchronisation; false when a gradient is not finite.
-    bool grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best);
+    // best_set (kCatWords words, may be null) receives a categorical
+    // winner's set.
+    bool grow_root(const Segment &seg, uint32_t slot, float lower, float upper, QBin *total, ScanBest *best,
+                   uint32_t *best_set = nullptr);
+    // Categorical features (HistCuts::is_categorical): at most kCatMaxBins
+    // bins each. Their trees are grown by host-decided levels: the device
+    // sweeps them (hbr_scan_categorical) and routes by table.
+    bool has_categorical() const { return n_cat_ > 0; }
+    bool is_categorical(uint32_t f) const { return n_cat_ > 0 && cat_rank_[f] != 0xffffffffu; }
     // Softmax gradients of every class (the margins' outputs, at most
     // kSoftmaxMaxClasses) from the device margins, with the host's bits,
     // class-major on the device, each class's scale folded; no
@@ -148,7 +161,7 @@ public:
     // Dense u8 index: margins of output `output` += the leaf each row reaches
     // through the tree (meta/left/value as WalkArgs lays them out); needs no
     // row segments, so the depth limit's level can skip its partition.
-    bool can_walk() const { return dense_u8_; }
+    bool can_walk() const { return dense_u8_ && n_cat_ == 0; }
     // With next_loss, the same pass also computes the next round's gradients
     // of the updated margins (like compute_gradients_async; can_walk_gradients).
     void walk_add(const std::vector<uint32_t> &meta, const std::vector<uint32_t> &left,
@@ -267,7 +280,7 @@ private:
                      const PartSplit *splits_dev, const PartOut *part_out_dev, const uint32_t *rows0 = nullptr,
                      const GrowCounts *grow = nullptr);
     void launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit *splits_dev, const PartOut *part_out_dev,
-                     ScanBest *best_dev, const GrowCounts *grow = nullptr);
+                     ScanBest *best_dev, const GrowCounts *grow = nullptr, uint32_t *best_sets_dev = nullptr);
     // the root's total, histogram and split search, queued (no synchronisation)
     void launch_root(const Segment &seg, uint32_t slot, float lower, float upper);
     // the roots of a device-grown batch (root t in slot t, of class t,
@@ -410,6 +423,11 @@ private:
     DBuf<uint8_t> d_walk_;  // a tree's meta, left and value tables, one after another
     DBuf<ScanNode> d_snodes_;
     DBuf<ScanBest> d_per_feature_, d_best_;
+    // categorical features: rank per feature, feature per rank, their
+    // per-(node, feature) sets and the root's winning set
+    uint32_t n_cat_ = 0;
+    std::vector<uint32_t> cat_rank_, cat_feature_;
+    DBuf<uint32_t> d_cat_rank_, d_cat_feature_, d_cat_sets_, d_root_set_;
     DBuf<LeafSeg> d_leaves_;
     DBuf<uint32_t> d_tile_leaf_, d_tile_row0_;
 

@@ -1,5 +1,6 @@
 #include "trainer.h"
 
+#include <algorithm>
 #include <cfloat>
 #include <cmath>
 #include <cstdlib>
@@ -37,7 +38,15 @@ TreeBuilder::Decision TreeBuilder::decide(const Open &o) const {
     const uint32_t f = b.feature, fs = fo[f], nb = fo[f + 1] - fs;
     d.feature = f;
     d.loss = (double)b.loss;
-    if (b.index < nb) {
+    if (b.flags & kScanCategorical) {
+        // the set's child on the left, missing values as flags bit 0 says
+        // (BestSplit::categorical with the children swapped, builder/categorical.rs:83-96)
+        d.categorical = true;
+        d.set = &o.best_set;
+        d.bin = -1;
+        d.limit = 0;
+        d.default_left = b.flags & 1u;
+    } else if (b.index < nb) {
         d.bin = (int64_t)fs + b.index;
         d.limit = b.index + 1;
         d.default_left = 0;
@@ -59,16 +68,53 @@ TreeBuilder::Decision TreeBuilder::decide(const Open &o) const {
     return d;
 }
 
+// A category code: the saturating `value as u32` of the category's cut
+// (in_category_set, tree/mod.rs:34-58).
+static uint32_t category_code(float v) {
+    if (!(v >= 0.0f)) return 0;
+    if (v >= 4294967296.0f) return 0xffffffffu;
+    return (uint32_t)v;
+}
+
 LevelSplit TreeBuilder::expand(Tree &t, const Open &o, const Decision &d, double cb[4]) {
     const int dir = d.feature < p_.monotone.size() ? p_.monotone[d.feature] : 0;
-    child_bounds(o.lower, o.upper, dir, (double)d.wl, (double)d.wr, cb);
+    if (d.categorical) {
+        // bounds in the orientation the split was scored in (builder/mod.rs:175-182)
+        double sw[4];
+        child_bounds(o.lower, o.upper, dir, (double)d.wr, (double)d.wl, sw);
+        cb[0] = sw[2];
+        cb[1] = sw[3];
+        cb[2] = sw[0];
+        cb[3] = sw[1];
+    } else {
+        child_bounds(o.lower, o.upper, dir, (double)d.wl, (double)d.wr, cb);
+    }
     TreeNode &n = t.nodes[o.nid];
     n.split_feature = d.feature;
-    n.split_cond = d.bin >= 0 ? e_.cut_values()[d.bin] : -FLT_MAX;
+    n.split_cond = d.categorical ? 0.0f : (d.bin >= 0 ? e_.cut_values()[d.bin] : -FLT_MAX);
     n.default_left = (uint8_t)d.default_left;
     n.split_bin = d.bin;
     n.split_limit = d.limit;
     n.split_gain = (float)d.loss;
+    std::array<uint32_t, kCatWords> table{};
+    if (d.categorical) {
+        // the set's codes, sorted (BestSplit's set.sort_unstable()), into the
+        // tree's pool; rows go left by their bin's code (categories_left,
+        // quantile.rs:316-333)
+        const auto &fo = e_.feature_offset();
+        const uint32_t fs = fo[d.feature], nb = fo[d.feature + 1] - fs;
+        std::vector<uint32_t> codes;
+        for (uint32_t i = 0; i < nb; i++)
+            if ((*d.set)[i / 32] >> (i % 32) & 1u) codes.push_back(category_code(e_.cut_values()[fs + i]));
+        std::sort(codes.begin(), codes.end());
+        n.is_categorical = 1;
+        n.cat_begin = (uint32_t)t.categories.size();
+        t.categories.insert(t.categories.end(), codes.begin(), codes.end());
+        n.cat_end = (uint32_t)t.categories.size();
+        for (uint32_t i = 0; i < nb; i++)
+            if (std::binary_search(codes.begin(), codes.end(), category_code(e_.cut_values()[fs + i])))
+                table[i / 32] |= 1u << (i % 32);
+    }
     const int32_t left = (int32_t)t.nodes.size();
     n.left = left;
     n.right = left + 1;
@@ -93,6 +139,8 @@ LevelSplit TreeBuilder::expand(Tree &t, const Open &o, const Decision &d, double
     s.feature = d.feature;
     s.limit = d.limit;
     s.default_left = d.default_left;
+    s.categorical = d.categorical;
+    s.table = table;
     s.child_total[0] = d.left;
     s.child_total[1] = d.right;
     s.child_root_gain[0] = xgb_node_gain(d.lg, d.lh, p_.reg, cb[0], cb[1]);
@@ -183,7 +231,8 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool 
         // computed on the device from the device total)
         root.slot = e_.alloc_slot();
         root.has_slot = true;
-        if (!e_.grow_root(root.seg, root.slot, (float)root.lower, (float)root.upper, &root.total, &root.best))
+        if (!e_.grow_root(root.seg, root.slot, (float)root.lower, (float)root.upper, &root.total, &root.best,
+                          root.best_set.data()))
             fail(kRefused, "a gradient is not finite: the round runs on the host");
         root.searched = true;
     } else {
@@ -238,6 +287,7 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool 
                         ch.slot = kids[2 * i + c].slot;
                         ch.has_slot = true;
                         ch.best = kids[2 * i + c].best;
+                        ch.best_set = kids[2 * i + c].best_set;
                         ch.searched = true;
                         next.push_back(ch);
                     }
@@ -325,6 +375,7 @@ Tree TreeBuilder::grow(std::vector<std::pair<Segment, float>> *leaves_out, bool 
                 ch.lower = lower_[ch.nid];
                 ch.upper = upper_[ch.nid];
                 ch.best = kids[c].best;
+                ch.best_set = kids[c].best_set;
                 ch.searched = true;
                 push(ch);
             }

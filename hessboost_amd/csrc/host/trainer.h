@@ -29,10 +29,15 @@ struct TreeNode {
     float leaf_value = 0.0f, sum_hess = 0.0f, split_gain = 0.0f;
     int64_t split_bin = -2;
     uint32_t split_limit = 0;  // present local bins below go left
+    // a categorical split (regtree.rs:59-66): its categories, which go left,
+    // are the tree's categories[cat_begin, cat_end)
+    uint8_t is_categorical = 0;
+    uint32_t cat_begin = 0, cat_end = 0;
 };
 
 struct Tree {
     std::vector<TreeNode> nodes;
+    std::vector<uint32_t> categories;
 };
 
 struct GrowParams {
@@ -70,6 +75,7 @@ private:
         QBin total;
         double lower, upper;
         ScanBest best;
+        std::array<uint32_t, kCatWords> best_set;  // a categorical winner's local bins
         bool searched;
     };
     struct Decision {
@@ -82,6 +88,8 @@ private:
         double lg = 0, lh = 0, rg = 0, rh = 0;
         float wl = 0, wr = 0;
         double loss = 0.0;
+        bool categorical = false;
+        const std::array<uint32_t, kCatWords> *set = nullptr;
     };
     Decision decide(const Open &o) const;
     // Expand node o by d: children appended to the tree; returns the level split.

@@ -2,8 +2,9 @@
 //
 // Replaces partition_rows (builder/partition.rs:106-242) for every split of a
 // level at once: a present local bin of the split feature below `limit`
-// goes left, a missing value follows default_left, and both children keep
-// the parent's ascending row order (left child first in the segment).
+// (for a categorical split: whose bit is set in its table) goes left, a
+// missing value follows default_left, and both children keep the parent's
+// ascending row order (left child first in the segment).
 //
 // Three passes over fixed tiles of kPartTile rows: count the left rows of
 // each tile (keeping each wave's 64-row ballot of decisions), scan the tile
@@ -18,6 +19,15 @@ namespace hbr {
 constexpr uint32_t kRowsPerThread = kPartTile / kPartThreads;  // 8
 constexpr uint32_t kBallots = kPartTile / kWave;                // 32 per tile
 
+// A present row's direction from its local bin: below the limit, or, for a
+// categorical split (RowRule::Table, src/tree/hist/mod.rs:173-178), the
+// bin's bit in the split's table (local bins of a categorical feature are
+// below kCatMaxBins).
+__device__ __forceinline__ bool present_left(const PartArgs &a, const PartSplit &sp, uint32_t local) {
+    if (sp.table) return (a.cat_tables[(size_t)(sp.table - 1u) * kCatWords + (local >> 5)] >> (local & 31u)) & 1u;
+    return local < sp.limit;
+}
+
 __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp, uint32_t r) {
     if (a.dense) {
         const size_t at = (size_t)sp.feature * a.n_rows + r;
@@ -26,7 +36,7 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
             if ((word >> (r & 63)) & 1ull) return sp.default_left != 0;
         }
         const uint32_t local = a.cols8 ? (uint32_t)a.cols8[at] : (uint32_t)a.cols16[at];
-        return local < sp.limit;
+        return present_left(a, sp, local);
     }
     // a row's global bins ascend (its entries are in feature order, and a
     // feature's bins follow the previous feature's): the first bin >= fs,
@@ -35,7 +45,7 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
     if (!a.csr_ascending) {  // entries in the caller's order: scan them
         for (uint64_t e = a.row_ptr[r]; e < a.row_ptr[r + 1]; e++) {
             const uint32_t gb = a.gbins[e];
-            if (gb >= fs && gb < fe) return gb - fs < sp.limit;
+            if (gb >= fs && gb < fe) return present_left(a, sp, gb - fs);
         }
         return sp.default_left != 0;
     }
@@ -47,7 +57,7 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
     }
     if (lo < a.row_ptr[r + 1]) {
         const uint32_t gb = a.gbins[lo];
-        if (gb < fe) return gb - fs < sp.limit;
+        if (gb < fe) return present_left(a, sp, gb - fs);
     }
     return sp.default_left != 0;
 }
@@ -91,7 +101,7 @@ __device__ __forceinline__ void route_dense8(const PartArgs &a, const PartSplit 
     }
 #pragma unroll
     for (uint32_t k = 0; k < kRowsPerThread; k++) {
-        bool l = b[k] < sp.limit;
+        bool l = r[k] != 0xffffffffu && present_left(a, sp, b[k]);
         if constexpr (MISSING) {
             if ((w[k] >> (r[k] & 63u)) & 1ull) l = sp.default_left != 0;
         }

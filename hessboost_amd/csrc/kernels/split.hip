@@ -144,7 +144,9 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
         tg = root_total->g;
         th = root_total->h;
     }
-    if (nb > 1) {
+    // a categorical feature's record comes from hbr_scan_categorical
+    const bool categorical = a.cat_rank && a.cat_rank[f] != 0xffffffffu;
+    if (nb > 1 && !categorical) {
         const int eg = a.scale[cls].exp_g, eh = a.scale[cls].exp_h;
         const int dir = a.monotone ? (int)a.monotone[f] : 0;
         const float root_gain = dev_root ? node_gain(dequant(tg, eg), dequant(th, eh), a.reg, nd.lower, nd.upper)
@@ -291,5 +293,235 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_merge(ScanArgs a) {
             o.flags |= nan_flag;
         }
         a.best[node] = o;
+    }
+    // a categorical winner's set, for the host's decision and partition
+    const uint32_t win = (uint32_t)__shfl((int)bf, 0, kWave);
+    if (a.best_sets && a.cat_rank && win != 0xffffffffu && a.cat_rank[win] != 0xffffffffu) {
+        const uint32_t *src = a.cat_sets + ((size_t)node * a.n_cat + a.cat_rank[win]) * kCatWords;
+        for (uint32_t w = lane; w < kCatWords; w += kWave) a.best_sets[(size_t)node * kCatWords + w] = src[w];
+    }
+}
+
+// ---- categorical features (builder/categorical.rs:48-170) ---------------------
+
+namespace hbr {
+
+// xgb_calc_weight (builder/shared.rs:86-97): unbounded, f64.
+__device__ __forceinline__ double calc_weight(double g, double h, const ScanParams &r) {
+    if (h <= 0.0) return 0.0;
+    double w = -threshold_l1(g, r.alpha) / (h + r.lambda);
+    if (r.max_delta_step != 0.0 && __builtin_fabs(w) > r.max_delta_step) w = __builtin_copysign(r.max_delta_step, w);
+    return w;
+}
+
+// need_replace (builder/mod.rs:313-326) against the feature's own entry.
+__device__ __forceinline__ bool beats(float loss, bool has, float incumbent) {
+    if (__builtin_isinf(loss) || __builtin_isnan(loss)) return false;
+    return loss > (has ? incumbent : 0.0f);
+}
+
+}  // namespace hbr
+
+// One wave per (node, categorical feature): XGBoost's categorical sweep.
+// Fewer than 4 categories: each alone, with missing values on either side
+// (one-hot). Otherwise the categories stably sorted by their weight
+// (CalcWeightCat: 0 below min_child_weight), then at most 64 deep a growing
+// prefix of the order on one side scanned forward (missing values on the
+// other side) and a growing suffix scanned backward (missing values with
+// the prefix). Each candidate is scored as the numeric ones are; a
+// direction keeps its first best, the backward best replaces the forward
+// one only when strictly greater. Every category of the feature takes part,
+// a category the node lacks with zero statistics. The record is written in
+// the recorded orientation: `left` is the set's child (the child XGBoost
+// calls right), flags bit0 sends missing values left, and the set (local
+// bins) goes to cat_sets.
+extern "C" __global__ __launch_bounds__(64) void hbr_scan_categorical(ScanArgs a) {
+    __shared__ int64_t s_g[kCatMaxBins], s_h[kCatMaxBins];
+    __shared__ float s_key[kCatMaxBins];
+    __shared__ uint16_t s_order[kCatMaxBins], s_pos[kCatMaxBins];
+    const uint32_t pair = blockIdx.x;
+    if (pair >= scan_nodes(a) * a.n_cat) return;  // uniform per workgroup
+    const uint32_t lane = threadIdx.x;
+    const uint32_t node = pair / a.n_cat, rank = pair % a.n_cat;
+    const uint32_t f = a.cat_feature[rank];
+    const ScanNode nd = a.nodes[node];
+    const uint32_t fs = a.feature_offset[f];
+    const uint32_t nb = min(a.feature_offset[f + 1] - fs, kCatMaxBins);  // the host refuses wider ones
+    const QBin *h = a.hist + (size_t)node_slot(a, nd) * a.total_bins + fs;
+    const bool dev_root = (nd.pad & kScanDeviceRoot) != 0;
+    const uint32_t cls = nd.pad >> kScanClassShift;
+    int64_t tg = nd.total.g, th = nd.total.h;
+    if (dev_root) {  // written by hbr_scan_features or hbr_total, earlier on the stream
+        tg = a.root_total[cls].g;
+        th = a.root_total[cls].h;
+    }
+    const int eg = a.scale[cls].exp_g, eh = a.scale[cls].exp_h;
+    const int dir = a.monotone ? (int)a.monotone[f] : 0;
+    const float root_gain =
+        dev_root ? node_gain(dequant(tg, eg), dequant(th, eh), a.reg, nd.lower, nd.upper) : nd.root_gain;
+    for (uint32_t b = lane; b < nb; b += kWave) {
+        const QBin v = h[b];
+        s_g[b] = v.g;
+        s_h[b] = v.h;
+    }
+    __syncthreads();
+
+    // the winner: its children in XGBoost's orientation (right = the set)
+    bool has = false;
+    float best_loss = 0.0f;
+    uint32_t xgb_dl = 0, set_size = 0, chosen = 0;
+    int64_t lg = 0, lh = 0, rg = 0, rh = 0;
+    bool onehot = nb < 4;
+    if (onehot) {
+        if (lane == 0) {
+            int64_t pg = 0, ph = 0;
+            for (uint32_t i = 0; i < nb; i++) {
+                pg += s_g[i];
+                ph += s_h[i];
+            }
+            const int64_t mg = tg - pg, mh = th - ph;
+            for (uint32_t i = 0; i < nb; i++) {
+                for (uint32_t with_missing = 0; with_missing < 2; with_missing++) {
+                    const int64_t cg = s_g[i] + (with_missing ? mg : 0), ch = s_h[i] + (with_missing ? mh : 0);
+                    float loss;
+                    if (score(dequant(tg - cg, eg), dequant(th - ch, eh), dequant(cg, eg), dequant(ch, eh), a.reg,
+                              nd.lower, nd.upper, dir, root_gain, &loss) &&
+                        beats(loss, has, best_loss)) {
+                        has = true;
+                        best_loss = loss;
+                        xgb_dl = with_missing ? 0u : 1u;
+                        lg = tg - cg;
+                        lh = th - ch;
+                        rg = cg;
+                        rh = ch;
+                        chosen = i;
+                    }
+                }
+            }
+        }
+    } else {
+        for (uint32_t b = lane; b < nb; b += kWave) {
+            const double g = dequant(s_g[b], eg), hh = dequant(s_h[b], eh);
+            float k = hh < a.reg.min_child_weight ? 0.0f : (float)calc_weight(g, hh, a.reg);
+            s_key[b] = k != k ? 0.0f : k;  // a NaN weight cannot arise from finite pairs; keep the order total
+        }
+        __syncthreads();
+        // stable ascending order: position = smaller keys + equal keys before
+        for (uint32_t b = lane; b < nb; b += kWave) {
+            const float k = s_key[b];
+            uint32_t pos = 0;
+            for (uint32_t j = 0; j < nb; j++) {
+                const float kj = s_key[j];
+                pos += (kj < k || (kj == k && j < b)) ? 1u : 0u;
+            }
+            s_pos[b] = (uint16_t)pos;
+            s_order[pos] = (uint16_t)b;
+        }
+        __syncthreads();
+        const uint32_t depth = min(nb, 64u), steps = depth - 1;
+        float dl_loss[2];
+        bool dl_has[2];
+        uint32_t dl_step[2];
+        int64_t dl_acc[2][2];
+        for (uint32_t forward = 0; forward < 2; forward++) {  // 0: forward, 1: backward
+            const bool fw = forward == 0;
+            int64_t vg = 0, vh = 0;
+            if (lane < steps) {
+                const uint32_t b = s_order[fw ? lane : nb - 1 - lane];
+                vg = s_g[b];
+                vh = s_h[b];
+            }
+            const int64_t ag = wave_inclusive_scan(vg), ah = wave_inclusive_scan(vh);
+            float loss = -__builtin_inff();
+            bool ok = false;
+            if (lane < steps) {
+                if (fw)
+                    ok = score(dequant(tg - ag, eg), dequant(th - ah, eh), dequant(ag, eg), dequant(ah, eh), a.reg,
+                               nd.lower, nd.upper, dir, root_gain, &loss);
+                else
+                    ok = score(dequant(ag, eg), dequant(ah, eh), dequant(tg - ag, eg), dequant(th - ah, eh), a.reg,
+                               nd.lower, nd.upper, dir, root_gain, &loss);
+                ok = ok && beats(loss, false, 0.0f);
+            }
+            // the first step of the largest loss
+            float bl = ok ? loss : -__builtin_inff();
+            uint32_t bi = ok ? lane : 0xffffffffu;
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) {
+                const float ol = __shfl_xor(bl, d, kWave);
+                const uint32_t oi = (uint32_t)__shfl_xor((int)bi, d, kWave);
+                if (oi != 0xffffffffu && (bi == 0xffffffffu || ol > bl || (ol == bl && oi < bi))) {
+                    bl = ol;
+                    bi = oi;
+                }
+            }
+            dl_has[forward] = bi != 0xffffffffu;
+            dl_loss[forward] = bl;
+            dl_step[forward] = bi;
+            dl_acc[forward][0] = wave_broadcast(ag, dl_has[forward] ? (int)bi : 0);
+            dl_acc[forward][1] = wave_broadcast(ah, dl_has[forward] ? (int)bi : 0);
+        }
+        const uint32_t pick = dl_has[1] && (!dl_has[0] || dl_loss[1] > dl_loss[0]) ? 1u : 0u;
+        if (dl_has[pick]) {
+            has = true;
+            best_loss = dl_loss[pick];
+            const int64_t ag = dl_acc[pick][0], ah = dl_acc[pick][1];
+            if (pick == 0) {  // set = the scanned prefix, missing values on the other side
+                xgb_dl = 1;
+                lg = tg - ag;
+                lh = th - ah;
+                rg = ag;
+                rh = ah;
+                set_size = dl_step[0] + 1;
+            } else {  // set = the unscanned prefix, missing values with it
+                xgb_dl = 0;
+                lg = ag;
+                lh = ah;
+                rg = tg - ag;
+                rh = th - ah;
+                set_size = nb - 1 - dl_step[1];
+            }
+        }
+    }
+    if (onehot) {  // lane 0 holds the one-hot winner
+        has = __shfl((int)has, 0, kWave) != 0;
+        best_loss = __shfl(best_loss, 0, kWave);
+        xgb_dl = (uint32_t)__shfl((int)xgb_dl, 0, kWave);
+        chosen = (uint32_t)__shfl((int)chosen, 0, kWave);
+        lg = wave_broadcast(lg, 0);
+        lh = wave_broadcast(lh, 0);
+        rg = wave_broadcast(rg, 0);
+        rh = wave_broadcast(rh, 0);
+    }
+    uint32_t *set = a.cat_sets + ((size_t)node * a.n_cat + rank) * kCatWords;
+    for (uint32_t w = lane; w < kCatWords; w += kWave) {
+        uint32_t bits = 0;
+        if (has) {
+            for (uint32_t i = 0; i < 32; i++) {
+                const uint32_t b = 32 * w + i;
+                if (b >= nb) break;
+                const bool in = onehot ? b == chosen : (uint32_t)s_pos[b] < set_size;
+                bits |= in ? 1u << i : 0u;
+            }
+        }
+        set[w] = bits;
+    }
+    if (lane == 0) {
+        ScanBest o;
+        o.feature = f;
+        if (has) {
+            o.loss = best_loss;
+            o.index = 0;
+            o.flags = kScanCategorical | (xgb_dl ? 0u : 1u);  // recorded: the set's child on the left
+            o.left = QBin{rg, rh};
+            o.right = QBin{lg, lh};
+        } else {
+            o.loss = -__builtin_inff();
+            o.index = 0xffffffffu;
+            o.flags = 0;
+            o.left = QBin{0, 0};
+            o.right = QBin{0, 0};
+        }
+        a.per_feature[(size_t)node * a.n_features + f] = o;
     }
 }

@@ -66,6 +66,18 @@ int hbr_cuts_from_dense(const float *x, uint64_t n_rows, uint64_t n_cols, uint32
 int hbr_cuts_from_csr(const uint64_t *row_ptr, const uint32_t *col, const float *val,
                       uint64_t n_rows, uint64_t n_cols, uint32_t max_bin, const float *weights,
                       hbr_cuts **out);
+/* The same with feature types (the DMatrix's feature_types,
+ * src/data/quantile.rs:120-131): categorical[f] != 0 makes feature f
+ * categorical, one bin per distinct present value, ascending
+ * (quantile.rs:524-689; bin_of: the bin holding the value exactly, else the
+ * feature's first bin, :285-296). categorical may be NULL. */
+int hbr_cuts_from_dense_typed(const float *x, uint64_t n_rows, uint64_t n_cols, uint32_t max_bin,
+                              const float *weights, float missing, const uint8_t *categorical, hbr_cuts **out);
+int hbr_cuts_from_csr_typed(const uint64_t *row_ptr, const uint32_t *col, const float *val, uint64_t n_rows,
+                            uint64_t n_cols, uint32_t max_bin, const float *weights, const uint8_t *categorical,
+                            hbr_cuts **out);
+/* Per feature 1 when categorical (n_cols bytes). */
+int hbr_cuts_categorical(const hbr_cuts *c, uint8_t *out);
 /* Cuts given by the caller (feature_offset[n_cols+1], cut_values). */
 int hbr_cuts_from_values(const uint32_t *feature_offset, const float *cut_values, uint64_t n_cols,
                          hbr_cuts **out);
@@ -99,6 +111,7 @@ typedef struct hbr_index_desc {
     uint32_t col_bin_width;         /* 1, 2 or 4 */
     uint32_t pad;
     const uint64_t *missing;        /* ceil(n_rows/64) words per feature, bit set = missing; or NULL */
+    const uint8_t *is_categorical;  /* per feature (HistCuts::is_categorical), or NULL: every feature numeric */
 } hbr_index_desc;
 
 /* A read-only view of an index built by hbr_index_from_* (valid while it lives). */
@@ -419,6 +432,13 @@ int hbr_trainer_tree_size(hbr_trainer *t, uint64_t tree, uint64_t *n_nodes);
 int hbr_trainer_tree(hbr_trainer *t, uint64_t tree, uint32_t *split_feature, float *split_cond,
                      uint8_t *default_left, int32_t *left, int32_t *right, float *leaf_value,
                      float *sum_hess, float *split_gain, int64_t *split_bin);
+/* A tree's categorical splits (src/tree/regtree.rs:59-66): per node
+ * is_categorical, and the range [cat_begin, cat_end) of the tree's pool of
+ * categories that go left; the pool's length in *n_categories (call first
+ * with categories NULL to size it). Trees grown on an index with
+ * categorical features (hbr_cuts_from_*_typed) hold them. */
+int hbr_trainer_tree_categories(hbr_trainer *t, uint64_t tree, uint8_t *is_categorical, uint32_t *cat_begin,
+                                uint32_t *cat_end, uint32_t *categories, uint64_t *n_categories);
 /* The training margins (n_rows * n_outputs). */
 int hbr_trainer_margins(hbr_trainer *t, float *out);
 /* An evaluation set (the `evals` of training, src/training/margins.rs:148-152

@@ -8,14 +8,15 @@ import hessboost_amd as hb
 from oracle import oracle as O
 
 
-def _compare(x=None, csr=None, n_cols=None, max_bin=256, weights=None, missing=np.nan):
+def _compare(x=None, csr=None, n_cols=None, max_bin=256, weights=None, missing=np.nan, feature_types=None):
     if csr is not None:
-        ref = O.Dataset(csr=csr, n_cols=n_cols, max_bin=max_bin, weights=weights)
-        cuts = hb.Cuts.from_csr(*csr, n_cols, max_bin=max_bin, weights=weights)
+        ref = O.Dataset(csr=csr, n_cols=n_cols, max_bin=max_bin, weights=weights, feature_types=feature_types)
+        cuts = hb.Cuts.from_csr(*csr, n_cols, max_bin=max_bin, weights=weights, feature_types=feature_types)
         ix = hb.BinnedIndex(cuts, csr=csr, n_cols=n_cols)
     else:
-        ref = O.Dataset(x, max_bin=max_bin, weights=weights, missing=missing)
-        cuts = hb.Cuts.from_dense(x, max_bin=max_bin, weights=weights, missing=missing)
+        ref = O.Dataset(x, max_bin=max_bin, weights=weights, missing=missing, feature_types=feature_types)
+        cuts = hb.Cuts.from_dense(x, max_bin=max_bin, weights=weights, missing=missing,
+                                  feature_types=feature_types)
         ix = hb.BinnedIndex(cuts, x=x, missing=missing)
     fo, cv = cuts.arrays()
     assert np.array_equal(fo, ref.feature_offset)
@@ -69,3 +70,29 @@ def test_csr_sparse():
 def test_four_features_golden_data():
     from tests.helpers import four_features
     _compare(four_features(), max_bin=256)
+
+
+def test_categorical_features_bin_by_category():
+    """quantile.rs:524-689: a categorical feature's bins are its distinct
+    present values, ascending (many more than max_bin allows a numeric
+    one), and a value bins to its own category; beside numeric features,
+    with missing values, in dense and CSR storage."""
+    rng = np.random.default_rng(15)
+    n = 30_000
+    x = rng.standard_normal((n, 5)).astype(np.float32)
+    x[:, 0] = rng.integers(0, 7, n)
+    x[:, 2] = rng.integers(0, 300, n) * 3  # 300 categories with max_bin 64
+    x[:, 4] = rng.choice([0.5, 1.0, 2.5, 1e6], n)  # non-integer and large codes
+    x[rng.random(x.shape) < 0.1] = np.nan
+    types = ["c", "q", "c", "q", "c"]
+    _compare(x, max_bin=64, feature_types=types)
+    present = ~np.isnan(x)
+    rp = np.zeros(n + 1, np.uint64)
+    rp[1:] = np.cumsum(present.sum(1))
+    r, c = np.nonzero(present)
+    _compare(csr=(rp, c.astype(np.uint32), x[r, c]), n_cols=5, max_bin=64, feature_types=types)
+    cuts = hb.Cuts.from_dense(x, max_bin=64, feature_types=types)
+    fo, cv = cuts.arrays()
+    assert list(cuts.categorical()) == [True, False, True, False, True]
+    assert np.array_equal(cv[fo[0]:fo[1]], np.arange(7, dtype=np.float32))
+    assert fo[3] - fo[2] == 300 and np.array_equal(cv[fo[4]:fo[5]], np.array([0.5, 1.0, 2.5, 1e6], np.float32))
