@@ -63,6 +63,92 @@ def cpu_model():
     return platform.processor()
 
 
+def cpu_host():
+    """What the CPU baselines ran on."""
+    return {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+
+
+def median_round_s(model, repeats):
+    """Median wall time of `repeats` single boosting rounds of an oracle
+    model (its first round already run as the warmup)."""
+    import statistics
+    ts = []
+    for _ in range(repeats):
+        t = time.perf_counter()
+        model.more(1)
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts), ts
+
+
+def cpu_training_baseline(args, x, y):
+    """The oracle (a C restatement of the reference's CPU hist path: f64
+    chain and blocked sums, depthwise growth) on the same workload: all
+    cores on the full matrix, and one thread on a row prefix, each the
+    median of `cpu_repeats` rounds after a warmup round."""
+    from oracle import oracle as O
+
+    p = O.params(objective=O.OBJ_LOGISTIC, max_depth=8, eta=0.1)
+    O.set_threads(args.cpu_threads)
+    t = time.time()
+    ds = O.Dataset(x, max_bin=256)
+    log(f"oracle binning in {time.time() - t:.1f}s (excluded)")
+    model = O.Model(ds, y, p, 1)
+    med, ts = median_round_s(model, args.cpu_repeats)
+    log(f"oracle, {args.cpu_threads} threads: rounds " + ", ".join(f"{v:.2f}" for v in ts) + f" s; median {med:.2f}")
+    del model, ds
+    rows1 = min(args.cpu_single_rows, x.shape[0])
+    ds = O.Dataset(x[:rows1], max_bin=256)
+    O.set_threads(1)
+    model = O.Model(ds, y[:rows1], p, 1)
+    med1, ts1 = median_round_s(model, args.cpu_repeats)
+    log(f"oracle, 1 thread, {rows1:,} rows: rounds " + ", ".join(f"{v:.2f}" for v in ts1) + f" s; median {med1:.2f}")
+    del model, ds
+    O.set_threads(0)
+    return {
+        "value": round(1 / med, 4), "unit": "rounds/s", "cores": args.cpu_threads, "kind": "port",
+        "sample": f"the same {x.shape[0]:,} x 28 matrix, median of {args.cpu_repeats} rounds after one warmup "
+                  f"round, {args.cpu_threads} OpenMP threads; C restatement of the reference CPU hist path",
+        "single_thread": {
+            "value": round(1 / med1, 4), "unit": "rounds/s", "cores": 1, "rows": rows1,
+            "value_scaled_to_full_rows": round(rows1 / x.shape[0] / med1, 5),
+            "sample": f"the first {rows1:,} rows (binned on their own), median of {args.cpu_repeats} rounds "
+                      "after one warmup round; the scaled value assumes time linear in rows",
+        },
+        **cpu_host(),
+    }
+
+
+def cpu_predict_baseline(args, arrs, xp):
+    """The reference's batch walk restated on the host (16 rows in
+    lock-step over a breadth-first key-compare arena, 256-row blocks in
+    parallel: compact/mod.rs:963-1095, model/predict.rs:203-236): all cores
+    and one thread, each the median of `cpu_repeats` runs after a warmup."""
+    import statistics
+
+    from oracle import oracle as O
+
+    legs = {}
+    for threads, rows in ((args.cpu_threads, min(len(xp), 200_000)), (1, min(len(xp), 20_000))):
+        O.set_threads(threads)
+        O.predict_margin_lockstep(arrs, xp[:rows])
+        ts = []
+        for _ in range(args.cpu_repeats):
+            t = time.perf_counter()
+            O.predict_margin_lockstep(arrs, xp[:rows])
+            ts.append(time.perf_counter() - t)
+        legs[threads] = (rows, statistics.median(ts))
+        log(f"oracle lock-step walk, {threads} threads, {rows:,} rows: median {legs[threads][1]:.3f} s")
+    O.set_threads(0)
+    (rows, med), (rows1, med1) = legs[args.cpu_threads], legs[1]
+    return {
+        "value": round(rows / med / 1e6, 4), "unit": "Mrows/s", "cores": args.cpu_threads, "kind": "port",
+        "sample": f"first {rows:,} rows, all trees, median of {args.cpu_repeats} runs after a warmup; "
+                  "16-row lock-step compact walk",
+        "single_thread": {"value": round(rows1 / med1 / 1e6, 5), "unit": "Mrows/s", "cores": 1, "rows": rows1},
+        **cpu_host(),
+    }
+
+
 def other_workload(args):
     """Training rounds/s of the multiclass or the sparse configuration: the
     matrix binned once (excluded), `warmup` rounds, then `steps` timed
@@ -80,14 +166,12 @@ def other_workload(args):
         dm = hb.DMatrix(x, label=y)
         workload = "multiclass softmax hist training, 2,000,000 x 50 f32, 10 classes, max_bin 256, max_depth 6, " \
                    "eta 0.3, depthwise (10 trees per round)"
-        cpu_rounds = 1
     else:
         (row_ptr, col, val), y, _ = synthetic.sparse_wide(n=500_000, f=2000, density=0.1, seed=0)
         params = {"objective": "reg:squarederror", "grow_policy": "lossguide", "max_depth": 0, "max_leaves": 255,
                   "eta": 0.3, "max_bin": 64}
         dm = hb.DMatrix((row_ptr, col, val), label=y, n_cols=2000)
         workload = "sparse hist training, 500,000 x 2,000 CSR f32 (90% missing), max_bin 64, lossguide 255 leaves"
-        cpu_rounds = 2
     log(f"generated {args.workload} data in {time.time() - t:.1f}s")
     eng = dm.engine(params["max_bin"])
     trainer = hb.Trainer(eng, params, y)
@@ -121,11 +205,13 @@ def other_workload(args):
             ds = O.Dataset(csr=(row_ptr, col, val), n_cols=2000, max_bin=64)
             p = O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=0, max_leaves=255, eta=0.3, max_bin=64)
         m = O.Model(ds, y, p, 1)
-        t = time.time()
-        m.more(cpu_rounds)
-        ce = (time.time() - t) / cpu_rounds
-        result["cpu_baseline"] = {"value": round(1 / ce, 4), "unit": "rounds/s", "cores": args.cpu_threads,
-                                  "kind": "port", "sample": f"{'round 2' if cpu_rounds == 1 else f'rounds 2-{1 + cpu_rounds}'} of the same workload, oracle"}
+        med, ts = median_round_s(m, args.cpu_repeats)
+        log(f"oracle, {args.cpu_threads} threads: rounds " + ", ".join(f"{v:.2f}" for v in ts) + " s")
+        O.set_threads(0)
+        result["cpu_baseline"] = {"value": round(1 / med, 4), "unit": "rounds/s", "cores": args.cpu_threads,
+                                  "kind": "port",
+                                  "sample": f"the same workload, median of {args.cpu_repeats} rounds after one "
+                                            "warmup round, oracle", **cpu_host()}
     print(json.dumps(result), flush=True)
 
 
@@ -148,7 +234,14 @@ def main():
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="first run a device-to-device copy of this many MiB (a known-size kernel for "
                          "scaling hardware byte counters in profiles)")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-threads", type=int, default=min(16, len(os.sched_getaffinity(0))),
+                    help="threads of the all-core CPU baseline (the single-thread one uses 1)")
+    ap.add_argument("--cpu-repeats", type=int, default=5,
+                    help="timed repeats of each CPU baseline leg (median reported), after one warmup")
+    ap.add_argument("--cpu-single-rows", type=int, default=1_050_000,
+                    help="rows of the training matrix the single-thread CPU leg trains on")
+    ap.add_argument("--fit-rounds", type=int, default=500,
+                    help="rounds of the timed full fit on the device (0: skip)")
     ap.add_argument("--workload", choices=("higgs", "multiclass", "sparse"), default="higgs",
                     help="higgs: the default line; multiclass (2M x 50, 10-class softmax, depth 6) and "
                          "sparse (500k x 2000 CSR, 90%% missing, lossguide 255 leaves): their training "
@@ -294,34 +387,28 @@ def main():
                          "note": "whole engine construction (binning, count scan, syncs) on rows in HBM"},
         },
     }
+
+    # ---------------- the configured 500-round fit on the device ------------------------
+    if args.fit_rounds > 0:
+        fit = hb.Trainer(eng, params, y)
+        t = time.perf_counter()
+        fit.boost(args.fit_rounds)
+        fit_trees = fit.trees()
+        t_fit = time.perf_counter() - t
+        log(f"{args.fit_rounds}-round fit in {t_fit:.2f}s ({len(fit_trees)} trees downloaded)")
+        result["fit"] = {
+            "rounds": args.fit_rounds, "s": round(t_fit, 3),
+            "s_with_binning": round(t_fit + t_bin, 3),
+            "s_with_sketch_and_binning": round(t_fit + t_bin + t_cuts, 3),
+            "note": "a fresh trainer on the resident index: every round, then the trees downloaded; "
+                    "binning from rows in HBM and the host sketch added in the other keys",
+        }
+        del fit
     del eng, trainer
 
     # ---------------- CPU baseline (oracle, same workload) -----------------------------
     if not args.no_cpu_baseline:
-        from oracle import oracle as O
-
-        O.set_threads(args.cpu_threads)
-        t = time.time()
-        ds = O.Dataset(x, max_bin=256)
-        log(f"oracle binning in {time.time() - t:.1f}s (excluded)")
-        p = O.params(objective=O.OBJ_LOGISTIC, max_depth=8, eta=0.1)
-        t = time.time()
-        model = O.Model(ds, y, p, 1)
-        first = time.time() - t
-        rounds = 2
-        t = time.time()
-        model.more(rounds)
-        cpu_elapsed = time.time() - t
-        cpu_rps = rounds / cpu_elapsed
-        log(f"oracle: first round {first:.1f}s, {rounds} more in {cpu_elapsed:.1f}s = {cpu_rps:.3f} rounds/s "
-            f"on {args.cpu_threads} threads")
-        result["cpu_baseline"] = {
-            "value": round(cpu_rps, 4), "unit": "rounds/s", "cores": args.cpu_threads, "kind": "port",
-            "sample": f"the same {args.rows:,} x 28 matrix, rounds 2-3 of the run (round 1 excluded), "
-                      f"C restatement of the reference CPU hist path (f64 chain/blocked sums), "
-                      f"{args.cpu_threads} OpenMP threads on {cpu_model()}",
-        }
-        del model, ds
+        result["cpu_baseline"] = cpu_training_baseline(args, x, y)
 
     # ---------------- batch prediction ---------------------------------------------------
     if not args.no_predict:
@@ -331,10 +418,11 @@ def main():
         trees = synthetic.forest(n_trees=args.predict_trees, depth=8, n_features=f, seed=0)
         xp = synthetic.predict_rows(n=n, f=f, seed=1)
         log(f"generated forest + {xp.shape} rows in {time.time() - t:.1f}s")
-        arrs = {}
-        from oracle import oracle as O
+        arrs = None
+        if not args.no_cpu_baseline:
+            from oracle import oracle as O
 
-        arrs = O.forest_arrays(trees) if not args.no_cpu_baseline else None
+            arrs = O.forest_arrays(trees)
         booster = hb.Booster(objective="reg:squarederror", base_score=np.zeros(1, np.float32), trees=trees,
                              n_outputs=1, n_features=f)
         forest = hb.Forest(booster.forest_desc(), 1, 0)
@@ -371,13 +459,7 @@ def main():
                          "node_steps_per_s": round(node_steps / (pms / max(1, pl) * 1e-3), 1) if pms else None},
         }
         if arrs is not None:
-            sample = min(n, 200_000)
-            t = time.time()
-            O.predict_margin(arrs, xp[:sample])
-            ce = time.time() - t
-            pred["cpu_baseline"] = {"value": round(sample / ce / 1e6, 4), "unit": "Mrows/s",
-                                    "cores": args.cpu_threads, "kind": "port",
-                                    "sample": f"first {sample:,} rows, all {args.predict_trees} trees, oracle walk"}
+            pred["cpu_baseline"] = cpu_predict_baseline(args, arrs, xp)
         result["predict"] = pred
     print(json.dumps(result), flush=True)
 

@@ -254,6 +254,11 @@ typedef struct or_forest_desc {
 /* margins out[n * n_outputs]; leaf ids (per tree, may be NULL) out_leaf[n * n_trees]. */
 void or_predict_margin(const or_forest_desc *fd, const float *x, size_t n,
                        size_t n_cols, float missing, float *out, int32_t *out_leaf);
+/* The same margins (NaN missing, numeric splits) by the reference's 16-row
+ * lock-step walk over a breadth-first key-compare arena; -1 for a forest it
+ * does not take (categorical or non-finite splits, a feature >= n_cols). */
+int or_predict_margin_lockstep(const or_forest_desc *fd, const float *x, size_t n,
+                               size_t n_cols, float *out);
 
 /* ---- training -------------------------------------------------------------- */
 typedef struct or_model or_model;

@@ -139,6 +139,8 @@ def lib():
         L.or_sigmoid.argtypes = [C.c_float]
         L.or_base_margins.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, P(Params), C.c_void_p]
         L.or_predict_margin.argtypes = [P(ForestDesc), C.c_void_p, C.c_size_t, C.c_size_t, C.c_float, C.c_void_p, C.c_void_p]
+        L.or_predict_margin_lockstep.restype = C.c_int
+        L.or_predict_margin_lockstep.argtypes = [P(ForestDesc), C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]
         L.or_train.restype = C.c_void_p
         L.or_train.argtypes = [P(Index), C.c_void_p, C.c_void_p, P(Params), C.c_size_t]
         L.or_train_more.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, P(Params), C.c_size_t]
@@ -435,9 +437,9 @@ def forest_arrays(trees, tree_weight=None, tree_output=None, n_outputs=1, base_s
     return arrs
 
 
-def predict_margin(arrs, x, missing=np.nan, with_leaf=False):
-    x = np.ascontiguousarray(x, np.float32)
-    n, f = x.shape
+def _forest_desc(arrs):
+    """The ForestDesc over `arrs` (forest_arrays' layout), and the arrays it
+    points into (kept alive by the caller while the walk runs)."""
     P = C.POINTER
     fd = ForestDesc(len(arrs["tree_offset"]) - 1,
                     arrs["tree_offset"].ctypes.data_as(P(C.c_uint32)),
@@ -450,6 +452,7 @@ def predict_margin(arrs, x, missing=np.nan, with_leaf=False):
                     arrs["tree_weight"].ctypes.data_as(P(C.c_float)),
                     arrs["tree_output"].ctypes.data_as(P(C.c_uint32)),
                     arrs["n_outputs"], arrs["base_score"].ctypes.data_as(P(C.c_float)))
+    cat = {}
     if arrs.get("is_categorical") is not None:
         cat = {key: np.ascontiguousarray(arrs[key], dt) for key, dt in
                (("is_categorical", np.uint8), ("cat_begin", np.uint32), ("cat_end", np.uint32),
@@ -460,11 +463,33 @@ def predict_margin(arrs, x, missing=np.nan, with_leaf=False):
         fd.cat_begin = cat["cat_begin"].ctypes.data_as(P(C.c_uint32))
         fd.cat_end = cat["cat_end"].ctypes.data_as(P(C.c_uint32))
         fd.categories = cat["categories"].ctypes.data_as(P(C.c_uint32))
+    return fd, cat
+
+
+def predict_margin(arrs, x, missing=np.nan, with_leaf=False):
+    x = np.ascontiguousarray(x, np.float32)
+    n, f = x.shape
+    fd, keep = _forest_desc(arrs)
     k = arrs["n_outputs"]
     out = np.empty(n * k, np.float32)
     leaf = np.empty(n * fd.n_trees, np.int32) if with_leaf else None
     lib().or_predict_margin(C.byref(fd), _ptr(x), n, f, missing, _ptr(out), _ptr(leaf))
+    del keep
     return (out, leaf.reshape(n, -1)) if with_leaf else out
+
+
+def predict_margin_lockstep(arrs, x):
+    """predict_margin's margins (NaN missing, numeric splits) through the
+    reference's 16-row lock-step compact walk; ValueError for a forest that
+    walk does not take here."""
+    x = np.ascontiguousarray(x, np.float32)
+    n, f = x.shape
+    fd, keep = _forest_desc(arrs)
+    out = np.empty(n * arrs["n_outputs"], np.float32)
+    if lib().or_predict_margin_lockstep(C.byref(fd), _ptr(x), n, f, _ptr(out)) != 0:
+        raise ValueError("the lock-step walk takes numeric splits with finite conditions on features < n_cols")
+    del keep
+    return out
 
 
 def set_threads(n: int) -> None:

@@ -95,3 +95,30 @@ def splitmix64(seed):
         z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
         z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
         yield z ^ (z >> 31)
+
+
+def random_tree(rng, n_features, max_depth):
+    """An unbalanced tree in the reference's node layout, nodes numbered in
+    depth-first order (the upload re-lays them out breadth-first)."""
+    nodes = []
+
+    def grow(depth):
+        i = len(nodes)
+        nodes.append(None)
+        if depth >= max_depth or rng.random() < 0.25 * depth / max(1, max_depth):
+            nodes[i] = (-1, -1, 0, 0.0, 0, float(rng.normal(0, 0.1)))
+            return i
+        f = int(rng.integers(0, n_features))
+        cond = float(np.float32(rng.normal()))
+        dl = int(rng.integers(0, 2))
+        left = grow(depth + 1)
+        right = grow(depth + 1)
+        nodes[i] = (left, right, f, cond, dl, 0.0)
+        return i
+
+    grow(0)
+    return dict(left=np.array([n[0] for n in nodes], np.int32), right=np.array([n[1] for n in nodes], np.int32),
+                split_feature=np.array([n[2] for n in nodes], np.uint32),
+                split_cond=np.array([n[3] for n in nodes], np.float32),
+                default_left=np.array([n[4] for n in nodes], np.uint8),
+                leaf_value=np.array([n[5] for n in nodes], np.float32))

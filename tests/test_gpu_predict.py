@@ -5,7 +5,7 @@ import pytest
 import hessboost_amd as hb
 from hessboost_amd import synthetic
 from oracle import oracle as O
-from tests.helpers import categorical_features, four_features, golden_forest, load_saved_models
+from tests.helpers import categorical_features, four_features, golden_forest, load_saved_models, random_tree
 
 pytestmark = pytest.mark.gpu
 
@@ -230,33 +230,6 @@ def test_malformed_forest_is_refused():
         hb.Forest(arrs, 1)
 
 
-def _random_tree(rng, n_features, max_depth):
-    """An unbalanced tree in the reference's node layout, nodes numbered in
-    depth-first order (the upload re-lays them out breadth-first)."""
-    nodes = []
-
-    def grow(depth):
-        i = len(nodes)
-        nodes.append(None)
-        if depth >= max_depth or rng.random() < 0.25 * depth / max(1, max_depth):
-            nodes[i] = (-1, -1, 0, 0.0, 0, float(rng.normal(0, 0.1)))
-            return i
-        f = int(rng.integers(0, n_features))
-        cond = float(np.float32(rng.normal()))
-        dl = int(rng.integers(0, 2))
-        left = grow(depth + 1)
-        right = grow(depth + 1)
-        nodes[i] = (left, right, f, cond, dl, 0.0)
-        return i
-
-    grow(0)
-    return dict(left=np.array([n[0] for n in nodes], np.int32), right=np.array([n[1] for n in nodes], np.int32),
-                split_feature=np.array([n[2] for n in nodes], np.uint32),
-                split_cond=np.array([n[3] for n in nodes], np.float32),
-                default_left=np.array([n[4] for n in nodes], np.uint8),
-                leaf_value=np.array([n[5] for n in nodes], np.float32))
-
-
 @pytest.mark.parametrize("seed", range(12))
 def test_random_forests_match_oracle(seed):
     """Random unbalanced forests (depth 0 to 12, several outputs, tree
@@ -266,7 +239,7 @@ def test_random_forests_match_oracle(seed):
     f = int(rng.integers(1, 40))
     n_trees = int(rng.integers(1, 90))
     k = int(rng.choice([1, 1, 3]))
-    trees = [_random_tree(rng, f, int(rng.integers(0, 13))) for _ in range(n_trees)]
+    trees = [random_tree(rng, f, int(rng.integers(0, 13))) for _ in range(n_trees)]
     arrs = O.forest_arrays(trees)
     arrs["tree_output"] = (np.arange(n_trees) % k).astype(np.uint32)
     arrs["tree_weight"] = rng.uniform(0.5, 1.5, n_trees).astype(np.float32)

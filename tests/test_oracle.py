@@ -12,7 +12,7 @@ import pytest
 
 from oracle import oracle as O
 from tests.helpers import (bits_to_f32, categorical_features, four_features, golden_forest, load_saved_models,
-                           train_labels)
+                           random_tree, train_labels)
 
 
 @pytest.fixture(scope="module")
@@ -62,6 +62,63 @@ def test_saved_model_margins_bit_exact(saved, name):
         out = O.predict_margin(forest, x)
         want = np.array(case["margins"], np.uint32)
         assert np.array_equal(out.view(np.uint32), want), f"{ver}/{name}"
+
+
+@pytest.mark.parametrize("name", ["early_stopping", "dart", "multiclass_forest", "quantiles", "expectiles", "aft",
+                                  "dist_normal", "dist_negbinomial"])
+def test_lockstep_walk_reproduces_saved_margins(saved, name):
+    """The reference's 16-row lock-step compact walk (compact/mod.rs:963-1095)
+    restated for the CPU baseline gives each saved numeric model's recorded
+    margins; 160 rows are ten full lane groups, 13 leave a tail only."""
+    x = four_features()
+    for ver in ("0.2.0", "0.4.3", "0.4.9"):
+        case = saved[f"{ver}/{name}"]
+        want = np.array(case["margins"], np.uint32).reshape(len(x), -1)
+        forest = golden_forest(case)
+        for rows in (slice(None), slice(0, 13), slice(5, 160)):
+            out = O.predict_margin_lockstep(forest, x[rows])
+            assert np.array_equal(out.view(np.uint32), want[rows].reshape(-1)), f"{ver}/{name} {rows}"
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_lockstep_walk_equals_the_scalar_walk(seed):
+    """Unbalanced forests (depth 0 to 20: deeper than 16 takes the early-exit
+    walk), several outputs and tree weights, NaN cells, signed zeros and
+    values equal to a threshold, row counts around the 16-row lanes and the
+    256-row blocks, widths beyond 64 features."""
+    rng = np.random.default_rng(900 + seed)
+    f = int(rng.choice([1, 7, 100]))
+    n_trees = int(rng.integers(1, 40))
+    k = int(rng.choice([1, 3]))
+    trees = [random_tree(rng, f, int(rng.integers(0, 21 if seed == 5 else 12))) for _ in range(n_trees)]
+    arrs = O.forest_arrays(trees)
+    arrs["tree_output"] = (np.arange(n_trees) % k).astype(np.uint32)
+    arrs["tree_weight"] = rng.uniform(0.5, 1.5, n_trees).astype(np.float32)
+    arrs["n_outputs"] = k
+    arrs["base_score"] = rng.normal(0, 1, k).astype(np.float32)
+    conds = arrs["split_cond"][arrs["left"] != -1]
+    conds[: len(conds) // 3] = 0.0
+    arrs["split_cond"][np.nonzero(arrs["left"] != -1)[0]] = conds
+    O.set_threads(3)
+    for n in (0, 1, 15, 16, 17, 255, 256, 257, 1_000):
+        x = rng.standard_normal((n, f)).astype(np.float32)
+        x[rng.random((n, f)) < 0.1] = np.nan
+        x[rng.random((n, f)) < 0.05] = -0.0
+        x[rng.random((n, f)) < 0.05] = 0.0
+        if n and len(conds):
+            hit = rng.random((n, f)) < 0.1
+            x[hit] = rng.choice(conds, int(hit.sum()))
+        want = O.predict_margin(arrs, x)
+        got = O.predict_margin_lockstep(arrs, x)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seed, n)
+    O.set_threads(0)
+
+
+def test_lockstep_walk_refuses_what_it_does_not_take(saved):
+    with pytest.raises(ValueError):
+        O.predict_margin_lockstep(golden_forest(saved["0.4.9/categorical_splits"]), categorical_features())
+    with pytest.raises(ValueError):
+        O.predict_margin_lockstep(golden_forest(saved["0.4.9/multiclass_forest"]), four_features()[:, :3])
 
 
 def test_categorical_casts_saturate_and_missing_follows_default():
