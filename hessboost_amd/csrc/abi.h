@@ -636,9 +636,25 @@ struct PredNode {
 // A compact forest node: value bits, then feature (16 bits), the left
 // child's offset from this node (14 bits; right = left + 1), default_left,
 // leaf.
-struct CompactNode {
+struct alignas(8) CompactNode {
     uint32_t value;
     uint32_t meta;
+};
+
+// LDS words per feature of a staged 64-row block (feature-major): lane l
+// reads row l of every feature from bank l, whatever the feature.
+constexpr uint32_t kPredPitch = 64;
+
+// Two levels of a complete tree (PredictArgs::pairs).
+struct alignas(16) PairRecord {
+    uint32_t t_node, t_first, t_second;
+    uint32_t s;  // s of the node | s of the first child << 8 | s of the second << 16
+};
+
+// A node of the mirror walk (PredictArgs::mirror).
+struct alignas(8) MirrorNode {
+    uint32_t t;  // threshold bits (a leaf: its value's)
+    uint32_t w;  // m << 31 | rel << 16 | slot
 };
 
 struct PredictArgs {
@@ -675,6 +691,39 @@ struct PredictArgs {
     // categories[value, node_cat_end[node])
     const uint32_t *categories;
     const uint32_t *node_cat_end;
+    // The forest as branch-free steps (hbr_predict_mirror*): each tree
+    // breadth-first with the child a missing value takes first and its
+    // sibling next to it. A node is (bits of t, m << 31 | rel << 16 | slot):
+    // a row steps to first + 1 when (value, its sign flipped when m) < t,
+    // else to first = this node + rel; slot is the feature + 1. A split
+    // whose missing values go right has m = 0 and t its threshold (first =
+    // the right child: NaN compares false); one whose missing values go left
+    // has m = 1 and t = -next_below(threshold) (first = the left child: -v <
+    // t is v >= threshold). A leaf is (bits of its value, 0): it steps to
+    // itself, reading slot 0, where every row holds NaN. Rows are staged
+    // with feature f in slot f + 1 and, when the missing value is not NaN,
+    // missing values as NaN and present NaNs as +inf (which go right, as a
+    // NaN compared with a threshold does).
+    const MirrorNode *mirror;
+    const uint32_t *mirror_root;   // n_trees
+    const int32_t *mirror_orig;    // per node: its id in its tree as the caller numbered it
+    const uint8_t *tree_depth;     // n_trees
+    uint32_t pair_levels;          // hbr_predict_pairs: D / 2 (every tree a complete tree of depth D)
+    uint32_t pad2;
+    // The forest as complete trees of even depth D, two levels per record
+    // (hbr_predict_pairs): a tree's records level by level (1, 4, 16, ...
+    // records: (4^(D/2) - 1) / 3 per tree), the record of the node at
+    // position i of level 2l followed by the value of each of its 2^D level-D
+    // positions. A record is (t of the node, t of its first child, t of its
+    // second child, s of the node | s of the first << 8 | s of the second <<
+    // 16) with t as in the mirror walk and s = m << 7 | slot: a row steps to
+    // the second child when (value of slot, its sign flipped when m) < t.
+    // The first child is where a missing value goes. A leaf above level D
+    // is continued by nodes that read slot 0 (NaN) and so always take their
+    // first child, down to its position at level D, which holds its value.
+    const PairRecord *pairs;
+    const uint32_t *pair_values;   // n_trees x 2^D leaf values (bits)
+    const int32_t *pair_orig;      // n_trees x 2^D: the caller's id of the leaf each position holds
 };
 constexpr uint32_t kPredCategorical = 1u << 29;
 

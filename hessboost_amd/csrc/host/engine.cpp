@@ -1529,7 +1529,7 @@ void Engine::launch_eval_walk(const EvalSet &set, const GrowTreeNode *tree, cons
     a.total_bins = (uint32_t)total_bins_;
     if (n_cols_ <= kEvalStagedCols && !std::getenv("HBROCM_EVAL_IN_PLACE")) {
         // 64-row blocks staged in LDS, one per wave, four waves per workgroup
-        const uint32_t lds = 4u * n_cols_ * 65u * (uint32_t)sizeof(float);
+        const uint32_t lds = 4u * n_cols_ * kPredPitch * (uint32_t)sizeof(float);
         const uint64_t blocks64 = (set.n_rows + 63) / 64;
         const uint32_t grid = (uint32_t)std::min<uint64_t>((blocks64 + 3) / 4, (uint64_t)dev_.cu_count() * 2);
         dev_.launch("hbr_eval_walk_staged", dim3(grid), dim3(256), a, lds);

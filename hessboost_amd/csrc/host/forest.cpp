@@ -1,8 +1,12 @@
 #include "forest.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <string>
+#include <tuple>
+#include <utility>
 
 namespace hbr {
 
@@ -104,6 +108,8 @@ Forest::Forest(int ordinal, const hbr_forest_desc &fd) : dev_(device(ordinal)) {
         if (f >= (1u << 16) || rel >= (1u << 14)) compact_ok_ = false;
         compact[i] = CompactNode{value[i], (f & 0xffffu) | ((rel & 0x3fffu) << 16) | (meta[i] & (1u << 30))};
     }
+    // one spare node past the end: the LDS walk copies 16-byte node pairs
+    compact.push_back(CompactNode{0u, 1u << 31});
     if (compact_ok_) up(compact_, compact);
     tree_nodes_.resize(n_trees_);
     for (uint64_t t = 0; t < n_trees_; t++) {
@@ -113,7 +119,159 @@ Forest::Forest(int ordinal, const hbr_forest_desc &fd) : dev_(device(ordinal)) {
     }
     up(weight_, weight);
     up(base_, base);
+    build_mirror(fd);
+    build_pairs(fd);
     dev_.sync();
+}
+
+// Largest finite float below c (c finite): v > next_below(c) is v >= c.
+static float next_below(float c) {
+    uint32_t b;
+    std::memcpy(&b, &c, 4);
+    if (c > 0.0f) b -= 1;
+    else if (c == 0.0f) b = 0x80000001u;  // -(the smallest subnormal)
+    else b += 1;
+    float r;
+    std::memcpy(&r, &b, 4);
+    return r;
+}
+
+// The pair layout (PredictArgs::pairs): every tree embedded in the
+// complete tree of the forest's largest depth rounded up to even, a split's
+// first child being the one its missing values take.
+void Forest::build_pairs(const hbr_forest_desc &fd) {
+    if (has_categorical_ || n_trees_ == 0 || max_feature_ >= 126) return;
+    uint32_t depth = 0;
+    // depths, and the checks the walk needs
+    std::vector<uint32_t> tree_depth(n_trees_, 0);
+    for (uint64_t t = 0; t < n_trees_; t++) {
+        const uint64_t lo = fd.tree_offset[t];
+        std::vector<std::pair<int32_t, uint32_t>> stack{{0, 0}};
+        while (!stack.empty()) {
+            const auto [id, lv] = stack.back();
+            stack.pop_back();
+            const uint64_t at = lo + (uint64_t)id;
+            tree_depth[t] = std::max(tree_depth[t], lv);
+            if (fd.left[at] == -1) continue;
+            if (!std::isfinite(fd.split_cond[at]) || lv >= 12) return;
+            stack.push_back({fd.left[at], lv + 1});
+            stack.push_back({fd.right[at], lv + 1});
+        }
+        depth = std::max(depth, tree_depth[t]);
+    }
+    depth += depth & 1u;
+    const uint32_t levels = depth / 2;
+    const uint64_t per_tree = ((1ull << depth) - 1) / 3, leaves = 1ull << depth;
+    // the complete trees may not outgrow the trees too far
+    const uint64_t bytes = n_trees_ * (per_tree * sizeof(PairRecord) + leaves * 8);
+    uint64_t real = 0;
+    for (uint64_t t = 0; t < n_trees_; t++) real += tree_nodes_[t];
+    if (bytes > (1ull << 30) || bytes > 64 * real * sizeof(MirrorNode)) return;
+    std::vector<PairRecord> recs(n_trees_ * per_tree);
+    std::vector<uint32_t> values(n_trees_ * leaves);
+    std::vector<int32_t> orig(n_trees_ * leaves);
+    std::vector<uint32_t> t_at, s_at;  // per complete position of levels < depth
+    for (uint64_t t = 0; t < n_trees_; t++) {
+        const uint64_t lo = fd.tree_offset[t];
+        t_at.assign((1ull << depth) - 1, 0u);
+        s_at.assign((1ull << depth) - 1, 0u);  // slot 0, m 0: the first child
+        // (node, level, position in its level)
+        std::vector<std::tuple<int32_t, uint32_t, uint64_t>> stack{{0, 0u, 0ull}};
+        while (!stack.empty()) {
+            const auto [id, lv, i] = stack.back();
+            stack.pop_back();
+            const uint64_t at = lo + (uint64_t)id;
+            if (fd.left[at] == -1) {
+                uint32_t bits;
+                std::memcpy(&bits, &fd.leaf_value[at], 4);
+                const uint64_t span = 1ull << (depth - lv);
+                for (uint64_t j = i * span; j < (i + 1) * span; j++) {
+                    values[t * leaves + j] = bits;
+                    orig[t * leaves + j] = id;
+                }
+                continue;
+            }
+            const bool dl = fd.default_left[at] != 0;
+            const float cond = fd.split_cond[at];
+            const float tc = dl ? -next_below(cond) : cond;
+            const uint64_t p = ((1ull << lv) - 1) + i;
+            std::memcpy(&t_at[p], &tc, 4);
+            s_at[p] = (dl ? 0x80u : 0u) | (fd.split_feature[at] + 1u);
+            stack.push_back({dl ? fd.left[at] : fd.right[at], lv + 1, 2 * i});
+            stack.push_back({dl ? fd.right[at] : fd.left[at], lv + 1, 2 * i + 1});
+        }
+        uint64_t r = t * per_tree;
+        for (uint32_t l = 0; l < levels; l++) {
+            const uint32_t lv = 2 * l;
+            for (uint64_t i = 0; i < (1ull << lv); i++) {
+                const uint64_t p = ((1ull << lv) - 1) + i;
+                const uint64_t c = ((1ull << (lv + 1)) - 1) + 2 * i;
+                recs[r++] = PairRecord{t_at[p], t_at[c], t_at[c + 1], s_at[p] | (s_at[c] << 8) | (s_at[c + 1] << 16)};
+            }
+        }
+    }
+    hipStream_t s = dev_.stream();
+    pairs_.resize(recs.size() ? recs.size() : 1);
+    if (!recs.empty()) pairs_.upload(recs.data(), recs.size(), s);
+    pair_values_.resize(values.size());
+    pair_values_.upload(values.data(), values.size(), s);
+    pair_orig_.resize(orig.size());
+    pair_orig_.upload(orig.data(), orig.size(), s);
+    pair_levels_ = levels;
+    pairs_ok_ = true;
+}
+
+// The mirror arena (PredictArgs::mirror): every tree breadth-first with a
+// missing value's child first; the trees were checked by the constructor.
+void Forest::build_mirror(const hbr_forest_desc &fd) {
+    if (has_categorical_ || n_trees_ == 0) return;
+    std::vector<MirrorNode> nodes;
+    std::vector<uint32_t> roots;
+    std::vector<int32_t> orig;
+    std::vector<uint8_t> depth;
+    for (uint64_t t = 0; t < n_trees_; t++) {
+        const uint64_t lo = fd.tree_offset[t];
+        const uint32_t base = (uint32_t)nodes.size();
+        roots.push_back(base);
+        std::vector<int32_t> queue{0};
+        std::vector<uint32_t> level{0};
+        uint32_t deepest = 0;
+        for (size_t i = 0; i < queue.size(); i++) {
+            const uint64_t at = lo + (uint64_t)queue[i];
+            orig.push_back(queue[i]);
+            deepest = std::max(deepest, level[i]);
+            uint32_t bits;
+            if (fd.left[at] == -1) {
+                std::memcpy(&bits, &fd.leaf_value[at], 4);
+                nodes.push_back(MirrorNode{bits, 0u});
+                continue;
+            }
+            const float cond = fd.split_cond[at];
+            const uint32_t rel = (uint32_t)(queue.size() - i);
+            if (!std::isfinite(cond) || fd.split_feature[at] >= 0xffffu || rel > 0x7fffu) return;
+            const bool dl = fd.default_left[at] != 0;
+            const float t_cond = dl ? -next_below(cond) : cond;
+            std::memcpy(&bits, &t_cond, 4);
+            nodes.push_back(MirrorNode{bits, (dl ? 1u << 31 : 0u) | (rel << 16) | (fd.split_feature[at] + 1u)});
+            queue.push_back(dl ? fd.left[at] : fd.right[at]);
+            queue.push_back(dl ? fd.right[at] : fd.left[at]);
+            level.push_back(level[i] + 1);
+            level.push_back(level[i] + 1);
+        }
+        if (deepest > 255) return;
+        depth.push_back((uint8_t)deepest);
+    }
+    nodes.push_back(MirrorNode{0u, 0u});  // a spare node: the LDS walk copies 16-byte pairs
+    hipStream_t s = dev_.stream();
+    mirror_.resize(nodes.size());
+    mirror_.upload(nodes.data(), nodes.size(), s);
+    mirror_root_.resize(roots.size());
+    mirror_root_.upload(roots.data(), roots.size(), s);
+    mirror_orig_.resize(orig.size());
+    mirror_orig_.upload(orig.data(), orig.size(), s);
+    tree_depth_.resize(depth.size());
+    tree_depth_.upload(depth.data(), depth.size(), s);
+    mirror_ok_ = true;
 }
 
 void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float missing, float *out,
@@ -146,27 +304,55 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
         dev_.launch("hbr_predict", dim3((uint32_t)((n + 255) / 256)), dim3(256), a);
         return;
     }
-    const uint64_t row_block = n_cols * 65ull * sizeof(float);
+    const uint64_t row_block = n_cols * (uint64_t)kPredPitch * sizeof(float);
     const uint64_t lds_total = 160ull * 1024;
-    // rows resident in LDS (one 64-row block per one-wave workgroup), trees
-    // streamed through the caches: the rows are read once, however large
-    // the forest (HBROCM_PRED_KERNEL=chunked selects the LDS-chunked walk)
+    // HBROCM_PRED_KERNEL selects a walk (pairs, mirror, resident or
+    // chunked); by default the first of pairs, mirror and resident that the
+    // forest and the rows allow. Each keeps a 64-row block in LDS per one-wave
+    // workgroup (rows read from HBM once, however large the forest) and
+    // reads the trees through the caches.
     const char *kind = std::getenv("HBROCM_PRED_KERNEL");
     const bool chunked = kind && std::strcmp(kind, "chunked") == 0;
+    const bool nan = missing != missing;
+    const uint64_t mirror_block = (n_cols + 1) * (uint64_t)kPredPitch * sizeof(float);
+    const uint64_t blocks = (n + 63) / 64;
+    // complete trees, two levels per record
+    if (n_trees_ && pairs_ok_ && (!kind || std::strcmp(kind, "pairs") == 0) && mirror_block <= lds_total / 4) {
+        a.pairs = pairs_.get();
+        a.pair_values = pair_values_.get();
+        a.pair_orig = pair_orig_.get();
+        a.pair_levels = pair_levels_;
+        const uint64_t grid = std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count() * (lds_total / mirror_block));
+        dev_.launch(nan ? "hbr_predict_pairs_nan" : "hbr_predict_pairs", dim3((uint32_t)grid), dim3(64), a,
+                    (uint32_t)mirror_block);
+        return;
+    }
+    // the mirror arena, one level per step
+    if (n_trees_ && mirror_ok_ && (!kind || std::strcmp(kind, "mirror") == 0) && mirror_block <= lds_total / 4) {
+        a.mirror = mirror_.get();
+        a.mirror_root = mirror_root_.get();
+        a.mirror_orig = mirror_orig_.get();
+        a.tree_depth = tree_depth_.get();
+        const uint64_t grid = std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count() * (lds_total / mirror_block));
+        dev_.launch(nan ? "hbr_predict_mirror_nan" : "hbr_predict_mirror", dim3((uint32_t)grid), dim3(64), a,
+                    (uint32_t)mirror_block);
+        return;
+    }
+    // compact records, one level per step (any threshold)
     if (n_trees_ && compact_ok_ && !chunked && row_block <= lds_total / 4) {
         a.compact = compact_.get();
-        const uint64_t blocks = (n + 63) / 64;
         const uint64_t grid = std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count() * (lds_total / row_block));
         dev_.launch(missing != missing ? "hbr_predict_resident_nan" : "hbr_predict_resident", dim3((uint32_t)grid),
                     dim3(64), a, (uint32_t)row_block);
         return;
     }
-    // trees resident in LDS, rows streamed: row blocks of `waves` waves plus
-    // a node table holding at least the largest tree
+    // trees resident in LDS, rows streamed (rows too wide for the walks
+    // above): row blocks of `waves` waves plus a node table holding at least
+    // the largest tree
+    const uint64_t tree_tables = 2ull * 256 * sizeof(uint32_t);  // roots and weights of a chunk
     uint32_t waves = 4;
     if (const char *v = std::getenv("HBROCM_PRED_WAVES")) waves = (uint32_t)std::max(1L, std::min(4L, std::strtol(v, nullptr, 10)));
     while (waves > 1 && waves * row_block > lds_total / 2) waves--;
-    const uint64_t tree_tables = 2ull * 256 * sizeof(uint32_t);  // roots and weights of a chunk
     if (n_trees_ && compact_ok_ && waves * row_block + tree_tables + 8ull * largest_tree_ <= lds_total) {
         const uint32_t cap = (uint32_t)((lds_total - waves * row_block - tree_tables) / 8);
         plan_chunks(cap);
@@ -183,7 +369,7 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
         return;
     }
     // rows staged in LDS when 64 of them fit in a quarter of a CU's LDS
-    const uint64_t lds = n_cols * 65ull * sizeof(float);
+    const uint64_t lds = n_cols * (uint64_t)kPredPitch * sizeof(float);
     if (n_trees_ && lds <= 40ull * 1024) {
         const uint64_t blocks = (n + 63) / 64;
         const uint64_t grid = std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count() * 64);

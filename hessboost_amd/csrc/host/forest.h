@@ -43,6 +43,24 @@ private:
     void plan_chunks(uint32_t cap);
     DBuf<int32_t> orig_;
     DBuf<float> weight_, base_;
+    // the mirror arena (absent with categorical splits, a non-finite
+    // threshold, a feature id of 2^16 - 1 or more, or a child beyond 2^15 - 1
+    // nodes of its parent)
+    bool mirror_ok_ = false;
+    DBuf<MirrorNode> mirror_;
+    DBuf<uint32_t> mirror_root_;
+    DBuf<int32_t> mirror_orig_;
+    DBuf<uint8_t> tree_depth_;
+    void build_mirror(const hbr_forest_desc &fd);
+    // the pair layout (PredictArgs::pairs): absent unless every split is
+    // numeric with a finite threshold on a feature below 127, and the
+    // complete trees stay small
+    bool pairs_ok_ = false;
+    uint32_t pair_levels_ = 0;
+    DBuf<PairRecord> pairs_;
+    DBuf<uint32_t> pair_values_;
+    DBuf<int32_t> pair_orig_;
+    void build_pairs(const hbr_forest_desc &fd);
 };
 
 }  // namespace hbr

@@ -8,21 +8,28 @@
 // present value left iff its category is in the node's set; forests with
 // such splits take hbr_predict (the category pool read from global memory).
 //
-// hbr_predict_resident (the default): a workgroup is one wave; it stages a
-// 64-row block in LDS once and walks it through every tree, 16 trees in
-// flight per lane, reading compact node records through the caches (below).
+// The walks that keep rows resident: a workgroup is one wave; it stages a
+// 64-row block in LDS once, feature-major (row l of feature f at f * 64 + l,
+// so that lane l reads bank l whatever the feature), and walks it through
+// every tree, 16 trees in flight per lane, reading the trees through the
+// caches. A wave-wide node load costs about 4 cycles of the texture path per
+// distinct 128-byte line it touches (16 at least, 64 at most) whatever its
+// width, so the walks spend their loads where the lanes' nodes diverge:
+//  - hbr_predict_pairs (the default where the forest allows): complete trees,
+//    one 16-byte record per two levels, the last load only the leaf's value;
+//  - hbr_predict_mirror: any numeric forest, one 8-byte node per level, the
+//    missing value's child first so that every step is a compare and an add;
+//  - hbr_predict_resident: compact records, for thresholds the mirror form
+//    cannot take (infinities).
 // hbr_predict_chunked keeps chunks of the forest in LDS instead and
 // re-stages the rows for every chunk; it serves rows too wide for the
-// resident walk's LDS block.
+// resident walks' LDS block.
 //
-// hbr_predict_staged: a workgroup is one wave and 64 rows. The rows are
-// copied into LDS feature-major (coalesced global reads; row `lane` of
-// feature f at f * 65 + lane, so lanes reading different features hit
-// different banks), then every lane walks its row through all trees, four
-// trees at a time so that four node loads are in flight; the leaf values
-// are still added one tree after another, in order. Nodes are 16-byte
+// hbr_predict_staged: a workgroup is one wave and 64 rows staged in LDS as
+// above; every lane walks its row through all trees, eight at a time, the
+// leaf values added one tree after another, in order. Nodes are 16-byte
 // records read through the caches. hbr_predict reads features from the
-// row-major rows directly (rows too wide for LDS).
+// row-major rows directly (rows too wide for LDS, categorical splits).
 #include "common.h"
 
 using namespace hbr;
@@ -62,17 +69,43 @@ __device__ __forceinline__ uint32_t walk(const PredictArgs &a, const float *row,
     }
 }
 
+// 1 when a row goes to the right child of a compact node: a present value
+// goes right unless value < threshold, a missing one unless default_left
+// (meta bit 30). Bit arithmetic rather than a select, which the compiler
+// would turn into a branch per chain. MISSING_NAN: the missing value is
+// NaN, which compares false and so goes right unless default_left.
+template <bool MISSING_NAN>
+__device__ __forceinline__ uint32_t goes_right(float v, uint32_t meta, uint32_t thr_bits, float missing) {
+    const uint32_t not_lt = v < __uint_as_float(thr_bits) ? 0u : 1u;
+    const uint32_t dl = (meta >> 30) & 1u;
+    if (MISSING_NAN) {
+        const uint32_t nan = v != v ? 1u : 0u;
+        return not_lt & ~(nan & dl);
+    }
+    const uint32_t miss = 0u - (v == missing ? 1u : 0u);
+    return (not_lt & ~miss) | ((dl ^ 1u) & miss);
+}
+
 constexpr uint32_t kPredLanes = 64;
-constexpr uint32_t kPredPitch = 65;  // LDS words per feature (64 rows + 1)
 constexpr int kPredChains = 8;
 
 // Copy a block of `rows` consecutive rows (rows * n_cols floats, contiguous;
 // 16-byte aligned when the rows are, blocks starting at multiples of 64 rows) into LDS
 // feature-major, s_x[f * kPredPitch + row]. The wave's lanes read 16 bytes
 // each, consecutive, several loads in flight.
-template <bool NT = false>
+// MIRROR: feature f goes to slot f + 1 (slot 0 holds NaN for the mirror
+// walk's leaves) and, unless MISSING_NAN, the missing value becomes NaN and
+// a present NaN +inf (mirror_value).
+template <bool MISSING_NAN>
+__device__ __forceinline__ float mirror_value(float v, float missing) {
+    if (MISSING_NAN) return v;
+    return v == missing ? __builtin_nanf("") : (v != v ? __builtin_inff() : v);
+}
+
+template <bool NT = false, bool MIRROR = false, bool MISSING_NAN = true>
 __device__ __forceinline__ void stage_rows(float *s_x, const float *src, uint32_t rows, uint32_t n_cols,
-                                           uint32_t lane) {
+                                           uint32_t lane, float missing = 0.0f) {
+    if (MIRROR) s_x += kPredPitch;
     const uint32_t total = rows * n_cols;
     const uint32_t n4 = ((uintptr_t)src & 15u) == 0 ? total / 4 : 0;  // an unaligned caller pointer: scalar
     const float inv = 1.0f / (float)n_cols;
@@ -90,7 +123,7 @@ __device__ __forceinline__ void stage_rows(float *s_x, const float *src, uint32_
         const float vals[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            s_x[f * kPredPitch + rl] = vals[j];
+            s_x[f * kPredPitch + rl] = MIRROR ? mirror_value<MISSING_NAN>(vals[j], missing) : vals[j];
             if (++f == n_cols) {
                 f = 0;
                 rl++;
@@ -99,7 +132,37 @@ __device__ __forceinline__ void stage_rows(float *s_x, const float *src, uint32_
     }
     for (uint32_t e = n4 * 4 + lane; e < total; e += kPredLanes) {
         const uint32_t rl = e / n_cols;
-        s_x[(e - rl * n_cols) * kPredPitch + rl] = src[e];
+        const float v = src[e];
+        s_x[(e - rl * n_cols) * kPredPitch + rl] = MIRROR ? mirror_value<MISSING_NAN>(v, missing) : v;
+    }
+}
+
+// One 8-byte node record in a single load (the records are 8-byte aligned).
+template <typename Node>
+__device__ __forceinline__ Node load_node(const Node *p, uint32_t i) {
+    static_assert(sizeof(Node) == 8, "8-byte node records");
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    const u2 v = reinterpret_cast<const u2 *>(p)[i];
+    return Node{v.x, v.y};
+}
+
+// CH chains of the mirror walk, `depth` steps each (every chain then sits
+// on its leaf): per step the value of the node's slot, its sign flipped by
+// the node's m bit, compared with t, and the next node.
+template <int CH>
+__device__ __forceinline__ void mirror_walk(const MirrorNode *nodes, const float *xr, uint32_t (&g)[CH],
+                                            MirrorNode (&nd)[CH], uint32_t depth) {
+    for (uint32_t s = 0; s < depth; s++) {
+        float v[CH];
+#pragma unroll
+        for (int k = 0; k < CH; k++) v[k] = xr[(nd[k].w & 0xffffu) * kPredPitch];
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            const float x = __uint_as_float(__float_as_uint(v[k]) ^ (nd[k].w & 0x80000000u));
+            g[k] += ((nd[k].w >> 16) & 0x7fffu) + (x < __uint_as_float(nd[k].t) ? 1u : 0u);
+        }
+#pragma unroll
+        for (int k = 0; k < CH; k++) nd[k] = load_node(nodes, g[k]);
     }
 }
 
@@ -255,7 +318,7 @@ __device__ __forceinline__ void predict_chunked(const PredictArgs &a) {
 #pragma unroll
                 for (int k = 0; k < kPredChains; k++) {
                     nid[k] = s_root[min(t0 + (uint32_t)k, t_hi - 1) - t_lo];
-                    nd[k] = s_nodes[nid[k]];
+                    nd[k] = load_node(s_nodes, nid[k]);
                 }
                 // branch-free rounds: a chain at its leaf re-reads it, so
                 // the LDS reads of all chains overlap
@@ -267,15 +330,13 @@ __device__ __forceinline__ void predict_chunked(const PredictArgs &a) {
 #pragma unroll
                     for (int k = 0; k < kPredChains; k++) {
                         const uint32_t meta = nd[k].meta;
-                        const bool miss = MISSING_NAN ? v[k] != v[k] : v[k] == a.missing;
-                        uint32_t right = v[k] < __uint_as_float(nd[k].value) ? 0u : 1u;
-                        right = miss ? (~meta >> 30) & 1u : right;  // missing: right unless default_left
+                        const uint32_t right = goes_right<MISSING_NAN>(v[k], meta, nd[k].value, a.missing);
                         const uint32_t next = nid[k] + ((meta >> 16) & 0x3fffu) + right;
                         nid[k] = (meta >> 31) ? nid[k] : next;
                     }
 #pragma unroll
                     for (int k = 0; k < kPredChains; k++) {
-                        nd[k] = s_nodes[nid[k]];
+                        nd[k] = load_node(s_nodes, nid[k]);
                         open = open || !(nd[k].meta >> 31);
                     }
                     if (!open) break;
@@ -337,7 +398,7 @@ __device__ __forceinline__ void predict_resident(const PredictArgs &a) {
 #pragma unroll
             for (int k = 0; k < CH; k++) {
                 g[k] = a.tree_root[min(t0 + (uint32_t)k, a.n_trees - 1)];
-                nd[k] = a.compact[g[k]];
+                nd[k] = load_node(a.compact, g[k]);
             }
             // branch-free rounds: a chain at its leaf re-reads it, so the
             // node loads of all chains are in flight together
@@ -348,16 +409,14 @@ __device__ __forceinline__ void predict_resident(const PredictArgs &a) {
 #pragma unroll
                 for (int k = 0; k < CH; k++) {
                     const uint32_t meta = nd[k].meta;
-                    const bool miss = MISSING_NAN ? v[k] != v[k] : v[k] == a.missing;
-                    uint32_t right = v[k] < __uint_as_float(nd[k].value) ? 0u : 1u;
-                    right = miss ? (~meta >> 30) & 1u : right;  // missing: right unless default_left
+                    const uint32_t right = goes_right<MISSING_NAN>(v[k], meta, nd[k].value, a.missing);
                     const uint32_t next = g[k] + ((meta >> 16) & 0x3fffu) + right;
                     g[k] = (meta >> 31) ? g[k] : next;
                 }
                 bool open = false;
 #pragma unroll
                 for (int k = 0; k < CH; k++) {
-                    nd[k] = a.compact[g[k]];
+                    nd[k] = load_node(a.compact, g[k]);
                     open = open || !(nd[k].meta >> 31);
                 }
                 if (!open) break;
@@ -390,6 +449,155 @@ extern "C" __global__ __launch_bounds__(64) void hbr_predict_resident_nan(Predic
 extern "C" __global__ __launch_bounds__(64) void hbr_predict_resident(PredictArgs a) {
     predict_resident<false, 16, true>(a);
 }
+
+// The mirror walk with rows resident in LDS and the nodes read through the
+// caches: a workgroup is one wave; it stages a 64-row block once (slot 0
+// NaN, feature f in slot f + 1) and walks it through every tree, CH trees
+// in flight per lane, each group for the largest depth among its trees.
+template <bool MISSING_NAN, int CH>
+__device__ __forceinline__ void predict_mirror(const PredictArgs &a) {
+    extern __shared__ float s_rows[];  // (n_cols + 1) * kPredPitch
+    const uint32_t lane = lane_id();
+    const float *xr = s_rows + lane;
+    s_rows[lane] = __builtin_nanf("");
+    const uint32_t n_blocks = (a.n + kPredLanes - 1) / kPredLanes;
+    for (uint32_t blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
+        const uint32_t r0 = blk * kPredLanes;
+        const uint32_t rows = min(kPredLanes, a.n - r0);
+        // the previous block's walk has read its rows: lanes finish in lockstep
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        stage_rows<true, true, MISSING_NAN>(s_rows, a.x + (size_t)r0 * a.n_cols, rows, a.n_cols, lane, a.missing);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane >= rows) continue;
+        const uint32_t r = r0 + lane;
+        float *out = a.out + (size_t)r * a.n_outputs;
+        if (a.n_outputs != 1)
+            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = a.base_score[o];
+        float acc = a.base_score[0];
+        for (uint32_t t0 = 0; t0 < a.n_trees; t0 += CH) {
+            uint32_t g[CH];
+            MirrorNode nd[CH];
+            uint32_t depth = 0;
+#pragma unroll
+            for (int k = 0; k < CH; k++) {
+                const uint32_t t = min(t0 + (uint32_t)k, a.n_trees - 1);
+                g[k] = a.mirror_root[t];
+                nd[k] = load_node(a.mirror, g[k]);
+                depth = max(depth, (uint32_t)a.tree_depth[t]);
+            }
+            mirror_walk<CH>(a.mirror, xr, g, nd, depth);
+#pragma unroll
+            for (int k = 0; k < CH; k++) {
+                const uint32_t t = t0 + (uint32_t)k;
+                if (t < a.n_trees) {
+                    if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.mirror_orig[g[k]];
+                    const float contrib = a.tree_weight[t] * __uint_as_float(nd[k].t);
+                    if (a.n_outputs == 1) {
+                        acc = acc + contrib;
+                    } else {
+                        float *o = out + a.tree_output[t];
+                        *o = *o + contrib;
+                    }
+                }
+            }
+        }
+        if (a.n_outputs == 1) out[0] = acc;
+    }
+}
+
+extern "C" __global__ __launch_bounds__(64) void hbr_predict_mirror_nan(PredictArgs a) { predict_mirror<true, 16>(a); }
+extern "C" __global__ __launch_bounds__(64) void hbr_predict_mirror(PredictArgs a) { predict_mirror<false, 16>(a); }
+
+// One test of the pair walk: 1 when the row goes to the second child.
+__device__ __forceinline__ uint32_t pair_test(const float *xr, uint32_t s8, uint32_t t) {
+    const float v = xr[(s8 & 0x7fu) * kPredPitch];
+    const float x = __uint_as_float(__float_as_uint(v) ^ ((s8 & 0x80u) << 24));
+    return x < __uint_as_float(t) ? 1u : 0u;
+}
+
+// Complete trees walked two levels per record (PredictArgs::pairs): rows
+// resident in LDS as in hbr_predict_mirror (one 64-row block per one-wave
+// workgroup, slot 0 NaN), CH trees in flight per lane; every record load
+// serves two levels and the last load reads only the leaf's value.
+template <bool MISSING_NAN, int CH>
+__device__ __forceinline__ void predict_pairs(const PredictArgs &a) {
+    extern __shared__ float s_rows[];  // (n_cols + 1) * kPredPitch
+    const uint32_t lane = lane_id();
+    const float *xr = s_rows + lane;
+    s_rows[lane] = __builtin_nanf("");
+    const uint32_t levels = a.pair_levels;
+    const uint32_t per_tree = ((1u << (2 * levels)) - 1u) / 3u;  // records
+    const uint32_t leaves = 1u << (2 * levels);
+    const uint32_t n_blocks = (a.n + kPredLanes - 1) / kPredLanes;
+    for (uint32_t blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
+        const uint32_t r0 = blk * kPredLanes;
+        const uint32_t rows = min(kPredLanes, a.n - r0);
+        // the previous block's walk has read its rows: lanes finish in lockstep
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        stage_rows<true, true, MISSING_NAN>(s_rows, a.x + (size_t)r0 * a.n_cols, rows, a.n_cols, lane, a.missing);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane >= rows) continue;
+        const uint32_t r = r0 + lane;
+        float *out = a.out + (size_t)r * a.n_outputs;
+        if (a.n_outputs != 1)
+            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = a.base_score[o];
+        float acc = a.base_score[0];
+        for (uint32_t t0 = 0; t0 < a.n_trees; t0 += CH) {
+            uint32_t pos[CH];
+#pragma unroll
+            for (int k = 0; k < CH; k++) pos[k] = 0;
+            uint32_t base = 0;  // first record of the level
+            for (uint32_t l = 0; l < levels; l++) {
+                PairRecord rec[CH];
+#pragma unroll
+                for (int k = 0; k < CH; k++) {
+                    const uint32_t t = min(t0 + (uint32_t)k, a.n_trees - 1);
+                    rec[k] = a.pairs[(size_t)t * per_tree + base + pos[k]];
+                }
+#pragma unroll
+                for (int k = 0; k < CH; k++) {
+                    const uint32_t s = rec[k].s;
+                    const uint32_t first = pair_test(xr, s, rec[k].t_node);
+                    const uint32_t t_c = first ? rec[k].t_second : rec[k].t_first;
+                    const uint32_t s_c = first ? s >> 16 : s >> 8;
+                    const uint32_t second = pair_test(xr, s_c, t_c);
+                    pos[k] = 4 * pos[k] + 2 * first + second;
+                }
+                base = 4 * base + 1;
+            }
+            uint32_t leaf[CH];
+#pragma unroll
+            for (int k = 0; k < CH; k++) {
+                const uint32_t t = min(t0 + (uint32_t)k, a.n_trees - 1);
+                leaf[k] = a.pair_values[(size_t)t * leaves + pos[k]];
+            }
+#pragma unroll
+            for (int k = 0; k < CH; k++) {
+                const uint32_t t = t0 + (uint32_t)k;
+                if (t < a.n_trees) {
+                    if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.pair_orig[(size_t)t * leaves + pos[k]];
+                    const float contrib = a.tree_weight[t] * __uint_as_float(leaf[k]);
+                    if (a.n_outputs == 1) {
+                        acc = acc + contrib;
+                    } else {
+                        float *o = out + a.tree_output[t];
+                        *o = *o + contrib;
+                    }
+                }
+            }
+        }
+        if (a.n_outputs == 1) out[0] = acc;
+    }
+}
+
+extern "C" __global__ __launch_bounds__(64) void hbr_predict_pairs_nan(PredictArgs a) { predict_pairs<true, 16>(a); }
+extern "C" __global__ __launch_bounds__(64) void hbr_predict_pairs(PredictArgs a) { predict_pairs<false, 16>(a); }
 
 // ---- evaluation sets --------------------------------------------------------
 //

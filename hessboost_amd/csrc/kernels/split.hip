@@ -107,11 +107,10 @@ __device__ __forceinline__ uint32_t node_slot(const ScanArgs &a, const ScanNode 
 
 using namespace hbr;
 
-extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) {
-    const uint32_t wave = threadIdx.x / kWave, lane = lane_id();
-    const uint32_t pair = blockIdx.x * (blockDim.x / kWave) + wave;
-    if (pair >= scan_nodes(a) * a.n_features) return;  // uniform per wave
-    const uint32_t node = pair / a.n_features, f = pair % a.n_features;
+// One wave: feature f of node `node`, its best candidate written to *out
+// by one lane.
+__device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, uint32_t f, ScanBest *out) {
+    const uint32_t lane = lane_id();
     const ScanNode nd = a.nodes[node];
     const uint32_t fs = a.feature_offset[f], nb = a.feature_offset[f + 1] - fs;
     Cand best;
@@ -226,7 +225,6 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
     }
     const uint64_t any_nan = __ballot(nan_seen);
     const uint64_t mine = __ballot(best.idx == bi && best.loss == bl && bi != 0xffffffffu);
-    ScanBest *out = a.per_feature + pair;
     if (mine == 0) {
         if (lane == 0) {
             ScanBest o;
@@ -250,17 +248,23 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
     }
 }
 
-// Per node: the feature-order merge. A candidate must beat the empty split
+extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) {
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t pair = blockIdx.x * (blockDim.x / kWave) + wave;
+    if (pair >= scan_nodes(a) * a.n_features) return;  // uniform per wave
+    scan_feature(a, pair / a.n_features, pair % a.n_features, a.per_feature + pair);
+}
+
+// One wave: the feature-order merge of a node's per-feature winners
+// (`per_node`, n_features records). A candidate must beat the empty split
 // (loss 0); equal losses keep the lower feature.
-extern "C" __global__ __launch_bounds__(64) void hbr_scan_merge(ScanArgs a) {
-    const uint32_t node = blockIdx.x;
-    if (node >= scan_nodes(a)) return;
+__device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, const ScanBest *per_node) {
     const uint32_t lane = lane_id();
     float bl = 0.0f;
     uint32_t bf = 0xffffffffu;
     uint32_t nan_flag = 0;
     for (uint32_t f = lane; f < a.n_features; f += kWave) {
-        const ScanBest c = a.per_feature[(size_t)node * a.n_features + f];
+        const ScanBest c = per_node[f];
         nan_flag |= c.flags & 2u;
         if (c.index == 0xffffffffu) continue;
         // features ascend within a lane: only a strictly larger loss replaces
@@ -289,7 +293,7 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_merge(ScanArgs a) {
             o.left = QBin{0, 0};
             o.right = QBin{0, 0};
         } else {
-            o = a.per_feature[(size_t)node * a.n_features + bf];
+            o = per_node[bf];
             o.flags |= nan_flag;
         }
         a.best[node] = o;
@@ -300,6 +304,12 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_merge(ScanArgs a) {
         const uint32_t *src = a.cat_sets + ((size_t)node * a.n_cat + a.cat_rank[win]) * kCatWords;
         for (uint32_t w = lane; w < kCatWords; w += kWave) a.best_sets[(size_t)node * kCatWords + w] = src[w];
     }
+}
+
+extern "C" __global__ __launch_bounds__(64) void hbr_scan_merge(ScanArgs a) {
+    const uint32_t node = blockIdx.x;
+    if (node >= scan_nodes(a)) return;
+    merge_node(a, node, a.per_feature + (size_t)node * a.n_features);
 }
 
 // ---- categorical features (builder/categorical.rs:48-170) ---------------------

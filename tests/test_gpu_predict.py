@@ -184,7 +184,7 @@ def test_resident_and_chunked_walks_agree_with_the_oracle():
     multi["n_outputs"] = 3
     multi["base_score"] = np.array([0.1, -0.2, 0.3], np.float32)
     want3 = O.predict_margin(multi, x)
-    for kind in ("resident", "chunked"):
+    for kind in ("pairs", "mirror", "resident", "chunked"):
         os.environ["HBROCM_PRED_KERNEL"] = kind
         try:
             f = hb.Forest(arrs, 1)
@@ -233,7 +233,9 @@ def test_malformed_forest_is_refused():
 @pytest.mark.parametrize("seed", range(12))
 def test_random_forests_match_oracle(seed):
     """Random unbalanced forests (depth 0 to 12, several outputs, tree
-    weights, NaN or a non-NaN missing value), both walks, bit for bit."""
+    weights, NaN or a non-NaN missing value), every walk, bit for bit; the
+    rows hold values equal to thresholds, signed zeros, infinities and (with
+    a non-NaN missing value) present NaNs."""
     import os
     rng = np.random.default_rng(500 + seed)
     f = int(rng.integers(1, 40))
@@ -248,9 +250,21 @@ def test_random_forests_match_oracle(seed):
     n = int(rng.choice([1, 63, 64, 65, 2_049]))
     x = rng.standard_normal((n, f)).astype(np.float32)
     missing = np.nan if rng.random() < 0.6 else -7.0
+    conds = arrs["split_cond"][arrs["left"] != -1]
+    if len(conds):
+        conds[: len(conds) // 4] = 0.0
+        arrs["split_cond"][np.nonzero(arrs["left"] != -1)[0]] = conds
+        hit = rng.random((n, f)) < 0.1
+        x[hit] = rng.choice(conds, int(hit.sum()))
+    x[rng.random((n, f)) < 0.03] = -0.0
+    x[rng.random((n, f)) < 0.03] = 0.0
+    x[rng.random((n, f)) < 0.02] = np.inf
+    x[rng.random((n, f)) < 0.02] = -np.inf
     x[rng.random((n, f)) < 0.1] = missing
+    if missing == missing:
+        x[rng.random((n, f)) < 0.03] = np.nan
     want, want_leaf = O.predict_margin(arrs, x, missing=missing, with_leaf=True)
-    for kind in ("resident", "chunked"):
+    for kind in ("pairs", "mirror", "resident", "chunked"):
         os.environ["HBROCM_PRED_KERNEL"] = kind
         try:
             fo = hb.Forest(arrs, k)
