@@ -138,6 +138,13 @@ struct GradArgs {
     float scale_pos_weight;
     float min_hess;
     float max_input;        // logistic vector range (80)
+    // Logistic pairs carried by the rows (set only for unit weights, a
+    // scale_pos_weight of 1 and labels 0 or 1, which make (g, h) a function
+    // of p and y alone): row i's word at pair_rows + i * pair_stride +
+    // pair_byte (padding bytes of the index) gets bits(p) | y << 31.
+    uint8_t *pair_rows;
+    uint32_t pair_stride;
+    uint32_t pair_byte;
 };
 
 // Softmax gradients of every class of every row (simd/mod.rs:502-600),
@@ -310,6 +317,11 @@ struct HistArgs {
     // CSR rows whose global bins ascend: row r's entries of bin range g are
     // row_ptr[r] + [csr_ranges[r * (groups + 1) + g], ... + g + 1]) (null: scan the row)
     const uint32_t *csr_ranges;
+    // Nonzero: the pairs are the logistic pairs the rows carry in the last
+    // word of their (single) 32-feature group (GradArgs::pair_rows), g = p - y
+    // and h = max(p * (1 - p), min_hess), instead of gpair.
+    uint32_t row_pairs;
+    float min_hess;
 };
 
 // Each CSR row's first entry of every kCsrGroupBins range (rows' global bins ascend).

@@ -65,6 +65,7 @@ void Engine::read_tunables() {
         if (t == 512 || t == 1024) hist_threads = (uint32_t)t;
     }
     if (const char *v = std::getenv("HBROCM_HIST_BIN_MAJOR")) hist_bin_major = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_ROW_PAIRS")) row_pairs = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_CSR_RANGES")) csr_range_table = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_WALK_BLOCKS")) {
@@ -369,6 +370,9 @@ void Engine::read_index(uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint6
     if (row_ptr && row_ptr_.size()) row_ptr_.download(row_ptr, n_rows_ + 1, s);
     if (gbins && !dense_ && gbins_.size()) gbins_.download(gbins, entries_, s);
     dev_.sync();
+    // a row's padding bytes read as zero (they may carry logistic pairs)
+    if (rows8 && rows8_.size() && stride_ > n_cols_)
+        for (uint64_t r = 0; r < n_rows_; r++) std::memset(rows8 + r * stride_ + n_cols_, 0, stride_ - n_cols_);
 }
 
 // ---- gradients -----------------------------------------------------------------
@@ -377,6 +381,7 @@ void Engine::load_margins(const float *m, uint64_t n, uint32_t outputs) {
     if (n != n_rows_ * outputs) fail(kInvalid, "load_margins: length is not n_rows * n_outputs");
     outputs_ = outputs;
     active_pairs_ = nullptr;
+    row_pairs_live_ = false;
     class_outputs_ = 0;
     margins_.resize(n);
     margins_.upload(m, n, dev_.stream());
@@ -394,6 +399,8 @@ void Engine::set_labels(const float *labels, const float *weights, uint64_t n) {
         weights_.resize(n);
         weights_.upload(weights, n, dev_.stream());
     }
+    labels_binary_ = true;
+    for (uint64_t i = 0; i < n && labels_binary_; i++) labels_binary_ = labels[i] == 0.0f || labels[i] == 1.0f;
     labels_loaded_ = true;
     dev_.sync();
 }
@@ -447,6 +454,7 @@ bool Engine::sums_exact(uint64_t m) const {
 
 void Engine::prepare(const float *gpair, uint64_t n) {
     if (n != n_rows_) fail(kInvalid, "prepare: one gradient pair per row");
+    row_pairs_live_ = false;
     active_pairs_ = nullptr;
     class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
@@ -486,8 +494,23 @@ static std::vector<uint64_t> expf_table() {
     return t;
 }
 
+// Logistic pairs a row can carry: with unit weights, a scale_pos_weight of
+// 1 and labels 0 or 1, (g, h) = (p - y, max(p (1 - p), min_hess)) follow
+// from p and y, which fit one word of the padding of a 32-byte row of at
+// most 28 features (the dense kernels' one 32-feature group).
+bool Engine::row_pairs_ok(const hbr_device_loss &loss) const {
+    return row_pairs && loss.kind == HBR_LOSS_LOGISTIC && loss.scale_pos_weight == 1.0f && !has_weights_ &&
+           labels_binary_ && dense_u8_ && stride_ == 32 && n_cols_ <= 28 && hist_features_per_group == 32 &&
+           outputs_ == 1;
+}
+
 GradArgs Engine::grad_args(const hbr_device_loss &loss) {
     GradArgs a{};
+    if (row_pairs_ok(loss)) {
+        a.pair_rows = rows8_.get();
+        a.pair_stride = stride_;
+        a.pair_byte = 28;
+    }
     a.margins = margins_.get();
     a.labels = labels_.get();
     a.weights = has_weights_ ? weights_.get() : nullptr;
@@ -515,6 +538,8 @@ void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     gpair_.resize(n_rows_ ? n_rows_ : 1);
     HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
     const GradArgs a = grad_args(loss);
+    row_pairs_live_ = a.pair_rows != nullptr;
+    row_pairs_min_hess_ = loss.min_hess;
     // grid-stride: a few workgroups per CU, one max fold each
     const uint32_t grad_blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)),
                                                     (uint32_t)dev_.cu_count() * 8);
@@ -574,6 +599,7 @@ void Engine::softmax_gradients_async(float min_hess) {
     if (k < 1 || k > kSoftmaxMaxClasses) fail(kRefused, "softmax gradients: 1 to 1024 classes");
     if (n_rows_ == 0) fail(kInvalid, "softmax gradients: no rows");
     hipStream_t s = dev_.stream();
+    row_pairs_live_ = false;
     active_pairs_ = nullptr;
     grains_known_ = false;
     class_pairs_.reserve((size_t)k * n_rows_);
@@ -769,11 +795,14 @@ bool Engine::reserve_slots(uint64_t n) {
 }
 
 // Per row: its bins (one byte per feature for a dense u8 index, else four
-// per stored entry), its gradient pair, and its id when the node's rows are
-// gathered through a row list.
+// per stored entry), its gradient pair (8 bytes, or the 4-byte word of a
+// pair the row carries), and its id when the node's rows are gathered
+// through a row list.
 uint64_t Engine::hist_bytes(uint64_t rows, bool gathered) const {
     const uint64_t bins = dense_u8_ ? n_cols_ : 4ull * (n_rows_ ? gbins_.size() / n_rows_ : 0);
-    return rows * (bins + 8 + (gathered ? 4 : 0));
+    // a pair carried by the row is its one word in the row's padding
+    const uint64_t pair = row_pairs_live_ && !level_pairs_ && dense_u8_ && stride_ == 32 ? 4 : 8;
+    return rows * (bins + pair + (gathered ? 4 : 0));
 }
 
 void Engine::set_scan_params(const ScanParams &p, const std::vector<int8_t> &monotone) {
@@ -848,6 +877,8 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.partial = d_partial_.get();
     a.total_bins = total_bins_;
     a.groups = groups;
+    a.row_pairs = row_pairs_live_ && !level_pairs_ && dense_u8_ && stride_ == 32 && fg == 32 ? 1u : 0u;
+    a.min_hess = row_pairs_min_hess_;
     const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"
                     : fg <= 8  ? "hbr_hist_dense8_fg8"
@@ -1465,6 +1496,8 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     WalkGradArgs wg{};
     wg.w = a;
     wg.g = grad_args(*next_loss);
+    row_pairs_live_ = wg.g.pair_rows != nullptr;
+    row_pairs_min_hess_ = next_loss->min_hess;
     dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
     FinishArgs f{scale_dev(), n_rows_, wg.g};
     dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
@@ -1658,6 +1691,8 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
         WalkGradArgs wg{};
         wg.w = a;
         wg.g = grad_args(*next_loss);
+        row_pairs_live_ = wg.g.pair_rows != nullptr;
+        row_pairs_min_hess_ = next_loss->min_hess;
         dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
         FinishArgs f{scale_dev(), n_rows_, wg.g};
         dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);

@@ -372,6 +372,11 @@ private:
                           uint32_t output, const uint32_t *poison, const float *cond = nullptr);
     uint32_t outputs_ = 1;
     bool labels_loaded_ = false, has_weights_ = false;
+    bool labels_binary_ = false;  // every label 0 or 1
+    // the staged pairs are the logistic pairs the rows carry (GradArgs::pair_rows)
+    bool row_pairs_live_ = false;
+    float row_pairs_min_hess_ = 0.0f;
+    bool row_pairs_ok(const hbr_device_loss &loss) const;
     // the per-tree scale, the root total and the root's winner, adjacent so
     // that the root's synchronisation reads them back with one copy
     struct RootBlock {
@@ -439,6 +444,7 @@ public:
     uint32_t hist_threads = 1024;
     uint32_t hist_waves = 1;
     bool hist_bin_major = true;  // [bin][feature] LDS layout (16 and 32 feature groups)
+    bool row_pairs = true;       // unit-weight logistic pairs carried in the rows' padding
     bool device_grow = true;     // depthwise trees decided on the device where eligible
     bool csr_range_table = true; // CSR histograms read each bin range's entries from a per-row table
     uint32_t walk_blocks_per_cu = 4;  // workgroups per CU of the device-tree margin walk (one resident wave)

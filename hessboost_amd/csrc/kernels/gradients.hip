@@ -76,19 +76,27 @@ namespace hbr {
 
 // The scalar sigmoid's pair (simd/mod.rs:425-427, simd/scalar.rs:8-29):
 // p = 1 / (expf(min(-m, 88.7)) + 1), w scaled for a label of exactly 1.
-__device__ __forceinline__ GPair logistic_scalar_pair(const GradArgs &a, float m, float y, float w) {
+__device__ __forceinline__ GPair logistic_scalar_pair(const GradArgs &a, float m, float y, float w, float *p_out) {
     const float p = 1.0f / (hbr_expf_libm(__builtin_fminf(-m, 88.7f), a.exp_table) + 1.0f);
     const float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
+    *p_out = p;
     return GPair{(p - y) * ww, __builtin_fmaxf(p * (1.0f - p), a.min_hess) * ww};
+}
+
+// The word a row carries for its logistic pair (GradArgs::pair_rows).
+__device__ __forceinline__ uint32_t pair_word(float p, float y) {
+    return __float_as_uint(p) | (y == 1.0f ? 0x80000000u : 0u);
 }
 
 // Row i's gradient pair from margin m, label y and weight w (all lanes of
 // the wave call it together: the logistic vector test is a ballot over
 // 8-row groups). kDefer: a row outside the vector path is listed for
 // hbr_finish_scale instead (keeping the f64 expf out of a hot loop).
+// *word: the row's pair word (pair_word) when its logistic pair is computed
+// here (left alone for a deferred row).
 template <bool kDefer>
 __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, bool active, float m, float y, float w,
-                                                uint32_t &mg, uint32_t &mh, uint32_t &bad) {
+                                                uint32_t &mg, uint32_t &mh, uint32_t &bad, uint32_t *word) {
     {
         float g = 0.0f, h = 0.0f;
         if (a.loss == kSquaredError) {
@@ -110,14 +118,17 @@ __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, b
                 g = (p - y) * ww;
                 float q = p * (1.0f - p);
                 h = (q > a.min_hess ? q : a.min_hess) * ww;
+                *word = pair_word(p, y);
             } else if (active) {
                 if (kDefer) {
                     a.scalar_list[atomicAdd(&a.scale->scalar_rows, 1u)] = i;
                     return;
                 }
-                const GPair q = logistic_scalar_pair(a, m, y, w);
+                float p;
+                const GPair q = logistic_scalar_pair(a, m, y, w, &p);
                 g = q.g;
                 h = q.h;
+                *word = pair_word(p, y);
             }
         }
         if (active) {
@@ -133,7 +144,10 @@ __device__ __forceinline__ void row_gradient(const GradArgs &a, uint32_t i, bool
                                              uint32_t &mh, uint32_t &bad) {
     const float y = active ? a.labels[i] : 0.0f;
     const float w = (active && a.weights) ? a.weights[i] : 1.0f;
-    row_gradient_yw<false>(a, i, active, m, y, w, mg, mh, bad);
+    uint32_t word = 0;
+    row_gradient_yw<false>(a, i, active, m, y, w, mg, mh, bad, &word);
+    if (a.pair_rows && active)  // uniform flag; one word in the row's padding
+        *reinterpret_cast<uint32_t *>(a.pair_rows + (size_t)i * a.pair_stride + a.pair_byte) = word;
 }
 
 }  // namespace hbr
@@ -239,8 +253,13 @@ extern "C" __global__ __launch_bounds__(256) void hbr_finish_scale(FinishArgs a)
     for (uint32_t j = threadIdx.x; j < listed; j += blockDim.x) {
         const uint32_t r = a.grad.scalar_list[j];
         const float w = a.grad.weights ? a.grad.weights[r] : 1.0f;
-        const GPair p = logistic_scalar_pair(a.grad, a.grad.margins[r], a.grad.labels[r], w);
+        const float y = a.grad.labels[r];
+        float pr;
+        const GPair p = logistic_scalar_pair(a.grad, a.grad.margins[r], y, w, &pr);
         a.grad.gpair[r] = p;
+        if (a.grad.pair_rows)
+            *reinterpret_cast<uint32_t *>(a.grad.pair_rows + (size_t)r * a.grad.pair_stride + a.grad.pair_byte) =
+                pair_word(pr, y);
         mg = max(mg, __float_as_uint(p.g) & 0x7fffffffu);
         mh = max(mh, __float_as_uint(p.h) & 0x7fffffffu);
         bad += (!__builtin_isfinite(p.g) || !__builtin_isfinite(p.h)) ? 1u : 0u;

@@ -117,11 +117,21 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
     const uint32_t lane = lane_id();
     const uint32_t rot = lane & (FG - 1);
     const uint32_t end = t.row0 + t.rows;
+    const bool row_pairs = a.row_pairs != 0;  // uniform
     for (uint32_t j = t.row0 + threadIdx.x; j < end; j += blockDim.x) {
         const uint32_t r = nd.contiguous ? nd.seg.offset + j : rows[j];
-        const GPair p = gpair[r];
         uint32_t w[W];
-        load_bins<FG>(a.bins8 + (size_t)r * a.stride + f0, w);
+        GPair p;
+        if (row_pairs) {  // the logistic pair from the row's last word (one cache line per row)
+            load_bins<FG>(a.bins8 + (size_t)r * a.stride + f0, w);
+            const float pv = __uint_as_float(w[W - 1] & 0x7fffffffu);
+            const float y = (w[W - 1] >> 31) ? 1.0f : 0.0f;
+            const float q = pv * (1.0f - pv);
+            p = GPair{(pv - y) * 1.0f, (q > a.min_hess ? q : a.min_hess) * 1.0f};
+        } else {
+            p = gpair[r];
+            load_bins<FG>(a.bins8 + (size_t)r * a.stride + f0, w);
+        }
         const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
         const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
         rotate_bytes<W>(w, rot);

@@ -431,7 +431,15 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
                     a.margins[(size_t)r * a.m_stride + a.output] = m[k];
                 }
             }
-            if (r < end) row_gradient_yw<true>(ga, r, active, m[k], y[k], wt[k], mg, mh, bad);
+            if (r < end) {
+                uint32_t word = w[k][7];  // a deferred row's word is written by hbr_finish_scale
+                row_gradient_yw<true>(ga, r, active, m[k], y[k], wt[k], mg, mh, bad, &word);
+                if (ga.pair_rows && active) {  // the whole 32-byte row back, its pair in the last word
+                    uint4 *dst = reinterpret_cast<uint4 *>(ga.pair_rows + (size_t)r * 32u);
+                    dst[0] = make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]);
+                    dst[1] = make_uint4(w[k][4], w[k][5], w[k][6], word);
+                }
+            }
         }
     }
     fold_block(ga.scale, mg, mh, bad);

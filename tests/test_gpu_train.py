@@ -356,3 +356,54 @@ def test_pipelined_rounds_with_rows_beyond_the_vector_range():
             assert np.array_equal(a[key], b[key]), key
     assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
     assert np.all(np.abs(ma[far]) > 80)
+
+
+@pytest.mark.parametrize("far_rows", [False, True])
+def test_row_carried_logistic_pairs_give_identical_trees(far_rows):
+    """Unit-weight logistic with labels 0 and 1 on rows of at most 28
+    features: the rows carry p and y in their padding and the histograms
+    derive (g, h) from them. The trees and margins equal, bit for bit, those
+    grown from the pair array (HBROCM_ROW_PAIRS=0), with rows beyond the
+    vector range (their pairs written by the scalar finish) or without; the
+    root's byte count shows which path ran (a 4-byte word against an 8-byte
+    pair per row)."""
+    import os
+    rng = np.random.default_rng(23)
+    n, f = 50_003, 20
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    x[:, 3] = np.round(x[:, 3])
+    y = (x[:, 0] + 0.5 * x[:, 3] * x[:, 1] + 0.3 * rng.standard_normal(n) > 0).astype(np.float32)
+    m0 = np.zeros(n, np.float32)
+    far = rng.choice(n, 300, replace=False)
+    m0[far] = np.where(rng.random(300) < 0.5, -100.0, 100.0).astype(np.float32)
+    params = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}
+    index = hb.DMatrix(x, label=y).index(256)
+    runs = []
+    for flag in (None, "0"):
+        old = os.environ.pop("HBROCM_ROW_PAIRS", None)
+        if flag is not None:
+            os.environ["HBROCM_ROW_PAIRS"] = flag
+        try:
+            eng = hb.Engine(index, 0)
+        finally:
+            os.environ.pop("HBROCM_ROW_PAIRS", None)
+            if old is not None:
+                os.environ["HBROCM_ROW_PAIRS"] = old
+        tr = hb.Trainer(eng, params, y)
+        if far_rows:
+            eng.load_margins(m0)
+            eng.gradients(LOSS_LOGISTIC, y)
+        before = eng.counters()
+        tr.boost(1)
+        after = eng.counters()
+        per_row = (after["hist_bytes"] - before["hist_bytes"]) / (after["hist_rows"] - before["hist_rows"])
+        tr.boost(3)
+        runs.append((tr.trees(), tr.margins(), per_row))
+    (ta, ma, ra), (tb, mb, rb) = runs
+    assert rb - ra == 4, (ra, rb)  # the 4-byte word, then the 8-byte pair per row
+    for a, b in zip(ta, tb):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
+    if far_rows:
+        assert np.all(np.abs(ma[far]) > 80)
