@@ -29,6 +29,11 @@ HIST_KERNEL = "hbr_hist_dense8"
 # (no published figure): every CU running a 1,024-thread workgroup of
 # conflict-free ds_add_u64 loops reaches 5.7 T lane-ops/s (32-bit adds: 8.4 T)
 LDS_ATOMIC_PEAK_T = 5.7
+# The prediction walks' bound: the texture path (vector memory address and
+# data units) spends at least 16 clocks of a CU on a wave-wide load (64
+# lanes; up to 64 clocks as the lanes' cache lines diverge), measured on
+# MI355X for 4-, 8- and 16-byte loads alike: 2.4 GHz x 256 CUs / 16.
+TEXTURE_PEAK_LOADS = 2.4e9 * 256 / 16
 
 
 def log(msg):
@@ -445,18 +450,29 @@ def main():
         pms = sum(pstats[k][0] for k in pkern)
         pl = sum(pstats[k][1] for k in pkern)
         pbytes = n * (4 * f + 4)
-        pach = pbytes / (pms / max(1, pl) * 1e-3) / 1e9 if pms > 0 else 0.0
+        launch_s = pms / max(1, pl) * 1e-3
+        pach = pbytes / launch_s / 1e9 if pms > 0 else 0.0
         node_steps = n * args.predict_trees * 8
-        log(f"predict: {mrows:.1f} Mrows/s; kernel {pms / max(1, pl):.2f} ms per launch, {pach:.0f} GB/s")
+        # wave-wide node loads of the walk that ran: the pair walk loads one
+        # record per two levels and the leaf's value (depth 8: 5 per tree),
+        # the mirror walk one node per level and the leaf (9)
+        per_tree = 5 if any("pairs" in k for k in pkern) else 9
+        loads = (n + 63) // 64 * args.predict_trees * per_tree
+        ptraffic, _, ptraffic_src = measured_traffic(pkern[0] if pkern else "hbr_predict")
+        log(f"predict: {mrows:.1f} Mrows/s; kernel {launch_s * 1e3:.2f} ms per launch, {pach:.0f} GB/s")
         pred = {
             "metric": "batch predict Mrows/s", "value": round(mrows, 2), "unit": "Mrows/s",
             "steps": args.predict_steps,
             "config": {"workload": f"{args.predict_trees}-tree depth-8 forest, {n:,} x {f} f32 rows, 2% NaN"},
-            "roofline": {"kernel": "/".join(pkern) or "hbr_predict", "bound": "hbm", "achieved": round(pach, 1),
-                         "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(pach / HBM_PEAK_GBS, 4), "traffic": None,
-                         "avg_launch_ms": round(pms / max(1, pl), 4),
-                         "node_steps_per_s": round(node_steps / (pms / max(1, pl) * 1e-3), 1) if pms else None},
+            "roofline": {"kernel": "/".join(pkern) or "hbr_predict", "bound": "texture path",
+                         "achieved": round(loads / launch_s, 1) if pms else 0.0, "peak": TEXTURE_PEAK_LOADS,
+                         "unit": "wave-wide loads/s",
+                         "frac": round(loads / launch_s / TEXTURE_PEAK_LOADS, 4) if pms else 0.0,
+                         "loads_per_launch": loads, "avg_launch_ms": round(launch_s * 1e3, 4),
+                         "node_steps_per_s": round(node_steps / launch_s, 1) if pms else None,
+                         "hbm": {"achieved": round(pach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(pach / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": pbytes,
+                                 "traffic": ptraffic, "traffic_source": ptraffic_src}},
         }
         if arrs is not None:
             pred["cpu_baseline"] = cpu_predict_baseline(args, arrs, xp)
