@@ -20,7 +20,9 @@ SUMS_EXACT, SUMS_FIXED_POINT = 0, 1
 LOSS_SQUARED_ERROR, LOSS_LOGISTIC, LOSS_SOFTMAX = 0, 1, 2
 OBJ_SQUARED_ERROR, OBJ_LOGISTIC, OBJ_SOFTMAX, OBJ_LOGITRAW = 0, 1, 2, 3
 GROW_DEPTHWISE, GROW_LOSSGUIDE = 0, 1
-SCAN_EMPTY, SCAN_NUMERIC = 0, 2
+SCAN_EMPTY, SCAN_REPLAY, SCAN_NUMERIC, SCAN_CATEGORICAL = 0, 1, 2, 3
+FALLBACK_NUMERIC_SCORE, FALLBACK_CATEGORICAL_ORDER, FALLBACK_CATEGORICAL_SCORE = 1, 2, 3
+TRANSFORM_SIGMOID, TRANSFORM_SOFTMAX, TRANSFORM_CLASS_INDEX = 1, 2, 3
 
 P = C.POINTER
 u32p, u64p, i64p, f32p, f64p, u8p, i8p, i32p = (P(C.c_uint32), P(C.c_uint64), P(C.c_int64), P(C.c_float),
@@ -54,7 +56,7 @@ class Segment(C.Structure):
 
 class RowSplit(C.Structure):
     _fields_ = [("seg", Segment), ("feature", C.c_uint32), ("below", C.c_uint32),
-                ("default_left", C.c_uint32), ("pad", C.c_uint32)]
+                ("default_left", C.c_uint32), ("n_table", C.c_uint32), ("table", u8p)]
 
 
 class Partitioned(C.Structure):
@@ -84,7 +86,9 @@ class NodeScan(C.Structure):
                 ("acc_g", C.c_double), ("acc_h", C.c_double), ("left_g", C.c_double),
                 ("left_h", C.c_double), ("right_g", C.c_double), ("right_h", C.c_double),
                 ("fixed_left_g", C.c_int64), ("fixed_left_h", C.c_int64),
-                ("fixed_right_g", C.c_int64), ("fixed_right_h", C.c_int64)]
+                ("fixed_right_g", C.c_int64), ("fixed_right_h", C.c_int64),
+                ("default_left", C.c_uint32), ("fallback", C.c_uint32), ("cat_begin", C.c_uint32),
+                ("cat_end", C.c_uint32)]
 
 
 class EngineCounters(C.Structure):
@@ -156,6 +160,7 @@ SIGNATURES = {
     "hbr_reserve_hists": (C.c_int, [C.c_void_p, C.c_uint64, P(C.c_int)]),
     "hbr_build_resident": (C.c_int, [C.c_void_p, P(Segment), C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p, C.c_uint64]),
     "hbr_scan_resident": (C.c_int, [C.c_void_p, P(RegParams), P(ScanRequest), C.c_uint64, P(NodeScan)]),
+    "hbr_scan_categories": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
     "hbr_read_hist": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p]),
     "hbr_engine_counters_read": (C.c_int, [C.c_void_p, P(EngineCounters)]),
     "hbr_set_profiling": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p]),
@@ -181,6 +186,9 @@ SIGNATURES = {
     "hbr_predict_margin": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_void_p]),
     "hbr_predict_margin_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_void_p, C.c_void_p]),
     "hbr_predict_leaf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_void_p]),
+    "hbr_predict_margin_from": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_void_p,
+                                          C.c_void_p]),
+    "hbr_pred_transform": (C.c_int, [C.c_int, C.c_void_p, C.c_uint64, C.c_uint32]),
     "hbr_forest_set_profiling": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p]),
     "hbr_forest_kernel_stats": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
     "hbr_device_alloc": (C.c_int, [C.c_int, C.c_uint64, P(C.c_void_p)]),

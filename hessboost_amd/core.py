@@ -264,13 +264,22 @@ class Engine:
         return (out, fx) if fixed else out
 
     def partition(self, splits):
-        """splits: [(segment, feature, below, default_left)] -> [(left, right)]."""
+        """splits: [(segment, feature, rule, default_left)] -> [(left, right)];
+        rule is RowRule::Below's limit (an int) or RowRule::Table's per-bin
+        directions (a sequence of bools, one per bin of the feature)."""
         arr = (A.RowSplit * len(splits))()
-        for i, (seg, f, below, dl) in enumerate(splits):
+        keep = []
+        for i, (seg, f, rule, dl) in enumerate(splits):
             arr[i].seg = seg
             arr[i].feature = f
-            arr[i].below = below
             arr[i].default_left = int(dl)
+            if np.ndim(rule) == 0:
+                arr[i].below = int(rule)
+            else:
+                table = np.ascontiguousarray(rule, np.uint8)
+                keep.append(table)
+                arr[i].n_table = table.size
+                arr[i].table = A.typed(table, C.c_uint8)
         out = (A.Partitioned * len(splits))()
         A.check(A.lib().hbr_partition(self._h, arr, len(splits), out))
         return [(out[i].left, out[i].right) for i in range(len(splits))]
@@ -376,7 +385,11 @@ class Engine:
         out = (A.NodeScan * len(requests))()
         rp = A.RegParams(*reg)
         A.check(A.lib().hbr_scan_resident(self._h, C.byref(rp), arr, len(requests), out))
-        return [out[i] for i in range(len(requests))]
+        scans = [out[i] for i in range(len(requests))]
+        pool = np.zeros(max([s.cat_end for s in scans if s.kind == A.SCAN_CATEGORICAL], default=0), np.uint32)
+        A.check(A.lib().hbr_scan_categories(self._h, A.ptr(pool), pool.size))
+        self.scan_categories = pool
+        return scans
 
     def read_hist(self, slot):
         out = np.empty(2 * self.total_bins, np.float64)
@@ -577,12 +590,19 @@ class Booster:
         m = m if self.n_outputs == 1 else m.reshape(-1, self.n_outputs)
         if output_margin or self.objective in ("reg:squarederror", "binary:logitraw"):
             return m
-        if self.objective in ("binary:logistic", "reg:logistic"):
-            # XGBoost's common::Sigmoid (simd/mod.rs:425-427) per value, in f32
-            t = np.minimum(-m, np.float32(88.7)).astype(np.float32)
-            return (np.float32(1.0) / (np.exp(t, dtype=np.float32) + np.float32(1.0))).astype(np.float32)
-        z = np.exp((m - m.max(axis=1, keepdims=True)).astype(np.float32))
-        return (z / z.sum(axis=1, keepdims=True)).astype(np.float32)
+        # the objective's transform on the host with the C library's expf
+        # (Transform::apply, model/transform.rs:74-104)
+        kind = {"binary:logistic": A.TRANSFORM_SIGMOID, "reg:logistic": A.TRANSFORM_SIGMOID,
+                "multi:softprob": A.TRANSFORM_SOFTMAX, "multi:softmax": A.TRANSFORM_CLASS_INDEX}.get(self.objective)
+        if kind is None:
+            raise NotImplementedError(f"the {self.objective} transform is not implemented; "
+                                      "predict(..., output_margin=True) gives the margins")
+        v = np.ascontiguousarray(m, np.float32).reshape(-1).copy()
+        n_rows = v.size // self.n_outputs
+        A.check(A.lib().hbr_pred_transform(kind, A.ptr(v), n_rows, self.n_outputs))
+        if kind == A.TRANSFORM_CLASS_INDEX:
+            return v[:n_rows]
+        return v if self.n_outputs == 1 else v.reshape(n_rows, self.n_outputs)
 
     # The reference's JSON model document (model/serde.rs:57-136): every
     # field predictions depend on is written, the nullable ones as null.
@@ -909,10 +929,20 @@ class Forest:
         except Exception:
             pass
 
-    def predict_margin(self, x, missing=np.nan):
+    def predict_margin(self, x, missing=np.nan, init_margins=None):
+        """Margins [n_rows * n_outputs]; init_margins (the same shape) are
+        each row's starting margins in place of the base scores."""
         x = np.ascontiguousarray(x, np.float32)
         out = np.empty(x.shape[0] * self.n_outputs, np.float32)
-        A.check(A.lib().hbr_predict_margin(self._h, A.ptr(x), x.shape[0], x.shape[1], float(missing), A.ptr(out)))
+        if init_margins is None:
+            A.check(A.lib().hbr_predict_margin(self._h, A.ptr(x), x.shape[0], x.shape[1], float(missing),
+                                               A.ptr(out)))
+        else:
+            init = np.ascontiguousarray(init_margins, np.float32).reshape(-1)
+            if init.size != out.size:
+                raise ValueError("init_margins must hold n_rows * n_outputs values")
+            A.check(A.lib().hbr_predict_margin_from(self._h, A.ptr(x), x.shape[0], x.shape[1], float(missing),
+                                                    A.ptr(init), A.ptr(out)))
         return out
 
     def predict_leaf(self, x, missing=np.nan):

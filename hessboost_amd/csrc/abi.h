@@ -398,14 +398,23 @@ struct ScanParams {
 constexpr uint32_t kCatMaxBins = 1024;
 constexpr uint32_t kCatWords = kCatMaxBins / 32;
 constexpr uint32_t kScanCategorical = 4u;
+// ScanBest::flags bits asking for a host replay of the node (the trait's
+// NodeScan::Replay reasons, src/tree/hist/mod.rs:313-331): a numeric
+// candidate's score is NaN; a categorical weight is not finite (the sort's
+// order is then not total); a categorical candidate's score is NaN.
+constexpr uint32_t kScanNumericNaN = 2u;
+constexpr uint32_t kScanCatOrder = 8u;
+constexpr uint32_t kScanCatNaN = 16u;
+constexpr uint32_t kScanReplay = kScanNumericNaN | kScanCatOrder | kScanCatNaN;
 
 // Best candidate of one feature (or of one node after the merge).
 struct ScanBest {
     float loss;              // -inf: none
     uint32_t feature;
     uint32_t index;          // candidate order within the feature
-    uint32_t flags;          // bit0 backward (categorical: missing values go left), bit1 NaN seen,
-                             // bit2 (kScanCategorical) a categorical split: `left` is its set's child
+    uint32_t flags;          // bit0 backward (categorical: missing values go left), bit2
+                             // (kScanCategorical) a categorical split: `left` is its set's child;
+                             // kScanReplay bits
     QBin left;
     QBin right;
 };
@@ -679,6 +688,7 @@ struct PredictArgs {
     const float *tree_weight;
     const uint32_t *tree_output;
     const float *base_score;
+    const float *init;            // n x n_outputs starting margins, or null: base_score
     const float *x;               // n x n_cols row-major
     float *out;                   // n x n_outputs
     int32_t *leaf_out;            // n x n_trees or null

@@ -1,5 +1,6 @@
 // The extern "C" boundary (include/hessboost_rocm.h): argument checks,
 // status codes, per-handle locking and the sticky failure flag.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -23,6 +24,7 @@ struct hbr_index {
 };
 struct hbr_engine {
     std::unique_ptr<Engine> e;
+    std::vector<uint32_t> scan_categories;  // the last scan's category pool
 };
 struct hbr_trainer {
     hbr_engine *engine;
@@ -146,6 +148,50 @@ size_t copy_string(const std::string &s, char *buf, size_t len) {
 extern "C" {
 
 size_t hbr_last_error(char *buf, size_t len) { return copy_string(g_error, buf, len); }
+
+int hbr_pred_transform(int kind, float *values, uint64_t n_rows, uint32_t n_outputs) {
+    return guard([&] {
+        if (!values && n_rows) fail(kInvalid, "transform: null values");
+        if (n_outputs == 0) fail(kInvalid, "transform: no outputs");
+        const int64_t rows = (int64_t)n_rows;
+        const uint32_t k = n_outputs;
+        switch (kind) {
+        case HBR_TRANSFORM_SIGMOID: {
+            const int64_t n = rows * (int64_t)k;
+#pragma omp parallel for schedule(static) if (n >= (1 << 15))
+            for (int64_t i = 0; i < n; i++) values[i] = 1.0f / (expf(fminf(-values[i], 88.7f)) + 1.0f);
+            break;
+        }
+        case HBR_TRANSFORM_SOFTMAX:
+#pragma omp parallel for schedule(static) if (rows * k >= (1 << 15))
+            for (int64_t r = 0; r < rows; r++) {
+                float *v = values + r * k;
+                float wmax = v[0];
+                for (uint32_t c = 1; c < k; c++) wmax = fmaxf(v[c], wmax);
+                double wsum = 0.0;
+                for (uint32_t c = 0; c < k; c++) {
+                    v[c] = expf(v[c] - wmax);
+                    wsum += (double)v[c];
+                }
+                const float s = (float)wsum;
+                for (uint32_t c = 0; c < k; c++) v[c] /= s;
+            }
+            break;
+        case HBR_TRANSFORM_CLASS_INDEX:
+            // row r lands at index r, at or before its own values
+            for (int64_t r = 0; r < rows; r++) {
+                const float *v = values + r * k;
+                uint32_t best = 0;
+                for (uint32_t c = 1; c < k; c++)
+                    if (v[c] > v[best]) best = c;
+                values[r] = (float)best;
+            }
+            break;
+        default:
+            fail(kInvalid, "transform: unknown kind");
+        }
+    });
+}
 
 int hbr_device_count(int *count) {
     return guard([&] {
@@ -380,12 +426,24 @@ int hbr_root_total(hbr_engine *h, const hbr_segment *seg, double out[2]) {
 int hbr_partition(hbr_engine *h, const hbr_row_split *splits, uint64_t n, hbr_partitioned *out) {
     return with_engine(h, [&](Engine &e) {
         std::vector<LevelSplit> ls(n);
+        const auto &fo = e.feature_offset();
         for (uint64_t i = 0; i < n; i++) {
-            ls[i].seg = seg_of(e, splits[i].seg);
-            if (splits[i].feature >= e.n_cols()) fail(kInvalid, "partition: feature beyond the index");
-            ls[i].feature = splits[i].feature;
-            ls[i].limit = splits[i].below;
-            ls[i].default_left = splits[i].default_left ? 1u : 0u;
+            const hbr_row_split &sp = splits[i];
+            ls[i].seg = seg_of(e, sp.seg);
+            if (sp.feature >= e.n_cols()) fail(kInvalid, "partition: feature beyond the index");
+            ls[i].feature = sp.feature;
+            ls[i].limit = sp.below;
+            ls[i].default_left = sp.default_left ? 1u : 0u;
+            if (sp.table) {
+                // RowRule::Table: the local bins that go left
+                const uint32_t nb = fo[sp.feature + 1] - fo[sp.feature];
+                if (sp.n_table != nb) fail(kInvalid, "partition: a table must hold one entry per bin of its feature");
+                if (!e.is_categorical(sp.feature)) fail(kRefused, "partition: a table on a numeric feature");
+                ls[i].categorical = true;
+                ls[i].limit = 0;
+                for (uint32_t b = 0; b < nb; b++)
+                    if (sp.table[b]) ls[i].table[b / 32] |= 1u << (b % 32);
+            }
         }
         auto kids = e.level(ls, true);
         for (uint64_t i = 0; i < n; i++) {
@@ -539,35 +597,70 @@ int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_r
             }
             in[i] = ScanInput{req[i].slot, t, req[i].root_gain, req[i].lower, req[i].upper};
         }
-        auto best = e.scan(in);
+        std::vector<uint32_t> sets;
+        auto best = e.scan(in, &sets);
         const auto &fo = e.feature_offset();
+        const float *cuts = e.cut_values().data();
+        const int eg = e.scale().exp_g, eh = e.scale().exp_h;
+        h->scan_categories.clear();
         for (uint64_t i = 0; i < n; i++) {
             hbr_node_scan o{};
             const ScanBest &b = best[i];
+            if (b.flags & kScanReplay) {
+                // a NaN score or a categorical order that is not total: the
+                // host replays the node from its histogram (NodeScan::Replay)
+                o.kind = HBR_SCAN_REPLAY;
+                o.fallback = (b.flags & kScanCatOrder)     ? HBR_FALLBACK_CATEGORICAL_ORDER
+                             : (b.flags & kScanCatNaN)     ? HBR_FALLBACK_CATEGORICAL_SCORE
+                                                           : HBR_FALLBACK_NUMERIC_SCORE;
+                out[i] = o;
+                continue;
+            }
             if (b.index == 0xffffffffu) {
                 o.kind = HBR_SCAN_EMPTY;
                 out[i] = o;
                 continue;
             }
-            const uint32_t nb = fo[b.feature + 1] - fo[b.feature];
-            o.kind = HBR_SCAN_NUMERIC;
             o.feature = b.feature;
             o.loss_chg = b.loss;
-            o.backward = b.index >= nb ? 1u : 0u;
-            o.offset = o.backward ? nb - 1 - (b.index - nb) : b.index;
-            const int eg = e.scale().exp_g, eh = e.scale().exp_h;
             o.left_g = std::ldexp((double)b.left.g, eg);
             o.left_h = std::ldexp((double)b.left.h, eh);
             o.right_g = std::ldexp((double)b.right.g, eg);
             o.right_h = std::ldexp((double)b.right.h, eh);
-            o.acc_g = o.backward ? o.right_g : o.left_g;
-            o.acc_h = o.backward ? o.right_h : o.left_h;
             o.fixed_left_g = b.left.g;
             o.fixed_left_h = b.left.h;
             o.fixed_right_g = b.right.g;
             o.fixed_right_h = b.right.h;
+            const uint32_t nb = fo[b.feature + 1] - fo[b.feature];
+            if (b.flags & kScanCategorical) {
+                // the set's category codes, ascending (BestSplit's sorted set)
+                o.kind = HBR_SCAN_CATEGORICAL;
+                o.default_left = b.flags & 1u;
+                const uint32_t *set = sets.data() + i * kCatWords;
+                std::vector<uint32_t> codes;
+                for (uint32_t k = 0; k < nb; k++)
+                    if (set[k / 32] >> (k % 32) & 1u) codes.push_back(category_code(cuts[fo[b.feature] + k]));
+                std::sort(codes.begin(), codes.end());
+                o.cat_begin = (uint32_t)h->scan_categories.size();
+                h->scan_categories.insert(h->scan_categories.end(), codes.begin(), codes.end());
+                o.cat_end = (uint32_t)h->scan_categories.size();
+                out[i] = o;
+                continue;
+            }
+            o.kind = HBR_SCAN_NUMERIC;
+            o.backward = b.index >= nb ? 1u : 0u;
+            o.offset = o.backward ? nb - 1 - (b.index - nb) : b.index;
+            o.acc_g = o.backward ? o.right_g : o.left_g;
+            o.acc_h = o.backward ? o.right_h : o.left_h;
             out[i] = o;
         }
+    });
+}
+
+int hbr_scan_categories(hbr_engine *h, uint32_t *out, uint64_t n) {
+    return with_engine(h, [&](Engine &) {
+        if (n != h->scan_categories.size()) fail(kInvalid, "scan categories: n must equal the pool's length");
+        if (n) std::memcpy(out, h->scan_categories.data(), n * sizeof(uint32_t));
     });
 }
 
@@ -746,12 +839,19 @@ int hbr_predict_margin_device(hbr_forest *h, const float *x, uint64_t n, uint64_
 }
 
 int hbr_predict_margin(hbr_forest *h, const float *x, uint64_t n, uint64_t n_cols, float missing, float *out) {
+    return hbr_predict_margin_from(h, x, n, n_cols, missing, nullptr, out);
+}
+
+int hbr_predict_margin_from(hbr_forest *h, const float *x, uint64_t n, uint64_t n_cols, float missing,
+                            const float *init_margins, float *out) {
     return with_forest(h, [&](Forest &f) {
         if (n == 0) return;
-        DBuf<float> dx(n * n_cols), dout(n * f.n_outputs());
+        const uint64_t k = f.n_outputs();
+        DBuf<float> dx(n * n_cols), dout(n * k), dinit(init_margins ? n * k : 0);
         dx.upload(x, n * n_cols, f.dev().stream());
-        f.predict_device(dx.get(), n, n_cols, missing, dout.get(), nullptr);
-        dout.download(out, n * f.n_outputs(), f.dev().stream());
+        if (init_margins) dinit.upload(init_margins, n * k, f.dev().stream());
+        f.predict_device(dx.get(), n, n_cols, missing, dout.get(), nullptr, init_margins ? dinit.get() : nullptr);
+        dout.download(out, n * k, f.dev().stream());
         f.dev().sync();
     });
 }

@@ -977,19 +977,26 @@ void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit 
 }
 
 // Scan nodes given on the host: upload, scan, copy the winners into `out`
-// (pinned; valid after the next synchronisation).
-void Engine::scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out) {
+// and, with categorical features, their sets into `sets` (both pinned; valid
+// after the next synchronisation).
+void Engine::scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out, uint32_t *sets) {
     hipStream_t s = dev_.stream();
     upload_vec(d_snodes_, nodes, stage_, s);
     d_best_.reserve(nodes.size());
-    launch_scan(d_snodes_.get(), (uint32_t)nodes.size(), nullptr, nullptr, d_best_.get());
+    uint32_t *sets_dev = nullptr;
+    if (n_cat_) {
+        d_scan_sets_.reserve(nodes.size() * kCatWords);
+        sets_dev = d_scan_sets_.get();
+    }
+    launch_scan(d_snodes_.get(), (uint32_t)nodes.size(), nullptr, nullptr, d_best_.get(), nullptr, sets_dev);
     d_best_.download(out, nodes.size(), s);
+    if (sets && sets_dev) d_scan_sets_.download(sets, nodes.size() * kCatWords, s);
 }
 
-std::vector<ScanBest> Engine::scan(const std::vector<ScanInput> &in) {
+std::vector<ScanBest> Engine::scan(const std::vector<ScanInput> &in, std::vector<uint32_t> *sets) {
     std::vector<ScanBest> out(in.size());
+    if (sets) sets->assign(in.size() * kCatWords, 0u);
     if (in.empty()) return out;
-    if (n_cat_) fail(kRefused, "scan: categorical features are searched by the engine's own tree growth");
     std::vector<ScanNode> nodes(in.size());
     for (size_t i = 0; i < in.size(); i++) {
         ScanNode n{};
@@ -1001,9 +1008,12 @@ std::vector<ScanBest> Engine::scan(const std::vector<ScanInput> &in) {
         nodes[i] = n;
     }
     ScanBest *staged = static_cast<ScanBest *>(stage_.alloc(in.size() * sizeof(ScanBest)));
-    scan_host_nodes(nodes, staged);
+    uint32_t *staged_sets =
+        n_cat_ ? static_cast<uint32_t *>(stage_.alloc(in.size() * kCatWords * sizeof(uint32_t))) : nullptr;
+    scan_host_nodes(nodes, staged, staged_sets);
     dev_.sync();
     std::memcpy(out.data(), staged, in.size() * sizeof(ScanBest));
+    if (sets && staged_sets) std::memcpy(sets->data(), staged_sets, in.size() * kCatWords * sizeof(uint32_t));
     stage_.reset();
     return out;
 }

@@ -23,6 +23,14 @@ struct Segment {
     uint32_t offset = 0, len = 0, buf = 0;
 };
 
+// A category code: the saturating `value as u32` of the category's cut
+// (in_category_set, tree/mod.rs:34-58).
+inline uint32_t category_code(float v) {
+    if (!(v >= 0.0f)) return 0;
+    if (v >= 4294967296.0f) return 0xffffffffu;
+    return (uint32_t)v;
+}
+
 // One split of a level: the parent's rows, slot and routing.
 struct LevelSplit {
     Segment seg;
@@ -153,7 +161,10 @@ public:
     // Build node histograms into their (zeroed) slots, then parent -= built.
     void build_nodes(const std::vector<Segment> &segs, const std::vector<uint32_t> &slots);
     void subtract(const std::vector<uint32_t> &parents, const std::vector<uint32_t> &built);
-    std::vector<ScanBest> scan(const std::vector<ScanInput> &nodes);
+    // The split search of nodes given on the host (numeric and categorical
+    // features); sets (may be null) receives kCatWords words per node, a
+    // categorical winner's set of local bins.
+    std::vector<ScanBest> scan(const std::vector<ScanInput> &nodes, std::vector<uint32_t> *sets = nullptr);
     // Partition + (non-terminal) smaller-child histograms, sibling subtraction
     // and the children's split search, with one host synchronisation.
     std::vector<LevelChild> level(const std::vector<LevelSplit> &splits, bool terminal);
@@ -322,7 +333,7 @@ private:
     DBuf<uint32_t> poison_;
     std::vector<int8_t> monotone_host_;
     PartArgs part_args() const;
-    void scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out);
+    void scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out, uint32_t *sets = nullptr);
     void launch_gradients(const hbr_device_loss &loss, uint32_t output);
     GradArgs grad_args(const hbr_device_loss &loss);
     bool check_scale(QScale folded);
@@ -432,7 +443,7 @@ private:
     // per-(node, feature) sets and the root's winning set
     uint32_t n_cat_ = 0;
     std::vector<uint32_t> cat_rank_, cat_feature_;
-    DBuf<uint32_t> d_cat_rank_, d_cat_feature_, d_cat_sets_, d_root_set_;
+    DBuf<uint32_t> d_cat_rank_, d_cat_feature_, d_cat_sets_, d_root_set_, d_scan_sets_;
     DBuf<LeafSeg> d_leaves_;
     DBuf<uint32_t> d_tile_leaf_, d_tile_row0_;
 

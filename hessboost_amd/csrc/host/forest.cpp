@@ -275,7 +275,7 @@ void Forest::build_mirror(const hbr_forest_desc &fd) {
 }
 
 void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float missing, float *out,
-                            int32_t *leaf_out) {
+                            int32_t *leaf_out, const float *init) {
     if (n == 0) return;
     if (n_trees_ && n_cols <= max_feature_) fail(kInvalid, "predict: rows have fewer columns than the forest reads");
     if (n >= (uint64_t)UINT32_MAX) fail(kRefused, "predict: more than 2^32 - 1 rows per call");
@@ -289,6 +289,7 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     a.tree_weight = weight_.get();
     a.tree_output = output_.get();
     a.base_score = base_.get();
+    a.init = init;
     a.x = x;
     a.out = out;
     a.leaf_out = leaf_out;
@@ -306,18 +307,19 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     }
     const uint64_t row_block = n_cols * (uint64_t)kPredPitch * sizeof(float);
     const uint64_t lds_total = 160ull * 1024;
-    // HBROCM_PRED_KERNEL selects a walk (pairs, mirror, resident or
-    // chunked); by default the first of pairs, mirror and resident that the
-    // forest and the rows allow. Each keeps a 64-row block in LDS per one-wave
+    // HBROCM_PRED_KERNEL selects a walk (pairs, mirror, resident, chunked,
+    // staged, or any other value for the generic walk); by default the first
+    // of pairs, mirror, resident, chunked and staged that the forest and the
+    // rows allow. Each keeps a 64-row block in LDS per one-wave
     // workgroup (rows read from HBM once, however large the forest) and
     // reads the trees through the caches.
     const char *kind = std::getenv("HBROCM_PRED_KERNEL");
-    const bool chunked = kind && std::strcmp(kind, "chunked") == 0;
+    auto allowed = [&](const char *walk) { return !kind || std::strcmp(kind, walk) == 0; };
     const bool nan = missing != missing;
     const uint64_t mirror_block = (n_cols + 1) * (uint64_t)kPredPitch * sizeof(float);
     const uint64_t blocks = (n + 63) / 64;
     // complete trees, two levels per record
-    if (n_trees_ && pairs_ok_ && (!kind || std::strcmp(kind, "pairs") == 0) && mirror_block <= lds_total / 4) {
+    if (n_trees_ && pairs_ok_ && allowed("pairs") && mirror_block <= lds_total / 4) {
         a.pairs = pairs_.get();
         a.pair_values = pair_values_.get();
         a.pair_orig = pair_orig_.get();
@@ -328,7 +330,7 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
         return;
     }
     // the mirror arena, one level per step
-    if (n_trees_ && mirror_ok_ && (!kind || std::strcmp(kind, "mirror") == 0) && mirror_block <= lds_total / 4) {
+    if (n_trees_ && mirror_ok_ && allowed("mirror") && mirror_block <= lds_total / 4) {
         a.mirror = mirror_.get();
         a.mirror_root = mirror_root_.get();
         a.mirror_orig = mirror_orig_.get();
@@ -339,7 +341,7 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
         return;
     }
     // compact records, one level per step (any threshold)
-    if (n_trees_ && compact_ok_ && !chunked && row_block <= lds_total / 4) {
+    if (n_trees_ && compact_ok_ && allowed("resident") && row_block <= lds_total / 4) {
         a.compact = compact_.get();
         const uint64_t grid = std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count() * (lds_total / row_block));
         dev_.launch(missing != missing ? "hbr_predict_resident_nan" : "hbr_predict_resident", dim3((uint32_t)grid),
@@ -353,7 +355,8 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     uint32_t waves = 4;
     if (const char *v = std::getenv("HBROCM_PRED_WAVES")) waves = (uint32_t)std::max(1L, std::min(4L, std::strtol(v, nullptr, 10)));
     while (waves > 1 && waves * row_block > lds_total / 2) waves--;
-    if (n_trees_ && compact_ok_ && waves * row_block + tree_tables + 8ull * largest_tree_ <= lds_total) {
+    if (n_trees_ && compact_ok_ && allowed("chunked") &&
+        waves * row_block + tree_tables + 8ull * largest_tree_ <= lds_total) {
         const uint32_t cap = (uint32_t)((lds_total - waves * row_block - tree_tables) / 8);
         plan_chunks(cap);
         a.compact = compact_.get();
@@ -370,7 +373,7 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     }
     // rows staged in LDS when 64 of them fit in a quarter of a CU's LDS
     const uint64_t lds = n_cols * (uint64_t)kPredPitch * sizeof(float);
-    if (n_trees_ && lds <= 40ull * 1024) {
+    if (n_trees_ && allowed("staged") && lds <= 40ull * 1024) {
         const uint64_t blocks = (n + 63) / 64;
         const uint64_t grid = std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count() * 64);
         dev_.launch("hbr_predict_staged", dim3((uint32_t)grid), dim3(64), a, (uint32_t)lds);

@@ -19,8 +19,10 @@ public:
     Device &dev() { return dev_; }
     uint32_t n_outputs() const { return n_outputs_; }
     uint64_t n_trees() const { return n_trees_; }
-    // x, out, leaf_out: device pointers.
-    void predict_device(const float *x, uint64_t n, uint64_t n_cols, float missing, float *out, int32_t *leaf_out);
+    // x, out, leaf_out, init: device pointers; init (n x n_outputs starting
+    // margins) may be null: the base scores.
+    void predict_device(const float *x, uint64_t n, uint64_t n_cols, float missing, float *out, int32_t *leaf_out,
+                        const float *init = nullptr);
 
 private:
     Device &dev_;

@@ -68,14 +68,6 @@ TreeBuilder::Decision TreeBuilder::decide(const Open &o) const {
     return d;
 }
 
-// A category code: the saturating `value as u32` of the category's cut
-// (in_category_set, tree/mod.rs:34-58).
-static uint32_t category_code(float v) {
-    if (!(v >= 0.0f)) return 0;
-    if (v >= 4294967296.0f) return 0xffffffffu;
-    return (uint32_t)v;
-}
-
 LevelSplit TreeBuilder::expand(Tree &t, const Open &o, const Decision &d, double cb[4]) {
     const int dir = d.feature < p_.monotone.size() ? p_.monotone[d.feature] : 0;
     if (d.categorical) {

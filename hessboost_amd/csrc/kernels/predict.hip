@@ -166,6 +166,12 @@ __device__ __forceinline__ void mirror_walk(const MirrorNode *nodes, const float
     }
 }
 
+// A row's starting margin of output o: the caller's (BoostedModel's
+// initial margins, a DMatrix's base_margin) or the base score.
+__device__ __forceinline__ float start_margin(const PredictArgs &a, uint32_t r, uint32_t o) {
+    return a.init ? a.init[(size_t)r * a.n_outputs + o] : a.base_score[o];
+}
+
 }  // namespace hbr
 
 extern "C" __global__ __launch_bounds__(256) void hbr_predict(PredictArgs a) {
@@ -174,7 +180,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_predict(PredictArgs a) {
     const float *row = a.x + (size_t)r * a.n_cols;
     float *out = a.out + (size_t)r * a.n_outputs;
     if (a.n_outputs == 1) {
-        float acc = a.base_score[0];
+        float acc = start_margin(a, r, 0);
         for (uint32_t t = 0; t < a.n_trees; t++) {
             const uint32_t leaf = walk(a, row, a.tree_root[t]);
             if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.node_orig[leaf];
@@ -184,7 +190,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_predict(PredictArgs a) {
         out[0] = acc;
         return;
     }
-    for (uint32_t c = 0; c < a.n_outputs; c++) out[c] = a.base_score[c];
+    for (uint32_t c = 0; c < a.n_outputs; c++) out[c] = start_margin(a, r, c);
     for (uint32_t t = 0; t < a.n_trees; t++) {
         const uint32_t leaf = walk(a, row, a.tree_root[t]);
         if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.node_orig[leaf];
@@ -208,9 +214,9 @@ extern "C" __global__ __launch_bounds__(64) void hbr_predict_staged(PredictArgs 
             const uint32_t r = r0 + lane;
             const float *xr = s_x + lane;
             float *out = a.out + (size_t)r * a.n_outputs;
-            float acc = a.base_score[0];
+            float acc = start_margin(a, r, 0);
             if (a.n_outputs != 1)
-                for (uint32_t c = 0; c < a.n_outputs; c++) out[c] = a.base_score[c];
+                for (uint32_t c = 0; c < a.n_outputs; c++) out[c] = start_margin(a, r, c);
             for (uint32_t t0 = 0; t0 < a.n_trees; t0 += kPredChains) {
                 uint32_t nid[kPredChains];
                 PredNode nd[kPredChains];
@@ -301,7 +307,7 @@ __device__ __forceinline__ void predict_chunked(const PredictArgs &a) {
             const float *src = a.x + (size_t)r0 * a.n_cols;
             const uint32_t r = r0 + min(lane, rows - 1);
             float *out = a.out + (size_t)r * a.n_outputs;
-            float acc = c == 0 ? a.base_score[0] : out[0];
+            float acc = c == 0 ? start_margin(a, r, 0) : out[0];
             // the wave's previous walk has read its block: lanes finish in lockstep
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -310,7 +316,7 @@ __device__ __forceinline__ void predict_chunked(const PredictArgs &a) {
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             if (c == 0 && lane < rows && a.n_outputs != 1)
-                for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = a.base_score[o];
+                for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = start_margin(a, r, o);
             if (lane >= rows) continue;
             for (uint32_t t0 = t_lo; t0 < t_hi; t0 += kPredChains) {
                 uint32_t nid[kPredChains];
@@ -390,8 +396,8 @@ __device__ __forceinline__ void predict_resident(const PredictArgs &a) {
         const uint32_t r = r0 + lane;
         float *out = a.out + (size_t)r * a.n_outputs;
         if (a.n_outputs != 1)
-            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = a.base_score[o];
-        float acc = a.base_score[0];
+            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = start_margin(a, r, o);
+        float acc = start_margin(a, r, 0);
         for (uint32_t t0 = 0; t0 < a.n_trees; t0 += CH) {
             uint32_t g[CH];
             CompactNode nd[CH];
@@ -475,8 +481,8 @@ __device__ __forceinline__ void predict_mirror(const PredictArgs &a) {
         const uint32_t r = r0 + lane;
         float *out = a.out + (size_t)r * a.n_outputs;
         if (a.n_outputs != 1)
-            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = a.base_score[o];
-        float acc = a.base_score[0];
+            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = start_margin(a, r, o);
+        float acc = start_margin(a, r, 0);
         for (uint32_t t0 = 0; t0 < a.n_trees; t0 += CH) {
             uint32_t g[CH];
             MirrorNode nd[CH];
@@ -546,8 +552,8 @@ __device__ __forceinline__ void predict_pairs(const PredictArgs &a) {
         const uint32_t r = r0 + lane;
         float *out = a.out + (size_t)r * a.n_outputs;
         if (a.n_outputs != 1)
-            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = a.base_score[o];
-        float acc = a.base_score[0];
+            for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = start_margin(a, r, o);
+        float acc = start_margin(a, r, 0);
         for (uint32_t t0 = 0; t0 < a.n_trees; t0 += CH) {
             uint32_t pos[CH];
 #pragma unroll

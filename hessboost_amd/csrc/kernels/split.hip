@@ -231,7 +231,7 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
             o.loss = -__builtin_inff();
             o.feature = f;
             o.index = 0xffffffffu;
-            o.flags = any_nan ? 2u : 0u;
+            o.flags = any_nan ? kScanNumericNaN : 0u;
             o.left = QBin{0, 0};
             o.right = QBin{0, 0};
             *out = o;
@@ -241,7 +241,7 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
         o.loss = bl;
         o.feature = f;
         o.index = bi;
-        o.flags = best.backward | (any_nan ? 2u : 0u);
+        o.flags = best.backward | (any_nan ? kScanNumericNaN : 0u);
         o.left = QBin{best.lg, best.lh};
         o.right = QBin{best.rg, best.rh};
         *out = o;
@@ -265,7 +265,7 @@ __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, con
     uint32_t nan_flag = 0;
     for (uint32_t f = lane; f < a.n_features; f += kWave) {
         const ScanBest c = per_node[f];
-        nan_flag |= c.flags & 2u;
+        nan_flag |= c.flags & kScanReplay;
         if (c.index == 0xffffffffu) continue;
         // features ascend within a lane: only a strictly larger loss replaces
         if (c.loss > 0.0f && (bf == 0xffffffffu || c.loss > bl)) {
@@ -380,6 +380,7 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_categorical(ScanArgs a
     bool has = false;
     float best_loss = 0.0f;
     uint32_t xgb_dl = 0, set_size = 0, chosen = 0;
+    uint32_t replay = 0;  // kScanCatOrder / kScanCatNaN
     int64_t lg = 0, lh = 0, rg = 0, rh = 0;
     bool onehot = nb < 4;
     if (onehot) {
@@ -394,9 +395,10 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_categorical(ScanArgs a
                 for (uint32_t with_missing = 0; with_missing < 2; with_missing++) {
                     const int64_t cg = s_g[i] + (with_missing ? mg : 0), ch = s_h[i] + (with_missing ? mh : 0);
                     float loss;
-                    if (score(dequant(tg - cg, eg), dequant(th - ch, eh), dequant(cg, eg), dequant(ch, eh), a.reg,
-                              nd.lower, nd.upper, dir, root_gain, &loss) &&
-                        beats(loss, has, best_loss)) {
+                    const bool ok = score(dequant(tg - cg, eg), dequant(th - ch, eh), dequant(cg, eg),
+                                          dequant(ch, eh), a.reg, nd.lower, nd.upper, dir, root_gain, &loss);
+                    if (ok && loss != loss) replay |= kScanCatNaN;
+                    if (ok && beats(loss, has, best_loss)) {
                         has = true;
                         best_loss = loss;
                         xgb_dl = with_missing ? 0u : 1u;
@@ -413,7 +415,8 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_categorical(ScanArgs a
         for (uint32_t b = lane; b < nb; b += kWave) {
             const double g = dequant(s_g[b], eg), hh = dequant(s_h[b], eh);
             float k = hh < a.reg.min_child_weight ? 0.0f : (float)calc_weight(g, hh, a.reg);
-            s_key[b] = k != k ? 0.0f : k;  // a NaN weight cannot arise from finite pairs; keep the order total
+            if (!__builtin_isfinite(k)) replay |= kScanCatOrder;  // the node is replayed on the host
+            s_key[b] = k != k ? 0.0f : k;  // keeps this sort total meanwhile
         }
         __syncthreads();
         // stable ascending order: position = smaller keys + equal keys before
@@ -451,6 +454,7 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_categorical(ScanArgs a
                 else
                     ok = score(dequant(ag, eg), dequant(ah, eh), dequant(tg - ag, eg), dequant(th - ah, eh), a.reg,
                                nd.lower, nd.upper, dir, root_gain, &loss);
+                if (ok && loss != loss) replay |= kScanCatNaN;
                 ok = ok && beats(loss, false, 0.0f);
             }
             // the first step of the largest loss
@@ -493,6 +497,8 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_categorical(ScanArgs a
             }
         }
     }
+    replay = (__ballot((replay & kScanCatOrder) != 0) ? kScanCatOrder : 0u) |
+             (__ballot((replay & kScanCatNaN) != 0) ? kScanCatNaN : 0u);
     if (onehot) {  // lane 0 holds the one-hot winner
         has = __shfl((int)has, 0, kWave) != 0;
         best_loss = __shfl(best_loss, 0, kWave);
@@ -522,13 +528,13 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_categorical(ScanArgs a
         if (has) {
             o.loss = best_loss;
             o.index = 0;
-            o.flags = kScanCategorical | (xgb_dl ? 0u : 1u);  // recorded: the set's child on the left
+            o.flags = kScanCategorical | (xgb_dl ? 0u : 1u) | replay;  // recorded: the set's child on the left
             o.left = QBin{rg, rh};
             o.right = QBin{lg, lh};
         } else {
             o.loss = -__builtin_inff();
             o.index = 0xffffffffu;
-            o.flags = 0;
+            o.flags = replay;
             o.left = QBin{0, 0};
             o.right = QBin{0, 0};
         }

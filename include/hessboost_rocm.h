@@ -223,15 +223,18 @@ int hbr_begin_tree(hbr_engine *e, uint64_t n_rows, hbr_segment *root);
  * fixed-point sums). */
 int hbr_root_total(hbr_engine *e, const hbr_segment *seg, double out[2]);
 
-/* One split to partition (RowSplit, src/tree/hist/mod.rs:180-190): present
- * feature-local bins below `below` go left, missing values follow
- * default_left. */
+/* One split to partition (RowRule, RowSplit: src/tree/hist/mod.rs:166-192): a
+ * present value goes left by its feature-local bin, as RowRule::Below
+ * (table NULL: bins below `below` go left) or RowRule::Table (table[bin] !=
+ * 0 goes left; n_table = the feature's bin count, at most 1,024, and the
+ * feature categorical in the index); missing values follow default_left. */
 typedef struct hbr_row_split {
     hbr_segment seg;
     uint32_t feature;
     uint32_t below;
     uint32_t default_left;
-    uint32_t pad;
+    uint32_t n_table;
+    const uint8_t *table;
 } hbr_row_split;
 
 typedef struct hbr_partitioned {
@@ -345,27 +348,45 @@ typedef struct hbr_scan_request {
     const int8_t *directions;
 } hbr_scan_request;
 
-/* NodeScan (src/tree/hist/mod.rs:327-350). */
+/* NodeScan (src/tree/hist/mod.rs:327-350), kinds in its order. */
 #define HBR_SCAN_EMPTY 0
+#define HBR_SCAN_REPLAY 1
 #define HBR_SCAN_NUMERIC 2
+#define HBR_SCAN_CATEGORICAL 3
+/* ScanFallback (src/tree/hist/mod.rs:313-324): why a node is replayed. */
+#define HBR_FALLBACK_NUMERIC_SCORE 1
+#define HBR_FALLBACK_CATEGORICAL_ORDER 2
+#define HBR_FALLBACK_CATEGORICAL_SCORE 3
 typedef struct hbr_node_scan {
     uint32_t kind;
     uint32_t feature;
     float loss_chg;
-    uint32_t backward;      /* the winner came from the missing-left pass */
-    uint32_t offset;        /* forward: last local bin going left; backward: first local bin going right */
+    uint32_t backward;      /* numeric: the winner came from the missing-left pass */
+    uint32_t offset;        /* numeric forward: last local bin going left; backward: first local bin going right */
     uint32_t pad;
-    double acc_g, acc_h;    /* the pass's accumulated statistics (left forward, right backward) */
+    double acc_g, acc_h;    /* numeric: the pass's accumulated statistics (left forward, right backward) */
     double left_g, left_h, right_g, right_h;
     int64_t fixed_left_g, fixed_left_h, fixed_right_g, fixed_right_h; /* exact sums */
+    /* categorical: missing values go left; the winner's categories
+     * (ascending codes) are [cat_begin, cat_end) of the scan's pool
+     * (hbr_scan_categories). left is the set's child: the orientation the
+     * tree records (XGBoost's children swapped). */
+    uint32_t default_left;
+    uint32_t fallback;      /* HBR_SCAN_REPLAY: an HBR_FALLBACK_* reason */
+    uint32_t cat_begin, cat_end;
 } hbr_node_scan;
 
 /* RowEngine::root_total with the exact fixed-point sums as well. */
 int hbr_root_total_fixed(hbr_engine *e, const hbr_segment *seg, double out[2], int64_t fixed[2]);
 
-/* RowEngine::scan_resident. */
+/* RowEngine::scan_resident: numeric and categorical features (the
+ * reference's sweep, src/tree/builder/categorical.rs:48-170: one-hot below 4
+ * categories, else the weight-sorted partition scans). */
 int hbr_scan_resident(hbr_engine *e, const hbr_reg_params *reg, const hbr_scan_request *requests,
                       uint64_t n, hbr_node_scan *out);
+/* The last hbr_scan_resident call's category pool: n entries (the largest
+ * cat_end of its categorical winners, 0 when it had none). */
+int hbr_scan_categories(hbr_engine *e, uint32_t *out, uint64_t n);
 
 /* RowEngine::read_hist: 2 * total_bins f64. */
 int hbr_read_hist(hbr_engine *e, uint32_t slot, double *out);
@@ -498,6 +519,12 @@ void hbr_forest_free(hbr_forest *f);
  * `missing` as for the matrix): out[n_rows * n_outputs]. */
 int hbr_predict_margin(hbr_forest *f, const float *x, uint64_t n_rows, uint64_t n_cols,
                        float missing, float *out);
+/* The same from each row's starting margins (n_rows * n_outputs, row-major;
+ * NULL: the base scores): the reference's initial margins, a DMatrix's
+ * base_margin (src/backend/shared.rs:218-239, plan_margins), to which the
+ * trees' leaf values are added in tree order. */
+int hbr_predict_margin_from(hbr_forest *f, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
+                            const float *init_margins, float *out);
 /* The same over device memory (x, out and optional leaf ids [n_rows * n_trees]
  * all device pointers): inputs already resident, nothing copied. The
  * outputs are complete when the call returns. */
@@ -508,6 +535,22 @@ int hbr_predict_leaf(hbr_forest *f, const float *x, uint64_t n_rows, uint64_t n_
                      int32_t *out);
 int hbr_forest_set_profiling(hbr_forest *f, int on, const char *kernel_prefix);
 int hbr_forest_kernel_stats(hbr_forest *f, char *buf, size_t len);
+
+/* The objective's prediction transform, on the host, in place: the
+ * reference's Transform::apply (src/model/transform.rs:74-104), which runs
+ * on the CPU after GpuModel::predict_margin (src/backend/cuda/predict.rs:
+ * 466-474). expf is the host C library's, as the reference's f32::exp.
+ *   HBR_TRANSFORM_SIGMOID      XGBoost's common::Sigmoid of each value,
+ *                              1 / (expf(min(-x, 88.7)) + 1) (simd/mod.rs:422-427);
+ *   HBR_TRANSFORM_SOFTMAX      common::Softmax of each row of n_outputs:
+ *                              shift by the row's maximum, expf, sum in f64,
+ *                              divide by the sum rounded to f32 (simd/mod.rs:557-573);
+ *   HBR_TRANSFORM_CLASS_INDEX  multi:softmax: row r's first largest margin's
+ *                              index, as f32, into values[r] (simd/mod.rs:750-758). */
+#define HBR_TRANSFORM_SIGMOID 1
+#define HBR_TRANSFORM_SOFTMAX 2
+#define HBR_TRANSFORM_CLASS_INDEX 3
+int hbr_pred_transform(int kind, float *values, uint64_t n_rows, uint32_t n_outputs);
 
 /* Device memory for callers that keep inputs resident (bytes on device
  * `ordinal`). */

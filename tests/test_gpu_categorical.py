@@ -140,3 +140,121 @@ def test_categorical_models_save_load_and_refuse_eval_sets(tmp_path):
         hb.train({"max_depth": 4}, hb.DMatrix(x, label=y, feature_types=types), 1,
                  evals=[(hb.DMatrix(x, feature_types=types), "train")])
     assert refused.value.status == A.REFUSED
+
+
+def exact_categorical_node(seed, n, n_cats, outlier_code=None):
+    """An engine and the oracle over numeric + categorical features, with
+    dyadic gradients (every sum exact) driven by the first categorical
+    feature's codes, staged and built at the root. outlier_code: that
+    category's rows get g = 2^100 and h = 2^-30, the others g scaled by 2^96,
+    so its weight G / H = 2^130 overflows f32 while every sum stays exact."""
+    x, _, types = categorical_data(seed, n, n_cats, missing=0.1)
+    rng = np.random.default_rng(seed)
+    effect = np.round(rng.standard_normal(n_cats[0]) * 16) / 8
+    codes = np.nan_to_num(x[:, 2], nan=-1).astype(np.int64)
+    g = np.where(codes >= 0, effect[np.maximum(codes, 0)], 0.0) + rng.integers(-2, 3, n) / 16
+    h = np.ones(n)
+    if outlier_code is not None:
+        g = g * 2.0 ** 96
+        g[codes == outlier_code] = 2.0 ** 100
+        h[codes == outlier_code] = 2.0 ** -30
+    gp = np.stack([g, h], 1).astype(np.float32)
+    eng = hb.DMatrix(x, feature_types=types).engine()
+    ref = O.Dataset(x, feature_types=types)
+    eng.prepare(gp)
+    root = eng.begin_tree()
+    tot, fixed = eng.root_total(root, fixed=True)
+    eng.reserve_hists(8)
+    eng.build_resident([(root, 0)])
+    hist = eng.read_hist(0)
+    want_hist = ref.build_hist(np.arange(n, dtype=np.uint32), gp)
+    assert np.array_equal(hist, want_hist)
+    return eng, ref, gp, root, tot, fixed, want_hist
+
+
+def oracle_partition_categorical(ref, rows, feature, cat_left, default_left):
+    rows = np.ascontiguousarray(rows, np.uint32)
+    left, right = np.empty(len(rows), np.uint32), np.empty(len(rows), np.uint32)
+    words = np.ascontiguousarray(cat_left, np.uint32)
+    nl = O.lib().or_partition_categorical(ref.index, rows.ctypes.data, len(rows), feature, words.ctypes.data,
+                                          int(default_left), left.ctypes.data, right.ctypes.data)
+    return left[:nl], right[:len(rows) - nl]
+
+
+@pytest.mark.parametrize("n_cats", [[12, 3], [3, 40]], ids=["partition-sweep", "one-hot"])
+def test_engine_categorical_scan_and_table_partition_match_oracle(n_cats):
+    """The resident search's NodeScan::Categorical (hbr_scan_resident: the
+    winning feature, loss, children in the tree's orientation, missing-value
+    direction and ascending category codes) against the oracle's sequential
+    search (builder/categorical.rs:48-170), then RowRule::Table routing
+    (hbr_partition with a table) against the oracle's categorical partition,
+    over two levels with a numeric split beside a table."""
+    n = 30_000
+    eng, ref, gp, root, tot, fixed, want_hist = exact_categorical_node(len(n_cats) + n_cats[0], n, n_cats)
+    p = O.params()
+    reg = (1.0, 0.0, 0.0, 1.0)
+    rg = O.lib().or_node_gain(tot[0], tot[1], -np.inf, np.inf, p)
+    scan, = eng.scan_resident(reg, [dict(slot=0, total=tuple(tot), fixed=tuple(fixed), root_gain=rg)])
+    want = ref.evaluate(want_hist, tot, p)
+    assert want.categorical and want.feature == 2
+    assert scan.kind == A.SCAN_CATEGORICAL
+    assert scan.feature == want.feature and np.float32(scan.loss_chg) == np.float32(want.loss_chg)
+    assert bool(scan.default_left) == bool(want.default_left)
+    assert (scan.left_g, scan.left_h, scan.right_g, scan.right_h) == \
+        (want.left_g, want.left_h, want.right_g, want.right_h)
+    fo, cuts = ref.feature_offset, ref.cut_values
+    fs, nb = int(fo[2]), int(fo[3] - fo[2])
+    in_set = [bool(want.cat_left[b // 32] >> (b % 32) & 1) for b in range(nb)]
+    codes = sorted(int(cuts[fs + b]) for b in range(nb) if in_set[b])
+    assert eng.scan_categories[scan.cat_begin:scan.cat_end].tolist() == codes
+
+    all_rows = np.arange(n, dtype=np.uint32)
+    (left, right), = eng.partition([(root, 2, in_set, scan.default_left)])
+    wl, wr = oracle_partition_categorical(ref, all_rows, 2, want.cat_left, want.default_left)
+    assert np.array_equal(eng.rows(left), wl) and np.array_equal(eng.rows(right), wr)
+    # the next level: a numeric split (RowRule::Below) beside a table on the other feature
+    nb3 = int(fo[4] - fo[3])
+    table3 = [b % 2 == 0 for b in range(nb3)]
+    words3 = np.zeros(32, np.uint32)
+    for b in range(nb3):
+        if table3[b]:
+            words3[b // 32] |= np.uint32(1 << (b % 32))
+    (l2, r2), (l3, r3) = eng.partition([(left, 0, 7, 1), (right, 3, table3, 0)])
+    a, b = ref.partition(wl, 0, int(fo[0]) + 6, 1)
+    c, d = oracle_partition_categorical(ref, wr, 3, words3, 0)
+    assert np.array_equal(eng.rows(l2), a) and np.array_equal(eng.rows(r2), b)
+    assert np.array_equal(eng.rows(l3), c) and np.array_equal(eng.rows(r3), d)
+
+
+def test_engine_scan_asks_for_replay_on_non_finite_category_weights():
+    """A category whose weight overflows f32 (lambda = 0, min_child_weight =
+    0) makes the sort's order not total: the node comes back as
+    NodeScan::Replay (src/tree/hist/mod.rs:313-331) rather than a winner, as
+    the reference's device search answers it (the same node's numeric scores
+    overflow too, which asks for the replay as well)."""
+    eng, ref, gp, root, tot, fixed, _ = exact_categorical_node(5, 20_000, [9, 2], outlier_code=4)
+    reg = (0.0, 0.0, 0.0, 0.0)
+    p = O.params(reg_lambda=0.0, min_child_weight=0.0)
+    rg = O.lib().or_node_gain(tot[0], tot[1], -np.inf, np.inf, p)
+    scan, = eng.scan_resident(reg, [dict(slot=0, total=tuple(tot), fixed=tuple(fixed), root_gain=rg)])
+    assert scan.kind == A.SCAN_REPLAY
+    assert scan.fallback in (A.FALLBACK_CATEGORICAL_ORDER, A.FALLBACK_NUMERIC_SCORE)
+    # ordinary gradients on the same features: a winner
+    eng, ref, gp, root, tot, fixed, _ = exact_categorical_node(5, 20_000, [9, 2])
+    p = O.params()
+    rg = O.lib().or_node_gain(tot[0], tot[1], -np.inf, np.inf, p)
+    scan, = eng.scan_resident((1.0, 0.0, 0.0, 1.0), [dict(slot=0, total=tuple(tot), fixed=tuple(fixed),
+                                                          root_gain=rg)])
+    assert scan.kind == A.SCAN_CATEGORICAL
+
+
+def test_table_partition_refuses_numeric_features_and_wrong_lengths():
+    eng, ref, gp, root, *_ = exact_categorical_node(6, 5_000, [5, 3])
+    nb0 = int(ref.feature_offset[1] - ref.feature_offset[0])
+    with pytest.raises(A.HbrError) as e:
+        eng.partition([(root, 0, [True] * nb0, 0)])
+    assert e.value.status == A.REFUSED
+    root = eng.begin_tree()
+    with pytest.raises(A.HbrError) as e:
+        eng.partition([(root, 2, [True, False], 0)])
+    assert e.value.status == A.INVALID

@@ -184,7 +184,7 @@ def test_resident_and_chunked_walks_agree_with_the_oracle():
     multi["n_outputs"] = 3
     multi["base_score"] = np.array([0.1, -0.2, 0.3], np.float32)
     want3 = O.predict_margin(multi, x)
-    for kind in ("pairs", "mirror", "resident", "chunked"):
+    for kind in ("pairs", "mirror", "resident", "chunked", "staged", "generic"):
         os.environ["HBROCM_PRED_KERNEL"] = kind
         try:
             f = hb.Forest(arrs, 1)
@@ -195,6 +195,45 @@ def test_resident_and_chunked_walks_agree_with_the_oracle():
             assert np.array_equal(f3.predict_margin(x).view(np.uint32), want3.view(np.uint32)), kind
         finally:
             os.environ.pop("HBROCM_PRED_KERNEL", None)
+
+
+def test_rows_start_from_their_own_margins_in_every_walk():
+    """hbr_predict_margin_from: each row starts from its own margins (the
+    reference's initial margins, a DMatrix's base_margin: plan_margins,
+    backend/shared.rs:218-239) and adds the trees' weighted leaf values in
+    tree order, as the f32 chain formed here from the oracle's leaf ids;
+    starting margins equal to the base scores give the base-score call's bits."""
+    import os
+    trees = synthetic.forest(n_trees=41, depth=6, n_features=19, seed=21)
+    x = synthetic.predict_rows(n=2_777, f=19, seed=22)
+    rng = np.random.default_rng(23)
+    for k in (1, 3):
+        arrs = dict(O.forest_arrays(trees))
+        arrs["tree_output"] = (np.arange(len(trees)) % k).astype(np.uint32)
+        arrs["n_outputs"] = k
+        arrs["base_score"] = np.linspace(-0.25, 0.5, k).astype(np.float32)
+        arrs["tree_weight"] = rng.choice([1.0, 0.5, 0.3], len(trees)).astype(np.float32)
+        _, leaf = O.predict_margin(arrs, x, with_leaf=True)
+        init = (rng.standard_normal((len(x), k)) * 3).astype(np.float32)
+        want = init.copy()
+        lv = np.asarray(arrs["leaf_value"], np.float32)
+        off = np.asarray(arrs["tree_offset"], np.int64)
+        for t in range(len(trees)):
+            o = arrs["tree_output"][t]
+            contrib = (arrs["tree_weight"][t] * lv[off[t] + leaf[:, t]]).astype(np.float32)
+            want[:, o] = (want[:, o] + contrib).astype(np.float32)
+        base = np.broadcast_to(arrs["base_score"], (len(x), k))
+        for kind in ("pairs", "mirror", "resident", "chunked", "staged", "generic"):
+            os.environ["HBROCM_PRED_KERNEL"] = kind
+            try:
+                f = hb.Forest(arrs, k)
+                got = f.predict_margin(x, init_margins=init)
+                assert np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32)), (kind, k)
+                plain = f.predict_margin(x)
+                assert np.array_equal(f.predict_margin(x, init_margins=base).view(np.uint32),
+                                      plain.view(np.uint32)), (kind, k)
+            finally:
+                os.environ.pop("HBROCM_PRED_KERNEL", None)
 
 
 def test_device_resident_prediction():
@@ -221,6 +260,41 @@ def test_trained_model_predictions_match_training_margins():
     t.boost(5)
     model = t.booster(8)
     assert np.array_equal(model.predict(x, output_margin=True).view(np.uint32), t.margins().view(np.uint32))
+
+
+@pytest.mark.parametrize("objective", ["binary:logistic", "multi:softprob", "multi:softmax"])
+def test_booster_predict_transforms_margins_with_the_hosts_expf(objective):
+    """Booster.predict: the margins from the GPU, then the objective's
+    transform on the host (Transform::apply, model/transform.rs:74-104):
+    XGBoost's sigmoid bit for bit as the oracle forms it with the C library's
+    expf, softmax rows summed in f64, multi:softmax's first largest class."""
+    import ctypes as C
+    import ctypes.util
+    libm = C.CDLL(ctypes.util.find_library("m"))
+    libm.expf.restype, libm.expf.argtypes = C.c_float, [C.c_float]
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((3_000, 6)).astype(np.float32)
+    if objective == "binary:logistic":
+        y = (x[:, 0] + 0.5 * x[:, 1] > 0).astype(np.float32)
+        params = {"objective": objective, "max_depth": 4}
+    else:
+        y = np.digitize(x[:, 0] + 0.3 * x[:, 2], [-0.5, 0.5]).astype(np.float32)
+        params = {"objective": objective, "num_class": 3, "max_depth": 3}
+    model = hb.train(params, hb.DMatrix(x, label=y), 4)
+    m = model.predict(x, output_margin=True)
+    p = model.predict(x)
+    if objective == "binary:logistic":
+        want = np.array([O.lib().or_sigmoid(float(v)) for v in m], np.float32)
+        assert np.array_equal(p.view(np.uint32), want.view(np.uint32))
+    elif objective == "multi:softprob":
+        want = np.empty_like(m)
+        for r, row in enumerate(m):
+            e = [np.float32(libm.expf(float(np.float32(v - row.max())))) for v in row]
+            s = np.float32(sum(float(v) for v in e))
+            want[r] = [np.float32(v / s) for v in e]
+        assert p.shape == m.shape and np.array_equal(p.view(np.uint32), want.view(np.uint32))
+    else:
+        assert p.shape == (len(x),) and np.array_equal(p, np.argmax(m, 1).astype(np.float32))
 
 
 def test_malformed_forest_is_refused():
@@ -264,7 +338,7 @@ def test_random_forests_match_oracle(seed):
     if missing == missing:
         x[rng.random((n, f)) < 0.03] = np.nan
     want, want_leaf = O.predict_margin(arrs, x, missing=missing, with_leaf=True)
-    for kind in ("pairs", "mirror", "resident", "chunked"):
+    for kind in ("pairs", "mirror", "resident", "chunked", "staged", "generic"):
         os.environ["HBROCM_PRED_KERNEL"] = kind
         try:
             fo = hb.Forest(arrs, k)
