@@ -326,6 +326,8 @@ extern "C" {
     pub fn hbr_forest_free(f: *mut hbr_forest);
     pub fn hbr_predict_margin(f: *mut hbr_forest, x: *const f32, n_rows: u64, n_cols: u64, missing: f32,
                               out: *mut f32) -> c_int;
+    pub fn hbr_predict_margin_from(f: *mut hbr_forest, x: *const f32, n_rows: u64, n_cols: u64, missing: f32,
+                                   init_margins: *const f32, out: *mut f32) -> c_int;
     pub fn hbr_predict_margin_device(f: *mut hbr_forest, x: *const f32, n_rows: u64, n_cols: u64,
                                      missing: f32, out: *mut f32, leaf_out: *mut i32) -> c_int;
     pub fn hbr_predict_leaf(f: *mut hbr_forest, x: *const f32, n_rows: u64, n_cols: u64, missing: f32,
