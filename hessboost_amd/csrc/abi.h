@@ -597,15 +597,16 @@ struct WalkArgs {
     uint32_t m_stride;           // outputs per row
     uint32_t output;
     uint32_t n_nodes;
-    uint32_t pad;
+    uint32_t guard_n;            // QScale records the guard checks (0 counts as 1)
     // A device-grown tree is read from its records (n_nodes from counts)
     // instead of meta/left/value.
     const GrowTreeNode *tree;
     const GrowCounts *counts;
-    // Non-null: the walk and the gradients happen only when the gradients
+    // Non-null: the walk (and the gradients) happen only when the gradients
     // the tree was grown from were final (no rows left to the host, none
-    // non-finite) and no earlier guarded walk was skipped; a skip sets
-    // *poison, which stays set until the host clears it.
+    // non-finite in any of the guard_n scales: a softmax round's classes)
+    // and no earlier guarded walk was skipped; a skip sets *poison, which
+    // stays set until the host clears it.
     const QScale *guard;
     uint32_t *poison;
 };

@@ -1466,7 +1466,8 @@ bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vecto
     return false;
 }
 
-void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree) {
+void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree, uint32_t guard_first,
+                              uint32_t guard_n) {
     if (!dense_u8_) fail(kRefused, "walk: the index has no row-major u8 bins");
     if (output >= outputs_) fail(kInvalid, "walk: no such output");
     // the staged walk: 32-byte rows and trees whose nodes fit its LDS table
@@ -1484,7 +1485,19 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     a.output = output;
     const uint32_t blocks =
         std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)), (uint32_t)dev_.cu_count() * walk_blocks_per_cu);
+    if (!poison_.size() && (next_loss || guard_n)) {
+        poison_.resize(1);
+        guard_scale_.resize(1);
+        HBR_HIP(hipMemsetAsync(poison_.get(), 0, sizeof(uint32_t), s));
+    }
     if (!next_loss) {
+        if (guard_n) {
+            if (!softmax_staged() || guard_first + guard_n > class_outputs_)
+                fail(kInvalid, "walk: no softmax class scales to guard by");
+            a.guard = class_scales_.get() + guard_first;
+            a.guard_n = guard_n;
+            a.poison = poison_.get();
+        }
         dev_.launch(staged ? "hbr_walk_leaves32" : "hbr_walk_leaves", dim3(blocks), dim3(256), a);
         return;
     }
@@ -1493,11 +1506,6 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     grains_known_ = false;
     class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
-    if (!poison_.size()) {
-        poison_.resize(1);
-        guard_scale_.resize(1);
-        HBR_HIP(hipMemsetAsync(poison_.get(), 0, sizeof(uint32_t), s));
-    }
     // the tree's scale aside (the walk's guard), the live one cleared for the fold
     RotateArgs r{scale_dev(), guard_scale_.get()};
     dev_.launch("hbr_scale_rotate", dim3(1), dim3(64), r);

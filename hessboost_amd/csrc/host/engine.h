@@ -214,13 +214,16 @@ public:
     // routed on the device from its records (no readback); with next_loss
     // also the next round's gradients, guarded: skipped (and every later
     // guarded walk with it, until drain) when the tree's own gradients were
-    // not finite.
+    // not finite. Without next_loss, guard_n > 0 guards the walk the same
+    // way by the softmax class scales [guard_first, guard_first + guard_n)
+    // (the tree's class, or every class of a batched round).
     bool can_walk_device_tree(uint64_t max_depth) const {
         return can_grow_device(max_depth) && stride_ == 32 && max_depth <= 9 && outputs_ == 1 && labels_loaded_;
     }
     // The walk alone (no gradients): any dense u8 index, any output.
     bool can_route_device_tree(uint64_t max_depth) const { return can_grow_device(max_depth); }
-    void walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree = 0);
+    void walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree = 0,
+                          uint32_t guard_first = 0, uint32_t guard_n = 0);
 
     // ---- evaluation sets ----------------------------------------------------------
     // A dense f32 matrix (row-major, the index's features, `missing` marks

@@ -584,7 +584,9 @@ void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
 // earlier tree has been walked into), then the round's trees, class by
 // class, each grown from its class's pairs and walked into its class's
 // margins on the device; up to three trees in flight before the host reads
-// the oldest back.
+// the oldest back. A tree whose class's gradients are not finite had its
+// walks skipped on the device, and so had every tree queued after it: the
+// margins and eval sets hold the trees before it, and training stops there.
 void Trainer::boost_softmax_pipelined(uint64_t rounds) {
     TreeBuilder b(e_, p_.grow);
     std::deque<Engine::TreeTicket> inflight;
@@ -596,8 +598,10 @@ void Trainer::boost_softmax_pipelined(uint64_t rounds) {
             if (c == 0) e_.softmax_gradients_async(kMinHess);
             e_.select_class(c);
             inflight.push_back(b.queue_device());
-            e_.walk_device_tree(c, nullptr);
-            e_.walk_evals_device(c, 0, false);
+            // guarded by the class's scale: a tree grown from gradients that
+            // are not finite, and every tree queued after it, reach no margins
+            e_.walk_device_tree(c, nullptr, 0, c, 1);
+            e_.walk_evals_device(c, 0, true);
             queued++;
         }
         std::vector<GrowTreeNode> nodes;
@@ -624,9 +628,10 @@ void Trainer::boost_softmax_batched(uint64_t rounds) {
         while (queued < rounds && inflight.size() < 3) {
             e_.softmax_gradients_async(kMinHess);
             inflight.push_back(b.queue_classes());
+            // guarded by every class's scale: the host keeps or drops a round whole
             for (uint32_t c = 0; c < k_; c++) {
-                e_.walk_device_tree(c, nullptr, c);
-                e_.walk_evals_device(c, c, false);
+                e_.walk_device_tree(c, nullptr, c, 0, k_);
+                e_.walk_evals_device(c, c, true);
             }
             queued++;
         }

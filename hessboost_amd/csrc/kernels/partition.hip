@@ -267,7 +267,20 @@ __device__ __forceinline__ uint32_t node_meta(const WalkArgs &a, uint32_t i, uin
     return t.left < 0 ? 1u << 31 : t.feature | (t.limit << 16);
 }
 
+// A guarded walk that must not happen: the tree's gradients (any of its
+// guard_n scales) were not finite, or an earlier guarded walk was skipped.
+// Every workgroup reads the same words, so the answer is uniform; the first
+// thread of the grid records the skip.
+__device__ __forceinline__ bool walk_skipped(const WalkArgs &a) {
+    if (!a.guard) return false;
+    uint32_t bad = *a.poison;
+    for (uint32_t i = 0; i < max(a.guard_n, 1u); i++) bad |= a.guard[i].nonfinite;
+    if (bad && blockIdx.x == 0 && threadIdx.x == 0) *a.poison = 1u;
+    return bad != 0;
+}
+
 extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves(WalkArgs a) {
+    if (walk_skipped(a)) return;
     const uint32_t n_nodes = walk_nodes(a);
     for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += gridDim.x * blockDim.x) {
         const uint8_t *b = a.bins8 + (size_t)r * a.stride;
@@ -357,6 +370,7 @@ __device__ __forceinline__ void load_row_bins(const WalkArgs &a, uint32_t r, uin
 extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves32(WalkArgs a) {
     __shared__ uint2 s_node[kWalkLdsNodes];
     __shared__ float s_value[kWalkLdsNodes];
+    if (walk_skipped(a)) return;
     const uint32_t n_nodes = load_walk_nodes(a, s_node, s_value);
     __syncthreads();
     const uint32_t stride = gridDim.x * blockDim.x;
@@ -392,13 +406,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
     const GradArgs &ga = args.g;
     __shared__ uint2 s_node[kWalkLdsNodes];
     __shared__ float s_value[kWalkLdsNodes];
-    if (a.guard) {  // uniform: every workgroup reads the same words
-        const QScale q = *a.guard;
-        if (q.nonfinite != 0 || *a.poison != 0) {
-            if (blockIdx.x == 0 && threadIdx.x == 0) *a.poison = 1u;
-            return;
-        }
-    }
+    if (walk_skipped(a)) return;
     const uint32_t n_nodes = load_walk_nodes(a, s_node, s_value);
     __syncthreads();
     uint32_t mg = 0, mh = 0, bad = 0;

@@ -272,3 +272,30 @@ def test_trees_discarded_by_the_device_are_added_to_no_eval_set():
     np.testing.assert_array_equal(t.eval_margins(own).view(np.uint32), expected(booster, x).view(np.uint32))
     ev = eval_matrix(1_000, 10, 26)
     np.testing.assert_array_equal(t.eval_margins(other).view(np.uint32), expected(booster, ev).view(np.uint32))
+
+
+@pytest.mark.parametrize("batched", ["1", "0"], ids=["batched", "pipelined"])
+def test_softmax_trees_discarded_by_the_device_reach_no_margins(batched, monkeypatch):
+    """Softmax rounds whose gradients overflow (eta 1e30, lambda 0): once a
+    class's margins reach infinity its next gradients are not finite. The
+    device skips the walks of that tree (batched: of that whole round) and
+    of every tree queued after it; training stops with an error, and the
+    training margins and each eval set hold exactly the kept trees."""
+    monkeypatch.setenv("HBROCM_SOFTMAX_BATCH", batched)
+    x, y = data(6_000, 10, 27, "multi:softprob", k=3)
+    dtrain = hb.DMatrix(x, label=y)
+    t = hb.Trainer(dtrain.engine(256), {"objective": "multi:softprob", "num_class": 3, "max_depth": 3,
+                                        "eta": 1e30, "lambda": 0.0}, y)
+    own = t.add_eval(dtrain)
+    other = t.add_eval(hb.DMatrix(eval_matrix(1_000, 10, 28)))
+    with pytest.raises(hb.HbrError, match="not finite"):
+        t.boost(8)
+    booster = t.booster(10)
+    assert 1 <= booster.num_trees() < 24
+    if batched == "1":
+        assert booster.num_trees() % 3 == 0  # a round is kept or dropped whole
+    want = expected(booster, x)
+    np.testing.assert_array_equal(t.margins().reshape(-1, 3).view(np.uint32), want.view(np.uint32))
+    np.testing.assert_array_equal(t.eval_margins(own).view(np.uint32), want.view(np.uint32))
+    ev = eval_matrix(1_000, 10, 28)
+    np.testing.assert_array_equal(t.eval_margins(other).view(np.uint32), expected(booster, ev).view(np.uint32))
