@@ -236,6 +236,9 @@ def main():
     ap.add_argument("--breakdown-steps", type=int, default=5)
     ap.add_argument("--no-kernel-events", action="store_true",
                     help="time the rounds without HIP events around the histogram kernel")
+    ap.add_argument("--hist-sample", type=int, default=5,
+                    help="time every N-th histogram launch with HIP events (each timed launch stalls the "
+                         "stream around its events; N coprime with the 8 levels of a tree samples every level)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="first run a device-to-device copy of this many MiB (a known-size kernel for "
                          "scaling hardware byte counters in profiles)")
@@ -309,8 +312,9 @@ def main():
     trainer.boost(args.warmup)
     log(f"{args.warmup} warmup rounds done")
     before = eng.counters()
-    # HIP events around the dense histogram kernel only, on the engine's stream
-    eng.set_profiling(not args.no_kernel_events, HIST_KERNEL)
+    # HIP events around a sample of the dense histogram kernel's launches
+    # (every hist_sample-th, so every level is sampled), on the engine's stream
+    eng.set_profiling(not args.no_kernel_events, HIST_KERNEL, every=max(1, args.hist_sample))
     t0 = time.perf_counter()
     trainer.boost(args.steps)
     t1 = time.perf_counter()
@@ -319,14 +323,18 @@ def main():
     eng.set_profiling(False)
     elapsed = t1 - t0
     rounds_per_s = args.steps / elapsed
-    hist_ms = sum(ms for k, (ms, n) in stats.items() if k.startswith(HIST_KERNEL))
-    hist_launches = sum(n for k, (ms, n) in stats.items() if k.startswith(HIST_KERNEL))
+    hist_timed_ms = sum(ms for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
+    hist_timed = sum(timed for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
+    hist_launches = sum(n for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
     hist_names = sorted(k for k in stats if k.startswith(HIST_KERNEL))
+    # the launches' total device time from the timed sample's average duration
+    hist_ms = hist_timed_ms / hist_timed * hist_launches if hist_timed else 0.0
     hist_bytes = after["hist_bytes"] - before["hist_bytes"]
     lds_atomics = (after["hist_rows"] - before["hist_rows"]) * x.shape[1] * 2
     achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
     log(f"{args.steps} rounds in {elapsed:.3f}s = {rounds_per_s:.1f} rounds/s; {'/'.join(hist_names)} "
-        f"{hist_ms:.1f} ms over {hist_launches} launches, {achieved:.0f} GB/s algorithmic")
+        f"{hist_ms / max(1, hist_launches):.4f} ms per launch ({hist_timed} of {hist_launches} launches timed), "
+        f"{achieved:.0f} GB/s algorithmic")
     # per-kernel time per round, from a few more rounds with every kernel timed
     breakdown = {}
     if args.breakdown_steps > 0:
@@ -335,8 +343,23 @@ def main():
         bstats = eng.kernel_stats()
         eng.set_profiling(False)
         breakdown = {k: round(ms / args.breakdown_steps, 4)
-                     for k, (ms, n) in sorted(bstats.items(), key=lambda kv: -kv[1][0])}
+                     for k, (ms, timed, n) in sorted(bstats.items(), key=lambda kv: -kv[1][0])}
         log("ms per round by kernel: " + ", ".join(f"{k} {v}" for k, v in breakdown.items()))
+    # the margin walk that also sums the next root's histogram: its
+    # algorithmic bytes per row (the 32-byte row read and written back with
+    # its pair word, the margin read and written, the label), its two 64-bit
+    # LDS adds per (row, feature column), over its time per round
+    walk_root = None
+    if breakdown.get("hbr_walk_grad_root"):
+        wms = breakdown["hbr_walk_grad_root"]
+        wbytes = x.shape[0] * (32 + 32 + 4 + 4 + 4)
+        wach = wbytes / (wms * 1e-3) / 1e9
+        watom = x.shape[0] * 32 * 2 / (wms * 1e-3) / 1e12
+        walk_root = {"kernel": "hbr_walk_grad_root", "bound": "hbm", "achieved": round(wach, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(wach / HBM_PEAK_GBS, 4),
+                     "avg_launch_ms": round(wms, 4), "algorithmic_bytes_per_launch": wbytes,
+                     "lds_atomics": {"achieved": round(watom, 3), "peak": LDS_ATOMIC_PEAK_T, "unit": "T lane-ops/s",
+                                     "frac": round(watom / LDS_ATOMIC_PEAK_T, 4)}}
     n_trees = len(trainer.trees())
     traffic, traffic_alg, traffic_src = measured_traffic(hist_names[0] if hist_names else HIST_KERNEL)
 
@@ -370,6 +393,7 @@ def main():
             "traffic_source": traffic_src,
             "traffic_run_algorithmic_bytes": traffic_alg,
             "launches": hist_launches,
+            "timed_launches": hist_timed,
             "avg_launch_ms": round(hist_ms / max(1, hist_launches), 4),
             "algorithmic_bytes_per_launch": int(hist_bytes / max(1, hist_launches)),
             # the kernel's other bound: two 64-bit LDS integer adds per (row, feature)
@@ -382,6 +406,7 @@ def main():
             },
         },
         "kernel_ms_per_round": breakdown,
+        **({"walk_root_roofline": walk_root} if walk_root else {}),
         # the index built on the device from the f32 rows (not part of the rounds)
         "binning": {
             "value": round(x.shape[0] / t_bin / 1e6, 1), "unit": "Mrows/s",

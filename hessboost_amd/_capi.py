@@ -237,10 +237,11 @@ def typed(a, ctype):
 
 
 def kernel_stats(text: str) -> dict:
-    """Parse hbr_kernel_stats' "name=ms,launches;" list."""
+    """Parse hbr_kernel_stats' "name=ms,timed,launches;" list into
+    name -> (ms over the timed launches, timed launches, launches)."""
     out = {}
     for item in filter(None, text.split(";")):
         name, rest = item.split("=")
-        ms, n = rest.split(",")
-        out[name] = (float(ms), int(n))
+        ms, timed, n = rest.split(",")
+        out[name] = (float(ms), int(timed), int(n))
     return out

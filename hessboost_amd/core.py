@@ -396,10 +396,11 @@ class Engine:
         A.check(A.lib().hbr_read_hist(self._h, slot, A.ptr(out)))
         return out.reshape(-1, 2)
 
-    def set_profiling(self, on=True, kernel_prefix=None):
+    def set_profiling(self, on=True, kernel_prefix=None, every=1):
         """Time kernels (those whose name starts with kernel_prefix) with HIP
-        events on the engine's stream."""
-        A.check(A.lib().hbr_set_profiling(self._h, int(on), None if kernel_prefix is None else kernel_prefix.encode()))
+        events on the engine's stream: every `every`-th launch of them."""
+        A.check(A.lib().hbr_set_profiling(self._h, int(every) if on else 0,
+                                          None if kernel_prefix is None else kernel_prefix.encode()))
 
     def kernel_stats(self):
         buf = C.create_string_buffer(1 << 16)
@@ -955,8 +956,8 @@ class Forest:
         A.check(A.lib().hbr_predict_margin_device(self._h, C.c_void_p(d_x), n_rows, n_cols, float(missing),
                                                   C.c_void_p(d_out), None if d_leaf is None else C.c_void_p(d_leaf)))
 
-    def set_profiling(self, on=True, kernel_prefix=None):
-        A.check(A.lib().hbr_forest_set_profiling(self._h, int(on),
+    def set_profiling(self, on=True, kernel_prefix=None, every=1):
+        A.check(A.lib().hbr_forest_set_profiling(self._h, int(every) if on else 0,
                                                   None if kernel_prefix is None else kernel_prefix.encode()))
 
     def kernel_stats(self):

@@ -44,6 +44,8 @@ struct QScale {
     uint32_t nonfinite;   // count of rows with a non-finite g or h
     uint32_t scalar_rows; // rows listed for the scalar sigmoid (until hbr_finish_scale)
     uint32_t pad[2];      // hbr_grain_fold: 1024 - (grain + 150) of g and of h (0: all zero)
+    uint32_t deferred;    // rows hbr_finish_scale took from the list (their pairs are its own)
+    uint32_t pad2;
 };
 
 // A node's rows: `len` row ids at `offset` of row buffer `buf` (0 or 1).
@@ -128,7 +130,7 @@ struct GradArgs {
     const float *margins;   // n (one output)
     const float *labels;    // n
     const float *weights;   // n or null
-    GPair *gpair;           // n
+    GPair *gpair;           // n (null: not written, the rows carry the pairs)
     QScale *scale;          // max folds (atomics) land here
     const uint64_t *exp_table;  // the expf restatement's 32 entries (scalar rows)
     uint32_t *scalar_list;  // where kernels that defer the scalar rows list them
@@ -462,6 +464,13 @@ struct FinishArgs {
     QScale *scale;
     uint64_t n_rows;
     GradArgs grad;
+    // Non-zero: the exponents come from these magnitudes (f32 bits), bounds
+    // the pairs cannot exceed (the unit-weight logistic loss: |g| <= 1,
+    // h <= 1/4), rather than from the folded maxima, so that a kernel can
+    // quantise the pairs as it computes them. The larger of the two is taken
+    // should a maximum ever exceed its bound.
+    uint32_t bound_g_bits;
+    uint32_t bound_h_bits;
 };
 
 // Every class's exponents from its folded maxima, in place (one thread per class).
@@ -641,6 +650,36 @@ struct EvalWalkArgs {
 struct WalkGradArgs {
     WalkArgs w;
     GradArgs g;
+    // hbr_walk_grad_root: the next tree's root histogram from the pairs the
+    // walk computes, quantised with these exponents (the bounds' exponents
+    // hbr_finish_scale will set), one partial of kRootTile bins per
+    // workgroup (feature-major: [f][256]); rows the walk defers are left to
+    // hbr_root_fixup.
+    QBin *root_partial;
+    int32_t root_exp_g;
+    int32_t root_exp_h;
+    uint32_t n_cols;
+    uint32_t pad;
+};
+
+// The bins of one root partial: 32 features of 256 bins (the dense
+// histogram kernel's fg32 layout, one feature group).
+constexpr uint32_t kRootFeatures = 32;
+constexpr uint32_t kRootTile = kRootFeatures * 256;
+
+// The root after hbr_walk_grad_root: the deferred rows' histogram into one
+// more partial (after the walk's n_walk_tiles), and the root's node record
+// for hbr_hist_reduce (n_tiles = n_walk_tiles + 1 from partial 0).
+struct RootFixupArgs {
+    const QScale *scale;        // the finished scale: deferred rows and exponents
+    const uint32_t *listed;     // the deferred rows (GradArgs::scalar_list)
+    const uint8_t *bins8;       // rows of 32 bytes: 28 bins (or fewer) and the pair word
+    QBin *partial;
+    HistNode *node;
+    uint32_t n_walk_tiles;
+    uint32_t n_cols;
+    float min_hess;
+    uint32_t pad;
 };
 
 // ---- prediction ---------------------------------------------------------------------

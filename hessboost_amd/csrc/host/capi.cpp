@@ -127,8 +127,8 @@ std::string stats_string(Device &d) {
     std::string s;
     for (auto &kv : d.kernel_stats()) {
         char buf[160];
-        std::snprintf(buf, sizeof buf, "%s=%.6f,%llu;", kv.first.c_str(), kv.second.total_ms,
-                      (unsigned long long)kv.second.launches);
+        std::snprintf(buf, sizeof buf, "%s=%.6f,%llu,%llu;", kv.first.c_str(), kv.second.total_ms,
+                      (unsigned long long)kv.second.launches, (unsigned long long)kv.second.calls);
         s += buf;
     }
     return s;
@@ -686,7 +686,7 @@ int hbr_engine_counters_read(hbr_engine *h, hbr_engine_counters *out) {
 }
 
 int hbr_set_profiling(hbr_engine *h, int on, const char *prefix) {
-    return with_engine(h, [&](Engine &e) { e.dev().set_profiling(on != 0, prefix ? prefix : ""); });
+    return with_engine(h, [&](Engine &e) { e.dev().set_profiling(on > 0 ? (uint32_t)on : 0u, prefix ? prefix : ""); });
 }
 
 int hbr_kernel_stats(hbr_engine *h, char *buf, size_t len) {
@@ -869,7 +869,7 @@ int hbr_predict_leaf(hbr_forest *h, const float *x, uint64_t n, uint64_t n_cols,
 }
 
 int hbr_forest_set_profiling(hbr_forest *h, int on, const char *prefix) {
-    return with_forest(h, [&](Forest &f) { f.dev().set_profiling(on != 0, prefix ? prefix : ""); });
+    return with_forest(h, [&](Forest &f) { f.dev().set_profiling(on > 0 ? (uint32_t)on : 0u, prefix ? prefix : ""); });
 }
 
 int hbr_forest_kernel_stats(hbr_forest *h, char *buf, size_t len) {

@@ -66,6 +66,7 @@ void Engine::read_tunables() {
     }
     if (const char *v = std::getenv("HBROCM_HIST_BIN_MAJOR")) hist_bin_major = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_ROW_PAIRS")) row_pairs = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_FUSED_ROOT")) fused_root = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_CSR_RANGES")) csr_range_table = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_WALK_BLOCKS")) {
@@ -382,6 +383,8 @@ void Engine::load_margins(const float *m, uint64_t n, uint32_t outputs) {
     outputs_ = outputs;
     active_pairs_ = nullptr;
     row_pairs_live_ = false;
+    root_partials_ = 0;  // the staged pairs are no longer the walk's
+    pair_array_stale_ = false;
     class_outputs_ = 0;
     margins_.resize(n);
     margins_.upload(m, n, dev_.stream());
@@ -412,6 +415,8 @@ void Engine::read_margins(float *out, uint64_t n) {
 }
 
 void Engine::read_gradients(float *out, uint64_t n) {
+    if (pair_array_stale_ && !softmax_staged())
+        fail(kRefused, "read_gradients: the last margin walk left its pairs in the rows only");
     if (softmax_staged() && n == n_rows_ * outputs_) {
         class_pairs_.download(reinterpret_cast<GPair *>(out), n, dev_.stream());
     } else {
@@ -455,6 +460,8 @@ bool Engine::sums_exact(uint64_t m) const {
 void Engine::prepare(const float *gpair, uint64_t n) {
     if (n != n_rows_) fail(kInvalid, "prepare: one gradient pair per row");
     row_pairs_live_ = false;
+    root_partials_ = 0;  // the staged pairs are no longer the walk's
+    pair_array_stale_ = false;
     active_pairs_ = nullptr;
     class_outputs_ = 0;  // the softmax pairs are no longer the staged gradients
     gpair_.resize(n_rows_ ? n_rows_ : 1);
@@ -504,6 +511,18 @@ bool Engine::row_pairs_ok(const hbr_device_loss &loss) const {
            outputs_ == 1;
 }
 
+bool Engine::bounded_logistic(const hbr_device_loss &loss) const {
+    return loss.kind == HBR_LOSS_LOGISTIC && loss.scale_pos_weight == 1.0f && !has_weights_ && labels_binary_ &&
+           loss.min_hess <= 0.25f && outputs_ == 1;
+}
+
+void Engine::set_bounds(const hbr_device_loss &loss, FinishArgs &f) const {
+    const bool b = bounded_logistic(loss);
+    const float g = 1.0f, h = 0.25f;
+    f.bound_g_bits = b ? abs_bits(g) : 0u;
+    f.bound_h_bits = b ? abs_bits(h) : 0u;
+}
+
 GradArgs Engine::grad_args(const hbr_device_loss &loss) {
     GradArgs a{};
     if (row_pairs_ok(loss)) {
@@ -539,6 +558,8 @@ void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     HBR_HIP(hipMemsetAsync(scale_dev(), 0, sizeof(QScale), s));
     const GradArgs a = grad_args(loss);
     row_pairs_live_ = a.pair_rows != nullptr;
+    root_partials_ = 0;  // the staged pairs are no longer the walk's
+    pair_array_stale_ = false;
     row_pairs_min_hess_ = loss.min_hess;
     // grid-stride: a few workgroups per CU, one max fold each
     const uint32_t grad_blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)),
@@ -548,9 +569,9 @@ void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
 
 // The exponents of the folded maxima, on the host (the device's rule), and
 // the scale back to the device; false when a gradient is not finite.
-bool Engine::check_scale(QScale host) {
-    host.exp_g = exp_for(host.max_g_bits, n_rows_);
-    host.exp_h = exp_for(host.max_h_bits, n_rows_);
+bool Engine::check_scale(QScale host, uint32_t bound_g_bits, uint32_t bound_h_bits) {
+    host.exp_g = exp_for(std::max(host.max_g_bits, bound_g_bits), n_rows_);
+    host.exp_h = exp_for(std::max(host.max_h_bits, bound_h_bits), n_rows_);
     scale_host_ = host;
     HBR_HIP(hipMemcpyAsync(scale_dev(), &scale_host_, sizeof(QScale), hipMemcpyHostToDevice, dev_.stream()));
     dev_.sync();
@@ -570,14 +591,17 @@ bool Engine::compute_gradients(const hbr_device_loss &loss, uint32_t output) {
     const QScale host = *q;
     stage_.reset();
     scale_checked_ = true;
-    const bool ok = check_scale(host);
+    FinishArgs bounds{};
+    set_bounds(loss, bounds);
+    const bool ok = check_scale(host, bounds.bound_g_bits, bounds.bound_h_bits);
     grains_known_ = true;
     return ok;
 }
 
 void Engine::compute_gradients_async(const hbr_device_loss &loss, uint32_t output) {
     launch_gradients(loss, output);
-    FinishArgs f{scale_dev(), n_rows_, grad_args(loss)};
+    FinishArgs f{scale_dev(), n_rows_, grad_args(loss), 0u, 0u};
+    set_bounds(loss, f);
     f.grad.scalar_list = nullptr;  // the gradient kernel lists no rows
     dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
     scale_checked_ = false;  // grow_root reads the scale back and checks it
@@ -600,6 +624,8 @@ void Engine::softmax_gradients_async(float min_hess) {
     if (n_rows_ == 0) fail(kInvalid, "softmax gradients: no rows");
     hipStream_t s = dev_.stream();
     row_pairs_live_ = false;
+    root_partials_ = 0;  // the staged pairs are no longer the walk's
+    pair_array_stale_ = false;
     active_pairs_ = nullptr;
     grains_known_ = false;
     class_pairs_.reserve((size_t)k * n_rows_);
@@ -829,6 +855,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
                          const PartSplit *splits_dev, const PartOut *part_out_dev, const uint32_t *rows0,
                          const GrowCounts *grow) {
     if (n == 0) return;
+    root_partials_ = 0;  // the partials are reused below
     if (!level_pairs_ && !pairs_staged()) fail(kInvalid, "histograms: no gradients staged");
     if (!dense_u8_ && grow) fail(kInvalid, "histograms: device-counted levels need the dense kernels");
     const uint32_t fg = hist_features_per_group;
@@ -1254,12 +1281,40 @@ void Engine::launch_device_roots(uint32_t n_trees) {
                         dim3(kThreads), a);
         }
     }
-    counters.hist_nodes += n_trees;
-    counters.hist_rows += n_trees * n_rows_;
-    counters.hist_bytes += n_trees * hist_bytes(n_rows_, false);
-    const HistNode *hn = reinterpret_cast<const HistNode *>(d_root_in_.get());
+    HistNode *hn = reinterpret_cast<HistNode *>(d_root_in_.get());
     const ScanNode *sn = reinterpret_cast<const ScanNode *>(d_root_in_.get() + n_trees * sizeof(HistNode));
-    launch_hist(hn, n_trees, nullptr, nullptr, nullptr);
+    const uint32_t fused = n_trees == 1 && !level_pairs_ && row_pairs_live_ ? root_partials_ : 0u;
+    root_partials_ = 0;
+    if (fused) {
+        // the margin walk summed the root's rows into `fused` partials; the
+        // rows it deferred go into one more, then the reduce makes the slot
+        RootFixupArgs f{};
+        f.scale = scale_dev();
+        f.listed = scalar_list_.get();
+        f.bins8 = rows8_.get();
+        f.partial = d_partial_.get();
+        f.node = hn;
+        f.n_walk_tiles = fused;
+        f.n_cols = n_cols_;
+        f.min_hess = row_pairs_min_hess_;
+        dev_.launch("hbr_root_fixup", dim3(1), dim3(1024), f);
+        ReduceArgs r{};
+        r.nodes = hn;
+        r.partial = d_partial_.get();
+        r.hist = hist_.get();
+        r.feature_offset = d_fo_.get();
+        r.n_cols = n_cols_;
+        r.total_bins = total_bins_;
+        r.groups = 1;
+        r.fg = kRootFeatures;
+        r.grow = nullptr;
+        dev_.launch("hbr_hist_reduce", dim3(n_cols_ * 4, 1), dim3(1024), r);
+    } else {
+        counters.hist_nodes += n_trees;
+        counters.hist_rows += n_trees * n_rows_;
+        counters.hist_bytes += n_trees * hist_bytes(n_rows_, false);
+        launch_hist(hn, n_trees, nullptr, nullptr, nullptr);
+    }
     launch_scan(sn, n_trees, nullptr, nullptr, n_trees == 1 ? root_best_dev() : d_best_.get());
 }
 
@@ -1516,8 +1571,26 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     wg.g = grad_args(*next_loss);
     row_pairs_live_ = wg.g.pair_rows != nullptr;
     row_pairs_min_hess_ = next_loss->min_hess;
-    dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
-    FinishArgs f{scale_dev(), n_rows_, wg.g};
+    FinishArgs f{scale_dev(), n_rows_, wg.g, 0u, 0u};
+    set_bounds(*next_loss, f);
+    // the next root's histogram in the same pass: row-carried pairs, whose
+    // bounds fix the exponents, and one 1024-thread workgroup per CU
+    const uint32_t root_tiles = std::min<uint32_t>((uint32_t)dev_.cu_count(), ceil_div(n_rows_, 1024));
+    root_partials_ = 0;
+    pair_array_stale_ = false;
+    if (fused_root && row_pairs_live_ && f.bound_g_bits && n_cols_ <= kRootFeatures && root_tiles >= 2) {
+        d_partial_.reserve((size_t)(root_tiles + 1) * kRootTile);
+        wg.root_partial = d_partial_.get();
+        wg.root_exp_g = exp_for(f.bound_g_bits, n_rows_);
+        wg.root_exp_h = exp_for(f.bound_h_bits, n_rows_);
+        wg.n_cols = n_cols_;
+        wg.g.gpair = nullptr;  // the rows carry every pair; the finish writes its deferred rows' both ways
+        dev_.launch("hbr_walk_grad_root", dim3(root_tiles), dim3(1024), wg);
+        root_partials_ = root_tiles;
+        pair_array_stale_ = true;
+    } else {
+        dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
+    }
     dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
     scale_checked_ = false;  // the next tree's finish checks the scale
 }
@@ -1710,9 +1783,12 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
         wg.w = a;
         wg.g = grad_args(*next_loss);
         row_pairs_live_ = wg.g.pair_rows != nullptr;
+        root_partials_ = 0;  // the staged pairs are no longer the walk's
+        pair_array_stale_ = false;
         row_pairs_min_hess_ = next_loss->min_hess;
         dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
-        FinishArgs f{scale_dev(), n_rows_, wg.g};
+        FinishArgs f{scale_dev(), n_rows_, wg.g, 0u, 0u};
+        set_bounds(*next_loss, f);
         dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
         scale_checked_ = false;  // grow_root reads the scale back and checks it
         return;

@@ -339,7 +339,9 @@ private:
     void scan_host_nodes(const std::vector<ScanNode> &nodes, ScanBest *out, uint32_t *sets = nullptr);
     void launch_gradients(const hbr_device_loss &loss, uint32_t output);
     GradArgs grad_args(const hbr_device_loss &loss);
-    bool check_scale(QScale folded);
+    // bounds: the pair bounds' f32 bits (0: none), whose exponents replace
+    // smaller maxima'
+    bool check_scale(QScale folded, uint32_t bound_g_bits = 0, uint32_t bound_h_bits = 0);
     const uint64_t *expf_table_dev();  // the expf restatement's table, uploaded once
     bool scale_checked_ = true;  // the host has seen the scale of the staged gradients
 
@@ -391,6 +393,17 @@ private:
     bool row_pairs_live_ = false;
     float row_pairs_min_hess_ = 0.0f;
     bool row_pairs_ok(const hbr_device_loss &loss) const;
+    // The unit-weight logistic loss (no weights, scale_pos_weight 1, labels
+    // 0 or 1) bounds its pairs, |g| <= 1 and h <= 1/4: the exponents are the
+    // bounds', known before the pairs are (FinishArgs::bound_*).
+    bool bounded_logistic(const hbr_device_loss &loss) const;
+    void set_bounds(const hbr_device_loss &loss, FinishArgs &f) const;
+    // Partials of the next root's histogram the fused walk left (0: none);
+    // the next device tree's root sums them instead of building its own.
+    uint32_t root_partials_ = 0;
+    // The fused walk wrote its pairs into the rows only (the pair array is
+    // stale until the next gradients are staged some other way).
+    bool pair_array_stale_ = false;
     // the per-tree scale, the root total and the root's winner, adjacent so
     // that the root's synchronisation reads them back with one copy
     struct RootBlock {
@@ -459,6 +472,7 @@ public:
     uint32_t hist_waves = 1;
     bool hist_bin_major = true;  // [bin][feature] LDS layout (16 and 32 feature groups)
     bool row_pairs = true;       // unit-weight logistic pairs carried in the rows' padding
+    bool fused_root = true;      // the margin walk also sums the next root's histogram (row pairs)
     bool device_grow = true;     // depthwise trees decided on the device where eligible
     bool csr_range_table = true; // CSR histograms read each bin range's entries from a per-row table
     uint32_t walk_blocks_per_cu = 4;  // workgroups per CU of the device-tree margin walk (one resident wave)

@@ -51,10 +51,13 @@ public:
 
     // Kernel timing with HIP events on this device's stream (off by default):
     // only kernels whose name starts with `prefix` (every kernel when empty).
-    void set_profiling(bool on, const std::string &prefix = "");
+    // every: 0 off; N >= 1 times every N-th launch of the kernels whose name
+    // starts with prefix (all of them are counted)
+    void set_profiling(uint32_t every, const std::string &prefix = "");
     struct KernelStat {
-        double total_ms = 0.0;
-        uint64_t launches = 0;
+        double total_ms = 0.0;  // over the timed launches
+        uint64_t launches = 0;  // timed
+        uint64_t calls = 0;     // every matching launch while profiling
     };
     std::unordered_map<std::string, KernelStat> kernel_stats();
     void reset_stats();
@@ -69,7 +72,8 @@ private:
     hipStream_t stream_ = nullptr;
     hipModule_t module_ = nullptr;
     std::unordered_map<std::string, hipFunction_t> functions_;
-    bool profiling_ = false;
+    uint32_t profile_every_ = 0;
+    uint64_t profile_seen_ = 0;
     std::string profile_prefix_;
     struct Pending {
         std::string name;

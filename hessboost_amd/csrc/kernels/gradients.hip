@@ -42,7 +42,7 @@ __device__ __forceinline__ float exp_vector(float x) {
 // Workgroup-wide fold of the magnitude maxima and the non-finite count,
 // then one atomic per workgroup (non-negative f32 bits order as integers).
 __device__ __forceinline__ void fold_block(QScale *s, uint32_t mg, uint32_t mh, uint32_t bad) {
-    __shared__ uint32_t red[3][256 / kWave];
+    __shared__ uint32_t red[3][1024 / kWave];  // workgroups of up to 1024 threads
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
         mg = max(mg, (uint32_t)__shfl_xor((int)mg, d, kWave));
@@ -93,10 +93,12 @@ __device__ __forceinline__ uint32_t pair_word(float p, float y) {
 // 8-row groups). kDefer: a row outside the vector path is listed for
 // hbr_finish_scale instead (keeping the f64 expf out of a hot loop).
 // *word: the row's pair word (pair_word) when its logistic pair is computed
-// here (left alone for a deferred row).
+// here (left alone for a deferred row). *pair (when given): the row's pair,
+// set for an active row whose pair is computed here.
 template <bool kDefer>
 __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, bool active, float m, float y, float w,
-                                                uint32_t &mg, uint32_t &mh, uint32_t &bad, uint32_t *word) {
+                                                uint32_t &mg, uint32_t &mh, uint32_t &bad, uint32_t *word,
+                                                GPair *pair = nullptr) {
     {
         float g = 0.0f, h = 0.0f;
         if (a.loss == kSquaredError) {
@@ -132,7 +134,8 @@ __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, b
             }
         }
         if (active) {
-            a.gpair[i] = GPair{g, h};
+            if (a.gpair) a.gpair[i] = GPair{g, h};  // null: the rows carry the pairs alone
+            if (pair) *pair = GPair{g, h};
             mg = max(mg, __float_as_uint(g) & 0x7fffffffu);
             mh = max(mh, __float_as_uint(h) & 0x7fffffffu);
             bad += (!__builtin_isfinite(g) || !__builtin_isfinite(h)) ? 1u : 0u;
@@ -284,9 +287,11 @@ extern "C" __global__ __launch_bounds__(256) void hbr_finish_scale(FinishArgs a)
         q.max_h_bits = max(q.max_h_bits, red[1][w]);
         q.nonfinite += red[2][w];
     }
+    q.deferred = listed;
     q.scalar_rows = 0;
-    q.exp_g = exponent_for(q.max_g_bits, a.n_rows);
-    q.exp_h = exponent_for(q.max_h_bits, a.n_rows);
+    // bounds (when given) in place of the maxima, the larger should a maximum exceed its bound
+    q.exp_g = exponent_for(max(q.max_g_bits, a.bound_g_bits), a.n_rows);
+    q.exp_h = exponent_for(max(q.max_h_bits, a.bound_h_bits), a.n_rows);
     *a.scale = q;
 }
 

@@ -452,3 +452,135 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
     }
     fold_block(ga.scale, mg, mh, bad);
 }
+
+// hbr_walk_grad32 that also sums the next tree's root histogram: each
+// active row's new pair, quantised with the bound exponents hbr_finish_scale
+// will set (the unit-weight logistic loss: |g| <= 1, h <= 1/4), goes into a
+// bin-major LDS histogram of 32 feature columns, as the dense histogram
+// kernel adds it (the lanes' features rotated; columns past the index's
+// features take the row's padding and pair bytes and are never written
+// out). One workgroup per CU, its sub-histogram written to its own partial
+// ([f][256]); rows the walk defers to hbr_finish_scale are summed by
+// hbr_root_fixup. The pair's bits equal those the histogram kernel derives
+// from the row's word, so the sums are the root histogram's.
+constexpr uint32_t kRootWalkRows = 4;
+
+extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradArgs args) {
+    const WalkArgs &a = args.w;
+    const GradArgs &ga = args.g;
+    __shared__ uint2 s_node[kWalkLdsNodes];
+    __shared__ float s_value[kWalkLdsNodes];
+    __shared__ unsigned long long lg[kRootTile], lh[kRootTile];
+    if (walk_skipped(a)) return;
+    for (uint32_t i = threadIdx.x; i < kRootTile; i += blockDim.x) {
+        lg[i] = 0ull;
+        lh[i] = 0ull;
+    }
+    const uint32_t n_nodes = load_walk_nodes(a, s_node, s_value);
+    __syncthreads();
+    const uint32_t rot = lane_id() & (kRootFeatures - 1u);
+    uint32_t mg = 0, mh = 0, bad = 0;
+    const uint32_t end = (a.n + kWave - 1) / kWave * kWave;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t r0 = blockIdx.x * blockDim.x + threadIdx.x; r0 < end; r0 += kRootWalkRows * stride) {
+        uint32_t w[kRootWalkRows][8];
+        float m[kRootWalkRows], y[kRootWalkRows];
+#pragma unroll
+        for (uint32_t k = 0; k < kRootWalkRows; k++) {
+            const uint32_t r = r0 + k * stride;
+            m[k] = 0.0f;
+            y[k] = 0.0f;
+            if (r < a.n) {
+                load_row_bins(a, r, w[k]);
+                m[k] = a.margins[(size_t)r * a.m_stride + a.output];
+                y[k] = ga.labels[r];
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kRootWalkRows; k++) {
+            const uint32_t r = r0 + k * stride;
+            const bool active = r < a.n;
+            if (active) {
+                const int32_t leaf = walk_row(s_node, n_nodes, w[k]);
+                if (leaf >= 0) {
+                    m[k] = m[k] + s_value[leaf];
+                    a.margins[(size_t)r * a.m_stride + a.output] = m[k];
+                }
+            }
+            if (r >= end) continue;
+            uint32_t word = w[k][7];
+            // p stays NaN unless the row's pair is computed here (a deferred
+            // row's is hbr_finish_scale's; a non-finite pair fails the tree)
+            GPair p{__builtin_nanf(""), 0.0f};
+            row_gradient_yw<true>(ga, r, active, m[k], y[k], 1.0f, mg, mh, bad, &word, &p);
+            const bool summed = active && p.g == p.g;
+            if (active) {  // the whole 32-byte row back, its pair in the last word
+                uint4 *dst = reinterpret_cast<uint4 *>(ga.pair_rows + (size_t)r * 32u);
+                dst[0] = make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]);
+                dst[1] = make_uint4(w[k][4], w[k][5], w[k][6], word);
+            }
+            if (summed) {
+                const unsigned long long qg = (unsigned long long)quantize(p.g, args.root_exp_g);
+                const unsigned long long qh = (unsigned long long)quantize(p.h, args.root_exp_h);
+                rotate_bytes<8>(w[k], rot);
+#pragma unroll
+                for (int f = 0; f < (int)kRootFeatures; f++) {
+                    const uint32_t ff = ((uint32_t)f + rot) & (kRootFeatures - 1u);
+                    const uint32_t bin = (w[k][f >> 2] >> ((f & 3) * 8)) & 0xffu;
+                    atomicAdd(&lg[bin * kRootFeatures + ff], qg);
+                    atomicAdd(&lh[bin * kRootFeatures + ff], qh);
+                }
+            }
+        }
+    }
+    fold_block(ga.scale, mg, mh, bad);
+    __syncthreads();
+    QBin *dst = args.root_partial + (size_t)blockIdx.x * kRootTile;
+    for (uint32_t i = threadIdx.x; i < kRootTile; i += blockDim.x) {
+        const uint32_t ff = i % kRootFeatures, bin = i / kRootFeatures;
+        if (ff < args.n_cols) dst[ff * 256u + bin] = QBin{(int64_t)lg[i], (int64_t)lh[i]};
+    }
+}
+
+// One workgroup after hbr_finish_scale: the rows the fused walk deferred
+// (their words now written) into partial n_walk_tiles, as the histogram
+// kernel derives their pairs from the words, then the root's node record
+// for hbr_hist_reduce: every partial from the first.
+extern "C" __global__ __launch_bounds__(1024) void hbr_root_fixup(RootFixupArgs a) {
+    __shared__ unsigned long long lg[kRootTile], lh[kRootTile];
+    for (uint32_t i = threadIdx.x; i < kRootTile; i += blockDim.x) {
+        lg[i] = 0ull;
+        lh[i] = 0ull;
+    }
+    __syncthreads();
+    const QScale q = *a.scale;
+    for (uint32_t j = threadIdx.x; j < q.deferred; j += blockDim.x) {
+        const uint32_t r = a.listed[j];
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.bins8 + (size_t)r * 32u);
+        const uint4 x = src[0], z = src[1];
+        const uint32_t w[8] = {x.x, x.y, x.z, x.w, z.x, z.y, z.z, z.w};
+        const float pv = __uint_as_float(w[7] & 0x7fffffffu);
+        const float y = (w[7] >> 31) ? 1.0f : 0.0f;
+        const float qv = pv * (1.0f - pv);
+        const GPair p{(pv - y) * 1.0f, (qv > a.min_hess ? qv : a.min_hess) * 1.0f};
+        const unsigned long long qg = (unsigned long long)quantize(p.g, q.exp_g);
+        const unsigned long long qh = (unsigned long long)quantize(p.h, q.exp_h);
+        for (uint32_t f = 0; f < a.n_cols; f++) {
+            const uint32_t bin = (w[f >> 2] >> ((f & 3u) * 8u)) & 0xffu;
+            atomicAdd(&lg[bin * kRootFeatures + f], qg);
+            atomicAdd(&lh[bin * kRootFeatures + f], qh);
+        }
+    }
+    __syncthreads();
+    QBin *dst = a.partial + (size_t)a.n_walk_tiles * kRootTile;
+    for (uint32_t i = threadIdx.x; i < kRootTile; i += blockDim.x) {
+        const uint32_t ff = i % kRootFeatures, bin = i / kRootFeatures;
+        if (ff < a.n_cols) dst[ff * 256u + bin] = QBin{(int64_t)lg[i], (int64_t)lh[i]};
+    }
+    if (threadIdx.x == 0) {
+        a.node->tile_begin = 0;
+        a.node->n_tiles = a.n_walk_tiles + 1u;
+        a.node->pad[0] = 0;
+        a.node->pad[1] = 0;
+    }
+}

@@ -402,9 +402,12 @@ typedef struct hbr_engine_counters {
 } hbr_engine_counters;
 int hbr_engine_counters_read(hbr_engine *e, hbr_engine_counters *out);
 
-/* Per-kernel device time (HIP events on the engine's stream); profiling is
- * off until enabled, and enabling it clears the previous statistics.
- * buf receives "name=ms,launches;..." */
+/* Per-kernel device time (HIP events on the engine's stream) of the kernels
+ * whose name starts with kernel_prefix; profiling is off until enabled, and
+ * enabling it clears the previous statistics. on = N >= 1 times every N-th
+ * matching launch (each timed launch stalls the stream for its events;
+ * N = 1 times them all) and counts them all; on = 0 turns it off.
+ * buf receives "name=ms,timed,launches;..." (ms over the timed launches). */
 int hbr_set_profiling(hbr_engine *e, int on, const char *kernel_prefix);
 int hbr_kernel_stats(hbr_engine *e, char *buf, size_t len);
 

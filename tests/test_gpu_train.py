@@ -231,7 +231,7 @@ def _grow_both(x, y, params, rounds):
         tr = hb.Trainer(eng, params, y)
         eng.set_profiling(True, "hbr_grow_decide")
         tr.boost(rounds)
-        launches = sum(n for _, (_, n) in eng.kernel_stats().items())
+        launches = sum(n for _, (_, _, n) in eng.kernel_stats().items())
         eng.set_profiling(False)
         out.append((tr.trees(), tr.margins(), launches))
     return out
@@ -362,11 +362,15 @@ def test_pipelined_rounds_with_rows_beyond_the_vector_range():
 def test_row_carried_logistic_pairs_give_identical_trees(far_rows):
     """Unit-weight logistic with labels 0 and 1 on rows of at most 28
     features: the rows carry p and y in their padding and the histograms
-    derive (g, h) from them. The trees and margins equal, bit for bit, those
-    grown from the pair array (HBROCM_ROW_PAIRS=0), with rows beyond the
-    vector range (their pairs written by the scalar finish) or without; the
-    root's byte count shows which path ran (a 4-byte word against an 8-byte
-    pair per row)."""
+    derive (g, h) from them, and the margin walk sums the next root's
+    histogram as it computes the pairs (the exponents are the loss's bounds,
+    known in advance). The trees and margins equal, bit for bit, those grown
+    with the root built by the histogram kernel (HBROCM_FUSED_ROOT=0) and
+    from the pair array (HBROCM_ROW_PAIRS=0), with rows beyond the vector
+    range (deferred to the scalar finish, whose rows the root fix-up sums)
+    or without; the root's byte count shows which pair path ran (a 4-byte
+    word against an 8-byte pair per row), the kernel statistics that the
+    fused walk ran."""
     import os
     rng = np.random.default_rng(23)
     n, f = 50_003, 20
@@ -379,16 +383,16 @@ def test_row_carried_logistic_pairs_give_identical_trees(far_rows):
     params = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}
     index = hb.DMatrix(x, label=y).index(256)
     runs = []
-    for flag in (None, "0"):
-        old = os.environ.pop("HBROCM_ROW_PAIRS", None)
-        if flag is not None:
-            os.environ["HBROCM_ROW_PAIRS"] = flag
+    for env in ({}, {"HBROCM_FUSED_ROOT": "0"}, {"HBROCM_ROW_PAIRS": "0"}):
+        saved = {k: os.environ.pop(k, None) for k in ("HBROCM_ROW_PAIRS", "HBROCM_FUSED_ROOT")}
+        os.environ.update(env)
         try:
             eng = hb.Engine(index, 0)
         finally:
-            os.environ.pop("HBROCM_ROW_PAIRS", None)
-            if old is not None:
-                os.environ["HBROCM_ROW_PAIRS"] = old
+            for k, v in saved.items():
+                os.environ.pop(k, None)
+                if v is not None:
+                    os.environ[k] = v
         tr = hb.Trainer(eng, params, y)
         if far_rows:
             eng.load_margins(m0)
@@ -397,13 +401,18 @@ def test_row_carried_logistic_pairs_give_identical_trees(far_rows):
         tr.boost(1)
         after = eng.counters()
         per_row = (after["hist_bytes"] - before["hist_bytes"]) / (after["hist_rows"] - before["hist_rows"])
+        eng.set_profiling(True, "hbr_walk_grad")
         tr.boost(3)
-        runs.append((tr.trees(), tr.margins(), per_row))
-    (ta, ma, ra), (tb, mb, rb) = runs
-    assert rb - ra == 4, (ra, rb)  # the 4-byte word, then the 8-byte pair per row
-    for a, b in zip(ta, tb):
-        for key in a:
-            assert np.array_equal(a[key], b[key]), key
-    assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
+        fused = sum(n for k, (_, _, n) in eng.kernel_stats().items() if k == "hbr_walk_grad_root")
+        eng.set_profiling(False)
+        runs.append((tr.trees(), tr.margins(), per_row, fused))
+    (ta, ma, ra, fa), (tb, mb, rb, fb), (tc, mc, rc, fc) = runs
+    assert fa == 3 and fb == 0 and fc == 0, (fa, fb, fc)
+    assert ra == rb and rc - ra == 4, (ra, rb, rc)  # the 4-byte word, then the 8-byte pair per row
+    for other, mo in ((tb, mb), (tc, mc)):
+        for a, b in zip(ta, other):
+            for key in a:
+                assert np.array_equal(a[key], b[key]), key
+        assert np.array_equal(ma.view(np.uint32), mo.view(np.uint32))
     if far_rows:
         assert np.all(np.abs(ma[far]) > 80)
