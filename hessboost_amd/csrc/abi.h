@@ -95,7 +95,22 @@ struct BinArgs {
     uint32_t total_bins;
     float missing_value;            // the absent marker (NaN: any NaN)
     uint32_t missing_is_nan;
-    uint32_t pad;
+    uint32_t row_mask;              // n_cols <= kMaskedMaxFeatures: the row's missing mask in its last word
+};
+
+// Dense u8 rows of a matrix with missing values (at most kMaskedMaxFeatures
+// features, rows of 32 bytes): a missing cell's byte is 0 and bit f of the
+// row's last word (kMaskWord) marks feature f missing. The histogram kernel
+// skips masked cells; the margin walks send them the split's default way.
+constexpr uint32_t kMaskedMaxFeatures = 28;
+constexpr uint32_t kMaskWord = 7;
+struct RowsFromColsArgs {
+    const uint8_t *cols8;       // [n_cols][n_rows]
+    const uint64_t *missing;    // [n_cols][words] or null
+    uint8_t *rows8;             // [n_rows][32]
+    uint64_t n_rows;
+    uint32_t n_cols;
+    uint32_t words;
 };
 
 // Exclusive scan of the rows' present counts into row_ptr (n_rows + 1):
@@ -324,6 +339,8 @@ struct HistArgs {
     // and h = max(p * (1 - p), min_hess), instead of gpair.
     uint32_t row_pairs;
     float min_hess;
+    uint32_t masked;            // rows carry a missing mask in word kMaskWord (32-byte rows, fg32)
+    uint32_t pad3;
 };
 
 // Each CSR row's first entry of every kCsrGroupBins range (rows' global bins ascend).
@@ -592,9 +609,11 @@ struct LeafArgs {
     uint32_t n_tiles;
 };
 
-// A grown tree routed over the binned rows: node meta is feature | limit
-// << 16 | leaf << 31 (present local bins below `limit` go left), left child
+// A grown tree routed over the binned rows: node meta is feature (bits
+// 0-14) | default_left << 15 | limit << 16 | leaf << 31 (present local bins
+// below `limit` go left, a missing value the default way), left child
 // absolute with the right child at left + 1, leaf values as f32.
+constexpr uint32_t kMetaDefaultLeft = 1u << 15;
 struct WalkArgs {
     const uint32_t *meta;
     const uint32_t *left;
@@ -618,6 +637,10 @@ struct WalkArgs {
     // stays set until the host clears it.
     const QScale *guard;
     uint32_t *poison;
+    // Rows carry a missing mask (kMaskWord): a masked feature sends the row
+    // the way of the node's default (meta bit 15 set: left).
+    uint32_t masked;
+    uint32_t pad;
 };
 
 // A finished tree added to the margins of an evaluation set by raw value:

@@ -67,6 +67,7 @@ void Engine::read_tunables() {
     if (const char *v = std::getenv("HBROCM_HIST_BIN_MAJOR")) hist_bin_major = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_ROW_PAIRS")) row_pairs = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_FUSED_ROOT")) fused_root = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_MASKED_ROWS")) masked_rows = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_CSR_RANGES")) csr_range_table = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_WALK_BLOCKS")) {
@@ -213,8 +214,25 @@ void Engine::upload_index(const hbr_index_desc &d) {
             missing_.resize((uint64_t)words_ * n_cols_);
             missing_.upload(d.missing, (uint64_t)words_ * n_cols_, s);
         }
+        make_masked_rows();
     }
     dev_.sync();
+}
+
+// A matrix with missing values and few features keeps dense u8 rows with a
+// missing mask (kMaskWord) beside its CSR rows: the histogram kernel and the
+// margin walks take them, the partition its columns and bitmap.
+void Engine::make_masked_rows() {
+    if (dense_ || !masked_rows || !cols8_.size() || n_cols_ == 0 || n_cols_ > kMaskedMaxFeatures) return;
+    for (uint32_t f = 0; f < n_cols_; f++)
+        if (fo_[f + 1] - fo_[f] > 256) return;
+    stride_ = 32;
+    rows8_.resize(n_rows_ * stride_);
+    RowsFromColsArgs a{cols8_.get(), missing_.size() ? missing_.get() : nullptr, rows8_.get(), n_rows_, n_cols_,
+                       words_};
+    dev_.launch("hbr_rows_from_cols", dim3(ceil_div(n_rows_, 256)), dim3(256), a);
+    dense_u8_ = true;
+    masked_ = true;
 }
 
 // The index binned on the device: one pass over the matrix writes the local
@@ -295,6 +313,7 @@ void Engine::bin_dense(const DenseSource &src) {
         a.total_bins = total_bins_;
         a.missing_value = src.missing;
         a.missing_is_nan = std::isnan(src.missing) ? 1u : 0u;
+        a.row_mask = masked_rows && n_cols_ <= kMaskedMaxFeatures && stride_ == 32 ? 1u : 0u;
         dev_.launch("hbr_bin_dense", dim3(ceil_div(rows, 256)), dim3(256), a);
         if (!src.on_device) dev_.sync();  // the staging buffer is reused
     }
@@ -325,8 +344,12 @@ void Engine::bin_dense(const DenseSource &src) {
         dev_.sync();
         return;
     }
-    rows8_.release();
-    stride_ = 0;
+    // missing values: CSR rows (and, with few features, the masked dense rows)
+    masked_ = masked_rows && n_cols_ <= kMaskedMaxFeatures && stride_ == 32;
+    if (!masked_) {
+        rows8_.release();
+        stride_ = 0;
+    }
     block_offset.upload(offsets.data(), blocks, s);
     row_ptr_.resize(n_rows_ + 1);
     c.block_offset = block_offset.get();
@@ -344,7 +367,10 @@ void Engine::bin_dense(const DenseSource &src) {
     g.words = words_;
     dev_.launch("hbr_csr_fill", dim3(ceil_div(n_rows_, 256)), dim3(256), g);
     dev_.sync();
-    if (cells <= 2 * entries) {
+    if (masked_) {  // the masked rows route by the columns and bitmap
+        dense_u8_ = true;
+        have_cols_ = true;
+    } else if (cells <= 2 * entries) {
         have_cols_ = true;
     } else {
         cols8_.release();
@@ -371,9 +397,11 @@ void Engine::read_index(uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint6
     if (row_ptr && row_ptr_.size()) row_ptr_.download(row_ptr, n_rows_ + 1, s);
     if (gbins && !dense_ && gbins_.size()) gbins_.download(gbins, entries_, s);
     dev_.sync();
-    // a row's padding bytes read as zero (they may carry logistic pairs)
-    if (rows8 && rows8_.size() && stride_ > n_cols_)
-        for (uint64_t r = 0; r < n_rows_; r++) std::memset(rows8 + r * stride_ + n_cols_, 0, stride_ - n_cols_);
+    // a row's padding bytes read as zero (they may carry logistic pairs);
+    // masked rows keep their missing mask
+    const uint32_t pad_end = masked_ ? 4 * kMaskWord : stride_;
+    if (rows8 && rows8_.size() && pad_end > n_cols_)
+        for (uint64_t r = 0; r < n_rows_; r++) std::memset(rows8 + r * stride_ + n_cols_, 0, pad_end - n_cols_);
 }
 
 // ---- gradients -----------------------------------------------------------------
@@ -506,7 +534,7 @@ static std::vector<uint64_t> expf_table() {
 // from p and y, which fit one word of the padding of a 32-byte row of at
 // most 28 features (the dense kernels' one 32-feature group).
 bool Engine::row_pairs_ok(const hbr_device_loss &loss) const {
-    return row_pairs && loss.kind == HBR_LOSS_LOGISTIC && loss.scale_pos_weight == 1.0f && !has_weights_ &&
+    return row_pairs && !masked_ && loss.kind == HBR_LOSS_LOGISTIC && loss.scale_pos_weight == 1.0f && !has_weights_ &&
            labels_binary_ && dense_u8_ && stride_ == 32 && n_cols_ <= 28 && hist_features_per_group == 32 &&
            outputs_ == 1;
 }
@@ -858,7 +886,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     root_partials_ = 0;  // the partials are reused below
     if (!level_pairs_ && !pairs_staged()) fail(kInvalid, "histograms: no gradients staged");
     if (!dense_u8_ && grow) fail(kInvalid, "histograms: device-counted levels need the dense kernels");
-    const uint32_t fg = hist_features_per_group;
+    const uint32_t fg = masked_ ? 32u : hist_features_per_group;  // masked rows: one group, the mask word
     // dense: feature groups of fg features; CSR: ranges of kCsrGroupBins
     // global bins (every range of every tile is written: no slot zeroing)
     const uint32_t groups = dense_u8_ ? ceil_div(n_cols_, fg) : ceil_div(total_bins_, kCsrGroupBins);
@@ -905,6 +933,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.total_bins = total_bins_;
     a.groups = groups;
     a.row_pairs = row_pairs_live_ && !level_pairs_ && dense_u8_ && stride_ == 32 && fg == 32 ? 1u : 0u;
+    a.masked = masked_ ? 1u : 0u;
     a.min_hess = row_pairs_min_hess_;
     const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"
@@ -1530,6 +1559,7 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     if (next_loss && !staged) fail(kRefused, "walk: gradients need 32-byte rows and depth <= 9");
     hipStream_t s = dev_.stream();
     WalkArgs a{};
+    a.masked = masked_ ? 1u : 0u;
     a.tree = ring_nodes(last_ring_, tree, last_stride_);
     a.counts = &ring_header(last_ring_, tree, last_stride_)->counts;
     a.bins8 = rows8_.get();
@@ -1742,7 +1772,7 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
     if (n == 0 || left.size() != n || value.size() != n) fail(kInvalid, "walk_add: one meta, left, value per node");
     for (size_t i = 0; i < n; i++) {
         if (meta[i] >> 31) continue;
-        if ((meta[i] & 0xffffu) >= n_cols_ || (uint64_t)left[i] + 1 >= n)
+        if ((meta[i] & (kMetaDefaultLeft - 1u)) >= n_cols_ || (uint64_t)left[i] + 1 >= n)
             fail(kInvalid, "walk_add: a split names a missing feature or child");
     }
     if (output >= outputs_) fail(kInvalid, "walk_add: no such output");
@@ -1757,6 +1787,7 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
     char *dev = reinterpret_cast<char *>(d_walk_.get());
     HBR_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, s));
     WalkArgs a{};
+    a.masked = masked_ ? 1u : 0u;
     a.meta = reinterpret_cast<const uint32_t *>(dev);
     a.left = reinterpret_cast<const uint32_t *>(dev + n * 4);
     a.value = reinterpret_cast<const float *>(dev + 2 * n * 4);
@@ -1828,7 +1859,7 @@ bool Engine::build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uin
     if (!level_pairs_ && !pairs_staged()) fail(kInvalid, "build: no gradients staged");
     if (m >= (uint64_t)UINT32_MAX) fail(kInvalid, "build: more than 2^32 - 2 rows in one call");
     if (!scratch || bytes <= kFixedPartialAt) fail(kInvalid, "build: no scratch");
-    const uint32_t fg = hist_features_per_group;
+    const uint32_t fg = masked_ ? 32u : hist_features_per_group;  // masked rows: one group, the mask word
     const uint32_t groups = dense_u8_ ? ceil_div(n_cols_, fg) : ceil_div(total_bins_, kCsrGroupBins);
     const uint64_t per_tile = (uint64_t)groups * (dense_u8_ ? fg * 256ull : (uint64_t)kCsrGroupBins) * sizeof(QBin);
     const uint64_t budget = bytes - kFixedPartialAt;
@@ -1892,6 +1923,7 @@ bool Engine::build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uin
     a.partial = partial;
     a.total_bins = total_bins_;
     a.groups = groups;
+    a.masked = masked_ ? 1u : 0u;
     const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"
                     : fg <= 8  ? "hbr_hist_dense8_fg8"

@@ -398,6 +398,10 @@ private:
     // bounds', known before the pairs are (FinishArgs::bound_*).
     bool bounded_logistic(const hbr_device_loss &loss) const;
     void set_bounds(const hbr_device_loss &loss, FinishArgs &f) const;
+    // Dense u8 rows with a missing mask (kMaskWord) of a matrix with missing
+    // values (dense_ false, dense_u8_ true).
+    bool masked_ = false;
+    void make_masked_rows();
     // Partials of the next root's histogram the fused walk left (0: none);
     // the next device tree's root sums them instead of building its own.
     uint32_t root_partials_ = 0;
@@ -473,6 +477,7 @@ public:
     bool hist_bin_major = true;  // [bin][feature] LDS layout (16 and 32 feature groups)
     bool row_pairs = true;       // unit-weight logistic pairs carried in the rows' padding
     bool fused_root = true;      // the margin walk also sums the next root's histogram (row pairs)
+    bool masked_rows = true;     // dense u8 rows with a missing mask for matrices with missing values
     bool device_grow = true;     // depthwise trees decided on the device where eligible
     bool csr_range_table = true; // CSR histograms read each bin range's entries from a per-row table
     uint32_t walk_blocks_per_cu = 4;  // workgroups per CU of the device-tree margin walk (one resident wave)

@@ -528,7 +528,7 @@ void Trainer::grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_los
                 meta[i] = 1u << 31;
                 value[i] = nd.leaf_value;
             } else {
-                meta[i] = nd.split_feature | (nd.split_limit << 16);
+                meta[i] = nd.split_feature | (nd.default_left ? kMetaDefaultLeft : 0u) | (nd.split_limit << 16);
                 left[i] = (uint32_t)nd.left;
             }
         }

@@ -134,6 +134,9 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
         }
         const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
         const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
+        // a row's missing cells (masked rows: one group of 32 features, the
+        // mask in the last word) add nowhere
+        const uint32_t mask = (FG == 32 && a.masked) ? w[kMaskWord % W] : 0u;
         rotate_bytes<W>(w, rot);
 #pragma unroll
         for (int f = 0; f < FG; f++) {
@@ -142,6 +145,7 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
             // bin-major: a feature past nf adds its (padding) byte into its
             // own column, which is never read back
             const uint32_t at = BIN_MAJOR ? bin * FG + ff : (ff < nf ? ff * kLdsFeature + bin : kDummy + lane);
+            if ((mask >> ff) & 1u) continue;
             atomicAdd(&lg[at], qg);
             atomicAdd(&lh[at], qh);
         }

@@ -52,7 +52,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_bin_dense(BinArgs a) {
     const bool active = i < a.chunk_rows;
     const uint64_t r = a.row0 + i;
     const float *row = a.x + (uint64_t)i * a.n_cols;
-    uint32_t count = 0;
+    uint32_t count = 0, mask = 0;
     for (uint32_t f0 = 0; f0 < a.n_cols; f0 += 4) {
         uint32_t word = 0;
 #pragma unroll
@@ -69,9 +69,12 @@ extern "C" __global__ __launch_bounds__(256) void hbr_bin_dense(BinArgs a) {
             const uint64_t miss = __ballot(active && absent);
             if (lane_id() == 0 && r < a.n_rows) a.missing[(uint64_t)f * a.words + (r >> 6)] = miss;
             count += active && !absent ? 1u : 0u;
+            mask |= absent ? 1u << f : 0u;
         }
         if (active && a.rows8) *reinterpret_cast<uint32_t *>(a.rows8 + r * a.stride + f0) = word;
     }
+    if (active && a.rows8 && a.row_mask)  // kept only when some cell is missing (else the word is padding)
+        *reinterpret_cast<uint32_t *>(a.rows8 + r * a.stride + 4 * kMaskWord) = mask;
     if (active) a.row_count[r] = count;
 }
 

@@ -264,7 +264,7 @@ __device__ __forceinline__ uint32_t node_meta(const WalkArgs &a, uint32_t i, uin
     }
     const GrowTreeNode t = a.tree[i];
     *left = t.left < 0 ? 0u : (uint32_t)t.left;
-    return t.left < 0 ? 1u << 31 : t.feature | (t.limit << 16);
+    return t.left < 0 ? 1u << 31 : t.feature | (t.default_left ? kMetaDefaultLeft : 0u) | (t.limit << 16);
 }
 
 // A guarded walk that must not happen: the tree's gradients (any of its
@@ -284,11 +284,13 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves(WalkArgs a) {
     const uint32_t n_nodes = walk_nodes(a);
     for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += gridDim.x * blockDim.x) {
         const uint8_t *b = a.bins8 + (size_t)r * a.stride;
+        const uint32_t mask = a.masked ? *reinterpret_cast<const uint32_t *>(b + 4 * kMaskWord) : 0u;
         uint32_t nid = 0, left;
         uint32_t meta = node_meta(a, 0, &left);
         for (uint32_t step = 0; step < n_nodes && !(meta >> 31); step++) {
-            const uint32_t f = meta & 0xffffu, lim = (meta >> 16) & 0x7fffu;
-            nid = left + ((uint32_t)b[f] < lim ? 0u : 1u);
+            const uint32_t f = meta & (kMetaDefaultLeft - 1u), lim = (meta >> 16) & 0x7fffu;
+            const bool right = ((mask >> f) & 1u) ? !(meta & kMetaDefaultLeft) : (uint32_t)b[f] >= lim;
+            nid = left + (right ? 1u : 0u);
             nid = nid < n_nodes ? nid : 0u;
             meta = node_meta(a, nid, &left);
         }
@@ -327,7 +329,7 @@ __device__ __forceinline__ uint32_t load_walk_nodes(const WalkArgs &a, uint2 *s_
         float value;
         if (a.tree) {
             const GrowTreeNode t = a.tree[i];
-            meta = t.left < 0 ? 1u << 31 : t.feature | (t.limit << 16);
+            meta = t.left < 0 ? 1u << 31 : t.feature | (t.default_left ? kMetaDefaultLeft : 0u) | (t.limit << 16);
             left = t.left < 0 ? 0u : (uint32_t)t.left;
             value = t.value;
         } else {
@@ -342,12 +344,15 @@ __device__ __forceinline__ uint32_t load_walk_nodes(const WalkArgs &a, uint2 *s_
 }
 
 // The leaf a row reaches (n_nodes steps at most; -1 when no leaf is reached).
-__device__ __forceinline__ int32_t walk_row(const uint2 *s_node, uint32_t n_nodes, const uint32_t (&w)[8]) {
+// mask: the row's missing features (masked rows), 0 otherwise.
+__device__ __forceinline__ int32_t walk_row(const uint2 *s_node, uint32_t n_nodes, const uint32_t (&w)[8],
+                                            uint32_t mask = 0u) {
     uint32_t nid = 0;
     uint2 nd = s_node[0];
     for (uint32_t step = 0; step < n_nodes && !(nd.x >> 31); step++) {
         const uint32_t f = nd.x & 31u, lim = (nd.x >> 16) & 0x7fffu;
-        nid = nd.y + (pick_byte(w, f) < lim ? 0u : 1u);
+        const bool right = ((mask >> f) & 1u) ? !(nd.x & kMetaDefaultLeft) : pick_byte(w, f) >= lim;
+        nid = nd.y + (right ? 1u : 0u);
         nid = nid < n_nodes ? nid : 0u;
         nd = s_node[nid];
     }
@@ -389,7 +394,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves32(WalkArgs a) 
         for (uint32_t k = 0; k < kWalkRows; k++) {
             const uint32_t r = r0 + k * stride;
             if (r >= a.n) continue;
-            const int32_t leaf = walk_row(s_node, n_nodes, w[k]);
+            const int32_t leaf = walk_row(s_node, n_nodes, w[k], a.masked ? w[k][kMaskWord] : 0u);
             if (leaf >= 0) a.margins[(size_t)r * a.m_stride + a.output] = m[k] + s_value[leaf];
         }
     }
@@ -433,7 +438,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
             const uint32_t r = r0 + k * stride;
             const bool active = r < a.n;
             if (active) {
-                const int32_t leaf = walk_row(s_node, n_nodes, w[k]);
+                const int32_t leaf = walk_row(s_node, n_nodes, w[k], a.masked ? w[k][kMaskWord] : 0u);
                 if (leaf >= 0) {
                     m[k] = m[k] + s_value[leaf];
                     a.margins[(size_t)r * a.m_stride + a.output] = m[k];
@@ -501,7 +506,7 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradAr
             const uint32_t r = r0 + k * stride;
             const bool active = r < a.n;
             if (active) {
-                const int32_t leaf = walk_row(s_node, n_nodes, w[k]);
+                const int32_t leaf = walk_row(s_node, n_nodes, w[k], a.masked ? w[k][kMaskWord] : 0u);
                 if (leaf >= 0) {
                     m[k] = m[k] + s_value[leaf];
                     a.margins[(size_t)r * a.m_stride + a.output] = m[k];
@@ -583,4 +588,22 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_root_fixup(RootFixupArgs 
         a.node->pad[0] = 0;
         a.node->pad[1] = 0;
     }
+}
+
+// Masked dense rows from an index's local u8 columns and missing bitmap (a
+// host-built index of a matrix with missing values): one thread per row,
+// its bins in bytes 0..n_cols-1 and its missing mask in word kMaskWord.
+extern "C" __global__ __launch_bounds__(256) void hbr_rows_from_cols(RowsFromColsArgs a) {
+    const uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= a.n_rows) return;
+    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t mask = 0;
+    for (uint32_t f = 0; f < a.n_cols; f++) {
+        w[f >> 2] |= (uint32_t)a.cols8[(uint64_t)f * a.n_rows + r] << ((f & 3u) * 8u);
+        if (a.missing) mask |= (uint32_t)((a.missing[(uint64_t)f * a.words + (r >> 6)] >> (r & 63u)) & 1ull) << f;
+    }
+    w[kMaskWord] = mask;
+    uint4 *dst = reinterpret_cast<uint4 *>(a.rows8 + r * 32u);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }

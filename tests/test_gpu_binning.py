@@ -96,3 +96,26 @@ def test_features_wider_than_256_bins_are_refused():
     cuts = hb.DMatrix(x).cuts(1024)
     with pytest.raises(hb.HbrError):
         hb.Engine.from_dense(x, cuts, 0)
+
+
+@pytest.mark.parametrize("on_device", [False, True])
+def test_few_features_with_missing_values_keep_masked_dense_rows(on_device):
+    """A matrix of at most 28 features with missing cells keeps, beside the
+    CSR rows, columns and bitmap the host builds, dense u8 rows of 32 bytes
+    whose last word marks the row's missing features; the device-binned rows
+    and those the engine makes from a host index's columns agree byte for
+    byte, and the masks equal the bitmap."""
+    rng = np.random.default_rng(26)
+    n, f = 20_011, 28
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    x[rng.random(x.shape) < 0.03] = np.nan
+    host, dev = _layouts(x, 256, on_device=on_device)
+    assert dev["dense"] == 0 and dev["dense_u8"] == 1 and dev["stride"] == 32
+    _same(host, dev)
+    rows = dev["rows8"].reshape(n, 32)
+    mask = rows[:, 28:32].copy().view(np.uint32).reshape(-1)
+    want = np.zeros(n, np.uint32)
+    for j in range(f):
+        want |= np.isnan(x[:, j]).astype(np.uint32) << np.uint32(j)
+    assert np.array_equal(mask, want)
+    assert np.all(rows[:, :28][np.isnan(x)] == 0)  # a missing cell's byte is 0
