@@ -937,6 +937,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.min_hess = row_pairs_min_hess_;
     const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"
+                    : masked_  ? "hbr_hist_dense8_fg32_bm_masked"
                     : fg <= 8  ? "hbr_hist_dense8_fg8"
                     : fg <= 16 ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
                                : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");
@@ -1926,6 +1927,7 @@ bool Engine::build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uin
     a.masked = masked_ ? 1u : 0u;
     const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"
+                    : masked_  ? "hbr_hist_dense8_fg32_bm_masked"
                     : fg <= 8  ? "hbr_hist_dense8_fg8"
                     : fg <= 16 ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
                                : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");

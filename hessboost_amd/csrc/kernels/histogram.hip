@@ -93,7 +93,7 @@ __device__ __forceinline__ void load_bins(const uint8_t *p, uint32_t (&w)[FG / 4
 // of each 16-lane group 16 different features: their atomics never share a
 // bank, whatever the bins. Otherwise [feature][257] (bins padded), where
 // the banks follow the data, and features past nf go to per-lane dummies.
-template <int FG, bool BIN_MAJOR>
+template <int FG, bool BIN_MAJOR, bool MASKED = false>
 __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
     constexpr int W = FG / 4;
     constexpr uint32_t kWords = BIN_MAJOR ? FG * 256 : FG * kLdsFeature + kWave;
@@ -136,7 +136,7 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
         const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
         // a row's missing cells (masked rows: one group of 32 features, the
         // mask in the last word) add nowhere
-        const uint32_t mask = (FG == 32 && a.masked) ? w[kMaskWord % W] : 0u;
+        const uint32_t mask = MASKED ? w[kMaskWord % W] : 0u;
         rotate_bytes<W>(w, rot);
 #pragma unroll
         for (int f = 0; f < FG; f++) {
@@ -145,7 +145,7 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
             // bin-major: a feature past nf adds its (padding) byte into its
             // own column, which is never read back
             const uint32_t at = BIN_MAJOR ? bin * FG + ff : (ff < nf ? ff * kLdsFeature + bin : kDummy + lane);
-            if ((mask >> ff) & 1u) continue;
+            if (MASKED && ((mask >> ff) & 1u)) continue;
             atomicAdd(&lg[at], qg);
             atomicAdd(&lh[at], qh);
         }
@@ -369,6 +369,10 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16(HistArgs
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32(HistArgs a) { hist_dense8<32, false>(a); }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16_bm(HistArgs a) { hist_dense8<16, true>(a); }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm(HistArgs a) { hist_dense8<32, true>(a); }
+// Masked rows (a missing mask in word kMaskWord): one group of 32 features.
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm_masked(HistArgs a) {
+    hist_dense8<32, true, true>(a);
+}
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_csr(HistArgs a) { hist_csr(a); }
 
 // Nodes cut into several tiles: the slot is the sum of the tiles' partials.

@@ -506,7 +506,8 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradAr
             const uint32_t r = r0 + k * stride;
             const bool active = r < a.n;
             if (active) {
-                const int32_t leaf = walk_row(s_node, n_nodes, w[k], a.masked ? w[k][kMaskWord] : 0u);
+                // rows carrying pairs hold no missing mask (word 7 is the pair)
+                const int32_t leaf = walk_row(s_node, n_nodes, w[k]);
                 if (leaf >= 0) {
                     m[k] = m[k] + s_value[leaf];
                     a.margins[(size_t)r * a.m_stride + a.output] = m[k];
