@@ -159,7 +159,8 @@ void Forest::build_pairs(const hbr_forest_desc &fd) {
         }
         depth = std::max(depth, tree_depth[t]);
     }
-    depth += depth & 1u;
+    // at least one record per tree: the walk reads every root record
+    depth = std::max(depth + (depth & 1u), 2u);
     const uint32_t levels = depth / 2;
     const uint64_t per_tree = ((1ull << depth) - 1) / 3, leaves = 1ull << depth;
     // the complete trees may not outgrow the trees too far

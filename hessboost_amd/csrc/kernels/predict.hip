@@ -524,10 +524,23 @@ __device__ __forceinline__ uint32_t pair_test(const float *xr, uint32_t s8, uint
     return x < __uint_as_float(t) ? 1u : 0u;
 }
 
+// A load every lane makes from the same address, through the scalar data
+// cache (s_load) instead of the texture path: the pointer is taken into the
+// constant address space, whose uniform loads the compiler turns into scalar
+// loads. Only for data no kernel writes while the walk runs.
+template <typename T>
+__device__ __forceinline__ T uniform_load(const T *p, size_t i) {
+    typedef const __attribute__((address_space(4))) T constant_t;
+    return ((constant_t *)p)[i];
+}
+
 // Complete trees walked two levels per record (PredictArgs::pairs): rows
 // resident in LDS as in hbr_predict_mirror (one 64-row block per one-wave
 // workgroup, slot 0 NaN), CH trees in flight per lane; every record load
-// serves two levels and the last load reads only the leaf's value.
+// serves two levels and the last load reads only the leaf's value. The root
+// record and the tree's weight are the same for every lane: scalar loads,
+// so a tree costs the texture path one load per level below the root's two
+// and one for the leaf.
 template <bool MISSING_NAN, int CH>
 __device__ __forceinline__ void predict_pairs(const PredictArgs &a) {
     extern __shared__ float s_rows[];  // (n_cols + 1) * kPredPitch
@@ -557,9 +570,17 @@ __device__ __forceinline__ void predict_pairs(const PredictArgs &a) {
         for (uint32_t t0 = 0; t0 < a.n_trees; t0 += CH) {
             uint32_t pos[CH];
 #pragma unroll
-            for (int k = 0; k < CH; k++) pos[k] = 0;
-            uint32_t base = 0;  // first record of the level
-            for (uint32_t l = 0; l < levels; l++) {
+            for (int k = 0; k < CH; k++) {
+                const uint32_t t = min(t0 + (uint32_t)k, a.n_trees - 1);
+                const PairRecord rec = uniform_load(a.pairs, (size_t)t * per_tree);
+                const uint32_t s = rec.s;
+                const uint32_t first = pair_test(xr, s, rec.t_node);
+                const uint32_t t_c = first ? rec.t_second : rec.t_first;
+                const uint32_t s_c = first ? s >> 16 : s >> 8;
+                pos[k] = 2 * first + pair_test(xr, s_c, t_c);
+            }
+            uint32_t base = 1;  // first record of the level
+            for (uint32_t l = 1; l < levels; l++) {
                 PairRecord rec[CH];
 #pragma unroll
                 for (int k = 0; k < CH; k++) {
@@ -588,7 +609,7 @@ __device__ __forceinline__ void predict_pairs(const PredictArgs &a) {
                 const uint32_t t = t0 + (uint32_t)k;
                 if (t < a.n_trees) {
                     if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.pair_orig[(size_t)t * leaves + pos[k]];
-                    const float contrib = a.tree_weight[t] * __uint_as_float(leaf[k]);
+                    const float contrib = uniform_load(a.tree_weight, t) * __uint_as_float(leaf[k]);
                     if (a.n_outputs == 1) {
                         acc = acc + contrib;
                     } else {
