@@ -355,9 +355,11 @@ def main():
         wbytes = x.shape[0] * (32 + 32 + 4 + 4 + 4)
         wach = wbytes / (wms * 1e-3) / 1e9
         watom = x.shape[0] * 32 * 2 / (wms * 1e-3) / 1e12
+        wtraffic, _, wtraffic_src = measured_traffic("hbr_walk_grad_root")
         walk_root = {"kernel": "hbr_walk_grad_root", "bound": "hbm", "achieved": round(wach, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(wach / HBM_PEAK_GBS, 4),
                      "avg_launch_ms": round(wms, 4), "algorithmic_bytes_per_launch": wbytes,
+                     "traffic": wtraffic, "traffic_source": wtraffic_src,
                      "lds_atomics": {"achieved": round(watom, 3), "peak": LDS_ATOMIC_PEAK_T, "unit": "T lane-ops/s",
                                      "frac": round(watom / LDS_ATOMIC_PEAK_T, 4)}}
     n_trees = len(trainer.trees())
@@ -479,9 +481,10 @@ def main():
         pach = pbytes / launch_s / 1e9 if pms > 0 else 0.0
         node_steps = n * args.predict_trees * 8
         # wave-wide node loads of the walk that ran: the pair walk loads one
-        # record per two levels and the leaf's value (depth 8: 5 per tree),
-        # the mirror walk one node per level and the leaf (9)
-        per_tree = 5 if any("pairs" in k for k in pkern) else 9
+        # record per two levels below the root's (a scalar load) and the
+        # leaf's value (depth 8: 4 per tree), the mirror walk one node per
+        # level and the leaf (9)
+        per_tree = 4 if any("pairs" in k for k in pkern) else 9
         loads = (n + 63) // 64 * args.predict_trees * per_tree
         ptraffic, _, ptraffic_src = measured_traffic(pkern[0] if pkern else "hbr_predict")
         log(f"predict: {mrows:.1f} Mrows/s; kernel {launch_s * 1e3:.2f} ms per launch, {pach:.0f} GB/s")
