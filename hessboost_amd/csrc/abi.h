@@ -78,6 +78,10 @@ struct EncodeArgs {
 // dense f32 matrix to feature-local u8 bins (features of at most 256 bins),
 // the missing bitmap and each row's count of present values. One thread per
 // row; a chunk starts at a multiple of 64 rows.
+// Cut values the binning kernels hold in LDS (more: read from memory by
+// hbr_bin_dense; hbr_bin_dense32 needs them in LDS).
+constexpr uint32_t kBinLdsCuts = 12288;
+
 struct BinArgs {
     const float *x;                 // the chunk's rows, row-major [chunk_rows][n_cols]
     const float *cut_values;        // total_bins

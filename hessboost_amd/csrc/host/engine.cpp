@@ -68,6 +68,7 @@ void Engine::read_tunables() {
     if (const char *v = std::getenv("HBROCM_ROW_PAIRS")) row_pairs = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_FUSED_ROOT")) fused_root = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_MASKED_ROWS")) masked_rows = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_BIN_ROWS_IN_REGISTERS")) bin_rows_in_registers = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_CSR_RANGES")) csr_range_table = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_WALK_BLOCKS")) {
@@ -280,7 +281,13 @@ void Engine::bin_dense(const DenseSource &src) {
     words_ = (uint32_t)((n_rows_ + 63) / 64);
     stride_ = (n_cols_ + 31) / 32 * 32;
     rows8_.resize(n_rows_ * stride_);
-    rows8_.zero(s);
+    // up to 32 features: rows read with 16-byte loads (into registers, or
+    // staged through LDS when n_cols is not a multiple of 4), every 32-byte
+    // row written whole
+    const bool wide32 = stride_ == 32 && total_bins_ <= kBinLdsCuts &&
+                        (!src.on_device || reinterpret_cast<uintptr_t>(src.x) % 16 == 0);
+    const bool in_regs = wide32 && n_cols_ % 4 == 0 && bin_rows_in_registers;
+    if (!wide32) rows8_.zero(s);
     cols8_.resize(n_rows_ * n_cols_);
     missing_.resize((uint64_t)words_ * n_cols_);
     DBuf<uint32_t> count(n_rows_);
@@ -314,7 +321,14 @@ void Engine::bin_dense(const DenseSource &src) {
         a.missing_value = src.missing;
         a.missing_is_nan = std::isnan(src.missing) ? 1u : 0u;
         a.row_mask = masked_rows && n_cols_ <= kMaskedMaxFeatures && stride_ == 32 ? 1u : 0u;
-        dev_.launch("hbr_bin_dense", dim3(ceil_div(rows, 256)), dim3(256), a);
+        if (in_regs)
+            dev_.launch("hbr_bin_dense32_rows", dim3(ceil_div(rows, 256)), dim3(256), a,
+                        (uint32_t)(total_bins_ * sizeof(float)));
+        else if (wide32)
+            dev_.launch("hbr_bin_dense32", dim3(ceil_div(rows, 256)), dim3(256), a,
+                        (uint32_t)((4 * 64 * n_cols_ + total_bins_) * sizeof(float)));
+        else
+            dev_.launch("hbr_bin_dense", dim3(ceil_div(rows, 256)), dim3(256), a);
         if (!src.on_device) dev_.sync();  // the staging buffer is reused
     }
     // the present counts: totals per block, their offsets on the host, row_ptr

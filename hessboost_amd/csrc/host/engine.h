@@ -478,6 +478,7 @@ public:
     bool row_pairs = true;       // unit-weight logistic pairs carried in the rows' padding
     bool fused_root = true;      // the margin walk also sums the next root's histogram (row pairs)
     bool masked_rows = true;     // dense u8 rows with a missing mask for matrices with missing values
+    bool bin_rows_in_registers = true;  // device binning of <= 32 features: rows into registers, else staged in LDS
     bool device_grow = true;     // depthwise trees decided on the device where eligible
     bool csr_range_table = true; // CSR histograms read each bin range's entries from a per-row table
     uint32_t walk_blocks_per_cu = 4;  // workgroups per CU of the device-tree margin walk (one resident wave)

@@ -83,6 +83,22 @@ def test_missing_marker_other_than_nan():
     _same(host, dev)
 
 
+@pytest.mark.parametrize("f", [1, 27, 32])
+@pytest.mark.parametrize("on_device", [False, True])
+def test_rows_of_up_to_32_features_staged_through_lds(f, on_device):
+    """hbr_bin_dense32: each wave's rows copied into LDS with 16-byte loads,
+    every 32-byte row written whole; a ragged last wave and workgroup, every
+    byte of the rows (padding included) against the host index."""
+    rng = np.random.default_rng(30 + f)
+    x = rng.standard_normal((20_037, f)).astype(np.float32)
+    x[:, 0] = np.round(x[:, 0] * 2)  # few distinct values: cells on the cut points
+    x[5, :] = np.inf
+    x[6, :] = -np.inf
+    host, dev = _layouts(x, 256, on_device=on_device)
+    assert dev["dense_u8"] == 1
+    _same(host, dev)
+
+
 def test_rows_already_on_the_device():
     rng = np.random.default_rng(24)
     x = rng.standard_normal((12_345, 28)).astype(np.float32)
