@@ -1044,7 +1044,7 @@ void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit 
     }
     dev_.launch("hbr_scan_features", dim3(ceil_div(pairs, 4)), dim3(256), a);
     if (n_cat_) dev_.launch("hbr_scan_categorical", dim3(n * n_cat_), dim3(64), a);
-    dev_.launch("hbr_scan_merge", dim3(n), dim3(64), a);
+    dev_.launch("hbr_scan_merge", dim3(n), dim3(256), a);
 }
 
 // Scan nodes given on the host: upload, scan, copy the winners into `out`

@@ -255,19 +255,30 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
     scan_feature(a, pair / a.n_features, pair % a.n_features, a.per_feature + pair);
 }
 
-// One wave: the feature-order merge of a node's per-feature winners
-// (`per_node`, n_features records). A candidate must beat the empty split
-// (loss 0); equal losses keep the lower feature.
+// The feature-order merge of a node's per-feature winners (`per_node`,
+// n_features records), by one workgroup of kMergeThreads: thread t takes
+// features t, t + kMergeThreads, ... (ascending, so within a thread only a
+// strictly larger loss replaces), then the threads' bests are reduced, higher
+// loss first, the lower feature on equal losses. A candidate must beat the
+// empty split (loss 0). Wide indexes (thousands of features) need the
+// threads; a node of 28 features leaves most of them idle.
+constexpr uint32_t kMergeThreads = 256;
+
+__device__ __forceinline__ bool merge_better(float ol, uint32_t of, float bl, uint32_t bf) {
+    return of != 0xffffffffu && (bf == 0xffffffffu || ol > bl || (ol == bl && of < bf));
+}
+
 __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, const ScanBest *per_node) {
-    const uint32_t lane = lane_id();
+    __shared__ float s_loss[kMergeThreads / kWave];
+    __shared__ uint32_t s_feat[kMergeThreads / kWave], s_nan[kMergeThreads / kWave];
+    const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
     float bl = 0.0f;
     uint32_t bf = 0xffffffffu;
     uint32_t nan_flag = 0;
-    for (uint32_t f = lane; f < a.n_features; f += kWave) {
+    for (uint32_t f = threadIdx.x; f < a.n_features; f += kMergeThreads) {
         const ScanBest c = per_node[f];
         nan_flag |= c.flags & kScanReplay;
         if (c.index == 0xffffffffu) continue;
-        // features ascend within a lane: only a strictly larger loss replaces
         if (c.loss > 0.0f && (bf == 0xffffffffu || c.loss > bl)) {
             bl = c.loss;
             bf = f;
@@ -278,7 +289,27 @@ __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, con
         const float ol = __shfl_xor(bl, d, kWave);
         const uint32_t of = (uint32_t)__shfl_xor((int)bf, d, kWave);
         nan_flag |= (uint32_t)__shfl_xor((int)nan_flag, d, kWave);
-        if (of != 0xffffffffu && (bf == 0xffffffffu || ol > bl || (ol == bl && of < bf))) {
+        if (merge_better(ol, of, bl, bf)) {
+            bl = ol;
+            bf = of;
+        }
+    }
+    if (lane == 0) {
+        s_loss[wave] = bl;
+        s_feat[wave] = bf;
+        s_nan[wave] = nan_flag;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    bl = lane < kMergeThreads / kWave ? s_loss[lane] : 0.0f;
+    bf = lane < kMergeThreads / kWave ? s_feat[lane] : 0xffffffffu;
+    nan_flag = lane < kMergeThreads / kWave ? s_nan[lane] : 0u;
+#pragma unroll
+    for (int d = 2; d >= 1; d >>= 1) {  // kMergeThreads / kWave = 4 candidates
+        const float ol = __shfl_xor(bl, d, kWave);
+        const uint32_t of = (uint32_t)__shfl_xor((int)bf, d, kWave);
+        nan_flag |= (uint32_t)__shfl_xor((int)nan_flag, d, kWave);
+        if (merge_better(ol, of, bl, bf)) {
             bl = ol;
             bf = of;
         }
@@ -306,9 +337,9 @@ __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, con
     }
 }
 
-extern "C" __global__ __launch_bounds__(64) void hbr_scan_merge(ScanArgs a) {
+extern "C" __global__ __launch_bounds__(kMergeThreads) void hbr_scan_merge(ScanArgs a) {
     const uint32_t node = blockIdx.x;
-    if (node >= scan_nodes(a)) return;
+    if (node >= scan_nodes(a)) return;  // uniform per workgroup
     merge_node(a, node, a.per_feature + (size_t)node * a.n_features);
 }
 
