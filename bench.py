@@ -223,7 +223,7 @@ def other_workload(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--rows", type=int, default=10_500_000)
     ap.add_argument("--predict-rows", type=int, default=10_000_000)
