@@ -368,6 +368,26 @@ def test_logistic_gradient_vector_and_scalar_paths():
         assert np.all(h >= np.float32(1e-16))
 
 
+def test_logistic_dispatch_is_close_to_scalar_as_the_reference_tests_it():
+    """The reference's own pin of its vector logistic path
+    (simd/tests.rs:53-75, logistic_gradient_dispatch_is_close_to_scalar):
+    4,103 sawtooth margins over [-20, 20], labels i % 2, no weights and
+    sawtooth weights, scale_pos_weight 1.5, min_hess 1e-16; every pair within
+    5e-7 (g) and 3e-7 (h) of the scalar rows (the C library's expf)."""
+    n = 4_103
+    preds = _sawtooth(n, 4_103, -20.0, 40.0 / 4_102.0)
+    labels = (np.arange(n) % 2).astype(np.float32)
+    for weights in (None, _sawtooth(n, 13, 0.5, 0.125)):
+        g = O.gradient(O.OBJ_LOGISTIC, preds, labels, weights, scale_pos_weight=1.5)
+        w = np.ones(n, np.float32) if weights is None else weights
+        w = np.where(labels == 1.0, w * np.float32(1.5), w).astype(np.float32)
+        p = np.array([O.lib().or_sigmoid(float(m)) for m in preds], np.float32)
+        eg = ((p - labels) * w).astype(np.float32)
+        eh = (np.maximum(p * (np.float32(1) - p), np.float32(1e-16)) * w).astype(np.float32)
+        assert np.all(np.abs(g[:, 0] - eg) <= 5.0e-7)
+        assert np.all(np.abs(g[:, 1] - eh) <= 3.0e-7)
+
+
 def test_softmax_gradient_closed_form():
     """objective/multiclass.rs:124-139: zero margins give p = 1/3, g = p - 1 on
     the label, h = 2p(1-p)."""
