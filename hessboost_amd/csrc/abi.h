@@ -644,8 +644,16 @@ struct WalkArgs {
     // Rows carry a missing mask (kMaskWord): a masked feature sends the row
     // the way of the node's default (meta bit 15 set: left).
     uint32_t masked;
+    // hbr_walk_leaves_batch: trees walked in one pass over the rows; tree c's
+    // records and counts sit c * tree_bytes after tree 0's, and its leaves
+    // go to output + c.
+    uint32_t n_trees;
+    uint32_t tree_bytes;
     uint32_t pad;
 };
+// Node tables of all the trees of one batched walk, in LDS.
+constexpr uint32_t kBatchWalkNodes = 2048;
+constexpr uint32_t kBatchWalkTrees = 64;
 
 // A finished tree added to the margins of an evaluation set by raw value:
 // a present value goes left iff value < cut_values[bin] (-FLT_MAX for bin

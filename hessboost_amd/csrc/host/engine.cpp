@@ -68,6 +68,7 @@ void Engine::read_tunables() {
     if (const char *v = std::getenv("HBROCM_ROW_PAIRS")) row_pairs = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_FUSED_ROOT")) fused_root = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_MASKED_ROWS")) masked_rows = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_BATCH_WALK")) batch_walk = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_BIN_ROWS_IN_REGISTERS")) bin_rows_in_registers = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_CSR_RANGES")) csr_range_table = std::strtol(v, nullptr, 10) != 0;
@@ -1563,6 +1564,43 @@ bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vecto
     if (finish_device_tree(t, nodes, nullptr) == kTreeOk) return true;
     drain();
     return false;
+}
+
+bool Engine::walk_device_trees(uint32_t first_output, uint32_t n_trees, uint32_t guard_first, uint32_t guard_n) {
+    // the batch's node tables must fit the kernel's LDS whatever the trees
+    const uint64_t most = (2ull << std::min<uint32_t>(last_depth_, 20u)) - 1;
+    if (!batch_walk || !dense_u8_ || (stride_ != 32 && stride_ != 64) || n_trees < 2 ||
+        n_trees > kBatchWalkTrees || n_trees * most > kBatchWalkNodes || first_output + n_trees > outputs_)
+        return false;
+    if (guard_n && (!softmax_staged() || guard_first + guard_n > class_outputs_))
+        fail(kInvalid, "walk: no softmax class scales to guard by");
+    hipStream_t s = dev_.stream();
+    if (!poison_.size() && guard_n) {
+        poison_.resize(1);
+        guard_scale_.resize(1);
+        HBR_HIP(hipMemsetAsync(poison_.get(), 0, sizeof(uint32_t), s));
+    }
+    WalkArgs a{};
+    a.masked = masked_ ? 1u : 0u;
+    a.tree = ring_nodes(last_ring_, 0, last_stride_);
+    a.counts = &ring_header(last_ring_, 0, last_stride_)->counts;
+    a.tree_bytes = (uint32_t)last_stride_;
+    a.n_trees = n_trees;
+    a.bins8 = rows8_.get();
+    a.margins = margins_.get();
+    a.stride = stride_;
+    a.n = (uint32_t)n_rows_;
+    a.m_stride = outputs_;
+    a.output = first_output;
+    if (guard_n) {
+        a.guard = class_scales_.get() + guard_first;
+        a.guard_n = guard_n;
+        a.poison = poison_.get();
+    }
+    const uint32_t blocks =
+        std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)), (uint32_t)dev_.cu_count() * walk_blocks_per_cu);
+    dev_.launch(stride_ == 32 ? "hbr_walk_leaves_batch32" : "hbr_walk_leaves_batch64", dim3(blocks), dim3(256), a);
+    return true;
 }
 
 void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree, uint32_t guard_first,

@@ -222,6 +222,11 @@ public:
     }
     // The walk alone (no gradients): any dense u8 index, any output.
     bool can_route_device_tree(uint64_t max_depth) const { return can_grow_device(max_depth); }
+    // The trees of the last queued batch (its trees 0..n_trees-1) added to
+    // margins outputs first_output.. in one pass over the rows, guarded as
+    // walk_device_tree; false (nothing queued) when the batch does not fit
+    // the kernel, for the caller to walk the trees one at a time.
+    bool walk_device_trees(uint32_t first_output, uint32_t n_trees, uint32_t guard_first, uint32_t guard_n);
     void walk_device_tree(uint32_t output, const hbr_device_loss *next_loss, uint32_t tree = 0,
                           uint32_t guard_first = 0, uint32_t guard_n = 0);
 
@@ -478,6 +483,7 @@ public:
     bool row_pairs = true;       // unit-weight logistic pairs carried in the rows' padding
     bool fused_root = true;      // the margin walk also sums the next root's histogram (row pairs)
     bool masked_rows = true;     // dense u8 rows with a missing mask for matrices with missing values
+    bool batch_walk = true;  // a softmax round's class trees added to the margins in one walk
     bool bin_rows_in_registers = true;  // device binning of <= 32 features: rows into registers, else staged in LDS
     bool device_grow = true;     // depthwise trees decided on the device where eligible
     bool csr_range_table = true; // CSR histograms read each bin range's entries from a per-row table

@@ -629,8 +629,9 @@ void Trainer::boost_softmax_batched(uint64_t rounds) {
             e_.softmax_gradients_async(kMinHess);
             inflight.push_back(b.queue_classes());
             // guarded by every class's scale: the host keeps or drops a round whole
+            const bool batched_walk = e_.walk_device_trees(0, k_, 0, k_);
             for (uint32_t c = 0; c < k_; c++) {
-                e_.walk_device_tree(c, nullptr, c, 0, k_);
+                if (!batched_walk) e_.walk_device_tree(c, nullptr, c, 0, k_);
                 e_.walk_evals_device(c, c, true);
             }
             queued++;

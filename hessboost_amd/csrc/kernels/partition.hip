@@ -322,6 +322,95 @@ __device__ __forceinline__ uint32_t pick_byte(const uint32_t (&w)[8], uint32_t f
     return (c >> ((f & 3u) * 8u)) & 0xffu;
 }
 
+// Byte f (f < 64) of a 64-byte row held in sixteen registers.
+__device__ __forceinline__ uint32_t pick_byte16(const uint32_t (&w)[16], uint32_t f) {
+    const uint32_t m8 = (f & 32u) ? ~0u : 0u;
+    uint32_t h[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = w[i] ^ ((w[i] ^ w[i + 8]) & m8);
+    return pick_byte(h, f & 31u);
+}
+
+// The class trees of a softmax round added to their margins in one pass
+// over the rows (32- or 64-byte rows, W words): every tree's node table in
+// LDS, each row's bins read once into registers, then walked through tree
+// 0, 1, ..., each leaf added to its own margin (output + c) with the same
+// single f32 add as hbr_walk_leaves, so the margins are those of one walk
+// per tree. The host checks that the tables fit (kBatchWalkNodes nodes,
+// kBatchWalkTrees trees).
+template <int W>
+__device__ __forceinline__ void walk_leaves_batch(const WalkArgs &a) {
+    __shared__ uint2 s_node[kBatchWalkNodes];
+    __shared__ float s_value[kBatchWalkNodes];
+    __shared__ uint32_t s_first[kBatchWalkTrees + 1];
+    if (walk_skipped(a)) return;
+    const uint32_t K = a.n_trees;
+    if (threadIdx.x == 0) {
+        uint32_t total = 0;
+        for (uint32_t c = 0; c < K; c++) {
+            s_first[c] = total;
+            const GrowCounts *cc = reinterpret_cast<const GrowCounts *>(
+                reinterpret_cast<const char *>(a.counts) + (size_t)c * a.tree_bytes);
+            total += min(cc->n_nodes, kBatchWalkNodes - total);
+        }
+        s_first[K] = total;
+    }
+    __syncthreads();
+    for (uint32_t c = 0; c < K; c++) {
+        const GrowTreeNode *tc = reinterpret_cast<const GrowTreeNode *>(
+            reinterpret_cast<const char *>(a.tree) + (size_t)c * a.tree_bytes);
+        const uint32_t first = s_first[c], n = s_first[c + 1] - first;
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+            const GrowTreeNode t = tc[i];
+            const uint32_t meta =
+                t.left < 0 ? 1u << 31 : t.feature | (t.default_left ? kMetaDefaultLeft : 0u) | (t.limit << 16);
+            s_node[first + i] = make_uint2(meta, t.left < 0 ? 0u : (uint32_t)t.left);
+            s_value[first + i] = t.value;
+        }
+    }
+    __syncthreads();
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += gridDim.x * blockDim.x) {
+        uint32_t w[W];
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.bins8 + (size_t)r * a.stride);
+#pragma unroll
+        for (int q = 0; q < W / 4; q++) {
+            const uint4 v = src[q];
+            w[4 * q] = v.x;
+            w[4 * q + 1] = v.y;
+            w[4 * q + 2] = v.z;
+            w[4 * q + 3] = v.w;
+        }
+        const uint32_t mask = (W == 8 && a.masked) ? w[kMaskWord] : 0u;
+        float *m = a.margins + (size_t)r * a.m_stride + a.output;
+        for (uint32_t c = 0; c < K; c++) {
+            const uint32_t first = s_first[c], n = s_first[c + 1] - first;
+            if (n == 0) continue;
+            uint32_t nid = 0;
+            uint2 nd = s_node[first];
+            for (uint32_t step = 0; step < n && !(nd.x >> 31); step++) {
+                const uint32_t f = nd.x & (kMetaDefaultLeft - 1u), lim = (nd.x >> 16) & 0x7fffu;
+                uint32_t bin;
+                if constexpr (W == 16) {
+                    bin = pick_byte16(w, f & 63u);
+                } else {
+                    uint32_t h[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) h[i] = w[i];
+                    bin = pick_byte(h, f & 31u);
+                }
+                const bool right = ((mask >> (f & 31u)) & 1u) ? !(nd.x & kMetaDefaultLeft) : bin >= lim;
+                nid = nd.y + (right ? 1u : 0u);
+                nid = nid < n ? nid : 0u;
+                nd = s_node[first + nid];
+            }
+            if (nd.x >> 31) m[c] = m[c] + s_value[first + nid];
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves_batch32(WalkArgs a) { walk_leaves_batch<8>(a); }
+extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves_batch64(WalkArgs a) { walk_leaves_batch<16>(a); }
+
 __device__ __forceinline__ uint32_t load_walk_nodes(const WalkArgs &a, uint2 *s_node, float *s_value) {
     const uint32_t n_nodes = min(walk_nodes(a), kWalkLdsNodes);
     for (uint32_t i = threadIdx.x; i < n_nodes; i += blockDim.x) {
