@@ -155,7 +155,7 @@ def cpu_predict_baseline(args, arrs, xp):
 
 
 def other_workload(args):
-    """Training rounds/s of the multiclass or the sparse configuration: the
+    """Training rounds/s of the regression, multiclass or sparse configuration: the
     matrix binned once (excluded), `warmup` rounds, then `steps` timed
     rounds with the index, labels and margins resident in HBM; the oracle
     times a bounded sample of the same rounds on the host."""
@@ -165,7 +165,12 @@ def other_workload(args):
     from hessboost_amd import synthetic
 
     t = time.time()
-    if args.workload == "multiclass":
+    if args.workload == "regression":
+        x, y = synthetic.regression_100k(n=100_000, f=32, seed=0)
+        params = {"objective": "reg:squarederror", "max_depth": 6, "eta": 0.1, "max_bin": 256}
+        dm = hb.DMatrix(x, label=y)
+        workload = "squared-error hist training, 100,000 x 32 f32, max_bin 256, max_depth 6, eta 0.1, depthwise"
+    elif args.workload == "multiclass":
         x, y = synthetic.multiclass(n=2_000_000, f=50, k=10, seed=0)
         params = {"objective": "multi:softprob", "num_class": 10, "max_depth": 6, "eta": 0.3, "max_bin": 256}
         dm = hb.DMatrix(x, label=y)
@@ -203,7 +208,10 @@ def other_workload(args):
     if not args.no_cpu_baseline:
         from oracle import oracle as O
         O.set_threads(args.cpu_threads)
-        if args.workload == "multiclass":
+        if args.workload == "regression":
+            ds = O.Dataset(x, max_bin=256)
+            p = O.params(max_depth=6, eta=0.1)
+        elif args.workload == "multiclass":
             ds = O.Dataset(x, max_bin=256)
             p = O.params(objective=O.OBJ_SOFTMAX, num_class=10, max_depth=6, eta=0.3)
         else:
@@ -250,7 +258,7 @@ def main():
                     help="rows of the training matrix the single-thread CPU leg trains on")
     ap.add_argument("--fit-rounds", type=int, default=500,
                     help="rounds of the timed full fit on the device (0: skip)")
-    ap.add_argument("--workload", choices=("higgs", "multiclass", "sparse"), default="higgs",
+    ap.add_argument("--workload", choices=("higgs", "regression", "multiclass", "sparse"), default="higgs",
                     help="higgs: the default line; multiclass (2M x 50, 10-class softmax, depth 6) and "
                          "sparse (500k x 2000 CSR, 90%% missing, lossguide 255 leaves): their training "
                          "rounds/s on a line of their own")
