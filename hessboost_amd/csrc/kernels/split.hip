@@ -108,7 +108,10 @@ __device__ __forceinline__ uint32_t node_slot(const ScanArgs &a, const ScanNode 
 using namespace hbr;
 
 // One wave: feature f of node `node`, its best candidate written to *out
-// by one lane.
+// by one lane. BPL bins per lane and pass: 4 (chunks of 256 bins), or 1 for
+// a feature of at most 64 bins, whose lanes would otherwise idle; the
+// candidates, and the (highest loss, lowest index) winner, are the same.
+template <uint32_t BPL>
 __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, uint32_t f, ScanBest *out) {
     const uint32_t lane = lane_id();
     const ScanNode nd = a.nodes[node];
@@ -152,12 +155,12 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
                                          : nd.root_gain;
         int64_t carry_g = 0, carry_h = 0;
         // forward pass: bins <= b left, missing right
-        for (uint32_t c0 = 0; c0 < nb; c0 += kScanChunk) {
-            const uint32_t b0 = c0 + 4 * lane;
-            int64_t sg[4], sh[4];
+        for (uint32_t c0 = 0; c0 < nb; c0 += kWave * BPL) {
+            const uint32_t b0 = c0 + BPL * lane;
+            int64_t sg[BPL], sh[BPL];
             int64_t rg = 0, rh = 0;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
+            for (int k = 0; k < (int)BPL; k++) {
                 QBin v = (b0 + k < nb) ? h[b0 + k] : QBin{0, 0};
                 rg += v.g;
                 rh += v.h;
@@ -167,7 +170,7 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
             const int64_t ig = wave_inclusive_scan(rg), ih = wave_inclusive_scan(rh);
             const int64_t xg = carry_g + ig - rg, xh = carry_h + ih - rh;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
+            for (int k = 0; k < (int)BPL; k++) {
                 if (b0 + k >= nb) break;
                 const int64_t ag = xg + sg[k], ah = xh + sh[k];
                 float loss;
@@ -182,12 +185,12 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
         if (!a.dense && (carry_g != tg || carry_h != th)) {
             const int64_t fg = carry_g, fh = carry_h;
             carry_g = carry_h = 0;
-            for (uint32_t c0 = 0; c0 < nb; c0 += kScanChunk) {
-                const uint32_t b0 = c0 + 4 * lane;
-                int64_t eg_[4], eh_[4];  // exclusive prefix of each bin
+            for (uint32_t c0 = 0; c0 < nb; c0 += kWave * BPL) {
+                const uint32_t b0 = c0 + BPL * lane;
+                int64_t eg_[BPL], eh_[BPL];  // exclusive prefix of each bin
                 int64_t rg = 0, rh = 0;
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
+                for (int k = 0; k < (int)BPL; k++) {
                     QBin v = (b0 + k < nb) ? h[b0 + k] : QBin{0, 0};
                     eg_[k] = rg;
                     eh_[k] = rh;
@@ -197,7 +200,7 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
                 const int64_t ig = wave_inclusive_scan(rg), ih = wave_inclusive_scan(rh);
                 const int64_t xg = carry_g + ig - rg, xh = carry_h + ih - rh;
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
+                for (int k = 0; k < (int)BPL; k++) {
                     const uint32_t o = b0 + k;
                     if (o >= nb) break;
                     const int64_t sgv = fg - (xg + eg_[k]), shv = fh - (xh + eh_[k]);  // suffix from bin o
@@ -252,7 +255,11 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t pair = blockIdx.x * (blockDim.x / kWave) + wave;
     if (pair >= scan_nodes(a) * a.n_features) return;  // uniform per wave
-    scan_feature(a, pair / a.n_features, pair % a.n_features, a.per_feature + pair);
+    const uint32_t f = pair % a.n_features;
+    if (a.feature_offset[f + 1] - a.feature_offset[f] <= kWave)  // uniform per wave
+        scan_feature<1>(a, pair / a.n_features, f, a.per_feature + pair);
+    else
+        scan_feature<4>(a, pair / a.n_features, f, a.per_feature + pair);
 }
 
 // The feature-order merge of a node's per-feature winners (`per_node`,
