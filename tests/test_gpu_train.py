@@ -166,6 +166,45 @@ def test_batched_class_trees_equal_one_class_at_a_time(k, depth, weighted):
     assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
 
 
+@pytest.mark.parametrize("f,k,depth,kernel", [(12, 3, 5, "hbr_walk_leaves_batch32"),
+                                               (50, 10, 6, "hbr_walk_leaves_batch64"),
+                                               (50, 10, 7, None)])
+def test_one_pass_class_walk_equals_a_walk_per_class_tree(f, k, depth, kernel):
+    """A batched softmax round adds its K class trees to the margins in one
+    pass over the rows (hbr_walk_leaves_batch32/64, 32- and 64-byte rows);
+    the trees and margins equal those of one walk per class tree bit for
+    bit. Ten depth-7 trees outgrow the one-pass walk's node tables, and the
+    round falls back to a walk per tree."""
+    import os
+    x, y = synthetic.multiclass(n=20_011, f=f, k=k, seed=40 + f)
+    params = {"objective": "multi:softprob", "num_class": k, "max_depth": depth, "eta": 0.3}
+    dm = hb.DMatrix(x, label=y)
+    runs = []
+    for flag in ("1", "0"):
+        os.environ["HBROCM_BATCH_WALK"] = flag
+        try:
+            eng = dm.engine(256)
+        finally:
+            os.environ.pop("HBROCM_BATCH_WALK", None)
+        tr = hb.Trainer(eng, params, y)
+        eng.set_profiling(True, "hbr_walk")
+        tr.boost(3)
+        stats = eng.kernel_stats()
+        eng.set_profiling(False)
+        runs.append((tr.trees(), tr.margins(), stats))
+    (ta, ma, sa), (tb, mb, sb) = runs
+    batch = {"hbr_walk_leaves_batch32", "hbr_walk_leaves_batch64"}
+    if kernel:
+        assert kernel in sa and not batch & set(sb)
+    else:
+        assert not batch & set(sa)
+    assert len(ta) == len(tb) == 3 * k
+    for a, b in zip(ta, tb):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
+
+
 @pytest.mark.parametrize("n,k", [(5, 3), (33, 3), (70, 1), (130, 7)])
 def test_batched_class_trees_on_tiny_inputs_match_oracle(n, k):
     """Batched class trees where rows are few (fewer than the classes, or a
