@@ -214,6 +214,7 @@ int hbr_cuts_from_csr(const uint64_t *row_ptr, const uint32_t *col, const float 
                       uint32_t max_bin, const float *weights, hbr_cuts **out) {
     return guard([&] {
         if (!out || !row_ptr || max_bin < 2) fail(kInvalid, "cuts: bad arguments");
+        if (row_ptr[n] && (!col || !val)) fail(kInvalid, "cuts: null col or val with entries present");
         for (uint64_t e = 0; e < row_ptr[n]; e++)
             if (col[e] >= f) fail(kInvalid, "cuts: column index beyond n_cols");
         *out = new hbr_cuts{cuts_from_csr(row_ptr, col, val, n, f, max_bin, weights)};
@@ -232,6 +233,7 @@ int hbr_cuts_from_csr_typed(const uint64_t *row_ptr, const uint32_t *col, const 
                             uint32_t max_bin, const float *weights, const uint8_t *categorical, hbr_cuts **out) {
     return guard([&] {
         if (!out || !row_ptr || max_bin < 2) fail(kInvalid, "cuts: bad arguments");
+        if (row_ptr[n] && (!col || !val)) fail(kInvalid, "cuts: null col or val with entries present");
         for (uint64_t e = 0; e < row_ptr[n]; e++)
             if (col[e] >= f) fail(kInvalid, "cuts: column index beyond n_cols");
         *out = new hbr_cuts{cuts_from_csr(row_ptr, col, val, n, f, max_bin, weights, categorical)};
@@ -390,6 +392,7 @@ int hbr_build_device_noalloc(hbr_engine *h, const uint32_t *rows, uint64_t m, do
     return with_engine(h, [&](Engine &e) {
         if (!out || (!rows && m)) fail(kInvalid, "build: null argument");
         require_exact(e, m, "build");
+        const auto held = fixed_scratch_lock(e.dev().ordinal());
         uint64_t bytes = 0;
         uint8_t *scratch = fixed_scratch(e.dev().ordinal(), &bytes);
         if (!e.build_rows_fixed(rows, m, out, scratch, bytes)) fail(kInvalid, "build: a row beyond the index");

@@ -948,6 +948,8 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.total_bins = total_bins_;
     a.groups = groups;
     a.row_pairs = row_pairs_live_ && !level_pairs_ && dense_u8_ && stride_ == 32 && fg == 32 ? 1u : 0u;
+    if (pair_array_stale_ && !a.row_pairs && !level_pairs_)
+        fail(kRefused, "histograms: the staged pairs are carried in the rows, which this kernel does not read");
     a.masked = masked_ ? 1u : 0u;
     a.min_hess = row_pairs_min_hess_;
     const bool bm = hist_bin_major && fg >= 16;
@@ -1976,7 +1978,14 @@ bool Engine::build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uin
     a.partial = partial;
     a.total_bins = total_bins_;
     a.groups = groups;
+    // the pairs live where the last gradient pass wrote them: in the rows'
+    // last word after a fused logistic walk (the pair array then holds an
+    // earlier round's), else in the pair array
+    a.row_pairs = row_pairs_live_ && !level_pairs_ && dense_u8_ && stride_ == 32 && fg == 32 ? 1u : 0u;
+    if (pair_array_stale_ && !a.row_pairs && !level_pairs_)
+        fail(kRefused, "build: the staged pairs are carried in the rows, which this index's kernel does not read");
     a.masked = masked_ ? 1u : 0u;
+    a.min_hess = row_pairs_min_hess_;
     const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"
                     : masked_  ? "hbr_hist_dense8_fg32_bm_masked"

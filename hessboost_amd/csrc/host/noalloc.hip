@@ -24,7 +24,13 @@ namespace {
 constexpr int kMaxOrdinals = 64;
 std::mutex g_mu;
 void *g_addr[kMaxOrdinals] = {};
+std::mutex g_use[kMaxOrdinals];  // one holder of a device's scratch at a time
 }  // namespace
+
+std::unique_lock<std::mutex> fixed_scratch_lock(int ordinal) {
+    if (ordinal < 0 || ordinal >= kMaxOrdinals) fail(kInvalid, "fixed scratch: device ordinal out of range");
+    return std::unique_lock<std::mutex>(g_use[ordinal]);
+}
 
 uint8_t *fixed_scratch(int ordinal, uint64_t *bytes) {
     if (ordinal < 0 || ordinal >= kMaxOrdinals) fail(kInvalid, "fixed scratch: device ordinal out of range");

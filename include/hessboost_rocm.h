@@ -189,8 +189,9 @@ int hbr_prepare(hbr_engine *e, const float *gpair, uint64_t n);
 int hbr_build(hbr_engine *e, const uint32_t *rows, uint64_t m, double *out);
 
 /* No counterpart in the reference: hbr_build for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc). rows (m ids, device memory) and
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc). It synchronises the engine's stream before it returns, so it
+ * is not for code under HIP graph capture. rows (m ids, device memory) and
  * out (2 * total_bins f64, device memory) are the caller's; the tile plan,
  * the tiles' partial sums, the node record and a row-check word live in one
  * fixed scratch array of the library per device (32 MiB + 128 KiB, held
@@ -200,8 +201,10 @@ int hbr_build(hbr_engine *e, const uint32_t *rows, uint64_t m, double *out);
  * the index's rows (out then holds zeros), when m >= 2^32 - 1, or when one
  * row tile's partial sums exceed the scratch (more than 8,192 features of a
  * dense u8 index, or more than 2,097,152 bins of a CSR index). Every call
- * on one GPU shares that GPU's scratch: calls that overlap on one GPU (two
- * engines on it used from two threads) race. */
+ * on one GPU shares that GPU's scratch and holds a per-GPU lock for its
+ * whole duration, so calls from several threads (two engines on one GPU)
+ * run one after another. HBR_REFUSED when the last gradient pass left the
+ * pairs in the rows only and the index's kernel cannot read them there. */
 int hbr_build_device_noalloc(hbr_engine *e, const uint32_t *rows, uint64_t m, double *out);
 
 /* A node's rows on the device (the reference's Segment, src/tree/hist/mod.rs:107-164):

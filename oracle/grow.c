@@ -365,6 +365,31 @@ static int heap_pop(heap_t *h, entry_t *out) {
     return 1;
 }
 
+/* Test hook: a record of the loss-guided queue's pushes and pops, for
+ * tests/test_oracle.py (best-first order under equal gains). One record per
+ * event: kind (0 push, 1 pop), node id, loss_chg bits, expandable. */
+static uint64_t *g_lg_trace;
+static size_t g_lg_cap, g_lg_len;
+
+void or_lossguide_trace(uint64_t *buf, size_t cap) {
+    g_lg_trace = buf;
+    g_lg_cap = cap;
+    g_lg_len = 0;
+}
+
+size_t or_lossguide_trace_len(void) { return g_lg_len; }
+
+static void lg_event(int kind, const entry_t *e, int expandable) {
+    if (!g_lg_trace || g_lg_len >= g_lg_cap) return;
+    uint64_t *r = g_lg_trace + 4 * g_lg_len++;
+    uint64_t bits;
+    memcpy(&bits, &e->best.loss_chg, 8);
+    r[0] = (uint64_t)kind;
+    r[1] = (uint64_t)e->nid;
+    r[2] = bits;
+    r[3] = (uint64_t)expandable;
+}
+
 static void finish_tree(ctx_t *c) {
     double lambda = (double)(float)c->p->lambda, alpha = (double)(float)c->p->alpha;
     double mds = (double)(float)c->p->max_delta_step;
@@ -446,9 +471,11 @@ or_tree *or_grow_tree(const or_index *ix, const float *gpair, const or_params *p
         size_t max_leaves = p->max_leaves > 0 ? (size_t)p->max_leaves : SIZE_MAX;
         heap_t h = {0};
         heap_push(&h, root);
+        lg_event(0, &root, root.depth < c.limit && or_split_valid(&root.best, p));
         size_t n_leaves = 1;
         entry_t e;
         while (heap_pop(&h, &e)) {
+            lg_event(1, &e, e.depth < c.limit && or_split_valid(&e.best, p));
             if (n_leaves >= max_leaves) {
                 record_leaf(&c, &e);
                 break;
@@ -462,7 +489,9 @@ or_tree *or_grow_tree(const or_index *ix, const float *gpair, const or_params *p
             build_children(&c, &s, &l, &r);
             n_leaves++;
             heap_push(&h, l);
+            lg_event(0, &l, l.depth < c.limit && or_split_valid(&l.best, p));
             heap_push(&h, r);
+            lg_event(0, &r, r.depth < c.limit && or_split_valid(&r.best, p));
         }
         for (size_t i = 0; i < h.len; i++) record_leaf(&c, &h.d[i]);
         free(h.d);

@@ -85,6 +85,21 @@ size_t or_cuts_total_bins(const or_cuts *c);
  * (quantile.rs:285-296). */
 uint32_t or_bin_of(const or_cuts *c, size_t f, float v);
 
+/* Test hooks of the sketch: summaries as 4 floats per entry (rmin, rmax,
+ * wmin, value). */
+size_t or_summary_budget(size_t max_bin, size_t n);
+size_t or_summary_from_sorted(const float *v, const float *w, size_t n, float *out);
+size_t or_summary_prune(float *entries, size_t n, size_t maxsize);
+size_t or_summary_combine(const float *a, size_t na, const float *b, size_t nb, float *out);
+size_t or_summary_query(const float *entries, size_t n, size_t max_bin, float *out);
+/* Test hook: record the loss-guided queue's events of the next trees grown
+ * on this thread into buf (4 u64 per event: kind 0 push / 1 pop, node id,
+ * loss_chg bits, expandable), at most cap events; buf NULL stops. */
+void or_lossguide_trace(uint64_t *buf, size_t cap);
+size_t or_lossguide_trace_len(void);
+long or_sketch_trace(const float *values, const float *weights, size_t n, size_t max_bin, float *buf,
+                     size_t buf_entries, uint64_t *recs, size_t rec_cap, size_t *n_recs, float *cuts);
+
 /* ---- binned index (GHistIndex) ------------------------------------------ */
 typedef struct or_index {
     size_t n_rows, n_cols;

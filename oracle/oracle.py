@@ -158,6 +158,21 @@ def lib():
         L.or_model_last_gpair.argtypes = [C.c_void_p]
         L.or_model_free.argtypes = [C.c_void_p]
         L.or_set_threads.argtypes = [C.c_int]
+        L.or_summary_budget.restype = C.c_size_t
+        L.or_summary_budget.argtypes = [C.c_size_t, C.c_size_t]
+        L.or_summary_from_sorted.restype = C.c_size_t
+        L.or_summary_from_sorted.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.or_summary_prune.restype = C.c_size_t
+        L.or_summary_prune.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t]
+        L.or_summary_combine.restype = C.c_size_t
+        L.or_summary_combine.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.or_summary_query.restype = C.c_size_t
+        L.or_summary_query.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]
+        L.or_sketch_trace.restype = C.c_long
+        L.or_sketch_trace.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t,
+                                      C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t), C.c_void_p]
+        L.or_lossguide_trace.argtypes = [C.c_void_p, C.c_size_t]
+        L.or_lossguide_trace_len.restype = C.c_size_t
         _lib = L
     return _lib
 
@@ -494,3 +509,78 @@ def predict_margin_lockstep(arrs, x):
 
 def set_threads(n: int) -> None:
     lib().or_set_threads(n)
+
+
+# ---- the sketch's summary operations (test hooks) --------------------------
+# A summary is an (k, 4) f32 array of entries (rmin, rmax, wmin, value).
+
+SUMMARY_KINDS = ("from_sorted", "prune", "combine", "summary", "final")
+
+
+def summary_budget(max_bin, n):
+    return lib().or_summary_budget(max_bin, n)
+
+
+def summary_from_sorted(values, weights):
+    v = np.ascontiguousarray(values, np.float32)
+    w = np.ascontiguousarray(weights, np.float32)
+    out = np.empty((max(len(v), 1), 4), np.float32)
+    k = lib().or_summary_from_sorted(_ptr(v), _ptr(w), len(v), _ptr(out))
+    return out[:k].copy()
+
+
+def summary_prune(entries, maxsize):
+    e = np.array(entries, np.float32, copy=True).reshape(-1, 4)
+    k = lib().or_summary_prune(_ptr(e), len(e), maxsize)
+    return e[:k].copy()
+
+
+def summary_combine(a, b):
+    a = np.ascontiguousarray(a, np.float32).reshape(-1, 4)
+    b = np.ascontiguousarray(b, np.float32).reshape(-1, 4)
+    out = np.empty((max(len(a) + len(b), 1), 4), np.float32)
+    k = lib().or_summary_combine(_ptr(a), len(a), _ptr(b), len(b), _ptr(out))
+    return out[:k].copy()
+
+
+def summary_query(entries, max_bin):
+    e = np.ascontiguousarray(entries, np.float32).reshape(-1, 4)
+    out = np.empty(max_bin + 2, np.float32)
+    k = lib().or_summary_query(_ptr(e), len(e), max_bin, _ptr(out))
+    return out[:k].copy()
+
+
+def sketch_trace(values, weights, max_bin, buf_entries=1 << 22, rec_cap=1 << 16):
+    """One feature's streaming sketch over `values` (weights None: 1): its
+    cut values and every summary it formed, as (kind, lo, hi, entries,
+    pruned_to), where [lo, hi) are the indices of the values the summary
+    covers and pruned_to the size a prune record was pruned to (else 0)."""
+    v = np.ascontiguousarray(values, np.float32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    buf = np.empty((buf_entries, 4), np.float32)
+    recs = np.empty((rec_cap, 6), np.uint64)
+    n_recs = C.c_size_t()
+    cuts = np.empty(max_bin + 2, np.float32)
+    k = lib().or_sketch_trace(_ptr(v), _ptr(w), len(v), max_bin, _ptr(buf), buf_entries, _ptr(recs), rec_cap,
+                              C.byref(n_recs), _ptr(cuts))
+    if k < 0:
+        raise RuntimeError("sketch trace: buffers too small")
+    out = []
+    for off, cnt, lo, hi, kind, size in recs[:n_recs.value].tolist():
+        out.append((SUMMARY_KINDS[kind], lo, hi, buf[off:off + cnt].copy(), size))
+    return cuts[:k].copy(), out
+
+
+def lossguide_events(ds, gpair, p, cap=1 << 16):
+    """Grow one tree and return it with its loss-guided queue's events:
+    (kind "push" / "pop", node id, loss_chg, expandable) in order."""
+    buf = np.zeros((cap, 4), np.uint64)
+    lib().or_lossguide_trace(_ptr(buf), cap)
+    try:
+        nodes, _ = ds.grow_tree(gpair, p)
+        n = lib().or_lossguide_trace_len()
+    finally:
+        lib().or_lossguide_trace(None, 0)
+    ev = [("push" if k == 0 else "pop", int(nid), float(np.array([bits], np.uint64).view(np.float64)[0]), bool(x))
+          for k, nid, bits, x in buf[:n].tolist()]
+    return nodes, ev

@@ -253,6 +253,16 @@ static void query_cut_values(const entry *data, size_t n, size_t max_bin,
 #undef PUSH
 }
 
+/* A record of every summary a traced sketch forms (or_sketch_trace): the
+ * entries, and the range [lo, hi) of the caller's value indices it covers. */
+typedef struct sk_trace {
+    float *buf;          /* 4 floats per entry */
+    size_t cap, len;     /* in entries */
+    uint64_t *recs;      /* 6 per record: offset, count, lo, hi, kind, prune size (0: none) */
+    size_t rec_cap, n_recs;
+    int overflow;
+} sk_trace;
+
 /* The sketch of one feature (sketch.rs:512-680). */
 typedef struct sketch {
     size_t max_bin, limit_size;
@@ -262,7 +272,39 @@ typedef struct sketch {
     size_t nlevels;
     vec_e temp, ws;
     size_t num_elements;
+    /* tracing only: the caller's index of the value being pushed, the
+     * first index of the queued batch, each level's and temp's coverage */
+    sk_trace *tr;
+    size_t pos, batch_lo, t_lo, t_hi;
+    size_t *lv_lo, *lv_hi;
 } sketch;
+
+enum { TR_FROM_SORTED = 0, TR_PRUNE = 1, TR_COMBINE = 2, TR_SUMMARY = 3, TR_FINAL = 4 };
+
+static void tr_record(sketch *s, const vec_e *v, size_t lo, size_t hi, int kind, size_t pruned_to) {
+    sk_trace *t = s->tr;
+    if (!t) return;
+    if (t->len + v->len > t->cap || t->n_recs >= t->rec_cap) {
+        t->overflow = 1;
+        return;
+    }
+    memcpy(t->buf + 4 * t->len, v->d, v->len * sizeof(entry));
+    uint64_t *r = t->recs + 6 * t->n_recs++;
+    r[0] = t->len;
+    r[1] = v->len;
+    r[2] = lo;
+    r[3] = hi;
+    r[4] = (uint64_t)kind;
+    r[5] = pruned_to;
+    t->len += v->len;
+}
+
+static void tr_levels(sketch *s, size_t nlevels) {
+    if (!s->tr) return;
+    s->lv_lo = (size_t *)realloc(s->lv_lo, nlevels * sizeof(size_t));
+    s->lv_hi = (size_t *)realloc(s->lv_hi, nlevels * sizeof(size_t));
+    s->lv_lo[nlevels - 1] = s->lv_hi[nlevels - 1] = 0;
+}
 
 static void sk_init(sketch *s, size_t n_values, size_t max_bin) {
     memset(s, 0, sizeof(*s));
@@ -279,6 +321,8 @@ static void sk_free(sketch *s) {
     free(s->levels);
     free(s->temp.d);
     free(s->ws.d);
+    free(s->lv_lo);
+    free(s->lv_hi);
 }
 
 /* Total order of f32 values (f32::total_cmp) as an unsigned key. */
@@ -307,14 +351,23 @@ static void sk_push_summary(sketch *s) {
             s->levels = (vec_e *)realloc(s->levels, (l + 1) * sizeof(vec_e));
             memset(&s->levels[l], 0, sizeof(vec_e));
             s->nlevels = l + 1;
+            tr_levels(s, s->nlevels);
         }
-        set_prune(&s->temp, s->limit_size);
+        const size_t keep = s->limit_size;
+        set_prune(&s->temp, keep);
+        tr_record(s, &s->temp, s->t_lo, s->t_hi, TR_PRUNE, keep);
+        if (s->tr && s->levels[l].len) s->t_lo = s->lv_lo[l];  /* the level holds the batches just before */
         set_combine(&s->temp, &s->levels[l], &s->ws);
+        tr_record(s, &s->temp, s->t_lo, s->t_hi, TR_COMBINE, 0);
         s->levels[l].len = 0;
         if (s->temp.len <= s->limit_size) break;
         l++;
     }
     ve_swap(&s->levels[l], &s->temp);
+    if (s->tr) {
+        s->lv_lo[l] = s->t_lo;
+        s->lv_hi[l] = s->t_hi;
+    }
 }
 
 /* sketch.rs:619-656 (Queue::PopSummary + PushSummary). The queue is sorted
@@ -339,6 +392,10 @@ static void sk_flush(sketch *s) {
     free(v);
     free(w);
     s->qlen = 0;
+    s->t_lo = s->batch_lo;
+    s->t_hi = s->pos;
+    s->batch_lo = s->pos;
+    tr_record(s, &s->temp, s->t_lo, s->t_hi, TR_FROM_SORTED, 0);
     sk_push_summary(s);
 }
 
@@ -362,11 +419,18 @@ static void sk_cut_values(sketch *s, float **out, size_t *out_len, size_t *out_c
     sk_flush(s);
     size_t prune_size = budget > s->limit_size ? budget : s->limit_size;
     vec_e sum = {0};
+    size_t lo = s->pos, hi = s->pos;
     for (size_t l = 0; l < s->nlevels; l++) {
+        if (s->tr && s->levels[l].len) {
+            lo = s->lv_lo[l];  /* levels run from the newest batches to the oldest */
+            if (sum.len == 0) hi = s->lv_hi[l];
+        }
         set_combine(&sum, &s->levels[l], &s->ws);
         set_prune(&sum, prune_size);
+        tr_record(s, &sum, lo, hi, TR_SUMMARY, prune_size);
     }
     set_prune(&sum, budget);
+    tr_record(s, &sum, lo, hi, TR_FINAL, budget);
     size_t mb = sum.len < s->max_bin ? sum.len : s->max_bin;
     query_cut_values(sum.d, sum.len, mb, out, out_len, out_cap);
     free(sum.d);
@@ -574,4 +638,85 @@ uint32_t or_bin_of(const or_cuts *c, size_t f, float v) {
     size_t n_cuts = end - start;
     size_t local = lo < (n_cuts ? n_cuts - 1 : 0) ? lo : (n_cuts ? n_cuts - 1 : 0);
     return (uint32_t)(start + local);
+}
+
+/* ---- test hooks: the summary operations on caller arrays -----------------
+ * An entry is 4 floats (rmin, rmax, wmin, value). Used by tests/test_oracle.py
+ * to check the summaries against brute-force ranks and against plain
+ * restatements of XGBoost's SetPrune / SetCombine. */
+
+static vec_e wrap(const float *e, size_t n) {
+    vec_e v = {0};
+    ve_reserve(&v, n ? n : 1);
+    if (n) memcpy(v.d, e, n * sizeof(entry));
+    v.len = n;
+    return v;
+}
+
+size_t or_summary_budget(size_t max_bin, size_t n) { return summary_budget(max_bin, n); }
+
+size_t or_summary_from_sorted(const float *v, const float *w, size_t n, float *out) {
+    vec_e o = {0};
+    set_from_sorted(v, w, n, &o);
+    if (o.len) memcpy(out, o.d, o.len * sizeof(entry));
+    size_t len = o.len;
+    free(o.d);
+    return len;
+}
+
+size_t or_summary_prune(float *entries, size_t n, size_t maxsize) {
+    vec_e v = wrap(entries, n);
+    set_prune(&v, maxsize);
+    if (v.len) memcpy(entries, v.d, v.len * sizeof(entry));
+    size_t len = v.len;
+    free(v.d);
+    return len;
+}
+
+size_t or_summary_combine(const float *a, size_t na, const float *b, size_t nb, float *out) {
+    vec_e va = wrap(a, na), vb = wrap(b, nb), ws = {0};
+    set_combine(&va, &vb, &ws);
+    if (va.len) memcpy(out, va.d, va.len * sizeof(entry));
+    size_t len = va.len;
+    free(va.d);
+    free(vb.d);
+    free(ws.d);
+    return len;
+}
+
+size_t or_summary_query(const float *entries, size_t n, size_t max_bin, float *out) {
+    float *cuts = NULL;
+    size_t len = 0, cap = 0;
+    query_cut_values((const entry *)entries, n, max_bin, &cuts, &len, &cap);
+    if (len) memcpy(out, cuts, len * sizeof(float));
+    free(cuts);
+    return len;
+}
+
+/* One feature's streaming sketch over values[0..n) with weights (NULL: 1),
+ * recording every summary it forms: after each queue flush (from sorted),
+ * each prune and each merge of the level-wise carry, each merge of the
+ * final summary, and the final summary. Returns the number of cut values
+ * written to `cuts` (at most max_bin + 1); -1 when the buffers overflow. */
+long or_sketch_trace(const float *values, const float *weights, size_t n, size_t max_bin, float *buf,
+                     size_t buf_entries, uint64_t *recs, size_t rec_cap, size_t *n_recs, float *cuts) {
+    sk_trace t = {buf, buf_entries, 0, recs, rec_cap, 0, 0};
+    size_t present = 0;
+    for (size_t i = 0; i < n; i++) present += (weights ? weights[i] : 1.0f) != 0.0f;
+    sketch s;
+    sk_init(&s, present, max_bin);
+    s.tr = &t;
+    for (size_t i = 0; i < n; i++) {
+        s.pos = i;
+        sk_push(&s, values[i], weights ? weights[i] : 1.0f);
+    }
+    s.pos = n;
+    float *out = NULL;
+    size_t len = 0, cap = 0;
+    sk_cut_values(&s, &out, &len, &cap);
+    sk_free(&s);
+    if (len) memcpy(cuts, out, len * sizeof(float));
+    free(out);
+    *n_recs = t.n_recs;
+    return t.overflow ? -1 : (long)len;
 }

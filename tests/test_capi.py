@@ -37,3 +37,23 @@ def test_error_reporting_without_device():
     st = L.hbr_cuts_from_dense(None, 10, 3, 256, None, float("nan"), ctypes.byref(out))
     assert st == A.INVALID
     assert "cuts" in A.last_error()
+
+
+def test_csr_cuts_refuse_null_entries_without_device():
+    """A CSR with entries but no column or value array is a caller error
+    (HBR_INVALID), for the untyped and the typed entry point alike."""
+    import numpy as np
+    L = A.lib()
+    rp = np.array([0, 2, 3], np.uint64)
+    col = np.array([0, 1, 1], np.uint32)
+    val = np.array([1.0, 2.0, 3.0], np.float32)
+    out = ctypes.c_void_p()
+    for c, v in ((None, A.ptr(val)), (A.ptr(col), None)):
+        st = L.hbr_cuts_from_csr(A.ptr(rp), c, v, 2, 2, 256, None, ctypes.byref(out))
+        assert st == A.INVALID and "null col or val" in A.last_error()
+        st = L.hbr_cuts_from_csr_typed(A.ptr(rp), c, v, 2, 2, 256, None, None, ctypes.byref(out))
+        assert st == A.INVALID and "null col or val" in A.last_error()
+    empty = np.zeros(3, np.uint64)
+    st = L.hbr_cuts_from_csr(A.ptr(empty), None, None, 2, 2, 256, None, ctypes.byref(out))
+    assert st == A.OK
+    L.hbr_cuts_free(out)

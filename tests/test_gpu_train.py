@@ -496,3 +496,22 @@ def test_missing_values_on_masked_dense_rows_match_oracle_and_csr_path(objective
             assert np.array_equal(a[key], b[key]), key
     assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
     assert np.max(np.abs(runs[0][1] - ref.margins())) <= 1e-5
+
+
+@pytest.mark.parametrize("leaves", [3, 6, 14])
+def test_lossguide_with_equal_gains_matches_oracle(leaves):
+    """Mirrored rows give every node below the root a twin of equal loss
+    change, and the leaf budgets cut between twins: the device-side
+    loss-guided growth breaks the ties as the oracle's restatement of the
+    reference's BinaryHeap does, for two rounds (the second round's
+    gradients are mirrored too)."""
+    from tests.test_oracle import _mirrored_data
+    x, gp = _mirrored_data(4)
+    y = -gp[:, 0]
+    params = {"grow_policy": "lossguide", "max_depth": 0, "max_leaves": leaves, "eta": 0.3, "max_bin": 64,
+              "base_score": 0.0}
+    ref = O.Model(O.Dataset(x, max_bin=64), y, O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=0, max_leaves=leaves,
+                                                        eta=0.3, max_bin=64, base_score=0.0), 2)
+    model = hb.train(params, hb.DMatrix(x, label=y), 2)
+    compare_trees(model.trees, ref.trees())
+    assert np.max(np.abs(model.predict(x, output_margin=True) - ref.margins())) <= 1e-5

@@ -775,3 +775,120 @@ def test_categorical_sweep_brute_force():
         assert best.categorical, trial
         assert abs(best.loss_chg - top) <= 1e-3 * max(1.0, abs(top)), (trial, best.loss_chg, top)
         assert any(abs(c[0] - top) <= 1e-3 * max(1.0, abs(top)) and c[1] == chosen for c in cands), trial
+
+
+def _mirrored_data(seed, n_half=2_000):
+    """Rows in mirrored pairs: feature 0 is 0 or 1, the other features are
+    shared, and the second row's gradient is the first's negated, so every
+    node under the root's split on feature 0 has a mirror image with the
+    same loss change bit for bit (f64 sums of negated values in the same
+    order are exact negations; gains square them)."""
+    rng = np.random.default_rng(seed)
+    base = rng.standard_normal((n_half, 3)).astype(np.float32)
+    x = np.zeros((2 * n_half, 4), np.float32)
+    x[0::2, 1:] = base
+    x[1::2, 1:] = base
+    x[1::2, 0] = 1.0
+    h = (1.5 + base[:, 0] + np.sin(2.0 * base[:, 1]) * base[:, 2]).astype(np.float32)
+    g = np.empty(2 * n_half, np.float32)
+    g[0::2], g[1::2] = -h, h
+    gp = np.stack([g, np.ones_like(g)], 1)
+    return x, gp
+
+
+class RustBinaryHeap:
+    """std::collections::BinaryHeap as the Rust standard library implements
+    it (library/alloc/src/collections/binary_heap/mod.rs): push appends and
+    sifts up, stopping at a parent the element is <= to; pop swaps the last
+    element into the root, sifts the hole down to the bottom through the
+    larger child (the right one when the left is <= it), then sifts up.
+    Elements are (key, payload) ordered by key alone."""
+
+    def __init__(self):
+        self.d = []
+
+    def _sift_up(self, start, pos):
+        elem = self.d[pos]
+        while pos > start:
+            parent = (pos - 1) // 2
+            if elem[0] <= self.d[parent][0]:
+                break
+            self.d[pos] = self.d[parent]
+            pos = parent
+        self.d[pos] = elem
+
+    def push(self, key, payload):
+        self.d.append((key, payload))
+        self._sift_up(0, len(self.d) - 1)
+
+    def pop(self):
+        item = self.d.pop()
+        if self.d:
+            item, self.d[0] = self.d[0], item
+            end, pos = len(self.d), 0
+            elem = self.d[0]
+            child = 1
+            while child <= max(end - 2, 0) and end >= 2:
+                if self.d[child][0] <= self.d[child + 1][0]:
+                    child += 1
+                self.d[pos] = self.d[child]
+                pos, child = child, 2 * child + 1
+            if child == end - 1:
+                self.d[pos] = self.d[child]
+                pos = child
+            self.d[pos] = elem
+            self._sift_up(0, pos)
+        return item
+
+
+def _total_key(x):
+    """f64::total_cmp as an integer key."""
+    b = int(np.array([x], np.float64).view(np.int64)[0])
+    return b ^ ((b >> 63) & 0x7FFFFFFFFFFFFFFF)
+
+
+@pytest.mark.parametrize("leaves", [3, 5, 6, 9, 14])
+def test_lossguide_with_equal_gains_is_best_first_in_rust_heap_order(leaves):
+    """Loss-guided growth on mirrored data, where every node below the root
+    has a twin of equal loss change, with leaf budgets that cut between
+    twins. Brute force: every pop takes a candidate whose loss change is the
+    largest left in the queue (ties allowed), an expanded node's two
+    children get the next two ids, and the budget stops expansion. Tie
+    order: the pops equal those of Rust's BinaryHeap (the reference's
+    queue, builder/hist/mod.rs:505-573, keyed by loss_chg.total_cmp,
+    :132-148) fed the same pushes."""
+    x, gp = _mirrored_data(4)
+    ds = O.Dataset(x, max_bin=64)
+    p = O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=0, max_leaves=leaves, eta=0.3)
+    nodes, ev = O.lossguide_events(ds, gp, p)
+    pushed = {nid: chg for kind, nid, chg, _ in ev if kind == "push"}
+    assert nodes[0]["split_feature"] == 0 and pushed[1] == pushed[2] > 0
+    queue, heap = {}, RustBinaryHeap()
+    next_id, n_leaves, ties, expanded = 1, 1, 0, []
+    i = 0
+    while i < len(ev):
+        kind, nid, chg, expandable = ev[i]
+        if kind == "push":
+            queue[nid] = chg
+            heap.push(_total_key(chg), nid)
+            i += 1
+            continue
+        best = max(_total_key(c) for c in queue.values())
+        assert _total_key(chg) == best, (i, nid)
+        ties += sum(_total_key(c) == best for c in queue.values()) - 1
+        assert heap.pop()[1] == nid, (i, nid)
+        del queue[nid]
+        i += 1
+        if n_leaves >= leaves:
+            assert i == len(ev), "growth continues past the leaf budget"
+            break
+        if not expandable:
+            continue
+        expanded.append(nid)
+        n_leaves += 1
+        assert [e[:2] for e in ev[i:i + 2]] == [("push", next_id), ("push", next_id + 1)], (i, nid)
+        assert nodes[nid]["left"] == next_id and nodes[nid]["right"] == next_id + 1
+        next_id += 2
+    assert ties > 0, "the data must put equal gains in the queue"
+    assert sum(nd["left"] == -1 for nd in nodes) == min(leaves, len(nodes))
+    assert len(expanded) == leaves - 1

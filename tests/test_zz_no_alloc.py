@@ -94,3 +94,29 @@ def test_noalloc_build_refuses_rows_beyond_the_index():
     st, got, _ = noalloc_build(e, ok)
     assert st == A.OK
     np.testing.assert_array_equal(got.view(np.uint64), e.build(ok).view(np.uint64))
+
+
+def test_noalloc_build_after_device_rounds_reads_the_row_carried_pairs():
+    """After device-resident logistic rounds the next pairs ride in the
+    rows' last word (the pair array holds an earlier round's): the no-alloc
+    build reads them there, as hbr_build does, and both equal the oracle's
+    histogram of the pairs recomputed from the trainer's margins."""
+    from hessboost_amd import synthetic
+    from oracle import oracle as O
+
+    x, y = synthetic.higgs_like(n=200_000, seed=3)
+    e = hb.DMatrix(x, label=y).engine(256)
+    t = hb.Trainer(e, {"objective": "binary:logistic", "max_depth": 6, "eta": 0.1}, y)
+    t.boost(3)
+    e.set_sums("fixed_point")
+    gpair = O.gradient(O.OBJ_LOGISTIC, t.margins(), y)
+    ds = O.Dataset(x, max_bin=256)
+    rng = np.random.default_rng(6)
+    for frac in (0.7, 0.1):
+        rows = np.sort(rng.choice(len(y), size=int(len(y) * frac), replace=False)).astype(np.uint32)
+        want = e.build(rows)
+        st, got, msg = noalloc_build(e, rows)
+        assert st == A.OK, msg
+        np.testing.assert_array_equal(got.view(np.uint64), want.view(np.uint64))
+        ref = ds.build_hist(rows, gpair).reshape(-1, 2)
+        np.testing.assert_allclose(got, ref, rtol=1e-9, atol=1e-9)
