@@ -78,6 +78,8 @@ def pack(trees, margins, n_rows, n_outputs, base_score):
 
 def unpack(z):
     """The fixture's trees as the node dicts `tests.test_gpu_train.compare_trees` reads."""
+    z = {k: np.asarray(z[k]) for k in ("n_nodes", "left", "right", "split_feature", "split_cond", "default_left",
+                                       "leaf_value")}
     out, s = [], 0
     for c in z["n_nodes"]:
         e = s + int(c)
