@@ -21,7 +21,7 @@ LOSS_SQUARED_ERROR, LOSS_LOGISTIC, LOSS_SOFTMAX = 0, 1, 2
 OBJ_SQUARED_ERROR, OBJ_LOGISTIC, OBJ_SOFTMAX, OBJ_LOGITRAW = 0, 1, 2, 3
 GROW_DEPTHWISE, GROW_LOSSGUIDE = 0, 1
 SCAN_EMPTY, SCAN_REPLAY, SCAN_NUMERIC, SCAN_CATEGORICAL = 0, 1, 2, 3
-FALLBACK_NUMERIC_SCORE, FALLBACK_CATEGORICAL_ORDER, FALLBACK_CATEGORICAL_SCORE = 1, 2, 3
+FALLBACK_NUMERIC_SCORE, FALLBACK_CATEGORICAL_ORDER, FALLBACK_CATEGORICAL_SCORE, FALLBACK_NEAR_TIE = 1, 2, 3, 4
 TRANSFORM_SIGMOID, TRANSFORM_SOFTMAX, TRANSFORM_CLASS_INDEX = 1, 2, 3
 
 P = C.POINTER
@@ -82,7 +82,7 @@ class ScanRequest(C.Structure):
 
 class NodeScan(C.Structure):
     _fields_ = [("kind", C.c_uint32), ("feature", C.c_uint32), ("loss_chg", C.c_float),
-                ("backward", C.c_uint32), ("offset", C.c_uint32), ("pad", C.c_uint32),
+                ("backward", C.c_uint32), ("offset", C.c_uint32), ("loss_err", C.c_float),
                 ("acc_g", C.c_double), ("acc_h", C.c_double), ("left_g", C.c_double),
                 ("left_h", C.c_double), ("right_g", C.c_double), ("right_h", C.c_double),
                 ("fixed_left_g", C.c_int64), ("fixed_left_h", C.c_int64),
@@ -93,7 +93,7 @@ class NodeScan(C.Structure):
 
 class EngineCounters(C.Structure):
     _fields_ = [("hist_nodes", C.c_uint64), ("hist_rows", C.c_uint64), ("hist_bytes", C.c_uint64),
-                ("partition_rows", C.c_uint64), ("trees", C.c_uint64)]
+                ("partition_rows", C.c_uint64), ("trees", C.c_uint64), ("near_ties", C.c_uint64)]
 
 
 class TrainParams(C.Structure):
@@ -162,6 +162,7 @@ SIGNATURES = {
     "hbr_scan_resident": (C.c_int, [C.c_void_p, P(RegParams), P(ScanRequest), C.c_uint64, P(NodeScan)]),
     "hbr_scan_categories": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
     "hbr_read_hist": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p]),
+    "hbr_engine_set_guard": (C.c_int, [C.c_void_p, C.c_int, C.c_double]),
     "hbr_engine_counters_read": (C.c_int, [C.c_void_p, P(EngineCounters)]),
     "hbr_set_profiling": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p]),
     "hbr_kernel_stats": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),

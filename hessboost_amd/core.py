@@ -242,6 +242,12 @@ class Engine:
         code = {"exact": A.SUMS_EXACT, "fixed_point": A.SUMS_FIXED_POINT}[mode]
         A.check(A.lib().hbr_engine_set_sums(self._h, code))
 
+    def set_guard(self, on=True, gamma=0.0):
+        """The fixed-point guard: with it, the resident scan reports a node
+        whose winner its sums cannot certify as a replay (and the trainer
+        counts such nodes); gamma is the split threshold it checks."""
+        A.check(A.lib().hbr_engine_set_guard(self._h, int(bool(on)), float(gamma)))
+
     def prepare(self, gpair):
         gpair = np.ascontiguousarray(gpair, np.float32).reshape(-1)
         A.check(A.lib().hbr_prepare(self._h, A.ptr(gpair), len(gpair) // 2))

@@ -217,6 +217,8 @@ struct GrowCounts {
     uint32_t error;         // nonzero: a level needed more slots than reserved
     uint64_t hist_rows;     // rows summed into built children this tree (root excluded)
     uint64_t part_rows;     // rows partitioned this tree
+    uint32_t near_ties;     // nodes decided this tree whose winner carried kScanNearTie
+    uint32_t pad;
 };
 
 // ---- partition -----------------------------------------------------------------
@@ -316,6 +318,39 @@ struct PlanArgs {
     const GrowCounts *grow;     // non-null: one node per split of the level, n_splits read from here
 };
 
+// The reference's CPU histogram in its own f64 order (replays): one
+// workgroup per block of `grain` rows, thread f owning feature f's bins in
+// LDS (each bin one thread's chain in row order from +0.0); every block's
+// partial then added to the output in block order.
+constexpr uint32_t kExactThreads = 256;     // features per index, at most
+constexpr uint32_t kExactMaxWords = 18432;  // f64 words of LDS: 2 x total_bins
+struct ExactArgs {
+    const uint32_t *rows;    // the node's row ids; null: rows first .. first + m - 1
+    uint32_t first;
+    uint32_t m;
+    uint32_t grain;          // rows per block (the last shorter)
+    uint32_t blk0;           // the launch's first block
+    const uint8_t *bins8;    // row-major u8 local bins
+    uint32_t stride;
+    uint32_t n_cols;
+    const uint32_t *feature_offset;
+    const GPair *gpair;      // or null with row_pairs
+    uint32_t row_pairs;      // the logistic pair from each row's last word
+    float min_hess;
+    uint32_t masked;         // the row's missing cells (mask word) add nowhere
+    uint32_t total_bins;
+    double *partial;         // per block of the launch: total_bins x (g, h)
+};
+
+struct ExactSumArgs {
+    const double *partial;
+    uint32_t n_blocks;
+    uint32_t first;          // 1: the output starts as block 0's partial
+    double *out;
+    uint32_t n;              // words (2 x total_bins)
+    const double *minus;     // non-null: out -= minus instead (a sibling from its parent)
+};
+
 struct HistArgs {
     const HistNode *nodes;
     const HistTile *tiles;
@@ -409,6 +444,8 @@ struct ScanNode {
     float root_gain;
     float lower, upper;
     uint32_t pad;            // flags (kScanDeviceRoot) | class << kScanClassShift
+    uint32_t rows;           // the node's row count (from_split: read from the partition)
+    uint32_t pad2;
 };
 
 struct ScanParams {
@@ -429,6 +466,13 @@ constexpr uint32_t kScanNumericNaN = 2u;
 constexpr uint32_t kScanCatOrder = 8u;
 constexpr uint32_t kScanCatNaN = 16u;
 constexpr uint32_t kScanReplay = kScanNumericNaN | kScanCatOrder | kScanCatNaN;
+// ScanBest::flags of a node's winner that the fixed-point sums cannot
+// certify: a rival candidate (another partition of the node's rows) scores
+// within the error bound of the winner, or the winner's loss is within the
+// bound of a validity threshold (0, kRtEps, gamma). The bound covers the
+// quantisation of every row's pair, the reference's f64 chain rounding and
+// the f32 roundings of the score; nodes whose sums are exact never carry it.
+constexpr uint32_t kScanNearTie = 32u;
 
 // Best candidate of one feature (or of one node after the merge).
 struct ScanBest {
@@ -440,6 +484,9 @@ struct ScanBest {
                              // kScanReplay bits
     QBin left;
     QBin right;
+    float err;               // the candidate's score error bound (0 without the guard)
+    float rival;             // feature records: the highest score + error bound of the feature's
+                             // other partitions (-inf: none); node records: of the node's rivals
 };
 
 struct ScanArgs {
@@ -455,6 +502,7 @@ struct ScanArgs {
     const QScale *scale;
     ScanParams reg;
     uint32_t dense;          // index without missing values: forward pass only
+    float gamma;             // the split validity threshold (with kRtEps) the guard checks against
     ScanBest *per_feature;   // n_nodes * n_features
     ScanBest *best;          // n_nodes
     QBin *root_total;        // nodes flagged kScanDeviceRoot: their total (read, or written when dense)
@@ -465,7 +513,7 @@ struct ScanArgs {
     const uint32_t *cat_rank;
     const uint32_t *cat_feature;  // the feature of each rank
     uint32_t n_cat;
-    uint32_t pad2;
+    uint32_t guard;          // 1: bound each candidate's error and flag near ties (kScanNearTie)
     uint32_t *cat_sets;
     uint32_t *best_sets;
 };

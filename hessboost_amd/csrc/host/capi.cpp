@@ -569,9 +569,12 @@ int hbr_build_resident(hbr_engine *h, const hbr_segment *segs, const uint32_t *s
     return with_engine(h, [&](Engine &e) {
         std::vector<Segment> ss;
         for (uint64_t i = 0; i < n; i++) ss.push_back(seg_of(e, segs[i]));
-        e.build_nodes(ss, std::vector<uint32_t>(slots, slots + n));
-        e.subtract(std::vector<uint32_t>(sib_parent, sib_parent + n_sib),
-                   std::vector<uint32_t>(sib_built, sib_built + n_sib));
+        const std::vector<uint32_t> built(slots, slots + n);
+        const std::vector<uint32_t> parents(sib_parent, sib_parent + n_sib), sib(sib_built, sib_built + n_sib);
+        e.build_nodes(ss, built);
+        e.subtract(parents, sib);
+        e.note_built(ss, built);
+        e.note_siblings(parents, sib);
         e.dev().sync();
     });
 }
@@ -588,6 +591,8 @@ int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_r
                 if (req[0].features[i] < e.n_cols()) dirs[req[0].features[i]] = req[0].directions[i];
         }
         e.set_scan_params(ScanParams{reg->lambda, reg->alpha, reg->max_delta_step, reg->min_child_weight}, dirs);
+        // fixed-point sums beyond the exact domain: the guard certifies each winner
+        e.guard_active = e.guard_on && !e.sums_exact(e.n_rows());
         std::vector<ScanInput> in(n);
         for (uint64_t i = 0; i < n; i++) {
             if (req[i].n_features != e.n_cols()) fail(kRefused, "scan: a feature subset (column sampling)");
@@ -609,13 +614,17 @@ int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_r
         for (uint64_t i = 0; i < n; i++) {
             hbr_node_scan o{};
             const ScanBest &b = best[i];
-            if (b.flags & kScanReplay) {
-                // a NaN score or a categorical order that is not total: the
-                // host replays the node from its histogram (NodeScan::Replay)
+            if (b.flags & (kScanReplay | kScanNearTie)) {
+                // a NaN score, a categorical order that is not total, or a
+                // winner the fixed-point sums cannot certify: the host
+                // replays the node from its histogram (NodeScan::Replay),
+                // which hbr_read_hist gives in the reference's own order
                 o.kind = HBR_SCAN_REPLAY;
                 o.fallback = (b.flags & kScanCatOrder)     ? HBR_FALLBACK_CATEGORICAL_ORDER
                              : (b.flags & kScanCatNaN)     ? HBR_FALLBACK_CATEGORICAL_SCORE
-                                                           : HBR_FALLBACK_NUMERIC_SCORE;
+                             : (b.flags & kScanNumericNaN) ? HBR_FALLBACK_NUMERIC_SCORE
+                                                           : HBR_FALLBACK_NEAR_TIE;
+                if (b.flags & kScanNearTie) e.counters.near_ties++;
                 out[i] = o;
                 continue;
             }
@@ -626,6 +635,7 @@ int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_r
             }
             o.feature = b.feature;
             o.loss_chg = b.loss;
+            o.loss_err = b.err;
             o.left_g = std::ldexp((double)b.left.g, eg);
             o.left_h = std::ldexp((double)b.left.h, eh);
             o.right_g = std::ldexp((double)b.right.g, eg);
@@ -669,8 +679,25 @@ int hbr_scan_categories(hbr_engine *h, uint32_t *out, uint64_t n) {
 
 int hbr_read_hist(hbr_engine *h, uint32_t slot, double *out) {
     return with_engine(h, [&](Engine &e) {
+        if (!out) fail(kInvalid, "read_hist: null output");
+        if (slot >= e.slot_capacity()) fail(kInvalid, "read_hist: no such slot");
+        // in the exact domain the fixed-point bins are the CPU's f64 sums;
+        // beyond it, the slot's rows summed on the device in the CPU's order
+        if (e.sums_exact(e.n_rows())) {
+            dequant_hist(e, e.read_slot(slot), out);
+            return;
+        }
+        if (e.exact_hist(slot, out)) return;
         require_exact(e, e.n_rows(), "read_hist");
         dequant_hist(e, e.read_slot(slot), out);
+    });
+}
+
+int hbr_engine_set_guard(hbr_engine *h, int on, double gamma) {
+    return with_engine(h, [&](Engine &e) {
+        if (!(gamma >= 0.0)) fail(kInvalid, "set_guard: gamma must be a non-negative number");
+        e.guard_on = on != 0;
+        e.guard_gamma = (float)gamma;
     });
 }
 

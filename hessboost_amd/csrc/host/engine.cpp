@@ -724,7 +724,114 @@ uint64_t Engine::begin_tree() {
     identity_rows0_ = true;
     rows0_written_ = false;
     counters.trees++;
+    for (auto &h : slot_history_) h.known = false;
     return ++tree_;
+}
+
+// ---- slot histories (exact-order replays) ---------------------------------------
+
+void Engine::note_built(const std::vector<Segment> &segs, const std::vector<uint32_t> &slots) {
+    for (size_t i = 0; i < segs.size() && i < slots.size(); i++) {
+        if (slots[i] >= slot_history_.size()) slot_history_.resize(slots[i] + 1);
+        SlotHistory &h = slot_history_[slots[i]];
+        h.known = true;
+        h.built = segs[i];
+        h.minus.clear();
+        h.rows = segs[i].len;
+    }
+}
+
+void Engine::note_siblings(const std::vector<uint32_t> &parents, const std::vector<uint32_t> &built) {
+    for (size_t i = 0; i < parents.size() && i < built.size(); i++) {
+        const uint32_t p = parents[i], b = built[i];
+        if (p >= slot_history_.size()) slot_history_.resize(p + 1);
+        SlotHistory &h = slot_history_[p];
+        const bool ok = h.known && b < slot_history_.size() && slot_history_[b].known &&
+                        slot_history_[b].minus.empty() && slot_history_[b].rows <= h.rows;
+        if (!ok) {
+            h.known = false;
+            continue;
+        }
+        h.minus.push_back(slot_history_[b].built);
+        h.rows -= slot_history_[b].rows;
+    }
+}
+
+uint32_t Engine::slot_rows(uint32_t slot) const {
+    return slot < slot_history_.size() && slot_history_[slot].known ? slot_history_[slot].rows : 0u;
+}
+
+void Engine::exact_segment(const Segment &sg, double *out_dev) {
+    hipStream_t s = dev_.stream();
+    const uint64_t m = sg.len;
+    ExactArgs a{};
+    bool contig = contiguous(sg);
+    if (!contig) {
+        write_identity_rows();
+        a.rows = rows_[sg.buf].get() + sg.offset;
+        if (m > 1) {
+            // the CPU sweeps a node whose rows are one ascending range by
+            // feature (contiguous_range, tree/hist/mod.rs:420-428)
+            uint32_t ends[2];
+            HBR_HIP(hipMemcpyAsync(&ends[0], a.rows, 4, hipMemcpyDeviceToHost, s));
+            HBR_HIP(hipMemcpyAsync(&ends[1], a.rows + m - 1, 4, hipMemcpyDeviceToHost, s));
+            dev_.sync();
+            contig = ends[1] - ends[0] == m - 1;
+        }
+    }
+    // sum_order (tree/hist/mod.rs:411-419): one chain, or len / 4096 blocks
+    constexpr uint64_t kParallelThreshold = 8192, kRowsPerTask = 4096, kGatherMaxRows = 1u << 18;
+    uint64_t grain = m ? m : 1;
+    if (!(m < kParallelThreshold || (dense_ && (contig || n_rows_ <= kGatherMaxRows)))) {
+        const uint64_t blocks = m / kRowsPerTask;
+        grain = (m + blocks - 1) / blocks;
+    }
+    const uint64_t blocks = m ? (m + grain - 1) / grain : 0;
+    const uint64_t wave = std::max<uint64_t>(1, std::min<uint64_t>(blocks, (uint64_t)dev_.cu_count()));
+    const uint64_t words = 2ull * total_bins_;
+    d_exact_.reserve(wave * words);
+    a.first = sg.offset;  // an identity run: rows offset .. offset + m - 1
+    a.m = (uint32_t)m;
+    a.grain = (uint32_t)grain;
+    a.bins8 = rows8_.get();
+    a.stride = stride_;
+    a.n_cols = n_cols_;
+    a.feature_offset = d_fo_.get();
+    a.row_pairs = row_pairs_live_ && stride_ == 32 ? 1u : 0u;
+    a.gpair = a.row_pairs ? nullptr : pairs();
+    a.min_hess = row_pairs_min_hess_;
+    a.masked = masked_ ? 1u : 0u;
+    a.total_bins = total_bins_;
+    a.partial = d_exact_.get();
+    if (blocks == 0) HBR_HIP(hipMemsetAsync(out_dev, 0, words * sizeof(double), s));
+    for (uint64_t b0 = 0; b0 < blocks; b0 += wave) {
+        const uint32_t nb = (uint32_t)std::min<uint64_t>(wave, blocks - b0);
+        a.blk0 = (uint32_t)b0;
+        dev_.launch("hbr_hist_exact", dim3(nb), dim3(kExactThreads), a);
+        ExactSumArgs c{d_exact_.get(), nb, b0 == 0 ? 1u : 0u, out_dev, (uint32_t)words, nullptr};
+        dev_.launch("hbr_hist_exact_sum", dim3(ceil_div(words, 256)), dim3(256), c);
+    }
+}
+
+bool Engine::exact_hist(uint32_t slot, double *out) {
+    if (slot >= slot_history_.size() || !slot_history_[slot].known) return false;
+    if (!dense_u8_ || n_cols_ == 0 || n_cols_ > kExactThreads || 2ull * total_bins_ > kExactMaxWords) return false;
+    if (level_pairs_ || softmax_staged()) return false;  // per-class pairs: one tree's pairs only
+    if (!(row_pairs_live_ && stride_ == 32) && (pair_array_stale_ || !pairs_staged())) return false;
+    const SlotHistory h = slot_history_[slot];
+    const uint64_t words = 2ull * total_bins_;
+    d_exact_out_.reserve(words);
+    exact_segment(h.built, d_exact_out_.get());
+    if (!h.minus.empty()) d_exact_minus_.reserve(words);
+    for (const Segment &sg : h.minus) {
+        // the sibling: parent - built, bin by bin in f64
+        exact_segment(sg, d_exact_minus_.get());
+        ExactSumArgs c{nullptr, 0, 0, d_exact_out_.get(), (uint32_t)words, d_exact_minus_.get()};
+        dev_.launch("hbr_hist_exact_sum", dim3(ceil_div(words, 256)), dim3(256), c);
+    }
+    d_exact_out_.download(out, words, dev_.stream());
+    dev_.sync();
+    return true;
 }
 
 void Engine::write_identity_rows() {
@@ -796,6 +903,7 @@ void Engine::launch_root(const Segment &seg, uint32_t slot, float lower, float u
     n.lower = lower;
     n.upper = upper;
     n.pad = kScanDeviceRoot;
+    n.rows = seg.len;
     struct RootIn {
         HistNode h;
         ScanNode s;
@@ -825,6 +933,7 @@ bool Engine::grow_root(const Segment &seg, uint32_t slot, float lower, float upp
     dev_.sync();
     *best = rb->best;
     *total = rb->total;
+    if (best->flags & kScanNearTie) counters.near_ties++;
     if (best_set && set) std::memcpy(best_set, set, kCatWords * sizeof(uint32_t));
     const QScale host = rb->scale;
     stage_.reset();
@@ -1032,6 +1141,8 @@ void Engine::launch_scan(const ScanNode *nodes_dev, uint32_t n, const PartSplit 
     a.scale = level_scale_ ? level_scale_ : scale_dev();
     a.reg = scan_params_;
     a.dense = dense_ ? 1u : 0u;
+    a.guard = guard_active ? 1u : 0u;
+    a.gamma = guard_gamma;
     a.per_feature = d_per_feature_.get();
     a.best = best_dev;
     a.root_total = level_totals_ ? level_totals_ : total_dev();
@@ -1079,6 +1190,8 @@ std::vector<ScanBest> Engine::scan(const std::vector<ScanInput> &in, std::vector
         n.root_gain = in[i].root_gain;
         n.lower = in[i].lower;
         n.upper = in[i].upper;
+        const uint32_t known = slot_rows(in[i].slot);
+        n.rows = in[i].rows ? in[i].rows : known ? known : (uint32_t)n_rows_;
         nodes[i] = n;
     }
     ScanBest *staged = static_cast<ScanBest *>(stage_.alloc(in.size() * sizeof(ScanBest)));
@@ -1245,6 +1358,7 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
             R.slot = built_left ? splits[i].parent_slot : fresh[i];
             L.best = best_staged[2 * i];
             R.best = best_staged[2 * i + 1];
+            counters.near_ties += ((L.best.flags & kScanNearTie) ? 1u : 0u) + ((R.best.flags & kScanNearTie) ? 1u : 0u);
             if (n_cat_) {
                 const uint32_t *sets = reinterpret_cast<const uint32_t *>(host_out + o_sets);
                 std::memcpy(L.best_set.data(), sets + (size_t)(2 * i) * kCatWords, kCatWords * sizeof(uint32_t));
@@ -1306,6 +1420,7 @@ void Engine::launch_device_roots(uint32_t n_trees) {
             r.lower = -std::numeric_limits<float>::infinity();
             r.upper = std::numeric_limits<float>::infinity();
             r.pad = kScanDeviceRoot | (t << kScanClassShift);
+            r.rows = (uint32_t)n_rows_;
             sn[t] = r;
         }
         d_root_in_.resize(bytes);
@@ -1531,6 +1646,7 @@ Engine::TreeState Engine::finish_device_forest(const TreeTicket &t, std::vector<
             counters.hist_rows += gc.hist_rows;
             counters.hist_bytes += hist_bytes(gc.hist_rows, true);
             counters.partition_rows += gc.part_rows;
+            counters.near_ties += gc.near_ties;
         }
         if (t.check && th.scale.nonfinite != 0) st = kTreeNotFinite;
         if (t.check && k == 0 && t.n_trees == 1 && st == kTreeOk) scale_host_ = th.scale;

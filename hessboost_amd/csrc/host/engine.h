@@ -58,6 +58,7 @@ struct ScanInput {
     uint32_t slot;
     QBin total;
     float root_gain, lower, upper;
+    uint32_t rows = 0;  // the node's row count (0: from the slot's segment, else every row)
 };
 
 class Engine {
@@ -148,6 +149,7 @@ public:
     // lossless). False when the staged pairs' grains are not known (the
     // trainer's fused rounds, softmax classes).
     bool sums_exact(uint64_t m) const;
+    uint32_t slot_capacity() const { return slot_cap_; }
     // The trait's contract for build / histograms / root_total / the
     // resident scan: when set, they refuse outside the exact domain.
     bool exact_sums_only = true;
@@ -277,6 +279,27 @@ public:
     void set_scan_params(const ScanParams &p, const std::vector<int8_t> &monotone);
 
     hbr_engine_counters counters{};
+    // ---- the fixed-point guard and exact-order replays ---------------------------
+    // The guard bounds every candidate's score error and flags the nodes it
+    // cannot certify (kScanNearTie); gamma is the caller's split threshold.
+    bool guard_on = true;
+    float guard_gamma = 0.0f;
+    bool guard_active = false;  // the next scans bound their candidates
+    // How each histogram slot of the current tree came about through the row
+    // engine's calls: built from a segment's rows, then (a sibling kept in
+    // its parent's slot) minus the built children's sums, in order.
+    void note_built(const std::vector<Segment> &segs, const std::vector<uint32_t> &slots);
+    void note_siblings(const std::vector<uint32_t> &parents, const std::vector<uint32_t> &built);
+    uint32_t slot_rows(uint32_t slot) const;  // the node's row count (0: unknown)
+    // The histogram of `slot` as the reference's CPU builder has it: each
+    // built node's bins summed in the CPU build's own f64 order (each bin's
+    // rows in row order from +0.0, in the blocks of sum_order;
+    // tree/hist/mod.rs:399-607) and a sibling's as its parent's minus the
+    // built child's (with_sibling, builder/partition.rs:244-256), computed
+    // on the device from the staged pairs; false when the slot's history is
+    // unknown or the index is not row-major u8 (out: 2 x total_bins, g and
+    // h interleaved).
+    bool exact_hist(uint32_t slot, double *out);
     // algorithmic bytes of summing `rows` rows into a histogram
     uint64_t hist_bytes(uint64_t rows, bool gathered) const;
 
@@ -290,6 +313,17 @@ private:
     DBuf<uint32_t> csr_ranges_;  // each CSR row's first entry of every histogram bin range
     void ensure_rows();
     bool contiguous(const Segment &sg) const;
+    struct SlotHistory {
+        bool known = false;
+        Segment built;               // the segment first summed into the slot
+        std::vector<Segment> minus;  // then subtracted from it, in order
+        uint32_t rows = 0;
+    };
+    std::vector<SlotHistory> slot_history_;
+    void exact_segment(const Segment &sg, double *out_dev);  // one node's CPU-order sums into out_dev
+    DBuf<double> d_exact_;
+    DBuf<double> d_exact_out_;
+    DBuf<double> d_exact_minus_;
     bool identity_rows0_ = false;
     bool rows0_written_ = false;
     void write_identity_rows();  // buffer 0 := 0..n-1, once per tree, when a row list is read

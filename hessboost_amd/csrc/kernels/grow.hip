@@ -116,6 +116,7 @@ __device__ __forceinline__ void grow_decide(const GrowArgs &a) {
         c0.error = 0;
         c0.hist_rows = 0;
         c0.part_rows = 0;
+        c0.near_ties = 0;
     }
     const uint32_t n_front = c0.n_front, node_base = c0.n_nodes;
     const int eg1 = BATCHED ? 0 : a.scale->exp_g, eh1 = BATCHED ? 0 : a.scale->exp_h;
@@ -124,6 +125,7 @@ __device__ __forceinline__ void grow_decide(const GrowArgs &a) {
 
     uint32_t split_carry = 0, tile_carry = 0;
     unsigned long long hist_rows = 0, part_rows = 0;
+    uint32_t near_ties = 0;
     for (uint32_t base = 0; base < n_front; base += kGrowThreads) {
         const uint32_t j = base + tid;
         const bool active = j < n_front;
@@ -163,6 +165,7 @@ __device__ __forceinline__ void grow_decide(const GrowArgs &a) {
                 hist_rows += po.built_left ? nl : sp.seg.len - nl;
             }
         }
+        if (active && (b.flags & kScanNearTie)) near_ties++;
         const int eg = BATCHED ? s_exp[active ? tree : 0u].x : eg1, eh = BATCHED ? s_exp[active ? tree : 0u].y : eh1;
         GrowTreeNode *records = BATCHED ? tree_of(a, tree) : a.tree;
         const double ng = dequant(total.g, eg), nh = dequant(total.h, eh);
@@ -355,27 +358,33 @@ __device__ __forceinline__ void grow_decide(const GrowArgs &a) {
             for (uint32_t t = tid; t < n_trees; t += kGrowThreads) a.tree_nodes[t] = s_base[t] + 2 * s_nsplit[t];
     }
     // per-thread row counts of the previous level's splits
-    __shared__ unsigned long long s_rows[2][kGrowThreads / kWave];
+    __shared__ unsigned long long s_rows[3][kGrowThreads / kWave];
+    unsigned long long nt = near_ties;
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
         hist_rows += __shfl_xor(hist_rows, d, kWave);
         part_rows += __shfl_xor(part_rows, d, kWave);
+        nt += __shfl_xor(nt, d, kWave);
     }
     if (lane_id() == 0) {
         s_rows[0][tid / kWave] = hist_rows;
         s_rows[1][tid / kWave] = part_rows;
+        s_rows[2][tid / kWave] = nt;
     }
     __syncthreads();
     if (tid == 0) {
-        unsigned long long hr = 0, pr = 0;
+        unsigned long long hr = 0, pr = 0, ties = 0;
         for (uint32_t w = 0; w < kGrowThreads / kWave; w++) {
             hr += s_rows[0][w];
             pr += s_rows[1][w];
+            ties += s_rows[2][w];
         }
         a.counts->hist_rows = c0.hist_rows + hr;
         a.counts->part_rows = c0.part_rows + pr;
+        a.counts->near_ties = c0.near_ties + (uint32_t)ties;
         s_final.hist_rows = c0.hist_rows + hr;
         s_final.part_rows = c0.part_rows + pr;
+        s_final.near_ties = c0.near_ties + (uint32_t)ties;
     }
     // each tree's header: its scale and node count, and the level counts
     // (a batch's totals)

@@ -497,3 +497,80 @@ extern "C" __global__ __launch_bounds__(256) void hbr_subtract(SubArgs a) {
     }
 }
 
+
+// ---- the reference's CPU sum order (replays) -----------------------------------
+// Each bin is the f64 chain of its rows' f32 values in row order, from +0.0,
+// within each block of `grain` rows (builder order of tree/hist/mod.rs:
+// accumulate, accumulate_blocks); thread f walks the block's rows and adds
+// into feature f's bins only, so no bin has two writers. Rows are fetched
+// eight at a time ahead of the adds.
+extern "C" __global__ __launch_bounds__(kExactThreads) void hbr_hist_exact(ExactArgs a) {
+    __shared__ double s_h[kExactMaxWords];
+    const uint32_t words = 2u * a.total_bins;
+    for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) s_h[i] = 0.0;
+    __syncthreads();
+    const uint32_t blk = a.blk0 + blockIdx.x;
+    const uint32_t start = blk * a.grain;
+    const uint32_t end = min(a.m, start + a.grain);
+    const uint32_t f = threadIdx.x;
+    if (f < a.n_cols) {
+        const uint32_t base = a.feature_offset[f];
+        constexpr uint32_t kAhead = 8;
+        for (uint32_t j0 = start; j0 < end; j0 += kAhead) {
+            uint32_t bin[kAhead], mask[kAhead];
+            GPair p[kAhead];
+#pragma unroll
+            for (uint32_t k = 0; k < kAhead; k++) {
+                const uint32_t j = j0 + k;
+                bin[k] = 0;
+                mask[k] = 1u;
+                p[k] = GPair{0.0f, 0.0f};
+                if (j >= end) continue;
+                const uint32_t r = a.rows ? a.rows[j] : a.first + j;
+                const uint8_t *row = a.bins8 + (size_t)r * a.stride;
+                bin[k] = row[f];
+                const uint32_t word = *reinterpret_cast<const uint32_t *>(row + 4 * kMaskWord);
+                mask[k] = a.masked ? (word >> f) & 1u : 0u;
+                if (a.row_pairs) {
+                    const float pv = __uint_as_float(word & 0x7fffffffu);
+                    const float y = (word >> 31) ? 1.0f : 0.0f;
+                    const float q = pv * (1.0f - pv);
+                    p[k] = GPair{(pv - y) * 1.0f, (q > a.min_hess ? q : a.min_hess) * 1.0f};
+                } else {
+                    p[k] = a.gpair[r];
+                }
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kAhead; k++) {
+                if (mask[k]) continue;
+                const uint32_t at = 2u * (base + bin[k]);
+                s_h[at] += (double)p[k].g;
+                s_h[at + 1] += (double)p[k].h;
+            }
+        }
+    }
+    __syncthreads();
+    double *dst = a.partial + (size_t)blockIdx.x * words;
+    for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) dst[i] = s_h[i];
+}
+
+// out = block 0's partial (first launch) then + each later block's, in order;
+// or out -= minus (a sibling's bins from its parent's and the built child's).
+extern "C" __global__ __launch_bounds__(256) void hbr_hist_exact_sum(ExactSumArgs a) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    if (a.minus) {
+        a.out[i] = a.out[i] - a.minus[i];
+        return;
+    }
+    uint32_t k = 0;
+    double v;
+    if (a.first) {
+        v = a.partial[i];
+        k = 1;
+    } else {
+        v = a.out[i];
+    }
+    for (; k < a.n_blocks; k++) v += a.partial[(size_t)k * a.n + i];
+    a.out[i] = v;
+}

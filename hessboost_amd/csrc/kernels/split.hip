@@ -63,11 +63,132 @@ __device__ __forceinline__ bool score(double lg, double lh, double rg, double rh
     return true;
 }
 
+// ---- the near-tie guard -------------------------------------------------------
+// A candidate's children are fixed-point sums; the reference scores the same
+// candidate from f64 chain sums of the same rows. Their difference per child
+// is bounded by the quantisation of each row (half a unit) plus the chain's
+// rounding (Higham: k u / (1 - k u) times the sum of |x| for k additions; a
+// child's sum is its bins' chains added bin by bin, k <= m + 512; the sum
+// of |x| is at most m max|x|), twice over for the right child (total minus
+// left). Candidates with equal fixed-point sums are one partition: they can
+// differ only by rows whose pairs quantise to zero (below half a unit,
+// 2^-62 / n of the largest pair), which moves a score by less than one f32
+// rounding in all but a vanishing share of cases. From those
+// bounds the error of each child's gain follows through the weight (itself
+// rounded to f32, clamped by max_delta_step and the monotone bounds, both
+// 1-Lipschitz) and the gain; each f32 rounding of the score adds one spacing.
+struct Bound {
+    double dg, dh;  // sums of one node's rows
+};
+
+// An upper bound on one f32 rounding step at |x|.
+__device__ __forceinline__ double ulp32(double x) { return __builtin_fabs(x) * 0x1p-23 + 0x1p-149; }
+
+__device__ __forceinline__ Bound node_bound(uint32_t m, int eg, int eh, float max_g, float max_h) {
+    const double md = (double)m;
+    // a child's sum is its bins' chains added bin by bin: at most m + 512 additions
+    const double chain = (md + 512.0) * 0x1p-53;
+    const double gamma_m = chain < 0.5 ? chain / (1.0 - chain) : 1e300;
+    return Bound{md * __builtin_ldexp(1.0, eg - 1) + gamma_m * md * (double)max_g,
+                 md * __builtin_ldexp(1.0, eh - 1) + gamma_m * md * (double)max_h};
+}
+
+// Error bound of one child's gain at weight w (before the gain's f32 rounding),
+// and the weight's own error through *dw.
+__device__ __forceinline__ double gain_err(double g, double h, float w, double dg, double dh, const ScanParams &r,
+                                           double *dw_out) {
+    const double hl = h + r.lambda;
+    const double den = hl - dh;
+    const double aw = __builtin_fabs((double)w);
+    const double dw = (den > 0.0 ? (dg + aw * dh) / den : 1e300) + 2.0 * ulp32(aw);
+    const double slope = 2.0 * __builtin_fabs(g + hl * (double)w) + 2.0 * r.alpha;
+    *dw_out = dw;
+    return 2.0 * aw * dg + aw * aw * dh + (slope + hl * dw) * dw;
+}
+
+// The guarded score of one candidate: `ok` as score() decides it; `rival`
+// when the reference might offer it (ok, or within the error of the
+// min_child_weight and monotone tests); `fragile` when ok but within that
+// error of failing them; the score and its error bound.
+struct Scored {
+    bool ok, rival, fragile;
+    float loss;
+    float err;
+};
+
+__device__ __forceinline__ Scored score_guarded(double lg, double lh, double rg, double rh, const ScanParams &r,
+                                                float lower, float upper, int dir, float root_gain, const Bound &b) {
+    Scored o{false, false, false, 0.0f, 0.0f};
+    if (!(lh > 0.0 && rh > 0.0)) return o;
+    const double dgl = b.dg, dhl = b.dh;
+    const double dgr = 2.0 * b.dg + __builtin_fabs(rg) * 0x1p-52, dhr = 2.0 * b.dh + rh * 0x1p-52;
+    const bool mcw_ok = lh >= r.min_child_weight && rh >= r.min_child_weight;
+    const bool mcw_near = lh + dhl >= r.min_child_weight && rh + dhr >= r.min_child_weight;
+    const bool mcw_edge = lh - dhl < r.min_child_weight || rh - dhr < r.min_child_weight;
+    if (!mcw_near) return o;
+    const float wl = bounded_weight(lg, lh, r, lower, upper);
+    const float wr = bounded_weight(rg, rh, r, lower, upper);
+    double dwl, dwr;
+    const double el = gain_err(lg, lh, wl, dgl, dhl, r, &dwl);
+    const double er = gain_err(rg, rh, wr, dgr, dhr, r, &dwr);
+    const double slack = dwl + dwr;
+    bool mono_ok = true, mono_near = true, mono_edge = false;
+    if (dir > 0) {
+        mono_ok = (double)wl <= (double)wr;
+        mono_near = (double)wl <= (double)wr + slack;
+        mono_edge = (double)wr - (double)wl <= slack;
+    } else if (dir < 0) {
+        mono_ok = (double)wl >= (double)wr;
+        mono_near = (double)wl + slack >= (double)wr;
+        mono_edge = (double)wl - (double)wr <= slack;
+    }
+    if (!mono_near) return o;
+    const float gl = (float)gain_at(lg, lh, r, wl), gr = (float)gain_at(rg, rh, r, wr);
+    const float gain = gl + gr;
+    o.loss = gain - root_gain;
+    o.ok = mcw_ok && mono_ok;
+    o.rival = true;
+    o.fragile = o.ok && (mcw_edge || (dir != 0 && mono_edge));
+    const double e = el + er + ulp32(gl) + ulp32(gr) + ulp32(gain) + ulp32(o.loss);
+    o.err = (float)(e * (1.0 + 0x1p-20));
+    return o;
+}
+
+// The two highest (score + error) of a lane's rival candidates whose left
+// sums differ: `top` with its sums, `second` the best of any other sums.
+struct Rivals {
+    float top, second;
+    int64_t tg, th;
+    __device__ __forceinline__ void init() {
+        top = second = -__builtin_inff();
+        tg = th = INT64_MIN;
+    }
+    __device__ __forceinline__ void offer(float v, int64_t g, int64_t h) {
+        if (!(v > -__builtin_inff()) || __builtin_isnan(v)) return;
+        if (g == tg && h == th) {
+            if (v > top) top = v;
+        } else if (v > top) {
+            second = top;
+            top = v;
+            tg = g;
+            th = h;
+        } else if (v > second) {
+            second = v;
+        }
+    }
+    // the best of the candidates whose sums differ from (g, h)
+    __device__ __forceinline__ float excluding(int64_t g, int64_t h) const {
+        return (g == tg && h == th) ? second : top;
+    }
+};
+
 struct Cand {
     float loss;
     uint32_t idx;
     int64_t lg, lh, rg, rh;
     uint32_t backward;
+    float err;
+    uint32_t fragile;
 };
 
 __device__ __forceinline__ bool better(float la, uint32_t ia, float lb, uint32_t ib) {
@@ -75,7 +196,8 @@ __device__ __forceinline__ bool better(float la, uint32_t ia, float lb, uint32_t
 }
 
 __device__ __forceinline__ void offer(Cand &best, bool &nan_seen, float loss, uint32_t idx, int64_t lg,
-                                      int64_t lh, int64_t rg, int64_t rh, uint32_t backward) {
+                                      int64_t lh, int64_t rg, int64_t rh, uint32_t backward, float err = 0.0f,
+                                      uint32_t fragile = 0u) {
     if (__builtin_isnan(loss)) {
         nan_seen = true;
         return;
@@ -89,6 +211,8 @@ __device__ __forceinline__ void offer(Cand &best, bool &nan_seen, float loss, ui
         best.rg = rg;
         best.rh = rh;
         best.backward = backward;
+        best.err = err;
+        best.fragile = fragile;
     }
 }
 
@@ -111,7 +235,25 @@ using namespace hbr;
 // by one lane. BPL bins per lane and pass: 4 (chunks of 256 bins), or 1 for
 // a feature of at most 64 bins, whose lanes would otherwise idle; the
 // candidates, and the (highest loss, lowest index) winner, are the same.
-template <uint32_t BPL>
+// A node's row count: its record's, or the partition's for a child of a split.
+__device__ __forceinline__ uint32_t node_rows(const ScanArgs &a, const ScanNode &nd) {
+    if (!nd.from_split) return nd.rows;
+    const uint32_t left = a.part_out[nd.split].left_len;
+    return nd.child == 0 ? left : a.splits[nd.split].seg.len - left;
+}
+
+// x rounded up to f32.
+__device__ __forceinline__ float up32(double x) {
+    float f = (float)x;
+    if ((double)f < x) {  // the next f32 above
+        uint32_t b = __float_as_uint(f);
+        b = f == 0.0f ? 1u : (f > 0.0f ? b + 1u : b - 1u);
+        f = __uint_as_float(b);
+    }
+    return f;
+}
+
+template <uint32_t BPL, bool GUARD>
 __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, uint32_t f, ScanBest *out) {
     const uint32_t lane = lane_id();
     const ScanNode nd = a.nodes[node];
@@ -121,7 +263,12 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
     best.idx = 0xffffffffu;
     best.lg = best.lh = best.rg = best.rh = 0;
     best.backward = 0;
+    best.err = 0.0f;
+    best.fragile = 0;
     bool nan_seen = false;
+    Rivals riv;
+    riv.init();
+    Bound bound{0.0, 0.0};
     const QBin *h = a.hist + (size_t)node_slot(a, nd) * a.total_bins + fs;
     const bool dev_root = (nd.pad & kScanDeviceRoot) != 0;
     const uint32_t cls = nd.pad >> kScanClassShift;
@@ -153,6 +300,9 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
         const int dir = a.monotone ? (int)a.monotone[f] : 0;
         const float root_gain = dev_root ? node_gain(dequant(tg, eg), dequant(th, eh), a.reg, nd.lower, nd.upper)
                                          : nd.root_gain;
+        if (GUARD)
+            bound = node_bound(node_rows(a, nd), eg, eh, __uint_as_float(a.scale[cls].max_g_bits),
+                               __uint_as_float(a.scale[cls].max_h_bits));
         int64_t carry_g = 0, carry_h = 0;
         // forward pass: bins <= b left, missing right
         for (uint32_t c0 = 0; c0 < nb; c0 += kWave * BPL) {
@@ -174,9 +324,16 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
                 if (b0 + k >= nb) break;
                 const int64_t ag = xg + sg[k], ah = xh + sh[k];
                 float loss;
-                if (score(dequant(ag, eg), dequant(ah, eh), dequant(tg - ag, eg), dequant(th - ah, eh),
-                          a.reg, nd.lower, nd.upper, dir, root_gain, &loss))
+                if (GUARD) {
+                    const Scored sc = score_guarded(dequant(ag, eg), dequant(ah, eh), dequant(tg - ag, eg),
+                                                    dequant(th - ah, eh), a.reg, nd.lower, nd.upper, dir, root_gain,
+                                                    bound);
+                    if (sc.ok) offer(best, nan_seen, sc.loss, b0 + k, ag, ah, tg - ag, th - ah, 0, sc.err, sc.fragile);
+                    if (sc.rival) riv.offer(up32((double)sc.loss + (double)sc.err), ag, ah);
+                } else if (score(dequant(ag, eg), dequant(ah, eh), dequant(tg - ag, eg), dequant(th - ah, eh), a.reg,
+                                 nd.lower, nd.upper, dir, root_gain, &loss)) {
                     offer(best, nan_seen, loss, b0 + k, ag, ah, tg - ag, th - ah, 0);
+                }
             }
             carry_g += wave_broadcast(ig, kWave - 1);
             carry_h += wave_broadcast(ih, kWave - 1);
@@ -205,9 +362,18 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
                     if (o >= nb) break;
                     const int64_t sgv = fg - (xg + eg_[k]), shv = fh - (xh + eh_[k]);  // suffix from bin o
                     float loss;
-                    if (score(dequant(tg - sgv, eg), dequant(th - shv, eh), dequant(sgv, eg), dequant(shv, eh),
-                              a.reg, nd.lower, nd.upper, dir, root_gain, &loss))
+                    if (GUARD) {
+                        const Scored sc = score_guarded(dequant(tg - sgv, eg), dequant(th - shv, eh), dequant(sgv, eg),
+                                                        dequant(shv, eh), a.reg, nd.lower, nd.upper, dir, root_gain,
+                                                        bound);
+                        if (sc.ok)
+                            offer(best, nan_seen, sc.loss, nb + (nb - 1 - o), tg - sgv, th - shv, sgv, shv, 1, sc.err,
+                                  sc.fragile);
+                        if (sc.rival) riv.offer(up32((double)sc.loss + (double)sc.err), tg - sgv, th - shv);
+                    } else if (score(dequant(tg - sgv, eg), dequant(th - shv, eh), dequant(sgv, eg),
+                                     dequant(shv, eh), a.reg, nd.lower, nd.upper, dir, root_gain, &loss)) {
                         offer(best, nan_seen, loss, nb + (nb - 1 - o), tg - sgv, th - shv, sgv, shv, 1);
+                    }
                 }
                 carry_g += wave_broadcast(ig, kWave - 1);
                 carry_h += wave_broadcast(ih, kWave - 1);
@@ -228,6 +394,15 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
     }
     const uint64_t any_nan = __ballot(nan_seen);
     const uint64_t mine = __ballot(best.idx == bi && best.loss == bl && bi != 0xffffffffu);
+    // the feature's rivals: every other partition of the node's rows it offers
+    float rival = -__builtin_inff();
+    if (GUARD) {
+        const int owner = mine ? __ffsll((unsigned long long)mine) - 1 : 0;
+        const int64_t wg = __shfl(best.lg, owner, kWave), wh = __shfl(best.lh, owner, kWave);
+        rival = mine ? riv.excluding(wg, wh) : riv.top;
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) rival = fmaxf(rival, __shfl_xor(rival, d, kWave));
+    }
     if (mine == 0) {
         if (lane == 0) {
             ScanBest o;
@@ -237,6 +412,8 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
             o.flags = any_nan ? kScanNumericNaN : 0u;
             o.left = QBin{0, 0};
             o.right = QBin{0, 0};
+            o.err = 0.0f;
+            o.rival = rival;
             *out = o;
         }
     } else if (lane == (uint32_t)(__ffsll((unsigned long long)mine) - 1)) {
@@ -244,9 +421,11 @@ __device__ __forceinline__ void scan_feature(const ScanArgs &a, uint32_t node, u
         o.loss = bl;
         o.feature = f;
         o.index = bi;
-        o.flags = best.backward | (any_nan ? kScanNumericNaN : 0u);
+        o.flags = best.backward | (any_nan ? kScanNumericNaN : 0u) | (best.fragile ? kScanNearTie : 0u);
         o.left = QBin{best.lg, best.lh};
         o.right = QBin{best.rg, best.rh};
+        o.err = best.err;
+        o.rival = rival;
         *out = o;
     }
 }
@@ -256,10 +435,17 @@ extern "C" __global__ __launch_bounds__(256) void hbr_scan_features(ScanArgs a) 
     const uint32_t pair = blockIdx.x * (blockDim.x / kWave) + wave;
     if (pair >= scan_nodes(a) * a.n_features) return;  // uniform per wave
     const uint32_t f = pair % a.n_features;
-    if (a.feature_offset[f + 1] - a.feature_offset[f] <= kWave)  // uniform per wave
-        scan_feature<1>(a, pair / a.n_features, f, a.per_feature + pair);
-    else
-        scan_feature<4>(a, pair / a.n_features, f, a.per_feature + pair);
+    const bool narrow = a.feature_offset[f + 1] - a.feature_offset[f] <= kWave;  // uniform per wave
+    if (a.guard) {
+        if (narrow)
+            scan_feature<1, true>(a, pair / a.n_features, f, a.per_feature + pair);
+        else
+            scan_feature<4, true>(a, pair / a.n_features, f, a.per_feature + pair);
+    } else if (narrow) {
+        scan_feature<1, false>(a, pair / a.n_features, f, a.per_feature + pair);
+    } else {
+        scan_feature<4, false>(a, pair / a.n_features, f, a.per_feature + pair);
+    }
 }
 
 // The feature-order merge of a node's per-feature winners (`per_node`,
@@ -276,7 +462,7 @@ __device__ __forceinline__ bool merge_better(float ol, uint32_t of, float bl, ui
 }
 
 __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, const ScanBest *per_node) {
-    __shared__ float s_loss[kMergeThreads / kWave];
+    __shared__ float s_loss[kMergeThreads / kWave], s_rival[kMergeThreads / kWave];
     __shared__ uint32_t s_feat[kMergeThreads / kWave], s_nan[kMergeThreads / kWave];
     const uint32_t lane = lane_id(), wave = threadIdx.x / kWave;
     float bl = 0.0f;
@@ -307,7 +493,8 @@ __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, con
         s_nan[wave] = nan_flag;
     }
     __syncthreads();
-    if (wave != 0) return;
+    // every wave reduces the waves' bests (the same four records), so all
+    // threads know the winner for the guard's pass over the rivals
     bl = lane < kMergeThreads / kWave ? s_loss[lane] : 0.0f;
     bf = lane < kMergeThreads / kWave ? s_feat[lane] : 0xffffffffu;
     nan_flag = lane < kMergeThreads / kWave ? s_nan[lane] : 0u;
@@ -321,6 +508,30 @@ __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, con
             bf = of;
         }
     }
+    bf = (uint32_t)__shfl((int)bf, 0, kWave);
+    nan_flag = (uint32_t)__shfl((int)nan_flag, 0, kWave);
+    float rival = -__builtin_inff();
+    if (a.guard) {
+        // the best score + error bound of any other partition of the node's rows
+        const bool has = bf != 0xffffffffu;
+        const int64_t wg = has ? per_node[bf].left.g : 0, wh = has ? per_node[bf].left.h : 0;
+        for (uint32_t f = threadIdx.x; f < a.n_features; f += kMergeThreads) {
+            const ScanBest c = per_node[f];
+            float v = c.rival;
+            const bool same = has && c.index != 0xffffffffu && c.left.g == wg && c.left.h == wh;
+            if (c.index != 0xffffffffu && !same && f != bf) v = fmaxf(v, up32((double)c.loss + (double)c.err));
+            rival = fmaxf(rival, v);
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) rival = fmaxf(rival, __shfl_xor(rival, d, kWave));
+        __syncthreads();  // the first reduction's records are read
+        if (lane == 0) s_rival[wave] = rival;
+        __syncthreads();
+        rival = -__builtin_inff();
+#pragma unroll
+        for (uint32_t w = 0; w < kMergeThreads / kWave; w++) rival = fmaxf(rival, s_rival[w]);
+    }
+    if (wave != 0) return;
     if (lane == 0) {
         ScanBest o;
         if (bf == 0xffffffffu) {
@@ -330,14 +541,45 @@ __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, con
             o.flags = nan_flag;
             o.left = QBin{0, 0};
             o.right = QBin{0, 0};
+            o.err = 0.0f;
         } else {
             o = per_node[bf];
             o.flags |= nan_flag;
         }
+        o.rival = rival;
+        if (a.guard) {
+            // certified when no rival can reach the winner's lower bound and
+            // the winner (or, with none, the best rival) stays on one side of
+            // the validity threshold (loss > kRtEps and loss >= gamma), the
+            // node's own gain included (the root gain is its rounded gain)
+            const ScanNode nd = a.nodes[node];
+            const uint32_t cls = nd.pad >> kScanClassShift;
+            const int eg = a.scale[cls].exp_g, eh = a.scale[cls].exp_h;
+            const Bound b = node_bound(node_rows(a, nd), eg, eh, __uint_as_float(a.scale[cls].max_g_bits),
+                                       __uint_as_float(a.scale[cls].max_h_bits));
+            const bool dev_root = (nd.pad & kScanDeviceRoot) != 0;
+            const QBin t = dev_root ? a.root_total[cls] : nd.total;
+            const double tg = dequant(t.g, eg), th = dequant(t.h, eh);
+            const float w = bounded_weight(tg, th, a.reg, nd.lower, nd.upper);
+            double dw;
+            const double e_root = th > 0.0 ? gain_err(tg, th, w, b.dg, b.dh, a.reg, &dw) + 2.0 * ulp32(gain_at(tg, th, a.reg, w))
+                                           : 0.0;
+            const double thr = fmax(1e-6, (double)a.gamma);
+            bool near;
+            if (bf == 0xffffffffu) {
+                near = (double)rival + e_root >= thr;
+            } else {
+                const double lo = (double)o.loss - (double)o.err - e_root, hi = (double)o.loss + (double)o.err + e_root;
+                const bool splits = hi >= thr;
+                near = (splits && (double)rival >= (double)o.loss - (double)o.err) || (lo <= thr && hi >= thr) ||
+                       (splits && (o.flags & kScanNearTie));
+            }
+            o.flags = (o.flags & ~kScanNearTie) | (near ? kScanNearTie : 0u);
+        }
         a.best[node] = o;
     }
     // a categorical winner's set, for the host's decision and partition
-    const uint32_t win = (uint32_t)__shfl((int)bf, 0, kWave);
+    const uint32_t win = bf;
     if (a.best_sets && a.cat_rank && win != 0xffffffffu && a.cat_rank[win] != 0xffffffffu) {
         const uint32_t *src = a.cat_sets + ((size_t)node * a.n_cat + a.cat_rank[win]) * kCatWords;
         for (uint32_t w = lane; w < kCatWords; w += kWave) a.best_sets[(size_t)node * kCatWords + w] = src[w];
@@ -576,6 +818,8 @@ extern "C" __global__ __launch_bounds__(64) void hbr_scan_categorical(ScanArgs a
             o.left = QBin{0, 0};
             o.right = QBin{0, 0};
         }
+        o.err = 0.0f;  // categorical sweeps are not bounded by the guard
+        o.rival = -__builtin_inff();
         a.per_feature[(size_t)node * a.n_features + f] = o;
     }
 }

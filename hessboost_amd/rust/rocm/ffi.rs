@@ -33,6 +33,7 @@ pub const HBR_SCAN_CATEGORICAL: u32 = 3;
 pub const HBR_FALLBACK_NUMERIC_SCORE: u32 = 1;
 pub const HBR_FALLBACK_CATEGORICAL_ORDER: u32 = 2;
 pub const HBR_FALLBACK_CATEGORICAL_SCORE: u32 = 3;
+pub const HBR_FALLBACK_NEAR_TIE: u32 = 4;
 
 pub const HBR_OBJ_SQUARED_ERROR: i32 = 0;
 pub const HBR_OBJ_LOGISTIC: i32 = 1;
@@ -169,7 +170,7 @@ pub struct hbr_node_scan {
     pub loss_chg: f32,
     pub backward: u32,
     pub offset: u32,
-    pub pad: u32,
+    pub loss_err: f32,
     pub acc_g: f64,
     pub acc_h: f64,
     pub left_g: f64,
@@ -194,6 +195,7 @@ pub struct hbr_engine_counters {
     pub hist_bytes: u64,
     pub partition_rows: u64,
     pub trees: u64,
+    pub near_ties: u64,
 }
 
 #[repr(C)]
@@ -301,6 +303,7 @@ extern "C" {
                              requests: *const hbr_scan_request, n: u64, out: *mut hbr_node_scan) -> c_int;
     pub fn hbr_scan_categories(e: *mut hbr_engine, out: *mut u32, n: u64) -> c_int;
     pub fn hbr_read_hist(e: *mut hbr_engine, slot: u32, out: *mut f64) -> c_int;
+    pub fn hbr_engine_set_guard(e: *mut hbr_engine, on: c_int, gamma: f64) -> c_int;
     pub fn hbr_engine_counters_read(e: *mut hbr_engine, out: *mut hbr_engine_counters) -> c_int;
     pub fn hbr_set_profiling(e: *mut hbr_engine, on: c_int, kernel_prefix: *const c_char) -> c_int;
     pub fn hbr_kernel_stats(e: *mut hbr_engine, buf: *mut c_char, len: usize) -> c_int;

@@ -360,13 +360,19 @@ typedef struct hbr_scan_request {
 #define HBR_FALLBACK_NUMERIC_SCORE 1
 #define HBR_FALLBACK_CATEGORICAL_ORDER 2
 #define HBR_FALLBACK_CATEGORICAL_SCORE 3
+/* No counterpart in the reference's ScanFallback: in HBR_SUMS_FIXED_POINT
+ * mode, a rival candidate scores within the error bound of the fixed-point
+ * sums of the winner, or the winner's loss is within it of the validity
+ * threshold; hbr_read_hist then returns the node's histogram in the
+ * reference's own f64 summation order for the host's replay. */
+#define HBR_FALLBACK_NEAR_TIE 4
 typedef struct hbr_node_scan {
     uint32_t kind;
     uint32_t feature;
     float loss_chg;
     uint32_t backward;      /* numeric: the winner came from the missing-left pass */
     uint32_t offset;        /* numeric forward: last local bin going left; backward: first local bin going right */
-    uint32_t pad;
+    float loss_err;         /* numeric, fixed-point guard on: a bound on |loss_chg - the CPU's loss_chg| */
     double acc_g, acc_h;    /* numeric: the pass's accumulated statistics (left forward, right backward) */
     double left_g, left_h, right_g, right_h;
     int64_t fixed_left_g, fixed_left_h, fixed_right_g, fixed_right_h; /* exact sums */
@@ -384,15 +390,36 @@ int hbr_root_total_fixed(hbr_engine *e, const hbr_segment *seg, double out[2], i
 
 /* RowEngine::scan_resident: numeric and categorical features (the
  * reference's sweep, src/tree/builder/categorical.rs:48-170: one-hot below 4
- * categories, else the weight-sorted partition scans). */
+ * categories, else the weight-sorted partition scans). In
+ * HBR_SUMS_FIXED_POINT mode beyond the exact domain each numeric winner is
+ * certified against its rivals: a node whose winner a rival partition could
+ * beat within the error bound of the fixed-point sums (or whose loss is
+ * within it of the validity threshold) is HBR_SCAN_REPLAY with
+ * HBR_FALLBACK_NEAR_TIE, for the host's replay from hbr_read_hist. */
 int hbr_scan_resident(hbr_engine *e, const hbr_reg_params *reg, const hbr_scan_request *requests,
                       uint64_t n, hbr_node_scan *out);
 /* The last hbr_scan_resident call's category pool: n entries (the largest
  * cat_end of its categorical winners, 0 when it had none). */
 int hbr_scan_categories(hbr_engine *e, uint32_t *out, uint64_t n);
 
-/* RowEngine::read_hist: 2 * total_bins f64. */
+/* RowEngine::read_hist (src/tree/hist/mod.rs:282-295, called for a
+ * NodeScan::Replay, src/tree/builder/hist/device.rs:633-646): 2 * total_bins
+ * f64. In the exact domain, the slot's fixed-point bins (equal to the CPU's
+ * sums). Beyond it, the slot's rows are summed on the device in the CPU
+ * build's own f64 order (each bin's rows in row order from +0.0, in the
+ * blocks of sum_order, tree/hist/mod.rs:399-607), so the host replays the
+ * node on the sums its CPU path would have: for row-major u8 indexes of at
+ * most 256 features and 9,216 bins whose slot the row-engine calls of this
+ * tree built (hbr_build_resident, siblings included). Otherwise the
+ * fixed-point bins (HBR_SUMS_FIXED_POINT) or HBR_REFUSED (HBR_SUMS_EXACT). */
 int hbr_read_hist(hbr_engine *e, uint32_t slot, double *out);
+
+/* No counterpart in the reference: the fixed-point guard of
+ * hbr_scan_resident and of the whole-round trainer. on: certify winners
+ * (the default); gamma: the caller's min_split_loss, the validity threshold
+ * the guard checks beside kRtEps (1e-6). Nodes the guard cannot certify are
+ * counted in hbr_engine_counters.near_ties. */
+int hbr_engine_set_guard(hbr_engine *e, int on, double gamma);
 
 /* Work counters since the engine opened (no counterpart in the reference;
  * they give the algorithmic bytes the roofline figures divide by). */
@@ -402,6 +429,8 @@ typedef struct hbr_engine_counters {
     uint64_t hist_bytes;       /* algorithmic bytes: rows * (bin bytes + 8 (+ 4 gathered)) */
     uint64_t partition_rows;   /* rows routed */
     uint64_t trees;
+    uint64_t near_ties;        /* decided nodes whose winner the fixed-point guard could not
+                                  certify (see hbr_engine_set_guard) */
 } hbr_engine_counters;
 int hbr_engine_counters_read(hbr_engine *e, hbr_engine_counters *out);
 
