@@ -58,19 +58,36 @@ def measured_traffic(kernel):
     return None, None, None
 
 
-def cpu_model():
+def cpu_info():
+    """The first processor's /proc/cpuinfo fields that name it."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
     except OSError:
         pass
-    return platform.processor()
+    return info
+
+
+def cpu_model():
+    return cpu_info().get("model name") or platform.processor()
 
 
 def cpu_host():
-    """What the CPU baselines ran on."""
-    return {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    """What the CPU baselines ran on: the model string, its family / model /
+    stepping numbers, the clock and the cores available."""
+    i = cpu_info()
+    out = {"cpu_model": cpu_model(), "cpu_vendor": i.get("vendor_id"),
+           "cpu_family_model_stepping": "/".join(i.get(k, "?") for k in ("cpu family", "model", "stepping")),
+           "cpu_mhz": i.get("cpu MHz"), "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    try:
+        out["cpu_max_mhz"] = int(open("/sys/devices/system/cpu/cpu0/cpufreq/cpuinfo_max_freq").read()) // 1000
+    except (OSError, ValueError):
+        pass
+    return out
 
 
 def median_round_s(model, repeats):
@@ -243,7 +260,7 @@ def main():
     ap.add_argument("--no-predict", action="store_true")
     ap.add_argument("--breakdown-steps", type=int, default=5)
     ap.add_argument("--no-kernel-events", action="store_true",
-                    help="time the rounds without HIP events around the histogram kernel")
+                    help="run the fit without timing events on the histogram kernel")
     ap.add_argument("--hist-sample", type=int, default=5,
                     help="time every N-th histogram launch with HIP events (each timed launch stalls the "
                          "stream around its events; N coprime with the 8 levels of a tree samples every level)")
@@ -257,7 +274,9 @@ def main():
     ap.add_argument("--cpu-single-rows", type=int, default=1_050_000,
                     help="rows of the training matrix the single-thread CPU leg trains on")
     ap.add_argument("--fit-rounds", type=int, default=500,
-                    help="rounds of the timed full fit on the device (0: skip)")
+                    help="rounds of the timed full fit on the device, the histogram roofline's window (0: skip)")
+    ap.add_argument("--row-engine-rounds", type=int, default=20,
+                    help="rounds through the row-engine call sequence of hessboost's device_round (0: skip)")
     ap.add_argument("--workload", choices=("higgs", "regression", "multiclass", "sparse"), default="higgs",
                     help="higgs: the default line; multiclass (2M x 50, 10-class softmax, depth 6) and "
                          "sparse (500k x 2000 CSR, 90%% missing, lossguide 255 leaves): their training "
@@ -319,30 +338,12 @@ def main():
         log(f"eval set: {min(args.eval_rows, x.shape[0]):,} rows")
     trainer.boost(args.warmup)
     log(f"{args.warmup} warmup rounds done")
-    before = eng.counters()
-    # HIP events around a sample of the dense histogram kernel's launches
-    # (every hist_sample-th, so every level is sampled), on the engine's stream
-    eng.set_profiling(not args.no_kernel_events, HIST_KERNEL, every=max(1, args.hist_sample))
     t0 = time.perf_counter()
     trainer.boost(args.steps)
     t1 = time.perf_counter()
-    stats = eng.kernel_stats()
-    after = eng.counters()
-    eng.set_profiling(False)
     elapsed = t1 - t0
     rounds_per_s = args.steps / elapsed
-    hist_timed_ms = sum(ms for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
-    hist_timed = sum(timed for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
-    hist_launches = sum(n for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
-    hist_names = sorted(k for k in stats if k.startswith(HIST_KERNEL))
-    # the launches' total device time from the timed sample's average duration
-    hist_ms = hist_timed_ms / hist_timed * hist_launches if hist_timed else 0.0
-    hist_bytes = after["hist_bytes"] - before["hist_bytes"]
-    lds_atomics = (after["hist_rows"] - before["hist_rows"]) * x.shape[1] * 2
-    achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
-    log(f"{args.steps} rounds in {elapsed:.3f}s = {rounds_per_s:.1f} rounds/s; {'/'.join(hist_names)} "
-        f"{hist_ms / max(1, hist_launches):.4f} ms per launch ({hist_timed} of {hist_launches} launches timed), "
-        f"{achieved:.0f} GB/s algorithmic")
+    log(f"{args.steps} rounds in {elapsed:.3f}s = {rounds_per_s:.1f} rounds/s")
     # per-kernel time per round, from a few more rounds with every kernel timed
     breakdown = {}
     if args.breakdown_steps > 0:
@@ -371,7 +372,78 @@ def main():
                      "lds_atomics": {"achieved": round(watom, 3), "peak": LDS_ATOMIC_PEAK_T, "unit": "T lane-ops/s",
                                      "frac": round(watom / LDS_ATOMIC_PEAK_T, 4)}}
     n_trees = len(trainer.trees())
-    traffic, traffic_alg, traffic_src = measured_traffic(hist_names[0] if hist_names else HIST_KERNEL)
+
+    # ---------------- the configured 500-round fit: the histogram roofline's window --------
+    # A fresh trainer on the resident index, every round then the trees
+    # downloaded. The dense histogram kernel's launches of the fit are timed
+    # by events the runtime records with each sampled dispatch's own begin
+    # and end (every hist_sample-th launch, so every level is sampled); the
+    # fit is the window of the committed kernel trace's and counters' figures.
+    fit_res, hist = None, None
+    if args.fit_rounds > 0:
+        fit = hb.Trainer(eng, params, y)
+        before = eng.counters()
+        eng.set_profiling(not args.no_kernel_events, HIST_KERNEL, every=max(1, args.hist_sample))
+        t = time.perf_counter()
+        fit.boost(args.fit_rounds)
+        fit_trees = fit.trees()
+        t_fit = time.perf_counter() - t
+        stats = eng.kernel_stats()
+        after = eng.counters()
+        eng.set_profiling(False)
+        hist_timed_ms = sum(ms for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
+        hist_timed = sum(timed for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
+        hist_launches = sum(n for k, (ms, timed, n) in stats.items() if k.startswith(HIST_KERNEL))
+        hist_names = sorted(k for k in stats if k.startswith(HIST_KERNEL))
+        avg_ms = hist_timed_ms / hist_timed if hist_timed else 0.0
+        hist_bytes = after["hist_bytes"] - before["hist_bytes"]
+        lds_atomics = (after["hist_rows"] - before["hist_rows"]) * x.shape[1] * 2
+        per_launch = hist_bytes / max(1, hist_launches)
+        achieved = per_launch / (avg_ms * 1e-3) / 1e9 if avg_ms > 0 else 0.0
+        hist = dict(names=hist_names, launches=hist_launches, timed=hist_timed, avg_ms=avg_ms,
+                    per_launch=per_launch, achieved=achieved, lds=lds_atomics / max(1, hist_launches),
+                    near_ties=after["near_ties"] - before["near_ties"])
+        log(f"{args.fit_rounds}-round fit in {t_fit:.2f}s ({len(fit_trees)} trees downloaded); "
+            f"{'/'.join(hist_names)} {avg_ms:.4f} ms per launch ({hist_timed} of {hist_launches} launches timed), "
+            f"{achieved:.0f} GB/s algorithmic; {hist['near_ties']} nodes the guard could not certify")
+        fit_res = {
+            "rounds": args.fit_rounds, "s": round(t_fit, 3), "rounds_per_s": round(args.fit_rounds / t_fit, 2),
+            "s_with_binning": round(t_fit + t_bin, 3),
+            "s_with_sketch_and_binning": round(t_fit + t_bin + t_cuts, 3),
+            "near_ties": hist["near_ties"],
+            "note": "a fresh trainer on the resident index: every round, then the trees downloaded; "
+                    "binning from rows in HBM and the host sketch added in the other keys; near_ties: nodes whose "
+                    "fixed-point winner the guard could not certify against the CPU's f64 sums",
+        }
+        del fit
+
+    # ---------------- hessboost's own route: the row-engine call sequence ------------------
+    row_engine = None
+    if args.row_engine_rounds > 0:
+        from hessboost_amd.rowengine import RowEngineRounds
+
+        eng.set_sums("fixed_point")
+        fo, cv = cuts.arrays()
+        drv = RowEngineRounds(eng, fo, cv, params)
+        m0 = np.full(len(y), np.float32(trainer.base_score()[0]), np.float32)
+        c0 = eng.counters()
+        drv.device_round(m0, y)
+        t = time.perf_counter()
+        for _ in range(args.row_engine_rounds):
+            drv.device_round(m0, y)
+        t_re = time.perf_counter() - t
+        c1 = eng.counters()
+        row_engine = {
+            "value": round(args.row_engine_rounds / t_re, 2), "unit": "rounds/s", "rounds": args.row_engine_rounds,
+            "near_ties": c1["near_ties"] - c0["near_ties"], "resolved": c1["near_ties_resolved"] - c0["near_ties_resolved"],
+            "note": "the same workload through hessboost's device_round / build_device_staged call sequence on the "
+                    "C ABI's row engine (hessboost_amd.rowengine, a Python host of the reference's builder): one "
+                    "call per level step, each synchronising; fixed-point sums with near ties resolved on the "
+                    "device; after one warmup round",
+        }
+        log(f"row-engine route: {row_engine['value']} rounds/s over {args.row_engine_rounds} rounds; "
+            f"{row_engine['near_ties']} near ties, {row_engine['resolved']} resolved on the device")
+    traffic, traffic_alg, traffic_src = measured_traffic(hist["names"][0] if hist and hist["names"] else HIST_KERNEL)
 
     result = {
         "metric": METRIC,
@@ -393,28 +465,32 @@ def main():
             **({"eval_rows": args.eval_rows} if args.eval_rows > 0 else {}),
         },
         "roofline": {
-            "kernel": "/".join(hist_names) or HIST_KERNEL,
+            "kernel": "/".join(hist["names"]) or HIST_KERNEL,
+            "window": f"the {args.fit_rounds}-round fit from a fresh trainer: every launch of the kernel "
+                      "(histogram levels 1-7 of each tree), every "
+                      f"{max(1, args.hist_sample)}-th timed by events on the dispatch's own begin and end",
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": round(hist["achieved"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac": round(hist["achieved"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
             "traffic_run_algorithmic_bytes": traffic_alg,
-            "launches": hist_launches,
-            "timed_launches": hist_timed,
-            "avg_launch_ms": round(hist_ms / max(1, hist_launches), 4),
-            "algorithmic_bytes_per_launch": int(hist_bytes / max(1, hist_launches)),
+            "launches": hist["launches"],
+            "timed_launches": hist["timed"],
+            "avg_launch_ms": round(hist["avg_ms"], 4),
+            "algorithmic_bytes_per_launch": int(hist["per_launch"]),
             # the kernel's other bound: two 64-bit LDS integer adds per (row, feature)
             "lds_atomics": {
-                "achieved": round(lds_atomics / (hist_ms * 1e-3) / 1e12, 3) if hist_ms > 0 else 0.0,
+                "achieved": round(hist["lds"] / (hist["avg_ms"] * 1e-3) / 1e12, 3) if hist["avg_ms"] > 0 else 0.0,
                 "peak": LDS_ATOMIC_PEAK_T,
                 "unit": "T lane-ops/s",
-                "frac": round(lds_atomics / (hist_ms * 1e-3) / 1e12 / LDS_ATOMIC_PEAK_T, 4) if hist_ms > 0 else 0.0,
-                "per_launch": int(lds_atomics / max(1, hist_launches)),
+                "frac": round(hist["lds"] / (hist["avg_ms"] * 1e-3) / 1e12 / LDS_ATOMIC_PEAK_T, 4)
+                if hist["avg_ms"] > 0 else 0.0,
+                "per_launch": int(hist["lds"]),
             },
-        },
+        } if hist else None,
         "kernel_ms_per_round": breakdown,
         **({"walk_root_roofline": walk_root} if walk_root else {}),
         # the index built on the device from the f32 rows (not part of the rounds)
@@ -428,22 +504,10 @@ def main():
         },
     }
 
-    # ---------------- the configured 500-round fit on the device ------------------------
-    if args.fit_rounds > 0:
-        fit = hb.Trainer(eng, params, y)
-        t = time.perf_counter()
-        fit.boost(args.fit_rounds)
-        fit_trees = fit.trees()
-        t_fit = time.perf_counter() - t
-        log(f"{args.fit_rounds}-round fit in {t_fit:.2f}s ({len(fit_trees)} trees downloaded)")
-        result["fit"] = {
-            "rounds": args.fit_rounds, "s": round(t_fit, 3),
-            "s_with_binning": round(t_fit + t_bin, 3),
-            "s_with_sketch_and_binning": round(t_fit + t_bin + t_cuts, 3),
-            "note": "a fresh trainer on the resident index: every round, then the trees downloaded; "
-                    "binning from rows in HBM and the host sketch added in the other keys",
-        }
-        del fit
+    if fit_res:
+        result["fit"] = fit_res
+    if row_engine:
+        result["row_engine"] = row_engine
     del eng, trainer
 
     # ---------------- CPU baseline (oracle, same workload) -----------------------------
@@ -481,6 +545,12 @@ def main():
         pstats = forest.kernel_stats()
         forest.set_profiling(False)
         mrows = n * args.predict_steps / (t1 - t0) / 1e6
+        # from host rows: the same walk with the 4 GB of rows copied in first (PCIe)
+        forest.predict_margin(xp[:1024])
+        t = time.perf_counter()
+        forest.predict_margin(xp)
+        t_host = time.perf_counter() - t
+        log(f"predict from host rows: {n / t_host / 1e6:.1f} Mrows/s ({t_host:.3f} s with the copy)")
         pkern = sorted(k for k in pstats if k.startswith("hbr_predict"))
         pms = sum(pstats[k][0] for k in pkern)
         pl = sum(pstats[k][1] for k in pkern)
@@ -499,6 +569,8 @@ def main():
         pred = {
             "metric": "batch predict Mrows/s", "value": round(mrows, 2), "unit": "Mrows/s",
             "steps": args.predict_steps,
+            "from_host_rows": {"value": round(n / t_host / 1e6, 2), "unit": "Mrows/s", "s": round(t_host, 4),
+                               "note": "rows in host memory, copied to HBM by the call (the resident rate is value)"},
             "config": {"workload": f"{args.predict_trees}-tree depth-8 forest, {n:,} x {f} f32 rows, 2% NaN"},
             "roofline": {"kernel": "/".join(pkern) or "hbr_predict", "bound": "texture path",
                          "achieved": round(loads / launch_s, 1) if pms else 0.0, "peak": TEXTURE_PEAK_LOADS,

@@ -17,6 +17,7 @@ CODE_OBJECT = os.path.join(LIB_DIR, "hbrocm_gfx950.hsaco")
 
 OK, REFUSED, DEVICE_ERROR, INVALID = 0, 1, 2, 3
 SUMS_EXACT, SUMS_FIXED_POINT = 0, 1
+GUARD_OFF, GUARD_REPLAY, GUARD_RESOLVE = 0, 1, 2
 LOSS_SQUARED_ERROR, LOSS_LOGISTIC, LOSS_SOFTMAX = 0, 1, 2
 OBJ_SQUARED_ERROR, OBJ_LOGISTIC, OBJ_SOFTMAX, OBJ_LOGITRAW = 0, 1, 2, 3
 GROW_DEPTHWISE, GROW_LOSSGUIDE = 0, 1
@@ -93,7 +94,8 @@ class NodeScan(C.Structure):
 
 class EngineCounters(C.Structure):
     _fields_ = [("hist_nodes", C.c_uint64), ("hist_rows", C.c_uint64), ("hist_bytes", C.c_uint64),
-                ("partition_rows", C.c_uint64), ("trees", C.c_uint64), ("near_ties", C.c_uint64)]
+                ("partition_rows", C.c_uint64), ("trees", C.c_uint64), ("near_ties", C.c_uint64),
+                ("near_ties_resolved", C.c_uint64)]
 
 
 class TrainParams(C.Structure):
@@ -163,6 +165,8 @@ SIGNATURES = {
     "hbr_scan_categories": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64]),
     "hbr_read_hist": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p]),
     "hbr_engine_set_guard": (C.c_int, [C.c_void_p, C.c_int, C.c_double]),
+    "hbr_node_gain": (C.c_int, [P(RegParams), C.c_double, C.c_double, C.c_double, C.c_double, P(C.c_float)]),
+    "hbr_leaf_weight": (C.c_int, [P(RegParams), C.c_double, C.c_double, C.c_double, C.c_double, P(C.c_float)]),
     "hbr_engine_counters_read": (C.c_int, [C.c_void_p, P(EngineCounters)]),
     "hbr_set_profiling": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p]),
     "hbr_kernel_stats": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),

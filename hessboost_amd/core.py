@@ -242,11 +242,14 @@ class Engine:
         code = {"exact": A.SUMS_EXACT, "fixed_point": A.SUMS_FIXED_POINT}[mode]
         A.check(A.lib().hbr_engine_set_sums(self._h, code))
 
-    def set_guard(self, on=True, gamma=0.0):
-        """The fixed-point guard: with it, the resident scan reports a node
-        whose winner its sums cannot certify as a replay (and the trainer
-        counts such nodes); gamma is the split threshold it checks."""
-        A.check(A.lib().hbr_engine_set_guard(self._h, int(bool(on)), float(gamma)))
+    def set_guard(self, mode="resolve", gamma=0.0):
+        """The fixed-point guard of the resident scan: a node whose winner
+        its sums cannot certify is searched again on the CPU builder's sums
+        on the device ("resolve", the default), reported for a host replay
+        ("replay"), or left as it is ("off"); gamma is the split threshold
+        it checks. The trainer counts such nodes."""
+        code = {"off": A.GUARD_OFF, "replay": A.GUARD_REPLAY, "resolve": A.GUARD_RESOLVE}[mode]
+        A.check(A.lib().hbr_engine_set_guard(self._h, code, float(gamma)))
 
     def prepare(self, gpair):
         gpair = np.ascontiguousarray(gpair, np.float32).reshape(-1)

@@ -489,6 +489,35 @@ struct ScanBest {
                              // other partitions (-inf: none); node records: of the node's rivals
 };
 
+// A near tie resolved on the device: the node's split search over its
+// histogram in the CPU builder's f64 sums (hbr_hist_exact), candidate for
+// candidate as the reference's host search scans (forward prefix in bin
+// order, the backward pass when the bins miss some of the node's total),
+// keeping the first best per feature and the lowest feature among equals.
+struct ExactBest {
+    float loss;              // 0 with no candidate (index 0xffffffff)
+    uint32_t feature;
+    uint32_t index;          // the fixed-point scan's candidate order (forward, then backward)
+    uint32_t flags;          // bit0 backward; kScanNumericNaN
+    double lg, lh, rg, rh;   // the winner's children (f64, the CPU's sums)
+    QBin left, right;        // the same partition's fixed-point sums
+};
+
+struct ExactScanArgs {
+    const double *hist;      // 2 x total_bins, g and h interleaved
+    const QBin *fixed;       // the node's fixed-point bins (its slot)
+    const uint32_t *feature_offset;
+    uint32_t n_cols;
+    uint32_t dense;          // forward pass only
+    double total_g, total_h; // the node's statistics as the caller holds them
+    QBin total_fixed;
+    float lower, upper;
+    ScanParams reg;
+    const int8_t *monotone;  // per feature or null
+    ExactBest *per_feature;  // n_cols records
+    ExactBest *best;         // one record
+};
+
 struct ScanArgs {
     const ScanNode *nodes;
     uint32_t n_nodes;

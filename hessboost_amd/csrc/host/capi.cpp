@@ -11,6 +11,7 @@
 #include "engine.h"
 #include "forest.h"
 #include "noalloc.h"
+#include "split_math.h"
 #include "hessboost_rocm.h"
 #include "trainer.h"
 
@@ -592,7 +593,7 @@ int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_r
         }
         e.set_scan_params(ScanParams{reg->lambda, reg->alpha, reg->max_delta_step, reg->min_child_weight}, dirs);
         // fixed-point sums beyond the exact domain: the guard certifies each winner
-        e.guard_active = e.guard_on && !e.sums_exact(e.n_rows());
+        e.guard_active = e.guard_on() && !e.sums_exact(e.n_rows());
         std::vector<ScanInput> in(n);
         for (uint64_t i = 0; i < n; i++) {
             if (req[i].n_features != e.n_cols()) fail(kRefused, "scan: a feature subset (column sampling)");
@@ -614,6 +615,44 @@ int hbr_scan_resident(hbr_engine *h, const hbr_reg_params *reg, const hbr_scan_r
         for (uint64_t i = 0; i < n; i++) {
             hbr_node_scan o{};
             const ScanBest &b = best[i];
+            if ((b.flags & kScanNearTie) && !(b.flags & kScanReplay) && e.guard_mode == Engine::kGuardResolve) {
+                // resolved on the device: the node searched on the CPU builder's sums
+                e.counters.near_ties++;
+                ExactBest x;
+                if (e.resolve_exact(in[i].slot, req[i].total_g, req[i].total_h, in[i].total, in[i].lower,
+                                    in[i].upper, &x) &&
+                    !(x.flags & kScanNumericNaN)) {
+                    e.counters.near_ties_resolved++;
+                    if (x.index == 0xffffffffu) {
+                        o.kind = HBR_SCAN_EMPTY;
+                        out[i] = o;
+                        continue;
+                    }
+                    const uint32_t nb = fo[x.feature + 1] - fo[x.feature];
+                    o.kind = HBR_SCAN_NUMERIC;
+                    o.feature = x.feature;
+                    o.loss_chg = x.loss;
+                    o.loss_err = 0.0f;
+                    o.left_g = x.lg;
+                    o.left_h = x.lh;
+                    o.right_g = x.rg;
+                    o.right_h = x.rh;
+                    o.fixed_left_g = x.left.g;
+                    o.fixed_left_h = x.left.h;
+                    o.fixed_right_g = x.right.g;
+                    o.fixed_right_h = x.right.h;
+                    o.backward = x.index >= nb ? 1u : 0u;
+                    o.offset = o.backward ? nb - 1 - (x.index - nb) : x.index;
+                    o.acc_g = o.backward ? o.right_g : o.left_g;
+                    o.acc_h = o.backward ? o.right_h : o.left_h;
+                    out[i] = o;
+                    continue;
+                }
+                o.kind = HBR_SCAN_REPLAY;
+                o.fallback = HBR_FALLBACK_NEAR_TIE;
+                out[i] = o;
+                continue;
+            }
             if (b.flags & (kScanReplay | kScanNearTie)) {
                 // a NaN score, a categorical order that is not total, or a
                 // winner the fixed-point sums cannot certify: the host
@@ -693,10 +732,28 @@ int hbr_read_hist(hbr_engine *h, uint32_t slot, double *out) {
     });
 }
 
-int hbr_engine_set_guard(hbr_engine *h, int on, double gamma) {
+int hbr_node_gain(const hbr_reg_params *reg, double g, double h, double lower, double upper, float *out) {
+    return guard([&] {
+        if (!reg || !out) fail(kInvalid, "node_gain: null argument");
+        const Reg r = reg_from(reg->lambda, reg->alpha, reg->max_delta_step, reg->min_child_weight);
+        *out = xgb_node_gain(g, h, r, lower, upper);
+    });
+}
+
+int hbr_leaf_weight(const hbr_reg_params *reg, double g, double h, double lower, double upper, float *out) {
+    return guard([&] {
+        if (!reg || !out) fail(kInvalid, "leaf_weight: null argument");
+        const Reg r = reg_from(reg->lambda, reg->alpha, reg->max_delta_step, reg->min_child_weight);
+        *out = (float)calc_weight_bounded(g, h, r, lower, upper);
+    });
+}
+
+int hbr_engine_set_guard(hbr_engine *h, int mode, double gamma) {
     return with_engine(h, [&](Engine &e) {
         if (!(gamma >= 0.0)) fail(kInvalid, "set_guard: gamma must be a non-negative number");
-        e.guard_on = on != 0;
+        if (mode != HBR_GUARD_OFF && mode != HBR_GUARD_REPLAY && mode != HBR_GUARD_RESOLVE)
+            fail(kInvalid, "set_guard: unknown mode");
+        e.guard_mode = mode;
         e.guard_gamma = (float)gamma;
     });
 }

@@ -814,6 +814,38 @@ void Engine::exact_segment(const Segment &sg, double *out_dev) {
 }
 
 bool Engine::exact_hist(uint32_t slot, double *out) {
+    if (!exact_hist_dev(slot)) return false;
+    d_exact_out_.download(out, 2ull * total_bins_, dev_.stream());
+    dev_.sync();
+    return true;
+}
+
+bool Engine::resolve_exact(uint32_t slot, double total_g, double total_h, QBin total_fixed, float lower, float upper,
+                           ExactBest *out) {
+    if (!exact_hist_dev(slot)) return false;
+    d_exact_best_.reserve(n_cols_ + 1);
+    ExactScanArgs a{};
+    a.hist = d_exact_out_.get();
+    a.fixed = hist_.get() + (size_t)slot * total_bins_;
+    a.feature_offset = d_fo_.get();
+    a.n_cols = n_cols_;
+    a.dense = dense_ ? 1u : 0u;
+    a.total_g = total_g;
+    a.total_h = total_h;
+    a.total_fixed = total_fixed;
+    a.lower = lower;
+    a.upper = upper;
+    a.reg = scan_params_;
+    a.monotone = has_monotone_ ? monotone_.get() : nullptr;
+    a.per_feature = d_exact_best_.get() + 1;
+    a.best = d_exact_best_.get();
+    dev_.launch("hbr_scan_exact", dim3(1), dim3(256), a);
+    d_exact_best_.download(out, 1, dev_.stream());
+    dev_.sync();
+    return true;
+}
+
+bool Engine::exact_hist_dev(uint32_t slot) {
     if (slot >= slot_history_.size() || !slot_history_[slot].known) return false;
     if (!dense_u8_ || n_cols_ == 0 || n_cols_ > kExactThreads || 2ull * total_bins_ > kExactMaxWords) return false;
     if (level_pairs_ || softmax_staged()) return false;  // per-class pairs: one tree's pairs only
@@ -829,8 +861,6 @@ bool Engine::exact_hist(uint32_t slot, double *out) {
         ExactSumArgs c{nullptr, 0, 0, d_exact_out_.get(), (uint32_t)words, d_exact_minus_.get()};
         dev_.launch("hbr_hist_exact_sum", dim3(ceil_div(words, 256)), dim3(256), c);
     }
-    d_exact_out_.download(out, words, dev_.stream());
-    dev_.sync();
     return true;
 }
 

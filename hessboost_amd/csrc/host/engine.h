@@ -282,7 +282,9 @@ public:
     // ---- the fixed-point guard and exact-order replays ---------------------------
     // The guard bounds every candidate's score error and flags the nodes it
     // cannot certify (kScanNearTie); gamma is the caller's split threshold.
-    bool guard_on = true;
+    enum GuardMode { kGuardOff = 0, kGuardReplay = 1, kGuardResolve = 2 };
+    int guard_mode = kGuardResolve;  // near ties: reported for a host replay, or resolved on the device
+    bool guard_on() const { return guard_mode != kGuardOff; }
     float guard_gamma = 0.0f;
     bool guard_active = false;  // the next scans bound their candidates
     // How each histogram slot of the current tree came about through the row
@@ -300,6 +302,11 @@ public:
     // unknown or the index is not row-major u8 (out: 2 x total_bins, g and
     // h interleaved).
     bool exact_hist(uint32_t slot, double *out);
+    // A near tie's node searched on those sums on the device (hbr_scan_exact):
+    // the CPU builder's winner, with its children in f64 and in fixed point;
+    // false when the slot's sums are not available (see exact_hist).
+    bool resolve_exact(uint32_t slot, double total_g, double total_h, QBin total_fixed, float lower, float upper,
+                       ExactBest *out);
     // algorithmic bytes of summing `rows` rows into a histogram
     uint64_t hist_bytes(uint64_t rows, bool gathered) const;
 
@@ -321,6 +328,8 @@ private:
     };
     std::vector<SlotHistory> slot_history_;
     void exact_segment(const Segment &sg, double *out_dev);  // one node's CPU-order sums into out_dev
+    bool exact_hist_dev(uint32_t slot);                       // the slot's CPU-order sums into d_exact_out_
+    DBuf<ExactBest> d_exact_best_;
     DBuf<double> d_exact_;
     DBuf<double> d_exact_out_;
     DBuf<double> d_exact_minus_;

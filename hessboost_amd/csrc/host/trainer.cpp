@@ -651,7 +651,7 @@ void Trainer::boost_softmax_batched(uint64_t rounds) {
 void Trainer::boost(uint64_t rounds) {
     // every sum of the whole-round trainer is fixed point: its scans bound
     // their candidates and count the nodes they cannot certify
-    e_.guard_active = e_.guard_on;
+    e_.guard_active = e_.guard_on();
     e_.guard_gamma = (float)p_.grow.gamma;
     if (p_.objective == HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE && softmax_batches &&
         e_.can_grow_device(p_.grow.max_depth, k_)) {

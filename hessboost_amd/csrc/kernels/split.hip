@@ -94,16 +94,19 @@ __device__ __forceinline__ Bound node_bound(uint32_t m, int eg, int eh, float ma
 }
 
 // Error bound of one child's gain at weight w (before the gain's f32 rounding),
-// and the weight's own error through *dw.
-__device__ __forceinline__ double gain_err(double g, double h, float w, double dg, double dh, const ScanParams &r,
-                                           double *dw_out) {
-    const double hl = h + r.lambda;
-    const double den = hl - dh;
-    const double aw = __builtin_fabs((double)w);
-    const double dw = (den > 0.0 ? (dg + aw * dh) / den : 1e300) + 2.0 * ulp32(aw);
-    const double slope = 2.0 * __builtin_fabs(g + hl * (double)w) + 2.0 * r.alpha;
+// and the weight's own error through *dw. Evaluated in f32 with the
+// hardware reciprocal: each step's relative error (<= 2^-22) is covered by
+// the 2^-12 the caller adds to the total.
+__device__ __forceinline__ float gain_err(double g, double h, float w, float dg, float dh, const ScanParams &r,
+                                          float *dw_out) {
+    const float hl = (float)(h + r.lambda);
+    const float den = hl - dh;
+    const float aw = __builtin_fabsf(w);
+    const float dw = (den > 0.0f ? (dg + aw * dh) * __builtin_amdgcn_rcpf(den) : __builtin_inff()) +
+                     2.0f * (float)ulp32(aw);
+    const float slope = 2.0f * __builtin_fabsf((float)(g + (h + r.lambda) * (double)w)) + 2.0f * (float)r.alpha;
     *dw_out = dw;
-    return 2.0 * aw * dg + aw * aw * dh + (slope + hl * dw) * dw;
+    return 2.0f * aw * dg + aw * aw * dh + (slope + hl * dw) * dw;
 }
 
 // The guarded score of one candidate: `ok` as score() decides it; `rival`
@@ -120,27 +123,27 @@ __device__ __forceinline__ Scored score_guarded(double lg, double lh, double rg,
                                                 float lower, float upper, int dir, float root_gain, const Bound &b) {
     Scored o{false, false, false, 0.0f, 0.0f};
     if (!(lh > 0.0 && rh > 0.0)) return o;
-    const double dgl = b.dg, dhl = b.dh;
-    const double dgr = 2.0 * b.dg + __builtin_fabs(rg) * 0x1p-52, dhr = 2.0 * b.dh + rh * 0x1p-52;
+    const float dgl = (float)b.dg, dhl = (float)b.dh;
+    const float dgr = 2.0f * dgl + (float)(__builtin_fabs(rg) * 0x1p-52), dhr = 2.0f * dhl + (float)(rh * 0x1p-52);
     const bool mcw_ok = lh >= r.min_child_weight && rh >= r.min_child_weight;
     const bool mcw_near = lh + dhl >= r.min_child_weight && rh + dhr >= r.min_child_weight;
     const bool mcw_edge = lh - dhl < r.min_child_weight || rh - dhr < r.min_child_weight;
     if (!mcw_near) return o;
     const float wl = bounded_weight(lg, lh, r, lower, upper);
     const float wr = bounded_weight(rg, rh, r, lower, upper);
-    double dwl, dwr;
-    const double el = gain_err(lg, lh, wl, dgl, dhl, r, &dwl);
-    const double er = gain_err(rg, rh, wr, dgr, dhr, r, &dwr);
-    const double slack = dwl + dwr;
+    float dwl, dwr;
+    const float el = gain_err(lg, lh, wl, dgl, dhl, r, &dwl);
+    const float er = gain_err(rg, rh, wr, dgr, dhr, r, &dwr);
+    const float slack = dwl + dwr;
     bool mono_ok = true, mono_near = true, mono_edge = false;
     if (dir > 0) {
-        mono_ok = (double)wl <= (double)wr;
-        mono_near = (double)wl <= (double)wr + slack;
-        mono_edge = (double)wr - (double)wl <= slack;
+        mono_ok = wl <= wr;
+        mono_near = wl <= wr + slack;
+        mono_edge = wr - wl <= slack;
     } else if (dir < 0) {
-        mono_ok = (double)wl >= (double)wr;
-        mono_near = (double)wl + slack >= (double)wr;
-        mono_edge = (double)wl - (double)wr <= slack;
+        mono_ok = wl >= wr;
+        mono_near = wl + slack >= wr;
+        mono_edge = wl - wr <= slack;
     }
     if (!mono_near) return o;
     const float gl = (float)gain_at(lg, lh, r, wl), gr = (float)gain_at(rg, rh, r, wr);
@@ -149,8 +152,9 @@ __device__ __forceinline__ Scored score_guarded(double lg, double lh, double rg,
     o.ok = mcw_ok && mono_ok;
     o.rival = true;
     o.fragile = o.ok && (mcw_edge || (dir != 0 && mono_edge));
-    const double e = el + er + ulp32(gl) + ulp32(gr) + ulp32(gain) + ulp32(o.loss);
-    o.err = (float)(e * (1.0 + 0x1p-20));
+    const float e = el + er + 1.2e-7f * (__builtin_fabsf(gl) + __builtin_fabsf(gr) + __builtin_fabsf(gain) +
+                                         __builtin_fabsf(o.loss)) + 0x1p-126f;
+    o.err = e * (1.0f + 0x1p-12f);
     return o;
 }
 
@@ -561,8 +565,10 @@ __device__ __forceinline__ void merge_node(const ScanArgs &a, uint32_t node, con
             const QBin t = dev_root ? a.root_total[cls] : nd.total;
             const double tg = dequant(t.g, eg), th = dequant(t.h, eh);
             const float w = bounded_weight(tg, th, a.reg, nd.lower, nd.upper);
-            double dw;
-            const double e_root = th > 0.0 ? gain_err(tg, th, w, b.dg, b.dh, a.reg, &dw) + 2.0 * ulp32(gain_at(tg, th, a.reg, w))
+            float dw;
+            const double e_root = th > 0.0 ? (double)gain_err(tg, th, w, (float)b.dg, (float)b.dh, a.reg, &dw) *
+                                                     (1.0 + 0x1p-12) +
+                                                 2.0 * ulp32(gain_at(tg, th, a.reg, w))
                                            : 0.0;
             const double thr = fmax(1e-6, (double)a.gamma);
             bool near;
@@ -590,6 +596,94 @@ extern "C" __global__ __launch_bounds__(kMergeThreads) void hbr_scan_merge(ScanA
     const uint32_t node = blockIdx.x;
     if (node >= scan_nodes(a)) return;  // uniform per workgroup
     merge_node(a, node, a.per_feature + (size_t)node * a.n_features);
+}
+
+// ---- near ties resolved on the CPU builder's sums -------------------------------
+// One workgroup per node: thread f walks feature f's bins in order with f64
+// prefix sums, as the reference's host search (builder/split.rs:391-470,
+// hist/search.rs:99-127); thread 0 then merges the features in order.
+extern "C" __global__ __launch_bounds__(256) void hbr_scan_exact(ExactScanArgs a) {
+    const uint32_t f = threadIdx.x;
+    const double tg = a.total_g, th = a.total_h;
+    const float root_gain = node_gain(tg, th, a.reg, a.lower, a.upper);
+    for (uint32_t ff = f; ff < a.n_cols; ff += blockDim.x) {
+        const uint32_t fs = a.feature_offset[ff], nb = a.feature_offset[ff + 1] - fs;
+        const int dir = a.monotone ? (int)a.monotone[ff] : 0;
+        ExactBest b{};
+        b.loss = -__builtin_inff();
+        b.feature = ff;
+        b.index = 0xffffffffu;
+        bool nan_seen = false;
+        auto offer_exact = [&](uint32_t idx, double lg, double lh, double rg, double rh, uint32_t backward) {
+            float loss;
+            if (!score(lg, lh, rg, rh, a.reg, a.lower, a.upper, dir, root_gain, &loss)) return;
+            if (__builtin_isnan(loss)) {
+                nan_seen = true;
+                return;
+            }
+            if (__builtin_isinf(loss) || !(loss > b.loss)) return;  // the first best of the feature
+            b.loss = loss;
+            b.index = idx;
+            b.flags = backward;
+            b.lg = lg;
+            b.lh = lh;
+            b.rg = rg;
+            b.rh = rh;
+        };
+        if (nb > 1) {
+            double ag = 0.0, ah = 0.0;
+            for (uint32_t k = 0; k < nb; k++) {
+                ag += a.hist[2 * (fs + k)];
+                ah += a.hist[2 * (fs + k) + 1];
+                offer_exact(k, ag, ah, tg - ag, th - ah, 0u);
+            }
+            if (!a.dense && !(ag == tg && ah == th)) {
+                double sg = 0.0, sh = 0.0;
+                for (uint32_t o = nb; o-- > 0;) {
+                    sg += a.hist[2 * (fs + o)];
+                    sh += a.hist[2 * (fs + o) + 1];
+                    offer_exact(nb + (nb - 1 - o), tg - sg, th - sh, sg, sh, 1u);
+                }
+            }
+        }
+        if (nan_seen) b.flags |= kScanNumericNaN;
+        a.per_feature[ff] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    ExactBest w{};
+    w.loss = 0.0f;
+    w.index = 0xffffffffu;
+    uint32_t nan_flag = 0;
+    for (uint32_t ff = 0; ff < a.n_cols; ff++) {
+        const ExactBest c = a.per_feature[ff];
+        nan_flag |= c.flags & kScanNumericNaN;
+        if (c.index != 0xffffffffu && c.loss > w.loss) w = c;  // only a higher loss displaces a lower feature
+    }
+    if (w.index != 0xffffffffu) {
+        // the winner's partition in fixed point (the sums the next scans take)
+        const uint32_t fs = a.feature_offset[w.feature], nb = a.feature_offset[w.feature + 1] - fs;
+        const QBin *h = a.fixed + fs;
+        int64_t sg = 0, sh = 0;
+        if (w.index < nb) {
+            for (uint32_t k = 0; k <= w.index; k++) {
+                sg += h[k].g;
+                sh += h[k].h;
+            }
+            w.left = QBin{sg, sh};
+            w.right = QBin{a.total_fixed.g - sg, a.total_fixed.h - sh};
+        } else {
+            const uint32_t o = nb - 1 - (w.index - nb);
+            for (uint32_t k = o; k < nb; k++) {
+                sg += h[k].g;
+                sh += h[k].h;
+            }
+            w.right = QBin{sg, sh};
+            w.left = QBin{a.total_fixed.g - sg, a.total_fixed.h - sh};
+        }
+    }
+    w.flags |= nan_flag;
+    *a.best = w;
 }
 
 // ---- categorical features (builder/categorical.rs:48-170) ---------------------

@@ -1,26 +1,29 @@
-"""hessboost's device-resident round, driven call for call through the row
-engine of the C ABI, as the reference issues it (test harness).
+"""A Python host of hessboost's device-resident round over the row engine
+of the C ABI: the caller's side of the RowEngine seam, call for call as the
+reference's Rust builder issues it, for hosts without the Rust shim.
 
-`device_round` follows src/training/round.rs:105-148: margins loaded once,
-the gradients computed on the device, one tree grown by
-`build_device_staged` (src/tree/builder/hist/device.rs:233-247 ->
-build_on_device :147-231, grow_device_depthwise :249-294,
+`RowEngineRounds.device_round` follows src/training/round.rs:105-148:
+margins loaded once, the gradients computed on the device, one tree grown
+as `build_device_staged` grows it (src/tree/builder/hist/device.rs:233-247
+-> build_on_device :147-231, grow_device_depthwise :249-294,
 resident_children :441-528, resident_search/resident_merge :530-627,
 resident_best :650-700), the leaves scaled by eta and added to the margins
-by their segments. The host-side arithmetic the reference performs between
-the calls (node gains, validity, leaf weights) comes from the oracle, which
-restates the reference's CPU builder; a replayed node (NodeScan::Replay) is
-evaluated by the oracle on the histogram hbr_read_hist returns, as
-resident_merge evaluates it on the host.
+by their segments. Depthwise growth, no column sampling, no monotone
+constraints. The host arithmetic the reference performs between the calls
+(node gains, leaf weights) comes from the library (hbr_node_gain,
+hbr_leaf_weight). The sums are fixed point with the guard resolving near
+ties on the device (HBR_GUARD_RESOLVE), so no node comes back for a host
+replay; one that does (a NaN score) stops the round with an error, the
+reference's `None`: the caller redoes the round on its own path.
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 
 import numpy as np
 
-from hessboost_amd import _capi as A
-from oracle import oracle as O
+from . import _capi as A
 
 F32_MAX = float(np.finfo(np.float32).max)
 
@@ -40,36 +43,42 @@ class Best:
         self.left, self.right, self.valid_split = left, right, valid_split
 
 
-class Driver:
-    """One engine over a dense index, driven through hbr_* row-engine calls."""
+class RowEngineRounds:
+    """Depthwise logistic or squared-error rounds over one engine (dense
+    index), driven through hbr_* row-engine calls."""
 
-    def __init__(self, engine, cuts_fo, cut_values, params: dict):
+    def __init__(self, engine, feature_offset, cut_values, params: dict, loss=A.LOSS_LOGISTIC):
         self.e = engine
-        self.fo = np.asarray(cuts_fo, np.int64)
+        self.fo = np.asarray(feature_offset, np.int64)
         self.cuts = np.asarray(cut_values, np.float32)
         self.max_depth = params.get("max_depth", 6)
-        self.eta = np.float32(params.get("eta", 0.3))
-        self.p = O.params(objective=O.OBJ_LOGISTIC, max_depth=self.max_depth, eta=float(self.eta),
-                          gamma=params.get("gamma", 0.0), reg_lambda=params.get("lambda", 1.0),
-                          min_child_weight=params.get("min_child_weight", 1.0))
-        self.reg = (params.get("lambda", 1.0), 0.0, 0.0, params.get("min_child_weight", 1.0))
+        self.eta = np.float32(params.get("eta", params.get("learning_rate", 0.3)))
+        self.gamma = float(params.get("gamma", 0.0))
+        self.mcw = float(params.get("min_child_weight", 1.0))
+        self.reg = (params.get("lambda", 1.0), params.get("alpha", 0.0), params.get("max_delta_step", 0.0), self.mcw)
+        self._rp = A.RegParams(*self.reg)
+        self.loss = loss
         self.replays = 0
-        self.audit = None  # a list: every certified numeric winner with the host's evaluation of its exact sums
+        self.audit = None  # a list: every certified numeric winner with read_hist's sums of its node
         self.margins_loaded = False
-        self.ds = None  # the oracle's index, for replays (set by the caller)
+        engine.set_guard("resolve", self.gamma)
 
-    # ---- host arithmetic (the reference's builder, as the oracle restates it) ----
+    # ---- host arithmetic (the reference's builder, through the library) --------
     def node_gain(self, st, lower=-math.inf, upper=math.inf):
-        return O.lib().or_node_gain(st.g, st.h, lower, upper, self.p)
+        out = C.c_float()
+        A.check(A.lib().hbr_node_gain(C.byref(self._rp), st.g, st.h, lower, upper, C.byref(out)))
+        return out.value
 
-    def valid(self, b: Best):
-        s = O.Split()
-        s.loss_chg, s.left_h, s.right_h = b.loss_chg, b.left.h, b.right.h
-        return bool(O.lib().or_split_valid(s, self.p))
+    def valid(self, b):
+        """BestSplit::valid (builder/mod.rs:167-193)."""
+        lh, rh = b.left.h, b.right.h
+        return (b.loss_chg > 1e-6 and b.loss_chg >= self.gamma and lh > 0.0 and rh > 0.0 and lh >= self.mcw
+                and rh >= self.mcw)
 
     def leaf_value(self, st):
-        w = np.float32(O.lib().or_calc_weight(st.g, st.h, self.p))
-        return np.float32(w * self.eta)
+        out = C.c_float()
+        A.check(A.lib().hbr_leaf_weight(C.byref(self._rp), st.g, st.h, -math.inf, math.inf, C.byref(out)))
+        return np.float32(np.float32(out.value) * self.eta)
 
     # ---- resident search (device.rs:530-700) -------------------------------------
     def search(self, nodes):
@@ -80,12 +89,9 @@ class Driver:
         out = []
         for (slot, st), sc in zip(nodes, scans):
             if sc.kind == A.SCAN_REPLAY:
-                # resident_merge: the node's histogram, evaluated on the host
+                # NodeScan::Replay (a NaN score): this host has no search of its own
                 self.replays += 1
-                hist = self.e.read_hist(slot)
-                s = self.ds.evaluate(hist, (st.g, st.h), self.p)
-                b = Best(s.loss_chg, s.feature, s.bin, bool(s.default_left), Stats(s.left_g, s.left_h),
-                         Stats(s.right_g, s.right_h))
+                raise RuntimeError(f"row engine: node in slot {slot} needs a host replay (reason {sc.fallback})")
             elif sc.kind == A.SCAN_EMPTY:
                 b = Best()
             else:
@@ -107,8 +113,9 @@ class Driver:
             if b.left is not None:
                 b.valid_split = self.valid(b)
             if self.audit is not None and sc.kind == A.SCAN_NUMERIC:
-                exact = self.ds.evaluate(self.e.read_hist(slot), (st.g, st.h), self.p)
-                self.audit.append((sc.feature, b.bin, b.default_left, sc.loss_chg, sc.loss_err, exact))
+                self.audit.append(dict(slot=slot, total=(st.g, st.h), feature=sc.feature, bin=b.bin,
+                                       default_left=b.default_left, loss=sc.loss_chg, err=sc.loss_err,
+                                       hist=self.e.read_hist(slot)))
             out.append(b)
         return out
 
@@ -120,7 +127,8 @@ class Driver:
         root = Stats(tot[0], tot[1], (int(fx[0]), int(fx[1])))
         n_rows = int(root_seg.len)
         reserved = min(1 << (self.max_depth - 1), max(n_rows, 1))
-        assert e.reserve_hists(reserved)
+        if not e.reserve_hists(reserved):
+            raise RuntimeError("row engine: the histogram slots do not fit")
         free, next_slot = [], [0]
 
         def take():
@@ -209,7 +217,8 @@ class Driver:
         if not self.margins_loaded:
             e.load_margins(margins)
             self.margins_loaded = True
-        assert e.gradients(A.LOSS_LOGISTIC, labels)
+        if not e.gradients(self.loss, labels):
+            raise RuntimeError("row engine: non-finite gradients (the reference grows this round on the host)")
         nodes, leaves = self.grow()
         e.add_leaf_values([seg for _, seg, _ in leaves], [nodes[nid]["leaf_value"] for nid, _, _ in leaves])
         return nodes

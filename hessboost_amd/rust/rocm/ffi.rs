@@ -34,6 +34,9 @@ pub const HBR_FALLBACK_NUMERIC_SCORE: u32 = 1;
 pub const HBR_FALLBACK_CATEGORICAL_ORDER: u32 = 2;
 pub const HBR_FALLBACK_CATEGORICAL_SCORE: u32 = 3;
 pub const HBR_FALLBACK_NEAR_TIE: u32 = 4;
+pub const HBR_GUARD_OFF: c_int = 0;
+pub const HBR_GUARD_REPLAY: c_int = 1;
+pub const HBR_GUARD_RESOLVE: c_int = 2;
 
 pub const HBR_OBJ_SQUARED_ERROR: i32 = 0;
 pub const HBR_OBJ_LOGISTIC: i32 = 1;
@@ -196,6 +199,7 @@ pub struct hbr_engine_counters {
     pub partition_rows: u64,
     pub trees: u64,
     pub near_ties: u64,
+    pub near_ties_resolved: u64,
 }
 
 #[repr(C)]
@@ -303,7 +307,10 @@ extern "C" {
                              requests: *const hbr_scan_request, n: u64, out: *mut hbr_node_scan) -> c_int;
     pub fn hbr_scan_categories(e: *mut hbr_engine, out: *mut u32, n: u64) -> c_int;
     pub fn hbr_read_hist(e: *mut hbr_engine, slot: u32, out: *mut f64) -> c_int;
-    pub fn hbr_engine_set_guard(e: *mut hbr_engine, on: c_int, gamma: f64) -> c_int;
+    pub fn hbr_engine_set_guard(e: *mut hbr_engine, mode: c_int, gamma: f64) -> c_int;
+    pub fn hbr_node_gain(reg: *const hbr_reg_params, g: f64, h: f64, lower: f64, upper: f64, out: *mut f32) -> c_int;
+    pub fn hbr_leaf_weight(reg: *const hbr_reg_params, g: f64, h: f64, lower: f64, upper: f64, out: *mut f32)
+                           -> c_int;
     pub fn hbr_engine_counters_read(e: *mut hbr_engine, out: *mut hbr_engine_counters) -> c_int;
     pub fn hbr_set_profiling(e: *mut hbr_engine, on: c_int, kernel_prefix: *const c_char) -> c_int;
     pub fn hbr_kernel_stats(e: *mut hbr_engine, buf: *mut c_char, len: usize) -> c_int;

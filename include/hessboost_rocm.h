@@ -415,11 +415,36 @@ int hbr_scan_categories(hbr_engine *e, uint32_t *out, uint64_t n);
 int hbr_read_hist(hbr_engine *e, uint32_t slot, double *out);
 
 /* No counterpart in the reference: the fixed-point guard of
- * hbr_scan_resident and of the whole-round trainer. on: certify winners
- * (the default); gamma: the caller's min_split_loss, the validity threshold
- * the guard checks beside kRtEps (1e-6). Nodes the guard cannot certify are
- * counted in hbr_engine_counters.near_ties. */
-int hbr_engine_set_guard(hbr_engine *e, int on, double gamma);
+ * hbr_scan_resident and of the whole-round trainer. Beyond the exact domain
+ * each numeric winner's score is bounded (the quantisation of every row's
+ * pair, the f64 rounding of the CPU's sums, the f32 roundings of the score)
+ * against every other partition of the node's rows and against the
+ * validity threshold. A node it cannot certify is:
+ *   HBR_GUARD_RESOLVE (the default): searched again on the device over its
+ *     histogram in the CPU builder's own f64 sums (hbr_read_hist's), and
+ *     returned as that search's winner (HBR_SCAN_NUMERIC or _EMPTY), with
+ *     the CPU's f64 child statistics and their fixed-point sums;
+ *   HBR_GUARD_REPLAY: returned as HBR_SCAN_REPLAY, HBR_FALLBACK_NEAR_TIE,
+ *     for the host's own replay from hbr_read_hist;
+ *   HBR_GUARD_OFF: returned as the fixed-point winner.
+ * gamma: the caller's min_split_loss, checked beside kRtEps (1e-6). The
+ * whole-round trainer counts the nodes its device decisions could not
+ * certify (hbr_engine_counters.near_ties). */
+/* No counterpart in the reference's interface (its builder computes them
+ * itself between row-engine calls): the host arithmetic a caller of the row
+ * engine needs, as the reference's CPU builder performs it with its
+ * RegParams rounded to f32 (tree/gain.rs:82-116): a node's gain at its
+ * bounded weight (xgb_node_gain, builder/shared.rs:131-141: the root_gain
+ * of a ScanRequest) and a leaf's bounded weight before eta
+ * (calc_weight_bounded, tree/constraints.rs; finish_leaf_values,
+ * builder/shared.rs:174-187). Host only: no device is touched. */
+int hbr_node_gain(const hbr_reg_params *reg, double g, double h, double lower, double upper, float *out);
+int hbr_leaf_weight(const hbr_reg_params *reg, double g, double h, double lower, double upper, float *out);
+
+#define HBR_GUARD_OFF 0
+#define HBR_GUARD_REPLAY 1
+#define HBR_GUARD_RESOLVE 2
+int hbr_engine_set_guard(hbr_engine *e, int mode, double gamma);
 
 /* Work counters since the engine opened (no counterpart in the reference;
  * they give the algorithmic bytes the roofline figures divide by). */
@@ -431,6 +456,7 @@ typedef struct hbr_engine_counters {
     uint64_t trees;
     uint64_t near_ties;        /* decided nodes whose winner the fixed-point guard could not
                                   certify (see hbr_engine_set_guard) */
+    uint64_t near_ties_resolved; /* of those, searched again on the CPU builder's sums on the device */
 } hbr_engine_counters;
 int hbr_engine_counters_read(hbr_engine *e, hbr_engine_counters *out);
 

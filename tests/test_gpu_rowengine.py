@@ -1,15 +1,17 @@
 """hessboost's device-resident rounds through the row-engine calls of the C
-ABI (the call sequence of build_device_staged, driven by tests/rowengine.py)
-with fixed-point sums and the guard that certifies each winner:
+ABI (the call sequence of build_device_staged, as hessboost_amd.rowengine
+issues it) with fixed-point sums and the guard that certifies each winner:
 
 * hbr_read_hist gives a node's histogram as the reference's CPU builder
   has it, bit for bit: built nodes summed in the CPU build's f64 order (one
   chain, or blocks of rows beyond 2^18 index rows), siblings as their
   parent's minus the built child's;
-* the guard replays a designed near tie (two features whose best
-  partitions differ by one row of tiny gradient) and certifies exact ties
-  of duplicate features; every winner it certifies is the one the host
-  would pick from the exact sums, within the loss bound it reports;
+* the guard catches a designed near tie (two features whose best
+  partitions differ by one row of small gradient): it resolves it on the
+  device to the winner of the CPU builder's sums (the oracle's split, bit
+  for bit), or reports it for a host replay; it certifies exact ties of
+  duplicate features; every winner it certifies is the one the host would
+  pick from the exact sums, within the loss bound it reports;
 * three rounds of the 10,500,000 x 28 logistic workload grown this way
   match the oracle's first three trees node for node.
 """
@@ -21,7 +23,7 @@ from hessboost_amd import _capi as A
 from hessboost_amd import synthetic
 from oracle import oracle as O
 from tests.golden.make_full_runs import unpack
-from tests.rowengine import Driver, as_tree
+from hessboost_amd.rowengine import RowEngineRounds, as_tree
 from tests.test_gpu_full_runs import fixture
 from tests.test_gpu_train import compare_trees
 
@@ -103,31 +105,46 @@ def root_scan(e, y, m):
     e.build_resident([(ds_root, 0)])
     p = O.params(objective=O.OBJ_LOGISTIC)
     gain = O.lib().or_node_gain(tot[0], tot[1], -np.inf, np.inf, p)
+    root_scan.total = tuple(tot)
     return e.scan_resident((1.0, 0.0, 0.0, 1.0), [dict(slot=0, total=tuple(tot), fixed=tuple(fx), root_gain=gain)])[0]
 
 
-def test_guard_replays_a_near_tie_and_certifies_duplicate_features():
+def test_guard_resolves_or_replays_a_near_tie_and_certifies_duplicate_features():
     x, y, m = near_tie_data(perturb=True)
-    e = logistic_engine(x, y, m)
-    sc = root_scan(e, y, m)
-    assert sc.kind == A.SCAN_REPLAY and sc.fallback == A.FALLBACK_NEAR_TIE
-    assert e.counters()["near_ties"] == 1
-    # the replay's sums are the CPU's, and the host's choice from them is the oracle's
     ds = O.Dataset(x, max_bin=256)
     gp = O.gradient(O.OBJ_LOGISTIC, m, y)
-    hist = e.read_hist(0)
-    assert np.array_equal(bits(hist), bits(ds.build_hist(np.arange(len(y), dtype=np.uint32), gp)))
+    rows = np.arange(len(y), dtype=np.uint32)
     nodes, _ = ds.grow_tree(gp, O.params(objective=O.OBJ_LOGISTIC, max_depth=1))
-    s = ds.evaluate(hist, O.sum_rows(gp, np.arange(len(y), dtype=np.uint32)), O.params(objective=O.OBJ_LOGISTIC))
+    # the default: resolved on the device, the CPU builder's winner
+    e = logistic_engine(x, y, m)
+    sc = root_scan(e, y, m)
+    assert sc.kind == A.SCAN_NUMERIC
+    c = e.counters()
+    assert c["near_ties"] == 1 and c["near_ties_resolved"] == 1
+    fs = int(ds.feature_offset[sc.feature])
+    bin_ = (fs + sc.offset - 1 if sc.offset else -1) if sc.backward else fs + sc.offset
+    assert (sc.feature, bin_, bool(sc.backward)) == (nodes[0]["split_feature"], nodes[0]["split_bin"],
+                                                   bool(nodes[0]["default_left"]))
+    s = ds.evaluate(e.read_hist(0), root_scan.total, O.params(objective=O.OBJ_LOGISTIC))
+    assert np.float32(sc.loss_chg) == np.float32(s.loss_chg) and sc.left_g == s.left_g and sc.left_h == s.left_h
+    # reported for a host replay: its sums are the CPU's, and the host's choice from them is the oracle's
+    e = logistic_engine(x, y, m)
+    e.set_guard("replay")
+    sc = root_scan(e, y, m)
+    assert sc.kind == A.SCAN_REPLAY and sc.fallback == A.FALLBACK_NEAR_TIE
+    hist = e.read_hist(0)
+    assert np.array_equal(bits(hist), bits(ds.build_hist(rows, gp)))
+    s = ds.evaluate(hist, O.sum_rows(gp, rows), O.params(objective=O.OBJ_LOGISTIC))
     assert (s.feature, s.bin) == (nodes[0]["split_feature"], nodes[0]["split_bin"])
     # without the guard the same scan is a plain winner
-    e.set_guard(False)
+    e.set_guard("off")
     assert root_scan(e, y, m).kind == A.SCAN_NUMERIC
     # exact duplicates are one partition: certified, the lower feature wins
     x2, y2, m2 = near_tie_data(perturb=False)
     e2 = logistic_engine(x2, y2, m2)
     sc2 = root_scan(e2, y2, m2)
     assert sc2.kind == A.SCAN_NUMERIC and sc2.feature == 0 and sc2.loss_err > 0
+    assert e2.counters()["near_ties"] == 0
 
 
 def test_certified_winners_are_the_exact_sums_winners():
@@ -140,16 +157,17 @@ def test_certified_winners_are_the_exact_sums_winners():
     e.set_sums("fixed_point")
     ds = O.Dataset(x, max_bin=256)
     fo, cuts = ds.feature_offset, ds.cut_values
-    d = Driver(e, fo, cuts, {"max_depth": 6, "eta": 0.3})
-    d.ds = ds
+    d = RowEngineRounds(e, fo, cuts, {"max_depth": 6, "eta": 0.3})
     d.audit = []
+    p = O.params(objective=O.OBJ_LOGISTIC, max_depth=6, eta=0.3)
     m = np.zeros(n, np.float32)
     for _ in range(2):
         d.device_round(m, y)
     assert len(d.audit) > 50
-    for feature, bin_, dl, loss, err, exact in d.audit:
-        assert (exact.feature, exact.bin, bool(exact.default_left)) == (feature, bin_, dl)
-        assert abs(float(exact.loss_chg) - float(loss)) <= float(err)
+    for a in d.audit:
+        exact = ds.evaluate(a["hist"], a["total"], p)
+        assert (exact.feature, exact.bin, bool(exact.default_left)) == (a["feature"], a["bin"], a["default_left"])
+        assert abs(float(exact.loss_chg) - float(a["loss"])) <= float(a["err"])
 
 
 def test_three_rounds_of_the_higgs_workload_through_the_row_engine_match_oracle():
@@ -164,12 +182,12 @@ def test_three_rounds_of_the_higgs_workload_through_the_row_engine_match_oracle(
     e.set_sums("fixed_point")
     cuts = d_x.cuts(256)
     fo, cv = cuts.arrays()
-    ds = O.Dataset(x, max_bin=256)
     del x
-    d = Driver(e, fo, cv, {"max_depth": 8, "eta": 0.1})
-    d.ds = ds
+    d = RowEngineRounds(e, fo, cv, {"max_depth": 8, "eta": 0.1})
     base = np.float32(z["base_score"][0])
     m = np.full(len(y), base, np.float32)
     got = [as_tree(d.device_round(m, y)) for _ in range(3)]
     compare_trees(got, want)
-    print(f"replays {d.replays}, near ties {e.counters()['near_ties']}")
+    c = e.counters()
+    print(f"near ties {c['near_ties']}, resolved {c['near_ties_resolved']}")
+    assert d.replays == 0
