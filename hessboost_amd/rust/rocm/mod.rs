@@ -13,8 +13,14 @@
 //! the GPU; each trait call is one library call. Histograms are summed in
 //! fixed point (exact integers in a per-tree unit): inside the exact domain
 //! of `backend/exact_sum.rs:14-37` they are the CPU's `f64` sums bit for
-//! bit; outside it the library refuses (`HBR_REFUSED`) and this module sums
-//! on the host, as `CudaHistBackend` does (src/backend/cuda/mod.rs:2758-2776).
+//! bit. Beyond it the training parameter `rocm_sums` ([`RocmSums`]) decides:
+//! `fixed_point` (the default for `device = rocm`) keeps every round on the
+//! device with the fixed-point sums, each split certified by the library's
+//! guard against the CPU's `f64` sums and any node it cannot certify
+//! searched again on the device over the node's histogram in the CPU
+//! builder's own summation order; `exact` makes the library refuse
+//! (`HBR_REFUSED`) and this module sum on the host, as `CudaHistBackend`
+//! does outside its exact domain (src/backend/cuda/mod.rs:2758-2776).
 //!
 //! **Prediction**: [`RocmModel`] ([`BoostedModel::to_rocm`]) uploads the
 //! forest once; margins are walked on the GPU, the objective's transform
@@ -110,6 +116,33 @@ impl StagedSlice {
         Self {
             ptr: gpair.as_ptr() as usize,
             len: gpair.len(),
+        }
+    }
+}
+
+/// How the backend sums beyond the exact domain (the training parameter
+/// `rocm_sums`, `fixed_point` or `exact`).
+#[derive(Debug, Clone, Copy, PartialEq, Eq, Default)]
+pub enum RocmSums {
+    /// Fixed-point sums on the device, every split certified against the
+    /// CPU's `f64` sums (near ties resolved on the device's copy of those
+    /// sums): whole rounds stay on the GPU. Tree structure equals the CPU's;
+    /// leaf values and statistics are within the fixed point's error (the
+    /// north star's 1e-5 relative).
+    #[default]
+    FixedPoint,
+    /// Only sums equal to the CPU's bit for bit: the library refuses beyond
+    /// the exact domain and the host sums, as the CUDA backend does.
+    Exact,
+}
+
+impl RocmSums {
+    /// The parameter's spellings.
+    pub fn parse(value: &str) -> Option<Self> {
+        match value {
+            "fixed_point" => Some(Self::FixedPoint),
+            "exact" => Some(Self::Exact),
+            _ => None,
         }
     }
 }
@@ -212,6 +245,21 @@ impl RocmHistBackend {
             failed: AtomicBool::new(false),
             staged: Mutex::new(None),
         })
+    }
+
+    /// The summing mode of a training run (`rocm_sums`) and its `gamma`
+    /// (`min_split_loss`), the validity threshold the guard checks: fixed
+    /// point selects `HBR_SUMS_FIXED_POINT` with the guard resolving near ties
+    /// on the device (`HBR_GUARD_RESOLVE`); exact keeps `HBR_SUMS_EXACT`.
+    pub fn with_sums(self, sums: RocmSums, gamma: f64) -> Result<Self> {
+        let mode = match sums {
+            RocmSums::FixedPoint => ffi::HBR_SUMS_FIXED_POINT,
+            RocmSums::Exact => ffi::HBR_SUMS_EXACT,
+        };
+        // SAFETY: a live handle; plain values.
+        check(unsafe { ffi::hbr_engine_set_sums(self.e(), mode) })?;
+        check(unsafe { ffi::hbr_engine_set_guard(self.e(), ffi::HBR_GUARD_RESOLVE, gamma) })?;
+        Ok(self)
     }
 
     /// The CUDA device ordinal's counterpart: the ROCm device this backend
@@ -611,6 +659,9 @@ impl RowEngine for RocmHistBackend {
                         right: GradStats::new(s.right_g, s.right_h),
                         categories: pool[s.cat_begin as usize..s.cat_end as usize].to_vec(),
                     },
+                    // a near tie comes back only with HBR_GUARD_REPLAY (this module
+                    // resolves them on the device): the builder replays the node from
+                    // read_hist, which returns the CPU builder's own sums
                     ffi::HBR_SCAN_REPLAY => NodeScan::Replay(match s.fallback {
                         ffi::HBR_FALLBACK_CATEGORICAL_ORDER => ScanFallback::CategoricalOrder,
                         ffi::HBR_FALLBACK_CATEGORICAL_SCORE => ScanFallback::CategoricalScore,

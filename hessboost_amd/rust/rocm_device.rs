@@ -17,12 +17,19 @@
 //! - `Device::is_compiled_in` (params.rs:231-240) answers [`COMPILED_IN`]
 //!   for `Rocm`, and `TrainingParams::validate` calls [`validate`];
 //! - `hist_backend` (src/training/prepare.rs:356-416) gains the arm
-//!   `Device::Rocm { ordinal } => rocm_device::hist_backend(index, ordinal)`.
+//!   `Device::Rocm { ordinal } => rocm_device::hist_backend(params, index, ordinal)`;
+//! - `TrainingParams` (src/config/params.rs) gains `rocm_sums: RocmSums`
+//!   (`"fixed_point"`, the default, or `"exact"`; parsed with
+//!   [`rocm::RocmSums::parse`] beside the other string parameters).
 //!
 //! Device-resident rounds (`Prepared::device_backend`, prepare.rs:94-103,
-//! and `device_round`, src/training/round.rs:105-148) need nothing more:
-//! they drive the same `RowEngine` calls.
+//! and `device_round`, src/training/round.rs:105-148) drive the same
+//! `RowEngine` calls. With `rocm_sums = fixed_point` they stay on the device
+//! past the exact domain (the 10.5M-row logistic workload leaves it from its
+//! second round); with `exact` the library refuses there and those rounds
+//! run on the host.
 
+use crate::config::TrainingParams;
 use crate::data::ghist::GHistIndex;
 use crate::error::{HessboostError, Result};
 use crate::tree::hist::HistogramBackend;
@@ -79,17 +86,19 @@ pub fn validate(_ordinal: usize) -> Result<()> {
     ))
 }
 
-/// The `Device::Rocm { ordinal }` arm of `hist_backend`.
+/// The `Device::Rocm { ordinal }` arm of `hist_backend`: the backend in the
+/// run's summing mode, its guard checking the run's `gamma`.
 #[cfg(all(target_os = "linux", feature = "rocm"))]
-pub fn hist_backend(index: &GHistIndex, ordinal: usize) -> Result<Box<dyn HistogramBackend>> {
-    let backend: Box<dyn HistogramBackend> = Box::new(rocm::RocmHistBackend::new(index, ordinal)?);
+pub fn hist_backend(params: &TrainingParams, index: &GHistIndex, ordinal: usize) -> Result<Box<dyn HistogramBackend>> {
+    let backend = rocm::RocmHistBackend::new(index, ordinal)?.with_sums(params.rocm_sums, params.gamma)?;
+    let backend: Box<dyn HistogramBackend> = Box::new(backend);
     Ok(backend)
 }
 
 /// Unreachable in practice where the backend is not compiled in:
 /// validation refuses `device = rocm` first, as for `cuda`.
 #[cfg(not(all(target_os = "linux", feature = "rocm")))]
-pub fn hist_backend(_index: &GHistIndex, _ordinal: usize) -> Result<Box<dyn HistogramBackend>> {
+pub fn hist_backend(_params: &TrainingParams, _index: &GHistIndex, _ordinal: usize) -> Result<Box<dyn HistogramBackend>> {
     validate(0).map(|()| unreachable!())
 }
 
