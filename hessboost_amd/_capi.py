@@ -120,6 +120,7 @@ class ForestDesc(C.Structure):
 SIGNATURES = {
     "hbr_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
     "hbr_device_count": (C.c_int, [P(C.c_int)]),
+    "hbr_device_name": (C.c_int, [C.c_int, C.c_char_p, C.c_size_t]),
     "hbr_cuts_from_dense": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.c_void_p, C.c_float, P(C.c_void_p)]),
     "hbr_cuts_from_csr": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.c_void_p, P(C.c_void_p)]),
     "hbr_cuts_from_values": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, P(C.c_void_p)]),

@@ -201,6 +201,16 @@ int hbr_device_count(int *count) {
     });
 }
 
+int hbr_device_name(int ordinal, char *buf, size_t len) {
+    return guard([&] {
+        if (!buf && len) fail(kInvalid, "device_name: null buffer");
+        if (ordinal < 0 || ordinal >= device_count()) fail(kInvalid, "device_name: no such device");
+        hipDeviceProp_t p;
+        HBR_HIP(hipGetDeviceProperties(&p, ordinal));
+        copy_string(std::string(p.name) + " (" + p.gcnArchName + ")", buf, len);
+    });
+}
+
 // ---- cuts and index -----------------------------------------------------------
 
 int hbr_cuts_from_dense(const float *x, uint64_t n, uint64_t f, uint32_t max_bin, const float *weights,

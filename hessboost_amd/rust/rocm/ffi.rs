@@ -249,6 +249,7 @@ pub struct hbr_forest_desc {
 extern "C" {
     pub fn hbr_last_error(buf: *mut c_char, len: usize) -> usize;
     pub fn hbr_device_count(count: *mut c_int) -> c_int;
+    pub fn hbr_device_name(ordinal: c_int, buf: *mut c_char, len: usize) -> c_int;
     pub fn hbr_cuts_from_dense(x: *const f32, n_rows: u64, n_cols: u64, max_bin: u32, weights: *const f32,
                                missing: f32, out: *mut *mut hbr_cuts) -> c_int;
     pub fn hbr_cuts_from_csr(row_ptr: *const u64, col: *const u32, val: *const f32, n_rows: u64, n_cols: u64,

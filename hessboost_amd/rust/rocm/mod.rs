@@ -103,6 +103,18 @@ pub fn available(ordinal: usize) -> bool {
     ordinal < device_count()
 }
 
+/// The name and architecture of ROCm device `ordinal`, if it exists.
+pub fn device_name(ordinal: usize) -> Option<String> {
+    let ordinal = c_int::try_from(ordinal).ok()?;
+    let mut buf = [0 as c_char; 256];
+    // SAFETY: the buffer's length bounds the write, NUL included.
+    if unsafe { ffi::hbr_device_name(ordinal, buf.as_mut_ptr(), buf.len()) } != ffi::HBR_OK {
+        return None;
+    }
+    // SAFETY: NUL-terminated within the buffer.
+    Some(unsafe { std::ffi::CStr::from_ptr(buf.as_ptr()) }.to_string_lossy().into_owned())
+}
+
 /// The gradient slice [`HistogramBackend::prepare`] staged, by address and
 /// length: a `build` of the same slice reads what the device holds.
 #[derive(Clone, Copy, PartialEq, Eq)]

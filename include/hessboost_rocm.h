@@ -48,6 +48,11 @@ size_t hbr_last_error(char *buf, size_t len);
 /* Number of ROCm devices visible to the process. */
 int hbr_device_count(int *count);
 
+/* The name and architecture of device `ordinal` (for diagnostics, as the
+ * Python GpuModel.device_name reports it, python/src/gpu.rs:196-203),
+ * NUL-terminated and cut to len bytes. */
+int hbr_device_name(int ordinal, char *buf, size_t len);
+
 /* ------------------------------------------------------------------------- */
 /* Cuts and binned index (host; once per dataset).                            */
 /* ------------------------------------------------------------------------- */
