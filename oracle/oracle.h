@@ -33,14 +33,22 @@
  * (simd/tests.rs:133-285) pin the 2- and 4-class vector batches to the
  * scalar rows (1e-6, and bit for bit on underflowing rows).
  *
+ * The sketch's prune/merge on data with more distinct values than max_bin
+ * is pinned by brute-force rank bounds on every summary it forms, by
+ * XGBoost's per-query SetPrune and three-case SetCombine as other
+ * formulations, and by the summary budget's definition
+ * (tests/test_sketch.py, through the or_summary_* and or_sketch_trace
+ * hooks below). The lossguide order under equal gains is pinned by a brute
+ * force over its queue events and by Rust's BinaryHeap algorithm
+ * (tests/test_oracle.py, through or_lossguide_trace).
+ *
  * Parity unpinned (nothing the reference holds reaches them):
- *   - the weighted sketch's prune/merge on data with more distinct values
- *     than max_bin (checked by quantile properties only);
- *   - the lossguide expansion order (heap ties), grow.c;
  *   - softmax gradients bit for bit: the scalar rows call the host libm
  *     expf, as the reference's f32::exp does, so bits match only for the
  *     same libm; the 2- and 4-class vector batches follow the reference's
- *     intrinsic sequence, pinned to 1e-6 only.
+ *     intrinsic sequence, pinned to 1e-6 only;
+ *   - the sketch's queue order with fractional weights (the reference's
+ *     unstable sort; whole-number weights sum exactly in any order).
  */
 #ifndef HB_ORACLE_H
 #define HB_ORACLE_H
