@@ -199,8 +199,14 @@ def other_workload(args):
                   "eta": 0.3, "max_bin": 64}
         dm = hb.DMatrix((row_ptr, col, val), label=y, n_cols=2000)
         workload = "sparse hist training, 500,000 x 2,000 CSR f32 (90% missing), max_bin 64, lossguide 255 leaves"
+    if args.nan_rate > 0 and args.workload != "sparse":
+        # missing cells: the masked dense rows (or, with HBROCM_MASKED_ROWS=0, CSR rows)
+        x[np.random.default_rng(1).random(x.shape, dtype=np.float32) < args.nan_rate] = np.nan
+        dm = hb.DMatrix(x, label=y)
+        workload += f", {args.nan_rate:.0%} of cells missing (NaN)"
     log(f"generated {args.workload} data in {time.time() - t:.1f}s")
     eng = dm.engine(params["max_bin"])
+    log(f"index: {eng.index_info()}")
     trainer = hb.Trainer(eng, params, y)
     trainer.boost(args.warmup)
     t0 = time.perf_counter()
@@ -281,6 +287,8 @@ def main():
                     help="higgs: the default line; multiclass (2M x 50, 10-class softmax, depth 6) and "
                          "sparse (500k x 2000 CSR, 90%% missing, lossguide 255 leaves): their training "
                          "rounds/s on a line of their own")
+    ap.add_argument("--nan-rate", type=float, default=0.0,
+                    help="regression and multiclass: this fraction of the cells set missing (NaN)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",

@@ -102,19 +102,26 @@ struct BinArgs {
     uint32_t row_mask;              // n_cols <= kMaskedMaxFeatures: the row's missing mask in its last word
 };
 
-// Dense u8 rows of a matrix with missing values (at most kMaskedMaxFeatures
-// features, rows of 32 bytes): a missing cell's byte is 0 and bit f of the
-// row's last word (kMaskWord) marks feature f missing. The histogram kernel
-// skips masked cells; the margin walks send them the split's default way.
+// Dense u8 rows of a matrix with missing values: a missing cell's byte is 0
+// and a mask bit marks it. At most kMaskedMaxFeatures features: rows of 32
+// bytes, bit f of the row's last word (kMaskWord) for feature f. Wider (at
+// most kMaskedWideMaxFeatures): the bins of G = ceil(F / 32) groups of 32
+// features, then a 32-byte chunk of mask words, word g (at byte 32 G + 4 g)
+// for group g's features. A row's mask words start at its `mask_at` byte
+// (28, or 32 G). The histogram kernel skips masked cells; the margin walks
+// send them the split's default way.
 constexpr uint32_t kMaskedMaxFeatures = 28;
+constexpr uint32_t kMaskedWideMaxFeatures = 256;
 constexpr uint32_t kMaskWord = 7;
 struct RowsFromColsArgs {
     const uint8_t *cols8;       // [n_cols][n_rows]
     const uint64_t *missing;    // [n_cols][words] or null
-    uint8_t *rows8;             // [n_rows][32]
+    uint8_t *rows8;             // [n_rows][stride]
     uint64_t n_rows;
     uint32_t n_cols;
     uint32_t words;
+    uint32_t stride;            // 32, or 32 G + 32
+    uint32_t mask_at;           // byte of the first mask word: 28, or 32 G
 };
 
 // Exclusive scan of the rows' present counts into row_ptr (n_rows + 1):
@@ -194,6 +201,8 @@ struct IotaArgs {
 };
 
 // ---- root totals -------------------------------------------------------------
+// One sum per blockIdx.y (a tree of a level of trees): its pairs from
+// gpair + y tree_pairs, its scale at scale + y, its sums into out + y.
 struct TotalArgs {
     const uint32_t *rows;   // null: contiguous from `first`
     uint32_t first;
@@ -201,7 +210,11 @@ struct TotalArgs {
     const GPair *gpair;
     const QScale *scale;
     QBin *out;              // accumulated with 64-bit atomics (zeroed before)
+    uint64_t tree_pairs;
 };
+// Workgroups per sum: few enough that their atomics on the one total do
+// not queue for longer than the rows take to read.
+constexpr uint32_t kTotalBlocks = 256;
 
 // ---- level counts on the device ---------------------------------------------------
 // A depthwise tree grown on the device: each level's decision kernel writes
@@ -337,7 +350,8 @@ struct ExactArgs {
     const GPair *gpair;      // or null with row_pairs
     uint32_t row_pairs;      // the logistic pair from each row's last word
     float min_hess;
-    uint32_t masked;         // the row's missing cells (mask word) add nowhere
+    uint32_t masked;         // the row's missing cells (mask words from byte mask_at) add nowhere
+    uint32_t mask_at;
     uint32_t total_bins;
     double *partial;         // per block of the launch: total_bins x (g, h)
 };
@@ -378,8 +392,8 @@ struct HistArgs {
     // and h = max(p * (1 - p), min_hess), instead of gpair.
     uint32_t row_pairs;
     float min_hess;
-    uint32_t masked;            // rows carry a missing mask in word kMaskWord (32-byte rows, fg32)
-    uint32_t pad3;
+    uint32_t masked;            // rows carry missing masks (fg32 groups; the mask words at mask_at)
+    uint32_t mask_at;           // masked: the byte of a row's first mask word (28: 32-byte rows)
 };
 
 // Each CSR row's first entry of every kCsrGroupBins range (rows' global bins ascend).
@@ -718,15 +732,16 @@ struct WalkArgs {
     // stays set until the host clears it.
     const QScale *guard;
     uint32_t *poison;
-    // Rows carry a missing mask (kMaskWord): a masked feature sends the row
-    // the way of the node's default (meta bit 15 set: left).
+    // Rows carry missing masks (their words from byte mask_at): a masked
+    // feature sends the row the way of the node's default (meta bit 15 set:
+    // left).
     uint32_t masked;
+    uint32_t mask_at;
     // hbr_walk_leaves_batch: trees walked in one pass over the rows; tree c's
     // records and counts sit c * tree_bytes after tree 0's, and its leaves
     // go to output + c.
     uint32_t n_trees;
     uint32_t tree_bytes;
-    uint32_t pad;
 };
 // Node tables of all the trees of one batched walk, in LDS.
 constexpr uint32_t kBatchWalkNodes = 2048;

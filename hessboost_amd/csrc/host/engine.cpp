@@ -221,17 +221,24 @@ void Engine::upload_index(const hbr_index_desc &d) {
     dev_.sync();
 }
 
-// A matrix with missing values and few features keeps dense u8 rows with a
-// missing mask (kMaskWord) beside its CSR rows: the histogram kernel and the
-// margin walks take them, the partition its columns and bitmap.
+// A matrix with missing values and at most kMaskedWideMaxFeatures features
+// keeps dense u8 rows with missing masks beside its CSR rows: the histogram
+// kernel and the margin walks take them, the partition its columns and
+// bitmap. Up to kMaskedMaxFeatures features a row is 32 bytes with its mask
+// in the last word; wider, the bins of G groups of 32 features and then a
+// 32-byte chunk of G mask words (32 G + 32 bytes).
 void Engine::make_masked_rows() {
-    if (dense_ || !masked_rows || !cols8_.size() || n_cols_ == 0 || n_cols_ > kMaskedMaxFeatures) return;
+    if (dense_ || !masked_rows || !cols8_.size() || n_cols_ == 0 || n_cols_ > kMaskedWideMaxFeatures) return;
     for (uint32_t f = 0; f < n_cols_; f++)
         if (fo_[f + 1] - fo_[f] > 256) return;
-    stride_ = 32;
+    const uint32_t groups = ceil_div(n_cols_, 32u);
+    const bool compact = n_cols_ <= kMaskedMaxFeatures;
+    stride_ = compact ? 32 : 32 * groups + 32;
+    mask_at_ = compact ? 4 * kMaskWord : 32 * groups;
+    rows8_.release();
     rows8_.resize(n_rows_ * stride_);
     RowsFromColsArgs a{cols8_.get(), missing_.size() ? missing_.get() : nullptr, rows8_.get(), n_rows_, n_cols_,
-                       words_};
+                       words_, stride_, mask_at_};
     dev_.launch("hbr_rows_from_cols", dim3(ceil_div(n_rows_, 256)), dim3(256), a);
     dense_u8_ = true;
     masked_ = true;
@@ -359,8 +366,11 @@ void Engine::bin_dense(const DenseSource &src) {
         dev_.sync();
         return;
     }
-    // missing values: CSR rows (and, with few features, the masked dense rows)
+    // missing values: CSR rows and, up to kMaskedWideMaxFeatures features,
+    // masked dense rows (those of 32 bytes written by the binning pass, wider
+    // ones from the columns once they are complete)
     masked_ = masked_rows && n_cols_ <= kMaskedMaxFeatures && stride_ == 32;
+    if (masked_) mask_at_ = 4 * kMaskWord;
     if (!masked_) {
         rows8_.release();
         stride_ = 0;
@@ -381,6 +391,7 @@ void Engine::bin_dense(const DenseSource &src) {
     g.n_cols = n_cols_;
     g.words = words_;
     dev_.launch("hbr_csr_fill", dim3(ceil_div(n_rows_, 256)), dim3(256), g);
+    if (!masked_) make_masked_rows();
     dev_.sync();
     if (masked_) {  // the masked rows route by the columns and bitmap
         dense_u8_ = true;
@@ -414,7 +425,7 @@ void Engine::read_index(uint8_t *rows8, uint8_t *cols8, uint64_t *missing, uint6
     dev_.sync();
     // a row's padding bytes read as zero (they may carry logistic pairs);
     // masked rows keep their missing mask
-    const uint32_t pad_end = masked_ ? 4 * kMaskWord : stride_;
+    const uint32_t pad_end = masked_ ? mask_at_ : stride_;
     if (rows8 && rows8_.size() && pad_end > n_cols_)
         for (uint64_t r = 0; r < n_rows_; r++) std::memset(rows8 + r * stride_ + n_cols_, 0, pad_end - n_cols_);
 }
@@ -801,6 +812,7 @@ void Engine::exact_segment(const Segment &sg, double *out_dev) {
     a.gpair = a.row_pairs ? nullptr : pairs();
     a.min_hess = row_pairs_min_hess_;
     a.masked = masked_ ? 1u : 0u;
+    a.mask_at = mask_at_;
     a.total_bins = total_bins_;
     a.partial = d_exact_.get();
     if (blocks == 0) HBR_HIP(hipMemsetAsync(out_dev, 0, words * sizeof(double), s));
@@ -888,7 +900,7 @@ QBin Engine::root_total(const Segment &sg) {
     a.gpair = pairs();
     a.scale = scale_dev();
     a.out = total_dev();
-    const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(sg.len, kThreads)), 2048);
+    const uint32_t blocks = std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(sg.len, kThreads)), kTotalBlocks);
     dev_.launch("hbr_total", dim3(blocks), dim3(kThreads), a);
     QBin *out = static_cast<QBin *>(stage_.alloc(sizeof(QBin)));
     HBR_HIP(hipMemcpyAsync(out, total_dev(), sizeof(QBin), hipMemcpyDeviceToHost, s));
@@ -916,7 +928,8 @@ void Engine::launch_root(const Segment &seg, uint32_t slot, float lower, float u
         t.gpair = pairs();
         t.scale = scale_dev();
         t.out = total_dev();
-        dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(seg.len, kThreads)), 2048)),
+        dev_.launch("hbr_total",
+                    dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(seg.len, kThreads)), kTotalBlocks)),
                     dim3(kThreads), t);
     }
     // the root's histogram node and scan node in one upload; the winner, the
@@ -1090,6 +1103,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     if (pair_array_stale_ && !a.row_pairs && !level_pairs_)
         fail(kRefused, "histograms: the staged pairs are carried in the rows, which this kernel does not read");
     a.masked = masked_ ? 1u : 0u;
+    a.mask_at = mask_at_;
     a.min_hess = row_pairs_min_hess_;
     const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"
@@ -1461,17 +1475,18 @@ void Engine::launch_device_roots(uint32_t n_trees) {
     QBin *totals = level_totals_ ? level_totals_ : total_dev();
     if (!(dense_ && n_cols_ > 0 && fo_[1] > fo_[0])) {
         HBR_HIP(hipMemsetAsync(totals, 0, n_trees * sizeof(QBin), s));
-        for (uint32_t t = 0; t < n_trees; t++) {
-            TotalArgs a{};
-            a.rows = nullptr;
-            a.first = 0;
-            a.n = (uint32_t)n_rows_;
-            a.gpair = (level_pairs_ ? level_pairs_ : pairs()) + (level_pairs_ ? (size_t)t * n_rows_ : 0);
-            a.scale = (level_scale_ ? level_scale_ : scale_dev()) + t;
-            a.out = totals + t;
-            dev_.launch("hbr_total", dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)), 2048)),
-                        dim3(kThreads), a);
-        }
+        // every tree's total in one launch (blockIdx.y: the tree)
+        TotalArgs a{};
+        a.rows = nullptr;
+        a.first = 0;
+        a.n = (uint32_t)n_rows_;
+        a.gpair = level_pairs_ ? level_pairs_ : pairs();
+        a.tree_pairs = level_pairs_ ? n_rows_ : 0;
+        a.scale = level_scale_ ? level_scale_ : scale_dev();
+        a.out = totals;
+        dev_.launch("hbr_total",
+                    dim3(std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, kThreads)), kTotalBlocks), n_trees),
+                    dim3(kThreads), a);
     }
     HistNode *hn = reinterpret_cast<HistNode *>(d_root_in_.get());
     const ScanNode *sn = reinterpret_cast<const ScanNode *>(d_root_in_.get() + n_trees * sizeof(HistNode));
@@ -1717,7 +1732,9 @@ bool Engine::grow_device(uint64_t max_depth, double gamma, float eta, std::vecto
 bool Engine::walk_device_trees(uint32_t first_output, uint32_t n_trees, uint32_t guard_first, uint32_t guard_n) {
     // the batch's node tables must fit the kernel's LDS whatever the trees
     const uint64_t most = (2ull << std::min<uint32_t>(last_depth_, 20u)) - 1;
-    if (!batch_walk || !dense_u8_ || (stride_ != 32 && stride_ != 64) || n_trees < 2 ||
+    // rows of 32 or 64 bytes, or masked rows of at most 64 features (96 bytes)
+    const bool rows_ok = stride_ == 32 || stride_ == 64 || (masked_ && stride_ == 96);
+    if (!batch_walk || !dense_u8_ || !rows_ok || n_trees < 2 ||
         n_trees > kBatchWalkTrees || n_trees * most > kBatchWalkNodes || first_output + n_trees > outputs_)
         return false;
     if (guard_n && (!softmax_staged() || guard_first + guard_n > class_outputs_))
@@ -1730,6 +1747,7 @@ bool Engine::walk_device_trees(uint32_t first_output, uint32_t n_trees, uint32_t
     }
     WalkArgs a{};
     a.masked = masked_ ? 1u : 0u;
+    a.mask_at = mask_at_;
     a.tree = ring_nodes(last_ring_, 0, last_stride_);
     a.counts = &ring_header(last_ring_, 0, last_stride_)->counts;
     a.tree_bytes = (uint32_t)last_stride_;
@@ -1761,6 +1779,7 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     hipStream_t s = dev_.stream();
     WalkArgs a{};
     a.masked = masked_ ? 1u : 0u;
+    a.mask_at = mask_at_;
     a.tree = ring_nodes(last_ring_, tree, last_stride_);
     a.counts = &ring_header(last_ring_, tree, last_stride_)->counts;
     a.bins8 = rows8_.get();
@@ -1989,6 +2008,7 @@ void Engine::walk_add(const std::vector<uint32_t> &meta, const std::vector<uint3
     HBR_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, s));
     WalkArgs a{};
     a.masked = masked_ ? 1u : 0u;
+    a.mask_at = mask_at_;
     a.meta = reinterpret_cast<const uint32_t *>(dev);
     a.left = reinterpret_cast<const uint32_t *>(dev + n * 4);
     a.value = reinterpret_cast<const float *>(dev + 2 * n * 4);
@@ -2131,6 +2151,7 @@ bool Engine::build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uin
     if (pair_array_stale_ && !a.row_pairs && !level_pairs_)
         fail(kRefused, "build: the staged pairs are carried in the rows, which this index's kernel does not read");
     a.masked = masked_ ? 1u : 0u;
+    a.mask_at = mask_at_;
     a.min_hess = row_pairs_min_hess_;
     const bool bm = hist_bin_major && fg >= 16;
     const char *k = !dense_u8_ ? "hbr_hist_csr"

@@ -449,6 +449,7 @@ private:
     // Dense u8 rows with a missing mask (kMaskWord) of a matrix with missing
     // values (dense_ false, dense_u8_ true).
     bool masked_ = false;
+    uint32_t mask_at_ = 0;  // masked rows: the byte of a row's first mask word
     void make_masked_rows();
     // Partials of the next root's histogram the fused walk left (0: none);
     // the next device tree's root sums them instead of building its own.

@@ -207,11 +207,14 @@ extern "C" __global__ __launch_bounds__(256) void hbr_iota(IotaArgs a) {
 // Root statistics: the exact integer sums of the quantized pairs of a
 // segment (order-free, so any launch shape gives the same totals).
 extern "C" __global__ __launch_bounds__(256) void hbr_total(TotalArgs a) {
-    const int eg = a.scale->exp_g, eh = a.scale->exp_h;
+    const QScale *scale = a.scale + blockIdx.y;
+    const GPair *gpair = a.gpair + blockIdx.y * a.tree_pairs;
+    QBin *out = a.out + blockIdx.y;
+    const int eg = scale->exp_g, eh = scale->exp_h;
     int64_t sg = 0, sh = 0;
     for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < a.n; j += gridDim.x * blockDim.x) {
         uint32_t r = a.rows ? a.rows[j] : a.first + j;
-        GPair p = a.gpair[r];
+        GPair p = gpair[r];
         sg += quantize(p.g, eg);
         sh += quantize(p.h, eh);
     }
@@ -231,8 +234,8 @@ extern "C" __global__ __launch_bounds__(256) void hbr_total(TotalArgs a) {
             sg += red[0][w];
             sh += red[1][w];
         }
-        atomicAdd((unsigned long long *)&a.out->g, (unsigned long long)sg);
-        atomicAdd((unsigned long long *)&a.out->h, (unsigned long long)sh);
+        atomicAdd((unsigned long long *)&out->g, (unsigned long long)sg);
+        atomicAdd((unsigned long long *)&out->h, (unsigned long long)sh);
     }
 }
 

@@ -134,9 +134,13 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
         }
         const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
         const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
-        // a row's missing cells (masked rows: one group of 32 features, the
-        // mask in the last word) add nowhere
-        const uint32_t mask = MASKED ? w[kMaskWord % W] : 0u;
+        // a row's missing cells add nowhere (masked rows: the group's mask
+        // word, the row's last word when a row is one group of 32 bytes)
+        uint32_t mask = 0u;
+        if (MASKED)
+            mask = a.mask_at == 4 * kMaskWord
+                       ? w[kMaskWord % W]
+                       : *reinterpret_cast<const uint32_t *>(a.bins8 + (size_t)r * a.stride + a.mask_at + 4 * grp);
         rotate_bytes<W>(w, rot);
 #pragma unroll
         for (int f = 0; f < FG; f++) {
@@ -530,7 +534,9 @@ extern "C" __global__ __launch_bounds__(kExactThreads) void hbr_hist_exact(Exact
                 const uint8_t *row = a.bins8 + (size_t)r * a.stride;
                 bin[k] = row[f];
                 const uint32_t word = *reinterpret_cast<const uint32_t *>(row + 4 * kMaskWord);
-                mask[k] = a.masked ? (word >> f) & 1u : 0u;
+                mask[k] = a.masked ? (*reinterpret_cast<const uint32_t *>(row + a.mask_at + 4 * (f >> 5)) >> (f & 31u)) &
+                                         1u
+                                   : 0u;
                 if (a.row_pairs) {
                     const float pv = __uint_as_float(word & 0x7fffffffu);
                     const float y = (word >> 31) ? 1.0f : 0.0f;

@@ -284,12 +284,14 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_leaves(WalkArgs a) {
     const uint32_t n_nodes = walk_nodes(a);
     for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += gridDim.x * blockDim.x) {
         const uint8_t *b = a.bins8 + (size_t)r * a.stride;
-        const uint32_t mask = a.masked ? *reinterpret_cast<const uint32_t *>(b + 4 * kMaskWord) : 0u;
         uint32_t nid = 0, left;
         uint32_t meta = node_meta(a, 0, &left);
         for (uint32_t step = 0; step < n_nodes && !(meta >> 31); step++) {
             const uint32_t f = meta & (kMetaDefaultLeft - 1u), lim = (meta >> 16) & 0x7fffu;
-            const bool right = ((mask >> f) & 1u) ? !(meta & kMetaDefaultLeft) : (uint32_t)b[f] >= lim;
+            // masked rows: feature f's bit of its group's mask word
+            const uint32_t mask =
+                a.masked ? *reinterpret_cast<const uint32_t *>(b + a.mask_at + 4 * (f >> 5)) >> (f & 31u) : 0u;
+            const bool right = (mask & 1u) ? !(meta & kMetaDefaultLeft) : (uint32_t)b[f] >= lim;
             nid = left + (right ? 1u : 0u);
             nid = nid < n_nodes ? nid : 0u;
             meta = node_meta(a, nid, &left);
@@ -332,7 +334,8 @@ __device__ __forceinline__ uint32_t pick_byte16(const uint32_t (&w)[16], uint32_
 }
 
 // The class trees of a softmax round added to their margins in one pass
-// over the rows (32- or 64-byte rows, W words): every tree's node table in
+// over the rows (32- or 64-byte rows, W words, or the first 64 bytes of a
+// masked row of at most 64 features): every tree's node table in
 // LDS, each row's bins read once into registers, then walked through tree
 // 0, 1, ..., each leaf added to its own margin (output + c) with the same
 // single f32 add as hbr_walk_leaves, so the margins are those of one walk
@@ -380,7 +383,15 @@ __device__ __forceinline__ void walk_leaves_batch(const WalkArgs &a) {
             w[4 * q + 2] = v.z;
             w[4 * q + 3] = v.w;
         }
-        const uint32_t mask = (W == 8 && a.masked) ? w[kMaskWord] : 0u;
+        // masked rows: the mask word of 32-byte rows; wider rows (at most 64
+        // features) keep their first two mask words at mask_at
+        uint2 mk = make_uint2(0u, 0u);
+        if (a.masked) {
+            if constexpr (W == 8)
+                mk.x = w[kMaskWord];
+            else
+                mk = *reinterpret_cast<const uint2 *>(a.bins8 + (size_t)r * a.stride + a.mask_at);
+        }
         float *m = a.margins + (size_t)r * a.m_stride + a.output;
         for (uint32_t c = 0; c < K; c++) {
             const uint32_t first = s_first[c], n = s_first[c + 1] - first;
@@ -398,6 +409,7 @@ __device__ __forceinline__ void walk_leaves_batch(const WalkArgs &a) {
                     for (int i = 0; i < 8; i++) h[i] = w[i];
                     bin = pick_byte(h, f & 31u);
                 }
+                const uint32_t mask = (W == 16 && (f & 32u)) ? mk.y : mk.x;
                 const bool right = ((mask >> (f & 31u)) & 1u) ? !(nd.x & kMetaDefaultLeft) : bin >= lim;
                 nid = nd.y + (right ? 1u : 0u);
                 nid = nid < n ? nid : 0u;
@@ -681,19 +693,26 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_root_fixup(RootFixupArgs 
 }
 
 // Masked dense rows from an index's local u8 columns and missing bitmap (a
-// host-built index of a matrix with missing values): one thread per row,
-// its bins in bytes 0..n_cols-1 and its missing mask in word kMaskWord.
+// host-built index of a matrix with missing values, or a wide matrix binned
+// on the device): one thread per row writes its whole record, word by word:
+// its bins in bytes 0..n_cols-1 (0 beyond), and its mask words from byte
+// mask_at (bit f % 32 of word f / 32: feature f missing; 32-byte rows keep
+// the one word in kMaskWord).
 extern "C" __global__ __launch_bounds__(256) void hbr_rows_from_cols(RowsFromColsArgs a) {
     const uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= a.n_rows) return;
-    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    uint32_t mask = 0;
-    for (uint32_t f = 0; f < a.n_cols; f++) {
-        w[f >> 2] |= (uint32_t)a.cols8[(uint64_t)f * a.n_rows + r] << ((f & 3u) * 8u);
-        if (a.missing) mask |= (uint32_t)((a.missing[(uint64_t)f * a.words + (r >> 6)] >> (r & 63u)) & 1ull) << f;
+    uint32_t *dst = reinterpret_cast<uint32_t *>(a.rows8 + r * a.stride);
+    const uint32_t words = a.stride / 4, mask0 = a.mask_at / 4;
+    for (uint32_t w = 0; w < words; w++) {
+        uint32_t v = 0;
+        if (w >= mask0) {
+            const uint32_t f0 = 32 * (w - mask0);
+            for (uint32_t j = 0; j < 32 && f0 + j < a.n_cols && a.missing; j++)
+                v |= (uint32_t)((a.missing[(uint64_t)(f0 + j) * a.words + (r >> 6)] >> (r & 63u)) & 1ull) << j;
+        } else {
+            for (uint32_t j = 0; j < 4 && 4 * w + j < a.n_cols; j++)
+                v |= (uint32_t)a.cols8[(uint64_t)(4 * w + j) * a.n_rows + r] << (8 * j);
+        }
+        dst[w] = v;
     }
-    w[kMaskWord] = mask;
-    uint4 *dst = reinterpret_cast<uint4 *>(a.rows8 + r * 32u);
-    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }

@@ -135,3 +135,29 @@ def test_few_features_with_missing_values_keep_masked_dense_rows(on_device):
         want |= np.isnan(x[:, j]).astype(np.uint32) << np.uint32(j)
     assert np.array_equal(mask, want)
     assert np.all(rows[:, :28][np.isnan(x)] == 0)  # a missing cell's byte is 0
+
+
+@pytest.mark.parametrize("f,on_device", [(29, False), (70, True), (256, False)])
+def test_wide_matrices_with_missing_values_keep_masked_rows_of_groups(f, on_device):
+    """Beyond 28 features, rows of G = ceil(f / 32) groups of 32 bins and a
+    32-byte chunk of mask words (stride 32 G + 32): a row's bins (0 where
+    missing), zeros up to its mask words, bit j % 32 of mask word j / 32 set
+    exactly where feature j is missing; the device-binned rows equal those
+    made from a host index's columns."""
+    rng = np.random.default_rng(27 + f)
+    n = 3_001
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    x[rng.random(x.shape) < 0.05] = np.nan
+    host, dev = _layouts(x, 256, on_device=on_device)
+    g = (f + 31) // 32
+    assert dev["dense"] == 0 and dev["dense_u8"] == 1 and dev["stride"] == 32 * g + 32
+    _same(host, dev)
+    rows = dev["rows8"].reshape(n, 32 * g + 32)
+    miss = np.isnan(x)
+    assert np.all(rows[:, :f][miss] == 0)
+    assert np.all(rows[:, f:32 * g] == 0)
+    words = rows[:, 32 * g:36 * g].copy().view(np.uint32)
+    bits = ((words[:, :, None] >> np.arange(32, dtype=np.uint32)) & 1).reshape(n, 32 * g).astype(bool)
+    assert np.array_equal(bits[:, :f], miss)
+    assert not bits[:, f:].any()
+    assert np.all(rows[:, 36 * g:] == 0)

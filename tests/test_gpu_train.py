@@ -498,6 +498,65 @@ def test_missing_values_on_masked_dense_rows_match_oracle_and_csr_path(objective
     assert np.max(np.abs(runs[0][1] - ref.margins())) <= 1e-5
 
 
+def _masked_and_csr_runs(x, y, params, rounds, device_grow="1"):
+    """Trees, margins and index info of the masked dense rows and of the CSR
+    path (HBROCM_MASKED_ROWS=0) for the same data."""
+    import os
+    runs = []
+    for masked in ("1", "0"):
+        saved = {k: os.environ.pop(k, None) for k in ("HBROCM_MASKED_ROWS", "HBROCM_DEVICE_GROW")}
+        os.environ.update({"HBROCM_MASKED_ROWS": masked, "HBROCM_DEVICE_GROW": device_grow})
+        try:
+            eng = hb.DMatrix(x, label=y).engine(256)
+            info = eng.index_info()
+            tr = hb.Trainer(eng, params, y)
+            tr.boost(rounds)
+        finally:
+            for k, v in saved.items():
+                os.environ.pop(k, None)
+                if v is not None:
+                    os.environ[k] = v
+        runs.append((tr.trees(), tr.margins(), info))
+    return runs
+
+
+@pytest.mark.parametrize("n_features,objective,device_grow", [
+    (50, "binary:logistic", "1"), (50, "reg:squarederror", "1"), (50, "multi:softprob", "1"),
+    (30, "binary:logistic", "0"), (97, "reg:squarederror", "1"), (256, "binary:logistic", "1")])
+def test_missing_values_on_wide_masked_rows_match_oracle_and_csr_path(n_features, objective, device_grow):
+    """Wider than 28 features, a matrix with 2% missing cells still trains
+    on masked dense rows: G = ceil(F / 32) groups of 32 bins, then a 32-byte
+    chunk of one mask word per group (row stride 32 G + 32). The oracle's
+    trees, and the CSR path's trees and margins bit for bit, with the levels
+    decided on the device and on the host."""
+    k = 4 if objective == "multi:softprob" else 1
+    x, y = synthetic.multiclass(n=20_000, f=n_features, k=max(k, 2), seed=n_features)
+    reg, _ = synthetic.regression_100k(n=20_000, f=n_features, seed=n_features)
+    rng = np.random.default_rng(7)
+    x[rng.random(x.shape) < 0.02] = np.nan
+    if objective == "reg:squarederror":
+        y = (2 * np.nan_to_num(x[:, 0]) - np.nan_to_num(x[:, n_features - 1]) + 0.1 * reg[:, 1]).astype(np.float32)
+    elif objective == "binary:logistic":
+        y = ((np.nan_to_num(x[:, 3]) + np.nan_to_num(x[:, n_features - 2]) + 0.5 * reg[:, 2]) > 0).astype(np.float32)
+    params = {"objective": objective, "max_depth": 6, "eta": 0.3}
+    if k > 1:
+        params["num_class"] = k
+    obj = {"binary:logistic": O.OBJ_LOGISTIC, "reg:squarederror": O.OBJ_SQUARED_ERROR,
+           "multi:softprob": O.OBJ_SOFTMAX}[objective]
+    ref = O.Model(O.Dataset(x), y, O.params(objective=obj, num_class=k, max_depth=6, eta=0.3), 3)
+    (tm, mm, im), (tc, mc, ic) = _masked_and_csr_runs(x, y, params, 3, device_grow)
+    groups = (n_features + 31) // 32
+    assert im["dense_u8"] == 1 and im["dense"] == 0
+    assert im["stride"] == (32 if n_features <= 28 else 32 * groups + 32), im
+    assert ic["dense_u8"] == 0
+    compare_trees(tm, ref.trees())
+    for a, b in zip(tm, tc):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(mm.view(np.uint32), mc.view(np.uint32))
+    assert np.max(np.abs(mm - ref.margins().reshape(mm.shape))) <= 1e-5
+
+
 @pytest.mark.parametrize("leaves", [3, 6, 14])
 def test_lossguide_with_equal_gains_matches_oracle(leaves):
     """Mirrored rows give every node below the root a twin of equal loss
