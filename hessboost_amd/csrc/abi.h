@@ -836,7 +836,7 @@ constexpr uint32_t kPredPitch = 64;
 // Two levels of a complete tree (PredictArgs::pairs).
 struct alignas(16) PairRecord {
     uint32_t t_node, t_first, t_second;
-    uint32_t s;  // s of the node | s of the first child << 8 | s of the second << 16
+    uint32_t s;  // slots and m bits of the node and its children (PredictArgs::pairs)
 };
 
 // A node of the mirror walk (PredictArgs::mirror).
@@ -904,9 +904,11 @@ struct PredictArgs {
     // records: (4^(D/2) - 1) / 3 per tree), the record of the node at
     // position i of level 2l followed by the value of each of its 2^D level-D
     // positions. A record is (t of the node, t of its first child, t of its
-    // second child, s of the node | s of the first << 8 | s of the second <<
-    // 16) with t as in the mirror walk and s = m << 7 | slot: a row steps to
-    // the second child when (value of slot, its sign flipped when m) < t.
+    // second child, s) with t as in the mirror walk; s holds each of the
+    // three nodes' slot and m (the node's slot at bits 8..14 and m at bit 31,
+    // the first child's at bits 16..22 and 7, the second's at bits 0..6 and
+    // 23): a row steps to the second child when (value of slot, its sign
+    // flipped when m) < t.
     // The first child is where a missing value goes. A leaf above level D
     // is continued by nodes that read slot 0 (NaN) and so always take their
     // first child, down to its position at level D, which holds its value.

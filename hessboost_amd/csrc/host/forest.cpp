@@ -201,13 +201,19 @@ void Forest::build_pairs(const hbr_forest_desc &fd) {
             stack.push_back({dl ? fd.left[at] : fd.right[at], lv + 1, 2 * i});
             stack.push_back({dl ? fd.right[at] : fd.left[at], lv + 1, 2 * i + 1});
         }
+        // s: the node's slot at bits 8..14 and m at 31, the first child's at
+        // 16..22 and 7, the second's at 0..6 and 23 (PredictArgs::pairs)
+        auto slot = [](uint32_t f) { return f & 0x7fu; };
+        auto m = [](uint32_t f) { return f >> 7; };
         uint64_t r = t * per_tree;
         for (uint32_t l = 0; l < levels; l++) {
             const uint32_t lv = 2 * l;
             for (uint64_t i = 0; i < (1ull << lv); i++) {
                 const uint64_t p = ((1ull << lv) - 1) + i;
                 const uint64_t c = ((1ull << (lv + 1)) - 1) + 2 * i;
-                recs[r++] = PairRecord{t_at[p], t_at[c], t_at[c + 1], s_at[p] | (s_at[c] << 8) | (s_at[c + 1] << 16)};
+                const uint32_t sw = (slot(s_at[p]) << 8) | (m(s_at[p]) << 31) | (slot(s_at[c]) << 16) |
+                                    (m(s_at[c]) << 7) | slot(s_at[c + 1]) | (m(s_at[c + 1]) << 23);
+                recs[r++] = PairRecord{t_at[p], t_at[c], t_at[c + 1], sw};
             }
         }
     }

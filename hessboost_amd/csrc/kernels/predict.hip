@@ -517,13 +517,6 @@ __device__ __forceinline__ void predict_mirror(const PredictArgs &a) {
 extern "C" __global__ __launch_bounds__(64) void hbr_predict_mirror_nan(PredictArgs a) { predict_mirror<true, 16>(a); }
 extern "C" __global__ __launch_bounds__(64) void hbr_predict_mirror(PredictArgs a) { predict_mirror<false, 16>(a); }
 
-// One test of the pair walk: 1 when the row goes to the second child.
-__device__ __forceinline__ uint32_t pair_test(const float *xr, uint32_t s8, uint32_t t) {
-    const float v = xr[(s8 & 0x7fu) * kPredPitch];
-    const float x = __uint_as_float(__float_as_uint(v) ^ ((s8 & 0x80u) << 24));
-    return x < __uint_as_float(t) ? 1u : 0u;
-}
-
 // A load every lane makes from the same address, through the scalar data
 // cache (s_load) instead of the texture path: the pointer is taken into the
 // constant address space, whose uniform loads the compiler turns into scalar
@@ -534,22 +527,64 @@ __device__ __forceinline__ T uniform_load(const T *p, size_t i) {
     return ((constant_t *)p)[i];
 }
 
-// Complete trees walked two levels per record (PredictArgs::pairs): rows
-// resident in LDS as in hbr_predict_mirror (one 64-row block per one-wave
-// workgroup, slot 0 NaN), CH trees in flight per lane; every record load
-// serves two levels and the last load reads only the leaf's value. The root
-// record and the tree's weight are the same for every lane: scalar loads,
-// so a tree costs the texture path one load per level below the root's two
-// and one for the leaf.
-template <bool MISSING_NAN, int CH>
+// One test of the pair walk. A field w of a record's s word (the node's own,
+// or a child's rotated into place) holds its slot at bits 8..14 and its m
+// at bit 31: the lane's value of that slot is read from LDS at byte
+// (w & 0x7f00) | 4 lane (slot * kPredPitch * 4 + 4 lane), its sign flipped
+// when m, and compared with t. 1 when the row goes to the second child.
+// The pair kernels declare no static LDS, so their dynamic block (the
+// staged rows) starts at LDS byte 0 and the and/or above is the whole
+// address.
+__device__ __forceinline__ bool pair_go(uint32_t lane4, uint32_t w, uint32_t t) {
+    typedef const __attribute__((address_space(3))) float lds_float;
+    const float v = *(lds_float *)(size_t)((w & 0x7f00u) | lane4);
+    const float x = __uint_as_float(__float_as_uint(v) ^ (w & 0x80000000u));
+    return x < __uint_as_float(t);
+}
+
+// 2 p + b in one add with carry-in (the compiler otherwise spends a select,
+// a shift and an or on it).
+__device__ __forceinline__ uint32_t double_add(uint32_t p, bool b) {
+    uint32_t r;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(b);
+    asm("v_addc_co_u32_e64 %0, vcc, %1, %1, %2" : "=v"(r) : "v"(p), "s"(m) : "vcc");
+    return r;
+}
+
+// One record (t_node, t_first, t_second, s): the node's test, then that of
+// the child it chose; the position 0..3 of the grandchild reached. s holds
+// the node's slot at bits 8..14 and m at bit 31, the first child's slot at
+// bits 16..22 and m at bit 7, the second's slot at bits 0..6 and m at bit
+// 23: rotating s right by 8 (first child) or 24 (second) brings the child's
+// slot and m to where the node's sit.
+// pos becomes 4 pos + that position (each doubling plus a test is one add
+// with the test's carry).
+__device__ __forceinline__ uint32_t pair_step(uint32_t lane4, uint4 rec, uint32_t pos) {
+    const bool go = pair_go(lane4, rec.w, rec.x);
+    const uint32_t c = __builtin_amdgcn_alignbit(rec.w, rec.w, go ? 24u : 8u);
+    const bool go_c = pair_go(lane4, c, go ? rec.z : rec.y);
+    return double_add(double_add(pos, go), go_c);
+}
+
+// Complete trees walked two levels per record (PredictArgs::pairs), LEVELS
+// records deep: rows resident in LDS as in hbr_predict_mirror (one 64-row
+// block per one-wave workgroup, slot 0 NaN), CH trees in flight per lane.
+// The root record and the tree's weight are the same for every lane (scalar
+// loads); a deeper record is read at the tree's level base, a uniform
+// address, plus the lane's 32-bit byte offset, and so is the leaf's value:
+// a tree costs the texture path one load per level below the root's two and
+// one for the leaf. The levels are unrolled so that a chain's next load can
+// issue as soon as its own step is done.
+// ONE: one output and no leaf indices (the margins alone, added in
+// registers).
+template <bool MISSING_NAN, int CH, int LEVELS, bool ONE>
 __device__ __forceinline__ void predict_pairs(const PredictArgs &a) {
     extern __shared__ float s_rows[];  // (n_cols + 1) * kPredPitch
     const uint32_t lane = lane_id();
-    const float *xr = s_rows + lane;
+    const uint32_t lane4 = lane * 4u;
     s_rows[lane] = __builtin_nanf("");
-    const uint32_t levels = a.pair_levels;
-    const uint32_t per_tree = ((1u << (2 * levels)) - 1u) / 3u;  // records
-    const uint32_t leaves = 1u << (2 * levels);
+    constexpr uint32_t per_tree = ((1u << (2 * LEVELS)) - 1u) / 3u;  // records
+    constexpr uint32_t leaves = 1u << (2 * LEVELS);
     const uint32_t n_blocks = (a.n + kPredLanes - 1) / kPredLanes;
     for (uint32_t blk = blockIdx.x; blk < n_blocks; blk += gridDim.x) {
         const uint32_t r0 = blk * kPredLanes;
@@ -568,48 +603,44 @@ __device__ __forceinline__ void predict_pairs(const PredictArgs &a) {
             for (uint32_t o = 0; o < a.n_outputs; o++) out[o] = start_margin(a, r, o);
         float acc = start_margin(a, r, 0);
         for (uint32_t t0 = 0; t0 < a.n_trees; t0 += CH) {
+            // the group's trees from one base: tree t0 + k at k' = min(k,
+            // last) trees past it (the last group repeats its last tree)
+            const uint32_t last = a.n_trees - 1 - t0;
+            const char *group = reinterpret_cast<const char *>(a.pairs + (size_t)t0 * per_tree);
+            const char *group_vals = reinterpret_cast<const char *>(a.pair_values + (size_t)t0 * leaves);
             uint32_t pos[CH];
 #pragma unroll
             for (int k = 0; k < CH; k++) {
-                const uint32_t t = min(t0 + (uint32_t)k, a.n_trees - 1);
-                const PairRecord rec = uniform_load(a.pairs, (size_t)t * per_tree);
-                const uint32_t s = rec.s;
-                const uint32_t first = pair_test(xr, s, rec.t_node);
-                const uint32_t t_c = first ? rec.t_second : rec.t_first;
-                const uint32_t s_c = first ? s >> 16 : s >> 8;
-                pos[k] = 2 * first + pair_test(xr, s_c, t_c);
+                const PairRecord rec = uniform_load(a.pairs, (size_t)(t0 + min((uint32_t)k, last)) * per_tree);
+                pos[k] = pair_step(lane4, make_uint4(rec.t_node, rec.t_first, rec.t_second, rec.s), 0u);
             }
-            uint32_t base = 1;  // first record of the level
-            for (uint32_t l = 1; l < levels; l++) {
-                PairRecord rec[CH];
+#pragma unroll
+            for (int l = 1; l < LEVELS; l++) {
+                const uint32_t base = ((1u << (2 * l)) - 1u) / 3u;  // first record of the level
+                uint4 rec[CH];
 #pragma unroll
                 for (int k = 0; k < CH; k++) {
-                    const uint32_t t = min(t0 + (uint32_t)k, a.n_trees - 1);
-                    rec[k] = a.pairs[(size_t)t * per_tree + base + pos[k]];
+                    const uint32_t at = (min((uint32_t)k, last) * per_tree + base) * 16u + (pos[k] << 4);
+                    rec[k] = *reinterpret_cast<const uint4 *>(group + at);
                 }
 #pragma unroll
-                for (int k = 0; k < CH; k++) {
-                    const uint32_t s = rec[k].s;
-                    const uint32_t first = pair_test(xr, s, rec[k].t_node);
-                    const uint32_t t_c = first ? rec[k].t_second : rec[k].t_first;
-                    const uint32_t s_c = first ? s >> 16 : s >> 8;
-                    const uint32_t second = pair_test(xr, s_c, t_c);
-                    pos[k] = 4 * pos[k] + 2 * first + second;
-                }
-                base = 4 * base + 1;
+                for (int k = 0; k < CH; k++) pos[k] = pair_step(lane4, rec[k], pos[k]);
             }
             uint32_t leaf[CH];
 #pragma unroll
-            for (int k = 0; k < CH; k++) {
-                const uint32_t t = min(t0 + (uint32_t)k, a.n_trees - 1);
-                leaf[k] = a.pair_values[(size_t)t * leaves + pos[k]];
-            }
+            for (int k = 0; k < CH; k++)
+                leaf[k] = *reinterpret_cast<const uint32_t *>(group_vals + min((uint32_t)k, last) * leaves * 4u +
+                                                              (pos[k] << 2));
 #pragma unroll
             for (int k = 0; k < CH; k++) {
                 const uint32_t t = t0 + (uint32_t)k;
                 if (t < a.n_trees) {
-                    if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.pair_orig[(size_t)t * leaves + pos[k]];
                     const float contrib = uniform_load(a.tree_weight, t) * __uint_as_float(leaf[k]);
+                    if (ONE) {
+                        acc = acc + contrib;
+                        continue;
+                    }
+                    if (a.leaf_out) a.leaf_out[(size_t)r * a.n_trees + t] = a.pair_orig[(size_t)t * leaves + pos[k]];
                     if (a.n_outputs == 1) {
                         acc = acc + contrib;
                     } else {
@@ -623,8 +654,37 @@ __device__ __forceinline__ void predict_pairs(const PredictArgs &a) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(64) void hbr_predict_pairs_nan(PredictArgs a) { predict_pairs<true, 16>(a); }
-extern "C" __global__ __launch_bounds__(64) void hbr_predict_pairs(PredictArgs a) { predict_pairs<false, 16>(a); }
+template <bool MISSING_NAN, bool ONE>
+__device__ __forceinline__ void predict_pairs_levels(const PredictArgs &a) {
+    switch (a.pair_levels) {
+    case 1: predict_pairs<MISSING_NAN, 16, 1, ONE>(a); break;
+    case 2: predict_pairs<MISSING_NAN, 16, 2, ONE>(a); break;
+    case 3: predict_pairs<MISSING_NAN, 16, 3, ONE>(a); break;
+    case 4: predict_pairs<MISSING_NAN, 16, 4, ONE>(a); break;
+    case 5: predict_pairs<MISSING_NAN, 16, 5, ONE>(a); break;
+    case 6: predict_pairs<MISSING_NAN, 16, 6, ONE>(a); break;
+    default: break;  // the host builds pair forests of depth 12 at most
+    }
+}
+
+template <bool MISSING_NAN>
+__device__ __forceinline__ void predict_pairs_dispatch(const PredictArgs &a) {
+    if (a.n_outputs == 1 && !a.leaf_out)
+        predict_pairs_levels<MISSING_NAN, true>(a);
+    else
+        predict_pairs_levels<MISSING_NAN, false>(a);
+}
+
+// The occupancy is the LDS row blocks' (a few waves per SIMD): the walk may
+// keep its sixteen chains' records in registers.
+extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void hbr_predict_pairs_nan(
+    PredictArgs a) {
+    predict_pairs_dispatch<true>(a);
+}
+extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) void hbr_predict_pairs(
+    PredictArgs a) {
+    predict_pairs_dispatch<false>(a);
+}
 
 // ---- evaluation sets --------------------------------------------------------
 //
