@@ -182,6 +182,8 @@ SIGNATURES = {
     "hbr_engine_add_eval": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_void_p,
                                       C.c_uint32, P(C.c_uint32)]),
     "hbr_engine_eval_add_tree": (C.c_int, [C.c_void_p] + [C.c_void_p] * 6 + [C.c_uint64, C.c_uint32]),
+    "hbr_engine_eval_add_tree_categorical": (C.c_int, [C.c_void_p] + [C.c_void_p] * 10 +
+                                             [C.c_uint64, C.c_uint64, C.c_uint32]),
     "hbr_engine_eval_margins": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p]),
     "hbr_trainer_add_eval": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_void_p,
                                        P(C.c_uint32)]),

@@ -348,12 +348,20 @@ class Engine:
         return idx.value
 
     def eval_add_tree(self, tree: dict, output=0):
-        """One tree (node arrays as the trainer returns them) added to every
-        eval set's margins of `output`, on the device."""
+        """One tree (node arrays as the trainer returns them, with its
+        categorical nodes and pool when it has them) added to every eval
+        set's margins of `output`, on the device."""
         arrs = [np.ascontiguousarray(tree[k], dt) for k, dt in
                 (("split_feature", np.uint32), ("split_cond", np.float32), ("default_left", np.uint8),
                  ("left", np.int32), ("right", np.int32), ("leaf_value", np.float32))]
-        A.check(A.lib().hbr_engine_eval_add_tree(self._h, *[A.ptr(a) for a in arrs], len(arrs[3]), output))
+        if not np.any(tree.get("is_categorical", ())):
+            A.check(A.lib().hbr_engine_eval_add_tree(self._h, *[A.ptr(a) for a in arrs], len(arrs[3]), output))
+            return
+        cats = [np.ascontiguousarray(tree[k], dt) for k, dt in
+                (("is_categorical", np.uint8), ("cat_begin", np.uint32), ("cat_end", np.uint32),
+                 ("categories", np.uint32))]
+        A.check(A.lib().hbr_engine_eval_add_tree_categorical(self._h, *[A.ptr(a) for a in arrs + cats],
+                                                             len(cats[3]), len(arrs[3]), output))
 
     def eval_margins(self, index):
         out = np.empty(self._eval_shapes[index], np.float32)

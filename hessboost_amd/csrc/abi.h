@@ -769,6 +769,13 @@ struct EvalWalkArgs {
     uint32_t missing_is_nan;
     uint32_t total_bins;         // cut_values' length
     uint32_t pad;
+    // Categorical splits (a tree grown on an index with categorical
+    // features), or null: node i's categories, which go left, are
+    // categories[cat_span[2 i], cat_span[2 i + 1] & 0x7fffffff), bit 31 of
+    // cat_span[2 i + 1] marking the split categorical; a present value goes
+    // left iff its category (the saturating cast) is among them.
+    const uint32_t *cat_span;
+    const uint32_t *categories;
 };
 
 // The margin walk of a finished tree followed, row by row, by the next

@@ -538,29 +538,69 @@ int hbr_engine_add_eval(hbr_engine *h, const float *x, uint64_t n_rows, uint64_t
     });
 }
 
+// The eval walk of a caller's tree (numeric, or with categorical nodes and
+// their pool of codes).
+static void eval_add_tree(Engine &e, const uint32_t *split_feature, const float *split_cond,
+                          const uint8_t *default_left, const int32_t *left, const int32_t *right,
+                          const float *leaf_value, uint64_t n_nodes, uint32_t output, const uint8_t *is_categorical,
+                          const uint32_t *cat_begin, const uint32_t *cat_end, const uint32_t *categories,
+                          uint64_t n_categories) {
+    if (!split_feature || !split_cond || !default_left || !left || !right || !leaf_value)
+        fail(kInvalid, "evaluation walk: null argument");
+    if (n_nodes == 0) fail(kInvalid, "evaluation walk: a tree without nodes");
+    std::vector<GrowTreeNode> nodes(n_nodes);
+    std::vector<float> cond(n_nodes, 0.0f);
+    std::unique_ptr<Engine::EvalCats> cats;
+    std::vector<uint32_t> pool;
+    if (is_categorical) {
+        if (!cat_begin || !cat_end || (n_categories && !categories))
+            fail(kInvalid, "evaluation walk: categorical nodes need cat_begin, cat_end and categories");
+        cats = std::make_unique<Engine::EvalCats>();
+        cats->span.assign(2 * n_nodes, 0u);
+        pool.assign(categories, categories + n_categories);
+        cats->categories = &pool;
+    }
+    for (uint64_t i = 0; i < n_nodes; i++) {
+        GrowTreeNode &g = nodes[i];
+        g = GrowTreeNode{};
+        g.left = left[i] < 0 ? -1 : left[i];
+        g.value = leaf_value[i];
+        if (left[i] < 0) continue;
+        if ((uint64_t)left[i] + 1 >= n_nodes || right[i] != left[i] + 1)
+            fail(kInvalid, "evaluation walk: children must be a pair of existing nodes (right = left + 1)");
+        if (split_feature[i] >= e.n_cols()) fail(kInvalid, "evaluation walk: split feature out of range");
+        g.feature = split_feature[i];
+        g.default_left = default_left[i] ? 1u : 0u;
+        cond[i] = split_cond[i];
+        if (cats && is_categorical[i]) {
+            if (cat_begin[i] > cat_end[i] || cat_end[i] > n_categories || cat_end[i] >= (1u << 31))
+                fail(kInvalid, "evaluation walk: a categorical split's categories are out of range");
+            cats->span[2 * i] = cat_begin[i];
+            cats->span[2 * i + 1] = cat_end[i] | (1u << 31);
+        }
+    }
+    e.walk_evals(nodes, output, &cond, cats.get());
+}
+
 int hbr_engine_eval_add_tree(hbr_engine *h, const uint32_t *split_feature, const float *split_cond,
                              const uint8_t *default_left, const int32_t *left, const int32_t *right,
                              const float *leaf_value, uint64_t n_nodes, uint32_t output) {
     return with_engine(h, [&](Engine &e) {
-        if (!split_feature || !split_cond || !default_left || !left || !right || !leaf_value)
-            fail(kInvalid, "evaluation walk: null argument");
-        if (n_nodes == 0) fail(kInvalid, "evaluation walk: a tree without nodes");
-        std::vector<GrowTreeNode> nodes(n_nodes);
-        std::vector<float> cond(n_nodes, 0.0f);
-        for (uint64_t i = 0; i < n_nodes; i++) {
-            GrowTreeNode &g = nodes[i];
-            g = GrowTreeNode{};
-            g.left = left[i] < 0 ? -1 : left[i];
-            g.value = leaf_value[i];
-            if (left[i] < 0) continue;
-            if ((uint64_t)left[i] + 1 >= n_nodes || right[i] != left[i] + 1)
-                fail(kInvalid, "evaluation walk: children must be a pair of existing nodes (right = left + 1)");
-            if (split_feature[i] >= e.n_cols()) fail(kInvalid, "evaluation walk: split feature out of range");
-            g.feature = split_feature[i];
-            g.default_left = default_left[i] ? 1u : 0u;
-            cond[i] = split_cond[i];
-        }
-        e.walk_evals(nodes, output, &cond);
+        eval_add_tree(e, split_feature, split_cond, default_left, left, right, leaf_value, n_nodes, output, nullptr,
+                      nullptr, nullptr, nullptr, 0);
+    });
+}
+
+int hbr_engine_eval_add_tree_categorical(hbr_engine *h, const uint32_t *split_feature, const float *split_cond,
+                                         const uint8_t *default_left, const int32_t *left, const int32_t *right,
+                                         const float *leaf_value, const uint8_t *is_categorical,
+                                         const uint32_t *cat_begin, const uint32_t *cat_end,
+                                         const uint32_t *categories, uint64_t n_categories, uint64_t n_nodes,
+                                         uint32_t output) {
+    return with_engine(h, [&](Engine &e) {
+        if (!is_categorical) fail(kInvalid, "evaluation walk: null argument");
+        eval_add_tree(e, split_feature, split_cond, default_left, left, right, leaf_value, n_nodes, output,
+                      is_categorical, cat_begin, cat_end, categories, n_categories);
     });
 }
 

@@ -1849,7 +1849,6 @@ uint32_t Engine::add_eval_set(const float *x, uint64_t n_rows, uint64_t n_cols, 
                               uint32_t outputs) {
     if (!x || !init) fail(kInvalid, "evaluation set: null argument");
     if (n_cols != n_cols_) fail(kInvalid, "evaluation set: not the training matrix's features");
-    if (n_cat_) fail(kRefused, "evaluation set: the device walk does not route categorical splits");
     if (n_rows == 0) fail(kInvalid, "evaluation set: no rows");
     if (outputs == 0) fail(kInvalid, "evaluation set: no outputs");
     hipStream_t s = dev_.stream();
@@ -1883,9 +1882,14 @@ void Engine::read_eval_margins(uint32_t set, float *out) {
 }
 
 void Engine::launch_eval_walk(const EvalSet &set, const GrowTreeNode *tree, const GrowCounts *counts,
-                              uint32_t n_nodes, uint32_t output, const uint32_t *poison, const float *cond) {
+                              uint32_t n_nodes, uint32_t output, const uint32_t *poison, const float *cond,
+                              const EvalCats *cats) {
     if (output >= set.outputs) fail(kInvalid, "evaluation walk: no such output");
     EvalWalkArgs a{};
+    if (cats) {  // uploaded by the caller of this walk
+        a.cat_span = d_eval_span_.get();
+        a.categories = d_eval_categories_.get();
+    }
     a.x = set.x.get();
     a.tree = tree;
     a.counts = counts;
@@ -1916,6 +1920,7 @@ void Engine::launch_eval_walk(const EvalSet &set, const GrowTreeNode *tree, cons
 
 void Engine::walk_evals_device(uint32_t output, uint32_t tree, bool guarded) {
     if (evals_.empty()) return;
+    if (n_cat_) fail(kInvalid, "evaluation walk: device-grown trees have no categorical splits to route");
     if (guarded && !poison_.size()) fail(kInvalid, "evaluation walk: no guarded walk before it");
     for (const auto &set : evals_)
         launch_eval_walk(*set, ring_nodes(last_ring_, tree, last_stride_),
@@ -1923,7 +1928,24 @@ void Engine::walk_evals_device(uint32_t output, uint32_t tree, bool guarded) {
                          guarded ? poison_.get() : nullptr);
 }
 
-void Engine::walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output, const std::vector<float> *cond) {
+// A tree's categorical splits for the next evaluation walks: spans checked
+// against the node count and the category pool.
+void Engine::upload_eval_cats(const EvalCats &cats, size_t n_nodes) {
+    const std::vector<uint32_t> empty;
+    const std::vector<uint32_t> &pool = cats.categories ? *cats.categories : empty;
+    if (cats.span.size() != 2 * n_nodes) fail(kInvalid, "evaluation walk: two category bounds per node");
+    for (size_t i = 0; i < n_nodes; i++) {
+        const uint32_t b = cats.span[2 * i], e = cats.span[2 * i + 1] & 0x7fffffffu;
+        if ((cats.span[2 * i + 1] >> 31) && (b > e || e > pool.size()))
+            fail(kInvalid, "evaluation walk: a categorical split's categories are out of range");
+    }
+    upload_vec(d_eval_span_, cats.span, stage_, dev_.stream());
+    if (!pool.empty()) upload_vec(d_eval_categories_, pool, stage_, dev_.stream());
+    else d_eval_categories_.reserve(1);
+}
+
+void Engine::walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output, const std::vector<float> *cond,
+                        const EvalCats *cats) {
     if (evals_.empty() || nodes.empty()) return;
     if (nodes.size() > UINT32_MAX) fail(kRefused, "evaluation walk: a tree of more than 2^32 - 1 nodes");
     for (const auto &set : evals_)
@@ -1933,16 +1955,20 @@ void Engine::walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output,
         if (cond->size() != nodes.size()) fail(kInvalid, "evaluation walk: one threshold per node");
         upload_vec(d_eval_cond_, *cond, stage_, dev_.stream());
     }
+    if (cats) upload_eval_cats(*cats, nodes.size());
     for (const auto &set : evals_)
         launch_eval_walk(*set, d_eval_tree_.get(), nullptr, (uint32_t)nodes.size(), output, nullptr,
-                         cond ? d_eval_cond_.get() : nullptr);
+                         cond ? d_eval_cond_.get() : nullptr, cats);
 }
 
-void Engine::walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output) {
+void Engine::walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output,
+                            const EvalCats *cats) {
     if (set >= evals_.size()) fail(kInvalid, "evaluation set: no such set");
     if (nodes.empty()) return;
     upload_vec(d_eval_tree_, nodes, stage_, dev_.stream());
-    launch_eval_walk(*evals_[set], d_eval_tree_.get(), nullptr, (uint32_t)nodes.size(), output, nullptr);
+    if (cats) upload_eval_cats(*cats, nodes.size());
+    launch_eval_walk(*evals_[set], d_eval_tree_.get(), nullptr, (uint32_t)nodes.size(), output, nullptr, nullptr,
+                     cats);
 }
 
 void Engine::add_leaves(const std::vector<Segment> &segs, const std::vector<float> &values, uint32_t output) {

@@ -244,11 +244,17 @@ public:
     // walk before it skipped the tree.
     void walk_evals_device(uint32_t output, uint32_t tree, bool guarded);
     // A tree given as records (a host-grown tree) into every set's margins;
-    // `cond`: per node thresholds instead of the split bins' cut values.
+    // `cond`: per node thresholds instead of the split bins' cut values;
+    // `cats`: its categorical splits (EvalWalkArgs::cat_span, categories).
+    struct EvalCats {
+        std::vector<uint32_t> span;
+        const std::vector<uint32_t> *categories = nullptr;
+    };
     void walk_evals(const std::vector<GrowTreeNode> &nodes, uint32_t output,
-                    const std::vector<float> *cond = nullptr);
+                    const std::vector<float> *cond = nullptr, const EvalCats *cats = nullptr);
     // ... into one set's margins only (a set added after trees were grown).
-    void walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output);
+    void walk_evals_one(uint32_t set, const std::vector<GrowTreeNode> &nodes, uint32_t output,
+                        const EvalCats *cats = nullptr);
     uint32_t n_eval_sets() const { return (uint32_t)evals_.size(); }
     // Drops every set; returns the new owner's number (eval_owner()).
     uint64_t clear_eval_sets() {
@@ -432,8 +438,11 @@ private:
     DBuf<float> d_cuts_;             // cut values for the evaluation walks
     DBuf<GrowTreeNode> d_eval_tree_; // a host-grown tree's records
     DBuf<float> d_eval_cond_;
+    DBuf<uint32_t> d_eval_span_, d_eval_categories_;  // a walked tree's categorical splits
+    void upload_eval_cats(const EvalCats &cats, size_t n_nodes);
     void launch_eval_walk(const EvalSet &set, const GrowTreeNode *tree, const GrowCounts *counts, uint32_t n_nodes,
-                          uint32_t output, const uint32_t *poison, const float *cond = nullptr);
+                          uint32_t output, const uint32_t *poison, const float *cond = nullptr,
+                          const EvalCats *cats = nullptr);
     uint32_t outputs_ = 1;
     bool labels_loaded_ = false, has_weights_ = false;
     bool labels_binary_ = false;  // every label 0 or 1

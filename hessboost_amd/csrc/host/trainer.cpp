@@ -7,8 +7,11 @@
 #include <cstring>
 #include <deque>
 #include <limits>
+#include <memory>
 
 namespace hbr {
+
+static std::unique_ptr<Engine::EvalCats> eval_cats_of(const Tree &t);
 
 namespace {
 
@@ -517,7 +520,7 @@ void Trainer::grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_los
     trees_.push_back(b.grow(&leaves, walk));
     const Tree &t = trees_.back();
     grads_ready_ = false;
-    if (e_.n_eval_sets()) e_.walk_evals(records_of(t), output);
+    if (e_.n_eval_sets()) e_.walk_evals(records_of(t), output, nullptr, eval_cats_of(t).get());
     if (walk) {
         const size_t n = t.nodes.size();
         std::vector<uint32_t> meta(n), left(n, 0);
@@ -700,6 +703,24 @@ hbr_device_loss Trainer::device_loss() const {
 
 void Trainer::margins(float *out) { e_.read_margins(out, n_ * k_); }
 
+// A tree's categorical splits as the evaluation walk reads them (null when
+// it has none).
+static std::unique_ptr<Engine::EvalCats> eval_cats_of(const Tree &t) {
+    bool any = false;
+    for (const TreeNode &n : t.nodes) any |= n.left >= 0 && n.is_categorical;
+    if (!any) return nullptr;
+    auto c = std::make_unique<Engine::EvalCats>();
+    c->span.assign(2 * t.nodes.size(), 0u);
+    for (size_t i = 0; i < t.nodes.size(); i++) {
+        const TreeNode &n = t.nodes[i];
+        if (n.left < 0 || !n.is_categorical) continue;
+        c->span[2 * i] = n.cat_begin;
+        c->span[2 * i + 1] = n.cat_end | (1u << 31);
+    }
+    c->categories = &t.categories;
+    return c;
+}
+
 // A tree's nodes as the device walks read them: split bin (the threshold is
 // its cut value), feature, default direction, children, leaf value.
 std::vector<GrowTreeNode> records_of(const Tree &t) {
@@ -727,7 +748,8 @@ uint32_t Trainer::add_eval(const float *x, uint64_t n, uint64_t n_cols, float mi
     for (uint64_t r = 0; r < n; r++)
         for (uint32_t c = 0; c < k_; c++) init[r * k_ + c] = base_margin ? base_margin[r * k_ + c] : base_[c];
     const uint32_t set = e_.add_eval_set(x, n, n_cols, missing, init.data(), k_);
-    for (size_t t = 0; t < trees_.size(); t++) e_.walk_evals_one(set, records_of(trees_[t]), (uint32_t)(t % k_));
+    for (size_t t = 0; t < trees_.size(); t++)
+        e_.walk_evals_one(set, records_of(trees_[t]), (uint32_t)(t % k_), eval_cats_of(trees_[t]).get());
     return set;
 }
 

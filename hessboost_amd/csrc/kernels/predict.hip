@@ -695,12 +695,14 @@ extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1
 // growth wrote them, so the walk queues behind the growth on the stream;
 // a split's threshold is the cut value of its bin boundary, as the tree's
 // host copy records it (or, for a tree the caller passes, its own
-// thresholds). Thread per row; the tree's nodes sit in LDS as
-// (threshold, feature | default_left << 31, left child or ~0 for a leaf,
-// value) when they fit.
+// thresholds; a categorical split sends a present value left iff its
+// category is among the node's, as the model's prediction does). Thread per
+// row; the tree's nodes sit in LDS (eval_node's records) when they fit.
 
 namespace {
 
+// A node of the evaluation walk: (threshold bits, feature | categorical <<
+// 30 | default_left << 31, left child or ~0 for a leaf, value bits).
 __device__ __forceinline__ uint4 eval_node(const EvalWalkArgs &a, uint32_t i) {
     const GrowTreeNode t = a.tree[i];
     uint4 w;
@@ -712,12 +714,24 @@ __device__ __forceinline__ uint4 eval_node(const EvalWalkArgs &a, uint32_t i) {
         const float cond = a.cond ? a.cond[i]
                            : t.bin >= 0 && (uint32_t)t.bin < a.total_bins ? a.cut_values[t.bin]
                                                                           : -__FLT_MAX__;
+        const bool cat = a.cat_span && (a.cat_span[2 * i + 1] >> 31);
         w.x = __float_as_uint(cond);
-        w.y = min(t.feature, a.n_cols - 1u) | (t.default_left ? 1u << 31 : 0u);
+        w.y = min(t.feature, a.n_cols - 1u) | (cat ? 1u << 30 : 0u) | (t.default_left ? 1u << 31 : 0u);
         w.z = (uint32_t)t.left;
     }
     w.w = __float_as_uint(t.value);
     return w;
+}
+
+// The step of a present value at node `id` (record nd): below the
+// threshold, or, for a categorical split, its category among the node's.
+__device__ __forceinline__ bool eval_present_left(const EvalWalkArgs &a, uint32_t id, const uint4 &nd, float v) {
+    if (!(nd.y & (1u << 30))) return v < __uint_as_float(nd.x);
+    const uint32_t c = category_of(v);
+    const uint32_t end = a.cat_span[2 * id + 1] & 0x7fffffffu;
+    bool hit = false;
+    for (uint32_t i = a.cat_span[2 * id]; i < end; i++) hit |= a.categories[i] == c;
+    return hit;
 }
 
 template <bool kLds>
@@ -726,14 +740,16 @@ __device__ __forceinline__ void eval_walk(const EvalWalkArgs &a, const uint4 *s_
     for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < a.n; r += stride) {
         const float *row = a.x + r * a.n_cols;
         uint4 nd = kLds ? s_node[0] : eval_node(a, 0);
+        uint32_t id = 0;
         bool leaf = nd.z == 0xffffffffu;
         for (uint32_t step = 0; step < n_nodes && !leaf; step++) {
-            const float v = row[nd.y & 0x7fffffffu];
+            const float v = row[nd.y & 0x3fffffffu];
             const bool absent = a.missing_is_nan ? __builtin_isnan(v) : v == a.missing_value;
-            const bool go_left = absent ? (nd.y >> 31) != 0u : v < __uint_as_float(nd.x);
+            const bool go_left = absent ? (nd.y >> 31) != 0u : eval_present_left(a, id, nd, v);
             const uint32_t nid = nd.z + (go_left ? 0u : 1u);
             if (nid >= n_nodes) break;  // a malformed record: the row gets nothing
             nd = kLds ? s_node[nid] : eval_node(a, nid);
+            id = nid;
             leaf = nd.z == 0xffffffffu;
         }
         if (leaf) {
@@ -775,14 +791,16 @@ extern "C" __global__ __launch_bounds__(256) void hbr_eval_walk_staged(EvalWalkA
         if (lane >= rows) continue;
         const float *row = s_x + lane;
         uint4 nd = lds_nodes ? s_node[0] : eval_node(a, 0);
+        uint32_t id = 0;
         bool leaf = nd.z == 0xffffffffu;
         for (uint32_t st = 0; st < n_nodes && !leaf; st++) {
-            const float v = row[(nd.y & 0x7fffffffu) * kPredPitch];
+            const float v = row[(nd.y & 0x3fffffffu) * kPredPitch];
             const bool absent = a.missing_is_nan ? __builtin_isnan(v) : v == a.missing_value;
-            const bool go_left = absent ? (nd.y >> 31) != 0u : v < __uint_as_float(nd.x);
+            const bool go_left = absent ? (nd.y >> 31) != 0u : eval_present_left(a, id, nd, v);
             const uint32_t nid = nd.z + (go_left ? 0u : 1u);
             if (nid >= n_nodes) break;  // a malformed record: the row gets nothing
             nd = lds_nodes ? s_node[nid] : eval_node(a, nid);
+            id = nid;
             leaf = nd.z == 0xffffffffu;
         }
         if (leaf) {

@@ -299,6 +299,12 @@ extern "C" {
     pub fn hbr_engine_eval_add_tree(e: *mut hbr_engine, split_feature: *const u32, split_cond: *const f32,
                                     default_left: *const u8, left: *const i32, right: *const i32,
                                     leaf_value: *const f32, n_nodes: u64, output: u32) -> c_int;
+    pub fn hbr_engine_eval_add_tree_categorical(e: *mut hbr_engine, split_feature: *const u32,
+                                                split_cond: *const f32, default_left: *const u8, left: *const i32,
+                                                right: *const i32, leaf_value: *const f32,
+                                                is_categorical: *const u8, cat_begin: *const u32,
+                                                cat_end: *const u32, categories: *const u32, n_categories: u64,
+                                                n_nodes: u64, output: u32) -> c_int;
     pub fn hbr_engine_eval_margins(e: *mut hbr_engine, index: u32, out: *mut f32) -> c_int;
     pub fn hbr_reserve_hists(e: *mut hbr_engine, slots: u64, fits: *mut c_int) -> c_int;
     pub fn hbr_build_resident(e: *mut hbr_engine, segs: *const hbr_segment, slots: *const u32, n: u64,

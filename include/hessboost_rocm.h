@@ -314,6 +314,18 @@ int hbr_engine_add_eval(hbr_engine *e, const float *x, uint64_t n_rows, uint64_t
 int hbr_engine_eval_add_tree(hbr_engine *e, const uint32_t *split_feature, const float *split_cond,
                              const uint8_t *default_left, const int32_t *left, const int32_t *right,
                              const float *leaf_value, uint64_t n_nodes, uint32_t output);
+/* hbr_engine_eval_add_tree for a tree with categorical splits (RegTree's
+ * categorical nodes, src/tree/regtree.rs:59-66): node i with
+ * is_categorical[i] sends a present value left iff its category (the
+ * saturating cast of the value, tree/mod.rs:34-36) is among
+ * categories[cat_begin[i], cat_end[i]) (the tree's pool, n_categories codes);
+ * a missing value follows default_left; other nodes compare split_cond. */
+int hbr_engine_eval_add_tree_categorical(hbr_engine *e, const uint32_t *split_feature, const float *split_cond,
+                                         const uint8_t *default_left, const int32_t *left, const int32_t *right,
+                                         const float *leaf_value, const uint8_t *is_categorical,
+                                         const uint32_t *cat_begin, const uint32_t *cat_end,
+                                         const uint32_t *categories, uint64_t n_categories, uint64_t n_nodes,
+                                         uint32_t output);
 /* Eval set `index`'s margins (n_rows * n_outputs, row-major). */
 int hbr_engine_eval_margins(hbr_engine *e, uint32_t index, float *out);
 

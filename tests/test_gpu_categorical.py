@@ -125,21 +125,50 @@ def test_categorical_csr_input_matches_oracle():
     compare_categories(model.trees, ref.trees())
 
 
-def test_categorical_models_save_load_and_refuse_eval_sets(tmp_path):
+def test_categorical_models_save_load(tmp_path):
     """A trained categorical model round-trips through the native format and
-    predicts the same margins; an evaluation set on an index with
-    categorical features is refused (the device's value walk does not route
-    category sets), leaving the caller to score it by prediction."""
+    predicts the same margins."""
     x, y, types = categorical_data(4, 6_000, [8], "reg:squarederror")
     model = hb.train({"max_depth": 4}, hb.DMatrix(x, label=y, feature_types=types), 3)
     model.save_model(tmp_path / "cat.bin")
     back = hb.Booster(objective="reg:squarederror", base_score=np.zeros(1, np.float32)).load_model(tmp_path / "cat.bin")
     assert np.array_equal(back.predict(x, output_margin=True).view(np.uint32),
                           model.predict(x, output_margin=True).view(np.uint32))
-    with pytest.raises(A.HbrError) as refused:
-        hb.train({"max_depth": 4}, hb.DMatrix(x, label=y, feature_types=types), 1,
-                 evals=[(hb.DMatrix(x, feature_types=types), "train")])
-    assert refused.value.status == A.REFUSED
+
+
+@pytest.mark.parametrize("objective,k", [("reg:squarederror", 1), ("binary:logistic", 1), ("multi:softprob", 3)])
+def test_categorical_eval_sets_follow_the_model(objective, k):
+    """Evaluation sets on an index with categorical features
+    (training/margins.rs:148-152, :186-196): the device walk routes each
+    categorical split by its category set (a present value's saturating
+    cast among the node's categories; missing values the default way, codes
+    never seen in training and negative or fractional values too), so after
+    every round the set's margins equal the model's own prediction bit for
+    bit; a set added after trees were grown takes them first."""
+    x, y, types = categorical_data(7, 8_000, [6, 40], objective, k)
+    xe, _, _ = categorical_data(8, 3_001, [9, 45], objective, k)  # codes beyond training's
+    xe[::7, 2] = -1.5
+    xe[::11, 3] = 2.5
+    xe[::13, 3] = 1e10
+    params = {"objective": objective, "max_depth": 5, "eta": 0.3}
+    if k > 1:
+        params["num_class"] = k
+    model = hb.train(params, hb.DMatrix(x, label=y, feature_types=types), 4,
+                     evals=[(hb.DMatrix(xe, feature_types=types), "eval"),
+                            (hb.DMatrix(x, feature_types=types), "train")])
+    assert any(np.any(t.get("is_categorical", ())) for t in model.trees)
+    for name, data in (("eval", xe), ("train", x)):
+        got = model.eval_margins[name].reshape(-1)
+        want = model.predict(data, output_margin=True).reshape(-1)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), name
+    eng = hb.DMatrix(x, label=y, feature_types=types).engine(256)
+    t = hb.Trainer(eng, params, y)
+    t.boost(2)
+    late = t.add_eval(hb.DMatrix(xe, feature_types=types))
+    t.boost(2)
+    b = t.booster(x.shape[1])
+    assert np.array_equal(t.eval_margins(late).reshape(-1).view(np.uint32),
+                          b.predict(xe, output_margin=True).reshape(-1).view(np.uint32))
 
 
 def exact_categorical_node(seed, n, n_cats, outlier_code=None):

@@ -252,6 +252,59 @@ def test_engine_level_eval_sets_take_caller_trees():
                                   left=[2, -1, -1], right=[1, -1, -1], leaf_value=[0.0, 1, 2]))
 
 
+def test_engine_level_eval_sets_take_categorical_caller_trees():
+    """hbr_engine_eval_add_tree_categorical: random trees mixing numeric and
+    categorical splits (sets of up to 40 codes from 0..59, pools per tree)
+    added to an eval set of two outputs, rows with fractional, negative and
+    missing codes: the oracle's prediction walk bit for bit; a categorical
+    node whose range leaves the pool is refused."""
+    rng = np.random.default_rng(41)
+    f = 5
+    x, y = data(2_000, f, 42)
+    engine = hb.DMatrix(x, label=y).engine(64)
+    e = (rng.integers(-3, 70, (3_333, f)) + rng.choice([0.0, 0.5], (3_333, f))).astype(np.float32)
+    e[rng.random(e.shape) < 0.05] = np.nan
+    init = rng.standard_normal((e.shape[0], 2)).astype(np.float32)
+    idx = engine.add_eval(e, init)
+    want = init.copy()
+    for t in range(12):
+        nodes, pool = [dict(leaf_value=float(rng.standard_normal()))], []
+        for _ in range(int(rng.integers(0, 25))):
+            i = int(rng.choice([j for j, nd in enumerate(nodes) if "left" not in nd]))
+            nodes[i].update(left=len(nodes), right=len(nodes) + 1, split_feature=int(rng.integers(0, f)),
+                            split_cond=float(np.float32(rng.standard_normal() * 20)),
+                            default_left=bool(rng.random() < 0.5), is_categorical=bool(rng.random() < 0.6))
+            nodes += [dict(leaf_value=float(rng.standard_normal())), dict(leaf_value=float(rng.standard_normal()))]
+        for nd in nodes:
+            for key, v in (("left", -1), ("right", -1), ("split_feature", 0), ("split_cond", 0.0),
+                           ("default_left", True), ("is_categorical", False)):
+                nd.setdefault(key, v)
+            if nd["is_categorical"] and nd["left"] != -1:
+                cats = np.sort(rng.choice(60, size=int(rng.integers(1, 41)), replace=False))
+                nd["cat_begin"], nd["cat_end"] = len(pool), len(pool) + len(cats)
+                pool.extend(int(c) for c in cats)
+            else:
+                nd["is_categorical"] = False
+                nd["cat_begin"] = nd["cat_end"] = 0
+        tree = {k: np.array([nd[k] for nd in nodes]) for k in nodes[0] if k not in ("cat_begin", "cat_end")}
+        tree.update(is_categorical=np.array([nd["is_categorical"] for nd in nodes], np.uint8),
+                    cat_begin=np.array([nd["cat_begin"] for nd in nodes], np.uint32),
+                    cat_end=np.array([nd["cat_end"] for nd in nodes], np.uint32),
+                    categories=np.array(pool, np.uint32))
+        out = t % 2
+        engine.eval_add_tree(tree, out)
+        one = O.forest_arrays([nodes], tree_output=[out], n_outputs=2, base_score=np.zeros(2))
+        one.update(is_categorical=tree["is_categorical"], cat_begin=tree["cat_begin"], cat_end=tree["cat_end"],
+                   categories=tree["categories"])
+        want = (want + O.predict_margin(one, e).reshape(-1, 2)).astype(np.float32)
+    np.testing.assert_array_equal(engine.eval_margins(idx).view(np.uint32), want.view(np.uint32))
+    bad = dict(split_feature=[0, 0, 0], split_cond=[0.0, 0, 0], default_left=[1, 1, 1], left=[1, -1, -1],
+               right=[2, -1, -1], leaf_value=[0.0, 1, 2], is_categorical=[1, 0, 0], cat_begin=[0, 0, 0],
+               cat_end=[3, 0, 0], categories=[1, 2])
+    with pytest.raises(hb.HbrError):
+        engine.eval_add_tree(bad)
+
+
 def test_trees_discarded_by_the_device_are_added_to_no_eval_set():
     """Pipelined rounds whose gradients overflow: with eta 1e30 the second
     tree's leaves overflow to infinity, so the third round's gradients are
