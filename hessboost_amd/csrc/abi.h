@@ -394,6 +394,27 @@ struct HistArgs {
     float min_hess;
     uint32_t masked;            // rows carry missing masks (fg32 groups; the mask words at mask_at)
     uint32_t mask_at;           // masked: the byte of a row's first mask word (28: 32-byte rows)
+    // Dense rows of u16 local bins (hbr_hist_dense16_*): row r's bin of
+    // feature f at bins16[r * stride16 + f]; partials of fg x (kWideLdsBins /
+    // fg) bins per (tile, feature group)
+    const uint16_t *bins16;
+    uint32_t stride16;          // elements per row (a multiple of 16)
+    uint32_t pad4;
+};
+
+// Dense indexes with a feature of more than 256 bins (at most kWideBinsMax):
+// rows of u16 local bins. A histogram workgroup holds fg features of
+// kWideLdsBins / fg bins each in LDS (fg = 16, 8, 4, 2 or 1: the widest
+// feature's bins rounded up to a power of two, times fg, is kWideLdsBins).
+constexpr uint32_t kWideBinsMax = 8192;
+constexpr uint32_t kWideLdsBins = 8192;
+struct Encode16Args {
+    const uint32_t *gbins;      // the dense index's global bins, row-major [n_rows][n_cols]
+    const uint32_t *feature_offset;
+    uint16_t *rows16;           // [n_rows][stride16], zero beyond n_cols
+    uint64_t n_rows;
+    uint32_t n_cols;
+    uint32_t stride16;
 };
 
 // Each CSR row's first entry of every kCsrGroupBins range (rows' global bins ascend).
@@ -438,6 +459,8 @@ struct ReduceArgs {
     uint32_t groups;
     uint32_t fg;
     const GrowCounts *grow;     // non-null: nodes = its n_splits (the grid covers the most)
+    uint32_t group_bins;        // bins per feature in a partial: 256 (u8 rows) or kWideLdsBins / fg
+    uint32_t quarters;          // workgroups per feature: group_bins / 64
 };
 
 // sibling = parent - built, in place in the parent's slot, for each split.

@@ -68,6 +68,7 @@ void Engine::read_tunables() {
     if (const char *v = std::getenv("HBROCM_ROW_PAIRS")) row_pairs = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_FUSED_ROOT")) fused_root = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_MASKED_ROWS")) masked_rows = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_WIDE_ROWS")) wide_rows = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_BATCH_WALK")) batch_walk = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_BIN_ROWS_IN_REGISTERS")) bin_rows_in_registers = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
@@ -218,7 +219,27 @@ void Engine::upload_index(const hbr_index_desc &d) {
         }
         make_masked_rows();
     }
+    // (every row holds n_cols entries in feature order)
+    if (wide_rows && dense_ && !dense_u8_ && widest <= kWideBinsMax && n_cols_ > 0 && csr_ascending_ &&
+        entries_ == n_rows_ * n_cols_)
+        make_rows16(widest);
     dev_.sync();
+}
+
+// A dense index whose widest feature has more than 256 bins: its global
+// bins (the dense CSR rows, n_cols entries a row in feature order) to rows
+// of u16 local bins, 16 elements (32 bytes) a row at least; a histogram
+// workgroup then holds fg16_ features of kWideLdsBins / fg16_ bins each.
+void Engine::make_rows16(uint32_t widest) {
+    uint32_t bins = 512;
+    while (bins < widest) bins *= 2;
+    fg16_ = std::min<uint32_t>(16, kWideLdsBins / bins);
+    stride16_ = (n_cols_ + 15) / 16 * 16;
+    rows16_.resize(n_rows_ * stride16_);
+    Encode16Args a{gbins_.get(), d_fo_.get(), rows16_.get(), n_rows_, n_cols_, stride16_};
+    const uint64_t cells = n_rows_ * stride16_;
+    dev_.launch("hbr_encode_dense16", dim3((uint32_t)std::min<uint64_t>(ceil_div(cells, 256), 65535)), dim3(256), a);
+    dense16_ = true;
 }
 
 // A matrix with missing values and at most kMaskedWideMaxFeatures features
@@ -255,7 +276,7 @@ void Engine::make_masked_rows() {
 // (when the table takes at most 1 GiB).
 void Engine::build_csr_ranges() {
     csr_ranges_.release();
-    if (!csr_range_table || dense_u8_ || !csr_ascending_ || n_rows_ == 0) return;
+    if (!csr_range_table || dense_u8_ || dense16_ || !csr_ascending_ || n_rows_ == 0) return;
     const uint32_t groups = ceil_div(total_bins_, kCsrGroupBins);
     const uint64_t words = n_rows_ * (uint64_t)(groups + 1);
     if (groups < 2 || words * sizeof(uint32_t) > (uint64_t(1) << 30)) return;
@@ -1020,7 +1041,7 @@ bool Engine::reserve_slots(uint64_t n) {
 // pair the row carries), and its id when the node's rows are gathered
 // through a row list.
 uint64_t Engine::hist_bytes(uint64_t rows, bool gathered) const {
-    const uint64_t bins = dense_u8_ ? n_cols_ : 4ull * (n_rows_ ? gbins_.size() / n_rows_ : 0);
+    const uint64_t bins = dense_u8_ ? n_cols_ : dense16_ ? 2ull * n_cols_ : 4ull * (n_rows_ ? gbins_.size() / n_rows_ : 0);
     // a pair carried by the row is its one word in the row's padding
     const uint64_t pair = row_pairs_live_ && !level_pairs_ && dense_u8_ && stride_ == 32 ? 4 : 8;
     return rows * (bins + pair + (gathered ? 4 : 0));
@@ -1053,17 +1074,20 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     root_partials_ = 0;  // the partials are reused below
     if (!level_pairs_ && !pairs_staged()) fail(kInvalid, "histograms: no gradients staged");
     if (!dense_u8_ && grow) fail(kInvalid, "histograms: device-counted levels need the dense kernels");
-    const uint32_t fg = masked_ ? 32u : hist_features_per_group;  // masked rows: one group, the mask word
+    const bool wide = dense16_;  // u16 rows
+    const uint32_t fg = wide ? fg16_ : masked_ ? 32u : hist_features_per_group;  // masked rows: fg32 groups
+    const uint32_t group_bins = wide ? kWideLdsBins / fg16_ : 256u;
+    const bool dense = dense_u8_ || wide;
     // dense: feature groups of fg features; CSR: ranges of kCsrGroupBins
     // global bins (every range of every tile is written: no slot zeroing)
-    const uint32_t groups = dense_u8_ ? ceil_div(n_cols_, fg) : ceil_div(total_bins_, kCsrGroupBins);
+    const uint32_t groups = dense ? ceil_div(n_cols_, fg) : ceil_div(total_bins_, kCsrGroupBins);
     // LDS per workgroup: fg features x 257 words x 16 bytes, or 128 KiB, of 160 KiB
     const uint32_t per_cu = !dense_u8_ ? 1 : fg <= 8 ? 4 : fg <= 16 ? 2 : 1;
     const uint32_t target = std::max<uint32_t>(1, (uint32_t)dev_.cu_count() * per_cu * hist_waves / groups);
     (void)host_nodes;
     d_htiles_.reserve(target + n);
     d_hcounts_.reserve(4);
-    d_partial_.reserve((size_t)(dense_u8_ ? 2 * target : target + n) * groups * (dense_u8_ ? fg * 256 : kCsrGroupBins));
+    d_partial_.reserve((size_t)(dense ? 2 * target : target + n) * groups * (dense ? fg * group_bins : kCsrGroupBins));
 
     HistNode *nodes_rw = const_cast<HistNode *>(nodes_dev);  // the plan kernel resolves them in place
     PlanArgs p{};
@@ -1075,7 +1099,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     p.tiles = d_htiles_.get();
     p.counts = d_hcounts_.get();
     p.min_rows = kHistMinRows;
-    p.fuse_subtract = dense_u8_ ? 1u : 0u;
+    p.fuse_subtract = dense ? 1u : 0u;
     p.grow = grow;
     dev_.launch("hbr_hist_plan", dim3(1), dim3(256), p);
 
@@ -1105,14 +1129,19 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.masked = masked_ ? 1u : 0u;
     a.mask_at = mask_at_;
     a.min_hess = row_pairs_min_hess_;
+    a.bins16 = rows16_.get();
+    a.stride16 = stride16_;
+    static const char *const wide_kernels[] = {"hbr_hist_dense16_fg1", "hbr_hist_dense16_fg2", "hbr_hist_dense16_fg4",
+                                               "hbr_hist_dense16_fg8", "hbr_hist_dense16_fg16"};
     const bool bm = hist_bin_major && fg >= 16;
-    const char *k = !dense_u8_ ? "hbr_hist_csr"
-                    : masked_  ? "hbr_hist_dense8_fg32_bm_masked"
-                    : fg <= 8  ? "hbr_hist_dense8_fg8"
-                    : fg <= 16 ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
-                               : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");
-    dev_.launch(k, dim3((target + n) * groups), dim3(dense_u8_ ? hist_threads : kCsrThreads), a);
-    if (!dense_u8_) {
+    const char *k = wide        ? wide_kernels[__builtin_ctz(fg)]
+                    : !dense_u8_ ? "hbr_hist_csr"
+                    : masked_    ? "hbr_hist_dense8_fg32_bm_masked"
+                    : fg <= 8    ? "hbr_hist_dense8_fg8"
+                    : fg <= 16   ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
+                                 : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");
+    dev_.launch(k, dim3((target + n) * groups), dim3(dense ? hist_threads : kCsrThreads), a);
+    if (!dense) {
         ReduceArgs r{};
         r.nodes = nodes_dev;
         r.partial = d_partial_.get();
@@ -1121,7 +1150,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
         r.groups = groups;
         dev_.launch("hbr_hist_reduce_csr", dim3(ceil_div(total_bins_, 256), n), dim3(256), r);
     }
-    if (dense_u8_) {
+    if (dense) {
         ReduceArgs r{};
         r.nodes = nodes_dev;
         r.partial = d_partial_.get();
@@ -1132,7 +1161,9 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
         r.groups = groups;
         r.fg = fg;
         r.grow = grow;
-        dev_.launch("hbr_hist_reduce", dim3(n_cols_ * 4, n), dim3(1024), r);
+        r.group_bins = group_bins;
+        r.quarters = group_bins / 64u;
+        dev_.launch("hbr_hist_reduce", dim3(n_cols_ * r.quarters, n), dim3(1024), r);
     }
 }
 
@@ -1376,7 +1407,7 @@ std::vector<LevelChild> Engine::level(const std::vector<LevelSplit> &splits, boo
 
     if (!terminal) {
         launch_hist(reinterpret_cast<const HistNode *>(dev_in + o_hnodes), P, &hn, splits_dev, pout_dev);
-        if (!dense_u8_) {  // the dense kernels turn each parent into the sibling as they finish
+        if (!dense_u8_ && !dense16_) {  // the dense kernels turn each parent into the sibling as they finish
             SubArgs sub{splits_dev, P, hist_.get(), total_bins_};
             dev_.launch("hbr_subtract", dim3(std::min<uint32_t>(ceil_div(total_bins_, 256), 64), P), dim3(256), sub);
         }
@@ -1514,6 +1545,8 @@ void Engine::launch_device_roots(uint32_t n_trees) {
         r.total_bins = total_bins_;
         r.groups = 1;
         r.fg = kRootFeatures;
+        r.group_bins = 256;
+        r.quarters = 4;
         r.grow = nullptr;
         dev_.launch("hbr_hist_reduce", dim3(n_cols_ * 4, 1), dim3(1024), r);
     } else {
@@ -2195,6 +2228,8 @@ bool Engine::build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uin
     r.total_bins = total_bins_;
     r.groups = groups;
     r.fg = fg;
+    r.group_bins = 256;
+    r.quarters = 4;
     if (dense_u8_)
         dev_.launch("hbr_hist_reduce", dim3(n_cols_ * 4, 1), dim3(1024), r);
     else

@@ -459,6 +459,13 @@ private:
     // values (dense_ false, dense_u8_ true).
     bool masked_ = false;
     uint32_t mask_at_ = 0;  // masked rows: the byte of a row's first mask word
+    // A dense index with a feature of more than 256 bins (at most
+    // kWideBinsMax): rows of u16 local bins for the histograms (the CSR
+    // rows and columns serve the rest), fg16_ features per workgroup.
+    bool dense16_ = false;
+    DBuf<uint16_t> rows16_;
+    uint32_t stride16_ = 0, fg16_ = 0;
+    void make_rows16(uint32_t widest);
     void make_masked_rows();
     // Partials of the next root's histogram the fused walk left (0: none);
     // the next device tree's root sums them instead of building its own.
@@ -536,6 +543,7 @@ public:
     bool row_pairs = true;       // unit-weight logistic pairs carried in the rows' padding
     bool fused_root = true;      // the margin walk also sums the next root's histogram (row pairs)
     bool masked_rows = true;     // dense u8 rows with a missing mask for matrices with missing values
+    bool wide_rows = true;       // dense u16 rows for the histograms of features of more than 256 bins
     bool batch_walk = true;  // a softmax round's class trees added to the margins in one walk
     bool bin_rows_in_registers = true;  // device binning of <= 32 features: rows into registers, else staged in LDS
     bool device_grow = true;     // depthwise trees decided on the device where eligible

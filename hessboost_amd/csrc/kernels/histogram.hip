@@ -367,12 +367,103 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
     }
 }
 
+// Dense rows of u16 local bins (features of more than 256 bins): a
+// workgroup sums one tile's rows for one group of FG features into an LDS
+// sub-histogram of FG x B u64 pairs ([feature][bin], B = kWideLdsBins / FG
+// bins per feature), each row's FG bins read with one vector load, its pair
+// from the pair array; then the node's slot (a node of one tile, its parent
+// turned into the sibling as for u8 rows) or the tile's partial, which
+// hbr_hist_reduce sums. Rows past a feature group's last feature hold zeros
+// and add nowhere.
+template <int FG>
+__device__ __forceinline__ void load_bins16(const uint16_t *p, uint32_t (&w)[(FG + 1) / 2]) {
+    if constexpr (FG == 16) {
+        const uint4 x = reinterpret_cast<const uint4 *>(p)[0], y = reinterpret_cast<const uint4 *>(p)[1];
+        w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w; w[4] = y.x; w[5] = y.y; w[6] = y.z; w[7] = y.w;
+    } else if constexpr (FG == 8) {
+        const uint4 x = reinterpret_cast<const uint4 *>(p)[0];
+        w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+    } else if constexpr (FG == 4) {
+        const uint2 x = reinterpret_cast<const uint2 *>(p)[0];
+        w[0] = x.x; w[1] = x.y;
+    } else if constexpr (FG == 2) {
+        w[0] = reinterpret_cast<const uint32_t *>(p)[0];
+    } else {
+        w[0] = p[0];
+    }
+}
+
+template <int FG>
+__device__ __forceinline__ void hist_dense16(const HistArgs &a) {
+    constexpr uint32_t B = kWideLdsBins / FG;
+    constexpr uint32_t kWords = FG * B;
+    __shared__ unsigned long long lg[kWords];
+    __shared__ unsigned long long lh[kWords];
+    const uint32_t entry = blockIdx.x / a.groups, grp = blockIdx.x % a.groups;
+    if (entry >= a.counts[0]) return;  // uniform across the workgroup
+    const HistTile t = a.tiles[entry];
+    const HistNode nd = a.nodes[t.node];
+    const uint32_t f0 = grp * FG;
+    const uint32_t nf = min((uint32_t)FG, a.n_cols - f0);
+    for (uint32_t i = threadIdx.x; i < kWords; i += blockDim.x) {
+        lg[i] = 0ull;
+        lh[i] = 0ull;
+    }
+    __syncthreads();
+    const int eg = a.scale[nd.cls].exp_g, eh = a.scale[nd.cls].exp_h;
+    const GPair *gpair = a.gpair + (size_t)nd.cls * a.class_rows;
+    const uint32_t *rows = a.rows[nd.seg.buf] + nd.seg.offset;
+    const uint32_t end = t.row0 + t.rows;
+    for (uint32_t j = t.row0 + threadIdx.x; j < end; j += blockDim.x) {
+        const uint32_t r = nd.contiguous ? nd.seg.offset + j : rows[j];
+        uint32_t w[(FG + 1) / 2];
+        load_bins16<FG>(a.bins16 + (size_t)r * a.stride16 + f0, w);
+        const GPair p = gpair[r];
+        const unsigned long long qg = (unsigned long long)quantize(p.g, eg);
+        const unsigned long long qh = (unsigned long long)quantize(p.h, eh);
+#pragma unroll
+        for (int f = 0; f < FG; f++) {
+            if ((uint32_t)f >= nf) break;
+            const uint32_t bin = FG == 1 ? w[0] & 0xffffu : (w[f >> 1] >> ((f & 1) * 16)) & 0xffffu;
+            atomicAdd(&lg[f * B + bin], qg);
+            atomicAdd(&lh[f * B + bin], qh);
+        }
+    }
+    __syncthreads();
+    const uint32_t *fo = a.feature_offset + f0;
+    QBin *dst = nd.n_tiles == 1 ? a.hist + (size_t)nd.slot * a.total_bins
+                                : a.partial + ((size_t)(nd.pad[0] + t.k) * a.groups + grp) * kWords;
+    for (uint32_t i = threadIdx.x; i < kWords; i += blockDim.x) {
+        const uint32_t ff = i / B, bin = i % B;
+        if (ff >= nf) continue;
+        const QBin v{(int64_t)lg[i], (int64_t)lh[i]};
+        if (nd.n_tiles == 1) {
+            const uint32_t lo = fo[ff], nb = fo[ff + 1] - lo;
+            if (bin < nb) {
+                dst[lo + bin] = v;
+                if (nd.pad[1]) {  // this workgroup alone completes these bins: sibling = parent - built
+                    QBin *par = a.hist + (size_t)(nd.pad[1] - 1u) * a.total_bins + lo + bin;
+                    const QBin pv = *par;
+                    *par = QBin{pv.g - v.g, pv.h - v.h};
+                }
+            }
+        } else {
+            dst[i] = v;
+        }
+    }
+}
+
 // Launched with 512 or 1024 threads.
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg8(HistArgs a) { hist_dense8<8, false>(a); }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16(HistArgs a) { hist_dense8<16, false>(a); }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32(HistArgs a) { hist_dense8<32, false>(a); }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg16_bm(HistArgs a) { hist_dense8<16, true>(a); }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm(HistArgs a) { hist_dense8<32, true>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense16_fg16(HistArgs a) { hist_dense16<16>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense16_fg8(HistArgs a) { hist_dense16<8>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense16_fg4(HistArgs a) { hist_dense16<4>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense16_fg2(HistArgs a) { hist_dense16<2>(a); }
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense16_fg1(HistArgs a) { hist_dense16<1>(a); }
 // Masked rows (a missing mask in word kMaskWord): one group of 32 features.
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm_masked(HistArgs a) {
     hist_dense8<32, true, true>(a);
@@ -380,11 +471,12 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm_maske
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_csr(HistArgs a) { hist_csr(a); }
 
 // Nodes cut into several tiles: the slot is the sum of the tiles' partials.
-// A workgroup takes 64 bins of one feature of one node; its 16 waves split
-// the node's tiles, then combine in LDS.
+// A workgroup takes 64 bins of one feature of one node (a.quarters
+// workgroups per feature); its 16 waves split the node's tiles, then
+// combine in LDS.
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_reduce(ReduceArgs a) {
     __shared__ int64_t acc[2][16][64];
-    const uint32_t f = blockIdx.x >> 2, quarter = blockIdx.x & 3u;
+    const uint32_t f = blockIdx.x / a.quarters, quarter = blockIdx.x % a.quarters;
     if (a.grow && blockIdx.y >= a.grow->n_splits) return;
     const HistNode nd = a.nodes[blockIdx.y];
     if (f >= a.n_cols || nd.n_tiles == 1) return;  // uniform across the workgroup
@@ -392,11 +484,11 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_hist_reduce(ReduceArgs a)
     if (quarter * 64u >= nb) return;
     const uint32_t col = threadIdx.x & 63u, ks = threadIdx.x >> 6;
     const uint32_t bin = quarter * 64u + col;
-    const uint32_t grp = f / a.fg, local = (f % a.fg) * 256u + bin;
+    const uint32_t grp = f / a.fg, local = (f % a.fg) * a.group_bins + bin;
     int64_t g = 0, h = 0;
     if (bin < nb) {
         for (uint32_t k = ks; k < nd.n_tiles; k += 16) {
-            const QBin q = a.partial[((size_t)(nd.pad[0] + k) * a.groups + grp) * (a.fg * 256u) + local];
+            const QBin q = a.partial[((size_t)(nd.pad[0] + k) * a.groups + grp) * (a.fg * a.group_bins) + local];
             g += q.g;
             h += q.h;
         }

@@ -19,6 +19,19 @@ extern "C" __global__ __launch_bounds__(256) void hbr_encode_dense(EncodeArgs a)
     }
 }
 
+// Dense indexes with a feature of more than 256 bins: the global bins of
+// the index's dense CSR rows (row r's entries at r * n_cols, in feature
+// order) to rows of u16 local bins, zero beyond n_cols.
+extern "C" __global__ __launch_bounds__(256) void hbr_encode_dense16(Encode16Args a) {
+    const uint64_t cells = a.n_rows * a.stride16;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cells;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = i / a.stride16;
+        const uint32_t f = (uint32_t)(i % a.stride16);
+        a.rows16[i] = f < a.n_cols ? (uint16_t)(a.gbins[r * a.n_cols + f] - a.feature_offset[f]) : (uint16_t)0;
+    }
+}
+
 // Binning a dense f32 matrix on the device. bin = #{cuts <= v} over the
 // feature's cuts (an upper bound), clamped to its last bin, as
 // HistCuts::bin_of (src/data/quantile.rs:285-296) and the host's

@@ -557,6 +557,48 @@ def test_missing_values_on_wide_masked_rows_match_oracle_and_csr_path(n_features
     assert np.max(np.abs(mm - ref.margins().reshape(mm.shape))) <= 1e-5
 
 
+@pytest.mark.parametrize("max_bin,objective,kernel", [(512, "binary:logistic", "hbr_hist_dense16_fg16"),
+                                                      (1024, "reg:squarederror", "hbr_hist_dense16_fg8"),
+                                                      (3000, "reg:squarederror", "hbr_hist_dense16_fg2")])
+def test_features_of_more_than_256_bins_train_on_u16_rows(max_bin, objective, kernel):
+    """A dense matrix whose features take more than 256 bins (max_bin 512,
+    1024, 3000; local bins u16 as in GHistIndex's columns) builds its
+    histograms from rows of u16 local bins, 16, 8 or 2 features per
+    workgroup: the oracle's trees, and the CSR path's
+    (HBROCM_WIDE_ROWS=0) trees and margins bit for bit."""
+    import os
+    x, y = synthetic.regression_100k(n=30_000, f=21, seed=max_bin)
+    x[:, 5] = np.round(x[:, 5] * 3)  # a feature of few bins beside the wide ones
+    if objective == "binary:logistic":
+        y = (y > 0).astype(np.float32)
+    params = {"objective": objective, "max_depth": 6, "eta": 0.3, "max_bin": max_bin}
+    obj = O.OBJ_LOGISTIC if objective == "binary:logistic" else O.OBJ_SQUARED_ERROR
+    ref = O.Model(O.Dataset(x, max_bin=max_bin), y, O.params(objective=obj, max_depth=6, eta=0.3, max_bin=max_bin), 3)
+    runs = []
+    for wide in ("1", "0"):
+        saved = os.environ.pop("HBROCM_WIDE_ROWS", None)
+        os.environ["HBROCM_WIDE_ROWS"] = wide
+        try:
+            eng = hb.DMatrix(x, label=y).engine(max_bin)
+            eng.set_profiling(True, "hbr_hist")
+            tr = hb.Trainer(eng, params, y)
+            tr.boost(3)
+            launched = set(eng.kernel_stats())
+            eng.set_profiling(False)
+        finally:
+            os.environ.pop("HBROCM_WIDE_ROWS", None)
+            if saved is not None:
+                os.environ["HBROCM_WIDE_ROWS"] = saved
+        assert (kernel in launched) == (wide == "1"), launched
+        runs.append((tr.trees(), tr.margins()))
+    compare_trees(runs[0][0], ref.trees())
+    for a, b in zip(runs[0][0], runs[1][0]):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+    assert np.max(np.abs(runs[0][1] - ref.margins())) <= 1e-5
+
+
 @pytest.mark.parametrize("leaves", [3, 6, 14])
 def test_lossguide_with_equal_gains_matches_oracle(leaves):
     """Mirrored rows give every node below the root a twin of equal loss
