@@ -83,6 +83,7 @@ CASES = [
     ("one-hot", 5_000, [3, 2], {"objective": "reg:squarederror", "max_depth": 4}, 0.05),
     ("partition", 20_000, [12, 9], {"objective": "reg:squarederror", "max_depth": 6}, 0.1),
     ("beyond the 64-deep scan", 30_000, [300], {"objective": "binary:logistic", "max_depth": 5}, 0.02),
+    ("300 categories on u16 rows", 30_000, [300], {"objective": "binary:logistic", "max_depth": 5}, 0.0),
     ("lossguide", 12_000, [7, 40], {"objective": "reg:squarederror", "grow_policy": "lossguide", "max_depth": 0,
                                     "max_leaves": 24}, 0.05),
     ("softmax", 9_000, [6], {"objective": "multi:softprob", "num_class": 3, "max_depth": 4}, 0.0),

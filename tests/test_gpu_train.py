@@ -599,6 +599,30 @@ def test_features_of_more_than_256_bins_train_on_u16_rows(max_bin, objective, ke
     assert np.max(np.abs(runs[0][1] - ref.margins())) <= 1e-5
 
 
+def test_u16_rows_softmax_lossguide_and_weights_match_oracle():
+    """The u16 rows under the other growth paths: 3-class softmax
+    (per-class pairs), loss-guided growth with sample weights, both at
+    max_bin 700, against the oracle."""
+    x, y = synthetic.multiclass(n=12_000, f=9, k=3, seed=12)
+    params = {"objective": "multi:softprob", "num_class": 3, "max_depth": 5, "eta": 0.3, "max_bin": 700}
+    ref = O.Model(O.Dataset(x, max_bin=700), y, O.params(objective=O.OBJ_SOFTMAX, num_class=3, max_depth=5,
+                                                         max_bin=700), 2)
+    eng = hb.DMatrix(x, label=y).engine(700)
+    eng.set_profiling(True, "hbr_hist")
+    tr = hb.Trainer(eng, params, y)
+    tr.boost(2)
+    assert "hbr_hist_dense16_fg8" in eng.kernel_stats()
+    compare_trees(tr.trees(), ref.trees())
+    x, y = synthetic.regression_100k(n=15_000, f=7, seed=13)
+    w = np.random.default_rng(13).random(len(y)).astype(np.float32) + 0.25
+    params = {"grow_policy": "lossguide", "max_depth": 0, "max_leaves": 40, "eta": 0.3, "max_bin": 700}
+    ref = O.Model(O.Dataset(x, max_bin=700, weights=w), y,
+                  O.params(grow_policy=O.GROW_LOSSGUIDE, max_depth=0, max_leaves=40, max_bin=700), 3, weights=w)
+    model = hb.train(params, hb.DMatrix(x, label=y, weight=w), 3)
+    compare_trees(model.trees, ref.trees())
+    assert np.max(np.abs(model.predict(x, output_margin=True) - ref.margins())) <= 1e-5
+
+
 @pytest.mark.parametrize("leaves", [3, 6, 14])
 def test_lossguide_with_equal_gains_matches_oracle(leaves):
     """Mirrored rows give every node below the root a twin of equal loss
