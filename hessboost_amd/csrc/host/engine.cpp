@@ -1878,6 +1878,38 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     scale_checked_ = false;  // the next tree's finish checks the scale
 }
 
+void Engine::walk_device_tree_then_gradients(const hbr_device_loss &next_loss) {
+    if (!dense_u8_) fail(kRefused, "walk: the index has no row-major u8 bins");
+    if (outputs_ != 1 || !labels_loaded_) fail(kInvalid, "walk: gradients need one output and labels");
+    hipStream_t s = dev_.stream();
+    if (!poison_.size()) {
+        poison_.resize(1);
+        guard_scale_.resize(1);
+        HBR_HIP(hipMemsetAsync(poison_.get(), 0, sizeof(uint32_t), s));
+    }
+    // the tree's scale aside (the walk's guard); the gradients clear the live one
+    RotateArgs r{scale_dev(), guard_scale_.get()};
+    dev_.launch("hbr_scale_rotate", dim3(1), dim3(64), r);
+    WalkArgs a{};
+    a.masked = masked_ ? 1u : 0u;
+    a.mask_at = mask_at_;
+    a.tree = ring_nodes(last_ring_, 0, last_stride_);
+    a.counts = &ring_header(last_ring_, 0, last_stride_)->counts;
+    a.bins8 = rows8_.get();
+    a.margins = margins_.get();
+    a.stride = stride_;
+    a.n = (uint32_t)n_rows_;
+    a.m_stride = outputs_;
+    a.output = 0;
+    a.guard = guard_scale_.get();
+    a.guard_n = 1;
+    a.poison = poison_.get();
+    const uint32_t blocks =
+        std::min<uint32_t>(std::max<uint32_t>(1, ceil_div(n_rows_, 256)), (uint32_t)dev_.cu_count() * walk_blocks_per_cu);
+    dev_.launch("hbr_walk_leaves", dim3(blocks), dim3(256), a);
+    compute_gradients_async(next_loss, 0);
+}
+
 uint32_t Engine::add_eval_set(const float *x, uint64_t n_rows, uint64_t n_cols, float missing, const float *init,
                               uint32_t outputs) {
     if (!x || !init) fail(kInvalid, "evaluation set: null argument");

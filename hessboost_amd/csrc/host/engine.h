@@ -224,6 +224,15 @@ public:
     }
     // The walk alone (no gradients): any dense u8 index, any output.
     bool can_route_device_tree(uint64_t max_depth) const { return can_grow_device(max_depth); }
+    // The last queued device tree's leaves onto the margins of one output by
+    // the walk of any row layout (wider rows, masked rows, deeper trees),
+    // guarded by the tree's own scale as walk_device_tree guards it, then
+    // the next round's gradients from the updated margins: the two passes
+    // the fused walk makes one.
+    bool can_walk_then_gradients(uint64_t max_depth) const {
+        return can_grow_device(max_depth) && outputs_ == 1 && labels_loaded_;
+    }
+    void walk_device_tree_then_gradients(const hbr_device_loss &next_loss);
     // The trees of the last queued batch (its trees 0..n_trees-1) added to
     // margins outputs first_output.. in one pass over the rows, guarded as
     // walk_device_tree; false (nothing queued) when the batch does not fit

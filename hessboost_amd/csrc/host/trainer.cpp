@@ -557,7 +557,7 @@ void Trainer::grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_los
 // waits for the host. A tree whose gradients turn out not to be finite had
 // its walk skipped on the device, and so had every tree queued after it:
 // the margins hold the trees before it, and training stops there.
-void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
+void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss, bool fused) {
     TreeBuilder b(e_, p_.grow);
     std::deque<Engine::TreeTicket> inflight;
     uint64_t queued = 0, done = 0;
@@ -565,7 +565,10 @@ void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss) {
         while (queued < rounds && inflight.size() < 3) {
             if (!grads_ready_) e_.compute_gradients_async(loss, 0);
             inflight.push_back(b.queue_device());
-            e_.walk_device_tree(0, &loss);
+            if (fused)
+                e_.walk_device_tree(0, &loss);
+            else
+                e_.walk_device_tree_then_gradients(loss);
             e_.walk_evals_device(0, 0, true);
             grads_ready_ = true;
             queued++;
@@ -668,7 +671,14 @@ void Trainer::boost(uint64_t rounds) {
     }
     if (p_.objective != HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE &&
         e_.can_walk_device_tree(p_.grow.max_depth)) {
-        boost_pipelined(rounds, device_loss());
+        boost_pipelined(rounds, device_loss(), true);
+        return;
+    }
+    // wider or masked rows, deeper trees: the same rounds with the walk and
+    // the next gradients as two passes
+    if (p_.objective != HBR_OBJ_SOFTMAX && p_.grow.policy == HBR_GROW_DEPTHWISE &&
+        e_.can_walk_then_gradients(p_.grow.max_depth)) {
+        boost_pipelined(rounds, device_loss(), false);
         return;
     }
     TreeBuilder b(e_, p_.grow);

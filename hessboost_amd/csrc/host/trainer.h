@@ -136,7 +136,7 @@ public:
 private:
     void boost_softmax_pipelined(uint64_t rounds);
     void boost_softmax_batched(uint64_t rounds);
-    void boost_pipelined(uint64_t rounds, const hbr_device_loss &loss);
+    void boost_pipelined(uint64_t rounds, const hbr_device_loss &loss, bool fused);
     hbr_device_loss device_loss() const;
     // one grown tree onto the margins of output `output` (and, given
     // next_loss, the next round's gradients in the same pass)

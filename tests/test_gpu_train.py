@@ -599,6 +599,53 @@ def test_features_of_more_than_256_bins_train_on_u16_rows(max_bin, objective, ke
     assert np.max(np.abs(runs[0][1] - ref.margins())) <= 1e-5
 
 
+@pytest.mark.parametrize("objective,f,depth", [("binary:logistic", 40, 7), ("reg:squarederror", 33, 6),
+                                               ("binary:logistic", 20, 11)])
+def test_device_rounds_on_wide_rows_and_deep_trees(objective, f, depth):
+    """Depthwise rounds decided on the device for rows wider than 32 bytes
+    or trees deeper than the fused walk takes (depth 11): the tree's leaves
+    walked onto the margins on any row layout, then the next gradients, all
+    queued ahead of the host: the host-decided rounds' trees, margins and
+    eval-set margins bit for bit (HBROCM_DEVICE_GROW=0), and the oracle's
+    trees."""
+    import os
+    x, y = synthetic.regression_100k(n=25_000, f=f, seed=f + depth)
+    if objective == "binary:logistic":
+        y = (y > 0).astype(np.float32)
+    xe = synthetic.regression_100k(n=3_000, f=f, seed=99)[0]
+    params = {"objective": objective, "max_depth": depth, "eta": 0.3}
+    obj = O.OBJ_LOGISTIC if objective == "binary:logistic" else O.OBJ_SQUARED_ERROR
+    ref = O.Model(O.Dataset(x), y, O.params(objective=obj, max_depth=depth, eta=0.3), 4)
+    runs = []
+    for grow in ("1", "0"):
+        saved = os.environ.pop("HBROCM_DEVICE_GROW", None)
+        os.environ["HBROCM_DEVICE_GROW"] = grow
+        try:
+            eng = hb.DMatrix(x, label=y).engine(256)
+            eng.set_profiling(True, "hbr_")
+            tr = hb.Trainer(eng, params, y)
+            ev = tr.add_eval(hb.DMatrix(xe))
+            tr.boost(4)
+            launched = set(eng.kernel_stats())
+            eng.set_profiling(False)
+        finally:
+            os.environ.pop("HBROCM_DEVICE_GROW", None)
+            if saved is not None:
+                os.environ["HBROCM_DEVICE_GROW"] = saved
+        assert ("hbr_grow_decide" in launched) == (grow == "1"), launched
+        if grow == "1":  # the walk of any layout, then the gradient pass
+            assert "hbr_walk_leaves" in launched and "hbr_gradients" in launched, launched
+            assert not any(k.startswith("hbr_walk_grad") for k in launched), launched
+        runs.append((tr.trees(), tr.margins(), tr.eval_margins(ev)))
+    compare_trees(runs[0][0], ref.trees())
+    for a, b in zip(runs[0][0], runs[1][0]):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
+    assert np.array_equal(runs[0][2].view(np.uint32), runs[1][2].view(np.uint32))
+    assert np.max(np.abs(runs[0][1] - ref.margins())) <= 1e-5
+
+
 def test_u16_rows_softmax_lossguide_and_weights_match_oracle():
     """The u16 rows under the other growth paths: 3-class softmax
     (per-class pairs), loss-guided growth with sample weights, both at
