@@ -173,6 +173,18 @@ struct GradArgs {
     uint8_t *pair_rows;
     uint32_t pair_stride;
     uint32_t pair_byte;
+    // Rows held in another order than the original one (a reorder by a
+    // tree's leaves; the fused walks only): position i holds original row
+    // perm[i], and the 8-row vectors are those of the original rows. A row
+    // then takes the vector path on its own margin's test; a row of the
+    // vector range that fails it marks its original vector g
+    // (group_stamp[g] = stamp; g listed once in bad_groups[1..], counted in
+    // bad_groups[0]), whose other rows hbr_regroup moves to the scalar path.
+    const uint32_t *perm;
+    uint32_t *group_stamp;  // [vec_rows / 8]
+    uint32_t *bad_groups;   // [1 + vec_rows / 8]
+    uint32_t stamp;         // this pass's mark (non-zero, new each pass)
+    uint32_t pad_perm;
 };
 
 // Softmax gradients of every class of every row (simd/mod.rs:502-600),
@@ -801,6 +813,33 @@ struct EvalWalkArgs {
     const uint32_t *categories;
 };
 
+// Rows reordered by a device-grown tree's leaves (the whole-round trainer
+// on 32-byte rows, so that the rows of later trees' nodes, which follow
+// much the same splits, sit together in memory): each row's leaf and the
+// leaves' row counts, their starts, then each row's new position
+// (perm[position] = the original row); the row-indexed arrays are then
+// gathered through perm (and back through its inverse).
+constexpr uint32_t kOrderMaxNodes = 1024;
+struct OrderArgs {
+    WalkArgs w;                 // the tree (its records and counts) and the 32-byte rows
+    uint32_t *leaf;             // [n] each row's leaf
+    uint32_t *count;            // [kOrderMaxNodes] rows per leaf
+    uint32_t *cursor;           // [kOrderMaxNodes] the scan: each leaf's next free position
+    uint32_t *perm;             // [n] position -> original row
+};
+struct GatherArgs {
+    const uint32_t *index;      // [n] position -> source row
+    const uint8_t *src8;        // records (row_bytes each) or columns ([n_cols][n] bytes)
+    uint8_t *dst8;
+    const float *src32;         // k values per row
+    float *dst32;
+    uint64_t n;
+    uint32_t row_bytes;         // a multiple of 16
+    uint32_t n_cols;
+    uint32_t k;
+    uint32_t pad;
+};
+
 // The margin walk of a finished tree followed, row by row, by the next
 // round's gradients of the updated margin (the gradient kernel's arithmetic
 // and max fold; w.margins and g.margins are the same array).
@@ -836,7 +875,23 @@ struct RootFixupArgs {
     uint32_t n_walk_tiles;
     uint32_t n_cols;
     float min_hess;
-    uint32_t pad;
+    uint32_t regroup_tile;  // 1: hbr_regroup wrote partial n_walk_tiles + 1 (rows held reordered)
+};
+
+// After a fused walk over reordered rows (GradArgs::perm): every row of a
+// marked original vector that took the vector path goes to the scalar list
+// for hbr_finish_scale; with root_partial, its vector pair (unit weight, as
+// hbr_walk_grad_root summed it) is subtracted into partial n_walk_tiles + 1
+// (written whole every time). One workgroup; clears bad_groups[0].
+struct RegroupArgs {
+    GradArgs g;
+    const uint32_t *perm_inv;   // [n] original row -> position
+    const uint8_t *bins8;       // rows of 32 bytes (root_partial only)
+    QBin *root_partial;         // null: no root histogram to correct
+    int32_t root_exp_g;
+    int32_t root_exp_h;
+    uint32_t n_walk_tiles;
+    uint32_t n_cols;
 };
 
 // ---- prediction ---------------------------------------------------------------------

@@ -59,15 +59,18 @@ int guard(F &&fn) {
     }
 }
 
-// Run fn under the engine's lock; a device error poisons the engine.
+// Run fn under the engine's lock; a device error poisons the engine. Rows
+// a trainer reordered go back to the caller's order first, except for the
+// trainer's own calls and those that touch no row (keep_order).
 template <typename F>
-int with_engine(hbr_engine *h, F &&fn) {
+int with_engine(hbr_engine *h, F &&fn, bool keep_order = false) {
     if (!h || !h->e) return set_error(HBR_INVALID, "null engine");
     Engine &e = *h->e;
     std::lock_guard<std::mutex> lock(e.mu);
     if (e.failed) return set_error(HBR_DEVICE_ERROR, "the engine failed earlier; every call is refused");
     int st = guard([&] {
         e.dev().activate();
+        if (!keep_order) e.restore_row_order();
         fn(e);
     });
     if (st == HBR_DEVICE_ERROR) e.failed = true;
@@ -805,29 +808,30 @@ int hbr_engine_set_guard(hbr_engine *h, int mode, double gamma) {
             fail(kInvalid, "set_guard: unknown mode");
         e.guard_mode = mode;
         e.guard_gamma = (float)gamma;
-    });
+    }, true);
 }
 
 int hbr_engine_set_sums(hbr_engine *h, int mode) {
     return with_engine(h, [&](Engine &e) {
         if (mode != HBR_SUMS_EXACT && mode != HBR_SUMS_FIXED_POINT) fail(kInvalid, "set_sums: unknown mode");
         e.exact_sums_only = mode == HBR_SUMS_EXACT;
-    });
+    }, true);
 }
 
 int hbr_engine_counters_read(hbr_engine *h, hbr_engine_counters *out) {
     return with_engine(h, [&](Engine &e) {
         if (!out) fail(kInvalid, "counters: null output");
         *out = e.counters;
-    });
+    }, true);
 }
 
 int hbr_set_profiling(hbr_engine *h, int on, const char *prefix) {
-    return with_engine(h, [&](Engine &e) { e.dev().set_profiling(on > 0 ? (uint32_t)on : 0u, prefix ? prefix : ""); });
+    return with_engine(
+        h, [&](Engine &e) { e.dev().set_profiling(on > 0 ? (uint32_t)on : 0u, prefix ? prefix : ""); }, true);
 }
 
 int hbr_kernel_stats(hbr_engine *h, char *buf, size_t len) {
-    return with_engine(h, [&](Engine &e) { copy_string(stats_string(e.dev()), buf, len); });
+    return with_engine(h, [&](Engine &e) { copy_string(stats_string(e.dev()), buf, len); }, true);
 }
 
 // ---- training ------------------------------------------------------------------------
@@ -863,7 +867,7 @@ int hbr_trainer_create(hbr_engine *h, const hbr_train_params *p, const float *la
 
 int hbr_trainer_boost(hbr_trainer *t, uint64_t rounds) {
     if (!t) return set_error(HBR_INVALID, "null trainer");
-    return with_engine(t->engine, [&](Engine &) { t->t->boost(rounds); });
+    return with_engine(t->engine, [&](Engine &) { t->t->boost(rounds); }, true);
 }
 
 int hbr_trainer_num_trees(hbr_trainer *t, uint64_t *n) {
@@ -932,19 +936,19 @@ int hbr_trainer_tree_categories(hbr_trainer *t, uint64_t tree, uint8_t *is_categ
 
 int hbr_trainer_margins(hbr_trainer *t, float *out) {
     if (!t) return set_error(HBR_INVALID, "null trainer");
-    return with_engine(t->engine, [&](Engine &) { t->t->margins(out); });
+    return with_engine(t->engine, [&](Engine &) { t->t->margins(out); }, true);
 }
 
 int hbr_trainer_add_eval(hbr_trainer *t, const float *x, uint64_t n_rows, uint64_t n_cols, float missing,
                          const float *base_margin, uint32_t *index) {
     if (!t || !x || !index) return set_error(HBR_INVALID, "trainer: null argument");
     return with_engine(t->engine,
-                       [&](Engine &) { *index = t->t->add_eval(x, n_rows, n_cols, missing, base_margin); });
+                       [&](Engine &) { *index = t->t->add_eval(x, n_rows, n_cols, missing, base_margin); }, true);
 }
 
 int hbr_trainer_eval_margins(hbr_trainer *t, uint32_t index, float *out) {
     if (!t || !out) return set_error(HBR_INVALID, "trainer: null argument");
-    return with_engine(t->engine, [&](Engine &) { t->t->eval_margins(index, out); });
+    return with_engine(t->engine, [&](Engine &) { t->t->eval_margins(index, out); }, true);
 }
 
 void hbr_trainer_free(hbr_trainer *t) { delete t; }

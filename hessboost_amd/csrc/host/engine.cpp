@@ -69,6 +69,9 @@ void Engine::read_tunables() {
     if (const char *v = std::getenv("HBROCM_FUSED_ROOT")) fused_root = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_MASKED_ROWS")) masked_rows = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_WIDE_ROWS")) wide_rows = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_ROW_ORDER")) row_order = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_ROW_ORDER_MIN_ROWS")) row_order_min_rows = std::strtoull(v, nullptr, 10);
+    if (const char *v = std::getenv("HBROCM_ROW_ORDER_EVERY")) row_order_every = std::strtoull(v, nullptr, 10);
     if (const char *v = std::getenv("HBROCM_BATCH_WALK")) batch_walk = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_BIN_ROWS_IN_REGISTERS")) bin_rows_in_registers = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_DEVICE_GROW")) device_grow = std::strtol(v, nullptr, 10) != 0;
@@ -485,8 +488,146 @@ void Engine::set_labels(const float *labels, const float *weights, uint64_t n) {
 
 void Engine::read_margins(float *out, uint64_t n) {
     if (n > margins_.size()) fail(kInvalid, "read_margins: longer than the margins");
+    if (permuted_ && n) {  // back to the original order on the way out
+        DBuf<float> tmp(margins_.size());
+        GatherArgs g{};
+        g.index = perm_inv_.get();
+        g.src32 = margins_.get();
+        g.dst32 = tmp.get();
+        g.n = n_rows_;
+        g.k = outputs_ ? outputs_ : 1u;
+        dev_.launch("hbr_gather_f32", dim3((uint32_t)std::min<uint64_t>(ceil_div(n_rows_ * g.k, 256), 65535)),
+                    dim3(256), g);
+        tmp.download(out, n, dev_.stream());
+        dev_.sync();
+        return;
+    }
     margins_.download(out, n, dev_.stream());
     dev_.sync();
+}
+
+// Every row-indexed array to the order `index` gives (position i takes
+// row index[i]): gathered into the spare buffers, which then swap with the
+// live ones, so that nothing is freed and nothing waits.
+void Engine::gather_rows(const uint32_t *index) {
+    const uint32_t grid = (uint32_t)std::min<uint64_t>(ceil_div(n_rows_, 256), 65535);
+    GatherArgs g{};
+    g.index = index;
+    g.n = n_rows_;
+    Spare &sp = spare_;
+    sp.rows.resize(rows8_.size());
+    g.src8 = rows8_.get();
+    g.dst8 = sp.rows.get();
+    g.row_bytes = stride_;
+    dev_.launch("hbr_gather_records", dim3(grid), dim3(256), g);
+    if (cols8_.size()) {  // rebuilt from the gathered rows, which hold every bin
+        sp.cols.resize(cols8_.size());
+        GatherArgs c = g;
+        c.src8 = sp.rows.get();
+        c.dst8 = sp.cols.get();
+        c.n_cols = n_cols_;
+        dev_.launch("hbr_columns_from_rows", dim3(grid), dim3(256), c);
+    }
+    auto f32 = [&](const float *src, float *dst, uint32_t k) {
+        GatherArgs h = g;
+        h.src32 = src;
+        h.dst32 = dst;
+        h.k = k;
+        dev_.launch("hbr_gather_f32", dim3((uint32_t)std::min<uint64_t>(ceil_div(n_rows_ * k, 256), 65535)),
+                    dim3(256), h);
+    };
+    // the staged pair array, when it holds the live pairs (two f32 a row)
+    const bool pairs_live = !active_pairs_ && !class_outputs_ && !pair_array_stale_ && gpair_.size() >= n_rows_;
+    if (pairs_live) {
+        sp.pairs.resize(gpair_.size());
+        f32(reinterpret_cast<const float *>(gpair_.get()), reinterpret_cast<float *>(sp.pairs.get()), 2u);
+        std::swap(gpair_, sp.pairs);
+    }
+    auto move = [&](DBuf<float> &live, DBuf<float> &spare, uint32_t k) {
+        if (!live.size()) return;
+        spare.resize(live.size());
+        f32(live.get(), spare.get(), k);
+        std::swap(live, spare);
+    };
+    move(margins_, sp.margins, outputs_ ? outputs_ : 1u);
+    move(labels_, sp.labels, 1u);
+    if (has_weights_) move(weights_, sp.weights, 1u);
+    std::swap(rows8_, sp.rows);
+    if (cols8_.size()) std::swap(cols8_, sp.cols);
+    // the rows carry their pair words with them; the rows a walk deferred
+    // are listed by their old positions, so the next root sums every row
+    root_partials_ = 0;
+    grains_known_ = false;
+}
+
+// The rows by the leaves of the last queued device tree (rows of one leaf
+// keep no particular order). Rows already reordered are reordered again
+// from where they are, the two orders composed.
+void Engine::order_rows_by_tree() {
+    if (!dense_ || !dense_u8_ || masked_ || stride_ != 32 || n_cols_ == 0 || n_cols_ > 32 || missing_.size() ||
+        cols16_.size() || rows16_.size() || class_outputs_ || n_rows_ < row_order_min_rows ||
+        n_rows_ >= (1ull << 32) || last_depth_ > 9 || (2ull << last_depth_) - 1 > kOrderMaxNodes || outputs_ != 1)
+        return;
+    hipStream_t s = dev_.stream();
+    Spare &sp = spare_;
+    sp.leaf.resize(n_rows_);
+    sp.order.resize(n_rows_);
+    sp.count.resize(kOrderMaxNodes);
+    sp.cursor.resize(kOrderMaxNodes);
+    if (!permuted_) {
+        perm_inv_.resize(n_rows_);
+        group_stamp_.resize(n_rows_ / 8 + 1);
+        bad_groups_.resize(n_rows_ / 8 + 2);
+        group_stamp_.zero(s);
+        bad_groups_.zero(s);
+        regroup_stamp_ = 0;
+    }
+    sp.count.zero(s);
+    OrderArgs o{};
+    o.w.tree = ring_nodes(last_ring_, 0, last_stride_);
+    o.w.counts = &ring_header(last_ring_, 0, last_stride_)->counts;
+    o.w.bins8 = rows8_.get();
+    o.w.stride = stride_;
+    o.w.n = (uint32_t)n_rows_;
+    o.leaf = sp.leaf.get();
+    o.count = sp.count.get();
+    o.cursor = sp.cursor.get();
+    o.perm = sp.order.get();  // new position -> present position
+    const uint32_t grid = std::min<uint32_t>(ceil_div(n_rows_, 256), (uint32_t)dev_.cu_count() * 8);
+    dev_.launch("hbr_order_leaves", dim3(grid), dim3(256), o);
+    dev_.launch("hbr_order_scan", dim3(1), dim3(1024), o);
+    dev_.launch("hbr_order_place", dim3(grid), dim3(256), o);
+    gather_rows(sp.order.get());
+    if (permuted_) {  // new position -> original row: perm_[order[i]]
+        GatherArgs c{};
+        c.index = sp.order.get();
+        c.n = n_rows_;
+        c.src32 = reinterpret_cast<const float *>(perm_.get());
+        c.dst32 = reinterpret_cast<float *>(sp.leaf.get());  // the leaves are spent
+        c.k = 1;
+        dev_.launch("hbr_gather_f32", dim3((uint32_t)std::min<uint64_t>(ceil_div(n_rows_, 256), 65535)), dim3(256), c);
+        std::swap(perm_, sp.leaf);
+    } else {
+        std::swap(perm_, sp.order);
+    }
+    GatherArgs inv{};
+    inv.index = perm_.get();
+    inv.dst8 = reinterpret_cast<uint8_t *>(perm_inv_.get());
+    inv.n = n_rows_;
+    dev_.launch("hbr_order_invert", dim3(ceil_div(n_rows_, 256)), dim3(256), inv);
+    permuted_ = true;
+}
+
+void Engine::restore_row_order() {
+    if (!permuted_) return;
+    gather_rows(perm_inv_.get());
+    dev_.sync();
+    permuted_ = false;
+    perm_.release();
+    perm_inv_.release();
+    group_stamp_.release();
+    bad_groups_.release();
+    spare_ = Spare{};
 }
 
 void Engine::read_gradients(float *out, uint64_t n) {
@@ -624,6 +765,7 @@ GradArgs Engine::grad_args(const hbr_device_loss &loss) {
 
 void Engine::launch_gradients(const hbr_device_loss &loss, uint32_t output) {
     if (!labels_loaded_) fail(kInvalid, "gradients: no labels since load_margins");
+    restore_row_order();  // the gradient kernel's 8-row vectors are consecutive rows
     if (outputs_ != 1 || output != 0) fail(kRefused, "device gradients run for one output");
     hipStream_t s = dev_.stream();
     grains_known_ = false;
@@ -697,6 +839,7 @@ void Engine::softmax_gradients_async(float min_hess) {
     const uint32_t k = outputs_;
     if (k < 1 || k > kSoftmaxMaxClasses) fail(kRefused, "softmax gradients: 1 to 1024 classes");
     if (n_rows_ == 0) fail(kInvalid, "softmax gradients: no rows");
+    restore_row_order();  // the vector batches are consecutive rows
     hipStream_t s = dev_.stream();
     row_pairs_live_ = false;
     root_partials_ = 0;  // the staged pairs are no longer the walk's
@@ -1535,6 +1678,7 @@ void Engine::launch_device_roots(uint32_t n_trees) {
         f.n_walk_tiles = fused;
         f.n_cols = n_cols_;
         f.min_hess = row_pairs_min_hess_;
+        f.regroup_tile = root_regroup_tile_;
         dev_.launch("hbr_root_fixup", dim3(1), dim3(1024), f);
         ReduceArgs r{};
         r.nodes = hn;
@@ -1860,9 +2004,21 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     // bounds fix the exponents, and one 1024-thread workgroup per CU
     const uint32_t root_tiles = std::min<uint32_t>((uint32_t)dev_.cu_count(), ceil_div(n_rows_, 1024));
     root_partials_ = 0;
+    root_regroup_tile_ = 0;
     pair_array_stale_ = false;
+    if (permuted_) {  // the original 8-row vectors through the marks and hbr_regroup
+        wg.g.perm = perm_.get();
+        wg.g.group_stamp = group_stamp_.get();
+        wg.g.bad_groups = bad_groups_.get();
+        if (++regroup_stamp_ == 0) {  // every mark of 2^32 passes ago cleared
+            group_stamp_.zero(s);
+            regroup_stamp_ = 1;
+        }
+        wg.g.stamp = regroup_stamp_;
+    }
+    RegroupArgs rg{};
     if (fused_root && row_pairs_live_ && f.bound_g_bits && n_cols_ <= kRootFeatures && root_tiles >= 2) {
-        d_partial_.reserve((size_t)(root_tiles + 1) * kRootTile);
+        d_partial_.reserve((size_t)(root_tiles + 2) * kRootTile);
         wg.root_partial = d_partial_.get();
         wg.root_exp_g = exp_for(f.bound_g_bits, n_rows_);
         wg.root_exp_h = exp_for(f.bound_h_bits, n_rows_);
@@ -1871,8 +2027,20 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
         dev_.launch("hbr_walk_grad_root", dim3(root_tiles), dim3(1024), wg);
         root_partials_ = root_tiles;
         pair_array_stale_ = true;
+        rg.root_partial = wg.root_partial;
+        rg.root_exp_g = wg.root_exp_g;
+        rg.root_exp_h = wg.root_exp_h;
+        rg.n_walk_tiles = root_tiles;
+        rg.n_cols = n_cols_;
+        rg.bins8 = rows8_.get();
+        root_regroup_tile_ = permuted_ ? 1u : 0u;
     } else {
         dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
+    }
+    if (permuted_) {
+        rg.g = wg.g;
+        rg.perm_inv = perm_inv_.get();
+        dev_.launch("hbr_regroup", dim3(1), dim3(1024), rg);
     }
     dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
     scale_checked_ = false;  // the next tree's finish checks the scale

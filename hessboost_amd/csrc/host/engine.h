@@ -140,6 +140,15 @@ public:
     // gradient that is not finite
     bool softmax_all_finite();
     void read_margins(float *out, uint64_t n);
+    // Rows reordered by the leaves of the last queued device tree (32-byte
+    // rows of a dense index, trees of at most kOrderMaxNodes nodes): the
+    // rows, columns, margins, labels and weights move to their new
+    // positions; read_margins still returns the original order. The
+    // whole-round trainer reorders once; every other caller restores the
+    // original order first (restore_row_order, a no-op when nothing moved).
+    void order_rows_by_tree();
+    void restore_row_order();
+    bool rows_permuted() const { return permuted_; }
     void read_gradients(float *out, uint64_t n);
     const QScale &scale() const { return scale_host_; }
     // Whether every sum of at most m staged pairs, in any order, is the
@@ -436,6 +445,23 @@ private:
     GPair *pairs() const { return active_pairs_ ? active_pairs_ : gpair_.get(); }
     bool pairs_staged() const { return active_pairs_ || (gpair_.size() >= n_rows_ && gpair_.get()); }
     DBuf<float> margins_, labels_, weights_;
+    // the reorder: position -> original row, and its inverse; the marks of
+    // the original 8-row vectors a fused walk found outside the vector
+    // range (GradArgs::perm)
+    bool permuted_ = false;
+    DBuf<uint32_t> perm_, perm_inv_, group_stamp_, bad_groups_;
+    uint32_t regroup_stamp_ = 0;
+    uint32_t root_regroup_tile_ = 0;  // the fused root's partials include hbr_regroup's
+    // what a reorder gathers into, swapped with the live arrays (nothing is
+    // freed while kernels may still read it), and the reorder's scratch
+    struct Spare {
+        DBuf<uint8_t> rows, cols;
+        DBuf<float> margins, labels, weights;
+        DBuf<GPair> pairs;
+        DBuf<uint32_t> leaf, order, count, cursor;
+    };
+    Spare spare_;
+    void gather_rows(const uint32_t *index);
     struct EvalSet {
         DBuf<float> x, margins;
         uint64_t n_rows = 0;
@@ -553,6 +579,9 @@ public:
     bool fused_root = true;      // the margin walk also sums the next root's histogram (row pairs)
     bool masked_rows = true;     // dense u8 rows with a missing mask for matrices with missing values
     bool wide_rows = true;       // dense u16 rows for the histograms of features of more than 256 bins
+    bool row_order = true;       // the whole-round trainer reorders 32-byte rows by its first tree's leaves
+    uint64_t row_order_min_rows = 1u << 16;  // ... of at least this many rows
+    uint64_t row_order_every = 0;            // ... and again every this many rounds (0: once)
     bool batch_walk = true;  // a softmax round's class trees added to the margins in one walk
     bool bin_rows_in_registers = true;  // device binning of <= 32 features: rows into registers, else staged in LDS
     bool device_grow = true;     // depthwise trees decided on the device where eligible

@@ -565,6 +565,15 @@ void Trainer::boost_pipelined(uint64_t rounds, const hbr_device_loss &loss, bool
         while (queued < rounds && inflight.size() < 3) {
             if (!grads_ready_) e_.compute_gradients_async(loss, 0);
             inflight.push_back(b.queue_device());
+            // before the first tree's walk (and every row_order_every trees
+            // after): the rows by that tree's leaves, so that later trees'
+            // deep nodes sit together in memory
+            if (fused && e_.row_order &&
+                (!e_.rows_permuted() || (e_.row_order_every && since_order_ >= e_.row_order_every))) {
+                e_.order_rows_by_tree();
+                since_order_ = 0;
+            }
+            since_order_++;
             if (fused)
                 e_.walk_device_tree(0, &loss);
             else

@@ -142,6 +142,7 @@ private:
     // next_loss, the next round's gradients in the same pass)
     void grow_and_add(TreeBuilder &b, uint32_t output, const hbr_device_loss *next_loss = nullptr);
     bool grads_ready_ = false;  // the device holds the next round's gradients
+    uint64_t since_order_ = 0;  // trees since the engine last reordered the rows
 
     Engine &e_;
     TrainParams p_;

@@ -88,17 +88,40 @@ __device__ __forceinline__ uint32_t pair_word(float p, float y) {
     return __float_as_uint(p) | (y == 1.0f ? 0x80000000u : 0u);
 }
 
+// The vector path's pair (simd/x86_64.rs:53-160, one lane): p from the
+// polynomial exponential of -|m|, w scaled for a label of exactly 1.
+__device__ __forceinline__ GPair logistic_vector_pair(const GradArgs &a, float m, float y, float w, float *p_out) {
+    const float e = exp_vector(0.0f - __builtin_fabsf(m));
+    const float den = 1.0f + e;
+    const float pos = 1.0f / den;
+    const float neg = e / den;
+    const float p = m >= 0.0f ? pos : neg;
+    const float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
+    const float q = p * (1.0f - p);
+    *p_out = p;
+    return GPair{(p - y) * ww, (q > a.min_hess ? q : a.min_hess) * ww};
+}
+
+// A row of the vector range whose margin fails the vector test marks its
+// original 8-row vector for hbr_regroup (rows held reordered).
+__device__ __forceinline__ void mark_group(const GradArgs &a, uint32_t orig) {
+    const uint32_t g = orig >> 3;
+    if (atomicExch(&a.group_stamp[g], a.stamp) != a.stamp) a.bad_groups[1u + atomicAdd(&a.bad_groups[0], 1u)] = g;
+}
+
 // Row i's gradient pair from margin m, label y and weight w (all lanes of
 // the wave call it together: the logistic vector test is a ballot over
-// 8-row groups). kDefer: a row outside the vector path is listed for
-// hbr_finish_scale instead (keeping the f64 expf out of a hot loop).
-// *word: the row's pair word (pair_word) when its logistic pair is computed
-// here (left alone for a deferred row). *pair (when given): the row's pair,
-// set for an active row whose pair is computed here.
+// 8-row groups). orig: the row's original index (i unless the rows are
+// held reordered, GradArgs::perm; the test is then the row's own, and
+// hbr_regroup finishes it). kDefer: a row outside the vector path is
+// listed for hbr_finish_scale instead (keeping the f64 expf out of a hot
+// loop). *word: the row's pair word (pair_word) when its logistic pair is
+// computed here (left alone for a deferred row). *pair (when given): the
+// row's pair, set for an active row whose pair is computed here.
 template <bool kDefer>
-__device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, bool active, float m, float y, float w,
-                                                uint32_t &mg, uint32_t &mh, uint32_t &bad, uint32_t *word,
-                                                GPair *pair = nullptr) {
+__device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, uint32_t orig, bool active, float m,
+                                                float y, float w, uint32_t &mg, uint32_t &mh, uint32_t &bad,
+                                                uint32_t *word, GPair *pair = nullptr) {
     {
         float g = 0.0f, h = 0.0f;
         if (a.loss == kSquaredError) {
@@ -107,19 +130,21 @@ __device__ __forceinline__ void row_gradient_yw(const GradArgs &a, uint32_t i, b
             h = w;
         } else {
             bool ok = active && __builtin_fabsf(m) <= a.max_input;
-            uint64_t ballot = __ballot(ok || !active);
-            uint64_t group = 0xffull << (lane_id() & ~7u);
-            bool vector = active && i < a.vec_rows && (ballot & group) == group;
+            bool vector;
+            if (a.perm) {
+                const bool in_range = orig < a.vec_rows;
+                vector = ok && in_range;
+                if (active && !ok && in_range) mark_group(a, orig);
+            } else {
+                uint64_t ballot = __ballot(ok || !active);
+                uint64_t group = 0xffull << (lane_id() & ~7u);
+                vector = active && i < a.vec_rows && (ballot & group) == group;
+            }
             if (vector) {
-                float e = exp_vector(0.0f - __builtin_fabsf(m));
-                float den = 1.0f + e;
-                float pos = 1.0f / den;
-                float neg = e / den;
-                float p = m >= 0.0f ? pos : neg;
-                float ww = w * (y == 1.0f ? a.scale_pos_weight : 1.0f);
-                g = (p - y) * ww;
-                float q = p * (1.0f - p);
-                h = (q > a.min_hess ? q : a.min_hess) * ww;
+                float p;
+                const GPair q = logistic_vector_pair(a, m, y, w, &p);
+                g = q.g;
+                h = q.h;
                 *word = pair_word(p, y);
             } else if (active) {
                 if (kDefer) {
@@ -148,7 +173,7 @@ __device__ __forceinline__ void row_gradient(const GradArgs &a, uint32_t i, bool
     const float y = active ? a.labels[i] : 0.0f;
     const float w = (active && a.weights) ? a.weights[i] : 1.0f;
     uint32_t word = 0;
-    row_gradient_yw<false>(a, i, active, m, y, w, mg, mh, bad, &word);
+    row_gradient_yw<false>(a, i, i, active, m, y, w, mg, mh, bad, &word);
     if (a.pair_rows && active)  // uniform flag; one word in the row's padding
         *reinterpret_cast<uint32_t *>(a.pair_rows + (size_t)i * a.pair_stride + a.pair_byte) = word;
 }

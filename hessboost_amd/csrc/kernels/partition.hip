@@ -519,7 +519,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
     const uint32_t end = (a.n + kWave - 1) / kWave * kWave;
     const uint32_t stride = gridDim.x * blockDim.x;
     for (uint32_t r0 = blockIdx.x * blockDim.x + threadIdx.x; r0 < end; r0 += kWalkRows * stride) {
-        uint32_t w[kWalkRows][8];
+        uint32_t w[kWalkRows][8], orig[kWalkRows];
         float m[kWalkRows], y[kWalkRows], wt[kWalkRows];
 #pragma unroll
         for (uint32_t k = 0; k < kWalkRows; k++) {
@@ -527,11 +527,13 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
             m[k] = 0.0f;
             y[k] = 0.0f;
             wt[k] = 1.0f;
+            orig[k] = r;
             if (r < a.n) {
                 load_row_bins(a, r, w[k]);
                 m[k] = a.margins[(size_t)r * a.m_stride + a.output];
                 y[k] = ga.labels[r];
                 if (ga.weights) wt[k] = ga.weights[r];
+                if (ga.perm) orig[k] = ga.perm[r];
             }
         }
 #pragma unroll
@@ -547,7 +549,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
             }
             if (r < end) {
                 uint32_t word = w[k][7];  // a deferred row's word is written by hbr_finish_scale
-                row_gradient_yw<true>(ga, r, active, m[k], y[k], wt[k], mg, mh, bad, &word);
+                row_gradient_yw<true>(ga, r, orig[k], active, m[k], y[k], wt[k], mg, mh, bad, &word);
                 if (ga.pair_rows && active) {  // the whole 32-byte row back, its pair in the last word
                     uint4 *dst = reinterpret_cast<uint4 *>(ga.pair_rows + (size_t)r * 32u);
                     dst[0] = make_uint4(w[k][0], w[k][1], w[k][2], w[k][3]);
@@ -589,17 +591,19 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradAr
     const uint32_t end = (a.n + kWave - 1) / kWave * kWave;
     const uint32_t stride = gridDim.x * blockDim.x;
     for (uint32_t r0 = blockIdx.x * blockDim.x + threadIdx.x; r0 < end; r0 += kRootWalkRows * stride) {
-        uint32_t w[kRootWalkRows][8];
+        uint32_t w[kRootWalkRows][8], orig[kRootWalkRows];
         float m[kRootWalkRows], y[kRootWalkRows];
 #pragma unroll
         for (uint32_t k = 0; k < kRootWalkRows; k++) {
             const uint32_t r = r0 + k * stride;
             m[k] = 0.0f;
             y[k] = 0.0f;
+            orig[k] = r;
             if (r < a.n) {
                 load_row_bins(a, r, w[k]);
                 m[k] = a.margins[(size_t)r * a.m_stride + a.output];
                 y[k] = ga.labels[r];
+                if (ga.perm) orig[k] = ga.perm[r];
             }
         }
 #pragma unroll
@@ -619,7 +623,7 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradAr
             // p stays NaN unless the row's pair is computed here (a deferred
             // row's is hbr_finish_scale's; a non-finite pair fails the tree)
             GPair p{__builtin_nanf(""), 0.0f};
-            row_gradient_yw<true>(ga, r, active, m[k], y[k], 1.0f, mg, mh, bad, &word, &p);
+            row_gradient_yw<true>(ga, r, orig[k], active, m[k], y[k], 1.0f, mg, mh, bad, &word, &p);
             const bool summed = active && p.g == p.g;
             if (active) {  // the whole 32-byte row back, its pair in the last word
                 uint4 *dst = reinterpret_cast<uint4 *>(ga.pair_rows + (size_t)r * 32u);
@@ -686,9 +690,56 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_root_fixup(RootFixupArgs 
     }
     if (threadIdx.x == 0) {
         a.node->tile_begin = 0;
-        a.node->n_tiles = a.n_walk_tiles + 1u;
+        a.node->n_tiles = a.n_walk_tiles + 1u + a.regroup_tile;
         a.node->pad[0] = 0;
         a.node->pad[1] = 0;
+    }
+}
+
+// One workgroup after a fused walk over reordered rows, before
+// hbr_finish_scale: each marked original vector's rows that took the vector
+// path on their own margins (|m| within the range) join the scalar list,
+// and, for hbr_walk_grad_root, their summed vector pairs come back out of
+// the root histogram through partial n_walk_tiles + 1 (hbr_root_fixup
+// then sums their scalar pairs in).
+extern "C" __global__ __launch_bounds__(1024) void hbr_regroup(RegroupArgs a) {
+    __shared__ unsigned long long lg[kRootTile], lh[kRootTile];
+    const GradArgs &ga = a.g;
+    if (a.root_partial) {
+        for (uint32_t i = threadIdx.x; i < kRootTile; i += blockDim.x) {
+            lg[i] = 0ull;
+            lh[i] = 0ull;
+        }
+        __syncthreads();
+    }
+    const uint32_t groups = ga.bad_groups[0];
+    for (uint32_t j = threadIdx.x; j < 8u * groups; j += blockDim.x) {
+        const uint32_t orig = 8u * ga.bad_groups[1u + j / 8u] + (j & 7u);
+        const uint32_t r = a.perm_inv[orig];
+        const float m = ga.margins[r];
+        if (orig >= ga.vec_rows || !(__builtin_fabsf(m) <= ga.max_input)) continue;  // already a scalar row
+        ga.scalar_list[atomicAdd(&ga.scale->scalar_rows, 1u)] = r;
+        if (!a.root_partial) continue;
+        float p;
+        const GPair q = logistic_vector_pair(ga, m, ga.labels[r], 1.0f, &p);
+        const unsigned long long qg = (unsigned long long)(-quantize(q.g, a.root_exp_g));
+        const unsigned long long qh = (unsigned long long)(-quantize(q.h, a.root_exp_h));
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.bins8 + (size_t)r * 32u);
+        const uint4 x = src[0], z = src[1];
+        const uint32_t w[8] = {x.x, x.y, x.z, x.w, z.x, z.y, z.z, z.w};
+        for (uint32_t f = 0; f < a.n_cols && f < kMaskedMaxFeatures; f++) {  // word 7 is the pair
+            const uint32_t bin = (w[f >> 2] >> ((f & 3u) * 8u)) & 0xffu;
+            atomicAdd(&lg[bin * kRootFeatures + f], qg);
+            atomicAdd(&lh[bin * kRootFeatures + f], qh);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) ga.bad_groups[0] = 0u;
+    if (!a.root_partial) return;
+    QBin *dst = a.root_partial + (size_t)(a.n_walk_tiles + 1u) * kRootTile;
+    for (uint32_t i = threadIdx.x; i < kRootTile; i += blockDim.x) {
+        const uint32_t ff = i % kRootFeatures, bin = i / kRootFeatures;
+        if (ff < a.n_cols) dst[ff * 256u + bin] = QBin{(int64_t)lg[i], (int64_t)lh[i]};
     }
 }
 
@@ -714,5 +765,102 @@ extern "C" __global__ __launch_bounds__(256) void hbr_rows_from_cols(RowsFromCol
                 v |= (uint32_t)a.cols8[(uint64_t)(4 * w + j) * a.n_rows + r] << (8 * j);
         }
         dst[w] = v;
+    }
+}
+
+// ---- rows reordered by a tree's leaves ------------------------------------------
+//
+// The whole-round trainer reorders the rows once, by the leaves of its
+// first tree: later trees split on much the same features, so the rows of
+// one of their deep nodes then share cache lines, and the gathers of the
+// histogram and of the partition's routing bytes fetch far fewer lines.
+// Every sum is an integer sum, so the trees do not depend on the order.
+
+// Each row's leaf in the tree (staged walk of its 32-byte row), and each
+// leaf's row count: a workgroup's counts in LDS, then one global add per
+// leaf it saw. The host checks that the tree's nodes fit kOrderMaxNodes.
+extern "C" __global__ __launch_bounds__(256) void hbr_order_leaves(OrderArgs a) {
+    __shared__ uint2 s_node[kWalkLdsNodes];
+    __shared__ float s_value[kWalkLdsNodes];
+    __shared__ uint32_t s_count[kOrderMaxNodes];
+    const uint32_t n_nodes = load_walk_nodes(a.w, s_node, s_value);
+    for (uint32_t i = threadIdx.x; i < kOrderMaxNodes; i += blockDim.x) s_count[i] = 0u;
+    __syncthreads();
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.w.n; r += gridDim.x * blockDim.x) {
+        uint32_t w[8];
+        load_row_bins(a.w, r, w);
+        const int32_t leaf = walk_row(s_node, n_nodes, w);
+        const uint32_t l = leaf >= 0 && (uint32_t)leaf < kOrderMaxNodes ? (uint32_t)leaf : 0u;
+        a.leaf[r] = l;
+        atomicAdd(&s_count[l], 1u);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < kOrderMaxNodes; i += blockDim.x)
+        if (s_count[i]) atomicAdd(&a.count[i], s_count[i]);
+}
+
+// One workgroup: each leaf's first position (exclusive scan of the counts).
+extern "C" __global__ __launch_bounds__(1024) void hbr_order_scan(OrderArgs a) {
+    static_assert(kOrderMaxNodes == 1024, "one count per thread");
+    uint32_t total;
+    const uint32_t v = a.count[threadIdx.x];
+    a.cursor[threadIdx.x] = block_exclusive_scan<1024>(v, &total);
+}
+
+// Each row's position: a workgroup counts its rows per leaf again (the
+// same rows as in hbr_order_leaves' grid-stride loop of the same launch
+// shape), takes a run of positions from each leaf's cursor with one
+// atomic per leaf, and hands them out to its rows through LDS atomics.
+extern "C" __global__ __launch_bounds__(256) void hbr_order_place(OrderArgs a) {
+    __shared__ uint32_t s_count[kOrderMaxNodes];
+    for (uint32_t i = threadIdx.x; i < kOrderMaxNodes; i += blockDim.x) s_count[i] = 0u;
+    __syncthreads();
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.w.n; r += gridDim.x * blockDim.x)
+        atomicAdd(&s_count[a.leaf[r]], 1u);
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < kOrderMaxNodes; i += blockDim.x)
+        s_count[i] = s_count[i] ? atomicAdd(&a.cursor[i], s_count[i]) : 0u;
+    __syncthreads();
+    for (uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < a.w.n; r += gridDim.x * blockDim.x)
+        a.perm[atomicAdd(&s_count[a.leaf[r]], 1u)] = r;
+}
+
+// inverse[perm[i]] = i
+extern "C" __global__ __launch_bounds__(256) void hbr_order_invert(GatherArgs a) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < a.n) reinterpret_cast<uint32_t *>(a.dst8)[a.index[i]] = (uint32_t)i;
+}
+
+// dst record i = src record index[i] (row_bytes each, 16 bytes at a time)
+extern "C" __global__ __launch_bounds__(256) void hbr_gather_records(GatherArgs a) {
+    const uint32_t words = a.row_bytes / 16u;
+    const uint64_t total = a.n * words;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t i = t / words;
+        const uint32_t q = (uint32_t)(t % words);
+        reinterpret_cast<uint4 *>(a.dst8)[t] =
+            reinterpret_cast<const uint4 *>(a.src8)[(uint64_t)a.index[i] * words + q];
+    }
+}
+
+// The columns of 32-byte rows (bins in bytes 0..n_cols-1): dst column f,
+// row i = byte f of src record i (the rows already in their new order).
+extern "C" __global__ __launch_bounds__(256) void hbr_columns_from_rows(GatherArgs a) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.src8 + i * 32u);
+        const uint4 x = src[0], z = src[1];
+        const uint32_t w[8] = {x.x, x.y, x.z, x.w, z.x, z.y, z.z, z.w};
+        for (uint32_t f = 0; f < a.n_cols && f < 32u; f++)
+            a.dst8[(uint64_t)f * a.n + i] = (uint8_t)(w[f >> 2] >> ((f & 3u) * 8u));
+    }
+}
+
+// dst row i = src row index[i] (k f32 values a row)
+extern "C" __global__ __launch_bounds__(256) void hbr_gather_f32(GatherArgs a) {
+    const uint64_t total = a.n * a.k;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t i = t / a.k;
+        const uint32_t c = (uint32_t)(t % a.k);
+        a.dst32[t] = a.src32[(uint64_t)a.index[i] * a.k + c];
     }
 }

@@ -457,6 +457,73 @@ def test_row_carried_logistic_pairs_give_identical_trees(far_rows):
         assert np.all(np.abs(ma[far]) > 80)
 
 
+def _engine_with_env(index, env):
+    import os
+    saved = {k: os.environ.pop(k, None) for k in env}
+    os.environ.update(env)
+    try:
+        return hb.Engine(index, 0)
+    finally:
+        for k, v in saved.items():
+            os.environ.pop(k, None)
+            if v is not None:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("case", ["fused_root", "weights", "no_fused_root", "every_round"])
+def test_rows_reordered_by_a_tree_give_identical_trees(case):
+    """The whole-round trainer holds the rows in the order of its first
+    tree's leaves (every later sum is an integer sum), while the logistic
+    8-row vectors stay those of the original rows: a row beyond the vector
+    range (|m| > 80) sends the other rows of its original vector to the
+    scalar sigmoid (hbr_regroup, which also takes their vector pairs back
+    out of the fused root histogram), and the tail of n % 8 rows stays
+    scalar. The trees and margins equal, bit for bit, those of the run
+    without the reorder; between two boosts, a call of the engine's own puts
+    the rows back in their order and the next boost reorders them again
+    (every_round: reordered again by each tree, the orders composed)."""
+    rng = np.random.default_rng(29)
+    n, f = 50_003, 20
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    x[:, 3] = np.round(x[:, 3])
+    y = (x[:, 0] + 0.5 * x[:, 3] * x[:, 1] + 0.3 * rng.standard_normal(n) > 0).astype(np.float32)
+    w = rng.uniform(0.5, 2.0, n).astype(np.float32) if case == "weights" else None
+    m0 = np.zeros(n, np.float32)
+    far = rng.choice(n, 300, replace=False)
+    m0[far] = np.where(rng.random(300) < 0.5, -100.0, 100.0).astype(np.float32)
+    params = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3}
+    index = hb.DMatrix(x, label=y).index(256)
+    extra = {"HBROCM_FUSED_ROOT": "0"} if case == "no_fused_root" else {}
+    every = {"HBROCM_ROW_ORDER_EVERY": "1"} if case == "every_round" else {}
+    runs = []
+    for env in ({"HBROCM_ROW_ORDER_MIN_ROWS": "1", **every}, {"HBROCM_ROW_ORDER": "0"}):
+        eng = _engine_with_env(index, {**env, **extra})
+        tr = hb.Trainer(eng, params, y, w)
+        eng.load_margins(m0)
+        eng.gradients(LOSS_LOGISTIC, y, w)
+        eng.set_profiling(True, "hbr_")
+        tr.boost(2)
+        mid = tr.margins()
+        back = eng.read_margins(n)  # the engine's own call: the rows in their order again
+        tr.boost(2)
+        stats = eng.kernel_stats()
+        eng.set_profiling(False)
+        count = lambda k: stats[k][2] if k in stats else 0
+        runs.append((tr.trees(), tr.margins(), mid, back, count("hbr_regroup"), count("hbr_walk_grad_root"),
+                     count("hbr_order_place")))
+    (ta, ma, mida, backa, ra, fa, oa), (tb, mb, midb, backb, rb, fb, ob) = runs
+    assert ra == 4 and rb == 0, (ra, rb)
+    assert oa == (4 if case == "every_round" else 2) and ob == 0, (oa, ob)
+    assert fa == fb == (0 if case in ("weights", "no_fused_root") else 4), (fa, fb)
+    assert len(ta) == len(tb) == 4
+    for a, b in zip(ta, tb):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    for u, v in ((ma, mb), (mida, midb), (backa, backb), (mida, backa)):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+    assert np.all(np.abs(ma[far]) > 80)
+
+
 @pytest.mark.parametrize("objective,device_grow", [("binary:logistic", "1"), ("reg:squarederror", "1"),
                                                    ("binary:logistic", "0")])
 def test_missing_values_on_masked_dense_rows_match_oracle_and_csr_path(objective, device_grow):
