@@ -364,12 +364,15 @@ def main():
         log("ms per round by kernel: " + ", ".join(f"{k} {v}" for k, v in breakdown.items()))
     # the margin walk that also sums the next root's histogram: its
     # algorithmic bytes per row (the 32-byte row read and written back with
-    # its pair word, the margin read and written, the label), its two 64-bit
-    # LDS adds per (row, feature column), over its time per round
+    # its pair word, the margin read and written, the label, and the row's
+    # original index when the trainer holds the rows in a tree's leaf
+    # order), its two 64-bit LDS adds per (row, feature column), over its
+    # time per round
     walk_root = None
     if breakdown.get("hbr_walk_grad_root"):
         wms = breakdown["hbr_walk_grad_root"]
-        wbytes = x.shape[0] * (32 + 32 + 4 + 4 + 4)
+        reordered = eng.counters()["row_orders"] > 0
+        wbytes = x.shape[0] * (32 + 32 + 4 + 4 + 4 + (4 if reordered else 0))
         wach = wbytes / (wms * 1e-3) / 1e9
         watom = x.shape[0] * 32 * 2 / (wms * 1e-3) / 1e12
         wtraffic, _, wtraffic_src = measured_traffic("hbr_walk_grad_root")

@@ -95,7 +95,7 @@ class NodeScan(C.Structure):
 class EngineCounters(C.Structure):
     _fields_ = [("hist_nodes", C.c_uint64), ("hist_rows", C.c_uint64), ("hist_bytes", C.c_uint64),
                 ("partition_rows", C.c_uint64), ("trees", C.c_uint64), ("near_ties", C.c_uint64),
-                ("near_ties_resolved", C.c_uint64)]
+                ("near_ties_resolved", C.c_uint64), ("row_orders", C.c_uint64)]
 
 
 class TrainParams(C.Structure):

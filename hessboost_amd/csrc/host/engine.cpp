@@ -616,6 +616,7 @@ void Engine::order_rows_by_tree() {
     inv.n = n_rows_;
     dev_.launch("hbr_order_invert", dim3(ceil_div(n_rows_, 256)), dim3(256), inv);
     permuted_ = true;
+    counters.row_orders++;
 }
 
 void Engine::restore_row_order() {

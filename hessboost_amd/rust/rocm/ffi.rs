@@ -200,6 +200,7 @@ pub struct hbr_engine_counters {
     pub trees: u64,
     pub near_ties: u64,
     pub near_ties_resolved: u64,
+    pub row_orders: u64,
 }
 
 #[repr(C)]

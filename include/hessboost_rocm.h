@@ -474,6 +474,7 @@ typedef struct hbr_engine_counters {
     uint64_t near_ties;        /* decided nodes whose winner the fixed-point guard could not
                                   certify (see hbr_engine_set_guard) */
     uint64_t near_ties_resolved; /* of those, searched again on the CPU builder's sums on the device */
+    uint64_t row_orders;       /* times the whole-round trainer put the rows in a tree's leaf order */
 } hbr_engine_counters;
 int hbr_engine_counters_read(hbr_engine *e, hbr_engine_counters *out);
 

@@ -509,6 +509,7 @@ def test_rows_reordered_by_a_tree_give_identical_trees(case):
         stats = eng.kernel_stats()
         eng.set_profiling(False)
         count = lambda k: stats[k][2] if k in stats else 0
+        assert eng.counters()["row_orders"] == count("hbr_order_place")
         runs.append((tr.trees(), tr.margins(), mid, back, count("hbr_regroup"), count("hbr_walk_grad_root"),
                      count("hbr_order_place")))
     (ta, ma, mida, backa, ra, fa, oa), (tb, mb, midb, backb, rb, fb, ob) = runs
