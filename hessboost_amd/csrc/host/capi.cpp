@@ -403,14 +403,22 @@ int hbr_build(hbr_engine *h, const uint32_t *rows, uint64_t m, double *out) {
 }
 
 int hbr_build_device_noalloc(hbr_engine *h, const uint32_t *rows, uint64_t m, double *out) {
-    return with_engine(h, [&](Engine &e) {
-        if (!out || (!rows && m)) fail(kInvalid, "build: null argument");
-        require_exact(e, m, "build");
-        const auto held = fixed_scratch_lock(e.dev().ordinal());
-        uint64_t bytes = 0;
-        uint8_t *scratch = fixed_scratch(e.dev().ordinal(), &bytes);
-        if (!e.build_rows_fixed(rows, m, out, scratch, bytes)) fail(kInvalid, "build: a row beyond the index");
-    });
+    // the rows stay where they are: putting a trainer's reordered rows back
+    // would allocate and free
+    return with_engine(
+        h,
+        [&](Engine &e) {
+            if (!out || (!rows && m)) fail(kInvalid, "build: null argument");
+            if (e.rows_permuted())
+                fail(kRefused, "build (no allocation): a trainer holds the rows in a tree's leaf order; any other "
+                               "engine call puts them back");
+            require_exact(e, m, "build");
+            const auto held = fixed_scratch_lock(e.dev().ordinal());
+            uint64_t bytes = 0;
+            uint8_t *scratch = fixed_scratch(e.dev().ordinal(), &bytes);
+            if (!e.build_rows_fixed(rows, m, out, scratch, bytes)) fail(kInvalid, "build: a row beyond the index");
+        },
+        true);
 }
 
 int hbr_begin_tree(hbr_engine *h, uint64_t n_rows, hbr_segment *root) {

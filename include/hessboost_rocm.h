@@ -209,7 +209,9 @@ int hbr_build(hbr_engine *e, const uint32_t *rows, uint64_t m, double *out);
  * on one GPU shares that GPU's scratch and holds a per-GPU lock for its
  * whole duration, so calls from several threads (two engines on one GPU)
  * run one after another. HBR_REFUSED when the last gradient pass left the
- * pairs in the rows only and the index's kernel cannot read them there. */
+ * pairs in the rows only and the index's kernel cannot read them there, and
+ * while a trainer holds the engine's rows in a tree's leaf order (any other
+ * engine call puts them back, which may allocate). */
 int hbr_build_device_noalloc(hbr_engine *e, const uint32_t *rows, uint64_t m, double *out);
 
 /* A node's rows on the device (the reference's Segment, src/tree/hist/mod.rs:107-164):

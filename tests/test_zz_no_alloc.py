@@ -100,7 +100,9 @@ def test_noalloc_build_after_device_rounds_reads_the_row_carried_pairs():
     """After device-resident logistic rounds the next pairs ride in the
     rows' last word (the pair array holds an earlier round's): the no-alloc
     build reads them there, as hbr_build does, and both equal the oracle's
-    histogram of the pairs recomputed from the trainer's margins."""
+    histogram of the pairs recomputed from the trainer's margins. While the
+    trainer holds the rows in its first tree's leaf order the no-alloc build
+    refuses (putting them back would allocate); hbr_build puts them back."""
     from hessboost_amd import synthetic
     from oracle import oracle as O
 
@@ -109,6 +111,9 @@ def test_noalloc_build_after_device_rounds_reads_the_row_carried_pairs():
     t = hb.Trainer(e, {"objective": "binary:logistic", "max_depth": 6, "eta": 0.1}, y)
     t.boost(3)
     e.set_sums("fixed_point")
+    assert e.counters()["row_orders"] == 1
+    st, _, msg = noalloc_build(e, np.arange(0, len(y), 3, dtype=np.uint32))
+    assert st == A.REFUSED and "leaf order" in msg, msg
     gpair = O.gradient(O.OBJ_LOGISTIC, t.margins(), y)
     ds = O.Dataset(x, max_bin=256)
     rng = np.random.default_rng(6)
