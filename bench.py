@@ -556,11 +556,17 @@ def main():
         pstats = forest.kernel_stats()
         forest.set_profiling(False)
         mrows = n * args.predict_steps / (t1 - t0) / 1e6
-        # from host rows: the same walk with the 4 GB of rows copied in first (PCIe)
-        forest.predict_margin(xp[:1024])
-        t = time.perf_counter()
-        forest.predict_margin(xp)
-        t_host = time.perf_counter() - t
+        # from host rows: the same walk with the 4 GB of rows copied in by the
+        # call (PCIe), in chunks through pinned staging buffers that the
+        # warmup call (over two chunks' worth of rows) allocates; the median
+        # of three calls
+        forest.predict_margin(xp[:min(n, 700_000)])
+        host_times = []
+        for _ in range(3):
+            t = time.perf_counter()
+            forest.predict_margin(xp)
+            host_times.append(time.perf_counter() - t)
+        t_host = sorted(host_times)[1]
         log(f"predict from host rows: {n / t_host / 1e6:.1f} Mrows/s ({t_host:.3f} s with the copy)")
         pkern = sorted(k for k in pstats if k.startswith("hbr_predict"))
         pms = sum(pstats[k][0] for k in pkern)
@@ -581,7 +587,9 @@ def main():
             "metric": "batch predict Mrows/s", "value": round(mrows, 2), "unit": "Mrows/s",
             "steps": args.predict_steps,
             "from_host_rows": {"value": round(n / t_host / 1e6, 2), "unit": "Mrows/s", "s": round(t_host, 4),
-                               "note": "rows in host memory, copied to HBM by the call (the resident rate is value)"},
+                               "note": "rows in host memory, copied to HBM by the call in chunks through pinned "
+                                       "staging buffers, overlapped with the walk; median of 3 calls (the resident "
+                                       "rate is value)"},
             "config": {"workload": f"{args.predict_trees}-tree depth-8 forest, {n:,} x {f} f32 rows, 2% NaN"},
             "roofline": {"kernel": "/".join(pkern) or "hbr_predict", "bound": "texture path",
                          "achieved": round(loads / launch_s, 1) if pms else 0.0, "peak": TEXTURE_PEAK_LOADS,

@@ -995,13 +995,8 @@ int hbr_predict_margin_from(hbr_forest *h, const float *x, uint64_t n, uint64_t 
                             const float *init_margins, float *out) {
     return with_forest(h, [&](Forest &f) {
         if (n == 0) return;
-        const uint64_t k = f.n_outputs();
-        DBuf<float> dx(n * n_cols), dout(n * k), dinit(init_margins ? n * k : 0);
-        dx.upload(x, n * n_cols, f.dev().stream());
-        if (init_margins) dinit.upload(init_margins, n * k, f.dev().stream());
-        f.predict_device(dx.get(), n, n_cols, missing, dout.get(), nullptr, init_margins ? dinit.get() : nullptr);
-        dout.download(out, n * k, f.dev().stream());
-        f.dev().sync();
+        if (!x || !out) fail(kInvalid, "predict: null argument");
+        f.predict_host(x, n, n_cols, missing, out, init_margins);
     });
 }
 

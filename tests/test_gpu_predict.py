@@ -236,6 +236,45 @@ def test_rows_start_from_their_own_margins_in_every_walk():
                 os.environ.pop("HBROCM_PRED_KERNEL", None)
 
 
+def test_host_rows_in_chunks_equal_device_rows():
+    """Rows in host memory beyond two 128 MiB chunks go to the device in
+    chunks (copied by the host's threads into two pinned staging buffers,
+    then by a copy stream, while the walk runs on the chunks already there):
+    the margins equal, bit for bit, those of the same rows already on the
+    device and those of slices small enough for one plain copy, across the
+    chunk boundaries, with and without starting margins, for one and three
+    outputs (a row of 37 features: 906,816 rows a chunk, the last ragged)."""
+    trees = synthetic.forest(n_trees=24, depth=8, n_features=37, seed=31)
+    n = 2_000_003
+    x = synthetic.predict_rows(n=n, f=37, seed=32)
+    arrs = O.forest_arrays(trees)
+    f = hb.Forest(arrs, 1)
+    got = f.predict_margin(x)
+    dx = hb.DeviceBuffer(x.nbytes)
+    dx.upload(x)
+    dout = hb.DeviceBuffer(4 * n)
+    f.predict_margin_device(dx.ptr, n, 37, dout.ptr)
+    assert np.array_equal(got.view(np.uint32), dout.download(np.float32, n).view(np.uint32))
+    del dx, dout
+    chunk = (128 << 20) // (37 * 4) // 64 * 64
+    rng = np.random.default_rng(33)
+    for k in (1, 3):
+        multi = dict(arrs)
+        multi["tree_output"] = (np.arange(len(trees)) % k).astype(np.uint32)
+        multi["n_outputs"] = k
+        multi["base_score"] = np.linspace(-0.5, 0.5, k).astype(np.float32)
+        fk = hb.Forest(multi, k)
+        init = rng.standard_normal((n, k)).astype(np.float32)
+        whole = fk.predict_margin(x, init_margins=init).reshape(n, k)
+        plain = fk.predict_margin(x).reshape(n, k)
+        for a in (0, chunk - 1000, 2 * chunk - 1, n - 3000):
+            b = min(n, a + 3000)
+            part = fk.predict_margin(x[a:b], init_margins=init[a:b]).reshape(-1, k)
+            assert np.array_equal(part.view(np.uint32), whole[a:b].view(np.uint32)), (k, a)
+            part = fk.predict_margin(x[a:b]).reshape(-1, k)
+            assert np.array_equal(part.view(np.uint32), plain[a:b].view(np.uint32)), (k, a)
+
+
 def test_device_resident_prediction():
     trees = synthetic.forest(n_trees=20, depth=6, n_features=30, seed=9)
     x = synthetic.predict_rows(n=5_000, f=30, seed=10)
