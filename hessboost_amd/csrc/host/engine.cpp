@@ -323,18 +323,14 @@ void Engine::bin_dense(const DenseSource &src) {
     cols8_.resize(n_rows_ * n_cols_);
     missing_.resize((uint64_t)words_ * n_cols_);
     DBuf<uint32_t> count(n_rows_);
-    // chunks of whole 64-row groups; host rows go through a staging buffer
+    // chunks of whole 64-row groups; host rows beyond two chunks go through
+    // the device's pinned staging (Device::host_rows: the binning of a chunk
+    // runs while the next is staged and copied), fewer through one copy
     const uint64_t row_bytes = n_cols_ * sizeof(float);
-    uint64_t chunk = std::max<uint64_t>(64, ((256ull << 20) / row_bytes) / 64 * 64);
+    constexpr uint64_t kChunkBytes = 128ull << 20;
+    uint64_t chunk = std::max<uint64_t>(64, (kChunkBytes / row_bytes) / 64 * 64);
     if (src.on_device) chunk = std::min<uint64_t>(n_rows_, (uint64_t)UINT32_MAX / 2) / 64 * 64 + 64;
-    DBuf<float> staging(src.on_device ? 0 : std::min<uint64_t>(chunk, n_rows_) * n_cols_);
-    for (uint64_t r0 = 0; r0 < n_rows_; r0 += chunk) {
-        const uint64_t rows = std::min<uint64_t>(chunk, n_rows_ - r0);
-        const float *xs = src.x + r0 * n_cols_;
-        if (!src.on_device) {
-            HBR_HIP(hipMemcpyAsync(staging.get(), xs, rows * row_bytes, hipMemcpyHostToDevice, s));
-            xs = staging.get();
-        }
+    auto bin_chunk = [&](const float *xs, uint64_t r0, uint64_t rows) {
         BinArgs a{};
         a.x = xs;
         a.cut_values = d_cuts.get();
@@ -361,7 +357,17 @@ void Engine::bin_dense(const DenseSource &src) {
                         (uint32_t)((4 * 64 * n_cols_ + total_bins_) * sizeof(float)));
         else
             dev_.launch("hbr_bin_dense", dim3(ceil_div(rows, 256)), dim3(256), a);
-        if (!src.on_device) dev_.sync();  // the staging buffer is reused
+    };
+    if (!src.on_device && n_rows_ * row_bytes >= 2 * kChunkBytes) {
+        dev_.host_rows(src.x, n_rows_, n_cols_, chunk, bin_chunk);
+    } else if (!src.on_device) {
+        DBuf<float> staging(n_rows_ * n_cols_);
+        staging.upload(src.x, n_rows_ * n_cols_, s);
+        bin_chunk(staging.get(), 0, n_rows_);
+        dev_.sync();
+    } else {
+        for (uint64_t r0 = 0; r0 < n_rows_; r0 += chunk)
+            bin_chunk(src.x + r0 * n_cols_, r0, std::min<uint64_t>(chunk, n_rows_ - r0));
     }
     // the present counts: totals per block, their offsets on the host, row_ptr
     const uint32_t blocks = ceil_div(n_rows_, kCountBlock);

@@ -389,39 +389,6 @@ void Forest::predict_device(const float *x, uint64_t n, uint64_t n_cols, float m
     dev_.launch("hbr_predict", dim3((uint32_t)((n + 255) / 256)), dim3(256), a);
 }
 
-Forest::~Forest() {
-    try {
-        dev_.activate();
-        if (pipe_.copy) {
-            (void)hipStreamSynchronize(pipe_.copy);
-            dev_.sync();
-            for (int s = 0; s < 2; s++) {
-                (void)hipEventDestroy(pipe_.copied[s]);
-                (void)hipEventDestroy(pipe_.used[s]);
-            }
-            (void)hipStreamDestroy(pipe_.copy);
-        }
-    } catch (...) {
-    }
-}
-
-namespace {
-
-// Pageable host bytes into pinned memory with the host's threads (one
-// thread's memcpy reaches a fraction of the link's rate).
-void copy_threads(void *dst, const void *src, uint64_t bytes) {
-    constexpr uint64_t kPiece = 4ull << 20;
-    const int64_t pieces = (int64_t)((bytes + kPiece - 1) / kPiece);
-#pragma omp parallel for schedule(static)
-    for (int64_t i = 0; i < pieces; i++) {
-        const uint64_t off = (uint64_t)i * kPiece;
-        std::memcpy(static_cast<char *>(dst) + off, static_cast<const char *>(src) + off,
-                    std::min<uint64_t>(kPiece, bytes - off));
-    }
-}
-
-}  // namespace
-
 void Forest::predict_host(const float *x, uint64_t n, uint64_t n_cols, float missing, float *out,
                           const float *init) {
     if (n == 0) return;
@@ -441,38 +408,12 @@ void Forest::predict_host(const float *x, uint64_t n, uint64_t n_cols, float mis
         return;
     }
     const uint64_t chunk_rows = std::max<uint64_t>(64, kChunkBytes / row_bytes / 64 * 64);
-    HostPipe &p = pipe_;
-    if (!p.copy) {
-        HBR_HIP(hipStreamCreateWithFlags(&p.copy, hipStreamNonBlocking));
-        for (int i = 0; i < 2; i++) {
-            HBR_HIP(hipEventCreateWithFlags(&p.copied[i], hipEventDisableTiming));
-            HBR_HIP(hipEventCreateWithFlags(&p.used[i], hipEventDisableTiming));
-        }
-    }
-    const uint64_t chunk_bytes = chunk_rows * row_bytes;
-    for (int i = 0; i < 2; i++) {
-        p.stage[i].reserve(chunk_bytes);
-        p.rows[i].reserve(chunk_rows * n_cols);
-    }
-    const uint64_t chunks = (n + chunk_rows - 1) / chunk_rows;
-    for (uint64_t c = 0; c < chunks; c++) {
-        const int b = (int)(c & 1u);
-        const uint64_t r0 = c * chunk_rows, rows = std::min(chunk_rows, n - r0);
-        // the copy two chunks back has read this staging buffer, and the
-        // walk two chunks back has read this device chunk
-        if (c >= 2) HBR_HIP(hipEventSynchronize(p.copied[b]));
-        copy_threads(p.stage[b].get(), x + r0 * n_cols, rows * row_bytes);
-        if (c >= 2) HBR_HIP(hipStreamWaitEvent(p.copy, p.used[b], 0));
-        HBR_HIP(hipMemcpyAsync(p.rows[b].get(), p.stage[b].get(), rows * row_bytes, hipMemcpyHostToDevice, p.copy));
-        HBR_HIP(hipEventRecord(p.copied[b], p.copy));
-        HBR_HIP(hipStreamWaitEvent(s, p.copied[b], 0));
-        predict_device(p.rows[b].get(), rows, n_cols, missing, dout.get() + r0 * k, nullptr,
+    dev_.host_rows(x, n, n_cols, chunk_rows, [&](const float *rows_dev, uint64_t r0, uint64_t rows) {
+        predict_device(rows_dev, rows, n_cols, missing, dout.get() + r0 * k, nullptr,
                        init ? dinit.get() + r0 * k : nullptr);
-        HBR_HIP(hipEventRecord(p.used[b], s));
-    }
+    });
     dout.download(out, n * k, s);
     dev_.sync();
-    HBR_HIP(hipStreamSynchronize(p.copy));
 }
 
 // Consecutive whole trees per chunk, as many as `cap` nodes hold (at most

@@ -19,15 +19,13 @@ public:
     Device &dev() { return dev_; }
     uint32_t n_outputs() const { return n_outputs_; }
     uint64_t n_trees() const { return n_trees_; }
-    ~Forest();
     // x, out, leaf_out, init: device pointers; init (n x n_outputs starting
     // margins) may be null: the base scores.
     void predict_device(const float *x, uint64_t n, uint64_t n_cols, float missing, float *out, int32_t *leaf_out,
                         const float *init = nullptr);
-    // The same with x, init and out in host memory (pageable): the rows go
-    // to the device in chunks, each copied by the host's threads into one of
-    // two pinned staging buffers and from there by a copy stream, while the
-    // walk runs on the chunks already on the device.
+    // The same with x, init and out in host memory (pageable): beyond two
+    // chunks of rows, through Device::host_rows (the walk runs on each chunk
+    // while the next is staged and copied).
     void predict_host(const float *x, uint64_t n, uint64_t n_cols, float missing, float *out, const float *init);
 
 private:
@@ -69,15 +67,6 @@ private:
     DBuf<uint32_t> pair_values_;
     DBuf<int32_t> pair_orig_;
     void build_pairs(const hbr_forest_desc &fd);
-    // predict_host's two staging buffers, their device chunks, the copy
-    // stream and its events (made on the first call that needs them)
-    struct HostPipe {
-        PinnedBuf stage[2];
-        DBuf<float> rows[2];
-        hipStream_t copy = nullptr;
-        hipEvent_t copied[2] = {nullptr, nullptr};  // a chunk's copy has read its staging buffer
-        hipEvent_t used[2] = {nullptr, nullptr};    // the walk has read a device chunk
-    } pipe_;
 };
 
 }  // namespace hbr

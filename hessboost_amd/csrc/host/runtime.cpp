@@ -9,6 +9,7 @@ extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalW
                                                hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
 
 #include <dlfcn.h>
+#include <algorithm>
 #include <cstdlib>
 
 #include <memory>
@@ -62,6 +63,16 @@ Device::Device(int ordinal) : ordinal_(ordinal) {
 
 Device::~Device() {
     if (stream_) (void)hipStreamSynchronize(stream_);
+    if (pipe_copy_) {
+        (void)hipStreamSynchronize(pipe_copy_);
+        for (int b = 0; b < 2; b++) {
+            (void)hipEventDestroy(pipe_copied_[b]);
+            (void)hipEventDestroy(pipe_used_[b]);
+            if (pipe_stage_[b]) (void)hipHostFree(pipe_stage_[b]);
+            if (pipe_rows_[b]) (void)hipFree(pipe_rows_[b]);
+        }
+        (void)hipStreamDestroy(pipe_copy_);
+    }
     for (auto &p : pending_) {
         (void)hipEventDestroy(p.start);
         (void)hipEventDestroy(p.stop);
@@ -162,6 +173,68 @@ std::unordered_map<std::string, Device::KernelStat> Device::kernel_stats() {
 void Device::reset_stats() {
     sync();
     stats_.clear();
+}
+
+// Pageable host bytes into pinned memory with the host's threads (one
+// thread's memcpy reaches a fraction of the link's rate).
+static void copy_threads(void *dst, const void *src, uint64_t bytes) {
+    constexpr uint64_t kPiece = 4ull << 20;
+    const int64_t pieces = (int64_t)((bytes + kPiece - 1) / kPiece);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < pieces; i++) {
+        const uint64_t off = (uint64_t)i * kPiece;
+        std::memcpy(static_cast<char *>(dst) + off, static_cast<const char *>(src) + off,
+                    std::min<uint64_t>(kPiece, bytes - off));
+    }
+}
+
+void Device::host_rows(const float *x, uint64_t n, uint64_t n_cols, uint64_t chunk_rows,
+                       const std::function<void(const float *, uint64_t, uint64_t)> &fn) {
+    if (n == 0) return;
+    if (chunk_rows == 0 || chunk_rows % 64) fail(kInvalid, "host rows: chunks of a multiple of 64 rows");
+    std::lock_guard<std::mutex> lock(pipe_mu_);
+    const uint64_t row_bytes = n_cols * sizeof(float);
+    const uint64_t bytes = std::min(chunk_rows, n) * row_bytes;
+    if (!pipe_copy_) {
+        HBR_HIP(hipStreamCreateWithFlags(&pipe_copy_, hipStreamNonBlocking));
+        for (int b = 0; b < 2; b++) {
+            HBR_HIP(hipEventCreateWithFlags(&pipe_copied_[b], hipEventDisableTiming));
+            HBR_HIP(hipEventCreateWithFlags(&pipe_used_[b], hipEventDisableTiming));
+        }
+    }
+    if (bytes > pipe_bytes_) {  // nothing in flight uses the old buffers (the last call waited for its copies)
+        sync();
+        for (int b = 0; b < 2; b++) {
+            if (pipe_stage_[b]) (void)hipHostFree(pipe_stage_[b]);
+            if (pipe_rows_[b]) (void)hipFree(pipe_rows_[b]);
+            pipe_stage_[b] = nullptr;
+            pipe_rows_[b] = nullptr;
+        }
+        pipe_bytes_ = 0;
+        for (int b = 0; b < 2; b++) {
+            HBR_HIP(hipHostMalloc(&pipe_stage_[b], bytes, hipHostMallocDefault));
+            HBR_HIP(hipMalloc((void **)&pipe_rows_[b], bytes));
+        }
+        pipe_bytes_ = bytes;
+    }
+    const uint64_t chunks = (n + chunk_rows - 1) / chunk_rows;
+    for (uint64_t c = 0; c < chunks; c++) {
+        const int b = (int)(c & 1u);
+        const uint64_t r0 = c * chunk_rows, rows = std::min(chunk_rows, n - r0);
+        // the copy two chunks back has read this staging buffer, and the
+        // work last queued on this device buffer has read it
+        if (c >= 2) HBR_HIP(hipEventSynchronize(pipe_copied_[b]));
+        copy_threads(pipe_stage_[b], x + r0 * n_cols, rows * row_bytes);
+        // (an earlier call's last chunks count: their work may still run)
+        if (pipe_used_set_[b]) HBR_HIP(hipStreamWaitEvent(pipe_copy_, pipe_used_[b], 0));
+        HBR_HIP(hipMemcpyAsync(pipe_rows_[b], pipe_stage_[b], rows * row_bytes, hipMemcpyHostToDevice, pipe_copy_));
+        HBR_HIP(hipEventRecord(pipe_copied_[b], pipe_copy_));
+        HBR_HIP(hipStreamWaitEvent(stream_, pipe_copied_[b], 0));
+        fn(pipe_rows_[b], r0, rows);
+        HBR_HIP(hipEventRecord(pipe_used_[b], stream_));
+        pipe_used_set_[b] = true;
+    }
+    HBR_HIP(hipStreamSynchronize(pipe_copy_));
 }
 
 static std::mutex g_devices_mu;

@@ -10,6 +10,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -62,6 +63,17 @@ public:
     std::unordered_map<std::string, KernelStat> kernel_stats();
     void reset_stats();
 
+    // Rows in host memory to the device in chunks of at most chunk_rows rows
+    // (a multiple of 64): the host's threads copy a chunk from the caller's
+    // pageable memory into one of two pinned staging buffers, a copy stream
+    // moves it into one of two device buffers, and fn(device rows, first
+    // row, rows) queues the chunk's work on stream() while the next chunk is
+    // staged; events order each buffer's reuse. Returns once the last chunk
+    // is copied (the queued work may still run). The buffers are the
+    // device's, kept until the process ends; one caller at a time.
+    void host_rows(const float *x, uint64_t n, uint64_t n_cols, uint64_t chunk_rows,
+                   const std::function<void(const float *, uint64_t, uint64_t)> &fn);
+
 private:
     void launch_raw(const char *kernel, dim3 grid, dim3 block, const void *args, uint32_t lds_bytes);
     hipFunction_t function(const char *kernel);
@@ -83,6 +95,15 @@ private:
     std::vector<hipEvent_t> event_pool_;
     hipEvent_t take_event();
     std::unordered_map<std::string, KernelStat> stats_;
+    // host_rows' staging
+    std::mutex pipe_mu_;
+    hipStream_t pipe_copy_ = nullptr;
+    hipEvent_t pipe_copied_[2] = {nullptr, nullptr};  // a chunk's copy has read its staging buffer
+    hipEvent_t pipe_used_[2] = {nullptr, nullptr};    // the queued work has read a device buffer
+    void *pipe_stage_[2] = {nullptr, nullptr};
+    float *pipe_rows_[2] = {nullptr, nullptr};
+    bool pipe_used_set_[2] = {false, false};
+    uint64_t pipe_bytes_ = 0;
 };
 
 // The process's Device for an ordinal (created on first use).

@@ -106,6 +106,26 @@ def test_rows_already_on_the_device():
     _same(host, dev)
 
 
+@pytest.mark.parametrize("f,n", [(28, 2_400_017), (45, 1_600_003)])
+def test_host_rows_in_chunks_bin_as_rows_on_the_device(f, n):
+    """Host rows beyond two 128 MiB chunks are binned chunk by chunk as they
+    arrive through the device's pinned staging buffers (the last chunk
+    ragged): every layout equals, byte for byte, the index binned from the
+    same rows already on the device, with missing cells (masked rows of 32
+    and of 64 bytes)."""
+    rng = np.random.default_rng(26 + f)
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    x[rng.random((n, f)) < 0.02] = np.nan
+    x[:, 3] = np.round(x[:, 3])
+    cuts = hb.DMatrix(x[:200_000]).cuts(256)
+    host_rows = hb.Engine.from_dense(x, cuts, 0).read_index()
+    buf = hb.DeviceBuffer(x.nbytes)
+    buf.upload(x)
+    dev_rows = hb.Engine.from_dense(buf, cuts, 0, n_rows=n, n_cols=f).read_index()
+    assert host_rows["dense_u8"] == 1
+    _same(dev_rows, host_rows)
+
+
 def test_features_wider_than_256_bins_are_refused():
     rng = np.random.default_rng(25)
     x = rng.standard_normal((5_000, 3)).astype(np.float32)
