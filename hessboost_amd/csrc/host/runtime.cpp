@@ -202,6 +202,9 @@ void Device::host_rows(const float *x, uint64_t n, uint64_t n_cols, uint64_t chu
             HBR_HIP(hipEventCreateWithFlags(&pipe_used_[b], hipEventDisableTiming));
         }
     }
+    // a call that ended early (its work refused) may have left a copy
+    // reading a staging buffer
+    HBR_HIP(hipStreamSynchronize(pipe_copy_));
     if (bytes > pipe_bytes_) {  // nothing in flight uses the old buffers (the last call waited for its copies)
         sync();
         for (int b = 0; b < 2; b++) {
