@@ -372,14 +372,18 @@ def main():
     # order), its two 64-bit LDS adds per (row, feature column), over its
     # time per round
     walk_root = None
-    if breakdown.get("hbr_walk_grad_root"):
-        wms = breakdown["hbr_walk_grad_root"]
+    walk_kernel = next((k for k in breakdown if k.startswith("hbr_walk_grad_root")), None)
+    if walk_kernel and breakdown[walk_kernel]:
+        wms = breakdown[walk_kernel]
         reordered = eng.counters()["row_orders"] > 0
         wbytes = x.shape[0] * (32 + 32 + 4 + 4 + 4 + (4 if reordered else 0))
         wach = wbytes / (wms * 1e-3) / 1e9
-        watom = x.shape[0] * 32 * 2 / (wms * 1e-3) / 1e12
-        wtraffic, _, wtraffic_src = measured_traffic("hbr_walk_grad_root")
-        walk_root = {"kernel": "hbr_walk_grad_root", "bound": "hbm", "achieved": round(wach, 1),
+        # 64-bit LDS adds per row: two per feature column the kernel sums
+        # (28 for rows of 25-28 features, else all 32 of the row's bytes)
+        wcols = 28 if walk_kernel.endswith("_nf28") else 32
+        watom = x.shape[0] * wcols * 2 / (wms * 1e-3) / 1e12
+        wtraffic, _, wtraffic_src = measured_traffic(walk_kernel)
+        walk_root = {"kernel": walk_kernel, "bound": "hbm", "achieved": round(wach, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(wach / HBM_PEAK_GBS, 4),
                      "avg_launch_ms": round(wms, 4), "algorithmic_bytes_per_launch": wbytes,
                      "traffic": wtraffic, "traffic_source": wtraffic_src,

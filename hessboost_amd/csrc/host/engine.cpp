@@ -65,6 +65,7 @@ void Engine::read_tunables() {
         if (t == 512 || t == 1024) hist_threads = (uint32_t)t;
     }
     if (const char *v = std::getenv("HBROCM_HIST_BIN_MAJOR")) hist_bin_major = std::strtol(v, nullptr, 10) != 0;
+    if (const char *v = std::getenv("HBROCM_HIST_NF28")) hist_nf28 = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_ROW_PAIRS")) row_pairs = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_FUSED_ROOT")) fused_root = std::strtol(v, nullptr, 10) != 0;
     if (const char *v = std::getenv("HBROCM_MASKED_ROWS")) masked_rows = std::strtol(v, nullptr, 10) != 0;
@@ -1197,6 +1198,19 @@ uint64_t Engine::hist_bytes(uint64_t rows, bool gathered) const {
     return rows * (bins + pair + (gathered ? 4 : 0));
 }
 
+// The dense u8 histogram kernel for groups of fg features: one group of 25
+// to 28 features (compact masked rows included) takes the instance whose
+// lanes rotate over those features alone.
+const char *Engine::dense8_kernel(uint32_t fg) const {
+    const bool bm = hist_bin_major && fg >= 16;
+    const bool nf28 = hist_nf28 && bm && fg == 32 && n_cols_ > 24 && n_cols_ <= 28 && (!masked_ || mask_at_ == 28);
+    if (masked_) return nf28 ? "hbr_hist_dense8_fg32_bm_masked_nf28" : "hbr_hist_dense8_fg32_bm_masked";
+    if (fg <= 8) return "hbr_hist_dense8_fg8";
+    if (fg <= 16) return bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16";
+    if (!bm) return "hbr_hist_dense8_fg32";
+    return nf28 ? "hbr_hist_dense8_fg32_bm_nf28" : "hbr_hist_dense8_fg32_bm";
+}
+
 void Engine::set_scan_params(const ScanParams &p, const std::vector<int8_t> &monotone) {
     scan_params_ = p;
     const bool same = has_monotone_ && monotone == monotone_host_;
@@ -1283,13 +1297,7 @@ void Engine::launch_hist(const HistNode *nodes_dev, uint32_t n, const std::vecto
     a.stride16 = stride16_;
     static const char *const wide_kernels[] = {"hbr_hist_dense16_fg1", "hbr_hist_dense16_fg2", "hbr_hist_dense16_fg4",
                                                "hbr_hist_dense16_fg8", "hbr_hist_dense16_fg16"};
-    const bool bm = hist_bin_major && fg >= 16;
-    const char *k = wide        ? wide_kernels[__builtin_ctz(fg)]
-                    : !dense_u8_ ? "hbr_hist_csr"
-                    : masked_    ? "hbr_hist_dense8_fg32_bm_masked"
-                    : fg <= 8    ? "hbr_hist_dense8_fg8"
-                    : fg <= 16   ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
-                                 : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");
+    const char *k = wide ? wide_kernels[__builtin_ctz(fg)] : !dense_u8_ ? "hbr_hist_csr" : dense8_kernel(fg);
     dev_.launch(k, dim3((target + n) * groups), dim3(dense ? hist_threads : kCsrThreads), a);
     if (!dense) {
         ReduceArgs r{};
@@ -2031,7 +2039,9 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
         wg.root_exp_h = exp_for(f.bound_h_bits, n_rows_);
         wg.n_cols = n_cols_;
         wg.g.gpair = nullptr;  // the rows carry every pair; the finish writes its deferred rows' both ways
-        dev_.launch("hbr_walk_grad_root", dim3(root_tiles), dim3(1024), wg);
+        // rows of 25 to 28 features: no atomics for the padding columns
+        const bool nf28 = hist_nf28 && n_cols_ > 24 && n_cols_ <= 28;
+        dev_.launch(nf28 ? "hbr_walk_grad_root_nf28" : "hbr_walk_grad_root", dim3(root_tiles), dim3(1024), wg);
         root_partials_ = root_tiles;
         pair_array_stale_ = true;
         rg.root_partial = wg.root_partial;
@@ -2419,12 +2429,7 @@ bool Engine::build_rows_fixed(const uint32_t *rows, uint64_t m, double *out, uin
     a.masked = masked_ ? 1u : 0u;
     a.mask_at = mask_at_;
     a.min_hess = row_pairs_min_hess_;
-    const bool bm = hist_bin_major && fg >= 16;
-    const char *k = !dense_u8_ ? "hbr_hist_csr"
-                    : masked_  ? "hbr_hist_dense8_fg32_bm_masked"
-                    : fg <= 8  ? "hbr_hist_dense8_fg8"
-                    : fg <= 16 ? (bm ? "hbr_hist_dense8_fg16_bm" : "hbr_hist_dense8_fg16")
-                               : (bm ? "hbr_hist_dense8_fg32_bm" : "hbr_hist_dense8_fg32");
+    const char *k = !dense_u8_ ? "hbr_hist_csr" : dense8_kernel(fg);
     dev_.launch(k, dim3((uint32_t)(target + 1) * groups), dim3(dense_u8_ ? hist_threads : kCsrThreads), a);
     ReduceArgs r{};
     r.nodes = node;

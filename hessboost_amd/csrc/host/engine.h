@@ -338,6 +338,7 @@ private:
     void upload_index(const hbr_index_desc &desc);
     void bin_dense(const DenseSource &src);
     void read_tunables();
+    const char *dense8_kernel(uint32_t fg) const;
     uint64_t entries_ = 0;
     bool csr_ascending_ = true;  // every CSR row's global bins ascend (device binning writes them so)
     void build_csr_ranges();
@@ -575,6 +576,7 @@ public:
     uint32_t hist_threads = 1024;
     uint32_t hist_waves = 1;
     bool hist_bin_major = true;  // [bin][feature] LDS layout (16 and 32 feature groups)
+    bool hist_nf28 = true;       // 25-28 features: the lanes rotate over the features alone (no padding atomics)
     bool row_pairs = true;       // unit-weight logistic pairs carried in the rows' padding
     bool fused_root = true;      // the margin walk also sums the next root's histogram (row pairs)
     bool masked_rows = true;     // dense u8 rows with a missing mask for matrices with missing values

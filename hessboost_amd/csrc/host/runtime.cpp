@@ -9,6 +9,7 @@ extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalW
                                                hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
 
 #include <dlfcn.h>
+#include <omp.h>
 #include <algorithm>
 #include <cstdlib>
 
@@ -176,11 +177,14 @@ void Device::reset_stats() {
 }
 
 // Pageable host bytes into pinned memory with the host's threads (one
-// thread's memcpy reaches a fraction of the link's rate).
+// thread's memcpy reaches a fraction of the link's rate). The thread count
+// is the processors', whatever the process last set for its own parallel
+// regions.
 static void copy_threads(void *dst, const void *src, uint64_t bytes) {
     constexpr uint64_t kPiece = 4ull << 20;
     const int64_t pieces = (int64_t)((bytes + kPiece - 1) / kPiece);
-#pragma omp parallel for schedule(static)
+    const int threads = std::max(1, std::min(32, omp_get_num_procs()));
+#pragma omp parallel for schedule(static) num_threads(threads)
     for (int64_t i = 0; i < pieces; i++) {
         const uint64_t off = (uint64_t)i * kPiece;
         std::memcpy(static_cast<char *>(dst) + off, static_cast<const char *>(src) + off,

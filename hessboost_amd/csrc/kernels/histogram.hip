@@ -93,9 +93,16 @@ __device__ __forceinline__ void load_bins(const uint8_t *p, uint32_t (&w)[FG / 4
 // of each 16-lane group 16 different features: their atomics never share a
 // bank, whatever the bins. Otherwise [feature][257] (bins padded), where
 // the banks follow the data, and features past nf go to per-lane dummies.
-template <int FG, bool BIN_MAJOR, bool MASKED = false>
+//
+// NF < FG (bin-major only): the row's first NF bytes are its features and
+// the lanes rotate over those alone (lane l starts at feature l mod NF, still
+// 16 different features in every 16-lane group), so no atomic goes to a
+// padding column: 28 features take 56 atomics a row instead of 64.
+template <int FG, bool BIN_MAJOR, bool MASKED = false, int NF = FG>
 __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
+    static_assert(NF == FG || (BIN_MAJOR && NF % 4 == 0 && NF < FG && NF >= 16), "NF: whole words, bin-major");
     constexpr int W = FG / 4;
+    constexpr int NW = NF / 4;
     constexpr uint32_t kWords = BIN_MAJOR ? FG * 256 : FG * kLdsFeature + kWave;
     constexpr uint32_t kDummy = FG * kLdsFeature;
     __shared__ unsigned long long lg[kWords];
@@ -115,7 +122,7 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
     const GPair *gpair = a.gpair + (size_t)nd.cls * a.class_rows;
     const uint32_t *rows = a.rows[nd.seg.buf] + nd.seg.offset;
     const uint32_t lane = lane_id();
-    const uint32_t rot = lane & (FG - 1);
+    const uint32_t rot = NF == FG ? lane & (FG - 1) : lane % (uint32_t)NF;
     const uint32_t end = t.row0 + t.rows;
     const bool row_pairs = a.row_pairs != 0;  // uniform
     for (uint32_t j = t.row0 + threadIdx.x; j < end; j += blockDim.x) {
@@ -141,11 +148,15 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
             mask = a.mask_at == 4 * kMaskWord
                        ? w[kMaskWord % W]
                        : *reinterpret_cast<const uint32_t *>(a.bins8 + (size_t)r * a.stride + a.mask_at + 4 * grp);
-        rotate_bytes<W>(w, rot);
+        uint32_t v[NW];
 #pragma unroll
-        for (int f = 0; f < FG; f++) {
-            const uint32_t ff = ((uint32_t)f + rot) & (FG - 1);
-            const uint32_t bin = (w[f >> 2] >> ((f & 3) * 8)) & 0xffu;
+        for (int i = 0; i < NW; i++) v[i] = w[i];
+        rotate_bytes<NW>(v, rot);
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+            uint32_t ff = (uint32_t)f + rot;
+            ff = NF == FG ? ff & (FG - 1) : (ff >= (uint32_t)NF ? ff - (uint32_t)NF : ff);
+            const uint32_t bin = (v[f >> 2] >> ((f & 3) * 8)) & 0xffu;
             // bin-major: a feature past nf adds its (padding) byte into its
             // own column, which is never read back
             const uint32_t at = BIN_MAJOR ? bin * FG + ff : (ff < nf ? ff * kLdsFeature + bin : kDummy + lane);
@@ -467,6 +478,13 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense16_fg1(HistArgs
 // Masked rows (a missing mask in word kMaskWord): one group of 32 features.
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm_masked(HistArgs a) {
     hist_dense8<32, true, true>(a);
+}
+// Rows of 25 to 28 features (one group): no atomics for the padding columns.
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm_nf28(HistArgs a) {
+    hist_dense8<32, true, false, 28>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void hbr_hist_dense8_fg32_bm_masked_nf28(HistArgs a) {
+    hist_dense8<32, true, true, 28>(a);
 }
 extern "C" __global__ __launch_bounds__(1024) void hbr_hist_csr(HistArgs a) { hist_csr(a); }
 

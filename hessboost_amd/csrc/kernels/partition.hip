@@ -573,7 +573,10 @@ extern "C" __global__ __launch_bounds__(256) void hbr_walk_grad32(WalkGradArgs a
 // from the row's word, so the sums are the root histogram's.
 constexpr uint32_t kRootWalkRows = 4;
 
-extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradArgs args) {
+// NF < 32: the row's first NF bytes are its features (25 to 28), and the
+// lanes rotate over those alone, so no atomic goes to a padding column.
+template <uint32_t NF>
+__device__ __forceinline__ void walk_grad_root(const WalkGradArgs &args) {
     const WalkArgs &a = args.w;
     const GradArgs &ga = args.g;
     __shared__ uint2 s_node[kWalkLdsNodes];
@@ -586,7 +589,7 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradAr
     }
     const uint32_t n_nodes = load_walk_nodes(a, s_node, s_value);
     __syncthreads();
-    const uint32_t rot = lane_id() & (kRootFeatures - 1u);
+    const uint32_t rot = NF == kRootFeatures ? lane_id() & (kRootFeatures - 1u) : lane_id() % NF;
     uint32_t mg = 0, mh = 0, bad = 0;
     const uint32_t end = (a.n + kWave - 1) / kWave * kWave;
     const uint32_t stride = gridDim.x * blockDim.x;
@@ -633,11 +636,15 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradAr
             if (summed) {
                 const unsigned long long qg = (unsigned long long)quantize(p.g, args.root_exp_g);
                 const unsigned long long qh = (unsigned long long)quantize(p.h, args.root_exp_h);
-                rotate_bytes<8>(w[k], rot);
+                uint32_t v[NF / 4];
 #pragma unroll
-                for (int f = 0; f < (int)kRootFeatures; f++) {
-                    const uint32_t ff = ((uint32_t)f + rot) & (kRootFeatures - 1u);
-                    const uint32_t bin = (w[k][f >> 2] >> ((f & 3) * 8)) & 0xffu;
+                for (uint32_t i = 0; i < NF / 4; i++) v[i] = w[k][i];
+                rotate_bytes<NF / 4>(v, rot);
+#pragma unroll
+                for (int f = 0; f < (int)NF; f++) {
+                    uint32_t ff = (uint32_t)f + rot;
+                    ff = NF == kRootFeatures ? ff & (kRootFeatures - 1u) : (ff >= NF ? ff - NF : ff);
+                    const uint32_t bin = (v[f >> 2] >> ((f & 3) * 8)) & 0xffu;
                     atomicAdd(&lg[bin * kRootFeatures + ff], qg);
                     atomicAdd(&lh[bin * kRootFeatures + ff], qh);
                 }
@@ -651,6 +658,13 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradAr
         const uint32_t ff = i % kRootFeatures, bin = i / kRootFeatures;
         if (ff < args.n_cols) dst[ff * 256u + bin] = QBin{(int64_t)lg[i], (int64_t)lh[i]};
     }
+}
+
+extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root(WalkGradArgs args) {
+    walk_grad_root<kRootFeatures>(args);
+}
+extern "C" __global__ __launch_bounds__(1024) void hbr_walk_grad_root_nf28(WalkGradArgs args) {
+    walk_grad_root<28>(args);
 }
 
 // One workgroup after hbr_finish_scale: the rows the fused walk deferred
