@@ -470,6 +470,39 @@ def _engine_with_env(index, env):
                 os.environ[k] = v
 
 
+@pytest.mark.parametrize("missing", [False, True])
+def test_28_feature_instances_equal_the_32_column_ones(missing):
+    """Rows of 25 to 28 features take histogram and fused-walk instances whose
+    lanes rotate over the features alone (no atomics into padding columns):
+    the trees and margins equal those of the 32-column instances
+    (HBROCM_HIST_NF28=0) bit for bit, on dense and on masked rows, and the
+    kernel statistics show which instances ran."""
+    x, y = synthetic.higgs_like(n=70_000, seed=12)
+    if missing:
+        rng = np.random.default_rng(12)
+        x[rng.random(x.shape) < 0.02] = np.nan
+    params = {"objective": "binary:logistic", "max_depth": 7, "eta": 0.3}
+    index = hb.DMatrix(x, label=y).index(256)
+    runs = []
+    for env in ({}, {"HBROCM_HIST_NF28": "0"}):
+        eng = _engine_with_env(index, env)
+        tr = hb.Trainer(eng, params, y)
+        eng.set_profiling(True, "hbr_")
+        tr.boost(3)
+        names = set(eng.kernel_stats())
+        eng.set_profiling(False)
+        runs.append((tr.trees(), tr.margins(), names))
+    (ta, ma, na), (tb, mb, nb) = runs
+    want = "hbr_hist_dense8_fg32_bm_masked_nf28" if missing else "hbr_hist_dense8_fg32_bm_nf28"
+    assert want in na and want not in nb, (na, nb)
+    if not missing:
+        assert "hbr_walk_grad_root_nf28" in na and "hbr_walk_grad_root" in nb
+    for a, b in zip(ta, tb):
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+    assert np.array_equal(ma.view(np.uint32), mb.view(np.uint32))
+
+
 @pytest.mark.parametrize("case", ["fused_root", "weights", "no_fused_root", "every_round"])
 def test_rows_reordered_by_a_tree_give_identical_trees(case):
     """The whole-round trainer holds the rows in the order of its first
