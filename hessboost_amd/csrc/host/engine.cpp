@@ -2054,10 +2054,12 @@ void Engine::walk_device_tree(uint32_t output, const hbr_device_loss *next_loss,
     } else {
         dev_.launch("hbr_walk_grad32", dim3(blocks), dim3(256), wg);
     }
-    if (permuted_) {
+    if (permuted_ && wg.g.loss == kLogistic) {  // only the logistic loss has 8-row vectors
         rg.g = wg.g;
         rg.perm_inv = perm_inv_.get();
         dev_.launch("hbr_regroup", dim3(1), dim3(1024), rg);
+    } else {
+        root_regroup_tile_ = 0;
     }
     dev_.launch("hbr_finish_scale", dim3(1), dim3(kThreads), f);
     scale_checked_ = false;  // the next tree's finish checks the scale

@@ -582,7 +582,7 @@ public:
     bool masked_rows = true;     // dense u8 rows with a missing mask for matrices with missing values
     bool wide_rows = true;       // dense u16 rows for the histograms of features of more than 256 bins
     bool row_order = true;       // the whole-round trainer reorders 32-byte rows by its first tree's leaves
-    uint64_t row_order_min_rows = 1u << 16;  // ... of at least this many rows
+    uint64_t row_order_min_rows = 1u << 20;  // ... of at least this many rows (smaller ones stay in the caches)
     uint64_t row_order_every = 0;            // ... and again every this many rounds (0: once)
     bool batch_walk = true;  // a softmax round's class trees added to the margins in one walk
     bool bin_rows_in_registers = true;  // device binning of <= 32 features: rows into registers, else staged in LDS

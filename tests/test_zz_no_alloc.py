@@ -106,8 +106,17 @@ def test_noalloc_build_after_device_rounds_reads_the_row_carried_pairs():
     from hessboost_amd import synthetic
     from oracle import oracle as O
 
+    import os
     x, y = synthetic.higgs_like(n=200_000, seed=3)
-    e = hb.DMatrix(x, label=y).engine(256)
+    old = os.environ.get("HBROCM_ROW_ORDER_MIN_ROWS")
+    os.environ["HBROCM_ROW_ORDER_MIN_ROWS"] = "1"  # the trainer reorders rows this few
+    try:
+        e = hb.DMatrix(x, label=y).engine(256)
+    finally:
+        if old is None:
+            os.environ.pop("HBROCM_ROW_ORDER_MIN_ROWS")
+        else:
+            os.environ["HBROCM_ROW_ORDER_MIN_ROWS"] = old
     t = hb.Trainer(e, {"objective": "binary:logistic", "max_depth": 6, "eta": 0.1}, y)
     t.boost(3)
     e.set_sums("fixed_point")
