@@ -637,7 +637,9 @@ int hbr_build_resident(hbr_engine *h, const hbr_segment *segs, const uint32_t *s
         e.subtract(parents, sib);
         e.note_built(ss, built);
         e.note_siblings(parents, sib);
-        e.dev().sync();
+        // nothing comes back: the histograms stay resident for the next
+        // call on the same stream, which waits for them (a device error
+        // surfaces at the next synchronising call)
     });
 }
 
