@@ -336,7 +336,10 @@ int hbr_engine_eval_margins(hbr_engine *e, uint32_t index, float *out);
 int hbr_reserve_hists(hbr_engine *e, uint64_t slots, int *fits);
 
 /* RowEngine::build_resident: build each node's histogram into its slot,
- * then turn each (parent, built) pair's parent slot into parent - built. */
+ * then turn each (parent, built) pair's parent slot into parent - built.
+ * Returns once the work is queued (nothing comes back): the engine's later
+ * calls run after it on the same stream, and a device error surfaces at the
+ * next call that waits for the device. */
 int hbr_build_resident(hbr_engine *e, const hbr_segment *segs, const uint32_t *slots, uint64_t n,
                        const uint32_t *sibling_parent, const uint32_t *sibling_built, uint64_t n_siblings);
 
