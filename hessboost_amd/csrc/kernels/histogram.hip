@@ -325,7 +325,7 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
         const uint32_t len = i < kPlanLdsNodes ? s_len[i] : a.nodes[i].seg.len;
         c += len / c32 + (len % c32 != 0 ? 1u : 0u);
     }
-    unsigned long long pick = c <= a.target_tiles || threadIdx.x == blockDim.x - 1 ? cand : ~0ull;
+    unsigned long long pick = c <= a.target_tiles ? cand : ~0ull;
     {
         __shared__ unsigned long long lds_min[256 / kWave];
 #pragma unroll
@@ -335,7 +335,13 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
         __syncthreads();
         for (uint32_t w = 0; w < 256 / kWave; w++) pick = min(pick, lds_min[w]);
     }
-    const unsigned long long size = pick;
+    // More nodes than the target (a batch of class trees' deep levels): no
+    // size fits, so the balanced one, lo, cuts the long nodes as it would
+    // cut them alone: at most target + n_nodes tiles, and the tiles of
+    // nodes of several tiles at most 2 x target (each such node's n tiles
+    // hold more than (n - 1) x lo rows), which the launch and the partial
+    // buffer reserve.
+    const unsigned long long size = pick == ~0ull ? lo : pick;
     const uint32_t tile_rows = (uint32_t)((size + kWave - 1) / kWave * kWave);
     uint32_t carry = 0, part_carry = 0;
     for (uint32_t base = 0; base < n_nodes; base += blockDim.x) {
