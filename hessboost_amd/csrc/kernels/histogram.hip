@@ -284,7 +284,7 @@ __device__ __forceinline__ unsigned long long block_sum(unsigned long long v) {
 constexpr uint32_t kPlanLdsNodes = 4096;
 
 extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
-    __shared__ uint32_t s_len[kPlanLdsNodes];  // node lengths, for the candidate counts
+    __shared__ __align__(16) uint32_t s_len[kPlanLdsNodes];  // node lengths, for the candidate counts
     __shared__ uint32_t s_first[256], s_count[256];
     const uint32_t n_nodes = a.grow ? a.grow->n_splits : a.n_nodes;
     unsigned long long sum = 0, longest = 0;
@@ -297,6 +297,9 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
         sum += s.len;
         longest = max(longest, (unsigned long long)s.len);
     }
+    // lengths padded with zeros (no tiles) to whole groups of four
+    const uint32_t n_lds = min(n_nodes, kPlanLdsNodes), n_lds4 = (n_lds + 3u) & ~3u;
+    if (threadIdx.x < n_lds4 - n_lds) s_len[n_lds + threadIdx.x] = 0u;
     const unsigned long long total = block_sum(sum);
     {
         __shared__ unsigned long long lds_max[256 / kWave];
@@ -320,11 +323,14 @@ extern "C" __global__ __launch_bounds__(256) void hbr_hist_plan(PlanArgs a) {
                                                                                           (double)(blockDim.x - 1)));
     cand = min(max(cand, lo), hi);
     const uint32_t c32 = (uint32_t)min(cand, 0xffffffffull);  // 32-bit divisions
+    auto tiles_of = [c32](uint32_t len) { return len / c32 + (len % c32 != 0 ? 1u : 0u); };
     unsigned long long c = 0;
-    for (uint32_t i = 0; i < n_nodes; i++) {
-        const uint32_t len = i < kPlanLdsNodes ? s_len[i] : a.nodes[i].seg.len;
-        c += len / c32 + (len % c32 != 0 ? 1u : 0u);
+    // four lengths per LDS read, their divisions independent
+    for (uint32_t i = 0; i < n_lds4; i += 4) {
+        const uint4 l = *reinterpret_cast<const uint4 *>(&s_len[i]);
+        c += (unsigned long long)(tiles_of(l.x) + tiles_of(l.y)) + (tiles_of(l.z) + tiles_of(l.w));
     }
+    for (uint32_t i = kPlanLdsNodes; i < n_nodes; i++) c += tiles_of(a.nodes[i].seg.len);
     unsigned long long pick = c <= a.target_tiles ? cand : ~0ull;
     {
         __shared__ unsigned long long lds_min[256 / kWave];

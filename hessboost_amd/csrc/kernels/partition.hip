@@ -64,8 +64,10 @@ __device__ __forceinline__ bool goes_left(const PartArgs &a, const PartSplit &sp
 
 // The split owning a tile: the last split whose first tile is at or before
 // it (a split without rows shares its first tile with the next split).
-__device__ __forceinline__ uint32_t split_of_tile(const PartArgs &a, uint32_t n_splits, uint32_t tile) {
-    if (a.tile_split) return a.tile_split[tile];
+// `listed`: the tile's entry of a.tile_split, loaded by the caller.
+__device__ __forceinline__ uint32_t split_of_tile(const PartArgs &a, uint32_t n_splits, uint32_t tile,
+                                                  uint32_t listed) {
+    if (a.tile_split) return listed;
     uint32_t lo = 0, hi = n_splits;
     while (hi - lo > 1) {
         const uint32_t mid = (lo + hi) / 2;
@@ -114,8 +116,11 @@ __device__ __forceinline__ void route_dense8(const PartArgs &a, const PartSplit 
 extern "C" __global__ __launch_bounds__(256) void hbr_part_count(PartArgs a) {
     __shared__ uint32_t wave_count[kPartThreads / kWave];
     const uint32_t tile = blockIdx.x;
+    // the tile's split, loaded with the tile count (the table covers the
+    // grid), so that the two loads take one trip to memory
+    const uint32_t listed = a.tile_split ? a.tile_split[tile] : 0u;
     if (tile >= part_tiles(a)) return;
-    const PartSplit sp = a.splits[split_of_tile(a, part_splits(a), tile)];
+    const PartSplit sp = a.splits[split_of_tile(a, part_splits(a), tile, listed)];
     const uint32_t base = (tile - sp.tile_begin) * kPartTile;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
     const uint32_t id0 = sp.identity ? sp.seg.offset % a.n_rows : 0u;  // a root of a batched level
@@ -161,13 +166,26 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_part_scan(PartArgs a) {
     const PartSplit sp = a.splits[s];
     const uint32_t n_tiles = (sp.seg.len + kPartTile - 1) / kPartTile;
     uint32_t carry = 0;
-    for (uint32_t t0 = 0; t0 < n_tiles; t0 += kScanThreads) {
-        const uint32_t t = t0 + threadIdx.x;
-        const uint32_t v = t < n_tiles ? a.tile_left[sp.tile_begin + t] : 0u;
-        uint32_t total;
-        const uint32_t ex = block_exclusive_scan<kScanThreads>(v, &total);
-        if (t < n_tiles) a.tile_left[sp.tile_begin + t] = carry + ex;
-        carry += total;
+    // the counts of up to kScanAhead blocks of tiles loaded at once (one
+    // trip to memory for a split of up to 8,192 tiles), then scanned block
+    // by block
+    constexpr uint32_t kScanAhead = 8;
+    for (uint32_t t0 = 0; t0 < n_tiles; t0 += kScanThreads * kScanAhead) {
+        uint32_t v[kScanAhead];
+#pragma unroll
+        for (uint32_t k = 0; k < kScanAhead; k++) {
+            const uint32_t t = t0 + k * kScanThreads + threadIdx.x;
+            v[k] = t < n_tiles ? a.tile_left[sp.tile_begin + t] : 0u;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kScanAhead; k++) {
+            if (t0 + k * kScanThreads >= n_tiles) break;  // uniform
+            const uint32_t t = t0 + k * kScanThreads + threadIdx.x;
+            uint32_t total;
+            const uint32_t ex = block_exclusive_scan<kScanThreads>(v[k], &total);
+            if (t < n_tiles) a.tile_left[sp.tile_begin + t] = carry + ex;
+            carry += total;
+        }
     }
     if (threadIdx.x == 0) {
         PartOut o;
@@ -184,21 +202,25 @@ extern "C" __global__ __launch_bounds__(1024) void hbr_part_scan(PartArgs a) {
 // run and right rows to the right child's, both in row order.
 extern "C" __global__ __launch_bounds__(256) void hbr_part_scatter(PartArgs a) {
     const uint32_t tile = blockIdx.x;
+    const uint32_t wave = threadIdx.x / kWave, lane = lane_id();
+    // everything indexed by the tile alone is loaded with the tile count
+    // (the tables cover the grid): one trip to memory before the split's
+    const uint32_t listed = a.tile_split ? a.tile_split[tile] : 0u;
+    const uint32_t left_before = a.tile_left[tile];
+    const uint64_t *dec = a.decisions + (size_t)tile * kBallots;
+    // ballot q sits in lane q
+    const uint64_t mine = lane < kBallots ? dec[lane] : 0ull;
     if (tile >= part_tiles(a)) return;
-    const uint32_t s = split_of_tile(a, part_splits(a), tile);
+    const uint32_t s = split_of_tile(a, part_splits(a), tile, listed);
     const PartSplit sp = a.splits[s];
     const uint32_t left_len = a.out[s].left_len;
     const uint32_t tile_pos = (tile - sp.tile_begin) * kPartTile;
-    const uint32_t left_before = a.tile_left[tile];
     const uint32_t right_before = tile_pos - left_before;
     const uint32_t *src = a.src_rows[sp.seg.buf] + sp.seg.offset;
     uint32_t *dst = a.dst_rows[sp.seg.buf ^ 1u] + sp.seg.offset;
     const uint32_t id0 = sp.identity ? sp.seg.offset % a.n_rows : 0u;
-    const uint64_t *dec = a.decisions + (size_t)tile * kBallots;
-    const uint32_t wave = threadIdx.x / kWave, lane = lane_id();
     const uint64_t below = (1ull << lane) - 1ull;
-    // ballot q sits in lane q; its left rows and the left rows before it
-    const uint64_t mine = lane < kBallots ? dec[lane] : 0ull;
+    // the ballot's left rows and the left rows before it
     const uint32_t cnt = (uint32_t)__popcll(mine);
     uint32_t incl = cnt;
 #pragma unroll
