@@ -105,18 +105,20 @@ __device__ __forceinline__ void hist_dense8(const HistArgs &a) {
     constexpr int NW = NF / 4;
     constexpr uint32_t kWords = BIN_MAJOR ? FG * 256 : FG * kLdsFeature + kWave;
     constexpr uint32_t kDummy = FG * kLdsFeature;
-    __shared__ unsigned long long lg[kWords];
-    __shared__ unsigned long long lh[kWords];
+    // NF < FG: g's last word (bin 255, column FG - 1) is a padding column
+    // no add reaches, so h's words start on it; a cell's h then sits
+    // (kWords - 1) x 8 bytes after its g, within an LDS instruction's
+    // 16-bit offset, and one address serves both adds
+    constexpr uint32_t kHAt = BIN_MAJOR && NF < FG ? kWords - 1 : kWords;
+    __shared__ unsigned long long lgh[kHAt + kWords];
+    unsigned long long *const lg = lgh, *const lh = lgh + kHAt;
     const uint32_t entry = blockIdx.x / a.groups, grp = blockIdx.x % a.groups;
     if (entry >= a.counts[0]) return;  // uniform across the workgroup
     const HistTile t = a.tiles[entry];
     const HistNode nd = a.nodes[t.node];
     const uint32_t f0 = grp * FG;
     const uint32_t nf = min((uint32_t)FG, a.n_cols - f0);
-    for (uint32_t i = threadIdx.x; i < kWords; i += blockDim.x) {
-        lg[i] = 0ull;
-        lh[i] = 0ull;
-    }
+    for (uint32_t i = threadIdx.x; i < kHAt + kWords; i += blockDim.x) lgh[i] = 0ull;
     __syncthreads();
     const int eg = a.scale[nd.cls].exp_g, eh = a.scale[nd.cls].exp_h;
     const GPair *gpair = a.gpair + (size_t)nd.cls * a.class_rows;

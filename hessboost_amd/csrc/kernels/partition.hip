@@ -603,12 +603,14 @@ __device__ __forceinline__ void walk_grad_root(const WalkGradArgs &args) {
     const GradArgs &ga = args.g;
     __shared__ uint2 s_node[kWalkLdsNodes];
     __shared__ float s_value[kWalkLdsNodes];
-    __shared__ unsigned long long lg[kRootTile], lh[kRootTile];
+    // NF < kRootFeatures: h's words start on g's last (bin 255, a padding
+    // column no add reaches), so that one address with an LDS offset
+    // serves both adds of a cell
+    constexpr uint32_t kHAt = NF < kRootFeatures ? kRootTile - 1 : kRootTile;
+    __shared__ unsigned long long lgh[kHAt + kRootTile];
+    unsigned long long *const lg = lgh, *const lh = lgh + kHAt;
     if (walk_skipped(a)) return;
-    for (uint32_t i = threadIdx.x; i < kRootTile; i += blockDim.x) {
-        lg[i] = 0ull;
-        lh[i] = 0ull;
-    }
+    for (uint32_t i = threadIdx.x; i < kHAt + kRootTile; i += blockDim.x) lgh[i] = 0ull;
     const uint32_t n_nodes = load_walk_nodes(a, s_node, s_value);
     __syncthreads();
     const uint32_t rot = NF == kRootFeatures ? lane_id() & (kRootFeatures - 1u) : lane_id() % NF;
